@@ -1,0 +1,221 @@
+/*
+ * qwfn_qsa.h -- C ABI of the MI355X (gfx950) q8_0 KV cache and Qwen Sparse
+ * Attention (QSA) decode path.
+ *
+ * The reference engine builds this path out of ggml graph nodes inside
+ * qwfn::graph_builder; every entry point below replaces one group of those
+ * nodes and names the reference lines it stands in for.  The caller owns all
+ * device memory (the reference's `state` owns the cache buffers,
+ * src/qwfn_state.cpp:74-87); nothing here allocates on the hot path.
+ *
+ * Conventions
+ *  - Every function returns QWFN_OK (0) or a negative QWFN_E* code; the message
+ *    of the last failure on the calling thread is qwfn_qsa_last_error().
+ *    Shapes, counts and sizes are validated on the host before anything is
+ *    enqueued; a failed validation enqueues nothing and touches no device
+ *    memory.  Nothing aborts.
+ *  - Work is only enqueued on `stream` (a hipStream_t passed as void*, NULL =
+ *    the null stream).  No call synchronises, so calls can be captured into a
+ *    hipGraph and replayed, as the reference replays its per-layer CUDA graphs
+ *    (src/qwfn_engine.cpp:2066-2081).
+ *  - Per-token indices (sequence ids, positions, sequence lengths) live in
+ *    device memory so a captured graph can be replayed with new values.  The
+ *    kernels bound-check them; a row, block or sequence that is out of range is
+ *    skipped and the matching QWFN_STATUS_* bit is OR-ed into view->status
+ *    (when non-NULL).  qwfn_qsa_read_status() fetches and clears it.
+ *  - Bit-exactness: q8_0 bytes, pooled keys of whole blocks, selected block ids
+ *    and gathered cells are deterministic and bit-exact against the CPU
+ *    restatement; attention outputs are fp32 within max-abs 2e-3 + 1e-3*|ref|.
+ *
+ * Device data layout (one K pool and one V pool per attention layer)
+ *  page  = n_head_kv * page_tokens * (head_dim + head_dim/16) bytes:
+ *    quants : int8  [n_head_kv][page_tokens/64][head_dim/16][64][16]
+ *             (64-token tiles; each 16-byte chunk of a token's head row is
+ *              interleaved with the same chunk of the tile's other 63 tokens,
+ *              so lane t of a wave reading chunk c of token t is one contiguous
+ *              1 KiB load)
+ *    scales : fp16  [n_head_kv][page_tokens][head_dim/32]  (one per q8_0 block)
+ *  A logical position t of sequence s lives in physical page
+ *  page_table[s*pages_per_seq + t/page_tokens] at row t%page_tokens.
+ *  pooled = fp32 [n_seq][n_head_kv][blocks_per_seq][head_dim], where
+ *  blocks_per_seq = pages_per_seq*page_tokens/block_tokens.
+ *  The reference's contiguous token-major cache (src/qwfn_state.cpp:52-54) is
+ *  the special case of one sequence with an identity page table.
+ */
+#ifndef QWFN_QSA_H
+#define QWFN_QSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWFN_QSA_ABI_VERSION 1
+
+/* return codes */
+#define QWFN_OK        0
+#define QWFN_EHIP     (-5)   /* a HIP runtime call failed */
+#define QWFN_EINVAL   (-22)  /* bad shape, pointer or count */
+#define QWFN_ERANGE   (-34)  /* a length or size exceeds what the view holds */
+#define QWFN_ENOTSUP  (-95)  /* a valid shape this build has no kernel for */
+
+/* q8_0 rounding variants of ggml's quantizer (block_q8_0: fp16 d; int8 qs[32])
+ *  X86_RNE   : id = 127/amax, q = round-half-even(x*id)  (ggml-cpu AVX path)
+ *  REF_ROUNDF: id = 1/d,      q = roundf(x*id)           (quantize_row_q8_0_ref,
+ *                                                          ggml-cuda set_rows)
+ * Both store d = fp16_rne(amax/127).  A non-finite x*id stores q = 0.        */
+#define QWFN_Q8_X86_RNE     0
+#define QWFN_Q8_REF_ROUNDF  1
+
+/* element type of K/V rows handed to the append */
+#define QWFN_SRC_F32  0
+#define QWFN_SRC_F16  1
+
+/* bits of view->status */
+#define QWFN_STATUS_POS_RANGE    0x1  /* a position >= the view's capacity     */
+#define QWFN_STATUS_SEQ_RANGE    0x2  /* a sequence id outside [0, n_seq)      */
+#define QWFN_STATUS_PAGE_RANGE   0x4  /* a page-table entry outside the pool   */
+#define QWFN_STATUS_LEN_RANGE    0x8  /* a seq_len < 1 or > max_seq_len        */
+#define QWFN_STATUS_BLOCK_RANGE  0x10 /* a block id beyond the view           */
+
+typedef struct qwfn_qsa_shape {
+    int32_t n_head;          /* query heads (16)                               */
+    int32_t n_head_kv;       /* KV heads (2); GQA group = n_head/n_head_kv     */
+    int32_t head_dim;        /* 128                                            */
+    int32_t block_tokens;    /* tokens pooled into one indexer block (64)      */
+    int32_t page_tokens;     /* tokens per cache page, a multiple of 64 (256)  */
+    int32_t top_k_blocks;    /* scored blocks kept (64); <= 0 = dense          */
+    int32_t sink_blocks;     /* leading blocks always kept (1)                 */
+    int32_t local_tokens;    /* trailing tokens whose blocks are kept (512)    */
+    int32_t relu_per_head;   /* 1: score = sum_h relu(q_h.p) (lightning idx)   */
+    int32_t shared_selection;/* 1: one selection for all KV heads (not built)  */
+    int32_t quant_variant;   /* QWFN_Q8_X86_RNE or QWFN_Q8_REF_ROUNDF          */
+} qwfn_qsa_shape;
+
+typedef struct qwfn_kv_view {
+    void          *k_pages;      /* [n_phys_pages][page bytes], device          */
+    void          *v_pages;      /* same for V                                  */
+    float         *pooled;       /* fp32 pooled keys, layout above, device      */
+    const int32_t *page_table;   /* [n_seq][pages_per_seq], device              */
+    int32_t       *status;       /* one device int32, or NULL                   */
+    int32_t        n_seq;
+    int32_t        pages_per_seq;
+    int32_t        n_phys_pages;
+} qwfn_kv_view;
+
+/* ---- introspection / sizing ------------------------------------------------ */
+int         qwfn_qsa_abi_version(void);
+const char *qwfn_qsa_last_error(void);
+/* Validates a shape (QWFN_EINVAL) and whether this build has kernels for it
+ * (QWFN_ENOTSUP).  Replaces the reference's shape constants
+ * (src/qwfn_hparams.h:22-36, src/qwfn_engine.cpp:382-435).                   */
+int qwfn_qsa_check_shape(const qwfn_qsa_shape *shape);
+/* Bytes of one K (or V) page.  Replaces the per-layer cache sizing of
+ * state::init (src/qwfn_state.cpp:39-54).                                      */
+int qwfn_qsa_page_bytes(const qwfn_qsa_shape *shape, size_t *bytes);
+/* Bytes of the pooled-key array for n_seq sequences of pages_per_seq pages
+ * (the reference's pool_cache_, src/qwfn_engine.cpp:389-394).                 */
+int qwfn_qsa_pooled_bytes(const qwfn_qsa_shape *shape, int32_t n_seq,
+                          int32_t pages_per_seq, size_t *bytes);
+/* Upper bound on blocks one (sequence, KV head) selects at a length up to
+ * max_seq_len: the reference's k_blocks plus the forced blocks
+ * (src/qwfn_engine.cpp:430, 748-753).                                          */
+int qwfn_qsa_max_selected(const qwfn_qsa_shape *shape, int32_t max_seq_len,
+                          int32_t *max_sel);
+/* Workspace for qwfn_indexer_topk / qwfn_sparse_decode_attn /
+ * qwfn_sparse_attn_decode at n_seq sequences up to max_seq_len tokens.  The
+ * workspace carries completion counters that every call leaves at zero:
+ * initialise a new workspace once with qwfn_qsa_workspace_init (a fill kernel,
+ * not a memset, so it may also be captured).  Calls that overlap on one
+ * workspace race.                                                              */
+int qwfn_qsa_workspace_bytes(const qwfn_qsa_shape *shape, int32_t n_seq,
+                             int32_t max_seq_len, size_t *bytes);
+int qwfn_qsa_workspace_init(void *ws, size_t ws_bytes, void *stream);
+/* Synchronously copies view->status to *status and clears it.                 */
+int qwfn_qsa_read_status(const qwfn_kv_view *view, int32_t *status, void *stream);
+
+/* ---- cache writes -------------------------------------------------------- */
+/* Quantize n_rows K and V rows ([n_head_kv][head_dim] each, F32 or F16) to
+ * q8_0 and write them at (seq_ids[i], pos[i]).  An idempotent overwrite: a
+ * rewritten position gets exactly the bytes a first write would.
+ * Replaces ggml_set_rows into the q8_0 cache at write_idx (decode,
+ * src/qwfn_graph.cpp:520-528) and ggml_cpy of a chunk into a view of the cache
+ * (prefill, src/qwfn_graph.cpp:349-360).  seq_ids may be NULL (all 0).        */
+int qwfn_kv_append_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                        const void *k_src, const void *v_src, int32_t src_dtype,
+                        const int32_t *seq_ids, const int32_t *pos,
+                        int32_t n_rows, void *stream);
+/* Recompute the pooled key of each listed block from its block_tokens
+ * dequantized K members: a sequential fp32 add chain, then *(1/block_tokens).
+ * Replaces qsa_pool_blocks' add chain and ggml_scale (src/qwfn_graph.cpp:
+ * 410-422) as used by the decode update (:471-476).  A block whose members are
+ * not all written gets an unspecified (but finite-input-deterministic) value;
+ * it is never scored while partial.  seq_ids may be NULL (all 0).             */
+int qwfn_pool_update(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                     const int32_t *seq_ids, const int32_t *block_ids,
+                     int32_t n_blocks, void *stream);
+/* Pool blocks [0, n_whole) of sequence `seq` (host value): the reference's
+ * qsa_pool_rebuild after a prefill (src/qwfn_graph.cpp:431-448,
+ * src/qwfn_engine.cpp:761-798).                                               */
+int qwfn_pool_rebuild(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                      int32_t seq, int32_t n_whole, void *stream);
+
+/* ---- selection ------------------------------------------------------------ */
+/* Indexer + top-k for one decode token per sequence.  q is fp32
+ * [n_seq][n_head][head_dim]; seq_len (device) is each sequence's length
+ * including the token just appended (the reference's n_past+1).  Per
+ * (sequence, KV head g) the score of whole block b is
+ *    sum over the group's heads h of dot(q_h, pooled[b][g])   (relu'd per head
+ *    when relu_per_head), in a fixed fp32 order shared with the CPU oracle;
+ * the forced set F = sink blocks U blocks meeting the last local_tokens tokens;
+ * the eligible set E = whole blocks not in F; the kept set is F U top_k(E) by
+ * (score desc, block asc).  sel receives the kept block ids ascending,
+ * [n_seq][n_head_kv][max_sel]; n_sel [n_seq][n_head_kv] their count.
+ * Replaces the scores / relu / sum_rows / bias add / ggml_top_k nodes
+ * (src/qwfn_graph.cpp:477-495) and the host bias window (src/qwfn_engine.cpp:
+ * 748-759).                                                                    */
+int qwfn_indexer_topk(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                      const float *q, const int32_t *seq_len, int32_t n_seq,
+                      int32_t max_seq_len, int32_t *sel, int32_t *n_sel,
+                      int32_t max_sel, void *ws, size_t ws_bytes, void *stream);
+/* The cells of a selection, dequantized: fp32 k_out/v_out
+ * [n_seq][n_head_kv][max_sel*block_tokens][head_dim], cells
+ * [n_seq][n_head_kv][max_sel*block_tokens] (-1 past seq_len or the count).
+ * A parity/debug entry point; the attention kernels gather in place.
+ * Replaces ggml_get_rows q8_0->f32 of the selected cells (src/qwfn_graph.cpp:
+ * 494-495, 530-537).                                                           */
+int qwfn_gather_dequant(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                        const int32_t *seq_len, int32_t n_seq,
+                        const int32_t *sel, const int32_t *n_sel, int32_t max_sel,
+                        float *k_out, float *v_out, int32_t *cells, void *stream);
+
+/* ---- attention ------------------------------------------------------------ */
+/* GQA softmax attention of one query token per sequence over the cells of a
+ * given selection (cells at positions >= seq_len are masked), scale
+ * 1/sqrt(head_dim), fp32 out [n_seq][n_head][head_dim].  sel == NULL means
+ * dense: every block below seq_len.  Replaces the cell mask
+ * (src/qwfn_graph.cpp:497-502) and ggml_flash_attn_ext with GGML_PREC_F32
+ * (:539-542).                                                                  */
+int qwfn_sparse_decode_attn(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                            const float *q, const int32_t *seq_len, int32_t n_seq,
+                            int32_t max_seq_len, const int32_t *sel,
+                            const int32_t *n_sel, int32_t max_sel, float *out,
+                            void *ws, size_t ws_bytes, void *stream);
+/* One decode token of graph_builder::sparse_attn_decode (src/qwfn_graph.cpp:
+ * 450-546) from the K/V projections on: append k_new/v_new
+ * ([n_seq][n_head_kv][head_dim], src_dtype) at position seq_len-1, re-pool the
+ * block that position completes, score + select, and attend.  sel_out/n_sel_out
+ * (optional) receive the selection as qwfn_indexer_topk would.  Two launches.  */
+int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                            const float *q, const void *k_new, const void *v_new,
+                            int32_t src_dtype, const int32_t *seq_len,
+                            int32_t n_seq, int32_t max_seq_len, float *out,
+                            int32_t *sel_out, int32_t *n_sel_out,
+                            void *ws, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWFN_QSA_H */

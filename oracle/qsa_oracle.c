@@ -1,0 +1,555 @@
+/*
+ * qsa_oracle.c -- CPU restatement of the q8_0 KV cache + QSA decode path.
+ * TEST INFRASTRUCTURE ONLY (see qsa_oracle.h): the checker for the HIP path
+ * and the CPU baseline of bench.py.  Built with -ffp-contract=off.
+ */
+#include "qsa_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* fp16                                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* IEEE binary32 -> binary16, round to nearest even.  ggml stores the q8_0
+ * scale with GGML_FP32_TO_FP16 (F16C _cvtss_sh with RNE on x86). */
+uint16_t qwfn_oracle_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) {                       /* inf / nan */
+        if (ax == 0x7F800000u) return sign | 0x7C00u;
+        return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    }
+    const int32_t exp = (int32_t)(ax >> 23);       /* biased, 0 = subnormal */
+    const uint32_t mant = ax & 0x7FFFFFu;
+    const int32_t e16 = exp - 127 + 15;
+    if (e16 >= 31) return sign | 0x7C00u;          /* >= 2^16: overflow */
+    if (e16 >= 1) {                                /* normal half */
+        uint32_t h = ((uint32_t)e16 << 10) | (mant >> 13);
+        const uint32_t rem = mant & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u; /* may carry to inf */
+        return (uint16_t)(sign | h);
+    }
+    if (exp == 0) return sign;                     /* f32 subnormal < 2^-126 */
+    /* subnormal half: value / 2^-24 = mf * 2^(exp-126) */
+    const uint32_t mf = mant | 0x800000u;
+    const int32_t sh = 126 - exp;                  /* >= 14 */
+    if (sh >= 25) return sign;                     /* < half of 2^-24 */
+    uint32_t h = mf >> sh;
+    const uint32_t rem = mf & ((1u << sh) - 1u);
+    const uint32_t half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+float qwfn_oracle_f16_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t e = ((uint32_t)h >> 10) & 0x1Fu;
+    const uint32_t m = (uint32_t)h & 0x3FFu;
+    uint32_t x;
+    if (e == 0x1Fu) {
+        x = sign | 0x7F800000u | (m << 13);
+    } else if (e != 0) {
+        x = sign | ((e - 15u + 127u) << 23) | (m << 13);
+    } else if (m == 0) {
+        x = sign;
+    } else {                                       /* subnormal half: m * 2^-24 */
+        const float v = (float)m * 5.9604644775390625e-08f;   /* exact */
+        memcpy(&x, &v, 4);
+        x |= sign;
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+void qwfn_oracle_f32_to_f16_n(const float *x, int64_t n, uint16_t *out) {
+    for (int64_t i = 0; i < n; i++) out[i] = qwfn_oracle_f32_to_f16(x[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* q8_0                                                                      */
+/* ------------------------------------------------------------------------ */
+
+static int8_t to_i8(float r) {
+    if (r != r) return 0;                          /* documented: NaN -> 0 */
+    if (r > 127.0f) return 127;
+    if (r < -128.0f) return -128;
+    return (int8_t)r;
+}
+
+/* ggml's q8_0 quantizer, restated from its published algorithm: amax over the
+ * 32 values, d = amax/127 stored as fp16, then either the x86 SIMD form
+ * (id = 127/amax, round half even) or the reference/CUDA form (id = 1/d,
+ * roundf).  Reached by ggml_set_rows / ggml_cpy into the q8_0 cache
+ * (/root/reference src/qwfn_graph.cpp:525-526, 353-360). */
+void qwfn_oracle_quantize_block(const float *x, int32_t variant, uint16_t *dout,
+                                int8_t *qs) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        const float a = fabsf(x[j]);
+        if (a > amax) amax = a;                    /* NaN never wins */
+    }
+    const float d = amax / 127.0f;
+    *dout = qwfn_oracle_f32_to_f16(d);
+    float id;
+    if (variant == QWFN_Q8_X86_RNE)
+        id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    else
+        id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int j = 0; j < 32; j++) {
+        const float v = x[j] * id;
+        const float r = (variant == QWFN_Q8_X86_RNE) ? rintf(v) : roundf(v);
+        qs[j] = to_i8(r);
+    }
+}
+
+void qwfn_oracle_quantize_row_ggml(const float *x, int64_t n, int32_t variant,
+                                   uint8_t *out) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        uint16_t d;
+        qwfn_oracle_quantize_block(x + 32 * b, variant, &d, (int8_t *)(out + 34 * b + 2));
+        memcpy(out + 34 * b, &d, 2);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* layout                                                                    */
+/* ------------------------------------------------------------------------ */
+
+static size_t quant_bytes_per_page(const qwfn_qsa_shape *s) {
+    return (size_t)s->n_head_kv * (size_t)s->page_tokens * (size_t)s->head_dim;
+}
+
+size_t qwfn_oracle_page_bytes(const qwfn_qsa_shape *s) {
+    return quant_bytes_per_page(s) +
+           (size_t)s->n_head_kv * (size_t)s->page_tokens * (size_t)(s->head_dim / 32) * 2u;
+}
+
+int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
+                                 int32_t d) {
+    const int64_t tiles = s->page_tokens / 64, chunks = s->head_dim / 16;
+    return (((int64_t)g * tiles + row / 64) * chunks + d / 16) * 1024 +
+           (int64_t)(row % 64) * 16 + d % 16;
+}
+
+int64_t qwfn_oracle_scale_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
+                                 int32_t j) {
+    return (int64_t)quant_bytes_per_page(s) +
+           (((int64_t)g * s->page_tokens + row) * (s->head_dim / 32) + j) * 2;
+}
+
+/* Physical page base for (seq, t), or NULL with *status bits set. */
+static uint8_t *page_of(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const void *pool,
+                        int32_t seq, int32_t t, int32_t *status) {
+    if (seq < 0 || seq >= v->n_seq) { *status |= QWFN_STATUS_SEQ_RANGE; return NULL; }
+    if (t < 0 || (int64_t)t >= (int64_t)v->pages_per_seq * s->page_tokens) {
+        *status |= QWFN_STATUS_POS_RANGE; return NULL;
+    }
+    const int32_t phys = v->page_table[(int64_t)seq * v->pages_per_seq + t / s->page_tokens];
+    if (phys < 0 || phys >= v->n_phys_pages) { *status |= QWFN_STATUS_PAGE_RANGE; return NULL; }
+    return (uint8_t *)pool + (size_t)phys * qwfn_oracle_page_bytes(s);
+}
+
+static float src_at(const void *src, int32_t dtype, int64_t i) {
+    if (dtype == QWFN_SRC_F16) return qwfn_oracle_f16_to_f32(((const uint16_t *)src)[i]);
+    return ((const float *)src)[i];
+}
+
+/* Decode append (src/qwfn_graph.cpp:520-528) and prefill chunk append
+ * (src/qwfn_graph.cpp:349-360): quantize each [n_head_kv][head_dim] row and
+ * overwrite it at its position.  Returns status bits (0 = every row written). */
+int qwfn_oracle_append(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                       const void *k_src, const void *v_src, int32_t src_dtype,
+                       const int32_t *seq_ids, const int32_t *pos, int32_t n_rows) {
+    const int32_t H = s->n_head_kv, hd = s->head_dim;
+    int32_t status = 0;
+    float x[32];
+    for (int32_t i = 0; i < n_rows; i++) {
+        const int32_t seq = seq_ids ? seq_ids[i] : 0, t = pos[i];
+        for (int which = 0; which < 2; which++) {
+            const void *src = which ? v_src : k_src;
+            uint8_t *page = page_of(s, v, which ? v->v_pages : v->k_pages, seq, t, &status);
+            if (!page) continue;
+            const int32_t row = t % s->page_tokens;
+            for (int32_t g = 0; g < H; g++)
+                for (int32_t j = 0; j < hd / 32; j++) {
+                    for (int e = 0; e < 32; e++)
+                        x[e] = src_at(src, src_dtype, ((int64_t)i * H + g) * hd + 32 * j + e);
+                    uint16_t d;
+                    int8_t qs[32];
+                    qwfn_oracle_quantize_block(x, s->quant_variant, &d, qs);
+                    memcpy(page + qwfn_oracle_scale_offset(s, g, row, j), &d, 2);
+                    for (int e = 0; e < 32; e++)
+                        page[qwfn_oracle_quant_offset(s, g, row, 32 * j + e)] = (uint8_t)qs[e];
+                }
+        }
+    }
+    return status;
+}
+
+/* ggml_get_rows of q8_0 -> f32 (src/qwfn_graph.cpp:531): x = fp32(d) * q, exact. */
+int qwfn_oracle_dequant_row(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                            const void *pool, int32_t seq, int32_t t, int32_t g,
+                            float *out) {
+    int32_t status = 0;
+    const uint8_t *page = page_of(s, v, pool, seq, t, &status);
+    if (!page) return status;
+    const int32_t row = t % s->page_tokens;
+    for (int32_t d = 0; d < s->head_dim; d++) {
+        uint16_t h;
+        memcpy(&h, page + qwfn_oracle_scale_offset(s, g, row, d / 32), 2);
+        const int8_t q = (int8_t)page[qwfn_oracle_quant_offset(s, g, row, d)];
+        out[d] = qwfn_oracle_f16_to_f32(h) * (float)q;
+    }
+    return 0;
+}
+
+static int64_t blocks_per_seq(const qwfn_qsa_shape *s, const qwfn_kv_view *v) {
+    return (int64_t)v->pages_per_seq * s->page_tokens / s->block_tokens;
+}
+
+/* Mean of a block's member keys: qsa_pool_blocks' sequential ggml_add chain over
+ * the r member slices, then ggml_scale(1/r) (src/qwfn_graph.cpp:415-422), with
+ * the members read from the dequantized K cache (the configuration pools K
+ * itself; no norm or rope follows). */
+int qwfn_oracle_pool_block(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                           int32_t seq, int32_t b) {
+    const int32_t hd = s->head_dim, bt = s->block_tokens;
+    if (seq < 0 || seq >= v->n_seq) return QWFN_STATUS_SEQ_RANGE;
+    if (b < 0 || b >= blocks_per_seq(s, v)) return QWFN_STATUS_BLOCK_RANGE;
+    float *acc = (float *)malloc(sizeof(float) * 2 * hd), *row = acc + hd;
+    int32_t status = 0;
+    for (int32_t g = 0; g < s->n_head_kv; g++) {
+        status |= qwfn_oracle_dequant_row(s, v, v->k_pages, seq, b * bt, g, acc);
+        for (int32_t t = 1; t < bt; t++) {
+            status |= qwfn_oracle_dequant_row(s, v, v->k_pages, seq, b * bt + t, g, row);
+            for (int32_t d = 0; d < hd; d++) acc[d] = acc[d] + row[d];
+        }
+        if (status) break;
+        const float inv = 1.0f / (float)bt;
+        float *dst = v->pooled + (((int64_t)seq * s->n_head_kv + g) * blocks_per_seq(s, v) + b) * hd;
+        for (int32_t d = 0; d < hd; d++) dst[d] = acc[d] * inv;
+    }
+    free(acc);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
+/* indexer + selection                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Score of one block for one KV head: for each head h of the group, the dot
+ * q_h . p as four fmaf chains (chain j takes the dims d with (d/4)%4 == j, in
+ * increasing d) combined as (c0+c1)+(c2+c3); optionally relu'd; then the heads
+ * summed in order.  This is the score of src/qwfn_graph.cpp:485-492 (mul_mat,
+ * relu, sum_rows over heads) at the configuration's shapes, in the fixed order
+ * the HIP indexer evaluates (four lanes share one dot). */
+float qwfn_oracle_block_score(const qwfn_qsa_shape *s, const float *q_group,
+                              const float *p) {
+    const int32_t hd = s->head_dim, G = s->n_head / s->n_head_kv;
+    float score = 0.0f;
+    for (int32_t h = 0; h < G; h++) {
+        const float *q = q_group + (int64_t)h * hd;
+        float c[4];
+        for (int j = 0; j < 4; j++) {
+            float acc = 0.0f;
+            for (int32_t i = 0; i < hd / 16; i++)
+                for (int e = 0; e < 4; e++) {
+                    const int32_t d = 16 * i + 4 * j + e;
+                    acc = fmaf(q[d], p[d], acc);
+                }
+            c[j] = acc;
+        }
+        float dot = (c[0] + c[1]) + (c[2] + c[3]);
+        if (s->relu_per_head) dot = dot > 0.0f ? dot : 0.0f;
+        score = (h == 0) ? dot : score + dot;
+    }
+    return score;
+}
+
+/* Forced and eligible ranges of one (sequence, KV head) at length seq_len.
+ * The reference forces the incomplete tail block with a +1e9 bias and leaves
+ * whole blocks at 0 (src/qwfn_engine.cpp:748-753, decode; :936-950, prefill);
+ * the configuration generalises the forced set to the sink blocks plus every
+ * block meeting the last local_tokens tokens.  Eligible = whole blocks in
+ * [sink_blocks, first_window_block). */
+static void qsa_ranges(const qwfn_qsa_shape *s, int32_t seq_len, int32_t *b_last,
+                       int32_t *fw, int32_t *e_lo, int32_t *e_hi) {
+    const int32_t bt = s->block_tokens, last = seq_len - 1;
+    const int32_t w0 = last - s->local_tokens + 1;
+    *b_last = last / bt;
+    *fw = w0 > 0 ? w0 / bt : 0;
+    const int32_t nbw = seq_len / bt;
+    *e_lo = s->sink_blocks;
+    *e_hi = nbw < *fw ? nbw : *fw;
+    if (*e_hi < *e_lo) *e_hi = *e_lo;
+}
+
+static uint32_t score_key(float x) {
+    uint32_t u;
+    if (x != x) return 0u;                         /* NaN ranks lowest */
+    if (x == 0.0f) x = 0.0f;                       /* -0 ties +0 */
+    memcpy(&u, &x, 4);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+typedef struct { uint32_t key; int32_t b; } cand_t;
+
+static int cand_cmp(const void *a, const void *b) {
+    const cand_t *x = (const cand_t *)a, *y = (const cand_t *)b;
+    if (x->key != y->key) return x->key > y->key ? -1 : 1;   /* score desc */
+    return x->b < y->b ? -1 : (x->b > y->b);                 /* index asc  */
+}
+
+static int int_cmp(const void *a, const void *b) {
+    const int32_t x = *(const int32_t *)a, y = *(const int32_t *)b;
+    return x < y ? -1 : (x > y);
+}
+
+int32_t qwfn_oracle_max_selected(const qwfn_qsa_shape *s, int32_t max_seq_len) {
+    const int32_t bt = s->block_tokens;
+    const int32_t all = (max_seq_len + bt - 1) / bt;
+    if (s->top_k_blocks <= 0) return all;
+    const int32_t win = (s->local_tokens + bt - 2) / bt + 1;
+    const int64_t cap = (int64_t)s->top_k_blocks + s->sink_blocks + win;
+    return cap < all ? (int32_t)cap : all;
+}
+
+/* ggml_top_k over the biased scores (src/qwfn_graph.cpp:493) with the tie rule
+ * the build fixes (score desc, then lower block index), the forced blocks
+ * added, emitted ascending. */
+int32_t qwfn_oracle_select(const qwfn_qsa_shape *s, const float *scores,
+                           int32_t seq_len, int32_t *sel, int32_t max_sel) {
+    if (seq_len < 1) return QWFN_EINVAL;
+    int32_t b_last, fw, e_lo, e_hi, n = 0;
+    qsa_ranges(s, seq_len, &b_last, &fw, &e_lo, &e_hi);
+    if (s->top_k_blocks <= 0) {
+        if (b_last + 1 > max_sel) return QWFN_ERANGE;
+        for (int32_t b = 0; b <= b_last; b++) sel[n++] = b;
+        return n;
+    }
+    /* forced */
+    int32_t *out = (int32_t *)malloc(sizeof(int32_t) * (size_t)(b_last + 1));
+    for (int32_t b = 0; b <= b_last; b++)
+        if (b < s->sink_blocks || b >= fw) out[n++] = b;
+    const int32_t ne = e_hi - e_lo;
+    if (ne <= s->top_k_blocks) {
+        for (int32_t b = e_lo; b < e_hi; b++) out[n++] = b;
+    } else {
+        cand_t *c = (cand_t *)malloc(sizeof(cand_t) * (size_t)ne);
+        for (int32_t i = 0; i < ne; i++) { c[i].key = score_key(scores[e_lo + i]); c[i].b = e_lo + i; }
+        qsort(c, (size_t)ne, sizeof(cand_t), cand_cmp);
+        for (int32_t i = 0; i < s->top_k_blocks; i++) out[n++] = c[i].b;
+        free(c);
+    }
+    qsort(out, (size_t)n, sizeof(int32_t), int_cmp);
+    int32_t rc = n;
+    if (n > max_sel) rc = QWFN_ERANGE;
+    else memcpy(sel, out, sizeof(int32_t) * (size_t)n);
+    free(out);
+    return rc;
+}
+
+int qwfn_oracle_indexer_topk(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                             const float *q, const int32_t *seq_len, int32_t n_seq,
+                             int32_t *sel, int32_t *n_sel, int32_t max_sel) {
+    const int32_t H = s->n_head_kv, hd = s->head_dim, G = s->n_head / H;
+    const int64_t bps = blocks_per_seq(s, v);
+    int32_t status = 0;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(bps > 0 ? bps : 1));
+    for (int32_t seq = 0; seq < n_seq; seq++) {
+        const int32_t L = seq_len[seq];
+        for (int32_t g = 0; g < H; g++) {
+            int32_t *ns = n_sel + (int64_t)seq * H + g;
+            *ns = 0;
+            if (L < 1 || (int64_t)L > (int64_t)v->pages_per_seq * s->page_tokens) {
+                status |= QWFN_STATUS_LEN_RANGE;
+                continue;
+            }
+            int32_t b_last, fw, e_lo, e_hi;
+            qsa_ranges(s, L, &b_last, &fw, &e_lo, &e_hi);
+            if (s->top_k_blocks > 0 && e_hi - e_lo > s->top_k_blocks) {
+                const float *qg = q + ((int64_t)seq * s->n_head + (int64_t)g * G) * hd;
+                const float *pb = v->pooled + ((int64_t)seq * H + g) * bps * hd;
+                for (int32_t b = e_lo; b < e_hi; b++)
+                    scores[b] = qwfn_oracle_block_score(s, qg, pb + (int64_t)b * hd);
+            }
+            const int32_t r = qwfn_oracle_select(s, scores, L, sel + ((int64_t)seq * H + g) * max_sel, max_sel);
+            if (r < 0) { free(scores); return r; }
+            *ns = r;
+        }
+    }
+    free(scores);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
+/* attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* ggml_flash_attn_ext (prec F32, scale 1/sqrt(hd), no bias or softcap) over the
+ * selected cells with the cell mask cell <= n_past (src/qwfn_graph.cpp:
+ * 497-502, 539-541), restated as the textbook softmax in fp64 on the exactly
+ * dequantized K/V.  GQA: query head h reads KV head h / (n_head/n_head_kv). */
+int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                              const float *q, const int32_t *seq_len, int32_t n_seq,
+                              const int32_t *sel, const int32_t *n_sel,
+                              int32_t max_sel, double *out) {
+    const int32_t H = s->n_head_kv, hd = s->head_dim, G = s->n_head / H, bt = s->block_tokens;
+    int32_t status = 0;
+    float *krow = (float *)malloc(sizeof(float) * 2 * hd), *vrow = krow + hd;
+    for (int32_t seq = 0; seq < n_seq; seq++) {
+        const int32_t L = seq_len[seq];
+        for (int32_t g = 0; g < H; g++) {
+            double *o = out + ((int64_t)seq * s->n_head + (int64_t)g * G) * hd;
+            memset(o, 0, sizeof(double) * (size_t)G * hd);
+            if (L < 1 || (int64_t)L > (int64_t)v->pages_per_seq * s->page_tokens) {
+                status |= QWFN_STATUS_LEN_RANGE;
+                continue;
+            }
+            const int32_t nb = sel ? n_sel[(int64_t)seq * H + g] : (L - 1) / bt + 1;
+            int64_t nc = 0;
+            int32_t *cells = (int32_t *)malloc(sizeof(int32_t) * (size_t)nb * bt + 1);
+            for (int32_t i = 0; i < nb; i++) {
+                const int32_t b = sel ? sel[((int64_t)seq * H + g) * max_sel + i] : i;
+                for (int32_t t = b * bt; t < b * bt + bt && t < L; t++) cells[nc++] = t;
+            }
+            double *lg = (double *)malloc(sizeof(double) * (size_t)(nc * G + 1));
+            const double scale = 1.0 / sqrt((double)hd);
+            for (int64_t c = 0; c < nc; c++) {
+                status |= qwfn_oracle_dequant_row(s, v, v->k_pages, seq, cells[c], g, krow);
+                for (int32_t h = 0; h < G; h++) {
+                    const float *qh = q + ((int64_t)seq * s->n_head + (int64_t)g * G + h) * hd;
+                    double acc = 0.0;
+                    for (int32_t d = 0; d < hd; d++) acc += (double)qh[d] * (double)krow[d];
+                    lg[c * G + h] = acc * scale;
+                }
+            }
+            for (int32_t h = 0; h < G; h++) {
+                double m = -INFINITY, l = 0.0;
+                for (int64_t c = 0; c < nc; c++) if (lg[c * G + h] > m) m = lg[c * G + h];
+                for (int64_t c = 0; c < nc; c++) {
+                    const double p = exp(lg[c * G + h] - m);
+                    lg[c * G + h] = p;
+                    l += p;
+                }
+                for (int64_t c = 0; c < nc; c++) lg[c * G + h] /= l;
+            }
+            for (int64_t c = 0; c < nc; c++) {
+                status |= qwfn_oracle_dequant_row(s, v, v->v_pages, seq, cells[c], g, vrow);
+                for (int32_t h = 0; h < G; h++)
+                    for (int32_t d = 0; d < hd; d++) o[(int64_t)h * hd + d] += lg[c * G + h] * (double)vrow[d];
+            }
+            free(lg);
+            free(cells);
+        }
+    }
+    free(krow);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
+/* CPU baseline: the whole decode token in fp32                              */
+/* ------------------------------------------------------------------------ */
+
+static float f16_round(float x) { return qwfn_oracle_f16_to_f32(qwfn_oracle_f32_to_f16(x)); }
+
+int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                                const float *q, const float *k_new,
+                                const float *v_new, const int32_t *seq_len,
+                                int32_t n_seq, float *out, int32_t *sel,
+                                int32_t *n_sel, int32_t max_sel) {
+    const int32_t H = s->n_head_kv, hd = s->head_dim, G = s->n_head / H, bt = s->block_tokens;
+    const int64_t bps = blocks_per_seq(s, v);
+    int threads = 1;
+#ifdef _OPENMP
+    threads = omp_get_max_threads();
+#endif
+    /* append + pool on completion (src/qwfn_graph.cpp:465-476, 520-528) */
+    for (int32_t seq = 0; seq < n_seq; seq++) {
+        const int32_t p = seq_len[seq] - 1;
+        if (qwfn_oracle_append(s, v, k_new + (int64_t)seq * H * hd, v_new + (int64_t)seq * H * hd,
+                               QWFN_SRC_F32, &seq, &p, 1))
+            return QWFN_ERANGE;
+        if ((p + 1) % bt == 0) qwfn_oracle_pool_block(s, v, seq, p / bt);
+    }
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(bps > 0 ? bps : 1));
+    for (int32_t seq = 0; seq < n_seq; seq++)
+        for (int32_t g = 0; g < H; g++) {
+            const int32_t L = seq_len[seq];
+            int32_t b_last, fw, e_lo, e_hi;
+            qsa_ranges(s, L, &b_last, &fw, &e_lo, &e_hi);
+            if (s->top_k_blocks > 0 && e_hi - e_lo > s->top_k_blocks) {
+                const float *qg = q + ((int64_t)seq * s->n_head + (int64_t)g * G) * hd;
+                const float *pb = v->pooled + ((int64_t)seq * H + g) * bps * hd;
+#pragma omp parallel for schedule(static)
+                for (int32_t b = e_lo; b < e_hi; b++)
+                    scores[b] = qwfn_oracle_block_score(s, qg, pb + (int64_t)b * hd);
+            }
+            n_sel[seq * H + g] = qwfn_oracle_select(s, scores, L, sel + ((int64_t)seq * H + g) * max_sel, max_sel);
+        }
+    free(scores);
+    /* attention: online softmax per (sequence, query head, split of blocks),
+     * gathered K/V cast to fp16 (src/qwfn_graph.cpp:530-541), then a merge. */
+    const int32_t splits = 8;
+    const int64_t n_task = (int64_t)n_seq * s->n_head * splits;
+    float *part = (float *)malloc(sizeof(float) * (size_t)n_task * (hd + 2));
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t task = 0; task < n_task; task++) {
+        const int32_t sp = (int32_t)(task % splits);
+        const int32_t hq = (int32_t)((task / splits) % s->n_head);
+        const int32_t seq = (int32_t)(task / splits / s->n_head);
+        const int32_t g = hq / G, L = seq_len[seq];
+        const int32_t nb = n_sel[seq * H + g];
+        const int32_t *sl = sel + ((int64_t)seq * H + g) * max_sel;
+        const float *qh = q + ((int64_t)seq * s->n_head + hq) * hd;
+        float *pp = part + task * (hd + 2);
+        float m = -INFINITY, l = 0.0f;
+        float kr[512], vr[512];
+        for (int32_t d = 0; d < hd; d++) pp[2 + d] = 0.0f;
+        const float scale = 1.0f / sqrtf((float)hd);
+        for (int32_t i = sp; i < nb; i += splits) {
+            const int32_t b = sl[i];
+            for (int32_t t = b * bt; t < b * bt + bt && t < L; t++) {
+                qwfn_oracle_dequant_row(s, v, v->k_pages, seq, t, g, kr);
+                float sc = 0.0f;
+                for (int32_t d = 0; d < hd; d++) sc += qh[d] * f16_round(kr[d]);
+                sc *= scale;
+                const float mn = sc > m ? sc : m;
+                const float corr = expf(m - mn), pw = expf(sc - mn);
+                qwfn_oracle_dequant_row(s, v, v->v_pages, seq, t, g, vr);
+                for (int32_t d = 0; d < hd; d++) pp[2 + d] = pp[2 + d] * corr + pw * f16_round(vr[d]);
+                l = l * corr + pw;
+                m = mn;
+            }
+        }
+        pp[0] = m;
+        pp[1] = l;
+    }
+    for (int32_t seq = 0; seq < n_seq; seq++)
+        for (int32_t hq = 0; hq < s->n_head; hq++) {
+            const float *pp = part + ((int64_t)seq * s->n_head + hq) * splits * (hd + 2);
+            float M = -INFINITY, Lsum = 0.0f;
+            for (int32_t sp = 0; sp < splits; sp++) if (pp[sp * (hd + 2)] > M) M = pp[sp * (hd + 2)];
+            float *o = out + ((int64_t)seq * s->n_head + hq) * hd;
+            for (int32_t d = 0; d < hd; d++) o[d] = 0.0f;
+            for (int32_t sp = 0; sp < splits; sp++) {
+                const float *x = pp + sp * (hd + 2);
+                if (x[1] == 0.0f) continue;
+                const float w = expf(x[0] - M);
+                Lsum += w * x[1];
+                for (int32_t d = 0; d < hd; d++) o[d] += w * x[2 + d];
+            }
+            for (int32_t d = 0; d < hd; d++) o[d] = Lsum > 0.0f ? o[d] / Lsum : 0.0f;
+        }
+    free(part);
+    return threads;
+}

@@ -1,0 +1,107 @@
+/*
+ * qsa_oracle.h -- CPU restatement of the q8_0 KV cache + QSA decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP path is
+ * compared against, and (qwfn_oracle_decode_step_f32) the CPU baseline timed
+ * beside it.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it; the product library never does.
+ *
+ * The arithmetic of the reference path lives in ggml (not vendored; pinned at
+ * unslothai/llama.cpp ca1426903fabe9af26cd10c42034cb4bbd2e0e11,
+ * /root/reference README.md:133-136) and cannot be built here, so each function
+ * restates the published algorithm and cites the reference call site it
+ * serves.  All buffers are host memory in the device layout documented in
+ * include/qwfn_qsa.h, so a device buffer copied to the host compares
+ * byte-for-byte.  fp32 throughout, no contraction (-ffp-contract=off), every
+ * fused multiply-add written as fmaf.
+ *
+ * Pinning (what checks each function independently of this restatement):
+ *   fp16 conversion   numpy float16 over special values and random sweeps
+ *   q8_0 quantize     closed-form known answers + numpy rint/round restatement
+ *   layout / gather   exact round trip, brute force over tiny caches
+ *   pooling           numpy sequential float32 chain + constant-block invariant
+ *   block score       exact rational arithmetic (fractions) on small cases
+ *   selection         brute-force sort in Python + special cases
+ *   attention (f64)   numpy float64 textbook softmax + closed-form cases
+ * No function is unpinned.
+ */
+#ifndef QWFN_QSA_ORACLE_H
+#define QWFN_QSA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/qwfn_qsa.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp32 <-> fp16, IEEE binary16, round to nearest even, subnormals kept. */
+uint16_t qwfn_oracle_f32_to_f16(float x);
+float    qwfn_oracle_f16_to_f32(uint16_t h);
+void     qwfn_oracle_f32_to_f16_n(const float *x, int64_t n, uint16_t *out);
+
+/* One q8_0 block (32 values): *d = fp16 scale, qs = quants. */
+void qwfn_oracle_quantize_block(const float *x, int32_t variant, uint16_t *d,
+                                int8_t *qs);
+/* n values (a multiple of 32) -> ggml block_q8_0 bytes (34 per block). */
+void qwfn_oracle_quantize_row_ggml(const float *x, int64_t n, int32_t variant,
+                                   uint8_t *out);
+
+/* Byte offsets inside one page (see include/qwfn_qsa.h). */
+size_t  qwfn_oracle_page_bytes(const qwfn_qsa_shape *s);
+int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
+                                 int32_t d);
+int64_t qwfn_oracle_scale_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
+                                 int32_t j);
+
+/* Host-memory cache operations on a qwfn_kv_view whose pointers are host
+ * pointers.  Return 0, or a negative QWFN_E* code on a bad index. */
+int qwfn_oracle_append(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                       const void *k_src, const void *v_src, int32_t src_dtype,
+                       const int32_t *seq_ids, const int32_t *pos, int32_t n_rows);
+/* Dequantized row of head g at position t of sequence seq from pool
+ * (k_pages or v_pages) -> out[head_dim]. */
+int qwfn_oracle_dequant_row(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                            const void *pool, int32_t seq, int32_t t, int32_t g,
+                            float *out);
+int qwfn_oracle_pool_block(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                           int32_t seq, int32_t b);
+
+/* Score of one block for one KV head: q_group = the G query heads of the group
+ * [G][head_dim], p = pooled key [head_dim]. */
+float qwfn_oracle_block_score(const qwfn_qsa_shape *s, const float *q_group,
+                              const float *p);
+/* Kept blocks of one (sequence, KV head) at length seq_len, ascending, given
+ * the scores of all blocks (scores[b] for b < seq_len/block_tokens; entries of
+ * non-eligible blocks are ignored).  Returns the count (<= max_sel) or < 0. */
+int32_t qwfn_oracle_select(const qwfn_qsa_shape *s, const float *scores,
+                           int32_t seq_len, int32_t *sel, int32_t max_sel);
+int32_t qwfn_oracle_max_selected(const qwfn_qsa_shape *s, int32_t max_seq_len);
+/* Scores + selection for every (sequence, KV head): q [n_seq][n_head][hd],
+ * sel [n_seq][n_head_kv][max_sel], n_sel [n_seq][n_head_kv]. */
+int qwfn_oracle_indexer_topk(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                             const float *q, const int32_t *seq_len, int32_t n_seq,
+                             int32_t *sel, int32_t *n_sel, int32_t max_sel);
+/* Reference attention in fp64 over a selection (sel == NULL: dense).
+ * out [n_seq][n_head][hd] as doubles. */
+int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                              const float *q, const int32_t *seq_len, int32_t n_seq,
+                              const int32_t *sel, const int32_t *n_sel,
+                              int32_t max_sel, double *out);
+
+/* CPU baseline: one decode token of the whole path in fp32 (append at
+ * seq_len-1, pool on block completion, scores, selection, attention with the
+ * gathered K/V cast to fp16 as the reference's decode does, online softmax),
+ * OpenMP over blocks and heads.  Returns the thread count used, or < 0. */
+int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
+                                const float *q, const float *k_new,
+                                const float *v_new, const int32_t *seq_len,
+                                int32_t n_seq, float *out, int32_t *sel,
+                                int32_t *n_sel, int32_t max_sel);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

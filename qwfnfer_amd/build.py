@@ -1,0 +1,57 @@
+"""Build libqwfn_qsa.so (gfx950) in-tree with hipcc.
+
+Run as ``python -m qwfnfer_amd.build``; ``__graft_entry__.build()`` calls
+:func:`build`.  The library is written next to this file so it travels with the
+source tree; nothing is installed.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libqwfn_qsa.so")
+SOURCES = ["qsa_kernels.hip", "qsa_abi.hip"]
+ARCH = "gfx950"
+
+# -packed-fp32-ops off: v_pk_{add,mul,fma}_f32 are never emitted.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libqwfn_qsa.so)")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the kernels and the C ABI into ``qwfnfer_amd/libqwfn_qsa.so``."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    if verbose and res.stderr.strip():
+        print(res.stderr, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

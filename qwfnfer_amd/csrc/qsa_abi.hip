@@ -1,0 +1,381 @@
+// qsa_abi.hip -- the extern "C" boundary of libqwfn_qsa.so: host-side
+// validation, workspace layout and kernel dispatch.  No allocation, no
+// synchronisation (except qwfn_qsa_read_status), no exceptions across the ABI.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "qsa_internal.h"
+
+using namespace qwfn_qsa;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return QWFN_OK;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(QWFN_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int check_shape(const qwfn_qsa_shape *s) {
+    if (!s) return fail(QWFN_EINVAL, "shape is NULL");
+    if (s->n_head_kv < 1 || s->n_head < s->n_head_kv || s->n_head % s->n_head_kv)
+        return fail(QWFN_EINVAL, "n_head (%d) must be a positive multiple of n_head_kv (%d)",
+                    s->n_head, s->n_head_kv);
+    if (s->head_dim < 32 || s->head_dim % 32)
+        return fail(QWFN_EINVAL, "head_dim (%d) must be a positive multiple of 32 (q8_0 block)", s->head_dim);
+    if (s->page_tokens < 64 || s->page_tokens % 64)
+        return fail(QWFN_EINVAL, "page_tokens (%d) must be a positive multiple of 64", s->page_tokens);
+    if (s->block_tokens < 1 || s->page_tokens % s->block_tokens)
+        return fail(QWFN_EINVAL, "block_tokens (%d) must divide page_tokens (%d)", s->block_tokens,
+                    s->page_tokens);
+    if (s->sink_blocks < 0) return fail(QWFN_EINVAL, "sink_blocks (%d) < 0", s->sink_blocks);
+    if (s->local_tokens < 1)
+        return fail(QWFN_EINVAL, "local_tokens (%d) < 1: the token being decoded must stay visible",
+                    s->local_tokens);
+    if (s->quant_variant != QWFN_Q8_X86_RNE && s->quant_variant != QWFN_Q8_REF_ROUNDF)
+        return fail(QWFN_EINVAL, "quant_variant %d unknown", s->quant_variant);
+    if ((s->relu_per_head | s->shared_selection) & ~1)
+        return fail(QWFN_EINVAL, "relu_per_head / shared_selection are 0 or 1");
+    if (s->shared_selection)
+        return fail(QWFN_ENOTSUP, "shared_selection (one selection for all KV heads) has no kernel in this build");
+    const int G = s->n_head / s->n_head_kv;
+    if (!kernels_for(s->head_dim, G))
+        return fail(QWFN_ENOTSUP, "no kernel instantiation for head_dim %d, group %d", s->head_dim, G);
+    return QWFN_OK;
+}
+
+int check_view(const qwfn_qsa_shape *s, const qwfn_kv_view *v) {
+    if (!v) return fail(QWFN_EINVAL, "view is NULL");
+    if (!v->k_pages || !v->v_pages || !v->pooled || !v->page_table)
+        return fail(QWFN_EINVAL, "view has a NULL k_pages / v_pages / pooled / page_table");
+    if (!aligned(v->k_pages, 16) || !aligned(v->v_pages, 16) || !aligned(v->pooled, 16))
+        return fail(QWFN_EINVAL, "k_pages, v_pages and pooled must be 16-byte aligned");
+    if (v->n_seq < 1 || v->pages_per_seq < 1 || v->n_phys_pages < 1)
+        return fail(QWFN_EINVAL, "view n_seq / pages_per_seq / n_phys_pages must be >= 1");
+    if ((int64_t)v->pages_per_seq * s->page_tokens > INT32_MAX / 2)
+        return fail(QWFN_ERANGE, "pages_per_seq * page_tokens overflows the position range");
+    return QWFN_OK;
+}
+
+// view_required: the call operates on a cache, so a NULL view is an error.
+int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_required = true) {
+    int rc = check_shape(s);
+    if (rc) return rc;
+    if (view_required && !v) return fail(QWFN_EINVAL, "view is NULL");
+    if (v && (rc = check_view(s, v))) return rc;
+    g->H = s->n_head; g->Hkv = s->n_head_kv; g->hd = s->head_dim; g->G = s->n_head / s->n_head_kv;
+    g->bt = s->block_tokens; g->pt = s->page_tokens;
+    g->topk = s->top_k_blocks > 0 ? s->top_k_blocks : 0;
+    g->sink = s->sink_blocks; g->local = s->local_tokens;
+    g->relu = s->relu_per_head; g->variant = s->quant_variant;
+    g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * s->head_dim;
+    g->page_bytes = g->qbytes + (int64_t)s->n_head_kv * s->page_tokens * (s->head_dim / 32) * 2;
+    g->inv_bt = 1.0f / (float)s->block_tokens;
+    g->scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)s->head_dim));
+    if (v) {
+        g->pps = v->pages_per_seq; g->n_phys = v->n_phys_pages; g->n_seq_view = v->n_seq;
+        g->bps = (int32_t)((int64_t)v->pages_per_seq * s->page_tokens / s->block_tokens);
+    } else {
+        g->pps = g->n_phys = g->n_seq_view = g->bps = 0;
+    }
+    return QWFN_OK;
+}
+
+int32_t max_selected(const qwfn_qsa_shape *s, int32_t max_seq_len) {
+    const int32_t bt = s->block_tokens, all = (max_seq_len + bt - 1) / bt;
+    if (s->top_k_blocks <= 0) return all;
+    const int32_t win = (s->local_tokens + bt - 2) / bt + 1;
+    const int64_t cap = (int64_t)s->top_k_blocks + s->sink_blocks + win;
+    return cap < all ? (int32_t)cap : all;
+}
+
+// Common checks of the per-call sequence arguments.
+int check_batch(const qwfn_qsa_shape *s, const qwfn_kv_view *v, int32_t n_seq, int32_t max_seq_len) {
+    if (n_seq < 1 || n_seq > v->n_seq)
+        return fail(QWFN_EINVAL, "n_seq %d outside [1, view n_seq %d]", n_seq, v->n_seq);
+    if ((int64_t)n_seq * s->n_head_kv > kMaxCounters)
+        return fail(QWFN_ERANGE, "n_seq * n_head_kv = %lld exceeds %d per call",
+                    (long long)n_seq * s->n_head_kv, kMaxCounters);
+    if (max_seq_len < 1) return fail(QWFN_EINVAL, "max_seq_len %d < 1", max_seq_len);
+    if ((int64_t)max_seq_len > (int64_t)v->pages_per_seq * s->page_tokens)
+        return fail(QWFN_ERANGE, "context exhausted: max_seq_len %d > capacity %lld", max_seq_len,
+                    (long long)v->pages_per_seq * s->page_tokens);
+    return QWFN_OK;
+}
+
+int bind_ws(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, void *ws,
+            size_t ws_bytes, Ws *out) {
+    const WsLayout l = ws_layout(g, n_seq, max_seq_len, max_sel);
+    if (!ws) return fail(QWFN_EINVAL, "workspace is NULL");
+    if (!aligned(ws, 256)) return fail(QWFN_EINVAL, "workspace must be 256-byte aligned");
+    if (ws_bytes < l.total)
+        return fail(QWFN_ERANGE, "workspace of %zu bytes < %zu needed for n_seq %d, max_seq_len %d",
+                    ws_bytes, l.total, n_seq, max_seq_len);
+    *out = ws_bind(ws, l);
+    return QWFN_OK;
+}
+
+}  // namespace
+
+namespace qwfn_qsa {
+
+WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
+    WsLayout l;
+    l.nb_cap = max_seq_len / g.bt > 0 ? max_seq_len / g.bt : 1;
+    l.max_sel = max_sel;
+    l.n_tiles = (int32_t)(((int64_t)max_sel * g.bt + 63) / 64);
+    const size_t pairs = (size_t)n_seq * g.Hkv;
+    size_t off = align256(2 * (size_t)kMaxCounters * sizeof(int32_t));
+    auto take = [&](size_t bytes) { const size_t o = off; off = align256(off + bytes); return o; };
+    l.sel = take(pairs * max_sel * sizeof(int32_t));
+    l.nsel = take(pairs * sizeof(int32_t));
+    l.scores = take(pairs * l.nb_cap * sizeof(float));
+    l.part_o = take(pairs * l.n_tiles * g.G * g.hd * sizeof(float));
+    l.part_ml = take(pairs * l.n_tiles * g.G * 2 * sizeof(float));
+    l.total = off;
+    return l;
+}
+
+Ws ws_bind(void *base, const WsLayout &l) {
+    uint8_t *b = (uint8_t *)base;
+    Ws w;
+    w.cnt_idx = (int32_t *)b;
+    w.cnt_attn = (int32_t *)b + kMaxCounters;
+    w.sel = (int32_t *)(b + l.sel);
+    w.nsel = (int32_t *)(b + l.nsel);
+    w.scores = (float *)(b + l.scores);
+    w.part_o = (float *)(b + l.part_o);
+    w.part_ml = (float *)(b + l.part_ml);
+    w.nb_cap = l.nb_cap;
+    w.max_sel = l.max_sel;
+    w.n_tiles = l.n_tiles;
+    return w;
+}
+
+}  // namespace qwfn_qsa
+
+extern "C" {
+
+int qwfn_qsa_abi_version(void) { return QWFN_QSA_ABI_VERSION; }
+
+const char *qwfn_qsa_last_error(void) { return g_err.c_str(); }
+
+int qwfn_qsa_check_shape(const qwfn_qsa_shape *shape) {
+    const int rc = check_shape(shape);
+    return rc ? rc : ok();
+}
+
+int qwfn_qsa_page_bytes(const qwfn_qsa_shape *shape, size_t *bytes) {
+    Geo g;
+    int rc = make_geo(shape, nullptr, &g, false);
+    if (rc) return rc;
+    if (!bytes) return fail(QWFN_EINVAL, "bytes is NULL");
+    *bytes = (size_t)g.page_bytes;
+    return ok();
+}
+
+int qwfn_qsa_pooled_bytes(const qwfn_qsa_shape *shape, int32_t n_seq, int32_t pages_per_seq,
+                          size_t *bytes) {
+    int rc = check_shape(shape);
+    if (rc) return rc;
+    if (!bytes || n_seq < 1 || pages_per_seq < 1)
+        return fail(QWFN_EINVAL, "pooled_bytes: bytes NULL or n_seq / pages_per_seq < 1");
+    const size_t bps = (size_t)pages_per_seq * shape->page_tokens / shape->block_tokens;
+    *bytes = (size_t)n_seq * shape->n_head_kv * bps * shape->head_dim * sizeof(float);
+    return ok();
+}
+
+int qwfn_qsa_max_selected(const qwfn_qsa_shape *shape, int32_t max_seq_len, int32_t *max_sel) {
+    int rc = check_shape(shape);
+    if (rc) return rc;
+    if (!max_sel || max_seq_len < 1) return fail(QWFN_EINVAL, "max_selected: max_sel NULL or max_seq_len < 1");
+    *max_sel = max_selected(shape, max_seq_len);
+    return ok();
+}
+
+int qwfn_qsa_workspace_bytes(const qwfn_qsa_shape *shape, int32_t n_seq, int32_t max_seq_len,
+                             size_t *bytes) {
+    Geo g;
+    int rc = make_geo(shape, nullptr, &g, false);
+    if (rc) return rc;
+    if (!bytes || n_seq < 1 || max_seq_len < 1)
+        return fail(QWFN_EINVAL, "workspace_bytes: bytes NULL or n_seq / max_seq_len < 1");
+    if ((int64_t)n_seq * shape->n_head_kv > kMaxCounters)
+        return fail(QWFN_ERANGE, "n_seq * n_head_kv exceeds %d", kMaxCounters);
+    *bytes = ws_layout(g, n_seq, max_seq_len, max_selected(shape, max_seq_len)).total;
+    return ok();
+}
+
+int qwfn_qsa_workspace_init(void *ws, size_t ws_bytes, void *stream) {
+    if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "workspace NULL or not 256-byte aligned");
+    const hipError_t e = launch_fill_zero(ws, ws_bytes, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "workspace_init");
+}
+
+int qwfn_qsa_read_status(const qwfn_kv_view *view, int32_t *status, void *stream) {
+    if (!view || !status) return fail(QWFN_EINVAL, "read_status: NULL view or status");
+    if (!view->status) { *status = 0; return ok(); }
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipMemcpyAsync(status, view->status, sizeof(int32_t), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = launch_fill_zero(view->status, sizeof(int32_t), st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? ok() : hip_fail(e, "read_status");
+}
+
+int qwfn_kv_append_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const void *k_src,
+                        const void *v_src, int32_t src_dtype, const int32_t *seq_ids,
+                        const int32_t *pos, int32_t n_rows, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16)
+        return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
+    if (!k_src || !v_src || !pos) return fail(QWFN_EINVAL, "append: NULL k_src / v_src / pos");
+    const size_t al = src_dtype == QWFN_SRC_F32 ? 16 : 8;
+    if (!aligned(k_src, al) || !aligned(v_src, al))
+        return fail(QWFN_EINVAL, "append: source rows must be %zu-byte aligned", al);
+    if (n_rows < 1) return fail(QWFN_EINVAL, "append: n_rows %d < 1", n_rows);
+    const hipError_t e = launch_append(g, *view, k_src, v_src, src_dtype == QWFN_SRC_F16, seq_ids, pos,
+                                       n_rows, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "append");
+}
+
+int qwfn_pool_update(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const int32_t *seq_ids,
+                     const int32_t *block_ids, int32_t n_blocks, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (!block_ids) return fail(QWFN_EINVAL, "pool_update: block_ids is NULL");
+    if (n_blocks < 1) return fail(QWFN_EINVAL, "pool_update: n_blocks %d < 1", n_blocks);
+    if (g.hd > 256) return fail(QWFN_ENOTSUP, "pool_update: head_dim > 256");
+    const hipError_t e = launch_pool(g, *view, seq_ids, block_ids, n_blocks, 0, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "pool_update");
+}
+
+int qwfn_pool_rebuild(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, int32_t seq,
+                      int32_t n_whole, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (seq < 0 || seq >= view->n_seq) return fail(QWFN_EINVAL, "pool_rebuild: seq %d outside the view", seq);
+    if (n_whole < 0) return fail(QWFN_EINVAL, "pool_rebuild: n_whole %d < 0", n_whole);
+    if (n_whole > g.bps) return fail(QWFN_ERANGE, "pool_rebuild: n_whole %d > %d blocks", n_whole, g.bps);
+    if (n_whole == 0) return ok();
+    const hipError_t e = launch_pool(g, *view, nullptr, nullptr, n_whole, seq, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "pool_rebuild");
+}
+
+int qwfn_indexer_topk(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                      const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, int32_t *sel,
+                      int32_t *n_sel, int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (!q || !aligned(q, 16) || !seq_len || !sel || !n_sel)
+        return fail(QWFN_EINVAL, "indexer_topk: NULL q / seq_len / sel / n_sel or q not 16-byte aligned");
+    const int32_t need = max_selected(shape, max_seq_len);
+    if (max_sel < need) return fail(QWFN_ERANGE, "indexer_topk: max_sel %d < %d", max_sel, need);
+    Ws w;
+    if ((rc = bind_ws(g, n_seq, max_seq_len, need, ws, ws_bytes, &w))) return rc;
+    const FusedAppend fa{nullptr, nullptr, 0, 0};
+    const hipError_t e = launch_indexer(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, w,
+                                        fa, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "indexer_topk");
+}
+
+int qwfn_gather_dequant(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                        const int32_t *seq_len, int32_t n_seq, const int32_t *sel,
+                        const int32_t *n_sel, int32_t max_sel, float *k_out, float *v_out,
+                        int32_t *cells, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (n_seq < 1 || n_seq > view->n_seq) return fail(QWFN_EINVAL, "gather: n_seq %d outside the view", n_seq);
+    if (!seq_len || !k_out || !v_out || !cells || (sel && !n_sel) || max_sel < 1)
+        return fail(QWFN_EINVAL, "gather: NULL argument or max_sel < 1");
+    if (g.hd > 256) return fail(QWFN_ENOTSUP, "gather: head_dim > 256");
+    const hipError_t e = launch_gather(g, *view, seq_len, n_seq, sel, n_sel, max_sel, k_out, v_out, cells,
+                                       (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "gather");
+}
+
+int qwfn_sparse_decode_attn(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                            const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                            const int32_t *sel, const int32_t *n_sel, int32_t max_sel, float *out,
+                            void *ws, size_t ws_bytes, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (!q || !aligned(q, 16) || !seq_len || !out || (sel && !n_sel))
+        return fail(QWFN_EINVAL, "decode_attn: NULL q / seq_len / out (or sel without n_sel), or q misaligned");
+    int32_t msel;
+    if (sel) {
+        if (max_sel < 1) return fail(QWFN_EINVAL, "decode_attn: max_sel %d < 1", max_sel);
+        msel = max_sel;
+    } else {
+        msel = (max_seq_len + g.bt - 1) / g.bt;       // dense: every block below seq_len
+    }
+    Ws w;
+    if ((rc = bind_ws(g, n_seq, max_seq_len, msel, ws, ws_bytes, &w))) return rc;
+    const hipError_t e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, msel, out,
+                                          w, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "decode_attn");
+}
+
+int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                            const void *k_new, const void *v_new, int32_t src_dtype,
+                            const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, float *out,
+                            int32_t *sel_out, int32_t *n_sel_out, void *ws, size_t ws_bytes,
+                            void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16)
+        return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
+    const size_t al = src_dtype == QWFN_SRC_F32 ? 16 : 8;
+    if (!q || !aligned(q, 16) || !k_new || !v_new || !aligned(k_new, al) || !aligned(v_new, al) ||
+        !seq_len || !out)
+        return fail(QWFN_EINVAL, "decode: NULL or misaligned q / k_new / v_new / seq_len / out");
+    if ((sel_out == nullptr) != (n_sel_out == nullptr))
+        return fail(QWFN_EINVAL, "decode: pass both sel_out and n_sel_out or neither");
+    const int32_t msel = max_selected(shape, max_seq_len);
+    Ws w;
+    if ((rc = bind_ws(g, n_seq, max_seq_len, msel, ws, ws_bytes, &w))) return rc;
+    int32_t *sel = sel_out ? sel_out : w.sel;
+    int32_t *nsel = n_sel_out ? n_sel_out : w.nsel;
+    const FusedAppend fa{k_new, v_new, src_dtype == QWFN_SRC_F16, 1};
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = launch_indexer(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, w, fa, st);
+    if (e != hipSuccess) return hip_fail(e, "decode: indexer");
+    e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st);
+    return e == hipSuccess ? ok() : hip_fail(e, "decode: attention");
+}
+
+}  // extern "C"

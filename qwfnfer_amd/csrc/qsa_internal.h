@@ -1,0 +1,77 @@
+// qsa_internal.h -- geometry, workspace map and launcher declarations shared by
+// the gfx950 kernels (qsa_kernels.hip) and the C ABI (qsa_abi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/qwfn_qsa.h"
+
+namespace qwfn_qsa {
+
+// Everything a kernel needs to know about the shape and the view, flattened
+// into one by-value kernel argument.
+struct Geo {
+    int32_t H, Hkv, hd, G;           // query heads, KV heads, head dim, group
+    int32_t bt, pt;                  // block tokens, page tokens
+    int32_t topk, sink, local;       // selection
+    int32_t relu, variant;           // indexer relu, q8_0 rounding
+    int32_t pps, n_phys, n_seq_view; // pages per sequence, pool pages, view seqs
+    int32_t bps;                     // pooled blocks per sequence
+    int64_t page_bytes, qbytes;      // page size, quant bytes per page
+    float inv_bt;                    // 1.0f / block_tokens (host-rounded)
+    float scale_log2;                // log2(e) / sqrt(head_dim)
+};
+
+// Device pointers into a caller workspace (see qwfn_qsa_workspace_bytes).
+// The counter region sits at a fixed offset with a fixed capacity so every
+// call layout agrees on it; all other regions are per-call scratch.
+constexpr int32_t kMaxCounters = 4096;   // (sequence, KV head) pairs per call
+struct Ws {
+    int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
+    int32_t *cnt_attn;   // [kMaxCounters] attention completion counters
+    int32_t *sel;        // [n_seq][Hkv][max_sel]  selection of the fused step
+    int32_t *nsel;       // [n_seq][Hkv]
+    float   *scores;     // [n_seq][Hkv][nb_cap]
+    float   *part_o;     // [n_seq][Hkv][n_tiles][G][hd]
+    float   *part_ml;    // [n_seq][Hkv][n_tiles][G][2]
+    int32_t  nb_cap, max_sel, n_tiles;
+};
+
+struct WsLayout {
+    size_t sel, nsel, scores, part_o, part_ml, total;
+    int32_t nb_cap, max_sel, n_tiles;
+};
+WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel);
+Ws ws_bind(void *base, const WsLayout &l);
+
+// Fused-append arguments of the decode step (enabled == 0: plain indexer).
+struct FusedAppend {
+    const void *k_new, *v_new;       // [n_seq][Hkv][hd]
+    int32_t src_f16, enabled;
+};
+
+bool kernels_for(int32_t hd, int32_t G);   // an instantiation exists
+
+hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
+hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
+                         int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
+                         int32_t n_rows, hipStream_t st);
+hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
+                       const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
+                       hipStream_t st);
+hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
+                          const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                          int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
+                          const FusedAppend &fa, hipStream_t st);
+hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
+                            const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                            const int32_t *sel, const int32_t *nsel, int32_t max_sel,
+                            float *out, const Ws &ws, hipStream_t st);
+hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len,
+                         int32_t n_seq, const int32_t *sel, const int32_t *nsel,
+                         int32_t max_sel, float *k_out, float *v_out, int32_t *cells,
+                         hipStream_t st);
+
+}  // namespace qwfn_qsa

@@ -1,0 +1,357 @@
+"""Host-side mirror of the reference's KV-cache / QSA decode interface.
+
+The reference engine owns the per-layer caches in ``qwfn::state``
+(/root/reference src/qwfn_state.cpp:18-96) and the pooled block keys in
+``engine`` (src/qwfn_engine.cpp:382-435); ``graph_builder::sparse_attn_decode``
+(src/qwfn_graph.cpp:450-546) appends the decode token, pools its block, scores,
+selects and attends.  This module keeps those roles -- ``KvState`` owns the
+device memory of every attention layer, the functions below issue the same
+steps -- but every step is one call into the C ABI of libqwfn_qsa.so
+(include/qwfn_qsa.h).  torch is used for device memory and streams only.
+
+Every function takes device tensors and enqueues on the current HIP stream
+(or ``stream=``); nothing here synchronises except :func:`read_status`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import KvView, QsaShape, call
+
+__all__ = [
+    "QsaConfig", "KvCache", "KvState", "Workspace",
+    "append_q8_0", "pool_update", "pool_rebuild", "indexer_topk", "gather_dequant",
+    "sparse_decode_attn", "sparse_attn_decode", "read_status",
+]
+
+
+@dataclass(frozen=True)
+class QsaConfig:
+    """Shape of the sparse-attention layer (the reference's hparams subset,
+    src/qwfn_hparams.h:22-36, generalised: BASELINE pools K itself in 64-token
+    blocks and keeps top-64 blocks + block 0 + the last 512 tokens)."""
+    n_head: int = 16
+    n_head_kv: int = 2
+    head_dim: int = 128
+    block_tokens: int = 64
+    page_tokens: int = 256
+    top_k_blocks: int = 64
+    sink_blocks: int = 1
+    local_tokens: int = 512
+    relu_per_head: int = 0
+    shared_selection: int = 0
+    quant_variant: int = _lib.Q8_X86_RNE
+
+    @property
+    def group(self) -> int:
+        return self.n_head // self.n_head_kv
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_head_kv * self.head_dim
+
+    def shape(self) -> QsaShape:
+        return QsaShape(self.n_head, self.n_head_kv, self.head_dim, self.block_tokens,
+                        self.page_tokens, self.top_k_blocks, self.sink_blocks,
+                        self.local_tokens, self.relu_per_head, self.shared_selection,
+                        self.quant_variant)
+
+    def check(self) -> None:
+        s = self.shape()
+        call("qwfn_qsa_check_shape", C.byref(s))
+
+    def page_bytes(self) -> int:
+        out = C.c_size_t()
+        s = self.shape()
+        call("qwfn_qsa_page_bytes", C.byref(s), C.byref(out))
+        return out.value
+
+    def max_selected(self, max_seq_len: int) -> int:
+        out = C.c_int32()
+        s = self.shape()
+        call("qwfn_qsa_max_selected", C.byref(s), max_seq_len, C.byref(out))
+        return out.value
+
+    def workspace_bytes(self, n_seq: int, max_seq_len: int) -> int:
+        out = C.c_size_t()
+        s = self.shape()
+        call("qwfn_qsa_workspace_bytes", C.byref(s), n_seq, max_seq_len, C.byref(out))
+        return out.value
+
+    def dense(self) -> "QsaConfig":
+        """The same layer with the selection switched off (the reference's
+        ``qsa == nullptr`` dense path, src/qwfn_graph.cpp:85-89)."""
+        return QsaConfig(**{**self.__dict__, "top_k_blocks": 0})
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, numel: Optional[int] = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name} has {t.numel()} elements, expected {numel}")
+
+
+@dataclass
+class KvCache:
+    """One attention layer's paged q8_0 K/V pools and pooled block keys.
+
+    ``page_table[s, p]`` is the physical page of logical page p of sequence s;
+    the reference's contiguous token-major cache is one sequence with the
+    identity table (src/qwfn_state.cpp:52-54)."""
+    cfg: QsaConfig
+    k_pages: torch.Tensor
+    v_pages: torch.Tensor
+    pooled: torch.Tensor
+    page_table: torch.Tensor
+    status: torch.Tensor
+    _view: KvView = field(default=None, repr=False)
+
+    @classmethod
+    def allocate(cls, cfg: QsaConfig, n_seq: int, pages_per_seq: int,
+                 page_table: Optional[torch.Tensor] = None, n_phys_pages: Optional[int] = None,
+                 device="cuda") -> "KvCache":
+        cfg.check()
+        if page_table is None:
+            page_table = torch.arange(n_seq * pages_per_seq, dtype=torch.int32).view(n_seq, pages_per_seq)
+        page_table = page_table.to(device=device, dtype=torch.int32).contiguous()
+        if tuple(page_table.shape) != (n_seq, pages_per_seq):
+            raise ValueError(f"page_table shape {tuple(page_table.shape)} != ({n_seq}, {pages_per_seq})")
+        if n_phys_pages is None:
+            n_phys_pages = n_seq * pages_per_seq
+        pb = cfg.page_bytes()
+        bps = pages_per_seq * cfg.page_tokens // cfg.block_tokens
+        # The reference leaves its caches unzeroed (src/qwfn_state.cpp:89); zeros
+        # here only make never-written rows deterministic.
+        k = torch.zeros(n_phys_pages * pb, dtype=torch.uint8, device=device)
+        v = torch.zeros(n_phys_pages * pb, dtype=torch.uint8, device=device)
+        pooled = torch.zeros((n_seq, cfg.n_head_kv, bps, cfg.head_dim), dtype=torch.float32, device=device)
+        status = torch.zeros(1, dtype=torch.int32, device=device)
+        return cls(cfg, k, v, pooled, page_table, status)
+
+    @property
+    def n_seq(self) -> int:
+        return self.page_table.shape[0]
+
+    @property
+    def pages_per_seq(self) -> int:
+        return self.page_table.shape[1]
+
+    @property
+    def capacity(self) -> int:
+        return self.pages_per_seq * self.cfg.page_tokens
+
+    @property
+    def n_phys_pages(self) -> int:
+        return self.k_pages.numel() // self.cfg.page_bytes()
+
+    def view(self) -> KvView:
+        if self._view is None:
+            self._view = KvView(self.k_pages.data_ptr(), self.v_pages.data_ptr(),
+                                self.pooled.data_ptr(), self.page_table.data_ptr(),
+                                self.status.data_ptr(), self.n_seq, self.pages_per_seq,
+                                self.n_phys_pages)
+        return self._view
+
+
+class KvState:
+    """Per-sequence-batch state of every sparse-attention layer: the
+    reference's ``state`` (K/V caches, src/qwfn_state.cpp:18-96) plus the
+    engine's pooled-key caches (src/qwfn_engine.cpp:382-435)."""
+
+    def __init__(self, cfg: QsaConfig, n_layer: int, n_ctx: int, n_seq: int = 1,
+                 page_table: Optional[torch.Tensor] = None, device="cuda"):
+        if n_ctx % cfg.page_tokens:
+            raise ValueError(f"n_ctx {n_ctx} must be a multiple of page_tokens {cfg.page_tokens}")
+        self.cfg = cfg
+        self.n_ctx = n_ctx
+        pps = n_ctx // cfg.page_tokens
+        self.layers: List[KvCache] = [
+            KvCache.allocate(cfg, n_seq, pps, page_table=page_table, device=device)
+            for _ in range(n_layer)]
+
+    def k_cache(self, il: int) -> torch.Tensor:
+        return self.layers[il].k_pages
+
+    def v_cache(self, il: int) -> torch.Tensor:
+        return self.layers[il].v_pages
+
+    def pool_cache(self, il: int) -> torch.Tensor:
+        return self.layers[il].pooled
+
+    def reset(self) -> None:
+        """The reference's reset leaves the caches alone and invalidates the
+        pooled keys (src/qwfn_engine.cpp:716-725); rows are rewritten as the
+        positions are decoded again, so nothing needs clearing here."""
+        for c in self.layers:
+            c.status.zero_()
+
+    def bytes(self) -> int:
+        return sum(c.k_pages.numel() + c.v_pages.numel() + c.pooled.numel() * 4 for c in self.layers)
+
+
+class Workspace:
+    """Caller-owned scratch of the indexer and the attention merge, sized for
+    (n_seq, max_seq_len) and zero-initialised once (a fill kernel)."""
+
+    def __init__(self, cfg: QsaConfig, n_seq: int, max_seq_len: int, device="cuda", stream=None):
+        self.nbytes = cfg.workspace_bytes(n_seq, max_seq_len)
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
+        call("qwfn_qsa_workspace_init", self.buf.data_ptr(), self.nbytes, _stream(stream))
+
+    def ptr(self) -> int:
+        return self.buf.data_ptr()
+
+
+def append_q8_0(cache: KvCache, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
+                seq_ids: Optional[torch.Tensor] = None, stream=None) -> None:
+    """ggml_set_rows / ggml_cpy into the q8_0 cache (src/qwfn_graph.cpp:520-528,
+    349-360): rows k, v [n_rows, n_head_kv, head_dim] (f32 or f16) written at
+    positions ``pos`` (int32, device) of ``seq_ids`` (default 0)."""
+    cfg = cache.cfg
+    if k.dtype not in (torch.float32, torch.float16) or v.dtype != k.dtype:
+        raise TypeError("k and v must both be float32 or both float16")
+    n_rows = pos.numel()
+    _need(k, "k", k.dtype, n_rows * cfg.kv_dim)
+    _need(v, "v", k.dtype, n_rows * cfg.kv_dim)
+    _need(pos, "pos", torch.int32)
+    if seq_ids is not None:
+        _need(seq_ids, "seq_ids", torch.int32, n_rows)
+    s = cfg.shape()
+    call("qwfn_kv_append_q8_0", C.byref(s), C.byref(cache.view()), k.data_ptr(), v.data_ptr(),
+         _lib.SRC_F16 if k.dtype == torch.float16 else _lib.SRC_F32, _ptr(seq_ids), pos.data_ptr(),
+         n_rows, _stream(stream))
+
+
+def pool_update(cache: KvCache, block_ids: torch.Tensor, seq_ids: Optional[torch.Tensor] = None,
+                stream=None) -> None:
+    """Recompute the pooled keys of the listed blocks (src/qwfn_graph.cpp:471-476)."""
+    _need(block_ids, "block_ids", torch.int32)
+    if seq_ids is not None:
+        _need(seq_ids, "seq_ids", torch.int32, block_ids.numel())
+    s = cache.cfg.shape()
+    call("qwfn_pool_update", C.byref(s), C.byref(cache.view()), _ptr(seq_ids), block_ids.data_ptr(),
+         block_ids.numel(), _stream(stream))
+
+
+def pool_rebuild(cache: KvCache, seq: int, n_whole: int, stream=None) -> None:
+    """qsa_pool_rebuild after a prefill: pool blocks [0, n_whole) of ``seq``
+    (src/qwfn_graph.cpp:431-448, src/qwfn_engine.cpp:761-798)."""
+    s = cache.cfg.shape()
+    call("qwfn_pool_rebuild", C.byref(s), C.byref(cache.view()), seq, n_whole, _stream(stream))
+
+
+def indexer_topk(cache: KvCache, q: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int,
+                 ws: Workspace, sel: Optional[torch.Tensor] = None,
+                 n_sel: Optional[torch.Tensor] = None, stream=None):
+    """Scores + top-k of one decode token per sequence (src/qwfn_graph.cpp:477-495).
+    Returns (sel [n_seq, n_head_kv, max_sel] ascending block ids, n_sel [n_seq, n_head_kv])."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    _need(q, "q", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    max_sel = cfg.max_selected(max_seq_len)
+    if sel is None:
+        sel = torch.empty((n_seq, cfg.n_head_kv, max_sel), dtype=torch.int32, device=q.device)
+    if n_sel is None:
+        n_sel = torch.empty((n_seq, cfg.n_head_kv), dtype=torch.int32, device=q.device)
+    _need(sel, "sel", torch.int32)
+    _need(n_sel, "n_sel", torch.int32, n_seq * cfg.n_head_kv)
+    s = cfg.shape()
+    call("qwfn_indexer_topk", C.byref(s), C.byref(cache.view()), q.data_ptr(), seq_len.data_ptr(), n_seq,
+         max_seq_len, sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], ws.ptr(), ws.nbytes, _stream(stream))
+    return sel, n_sel
+
+
+def gather_dequant(cache: KvCache, seq_len: torch.Tensor, sel: Optional[torch.Tensor],
+                   n_sel: Optional[torch.Tensor], max_sel: int, stream=None):
+    """Dequantized cells of a selection (src/qwfn_graph.cpp:494-495, 530-537):
+    (k [n_seq, Hkv, max_sel*bt, hd], v, cells [n_seq, Hkv, max_sel*bt])."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    nc = max_sel * cfg.block_tokens
+    dev = seq_len.device
+    k = torch.empty((n_seq, cfg.n_head_kv, nc, cfg.head_dim), dtype=torch.float32, device=dev)
+    v = torch.empty_like(k)
+    cells = torch.empty((n_seq, cfg.n_head_kv, nc), dtype=torch.int32, device=dev)
+    s = cfg.shape()
+    call("qwfn_gather_dequant", C.byref(s), C.byref(cache.view()), seq_len.data_ptr(), n_seq, _ptr(sel),
+         _ptr(n_sel), max_sel, k.data_ptr(), v.data_ptr(), cells.data_ptr(), _stream(stream))
+    return k, v, cells
+
+
+def sparse_decode_attn(cache: KvCache, q: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int,
+                       ws: Workspace, sel: Optional[torch.Tensor] = None,
+                       n_sel: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                       stream=None) -> torch.Tensor:
+    """Masked GQA softmax attention over a selection (sel None: dense), the
+    reference's cell mask + ggml_flash_attn_ext (src/qwfn_graph.cpp:497-542)."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    _need(q, "q", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    if out is None:
+        out = torch.empty((n_seq, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    max_sel = sel.shape[-1] if sel is not None else 0
+    s = cfg.shape()
+    call("qwfn_sparse_decode_attn", C.byref(s), C.byref(cache.view()), q.data_ptr(), seq_len.data_ptr(),
+         n_seq, max_seq_len, _ptr(sel), _ptr(n_sel), max_sel, out.data_ptr(), ws.ptr(), ws.nbytes,
+         _stream(stream))
+    return out
+
+
+def sparse_attn_decode(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                       seq_len: torch.Tensor, max_seq_len: int, ws: Workspace,
+                       out: Optional[torch.Tensor] = None, sel: Optional[torch.Tensor] = None,
+                       n_sel: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """One decode token of graph_builder::sparse_attn_decode
+    (src/qwfn_graph.cpp:450-546) from the projections on: append k_new/v_new at
+    seq_len-1, pool the block it completes, select, attend.  ``sel``/``n_sel``
+    (optional, both or neither) receive the selection."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    _need(q, "q", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype:
+        raise TypeError("k_new and v_new must both be float32 or both float16")
+    _need(k_new, "k_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(v_new, "v_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    if out is None:
+        out = torch.empty((n_seq, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
+    if (sel is None) != (n_sel is None):
+        raise ValueError("pass both sel and n_sel or neither")
+    s = cfg.shape()
+    call("qwfn_sparse_attn_decode", C.byref(s), C.byref(cache.view()), q.data_ptr(), k_new.data_ptr(),
+         v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,
+         seq_len.data_ptr(), n_seq, max_seq_len, out.data_ptr(), _ptr(sel), _ptr(n_sel), ws.ptr(),
+         ws.nbytes, _stream(stream))
+    return out
+
+
+def read_status(cache: KvCache, stream=None) -> int:
+    """Fetch and clear the device status bits of a cache (synchronises)."""
+    out = C.c_int32()
+    call("qwfn_qsa_read_status", C.byref(cache.view()), C.byref(out), _stream(stream))
+    return out.value

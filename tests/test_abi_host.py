@@ -1,0 +1,113 @@
+"""libqwfn_qsa.so loads, exports every function include/qwfn_qsa.h declares,
+and validates shapes/arguments on the host (no GPU call is reached)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from qwfnfer_amd import _lib
+from qwfnfer_amd.qsa import QsaConfig
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    txt = open(os.path.join(ROOT, "include", "qwfn_qsa.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return set(re.findall(r"\b(qwfn_[a-z0-9_]+)\s*\(", txt))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == set(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.qwfn_qsa_abi_version() == 1
+
+
+def _code(name, *args):
+    return getattr(_lib.load(), name)(*args)
+
+
+def test_shape_validation():
+    ok = QsaConfig()
+    s = ok.shape()
+    assert _code("qwfn_qsa_check_shape", C.byref(s)) == 0
+    bad = [
+        dict(n_head=15), dict(head_dim=100), dict(page_tokens=100), dict(block_tokens=48),
+        dict(local_tokens=0), dict(sink_blocks=-1), dict(quant_variant=3), dict(relu_per_head=2),
+    ]
+    for kw in bad:
+        s = QsaConfig(**{**ok.__dict__, **kw}).shape()
+        assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_EINVAL, kw
+        assert _lib.load().qwfn_qsa_last_error()
+    s = QsaConfig(**{**ok.__dict__, "shared_selection": 1}).shape()
+    assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_ENOTSUP
+    s = QsaConfig(**{**ok.__dict__, "n_head": 6, "n_head_kv": 2, "head_dim": 96}).shape()
+    assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_ENOTSUP
+
+
+def test_sizes():
+    cfg = QsaConfig()
+    assert cfg.page_bytes() == 2 * 256 * (128 + 8) == 69632
+    assert cfg.max_selected(32768) == 64 + 1 + 9
+    assert cfg.max_selected(4096) == 64
+    assert cfg.dense().max_selected(4096) == 64
+    assert cfg.workspace_bytes(8, 262144) > 0
+    out = C.c_size_t()
+    s = cfg.shape()
+    assert _code("qwfn_qsa_pooled_bytes", C.byref(s), 1, 640, C.byref(out)) == 0
+    assert out.value == 2560 * 2 * 128 * 4
+
+
+def _view(k=1, v=1, pooled=16, pt=16, n_seq=1, pps=4, nphys=4):
+    return _lib.KvView(k * 4096, v * 4096, pooled * 4096, pt * 4096, None, n_seq, pps, nphys)
+
+
+def test_append_rejects_bad_arguments_before_launch():
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view()
+    f = "qwfn_kv_append_q8_0"
+    assert _code(f, C.byref(s), None, 4096, 4096, 0, None, 4096, 1, None) == _lib.QWFN_EINVAL
+    assert _code(f, C.byref(s), C.byref(v), None, 4096, 0, None, 4096, 1, None) == _lib.QWFN_EINVAL
+    assert _code(f, C.byref(s), C.byref(v), 4096, 4096, 2, None, 4096, 1, None) == _lib.QWFN_EINVAL
+    assert _code(f, C.byref(s), C.byref(v), 4100, 4096, 0, None, 4096, 1, None) == _lib.QWFN_EINVAL
+    assert _code(f, C.byref(s), C.byref(v), 4096, 4096, 0, None, 4096, 0, None) == _lib.QWFN_EINVAL
+    bad = _lib.KvView(4097 * 16 + 1, 4096, 4096, 4096, None, 1, 4, 4)
+    assert _code(f, C.byref(s), C.byref(bad), 4096, 4096, 0, None, 4096, 1, None) == _lib.QWFN_EINVAL
+
+
+def test_decode_rejects_exhausted_context_and_small_workspace():
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view(pps=4)                       # capacity 1024 tokens
+    f = "qwfn_sparse_attn_decode"
+    args = lambda max_len, ws_bytes, n_seq=1: (C.byref(s), C.byref(v), 4096, 4096, 4096, 0, 4096, n_seq,
+                                               max_len, 4096, None, None, 256 * 64, ws_bytes, None)
+    assert _code(f, *args(1025, 1 << 30)) == _lib.QWFN_ERANGE
+    assert _code(f, *args(1024, 100)) == _lib.QWFN_ERANGE
+    assert _code(f, *args(0, 1 << 30)) == _lib.QWFN_EINVAL
+    assert _code(f, *args(1024, 1 << 30, n_seq=2)) == _lib.QWFN_EINVAL
+    msg = _lib.load().qwfn_qsa_last_error().decode()
+    assert "n_seq" in msg
+
+
+def test_indexer_rejects_short_selection_buffer():
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view(pps=256)
+    rc = _code("qwfn_indexer_topk", C.byref(s), C.byref(v), 4096, 4096, 1, 32768, 4096, 4096, 70,
+               256 * 64, 1 << 30, None)
+    assert rc == _lib.QWFN_ERANGE
+
+
+def test_python_errors_carry_the_message():
+    cfg = QsaConfig(n_head=15)
+    with pytest.raises(_lib.QsaError) as ei:
+        cfg.check()
+    assert ei.value.code == _lib.QWFN_EINVAL and "n_head" in str(ei.value)

@@ -1,0 +1,256 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.
+
+Bit-exact: q8_0 bytes, pooled keys of whole blocks, selected block ids,
+gathered cells.  Attention: |o - o_ref| <= 2e-3 + 1e-3 |o_ref| against the fp64
+oracle on the same dequantized cache.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _gpu import assert_close_attn, cfg_of, fill, kv_rows, make_pair, np_of
+from _refs import BASELINE, TINY, Cfg
+from qwfnfer_amd import _lib, qsa
+
+pytestmark = pytest.mark.gpu
+
+G12 = Cfg(n_head=24, n_head_kv=2, head_dim=256, block_tokens=4, page_tokens=128, top_k_blocks=40,
+          sink_blocks=1, local_tokens=16)          # the checkpoint's head shapes, small selection
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_append_bytes_match_oracle(variant, dtype):
+    cfg = Cfg(quant_variant=variant)
+    rng = np.random.default_rng(100 + variant)
+    dev, host = make_pair(cfg, 2, 3, seed=7, spare=2)
+    n = 300
+    seq = rng.integers(0, 2, n).astype(np.int32)
+    pos = rng.permutation(2 * 3 * 256)[:n].astype(np.int32) % (3 * 256)
+    key = seq.astype(np.int64) * 10**6 + pos
+    _, keep = np.unique(key, return_index=True)
+    seq, pos = seq[keep], pos[keep]
+    k, v = kv_rows(rng, len(pos), cfg)
+    k, v = k.astype(dtype), v.astype(dtype)
+    assert host.append(k, v, pos, seq) == 0
+    for _ in range(2):                                   # idempotent overwrite
+        qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                        torch.from_numpy(pos).cuda(), torch.from_numpy(seq).cuda())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+        np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
+    assert qsa.read_status(dev) == 0
+
+
+def test_append_edge_values():
+    cfg = BASELINE
+    dev, host = make_pair(cfg, 1, 1)
+    rows = np.zeros((8, 2, 128), np.float32)
+    rows[1] = 1e-3                                      # constant block
+    rows[2, :, ::7] = -5.0                              # sparse spikes
+    rows[3] = np.ldexp(1.0, -20)                        # fp16-subnormal scale
+    rows[4] = 3e4                                       # large scale
+    rows[5, :, :32] = np.arange(32) - 15.5              # exact half-ties under id = 127/amax? (not exact)
+    rows[6] = (np.arange(256).reshape(2, 128) % 17 - 8) * 0.25
+    rows[7] = np.float32(1e-40)                         # fp32 subnormal inputs
+    pos = np.arange(8, dtype=np.int32)
+    host.append(rows, rows, pos)
+    qsa.append_q8_0(dev, torch.from_numpy(rows).cuda(), torch.from_numpy(rows).cuda(),
+                    torch.from_numpy(pos).cuda())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+
+
+def test_append_reports_out_of_range_rows():
+    cfg = BASELINE
+    dev, host = make_pair(cfg, 1, 2)
+    k = np.ones((2, 2, 128), np.float32)
+    before = np_of(dev.k_pages).copy()
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(k).cuda(),
+                    torch.tensor([512, -1], dtype=torch.int32, device="cuda"))
+    assert qsa.read_status(dev) == _lib.STATUS_POS_RANGE
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(k).cuda(),
+                    torch.tensor([0, 1], dtype=torch.int32, device="cuda"),
+                    torch.tensor([1, 5], dtype=torch.int32, device="cuda"))
+    assert qsa.read_status(dev) == _lib.STATUS_SEQ_RANGE
+    np.testing.assert_array_equal(np_of(dev.k_pages), before)
+
+
+@pytest.mark.parametrize("cfg", [BASELINE, TINY, G12])
+def test_pool_matches_oracle(cfg):
+    rng = np.random.default_rng(110)
+    dev, host = make_pair(cfg, 2, 3, seed=3)
+    lengths = [3 * cfg.page_tokens, 2 * cfg.page_tokens + 5]
+    fill(dev, host, rng, lengths)
+    for s, L in enumerate(lengths):
+        nw = L // cfg.block_tokens
+        np.testing.assert_array_equal(np_of(dev.pooled)[s, :, :nw], host.pooled[s, :, :nw])
+    # pool_update of a listed subset recomputes the same values
+    dev.pooled.zero_()
+    ids = torch.tensor([0, 5, 7], dtype=torch.int32, device="cuda")
+    sids = torch.tensor([1, 1, 0], dtype=torch.int32, device="cuda")
+    qsa.pool_update(dev, ids, sids)
+    torch.cuda.synchronize()
+    got = np_of(dev.pooled)
+    for b, s in ((0, 1), (5, 1), (7, 0)):
+        np.testing.assert_array_equal(got[s, :, b], host.pooled[s, :, b])
+
+
+def _indexer_case(cfg, lengths, seed, equal_scores=False):
+    rng = np.random.default_rng(seed)
+    pps = max(lengths) // cfg.page_tokens + 1
+    dev, host = make_pair(cfg, len(lengths), pps, seed=seed)
+    fill(dev, host, rng, lengths)
+    if equal_scores:                                   # every pooled key identical -> all ties
+        host.pooled[...] = host.pooled[:, :, :1]
+        dev.pooled.copy_(torch.from_numpy(host.pooled))
+    q = rng.standard_normal((len(lengths), cfg.n_head, cfg.head_dim), dtype=np.float32)
+    L = np.array(lengths, np.int32)
+    max_len = int(L.max())
+    ws = qsa.Workspace(cfg_of(cfg), len(lengths), max_len)
+    sel, nsel = qsa.indexer_topk(dev, torch.from_numpy(q).cuda(), torch.from_numpy(L).cuda(), max_len, ws)
+    torch.cuda.synchronize()
+    hs, hn = host.indexer_topk(q, L, max_sel=sel.shape[-1])
+    sel, nsel = np_of(sel), np_of(nsel)
+    np.testing.assert_array_equal(nsel, hn)
+    for s in range(len(lengths)):
+        for g in range(cfg.n_head_kv):
+            np.testing.assert_array_equal(sel[s, g, :nsel[s, g]], hs[s, g, :hn[s, g]],
+                                          err_msg=f"seq {s} len {lengths[s]} head {g}")
+    return dev, host, q, L, sel, nsel, ws
+
+
+@pytest.mark.parametrize("lengths", [[1], [63, 64, 65], [511, 512, 513], [4096], [4097, 4160],
+                                     [32768], [20000, 100, 9000, 64 * 70]])
+def test_indexer_matches_oracle(lengths):
+    _indexer_case(BASELINE, lengths, seed=200 + len(lengths))
+
+
+def test_indexer_ties_resolve_to_lower_index():
+    _, _, _, _, sel, nsel, _ = _indexer_case(BASELINE, [32768], seed=210, equal_scores=True)
+    assert list(sel[0, 0, :nsel[0, 0]]) == [0] + list(range(1, 65)) + list(range(504, 512))
+
+
+@pytest.mark.parametrize("cfg", [TINY, G12, Cfg(relu_per_head=1), Cfg(top_k_blocks=3, sink_blocks=2, local_tokens=100)])
+def test_indexer_other_shapes(cfg):
+    _indexer_case(cfg, [3 * cfg.page_tokens - 1, cfg.page_tokens + 7], seed=220)
+
+
+def test_gather_matches_oracle():
+    cfg = BASELINE
+    dev, host, q, L, sel, nsel, ws = _indexer_case(cfg, [20000, 4500], seed=230)
+    seq_len = torch.from_numpy(L).cuda()
+    k, v, cells = qsa.gather_dequant(dev, seq_len, torch.from_numpy(sel).cuda(),
+                                     torch.from_numpy(nsel).cuda(), sel.shape[-1])
+    torch.cuda.synchronize()
+    k, v, cells = np_of(k), np_of(v), np_of(cells)
+    for s in range(2):
+        for g in range(2):
+            ids = [t for b in sel[s, g, :nsel[s, g]] for t in range(64 * b, 64 * b + 64) if t < L[s]]
+            assert list(cells[s, g, :len(ids)]) == ids and (cells[s, g, len(ids):] == -1).all()
+            for i in (0, 1, len(ids) // 2, len(ids) - 1):
+                np.testing.assert_array_equal(k[s, g, i], host.dequant_row("k", s, ids[i], g))
+                np.testing.assert_array_equal(v[s, g, i], host.dequant_row("v", s, ids[i], g))
+
+
+@pytest.mark.parametrize("cfg,lengths", [(BASELINE, [32768]), (BASELINE, [700, 4096, 9000]),
+                                         (TINY, [250, 77]), (G12, [300])])
+def test_sparse_attention_matches_f64(cfg, lengths):
+    dev, host, q, L, sel, nsel, ws = _indexer_case(cfg, lengths, seed=240)
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), torch.from_numpy(L).cuda(), int(L.max()), ws,
+                                 torch.from_numpy(sel).cuda(), torch.from_numpy(nsel).cuda())
+    torch.cuda.synchronize()
+    ref = host.attention_f64(q, L, sel, nsel)
+    assert_close_attn(np_of(out), ref, "sparse attention")
+
+
+@pytest.mark.parametrize("L", [1, 64, 1000, 4096])
+def test_dense_attention_matches_f64(L):
+    cfg = Cfg(top_k_blocks=0)                          # config 1: dense GQA over every key
+    rng = np.random.default_rng(250)
+    dev, host = make_pair(cfg, 1, L // 256 + 1)
+    fill(dev, host, rng, [L], scaled=False, pool=False)
+    q = rng.standard_normal((1, 16, 128), dtype=np.float32)
+    ws = qsa.Workspace(cfg_of(cfg), 1, L)
+    Lt = torch.tensor([L], dtype=torch.int32, device="cuda")
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), Lt, L, ws)
+    torch.cuda.synchronize()
+    assert_close_attn(np_of(out), host.attention_f64(q, [L]), "dense attention")
+
+
+def _decode_steps(cfg, lengths, steps, seed, dtype=np.float32):
+    """Fused decode steps on a batch of sequences vs the oracle's append + pool on
+    completion + indexer + fp64 attention."""
+    rng = np.random.default_rng(seed)
+    n_seq = len(lengths)
+    pps = (max(lengths) + steps) // cfg.page_tokens + 1
+    dev, host = make_pair(cfg, n_seq, pps, seed=seed)
+    fill(dev, host, rng, lengths)
+    cur = np.array(lengths, np.int32)
+    max_len = int(cur.max()) + steps
+    ws = qsa.Workspace(cfg_of(cfg), n_seq, max_len)
+    msel = cfg_of(cfg).max_selected(max_len)
+    sel = torch.empty((n_seq, cfg.n_head_kv, msel), dtype=torch.int32, device="cuda")
+    nsel = torch.empty((n_seq, cfg.n_head_kv), dtype=torch.int32, device="cuda")
+    outs = []
+    for step in range(steps):
+        cur = cur + 1
+        q = rng.standard_normal((n_seq, cfg.n_head, cfg.head_dim), dtype=np.float32)
+        kn, vn = kv_rows(rng, n_seq, cfg)
+        kn, vn = kn.astype(dtype), vn.astype(dtype)
+        out = qsa.sparse_attn_decode(dev, torch.from_numpy(q).cuda(), torch.from_numpy(kn).cuda(),
+                                     torch.from_numpy(vn).cuda(), torch.from_numpy(cur).cuda(), max_len, ws,
+                                     sel=sel, n_sel=nsel)
+        torch.cuda.synchronize()
+        for s in range(n_seq):
+            p = int(cur[s]) - 1
+            assert host.append(kn[s:s + 1], vn[s:s + 1], [p], [s]) == 0
+            if cur[s] % cfg.block_tokens == 0:
+                host.pool_block(s, p // cfg.block_tokens)
+        hs, hn = host.indexer_topk(q, cur, max_sel=msel)
+        gs, gn = np_of(sel), np_of(nsel)
+        np.testing.assert_array_equal(gn, hn, err_msg=f"step {step}")
+        for s in range(n_seq):
+            for g in range(cfg.n_head_kv):
+                np.testing.assert_array_equal(gs[s, g, :gn[s, g]], hs[s, g, :hn[s, g]],
+                                              err_msg=f"step {step} seq {s} head {g}")
+        ref = host.attention_f64(q, cur, hs, hn)
+        assert_close_attn(np_of(out), ref, f"decode step {step}")
+        outs.append(np_of(out))
+    np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+    np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
+    for s in range(n_seq):
+        nw = int(cur[s]) // cfg.block_tokens
+        np.testing.assert_array_equal(np_of(dev.pooled)[s, :, :nw], host.pooled[s, :, :nw])
+    return outs
+
+
+def test_decode_steps_cross_block_boundaries():
+    _decode_steps(BASELINE, [4096 - 3], steps=70, seed=300)
+
+
+def test_decode_steps_batched_paged():
+    # config 5 in miniature: several sequences, permuted pages, different lengths
+    _decode_steps(BASELINE, [5000, 700, 12345, 64 * 9 - 1], steps=6, seed=310, dtype=np.float16)
+
+
+def test_decode_steps_tiny_and_checkpoint_shapes():
+    _decode_steps(TINY, [61, 130], steps=10, seed=320)
+    _decode_steps(G12, [250], steps=6, seed=321)
+
+
+def test_decode_is_deterministic():
+    cfg = BASELINE
+    rng = np.random.default_rng(330)
+    res = []
+    for rep in range(2):
+        dev, host = make_pair(cfg, 2, 40, seed=5)
+        fill(dev, host, np.random.default_rng(331), [9000, 6000])
+        ws = qsa.Workspace(cfg_of(cfg), 2, 10000)
+        q = torch.from_numpy(np.random.default_rng(332).standard_normal((2, 16, 128), dtype=np.float32)).cuda()
+        kn = torch.from_numpy(np.random.default_rng(333).standard_normal((2, 2, 128), dtype=np.float32)).cuda()
+        L = torch.tensor([9001, 6001], dtype=torch.int32, device="cuda")
+        out = qsa.sparse_attn_decode(dev, q, kn, kn, L, 10000, ws)
+        torch.cuda.synchronize()
+        res.append((np_of(out).tobytes(), np_of(dev.k_pages).tobytes(), np_of(dev.pooled).tobytes()))
+    assert res[0] == res[1]
