@@ -1,0 +1,385 @@
+#!/usr/bin/env python3
+"""bench.py -- sparse q8_0 decode attention on one MI355X.
+
+Workload: 12 sparse-attention layers (16 q heads, 2 KV
+heads, head_dim 128), q8_0 K/V ~ N(0,1) with a log-uniform [0.1, 10] scale per
+q8_0 block, 64-token pooled blocks, top-64 blocks + block 0 + the last 512
+tokens, one decode token per step at contexts 4096, 65536 and 163840.
+
+A step = one decode token through all 12 layers; each layer is the fused path
+of graph_builder::sparse_attn_decode: append the token's K/V (q8_0), re-pool
+the block it completes, score the pooled blocks, select, attend (two kernels:
+append+select, attention).  seq_len stays at the context, so every step
+rewrites position ctx-1 (an idempotent overwrite) and re-pools its block.
+Inputs are resident in HBM before the timed region; per-context working sets
+below 512 MiB are replicated and rotated so the 256 MB MALL does not serve them.
+
+Prints one JSON line: value = us per layer at the largest context.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "sparse decode attn µs/layer @4K & 160K ctx (q8_0 KV); % of HBM roofline"
+HBM_PEAK_GBS = 8000.0          # MI355X published HBM3E peak
+ROTATE_BYTES = 512 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--contexts", default="4096,65536,163840")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
+    ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
+    ap.add_argument("--seed", type=int, default=3)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+
+def fill_layer(qsa, torch, cache, lengths, gen, chunk=32768):
+    """K/V ~ N(0,1) times a per-q8_0-block log-uniform [0.1, 10] scale, appended
+    for tokens [0, L_s) of each sequence, then every whole block pooled."""
+    cfg = cache.cfg
+    nb = cfg.head_dim // 32
+    for s, L in enumerate(lengths):
+        for t0 in range(0, L, chunk):
+            n = min(chunk, L - t0)
+            kv = []
+            for _ in range(2):
+                x = torch.randn((n, cfg.n_head_kv, nb, 32), device="cuda", generator=gen)
+                sc = torch.exp(torch.empty((n, cfg.n_head_kv, nb, 1), device="cuda").uniform_(
+                    math.log(0.1), math.log(10.0), generator=gen))
+                kv.append((x * sc).reshape(n, cfg.n_head_kv, cfg.head_dim).contiguous())
+            pos = torch.arange(t0, t0 + n, dtype=torch.int32, device="cuda")
+            sid = torch.full((n,), s, dtype=torch.int32, device="cuda")
+            qsa.append_q8_0(cache, kv[0], kv[1], pos, sid)
+        if L // cfg.block_tokens:
+            qsa.pool_rebuild(cache, s, L // cfg.block_tokens)
+
+
+def selected_cells(sel, nsel, lengths, bt):
+    """Cells attended per (sequence, KV head), from a selection read back."""
+    tot = 0
+    for s, L in enumerate(lengths):
+        for g in range(sel.shape[1]):
+            for b in sel[s, g, : nsel[s, g]]:
+                tot += max(0, min(bt, L - int(b) * bt))
+    return tot
+
+
+class Runner:
+    """n_inst replicas of an n_layer stack of caches at fixed sequence lengths,
+    stepped by the fused decode (append+select, attention per layer)."""
+
+    def __init__(self, qsa, torch, cfg, lengths, n_layer, pages_per_seq, page_table, gen):
+        self.qsa, self.torch, self.cfg = qsa, torch, cfg
+        self.lengths = lengths
+        n_seq = len(lengths)
+        self.n_seq = n_seq
+        self.max_len = max(lengths)
+        pb = cfg.page_bytes()
+        per_stack = n_layer * 2 * page_table.numel() * pb
+        self.n_inst = max(1, math.ceil(ROTATE_BYTES / per_stack))
+        self.stacks = []
+        for _ in range(self.n_inst):
+            layers = []
+            for _ in range(n_layer):
+                c = qsa.KvCache.allocate(cfg, n_seq, pages_per_seq, page_table=page_table,
+                                         n_phys_pages=int(page_table.max()) + 1)
+                fill_layer(qsa, torch, c, lengths, gen)
+                layers.append(c)
+            self.stacks.append(layers)
+        self.q = [torch.randn((n_seq, cfg.n_head, cfg.head_dim), device="cuda", generator=gen)
+                  for _ in range(n_layer)]
+        self.kn = [torch.randn((n_seq, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
+                   for _ in range(n_layer)]
+        self.vn = [torch.randn((n_seq, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
+                   for _ in range(n_layer)]
+        self.out = [torch.empty((n_seq, cfg.n_head, cfg.head_dim), device="cuda") for _ in range(n_layer)]
+        self.seq_len = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+        self.ws = qsa.Workspace(cfg, n_seq, self.max_len)
+        msel = cfg.max_selected(self.max_len)
+        self.sel = torch.empty((n_seq, cfg.n_head_kv, msel), dtype=torch.int32, device="cuda")
+        self.nsel = torch.empty((n_seq, cfg.n_head_kv), dtype=torch.int32, device="cuda")
+        self.n_layer = n_layer
+        self.graphs = None
+        torch.cuda.synchronize()
+        for layers in self.stacks:
+            for c in layers:
+                if qsa.read_status(c):
+                    raise RuntimeError("cache fill reported out-of-range rows")
+
+    def layer(self, inst, il, ev=None):
+        qsa = self.qsa
+        c = self.stacks[inst][il]
+        if ev is not None:
+            ev[0].record()
+        qsa.decode_append_select(c, self.q[il], self.kn[il], self.vn[il], self.seq_len, self.max_len, self.ws,
+                                 self.sel, self.nsel)
+        if ev is not None:
+            ev[1].record()
+        qsa.sparse_decode_attn(c, self.q[il], self.seq_len, self.max_len, self.ws, self.sel, self.nsel,
+                               out=self.out[il])
+        if ev is not None:
+            ev[2].record()
+
+    def step(self, i):
+        inst = i % self.n_inst
+        for il in range(self.n_layer):
+            self.layer(inst, il)
+
+    def capture(self):
+        """One hipGraph per replica holding a whole step (2 launches per layer).
+        Every replay is checked against an eager step on the same inputs."""
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graphs = []
+        with torch.cuda.stream(s):
+            for inst in range(self.n_inst):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=s):
+                    for il in range(self.n_layer):
+                        self.layer(inst, il)
+                graphs.append(g)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for inst in range(self.n_inst):
+            self.step(inst)
+            torch.cuda.synchronize()
+            ref = [o.clone() for o in self.out]
+            for rep in range(3 if inst == 0 else 1):
+                for o in self.out:
+                    o.fill_(float("nan"))
+                graphs[inst].replay()
+                torch.cuda.synchronize()
+                if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
+                    raise RuntimeError(f"graph {inst} replay {rep} differs from the eager step")
+                self.step(inst)                 # eager work between replays
+                torch.cuda.synchronize()
+        self.graphs = graphs
+
+    def graph_step(self, i):
+        self.graphs[i % self.n_inst].replay()
+
+    def time_steps(self, steps, warmup, graph):
+        torch = self.torch
+        fn = self.graph_step if graph else self.step
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps            # ms per step
+
+    def time_kernels(self, steps):
+        """Average device time of the append+select and attention launches,
+        from HIP events around each launch on the launch stream."""
+        torch = self.torch
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps * self.n_layer)]
+        k = 0
+        for i in range(steps):
+            for il in range(self.n_layer):
+                self.layer(i % self.n_inst, il, evs[k])
+                k += 1
+        torch.cuda.synchronize()
+        sel_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
+        att_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
+        return sel_ms * 1e3, att_ms * 1e3
+
+    def bytes_per_layer(self):
+        """Algorithmic bytes of one layer: selected KV (q8_0, K and V) read by the
+        attention kernel; pooled keys scanned by the select kernel."""
+        cfg = self.cfg
+        sel = self.sel.cpu().numpy()
+        nsel = self.nsel.cpu().numpy()
+        cells = selected_cells(sel, nsel, self.lengths, cfg.block_tokens)
+        row = cfg.head_dim + cfg.head_dim // 32 * 2              # 136 B per (token, KV head)
+        kv = cells * row * 2
+        pooled = 0
+        for L in self.lengths:
+            last = L - 1
+            fw = max(0, last - cfg.local_tokens + 1) // cfg.block_tokens
+            elig = max(0, min(L // cfg.block_tokens, fw) - cfg.sink_blocks)
+            if elig > cfg.top_k_blocks:
+                pooled += elig * cfg.n_head_kv * cfg.head_dim * 4
+        return kv, pooled, cells
+
+
+def cpu_baseline(cfg, ctx, seconds, seed):
+    """The oracle's fp32 decode step (the ggml CPU path restated: append,
+    pool, scores, selection, attention over fp16-cast K/V) on one layer at
+    ctx, repeated for about `seconds`."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(seed)
+    pps = ctx // cfg.page_tokens
+    host = O.HostCache(cfg, 1, pps)
+    nb = cfg.head_dim // 32
+    for t0 in range(0, ctx, 16384):
+        n = min(16384, ctx - t0)
+        kv = []
+        for _ in range(2):
+            x = rng.standard_normal((n, cfg.n_head_kv, nb, 32), dtype=np.float32)
+            x *= np.exp(rng.uniform(np.log(0.1), np.log(10.0), (n, cfg.n_head_kv, nb, 1))).astype(np.float32)
+            kv.append(x.reshape(n, cfg.n_head_kv, cfg.head_dim))
+        host.append(kv[0], kv[1], np.arange(t0, t0 + n, dtype=np.int32))
+    for b in range(ctx // cfg.block_tokens):
+        host.pool_block(0, b)
+    q = rng.standard_normal((1, cfg.n_head, cfg.head_dim), dtype=np.float32)
+    kn = rng.standard_normal((1, cfg.n_head_kv, cfg.head_dim), dtype=np.float32)
+    host.decode_step_f32(q, kn, kn, [ctx])                       # warm-up
+    n, t0 = 0, time.perf_counter()
+    threads = 1
+    while time.perf_counter() - t0 < seconds:
+        _, _, _, threads = host.decode_step_f32(q, kn, kn, [ctx])
+        n += 1
+    dt = time.perf_counter() - t0
+    return dt / n * 1e6, threads, n
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the QSA path "
+              "shards across GPUs only by sequence or KV head, which this build does not run.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from qwfnfer_amd import qsa
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    cfg = qsa.QsaConfig()
+    contexts = [int(c) for c in args.contexts.split(",")]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    dev = torch.cuda.get_device_name(0)
+    log(f"[bench] {dev}; {args.layers} layers, contexts {contexts}, steps {args.steps}, warmup {args.warmup}")
+
+    per_ctx = {}
+    for ctx in contexts:
+        pps = ctx // cfg.page_tokens
+        pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+        r = Runner(qsa, torch, cfg, [ctx], args.layers, pps, pt, gen)
+        eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
+        graph_ms = None
+        if not args.no_graph:
+            r.capture()
+            graph_ms = r.time_steps(args.steps, args.warmup, graph=True)
+        sel_us, att_us = r.time_kernels(max(20, args.steps // 4))
+        kv, pooled, cells = r.bytes_per_layer()
+        ms = graph_ms if graph_ms is not None else eager_ms
+        res = dict(us_per_layer=ms * 1e3 / args.layers, eager_us_per_layer=eager_ms * 1e3 / args.layers,
+                   graph_us_per_layer=None if graph_ms is None else graph_ms * 1e3 / args.layers,
+                   ms_per_step=ms, select_kernel_us=sel_us, attn_kernel_us=att_us,
+                   selected_kv_bytes=kv, pooled_scan_bytes=pooled, cells_per_layer=cells,
+                   replicas=r.n_inst)
+        res["attn_gbs"] = kv / (att_us * 1e-6) / 1e9
+        res["layer_gbs_selected"] = kv / (res["us_per_layer"] * 1e-6) / 1e9
+        res["layer_gbs_all"] = (kv + pooled) / (res["us_per_layer"] * 1e-6) / 1e9
+        per_ctx[ctx] = res
+        log(f"[bench] ctx {ctx}: {res['us_per_layer']:.2f} us/layer (eager {res['eager_us_per_layer']:.2f}), "
+            f"select {sel_us:.2f} us, attn {att_us:.2f} us = {res['attn_gbs']:.0f} GB/s on {kv} B, "
+            f"pooled scan {pooled} B, replicas {r.n_inst}")
+        del r
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+    batched = None
+    if not args.no_batched:
+        import numpy as np
+        rng = np.random.default_rng(args.seed)
+        lens = [int(math.exp(rng.uniform(math.log(4096), math.log(262144)))) for _ in range(8)]
+        pps = max(lens) // cfg.page_tokens + 1
+        perm = torch.from_numpy(rng.permutation(8 * pps).astype(np.int32)).view(8, pps)
+        r = Runner(qsa, torch, cfg, lens, 1, pps, perm, gen)
+        ms = r.time_steps(args.steps, args.warmup, graph=False)
+        sel_us, att_us = r.time_kernels(max(20, args.steps // 4))
+        kv, pooled, cells = r.bytes_per_layer()
+        batched = dict(lengths=lens, us_per_launch_pair=ms * 1e3, select_kernel_us=sel_us, attn_kernel_us=att_us,
+                       selected_kv_bytes=kv, pooled_scan_bytes=pooled,
+                       attn_gbs=kv / (att_us * 1e-6) / 1e9,
+                       attn_frac=kv / (att_us * 1e-6) / 1e9 / HBM_PEAK_GBS)
+        log(f"[bench] config 5 batched (8 seqs {lens}): {ms * 1e3:.2f} us per layer-step, attn {att_us:.2f} us "
+            f"= {batched['attn_gbs']:.0f} GB/s")
+        del r
+        torch.cuda.empty_cache()
+
+    big = max(contexts)
+    small = min(contexts)
+    top = per_ctx[big]
+    cpu = None
+    if not args.no_cpu:
+        cpu_us, threads, n = cpu_baseline(cfg, big, args.cpu_seconds, args.seed)
+        cpu = {"value": round(cpu_us, 2), "unit": "us/layer", "cores": threads, "kind": "port",
+               "sample": f"{n} decode steps of one layer at ctx {big} (oracle/qsa_oracle.c "
+                         f"qwfn_oracle_decode_step_f32, OpenMP), ~{args.cpu_seconds:.0f} s"}
+        log(f"[bench] cpu baseline: {cpu_us:.1f} us/layer on {threads} threads ({n} steps)")
+
+    attn_gbs = top["attn_gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(top["us_per_layer"], 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(top["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config3: {args.layers} sparse layers, ctx {big}, 16q/2kv heads x 128, q8_0 KV, "
+                        f"top-64 64-token blocks + block 0 + 512-token window, 1 decode token/step",
+            "contexts": contexts,
+            "launch": "hipGraph" if top["graph_us_per_layer"] is not None else "eager",
+        },
+        "us_per_layer": {str(c): round(v["us_per_layer"], 3) for c, v in per_ctx.items()},
+        "flatness": round(top["us_per_layer"] / per_ctx[small]["us_per_layer"], 4),
+        "per_context": {str(c): {k: (round(x, 3) if isinstance(x, float) else x) for k, x in v.items()}
+                        for c, v in per_ctx.items()},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_attn (sparse decode attention, selected q8_0 K+V)",
+            "achieved": round(attn_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": top["selected_kv_bytes"],
+            "launch_us": round(top["attn_kernel_us"], 3),
+        },
+        "layer_roofline_frac": round(top["layer_gbs_selected"] / HBM_PEAK_GBS, 4),
+        "batched_config5": batched,
+        "cpu_baseline": cpu,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -203,11 +203,23 @@ int qwfn_sparse_decode_attn(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             int32_t max_seq_len, const int32_t *sel,
                             const int32_t *n_sel, int32_t max_sel, float *out,
                             void *ws, size_t ws_bytes, void *stream);
+/* The first launch of qwfn_sparse_attn_decode on its own: append k_new/v_new
+ * at seq_len-1, re-pool the block that position completes, score and select
+ * (sel/n_sel as in qwfn_indexer_topk, max_sel >= qwfn_qsa_max_selected).
+ * Replaces src/qwfn_graph.cpp:465-495 and 520-528 (the writes, scores and
+ * top-k of one decode token).                                                  */
+int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                              const float *q, const void *k_new, const void *v_new,
+                              int32_t src_dtype, const int32_t *seq_len,
+                              int32_t n_seq, int32_t max_seq_len, int32_t *sel,
+                              int32_t *n_sel, int32_t max_sel,
+                              void *ws, size_t ws_bytes, void *stream);
 /* One decode token of graph_builder::sparse_attn_decode (src/qwfn_graph.cpp:
  * 450-546) from the K/V projections on: append k_new/v_new
  * ([n_seq][n_head_kv][head_dim], src_dtype) at position seq_len-1, re-pool the
  * block that position completes, score + select, and attend.  sel_out/n_sel_out
- * (optional) receive the selection as qwfn_indexer_topk would.  Two launches.  */
+ * (optional) receive the selection as qwfn_indexer_topk would.  Two launches:
+ * qwfn_decode_append_select, then qwfn_sparse_decode_attn's kernel.           */
 int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                             const float *q, const void *k_new, const void *v_new,
                             int32_t src_dtype, const int32_t *seq_len,

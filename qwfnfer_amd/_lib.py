@@ -43,6 +43,7 @@ EXPORTS = (
     "qwfn_indexer_topk",
     "qwfn_gather_dequant",
     "qwfn_sparse_decode_attn",
+    "qwfn_decode_append_select",
     "qwfn_sparse_attn_decode",
 )
 
@@ -109,6 +110,7 @@ _SIGS = {
     "qwfn_indexer_topk": (C.c_int, [_S, _V, _P, _P, _I, _I, _P, _P, _I, _P, _Z, _P]),
     "qwfn_gather_dequant": (C.c_int, [_S, _V, _P, _I, _P, _P, _I, _P, _P, _P, _P]),
     "qwfn_sparse_decode_attn": (C.c_int, [_S, _V, _P, _P, _I, _I, _P, _P, _I, _P, _P, _Z, _P]),
+    "qwfn_decode_append_select": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _P, _Z, _P]),
     "qwfn_sparse_attn_decode": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _Z, _P]),
 }
 
@@ -122,6 +124,14 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         raise RuntimeError(
             f"{path} is missing: build it with `python -m qwfnfer_amd.build` "
             "(the QSA path has no CPU fallback)")
+    # torch ships its own libamdhip64.so.7.  Loading torch first makes this
+    # library's libamdhip64.so.7 dependency bind to that copy, so the process
+    # has one HIP runtime and the streams and memory torch hands over are the
+    # runtime's own.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(path)
     for name, (res, args) in _SIGS.items():
         fn = getattr(lib, name)

@@ -348,6 +348,30 @@ int qwfn_sparse_decode_attn(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
     return e == hipSuccess ? ok() : hip_fail(e, "decode_attn");
 }
 
+int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                              const void *k_new, const void *v_new, int32_t src_dtype,
+                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, int32_t *sel,
+                              int32_t *n_sel, int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16)
+        return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
+    const size_t al = src_dtype == QWFN_SRC_F32 ? 16 : 8;
+    if (!q || !aligned(q, 16) || !k_new || !v_new || !aligned(k_new, al) || !aligned(v_new, al) ||
+        !seq_len || !sel || !n_sel)
+        return fail(QWFN_EINVAL, "append_select: NULL or misaligned q / k_new / v_new / seq_len / sel / n_sel");
+    const int32_t need = max_selected(shape, max_seq_len);
+    if (max_sel < need) return fail(QWFN_ERANGE, "append_select: max_sel %d < %d", max_sel, need);
+    Ws w;
+    if ((rc = bind_ws(g, n_seq, max_seq_len, need, ws, ws_bytes, &w))) return rc;
+    const FusedAppend fa{k_new, v_new, src_dtype == QWFN_SRC_F16, 1};
+    const hipError_t e = launch_indexer(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, w, fa,
+                                        (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "append_select");
+}
+
 int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
                             const void *k_new, const void *v_new, int32_t src_dtype,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, float *out,

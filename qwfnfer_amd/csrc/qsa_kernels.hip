@@ -54,27 +54,88 @@ __device__ __forceinline__ uint32_t score_key(float x) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+// Cross-lane steps on the DPP network (gfx9 encodings): a wave64 reduction
+// is quad xor-1, quad xor-2, half-row mirror, row mirror, then row_bcast:15
+// into rows 1/3 and row_bcast:31 into rows 2/3, leaving the total in lane 63;
+// no LDS traffic, unlike ds_bpermute shuffles.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_ZERO = false>
+__device__ __forceinline__ float dppf(float old, float src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, src), CTRL,
+                                                                 ROW_MASK, BANK_MASK, BOUND_ZERO));
 }
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_ZERO = false>
+__device__ __forceinline__ int dppi(int old, int src) {
+    return __builtin_amdgcn_update_dpp(old, src, CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO);
+}
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+constexpr int kDppRowShr = 0x110, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+__device__ __forceinline__ float lane63(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Maximum over the wave, returned to every lane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dppf<kDppQuadXor1>(v, v));
+    v = fmaxf(v, dppf<kDppQuadXor2>(v, v));
+    v = fmaxf(v, dppf<kDppRowHalfMirror>(v, v));
+    v = fmaxf(v, dppf<kDppRowMirror>(v, v));
+    v = fmaxf(v, dppf<kDppRowBcast15, 0xa>(v, v));
+    v = fmaxf(v, dppf<kDppRowBcast31, 0xc>(v, v));
+    return lane63(v);
+}
+
+// Sum over the wave, returned to every lane.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dppf<kDppQuadXor1>(0.0f, v);
+    v += dppf<kDppQuadXor2>(0.0f, v);
+    v += dppf<kDppRowHalfMirror>(0.0f, v);
+    v += dppf<kDppRowMirror>(0.0f, v);
+    v += dppf<kDppRowBcast15, 0xa>(0.0f, v);
+    v += dppf<kDppRowBcast31, 0xc>(0.0f, v);
+    return lane63(v);
+}
+
+// Inclusive prefix sum over the wave (Hillis-Steele inside each 16-lane row,
+// then the row totals broadcast forward).
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += dppi<kDppRowShr + 1, 0xf, 0xf, true>(0, x);
+    x += dppi<kDppRowShr + 2, 0xf, 0xf, true>(0, x);
+    x += dppi<kDppRowShr + 4, 0xf, 0xf, true>(0, x);
+    x += dppi<kDppRowShr + 8, 0xf, 0xf, true>(0, x);
+    x += dppi<kDppRowBcast15, 0xa>(0, x);
+    x += dppi<kDppRowBcast31, 0xc>(0, x);
+    return x;
+}
+
+// Completion protocol of a split reduction, called by EVERY thread of a
+// workgroup that has finished writing its share (the barriers inside must be
+// reached from one call site by all waves).  Each thread waits for its own
+// stores, the barrier orders them before thread 0's agent-scope release fence
+// and the counter increment; only the workgroup that arrives last takes the
+// acquire fence before reading the others' results.  One fence pair per
+// workgroup rather than per wave: on gfx950 an agent-scope fence writes back
+// and invalidates the XCD's L2.  Returns true in the last workgroup.
+__device__ __forceinline__ bool arrive_last(int32_t *counter, int expected, int *flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old == expected - 1;
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        *flag = last;
+    }
+    __syncthreads();
+    return *flag != 0;
 }
 
 // Exclusive prefix sum over the NT threads of a workgroup; *total = the sum.
 template <int NT>
 __device__ __forceinline__ int block_excl_sum(int v, int *tmp, int *total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o);
-        if (lane >= o) x += y;
-    }
+    const int x = wave_incl_scan(v);
     if (lane == 63) tmp[w] = x;
     __syncthreads();
     int base = 0, tot = 0;
@@ -204,38 +265,81 @@ hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, con
 // pooled keys: sequential fp32 add chain over the block's members, * 1/bt
 // ---------------------------------------------------------------------------
 
+// One dequantized member value straight from global memory (gather path).
 __device__ __forceinline__ float member_k(const Geo &g, const uint8_t *page, int gh, int row, int d) {
     const int8_t q = (int8_t)page[quant_off(g, gh, row, d)];
     const uint16_t s = *reinterpret_cast<const uint16_t *>(page + scale_off(g, gh, row, d / 32));
     return h2f(s) * (float)q;
 }
 
-// grid (n_blocks, Hkv), block = hd threads; thread d owns one dimension.
+constexpr int kStageRows = 64;   // member rows staged through LDS per round
+
+// Rows [row0, row0+n) (n <= kStageRows) of KV head gh of one page, copied into
+// LDS as int8 q8[n][HD] and fp16 sc[n][HD/32] -- every load issued before any
+// is consumed, so the copy costs one memory round trip.
+template <int HD>
+__device__ __forceinline__ void stage_rows(const Geo &g, const uint8_t *page, int gh, int row0, int n,
+                                           int8_t *q8, uint16_t *sc, int tid, int nt) {
+    constexpr int CH = HD / 16;
+#pragma unroll 4
+    for (int k = tid; k < n * CH; k += nt) {
+        const int r = k % n, c = k / n, row = row0 + r;
+        const uint4 val = *reinterpret_cast<const uint4 *>(
+            page + ((int64_t)(gh * (g.pt / 64) + row / 64) * CH + c) * 1024 + (row % 64) * 16);
+        *reinterpret_cast<uint4 *>(q8 + r * HD + c * 16) = val;
+    }
+    const uint16_t *s = reinterpret_cast<const uint16_t *>(page + scale_off(g, gh, row0, 0));
+#pragma unroll 4
+    for (int k = tid; k < n * (HD / 32); k += nt) sc[k] = s[k];
+}
+
+// Pooled key of one block of KV head gh: thread d < HD keeps dimension d's
+// chain acc = m_0 + m_1 + ... + m_{bt-1}, then * (1/bt).  With `last` set the
+// final member is taken from it (the decode token, still in LDS) instead of
+// memory.  All nt threads must call (it synchronises).
+template <int HD>
+__device__ void pool_block_dev(const Geo &g, const uint8_t *page, int gh, int row0, float *dst,
+                               const float *last, int8_t *q8, uint16_t *sc, int tid, int nt) {
+#pragma clang fp contract(off)
+    const int from_mem = last ? g.bt - 1 : g.bt;
+    float acc = 0.0f;
+    for (int r0 = 0; r0 < from_mem; r0 += kStageRows) {
+        const int n = min(kStageRows, from_mem - r0);
+        stage_rows<HD>(g, page, gh, row0 + r0, n, q8, sc, tid, nt);
+        __syncthreads();
+        if (tid < HD) {
+#pragma unroll 8
+            for (int t = 0; t < n; ++t) {
+                const float m = h2f(sc[t * (HD / 32) + tid / 32]) * (float)q8[t * HD + tid];
+                acc = (r0 + t == 0) ? m : acc + m;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < HD) {
+        if (last) acc = (g.bt == 1) ? last[tid] : acc + last[tid];
+        dst[tid] = acc * g.inv_bt;
+    }
+}
+
+// grid (n_blocks, Hkv), 256 threads
+template <int HD>
 __global__ void __launch_bounds__(256)
 k_pool(Geo g, qwfn_kv_view v, const int32_t *seq_ids, const int32_t *block_ids, int32_t seq_const) {
-#pragma clang fp contract(off)
-    const int bi = blockIdx.x, gh = blockIdx.y, d = threadIdx.x;
+    __shared__ int8_t q8[kStageRows * HD];
+    __shared__ uint16_t sc[kStageRows * (HD / 32)];
+    const int bi = blockIdx.x, gh = blockIdx.y, tid = threadIdx.x;
     const int seq = seq_ids ? seq_ids[bi] : seq_const;
     const int b = block_ids ? block_ids[bi] : bi;
-    const bool report = (gh == 0 && d == 0);
+    const bool report = (gh == 0 && tid == 0);
     if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
     if (b < 0 || b >= g.bps) { if (report) set_status(v.status, QWFN_STATUS_BLOCK_RANGE); return; }
     const int t0 = b * g.bt;
     const int32_t pp = phys_page(g, v.page_table, seq, t0);   // a block never straddles pages
     if (pp < 0) { if (report) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
     const uint8_t *page = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
-    const int row0 = t0 % g.pt;
-    float acc = member_k(g, page, gh, row0, d);
-    for (int t = 1; t < g.bt; ++t) acc = acc + member_k(g, page, gh, row0 + t, d);
-    v.pooled[(((int64_t)seq * g.Hkv + gh) * g.bps + b) * g.hd + d] = acc * g.inv_bt;
-}
-
-hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
-                       const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
-                       hipStream_t st) {
-    hipLaunchKernelGGL(k_pool, dim3((unsigned)n_blocks, (unsigned)g.Hkv), dim3((unsigned)g.hd), 0, st,
-                       g, v, seq_ids, block_ids, seq_const);
-    return hipGetLastError();
+    pool_block_dev<HD>(g, page, gh, t0 % g.pt, v.pooled + (((int64_t)seq * g.Hkv + gh) * g.bps + b) * HD,
+                       nullptr, q8, sc, tid, 256);
 }
 
 // ---------------------------------------------------------------------------
@@ -258,23 +362,33 @@ __device__ __forceinline__ Ranges qsa_ranges(const Geo &g, int L) {
 
 constexpr int kIdxThreads = 256;
 constexpr int kBlocksPerChunk = kIdxThreads / 4;   // 4 lanes share one block's dot
+constexpr int kKeysMax = 8192;                     // eligible blocks whose keys fit in LDS
+
+constexpr int kCandMax = 256;                      // threshold-bin candidates ranked exactly
 
 struct IdxShared {
-    float q[16 * 256];            // the group's query heads, G <= 16, hd <= 256
+    union {
+        float q[16 * 256];                         // scoring: the group's query heads
+        uint32_t keys[kKeysMax];                   // selection: orderable score keys
+        struct { int8_t q8[kStageRows * 256]; uint16_t sc[kStageRows * 8]; } st;  // pooling
+    } u;
     uint32_t hist[4096];
+    uint32_t cand_key[kCandMax];
+    int32_t cand_b[kCandMax];
+    uint32_t selbits[kKeysMax / 32];
     float newk[256];
-    int tmp[8];
-    int flag, bin, need;
+    int tmp[16];
+    int flag, bin, need, ncand;
 };
 
 // Append of the decode token (K and V rows of KV head gh) and, when it
 // completes its block, the block's pooled key -- the decode writes of
 // src/qwfn_graph.cpp:465-476, 520-528 as one workgroup.  The new K row is
-// also kept dequantized in LDS as the block's last member.
+// kept dequantized in LDS as the block's last member.
+template <int HD>
 __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const FusedAppend &fa,
                                   int s, int gh, int L, IdxShared &sh) {
-#pragma clang fp contract(off)
-    const int tid = threadIdx.x, nj = g.hd / 32, per = nj * 8;   // lanes per row
+    const int tid = threadIdx.x, per = (HD / 32) * 8;   // lanes per row
     const int p = L - 1;
     const int32_t pp = phys_page(g, v.page_table, s, p);
     if (pp < 0) { if (tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
@@ -282,7 +396,7 @@ __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const Fus
     if (tid < 2 * per) {
         const int which = tid / per, j = (tid % per) / 8, e4 = tid % 8;
         float x[4], dq[4];
-        load4(which ? fa.v_new : fa.k_new, fa.src_f16, ((int64_t)s * g.Hkv + gh) * g.hd + 32 * j + 4 * e4, x);
+        load4(which ? fa.v_new : fa.k_new, fa.src_f16, ((int64_t)s * g.Hkv + gh) * HD + 32 * j + 4 * e4, x);
         uint16_t dh;
         const uint32_t pk = quant4(x, g.variant, &dh, dq);
         uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
@@ -293,42 +407,53 @@ __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const Fus
     }
     __syncthreads();
     if (L % g.bt != 0) return;                     // the block is not complete yet
-    const int b = p / g.bt, row0 = row - (g.bt - 1);
-    const uint8_t *page = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
-    for (int d = tid; d < g.hd; d += kIdxThreads) {
-        float acc = sh.newk[d];
-        if (g.bt > 1) {
-            acc = member_k(g, page, gh, row0, d);
-            for (int t = 1; t < g.bt - 1; ++t) acc = acc + member_k(g, page, gh, row0 + t, d);
-            acc = acc + sh.newk[d];
-        }
-        v.pooled[(((int64_t)s * g.Hkv + gh) * g.bps + b) * g.hd + d] = acc * g.inv_bt;
-    }
+    const int b = p / g.bt;
+    const uint8_t *kpage = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
+    pool_block_dev<HD>(g, kpage, gh, row - (g.bt - 1), v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + b) * HD,
+                       sh.newk, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
 }
 
+__device__ __forceinline__ uint32_t key_at(const IdxShared &sh, const float *sc, int e_lo, int b, bool lds) {
+    return lds ? sh.u.keys[b - e_lo] : score_key(sc[b]);
+}
+
+template <int NB> __device__ void find_bin(IdxShared &sh, int need);
+
 // One radix pass over the eligible keys that match `prefix` above bit
-// shift+bits: histogram of the `bits`-bit digit at `shift`, then the digit of
-// the need-th largest key.  Updates *prefix (appending the digit) and *need.
+// shift+BITS: histogram of the BITS-bit digit at `shift`, then the digit of
+// the need-th largest key.  Updates prefix (appending the digit) and need.
 template <int BITS>
-__device__ void radix_pass(const float *sc, int e_lo, int e_hi, int shift, uint32_t &prefix,
-                           int &need, bool first, IdxShared &sh) {
-    constexpr int NB = 1 << BITS, PER = NB / kIdxThreads > 0 ? NB / kIdxThreads : 1;
+__device__ void radix_pass(const IdxShared &shc, IdxShared &sh, const float *sc, int e_lo, int e_hi,
+                           bool lds, int shift, uint32_t &prefix, int &need, bool first) {
+    constexpr int NB = 1 << BITS;
     const int tid = threadIdx.x;
     for (int i = tid; i < NB; i += kIdxThreads) sh.hist[i] = 0u;
     __syncthreads();
     for (int b = e_lo + tid; b < e_hi; b += kIdxThreads) {
-        const uint32_t k = score_key(sc[b]);
+        const uint32_t k = key_at(shc, sc, e_lo, b, lds);
         if (first || (k >> (shift + BITS)) == prefix) atomicAdd(&sh.hist[(k >> shift) & (NB - 1)], 1u);
     }
     __syncthreads();
-    // suffix counts: thread t owns bins [t*PER, t*PER+PER) (all threads when
-    // NB >= 256; threads >= NB own nothing)
+    find_bin<NB>(sh, need);
+    prefix = first ? (uint32_t)sh.bin : ((prefix << BITS) | (uint32_t)sh.bin);
+    need = sh.need;
+    __syncthreads();
+}
+
+// The digit of the need-th largest key from an NB-bin histogram in LDS
+// (bins in ascending key order): sh.bin = that digit, sh.need = how many keys
+// of that bin are still needed.  All threads call.
+template <int NB>
+__device__ void find_bin(IdxShared &sh, int need) {
+    constexpr int PER = NB / kIdxThreads > 0 ? NB / kIdxThreads : 1;
+    const int tid = threadIdx.x;
     int own = 0;
     if (tid * PER < NB)
+#pragma unroll
         for (int i = 0; i < PER; ++i) own += (int)sh.hist[tid * PER + i];
     int total;
     const int excl = block_excl_sum<kIdxThreads>(own, sh.tmp, &total);
-    const int above = total - excl - own;        // keys in bins owned by higher threads
+    const int above = total - excl - own;          // keys in the bins of higher threads
     if (tid * PER < NB && above < need && above + own >= need) {
         int run = above;
         for (int i = PER - 1; i >= 0; --i) {
@@ -338,12 +463,15 @@ __device__ void radix_pass(const float *sc, int e_lo, int e_hi, int shift, uint3
         }
     }
     __syncthreads();
-    prefix = first ? (uint32_t)sh.bin : ((prefix << BITS) | (uint32_t)sh.bin);
-    need = sh.need;
-    __syncthreads();
 }
 
-// Selection of one (sequence, KV head) by the last scoring workgroup.
+// Selection of one (sequence, KV head) by the last scoring workgroup: the
+// top_k eligible blocks by (score desc, index asc) on orderable 32-bit keys.
+// One 12-bit histogram pass finds the bin holding the threshold; the keys of
+// that bin (few, for scores of any spread) are ranked exactly against each
+// other; an ordered compaction emits the winners ascending between the
+// forced sink and window blocks.  A bin of more than kCandMax keys (heavy
+// ties) falls back to two more radix passes and an index-ordered tie count.
 __device__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out, int32_t *nout,
                               IdxShared &sh) {
     const int tid = threadIdx.x;
@@ -355,36 +483,83 @@ __device__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out
         if (tid == 0) *nout = n;
         return;
     }
-    uint32_t prefix = 0;
-    int need = g.topk;
-    radix_pass<12>(sc, r.e_lo, r.e_hi, 20, prefix, need, true, sh);
-    radix_pass<12>(sc, r.e_lo, r.e_hi, 8, prefix, need, false, sh);
-    radix_pass<8>(sc, r.e_lo, r.e_hi, 0, prefix, need, false, sh);
-    const uint32_t T = prefix;
-    // ordered compaction: thread t owns the contiguous range [b0, b1)
+    const bool lds = ne <= kKeysMax;
+    if (lds) {
+#pragma unroll 8
+        for (int i = tid; i < ne; i += kIdxThreads) sh.u.keys[i] = score_key(sc[r.e_lo + i]);
+    }
+    for (int i = tid; i < 4096; i += kIdxThreads) sh.hist[i] = 0u;
+    for (int i = tid; i < kKeysMax / 32; i += kIdxThreads) sh.selbits[i] = 0u;
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+    // pass 1: histogram of the top 12 bits
+    for (int b = r.e_lo + tid; b < r.e_hi; b += kIdxThreads)
+        atomicAdd(&sh.hist[key_at(sh, sc, r.e_lo, b, lds) >> 20], 1u);
+    __syncthreads();
+    find_bin<4096>(sh, g.topk);
+    const uint32_t B = (uint32_t)sh.bin;
+    const int need = sh.need;
+    const int cB = (int)sh.hist[B];
     const int per = (ne + kIdxThreads - 1) / kIdxThreads;
     const int b0 = r.e_lo + tid * per;
     const int b1 = min(b0 + per, r.e_hi);
-    int eq = 0;
-    for (int b = b0; b < b1; ++b) eq += (score_key(sc[b]) == T);
-    int tot;
-    int eqi = block_excl_sum<kIdxThreads>(eq, sh.tmp, &tot);
-    int cnt = 0;
-    {
-        int e2 = eqi;
+    int tot, pos;
+    if (lds && cB <= kCandMax) {
         for (int b = b0; b < b1; ++b) {
-            const uint32_t k = score_key(sc[b]);
-            bool take = k > T;
-            if (k == T) take = (e2++ < need);
-            cnt += take;
+            const uint32_t k = sh.u.keys[b - r.e_lo];
+            if ((k >> 20) == B) {
+                const int slot = atomicAdd(&sh.ncand, 1);
+                sh.cand_key[slot] = k;
+                sh.cand_b[slot] = b;
+            }
         }
-    }
-    int pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
-    for (int b = b0; b < b1; ++b) {
-        const uint32_t k = score_key(sc[b]);
-        bool take = k > T;
-        if (k == T) take = (eqi++ < need);
-        if (take) out[pos++] = b;
+        __syncthreads();
+        if (tid < cB) {
+            const uint32_t k = sh.cand_key[tid];
+            const int b = sh.cand_b[tid];
+            int rank = 0;
+            for (int j = 0; j < cB; ++j) {
+                const uint32_t kj = sh.cand_key[j];
+                rank += (kj > k) || (kj == k && sh.cand_b[j] < b);
+            }
+            if (rank < need) atomicOr(&sh.selbits[(b - r.e_lo) >> 5], 1u << ((b - r.e_lo) & 31));
+        }
+        __syncthreads();
+        auto take = [&](int b) {
+            const uint32_t d = sh.u.keys[b - r.e_lo] >> 20;
+            return d > B || (d == B && ((sh.selbits[(b - r.e_lo) >> 5] >> ((b - r.e_lo) & 31)) & 1u));
+        };
+        int cnt = 0;
+        for (int b = b0; b < b1; ++b) cnt += take(b);
+        pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
+        for (int b = b0; b < b1; ++b)
+            if (take(b) && pos < g.sink + g.topk) out[pos++] = b;
+    } else {
+        uint32_t prefix = B;
+        int need2 = need;
+        radix_pass<12>(sh, sh, sc, r.e_lo, r.e_hi, lds, 8, prefix, need2, false);
+        radix_pass<8>(sh, sh, sc, r.e_lo, r.e_hi, lds, 0, prefix, need2, false);
+        const uint32_t T = prefix;
+        int eq = 0;
+        for (int b = b0; b < b1; ++b) eq += (key_at(sh, sc, r.e_lo, b, lds) == T);
+        int eqi = block_excl_sum<kIdxThreads>(eq, sh.tmp, &tot);
+        int cnt = 0;
+        {
+            int e2 = eqi;
+            for (int b = b0; b < b1; ++b) {
+                const uint32_t k = key_at(sh, sc, r.e_lo, b, lds);
+                bool tk = k > T;
+                if (k == T) tk = (e2++ < need2);
+                cnt += tk;
+            }
+        }
+        pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
+        for (int b = b0; b < b1; ++b) {
+            const uint32_t k = key_at(sh, sc, r.e_lo, b, lds);
+            bool tk = k > T;
+            if (k == T) tk = (eqi++ < need2);
+            if (tk && pos < g.sink + g.topk) out[pos++] = b;
+        }
     }
     for (int i = tid; i < g.sink; i += kIdxThreads) out[i] = i;
     const int nwin = r.b_last - r.fw + 1;
@@ -393,9 +568,9 @@ __device__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out
 }
 
 // grid (n_chunks [+1 with the fused append], Hkv, n_seq)
-template <int G>
+template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
-k_indexer(Geo g, qwfn_kv_view v, const float *q, const int32_t *seq_len, int32_t max_seq_len,
+k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
           int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t n_chunks, FusedAppend fa) {
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
@@ -403,38 +578,43 @@ k_indexer(Geo g, qwfn_kv_view v, const float *q, const int32_t *seq_len, int32_t
     const int L = seq_len[s];
     const bool ok = L >= 1 && L <= max_seq_len;
     if (fa.enabled && c == n_chunks) {             // the append workgroup
-        if (ok) fused_append_pool(g, v, fa, s, gh, L, sh);
+        if (ok) fused_append_pool<HD>(g, v, fa, s, gh, L, sh);
         return;
     }
     const int pair = s * g.Hkv + gh;
     float *sc = ws.scores + (int64_t)pair * ws.nb_cap;
+    // The pooled keys this lane scores do not depend on the sequence length
+    // (eligible blocks start at sink_blocks), so their loads go out together
+    // with the length's; the length only decides which scores are kept.
+    const int bl = tid >> 2, j = tid & 3;
+    const int bi = c * kBlocksPerChunk + bl;
+    const int bp = min(g.sink + bi, g.bps - 1);
+    const float *P = v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + bp) * HD;
+    float4 p4[HD / 16];
+#pragma unroll
+    for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
     if (ok && g.topk > 0) {
         const Ranges r = qsa_ranges(g, L);
         const int ne = r.e_hi - r.e_lo;
         if (ne > g.topk && c * kBlocksPerChunk < ne) {
-            const float *qg = q + ((int64_t)s * g.H + (int64_t)gh * G) * g.hd;
-            for (int i = tid * 4; i < G * g.hd; i += kIdxThreads * 4)
-                *reinterpret_cast<float4 *>(&sh.q[i]) = *reinterpret_cast<const float4 *>(qg + i);
-            __syncthreads();
-            const int bl = tid >> 2, j = tid & 3;
-            const int bi = c * kBlocksPerChunk + bl;
             const bool act = bi < ne;
-            const int b = r.e_lo + (act ? bi : 0);
-            const float *P = v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + b) * g.hd;
+            const int b = r.e_lo + bi;
+            const float *qg = q + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
+            for (int i = tid * 4; i < G * HD; i += kIdxThreads * 4)
+                *reinterpret_cast<float4 *>(&sh.u.q[i]) = *reinterpret_cast<const float4 *>(qg + i);
+            __syncthreads();
             float acc[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) acc[h] = 0.0f;
-            if (act) {
-                for (int i = 0; i < g.hd / 16; ++i) {
-                    const float4 p4 = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
 #pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        const float4 q4 = *reinterpret_cast<const float4 *>(&sh.q[h * g.hd + 16 * i + 4 * j]);
-                        acc[h] = fmaf(q4.x, p4.x, acc[h]);
-                        acc[h] = fmaf(q4.y, p4.y, acc[h]);
-                        acc[h] = fmaf(q4.z, p4.z, acc[h]);
-                        acc[h] = fmaf(q4.w, p4.w, acc[h]);
-                    }
+            for (int i = 0; i < HD / 16; ++i) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float4 q4 = *reinterpret_cast<const float4 *>(&sh.u.q[h * HD + 16 * i + 4 * j]);
+                    acc[h] = fmaf(q4.x, p4[i].x, acc[h]);
+                    acc[h] = fmaf(q4.y, p4[i].y, acc[h]);
+                    acc[h] = fmaf(q4.z, p4[i].z, acc[h]);
+                    acc[h] = fmaf(q4.w, p4[i].w, acc[h]);
                 }
             }
             float score = 0.0f;
@@ -446,18 +626,11 @@ k_indexer(Geo g, qwfn_kv_view v, const float *q, const int32_t *seq_len, int32_t
                 score = (h == 0) ? dot : score + dot;
             }
             if (act && j == 0) sc[b] = score;
+            __syncthreads();                       // q reads done before the union is reused
         }
     }
     // completion count: the last workgroup of this (sequence, KV head) selects
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int old = atomicAdd(&ws.cnt_idx[pair], 1);
-        sh.flag = (old == n_chunks - 1);
-    }
-    __syncthreads();
-    if (!sh.flag) return;
-    __threadfence();
+    if (!arrive_last(&ws.cnt_idx[pair], n_chunks, &sh.flag)) return;
     if (tid == 0) ws.cnt_idx[pair] = 0;
     int32_t *out = sel + (int64_t)pair * max_sel;
     if (!ok) {
@@ -467,8 +640,8 @@ k_indexer(Geo g, qwfn_kv_view v, const float *q, const int32_t *seq_len, int32_t
     select_blocks(g, sc, L, out, nsel + pair, sh);
 }
 
-template <int G>
-static void launch_indexer_g(const Geo &g, const qwfn_kv_view &v, const float *q,
+template <int HD, int G>
+static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                              int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                              const FusedAppend &fa, hipStream_t st) {
@@ -476,45 +649,60 @@ static void launch_indexer_g(const Geo &g, const qwfn_kv_view &v, const float *q
     int n_chunks = (nb_max + kBlocksPerChunk - 1) / kBlocksPerChunk;
     if (n_chunks < 1) n_chunks = 1;
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
-    hipLaunchKernelGGL(k_indexer<G>, grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
+    hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
                        sel, nsel, max_sel, ws, n_chunks, fa);
 }
 
 // ---------------------------------------------------------------------------
-// attention: one 64-cell tile per workgroup, partial softmax state per tile,
-// the last workgroup of a (sequence, KV head) merges the partials
+// attention: TG groups of NW waves per workgroup, one 64-cell tile per group;
+// the groups merge in LDS into one partial softmax state per workgroup, and
+// the last workgroup of a (sequence, KV head) merges the partials.
 // ---------------------------------------------------------------------------
 
-template <int HD, int G>
+template <int HD, int G, int TG>
 struct AttnCfg {
-    static constexpr int NW = G >= 4 ? 4 : G;          // waves per workgroup
+    static constexpr int NW = G >= 4 ? 4 : G;          // waves per group
     static constexpr int HPW = G / NW;                 // query heads per wave
-    static constexpr int NT = NW * 64;
+    static constexpr int NTG = NW * 64;                // threads per group
+    static constexpr int NT = TG * NTG;                // threads per workgroup
     static constexpr int CH = HD / 16;                 // 16-byte chunks per head row
     static constexpr int ROWF = HD + 4;                // padded LDS row (floats)
     static constexpr int DPL = HD / 64;                // PV dims per lane
+    static constexpr int PER = (64 * CH + NTG - 1) / NTG;   // 16-byte K (and V) loads per thread
+    static constexpr int MAXP = 32;                    // partials a combine thread prefetches
+    static constexpr int OPT = (G * HD + NT - 1) / NT; // merged outputs per thread
     static_assert(G % NW == 0, "group size");
     static_assert(HD % 64 == 0, "head_dim");
 };
 
 template <int HD, int G>
-struct AttnShared {
-    float kv[64 * AttnCfg<HD, G>::ROWF];
+struct AttnGroup {
+    float kv[64 * (HD + 4)];                   // K' then V' (dequantized), then the group's O
     float p[G][64];
     uint16_t ksc[64][HD / 32], vsc[64][HD / 32];
-    int32_t kpage[64], row[64];
+    int32_t page[64], row[64];
+    float m[G], l[G];
+};
+
+template <int HD, int G, int TG>
+struct AttnShared {
+    AttnGroup<HD, G> grp[TG];
+    float q[G * HD];                           // the KV head's query heads
     float Mh[G], Lh[G];
     int flag;
 };
 
-template <int HD, int G>
-__global__ void __launch_bounds__((AttnCfg<HD, G>::NT))
+template <int HD, int G, int TG>
+__global__ void __launch_bounds__((AttnCfg<HD, G, TG>::NT))
 k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len,
        int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
-       float *__restrict__ out, Ws ws, int32_t n_tiles) {
-    using C = AttnCfg<HD, G>;
-    __shared__ AttnShared<HD, G> sh;
-    const int tid = threadIdx.x, tile = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
+       float *__restrict__ out, Ws ws, int32_t n_parts) {
+    using C = AttnCfg<HD, G, TG>;
+    __shared__ AttnShared<HD, G, TG> sh;
+    const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);   // tile group (wave-uniform)
+    const int lt = tid % C::NTG;
+    AttnGroup<HD, G> &gr = sh.grp[gi];
     const int pair = s * g.Hkv + gh;
     const int L = seq_len[s];
     const bool ok = L >= 1 && L <= max_seq_len;
@@ -524,113 +712,118 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         n = n < max_sel ? n : max_sel;
     }
     const int tiles_act = (n * g.bt + 63) / 64;
-    if (ok && tile < tiles_act) {
-        // cells of this tile -> (token, K page, V page)
-        if (tid < 64) {
-            const int cidx = tile * 64 + tid, slot = cidx / g.bt;
-            int kp = -1, rw = -1;
-            if (slot < n) {
+    const int parts_act = (tiles_act + TG - 1) / TG;
+    const int part = blockIdx.x;
+    if (ok && part < parts_act) {
+        {   // the group of query heads, staged once for all waves
+            const float *qg = q + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
+            for (int i = tid * 4; i < G * HD; i += C::NT * 4)
+                *reinterpret_cast<float4 *>(&sh.q[i]) = *reinterpret_cast<const float4 *>(qg + i);
+        }
+        const int tile = part * TG + gi;
+        const bool active = tile < tiles_act;
+        // cells of this group's tile -> (physical page, row) or row -1
+        if (lt < 64) {
+            int pg = -1, rw = -1;
+            const int cidx = tile * 64 + lt, slot = cidx / g.bt;
+            if (active && slot < n) {
                 const int blk = sel ? sel[(int64_t)pair * max_sel + slot] : slot;
                 const int t = blk * g.bt + cidx % g.bt;
                 if (blk >= 0 && t < L) {
-                    kp = phys_page(g, v.page_table, s, t);
+                    pg = phys_page(g, v.page_table, s, t);
                     rw = t % g.pt;
-                    if (kp < 0) { set_status(v.status, QWFN_STATUS_PAGE_RANGE); rw = -1; }
+                    if (pg < 0) { set_status(v.status, QWFN_STATUS_PAGE_RANGE); rw = -1; }
                 }
             }
-            sh.kpage[tid] = kp;
-            sh.row[tid] = rw;
+            gr.page[lt] = pg;
+            gr.row[lt] = rw;
         }
         __syncthreads();
-        // issue every global load of the tile before any use
-        constexpr int PER = (64 * C::CH + C::NT - 1) / C::NT;
-        uint4 kq[PER], vq[PER];
+        // every global load of the tile is issued before any is consumed
+        uint4 kq[C::PER], vq[C::PER];
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int k = tid + i * C::NT;
+        for (int i = 0; i < C::PER; ++i) {
+            const int k = lt + i * C::NTG;
             kq[i] = make_uint4(0, 0, 0, 0);
             vq[i] = make_uint4(0, 0, 0, 0);
             if (k < 64 * C::CH) {
-                const int cell = k % 64, ch = k / 64, rw = sh.row[cell];
+                const int cell = k % 64, ch = k / 64, rw = gr.row[cell];
                 if (rw >= 0) {
-                    const int64_t off = (int64_t)sh.kpage[cell] * g.page_bytes +
-                                        ((int64_t)(gh * (g.pt / 64) + rw / 64) * C::CH + ch) * 1024 +
-                                        (rw % 64) * 16;
+                    const int64_t off = (int64_t)gr.page[cell] * g.page_bytes +
+                                        ((int64_t)(gh * (g.pt / 64) + rw / 64) * C::CH + ch) * 1024 + (rw % 64) * 16;
                     kq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.k_pages + off);
                     vq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.v_pages + off);
                 }
             }
         }
-        for (int k = tid; k < 128; k += C::NT) {
-            const int cell = k % 64, rw = sh.row[cell];
+        for (int k = lt; k < 128; k += C::NTG) {
+            const int cell = k % 64, rw = gr.row[cell];
             const bool isv = k >= 64;
-            uint16_t *dst = isv ? sh.vsc[cell] : sh.ksc[cell];
+            uint16_t *dst = isv ? gr.vsc[cell] : gr.ksc[cell];
             if (rw >= 0) {
-                const uint8_t *base = (const uint8_t *)(isv ? v.v_pages : v.k_pages) +
-                                      (int64_t)sh.kpage[cell] * g.page_bytes +
-                                      g.qbytes + ((int64_t)(gh * g.pt + rw) * (HD / 32)) * 2;
+                const uint16_t *src = reinterpret_cast<const uint16_t *>(
+                    (const uint8_t *)(isv ? v.v_pages : v.k_pages) + (int64_t)gr.page[cell] * g.page_bytes +
+                    g.qbytes + ((int64_t)(gh * g.pt + rw) * (HD / 32)) * 2);
 #pragma unroll
-                for (int jj = 0; jj < HD / 32; ++jj) dst[jj] = reinterpret_cast<const uint16_t *>(base)[jj];
+                for (int jj = 0; jj < HD / 32; ++jj) dst[jj] = src[jj];
             } else {
 #pragma unroll
                 for (int jj = 0; jj < HD / 32; ++jj) dst[jj] = 0;
             }
         }
         __syncthreads();
-        // dequantize K into LDS (exact: fp16 scale times int8)
+        // dequantize (exact: fp16 scale times int8) into the group's LDS tile
         auto dequant = [&](const uint4 *qv, uint16_t (*scl)[HD / 32]) {
 #pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const int k = tid + i * C::NT;
+            for (int i = 0; i < C::PER; ++i) {
+                const int k = lt + i * C::NTG;
                 if (k < 64 * C::CH) {
                     const int cell = k % 64, ch = k / 64;
-                    const float sc = h2f(scl[cell][ch / 2]);
+                    const float scf = h2f(scl[cell][ch / 2]);
                     const uint32_t w[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
-                    float *dst = &sh.kv[cell * C::ROWF + ch * 16];
+                    float *dst = &gr.kv[cell * C::ROWF + ch * 16];
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         float4 f;
-                        f.x = sc * (float)(int8_t)(w[u] & 0xFF);
-                        f.y = sc * (float)(int8_t)((w[u] >> 8) & 0xFF);
-                        f.z = sc * (float)(int8_t)((w[u] >> 16) & 0xFF);
-                        f.w = sc * (float)(int8_t)(w[u] >> 24);
+                        f.x = scf * (float)(int8_t)(w[u] & 0xFF);
+                        f.y = scf * (float)(int8_t)((w[u] >> 8) & 0xFF);
+                        f.z = scf * (float)(int8_t)((w[u] >> 16) & 0xFF);
+                        f.w = scf * (float)(int8_t)(w[u] >> 24);
                         *reinterpret_cast<float4 *>(dst + 4 * u) = f;
                     }
                 }
             }
         };
-        dequant(kq, sh.ksc);
+        dequant(kq, gr.ksc);
         __syncthreads();
-        // QK: lane = cell, wave w owns heads [w*HPW, (w+1)*HPW)
-        const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+        // QK: lane = cell, wave w of the group owns heads [w*HPW, (w+1)*HPW)
+        const int w = __builtin_amdgcn_readfirstlane(lt >> 6), lane = lt & 63;
         const int h0 = w * C::HPW;
-        const float *qg = q + ((int64_t)s * g.H + (int64_t)gh * G + h0) * HD;
         float sacc[C::HPW];
 #pragma unroll
         for (int hh = 0; hh < C::HPW; ++hh) sacc[hh] = 0.0f;
-        const float *krow = &sh.kv[lane * C::ROWF];
-#pragma unroll 8
+        const float *krow = &gr.kv[lane * C::ROWF];
+#pragma unroll 4
         for (int d4 = 0; d4 < HD / 4; ++d4) {
             const float4 kf = *reinterpret_cast<const float4 *>(krow + 4 * d4);
 #pragma unroll
             for (int hh = 0; hh < C::HPW; ++hh) {
-                const float4 qv = *reinterpret_cast<const float4 *>(qg + hh * HD + 4 * d4);
+                const float4 qv = *reinterpret_cast<const float4 *>(&sh.q[(h0 + hh) * HD + 4 * d4]);
                 sacc[hh] += qv.x * kf.x + qv.y * kf.y + qv.z * kf.z + qv.w * kf.w;
             }
         }
-        const bool valid = sh.row[lane] >= 0;
-        float m_h[C::HPW], l_h[C::HPW];
+        const bool valid = gr.row[lane] >= 0;
 #pragma unroll
         for (int hh = 0; hh < C::HPW; ++hh) {
             const float s2 = valid ? sacc[hh] * g.scale_log2 : -INFINITY;
             const float m = wave_max(s2);
             const float p = valid ? exp2f(s2 - m) : 0.0f;
-            m_h[hh] = m;
-            l_h[hh] = wave_sum(p);
-            sh.p[h0 + hh][lane] = p;
+            const float l = wave_sum(p);
+            gr.p[h0 + hh][lane] = p;
+            if (lane == 0) { gr.m[h0 + hh] = m; gr.l[h0 + hh] = l; }
         }
         __syncthreads();                          // K reads done, p visible
-        dequant(vq, sh.vsc);
+        dequant(vq, gr.vsc);
         __syncthreads();
         // PV: lane owns DPL consecutive dims of each of the wave's heads
         float o[C::HPW][C::DPL];
@@ -638,106 +831,149 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         for (int hh = 0; hh < C::HPW; ++hh)
 #pragma unroll
             for (int k = 0; k < C::DPL; ++k) o[hh][k] = 0.0f;
-#pragma unroll 4
-        for (int cell = 0; cell < 64; ++cell) {
-            float vv[C::DPL];
+#pragma unroll 2
+        for (int c4 = 0; c4 < 64; c4 += 4) {
+            float4 p4[C::HPW];
 #pragma unroll
-            for (int k = 0; k < C::DPL; ++k) vv[k] = sh.kv[cell * C::ROWF + lane * C::DPL + k];
+            for (int hh = 0; hh < C::HPW; ++hh) p4[hh] = *reinterpret_cast<const float4 *>(&gr.p[h0 + hh][c4]);
 #pragma unroll
-            for (int hh = 0; hh < C::HPW; ++hh) {
-                const float p = sh.p[h0 + hh][cell];
+            for (int cc = 0; cc < 4; ++cc) {
+                float vv[C::DPL];
 #pragma unroll
-                for (int k = 0; k < C::DPL; ++k) o[hh][k] += p * vv[k];
+                for (int k = 0; k < C::DPL; ++k) vv[k] = gr.kv[(c4 + cc) * C::ROWF + lane * C::DPL + k];
+#pragma unroll
+                for (int hh = 0; hh < C::HPW; ++hh) {
+                    const float p = cc == 0 ? p4[hh].x : cc == 1 ? p4[hh].y : cc == 2 ? p4[hh].z : p4[hh].w;
+#pragma unroll
+                    for (int k = 0; k < C::DPL; ++k) o[hh][k] += p * vv[k];
+                }
             }
         }
-        const int64_t tb = ((int64_t)pair * n_tiles + tile) * G;
+        __syncthreads();                          // V' reads done: kv becomes the group's O
 #pragma unroll
-        for (int hh = 0; hh < C::HPW; ++hh) {
+        for (int hh = 0; hh < C::HPW; ++hh)
 #pragma unroll
-            for (int k = 0; k < C::DPL; ++k)
-                ws.part_o[(tb + h0 + hh) * HD + lane * C::DPL + k] = o[hh][k];
-            if (lane == 0) {
-                ws.part_ml[(tb + h0 + hh) * 2 + 0] = m_h[hh];
-                ws.part_ml[(tb + h0 + hh) * 2 + 1] = l_h[hh];
+            for (int k = 0; k < C::DPL; ++k) gr.kv[(h0 + hh) * HD + lane * C::DPL + k] = o[hh][k];
+        __syncthreads();
+        // merge the TG groups into this workgroup's partial (unnormalised O, max, sum)
+        const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
+#pragma unroll
+        for (int r = 0; r < C::OPT; ++r) {
+            const int k = tid + r * C::NT;
+            if (k < G * HD) {
+                const int h = k / HD;
+                float M = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < TG; ++t)
+                    if (part * TG + t < tiles_act) M = fmaxf(M, sh.grp[t].m[h]);
+                float O = 0.0f, Ls = 0.0f;
+#pragma unroll
+                for (int t = 0; t < TG; ++t) {
+                    if (part * TG + t < tiles_act) {
+                        const float mt = sh.grp[t].m[h];
+                        const float wt = mt == -INFINITY ? 0.0f : exp2f(mt - M);
+                        O += wt * sh.grp[t].kv[k];
+                        Ls += wt * sh.grp[t].l[h];
+                    }
+                }
+                ws.part_o[pb * HD + k] = O;
+                if (k % HD == 0) {
+                    ws.part_ml[(pb + h) * 2 + 0] = M;
+                    ws.part_ml[(pb + h) * 2 + 1] = Ls;
+                }
             }
         }
     }
-    // completion count; the last workgroup of the pair merges
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int old = atomicAdd(&ws.cnt_attn[pair], 1);
-        sh.flag = (old == (int)gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!sh.flag) return;
-    __threadfence();
+    // completion count; the last workgroup of the pair merges the partials
+    if (!arrive_last(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
     if (tid == 0) ws.cnt_attn[pair] = 0;
     float *og = out + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
-    if (!ok || tiles_act == 0) {
+    if (!ok || parts_act == 0) {
         for (int i = tid; i < G * HD; i += C::NT) og[i] = 0.0f;
         if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    // merge: M = max_i m_i, w_i = exp2(m_i - M), O = sum_i w_i O_i / sum_i w_i l_i,
-    // the weights staged through LDS (the kv tile) one chunk of tiles at a time
-    const int64_t pb = (int64_t)pair * n_tiles * G;
+    // M_h = max_i m_i, w_i = exp2(m_i - M_h), O = sum_i w_i O_i / sum_i w_i l_i;
+    // the partials' O values a thread needs are loaded together with the maxima
+    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
+    float ov[C::OPT][C::MAXP];
+#pragma unroll
+    for (int r = 0; r < C::OPT; ++r) {
+        const int k = tid + r * C::NT;
+#pragma unroll
+        for (int i = 0; i < C::MAXP; ++i)
+            ov[r][i] = (k < G * HD && i < parts_act) ? ws.part_o[(pb + (int64_t)i * G) * HD + k] : 0.0f;
+    }
+    float *ml = sh.grp[0].kv;                    // [parts][G][2] maxima and sums, then weights
+    const int nml = min(parts_act, (64 * C::ROWF) / (3 * G));
+    for (int k = tid; k < nml * G * 2; k += C::NT) ml[k] = ws.part_ml[pb * 2 + k];
+    __syncthreads();
+    float *wt = ml + nml * G * 2;                // [parts][G] weights
     if (tid < G) {
         float M = -INFINITY;
-        for (int i = 0; i < tiles_act; ++i) M = fmaxf(M, ws.part_ml[(pb + (int64_t)i * G + tid) * 2]);
+        for (int i = 0; i < parts_act; ++i)
+            M = fmaxf(M, i < nml ? ml[(i * G + tid) * 2] : ws.part_ml[(pb + (int64_t)i * G + tid) * 2]);
         sh.Mh[tid] = M;
-        sh.Lh[tid] = 0.0f;
     }
     __syncthreads();
-    constexpr int CHK = (64 * C::ROWF) / G;
-    constexpr int OPT = (G * HD + C::NT - 1) / C::NT;
-    float *wts = sh.kv;
-    float acc[OPT];
-#pragma unroll
-    for (int r = 0; r < OPT; ++r) acc[r] = 0.0f;
-    for (int i0 = 0; i0 < tiles_act; i0 += CHK) {
-        const int ni = min(CHK, tiles_act - i0);
-        for (int k = tid; k < ni * G; k += C::NT) {
-            const int h = k % G;
-            const float m = ws.part_ml[(pb + (int64_t)(i0 + k / G) * G + h) * 2];
-            wts[k] = (m == -INFINITY) ? 0.0f : exp2f(m - sh.Mh[h]);
-        }
-        __syncthreads();
-        if (tid < G) {
-            float Ls = sh.Lh[tid];
-            for (int i = 0; i < ni; ++i)
-                Ls += wts[i * G + tid] * ws.part_ml[(pb + (int64_t)(i0 + i) * G + tid) * 2 + 1];
-            sh.Lh[tid] = Ls;
-        }
-#pragma unroll
-        for (int r = 0; r < OPT; ++r) {
-            const int k = tid + r * C::NT;
-            if (k < G * HD) {
-                const int h = k / HD, d = k % HD;
-                for (int i = 0; i < ni; ++i)
-                    acc[r] += wts[i * G + h] * ws.part_o[(pb + (int64_t)(i0 + i) * G + h) * HD + d];
-            }
-        }
-        __syncthreads();
+    for (int k = tid; k < nml * G; k += C::NT) {
+        const float m = ml[k * 2];
+        wt[k] = m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[k % G]);
     }
+    __syncthreads();
+    if (tid < G) {
+        float Ls = 0.0f;
+        for (int i = 0; i < parts_act; ++i) {
+            float wi, li;
+            if (i < nml) { wi = wt[i * G + tid]; li = ml[(i * G + tid) * 2 + 1]; }
+            else {
+                const float m = ws.part_ml[(pb + (int64_t)i * G + tid) * 2];
+                wi = m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[tid]);
+                li = ws.part_ml[(pb + (int64_t)i * G + tid) * 2 + 1];
+            }
+            Ls += wi * li;
+        }
+        sh.Lh[tid] = Ls;
+    }
+    __syncthreads();
 #pragma unroll
-    for (int r = 0; r < OPT; ++r) {
+    for (int r = 0; r < C::OPT; ++r) {
         const int k = tid + r * C::NT;
         if (k < G * HD) {
-            const float Ls = sh.Lh[k / HD];
-            og[k] = Ls > 0.0f ? acc[r] / Ls : 0.0f;
+            const int h = k / HD;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < C::MAXP; ++i)
+                if (i < parts_act) acc += (i < nml ? wt[i * G + h] : 0.0f) * ov[r][i];
+            for (int i = C::MAXP; i < parts_act; ++i) {
+                float wi;
+                if (i < nml) wi = wt[i * G + h];
+                else {
+                    const float m = ws.part_ml[(pb + (int64_t)i * G + h) * 2];
+                    wi = m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[h]);
+                }
+                acc += wi * ws.part_o[(pb + (int64_t)i * G) * HD + k];
+            }
+            // parts below MAXP but beyond the LDS-staged weights
+            for (int i = nml; i < min(parts_act, C::MAXP); ++i) {
+                const float m = ws.part_ml[(pb + (int64_t)i * G + h) * 2];
+                acc += (m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[h])) * ov[r][i];
+            }
+            const float Ls = sh.Lh[h];
+            og[k] = Ls > 0.0f ? acc / Ls : 0.0f;
         }
     }
 }
 
-template <int HD, int G>
+template <int HD, int G, int TG>
 static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
                           const Ws &ws, hipStream_t st) {
-    const dim3 grid((unsigned)ws.n_tiles, (unsigned)g.Hkv, (unsigned)n_seq);
-    hipLaunchKernelGGL((k_attn<HD, G>), grid, dim3(AttnCfg<HD, G>::NT), 0, st, g, v, q, seq_len,
-                       max_seq_len, sel, nsel, max_sel, out, ws, ws.n_tiles);
+    const int n_parts = (ws.n_tiles + TG - 1) / TG;
+    const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
+    hipLaunchKernelGGL((k_attn<HD, G, TG>), grid, dim3(AttnCfg<HD, G, TG>::NT), 0, st, g, v, q, seq_len,
+                       max_seq_len, sel, nsel, max_sel, out, ws, n_parts);
 }
 
 // ---------------------------------------------------------------------------
@@ -786,36 +1022,50 @@ hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq
 // dispatch over the instantiated (head_dim, group) pairs
 // ---------------------------------------------------------------------------
 
-#define QWFN_FOR_EACH_SHAPE(X) X(128, 8) X(128, 4) X(128, 2) X(64, 8) X(256, 12) X(256, 8)
+// (head_dim, group, tile groups per attention workgroup)
+#define QWFN_FOR_EACH_SHAPE(X) X(128, 8, 4) X(128, 4, 4) X(128, 2, 4) X(64, 8, 4) X(256, 12, 2) X(256, 8, 2)
 
 bool kernels_for(int32_t hd, int32_t G) {
-#define X(HD_, G_) if (hd == HD_ && G == G_) return true;
+#define X(HD_, G_, TG_) if (hd == HD_ && G == G_) return true;
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
     return false;
+}
+
+hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
+                       const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
+                       hipStream_t st) {
+    const dim3 grid((unsigned)n_blocks, (unsigned)g.Hkv);
+    switch (g.hd) {
+    case 64:  hipLaunchKernelGGL(k_pool<64>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const); break;
+    case 128: hipLaunchKernelGGL(k_pool<128>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const); break;
+    case 256: hipLaunchKernelGGL(k_pool<256>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                           const FusedAppend &fa, hipStream_t st) {
-    switch (g.G) {
-    case 2:  launch_indexer_g<2>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); break;
-    case 4:  launch_indexer_g<4>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); break;
-    case 8:  launch_indexer_g<8>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); break;
-    case 12: launch_indexer_g<12>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); break;
-    default: return hipErrorInvalidValue;
+#define X(HD_, G_, TG_)                                                                          \
+    if (g.hd == HD_ && g.G == G_) {                                                              \
+        launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); \
+        return hipGetLastError();                                                                \
     }
-    return hipGetLastError();
+    QWFN_FOR_EACH_SHAPE(X)
+#undef X
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,
                             float *out, const Ws &ws, hipStream_t st) {
-#define X(HD_, G_)                                                                              \
+#define X(HD_, G_, TG_)                                                                         \
     if (g.hd == HD_ && g.G == G_) {                                                             \
-        launch_attn_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
+        launch_attn_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
         return hipGetLastError();                                                               \
     }
     QWFN_FOR_EACH_SHAPE(X)

@@ -26,7 +26,7 @@ from ._lib import KvView, QsaShape, call
 __all__ = [
     "QsaConfig", "KvCache", "KvState", "Workspace",
     "append_q8_0", "pool_update", "pool_rebuild", "indexer_topk", "gather_dequant",
-    "sparse_decode_attn", "sparse_attn_decode", "read_status",
+    "sparse_decode_attn", "decode_append_select", "sparse_attn_decode", "read_status",
 ]
 
 
@@ -348,6 +348,29 @@ def sparse_attn_decode(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_n
          seq_len.data_ptr(), n_seq, max_seq_len, out.data_ptr(), _ptr(sel), _ptr(n_sel), ws.ptr(),
          ws.nbytes, _stream(stream))
     return out
+
+
+def decode_append_select(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                         seq_len: torch.Tensor, max_seq_len: int, ws: Workspace, sel: torch.Tensor,
+                         n_sel: torch.Tensor, stream=None) -> None:
+    """The first launch of :func:`sparse_attn_decode`: append at seq_len-1, pool
+    on block completion, score and select into sel / n_sel
+    (src/qwfn_graph.cpp:465-495, 520-528)."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    _need(q, "q", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype:
+        raise TypeError("k_new and v_new must both be float32 or both float16")
+    _need(k_new, "k_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(v_new, "v_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    _need(sel, "sel", torch.int32)
+    _need(n_sel, "n_sel", torch.int32, n_seq * cfg.n_head_kv)
+    s = cfg.shape()
+    call("qwfn_decode_append_select", C.byref(s), C.byref(cache.view()), q.data_ptr(), k_new.data_ptr(),
+         v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,
+         seq_len.data_ptr(), n_seq, max_seq_len, sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], ws.ptr(),
+         ws.nbytes, _stream(stream))
 
 
 def read_status(cache: KvCache, stream=None) -> int:
