@@ -58,7 +58,7 @@ def lib() -> C.CDLL:
             "qwfn_oracle_quantize_block": (None, [P, I, P, P]),
             "qwfn_oracle_quantize_row_ggml": (None, [P, C.c_int64, I, P]),
             "qwfn_oracle_page_bytes": (C.c_size_t, [S]),
-            "qwfn_oracle_quant_offset": (C.c_int64, [S, I, I, I]),
+            "qwfn_oracle_quant_offset": (C.c_int64, [S, I, I, I, I]),
             "qwfn_oracle_scale_offset": (C.c_int64, [S, I, I, I]),
             "qwfn_oracle_append": (C.c_int, [S, V, P, P, I, P, P, I]),
             "qwfn_oracle_dequant_row": (C.c_int, [S, V, P, I, I, I, P]),
@@ -253,9 +253,9 @@ def max_selected(cfg, max_seq_len: int) -> int:
     return int(lib().qwfn_oracle_max_selected(C.byref(s), max_seq_len))
 
 
-def quant_offset(cfg, g: int, row: int, d: int) -> int:
+def quant_offset(cfg, g: int, row: int, d: int, which: int = 0) -> int:
     s = shape_of(cfg)
-    return int(lib().qwfn_oracle_quant_offset(C.byref(s), g, row, d))
+    return int(lib().qwfn_oracle_quant_offset(C.byref(s), which, g, row, d))
 
 
 def scale_offset(cfg, g: int, row: int, j: int) -> int:

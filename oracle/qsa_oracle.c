@@ -133,9 +133,11 @@ size_t qwfn_oracle_page_bytes(const qwfn_qsa_shape *s) {
            (size_t)s->n_head_kv * (size_t)s->page_tokens * (size_t)(s->head_dim / 32) * 2u;
 }
 
-int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
-                                 int32_t d) {
+int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t which, int32_t g,
+                                 int32_t row, int32_t d) {
     const int64_t tiles = s->page_tokens / 64, chunks = s->head_dim / 16;
+    if (which && s->block_tokens % 64 == 0)       /* V, dim-major 64-token tiles */
+        return (((int64_t)g * tiles + row / 64) * s->head_dim + d) * 64 + row % 64;
     return (((int64_t)g * tiles + row / 64) * chunks + d / 16) * 1024 +
            (int64_t)(row % 64) * 16 + d % 16;
 }
@@ -188,7 +190,7 @@ int qwfn_oracle_append(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                     qwfn_oracle_quantize_block(x, s->quant_variant, &d, qs);
                     memcpy(page + qwfn_oracle_scale_offset(s, g, row, j), &d, 2);
                     for (int e = 0; e < 32; e++)
-                        page[qwfn_oracle_quant_offset(s, g, row, 32 * j + e)] = (uint8_t)qs[e];
+                        page[qwfn_oracle_quant_offset(s, which, g, row, 32 * j + e)] = (uint8_t)qs[e];
                 }
         }
     }
@@ -203,10 +205,11 @@ int qwfn_oracle_dequant_row(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
     const uint8_t *page = page_of(s, v, pool, seq, t, &status);
     if (!page) return status;
     const int32_t row = t % s->page_tokens;
+    const int32_t which = pool == v->v_pages;
     for (int32_t d = 0; d < s->head_dim; d++) {
         uint16_t h;
         memcpy(&h, page + qwfn_oracle_scale_offset(s, g, row, d / 32), 2);
-        const int8_t q = (int8_t)page[qwfn_oracle_quant_offset(s, g, row, d)];
+        const int8_t q = (int8_t)page[qwfn_oracle_quant_offset(s, which, g, row, d)];
         out[d] = qwfn_oracle_f16_to_f32(h) * (float)q;
     }
     return 0;

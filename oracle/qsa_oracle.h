@@ -49,10 +49,11 @@ void qwfn_oracle_quantize_block(const float *x, int32_t variant, uint16_t *d,
 void qwfn_oracle_quantize_row_ggml(const float *x, int64_t n, int32_t variant,
                                    uint8_t *out);
 
-/* Byte offsets inside one page (see include/qwfn_qsa.h). */
+/* Byte offsets inside one page (see include/qwfn_qsa.h); which = 0 for a K
+ * page, 1 for a V page (V quants are dim-major when block_tokens % 64 == 0). */
 size_t  qwfn_oracle_page_bytes(const qwfn_qsa_shape *s);
-int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
-                                 int32_t d);
+int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t which, int32_t g,
+                                 int32_t row, int32_t d);
 int64_t qwfn_oracle_scale_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
                                  int32_t j);
 

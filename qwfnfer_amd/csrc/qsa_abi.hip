@@ -94,6 +94,7 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * s->head_dim;
     g->page_bytes = g->qbytes + (int64_t)s->n_head_kv * s->page_tokens * (s->head_dim / 32) * 2;
     g->inv_bt = 1.0f / (float)s->block_tokens;
+    g->vdim = s->block_tokens % 64 == 0;
     g->scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)s->head_dim));
     if (v) {
         g->pps = v->pages_per_seq; g->n_phys = v->n_phys_pages; g->n_seq_view = v->n_seq;

@@ -19,6 +19,7 @@ struct Geo {
     int32_t relu, variant;           // indexer relu, q8_0 rounding
     int32_t pps, n_phys, n_seq_view; // pages per sequence, pool pages, view seqs
     int32_t bps;                     // pooled blocks per sequence
+    int32_t vdim;                    // V quants dim-major per 64-token tile (bt % 64 == 0)
     int64_t page_bytes, qbytes;      // page size, quant bytes per page
     float inv_bt;                    // 1.0f / block_tokens (host-rounded)
     float scale_log2;                // log2(e) / sqrt(head_dim)

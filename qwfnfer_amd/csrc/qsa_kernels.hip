@@ -25,6 +25,12 @@ __device__ __forceinline__ int64_t quant_off(const Geo &g, int gh, int row, int 
     return ((int64_t)(gh * (g.pt / 64) + row / 64) * (g.hd / 16) + d / 16) * 1024 +
            (row % 64) * 16 + d % 16;
 }
+// V quants when the block size is a multiple of 64: per 64-token tile, each
+// dimension's 64 cells are contiguous, so a lane owning a dimension reads its
+// cells with wide loads for the dot2 products of the attention.
+__device__ __forceinline__ int64_t vquant_off(const Geo &g, int gh, int row, int d) {
+    return ((int64_t)(gh * (g.pt / 64) + row / 64) * g.hd + d) * 64 + row % 64;
+}
 __device__ __forceinline__ int64_t scale_off(const Geo &g, int gh, int row, int j) {
     return g.qbytes + ((int64_t)(gh * g.pt + row) * (g.hd / 32) + j) * 2;
 }
@@ -187,6 +193,20 @@ __device__ __forceinline__ uint32_t quant4(const float x[4], int variant, uint16
     return pk;
 }
 
+// Four quants (dims d..d+3 of one row, packed little-endian) into a K or V page.
+__device__ __forceinline__ void store_q4(const Geo &g, uint8_t *page, bool is_v, int gh, int row, int d,
+                                         uint32_t pk) {
+    if (is_v && g.vdim) {
+        const int64_t o = vquant_off(g, gh, row, d);
+        page[o] = (uint8_t)pk;
+        page[o + 64] = (uint8_t)(pk >> 8);
+        page[o + 128] = (uint8_t)(pk >> 16);
+        page[o + 192] = (uint8_t)(pk >> 24);
+    } else {
+        *reinterpret_cast<uint32_t *>(page + quant_off(g, gh, row, d)) = pk;
+    }
+}
+
 __device__ __forceinline__ void load4(const void *src, int32_t f16, int64_t idx, float x[4]) {
     if (f16) {
         const uint2 u = *reinterpret_cast<const uint2 *>((const uint16_t *)src + idx);
@@ -247,7 +267,7 @@ k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
     const uint32_t pk = quant4(x, g.variant, &dh, nullptr);
     uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
     const int row = t % g.pt;
-    *reinterpret_cast<uint32_t *>(page + quant_off(g, gh, row, 32 * j + 4 * e4)) = pk;
+    store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
     if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
 }
 
@@ -266,8 +286,9 @@ hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, con
 // ---------------------------------------------------------------------------
 
 // One dequantized member value straight from global memory (gather path).
-__device__ __forceinline__ float member_k(const Geo &g, const uint8_t *page, int gh, int row, int d) {
-    const int8_t q = (int8_t)page[quant_off(g, gh, row, d)];
+__device__ __forceinline__ float member_k(const Geo &g, const uint8_t *page, int gh, int row, int d,
+                                          bool is_v = false) {
+    const int8_t q = (int8_t)page[(is_v && g.vdim) ? vquant_off(g, gh, row, d) : quant_off(g, gh, row, d)];
     const uint16_t s = *reinterpret_cast<const uint16_t *>(page + scale_off(g, gh, row, d / 32));
     return h2f(s) * (float)q;
 }
@@ -400,7 +421,7 @@ __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const Fus
         uint16_t dh;
         const uint32_t pk = quant4(x, g.variant, &dh, dq);
         uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
-        *reinterpret_cast<uint32_t *>(page + quant_off(g, gh, row, 32 * j + 4 * e4)) = pk;
+        store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
         if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
         if (which == 0)
             for (int k = 0; k < 4; ++k) sh.newk[32 * j + 4 * e4 + k] = dq[k];
@@ -518,6 +539,7 @@ __device__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out
             const uint32_t k = sh.cand_key[tid];
             const int b = sh.cand_b[tid];
             int rank = 0;
+#pragma unroll 8
             for (int j = 0; j < cB; ++j) {
                 const uint32_t kj = sh.cand_key[j];
                 rank += (kj > k) || (kj == k && sh.cand_b[j] < b);
@@ -658,6 +680,83 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
 // the groups merge in LDS into one partial softmax state per workgroup, and
 // the last workgroup of a (sequence, KV head) merges the partials.
 // ---------------------------------------------------------------------------
+
+// The last workgroup of a (sequence, KV head) merges the parts' (m, l, O):
+// og = sum_i w_i O_i / sum_i w_i l_i with w_i = exp2(m_i - max_i m_i).  The O
+// values a thread needs are prefetched (up to MAXP parts) together with the
+// maxima; `scratch` is LDS of scratch_floats floats.  All threads call.
+template <int G, int HD, int NT, int MAXP, int OPT>
+__device__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Mh, float *Lh,
+                               float *scratch, int scratch_floats) {
+    const int tid = threadIdx.x;
+    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
+    // every part's (m, l) into LDS, then M_h, the weights and L_h
+    float *ml = scratch;                                  // [parts][G][2]
+    const int nml = min(parts_act, scratch_floats / (3 * G));
+    float *wt = ml + nml * G * 2;                         // [parts][G]
+    for (int k = tid; k < nml * G * 2; k += NT) ml[k] = ws.part_ml[pb * 2 + k];
+    // the first batch of O values goes out with the (m, l) loads
+    float ov[OPT][MAXP];
+#pragma unroll
+    for (int r = 0; r < OPT; ++r) {
+        const int k = tid + r * NT;
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            ov[r][i] = (k < G * HD && i < parts_act) ? ws.part_o[(pb + (int64_t)i * G) * HD + k] : 0.0f;
+    }
+    __syncthreads();
+    auto m_of = [&](int i, int h) {
+        return i < nml ? ml[(i * G + h) * 2] : ws.part_ml[(pb + (int64_t)i * G + h) * 2];
+    };
+    auto l_of = [&](int i, int h) {
+        return i < nml ? ml[(i * G + h) * 2 + 1] : ws.part_ml[(pb + (int64_t)i * G + h) * 2 + 1];
+    };
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int i = 0; i < parts_act; ++i) M = fmaxf(M, m_of(i, tid));
+        Mh[tid] = M;
+    }
+    __syncthreads();
+    for (int k = tid; k < nml * G; k += NT) {
+        const float m = ml[k * 2];
+        wt[k] = m == -INFINITY ? 0.0f : exp2f(m - Mh[k % G]);
+    }
+    __syncthreads();
+    auto w_of = [&](int i, int h) {
+        if (i < nml) return wt[i * G + h];
+        const float m = m_of(i, h);
+        return m == -INFINITY ? 0.0f : exp2f(m - Mh[h]);
+    };
+    if (tid < G) {
+        float Ls = 0.0f;
+        for (int i = 0; i < parts_act; ++i) Ls += w_of(i, tid) * l_of(i, tid);
+        Lh[tid] = Ls;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < OPT; ++r) {
+        const int k = tid + r * NT;
+        if (k < G * HD) {
+            const int h = k / HD;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i)
+                if (i < parts_act) acc += w_of(i, h) * ov[r][i];
+            // further parts, MAXP loads in flight per batch
+            for (int i0 = MAXP; i0 < parts_act; i0 += MAXP) {
+                float ob[MAXP];
+#pragma unroll
+                for (int i = 0; i < MAXP; ++i)
+                    ob[i] = i0 + i < parts_act ? ws.part_o[(pb + (int64_t)(i0 + i) * G) * HD + k] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < MAXP; ++i)
+                    if (i0 + i < parts_act) acc += w_of(i0 + i, h) * ob[i];
+            }
+            const float Ls = Lh[h];
+            og[k] = Ls > 0.0f ? acc / Ls : 0.0f;
+        }
+    }
+}
 
 template <int HD, int G, int TG>
 struct AttnCfg {
@@ -893,76 +992,8 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    // M_h = max_i m_i, w_i = exp2(m_i - M_h), O = sum_i w_i O_i / sum_i w_i l_i;
-    // the partials' O values a thread needs are loaded together with the maxima
-    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
-    float ov[C::OPT][C::MAXP];
-#pragma unroll
-    for (int r = 0; r < C::OPT; ++r) {
-        const int k = tid + r * C::NT;
-#pragma unroll
-        for (int i = 0; i < C::MAXP; ++i)
-            ov[r][i] = (k < G * HD && i < parts_act) ? ws.part_o[(pb + (int64_t)i * G) * HD + k] : 0.0f;
-    }
-    float *ml = sh.grp[0].kv;                    // [parts][G][2] maxima and sums, then weights
-    const int nml = min(parts_act, (64 * C::ROWF) / (3 * G));
-    for (int k = tid; k < nml * G * 2; k += C::NT) ml[k] = ws.part_ml[pb * 2 + k];
-    __syncthreads();
-    float *wt = ml + nml * G * 2;                // [parts][G] weights
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int i = 0; i < parts_act; ++i)
-            M = fmaxf(M, i < nml ? ml[(i * G + tid) * 2] : ws.part_ml[(pb + (int64_t)i * G + tid) * 2]);
-        sh.Mh[tid] = M;
-    }
-    __syncthreads();
-    for (int k = tid; k < nml * G; k += C::NT) {
-        const float m = ml[k * 2];
-        wt[k] = m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[k % G]);
-    }
-    __syncthreads();
-    if (tid < G) {
-        float Ls = 0.0f;
-        for (int i = 0; i < parts_act; ++i) {
-            float wi, li;
-            if (i < nml) { wi = wt[i * G + tid]; li = ml[(i * G + tid) * 2 + 1]; }
-            else {
-                const float m = ws.part_ml[(pb + (int64_t)i * G + tid) * 2];
-                wi = m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[tid]);
-                li = ws.part_ml[(pb + (int64_t)i * G + tid) * 2 + 1];
-            }
-            Ls += wi * li;
-        }
-        sh.Lh[tid] = Ls;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < C::OPT; ++r) {
-        const int k = tid + r * C::NT;
-        if (k < G * HD) {
-            const int h = k / HD;
-            float acc = 0.0f;
-#pragma unroll
-            for (int i = 0; i < C::MAXP; ++i)
-                if (i < parts_act) acc += (i < nml ? wt[i * G + h] : 0.0f) * ov[r][i];
-            for (int i = C::MAXP; i < parts_act; ++i) {
-                float wi;
-                if (i < nml) wi = wt[i * G + h];
-                else {
-                    const float m = ws.part_ml[(pb + (int64_t)i * G + h) * 2];
-                    wi = m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[h]);
-                }
-                acc += wi * ws.part_o[(pb + (int64_t)i * G) * HD + k];
-            }
-            // parts below MAXP but beyond the LDS-staged weights
-            for (int i = nml; i < min(parts_act, C::MAXP); ++i) {
-                const float m = ws.part_ml[(pb + (int64_t)i * G + h) * 2];
-                acc += (m == -INFINITY ? 0.0f : exp2f(m - sh.Mh[h])) * ov[r][i];
-            }
-            const float Ls = sh.Lh[h];
-            og[k] = Ls > 0.0f ? acc / Ls : 0.0f;
-        }
-    }
+    merge_partials<G, HD, C::NT, C::MAXP, C::OPT>(ws, pair, parts_act, og, sh.Mh, sh.Lh, sh.grp[0].kv,
+                                                  64 * C::ROWF);
 }
 
 template <int HD, int G, int TG>
@@ -974,6 +1005,311 @@ static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
     const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
     hipLaunchKernelGGL((k_attn<HD, G, TG>), grid, dim3(AttnCfg<HD, G, TG>::NT), 0, st, g, v, q, seq_len,
                        max_seq_len, sel, nsel, max_sel, out, ws, n_parts);
+}
+
+// ---------------------------------------------------------------------------
+// attention, q8_0 fast path (block_tokens a multiple of 64): one tile = 64
+// consecutive tokens of one selected block.  Wave w of a tile owns q8_0
+// block w of the head dims (32 dims) for every query head of the group, so K
+// and V are each read exactly once per tile:
+//   QK  lane = cell; exact int32 dot4 of the int8 key quants against the
+//       query's three int8 parts; per-wave partial logits summed in LDS in
+//       wave order.
+//   softmax per head (DPP), p' = p * dv * 2^sh as an fp16 high part plus an
+//       fp16 remainder ([head][block][cell]), sh a per-tile power of two that
+//       keeps p' inside fp16's range.
+//   PV  lane = (dim, half of the cells); V quants of a dim are 64 contiguous
+//       bytes (dim-major tiles) converted exactly to fp16 pairs; dot2 with
+//       the p' pairs, fp32 accumulation, then * 2^-sh.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Four int8 quants of consecutive cells -> two exact fp16 pairs: bias to
+// unsigned, splice under the fp16 exponent of 1024, subtract 1152.
+__device__ __forceinline__ void q8x4_to_h2(uint32_t w, half2v &lo, half2v &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    lo = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + bias;
+    hi = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + bias;
+}
+
+template <int HD, int G, int TG>
+struct FastCfg {
+    static constexpr int NB = HD / 32;                 // q8_0 blocks per head row = waves per tile
+    static constexpr int NTG = NB * 64;                // threads per tile group
+    static constexpr int NT = TG * NTG;
+    static constexpr int MAXP = 32;                    // partials a combine thread prefetches
+    static constexpr int OPT = (G * HD + NT - 1) / NT;
+};
+
+template <int HD, int G>
+struct FastGroup {
+    float lg[HD / 32][G][64];                  // partial logits, one per owning wave
+    uint16_t pp[G][HD / 32][64];               // fp16 p * dv * 2^sh (high part)
+    uint16_t pl[G][HD / 32][64];               // its fp16 remainder (low part)
+    float o[2][G][HD];                         // the tile's O, one slice per cell half
+    float m[G], l[G];
+    int page, row0, nvalid;
+};
+
+template <int HD, int G, int TG>
+struct FastShared {
+    FastGroup<HD, G> grp[TG];
+    int32_t qa[G][HD / 4], qb[G][HD / 4], qc[G][HD / 4];   // the query as three int8 parts, packed
+    float qs[G];                               // q ~= qs * (qa + qb/254 + qc/254^2)
+    float Mh[G], Lh[G];
+    int flag;
+};
+
+template <int HD, int G, int TG>
+__global__ void __launch_bounds__((FastCfg<HD, G, TG>::NT))
+k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
+          const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *__restrict__ out, Ws ws) {
+    using C = FastCfg<HD, G, TG>;
+    constexpr int NB = C::NB;
+    __shared__ FastShared<HD, G, TG> sh;
+    const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);
+    const int lt = tid % C::NTG;
+    const int w = __builtin_amdgcn_readfirstlane(lt >> 6), lane = lt & 63;
+    FastGroup<HD, G> &gr = sh.grp[gi];
+    const int pair = s * g.Hkv + gh;
+    const int L = seq_len[s];
+    const bool ok = L >= 1 && L <= max_seq_len;
+    int n = 0;
+    if (ok) {
+        n = sel ? nsel[pair] : (L - 1) / g.bt + 1;
+        n = n < max_sel ? n : max_sel;
+    }
+    const int tiles_act = n * (g.bt / 64);
+    const int parts_act = (tiles_act + TG - 1) / TG;
+    const int part = blockIdx.x;
+    if (ok && part < parts_act) {
+        const int tile = part * TG + gi;
+        if (lt == 0) {
+            int pg = -1, row0 = 0, nv = 0;
+            if (tile < tiles_act) {
+                const int slot = tile / (g.bt / 64), off = (tile % (g.bt / 64)) * 64;
+                const int blk = sel ? sel[(int64_t)pair * max_sel + slot] : slot;
+                const int t0 = blk * g.bt + off;
+                if (blk >= 0 && t0 < L) {
+                    pg = phys_page(g, v.page_table, s, t0);
+                    row0 = t0 % g.pt;
+                    nv = min(64, L - t0);
+                    if (pg < 0) { set_status(v.status, QWFN_STATUS_PAGE_RANGE); nv = 0; }
+                }
+            }
+            gr.page = pg; gr.row0 = row0; gr.nvalid = nv;
+        }
+        __syncthreads();
+        const int nv = gr.nvalid, row0 = gr.row0;
+        const int64_t pbase = (int64_t)(nv > 0 ? gr.page : 0) * g.page_bytes;
+        const uint8_t *kp = (const uint8_t *)v.k_pages + pbase;
+        const uint8_t *vp = (const uint8_t *)v.v_pages + pbase;
+        const int tl = gh * (g.pt / 64) + row0 / 64;       // tile index inside the pool page
+        // every load of the tile first: K block w of cell `lane`, its scale,
+        // V of dim d for one half of the cells, the V scales of cell `lane`
+        const uint8_t *kq = kp + ((int64_t)tl * (HD / 16) + 2 * w) * 1024 + lane * 16;
+        const int d = 32 * w + (lane & 31), half = lane >> 5;
+        const uint8_t *vq = vp + ((int64_t)tl * HD + d) * 64 + half * 32;
+        uint4 k0 = make_uint4(0, 0, 0, 0), k1 = k0, v0 = k0, v1 = k0;
+        uint16_t dkh = 0, dvh[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) dvh[j] = 0;
+        if (nv > 0) {
+            k0 = *reinterpret_cast<const uint4 *>(kq);
+            k1 = *reinterpret_cast<const uint4 *>(kq + 1024);
+            v0 = *reinterpret_cast<const uint4 *>(vq);
+            v1 = *reinterpret_cast<const uint4 *>(vq + 16);
+            const int64_t so = g.qbytes + ((int64_t)(gh * g.pt + row0 + lane) * NB) * 2;
+            dkh = *reinterpret_cast<const uint16_t *>(kp + so + 2 * w);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) dvh[j] = *reinterpret_cast<const uint16_t *>(vp + so + 2 * j);
+        }
+        // The group's query heads split into three int8 parts per head,
+        // q ~= qs * (qa + qb/254 + qc/254^2), qs = amax/127 (residual below
+        // 2e-7 * amax): the operands of exact integer dot products against the
+        // int8 key quants.  One wave per head.
+        {
+            constexpr int DPL = HD / 64;
+            const int wid = tid >> 6, nwv = C::NT >> 6;
+            for (int h = wid; h < G; h += nwv) {
+                const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + h) * HD + lane * DPL;
+                float x[DPL], a = 0.0f;
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) { x[k] = qh[k]; a = fmaxf(a, fabsf(x[k])); }
+                const float amax = wave_max(a);
+                const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+                int8_t *pa = reinterpret_cast<int8_t *>(sh.qa[h]) + lane * DPL;
+                int8_t *pb = reinterpret_cast<int8_t *>(sh.qb[h]) + lane * DPL;
+                int8_t *pc = reinterpret_cast<int8_t *>(sh.qc[h]) + lane * DPL;
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) {
+                    const float t = x[k] * inv;
+                    const float ai = __builtin_rintf(t);
+                    const float r1 = (t - ai) * 254.0f;
+                    const float bi = __builtin_rintf(r1);
+                    const float ci = __builtin_rintf((r1 - bi) * 254.0f);
+                    pa[k] = (int8_t)max(-127, min(127, ai == ai ? (int)ai : 0));
+                    pb[k] = (int8_t)max(-127, min(127, bi == bi ? (int)bi : 0));
+                    pc[k] = (int8_t)max(-127, min(127, ci == ci ? (int)ci : 0));
+                }
+                if (lane == 0) sh.qs[h] = amax / 127.0f;
+            }
+        }
+        __syncthreads();
+        // QK over block w: exact int32 dots, one fp32 rescale
+        {
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const float dk = h2f(dkh);
+            constexpr int HQ = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);   // heads per batch of LDS reads
+#pragma unroll
+            for (int h0 = 0; h0 < G; h0 += HQ) {
+                uint4 qv[HQ][3][2];
+#pragma unroll
+                for (int hh = 0; hh < HQ; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        qv[hh][0][r] = reinterpret_cast<const uint4 *>(&sh.qa[h0 + hh][8 * w])[r];
+                        qv[hh][1][r] = reinterpret_cast<const uint4 *>(&sh.qb[h0 + hh][8 * w])[r];
+                        qv[hh][2][r] = reinterpret_cast<const uint4 *>(&sh.qc[h0 + hh][8 * w])[r];
+                    }
+#pragma unroll
+                for (int hh = 0; hh < HQ; ++hh) {
+                    int acc3[3];
+#pragma unroll
+                    for (int part = 0; part < 3; ++part) {
+                        const int32_t qw[8] = {(int)qv[hh][part][0].x, (int)qv[hh][part][0].y, (int)qv[hh][part][0].z,
+                                               (int)qv[hh][part][0].w, (int)qv[hh][part][1].x, (int)qv[hh][part][1].y,
+                                               (int)qv[hh][part][1].z, (int)qv[hh][part][1].w};
+                        int a = 0;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) a = __builtin_amdgcn_sdot4((int)kw[i], qw[i], a, false);
+                        acc3[part] = a;
+                    }
+                    gr.lg[w][h0 + hh][lane] =
+                        dk * ((float)acc3[0] + ((float)acc3[1] + (float)acc3[2] * (1.0f / 254.0f)) * (1.0f / 254.0f));
+                }
+            }
+        }
+        __syncthreads();
+        // softmax: wave w owns heads w, w+NB, ...; lane = cell
+        {
+            const bool valid = lane < nv;
+            float dvf[NB], dvm = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) { dvf[j] = h2f(dvh[j]); dvm = fmaxf(dvm, dvf[j]); }
+            dvm = wave_max(valid ? dvm : 0.0f);
+            int e = 0;
+            frexpf(dvm, &e);
+            const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e) : 1.0f;
+            for (int h = w; h < G; h += NB) {
+                float lsum = gr.lg[0][h][lane];
+#pragma unroll
+                for (int ww = 1; ww < NB; ++ww) lsum += gr.lg[ww][h][lane];
+                const float s2 = valid ? lsum * sh.qs[h] * g.scale_log2 : -INFINITY;
+                const float m = wave_max(s2);
+                const float p = valid ? exp2f(s2 - m) : 0.0f;
+                const float l = wave_sum(p);
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const float pj = p * dvf[j] * up;
+                    const uint16_t hi = f2h(pj);
+                    gr.pp[h][j][lane] = hi;
+                    gr.pl[h][j][lane] = f2h(pj - h2f(hi));
+                }
+                if (lane == 0) { gr.m[h] = m; gr.l[h] = l; }
+            }
+            const float down = 1.0f / up;              // exact: up is a power of two
+            __syncthreads();
+            // PV: lane = (dim d, half); 32 cells = 16 fp16 pairs
+            half2v vp2[16];
+            const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q8x4_to_h2(vw[i], vp2[2 * i], vp2[2 * i + 1]);
+            constexpr int HB = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);   // heads per batch of LDS reads
+#pragma unroll
+            for (int h0 = 0; h0 < G; h0 += HB) {
+                uint4 ph[HB][4], pl[HB][4];
+#pragma unroll
+                for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        ph[hh][r] = reinterpret_cast<const uint4 *>(&gr.pp[h0 + hh][w][half * 32])[r];
+                        pl[hh][r] = reinterpret_cast<const uint4 *>(&gr.pl[h0 + hh][w][half * 32])[r];
+                    }
+#pragma unroll
+                for (int hh = 0; hh < HB; ++hh) {
+                    float acc = 0.0f, accl = 0.0f;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint4 pq = ph[hh][r], pq2 = pl[hh][r];
+                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.x), vp2[4 * r + 0], acc, false);
+                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.y), vp2[4 * r + 1], acc, false);
+                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.z), vp2[4 * r + 2], acc, false);
+                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.w), vp2[4 * r + 3], acc, false);
+                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.x), vp2[4 * r + 0], accl, false);
+                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.y), vp2[4 * r + 1], accl, false);
+                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.z), vp2[4 * r + 2], accl, false);
+                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.w), vp2[4 * r + 3], accl, false);
+                    }
+                    gr.o[half][h0 + hh][d] = (acc + accl) * down;
+                }
+            }
+        }
+        __syncthreads();
+        // merge the TG tiles into this workgroup's partial (unnormalised O, max, sum)
+        const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
+#pragma unroll
+        for (int r = 0; r < C::OPT; ++r) {
+            const int k = tid + r * C::NT;
+            if (k < G * HD) {
+                const int h = k / HD, dd = k % HD;
+                float M = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < TG; ++t)
+                    if (part * TG + t < tiles_act) M = fmaxf(M, sh.grp[t].m[h]);
+                float O = 0.0f, Ls = 0.0f;
+#pragma unroll
+                for (int t = 0; t < TG; ++t) {
+                    if (part * TG + t < tiles_act) {
+                        const float mt = sh.grp[t].m[h];
+                        const float wt = mt == -INFINITY ? 0.0f : exp2f(mt - M);
+                        O += wt * (sh.grp[t].o[0][h][dd] + sh.grp[t].o[1][h][dd]);
+                        Ls += wt * sh.grp[t].l[h];
+                    }
+                }
+                ws.part_o[pb * HD + k] = O;
+                if (dd == 0) {
+                    ws.part_ml[(pb + h) * 2 + 0] = M;
+                    ws.part_ml[(pb + h) * 2 + 1] = Ls;
+                }
+            }
+        }
+    }
+    if (!arrive_last(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
+    if (tid == 0) ws.cnt_attn[pair] = 0;
+    float *og = out + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
+    if (!ok || parts_act == 0) {
+        for (int i = tid; i < G * HD; i += C::NT) og[i] = 0.0f;
+        if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
+        return;
+    }
+    merge_partials<G, HD, C::NT, C::MAXP, C::OPT>(ws, pair, parts_act, og, sh.Mh, sh.Lh,
+                                                  reinterpret_cast<float *>(&sh.grp[0]),
+                                                  (int)(sizeof(FastGroup<HD, G>) / sizeof(float)));
+}
+
+template <int HD, int G, int TG>
+static void launch_attn_q8_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                             int32_t n_seq,
+                             int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
+                             float *out, const Ws &ws, hipStream_t st) {
+    const int n_parts = (ws.n_tiles + TG - 1) / TG;
+    const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
+    hipLaunchKernelGGL((k_attn_q8<HD, G, TG>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q, seq_len,
+                       max_seq_len, sel, nsel, max_sel, out, ws);
 }
 
 // ---------------------------------------------------------------------------
@@ -1005,7 +1341,7 @@ k_gather(Geo g, qwfn_kv_view v, const int32_t *seq_len, const int32_t *sel, cons
     if (t < 0) { k_out[o] = 0.0f; v_out[o] = 0.0f; return; }
     const int rw = t % g.pt;
     k_out[o] = member_k(g, (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes, gh, rw, d);
-    v_out[o] = member_k(g, (const uint8_t *)v.v_pages + (int64_t)pp * g.page_bytes, gh, rw, d);
+    v_out[o] = member_k(g, (const uint8_t *)v.v_pages + (int64_t)pp * g.page_bytes, gh, rw, d, true);
 }
 
 hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len,
@@ -1059,10 +1395,23 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
     return hipErrorInvalidValue;
 }
 
+// q8_0 fast attention instantiations (head_dim, group, tiles per workgroup);
+// used when block_tokens is a multiple of 64
+#define QWFN_FOR_EACH_FAST(X) X(128, 8, 2) X(128, 4, 2) X(128, 2, 2) X(64, 8, 2) X(256, 12, 1) X(256, 8, 1)
+
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,
                             float *out, const Ws &ws, hipStream_t st) {
+    if (g.vdim) {
+#define F(HD_, G_, TG_)                                                                          \
+        if (g.hd == HD_ && g.G == G_) {                                                          \
+            launch_attn_q8_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
+            return hipGetLastError();                                                            \
+        }
+        QWFN_FOR_EACH_FAST(F)
+#undef F
+    }
 #define X(HD_, G_, TG_)                                                                         \
     if (g.hd == HD_ && g.G == G_) {                                                             \
         launch_attn_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \

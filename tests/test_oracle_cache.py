@@ -7,16 +7,20 @@ import pytest
 from _refs import BASELINE, TINY, Cfg, dequant_ref, q8_block_ref
 
 
-def _offsets_ref(cfg, g, row, d):
+def _offsets_ref(cfg, g, row, d, which=0):
     tiles, ch = cfg.page_tokens // 64, cfg.head_dim // 16
-    q = ((g * tiles + row // 64) * ch + d // 16) * 1024 + (row % 64) * 16 + d % 16
+    if which and cfg.block_tokens % 64 == 0:       # V quants: dim-major 64-token tiles
+        q = ((g * tiles + row // 64) * cfg.head_dim + d) * 64 + row % 64
+    else:
+        q = ((g * tiles + row // 64) * ch + d // 16) * 1024 + (row % 64) * 16 + d % 16
     qbytes = cfg.n_head_kv * cfg.page_tokens * cfg.head_dim
     s = qbytes + ((g * cfg.page_tokens + row) * (cfg.head_dim // 32) + d // 32) * 2
     return q, s
 
 
+@pytest.mark.parametrize("which", [0, 1])
 @pytest.mark.parametrize("cfg", [BASELINE, TINY, Cfg(head_dim=256, n_head=24, page_tokens=128)])
-def test_layout_is_a_bijection(oracle, cfg):
+def test_layout_is_a_bijection(oracle, cfg, which):
     pb = cfg.n_head_kv * cfg.page_tokens * (cfg.head_dim + cfg.head_dim // 16)
     from oracle.oracle import shape_of, lib
     import ctypes as C
@@ -26,14 +30,14 @@ def test_layout_is_a_bijection(oracle, cfg):
     for g in range(cfg.n_head_kv):
         for row in range(cfg.page_tokens):
             for d in range(cfg.head_dim):
-                qo, so = _offsets_ref(cfg, g, row, d)
+                qo, so = _offsets_ref(cfg, g, row, d, which)
                 hits[qo] += 1
                 if d % 32 == 0:
                     hits[so] += 1
                     hits[so + 1] += 1
             if rng.random() < 0.05:   # spot-check the oracle's own offsets
                 d = int(rng.integers(cfg.head_dim))
-                assert oracle.quant_offset(cfg, g, row, d) == _offsets_ref(cfg, g, row, d)[0]
+                assert oracle.quant_offset(cfg, g, row, d, which) == _offsets_ref(cfg, g, row, d, which)[0]
                 assert oracle.scale_offset(cfg, g, row, d // 32) == _offsets_ref(cfg, g, row, d)[1]
     assert (hits == 1).all()
 
@@ -60,11 +64,12 @@ def test_append_bytes_and_dequant_roundtrip(oracle, variant):
             for which, src, pool in (("k", k, c.k_pages), ("v", v, c.v_pages)):
                 page = pool[phys * c.page_bytes:(phys + 1) * c.page_bytes]
                 deq = c.dequant_row(which, int(seq[i]), int(pos[i]), g)
+                wh = 0 if which == "k" else 1
                 for j in range(4):
                     d16, q = q8_block_ref(src[i, g, 32 * j:32 * j + 32], variant)
-                    qo, so = _offsets_ref(cfg, g, row, 32 * j)
+                    qo, so = _offsets_ref(cfg, g, row, 32 * j, wh)
                     assert int(page[so:so + 2].view(np.uint16)[0]) == d16
-                    got_q = np.array([page[_offsets_ref(cfg, g, row, 32 * j + e)[0]] for e in range(32)],
+                    got_q = np.array([page[_offsets_ref(cfg, g, row, 32 * j + e, wh)[0]] for e in range(32)],
                                      dtype=np.uint8).view(np.int8)
                     np.testing.assert_array_equal(got_q, q)
                     np.testing.assert_array_equal(deq[32 * j:32 * j + 32], dequant_ref(d16, q))
