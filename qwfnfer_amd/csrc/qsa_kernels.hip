@@ -54,10 +54,10 @@ __device__ __forceinline__ int8_t to_i8(float r) {
 
 // Orderable key of a score: larger key = larger score; NaN lowest; -0 == +0.
 __device__ __forceinline__ uint32_t score_key(float x) {
-    if (x != x) return 0u;
-    if (x == 0.0f) return 0x80000000u;
     const uint32_t u = __float_as_uint(x);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    k = x == 0.0f ? 0x80000000u : k;               // -0 == +0
+    return x != x ? 0u : k;                        // NaN lowest
 }
 
 // Cross-lane steps on the DPP network (gfx9 encodings): a wave64 reduction
@@ -383,21 +383,23 @@ __device__ __forceinline__ Ranges qsa_ranges(const Geo &g, int L) {
 
 constexpr int kIdxThreads = 256;
 constexpr int kBlocksPerChunk = kIdxThreads / 4;   // 4 lanes share one block's dot
-constexpr int kKeysMax = 8192;                     // eligible blocks whose keys fit in LDS
+constexpr int kKeysMax = 8192;                     // eligible blocks the register selection holds
 
 constexpr int kCandMax = 256;                      // threshold-bin candidates ranked exactly
+constexpr int kStageSel = 1024;                    // top_k the register selection stages in LDS
 
 struct IdxShared {
     union {
         float q[16 * 256];                         // scoring: the group's query heads
-        uint32_t keys[kKeysMax];                   // selection: orderable score keys
         struct { int8_t q8[kStageRows * 256]; uint16_t sc[kStageRows * 8]; } st;  // pooling
     } u;
-    uint32_t hist[4096];
-    uint32_t cand_key[kCandMax];
-    int32_t cand_b[kCandMax];
+    uint32_t hist[4096 + 4];                       // + a trash bin for masked-off lanes
+    uint32_t cand_key[kCandMax + 1];               // + a trash slot
+    int32_t cand_b[kCandMax + 1];
+    int32_t stage[kStageSel + 1];                  // selected blocks in output order, + a trash slot
     uint32_t selbits[kKeysMax / 32];
     float newk[256];
+    float red[16];                                 // selection: per-wave max, min
     int tmp[16];
     int flag, bin, need, ncand;
 };
@@ -434,9 +436,6 @@ __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const Fus
                        sh.newk, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
 }
 
-__device__ __forceinline__ uint32_t key_at(const IdxShared &sh, const float *sc, int e_lo, int b, bool lds) {
-    return lds ? sh.u.keys[b - e_lo] : score_key(sc[b]);
-}
 
 template <int NB> __device__ void find_bin(IdxShared &sh, int need);
 
@@ -444,14 +443,14 @@ template <int NB> __device__ void find_bin(IdxShared &sh, int need);
 // shift+BITS: histogram of the BITS-bit digit at `shift`, then the digit of
 // the need-th largest key.  Updates prefix (appending the digit) and need.
 template <int BITS>
-__device__ void radix_pass(const IdxShared &shc, IdxShared &sh, const float *sc, int e_lo, int e_hi,
-                           bool lds, int shift, uint32_t &prefix, int &need, bool first) {
+__device__ void radix_pass(IdxShared &sh, const float *sc, int e_lo, int e_hi, int shift, uint32_t &prefix,
+                           int &need, bool first) {
     constexpr int NB = 1 << BITS;
     const int tid = threadIdx.x;
     for (int i = tid; i < NB; i += kIdxThreads) sh.hist[i] = 0u;
     __syncthreads();
     for (int b = e_lo + tid; b < e_hi; b += kIdxThreads) {
-        const uint32_t k = key_at(shc, sc, e_lo, b, lds);
+        const uint32_t k = score_key(sc[b]);
         if (first || (k >> (shift + BITS)) == prefix) atomicAdd(&sh.hist[(k >> shift) & (NB - 1)], 1u);
     }
     __syncthreads();
@@ -487,14 +486,176 @@ __device__ void find_bin(IdxShared &sh, int need) {
 }
 
 // Selection of one (sequence, KV head) by the last scoring workgroup: the
-// top_k eligible blocks by (score desc, index asc) on orderable 32-bit keys.
-// One 12-bit histogram pass finds the bin holding the threshold; the keys of
-// that bin (few, for scores of any spread) are ranked exactly against each
-// other; an ordered compaction emits the winners ascending between the
-// forced sink and window blocks.  A bin of more than kCandMax keys (heavy
-// ties) falls back to two more radix passes and an index-ordered tie count.
-__device__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out, int32_t *nout,
-                              IdxShared &sh) {
+// top_k eligible blocks by (score desc, index asc) on orderable 32-bit keys,
+// emitted ascending between the forced sink and window blocks.
+//
+// Register path (select_regs): thread t holds the KPT scores of blocks
+// e_lo + [t*KPT, t*KPT+KPT) in registers, loaded in one round trip.  A
+// 4096-bin histogram, linear in the score between the smallest and largest
+// score (monotone in the key order, NaN in bin 0; scores with no finite
+// spread bin on the top 12 key bits instead), finds the bin holding the
+// threshold; the keys of that bin (a handful for any continuous spread) are
+// ranked exactly against each other; an ordered compaction writes the
+// winners.  The code is straight-line and predicated: this runs once per
+// layer in one workgroup, from a cold instruction cache, where each taken
+// branch costs a fetch round trip.
+//
+// Fallback (select_radix): a threshold bin of more than kCandMax keys (heavy
+// ties) or more than kKeysMax eligible blocks takes three radix passes over
+// the keys in memory and an index-ordered tie count.
+template <int KPT>
+__device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const Ranges &r, int32_t *out,
+                                            IdxShared &sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int b0 = r.e_lo + tid * KPT;
+    float sv[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) sv[i] = sc[min(b0 + i, r.e_hi - 1)];
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const bool use = b0 + i < r.e_hi && sv[i] == sv[i];
+        lo = fminf(lo, use ? sv[i] : INFINITY);
+        hi = fmaxf(hi, use ? sv[i] : -INFINITY);
+    }
+    hi = wave_max(hi);
+    lo = -wave_max(-lo);
+    if (lane == 0) { sh.red[wid] = hi; sh.red[8 + wid] = lo; }
+    uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
+#pragma unroll
+    for (int i = 0; i < 4096 / 4 / kIdxThreads; ++i) h4[tid + i * kIdxThreads] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < KPT * kIdxThreads / 32) sh.selbits[tid] = 0u;
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kIdxThreads / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[8 + i]); }
+    const float span = hi - lo, scale = 4096.0f / span;
+    const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
+    // both bin maps, blended with a uniform mask (no per-element branch)
+    const uint32_t lm = lin ? 0xffffffffu : 0u;
+    uint32_t bin[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const uint32_t lb = (uint32_t)fminf((sv[i] - lo) * scale, 4095.0f);   // sv - lo >= 0 unless NaN
+        bin[i] = ((sv[i] == sv[i] ? lb : 0u) & lm) | ((score_key(sv[i]) >> 20) & ~lm);
+        atomicAdd(&sh.hist[b0 + i < r.e_hi ? bin[i] : 4096u], 1u);   // unconditional: no skip branch
+    }
+    __syncthreads();
+    // threshold bin: thread t owns bins [16t, 16t+16); the need-th largest
+    // key lies in the thread whose bins straddle it
+    {
+        constexpr int PER = 4096 / kIdxThreads;
+        uint32_t c[PER];
+#pragma unroll
+        for (int i = 0; i < PER / 4; ++i) {
+            const uint4 x = h4[tid * (PER / 4) + i];
+            c[4 * i] = x.x; c[4 * i + 1] = x.y; c[4 * i + 2] = x.z; c[4 * i + 3] = x.w;
+        }
+        int own = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) own += (int)c[i];
+        int total;
+        const int excl = block_excl_sum<kIdxThreads>(own, sh.tmp, &total);
+        int run = total - excl - own, fb = -1, fneed = 0;   // keys in higher bins
+#pragma unroll
+        for (int i = PER - 1; i >= 0; --i) {
+            const bool hit = run < g.topk && run + (int)c[i] >= g.topk;   // exactly one bin overall
+            fb = hit ? tid * PER + i : fb;
+            fneed = hit ? g.topk - run : fneed;
+            run += (int)c[i];
+        }
+        if (fb >= 0) { sh.bin = fb; sh.need = fneed; }
+    }
+    __syncthreads();
+    const uint32_t B = (uint32_t)sh.bin;
+    const int need = sh.need;
+    const int cB = (int)sh.hist[B];
+    if (cB > kCandMax) return false;
+    int nc = 0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) nc += (b0 + i < r.e_hi && bin[i] == B);
+    if (nc > 0) {
+        int slot = atomicAdd(&sh.ncand, nc);
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool c = b0 + i < r.e_hi && bin[i] == B;
+            const int at = c ? slot : kCandMax;
+            sh.cand_key[at] = score_key(sv[i]);
+            sh.cand_b[at] = b0 + i;
+            slot += c;
+        }
+    }
+    __syncthreads();
+    if (tid < cB) {
+        const uint32_t k = sh.cand_key[tid];
+        const int b = sh.cand_b[tid];
+        int rank = 0;
+        for (int j = 0; j < cB; ++j) {
+            const uint32_t kj = sh.cand_key[j];
+            rank += (kj > k) || (kj == k && sh.cand_b[j] < b);
+        }
+        if (rank < need) atomicOr(&sh.selbits[(b - r.e_lo) >> 5], 1u << ((b - r.e_lo) & 31));
+    }
+    __syncthreads();
+    // KPT divides 32: the thread's bits sit in one word
+    const uint32_t wb = sh.selbits[(tid * KPT) >> 5] >> ((tid * KPT) & 31);
+    bool take[KPT];
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        take[i] = b0 + i < r.e_hi && (bin[i] > B || (bin[i] == B && ((wb >> i) & 1u)));
+        cnt += take[i];
+    }
+    int tot;
+    int pos = block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        sh.stage[take[i] && pos < g.topk ? pos : kStageSel] = b0 + i;
+        pos += take[i];
+    }
+    __syncthreads();
+    for (int i = tid; i < g.topk; i += kIdxThreads) out[g.sink + i] = sh.stage[i];
+    return true;
+}
+
+__device__ __attribute__((noinline)) void select_radix(const Geo &g, const float *sc, const Ranges &r,
+                                                       int32_t *out, IdxShared &sh) {
+    const int tid = threadIdx.x;
+    const int ne = r.e_hi - r.e_lo;
+    const int per = (ne + kIdxThreads - 1) / kIdxThreads;
+    const int b0 = r.e_lo + tid * per;
+    const int b1 = min(b0 + per, r.e_hi);
+    __syncthreads();                               // the register path may still read sh.hist
+    uint32_t prefix = 0;
+    int need = g.topk;
+    radix_pass<12>(sh, sc, r.e_lo, r.e_hi, 20, prefix, need, true);
+    radix_pass<12>(sh, sc, r.e_lo, r.e_hi, 8, prefix, need, false);
+    radix_pass<8>(sh, sc, r.e_lo, r.e_hi, 0, prefix, need, false);
+    const uint32_t T = prefix;
+    int tot, eq = 0;
+    for (int b = b0; b < b1; ++b) eq += (score_key(sc[b]) == T);
+    int eqi = block_excl_sum<kIdxThreads>(eq, sh.tmp, &tot);
+    int cnt = 0;
+    {
+        int e2 = eqi;
+        for (int b = b0; b < b1; ++b) {
+            const uint32_t k = score_key(sc[b]);
+            bool tk = k > T;
+            if (k == T) tk = (e2++ < need);
+            cnt += tk;
+        }
+    }
+    int pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
+    for (int b = b0; b < b1; ++b) {
+        const uint32_t k = score_key(sc[b]);
+        bool tk = k > T;
+        if (k == T) tk = (eqi++ < need);
+        if (tk && pos < g.sink + g.topk) out[pos++] = b;
+    }
+}
+
+__device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out, int32_t *nout,
+                                              IdxShared &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     const int ne = r.e_hi - r.e_lo;
@@ -504,85 +665,12 @@ __device__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out
         if (tid == 0) *nout = n;
         return;
     }
-    const bool lds = ne <= kKeysMax;
-    if (lds) {
-#pragma unroll 8
-        for (int i = tid; i < ne; i += kIdxThreads) sh.u.keys[i] = score_key(sc[r.e_lo + i]);
-    }
-    for (int i = tid; i < 4096; i += kIdxThreads) sh.hist[i] = 0u;
-    for (int i = tid; i < kKeysMax / 32; i += kIdxThreads) sh.selbits[i] = 0u;
-    if (tid == 0) sh.ncand = 0;
-    __syncthreads();
-    // pass 1: histogram of the top 12 bits
-    for (int b = r.e_lo + tid; b < r.e_hi; b += kIdxThreads)
-        atomicAdd(&sh.hist[key_at(sh, sc, r.e_lo, b, lds) >> 20], 1u);
-    __syncthreads();
-    find_bin<4096>(sh, g.topk);
-    const uint32_t B = (uint32_t)sh.bin;
-    const int need = sh.need;
-    const int cB = (int)sh.hist[B];
-    const int per = (ne + kIdxThreads - 1) / kIdxThreads;
-    const int b0 = r.e_lo + tid * per;
-    const int b1 = min(b0 + per, r.e_hi);
-    int tot, pos;
-    if (lds && cB <= kCandMax) {
-        for (int b = b0; b < b1; ++b) {
-            const uint32_t k = sh.u.keys[b - r.e_lo];
-            if ((k >> 20) == B) {
-                const int slot = atomicAdd(&sh.ncand, 1);
-                sh.cand_key[slot] = k;
-                sh.cand_b[slot] = b;
-            }
-        }
-        __syncthreads();
-        if (tid < cB) {
-            const uint32_t k = sh.cand_key[tid];
-            const int b = sh.cand_b[tid];
-            int rank = 0;
-#pragma unroll 8
-            for (int j = 0; j < cB; ++j) {
-                const uint32_t kj = sh.cand_key[j];
-                rank += (kj > k) || (kj == k && sh.cand_b[j] < b);
-            }
-            if (rank < need) atomicOr(&sh.selbits[(b - r.e_lo) >> 5], 1u << ((b - r.e_lo) & 31));
-        }
-        __syncthreads();
-        auto take = [&](int b) {
-            const uint32_t d = sh.u.keys[b - r.e_lo] >> 20;
-            return d > B || (d == B && ((sh.selbits[(b - r.e_lo) >> 5] >> ((b - r.e_lo) & 31)) & 1u));
-        };
-        int cnt = 0;
-        for (int b = b0; b < b1; ++b) cnt += take(b);
-        pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
-        for (int b = b0; b < b1; ++b)
-            if (take(b) && pos < g.sink + g.topk) out[pos++] = b;
-    } else {
-        uint32_t prefix = B;
-        int need2 = need;
-        radix_pass<12>(sh, sh, sc, r.e_lo, r.e_hi, lds, 8, prefix, need2, false);
-        radix_pass<8>(sh, sh, sc, r.e_lo, r.e_hi, lds, 0, prefix, need2, false);
-        const uint32_t T = prefix;
-        int eq = 0;
-        for (int b = b0; b < b1; ++b) eq += (key_at(sh, sc, r.e_lo, b, lds) == T);
-        int eqi = block_excl_sum<kIdxThreads>(eq, sh.tmp, &tot);
-        int cnt = 0;
-        {
-            int e2 = eqi;
-            for (int b = b0; b < b1; ++b) {
-                const uint32_t k = key_at(sh, sc, r.e_lo, b, lds);
-                bool tk = k > T;
-                if (k == T) tk = (e2++ < need2);
-                cnt += tk;
-            }
-        }
-        pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
-        for (int b = b0; b < b1; ++b) {
-            const uint32_t k = key_at(sh, sc, r.e_lo, b, lds);
-            bool tk = k > T;
-            if (k == T) tk = (eqi++ < need2);
-            if (tk && pos < g.sink + g.topk) out[pos++] = b;
-        }
-    }
+    bool done = false;
+    if (g.topk > kStageSel) done = false;
+    else if (ne <= 4 * kIdxThreads) done = select_regs<4>(g, sc, r, out, sh);
+    else if (ne <= 16 * kIdxThreads) done = select_regs<16>(g, sc, r, out, sh);
+    else if (ne <= kKeysMax) done = select_regs<kKeysMax / kIdxThreads>(g, sc, r, out, sh);
+    if (!done) select_radix(g, sc, r, out, sh);
     for (int i = tid; i < g.sink; i += kIdxThreads) out[i] = i;
     const int nwin = r.b_last - r.fw + 1;
     for (int i = tid; i < nwin; i += kIdxThreads) out[g.sink + g.topk + i] = r.fw + i;
@@ -682,78 +770,95 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
 // ---------------------------------------------------------------------------
 
 // The last workgroup of a (sequence, KV head) merges the parts' (m, l, O):
-// og = sum_i w_i O_i / sum_i w_i l_i with w_i = exp2(m_i - max_i m_i).  The O
-// values a thread needs are prefetched (up to MAXP parts) together with the
-// maxima; `scratch` is LDS of scratch_floats floats.  All threads call.
-template <int G, int HD, int NT, int MAXP, int OPT>
-__device__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Mh, float *Lh,
+// og = sum_i w_i O_i / sum_i w_i l_i with w_i = exp2(m_i - max_i m_i).  One
+// wave per head reduces the parts' m and l with DPP while the O loads are in
+// flight; each thread owns VW consecutive output dims and keeps up to MAXP
+// parts of them in registers, so a combine of MAXP parts or fewer costs one
+// round trip.  `scratch` is LDS of scratch_floats floats, `Lh` LDS of 2*G
+// floats.  All threads call.
+template <int G, int HD, int NT>
+struct MergeCfg {
+    static constexpr int VW = (G * HD >= 4 * NT && HD % 4 == 0) ? 4 : (G * HD >= 2 * NT && HD % 2 == 0) ? 2 : 1;
+    static constexpr int OPT = (G * HD / VW + NT - 1) / NT;      // output vectors per thread
+    static constexpr int MAXP = 80 / (VW * OPT) > 40 ? 40 : 80 / (VW * OPT);
+};
+
+template <int G, int HD, int NT>
+__device__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Lh,
                                float *scratch, int scratch_floats) {
-    const int tid = threadIdx.x;
+    using M = MergeCfg<G, HD, NT>;
+    constexpr int VW = M::VW, OPT = M::OPT, MAXP = M::MAXP, NV = G * HD / VW;
+    constexpr int NW = NT / 64;
+    using vec = float __attribute__((ext_vector_type(VW)));
+    const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
     const int64_t pb = (int64_t)pair * ws.n_tiles * G;
-    // every part's (m, l) into LDS, then M_h, the weights and L_h
-    float *ml = scratch;                                  // [parts][G][2]
-    const int nml = min(parts_act, scratch_floats / (3 * G));
-    float *wt = ml + nml * G * 2;                         // [parts][G]
-    for (int k = tid; k < nml * G * 2; k += NT) ml[k] = ws.part_ml[pb * 2 + k];
-    // the first batch of O values goes out with the (m, l) loads
-    float ov[OPT][MAXP];
+    const float *pml = ws.part_ml + pb * 2;
+    const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
+    // the first (m, l) of this wave's first head, then the first batch of O
+    float2 ml0 = make_float2(-INFINITY, 0.0f);
+    if (wv < G && ln < parts_act) ml0 = *reinterpret_cast<const float2 *>(pml + ((int64_t)ln * G + wv) * 2);
+    vec ov[OPT][MAXP];
 #pragma unroll
     for (int r = 0; r < OPT; ++r) {
         const int k = tid + r * NT;
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
-            ov[r][i] = (k < G * HD && i < parts_act) ? ws.part_o[(pb + (int64_t)i * G) * HD + k] : 0.0f;
+            ov[r][i] = (k < NV && i < parts_act) ? po[(int64_t)i * NV + k] : vec(0.0f);
     }
-    __syncthreads();
-    auto m_of = [&](int i, int h) {
-        return i < nml ? ml[(i * G + h) * 2] : ws.part_ml[(pb + (int64_t)i * G + h) * 2];
-    };
-    auto l_of = [&](int i, int h) {
-        return i < nml ? ml[(i * G + h) * 2 + 1] : ws.part_ml[(pb + (int64_t)i * G + h) * 2 + 1];
-    };
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int i = 0; i < parts_act; ++i) M = fmaxf(M, m_of(i, tid));
-        Mh[tid] = M;
-    }
-    __syncthreads();
-    for (int k = tid; k < nml * G; k += NT) {
-        const float m = ml[k * 2];
-        wt[k] = m == -INFINITY ? 0.0f : exp2f(m - Mh[k % G]);
-    }
-    __syncthreads();
-    auto w_of = [&](int i, int h) {
-        if (i < nml) return wt[i * G + h];
-        const float m = m_of(i, h);
-        return m == -INFINITY ? 0.0f : exp2f(m - Mh[h]);
-    };
-    if (tid < G) {
+    // weights w_i,h = 2^(m_i,h - M_h) into LDS, L_h = sum_i w_i,h l_i,h
+    const int nwt = min(parts_act, scratch_floats / G);
+    float *wt = scratch;                                   // [nwt][G]
+    for (int h = wv; h < G; h += NW) {
+        float Mx = -INFINITY;
+        for (int i0 = 0; i0 < parts_act; i0 += 64) {
+            const int i = i0 + ln;
+            float m = -INFINITY;
+            if (h == wv && i0 == 0) m = ml0.x;
+            else if (i < parts_act) m = pml[((int64_t)i * G + h) * 2];
+            Mx = fmaxf(Mx, m);
+        }
+        Mx = wave_max(Mx);
         float Ls = 0.0f;
-        for (int i = 0; i < parts_act; ++i) Ls += w_of(i, tid) * l_of(i, tid);
-        Lh[tid] = Ls;
+        for (int i0 = 0; i0 < parts_act; i0 += 64) {
+            const int i = i0 + ln;
+            float2 ml = ml0;
+            if (!(h == wv && i0 == 0))
+                ml = i < parts_act ? *reinterpret_cast<const float2 *>(pml + ((int64_t)i * G + h) * 2)
+                                   : make_float2(-INFINITY, 0.0f);
+            const float w = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - Mx);
+            if (i < nwt) wt[i * G + h] = w;
+            Ls += w * ml.y;
+        }
+        Ls = wave_sum(Ls);
+        if (ln == 0) { Lh[h] = Ls; Lh[G + h] = Mx; }
     }
     __syncthreads();
+    auto w_of = [&](int i, int h) -> float {
+        if (i < nwt) return wt[i * G + h];
+        const float m = pml[((int64_t)i * G + h) * 2];
+        return m == -INFINITY ? 0.0f : exp2f(m - Lh[G + h]);
+    };
 #pragma unroll
     for (int r = 0; r < OPT; ++r) {
         const int k = tid + r * NT;
-        if (k < G * HD) {
-            const int h = k / HD;
-            float acc = 0.0f;
+        if (k < NV) {
+            const int h = k * VW / HD;
+            vec acc = vec(0.0f);
 #pragma unroll
             for (int i = 0; i < MAXP; ++i)
                 if (i < parts_act) acc += w_of(i, h) * ov[r][i];
-            // further parts, MAXP loads in flight per batch
+            // parts beyond MAXP: further batches, MAXP loads in flight each
             for (int i0 = MAXP; i0 < parts_act; i0 += MAXP) {
-                float ob[MAXP];
+                vec ob[MAXP];
 #pragma unroll
-                for (int i = 0; i < MAXP; ++i)
-                    ob[i] = i0 + i < parts_act ? ws.part_o[(pb + (int64_t)(i0 + i) * G) * HD + k] : 0.0f;
+                for (int i = 0; i < MAXP; ++i) ob[i] = i0 + i < parts_act ? po[(int64_t)(i0 + i) * NV + k] : vec(0.0f);
 #pragma unroll
                 for (int i = 0; i < MAXP; ++i)
                     if (i0 + i < parts_act) acc += w_of(i0 + i, h) * ob[i];
             }
             const float Ls = Lh[h];
-            og[k] = Ls > 0.0f ? acc / Ls : 0.0f;
+            const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+            reinterpret_cast<vec *>(og)[k] = Ls > 0.0f ? acc * inv : vec(0.0f);
         }
     }
 }
@@ -768,7 +873,6 @@ struct AttnCfg {
     static constexpr int ROWF = HD + 4;                // padded LDS row (floats)
     static constexpr int DPL = HD / 64;                // PV dims per lane
     static constexpr int PER = (64 * CH + NTG - 1) / NTG;   // 16-byte K (and V) loads per thread
-    static constexpr int MAXP = 32;                    // partials a combine thread prefetches
     static constexpr int OPT = (G * HD + NT - 1) / NT; // merged outputs per thread
     static_assert(G % NW == 0, "group size");
     static_assert(HD % 64 == 0, "head_dim");
@@ -787,7 +891,7 @@ template <int HD, int G, int TG>
 struct AttnShared {
     AttnGroup<HD, G> grp[TG];
     float q[G * HD];                           // the KV head's query heads
-    float Mh[G], Lh[G];
+    float Lh[2 * G];                           // combine: L_h, then M_h
     int flag;
 };
 
@@ -992,8 +1096,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    merge_partials<G, HD, C::NT, C::MAXP, C::OPT>(ws, pair, parts_act, og, sh.Mh, sh.Lh, sh.grp[0].kv,
-                                                  64 * C::ROWF);
+    merge_partials<G, HD, C::NT>(ws, pair, parts_act, og, sh.Lh, sh.grp[0].kv, 64 * C::ROWF);
 }
 
 template <int HD, int G, int TG>
@@ -1039,7 +1142,6 @@ struct FastCfg {
     static constexpr int NB = HD / 32;                 // q8_0 blocks per head row = waves per tile
     static constexpr int NTG = NB * 64;                // threads per tile group
     static constexpr int NT = TG * NTG;
-    static constexpr int MAXP = 32;                    // partials a combine thread prefetches
     static constexpr int OPT = (G * HD + NT - 1) / NT;
 };
 
@@ -1058,7 +1160,7 @@ struct FastShared {
     FastGroup<HD, G> grp[TG];
     int32_t qa[G][HD / 4], qb[G][HD / 4], qc[G][HD / 4];   // the query as three int8 parts, packed
     float qs[G];                               // q ~= qs * (qa + qb/254 + qc/254^2)
-    float Mh[G], Lh[G];
+    float Lh[2 * G];                           // combine: L_h, then M_h
     int flag;
 };
 
@@ -1296,9 +1398,8 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    merge_partials<G, HD, C::NT, C::MAXP, C::OPT>(ws, pair, parts_act, og, sh.Mh, sh.Lh,
-                                                  reinterpret_cast<float *>(&sh.grp[0]),
-                                                  (int)(sizeof(FastGroup<HD, G>) / sizeof(float)));
+    merge_partials<G, HD, C::NT>(ws, pair, parts_act, og, sh.Lh, reinterpret_cast<float *>(&sh.grp[0]),
+                                 (int)(sizeof(FastGroup<HD, G>) / sizeof(float)));
 }
 
 template <int HD, int G, int TG>

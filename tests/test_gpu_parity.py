@@ -96,15 +96,18 @@ def test_pool_matches_oracle(cfg):
         np.testing.assert_array_equal(got[s, :, b], host.pooled[s, :, b])
 
 
-def _indexer_case(cfg, lengths, seed, equal_scores=False):
+def _indexer_case(cfg, lengths, seed, equal_scores=False, mutate=None):
     rng = np.random.default_rng(seed)
     pps = max(lengths) // cfg.page_tokens + 1
     dev, host = make_pair(cfg, len(lengths), pps, seed=seed)
     fill(dev, host, rng, lengths)
+    q = rng.standard_normal((len(lengths), cfg.n_head, cfg.head_dim), dtype=np.float32)
     if equal_scores:                                   # every pooled key identical -> all ties
         host.pooled[...] = host.pooled[:, :, :1]
+    if mutate is not None:                             # edit the pooled keys and queries on the host
+        mutate(host.pooled, q, rng)
+    if equal_scores or mutate is not None:
         dev.pooled.copy_(torch.from_numpy(host.pooled))
-    q = rng.standard_normal((len(lengths), cfg.n_head, cfg.head_dim), dtype=np.float32)
     L = np.array(lengths, np.int32)
     max_len = int(L.max())
     ws = qsa.Workspace(cfg_of(cfg), len(lengths), max_len)
@@ -129,6 +132,38 @@ def test_indexer_matches_oracle(lengths):
 def test_indexer_ties_resolve_to_lower_index():
     _, _, _, _, sel, nsel, _ = _indexer_case(BASELINE, [32768], seed=210, equal_scores=True)
     assert list(sel[0, 0, :nsel[0, 0]]) == [0] + list(range(1, 65)) + list(range(504, 512))
+
+
+def _inf_nan(p, q, rng):                               # +inf, -inf and NaN scores among finite ones
+    q[..., 0] = np.abs(q[..., 0]) + np.float32(0.5)
+    p[:, :, 5:40:7, 0] = np.inf
+    p[:, :, 9:60:11, 0] = -np.inf
+    p[:, :, 13:300:17, 3] = np.nan
+
+
+def _outlier(p, q, rng):                               # one huge score squeezes the linear bins
+    p[:, :, 77] *= np.float32(1e30)
+
+
+def _half_ties(p, q, rng):                             # 200 equal scores among distinct ones
+    p[:, :, 1:400:2] = p[:, :, 1:2]
+
+
+def _small_spread(p, q, rng):                          # scores a few ulps apart
+    p[...] = p[:, :, :1] + rng.standard_normal(p.shape).astype(np.float32) * np.float32(1e-6)
+
+
+@pytest.mark.parametrize("mutate", [_inf_nan, _outlier, _half_ties, _small_spread])
+def test_indexer_extreme_scores(mutate):
+    _indexer_case(BASELINE, [32768, 20000], seed=230, mutate=mutate)
+
+
+def test_indexer_more_blocks_than_lds_keys():
+    # more than 8192 eligible blocks: the selection reads its keys from memory
+    cfg = Cfg(n_head=8, n_head_kv=1, head_dim=64, block_tokens=2, page_tokens=64, top_k_blocks=40,
+              sink_blocks=1, local_tokens=5)
+    _indexer_case(cfg, [16600], seed=240)
+    _indexer_case(cfg, [16600], seed=241, equal_scores=True)
 
 
 @pytest.mark.parametrize("cfg", [TINY, G12, Cfg(relu_per_head=1), Cfg(top_k_blocks=3, sink_blocks=2, local_tokens=100)])
