@@ -7,10 +7,12 @@ q8_0 block, 64-token pooled blocks, top-64 blocks + block 0 + the last 512
 tokens, one decode token per step at contexts 4096, 65536 and 163840.
 
 A step = one decode token through all 12 layers; each layer is the fused path
-of graph_builder::sparse_attn_decode: append the token's K/V (q8_0), re-pool
-the block it completes, score the pooled blocks, select, attend (two kernels:
-append+select, attention).  seq_len stays at the context, so every step
-rewrites position ctx-1 (an idempotent overwrite) and re-pools its block.
+of graph_builder::sparse_attn_decode: append the token's K/V (q8_0), pool the
+block it completes, score the pooled blocks, select, attend (two kernels:
+append+select, attention).  The decode position walks the last 64 positions
+of the context (seq_len = ctx-64 .. ctx-1, advanced on the device at the
+start of every step), so one step in 64 completes a block and pools it, as in a
+real decode; each step rewrites its position (an idempotent overwrite).
 Inputs are resident in HBM before the timed region; per-context working sets
 below 512 MiB are replicated and rotated so the 256 MB MALL does not serve them.
 
@@ -114,6 +116,10 @@ class Runner:
         self.vn = [torch.randn((n_seq, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
                    for _ in range(n_layer)]
         self.out = [torch.empty((n_seq, cfg.n_head, cfg.head_dim), device="cuda") for _ in range(n_layer)]
+        # seq_len = base + (ctr & 63), advanced at the start of every step
+        self.base = torch.tensor([max(0, L - 64) for L in lengths], dtype=torch.int32, device="cuda")
+        self.ctr = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.ph = torch.zeros(1, dtype=torch.int32, device="cuda")
         self.seq_len = torch.tensor(lengths, dtype=torch.int32, device="cuda")
         self.ws = qsa.Workspace(cfg, n_seq, self.max_len)
         msel = cfg.max_selected(self.max_len)
@@ -141,8 +147,17 @@ class Runner:
         if ev is not None:
             ev[2].record()
 
+    def advance(self):
+        """Next decode position (three tiny device ops, part of the step)."""
+        torch = self.torch
+        self.ctr.add_(1)
+        torch.bitwise_and(self.ctr, 63, out=self.ph)
+        torch.add(self.base, self.ph, out=self.seq_len)
+        self.seq_len.clamp_(min=1)
+
     def step(self, i):
         inst = i % self.n_inst
+        self.advance()
         for il in range(self.n_layer):
             self.layer(inst, il)
 
@@ -157,18 +172,21 @@ class Runner:
             for inst in range(self.n_inst):
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g, stream=s):
+                    self.advance()
                     for il in range(self.n_layer):
                         self.layer(inst, il)
                 graphs.append(g)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         for inst in range(self.n_inst):
+            c0 = int(self.ctr.item())
             self.step(inst)
             torch.cuda.synchronize()
             ref = [o.clone() for o in self.out]
             for rep in range(3 if inst == 0 else 1):
                 for o in self.out:
                     o.fill_(float("nan"))
+                self.ctr.fill_(c0)
                 graphs[inst].replay()
                 torch.cuda.synchronize()
                 if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
@@ -201,6 +219,7 @@ class Runner:
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps * self.n_layer)]
         k = 0
         for i in range(steps):
+            self.advance()
             for il in range(self.n_layer):
                 self.layer(i % self.n_inst, il, evs[k])
                 k += 1

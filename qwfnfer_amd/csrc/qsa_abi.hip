@@ -145,7 +145,9 @@ namespace qwfn_qsa {
 
 WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
     WsLayout l;
-    l.nb_cap = max_seq_len / g.bt > 0 ? max_seq_len / g.bt : 1;
+    // per-pair score rows padded to 64 floats: 16-byte vector loads of a row
+    // stay aligned and inside it
+    l.nb_cap = (int32_t)((((int64_t)(max_seq_len / g.bt > 0 ? max_seq_len / g.bt : 1)) + 63) / 64 * 64);
     l.max_sel = max_sel;
     l.n_tiles = (int32_t)(((int64_t)max_sel * g.bt + 63) / 64);
     const size_t pairs = (size_t)n_seq * g.Hkv;

@@ -169,11 +169,11 @@ __device__ __forceinline__ uint32_t quant4(const float x[4], int variant, uint16
         const float ax = fabsf(x[k]);
         a = ax > a ? ax : a;
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-        const float b = __shfl_xor(a, o);
-        a = b > a ? b : a;
-    }
+    // max over the block's 8 lanes (aligned groups of 8): quad xor 1, quad
+    // xor 2, then the half-row mirror pairs the two quads
+    a = fmaxf(a, dppf<kDppQuadXor1>(a, a));
+    a = fmaxf(a, dppf<kDppQuadXor2>(a, a));
+    a = fmaxf(a, dppf<kDppRowHalfMirror>(a, a));
     const float d = a / 127.0f;
     const uint16_t dh = f2h(d);
     float id;
@@ -318,6 +318,20 @@ __device__ __forceinline__ void stage_rows(const Geo &g, const uint8_t *page, in
 // chain acc = m_0 + m_1 + ... + m_{bt-1}, then * (1/bt).  With `last` set the
 // final member is taken from it (the decode token, still in LDS) instead of
 // memory.  All nt threads must call (it synchronises).
+// Dimension tid's chain over n staged rows: acc + m_0 + ... + m_{n-1}, or
+// m_0 + ... when `first` (the block's first member starts the chain).
+template <int HD>
+__device__ __forceinline__ float pool_chain(const int8_t *q8, const uint16_t *sc, int n, int tid, float acc,
+                                            bool first) {
+#pragma clang fp contract(off)
+#pragma unroll 8
+    for (int t = 0; t < n; ++t) {
+        const float m = h2f(sc[t * (HD / 32) + tid / 32]) * (float)q8[t * HD + tid];
+        acc = (first && t == 0) ? m : acc + m;
+    }
+    return acc;
+}
+
 template <int HD>
 __device__ void pool_block_dev(const Geo &g, const uint8_t *page, int gh, int row0, float *dst,
                                const float *last, int8_t *q8, uint16_t *sc, int tid, int nt) {
@@ -328,13 +342,7 @@ __device__ void pool_block_dev(const Geo &g, const uint8_t *page, int gh, int ro
         const int n = min(kStageRows, from_mem - r0);
         stage_rows<HD>(g, page, gh, row0 + r0, n, q8, sc, tid, nt);
         __syncthreads();
-        if (tid < HD) {
-#pragma unroll 8
-            for (int t = 0; t < n; ++t) {
-                const float m = h2f(sc[t * (HD / 32) + tid / 32]) * (float)q8[t * HD + tid];
-                acc = (r0 + t == 0) ? m : acc + m;
-            }
-        }
+        if (tid < HD) acc = pool_chain<HD>(q8, sc, n, tid, acc, r0 == 0);
         __syncthreads();
     }
     if (tid < HD) {
@@ -383,25 +391,24 @@ __device__ __forceinline__ Ranges qsa_ranges(const Geo &g, int L) {
 
 constexpr int kIdxThreads = 256;
 constexpr int kBlocksPerChunk = kIdxThreads / 4;   // 4 lanes share one block's dot
-constexpr int kKeysMax = 8192;                     // eligible blocks the register selection holds
+constexpr int kKeysMax = 32 * kIdxThreads;        // eligible blocks the register selection holds
 
 constexpr int kCandMax = 256;                      // threshold-bin candidates ranked exactly
-constexpr int kStageSel = 1024;                    // top_k the register selection stages in LDS
 
 struct IdxShared {
     union {
         float q[16 * 256];                         // scoring: the group's query heads
         struct { int8_t q8[kStageRows * 256]; uint16_t sc[kStageRows * 8]; } st;  // pooling
     } u;
-    uint32_t hist[4096 + 4];                       // + a trash bin for masked-off lanes
+    uint32_t hist[4096 + 64];                      // + one trash bin per lane for masked-off keys
     uint32_t cand_key[kCandMax + 1];               // + a trash slot
     int32_t cand_b[kCandMax + 1];
-    int32_t stage[kStageSel + 1];                  // selected blocks in output order, + a trash slot
-    uint32_t selbits[kKeysMax / 32];
+    uint32_t tmask[kIdxThreads];                   // selection: each thread's taken-block bits
+    uint32_t selbits[kKeysMax / 32 + 1];
     float newk[256];
-    float red[16];                                 // selection: per-wave max, min
+    float red[2 * (kIdxThreads / 64)];             // selection: per-wave max, min
     int tmp[16];
-    int flag, bin, need, ncand;
+    int flag, bin, need, ncand, cnt_b;
 };
 
 // Append of the decode token (K and V rows of KV head gh) and, when it
@@ -410,18 +417,27 @@ struct IdxShared {
 // kept dequantized in LDS as the block's last member.
 template <int HD>
 __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const FusedAppend &fa,
-                                  int s, int gh, int L, IdxShared &sh) {
+                                  int s, int gh, const int32_t *seq_len, int32_t max_seq_len, IdxShared &sh) {
     const int tid = threadIdx.x, per = (HD / 32) * 8;   // lanes per row
+    const int which = tid / per, j = (tid % per) / 8, e4 = tid % 8;
+    // the new rows do not depend on the length: their loads go out first
+    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dq[4];
+    if (tid < 2 * per)
+        load4(which ? fa.v_new : fa.k_new, fa.src_f16, ((int64_t)s * g.Hkv + gh) * HD + 32 * j + 4 * e4, x);
+    const int L = seq_len[s];
+    if (L < 1 || L > max_seq_len) return;
     const int p = L - 1;
     const int32_t pp = phys_page(g, v.page_table, s, p);
     if (pp < 0) { if (tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
     const int row = p % g.pt;
+    // a completed block's older members go to LDS while the new row is quantized
+    const bool complete = L % g.bt == 0;
+    const bool early = complete && g.bt > 1 && g.bt - 1 <= kStageRows;
+    const uint8_t *kpage = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
+    if (early) stage_rows<HD>(g, kpage, gh, row - (g.bt - 1), g.bt - 1, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
+    uint16_t dh;
+    const uint32_t pk = quant4(x, g.variant, &dh, dq);   // all lanes: DPP needs full groups
     if (tid < 2 * per) {
-        const int which = tid / per, j = (tid % per) / 8, e4 = tid % 8;
-        float x[4], dq[4];
-        load4(which ? fa.v_new : fa.k_new, fa.src_f16, ((int64_t)s * g.Hkv + gh) * HD + 32 * j + 4 * e4, x);
-        uint16_t dh;
-        const uint32_t pk = quant4(x, g.variant, &dh, dq);
         uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
         store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
         if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
@@ -429,11 +445,16 @@ __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const Fus
             for (int k = 0; k < 4; ++k) sh.newk[32 * j + 4 * e4 + k] = dq[k];
     }
     __syncthreads();
-    if (L % g.bt != 0) return;                     // the block is not complete yet
+    if (!complete) return;                         // the block is not complete yet
     const int b = p / g.bt;
-    const uint8_t *kpage = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
-    pool_block_dev<HD>(g, kpage, gh, row - (g.bt - 1), v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + b) * HD,
-                       sh.newk, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
+    float *dst = v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + b) * HD;
+    if (early) {
+#pragma clang fp contract(off)
+        if (tid < HD) dst[tid] = (pool_chain<HD>(sh.u.st.q8, sh.u.st.sc, g.bt - 1, tid, 0.0f, true) + sh.newk[tid]) *
+                                 g.inv_bt;
+        return;
+    }
+    pool_block_dev<HD>(g, kpage, gh, row - (g.bt - 1), dst, sh.newk, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
 }
 
 
@@ -490,45 +511,56 @@ __device__ void find_bin(IdxShared &sh, int need) {
 // emitted ascending between the forced sink and window blocks.
 //
 // Register path (select_regs): thread t holds the KPT scores of blocks
-// e_lo + [t*KPT, t*KPT+KPT) in registers, loaded in one round trip.  A
-// 4096-bin histogram, linear in the score between the smallest and largest
-// score (monotone in the key order, NaN in bin 0; scores with no finite
-// spread bin on the top 12 key bits instead), finds the bin holding the
-// threshold; the keys of that bin (a handful for any continuous spread) are
-// ranked exactly against each other; an ordered compaction writes the
-// winners.  The code is straight-line and predicated: this runs once per
-// layer in one workgroup, from a cold instruction cache, where each taken
-// branch costs a fetch round trip.
+// base + [t*KPT, t*KPT+KPT) (base = e_lo rounded down to 4) in registers,
+// loaded as aligned 16-byte vectors in one round trip.  A 4096-bin histogram,
+// linear in the score between the smallest and largest score (monotone in
+// the key order, NaN in bin 0; scores with no finite spread bin on the top 12
+// key bits instead), locates the threshold bin; wave 0 finds it with DPP
+// scans and ballots.  When that bin holds exactly the keys still needed (the
+// usual case: near the threshold a bin holds about one key) every key of it
+// is taken; otherwise its keys are ranked exactly against each other.  Each
+// thread then publishes a bit mask of its taken blocks and wave 0 writes them
+// in order.  The code is straight-line and predicated where it can be: it
+// runs once per layer in one workgroup, from a cold instruction cache.
 //
 // Fallback (select_radix): a threshold bin of more than kCandMax keys (heavy
-// ties) or more than kKeysMax eligible blocks takes three radix passes over
-// the keys in memory and an index-ordered tie count.
+// ties) or more eligible blocks than the register path holds takes three
+// radix passes over the keys in memory and an index-ordered tie count.
 template <int KPT>
 __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const Ranges &r, int32_t *out,
                                             IdxShared &sh) {
+    static_assert(KPT % 4 == 0 && KPT <= 32, "KPT: whole 16-byte vectors, at most 32 bits per thread");
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int b0 = r.e_lo + tid * KPT;
+    const int base = r.e_lo & ~3;
+    const int b0 = base + tid * KPT;
+    // sc is 16-byte aligned and padded to a multiple of 4 floats
+    const float4 *s4 = reinterpret_cast<const float4 *>(sc);
+    const int last4 = (r.e_hi - 1) >> 2;
     float sv[KPT];
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) sv[i] = sc[min(b0 + i, r.e_hi - 1)];
+    for (int k = 0; k < KPT / 4; ++k) {
+        const float4 x = s4[min((b0 >> 2) + k, last4)];
+        sv[4 * k] = x.x; sv[4 * k + 1] = x.y; sv[4 * k + 2] = x.z; sv[4 * k + 3] = x.w;
+    }
+    auto valid = [&](int i) { return b0 + i >= r.e_lo && b0 + i < r.e_hi; };
     float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-        const bool use = b0 + i < r.e_hi && sv[i] == sv[i];
+        const bool use = valid(i) && sv[i] == sv[i];
         lo = fminf(lo, use ? sv[i] : INFINITY);
         hi = fmaxf(hi, use ? sv[i] : -INFINITY);
     }
     hi = wave_max(hi);
     lo = -wave_max(-lo);
-    if (lane == 0) { sh.red[wid] = hi; sh.red[8 + wid] = lo; }
+    if (lane == 0) { sh.red[wid] = hi; sh.red[kIdxThreads / 64 + wid] = lo; }
     uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
 #pragma unroll
     for (int i = 0; i < 4096 / 4 / kIdxThreads; ++i) h4[tid + i * kIdxThreads] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < KPT * kIdxThreads / 32) sh.selbits[tid] = 0u;
+    for (int i = tid; i < KPT * kIdxThreads / 32 + 1; i += kIdxThreads) sh.selbits[i] = 0u;
     if (tid == 0) sh.ncand = 0;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kIdxThreads / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[8 + i]); }
+    for (int i = 0; i < kIdxThreads / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[kIdxThreads / 64 + i]); }
     const float span = hi - lo, scale = 4096.0f / span;
     const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
     // both bin maps, blended with a uniform mask (no per-element branch)
@@ -538,83 +570,99 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     for (int i = 0; i < KPT; ++i) {
         const uint32_t lb = (uint32_t)fminf((sv[i] - lo) * scale, 4095.0f);   // sv - lo >= 0 unless NaN
         bin[i] = ((sv[i] == sv[i] ? lb : 0u) & lm) | ((score_key(sv[i]) >> 20) & ~lm);
-        atomicAdd(&sh.hist[b0 + i < r.e_hi ? bin[i] : 4096u], 1u);   // unconditional: no skip branch
+        // unconditional (no skip branch); masked-off keys go to this lane's
+        // trash bin, so they never pile onto one address
+        atomicAdd(&sh.hist[valid(i) ? bin[i] : 4096u + (uint32_t)lane], 1u);
     }
     __syncthreads();
-    // threshold bin: thread t owns bins [16t, 16t+16); the need-th largest
-    // key lies in the thread whose bins straddle it
-    {
-        constexpr int PER = 4096 / kIdxThreads;
-        uint32_t c[PER];
+    // threshold bin, by wave 0: lane l sums bins [64l, 64l+64); the lane whose
+    // bins straddle the top_k-th largest key is found by a scan and a ballot,
+    // then its 64 bins are spread over the wave for the same search
+    if (wid == 0) {
+        uint32_t own = 0;
 #pragma unroll
-        for (int i = 0; i < PER / 4; ++i) {
-            const uint4 x = h4[tid * (PER / 4) + i];
-            c[4 * i] = x.x; c[4 * i + 1] = x.y; c[4 * i + 2] = x.z; c[4 * i + 3] = x.w;
+        for (int k = 0; k < 16; ++k) {
+            const uint4 x = h4[lane * 16 + k];
+            own += x.x + x.y + x.z + x.w;
         }
-        int own = 0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) own += (int)c[i];
-        int total;
-        const int excl = block_excl_sum<kIdxThreads>(own, sh.tmp, &total);
-        int run = total - excl - own, fb = -1, fneed = 0;   // keys in higher bins
-#pragma unroll
-        for (int i = PER - 1; i >= 0; --i) {
-            const bool hit = run < g.topk && run + (int)c[i] >= g.topk;   // exactly one bin overall
-            fb = hit ? tid * PER + i : fb;
-            fneed = hit ? g.topk - run : fneed;
-            run += (int)c[i];
-        }
-        if (fb >= 0) { sh.bin = fb; sh.need = fneed; }
+        const int incl = wave_incl_scan((int)own);
+        const int total = __builtin_amdgcn_readlane(incl, 63);
+        const int above = total - incl;               // keys in the bins of higher lanes
+        const int ls = __builtin_ctzll(__ballot(above < g.topk && above + (int)own >= g.topk));
+        const int above_l = __builtin_amdgcn_readlane(above, ls);
+        const int c = (int)sh.hist[ls * 64 + lane];
+        const int ic = wave_incl_scan(c);
+        const int run = above_l + __builtin_amdgcn_readlane(ic, 63) - ic;   // keys in higher bins
+        const int j = __builtin_ctzll(__ballot(run < g.topk && run + c >= g.topk));
+        if (lane == j) { sh.bin = ls * 64 + j; sh.need = g.topk - run; sh.cnt_b = c; }
     }
     __syncthreads();
     const uint32_t B = (uint32_t)sh.bin;
     const int need = sh.need;
-    const int cB = (int)sh.hist[B];
+    const int cB = sh.cnt_b;
     if (cB > kCandMax) return false;
-    int nc = 0;
+    if (cB > need) {
+        // rank the threshold bin's keys exactly: (key desc, index asc)
+        int nc = 0;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) nc += (b0 + i < r.e_hi && bin[i] == B);
-    if (nc > 0) {
-        int slot = atomicAdd(&sh.ncand, nc);
+        for (int i = 0; i < KPT; ++i) nc += (valid(i) && bin[i] == B);
+        if (nc > 0) {
+            int slot = atomicAdd(&sh.ncand, nc);
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const bool c = b0 + i < r.e_hi && bin[i] == B;
-            const int at = c ? slot : kCandMax;
-            sh.cand_key[at] = score_key(sv[i]);
-            sh.cand_b[at] = b0 + i;
-            slot += c;
+            for (int i = 0; i < KPT; ++i) {
+                const bool c = valid(i) && bin[i] == B;
+                const int at = c ? slot : kCandMax;
+                sh.cand_key[at] = score_key(sv[i]);
+                sh.cand_b[at] = b0 + i;
+                slot += c;
+            }
         }
-    }
-    __syncthreads();
-    if (tid < cB) {
-        const uint32_t k = sh.cand_key[tid];
-        const int b = sh.cand_b[tid];
-        int rank = 0;
-        for (int j = 0; j < cB; ++j) {
-            const uint32_t kj = sh.cand_key[j];
-            rank += (kj > k) || (kj == k && sh.cand_b[j] < b);
+        __syncthreads();
+        if (tid < cB) {
+            const uint32_t k = sh.cand_key[tid];
+            const int b = sh.cand_b[tid];
+            int rank = 0;
+            for (int jj = 0; jj < cB; ++jj) {
+                const uint32_t kj = sh.cand_key[jj];
+                rank += (kj > k) || (kj == k && sh.cand_b[jj] < b);
+            }
+            if (rank < need) atomicOr(&sh.selbits[(b - base) >> 5], 1u << ((b - base) & 31));
         }
-        if (rank < need) atomicOr(&sh.selbits[(b - r.e_lo) >> 5], 1u << ((b - r.e_lo) & 31));
+        __syncthreads();
     }
-    __syncthreads();
-    // KPT divides 32: the thread's bits sit in one word
-    const uint32_t wb = sh.selbits[(tid * KPT) >> 5] >> ((tid * KPT) & 31);
-    bool take[KPT];
-    int cnt = 0;
+    // the thread's KPT bits start at bit tid*KPT: two words cover them
+    uint32_t wb = 0xffffffffu;
+    if (cB > need) {
+        const int e = tid * KPT;
+        const uint64_t w2 = (uint64_t)sh.selbits[e >> 5] | ((uint64_t)sh.selbits[(e >> 5) + 1] << 32);
+        wb = (uint32_t)(w2 >> (e & 31));
+    }
+    uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-        take[i] = b0 + i < r.e_hi && (bin[i] > B || (bin[i] == B && ((wb >> i) & 1u)));
-        cnt += take[i];
+        const bool take = valid(i) && (bin[i] > B || (bin[i] == B && ((wb >> i) & 1u)));
+        m |= (uint32_t)take << i;
     }
-    int tot;
-    int pos = block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-        sh.stage[take[i] && pos < g.topk ? pos : kStageSel] = b0 + i;
-        pos += take[i];
-    }
+    sh.tmask[tid] = m;
     __syncthreads();
-    for (int i = tid; i < g.topk; i += kIdxThreads) out[g.sink + i] = sh.stage[i];
+    // ordered emission by wave 0: lane l owns threads 4l .. 4l+3
+    if (wid == 0) {
+        const uint4 mm = reinterpret_cast<const uint4 *>(sh.tmask)[lane];
+        const uint32_t w4[4] = {mm.x, mm.y, mm.z, mm.w};
+        const int cnt = __builtin_popcount(mm.x) + __builtin_popcount(mm.y) + __builtin_popcount(mm.z) +
+                        __builtin_popcount(mm.w);
+        int pos = wave_incl_scan(cnt) - cnt;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t x = w4[q];
+            const int tb = base + (4 * lane + q) * KPT;
+            while (x) {
+                if (pos < g.topk) out[g.sink + pos] = tb + __builtin_ctz(x);
+                ++pos;
+                x &= x - 1u;
+            }
+        }
+    }
     return true;
 }
 
@@ -666,10 +714,13 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
         return;
     }
     bool done = false;
-    if (g.topk > kStageSel) done = false;
-    else if (ne <= 4 * kIdxThreads) done = select_regs<4>(g, sc, r, out, sh);
-    else if (ne <= 16 * kIdxThreads) done = select_regs<16>(g, sc, r, out, sh);
-    else if (ne <= kKeysMax) done = select_regs<kKeysMax / kIdxThreads>(g, sc, r, out, sh);
+    const int span = r.e_hi - (r.e_lo & ~3);      // blocks the register path covers
+    if (span <= 4 * kIdxThreads) done = select_regs<4>(g, sc, r, out, sh);
+    else if (span <= 8 * kIdxThreads) done = select_regs<8>(g, sc, r, out, sh);
+    else if (span <= 12 * kIdxThreads) done = select_regs<12>(g, sc, r, out, sh);
+    else if (span <= 16 * kIdxThreads) done = select_regs<16>(g, sc, r, out, sh);
+    else if (span <= 24 * kIdxThreads) done = select_regs<24>(g, sc, r, out, sh);
+    else if (span <= kKeysMax) done = select_regs<kKeysMax / kIdxThreads>(g, sc, r, out, sh);
     if (!done) select_radix(g, sc, r, out, sh);
     for (int i = tid; i < g.sink; i += kIdxThreads) out[i] = i;
     const int nwin = r.b_last - r.fw + 1;
@@ -685,12 +736,18 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
-    const int L = seq_len[s];
-    const bool ok = L >= 1 && L <= max_seq_len;
     if (fa.enabled && c == n_chunks) {             // the append workgroup
-        if (ok) fused_append_pool<HD>(g, v, fa, s, gh, L, sh);
+        fused_append_pool<HD>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
         return;
     }
+    // the group's query rows do not depend on the length either
+    constexpr int QV = (G * HD / 4 + kIdxThreads - 1) / kIdxThreads;
+    const float4 *qg4 = reinterpret_cast<const float4 *>(q + ((int64_t)s * g.H + (int64_t)gh * G) * HD);
+    float4 qv[QV];
+#pragma unroll
+    for (int i = 0; i < QV; ++i) qv[i] = qg4[min(tid + i * kIdxThreads, G * HD / 4 - 1)];
+    const int L = seq_len[s];
+    const bool ok = L >= 1 && L <= max_seq_len;
     const int pair = s * g.Hkv + gh;
     float *sc = ws.scores + (int64_t)pair * ws.nb_cap;
     // The pooled keys this lane scores do not depend on the sequence length
@@ -709,9 +766,9 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         if (ne > g.topk && c * kBlocksPerChunk < ne) {
             const bool act = bi < ne;
             const int b = r.e_lo + bi;
-            const float *qg = q + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
-            for (int i = tid * 4; i < G * HD; i += kIdxThreads * 4)
-                *reinterpret_cast<float4 *>(&sh.u.q[i]) = *reinterpret_cast<const float4 *>(qg + i);
+#pragma unroll
+            for (int i = 0; i < QV; ++i)
+                if (tid + i * kIdxThreads < G * HD / 4) reinterpret_cast<float4 *>(sh.u.q)[tid + i * kIdxThreads] = qv[i];
             __syncthreads();
             float acc[G];
 #pragma unroll
@@ -784,82 +841,102 @@ struct MergeCfg {
 };
 
 template <int G, int HD, int NT>
-__device__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Lh,
-                               float *scratch, int scratch_floats) {
+__device__ __attribute__((noinline)) void merge_partials_general(const Ws &ws, int pair, int parts_act, float *og,
+                                                                 float *Lh) {
     using M = MergeCfg<G, HD, NT>;
-    constexpr int VW = M::VW, OPT = M::OPT, MAXP = M::MAXP, NV = G * HD / VW;
-    constexpr int NW = NT / 64;
+    constexpr int VW = M::VW, OPT = M::OPT, NV = G * HD / VW, NW = NT / 64;
     using vec = float __attribute__((ext_vector_type(VW)));
     const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
     const int64_t pb = (int64_t)pair * ws.n_tiles * G;
     const float *pml = ws.part_ml + pb * 2;
     const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
-    // the first (m, l) of this wave's first head, then the first batch of O
-    float2 ml0 = make_float2(-INFINITY, 0.0f);
-    if (wv < G && ln < parts_act) ml0 = *reinterpret_cast<const float2 *>(pml + ((int64_t)ln * G + wv) * 2);
-    vec ov[OPT][MAXP];
-#pragma unroll
-    for (int r = 0; r < OPT; ++r) {
-        const int k = tid + r * NT;
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i)
-            ov[r][i] = (k < NV && i < parts_act) ? po[(int64_t)i * NV + k] : vec(0.0f);
-    }
-    // weights w_i,h = 2^(m_i,h - M_h) into LDS, L_h = sum_i w_i,h l_i,h
-    const int nwt = min(parts_act, scratch_floats / G);
-    float *wt = scratch;                                   // [nwt][G]
     for (int h = wv; h < G; h += NW) {
         float Mx = -INFINITY;
-        for (int i0 = 0; i0 < parts_act; i0 += 64) {
-            const int i = i0 + ln;
-            float m = -INFINITY;
-            if (h == wv && i0 == 0) m = ml0.x;
-            else if (i < parts_act) m = pml[((int64_t)i * G + h) * 2];
-            Mx = fmaxf(Mx, m);
-        }
+        for (int i = ln; i < parts_act; i += 64) Mx = fmaxf(Mx, pml[((int64_t)i * G + h) * 2]);
         Mx = wave_max(Mx);
         float Ls = 0.0f;
-        for (int i0 = 0; i0 < parts_act; i0 += 64) {
-            const int i = i0 + ln;
-            float2 ml = ml0;
-            if (!(h == wv && i0 == 0))
-                ml = i < parts_act ? *reinterpret_cast<const float2 *>(pml + ((int64_t)i * G + h) * 2)
-                                   : make_float2(-INFINITY, 0.0f);
-            const float w = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - Mx);
-            if (i < nwt) wt[i * G + h] = w;
-            Ls += w * ml.y;
+        for (int i = ln; i < parts_act; i += 64) {
+            const float m = pml[((int64_t)i * G + h) * 2], l = pml[((int64_t)i * G + h) * 2 + 1];
+            Ls += (m == -INFINITY ? 0.0f : exp2f(m - Mx)) * l;
         }
         Ls = wave_sum(Ls);
         if (ln == 0) { Lh[h] = Ls; Lh[G + h] = Mx; }
     }
     __syncthreads();
-    auto w_of = [&](int i, int h) -> float {
-        if (i < nwt) return wt[i * G + h];
-        const float m = pml[((int64_t)i * G + h) * 2];
-        return m == -INFINITY ? 0.0f : exp2f(m - Lh[G + h]);
-    };
+    for (int r = 0; r < OPT; ++r) {
+        const int k = tid + r * NT;
+        if (k >= NV) break;
+        const int h = k * VW / HD;
+        const float Mx = Lh[G + h], Ls = Lh[h];
+        vec acc = vec(0.0f);
+        for (int i = 0; i < parts_act; ++i) {
+            const float m = pml[((int64_t)i * G + h) * 2];
+            if (m != -INFINITY) acc += exp2f(m - Mx) * po[(int64_t)i * NV + k];
+        }
+        reinterpret_cast<vec *>(og)[k] = Ls > 0.0f ? acc * (1.0f / Ls) : vec(0.0f);
+    }
+}
+
+template <int G, int HD, int NT>
+__device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Lh,
+                                               float *scratch, int scratch_floats) {
+    using M = MergeCfg<G, HD, NT>;
+    constexpr int VW = M::VW, OPT = M::OPT, MAXP = M::MAXP, NV = G * HD / VW;
+    constexpr int NW = NT / 64, HPW = (G + NW - 1) / NW;
+    using vec = float __attribute__((ext_vector_type(VW)));
+    if (parts_act > MAXP || 64 * G > scratch_floats) {
+        merge_partials_general<G, HD, NT>(ws, pair, parts_act, og, Lh);
+        return;
+    }
+    // Straight-line path: every load unconditional (clamped to the last part),
+    // masked by selects, so a cold instruction cache sees no taken branch.
+    const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
+    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
+    const float *pml = ws.part_ml + pb * 2;
+    const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
+    const int lp = parts_act - 1;
+    float2 ml[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+        const int h = min(wv + j * NW, G - 1);
+        ml[j] = *reinterpret_cast<const float2 *>(pml + ((int64_t)min(ln, lp) * G + h) * 2);
+    }
+    vec ov[OPT][MAXP];
+#pragma unroll
+    for (int r = 0; r < OPT; ++r) {
+        const int k = min(tid + r * NT, NV - 1);
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) ov[r][i] = po[(int64_t)min(i, lp) * NV + k];
+    }
+    // weights w_i,h = 2^(m_i,h - M_h) into LDS (lane = part), L_h = sum_i w_i,h l_i,h
+    float *wt = scratch;                                   // [64][G]
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+        const int h = wv + j * NW;
+        if (h < G) {
+            const bool valid = ln < parts_act;
+            const float m = valid ? ml[j].x : -INFINITY;
+            const float Mx = wave_max(m);
+            const float w = m == -INFINITY ? 0.0f : exp2f(m - Mx);
+            wt[ln * G + h] = w;
+            const float Ls = wave_sum(valid ? w * ml[j].y : 0.0f);
+            if (ln == 0) Lh[h] = Ls;
+        }
+    }
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < OPT; ++r) {
         const int k = tid + r * NT;
-        if (k < NV) {
-            const int h = k * VW / HD;
-            vec acc = vec(0.0f);
+        const int h = min(k, NV - 1) * VW / HD;
+        vec acc = vec(0.0f);
 #pragma unroll
-            for (int i = 0; i < MAXP; ++i)
-                if (i < parts_act) acc += w_of(i, h) * ov[r][i];
-            // parts beyond MAXP: further batches, MAXP loads in flight each
-            for (int i0 = MAXP; i0 < parts_act; i0 += MAXP) {
-                vec ob[MAXP];
-#pragma unroll
-                for (int i = 0; i < MAXP; ++i) ob[i] = i0 + i < parts_act ? po[(int64_t)(i0 + i) * NV + k] : vec(0.0f);
-#pragma unroll
-                for (int i = 0; i < MAXP; ++i)
-                    if (i0 + i < parts_act) acc += w_of(i0 + i, h) * ob[i];
-            }
-            const float Ls = Lh[h];
-            const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-            reinterpret_cast<vec *>(og)[k] = Ls > 0.0f ? acc * inv : vec(0.0f);
+        for (int i = 0; i < MAXP; ++i) {
+            const vec t = wt[i * G + h] * ov[r][i];
+            acc += i < parts_act ? t : vec(0.0f);
         }
+        const float Ls = Lh[h];
+        const vec o = Ls > 0.0f ? acc * (1.0f / Ls) : vec(0.0f);
+        if (k < NV) reinterpret_cast<vec *>(og)[k] = o;
     }
 }
 
@@ -1152,7 +1229,6 @@ struct FastGroup {
     uint16_t pl[G][HD / 32][64];               // its fp16 remainder (low part)
     float o[2][G][HD];                         // the tile's O, one slice per cell half
     float m[G], l[G];
-    int page, row0, nvalid;
 };
 
 template <int HD, int G, int TG>
@@ -1164,10 +1240,12 @@ struct FastShared {
     int flag;
 };
 
-template <int HD, int G, int TG>
+// DENSE: attend every block of the sequence (sel is not read).
+template <int HD, int G, int TG, bool DENSE>
 __global__ void __launch_bounds__((FastCfg<HD, G, TG>::NT))
-k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
-          const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *__restrict__ out, Ws ws) {
+k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len,
+          int32_t max_seq_len, const int32_t *__restrict__ sel, const int32_t *__restrict__ nsel, int32_t max_sel,
+          float *__restrict__ out, Ws ws) {
     using C = FastCfg<HD, G, TG>;
     constexpr int NB = C::NB;
     __shared__ FastShared<HD, G, TG> sh;
@@ -1177,36 +1255,54 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     const int w = __builtin_amdgcn_readfirstlane(lt >> 6), lane = lt & 63;
     FastGroup<HD, G> &gr = sh.grp[gi];
     const int pair = s * g.Hkv + gh;
+    const int part = blockIdx.x;
+    const int tile = part * TG + gi;                   // uniform per tile group
+    const int tpb = g.bt / 64;                         // tiles per block
+    // The length, the selection count and this tile's selected block go out
+    // together (the block index is clamped for the load and checked after),
+    // and so do the query rows of the heads this wave quantizes.
+    // Unconditional loads from selected pointers, all issued before any is
+    // used: no branch may sit between them (a branch makes the compiler wait
+    // for every load in flight).
     const int L = seq_len[s];
+    const int n_raw = DENSE ? 0 : nsel[pair];
+    const int blk_raw = DENSE ? 0 : sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
+    constexpr int DPL = HD / 64, NWV = C::NT / 64, QPW = (G + NWV - 1) / NWV;
+    float xq[QPW][DPL];
+    {
+        const int wid = tid >> 6;
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const int h = min(wid + j * NWV, G - 1);
+            const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + h) * HD + lane * DPL;
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) xq[j][k] = qh[k];
+        }
+    }
+    const int blk = DENSE ? tile / tpb : blk_raw;
+    // the tile's page-table entry needs only the block: its load goes out
+    // before the length and the count are known (clamped into the table)
+    const int off = (tile % tpb) * 64;
+    const int64_t t0 = (int64_t)blk * g.bt + off;
+    const int t0c = (int)min(max(t0, (int64_t)0), (int64_t)g.pps * g.pt - 1);
+    const int32_t *__restrict__ ptab = v.page_table;
+    const int32_t praw = ptab[(int64_t)s * g.pps + t0c / g.pt];
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
-        n = sel ? nsel[pair] : (L - 1) / g.bt + 1;
+        n = DENSE ? (L - 1) / g.bt + 1 : n_raw;
         n = n < max_sel ? n : max_sel;
     }
-    const int tiles_act = n * (g.bt / 64);
+    const int tiles_act = n * tpb;
     const int parts_act = (tiles_act + TG - 1) / TG;
-    const int part = blockIdx.x;
     if (ok && part < parts_act) {
-        const int tile = part * TG + gi;
-        if (lt == 0) {
-            int pg = -1, row0 = 0, nv = 0;
-            if (tile < tiles_act) {
-                const int slot = tile / (g.bt / 64), off = (tile % (g.bt / 64)) * 64;
-                const int blk = sel ? sel[(int64_t)pair * max_sel + slot] : slot;
-                const int t0 = blk * g.bt + off;
-                if (blk >= 0 && t0 < L) {
-                    pg = phys_page(g, v.page_table, s, t0);
-                    row0 = t0 % g.pt;
-                    nv = min(64, L - t0);
-                    if (pg < 0) { set_status(v.status, QWFN_STATUS_PAGE_RANGE); nv = 0; }
-                }
-            }
-            gr.page = pg; gr.row0 = row0; gr.nvalid = nv;
-        }
-        __syncthreads();
-        const int nv = gr.nvalid, row0 = gr.row0;
-        const int64_t pbase = (int64_t)(nv > 0 ? gr.page : 0) * g.page_bytes;
+        // the tile's page, computed by every lane of the group (no LDS hand-off)
+        const bool in = tile < tiles_act && blk >= 0 && t0 < L;
+        const bool pg_ok = praw >= 0 && praw < g.n_phys;
+        if (in && !pg_ok && lt == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+        const int nv = in && pg_ok ? min(64, L - t0c) : 0;
+        const int row0 = t0c % g.pt;
+        const int64_t pbase = (int64_t)(nv > 0 ? praw : 0) * g.page_bytes;
         const uint8_t *kp = (const uint8_t *)v.k_pages + pbase;
         const uint8_t *vp = (const uint8_t *)v.v_pages + pbase;
         const int tl = gh * (g.pt / 64) + row0 / 64;       // tile index inside the pool page
@@ -1234,13 +1330,14 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         // 2e-7 * amax): the operands of exact integer dot products against the
         // int8 key quants.  One wave per head.
         {
-            constexpr int DPL = HD / 64;
-            const int wid = tid >> 6, nwv = C::NT >> 6;
-            for (int h = wid; h < G; h += nwv) {
-                const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + h) * HD + lane * DPL;
+            const int wid = tid >> 6;
+#pragma unroll
+            for (int jq = 0; jq < QPW; ++jq) {
+                const int h = wid + jq * NWV;
+                if (h >= G) break;
                 float x[DPL], a = 0.0f;
 #pragma unroll
-                for (int k = 0; k < DPL; ++k) { x[k] = qh[k]; a = fmaxf(a, fabsf(x[k])); }
+                for (int k = 0; k < DPL; ++k) { x[k] = xq[jq][k]; a = fmaxf(a, fabsf(x[k])); }
                 const float amax = wave_max(a);
                 const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
                 int8_t *pa = reinterpret_cast<int8_t *>(sh.qa[h]) + lane * DPL;
@@ -1409,8 +1506,12 @@ static void launch_attn_q8_t(const Geo &g, const qwfn_kv_view &v, const float *q
                              float *out, const Ws &ws, hipStream_t st) {
     const int n_parts = (ws.n_tiles + TG - 1) / TG;
     const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
-    hipLaunchKernelGGL((k_attn_q8<HD, G, TG>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q, seq_len,
-                       max_seq_len, sel, nsel, max_sel, out, ws);
+    if (sel)
+        hipLaunchKernelGGL((k_attn_q8<HD, G, TG, false>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q,
+                           seq_len, max_seq_len, sel, nsel, max_sel, out, ws);
+    else
+        hipLaunchKernelGGL((k_attn_q8<HD, G, TG, true>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q,
+                           seq_len, max_seq_len, sel, nsel, max_sel, out, ws);
 }
 
 // ---------------------------------------------------------------------------
