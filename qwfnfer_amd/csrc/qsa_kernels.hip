@@ -81,6 +81,36 @@ __device__ __forceinline__ float lane63(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Raw buffer loads: one descriptor per array, a per-lane byte offset and a
+// uniform (SGPR) byte offset, so a run of loads costs one instruction each
+// with no 64-bit address arithmetic.  Offsets at or past `bytes` read 0.
+using BufRsrc = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ BufRsrc buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+// Cache policy of a load that must see other workgroups' released stores
+// without an L2 invalidate: sc1, the agent-scope coherent load.
+constexpr int kCpolSc1 = 16;
+template <int VW, int CP = 0> struct BufLoad;
+template <int CP> struct BufLoad<1, CP> {
+    using T = float __attribute__((ext_vector_type(1)));
+    static __device__ __forceinline__ T at(BufRsrc r, int voff, int soff) {
+        T v; v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CP)); return v;
+    }
+};
+template <int CP> struct BufLoad<2, CP> {
+    using T = float __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ T at(BufRsrc r, int voff, int soff) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, CP));
+    }
+};
+template <int CP> struct BufLoad<4, CP> {
+    using T = float __attribute__((ext_vector_type(4)));
+    static __device__ __forceinline__ T at(BufRsrc r, int voff, int soff) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CP));
+    }
+};
+
 // Maximum over the wave, returned to every lane.
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dppf<kDppQuadXor1>(v, v));
@@ -123,6 +153,12 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
 // acquire fence before reading the others' results.  One fence pair per
 // workgroup rather than per wave: on gfx950 an agent-scope fence writes back
 // and invalidates the XCD's L2.  Returns true in the last workgroup.
+//
+// ACQ = false skips the acquire fence (an L2 invalidate, ~0.5 us): the last
+// workgroup must then read the others' results only through device-coherent
+// loads (buffer loads with kCpolSc1), or take the fence itself before plain
+// loads.
+template <bool ACQ = true>
 __device__ __forceinline__ bool arrive_last(int32_t *counter, int expected, int *flag) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -130,7 +166,7 @@ __device__ __forceinline__ bool arrive_last(int32_t *counter, int expected, int 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool last = old == expected - 1;
-        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        if (ACQ && last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         *flag = last;
     }
     __syncthreads();
@@ -533,14 +569,14 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int base = r.e_lo & ~3;
     const int b0 = base + tid * KPT;
-    // sc is 16-byte aligned and padded to a multiple of 4 floats
-    const float4 *s4 = reinterpret_cast<const float4 *>(sc);
-    const int last4 = (r.e_hi - 1) >> 2;
+    // sc is 16-byte aligned; device-coherent buffer loads (the scoring
+    // workgroups' released stores, no L2 invalidate), reads past e_hi give 0
+    const BufRsrc rs = buf_rsrc(sc, (uint32_t)((r.e_hi + 3) & ~3) * 4u);   // whole vectors (row padded to 64)
     float sv[KPT];
 #pragma unroll
     for (int k = 0; k < KPT / 4; ++k) {
-        const float4 x = s4[min((b0 >> 2) + k, last4)];
-        sv[4 * k] = x.x; sv[4 * k + 1] = x.y; sv[4 * k + 2] = x.z; sv[4 * k + 3] = x.w;
+        const auto x = BufLoad<4, kCpolSc1>::at(rs, b0 * 4 + 16 * k, 0);
+        sv[4 * k] = x[0]; sv[4 * k + 1] = x[1]; sv[4 * k + 2] = x[2]; sv[4 * k + 3] = x[3];
     }
     auto valid = [&](int i) { return b0 + i >= r.e_lo && b0 + i < r.e_hi; };
     float lo = INFINITY, hi = -INFINITY;
@@ -666,8 +702,9 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     return true;
 }
 
-__device__ __attribute__((noinline)) void select_radix(const Geo &g, const float *sc, const Ranges &r,
+__device__ __forceinline__ void select_radix(const Geo &g, const float *sc, const Ranges &r,
                                                        int32_t *out, IdxShared &sh) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads of the scores below
     const int tid = threadIdx.x;
     const int ne = r.e_hi - r.e_lo;
     const int per = (ne + kIdxThreads - 1) / kIdxThreads;
@@ -797,7 +834,8 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         }
     }
     // completion count: the last workgroup of this (sequence, KV head) selects
-    if (!arrive_last(&ws.cnt_idx[pair], n_chunks, &sh.flag)) return;
+    // the selection reads the scores with device-coherent loads (or fences)
+    if (!arrive_last<false>(&ws.cnt_idx[pair], n_chunks, &sh.flag)) return;
     if (tid == 0) ws.cnt_idx[pair] = 0;
     int32_t *out = sel + (int64_t)pair * max_sel;
     if (!ok) {
@@ -841,11 +879,12 @@ struct MergeCfg {
 };
 
 template <int G, int HD, int NT>
-__device__ __attribute__((noinline)) void merge_partials_general(const Ws &ws, int pair, int parts_act, float *og,
+__device__ __forceinline__ void merge_partials_general(const Ws &ws, int pair, int parts_act, float *og,
                                                                  float *Lh) {
     using M = MergeCfg<G, HD, NT>;
     constexpr int VW = M::VW, OPT = M::OPT, NV = G * HD / VW, NW = NT / 64;
     using vec = float __attribute__((ext_vector_type(VW)));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads below
     const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
     const int64_t pb = (int64_t)pair * ws.n_tiles * G;
     const float *pml = ws.part_ml + pb * 2;
@@ -888,25 +927,27 @@ __device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts
         merge_partials_general<G, HD, NT>(ws, pair, parts_act, og, Lh);
         return;
     }
-    // Straight-line path: every load unconditional (clamped to the last part),
-    // masked by selects, so a cold instruction cache sees no taken branch.
+    // Straight-line path: every load unconditional, through buffer
+    // descriptors sized to the live parts (loads past them read 0), so a cold
+    // instruction cache sees no taken branch.
     const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
     const int64_t pb = (int64_t)pair * ws.n_tiles * G;
-    const float *pml = ws.part_ml + pb * 2;
-    const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
-    const int lp = parts_act - 1;
+    using L = BufLoad<VW, kCpolSc1>;
+    const BufRsrc rm = buf_rsrc(ws.part_ml + pb * 2, (uint32_t)parts_act * G * 8u);
+    const BufRsrc ro = buf_rsrc(ws.part_o + pb * HD, (uint32_t)parts_act * G * HD * 4u);
     float2 ml[HPW];
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
         const int h = min(wv + j * NW, G - 1);
-        ml[j] = *reinterpret_cast<const float2 *>(pml + ((int64_t)min(ln, lp) * G + h) * 2);
+        const auto x = BufLoad<2, kCpolSc1>::at(rm, (ln * G + h) * 8, 0);
+        ml[j] = make_float2(x[0], x[1]);
     }
-    vec ov[OPT][MAXP];
+    typename L::T ov[OPT][MAXP];
 #pragma unroll
     for (int r = 0; r < OPT; ++r) {
         const int k = min(tid + r * NT, NV - 1);
 #pragma unroll
-        for (int i = 0; i < MAXP; ++i) ov[r][i] = po[(int64_t)min(i, lp) * NV + k];
+        for (int i = 0; i < MAXP; ++i) ov[r][i] = L::at(ro, k * VW * 4, i * G * HD * 4);
     }
     // weights w_i,h = 2^(m_i,h - M_h) into LDS (lane = part), L_h = sum_i w_i,h l_i,h
     float *wt = scratch;                                   // [64][G]
@@ -929,11 +970,9 @@ __device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts
         const int k = tid + r * NT;
         const int h = min(k, NV - 1) * VW / HD;
         vec acc = vec(0.0f);
+        // parts past parts_act read 0 with weight 0
 #pragma unroll
-        for (int i = 0; i < MAXP; ++i) {
-            const vec t = wt[i * G + h] * ov[r][i];
-            acc += i < parts_act ? t : vec(0.0f);
-        }
+        for (int i = 0; i < MAXP; ++i) acc += wt[i * G + h] * ov[r][i];
         const float Ls = Lh[h];
         const vec o = Ls > 0.0f ? acc * (1.0f / Ls) : vec(0.0f);
         if (k < NV) reinterpret_cast<vec *>(og)[k] = o;
@@ -1165,7 +1204,8 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         }
     }
     // completion count; the last workgroup of the pair merges the partials
-    if (!arrive_last(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
+    // the combine reads the partials with device-coherent loads (or fences)
+    if (!arrive_last<false>(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
     if (tid == 0) ws.cnt_attn[pair] = 0;
     float *og = out + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
     if (!ok || parts_act == 0) {
@@ -1487,7 +1527,8 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
             }
         }
     }
-    if (!arrive_last(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
+    // the combine reads the partials with device-coherent loads (or fences)
+    if (!arrive_last<false>(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
     if (tid == 0) ws.cnt_attn[pair] = 0;
     float *og = out + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
     if (!ok || parts_act == 0) {
