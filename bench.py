@@ -9,10 +9,11 @@ tokens, one decode token per step at contexts 4096, 65536 and 163840.
 A step = one decode token through all 12 layers; each layer is the fused path
 of graph_builder::sparse_attn_decode: append the token's K/V (q8_0), pool the
 block it completes, score the pooled blocks, select, attend (two kernels:
-append+select, attention).  The decode position walks the last 64 positions
-of the context (seq_len = ctx-64 .. ctx-1, advanced on the device at the
-start of every step), so one step in 64 completes a block and pools it, as in a
-real decode; each step rewrites its position (an idempotent overwrite).
+append+select, attention).  The decode position advances one token per step
+(seq_len += 1 on the device at the start of every step, one small kernel), so
+one step in 64 completes a block and pools it, as in a real decode; every
+replica keeps its own position and its caches have room for DECODE_ROOM more
+tokens past the context.
 Inputs are resident in HBM before the timed region; per-context working sets
 below 512 MiB are replicated and rotated so the 256 MB MALL does not serve them.
 
@@ -32,7 +33,9 @@ sys.path.insert(0, ROOT)
 
 METRIC = "sparse decode attn µs/layer @4K & 160K ctx (q8_0 KV); % of HBM roofline"
 HBM_PEAK_GBS = 8000.0          # MI355X published HBM3E peak
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")   # rocprofv3 PMC summary (FETCH/WRITE_SIZE)
 ROTATE_BYTES = 512 << 20
+DECODE_ROOM = 2048             # tokens a replica may decode past its context
 
 
 def log(*a):
@@ -51,6 +54,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
     ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
+                    help="first copy BYTES device-to-device 3 times (a plain copy kernel of known size, "
+                         "the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -96,7 +102,8 @@ class Runner:
         self.lengths = lengths
         n_seq = len(lengths)
         self.n_seq = n_seq
-        self.max_len = max(lengths)
+        self.max_len = max(lengths) + DECODE_ROOM
+        assert pages_per_seq * cfg.page_tokens >= self.max_len, "page table leaves no decode room"
         pb = cfg.page_bytes()
         per_stack = n_layer * 2 * page_table.numel() * pb
         self.n_inst = max(1, math.ceil(ROTATE_BYTES / per_stack))
@@ -116,11 +123,8 @@ class Runner:
         self.vn = [torch.randn((n_seq, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
                    for _ in range(n_layer)]
         self.out = [torch.empty((n_seq, cfg.n_head, cfg.head_dim), device="cuda") for _ in range(n_layer)]
-        # seq_len = base + (ctr & 63), advanced at the start of every step
-        self.base = torch.tensor([max(0, L - 64) for L in lengths], dtype=torch.int32, device="cuda")
-        self.ctr = torch.zeros(1, dtype=torch.int32, device="cuda")
-        self.ph = torch.zeros(1, dtype=torch.int32, device="cuda")
-        self.seq_len = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+        # one position per replica, advanced by one token at the start of every step
+        self.seq_lens = [torch.tensor(lengths, dtype=torch.int32, device="cuda") for _ in range(self.n_inst)]
         self.ws = qsa.Workspace(cfg, n_seq, self.max_len)
         msel = cfg.max_selected(self.max_len)
         self.sel = torch.empty((n_seq, cfg.n_head_kv, msel), dtype=torch.int32, device="cuda")
@@ -133,33 +137,29 @@ class Runner:
                 if qsa.read_status(c):
                     raise RuntimeError("cache fill reported out-of-range rows")
 
-    def layer(self, inst, il, ev=None):
+    def layer(self, inst, il):
         qsa = self.qsa
         c = self.stacks[inst][il]
-        if ev is not None:
-            ev[0].record()
-        qsa.decode_append_select(c, self.q[il], self.kn[il], self.vn[il], self.seq_len, self.max_len, self.ws,
+        sl = self.seq_lens[inst]
+        qsa.decode_append_select(c, self.q[il], self.kn[il], self.vn[il], sl, self.max_len, self.ws,
                                  self.sel, self.nsel)
-        if ev is not None:
-            ev[1].record()
-        qsa.sparse_decode_attn(c, self.q[il], self.seq_len, self.max_len, self.ws, self.sel, self.nsel,
-                               out=self.out[il])
-        if ev is not None:
-            ev[2].record()
+        qsa.sparse_decode_attn(c, self.q[il], sl, self.max_len, self.ws, self.sel, self.nsel, out=self.out[il])
 
-    def advance(self):
-        """Next decode position (three tiny device ops, part of the step)."""
-        torch = self.torch
-        self.ctr.add_(1)
-        torch.bitwise_and(self.ctr, 63, out=self.ph)
-        torch.add(self.base, self.ph, out=self.seq_len)
-        self.seq_len.clamp_(min=1)
+    def advance(self, inst):
+        """Next decode position of replica inst (one small device op, part of the step)."""
+        self.seq_lens[inst].add_(1)
 
     def step(self, i):
         inst = i % self.n_inst
-        self.advance()
+        self.advance(inst)
         for il in range(self.n_layer):
             self.layer(inst, il)
+
+    def check_room(self):
+        """Every replica's position is still inside its caches."""
+        for sl in self.seq_lens:
+            if int(sl.max().item()) > self.max_len:
+                raise RuntimeError("decode ran past DECODE_ROOM; raise it or take fewer steps")
 
     def capture(self):
         """One hipGraph per replica holding a whole step (2 launches per layer).
@@ -172,21 +172,21 @@ class Runner:
             for inst in range(self.n_inst):
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g, stream=s):
-                    self.advance()
+                    self.advance(inst)
                     for il in range(self.n_layer):
                         self.layer(inst, il)
                 graphs.append(g)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         for inst in range(self.n_inst):
-            c0 = int(self.ctr.item())
+            p0 = self.seq_lens[inst].clone()
             self.step(inst)
             torch.cuda.synchronize()
             ref = [o.clone() for o in self.out]
             for rep in range(3 if inst == 0 else 1):
                 for o in self.out:
                     o.fill_(float("nan"))
-                self.ctr.fill_(c0)
+                self.seq_lens[inst].copy_(p0)
                 graphs[inst].replay()
                 torch.cuda.synchronize()
                 if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
@@ -212,33 +212,60 @@ class Runner:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps            # ms per step
 
-    def time_kernels(self, steps):
-        """Average device time of the append+select and attention launches,
-        from HIP events around each launch on the launch stream."""
-        torch = self.torch
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps * self.n_layer)]
-        k = 0
-        for i in range(steps):
-            self.advance()
-            for il in range(self.n_layer):
-                self.layer(i % self.n_inst, il, evs[k])
-                k += 1
+    def time_kernels(self, steps, per_graph=16):
+        """Average device time per launch of the append+select kernel and of
+        the attention kernel: each is captured `per_graph` times back to back
+        (layer 0 of every replica in turn, after a step has set the
+        selection; both kernels are idempotent at a fixed position), and the
+        replays are timed with HIP events on the capturing stream."""
+        torch, qsa = self.torch, self.qsa
+        self.step(0)
         torch.cuda.synchronize()
-        sel_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
-        att_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
-        return sel_ms * 1e3, att_ms * 1e3
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        gs, ga = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(gs, stream=s):
+                for k in range(per_graph):
+                    c = self.stacks[k % self.n_inst][0]
+                    qsa.decode_append_select(c, self.q[0], self.kn[0], self.vn[0], self.seq_lens[k % self.n_inst],
+                                             self.max_len, self.ws, self.sel, self.nsel)
+            with torch.cuda.graph(ga, stream=s):
+                for k in range(per_graph):
+                    c = self.stacks[k % self.n_inst][0]
+                    qsa.sparse_decode_attn(c, self.q[0], self.seq_lens[k % self.n_inst], self.max_len, self.ws,
+                                           self.sel, self.nsel, out=self.out[0])
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        res = []
+        for g in (gs, ga):
+            g.replay()
+            torch.cuda.synchronize()
+            reps = max(1, steps // per_graph)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(s):
+                e0.record(s)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(s)
+            torch.cuda.synchronize()
+            res.append(e0.elapsed_time(e1) / (reps * per_graph) * 1e3)
+        return res[0], res[1]
 
     def bytes_per_layer(self):
         """Algorithmic bytes of one layer: selected KV (q8_0, K and V) read by the
         attention kernel; pooled keys scanned by the select kernel."""
         cfg = self.cfg
+        self.step(0)                        # a fresh selection at replica 0's current position
+        self.torch.cuda.synchronize()
+        lengths = [int(x) for x in self.seq_lens[0].tolist()]
         sel = self.sel.cpu().numpy()
         nsel = self.nsel.cpu().numpy()
-        cells = selected_cells(sel, nsel, self.lengths, cfg.block_tokens)
+        cells = selected_cells(sel, nsel, lengths, cfg.block_tokens)
         row = cfg.head_dim + cfg.head_dim // 32 * 2              # 136 B per (token, KV head)
         kv = cells * row * 2
         pooled = 0
-        for L in self.lengths:
+        for L in lengths:
             last = L - 1
             fw = max(0, last - cfg.local_tokens + 1) // cfg.block_tokens
             elig = max(0, min(L // cfg.block_tokens, fw) - cfg.sink_blocks)
@@ -297,9 +324,20 @@ def main():
     dev = torch.cuda.get_device_name(0)
     log(f"[bench] {dev}; {args.layers} layers, contexts {contexts}, steps {args.steps}, warmup {args.warmup}")
 
+    if args.copy_calib:
+        n = args.copy_calib // 4
+        a = torch.empty(n, dtype=torch.float32, device="cuda").fill_(1.0)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 3 x {args.copy_calib} B device-to-device")
+        del a, b
+
     per_ctx = {}
     for ctx in contexts:
-        pps = ctx // cfg.page_tokens
+        pps = (ctx + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
         r = Runner(qsa, torch, cfg, [ctx], args.layers, pps, pt, gen)
         eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
@@ -307,7 +345,8 @@ def main():
         if not args.no_graph:
             r.capture()
             graph_ms = r.time_steps(args.steps, args.warmup, graph=True)
-        sel_us, att_us = r.time_kernels(max(20, args.steps // 4))
+        sel_us, att_us = r.time_kernels(max(64, args.steps))
+        r.check_room()
         kv, pooled, cells = r.bytes_per_layer()
         ms = graph_ms if graph_ms is not None else eager_ms
         res = dict(us_per_layer=ms * 1e3 / args.layers, eager_us_per_layer=eager_ms * 1e3 / args.layers,
@@ -331,11 +370,12 @@ def main():
         import numpy as np
         rng = np.random.default_rng(args.seed)
         lens = [int(math.exp(rng.uniform(math.log(4096), math.log(262144)))) for _ in range(8)]
-        pps = max(lens) // cfg.page_tokens + 1
+        pps = (max(lens) + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         perm = torch.from_numpy(rng.permutation(8 * pps).astype(np.int32)).view(8, pps)
         r = Runner(qsa, torch, cfg, lens, 1, pps, perm, gen)
         ms = r.time_steps(args.steps, args.warmup, graph=False)
-        sel_us, att_us = r.time_kernels(max(20, args.steps // 4))
+        sel_us, att_us = r.time_kernels(max(64, args.steps))
+        r.check_room()
         kv, pooled, cells = r.bytes_per_layer()
         batched = dict(lengths=lens, us_per_launch_pair=ms * 1e3, select_kernel_us=sel_us, attn_kernel_us=att_us,
                        selected_kv_bytes=kv, pooled_scan_bytes=pooled,
@@ -358,6 +398,12 @@ def main():
         log(f"[bench] cpu baseline: {cpu_us:.1f} us/layer on {threads} threads ({n} steps)")
 
     attn_gbs = top["attn_gbs"]
+    traffic = None
+    if os.path.exists(TRAFFIC_JSON):
+        with open(TRAFFIC_JSON) as f:
+            tj = json.load(f).get("k_attn_q8", {})
+        if tj.get("context") == big:
+            traffic = tj.get("hbm_bytes_per_launch")
     line = {
         "metric": METRIC,
         "value": round(top["us_per_layer"], 3),
@@ -383,12 +429,12 @@ def main():
                         for c, v in per_ctx.items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_attn (sparse decode attention, selected q8_0 K+V)",
+            "kernel": "k_attn_q8 (sparse decode attention, selected q8_0 K+V)",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": top["selected_kv_bytes"],
             "launch_us": round(top["attn_kernel_us"], 3),
         },

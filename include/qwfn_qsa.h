@@ -29,11 +29,15 @@
  *
  * Device data layout (one K pool and one V pool per attention layer)
  *  page  = n_head_kv * page_tokens * (head_dim + head_dim/16) bytes:
- *    quants : int8  [n_head_kv][page_tokens/64][head_dim/16][64][16]
+ *    K quants : int8  [n_head_kv][page_tokens/64][head_dim/16][64][16]
  *             (64-token tiles; each 16-byte chunk of a token's head row is
  *              interleaved with the same chunk of the tile's other 63 tokens,
  *              so lane t of a wave reading chunk c of token t is one contiguous
  *              1 KiB load)
+ *    V quants : int8  [n_head_kv][page_tokens/64][head_dim][64] when
+ *             block_tokens % 64 == 0 (dim-major tiles: dim d of the tile's 64
+ *             tokens is 64 contiguous bytes, the operand of a per-dim dot
+ *             product over tokens); otherwise the K layout
  *    scales : fp16  [n_head_kv][page_tokens][head_dim/32]  (one per q8_0 block)
  *  A logical position t of sequence s lives in physical page
  *  page_table[s*pages_per_seq + t/page_tokens] at row t%page_tokens.
