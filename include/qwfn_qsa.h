@@ -231,6 +231,39 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             int32_t *sel_out, int32_t *n_sel_out,
                             void *ws, size_t ws_bytes, void *stream);
 
+/* ---- prefill ------------------------------------------------------------- */
+
+/* Workspace for qwfn_sparse_attn_prefill processing q_batch queries per
+ * launch pair, contexts up to max_seq_len.  A larger workspace lets the call
+ * take more queries per launch; any size from q_batch = 1 up works. */
+int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_seq_len,
+                                     int32_t q_batch, size_t *bytes);
+
+/* Prefill chunk of sequence `seq`: queries at positions pos0 .. pos0+n_q-1.
+ * Replaces the QSA part of graph_builder::sparse_attn / qsa_top_k
+ * (src/qwfn_graph.cpp:235-408: the chunk's block pooling :257-269, per-query
+ * scores, bias and ggml_top_k :282-305, the K/V copy into the cache :349-360,
+ * the selected-cell causal mask :367-398 and the masked flash-attention
+ * :400-403) and the host-built per-chunk tables and bias of
+ * src/qwfn_engine.cpp:884-957.
+ *  - k_new/v_new ([n_q][n_head_kv][head_dim], src_dtype), when non-NULL, are
+ *    appended at pos0.. and every whole block in [pos0/bt, (pos0+n_q)/bt) is
+ *    re-pooled.  With NULL the rows and pooled keys must already be in place.
+ *  - Query i (q [n_q][n_head][head_dim] fp32) attends causally over its own
+ *    selection, exactly as a decode step at seq_len = pos0 + i + 1: the sink
+ *    blocks, its top_k eligible blocks by pooled-key score, the blocks of its
+ *    local window, cells <= pos0 + i.  out [n_q][n_head][head_dim] fp32.
+ *  - sel_out [n_q][n_head_kv][max_sel] / n_sel_out [n_q][n_head_kv] (optional)
+ *    receive each query's selection.
+ * The queries are processed in batches sized to ws_bytes (see
+ * qwfn_qsa_prefill_workspace_bytes), each batch an indexer launch and an
+ * attention launch on `stream`. */
+int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                             const float *q, const void *k_new, const void *v_new,
+                             int32_t src_dtype, int32_t seq, int32_t pos0, int32_t n_q,
+                             float *out, int32_t *sel_out, int32_t *n_sel_out,
+                             int32_t max_sel, void *ws, size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,7 @@ def lib() -> C.CDLL:
             "qwfn_oracle_indexer_topk": (C.c_int, [S, V, P, P, I, P, P, I]),
             "qwfn_oracle_attention_f64": (C.c_int, [S, V, P, P, I, P, P, I, P]),
             "qwfn_oracle_decode_step_f32": (C.c_int, [S, V, P, P, P, P, I, P, P, P, I]),
+            "qwfn_oracle_prefill_f64": (C.c_int, [S, V, P, I, I, I, P, P, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -209,6 +210,23 @@ class HostCache:
         if rc < 0:
             raise RuntimeError(f"oracle attention -> {rc}")
         return out
+
+    def prefill_f64(self, q, seq: int, pos0: int, max_sel=None):
+        """Selections and fp64 outputs of prefill queries pos0.. of sequence seq
+        (rows and pooled keys already in place)."""
+        q = np.ascontiguousarray(np.asarray(q, dtype=np.float32))
+        n_q = q.size // (self.cfg.n_head * self.cfg.head_dim)
+        if max_sel is None:
+            max_sel = max_selected(self.cfg, pos0 + n_q)
+        sel = np.full((n_q, self.cfg.n_head_kv, max_sel), -1, dtype=np.int32)
+        nsel = np.zeros((n_q, self.cfg.n_head_kv), dtype=np.int32)
+        out = np.zeros((n_q, self.cfg.n_head, self.cfg.head_dim), dtype=np.float64)
+        view = self.view()
+        rc = lib().qwfn_oracle_prefill_f64(C.byref(self.shape), C.byref(view), _p(q), seq, pos0, n_q,
+                                           _p(sel), _p(nsel), max_sel, _p(out))
+        if rc < 0:
+            raise RuntimeError(f"oracle prefill -> {rc}")
+        return sel, nsel, out
 
     def decode_step_f32(self, q, k_new, v_new, seq_len):
         q = np.ascontiguousarray(np.asarray(q, dtype=np.float32))

@@ -461,6 +461,39 @@ int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
 
 /* ------------------------------------------------------------------------ */
 /* CPU baseline: the whole decode token in fp32                              */
+/* Prefill of queries pos0 .. pos0+n_q-1 of sequence seq over a cache whose
+ * rows and whole-block pooled keys are in place: query i is a decode step at
+ * seq_len = pos0+i+1 without the append (its selection by
+ * qwfn_oracle_indexer_topk, its attention by qwfn_oracle_attention_f64), the
+ * per-query causal rule the reference's prefill builds with the bias of
+ * src/qwfn_engine.cpp:936-950 and the mask of src/qwfn_graph.cpp:367-398.
+ * sel [n_q][n_head_kv][max_sel], n_sel [n_q][n_head_kv], out [n_q][n_head][hd]
+ * (doubles).  OpenMP over queries. */
+int qwfn_oracle_prefill_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const float *q,
+                            int32_t seq, int32_t pos0, int32_t n_q, int32_t *sel, int32_t *n_sel,
+                            int32_t max_sel, double *out) {
+    if (seq < 0 || seq >= v->n_seq || pos0 < 0 || n_q < 1) return QWFN_EINVAL;
+    if ((int64_t)pos0 + n_q > (int64_t)v->pages_per_seq * s->page_tokens) return QWFN_ERANGE;
+    qwfn_kv_view sv = *v;                          /* the one sequence as a view */
+    const int64_t bps = (int64_t)v->pages_per_seq * s->page_tokens / s->block_tokens;
+    sv.pooled = v->pooled + (int64_t)seq * s->n_head_kv * bps * s->head_dim;
+    sv.page_table = v->page_table + (int64_t)seq * v->pages_per_seq;
+    sv.n_seq = 1;
+    const int64_t qstride = (int64_t)s->n_head * s->head_dim;
+    int rc_all = 0;
+#pragma omp parallel for schedule(dynamic) reduction(min : rc_all)
+    for (int32_t i = 0; i < n_q; ++i) {
+        int32_t L = pos0 + i + 1;
+        int32_t *si = sel + (int64_t)i * s->n_head_kv * max_sel;
+        int32_t *ni = n_sel + (int64_t)i * s->n_head_kv;
+        int rc = qwfn_oracle_indexer_topk(s, &sv, q + i * qstride, &L, 1, si, ni, max_sel);
+        if (rc >= 0) rc = qwfn_oracle_attention_f64(s, &sv, q + i * qstride, &L, 1, si, ni, max_sel,
+                                                    out + i * qstride);
+        if (rc < rc_all) rc_all = rc;
+    }
+    return rc_all < 0 ? rc_all : 0;
+}
+
 /* ------------------------------------------------------------------------ */
 
 static float f16_round(float x) { return qwfn_oracle_f16_to_f32(qwfn_oracle_f32_to_f16(x)); }

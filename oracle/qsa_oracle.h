@@ -92,6 +92,13 @@ int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                               const int32_t *sel, const int32_t *n_sel,
                               int32_t max_sel, double *out);
 
+/* Prefill of queries pos0 .. pos0+n_q-1 of sequence seq (rows and pooled keys
+ * in place): query i is the decode rule at seq_len = pos0+i+1 without the
+ * append.  sel [n_q][n_head_kv][max_sel], n_sel [n_q][n_head_kv],
+ * out [n_q][n_head][hd] as doubles. */
+int qwfn_oracle_prefill_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const float *q,
+                            int32_t seq, int32_t pos0, int32_t n_q, int32_t *sel, int32_t *n_sel,
+                            int32_t max_sel, double *out);
 /* CPU baseline: one decode token of the whole path in fp32 (append at
  * seq_len-1, pool on block completion, scores, selection, attention with the
  * gathered K/V cast to fp16 as the reference's decode does, online softmax),

@@ -3,6 +3,7 @@
 // synchronisation (except qwfn_qsa_read_status), no exceptions across the ABI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -96,6 +97,7 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->inv_bt = 1.0f / (float)s->block_tokens;
     g->vdim = s->block_tokens % 64 == 0;
     g->scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)s->head_dim));
+    g->pf = 0; g->pf_seq = 0; g->pf_pos0 = 0;
     if (v) {
         g->pps = v->pages_per_seq; g->n_phys = v->n_phys_pages; g->n_seq_view = v->n_seq;
         g->bps = (int32_t)((int64_t)v->pages_per_seq * s->page_tokens / s->block_tokens);
@@ -263,7 +265,7 @@ int qwfn_kv_append_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, c
         return fail(QWFN_EINVAL, "append: source rows must be %zu-byte aligned", al);
     if (n_rows < 1) return fail(QWFN_EINVAL, "append: n_rows %d < 1", n_rows);
     const hipError_t e = launch_append(g, *view, k_src, v_src, src_dtype == QWFN_SRC_F16, seq_ids, pos,
-                                       n_rows, (hipStream_t)stream);
+                                       n_rows, 0, 0, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "append");
 }
 
@@ -275,7 +277,7 @@ int qwfn_pool_update(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, cons
     if (!block_ids) return fail(QWFN_EINVAL, "pool_update: block_ids is NULL");
     if (n_blocks < 1) return fail(QWFN_EINVAL, "pool_update: n_blocks %d < 1", n_blocks);
     if (g.hd > 256) return fail(QWFN_ENOTSUP, "pool_update: head_dim > 256");
-    const hipError_t e = launch_pool(g, *view, seq_ids, block_ids, n_blocks, 0, (hipStream_t)stream);
+    const hipError_t e = launch_pool(g, *view, seq_ids, block_ids, n_blocks, 0, 0, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "pool_update");
 }
 
@@ -288,7 +290,7 @@ int qwfn_pool_rebuild(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, int
     if (n_whole < 0) return fail(QWFN_EINVAL, "pool_rebuild: n_whole %d < 0", n_whole);
     if (n_whole > g.bps) return fail(QWFN_ERANGE, "pool_rebuild: n_whole %d > %d blocks", n_whole, g.bps);
     if (n_whole == 0) return ok();
-    const hipError_t e = launch_pool(g, *view, nullptr, nullptr, n_whole, seq, (hipStream_t)stream);
+    const hipError_t e = launch_pool(g, *view, nullptr, nullptr, n_whole, seq, 0, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "pool_rebuild");
 }
 
@@ -403,6 +405,87 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
     if (e != hipSuccess) return hip_fail(e, "decode: indexer");
     e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st);
     return e == hipSuccess ? ok() : hip_fail(e, "decode: attention");
+}
+
+int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_seq_len, int32_t q_batch,
+                                     size_t *bytes) {
+    Geo g;
+    int rc = make_geo(shape, nullptr, &g, false);
+    if (rc) return rc;
+    if (!bytes || max_seq_len < 1 || q_batch < 1)
+        return fail(QWFN_EINVAL, "prefill_workspace_bytes: bytes NULL or max_seq_len / q_batch < 1");
+    if ((int64_t)q_batch * shape->n_head_kv > kMaxCounters)
+        return fail(QWFN_ERANGE, "q_batch * n_head_kv exceeds %d", kMaxCounters);
+    *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len)).total;
+    return ok();
+}
+
+int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                             const void *k_new, const void *v_new, int32_t src_dtype, int32_t seq,
+                             int32_t pos0, int32_t n_q, float *out, int32_t *sel_out, int32_t *n_sel_out,
+                             int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (seq < 0 || seq >= view->n_seq) return fail(QWFN_EINVAL, "prefill: seq %d outside the view", seq);
+    if (pos0 < 0 || n_q < 1) return fail(QWFN_EINVAL, "prefill: pos0 %d < 0 or n_q %d < 1", pos0, n_q);
+    const int64_t end = (int64_t)pos0 + n_q;
+    if (end > (int64_t)view->pages_per_seq * shape->page_tokens)
+        return fail(QWFN_ERANGE, "prefill: context exhausted: pos0 + n_q = %lld > capacity %lld", (long long)end,
+                    (long long)view->pages_per_seq * shape->page_tokens);
+    if ((k_new == nullptr) != (v_new == nullptr))
+        return fail(QWFN_EINVAL, "prefill: pass both k_new and v_new or neither");
+    if (k_new && src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16)
+        return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
+    const size_t al = src_dtype == QWFN_SRC_F32 ? 16 : 8;
+    if (!q || !aligned(q, 16) || !out || (k_new && (!aligned(k_new, al) || !aligned(v_new, al))))
+        return fail(QWFN_EINVAL, "prefill: NULL or misaligned q / out / k_new / v_new");
+    if ((sel_out == nullptr) != (n_sel_out == nullptr))
+        return fail(QWFN_EINVAL, "prefill: pass both sel_out and n_sel_out or neither");
+    const int32_t max_len = (int32_t)end;
+    const int32_t need = max_selected(shape, max_len);
+    if (sel_out && max_sel < need) return fail(QWFN_ERANGE, "prefill: max_sel %d < %d", max_sel, need);
+    const int32_t sel_stride = sel_out ? max_sel : need;
+    // the largest query batch whose workspace fits
+    if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "prefill: workspace NULL or not 256-byte aligned");
+    int32_t batch = std::min<int64_t>(n_q, kMaxCounters / shape->n_head_kv);
+    while (batch > 1 && ws_layout(g, batch, max_len, need).total > ws_bytes) batch = (batch + 1) / 2;
+    if (ws_layout(g, batch, max_len, need).total > ws_bytes)
+        return fail(QWFN_ERANGE, "prefill: workspace of %zu bytes holds no query batch (need %zu)", ws_bytes,
+                    ws_layout(g, 1, max_len, need).total);
+    const Ws w = ws_bind(ws, ws_layout(g, batch, max_len, need));
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    // the chunk's rows, then every block they complete (and a block they finish)
+    if (k_new) {
+        e = launch_append(g, *view, k_new, v_new, src_dtype == QWFN_SRC_F16, nullptr, nullptr, n_q, seq, pos0, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill: append");
+        const int32_t b0 = pos0 / g.bt, b1 = max_len / g.bt;   // whole blocks [b0, b1)
+        if (b1 > b0) {
+            e = launch_pool(g, *view, nullptr, nullptr, b1 - b0, seq, b0, st);
+            if (e != hipSuccess) return hip_fail(e, "prefill: pool");
+        }
+    }
+    Geo gp = g;
+    gp.pf = 1;
+    gp.pf_seq = seq;
+    const FusedAppend fa{nullptr, nullptr, 0, 0};
+    for (int32_t i0 = 0; i0 < n_q; i0 += batch) {
+        const int32_t nb = std::min(batch, n_q - i0);
+        gp.pf_pos0 = pos0 + i0;
+        const float *qb = q + (int64_t)i0 * g.H * g.hd;
+        float *ob = out + (int64_t)i0 * g.H * g.hd;
+        int32_t *sb = sel_out ? sel_out + (int64_t)i0 * g.Hkv * sel_stride : w.sel;
+        int32_t *nsb = n_sel_out ? n_sel_out + (int64_t)i0 * g.Hkv : w.nsel;
+        // prefill mode ignores the seq_len value; the pointer only has to be
+        // a readable device int that aliases no output of the attention kernel
+        const int32_t *dummy_len = reinterpret_cast<const int32_t *>(w.scores);
+        e = launch_indexer(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, w, fa, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill: indexer");
+        e = launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill: attention");
+    }
+    return ok();
 }
 
 }  // extern "C"

@@ -23,6 +23,9 @@ struct Geo {
     int64_t page_bytes, qbytes;      // page size, quant bytes per page
     float inv_bt;                    // 1.0f / block_tokens (host-rounded)
     float scale_log2;                // log2(e) / sqrt(head_dim)
+    // Prefill mode (pf = 1): "sequence" s of a launch is query s of cache
+    // sequence pf_seq at position pf_pos0 + s, i.e. seq_len pf_pos0 + s + 1.
+    int32_t pf, pf_seq, pf_pos0;
 };
 
 // Device pointers into a caller workspace (see qwfn_qsa_workspace_bytes).
@@ -56,12 +59,14 @@ struct FusedAppend {
 bool kernels_for(int32_t hd, int32_t G);   // an instantiation exists
 
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
+// seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r.
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
                          int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
-                         int32_t n_rows, hipStream_t st);
+                         int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st);
+// seq_ids NULL: every block in seq_const; block_ids NULL: blocks blk0 + [0, n_blocks).
 hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
-                       hipStream_t st);
+                       int32_t blk0, hipStream_t st);
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,

@@ -39,6 +39,11 @@ __device__ __forceinline__ void set_status(int32_t *st, int32_t bits) {
     if (st) atomicOr(st, bits);
 }
 
+// Cache sequence and length of launch sequence s (prefill: query s of one
+// cache sequence, see Geo::pf).  `raw` is seq_len[s] as loaded.
+__device__ __forceinline__ int cache_seq(const Geo &g, int s) { return g.pf ? g.pf_seq : s; }
+__device__ __forceinline__ int seq_length(const Geo &g, int raw, int s) { return g.pf ? g.pf_pos0 + s + 1 : raw; }
+
 // Physical page of (seq, t) or -1.  Caller has range-checked seq and t.
 __device__ __forceinline__ int32_t phys_page(const Geo &g, const int32_t *pt, int seq, int t) {
     const int32_t p = pt[(int64_t)seq * g.pps + t / g.pt];
@@ -279,7 +284,7 @@ hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st) {
 // Lane i: 4 values of one q8_0 block; blocks enumerate (row, K|V, head, j).
 __global__ void __launch_bounds__(256)
 k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
-         const int32_t *seq_ids, const int32_t *pos, int32_t n_rows) {
+         const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, int32_t seq_const, int32_t pos0) {
     const int nj = g.hd / 32;
     const int64_t total = (int64_t)n_rows * 2 * g.Hkv * nj * 8;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -290,8 +295,8 @@ k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
     const int gh = (int)(qb % g.Hkv); qb /= g.Hkv;
     const int which = (int)(qb & 1);
     const int r = (int)(qb >> 1);
-    const int seq = seq_ids ? seq_ids[r] : 0;
-    const int t = pos[r];
+    const int seq = seq_ids ? seq_ids[r] : seq_const;
+    const int t = pos ? pos[r] : pos0 + r;
     const bool report = (e4 == 0 && j == 0 && gh == 0 && which == 0);
     if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
     if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (report) set_status(v.status, QWFN_STATUS_POS_RANGE); return; }
@@ -309,11 +314,11 @@ k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
 
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
                          int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
-                         int32_t n_rows, hipStream_t st) {
+                         int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st) {
     const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
     const int64_t blocks = (total + 255) / 256;
     hipLaunchKernelGGL(k_append, dim3((unsigned)blocks), dim3(256), 0, st, g, v, k, vv, src_f16,
-                       seq_ids, pos, n_rows);
+                       seq_ids, pos, n_rows, seq_const, pos0);
     return hipGetLastError();
 }
 
@@ -390,12 +395,13 @@ __device__ void pool_block_dev(const Geo &g, const uint8_t *page, int gh, int ro
 // grid (n_blocks, Hkv), 256 threads
 template <int HD>
 __global__ void __launch_bounds__(256)
-k_pool(Geo g, qwfn_kv_view v, const int32_t *seq_ids, const int32_t *block_ids, int32_t seq_const) {
+k_pool(Geo g, qwfn_kv_view v, const int32_t *seq_ids, const int32_t *block_ids, int32_t seq_const,
+       int32_t blk0) {
     __shared__ int8_t q8[kStageRows * HD];
     __shared__ uint16_t sc[kStageRows * (HD / 32)];
     const int bi = blockIdx.x, gh = blockIdx.y, tid = threadIdx.x;
     const int seq = seq_ids ? seq_ids[bi] : seq_const;
-    const int b = block_ids ? block_ids[bi] : bi;
+    const int b = block_ids ? block_ids[bi] : blk0 + bi;
     const bool report = (gh == 0 && tid == 0);
     if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
     if (b < 0 || b >= g.bps) { if (report) set_status(v.status, QWFN_STATUS_BLOCK_RANGE); return; }
@@ -783,7 +789,7 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     float4 qv[QV];
 #pragma unroll
     for (int i = 0; i < QV; ++i) qv[i] = qg4[min(tid + i * kIdxThreads, G * HD / 4 - 1)];
-    const int L = seq_len[s];
+    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
     const bool ok = L >= 1 && L <= max_seq_len;
     const int pair = s * g.Hkv + gh;
     float *sc = ws.scores + (int64_t)pair * ws.nb_cap;
@@ -793,7 +799,7 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     const int bl = tid >> 2, j = tid & 3;
     const int bi = c * kBlocksPerChunk + bl;
     const int bp = min(g.sink + bi, g.bps - 1);
-    const float *P = v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + bp) * HD;
+    const float *P = v.pooled + (((int64_t)cache_seq(g, s) * g.Hkv + gh) * g.bps + bp) * HD;
     float4 p4[HD / 16];
 #pragma unroll
     for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
@@ -1023,7 +1029,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     const int lt = tid % C::NTG;
     AttnGroup<HD, G> &gr = sh.grp[gi];
     const int pair = s * g.Hkv + gh;
-    const int L = seq_len[s];
+    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
@@ -1049,7 +1055,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
                 const int blk = sel ? sel[(int64_t)pair * max_sel + slot] : slot;
                 const int t = blk * g.bt + cidx % g.bt;
                 if (blk >= 0 && t < L) {
-                    pg = phys_page(g, v.page_table, s, t);
+                    pg = phys_page(g, v.page_table, cache_seq(g, s), t);
                     rw = t % g.pt;
                     if (pg < 0) { set_status(v.status, QWFN_STATUS_PAGE_RANGE); rw = -1; }
                 }
@@ -1304,7 +1310,7 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
     // Unconditional loads from selected pointers, all issued before any is
     // used: no branch may sit between them (a branch makes the compiler wait
     // for every load in flight).
-    const int L = seq_len[s];
+    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
     const int n_raw = DENSE ? 0 : nsel[pair];
     const int blk_raw = DENSE ? 0 : sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
     constexpr int DPL = HD / 64, NWV = C::NT / 64, QPW = (G + NWV - 1) / NWV;
@@ -1326,7 +1332,7 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
     const int64_t t0 = (int64_t)blk * g.bt + off;
     const int t0c = (int)min(max(t0, (int64_t)0), (int64_t)g.pps * g.pt - 1);
     const int32_t *__restrict__ ptab = v.page_table;
-    const int32_t praw = ptab[(int64_t)s * g.pps + t0c / g.pt];
+    const int32_t praw = ptab[(int64_t)cache_seq(g, s) * g.pps + t0c / g.pt];
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
@@ -1613,12 +1619,12 @@ bool kernels_for(int32_t hd, int32_t G) {
 
 hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
-                       hipStream_t st) {
+                       int32_t blk0, hipStream_t st) {
     const dim3 grid((unsigned)n_blocks, (unsigned)g.Hkv);
     switch (g.hd) {
-    case 64:  hipLaunchKernelGGL(k_pool<64>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const); break;
-    case 128: hipLaunchKernelGGL(k_pool<128>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const); break;
-    case 256: hipLaunchKernelGGL(k_pool<256>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const); break;
+    case 64:  hipLaunchKernelGGL(k_pool<64>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0); break;
+    case 128: hipLaunchKernelGGL(k_pool<128>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0); break;
+    case 256: hipLaunchKernelGGL(k_pool<256>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

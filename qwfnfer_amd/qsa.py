@@ -83,6 +83,12 @@ class QsaConfig:
         call("qwfn_qsa_workspace_bytes", C.byref(s), n_seq, max_seq_len, C.byref(out))
         return out.value
 
+    def prefill_workspace_bytes(self, max_seq_len: int, q_batch: int) -> int:
+        out = C.c_size_t()
+        s = self.shape()
+        call("qwfn_qsa_prefill_workspace_bytes", C.byref(s), max_seq_len, q_batch, C.byref(out))
+        return out.value
+
     def dense(self) -> "QsaConfig":
         """The same layer with the selection switched off (the reference's
         ``qsa == nullptr`` dense path, src/qwfn_graph.cpp:85-89)."""
@@ -216,10 +222,17 @@ class Workspace:
     """Caller-owned scratch of the indexer and the attention merge, sized for
     (n_seq, max_seq_len) and zero-initialised once (a fill kernel)."""
 
-    def __init__(self, cfg: QsaConfig, n_seq: int, max_seq_len: int, device="cuda", stream=None):
-        self.nbytes = cfg.workspace_bytes(n_seq, max_seq_len)
+    def __init__(self, cfg: QsaConfig, n_seq: int, max_seq_len: int, device="cuda", stream=None,
+                 nbytes: Optional[int] = None):
+        self.nbytes = cfg.workspace_bytes(n_seq, max_seq_len) if nbytes is None else nbytes
         self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
         call("qwfn_qsa_workspace_init", self.buf.data_ptr(), self.nbytes, _stream(stream))
+
+    @classmethod
+    def for_prefill(cls, cfg: QsaConfig, max_seq_len: int, q_batch: int, device="cuda",
+                    stream=None) -> "Workspace":
+        """Workspace for :func:`sparse_attn_prefill` taking q_batch queries per launch pair."""
+        return cls(cfg, 1, max_seq_len, device, stream, nbytes=cfg.prefill_workspace_bytes(max_seq_len, q_batch))
 
     def ptr(self) -> int:
         return self.buf.data_ptr()
@@ -347,6 +360,44 @@ def sparse_attn_decode(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_n
          v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,
          seq_len.data_ptr(), n_seq, max_seq_len, out.data_ptr(), _ptr(sel), _ptr(n_sel), ws.ptr(),
          ws.nbytes, _stream(stream))
+    return out
+
+
+def sparse_attn_prefill(cache: KvCache, q: torch.Tensor, seq: int, pos0: int, ws: Workspace,
+                        k_new: Optional[torch.Tensor] = None, v_new: Optional[torch.Tensor] = None,
+                        out: Optional[torch.Tensor] = None, sel: Optional[torch.Tensor] = None,
+                        n_sel: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Prefill chunk of sequence ``seq`` at positions pos0 .. pos0+n_q-1, the QSA
+    part of graph_builder::sparse_attn / qsa_top_k (src/qwfn_graph.cpp:235-408).
+    ``k_new``/``v_new`` ([n_q][n_head_kv][head_dim]), when given, are appended
+    and the blocks they complete re-pooled first.  Query i attends as a decode
+    step at seq_len = pos0 + i + 1.  ``sel``/``n_sel`` (optional, both or
+    neither; sel [n_q][n_head_kv][max_sel]) receive every query's selection."""
+    cfg = cache.cfg
+    n_q = q.numel() // (cfg.n_head * cfg.head_dim)
+    _need(q, "q", torch.float32, n_q * cfg.n_head * cfg.head_dim)
+    src = _lib.SRC_F32
+    if (k_new is None) != (v_new is None):
+        raise ValueError("pass both k_new and v_new or neither")
+    if k_new is not None:
+        if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype:
+            raise TypeError("k_new and v_new must both be float32 or both float16")
+        _need(k_new, "k_new", k_new.dtype, n_q * cfg.kv_dim)
+        _need(v_new, "v_new", k_new.dtype, n_q * cfg.kv_dim)
+        src = _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32
+    if out is None:
+        out = torch.empty((n_q, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
+    if (sel is None) != (n_sel is None):
+        raise ValueError("pass both sel and n_sel or neither")
+    max_sel = 0
+    if sel is not None:
+        _need(sel, "sel", torch.int32)
+        _need(n_sel, "n_sel", torch.int32, n_q * cfg.n_head_kv)
+        max_sel = sel.shape[-1]
+    s = cfg.shape()
+    call("qwfn_sparse_attn_prefill", C.byref(s), C.byref(cache.view()), q.data_ptr(), _ptr(k_new), _ptr(v_new),
+         src, seq, pos0, n_q, out.data_ptr(), _ptr(sel), _ptr(n_sel), max_sel, ws.ptr(), ws.nbytes,
+         _stream(stream))
     return out
 
 

@@ -111,3 +111,29 @@ def test_python_errors_carry_the_message():
     with pytest.raises(_lib.QsaError) as ei:
         cfg.check()
     assert ei.value.code == _lib.QWFN_EINVAL and "n_head" in str(ei.value)
+
+
+def test_prefill_rejects_bad_arguments_before_launch():
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view(pps=8, nphys=8)              # capacity 2048 tokens
+    f = "qwfn_sparse_attn_prefill"
+
+    def call(seq=0, pos0=0, n_q=16, k=4096, vv=4096, ws_bytes=1 << 30, sel=None, nsel=None, max_sel=0):
+        return _code(f, C.byref(s), C.byref(v), 4096, k, vv, 0, seq, pos0, n_q, 4096, sel, nsel, max_sel,
+                     256 * 64, ws_bytes, None)
+
+    assert call(n_q=0) == _lib.QWFN_EINVAL
+    assert call(pos0=-1) == _lib.QWFN_EINVAL
+    assert call(seq=1) == _lib.QWFN_EINVAL
+    assert call(pos0=2040, n_q=9) == _lib.QWFN_ERANGE          # past the view's capacity
+    assert call(k=None) == _lib.QWFN_EINVAL                    # K without V
+    assert call(ws_bytes=1000) == _lib.QWFN_ERANGE             # holds no query batch
+    assert call(sel=4096, nsel=None) == _lib.QWFN_EINVAL
+    assert call(pos0=1000, sel=4096, nsel=4096, max_sel=10) == _lib.QWFN_ERANGE
+    out = C.c_size_t()
+    assert _code("qwfn_qsa_prefill_workspace_bytes", C.byref(s), 163840, 256, C.byref(out)) == 0
+    one = C.c_size_t()
+    assert _code("qwfn_qsa_prefill_workspace_bytes", C.byref(s), 163840, 1, C.byref(one)) == 0
+    assert out.value > one.value > 0
+    assert _code("qwfn_qsa_prefill_workspace_bytes", C.byref(s), 163840, 1 << 20, C.byref(out)) == _lib.QWFN_ERANGE

@@ -289,3 +289,79 @@ def test_decode_is_deterministic():
         torch.cuda.synchronize()
         res.append((np_of(out).tobytes(), np_of(dev.k_pages).tobytes(), np_of(dev.pooled).tobytes()))
     assert res[0] == res[1]
+
+
+# ---- prefill ------------------------------------------------------------------------
+
+def _prefill_case(cfg, pre, n_q, seed, q_batch=None, rows=True, dtype=np.float32, seq=1):
+    """A prefill chunk of sequence `seq` at positions pre .. pre+n_q-1 (the rows
+    appended and the completed blocks pooled by the call when `rows`) against
+    the oracle: cache bytes and pooled keys bit-exact, every query's selection
+    bit-exact, outputs within the attention tolerance."""
+    rng = np.random.default_rng(seed)
+    max_len = pre + n_q
+    pps = max_len // cfg.page_tokens + 1
+    dev, host = make_pair(cfg, 2, pps, seed=seed)
+    fill(dev, host, rng, [pre // 2, pre] if seq == 1 else [pre, pre // 2])
+    kn, vn = kv_rows(rng, n_q, cfg)
+    kn, vn = kn.astype(dtype), vn.astype(dtype)
+    q = rng.standard_normal((n_q, cfg.n_head, cfg.head_dim), dtype=np.float32)
+    bt = cfg.block_tokens
+    assert host.append(kn, vn, np.arange(pre, max_len, dtype=np.int32), np.full(n_q, seq, np.int32)) == 0
+    for b in range(pre // bt, max_len // bt):
+        assert host.pool_block(seq, b) == 0
+    c = cfg_of(cfg)
+    msel = c.max_selected(max_len)
+    sel = torch.empty((n_q, cfg.n_head_kv, msel), dtype=torch.int32, device="cuda")
+    nsel = torch.empty((n_q, cfg.n_head_kv), dtype=torch.int32, device="cuda")
+    ws = qsa.Workspace.for_prefill(c, max_len, q_batch or n_q)
+    qd = torch.from_numpy(q).cuda()
+    if rows:
+        out = qsa.sparse_attn_prefill(dev, qd, seq, pre, ws, torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda(),
+                                      sel=sel, n_sel=nsel)
+    else:
+        qsa.append_q8_0(dev, torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda(),
+                        torch.arange(pre, max_len, dtype=torch.int32, device="cuda"),
+                        torch.full((n_q,), seq, dtype=torch.int32, device="cuda"))
+        qsa.pool_rebuild(dev, seq, max_len // bt)
+        out = qsa.sparse_attn_prefill(dev, qd, seq, pre, ws, sel=sel, n_sel=nsel)
+    torch.cuda.synchronize()
+    assert qsa.read_status(dev) == 0
+    np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+    np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
+    np.testing.assert_array_equal(np_of(dev.pooled)[:, :, :max_len // bt], host.pooled[:, :, :max_len // bt])
+    hs, hn, ref = host.prefill_f64(q, seq, pre, max_sel=msel)
+    gs, gn = np_of(sel), np_of(nsel)
+    np.testing.assert_array_equal(gn, hn)
+    for i in range(n_q):
+        for g in range(cfg.n_head_kv):
+            np.testing.assert_array_equal(gs[i, g, :gn[i, g]], hs[i, g, :hn[i, g]],
+                                          err_msg=f"query {i} (pos {pre + i}) head {g}")
+    assert_close_attn(np_of(out), ref, f"prefill pre={pre} n_q={n_q}")
+    return np_of(out), gs, gn
+
+
+def test_prefill_matches_oracle():
+    # 6000..6159: eligible sets beyond top-64, chunk crosses blocks; config 4 in miniature
+    _prefill_case(BASELINE, 6000, 160, seed=600)
+
+
+def test_prefill_batches_are_invisible():
+    # a workspace of 24 queries per launch pair gives the same bytes as one batch
+    a = _prefill_case(BASELINE, 5000, 100, seed=610)
+    b = _prefill_case(BASELINE, 5000, 100, seed=610, q_batch=24)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+
+
+def test_prefill_from_the_first_token_and_f16_rows():
+    _prefill_case(BASELINE, 0, 700, seed=620, dtype=np.float16, seq=0)
+
+
+def test_prefill_rows_already_in_place():
+    _prefill_case(BASELINE, 4200, 64, seed=630, rows=False)
+
+
+def test_prefill_other_shapes():
+    _prefill_case(TINY, 90, 70, seed=640)            # 4-token blocks: the general attention kernel
+    _prefill_case(G12, 200, 40, seed=641)
