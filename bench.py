@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
+    ap.add_argument("--prefill-batch", type=int, default=1024,
+                    help="queries per launch pair of the prefill chunk (sizes its workspace)")
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="first copy BYTES device-to-device 3 times (a plain copy kernel of known size, "
@@ -274,6 +277,63 @@ class Runner:
         return kv, pooled, cells
 
 
+PREFILL_POS0, PREFILL_N = 155648, 8192      # config 4: a chunk ending at 163840
+
+
+def bench_prefill(qsa, torch, cfg, gen, q_batch, reps=3):
+    """Config 4: fp16 K/V rows of 8192 tokens appended at 155648 into a cache
+    holding [0, 155648), the 128 blocks they complete pooled, and 8192 queries
+    attending causally over their own selections -- one qwfn_sparse_attn_prefill
+    call, timed with HIP events (one untimed call first; every call rewrites the
+    same rows, an idempotent overwrite)."""
+    import numpy as np
+    end = PREFILL_POS0 + PREFILL_N
+    pps = end // cfg.page_tokens
+    pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+    cache = qsa.KvCache.allocate(cfg, 1, pps, page_table=pt, n_phys_pages=pps)
+    fill_layer(qsa, torch, cache, [PREFILL_POS0], gen)
+    kn = torch.randn((PREFILL_N, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen).half()
+    vn = torch.randn((PREFILL_N, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen).half()
+    q = torch.randn((PREFILL_N, cfg.n_head, cfg.head_dim), device="cuda", generator=gen)
+    ws = qsa.Workspace.for_prefill(cfg, end, q_batch)
+    msel = cfg.max_selected(end)
+    sel = torch.empty((PREFILL_N, cfg.n_head_kv, msel), dtype=torch.int32, device="cuda")
+    nsel = torch.empty((PREFILL_N, cfg.n_head_kv), dtype=torch.int32, device="cuda")
+    out = torch.empty((PREFILL_N, cfg.n_head, cfg.head_dim), device="cuda")
+    run = lambda: qsa.sparse_attn_prefill(cache, q, 0, PREFILL_POS0, ws, kn, vn, out=out, sel=sel, n_sel=nsel)
+    run()
+    torch.cuda.synchronize()
+    if qsa.read_status(cache):
+        raise RuntimeError("prefill reported out-of-range rows")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    # algorithmic work: every query's selected cells (<= its position), QK and PV
+    s_np, n_np = sel.cpu().numpy(), nsel.cpu().numpy()
+    bt = cfg.block_tokens
+    cells = 0
+    for i in range(PREFILL_N):
+        L = PREFILL_POS0 + i + 1
+        for g in range(cfg.n_head_kv):
+            b = s_np[i, g, :n_np[i, g]].astype(np.int64)
+            cells += int(np.minimum(bt, L - b * bt).clip(min=0).sum())
+    group = cfg.n_head // cfg.n_head_kv
+    flops = cells * group * cfg.head_dim * 2 * 2
+    del cache, ws, sel, nsel, out
+    torch.cuda.empty_cache()
+    return dict(queries=PREFILL_N, pos0=PREFILL_POS0, ms_per_chunk=ms, selected_cells=cells,
+                attn_gflop=flops / 1e9, attn_tflops=flops / (ms * 1e-3) / 1e12,
+                mfma_bf16_peak_tflops=2500.0, frac=flops / (ms * 1e-3) / 2.5e15,
+                append_bytes=PREFILL_N * cfg.n_head_kv * cfg.head_dim * 2 * 2 +
+                PREFILL_N * cfg.n_head_kv * (cfg.head_dim + cfg.head_dim // 32 * 2) * 2,
+                q_batch=q_batch, note="QK on int8 dot products and PV on fp16 dot products (VALU); "
+                "the bf16 MFMA peak is the config's stated roofline")
+
+
 def cpu_baseline(cfg, ctx, seconds, seed):
     """The oracle's fp32 decode step (the ggml CPU path restated: append,
     pool, scores, selection, attention over fp16-cast K/V) on one layer at
@@ -386,6 +446,12 @@ def main():
         del r
         torch.cuda.empty_cache()
 
+    prefill = None
+    if not args.no_prefill:
+        prefill = bench_prefill(qsa, torch, cfg, gen, args.prefill_batch)
+        log(f"[bench] config 4 prefill chunk (8192 queries at 155648): {prefill['ms_per_chunk']:.3f} ms, "
+            f"{prefill['attn_tflops']:.1f} TFLOP/s on the selected-cell FLOPs")
+
     big = max(contexts)
     small = min(contexts)
     top = per_ctx[big]
@@ -440,6 +506,7 @@ def main():
         },
         "layer_roofline_frac": round(top["layer_gbs_selected"] / HBM_PEAK_GBS, 4),
         "batched_config5": batched,
+        "prefill_config4": prefill,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }

@@ -469,7 +469,6 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
     Geo gp = g;
     gp.pf = 1;
     gp.pf_seq = seq;
-    const FusedAppend fa{nullptr, nullptr, 0, 0};
     for (int32_t i0 = 0; i0 < n_q; i0 += batch) {
         const int32_t nb = std::min(batch, n_q - i0);
         gp.pf_pos0 = pos0 + i0;
@@ -480,7 +479,7 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
         // prefill mode ignores the seq_len value; the pointer only has to be
         // a readable device int that aliases no output of the attention kernel
         const int32_t *dummy_len = reinterpret_cast<const int32_t *>(w.scores);
-        e = launch_indexer(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, w, fa, st);
+        e = launch_prefill_index(gp, *view, qb, nb, max_len, sb, nsb, sel_stride, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer");
         e = launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: attention");

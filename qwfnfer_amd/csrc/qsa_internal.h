@@ -71,6 +71,11 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                           const FusedAppend &fa, hipStream_t st);
+// Prefill: scores of n_q queries (Geo::pf) into ws.scores, then each query's
+// selection into sel / nsel.
+hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                                int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                                const Ws &ws, hipStream_t st);
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,

@@ -1604,6 +1604,134 @@ hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq
 }
 
 // ---------------------------------------------------------------------------
+// prefill: scores of a chunk's queries, then one selection per (query, KV head)
+// ---------------------------------------------------------------------------
+
+constexpr int kPfQ = 64, kPfB = 64;      // queries x blocks per scoring workgroup
+
+template <int HD>
+struct PfScoreShared {
+    float4 p[HD / 4][kPfB];              // the tile's pooled keys, dim-chunk major
+    float4 q[HD / 4][kPfQ];              // the current head's query rows, dim-chunk major
+};
+
+// grid (ceil((n_blk - sink) / 64), ceil(n_q / 64), Hkv), 256 threads.  The
+// workgroup scores 64 queries against 64 pooled blocks of one KV head, every
+// pooled key and query row loaded once into LDS and reused 64 times; thread t
+// owns queries 4*(t/16) .. +4 x blocks 4*(t%16) .. +4.  Each dot is formed in
+// the decode indexer's order (chain j over the dims d with (d/4)%4 == j in
+// increasing order, then (c0+c1)+(c2+c3), relu when set, heads summed in
+// order), so a query's scores are bit-identical to a decode step's at its
+// length.  Scores go to scores[(query * Hkv + gh) * nb_cap + block] for
+// blocks sink .. n_blk-1.
+template <int HD, int G>
+__global__ void __launch_bounds__(256)
+k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int32_t n_blk,
+            float *__restrict__ scores, int32_t nb_cap) {
+#pragma clang fp contract(off)
+    __shared__ PfScoreShared<HD> sh;
+    constexpr int NDC = HD / 4;
+    const int tid = threadIdx.x, gh = blockIdx.z;
+    const int b_base = g.sink + (int)blockIdx.x * kPfB;
+    const int q_base = (int)blockIdx.y * kPfQ;
+    const float *P = v.pooled + ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps * HD;
+    for (int i = tid; i < kPfB * NDC; i += 256) {
+        const int b = i / NDC, dc = i % NDC;
+        const int bb = min(b_base + b, g.bps - 1);
+        sh.p[dc][b] = *reinterpret_cast<const float4 *>(P + (int64_t)bb * HD + 4 * dc);
+    }
+    const int qi0 = 4 * (tid / 16), bi0 = 4 * (tid % 16);
+    float score[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) score[a][b] = 0.0f;
+    for (int h = 0; h < G; ++h) {
+        __syncthreads();                             // the previous head's rows are consumed
+        for (int i = tid; i < kPfQ * NDC; i += 256) {
+            const int qq = i / NDC, dc = i % NDC;
+            const int qn = min(q_base + qq, n_q - 1);
+            sh.q[dc][qq] = *reinterpret_cast<const float4 *>(q + ((int64_t)qn * g.H + gh * G + h) * HD + 4 * dc);
+        }
+        __syncthreads();
+        float c[4][4][4];                            // [query][block][chain]
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[a][b][j] = 0.0f;
+        for (int d16 = 0; d16 < HD / 16; ++d16) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {            // dims 16*d16 + 4j .. +3 belong to chain j
+                const int dc = 4 * d16 + j;
+                float4 qv[4], pv[4];
+#pragma unroll
+                for (int a = 0; a < 4; ++a) qv[a] = sh.q[dc][qi0 + a];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) pv[b] = sh.p[dc][bi0 + b];
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        float x = c[a][b][j];
+                        x = fmaf(qv[a].x, pv[b].x, x);
+                        x = fmaf(qv[a].y, pv[b].y, x);
+                        x = fmaf(qv[a].z, pv[b].z, x);
+                        x = fmaf(qv[a].w, pv[b].w, x);
+                        c[a][b][j] = x;
+                    }
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                float dot = (c[a][b][0] + c[a][b][1]) + (c[a][b][2] + c[a][b][3]);
+                if (g.relu) dot = dot > 0.0f ? dot : 0.0f;
+                score[a][b] = h == 0 ? dot : score[a][b] + dot;
+            }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        const int qn = q_base + qi0 + a;
+        if (qn >= n_q) continue;
+        float *row = scores + ((int64_t)qn * g.Hkv + gh) * nb_cap;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int blk = b_base + bi0 + b;
+            if (blk < n_blk) row[blk] = score[a][b];
+        }
+    }
+}
+
+// grid (Hkv, n_q), kIdxThreads: query s's selection at its length pf_pos0+s+1
+// from the scores k_pf_scores wrote (the decode selection, same rule).
+__global__ void __launch_bounds__(kIdxThreads)
+k_pf_select(Geo g, const float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, int32_t max_sel) {
+    __shared__ IdxShared sh;
+    const int gh = blockIdx.x, s = blockIdx.y;
+    const int pair = s * g.Hkv + gh;
+    select_blocks(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
+                  nsel + pair, sh);
+}
+
+template <int HD, int G>
+static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                              int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                              const Ws &ws, hipStream_t st) {
+    const int32_t n_blk = max_seq_len / g.bt;                   // whole blocks of the longest query
+    if (g.topk > 0 && n_blk > g.sink) {
+        const dim3 grid((unsigned)((n_blk - g.sink + kPfB - 1) / kPfB), (unsigned)((n_q + kPfQ - 1) / kPfQ),
+                        (unsigned)g.Hkv);
+        hipLaunchKernelGGL((k_pf_scores<HD, G>), grid, dim3(256), 0, st, g, v, q, n_q, n_blk, ws.scores,
+                           ws.nb_cap);
+    }
+    hipLaunchKernelGGL(k_pf_select, dim3((unsigned)g.Hkv, (unsigned)n_q), dim3(kIdxThreads), 0, st, g,
+                       ws.scores, ws.nb_cap, sel, nsel, max_sel);
+}
+
+// ---------------------------------------------------------------------------
 // dispatch over the instantiated (head_dim, group) pairs
 // ---------------------------------------------------------------------------
 
@@ -1639,6 +1767,15 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
         launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); \
         return hipGetLastError();                                                                \
     }
+    QWFN_FOR_EACH_SHAPE(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                                int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                                const Ws &ws, hipStream_t st) {
+#define X(HD_, G_, TG_)                                                                              if (g.hd == HD_ && g.G == G_) {                                                                      launch_pf_index_t<HD_, G_>(g, v, q, n_q, max_seq_len, sel, nsel, max_sel, ws, st);              return hipGetLastError();                                                                    }
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
     return hipErrorInvalidValue;
