@@ -145,7 +145,7 @@ int bind_ws(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, v
 
 namespace qwfn_qsa {
 
-WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
+WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, bool partials) {
     WsLayout l;
     // per-pair score rows padded to 64 floats: 16-byte vector loads of a row
     // stay aligned and inside it
@@ -158,8 +158,8 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.sel = take(pairs * max_sel * sizeof(int32_t));
     l.nsel = take(pairs * sizeof(int32_t));
     l.scores = take(pairs * l.nb_cap * sizeof(float));
-    l.part_o = take(pairs * l.n_tiles * g.G * g.hd * sizeof(float));
-    l.part_ml = take(pairs * l.n_tiles * g.G * 2 * sizeof(float));
+    l.part_o = take(partials ? pairs * l.n_tiles * g.G * g.hd * sizeof(float) : 0);
+    l.part_ml = take(partials ? pairs * l.n_tiles * g.G * 2 * sizeof(float) : 0);
     l.total = off;
     return l;
 }
@@ -416,7 +416,7 @@ int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_se
         return fail(QWFN_EINVAL, "prefill_workspace_bytes: bytes NULL or max_seq_len / q_batch < 1");
     if ((int64_t)q_batch * shape->n_head_kv > kMaxCounters)
         return fail(QWFN_ERANGE, "q_batch * n_head_kv exceeds %d", kMaxCounters);
-    *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len)).total;
+    *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len), !g.vdim).total;
     return ok();
 }
 
@@ -448,12 +448,13 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
     const int32_t sel_stride = sel_out ? max_sel : need;
     // the largest query batch whose workspace fits
     if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "prefill: workspace NULL or not 256-byte aligned");
+    const bool parts = !g.vdim;                    // the general kernel merges partials in memory
     int32_t batch = std::min<int64_t>(n_q, kMaxCounters / shape->n_head_kv);
-    while (batch > 1 && ws_layout(g, batch, max_len, need).total > ws_bytes) batch = (batch + 1) / 2;
-    if (ws_layout(g, batch, max_len, need).total > ws_bytes)
+    while (batch > 1 && ws_layout(g, batch, max_len, need, parts).total > ws_bytes) batch = (batch + 1) / 2;
+    if (ws_layout(g, batch, max_len, need, parts).total > ws_bytes)
         return fail(QWFN_ERANGE, "prefill: workspace of %zu bytes holds no query batch (need %zu)", ws_bytes,
-                    ws_layout(g, 1, max_len, need).total);
-    const Ws w = ws_bind(ws, ws_layout(g, batch, max_len, need));
+                    ws_layout(g, 1, max_len, need, parts).total);
+    const Ws w = ws_bind(ws, ws_layout(g, batch, max_len, need, parts));
     hipStream_t st = (hipStream_t)stream;
     hipError_t e = hipSuccess;
     // the chunk's rows, then every block they complete (and a block they finish)
@@ -481,7 +482,8 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
         const int32_t *dummy_len = reinterpret_cast<const int32_t *>(w.scores);
         e = launch_prefill_index(gp, *view, qb, nb, max_len, sb, nsb, sel_stride, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer");
-        e = launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
+        e = g.vdim ? launch_prefill_attention(gp, *view, qb, nb, sb, nsb, sel_stride, ob, st)
+                   : launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: attention");
     }
     return ok();

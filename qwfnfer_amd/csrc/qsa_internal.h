@@ -47,7 +47,8 @@ struct WsLayout {
     size_t sel, nsel, scores, part_o, part_ml, total;
     int32_t nb_cap, max_sel, n_tiles;
 };
-WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel);
+// partials = false: no attention partials (the prefill kernel keeps its state on chip)
+WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, bool partials = true);
 Ws ws_bind(void *base, const WsLayout &l);
 
 // Fused-append arguments of the decode step (enabled == 0: plain indexer).
@@ -76,6 +77,11 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                                 int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                                 const Ws &ws, hipStream_t st);
+// Prefill attention on the matrix cores (block_tokens % 64 == 0): one wave
+// per (query, KV head) over its selection, no partials.
+hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                                    const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
+                                    hipStream_t st);
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,

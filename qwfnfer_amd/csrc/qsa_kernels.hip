@@ -1444,7 +1444,7 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
             const bool valid = lane < nv;
             float dvf[NB], dvm = 0.0f;
 #pragma unroll
-            for (int j = 0; j < NB; ++j) { dvf[j] = h2f(dvh[j]); dvm = fmaxf(dvm, dvf[j]); }
+            for (int j = 0; j < NB; ++j) { dvf[j] = valid ? h2f(dvh[j]) : 0.0f; dvm = fmaxf(dvm, dvf[j]); }
             dvm = wave_max(valid ? dvm : 0.0f);
             int e = 0;
             frexpf(dvm, &e);
@@ -1765,6 +1765,246 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
 #define X(HD_, G_, TG_)                                                                          \
     if (g.hd == HD_ && g.G == G_) {                                                              \
         launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); \
+        return hipGetLastError();                                                                \
+    }
+    QWFN_FOR_EACH_SHAPE(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// prefill attention on the matrix cores: one wave per (query, KV head)
+// ---------------------------------------------------------------------------
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kPfAttnWaves = 4;
+
+// Eight int8 quants -> eight exact fp16 values, in order.
+__device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
+    half2v a, b, c, d;
+    q8x4_to_h2(w.x, a, b);
+    q8x4_to_h2(w.y, c, d);
+    h8v r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+    return r;
+}
+
+// LDS exchange between the lanes of one wave (no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// grid ceil(n_q * Hkv / 4), 4 waves; wave w owns (query s, KV head gh) =
+// pair blockIdx.x*4 + w and walks its selected 64-cell tiles with an online
+// softmax, every contraction on v_mfma_f32_16x16x32_f16 (one output column per
+// query head of the group, up to 16):
+//  - QK: S[cell][head] = sum_j dk(cell, j) * (K_j[cell][:] . q_j[:, head]) per
+//    32-dim q8_0 block j, the int8 keys exact in fp16 and the query row (scaled
+//    by a power of two qs) as fp16 hi + lo, so the products are exact and
+//    only the fp32 accumulation rounds;
+//  - PV: O[dim][head] += V[dim][cell] * P'_j[cell][head] with the V quants
+//    exact in fp16 and P'_j = p * dv(cell, j) * 2^k split into fp16 hi + lo
+//    (2^k keeps the tile's largest V scale near 2^15; O is carried in the
+//    current tile's units and rescaled with the softmax).
+// The tile's softmax weights cross lanes through the wave's own LDS strip.
+// Cells past the query's position have weight 0 and their V scale masked.
+template <int HD, int G>
+__global__ void __launch_bounds__(kPfAttnWaves * 64)
+k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const int32_t *__restrict__ sel,
+          const int32_t *__restrict__ nsel, int32_t max_sel, float *__restrict__ out) {
+    constexpr int NJ = HD / 32, ND = HD / 16;
+    static_assert(G <= 16, "one MFMA output column per query head");
+    __shared__ float shp[kPfAttnWaves][16][64 + 4];
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int pair = (int)blockIdx.x * kPfAttnWaves + wv;
+    if (pair >= n_q * g.Hkv) return;                 // a whole wave; no workgroup barrier follows
+    const int s = pair / g.Hkv, gh = pair - s * g.Hkv;
+    const int L = g.pf_pos0 + s + 1;
+    const int hn = l & 15, lg = l >> 4;              // MFMA column (head) and k-group of this lane
+    const bool hv = hn < G;
+    const int n = min(nsel[pair], max_sel);
+    const int tpb = g.bt / 64;
+    const int32_t *selp = sel + (int64_t)pair * max_sel;
+    // query head hn, dims 32j + 8lg .. +8, as fp16 hi + lo of q / qs
+    const float *qrow = q + ((int64_t)s * g.H + gh * G + (hv ? hn : 0)) * HD;
+    float x[NJ][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg);
+        const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg + 4);
+        x[j][0] = x0.x; x[j][1] = x0.y; x[j][2] = x0.z; x[j][3] = x0.w;
+        x[j][4] = x1.x; x[j][5] = x1.y; x[j][6] = x1.z; x[j][7] = x1.w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[j][i]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    int ex = 0;
+    frexpf(amax, &ex);
+    const float qs = amax > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f;   // |q / qs| < 2^14
+    const float qinv = 1.0f / qs;                                   // a power of two: exact
+    h8v qh[NJ], ql[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float y = hv ? x[j][i] * qinv : 0.0f;
+            const _Float16 hi = (_Float16)y;
+            qh[j][i] = hi;
+            ql[j][i] = (_Float16)(y - (float)hi);
+        }
+    const float lscale = qs * g.scale_log2;
+    f4v o[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o[d] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, lsum = 0.0f, up_cur = 1.0f;
+    float (*pw)[64 + 4] = shp[wv];
+    const int n_tiles = n * tpb;
+    for (int t = 0; t < n_tiles; ++t) {
+        const int blk = selp[t / tpb];
+        const int64_t t0 = (int64_t)blk * g.bt + (t % tpb) * 64;
+        const int nv = (blk < 0 || t0 >= L) ? 0 : (int)min((int64_t)64, (int64_t)L - t0);
+        if (nv == 0) continue;                       // uniform over the wave
+        const int tt = (int)t0;
+        const int32_t pg = phys_page(g, v.page_table, g.pf_seq, tt);
+        if (pg < 0) {
+            if (l == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+            continue;
+        }
+        const int row0 = tt % g.pt;
+        const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
+        const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
+        const int tl = gh * (g.pt / 64) + row0 / 64;
+        // ---- QK
+        float sv[4][4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const uint16_t *dks = reinterpret_cast<const uint16_t *>(kp + scale_off(g, gh, row0 + 16 * mb + 4 * lg, 0));
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const uint2 kw = *reinterpret_cast<const uint2 *>(
+                    kp + ((int64_t)(tl * (HD / 16) + 2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
+                const h8v kh = q8x8_to_h8(kw);
+                f4v c = {0.0f, 0.0f, 0.0f, 0.0f};
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], c, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] += h2f(dks[i * NJ + j]) * c[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int cell = 16 * mb + 4 * lg + i;
+                sv[mb][i] = (hv && cell < nv) ? acc[i] * lscale : -INFINITY;
+            }
+        }
+        // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32)
+        float tm = -INFINITY;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float m_new = fmaxf(m, tm);
+        const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
+        float tsum = 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = sv[mb][i] == -INFINITY ? 0.0f : exp2f(sv[mb][i] - m_new);
+                tsum += p;
+                pw[hn][16 * mb + 4 * lg + i] = p;
+            }
+        tsum += __shfl_xor(tsum, 16);
+        tsum += __shfl_xor(tsum, 32);
+        lsum = lsum * alpha + tsum;
+        m = m_new;
+        // V scales of this lane's B-operand cells (32ks + 8lg + i); the tile's exponent
+        float dv[2][8][NJ];
+        float dvm = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const uint16_t *dvs = reinterpret_cast<const uint16_t *>(vp + scale_off(g, gh, row0 + 32 * ks + 8 * lg, 0));
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const bool ok = 32 * ks + 8 * lg + i < nv;
+                    dv[ks][i][j] = ok ? h2f(dvs[i * NJ + j]) : 0.0f;
+                    dvm = fmaxf(dvm, dv[ks][i][j]);
+                }
+        }
+        dvm = wave_max(dvm);
+        int e2 = 0;
+        frexpf(dvm, &e2);
+        const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e2) : 1.0f;
+        const float rs = alpha * (up / up_cur);    // O moves to this tile's units (a power-of-two ratio)
+        up_cur = up;
+#pragma unroll
+        for (int d = 0; d < ND; ++d) o[d] *= rs;
+        wave_lds_sync();
+        // ---- PV
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const float4 p0 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg]);
+            const float4 p1 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg + 4]);
+            const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                h8v bh, bl;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float y = pc[i] * dv[ks][i][j] * up;
+                    const _Float16 hi = (_Float16)y;
+                    bh[i] = hi;
+                    bl[i] = (_Float16)(y - (float)hi);
+                }
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    const int dblk = 2 * j + db;
+                    const uint2 vw = *reinterpret_cast<const uint2 *>(
+                        vp + vquant_off(g, gh, row0 + 32 * ks + 8 * lg, 16 * dblk + hn));
+                    const h8v vh = q8x8_to_h8(vw);
+                    o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
+                    o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                }
+            }
+        }
+        wave_lds_sync();                             // the strip is rewritten by the next tile
+    }
+    if (hv) {
+        const float inv = lsum > 0.0f ? 1.0f / (lsum * up_cur) : 0.0f;
+        float *orow = out + ((int64_t)s * g.H + gh * G + hn) * HD;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+            *reinterpret_cast<float4 *>(orow + 16 * d + 4 * lg) =
+                make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
+    }
+}
+
+template <int HD, int G>
+static void launch_pf_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                             const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
+                             hipStream_t st) {
+    const int pairs = n_q * g.Hkv;
+    hipLaunchKernelGGL((k_pf_attn<HD, G>), dim3((unsigned)((pairs + kPfAttnWaves - 1) / kPfAttnWaves)),
+                       dim3(kPfAttnWaves * 64), 0, st, g, v, q, n_q, sel, nsel, max_sel, out);
+}
+
+hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                                    const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
+                                    hipStream_t st) {
+#define X(HD_, G_, TG_)                                                                          \
+    if (g.hd == HD_ && g.G == G_) {                                                              \
+        launch_pf_attn_t<HD_, G_>(g, v, q, n_q, sel, nsel, max_sel, out, st);                   \
         return hipGetLastError();                                                                \
     }
     QWFN_FOR_EACH_SHAPE(X)
