@@ -1866,119 +1866,159 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
     float m = -INFINITY, lsum = 0.0f, up_cur = 1.0f;
     float (*pw)[64 + 4] = shp[wv];
     const int n_tiles = n * tpb;
-    for (int t = 0; t < n_tiles; ++t) {
-        const int blk = selp[t / tpb];
-        const int64_t t0 = (int64_t)blk * g.bt + (t % tpb) * 64;
-        const int nv = (blk < 0 || t0 >= L) ? 0 : (int)min((int64_t)64, (int64_t)L - t0);
-        if (nv == 0) continue;                       // uniform over the wave
-        const int tt = (int)t0;
-        const int32_t pg = phys_page(g, v.page_table, g.pf_seq, tt);
-        if (pg < 0) {
-            if (l == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
-            continue;
-        }
-        const int row0 = tt % g.pt;
-        const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
-        const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
-        const int tl = gh * (g.pt / 64) + row0 / 64;
-        // ---- QK
-        float sv[4][4];
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            const uint16_t *dks = reinterpret_cast<const uint16_t *>(kp + scale_off(g, gh, row0 + 16 * mb + 4 * lg, 0));
-            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const uint2 kw = *reinterpret_cast<const uint2 *>(
-                    kp + ((int64_t)(tl * (HD / 16) + 2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
-                const h8v kh = q8x8_to_h8(kw);
-                f4v c = {0.0f, 0.0f, 0.0f, 0.0f};
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], c, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i] += h2f(dks[i * NJ + j]) * c[i];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int cell = 16 * mb + 4 * lg + i;
-                sv[mb][i] = (hv && cell < nv) ? acc[i] * lscale : -INFINITY;
+    for (int tc = 0; tc < n_tiles; tc += 64) {
+        // lane l describes tile tc + l: page, first row, cells at or before the
+        // query -- looked up for 64 tiles at once, read back per tile by readlane
+        int pg_l = 0, r0_l = 0, nv_l = 0;
+        {
+            const int t = tc + l;
+            if (t < n_tiles) {
+                const int blk = selp[t / tpb];
+                const int64_t t0 = (int64_t)blk * g.bt + (t % tpb) * 64;
+                if (blk >= 0 && t0 < L) {
+                    const int32_t pg = phys_page(g, v.page_table, g.pf_seq, (int)t0);
+                    if (pg >= 0) {
+                        pg_l = pg;
+                        r0_l = (int)(t0 % g.pt);
+                        nv_l = (int)min((int64_t)64, (int64_t)L - t0);
+                    } else {
+                        set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+                    }
+                }
             }
         }
-        // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32)
-        float tm = -INFINITY;
+        const int t_end = min(n_tiles - tc, 64);
+        for (int ti = 0; ti < t_end; ++ti) {
+            const int nv = __builtin_amdgcn_readlane(nv_l, ti);
+            if (nv == 0) continue;                   // uniform over the wave
+            const int pg = __builtin_amdgcn_readlane(pg_l, ti);
+            const int row0 = __builtin_amdgcn_readlane(r0_l, ti);
+            const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
+            const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
+            const int tl = gh * (g.pt / 64) + row0 / 64;
+            // every load of the tile first: K operands and scales, V scales and operands
+            uint2 kw[4][NJ];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
-        tm = fmaxf(tm, __shfl_xor(tm, 16));
-        tm = fmaxf(tm, __shfl_xor(tm, 32));
-        const float m_new = fmaxf(m, tm);
-        const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
-        float tsum = 0.0f;
+                for (int j = 0; j < NJ; ++j)
+                    kw[mb][j] = *reinterpret_cast<const uint2 *>(
+                        kp + ((int64_t)(tl * (HD / 16) + 2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
+            // 4 cells x NJ fp16 scales of rows 16mb + 4lg .. +4: 8*NJ bytes, contiguous
+            static_assert(NJ % 2 == 0, "scale rows as whole 16-byte vectors");
+            constexpr int KSV = NJ / 2;              // uint4 per 4 cells
+            uint4 dkv[4][KSV];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = sv[mb][i] == -INFINITY ? 0.0f : exp2f(sv[mb][i] - m_new);
-                tsum += p;
-                pw[hn][16 * mb + 4 * lg + i] = p;
-            }
-        tsum += __shfl_xor(tsum, 16);
-        tsum += __shfl_xor(tsum, 32);
-        lsum = lsum * alpha + tsum;
-        m = m_new;
-        // V scales of this lane's B-operand cells (32ks + 8lg + i); the tile's exponent
-        float dv[2][8][NJ];
-        float dvm = 0.0f;
+                for (int k = 0; k < KSV; ++k)
+                    dkv[mb][k] = reinterpret_cast<const uint4 *>(kp + scale_off(g, gh, row0 + 16 * mb + 4 * lg, 0))[k];
+            constexpr int VSV = NJ;                  // uint4 per 8 cells
+            uint4 dvv[2][VSV];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const uint16_t *dvs = reinterpret_cast<const uint16_t *>(vp + scale_off(g, gh, row0 + 32 * ks + 8 * lg, 0));
+            for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+                for (int k = 0; k < VSV; ++k)
+                    dvv[ks][k] = reinterpret_cast<const uint4 *>(vp + scale_off(g, gh, row0 + 32 * ks + 8 * lg, 0))[k];
+            uint2 vw[2][ND];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+                    vw[ks][d] = *reinterpret_cast<const uint2 *>(vp + vquant_off(g, gh, row0 + 32 * ks + 8 * lg, 16 * d + hn));
+            // ---- QK
+            float sv[4][4];
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const uint16_t *dks = reinterpret_cast<const uint16_t *>(&dkv[mb][0]);
+                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    const bool ok = 32 * ks + 8 * lg + i < nv;
-                    dv[ks][i][j] = ok ? h2f(dvs[i * NJ + j]) : 0.0f;
-                    dvm = fmaxf(dvm, dv[ks][i][j]);
-                }
-        }
-        dvm = wave_max(dvm);
-        int e2 = 0;
-        frexpf(dvm, &e2);
-        const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e2) : 1.0f;
-        const float rs = alpha * (up / up_cur);    // O moves to this tile's units (a power-of-two ratio)
-        up_cur = up;
+                    const h8v kh = q8x8_to_h8(kw[mb][j]);
+                    f4v c = {0.0f, 0.0f, 0.0f, 0.0f};
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], c, 0, 0, 0);
 #pragma unroll
-        for (int d = 0; d < ND; ++d) o[d] *= rs;
-        wave_lds_sync();
-        // ---- PV
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const float4 p0 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg]);
-            const float4 p1 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg + 4]);
-            const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                h8v bh, bl;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float y = pc[i] * dv[ks][i][j] * up;
-                    const _Float16 hi = (_Float16)y;
-                    bh[i] = hi;
-                    bl[i] = (_Float16)(y - (float)hi);
+                    for (int i = 0; i < 4; ++i) acc[i] += h2f(dks[i * NJ + j]) * c[i];
                 }
 #pragma unroll
-                for (int db = 0; db < 2; ++db) {
-                    const int dblk = 2 * j + db;
-                    const uint2 vw = *reinterpret_cast<const uint2 *>(
-                        vp + vquant_off(g, gh, row0 + 32 * ks + 8 * lg, 16 * dblk + hn));
-                    const h8v vh = q8x8_to_h8(vw);
-                    o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
-                    o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                for (int i = 0; i < 4; ++i) {
+                    const int cell = 16 * mb + 4 * lg + i;
+                    sv[mb][i] = (hv && cell < nv) ? acc[i] * lscale : -INFINITY;
                 }
             }
+            // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32)
+            float tm = -INFINITY;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
+            tm = fmaxf(tm, __shfl_xor(tm, 16));
+            tm = fmaxf(tm, __shfl_xor(tm, 32));
+            const float m_new = fmaxf(m, tm);
+            const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
+            float tsum = 0.0f;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = sv[mb][i] == -INFINITY ? 0.0f : exp2f(sv[mb][i] - m_new);
+                    tsum += p;
+                    pw[hn][16 * mb + 4 * lg + i] = p;
+                }
+            tsum += __shfl_xor(tsum, 16);
+            tsum += __shfl_xor(tsum, 32);
+            lsum = lsum * alpha + tsum;
+            m = m_new;
+            // the tile's largest V scale over its valid cells sets the weight exponent
+            float dvm = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const uint16_t *dvs = reinterpret_cast<const uint16_t *>(&dvv[ks][0]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        if (32 * ks + 8 * lg + i < nv) dvm = fmaxf(dvm, h2f(dvs[i * NJ + j]));
+            }
+            dvm = wave_max(dvm);
+            int e2 = 0;
+            frexpf(dvm, &e2);
+            const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e2) : 1.0f;
+            const float rs = alpha * (up / up_cur);  // O moves to this tile's units (a power-of-two ratio)
+            up_cur = up;
+#pragma unroll
+            for (int d = 0; d < ND; ++d) o[d] *= rs;
+            wave_lds_sync();
+            // ---- PV
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const float4 p0 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg]);
+                const float4 p1 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg + 4]);
+                const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                const uint16_t *dvs = reinterpret_cast<const uint16_t *>(&dvv[ks][0]);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    h8v bh, bl;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const bool ok = 32 * ks + 8 * lg + i < nv;
+                        const float y = ok ? pc[i] * h2f(dvs[i * NJ + j]) * up : 0.0f;
+                        const _Float16 hi = (_Float16)y;
+                        bh[i] = hi;
+                        bl[i] = (_Float16)(y - (float)hi);
+                    }
+#pragma unroll
+                    for (int db = 0; db < 2; ++db) {
+                        const int dblk = 2 * j + db;
+                        const h8v vh = q8x8_to_h8(vw[ks][dblk]);
+                        o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
+                        o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                    }
+                }
+            }
+            wave_lds_sync();                         // the strip is rewritten by the next tile
         }
-        wave_lds_sync();                             // the strip is rewritten by the next tile
     }
     if (hv) {
         const float inv = lsum > 0.0f ? 1.0f / (lsum * up_cur) : 0.0f;
