@@ -330,8 +330,8 @@ def bench_prefill(qsa, torch, cfg, gen, q_batch, reps=3):
                 mfma_bf16_peak_tflops=2500.0, frac=flops / (ms * 1e-3) / 2.5e15,
                 append_bytes=PREFILL_N * cfg.n_head_kv * cfg.head_dim * 2 * 2 +
                 PREFILL_N * cfg.n_head_kv * (cfg.head_dim + cfg.head_dim // 32 * 2) * 2,
-                q_batch=q_batch, note="QK on int8 dot products and PV on fp16 dot products (VALU); "
-                "the bf16 MFMA peak is the config's stated roofline")
+                q_batch=q_batch, note="QK and PV on v_mfma_f32_16x16x32_f16 (int8 quants exact in fp16, "
+                "fp32 operands as fp16 hi + lo pairs); frac is against the dense fp16/bf16 MFMA peak")
 
 
 def cpu_baseline(cfg, ctx, seconds, seed):

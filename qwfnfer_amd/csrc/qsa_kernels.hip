@@ -1778,8 +1778,7 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
-
-constexpr int kPfAttnWaves = 4;
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));   // plain 16-byte load/store (no struct copy)
 
 // Eight int8 quants -> eight exact fp16 values, in order.
 __device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
@@ -1792,17 +1791,91 @@ __device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
     return r;
 }
 
-// LDS exchange between the lanes of one wave (no workgroup barrier).
+// Order LDS traffic between the lanes of one wave: a wave's LDS operations
+// execute in order, so only the compiler has to be kept from reordering (no
+// wait is emitted; in-flight global loads stay in flight).
 __device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
-// grid ceil(n_q * Hkv / 4), 4 waves; wave w owns (query s, KV head gh) =
-// pair blockIdx.x*4 + w and walks its selected 64-cell tiles with an online
-// softmax, every contraction on v_mfma_f32_16x16x32_f16 (one output column per
-// query head of the group, up to 16):
+// Sum / max over the lanes l, l^16, l^32, l^48 (the four k-groups of one MFMA
+// column), by the gfx950 row swaps: v_permlane32_swap pairs lane l with l^32
+// and v_permlane16_swap pairs row 2r with 2r+1; both results are symmetric, so
+// every lane of the column ends with the same value.
+__device__ __forceinline__ unsigned opaque_copy(unsigned x) {
+    unsigned y;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+    return y;
+}
+// Lane l with lane l ^ 32 (permlane32) or l ^ 16 (permlane16), combined by op.
+// The swap gets two registers the compiler cannot prove equal: given one value
+// twice it would take the two results as equal and keep only the first.
+template <typename Op>
+__device__ __forceinline__ float swap32_op(float v, Op op) {
+    const unsigned b = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, opaque_copy(b), false, false);
+    const unsigned r0 = r[0], r1 = r[1];                  // (bit_cast of r[i] reads element 0)
+    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+template <typename Op>
+__device__ __forceinline__ float swap16_op(float v, Op op) {
+    const unsigned b = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, opaque_copy(b), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float col_sum4(float v) {
+    const auto add = [](float a, float b) { return a + b; };
+    return swap16_op(swap32_op(v, add), add);
+}
+__device__ __forceinline__ float col_max4(float v) {
+    const auto mx = [](float a, float b) { return fmaxf(a, b); };
+    return swap16_op(swap32_op(v, mx), mx);
+}
+
+// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): lane
+// l's 16 bytes land at LDS byte address lds + 16 l.  Issued from asm so the
+// compiler adds no wait of its own; the caller waits with wait_vmem_all()
+// before reading the destination.  m0 (the LDS base operand) is restored.
+__device__ __forceinline__ void lds_dma16(const void *gsrc, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(gsrc), "s"(lds)
+                 : "memory");
+}
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int HD>
+struct PfAttnCfg {
+    static constexpr int WAVES = HD >= 256 ? 2 : 4;      // per workgroup, bounded by LDS
+    static constexpr int NK4 = HD / 16;                   // 1 KB transfers per K (or V) tile
+    static constexpr int NS4 = HD / 4;                    // 16-byte chunks of one tile's scale rows
+    static constexpr int SCI = (2 * NS4 + 63) / 64;       // 1 KB transfers for both scale rows
+    static constexpr int KOFF = 0, VOFF = HD * 64, SOFF = 2 * HD * 64;   // byte offsets in a buffer
+    static constexpr int BUF16 = (2 * HD * 64 + 64 * SCI * 16) / 16;      // 16-byte chunks per buffer
+};
+
+// A wave's LDS: two tile buffers (K tile as in memory; V tile with each 64-byte
+// dim row's four 16-byte quarters rotated by (dim / 4) % 4, so the PV operand
+// reads of 16 dims are bank-conflict free; the K then V scale rows) and the
+// softmax weights.
+template <int HD>
+struct PfAttnLds {
+    u4v buf[2][PfAttnCfg<HD>::BUF16];
+    float p[16][64 + 4];
+};
+
+// grid ceil(n_q * Hkv / WAVES), WAVES waves; wave w owns (query s, KV head gh)
+// = pair blockIdx.x*WAVES + w and walks its selected 64-cell tiles with an
+// online softmax.  The tiles are double-buffered in the wave's own LDS: while
+// tile t is computed from one buffer, tile t+1's K, V and scale bytes (17 KB at
+// hd 128, coalesced 16-byte global -> LDS transfers that hold no registers)
+// land in the other, so one wave per SIMD hides the memory latency.  Every
+// contraction runs on
+// v_mfma_f32_16x16x32_f16 (one output column per query head, up to 16):
 //  - QK: S[cell][head] = sum_j dk(cell, j) * (K_j[cell][:] . q_j[:, head]) per
 //    32-dim q8_0 block j, the int8 keys exact in fp16 and the query row (scaled
 //    by a power of two qs) as fp16 hi + lo, so the products are exact and
@@ -1811,18 +1884,19 @@ __device__ __forceinline__ void wave_lds_sync() {
 //    exact in fp16 and P'_j = p * dv(cell, j) * 2^k split into fp16 hi + lo
 //    (2^k keeps the tile's largest V scale near 2^15; O is carried in the
 //    current tile's units and rescaled with the softmax).
-// The tile's softmax weights cross lanes through the wave's own LDS strip.
 // Cells past the query's position have weight 0 and their V scale masked.
 template <int HD, int G>
-__global__ void __launch_bounds__(kPfAttnWaves * 64)
+__global__ void __launch_bounds__(PfAttnCfg<HD>::WAVES * 64)
 k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const int32_t *__restrict__ sel,
           const int32_t *__restrict__ nsel, int32_t max_sel, float *__restrict__ out) {
-    constexpr int NJ = HD / 32, ND = HD / 16;
+    using C = PfAttnCfg<HD>;
+    constexpr int NJ = HD / 32, ND = HD / 16, NK4 = C::NK4, NS4 = C::NS4;
     static_assert(G <= 16, "one MFMA output column per query head");
-    __shared__ float shp[kPfAttnWaves][16][64 + 4];
+    __shared__ PfAttnLds<HD> shw[C::WAVES];
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int pair = (int)blockIdx.x * kPfAttnWaves + wv;
+    const int pair = (int)blockIdx.x * C::WAVES + wv;
     if (pair >= n_q * g.Hkv) return;                 // a whole wave; no workgroup barrier follows
+    PfAttnLds<HD> &W = shw[wv];
     const int s = pair / g.Hkv, gh = pair - s * g.Hkv;
     const int L = g.pf_pos0 + s + 1;
     const int hn = l & 15, lg = l >> 4;              // MFMA column (head) and k-group of this lane
@@ -1832,39 +1906,43 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
     const int32_t *selp = sel + (int64_t)pair * max_sel;
     // query head hn, dims 32j + 8lg .. +8, as fp16 hi + lo of q / qs
     const float *qrow = q + ((int64_t)s * g.H + gh * G + (hv ? hn : 0)) * HD;
-    float x[NJ][8];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg);
-        const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg + 4);
-        x[j][0] = x0.x; x[j][1] = x0.y; x[j][2] = x0.z; x[j][3] = x0.w;
-        x[j][4] = x1.x; x[j][5] = x1.y; x[j][6] = x1.z; x[j][7] = x1.w;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[j][i]));
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    int ex = 0;
-    frexpf(amax, &ex);
-    const float qs = amax > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f;   // |q / qs| < 2^14
-    const float qinv = 1.0f / qs;                                   // a power of two: exact
     h8v qh[NJ], ql[NJ];
+    float qs;
+    {
+        float x[NJ][8];
+        float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+        for (int j = 0; j < NJ; ++j) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg + 4);
+            x[j][0] = x0.x; x[j][1] = x0.y; x[j][2] = x0.z; x[j][3] = x0.w;
+            x[j][4] = x1.x; x[j][5] = x1.y; x[j][6] = x1.z; x[j][7] = x1.w;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float y = hv ? x[j][i] * qinv : 0.0f;
-            const _Float16 hi = (_Float16)y;
-            qh[j][i] = hi;
-            ql[j][i] = (_Float16)(y - (float)hi);
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[j][i]));
         }
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        int ex = 0;
+        frexpf(amax, &ex);
+        qs = amax > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f;   // |q / qs| < 2^14
+        const float qinv = 1.0f / qs;                        // a power of two: exact
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float y = hv ? x[j][i] * qinv : 0.0f;
+                const _Float16 hi = (_Float16)y;
+                qh[j][i] = hi;
+                ql[j][i] = (_Float16)(y - (float)hi);
+            }
+    }
     const float lscale = qs * g.scale_log2;
     f4v o[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) o[d] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-    float m = -INFINITY, lsum = 0.0f, up_cur = 1.0f;
-    float (*pw)[64 + 4] = shp[wv];
+    // running max starts at a finite floor far below any score, so exp2 of
+    // (score - max) never sees inf - inf
+    float m = -1e30f, lsum = 0.0f, up_cur = 1.0f;
     const int n_tiles = n * tpb;
     for (int tc = 0; tc < n_tiles; tc += 64) {
         // lane l describes tile tc + l: page, first row, cells at or before the
@@ -1888,136 +1966,160 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
             }
         }
         const int t_end = min(n_tiles - tc, 64);
-        for (int ti = 0; ti < t_end; ++ti) {
-            const int nv = __builtin_amdgcn_readlane(nv_l, ti);
-            if (nv == 0) continue;                   // uniform over the wave
+        // tile ti -> buffer bi: K chunks as in memory, V chunks rotated, scale rows
+        auto issue = [&](int ti, int bi) {
             const int pg = __builtin_amdgcn_readlane(pg_l, ti);
             const int row0 = __builtin_amdgcn_readlane(r0_l, ti);
             const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
             const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
             const int tl = gh * (g.pt / 64) + row0 / 64;
-            // every load of the tile first: K operands and scales, V scales and operands
-            uint2 kw[4][NJ];
+            const uint32_t base = __builtin_amdgcn_readfirstlane(
+                (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&W.buf[bi][0]);
+            const uint8_t *ksrc = kp + (int64_t)tl * (HD / 16) * 1024 + 16 * l;
+            const uint8_t *vsrc = vp + (int64_t)tl * HD * 64 + (l >> 2) * 64 + (((l & 3) ^ ((l >> 4) & 3)) << 4);
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int i = 0; i < NK4; ++i) lds_dma16(ksrc + i * 1024, base + C::KOFF + i * 1024);
 #pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    kw[mb][j] = *reinterpret_cast<const uint2 *>(
-                        kp + ((int64_t)(tl * (HD / 16) + 2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
-            // 4 cells x NJ fp16 scales of rows 16mb + 4lg .. +4: 8*NJ bytes, contiguous
-            static_assert(NJ % 2 == 0, "scale rows as whole 16-byte vectors");
-            constexpr int KSV = NJ / 2;              // uint4 per 4 cells
-            uint4 dkv[4][KSV];
+            for (int i = 0; i < NK4; ++i) lds_dma16(vsrc + i * 1024, base + C::VOFF + i * 1024);
+            const uint8_t *kss = kp + scale_off(g, gh, row0, 0);
+            const uint8_t *vss = vp + scale_off(g, gh, row0, 0);
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-                for (int k = 0; k < KSV; ++k)
-                    dkv[mb][k] = reinterpret_cast<const uint4 *>(kp + scale_off(g, gh, row0 + 16 * mb + 4 * lg, 0))[k];
-            constexpr int VSV = NJ;                  // uint4 per 8 cells
-            uint4 dvv[2][VSV];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int k = 0; k < VSV; ++k)
-                    dvv[ks][k] = reinterpret_cast<const uint4 *>(vp + scale_off(g, gh, row0 + 32 * ks + 8 * lg, 0))[k];
-            uint2 vw[2][ND];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int d = 0; d < ND; ++d)
-                    vw[ks][d] = *reinterpret_cast<const uint2 *>(vp + vquant_off(g, gh, row0 + 32 * ks + 8 * lg, 16 * d + hn));
-            // ---- QK
-            float sv[4][4];
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const uint16_t *dks = reinterpret_cast<const uint16_t *>(&dkv[mb][0]);
-                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    const h8v kh = q8x8_to_h8(kw[mb][j]);
-                    f4v c = {0.0f, 0.0f, 0.0f, 0.0f};
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], c, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i] += h2f(dks[i * NJ + j]) * c[i];
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int cell = 16 * mb + 4 * lg + i;
-                    sv[mb][i] = (hv && cell < nv) ? acc[i] * lscale : -INFINITY;
-                }
+            for (int c = 0; c < C::SCI; ++c) {
+                const int r = 64 * c + l;
+                if (r < 2 * NS4) lds_dma16(r < NS4 ? kss + 16 * r : vss + 16 * (r - NS4), base + C::SOFF + c * 1024);
             }
-            // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32)
-            float tm = -INFINITY;
+        };
+        issue(0, 0);
+        for (int ti = 0; ti < t_end; ++ti) {
+            const int nv = __builtin_amdgcn_readlane(nv_l, ti);
+            wait_vmem_all();                         // tile ti has landed in buffer ti & 1
+            if (ti + 1 < t_end) issue(ti + 1, (ti + 1) & 1);
+            if (nv > 0) {                            // uniform over the wave
+                const uint8_t *wk = reinterpret_cast<const uint8_t *>(&W.buf[ti & 1][0]) + C::KOFF;
+                const uint8_t *wvb = reinterpret_cast<const uint8_t *>(&W.buf[ti & 1][0]) + C::VOFF;
+                // cell c's NJ fp16 scales: halfs c*NJ .. c*NJ+NJ of the K (V) scale row
+                const u4v *wks = reinterpret_cast<const u4v *>(reinterpret_cast<const uint8_t *>(&W.buf[ti & 1][0]) + C::SOFF);
+                const u4v *wvs = wks + NS4;
+                // ---- QK
+                float sv[4][4];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+                for (int mb = 0; mb < 4; ++mb) {
+                    h8v dk[NJ / 2];                  // cells 16mb+4lg .. +4, every block
 #pragma unroll
-                for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
-            tm = fmaxf(tm, __shfl_xor(tm, 16));
-            tm = fmaxf(tm, __shfl_xor(tm, 32));
-            const float m_new = fmaxf(m, tm);
-            const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
-            float tsum = 0.0f;
+                    for (int w = 0; w < NJ / 2; ++w)
+                        dk[w] = __builtin_bit_cast(h8v, wks[(16 * mb + 4 * lg) * NJ / 8 + w]);
+                    f4v c[NJ];                       // block j's dot products, independent chains
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = sv[mb][i] == -INFINITY ? 0.0f : exp2f(sv[mb][i] - m_new);
-                    tsum += p;
-                    pw[hn][16 * mb + 4 * lg + i] = p;
-                }
-            tsum += __shfl_xor(tsum, 16);
-            tsum += __shfl_xor(tsum, 32);
-            lsum = lsum * alpha + tsum;
-            m = m_new;
-            // the tile's largest V scale over its valid cells sets the weight exponent
-            float dvm = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const uint16_t *dvs = reinterpret_cast<const uint16_t *>(&dvv[ks][0]);
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
+                    for (int j = 0; j < NJ; ++j) {
+                        const uint2 kw = *reinterpret_cast<const uint2 *>(
+                            wk + ((2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
+                        const h8v kh = q8x8_to_h8(kw);
+                        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], c[j], 0, 0, 0);
+                    }
+                    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
-                        if (32 * ks + 8 * lg + i < nv) dvm = fmaxf(dvm, h2f(dvs[i * NJ + j]));
-            }
-            dvm = wave_max(dvm);
-            int e2 = 0;
-            frexpf(dvm, &e2);
-            const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e2) : 1.0f;
-            const float rs = alpha * (up / up_cur);  // O moves to this tile's units (a power-of-two ratio)
-            up_cur = up;
 #pragma unroll
-            for (int d = 0; d < ND; ++d) o[d] *= rs;
-            wave_lds_sync();
-            // ---- PV
+                        for (int i = 0; i < 4; ++i)
+                            acc[i] = __builtin_fmaf((float)dk[(i * NJ + j) / 8][(i * NJ + j) % 8], c[j][i], acc[i]);
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const float4 p0 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg]);
-                const float4 p1 = *reinterpret_cast<const float4 *>(&pw[hn][32 * ks + 8 * lg + 4]);
-                const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                const uint16_t *dvs = reinterpret_cast<const uint16_t *>(&dvv[ks][0]);
+                    for (int i = 0; i < 4; ++i) sv[mb][i] = acc[i] * lscale;
+                }
+                // V scales of this lane's PV cells 32ks+8lg .. +8, every block (NJ words per ks)
+                u4v dvw[2][NJ];
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    h8v bh, bl;
+                for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const bool ok = 32 * ks + 8 * lg + i < nv;
-                        const float y = ok ? pc[i] * h2f(dvs[i * NJ + j]) * up : 0.0f;
-                        const _Float16 hi = (_Float16)y;
-                        bh[i] = hi;
-                        bl[i] = (_Float16)(y - (float)hi);
+                    for (int w = 0; w < NJ; ++w) dvw[ks][w] = wvs[(32 * ks + 8 * lg) * NJ / 8 + w];
+                if (nv < 64) {                       // a partial tile: cells past the query carry no data
+#pragma unroll
+                    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (16 * mb + 4 * lg + i >= nv) sv[mb][i] = -INFINITY;
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                        for (int w = 0; w < NJ; ++w)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)  // a dword holds two blocks of one cell (NJ even)
+                                if (32 * ks + 8 * lg + (8 * w + 2 * e) / NJ >= nv) dvw[ks][w][e] = 0u;
+                }
+                // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32).
+                // Columns past the group's heads see q = 0: their weights are finite and unused.
+                float tm = -INFINITY;
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
+                tm = col_max4(tm);
+                const float m_new = fmaxf(m, tm);
+                const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+                float tsum = 0.0f;
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float p = __builtin_amdgcn_exp2f(sv[mb][i] - m_new);
+                        tsum += p;
+                        W.p[hn][16 * mb + 4 * lg + i] = p;
                     }
+                tsum = col_sum4(tsum);
+                lsum = lsum * alpha + tsum;
+                m = m_new;
+                // the tile's largest V scale sets the weight exponent (scales are >= 0)
+                h8v dmx = __builtin_bit_cast(h8v, dvw[0][0]);
 #pragma unroll
-                    for (int db = 0; db < 2; ++db) {
-                        const int dblk = 2 * j + db;
-                        const h8v vh = q8x8_to_h8(vw[ks][dblk]);
-                        o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
-                        o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int w = 0; w < NJ; ++w)
+                        dmx = __builtin_elementwise_max(dmx, __builtin_bit_cast(h8v, dvw[ks][w]));
+                float dvm = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dvm = fmaxf(dvm, (float)dmx[e]);
+                dvm = wave_max(dvm);
+                int e2 = 0;
+                frexpf(dvm, &e2);
+                const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e2) : 1.0f;
+                const float rs = alpha * (up / up_cur);  // O moves to this tile's units (power-of-two ratio)
+                up_cur = up;
+                if (__builtin_amdgcn_ballot_w64(rs != 1.0f) != 0) {
+#pragma unroll
+                    for (int d = 0; d < ND; ++d) o[d] *= rs;
+                }
+                wave_lds_sync();
+                // ---- PV
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const float4 p0 = *reinterpret_cast<const float4 *>(&W.p[hn][32 * ks + 8 * lg]);
+                    const float4 p1 = *reinterpret_cast<const float4 *>(&W.p[hn][32 * ks + 8 * lg + 4]);
+                    const float pc[8] = {p0.x * up, p0.y * up, p0.z * up, p0.w * up,
+                                         p1.x * up, p1.y * up, p1.z * up, p1.w * up};
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        h8v bh, bl;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const h8v dw = __builtin_bit_cast(h8v, dvw[ks][(i * NJ + j) / 8]);
+                            const float dv = (float)dw[(i * NJ + j) % 8];
+                            const _Float16 hi = (_Float16)__builtin_fmaf(pc[i], dv, 0.0f);
+                            bh[i] = hi;
+                            bl[i] = (_Float16)__builtin_fmaf(pc[i], dv, -(float)hi);
+                        }
+#pragma unroll
+                        for (int db = 0; db < 2; ++db) {
+                            const int dblk = 2 * j + db;
+                            const uint2 vw = *reinterpret_cast<const uint2 *>(
+                                wvb + (16 * dblk + hn) * 64 + (((2 * ks + (lg >> 1)) ^ (hn >> 2)) << 4) + 8 * (lg & 1));
+                            const h8v vh = q8x8_to_h8(vw);
+                            o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
+                            o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                        }
                     }
                 }
             }
-            wave_lds_sync();                         // the strip is rewritten by the next tile
+            wave_lds_sync();                         // the weight strip is rewritten next
         }
     }
     if (hv) {
@@ -2034,9 +2136,10 @@ template <int HD, int G>
 static void launch_pf_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                              const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
                              hipStream_t st) {
+    constexpr int WAVES = PfAttnCfg<HD>::WAVES;
     const int pairs = n_q * g.Hkv;
-    hipLaunchKernelGGL((k_pf_attn<HD, G>), dim3((unsigned)((pairs + kPfAttnWaves - 1) / kPfAttnWaves)),
-                       dim3(kPfAttnWaves * 64), 0, st, g, v, q, n_q, sel, nsel, max_sel, out);
+    hipLaunchKernelGGL((k_pf_attn<HD, G>), dim3((unsigned)((pairs + WAVES - 1) / WAVES)), dim3(WAVES * 64), 0, st, g,
+                       v, q, n_q, sel, nsel, max_sel, out);
 }
 
 hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
