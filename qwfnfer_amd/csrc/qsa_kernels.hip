@@ -1237,16 +1237,17 @@ static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
 // attention, q8_0 fast path (block_tokens a multiple of 64): one tile = 64
 // consecutive tokens of one selected block.  Wave w of a tile owns q8_0
 // block w of the head dims (32 dims) for every query head of the group, so K
-// and V are each read exactly once per tile:
-//   QK  lane = cell; exact int32 dot4 of the int8 key quants against the
-//       query's three int8 parts; per-wave partial logits summed in LDS in
-//       wave order.
+// and V are each read exactly once per tile, in matrix-core operand layouts:
+//   QK  v_mfma_i32_16x16x32_i8 of the int8 key quants (16 cells x 32 dims)
+//       against each of the query's three int8 parts (32 dims x 16 heads):
+//       exact int32 dots, combined once in fp32; per-wave partial logits
+//       scaled by the key scale and summed in wave order by the softmax.
 //   softmax per head (DPP), p' = p * dv * 2^sh as an fp16 high part plus an
 //       fp16 remainder ([head][block][cell]), sh a per-tile power of two that
 //       keeps p' inside fp16's range.
-//   PV  lane = (dim, half of the cells); V quants of a dim are 64 contiguous
-//       bytes (dim-major tiles) converted exactly to fp16 pairs; dot2 with
-//       the p' pairs, fp32 accumulation, then * 2^-sh.
+//   PV  v_mfma_f32_16x16x32_f16 of the V quants (exact in fp16, 16 dims x 32
+//       cells of the dim-major tile) against p' high and low (32 cells x 16
+//       heads), fp32 accumulation, then * 2^-sh.
 // ---------------------------------------------------------------------------
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -1260,6 +1261,30 @@ __device__ __forceinline__ void q8x4_to_h2(uint32_t w, half2v &lo, half2v &hi) {
     hi = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + bias;
 }
 
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef int32_t i4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));   // plain 16-byte load/store (no struct copy)
+
+// Eight int8 quants -> eight exact fp16 values, in order.
+__device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
+    half2v a, b, c, d;
+    q8x4_to_h2(w.x, a, b);
+    q8x4_to_h2(w.y, c, d);
+    h8v r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+    return r;
+}
+
+// Matrix-core operand layouts (v_mfma_*_16x16x32_*, wave64), lane l = 16*lg + hn:
+//   A: row hn, k = 8*lg .. 8*lg+7;  B: column hn, k = 8*lg .. 8*lg+7;
+//   D: rows 4*lg .. 4*lg+3, column hn.
+__device__ __forceinline__ i4v mfma_i8(uint2 a, uint2 b, i4v c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)__builtin_bit_cast(uint64_t, a),
+                                                 (long)__builtin_bit_cast(uint64_t, b), c, 0, 0, 0);
+}
+
 template <int HD, int G, int TG>
 struct FastCfg {
     static constexpr int NB = HD / 32;                 // q8_0 blocks per head row = waves per tile
@@ -1269,11 +1294,11 @@ struct FastCfg {
 };
 
 template <int HD, int G>
-struct FastGroup {
-    float lg[HD / 32][G][64];                  // partial logits, one per owning wave
+struct alignas(16) FastGroup {
+    float lg[HD / 32][G][64];                  // unscaled partial logits, one per owning wave
     uint16_t pp[G][HD / 32][64];               // fp16 p * dv * 2^sh (high part)
     uint16_t pl[G][HD / 32][64];               // its fp16 remainder (low part)
-    float o[2][G][HD];                         // the tile's O, one slice per cell half
+    float o[G][HD];                            // the tile's O
     float m[G], l[G];
 };
 
@@ -1294,6 +1319,7 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
           float *__restrict__ out, Ws ws) {
     using C = FastCfg<HD, G, TG>;
     constexpr int NB = C::NB;
+    static_assert(G <= 16, "one matrix-core column per query head");
     __shared__ FastShared<HD, G, TG> sh;
     const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);
@@ -1352,24 +1378,33 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
         const uint8_t *kp = (const uint8_t *)v.k_pages + pbase;
         const uint8_t *vp = (const uint8_t *)v.v_pages + pbase;
         const int tl = gh * (g.pt / 64) + row0 / 64;       // tile index inside the pool page
-        // every load of the tile first: K block w of cell `lane`, its scale,
-        // V of dim d for one half of the cells, the V scales of cell `lane`
-        const uint8_t *kq = kp + ((int64_t)tl * (HD / 16) + 2 * w) * 1024 + lane * 16;
-        const int d = 32 * w + (lane & 31), half = lane >> 5;
-        const uint8_t *vq = vp + ((int64_t)tl * HD + d) * 64 + half * 32;
-        uint4 k0 = make_uint4(0, 0, 0, 0), k1 = k0, v0 = k0, v1 = k0;
-        uint16_t dkh = 0, dvh[NB];
+        // every load of the tile first, in operand layout (lane = 16*lg + hn):
+        // K of cells 16mb+hn, dims 32w+8lg .. +8 (mb = 0..3); V of dims
+        // 32w+16db+hn, cells 32ks+8lg .. +8; the K and V scale rows of cell `lane`
+        const int hn = lane & 15, lg = lane >> 4;
+        const uint8_t *kq = kp + ((int64_t)tl * (HD / 16) + 2 * w + (lg >> 1)) * 1024 + hn * 16 + 8 * (lg & 1);
+        const uint8_t *vq = vp + ((int64_t)tl * HD + 32 * w + hn) * 64 + 8 * lg;
+        uint2 kw[4], vw[2][2];
+        uint16_t dkh[NB], dvh[NB];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) dvh[j] = 0;
+        for (int i = 0; i < 4; ++i) kw[i] = make_uint2(0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vw[i / 2][i % 2] = make_uint2(0, 0);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) dkh[j] = dvh[j] = 0;
         if (nv > 0) {
-            k0 = *reinterpret_cast<const uint4 *>(kq);
-            k1 = *reinterpret_cast<const uint4 *>(kq + 1024);
-            v0 = *reinterpret_cast<const uint4 *>(vq);
-            v1 = *reinterpret_cast<const uint4 *>(vq + 16);
-            const int64_t so = g.qbytes + ((int64_t)(gh * g.pt + row0 + lane) * NB) * 2;
-            dkh = *reinterpret_cast<const uint16_t *>(kp + so + 2 * w);
 #pragma unroll
-            for (int j = 0; j < NB; ++j) dvh[j] = *reinterpret_cast<const uint16_t *>(vp + so + 2 * j);
+            for (int mb = 0; mb < 4; ++mb) kw[mb] = *reinterpret_cast<const uint2 *>(kq + mb * 256);
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) vw[db][ks] = *reinterpret_cast<const uint2 *>(vq + db * 1024 + ks * 32);
+            const int64_t so = g.qbytes + ((int64_t)(gh * g.pt + row0 + lane) * NB) * 2;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                dkh[j] = *reinterpret_cast<const uint16_t *>(kp + so + 2 * j);
+                dvh[j] = *reinterpret_cast<const uint16_t *>(vp + so + 2 * j);
+            }
         }
         // The group's query heads split into three int8 parts per head,
         // q ~= qs * (qa + qb/254 + qc/254^2), qs = amax/127 (residual below
@@ -1404,38 +1439,33 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
             }
         }
         __syncthreads();
-        // QK over block w: exact int32 dots, one fp32 rescale
+        // QK over block w on the matrix cores: exact int32 dots of the key
+        // quants against each query part, combined once in fp32 (the key
+        // scale is applied by the softmax)
         {
-            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-            const float dk = h2f(dkh);
-            constexpr int HQ = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);   // heads per batch of LDS reads
+            const int hq = min(hn, G - 1);
+            uint2 qp[3];
+            {
+                const uint2 *pa = reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(sh.qa[hq]) + 32 * w + 8 * lg);
+                const uint2 *pb = reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(sh.qb[hq]) + 32 * w + 8 * lg);
+                const uint2 *pc = reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(sh.qc[hq]) + 32 * w + 8 * lg);
+                const uint2 z = make_uint2(0, 0);
+                qp[0] = hn < G ? *pa : z;
+                qp[1] = hn < G ? *pb : z;
+                qp[2] = hn < G ? *pc : z;
+            }
 #pragma unroll
-            for (int h0 = 0; h0 < G; h0 += HQ) {
-                uint4 qv[HQ][3][2];
+            for (int mb = 0; mb < 4; ++mb) {
+                const i4v zero = {0, 0, 0, 0};
+                const i4v da = mfma_i8(kw[mb], qp[0], zero);
+                const i4v db = mfma_i8(kw[mb], qp[1], zero);
+                const i4v dc = mfma_i8(kw[mb], qp[2], zero);
+                float r[4];
 #pragma unroll
-                for (int hh = 0; hh < HQ; ++hh)
-#pragma unroll
-                    for (int r = 0; r < 2; ++r) {
-                        qv[hh][0][r] = reinterpret_cast<const uint4 *>(&sh.qa[h0 + hh][8 * w])[r];
-                        qv[hh][1][r] = reinterpret_cast<const uint4 *>(&sh.qb[h0 + hh][8 * w])[r];
-                        qv[hh][2][r] = reinterpret_cast<const uint4 *>(&sh.qc[h0 + hh][8 * w])[r];
-                    }
-#pragma unroll
-                for (int hh = 0; hh < HQ; ++hh) {
-                    int acc3[3];
-#pragma unroll
-                    for (int part = 0; part < 3; ++part) {
-                        const int32_t qw[8] = {(int)qv[hh][part][0].x, (int)qv[hh][part][0].y, (int)qv[hh][part][0].z,
-                                               (int)qv[hh][part][0].w, (int)qv[hh][part][1].x, (int)qv[hh][part][1].y,
-                                               (int)qv[hh][part][1].z, (int)qv[hh][part][1].w};
-                        int a = 0;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) a = __builtin_amdgcn_sdot4((int)kw[i], qw[i], a, false);
-                        acc3[part] = a;
-                    }
-                    gr.lg[w][h0 + hh][lane] =
-                        dk * ((float)acc3[0] + ((float)acc3[1] + (float)acc3[2] * (1.0f / 254.0f)) * (1.0f / 254.0f));
-                }
+                for (int i = 0; i < 4; ++i)
+                    r[i] = (float)da[i] + ((float)db[i] + (float)dc[i] * (1.0f / 254.0f)) * (1.0f / 254.0f);
+                if (hn < G)
+                    *reinterpret_cast<float4 *>(&gr.lg[w][hn][16 * mb + 4 * lg]) = make_float4(r[0], r[1], r[2], r[3]);
             }
         }
         __syncthreads();
@@ -1449,10 +1479,14 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
             int e = 0;
             frexpf(dvm, &e);
             const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e) : 1.0f;
-            for (int h = w; h < G; h += NB) {
-                float lsum = gr.lg[0][h][lane];
+            float dkf[NB];
 #pragma unroll
-                for (int ww = 1; ww < NB; ++ww) lsum += gr.lg[ww][h][lane];
+            for (int j = 0; j < NB; ++j) dkf[j] = h2f(dkh[j]);
+            for (int h = w; h < G; h += NB) {
+#pragma clang fp contract(off)
+                float lsum = dkf[0] * gr.lg[0][h][lane];
+#pragma unroll
+                for (int ww = 1; ww < NB; ++ww) lsum += dkf[ww] * gr.lg[ww][h][lane];
                 const float s2 = valid ? lsum * sh.qs[h] * g.scale_log2 : -INFINITY;
                 const float m = wave_max(s2);
                 const float p = valid ? exp2f(s2 - m) : 0.0f;
@@ -1468,38 +1502,28 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
             }
             const float down = 1.0f / up;              // exact: up is a power of two
             __syncthreads();
-            // PV: lane = (dim d, half); 32 cells = 16 fp16 pairs
-            half2v vp2[16];
-            const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            // PV on the matrix cores: O[dim][head] over dims 32w+16db .. +16,
+            // cells in two steps of 32, p' high then low
+            {
+                const int hq = min(hn, G - 1);
+                f4v o2[2] = {f4v{0.0f, 0.0f, 0.0f, 0.0f}, f4v{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) q8x4_to_h2(vw[i], vp2[2 * i], vp2[2 * i + 1]);
-            constexpr int HB = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);   // heads per batch of LDS reads
+                for (int ks = 0; ks < 2; ++ks) {
+                    const h8v z = {};
+                    const h8v bh = hn < G ? *reinterpret_cast<const h8v *>(&gr.pp[hq][w][32 * ks + 8 * lg]) : z;
+                    const h8v bl = hn < G ? *reinterpret_cast<const h8v *>(&gr.pl[hq][w][32 * ks + 8 * lg]) : z;
 #pragma unroll
-            for (int h0 = 0; h0 < G; h0 += HB) {
-                uint4 ph[HB][4], pl[HB][4];
-#pragma unroll
-                for (int hh = 0; hh < HB; ++hh)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        ph[hh][r] = reinterpret_cast<const uint4 *>(&gr.pp[h0 + hh][w][half * 32])[r];
-                        pl[hh][r] = reinterpret_cast<const uint4 *>(&gr.pl[h0 + hh][w][half * 32])[r];
+                    for (int db = 0; db < 2; ++db) {
+                        const h8v va = q8x8_to_h8(vw[db][ks]);
+                        o2[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, bh, o2[db], 0, 0, 0);
+                        o2[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, bl, o2[db], 0, 0, 0);
                     }
+                }
+                if (hn < G) {
 #pragma unroll
-                for (int hh = 0; hh < HB; ++hh) {
-                    float acc = 0.0f, accl = 0.0f;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint4 pq = ph[hh][r], pq2 = pl[hh][r];
-                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.x), vp2[4 * r + 0], acc, false);
-                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.y), vp2[4 * r + 1], acc, false);
-                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.z), vp2[4 * r + 2], acc, false);
-                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq.w), vp2[4 * r + 3], acc, false);
-                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.x), vp2[4 * r + 0], accl, false);
-                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.y), vp2[4 * r + 1], accl, false);
-                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.z), vp2[4 * r + 2], accl, false);
-                        accl = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pq2.w), vp2[4 * r + 3], accl, false);
-                    }
-                    gr.o[half][h0 + hh][d] = (acc + accl) * down;
+                    for (int db = 0; db < 2; ++db)
+                        *reinterpret_cast<float4 *>(&gr.o[hn][32 * w + 16 * db + 4 * lg]) =
+                            make_float4(o2[db][0] * down, o2[db][1] * down, o2[db][2] * down, o2[db][3] * down);
                 }
             }
         }
@@ -1521,7 +1545,7 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
                     if (part * TG + t < tiles_act) {
                         const float mt = sh.grp[t].m[h];
                         const float wt = mt == -INFINITY ? 0.0f : exp2f(mt - M);
-                        O += wt * (sh.grp[t].o[0][h][dd] + sh.grp[t].o[1][h][dd]);
+                        O += wt * sh.grp[t].o[h][dd];
                         Ls += wt * sh.grp[t].l[h];
                     }
                 }
@@ -1775,21 +1799,6 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
 // ---------------------------------------------------------------------------
 // prefill attention on the matrix cores: one wave per (query, KV head)
 // ---------------------------------------------------------------------------
-
-typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));   // plain 16-byte load/store (no struct copy)
-
-// Eight int8 quants -> eight exact fp16 values, in order.
-__device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
-    half2v a, b, c, d;
-    q8x4_to_h2(w.x, a, b);
-    q8x4_to_h2(w.y, c, d);
-    h8v r;
-    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-    return r;
-}
 
 // Order LDS traffic between the lanes of one wave: a wave's LDS operations
 // execute in order, so only the compiler has to be kept from reordering (no
