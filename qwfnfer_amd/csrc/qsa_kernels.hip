@@ -2174,7 +2174,11 @@ hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float
 }
 
 // q8_0 fast attention instantiations (head_dim, group, tiles per workgroup);
-// used when block_tokens is a multiple of 64
+// used when block_tokens is a multiple of 64.  One sequence wants small
+// workgroups (latency: the compute phase runs with fewer waves per CU); a
+// batch of sequences fills the chip anyway and wants fewer partials to merge.
+#define QWFN_FOR_EACH_FAST_BATCH(X) X(128, 8, 4)
+constexpr int32_t kFastBatchSeqs = 4;              // from this many sequences on
 #define QWFN_FOR_EACH_FAST(X) X(128, 8, 2) X(128, 4, 2) X(128, 2, 2) X(64, 8, 2) X(256, 12, 1) X(256, 8, 1)
 
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
@@ -2187,6 +2191,7 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
             launch_attn_q8_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
             return hipGetLastError();                                                            \
         }
+        if (n_seq >= kFastBatchSeqs) { QWFN_FOR_EACH_FAST_BATCH(F) }
         QWFN_FOR_EACH_FAST(F)
 #undef F
     }
