@@ -140,6 +140,27 @@ int qwfn_qsa_workspace_init(void *ws, size_t ws_bytes, void *stream);
 /* Synchronously copies view->status to *status and clears it.                 */
 int qwfn_qsa_read_status(const qwfn_kv_view *view, int32_t *status, void *stream);
 
+/* ---- format interop ------------------------------------------------------ */
+/* Format interop with the reference's cache tensors: per attention layer a
+ * 1-D q8_0 tensor whose row t holds the token's n_head_kv * head_dim elements,
+ * head-major (src/qwfn_state.cpp:40, 52-53), i.e. n_head_kv * head_dim / 32
+ * ggml block_q8_0 {fp16 d; int8 qs[32]} of 34 bytes, rows back to back.
+ * qwfn_kv_row_bytes gives one row's size.  Export copies positions
+ * [pos0, pos0 + n_tokens) of sequence `seq` out of the paged cache into such
+ * rows (device memory, 2-byte aligned); import writes such rows into the pages
+ * byte for byte (an idempotent overwrite).  Import leaves the pooled keys
+ * alone: pool the blocks it completes with qwfn_pool_rebuild /
+ * qwfn_pool_update.  Either row pointer may be NULL (K or V only).  These
+ * replace no reference call: they convert its state layout (the tensors of
+ * state::init, src/qwfn_state.cpp:50-54) to and from the paged layout.      */
+int qwfn_kv_row_bytes(const qwfn_qsa_shape *shape, size_t *bytes);
+int qwfn_kv_export_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                        int32_t seq, int32_t pos0, int32_t n_tokens,
+                        void *k_rows, void *v_rows, void *stream);
+int qwfn_kv_import_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                        int32_t seq, int32_t pos0, int32_t n_tokens,
+                        const void *k_rows, const void *v_rows, void *stream);
+
 /* ---- cache writes -------------------------------------------------------- */
 /* Quantize n_rows K and V rows ([n_head_kv][head_dim] each, F32 or F16) to
  * q8_0 and write them at (seq_ids[i], pos[i]).  An idempotent overwrite: a

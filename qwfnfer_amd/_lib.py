@@ -37,6 +37,9 @@ EXPORTS = (
     "qwfn_qsa_workspace_bytes",
     "qwfn_qsa_workspace_init",
     "qwfn_qsa_read_status",
+    "qwfn_kv_row_bytes",
+    "qwfn_kv_export_q8_0",
+    "qwfn_kv_import_q8_0",
     "qwfn_kv_append_q8_0",
     "qwfn_pool_update",
     "qwfn_pool_rebuild",
@@ -109,6 +112,9 @@ _SIGS = {
     "qwfn_kv_append_q8_0": (C.c_int, [_S, _V, _P, _P, _I, _P, _P, _I, _P]),
     "qwfn_pool_update": (C.c_int, [_S, _V, _P, _P, _I, _P]),
     "qwfn_pool_rebuild": (C.c_int, [_S, _V, _I, _I, _P]),
+    "qwfn_kv_row_bytes": (C.c_int, [_S, C.POINTER(_Z)]),
+    "qwfn_kv_export_q8_0": (C.c_int, [_S, _V, _I, _I, _I, _P, _P, _P]),
+    "qwfn_kv_import_q8_0": (C.c_int, [_S, _V, _I, _I, _I, _P, _P, _P]),
     "qwfn_indexer_topk": (C.c_int, [_S, _V, _P, _P, _I, _I, _P, _P, _I, _P, _Z, _P]),
     "qwfn_gather_dequant": (C.c_int, [_S, _V, _P, _I, _P, _P, _I, _P, _P, _P, _P]),
     "qwfn_sparse_decode_attn": (C.c_int, [_S, _V, _P, _P, _I, _I, _P, _P, _I, _P, _P, _Z, _P]),

@@ -269,6 +269,44 @@ int qwfn_kv_append_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, c
     return e == hipSuccess ? ok() : hip_fail(e, "append");
 }
 
+int qwfn_kv_row_bytes(const qwfn_qsa_shape *shape, size_t *bytes) {
+    Geo g;
+    int rc = make_geo(shape, nullptr, &g, false);
+    if (rc) return rc;
+    if (!bytes) return fail(QWFN_EINVAL, "bytes is NULL");
+    *bytes = (size_t)g.Hkv * (size_t)(g.hd / 32) * 34u;
+    return ok();
+}
+
+static int kv_rows(const char *what, bool to_rows, const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                   int32_t seq, int32_t pos0, int32_t n_tokens, const void *k_rows, const void *v_rows,
+                   void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (!k_rows && !v_rows) return fail(QWFN_EINVAL, "%s: k_rows and v_rows are both NULL", what);
+    if (!aligned(k_rows, 2) || !aligned(v_rows, 2)) return fail(QWFN_EINVAL, "%s: rows must be 2-byte aligned", what);
+    if (seq < 0 || seq >= view->n_seq) return fail(QWFN_EINVAL, "%s: seq %d outside the view", what, seq);
+    if (pos0 < 0 || n_tokens < 1) return fail(QWFN_EINVAL, "%s: pos0 %d < 0 or n_tokens %d < 1", what, pos0, n_tokens);
+    const int64_t end = (int64_t)pos0 + n_tokens;
+    if (end > (int64_t)view->pages_per_seq * shape->page_tokens)
+        return fail(QWFN_ERANGE, "%s: pos0 + n_tokens = %lld > capacity %lld", what, (long long)end,
+                    (long long)view->pages_per_seq * shape->page_tokens);
+    const hipError_t e = launch_kv_rows(g, *view, to_rows, seq, pos0, n_tokens, const_cast<void *>(k_rows),
+                                        const_cast<void *>(v_rows), (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, what);
+}
+
+int qwfn_kv_export_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, int32_t seq, int32_t pos0,
+                        int32_t n_tokens, void *k_rows, void *v_rows, void *stream) {
+    return kv_rows("kv_export", true, shape, view, seq, pos0, n_tokens, k_rows, v_rows, stream);
+}
+
+int qwfn_kv_import_q8_0(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, int32_t seq, int32_t pos0,
+                        int32_t n_tokens, const void *k_rows, const void *v_rows, void *stream) {
+    return kv_rows("kv_import", false, shape, view, seq, pos0, n_tokens, k_rows, v_rows, stream);
+}
+
 int qwfn_pool_update(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const int32_t *seq_ids,
                      const int32_t *block_ids, int32_t n_blocks, void *stream) {
     Geo g;

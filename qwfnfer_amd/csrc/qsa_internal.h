@@ -86,6 +86,10 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,
                             float *out, const Ws &ws, hipStream_t st);
+// Positions pos0 .. pos0+n-1 of sequence seq between the paged layout and the
+// reference's token-major block_q8_0 rows (to_rows: export; else import).
+hipError_t launch_kv_rows(const Geo &g, const qwfn_kv_view &v, bool to_rows, int32_t seq, int32_t pos0,
+                          int32_t n, void *k_rows, void *v_rows, hipStream_t st);
 hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len,
                          int32_t n_seq, const int32_t *sel, const int32_t *nsel,
                          int32_t max_sel, float *k_out, float *v_out, int32_t *cells,

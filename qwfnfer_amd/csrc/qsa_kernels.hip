@@ -1586,6 +1586,89 @@ static void launch_attn_q8_t(const Geo &g, const qwfn_kv_view &v, const float *q
 }
 
 // ---------------------------------------------------------------------------
+// the reference's cache rows <-> the paged layout (format interop)
+// ---------------------------------------------------------------------------
+
+// One thread per (token, KV head, q8_0 block j) of positions pos0 .. pos0+n-1
+// of sequence seq.  A row of the reference's cache is n_head_kv * head_dim / 32
+// ggml blocks {fp16 d, int8 qs[32]} of 34 bytes, head-major, so block (h, j) of
+// token t sits at row byte (h * head_dim/32 + j) * 34; rows are back to back.
+// EXPORT copies the paged bytes out into rows, otherwise rows are written into
+// the pages (an overwrite: the same bytes an append of the same values makes).
+template <bool EXPORT>
+__global__ void __launch_bounds__(256)
+k_kv_rows(Geo g, qwfn_kv_view v, int32_t seq, int32_t pos0, int32_t n, uint8_t *k_rows, uint8_t *v_rows) {
+    const int nb = g.hd / 32;
+    const int64_t per_tok = (int64_t)g.Hkv * nb;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)n * per_tok) return;
+    const int tl = (int)(i / per_tok), rem = (int)(i % per_tok);
+    const int gh = rem / nb, j = rem % nb;
+    const int t = pos0 + tl;
+    const int32_t pp = phys_page(g, v.page_table, seq, t);
+    if (pp < 0) { set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
+    const int row = t % g.pt;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        uint8_t *rows = which ? v_rows : k_rows;
+        if (!rows) continue;
+        uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
+        uint16_t *rb = reinterpret_cast<uint16_t *>(rows + i * 34);          // 2-byte aligned
+        uint16_t *sp = reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j));
+        if (!(which && g.vdim)) {                  // 16 dims of one token per 16-byte chunk
+            uint4 *c0 = reinterpret_cast<uint4 *>(page + quant_off(g, gh, row, 32 * j));
+            uint4 *c1 = reinterpret_cast<uint4 *>(page + quant_off(g, gh, row, 32 * j + 16));
+            if (EXPORT) {
+                const uint4 a = *c0, b = *c1;
+                const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                rb[0] = *sp;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    rb[1 + 2 * k] = (uint16_t)w[k];
+                    rb[2 + 2 * k] = (uint16_t)(w[k] >> 16);
+                }
+            } else {
+                uint32_t w[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) w[k] = (uint32_t)rb[1 + 2 * k] | ((uint32_t)rb[2 + 2 * k] << 16);
+                *c0 = make_uint4(w[0], w[1], w[2], w[3]);
+                *c1 = make_uint4(w[4], w[5], w[6], w[7]);
+                *sp = rb[0];
+            }
+        } else {                                   // V, dim-major tiles: one byte per dim
+            if (EXPORT) {
+                rb[0] = *sp;
+#pragma unroll
+                for (int e = 0; e < 32; e += 2)
+                    rb[1 + e / 2] = (uint16_t)(page[vquant_off(g, gh, row, 32 * j + e)] |
+                                               (page[vquant_off(g, gh, row, 32 * j + e + 1)] << 8));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 32; e += 2) {
+                    const uint16_t x = rb[1 + e / 2];
+                    page[vquant_off(g, gh, row, 32 * j + e)] = (uint8_t)x;
+                    page[vquant_off(g, gh, row, 32 * j + e + 1)] = (uint8_t)(x >> 8);
+                }
+                *sp = rb[0];
+            }
+        }
+    }
+}
+
+hipError_t launch_kv_rows(const Geo &g, const qwfn_kv_view &v, bool to_rows, int32_t seq, int32_t pos0,
+                          int32_t n, void *k_rows, void *v_rows, hipStream_t st) {
+    const int64_t threads = (int64_t)n * g.Hkv * (g.hd / 32);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (to_rows)
+        hipLaunchKernelGGL(k_kv_rows<true>, grid, dim3(256), 0, st, g, v, seq, pos0, n, (uint8_t *)k_rows,
+                           (uint8_t *)v_rows);
+    else
+        hipLaunchKernelGGL(k_kv_rows<false>, grid, dim3(256), 0, st, g, v, seq, pos0, n, (uint8_t *)k_rows,
+                           (uint8_t *)v_rows);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // gather + dequant of a selection (parity / debug entry point)
 // ---------------------------------------------------------------------------
 

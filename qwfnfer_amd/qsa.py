@@ -26,7 +26,8 @@ from ._lib import KvView, QsaShape, call
 __all__ = [
     "QsaConfig", "KvCache", "KvState", "Workspace",
     "append_q8_0", "pool_update", "pool_rebuild", "indexer_topk", "gather_dequant",
-    "sparse_decode_attn", "decode_append_select", "sparse_attn_decode", "read_status",
+    "sparse_decode_attn", "decode_append_select", "sparse_attn_decode", "sparse_attn_prefill",
+    "export_rows_q8_0", "import_rows_q8_0", "read_status",
 ]
 
 
@@ -81,6 +82,14 @@ class QsaConfig:
         out = C.c_size_t()
         s = self.shape()
         call("qwfn_qsa_workspace_bytes", C.byref(s), n_seq, max_seq_len, C.byref(out))
+        return out.value
+
+    def row_bytes(self) -> int:
+        """Bytes of one token's row in the reference's q8_0 cache tensor
+        (n_head_kv * head_dim / 32 ggml blocks of 34 bytes)."""
+        out = C.c_size_t()
+        s = self.shape()
+        call("qwfn_kv_row_bytes", C.byref(s), C.byref(out))
         return out.value
 
     def prefill_workspace_bytes(self, max_seq_len: int, q_batch: int) -> int:
@@ -274,6 +283,43 @@ def pool_rebuild(cache: KvCache, seq: int, n_whole: int, stream=None) -> None:
     (src/qwfn_graph.cpp:431-448, src/qwfn_engine.cpp:761-798)."""
     s = cache.cfg.shape()
     call("qwfn_pool_rebuild", C.byref(s), C.byref(cache.view()), seq, n_whole, _stream(stream))
+
+
+def export_rows_q8_0(cache: KvCache, seq: int, pos0: int, n_tokens: int, k: bool = True, v: bool = True,
+                     stream=None):
+    """Positions [pos0, pos0+n_tokens) of ``seq`` as the reference's cache rows:
+    uint8 [n_tokens, row_bytes] device tensors, row t = the token's ggml
+    block_q8_0 blocks, head-major (src/qwfn_state.cpp:40, 52-53).  Returns
+    (k_rows, v_rows); a side not asked for is None."""
+    cfg = cache.cfg
+    rb = cfg.row_bytes()
+    dev = cache.k_pages.device
+    kr = torch.empty((n_tokens, rb), dtype=torch.uint8, device=dev) if k else None
+    vr = torch.empty((n_tokens, rb), dtype=torch.uint8, device=dev) if v else None
+    s = cfg.shape()
+    call("qwfn_kv_export_q8_0", C.byref(s), C.byref(cache.view()), seq, pos0, n_tokens, _ptr(kr), _ptr(vr),
+         _stream(stream))
+    return kr, vr
+
+
+def import_rows_q8_0(cache: KvCache, seq: int, pos0: int, k_rows: Optional[torch.Tensor],
+                     v_rows: Optional[torch.Tensor], stream=None) -> None:
+    """Write the reference's cache rows (uint8 [n_tokens, row_bytes], device)
+    into positions [pos0, pos0+n_tokens) of ``seq``, byte for byte.  The pooled
+    keys are left alone: pool the completed blocks afterwards
+    (:func:`pool_rebuild` / :func:`pool_update`)."""
+    cfg = cache.cfg
+    rb = cfg.row_bytes()
+    ref = k_rows if k_rows is not None else v_rows
+    if ref is None:
+        raise ValueError("import_rows_q8_0: k_rows and v_rows are both None")
+    n_tokens = ref.numel() // rb
+    for t, name in ((k_rows, "k_rows"), (v_rows, "v_rows")):
+        if t is not None:
+            _need(t, name, torch.uint8, n_tokens * rb)
+    s = cfg.shape()
+    call("qwfn_kv_import_q8_0", C.byref(s), C.byref(cache.view()), seq, pos0, n_tokens, _ptr(k_rows),
+         _ptr(v_rows), _stream(stream))
 
 
 def indexer_topk(cache: KvCache, q: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int,

@@ -137,3 +137,23 @@ def test_prefill_rejects_bad_arguments_before_launch():
     assert _code("qwfn_qsa_prefill_workspace_bytes", C.byref(s), 163840, 1, C.byref(one)) == 0
     assert out.value > one.value > 0
     assert _code("qwfn_qsa_prefill_workspace_bytes", C.byref(s), 163840, 1 << 20, C.byref(out)) == _lib.QWFN_ERANGE
+
+
+def test_row_interop_rejects_bad_arguments_before_launch():
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view(pps=4)                       # capacity 1024 tokens
+    out = C.c_size_t()
+    assert _code("qwfn_kv_row_bytes", C.byref(s), C.byref(out)) == 0
+    assert out.value == 2 * 4 * 34 == cfg.row_bytes()
+    for f in ("qwfn_kv_export_q8_0", "qwfn_kv_import_q8_0"):
+        call = lambda seq=0, pos0=0, n=4, k=4096, vv=4096: _code(f, C.byref(s), C.byref(v), seq, pos0, n, k, vv,
+                                                                 None)
+        assert call(k=None, vv=None) == _lib.QWFN_EINVAL      # nothing to move
+        assert call(k=4097) == _lib.QWFN_EINVAL               # rows are 2-byte aligned
+        assert call(seq=1) == _lib.QWFN_EINVAL
+        assert call(seq=-1) == _lib.QWFN_EINVAL
+        assert call(pos0=-1) == _lib.QWFN_EINVAL
+        assert call(n=0) == _lib.QWFN_EINVAL
+        assert call(pos0=1020, n=5) == _lib.QWFN_ERANGE       # past the view's capacity
+        assert "capacity" in _lib.load().qwfn_qsa_last_error().decode()
