@@ -1725,7 +1725,8 @@ struct PfScoreShared {
 // grid (ceil((n_blk - sink) / 64), ceil(n_q / 64), Hkv), 256 threads.  The
 // workgroup scores 64 queries against 64 pooled blocks of one KV head, every
 // pooled key and query row loaded once into LDS and reused 64 times; thread t
-// owns queries 4*(t/16) .. +4 x blocks 4*(t%16) .. +4.  Each dot is formed in
+// owns queries 4*(t/16) .. +4 x blocks t%16 + {0, 16, 32, 48} (16 consecutive
+// blocks per read across a row of lanes: no LDS bank conflicts).  Each dot is formed in
 // the decode indexer's order (chain j over the dims d with (d/4)%4 == j in
 // increasing order, then (c0+c1)+(c2+c3), relu when set, heads summed in
 // order), so a query's scores are bit-identical to a decode step's at its
@@ -1747,7 +1748,7 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
         const int bb = min(b_base + b, g.bps - 1);
         sh.p[dc][b] = *reinterpret_cast<const float4 *>(P + (int64_t)bb * HD + 4 * dc);
     }
-    const int qi0 = 4 * (tid / 16), bi0 = 4 * (tid % 16);
+    const int qi0 = 4 * (tid / 16), bi0 = tid % 16;
     float score[4][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -1776,7 +1777,7 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
 #pragma unroll
                 for (int a = 0; a < 4; ++a) qv[a] = sh.q[dc][qi0 + a];
 #pragma unroll
-                for (int b = 0; b < 4; ++b) pv[b] = sh.p[dc][bi0 + b];
+                for (int b = 0; b < 4; ++b) pv[b] = sh.p[dc][bi0 + 16 * b];
 #pragma unroll
                 for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -1806,7 +1807,7 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
         float *row = scores + ((int64_t)qn * g.Hkv + gh) * nb_cap;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const int blk = b_base + bi0 + b;
+            const int blk = b_base + bi0 + 16 * b;
             if (blk < n_blk) row[blk] = score[a][b];
         }
     }
