@@ -1941,33 +1941,35 @@ __device__ __forceinline__ void lds_dma16(const void *gsrc, uint32_t lds) {
 }
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int HD>
+template <int HD, int G>
 struct PfAttnCfg {
-    static constexpr int WAVES = HD >= 256 ? 2 : 4;      // per workgroup, bounded by LDS
     static constexpr int NK4 = HD / 16;                   // 1 KB transfers per K (or V) tile
     static constexpr int NS4 = HD / 4;                    // 16-byte chunks of one tile's scale rows
     static constexpr int SCI = (2 * NS4 + 63) / 64;       // 1 KB transfers for both scale rows
     static constexpr int KOFF = 0, VOFF = HD * 64, SOFF = 2 * HD * 64;   // byte offsets in a buffer
     static constexpr int BUF16 = (2 * HD * 64 + 64 * SCI * 16) / 16;      // 16-byte chunks per buffer
+    static constexpr int PER_WAVE = BUF16 * 16 + G * (64 + 4) * 4;        // LDS bytes per wave
+    static constexpr int WAVES = 160 * 1024 / PER_WAVE >= 8 ? 8 : 160 * 1024 / PER_WAVE;   // per CU
 };
 
-// A wave's LDS: two tile buffers (K tile as in memory; V tile with each 64-byte
+// A wave's LDS: the tile buffer (K tile as in memory; V tile with each 64-byte
 // dim row's four 16-byte quarters rotated by (dim / 4) % 4, so the PV operand
 // reads of 16 dims are bank-conflict free; the K then V scale rows) and the
-// softmax weights.
-template <int HD>
+// softmax weights of the group's heads.
+template <int HD, int G>
 struct PfAttnLds {
-    u4v buf[2][PfAttnCfg<HD>::BUF16];
-    float p[16][64 + 4];
+    u4v buf[PfAttnCfg<HD, G>::BUF16];
+    float p[G][64 + 4];
 };
 
 // grid ceil(n_q * Hkv / WAVES), WAVES waves; wave w owns (query s, KV head gh)
 // = pair blockIdx.x*WAVES + w and walks its selected 64-cell tiles with an
-// online softmax.  The tiles are double-buffered in the wave's own LDS: while
-// tile t is computed from one buffer, tile t+1's K, V and scale bytes (17 KB at
-// hd 128, coalesced 16-byte global -> LDS transfers that hold no registers)
-// land in the other, so one wave per SIMD hides the memory latency.  Every
-// contraction runs on
+// online softmax.  A tile's K, V and scale bytes (17 KB at hd 128) reach the
+// wave's LDS buffer by coalesced 16-byte global -> LDS transfers that hold no
+// registers; the next tile's transfer goes out as soon as the current tile's
+// operands are in registers, and the other wave of the SIMD (two per SIMD:
+// 19.6 KB of LDS per wave at hd 128) computes meanwhile.  Every contraction
+// runs on
 // v_mfma_f32_16x16x32_f16 (one output column per query head, up to 16):
 //  - QK: S[cell][head] = sum_j dk(cell, j) * (K_j[cell][:] . q_j[:, head]) per
 //    32-dim q8_0 block j, the int8 keys exact in fp16 and the query row (scaled
@@ -1979,17 +1981,17 @@ struct PfAttnLds {
 //    current tile's units and rescaled with the softmax).
 // Cells past the query's position have weight 0 and their V scale masked.
 template <int HD, int G>
-__global__ void __launch_bounds__(PfAttnCfg<HD>::WAVES * 64)
+__global__ void __launch_bounds__((PfAttnCfg<HD, G>::WAVES * 64))
 k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const int32_t *__restrict__ sel,
           const int32_t *__restrict__ nsel, int32_t max_sel, float *__restrict__ out) {
-    using C = PfAttnCfg<HD>;
+    using C = PfAttnCfg<HD, G>;
     constexpr int NJ = HD / 32, ND = HD / 16, NK4 = C::NK4, NS4 = C::NS4;
     static_assert(G <= 16, "one MFMA output column per query head");
-    __shared__ PfAttnLds<HD> shw[C::WAVES];
+    __shared__ PfAttnLds<HD, G> shw[C::WAVES];
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int pair = (int)blockIdx.x * C::WAVES + wv;
     if (pair >= n_q * g.Hkv) return;                 // a whole wave; no workgroup barrier follows
-    PfAttnLds<HD> &W = shw[wv];
+    PfAttnLds<HD, G> &W = shw[wv];
     const int s = pair / g.Hkv, gh = pair - s * g.Hkv;
     const int L = g.pf_pos0 + s + 1;
     const int hn = l & 15, lg = l >> 4;              // MFMA column (head) and k-group of this lane
@@ -2059,15 +2061,15 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
             }
         }
         const int t_end = min(n_tiles - tc, 64);
-        // tile ti -> buffer bi: K chunks as in memory, V chunks rotated, scale rows
-        auto issue = [&](int ti, int bi) {
+        // tile ti -> the buffer: K chunks as in memory, V chunks rotated, scale rows
+        auto issue = [&](int ti) {
             const int pg = __builtin_amdgcn_readlane(pg_l, ti);
             const int row0 = __builtin_amdgcn_readlane(r0_l, ti);
             const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
             const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
             const int tl = gh * (g.pt / 64) + row0 / 64;
             const uint32_t base = __builtin_amdgcn_readfirstlane(
-                (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&W.buf[bi][0]);
+                (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&W.buf[0]);
             const uint8_t *ksrc = kp + (int64_t)tl * (HD / 16) * 1024 + 16 * l;
             const uint8_t *vsrc = vp + (int64_t)tl * HD * 64 + (l >> 2) * 64 + (((l & 3) ^ ((l >> 4) & 3)) << 4);
 #pragma unroll
@@ -2082,16 +2084,19 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 if (r < 2 * NS4) lds_dma16(r < NS4 ? kss + 16 * r : vss + 16 * (r - NS4), base + C::SOFF + c * 1024);
             }
         };
-        issue(0, 0);
+        issue(0);
         for (int ti = 0; ti < t_end; ++ti) {
             const int nv = __builtin_amdgcn_readlane(nv_l, ti);
-            wait_vmem_all();                         // tile ti has landed in buffer ti & 1
-            if (ti + 1 < t_end) issue(ti + 1, (ti + 1) & 1);
+            wait_vmem_all();                         // tile ti has landed in the buffer
+            // PV operands, read out of LDS before the next tile's transfer
+            uint2 vwr[2][NJ][2];
+            float pcr[2][8];
+            u4v dvw_pv[2][NJ];
             if (nv > 0) {                            // uniform over the wave
-                const uint8_t *wk = reinterpret_cast<const uint8_t *>(&W.buf[ti & 1][0]) + C::KOFF;
-                const uint8_t *wvb = reinterpret_cast<const uint8_t *>(&W.buf[ti & 1][0]) + C::VOFF;
+                const uint8_t *wk = reinterpret_cast<const uint8_t *>(&W.buf[0]) + C::KOFF;
+                const uint8_t *wvb = reinterpret_cast<const uint8_t *>(&W.buf[0]) + C::VOFF;
                 // cell c's NJ fp16 scales: halfs c*NJ .. c*NJ+NJ of the K (V) scale row
-                const u4v *wks = reinterpret_cast<const u4v *>(reinterpret_cast<const uint8_t *>(&W.buf[ti & 1][0]) + C::SOFF);
+                const u4v *wks = reinterpret_cast<const u4v *>(reinterpret_cast<const uint8_t *>(&W.buf[0]) + C::SOFF);
                 const u4v *wvs = wks + NS4;
                 // ---- QK
                 float sv[4][4];
@@ -2156,7 +2161,7 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                     for (int i = 0; i < 4; ++i) {
                         const float p = __builtin_amdgcn_exp2f(sv[mb][i] - m_new);
                         tsum += p;
-                        W.p[hn][16 * mb + 4 * lg + i] = p;
+                        if (hv) W.p[hn][16 * mb + 4 * lg + i] = p;
                     }
                 tsum = col_sum4(tsum);
                 lsum = lsum * alpha + tsum;
@@ -2182,30 +2187,52 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                     for (int d = 0; d < ND; ++d) o[d] *= rs;
                 }
                 wave_lds_sync();
+                // ---- PV operands: the weights of head hn and the V quants this lane feeds
+                {
+                    const int hq = min(hn, G - 1);
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const float4 p0 = *reinterpret_cast<const float4 *>(&W.p[hq][32 * ks + 8 * lg]);
+                        const float4 p1 = *reinterpret_cast<const float4 *>(&W.p[hq][32 * ks + 8 * lg + 4]);
+                        const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) pcr[ks][i] = hv ? pc[i] * up : 0.0f;
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                            for (int db = 0; db < 2; ++db)
+                                vwr[ks][j][db] = *reinterpret_cast<const uint2 *>(
+                                    wvb + (16 * (2 * j + db) + hn) * 64 + (((2 * ks + (lg >> 1)) ^ (hn >> 2)) << 4) +
+                                    8 * (lg & 1));
+                    }
+                }
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int w = 0; w < NJ; ++w) dvw_pv[ks][w] = dvw[ks][w];
+            }
+            // every LDS read of the tile has returned: the next tile may land
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (ti + 1 < t_end) issue(ti + 1);
+            if (nv > 0) {
                 // ---- PV
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const float4 p0 = *reinterpret_cast<const float4 *>(&W.p[hn][32 * ks + 8 * lg]);
-                    const float4 p1 = *reinterpret_cast<const float4 *>(&W.p[hn][32 * ks + 8 * lg + 4]);
-                    const float pc[8] = {p0.x * up, p0.y * up, p0.z * up, p0.w * up,
-                                         p1.x * up, p1.y * up, p1.z * up, p1.w * up};
 #pragma unroll
                     for (int j = 0; j < NJ; ++j) {
                         h8v bh, bl;
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
-                            const h8v dw = __builtin_bit_cast(h8v, dvw[ks][(i * NJ + j) / 8]);
+                            const h8v dw = __builtin_bit_cast(h8v, dvw_pv[ks][(i * NJ + j) / 8]);
                             const float dv = (float)dw[(i * NJ + j) % 8];
-                            const _Float16 hi = (_Float16)__builtin_fmaf(pc[i], dv, 0.0f);
+                            const _Float16 hi = (_Float16)__builtin_fmaf(pcr[ks][i], dv, 0.0f);
                             bh[i] = hi;
-                            bl[i] = (_Float16)__builtin_fmaf(pc[i], dv, -(float)hi);
+                            bl[i] = (_Float16)__builtin_fmaf(pcr[ks][i], dv, -(float)hi);
                         }
 #pragma unroll
                         for (int db = 0; db < 2; ++db) {
                             const int dblk = 2 * j + db;
-                            const uint2 vw = *reinterpret_cast<const uint2 *>(
-                                wvb + (16 * dblk + hn) * 64 + (((2 * ks + (lg >> 1)) ^ (hn >> 2)) << 4) + 8 * (lg & 1));
-                            const h8v vh = q8x8_to_h8(vw);
+                            const h8v vh = q8x8_to_h8(vwr[ks][j][db]);
                             o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
                             o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
                         }
@@ -2229,7 +2256,7 @@ template <int HD, int G>
 static void launch_pf_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                              const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
                              hipStream_t st) {
-    constexpr int WAVES = PfAttnCfg<HD>::WAVES;
+    constexpr int WAVES = PfAttnCfg<HD, G>::WAVES;
     const int pairs = n_q * g.Hkv;
     hipLaunchKernelGGL((k_pf_attn<HD, G>), dim3((unsigned)((pairs + WAVES - 1) / WAVES)), dim3(WAVES * 64), 0, st, g,
                        v, q, n_q, sel, nsel, max_sel, out);
