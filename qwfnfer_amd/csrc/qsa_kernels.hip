@@ -2061,21 +2061,24 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
             }
         }
         const int t_end = min(n_tiles - tc, 64);
-        // tile ti -> the buffer: K chunks as in memory, V chunks rotated, scale rows
-        auto issue = [&](int ti) {
+        // tile ti -> the buffer, in two parts: the K chunks (as in memory) with
+        // both scale rows, read by QK; the V chunks (rotated), read by PV
+        const uint32_t base = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&W.buf[0]);
+        auto tile_src = [&](int ti, const uint8_t *&kp, const uint8_t *&vp, int &tl, int &row0) {
             const int pg = __builtin_amdgcn_readlane(pg_l, ti);
-            const int row0 = __builtin_amdgcn_readlane(r0_l, ti);
-            const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
-            const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
-            const int tl = gh * (g.pt / 64) + row0 / 64;
-            const uint32_t base = __builtin_amdgcn_readfirstlane(
-                (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)&W.buf[0]);
+            row0 = __builtin_amdgcn_readlane(r0_l, ti);
+            kp = (const uint8_t *)v.k_pages + (int64_t)pg * g.page_bytes;
+            vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
+            tl = gh * (g.pt / 64) + row0 / 64;
+        };
+        auto issue_k = [&](int ti) {
+            const uint8_t *kp, *vp;
+            int tl, row0;
+            tile_src(ti, kp, vp, tl, row0);
             const uint8_t *ksrc = kp + (int64_t)tl * (HD / 16) * 1024 + 16 * l;
-            const uint8_t *vsrc = vp + (int64_t)tl * HD * 64 + (l >> 2) * 64 + (((l & 3) ^ ((l >> 4) & 3)) << 4);
 #pragma unroll
             for (int i = 0; i < NK4; ++i) lds_dma16(ksrc + i * 1024, base + C::KOFF + i * 1024);
-#pragma unroll
-            for (int i = 0; i < NK4; ++i) lds_dma16(vsrc + i * 1024, base + C::VOFF + i * 1024);
             const uint8_t *kss = kp + scale_off(g, gh, row0, 0);
             const uint8_t *vss = vp + scale_off(g, gh, row0, 0);
 #pragma unroll
@@ -2084,7 +2087,16 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 if (r < 2 * NS4) lds_dma16(r < NS4 ? kss + 16 * r : vss + 16 * (r - NS4), base + C::SOFF + c * 1024);
             }
         };
-        issue(0);
+        auto issue_v = [&](int ti) {
+            const uint8_t *kp, *vp;
+            int tl, row0;
+            tile_src(ti, kp, vp, tl, row0);
+            const uint8_t *vsrc = vp + (int64_t)tl * HD * 64 + (l >> 2) * 64 + (((l & 3) ^ ((l >> 4) & 3)) << 4);
+#pragma unroll
+            for (int i = 0; i < NK4; ++i) lds_dma16(vsrc + i * 1024, base + C::VOFF + i * 1024);
+        };
+        issue_k(0);
+        issue_v(0);
         for (int ti = 0; ti < t_end; ++ti) {
             const int nv = __builtin_amdgcn_readlane(nv_l, ti);
             wait_vmem_all();                         // tile ti has landed in the buffer
@@ -2130,6 +2142,9 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                     for (int w = 0; w < NJ; ++w) dvw[ks][w] = wvs[(32 * ks + 8 * lg) * NJ / 8 + w];
+                // the K chunks and scale rows are consumed: the next tile's may land
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (ti + 1 < t_end) issue_k(ti + 1);
                 if (nv < 64) {                       // a partial tile: cells past the query carry no data
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb)
@@ -2211,9 +2226,12 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
 #pragma unroll
                     for (int w = 0; w < NJ; ++w) dvw_pv[ks][w] = dvw[ks][w];
             }
-            // every LDS read of the tile has returned: the next tile may land
+            // every LDS read of the tile has returned: the next tile's V may land
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (ti + 1 < t_end) issue(ti + 1);
+            if (ti + 1 < t_end) {
+                if (nv <= 0) issue_k(ti + 1);        // (a skipped tile issued no K part above)
+                issue_v(ti + 1);
+            }
             if (nv > 0) {
                 // ---- PV
 #pragma unroll
