@@ -94,7 +94,9 @@ typedef struct qwfn_qsa_shape {
     int32_t sink_blocks;     /* leading blocks always kept (1)                 */
     int32_t local_tokens;    /* trailing tokens whose blocks are kept (512)    */
     int32_t relu_per_head;   /* 1: score = sum_h relu(q_h.p) (lightning idx)   */
-    int32_t shared_selection;/* 1: one selection for all KV heads (not built)  */
+    int32_t shared_selection;/* 1: one selection for all KV heads, on their
+                              * scores summed in head order (the checkpoint's
+                              * rule, src/qwfn_graph.cpp:477-495)            */
     int32_t quant_variant;   /* QWFN_Q8_X86_RNE or QWFN_Q8_REF_ROUNDF          */
 } qwfn_qsa_shape;
 

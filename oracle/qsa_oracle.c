@@ -368,6 +368,7 @@ int qwfn_oracle_indexer_topk(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
     const int64_t bps = blocks_per_seq(s, v);
     int32_t status = 0;
     float *scores = (float *)malloc(sizeof(float) * (size_t)(bps > 0 ? bps : 1));
+    float *sum = (float *)malloc(sizeof(float) * (size_t)(bps > 0 ? bps : 1));
     for (int32_t seq = 0; seq < n_seq; seq++) {
         const int32_t L = seq_len[seq];
         for (int32_t g = 0; g < H; g++) {
@@ -384,13 +385,25 @@ int qwfn_oracle_indexer_topk(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                 const float *pb = v->pooled + ((int64_t)seq * H + g) * bps * hd;
                 for (int32_t b = e_lo; b < e_hi; b++)
                     scores[b] = qwfn_oracle_block_score(s, qg, pb + (int64_t)b * hd);
+                /* shared selection: the heads' scores summed in head order */
+                if (s->shared_selection)
+                    for (int32_t b = e_lo; b < e_hi; b++) sum[b] = g == 0 ? scores[b] : sum[b] + scores[b];
             }
-            const int32_t r = qwfn_oracle_select(s, scores, L, sel + ((int64_t)seq * H + g) * max_sel, max_sel);
-            if (r < 0) { free(scores); return r; }
+            if (s->shared_selection && g < H - 1) continue;   /* select once, after the last head */
+            const int32_t r = qwfn_oracle_select(s, s->shared_selection ? sum : scores, L,
+                                                 sel + ((int64_t)seq * H + g) * max_sel, max_sel);
+            if (r < 0) { free(scores); free(sum); return r; }
             *ns = r;
+            if (s->shared_selection)                          /* the same selection for every head */
+                for (int32_t h = 0; h < H - 1; h++) {
+                    memcpy(sel + ((int64_t)seq * H + h) * max_sel, sel + ((int64_t)seq * H + g) * max_sel,
+                           sizeof(int32_t) * (size_t)r);
+                    n_sel[(int64_t)seq * H + h] = r;
+                }
         }
     }
     free(scores);
+    free(sum);
     return status;
 }
 
@@ -518,7 +531,11 @@ int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
         if ((p + 1) % bt == 0) qwfn_oracle_pool_block(s, v, seq, p / bt);
     }
     float *scores = (float *)malloc(sizeof(float) * (size_t)(bps > 0 ? bps : 1));
-    for (int32_t seq = 0; seq < n_seq; seq++)
+    if (s->shared_selection) {                    /* the general (serial) indexer handles the sum */
+        const int rc = qwfn_oracle_indexer_topk(s, v, q, seq_len, n_seq, sel, n_sel, max_sel);
+        if (rc < 0) { free(scores); return rc; }
+    }
+    for (int32_t seq = 0; seq < n_seq && !s->shared_selection; seq++)
         for (int32_t g = 0; g < H; g++) {
             const int32_t L = seq_len[seq];
             int32_t b_last, fw, e_lo, e_hi;

@@ -60,8 +60,6 @@ int check_shape(const qwfn_qsa_shape *s) {
         return fail(QWFN_EINVAL, "quant_variant %d unknown", s->quant_variant);
     if ((s->relu_per_head | s->shared_selection) & ~1)
         return fail(QWFN_EINVAL, "relu_per_head / shared_selection are 0 or 1");
-    if (s->shared_selection)
-        return fail(QWFN_ENOTSUP, "shared_selection (one selection for all KV heads) has no kernel in this build");
     const int G = s->n_head / s->n_head_kv;
     if (!kernels_for(s->head_dim, G))
         return fail(QWFN_ENOTSUP, "no kernel instantiation for head_dim %d, group %d", s->head_dim, G);
@@ -91,7 +89,7 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->bt = s->block_tokens; g->pt = s->page_tokens;
     g->topk = s->top_k_blocks > 0 ? s->top_k_blocks : 0;
     g->sink = s->sink_blocks; g->local = s->local_tokens;
-    g->relu = s->relu_per_head; g->variant = s->quant_variant;
+    g->relu = s->relu_per_head; g->variant = s->quant_variant; g->shared = s->shared_selection;
     g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * s->head_dim;
     g->page_bytes = g->qbytes + (int64_t)s->n_head_kv * s->page_tokens * (s->head_dim / 32) * 2;
     g->inv_bt = 1.0f / (float)s->block_tokens;

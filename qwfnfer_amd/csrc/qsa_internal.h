@@ -17,6 +17,7 @@ struct Geo {
     int32_t bt, pt;                  // block tokens, page tokens
     int32_t topk, sink, local;       // selection
     int32_t relu, variant;           // indexer relu, q8_0 rounding
+    int32_t shared;                  // one selection for all KV heads (scores summed in head order)
     int32_t pps, n_phys, n_seq_view; // pages per sequence, pool pages, view seqs
     int32_t bps;                     // pooled blocks per sequence
     int32_t vdim;                    // V quants dim-major per 64-token tile (bt % 64 == 0)

@@ -771,6 +771,39 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
     if (tid == 0) *nout = g.sink + g.topk + nwin;
 }
 
+// Shared selection (shared_selection = 1): one selection for every KV head of
+// a sequence, on the sum of the heads' block scores taken in head order
+// (score = sum over all query heads of their -- relu'd when set -- dots, each
+// KV head's group summed first).  Called by the one workgroup that saw every
+// head's scores: it sums the rows into row 0 (device-coherent loads of the
+// other workgroups' stores), selects on it and copies the selection, and its
+// count, to every head's row.
+__device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t sc_stride, int L, int32_t *out0,
+                                              int64_t out_stride, int32_t *nout0, IdxShared &sh) {
+    const int tid = threadIdx.x;
+    const Ranges r = qsa_ranges(g, L);
+    const BufRsrc rs = buf_rsrc(sc0, (uint32_t)(((int64_t)(g.Hkv - 1) * sc_stride + r.e_hi) * 4));
+    for (int b = r.e_lo + tid; b < r.e_hi; b += kIdxThreads) {
+        float acc = BufLoad<1, kCpolSc1>::at(rs, b * 4, 0)[0];
+        for (int h = 1; h < g.Hkv; ++h) acc += BufLoad<1, kCpolSc1>::at(rs, (int)((h * sc_stride + b) * 4), 0)[0];
+        sc0[b] = acc;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the summed row, for the selection's loads
+    __syncthreads();
+    select_blocks(g, sc0, L, out0, nout0, sh);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the selection, for the copy below
+    __syncthreads();
+    const BufRsrc ro = buf_rsrc(out0, (uint32_t)out_stride * 4u);
+    const BufRsrc rn = buf_rsrc(nout0, 4u);
+    const int n = __builtin_bit_cast(int, BufLoad<1, kCpolSc1>::at(rn, 0, 0)[0]);
+    for (int i = tid; i < n; i += kIdxThreads) {
+        const int32_t x = __builtin_bit_cast(int32_t, BufLoad<1, kCpolSc1>::at(ro, i * 4, 0)[0]);
+        for (int h = 1; h < g.Hkv; ++h) out0[h * out_stride + i] = x;
+    }
+    if (tid == 0)
+        for (int h = 1; h < g.Hkv; ++h) nout0[h] = n;
+}
+
 // grid (n_chunks [+1 with the fused append], Hkv, n_seq)
 template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
@@ -839,16 +872,25 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
             __syncthreads();                       // q reads done before the union is reused
         }
     }
-    // completion count: the last workgroup of this (sequence, KV head) selects
-    // the selection reads the scores with device-coherent loads (or fences)
-    if (!arrive_last<false>(&ws.cnt_idx[pair], n_chunks, &sh.flag)) return;
-    if (tid == 0) ws.cnt_idx[pair] = 0;
+    // completion count: the last workgroup of this (sequence, KV head) -- of
+    // this sequence with a shared selection -- selects; the selection reads
+    // the scores with device-coherent loads (or fences)
+    const int cpair = g.shared ? s * g.Hkv : pair;
+    if (!arrive_last<false>(&ws.cnt_idx[cpair], g.shared ? n_chunks * g.Hkv : n_chunks, &sh.flag)) return;
+    if (tid == 0) ws.cnt_idx[cpair] = 0;
     int32_t *out = sel + (int64_t)pair * max_sel;
     if (!ok) {
-        if (tid == 0) { nsel[pair] = 0; if (gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE); }
+        if (tid == 0) {
+            for (int h = g.shared ? 0 : gh; h <= (g.shared ? g.Hkv - 1 : gh); ++h) nsel[s * g.Hkv + h] = 0;
+            set_status(v.status, QWFN_STATUS_LEN_RANGE);
+        }
         return;
     }
-    select_blocks(g, sc, L, out, nsel + pair, sh);
+    if (g.shared)
+        select_shared(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L, sel + (int64_t)s * g.Hkv * max_sel,
+                      max_sel, nsel + s * g.Hkv, sh);
+    else
+        select_blocks(g, sc, L, out, nsel + pair, sh);
 }
 
 template <int HD, int G>
@@ -1816,12 +1858,16 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
 // grid (Hkv, n_q), kIdxThreads: query s's selection at its length pf_pos0+s+1
 // from the scores k_pf_scores wrote (the decode selection, same rule).
 __global__ void __launch_bounds__(kIdxThreads)
-k_pf_select(Geo g, const float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, int32_t max_sel) {
+k_pf_select(Geo g, float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, int32_t max_sel) {
     __shared__ IdxShared sh;
-    const int gh = blockIdx.x, s = blockIdx.y;
+    const int gh = blockIdx.x, s = blockIdx.y;             // (gh = 0 with a shared selection)
     const int pair = s * g.Hkv + gh;
-    select_blocks(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
-                  nsel + pair, sh);
+    if (g.shared)
+        select_shared(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
+                      max_sel, nsel + pair, sh);
+    else
+        select_blocks(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
+                      nsel + pair, sh);
 }
 
 template <int HD, int G>
@@ -1835,8 +1881,8 @@ static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *
         hipLaunchKernelGGL((k_pf_scores<HD, G>), grid, dim3(256), 0, st, g, v, q, n_q, n_blk, ws.scores,
                            ws.nb_cap);
     }
-    hipLaunchKernelGGL(k_pf_select, dim3((unsigned)g.Hkv, (unsigned)n_q), dim3(kIdxThreads), 0, st, g,
-                       ws.scores, ws.nb_cap, sel, nsel, max_sel);
+    hipLaunchKernelGGL(k_pf_select, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_q), dim3(kIdxThreads), 0, st,
+                       g, ws.scores, ws.nb_cap, sel, nsel, max_sel);
 }
 
 // ---------------------------------------------------------------------------

@@ -46,7 +46,9 @@ def test_shape_validation():
         assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_EINVAL, kw
         assert _lib.load().qwfn_qsa_last_error()
     s = QsaConfig(**{**ok.__dict__, "shared_selection": 1}).shape()
-    assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_ENOTSUP
+    assert _code("qwfn_qsa_check_shape", C.byref(s)) == 0          # one selection for all KV heads
+    s = QsaConfig(**{**ok.__dict__, "shared_selection": 2}).shape()
+    assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_EINVAL
     s = QsaConfig(**{**ok.__dict__, "n_head": 6, "n_head_kv": 2, "head_dim": 96}).shape()
     assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_ENOTSUP
 

@@ -269,6 +269,16 @@ def test_decode_steps_batched_paged():
     _decode_steps(BASELINE, [5000, 700, 12345, 64 * 9 - 1], steps=6, seed=310, dtype=np.float16)
 
 
+@pytest.mark.parametrize("relu", [0, 1])
+def test_decode_steps_shared_selection(relu):
+    # one selection for both KV heads on the heads' summed scores (the
+    # checkpoint's selection rule); the oracle copies it to every head
+    cfg = Cfg(shared_selection=1, relu_per_head=relu)
+    _decode_steps(cfg, [5000, 64 * 40 - 2], steps=4, seed=340 + relu)
+    _decode_steps(Cfg(**{**TINY.__dict__, "shared_selection": 1, "relu_per_head": relu}), [130], steps=5,
+                  seed=342 + relu)
+
+
 def test_decode_steps_tiny_and_checkpoint_shapes():
     _decode_steps(TINY, [61, 130], steps=10, seed=320)
     _decode_steps(G12, [250], steps=6, seed=321)
@@ -365,3 +375,8 @@ def test_prefill_rows_already_in_place():
 def test_prefill_other_shapes():
     _prefill_case(TINY, 90, 70, seed=640)            # 4-token blocks: the general attention kernel
     _prefill_case(G12, 200, 40, seed=641)
+
+
+def test_prefill_shared_selection():
+    _prefill_case(Cfg(shared_selection=1), 6000, 96, seed=650)
+    _prefill_case(Cfg(**{**TINY.__dict__, "shared_selection": 1, "relu_per_head": 1}), 90, 70, seed=651)
