@@ -54,8 +54,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
-    ap.add_argument("--prefill-batch", type=int, default=1024,
-                    help="queries per launch pair of the prefill chunk (sizes its workspace)")
+    ap.add_argument("--prefill-batch", type=int, default=8192,
+                    help="queries per batch of the prefill chunk (sizes its workspace; 8192 = the whole "
+                         "chunk in one batch, ~170 MB)")
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="first copy BYTES device-to-device 3 times (a plain copy kernel of known size, "

@@ -33,6 +33,7 @@ struct Geo {
 // The counter region sits at a fixed offset with a fixed capacity so every
 // call layout agrees on it; all other regions are per-call scratch.
 constexpr int32_t kMaxCounters = 4096;   // (sequence, KV head) pairs per call
+constexpr int32_t kPrefillBatchMax = 32768;   // queries per prefill batch (one grid dimension)
 struct Ws {
     int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
     int32_t *cnt_attn;   // [kMaxCounters] attention completion counters
