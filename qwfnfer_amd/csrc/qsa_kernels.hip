@@ -1756,31 +1756,36 @@ hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq
 // prefill: scores of a chunk's queries, then one selection per (query, KV head)
 // ---------------------------------------------------------------------------
 
-constexpr int kPfQ = 64, kPfB = 64;      // queries x blocks per scoring workgroup
+constexpr int kPfQA = 8;                   // queries per thread
+constexpr int kPfQ = 16 * kPfQA, kPfB = 64;  // queries x blocks per scoring workgroup
+constexpr int kPfSD = 16;                  // 16-byte dim chunks of the query rows per LDS stage
 
 template <int HD>
 struct PfScoreShared {
-    float4 p[HD / 4][kPfB];              // the tile's pooled keys, dim-chunk major
-    float4 q[HD / 4][kPfQ];              // the current head's query rows, dim-chunk major
+    float4 p[HD / 4][kPfB];                // the tile's pooled keys, dim-chunk major
+    float4 q[kPfSD][kPfQ];                 // a 64-dim stage of the current head's query rows
 };
 
-// grid (ceil((n_blk - sink) / 64), ceil(n_q / 64), Hkv), 256 threads.  The
-// workgroup scores 64 queries against 64 pooled blocks of one KV head, every
-// pooled key and query row loaded once into LDS and reused 64 times; thread t
-// owns queries 4*(t/16) .. +4 x blocks t%16 + {0, 16, 32, 48} (16 consecutive
-// blocks per read across a row of lanes: no LDS bank conflicts).  Each dot is formed in
-// the decode indexer's order (chain j over the dims d with (d/4)%4 == j in
-// increasing order, then (c0+c1)+(c2+c3), relu when set, heads summed in
-// order), so a query's scores are bit-identical to a decode step's at its
-// length.  Scores go to scores[(query * Hkv + gh) * nb_cap + block] for
-// blocks sink .. n_blk-1.
+// grid (ceil((n_blk - sink) / 64), ceil(n_q / 128), Hkv), 256 threads.  The
+// workgroup scores 128 queries against 64 pooled blocks of one KV head: the
+// pooled keys are loaded once into LDS (reused 128 times), the query rows
+// 64 dims at a time (reused 64 times); thread t owns queries 8*(t/16) .. +8 x
+// blocks t%16 + {0, 16, 32, 48} (16 consecutive blocks per read across a row
+// of lanes: no LDS bank conflicts), so each pooled-key read feeds 32 FMAs.
+// Each dot is formed in the decode indexer's order (chain j over the dims d
+// with (d/4)%4 == j in increasing order, then (c0+c1)+(c2+c3), relu when set,
+// heads summed in order), so a query's scores are bit-identical to a decode
+// step's at its length.  Scores go to scores[(query * Hkv + gh) * nb_cap +
+// block] for blocks sink .. n_blk-1.
 template <int HD, int G>
 __global__ void __launch_bounds__(256)
 k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int32_t n_blk,
             float *__restrict__ scores, int32_t nb_cap) {
 #pragma clang fp contract(off)
     __shared__ PfScoreShared<HD> sh;
-    constexpr int NDC = HD / 4;
+    constexpr int NDC = HD / 4, QA = kPfQA;
+    constexpr int SD = NDC < kPfSD ? NDC : kPfSD;          // dim chunks per stage
+    static_assert(NDC % SD == 0 && SD % 4 == 0, "whole stages of whole 16-dim groups");
     const int tid = threadIdx.x, gh = blockIdx.z;
     const int b_base = g.sink + (int)blockIdx.x * kPfB;
     const int q_base = (int)blockIdx.y * kPfQ;
@@ -1790,51 +1795,54 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
         const int bb = min(b_base + b, g.bps - 1);
         sh.p[dc][b] = *reinterpret_cast<const float4 *>(P + (int64_t)bb * HD + 4 * dc);
     }
-    const int qi0 = 4 * (tid / 16), bi0 = tid % 16;
-    float score[4][4];
+    const int qi0 = QA * (tid / 16), bi0 = tid % 16;
+    float score[QA][4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < QA; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) score[a][b] = 0.0f;
     for (int h = 0; h < G; ++h) {
-        __syncthreads();                             // the previous head's rows are consumed
-        for (int i = tid; i < kPfQ * NDC; i += 256) {
-            const int qq = i / NDC, dc = i % NDC;
-            const int qn = min(q_base + qq, n_q - 1);
-            sh.q[dc][qq] = *reinterpret_cast<const float4 *>(q + ((int64_t)qn * g.H + gh * G + h) * HD + 4 * dc);
-        }
-        __syncthreads();
-        float c[4][4][4];                            // [query][block][chain]
+        float c[QA][4][4];                           // [query][block][chain]
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < QA; ++a)
 #pragma unroll
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) c[a][b][j] = 0.0f;
-        for (int d16 = 0; d16 < HD / 16; ++d16) {
+        for (int st = 0; st < NDC; st += SD) {
+            __syncthreads();                         // the previous stage's rows are consumed
+            for (int i = tid; i < kPfQ * SD; i += 256) {
+                const int qq = i / SD, dc = i % SD;
+                const int qn = min(q_base + qq, n_q - 1);
+                sh.q[dc][qq] =
+                    *reinterpret_cast<const float4 *>(q + ((int64_t)qn * g.H + gh * G + h) * HD + 4 * (st + dc));
+            }
+            __syncthreads();
+            for (int d16 = 0; d16 < SD / 4; ++d16) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {            // dims 16*d16 + 4j .. +3 belong to chain j
-                const int dc = 4 * d16 + j;
-                float4 qv[4], pv[4];
+                for (int j = 0; j < 4; ++j) {        // dims 16*d16 + 4j .. +3 belong to chain j
+                    const int dcl = 4 * d16 + j;
+                    float4 qv[QA], pv[4];
 #pragma unroll
-                for (int a = 0; a < 4; ++a) qv[a] = sh.q[dc][qi0 + a];
+                    for (int a = 0; a < QA; ++a) qv[a] = sh.q[dcl][qi0 + a];
 #pragma unroll
-                for (int b = 0; b < 4; ++b) pv[b] = sh.p[dc][bi0 + 16 * b];
+                    for (int b = 0; b < 4; ++b) pv[b] = sh.p[st + dcl][bi0 + 16 * b];
 #pragma unroll
-                for (int a = 0; a < 4; ++a)
+                    for (int a = 0; a < QA; ++a)
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        float x = c[a][b][j];
-                        x = fmaf(qv[a].x, pv[b].x, x);
-                        x = fmaf(qv[a].y, pv[b].y, x);
-                        x = fmaf(qv[a].z, pv[b].z, x);
-                        x = fmaf(qv[a].w, pv[b].w, x);
-                        c[a][b][j] = x;
-                    }
+                        for (int b = 0; b < 4; ++b) {
+                            float x = c[a][b][j];
+                            x = fmaf(qv[a].x, pv[b].x, x);
+                            x = fmaf(qv[a].y, pv[b].y, x);
+                            x = fmaf(qv[a].z, pv[b].z, x);
+                            x = fmaf(qv[a].w, pv[b].w, x);
+                            c[a][b][j] = x;
+                        }
+                }
             }
         }
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < QA; ++a)
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 float dot = (c[a][b][0] + c[a][b][1]) + (c[a][b][2] + c[a][b][3]);
@@ -1843,7 +1851,7 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
             }
     }
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
+    for (int a = 0; a < QA; ++a) {
         const int qn = q_base + qi0 + a;
         if (qn >= n_q) continue;
         float *row = scores + ((int64_t)qn * g.Hkv + gh) * nb_cap;
