@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define QWFN_QSA_ABI_VERSION 1
+#define QWFN_QSA_ABI_VERSION 2
 
 /* return codes */
 #define QWFN_OK        0
@@ -92,12 +92,22 @@ typedef struct qwfn_qsa_shape {
     int32_t page_tokens;     /* tokens per cache page, a multiple of 64 (256)  */
     int32_t top_k_blocks;    /* scored blocks kept (64); <= 0 = dense          */
     int32_t sink_blocks;     /* leading blocks always kept (1)                 */
-    int32_t local_tokens;    /* trailing tokens whose blocks are kept (512)    */
+    int32_t local_tokens;    /* trailing tokens whose blocks are kept (512);
+                              * 0: only a partial tail block is kept (the
+                              * checkpoint's bias, src/qwfn_engine.cpp:748-753:
+                              * 1e9 for the incomplete tail block, 0 for every
+                              * whole block, the tail's included)           */
     int32_t relu_per_head;   /* 1: score = sum_h relu(q_h.p) (lightning idx)   */
     int32_t shared_selection;/* 1: one selection for all KV heads, on their
                               * scores summed in head order (the checkpoint's
                               * rule, src/qwfn_graph.cpp:477-495)            */
     int32_t quant_variant;   /* QWFN_Q8_X86_RNE or QWFN_Q8_REF_ROUNDF          */
+    int32_t topk_counts_forced; /* 1: the kept set is top_k_blocks blocks in
+                              * all, the forced ones included (top_k of the
+                              * biased scores with k_blocks = top_k_blocks,
+                              * src/qwfn_graph.cpp:493, src/qwfn_engine.cpp:
+                              * 430); 0: top_k_blocks scored blocks on top of
+                              * the forced ones                              */
 } qwfn_qsa_shape;
 
 typedef struct qwfn_kv_view {
@@ -286,6 +296,109 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
                              int32_t src_dtype, int32_t seq, int32_t pos0, int32_t n_q,
                              float *out, int32_t *sel_out, int32_t *n_sel_out,
                              int32_t max_sel, void *ws, size_t ws_bytes, void *stream);
+
+/* ---- the checkpoint's own indexer ---------------------------------------- */
+/* The released checkpoint scores blocks with a separate indexer
+ * (src/qwfn_graph.cpp:233-305 prefill, 410-495 decode): per token a RAW key of
+ * idx_dim values is cached as F16 (the idx cache, :244-254, 465-470); a block
+ * of block_tokens (its ratio r, 4) is keyed by the mean of its members' raw
+ * keys, RMSNorm'd * indexer.k_norm and rotated to the block's first position
+ * (qsa_pool_blocks, :410-429), held in an F16 pool cache
+ * (src/qwfn_engine.cpp:389-394); the score of a block is
+ * sum over the n_idx_head indexer query heads of relu(q_h . pooled[b]) (:477-
+ * 492), and ONE top-k selection serves every KV head.
+ *
+ * Here the raw keys are paged like K and V (the KV view's page table and
+ * page_tokens); the pooled keys are kept as fp32 holding the fp16-rounded
+ * values.  The selection rule comes from qwfn_qsa_shape as usual: the
+ * checkpoint's is sink_blocks 0, local_tokens 0, topk_counts_forced 1,
+ * top_k_blocks = k_blocks (513 = ceil((idx_top_k + r - 1) / r), src/
+ * qwfn_engine.cpp:430), relu_per_head 1.  The selection is written to each of
+ * the n_head_kv rows of sel, so qwfn_sparse_decode_attn takes it unchanged.
+ *
+ * Pooling arithmetic (fixed, and repeated by the CPU oracle):
+ *   mean    fp32 add chain over the members in position order, * fp32(1/r)
+ *   RMSNorm sum of fp32 squares in fp64, lane partials (dims d = l + 64k)
+ *           then a butterfly over lanes 32..1; scale = 1/sqrtf(fp32(sum/D) +
+ *           eps); x * scale * k_norm[d]
+ *   rotary  pairs (i, i + rope_dim/2), angle = pos * base^(-2i/rope_dim) in
+ *           fp64, cos / sin rounded to fp32; dims >= rope_dim pass through.
+ *           The reference's IMROPE gives all four position sections the same
+ *           position for text (src/qwfn_engine.cpp:741, 781, 926, 934), which
+ *           makes it this rotation; per-section (vision) positions are not
+ *           supported.
+ *   store   fp16 round to nearest even, kept as fp32.                        */
+typedef struct qwfn_idx_shape {
+    int32_t idx_dim;         /* 128: indexer key length (src/qwfn_hparams.h:53) */
+    int32_t n_idx_head;      /* 4: indexer query heads (:52)                     */
+    int32_t rope_dim;        /* 64: rotated dims (:35)                           */
+    float   rope_freq_base;  /* the checkpoint's rope_freq_base                  */
+    float   rms_eps;         /* the checkpoint's rms_eps                         */
+} qwfn_idx_shape;
+
+typedef struct qwfn_idx_view {
+    void        *raw;        /* fp16 [n_phys_pages][page_tokens][idx_dim], device,
+                              * paged by the KV view's page_table (16-B aligned) */
+    float       *pooled;     /* fp32 [n_seq][blocks_per_seq][idx_dim], device   */
+    const float *k_norm;     /* fp32 [idx_dim] indexer.k_norm.weight, device    */
+} qwfn_idx_view;
+
+/* Bytes of one raw-key page and of the pooled keys of n_seq sequences
+ * (replaces the idx cache and pool cache sizing, src/qwfn_state.cpp via
+ * st_->idx_cache and src/qwfn_engine.cpp:389-394). */
+int qwfn_idx_cache_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *ishape,
+                         int32_t n_seq, int32_t pages_per_seq,
+                         size_t *raw_page_bytes, size_t *pooled_bytes);
+/* Workspace of qwfn_idx_select (counters shared with qwfn_qsa_workspace_*:
+ * one workspace initialised once serves both when it is the larger size). */
+int qwfn_idx_workspace_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *ishape,
+                             int32_t n_seq, int32_t max_seq_len, size_t *bytes);
+/* Write n_rows raw keys k_raw [n_rows][idx_dim] (F32 rounded to fp16, or F16)
+ * at (seq_ids[i] or 0, pos[i]), then re-pool the block holding each row from
+ * its members (written or not, as the decode update does: the block is forced
+ * while partial, so its key is only read once it is whole).  A run of rows in
+ * one block pools it once.  Replaces the raw-key set_rows and the one-block
+ * pool update of a decode step (src/qwfn_graph.cpp:463-476; inputs
+ * src/qwfn_engine.cpp:737-744). */
+int qwfn_idx_append_pool(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                         const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
+                         const void *k_raw, int32_t src_dtype, const int32_t *seq_ids,
+                         const int32_t *pos, int32_t n_rows, void *stream);
+/* Pool blocks [0, n_whole) of sequence seq from the raw keys: the rebuild after
+ * a prefill (qsa_pool_rebuild, src/qwfn_graph.cpp:431-448; src/qwfn_engine.cpp:
+ * 761-798). */
+int qwfn_idx_pool_rebuild(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                          const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
+                          int32_t seq, int32_t n_whole, void *stream);
+/* Scores and selection of one decode token per sequence: q_idx fp32
+ * [n_seq][n_idx_head][idx_dim] (RMSNorm'd and rotated by the caller, src/
+ * qwfn_graph.cpp:480-484), seq_len as in qwfn_indexer_topk.  Block score =
+ * dots of the heads (each over idx_dim in four strided fp32 fma chains
+ * combined (c0+c1)+(c2+c3)), relu'd when relu_per_head, summed in head order;
+ * the kept set follows the shape's rule; sel [n_seq][n_head_kv][max_sel] gets
+ * the same ascending block ids in every row, n_sel [n_seq][n_head_kv] the
+ * count.  Replaces src/qwfn_graph.cpp:477-495 and the bias window
+ * (src/qwfn_engine.cpp:748-759). */
+int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                    const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
+                    const float *q_idx, const int32_t *seq_len, int32_t n_seq,
+                    int32_t max_seq_len, int32_t *sel, int32_t *n_sel, int32_t max_sel,
+                    void *ws, size_t ws_bytes, void *stream);
+/* qwfn_sparse_attn_prefill with the checkpoint's indexer: k_raw (optional,
+ * with k_new / v_new) [n_q][idx_dim] is written at pos0.. and every block it
+ * touches re-pooled; query i is selected by q_idx [n_q][n_idx_head][idx_dim]
+ * against the indexer's pooled keys (one selection for every KV head), then
+ * attends as in qwfn_sparse_attn_prefill.  Workspace: qwfn_qsa_prefill_
+ * workspace_bytes of the attention shape.  Replaces qsa_top_k and the masked
+ * attention of graph_builder::sparse_attn (src/qwfn_graph.cpp:233-408) and the
+ * per-chunk tables of src/qwfn_engine.cpp:884-957. */
+int qwfn_idx_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                                 const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
+                                 const float *q, const float *q_idx, const void *k_new,
+                                 const void *v_new, const void *k_raw, int32_t src_dtype,
+                                 int32_t seq, int32_t pos0, int32_t n_q, float *out,
+                                 int32_t *sel_out, int32_t *n_sel_out, int32_t max_sel,
+                                 void *ws, size_t ws_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,13 @@ SRC_F16 = 1
 class Shape(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_head", "n_head_kv", "head_dim", "block_tokens", "page_tokens", "top_k_blocks",
-        "sink_blocks", "local_tokens", "relu_per_head", "shared_selection", "quant_variant")]
+        "sink_blocks", "local_tokens", "relu_per_head", "shared_selection", "quant_variant",
+        "topk_counts_forced")]
+
+
+class IdxShape(C.Structure):
+    _fields_ = [("idx_dim", C.c_int32), ("n_idx_head", C.c_int32), ("rope_dim", C.c_int32),
+                ("rope_freq_base", C.c_float), ("rms_eps", C.c_float)]
 
 
 class View(C.Structure):
@@ -70,6 +76,7 @@ def lib() -> C.CDLL:
             "qwfn_oracle_attention_f64": (C.c_int, [S, V, P, P, I, P, P, I, P]),
             "qwfn_oracle_decode_step_f32": (C.c_int, [S, V, P, P, P, P, I, P, P, P, I]),
             "qwfn_oracle_prefill_f64": (C.c_int, [S, V, P, I, I, I, P, P, I, P]),
+            "qwfn_oracle_idx_pool_block": (C.c_int, [S, C.POINTER(IdxShape), P, P, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -90,7 +97,7 @@ def shape_of(cfg) -> Shape:
     """A Shape from any object with the QsaConfig field names."""
     return Shape(cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.block_tokens, cfg.page_tokens,
                  cfg.top_k_blocks, cfg.sink_blocks, cfg.local_tokens, cfg.relu_per_head,
-                 cfg.shared_selection, cfg.quant_variant)
+                 cfg.shared_selection, cfg.quant_variant, getattr(cfg, "topk_counts_forced", 0))
 
 
 # ---- scalar / block helpers -------------------------------------------------
@@ -264,6 +271,26 @@ def select(cfg, scores, seq_len: int, max_sel: int | None = None) -> np.ndarray:
     if n < 0:
         raise RuntimeError(f"oracle select -> {n}")
     return out[:n].copy()
+
+
+def idx_shape_of(icfg) -> IdxShape:
+    """An IdxShape from any object with the qwfnfer_amd.qsa.IdxConfig field names."""
+    return IdxShape(icfg.idx_dim, icfg.n_idx_head, icfg.rope_dim, icfg.rope_freq_base, icfg.rms_eps)
+
+
+def idx_pool_block(cfg, icfg, members_f16, k_norm, b: int) -> np.ndarray:
+    """The checkpoint indexer's pooled key of block b from its block_tokens raw
+    fp16 members ([bt][idx_dim], float16 or uint16 bits)."""
+    s, i = shape_of(cfg), idx_shape_of(icfg)
+    m = np.ascontiguousarray(np.asarray(members_f16).astype(np.float16).view(np.uint16)
+                             if np.asarray(members_f16).dtype != np.uint16 else members_f16)
+    assert m.shape == (cfg.block_tokens, icfg.idx_dim), m.shape
+    w = np.ascontiguousarray(np.asarray(k_norm, dtype=np.float32))
+    out = np.zeros(icfg.idx_dim, dtype=np.float32)
+    rc = lib().qwfn_oracle_idx_pool_block(C.byref(s), C.byref(i), _p(m), _p(w), b, _p(out))
+    if rc < 0:
+        raise RuntimeError(f"oracle idx_pool_block -> {rc}")
+    return out
 
 
 def max_selected(cfg, max_seq_len: int) -> int:

@@ -296,6 +296,16 @@ static void qsa_ranges(const qwfn_qsa_shape *s, int32_t seq_len, int32_t *b_last
     if (*e_hi < *e_lo) *e_hi = *e_lo;
 }
 
+/* Eligible blocks kept at this length: top_k_blocks, less the forced ones
+ * (sink + window) when topk_counts_forced says the count includes them. */
+static int32_t eff_topk(const qwfn_qsa_shape *s, int32_t seq_len) {
+    int32_t b_last, fw, e_lo, e_hi;
+    qsa_ranges(s, seq_len, &b_last, &fw, &e_lo, &e_hi);
+    if (!s->topk_counts_forced) return s->top_k_blocks;
+    const int32_t k = s->top_k_blocks - s->sink_blocks - (b_last - fw + 1);
+    return k > 0 ? k : 0;
+}
+
 static uint32_t score_key(float x) {
     uint32_t u;
     if (x != x) return 0u;                         /* NaN ranks lowest */
@@ -343,14 +353,14 @@ int32_t qwfn_oracle_select(const qwfn_qsa_shape *s, const float *scores,
     int32_t *out = (int32_t *)malloc(sizeof(int32_t) * (size_t)(b_last + 1));
     for (int32_t b = 0; b <= b_last; b++)
         if (b < s->sink_blocks || b >= fw) out[n++] = b;
-    const int32_t ne = e_hi - e_lo;
-    if (ne <= s->top_k_blocks) {
+    const int32_t ne = e_hi - e_lo, k = eff_topk(s, seq_len);
+    if (ne <= k) {
         for (int32_t b = e_lo; b < e_hi; b++) out[n++] = b;
     } else {
         cand_t *c = (cand_t *)malloc(sizeof(cand_t) * (size_t)ne);
         for (int32_t i = 0; i < ne; i++) { c[i].key = score_key(scores[e_lo + i]); c[i].b = e_lo + i; }
         qsort(c, (size_t)ne, sizeof(cand_t), cand_cmp);
-        for (int32_t i = 0; i < s->top_k_blocks; i++) out[n++] = c[i].b;
+        for (int32_t i = 0; i < k; i++) out[n++] = c[i].b;
         free(c);
     }
     qsort(out, (size_t)n, sizeof(int32_t), int_cmp);
@@ -380,7 +390,7 @@ int qwfn_oracle_indexer_topk(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
             }
             int32_t b_last, fw, e_lo, e_hi;
             qsa_ranges(s, L, &b_last, &fw, &e_lo, &e_hi);
-            if (s->top_k_blocks > 0 && e_hi - e_lo > s->top_k_blocks) {
+            if (s->top_k_blocks > 0 && e_hi - e_lo > eff_topk(s, L)) {
                 const float *qg = q + ((int64_t)seq * s->n_head + (int64_t)g * G) * hd;
                 const float *pb = v->pooled + ((int64_t)seq * H + g) * bps * hd;
                 for (int32_t b = e_lo; b < e_hi; b++)
@@ -540,7 +550,7 @@ int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
             const int32_t L = seq_len[seq];
             int32_t b_last, fw, e_lo, e_hi;
             qsa_ranges(s, L, &b_last, &fw, &e_lo, &e_hi);
-            if (s->top_k_blocks > 0 && e_hi - e_lo > s->top_k_blocks) {
+            if (s->top_k_blocks > 0 && e_hi - e_lo > eff_topk(s, L)) {
                 const float *qg = q + ((int64_t)seq * s->n_head + (int64_t)g * G) * hd;
                 const float *pb = v->pooled + ((int64_t)seq * H + g) * bps * hd;
 #pragma omp parallel for schedule(static)
@@ -605,4 +615,61 @@ int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
         }
     free(part);
     return threads;
+}
+
+/* ---- the checkpoint's own indexer keys ------------------------------------ */
+
+/* Pooled key of block b from its block_tokens raw fp16 members [bt][D]
+ * (qsa_pool_blocks, src/qwfn_graph.cpp:410-429): the mean by a sequential
+ * fp32 add chain then * fp32(1/bt) (:415-422); RMSNorm with the fp32 squares
+ * summed in fp64 (ggml_rms_norm sums in fp64 too) -- 64 lane partials over
+ * dims l + 64k, then a butterfly over lane distances 32..1 --, mean =
+ * fp32(sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm (:423);
+ * then the rotation of the block's first position b*bt (IMROPE with every
+ * section at that position, :425-427; src/qwfn_engine.cpp:741, 781, 926,
+ * 934): pairs (i, i + nd/2), angle pos * base^(-2i/nd) in fp64, cos / sin
+ * rounded to fp32; finally fp16 round to nearest even (the F16 pool cache,
+ * src/qwfn_engine.cpp:389-394), returned as fp32. */
+int qwfn_oracle_idx_pool_block(const qwfn_qsa_shape *s, const qwfn_idx_shape *is,
+                               const uint16_t *members, const float *k_norm, int32_t b,
+                               float *out) {
+    const int32_t D = is->idx_dim, nd = is->rope_dim, bt = s->block_tokens;
+    if (D % 64 || D > 256 || nd < 0 || nd % 2 || nd > D) return QWFN_EINVAL;
+    float x[256], y[256];
+    for (int32_t d = 0; d < D; d++) {
+        float a = qwfn_oracle_f16_to_f32(members[d]);
+        for (int32_t r = 1; r < bt; r++) a = a + qwfn_oracle_f16_to_f32(members[(int64_t)r * D + d]);
+        x[d] = a * (1.0f / (float)bt);
+    }
+    double lanes[64];
+    for (int32_t l = 0; l < 64; l++) {
+        double acc = 0.0;
+        for (int32_t k = 0; k < D / 64; k++) {
+            const float sq = x[l + 64 * k] * x[l + 64 * k];
+            acc = acc + (double)sq;
+        }
+        lanes[l] = acc;
+    }
+    for (int32_t off = 32; off >= 1; off >>= 1) {
+        double nxt[64];
+        for (int32_t l = 0; l < 64; l++) nxt[l] = lanes[l] + lanes[l ^ off];
+        memcpy(lanes, nxt, sizeof lanes);
+    }
+    const float mean = (float)(lanes[0] / (double)D);
+    const float scale = 1.0f / sqrtf(mean + is->rms_eps);
+    for (int32_t d = 0; d < D; d++) y[d] = (x[d] * scale) * k_norm[d];
+    const int32_t half = nd / 2, t0 = b * bt;
+    for (int32_t d = 0; d < D; d++) {
+        float o = y[d];
+        if (d < nd) {
+            const int32_t i = d < half ? d : d - half;
+            const double invf = pow((double)is->rope_freq_base, -2.0 * i / (double)nd);
+            const double th = (double)t0 * invf;
+            const float c = (float)cos(th), sn = (float)sin(th);
+            const float x0 = y[i], x1 = y[i + half];
+            o = d < half ? x0 * c - x1 * sn : x0 * sn + x1 * c;
+        }
+        out[d] = f16_round(o);
+    }
+    return 0;
 }

@@ -23,6 +23,9 @@
  *   block score       exact rational arithmetic (fractions) on small cases
  *   selection         brute-force sort in Python + special cases
  *   attention (f64)   numpy float64 textbook softmax + closed-form cases
+ *   indexer pooling   numpy float64 mean / RMSNorm on unrotated blocks, the
+ *                     rotation's closed form on basis vectors, norm and
+ *                     pass-through invariants
  * No function is unpinned.
  */
 #ifndef QWFN_QSA_ORACLE_H
@@ -108,6 +111,13 @@ int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                                 const float *v_new, const int32_t *seq_len,
                                 int32_t n_seq, float *out, int32_t *sel,
                                 int32_t *n_sel, int32_t max_sel);
+
+/* The checkpoint indexer's pooled key of block b: members = the block's
+ * block_tokens raw fp16 keys [bt][idx_dim]; out [idx_dim] (fp16-rounded values
+ * as fp32).  Arithmetic order as documented for qwfn_idx_append_pool. */
+int qwfn_oracle_idx_pool_block(const qwfn_qsa_shape *s, const qwfn_idx_shape *is,
+                               const uint16_t *members, const float *k_norm, int32_t b,
+                               float *out);
 
 #ifdef __cplusplus
 }

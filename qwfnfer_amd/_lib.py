@@ -50,6 +50,12 @@ EXPORTS = (
     "qwfn_sparse_attn_decode",
     "qwfn_qsa_prefill_workspace_bytes",
     "qwfn_sparse_attn_prefill",
+    "qwfn_idx_cache_bytes",
+    "qwfn_idx_workspace_bytes",
+    "qwfn_idx_append_pool",
+    "qwfn_idx_pool_rebuild",
+    "qwfn_idx_select",
+    "qwfn_idx_sparse_attn_prefill",
 )
 
 
@@ -66,6 +72,7 @@ class QsaShape(C.Structure):
         ("relu_per_head", C.c_int32),
         ("shared_selection", C.c_int32),
         ("quant_variant", C.c_int32),
+        ("topk_counts_forced", C.c_int32),
     ]
 
 
@@ -82,6 +89,24 @@ class KvView(C.Structure):
     ]
 
 
+class IdxShape(C.Structure):
+    _fields_ = [
+        ("idx_dim", C.c_int32),
+        ("n_idx_head", C.c_int32),
+        ("rope_dim", C.c_int32),
+        ("rope_freq_base", C.c_float),
+        ("rms_eps", C.c_float),
+    ]
+
+
+class IdxView(C.Structure):
+    _fields_ = [
+        ("raw", C.c_void_p),
+        ("pooled", C.c_void_p),
+        ("k_norm", C.c_void_p),
+    ]
+
+
 class QsaError(RuntimeError):
     """A negative return code of the C ABI, with qwfn_qsa_last_error()."""
 
@@ -95,6 +120,8 @@ _lib = None
 
 _S = C.POINTER(QsaShape)
 _V = C.POINTER(KvView)
+_IS = C.POINTER(IdxShape)
+_IV = C.POINTER(IdxView)
 _P = C.c_void_p
 _I = C.c_int32
 _Z = C.c_size_t
@@ -122,6 +149,13 @@ _SIGS = {
     "qwfn_sparse_attn_decode": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _Z, _P]),
     "qwfn_qsa_prefill_workspace_bytes": (C.c_int, [_S, _I, _I, C.POINTER(_Z)]),
     "qwfn_sparse_attn_prefill": (C.c_int, [_S, _V, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _Z, _P]),
+    "qwfn_idx_cache_bytes": (C.c_int, [_S, _IS, _I, _I, C.POINTER(_Z), C.POINTER(_Z)]),
+    "qwfn_idx_workspace_bytes": (C.c_int, [_S, _IS, _I, _I, C.POINTER(_Z)]),
+    "qwfn_idx_append_pool": (C.c_int, [_S, _V, _IS, _IV, _P, _I, _P, _P, _I, _P]),
+    "qwfn_idx_pool_rebuild": (C.c_int, [_S, _V, _IS, _IV, _I, _I, _P]),
+    "qwfn_idx_select": (C.c_int, [_S, _V, _IS, _IV, _P, _P, _I, _I, _P, _P, _I, _P, _Z, _P]),
+    "qwfn_idx_sparse_attn_prefill": (C.c_int, [_S, _V, _IS, _IV, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P,
+                                               _I, _P, _Z, _P]),
 }
 
 

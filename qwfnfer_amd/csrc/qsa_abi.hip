@@ -53,13 +53,15 @@ int check_shape(const qwfn_qsa_shape *s) {
         return fail(QWFN_EINVAL, "block_tokens (%d) must divide page_tokens (%d)", s->block_tokens,
                     s->page_tokens);
     if (s->sink_blocks < 0) return fail(QWFN_EINVAL, "sink_blocks (%d) < 0", s->sink_blocks);
-    if (s->local_tokens < 1)
-        return fail(QWFN_EINVAL, "local_tokens (%d) < 1: the token being decoded must stay visible",
-                    s->local_tokens);
+    if (s->local_tokens < 0) return fail(QWFN_EINVAL, "local_tokens (%d) < 0", s->local_tokens);
     if (s->quant_variant != QWFN_Q8_X86_RNE && s->quant_variant != QWFN_Q8_REF_ROUNDF)
         return fail(QWFN_EINVAL, "quant_variant %d unknown", s->quant_variant);
-    if ((s->relu_per_head | s->shared_selection) & ~1)
-        return fail(QWFN_EINVAL, "relu_per_head / shared_selection are 0 or 1");
+    if ((s->relu_per_head | s->shared_selection | s->topk_counts_forced) & ~1)
+        return fail(QWFN_EINVAL, "relu_per_head / shared_selection / topk_counts_forced are 0 or 1");
+    if (s->topk_counts_forced && s->top_k_blocks > 0 &&
+        s->top_k_blocks < s->sink_blocks + (s->local_tokens + s->block_tokens - 2) / s->block_tokens + 1)
+        return fail(QWFN_EINVAL, "topk_counts_forced: top_k_blocks (%d) must hold the sink and window blocks",
+                    s->top_k_blocks);
     const int G = s->n_head / s->n_head_kv;
     if (!kernels_for(s->head_dim, G))
         return fail(QWFN_ENOTSUP, "no kernel instantiation for head_dim %d, group %d", s->head_dim, G);
@@ -90,6 +92,8 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->topk = s->top_k_blocks > 0 ? s->top_k_blocks : 0;
     g->sink = s->sink_blocks; g->local = s->local_tokens;
     g->relu = s->relu_per_head; g->variant = s->quant_variant; g->shared = s->shared_selection;
+    g->keep_total = s->topk_counts_forced;
+    g->sel_rows = s->n_head_kv;
     g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * s->head_dim;
     g->page_bytes = g->qbytes + (int64_t)s->n_head_kv * s->page_tokens * (s->head_dim / 32) * 2;
     g->inv_bt = 1.0f / (float)s->block_tokens;
@@ -459,10 +463,24 @@ int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_se
     return ok();
 }
 
-int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
-                             const void *k_new, const void *v_new, int32_t src_dtype, int32_t seq,
-                             int32_t pos0, int32_t n_q, float *out, int32_t *sel_out, int32_t *n_sel_out,
-                             int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// The checkpoint indexer's part of a prefill call (qwfn_idx_sparse_attn_prefill).
+struct IdxPrefill {
+    Geo gi;                       // scoring geometry (idx_geo)
+    IdxGeo ig;
+    qwfn_kv_view vi;              // the KV view with the indexer's pooled keys
+    const qwfn_idx_view *iv;
+    const float *q_idx;           // [n_q][n_idx_head][idx_dim]
+    const void *k_raw;            // [n_q][idx_dim] or NULL
+};
+
+int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const IdxPrefill *ix, const float *q,
+                 const void *k_new, const void *v_new, int32_t src_dtype, int32_t seq, int32_t pos0, int32_t n_q,
+                 float *out, int32_t *sel_out, int32_t *n_sel_out, int32_t max_sel, void *ws, size_t ws_bytes,
+                 void *stream) {
     Geo g;
     int rc = make_geo(shape, view, &g);
     if (rc) return rc;
@@ -506,6 +524,17 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
             if (e != hipSuccess) return hip_fail(e, "prefill: pool");
         }
     }
+    if (ix && ix->k_raw) {
+        // the chunk's raw indexer keys, then every block they touch (a
+        // partial last block too: it is forced while partial, as in decode)
+        e = launch_idx_write(g, *view, ix->ig, (uint16_t *)ix->iv->raw, ix->k_raw, src_dtype == QWFN_SRC_F16,
+                             nullptr, nullptr, n_q, seq, pos0, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill: indexer keys");
+        const int32_t b0 = pos0 / g.bt, b1 = (max_len + g.bt - 1) / g.bt;
+        e = launch_idx_pool(g, *view, ix->ig, (const uint16_t *)ix->iv->raw, ix->iv->pooled, ix->iv->k_norm,
+                            nullptr, nullptr, b1 - b0, seq, b0, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill: indexer pool");
+    }
     Geo gp = g;
     gp.pf = 1;
     gp.pf_seq = seq;
@@ -519,13 +548,191 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
         // prefill mode ignores the seq_len value; the pointer only has to be
         // a readable device int that aliases no output of the attention kernel
         const int32_t *dummy_len = reinterpret_cast<const int32_t *>(w.scores);
-        e = launch_prefill_index(gp, *view, qb, nb, max_len, sb, nsb, sel_stride, w, st);
+        if (ix) {
+            Geo gi = ix->gi;
+            gi.pf = 1; gi.pf_seq = seq; gi.pf_pos0 = gp.pf_pos0;
+            const float *qib = ix->q_idx + (int64_t)i0 * gi.H * gi.hd;
+            e = launch_prefill_index(gi, ix->vi, qib, nb, max_len, sb, nsb, sel_stride, w, st);
+        } else {
+            e = launch_prefill_index(gp, *view, qb, nb, max_len, sb, nsb, sel_stride, w, st);
+        }
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer");
         e = g.vdim ? launch_prefill_attention(gp, *view, qb, nb, sb, nsb, sel_stride, ob, st)
                    : launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: attention");
     }
     return ok();
+}
+
+// ---- the checkpoint's own indexer (qwfn_idx_*) ----------------------------
+
+int make_idx_geo(const qwfn_qsa_shape *s, const qwfn_idx_shape *is, IdxGeo *ig) {
+    if (!is) return fail(QWFN_EINVAL, "idx shape is NULL");
+    if (!idx_kernels_for(is->idx_dim))
+        return fail(QWFN_ENOTSUP, "idx_dim %d: this build pools 64, 128 or 256", is->idx_dim);
+    if (is->n_idx_head < 1) return fail(QWFN_EINVAL, "n_idx_head %d < 1", is->n_idx_head);
+    if (!kernels_for(is->idx_dim, is->n_idx_head))
+        return fail(QWFN_ENOTSUP, "no indexer instantiation for idx_dim %d, %d heads", is->idx_dim, is->n_idx_head);
+    if (is->rope_dim < 0 || is->rope_dim % 2 || is->rope_dim > is->idx_dim || is->rope_dim / 2 > kIdxMaxPairs)
+        return fail(QWFN_EINVAL, "rope_dim %d: even, at most idx_dim and %d", is->rope_dim, 2 * kIdxMaxPairs);
+    if (!(is->rope_freq_base > 0.0f) || !std::isfinite(is->rope_freq_base))
+        return fail(QWFN_EINVAL, "rope_freq_base must be positive and finite");
+    if (!(is->rms_eps >= 0.0f) || !std::isfinite(is->rms_eps))
+        return fail(QWFN_EINVAL, "rms_eps must be >= 0 and finite");
+    (void)s;
+    ig->dim = is->idx_dim;
+    ig->nd = is->rope_dim;
+    ig->eps = is->rms_eps;
+    for (int i = 0; i < kIdxMaxPairs; ++i)
+        ig->invf[i] = i < is->rope_dim / 2 ? std::pow((double)is->rope_freq_base, -2.0 * i / (double)is->rope_dim) : 0.0;
+    return QWFN_OK;
+}
+
+// The indexer's scoring geometry: one "KV head" of n_idx_head query heads over
+// the indexer's pooled keys, one selection per sequence written to every one
+// of the attention's n_head_kv rows.
+Geo idx_scoring_geo(const Geo &g, const qwfn_idx_shape *is) {
+    Geo gi = g;
+    gi.H = is->n_idx_head; gi.Hkv = 1; gi.hd = is->idx_dim; gi.G = is->n_idx_head;
+    gi.shared = 1;
+    gi.sel_rows = g.Hkv;
+    return gi;
+}
+
+int check_idx_view(const qwfn_idx_view *iv, bool raw, bool pooled, bool norm) {
+    if (!iv) return fail(QWFN_EINVAL, "idx view is NULL");
+    if ((raw && (!iv->raw || !aligned(iv->raw, 16))) || (pooled && (!iv->pooled || !aligned(iv->pooled, 16))) ||
+        (norm && (!iv->k_norm || !aligned(iv->k_norm, 4))))
+        return fail(QWFN_EINVAL, "idx view: NULL or misaligned raw (16) / pooled (16) / k_norm (4)");
+    return QWFN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                             const void *k_new, const void *v_new, int32_t src_dtype, int32_t seq,
+                             int32_t pos0, int32_t n_q, float *out, int32_t *sel_out, int32_t *n_sel_out,
+                             int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+    return prefill_impl(shape, view, nullptr, q, k_new, v_new, src_dtype, seq, pos0, n_q, out, sel_out, n_sel_out,
+                        max_sel, ws, ws_bytes, stream);
+}
+
+int qwfn_idx_cache_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *ishape, int32_t n_seq,
+                         int32_t pages_per_seq, size_t *raw_page_bytes, size_t *pooled_bytes) {
+    int rc = check_shape(shape);
+    if (rc) return rc;
+    IdxGeo ig;
+    if ((rc = make_idx_geo(shape, ishape, &ig))) return rc;
+    if (!raw_page_bytes || !pooled_bytes || n_seq < 1 || pages_per_seq < 1)
+        return fail(QWFN_EINVAL, "idx_cache_bytes: NULL output or n_seq / pages_per_seq < 1");
+    *raw_page_bytes = (size_t)shape->page_tokens * ishape->idx_dim * 2;
+    *pooled_bytes = (size_t)n_seq * ((size_t)pages_per_seq * shape->page_tokens / shape->block_tokens) *
+                    ishape->idx_dim * 4;
+    return ok();
+}
+
+int qwfn_idx_workspace_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *ishape, int32_t n_seq,
+                             int32_t max_seq_len, size_t *bytes) {
+    Geo g;
+    int rc = make_geo(shape, nullptr, &g, false);
+    if (rc) return rc;
+    IdxGeo ig;
+    if ((rc = make_idx_geo(shape, ishape, &ig))) return rc;
+    if (!bytes || n_seq < 1 || max_seq_len < 1)
+        return fail(QWFN_EINVAL, "idx_workspace_bytes: bytes NULL or n_seq / max_seq_len < 1");
+    if (n_seq > kMaxCounters) return fail(QWFN_ERANGE, "n_seq exceeds %d", kMaxCounters);
+    *bytes = ws_layout(idx_scoring_geo(g, ishape), n_seq, max_seq_len, max_selected(shape, max_seq_len), false).total;
+    return ok();
+}
+
+int qwfn_idx_append_pool(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const qwfn_idx_shape *ishape,
+                         const qwfn_idx_view *iview, const void *k_raw, int32_t src_dtype, const int32_t *seq_ids,
+                         const int32_t *pos, int32_t n_rows, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    IdxGeo ig;
+    if ((rc = make_idx_geo(shape, ishape, &ig)) || (rc = check_idx_view(iview, true, true, true))) return rc;
+    if (src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16) return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
+    if (!k_raw || !aligned(k_raw, 16) || !pos || n_rows < 0)
+        return fail(QWFN_EINVAL, "idx_append_pool: NULL or misaligned k_raw (16) / NULL pos / n_rows < 0");
+    if (n_rows == 0) return ok();
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = launch_idx_write(g, *view, ig, (uint16_t *)iview->raw, k_raw, src_dtype == QWFN_SRC_F16, seq_ids,
+                                    pos, n_rows, 0, 0, st);
+    if (e != hipSuccess) return hip_fail(e, "idx_append_pool: write");
+    e = launch_idx_pool(g, *view, ig, (const uint16_t *)iview->raw, iview->pooled, iview->k_norm, seq_ids, pos,
+                        n_rows, 0, 0, st);
+    return e == hipSuccess ? ok() : hip_fail(e, "idx_append_pool: pool");
+}
+
+int qwfn_idx_pool_rebuild(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const qwfn_idx_shape *ishape,
+                          const qwfn_idx_view *iview, int32_t seq, int32_t n_whole, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    IdxGeo ig;
+    if ((rc = make_idx_geo(shape, ishape, &ig)) || (rc = check_idx_view(iview, true, true, true))) return rc;
+    if (seq < 0 || seq >= view->n_seq) return fail(QWFN_EINVAL, "idx_pool_rebuild: seq %d outside the view", seq);
+    if (n_whole < 0) return fail(QWFN_EINVAL, "idx_pool_rebuild: n_whole %d < 0", n_whole);
+    if (n_whole > g.bps) return fail(QWFN_ERANGE, "idx_pool_rebuild: n_whole %d > %d blocks", n_whole, g.bps);
+    const hipError_t e = launch_idx_pool(g, *view, ig, (const uint16_t *)iview->raw, iview->pooled, iview->k_norm,
+                                         nullptr, nullptr, n_whole, seq, 0, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "idx_pool_rebuild");
+}
+
+int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const qwfn_idx_shape *ishape,
+                    const qwfn_idx_view *iview, const float *q_idx, const int32_t *seq_len, int32_t n_seq,
+                    int32_t max_seq_len, int32_t *sel, int32_t *n_sel, int32_t max_sel, void *ws, size_t ws_bytes,
+                    void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    IdxGeo ig;
+    if ((rc = make_idx_geo(shape, ishape, &ig)) || (rc = check_idx_view(iview, false, true, false))) return rc;
+    if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (!q_idx || !aligned(q_idx, 16) || !seq_len || !sel || !n_sel)
+        return fail(QWFN_EINVAL, "idx_select: NULL q_idx / seq_len / sel / n_sel or q_idx not 16-byte aligned");
+    const int32_t need = max_selected(shape, max_seq_len);
+    if (max_sel < need) return fail(QWFN_ERANGE, "idx_select: max_sel %d < %d", max_sel, need);
+    const Geo gi = idx_scoring_geo(g, ishape);
+    const WsLayout l = ws_layout(gi, n_seq, max_seq_len, need, false);
+    if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "idx_select: workspace NULL or not 256-byte aligned");
+    if (ws_bytes < l.total) return fail(QWFN_ERANGE, "idx_select: workspace of %zu bytes < %zu", ws_bytes, l.total);
+    const Ws w = ws_bind(ws, l);
+    qwfn_kv_view vi = *view;
+    vi.pooled = iview->pooled;
+    const FusedAppend fa{nullptr, nullptr, 0, 0};
+    const hipError_t e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, w, fa,
+                                        (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "idx_select");
+}
+
+int qwfn_idx_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                                 const qwfn_idx_shape *ishape, const qwfn_idx_view *iview, const float *q,
+                                 const float *q_idx, const void *k_new, const void *v_new, const void *k_raw,
+                                 int32_t src_dtype, int32_t seq, int32_t pos0, int32_t n_q, float *out,
+                                 int32_t *sel_out, int32_t *n_sel_out, int32_t max_sel, void *ws, size_t ws_bytes,
+                                 void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    IdxPrefill ix;
+    if ((rc = make_idx_geo(shape, ishape, &ix.ig)) || (rc = check_idx_view(iview, k_raw != nullptr, true, k_raw != nullptr)))
+        return rc;
+    if (!q_idx || !aligned(q_idx, 16)) return fail(QWFN_EINVAL, "idx prefill: NULL or misaligned q_idx");
+    if (k_raw && (!aligned(k_raw, 16) || !k_new))
+        return fail(QWFN_EINVAL, "idx prefill: k_raw must be 16-byte aligned and come with k_new / v_new");
+    ix.gi = idx_scoring_geo(g, ishape);
+    ix.vi = *view;
+    ix.vi.pooled = iview->pooled;
+    ix.iv = iview;
+    ix.q_idx = q_idx;
+    ix.k_raw = k_raw;
+    return prefill_impl(shape, view, &ix, q, k_new, v_new, src_dtype, seq, pos0, n_q, out, sel_out, n_sel_out,
+                        max_sel, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

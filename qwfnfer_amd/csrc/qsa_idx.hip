@@ -1,0 +1,160 @@
+// qsa_idx.hip -- gfx950 kernels of the checkpoint's own indexer keys
+// (src/qwfn_graph.cpp:244-275, 410-448, 463-476): a raw fp16 key cache of
+// idx_dim values per token, paged like K and V, and its pooled block keys --
+// the mean of a block's block_tokens raw keys, RMSNorm * k_norm, then the
+// rotary position of the block's first token -- rounded to fp16 as the
+// reference's fp16 pool cache holds them (src/qwfn_engine.cpp:389-394) and
+// stored as fp32 for the indexer's scoring.
+//
+// Everything here is bandwidth- or latency-trivial next to the attention (one
+// block per decode step, a few MB for a rebuild), so the kernels favour an
+// evaluation order the CPU oracle repeats exactly over speed.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "qsa_device.h"
+
+namespace qwfn_qsa {
+
+bool idx_kernels_for(int32_t dim) { return dim == 64 || dim == 128 || dim == 256; }
+
+// One thread per 8 values of one row.  seq_ids NULL: every row in seq_const;
+// pos NULL: row r at position pos0 + r.
+__global__ void __launch_bounds__(256)
+k_idx_write(Geo g, qwfn_kv_view v, int32_t dim, uint16_t *raw, const void *src, int32_t f16,
+            const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, int32_t seq_const, int32_t pos0) {
+    const int per = dim / 8;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)n_rows * per) return;
+    const int r = (int)(i / per), c = (int)(i % per);
+    const int seq = seq_ids ? seq_ids[r] : seq_const;
+    const int t = pos ? pos[r] : pos0 + r;
+    const bool report = c == 0;
+    if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
+    if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (report) set_status(v.status, QWFN_STATUS_POS_RANGE); return; }
+    const int32_t pp = phys_page(g, v.page_table, seq, t);
+    if (pp < 0) { if (report) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
+    uint4 out;
+    if (f16) {
+        out = reinterpret_cast<const uint4 *>((const uint16_t *)src + (int64_t)r * dim)[c];
+    } else {
+        const float4 *s4 = reinterpret_cast<const float4 *>((const float *)src + (int64_t)r * dim) + 2 * c;
+        const float4 a = s4[0], b = s4[1];
+        out.x = (uint32_t)f2h(a.x) | (uint32_t)f2h(a.y) << 16;
+        out.y = (uint32_t)f2h(a.z) | (uint32_t)f2h(a.w) << 16;
+        out.z = (uint32_t)f2h(b.x) | (uint32_t)f2h(b.y) << 16;
+        out.w = (uint32_t)f2h(b.z) | (uint32_t)f2h(b.w) << 16;
+    }
+    reinterpret_cast<uint4 *>(raw + ((int64_t)pp * g.pt + t % g.pt) * dim)[c] = out;
+}
+
+hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
+                            const void *src, int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
+                            int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st) {
+    const int64_t total = (int64_t)n_rows * (ig.dim / 8);
+    hipLaunchKernelGGL(k_idx_write, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, g, v, ig.dim, raw,
+                       src, src_f16, seq_ids, pos, n_rows, seq_const, pos0);
+    return hipGetLastError();
+}
+
+// One wave per block; lane l owns dims l + 64k (k < D/64).
+//   mean   : fp32 add chain over the members in position order, * (1/bt)
+//            (ggml_add chain + ggml_scale, src/qwfn_graph.cpp:415-422)
+//   RMSNorm: sum of the fp32 squares in fp64 -- per lane in k order, then a
+//            butterfly over lane distance 32, 16, .., 1 --, mean = (float)
+//            (sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm[d]
+//            (ggml_rms_norm also sums in fp64; :423)
+//   rotary : pair (i, i + nd/2), angle pos * invf[i] in fp64, cos/sin rounded
+//            to fp32: (x0 c - x1 s, x0 s + x1 c); dims >= nd unchanged.  The
+//            reference's IMROPE (:425-427) is this rotation: it gives every
+//            position section the same position for text (src/qwfn_engine.cpp:
+//            741, 781, 926, 934).
+//   store  : rounded to fp16, as fp32.
+template <int D>
+__global__ void __launch_bounds__(256)
+k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, float *__restrict__ pooled,
+           const float *__restrict__ k_norm, const int32_t *seq_ids, const int32_t *pos, int32_t n_items,
+           int32_t seq_const, int32_t blk0) {
+#pragma clang fp contract(off)
+    constexpr int K = D / 64;
+    __shared__ float ys[4][D];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int item = blockIdx.x * 4 + w;
+    if (item >= n_items) return;                   // whole waves: no barrier below spans waves
+    int seq, b;
+    if (pos) {
+        seq = seq_ids ? seq_ids[item] : 0;
+        const int t = pos[item];
+        if (seq < 0 || seq >= g.n_seq_view || t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) return;   // reported by the write
+        b = t / g.bt;
+        if (item + 1 < n_items) {                  // the run's last row pools its block
+            const int s2 = seq_ids ? seq_ids[item + 1] : 0, t2 = pos[item + 1];
+            if (s2 == seq && t2 >= 0 && t2 / g.bt == b) return;
+        }
+    } else {
+        seq = seq_const;
+        b = blk0 + item;
+    }
+    const int t0 = b * g.bt;
+    const int32_t pp = phys_page(g, v.page_table, seq, t0);
+    if (pp < 0) { if (lane == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
+    const uint16_t *m = raw + ((int64_t)pp * g.pt + t0 % g.pt) * D;
+    float x[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) x[k] = h2f(m[lane + 64 * k]);
+    for (int r = 1; r < g.bt; ++r)
+#pragma unroll
+        for (int k = 0; k < K; ++k) x[k] = x[k] + h2f(m[(int64_t)r * D + lane + 64 * k]);
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        x[k] = x[k] * g.inv_bt;
+        const float sq = x[k] * x[k];
+        ss = ss + (double)sq;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off);
+    const float mean = (float)(ss / (double)D);
+    const float scale = 1.0f / sqrtf(mean + ig.eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int d = lane + 64 * k;
+        ys[w][d] = (x[k] * scale) * k_norm[d];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    float *dst = pooled + ((int64_t)seq * g.bps + b) * D;
+    const int half = ig.nd / 2;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int d = lane + 64 * k;
+        float o = ys[w][d];
+        if (d < ig.nd) {
+            const int i = d < half ? d : d - half;
+            const double th = (double)t0 * ig.invf[i];
+            const float c = (float)cos(th), s = (float)sin(th);
+            const float x0 = ys[w][i], x1 = ys[w][i + half];
+            o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
+        }
+        dst[d] = h2f(f2h(o));
+    }
+}
+
+hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,
+                           float *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
+                           int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st) {
+    if (n_items <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n_items + 3) / 4));
+    switch (ig.dim) {
+    case 64:  hipLaunchKernelGGL(k_idx_pool<64>, grid, dim3(256), 0, st, g, v, ig, raw, pooled, k_norm, seq_ids, pos, n_items, seq_const, blk0); break;
+    case 128: hipLaunchKernelGGL(k_idx_pool<128>, grid, dim3(256), 0, st, g, v, ig, raw, pooled, k_norm, seq_ids, pos, n_items, seq_const, blk0); break;
+    case 256: hipLaunchKernelGGL(k_idx_pool<256>, grid, dim3(256), 0, st, g, v, ig, raw, pooled, k_norm, seq_ids, pos, n_items, seq_const, blk0); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace qwfn_qsa

@@ -18,6 +18,9 @@ struct Geo {
     int32_t topk, sink, local;       // selection
     int32_t relu, variant;           // indexer relu, q8_0 rounding
     int32_t shared;                  // one selection for all KV heads (scores summed in head order)
+    int32_t keep_total;              // top_k counts the forced blocks (topk_counts_forced)
+    int32_t sel_rows;                // rows a shared selection is written to per sequence (Hkv;
+                                     // the attention's n_head_kv for the checkpoint indexer)
     int32_t pps, n_phys, n_seq_view; // pages per sequence, pool pages, view seqs
     int32_t bps;                     // pooled blocks per sequence
     int32_t vdim;                    // V quants dim-major per 64-token tile (bt % 64 == 0)
@@ -62,6 +65,29 @@ struct FusedAppend {
 bool kernels_for(int32_t hd, int32_t G);   // an instantiation exists
 
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
+
+// The checkpoint's own indexer keys (qwfn_idx_shape): raw fp16 keys of `dim`
+// values per token, pooled per block with RMSNorm * k_norm, then the first nd
+// dims rotated in pairs (i, i + nd/2) by angle pos * invf[i] at the block's
+// first position.  invf[i] = base^(-2i/nd) in fp64, computed on the host.
+constexpr int kIdxMaxPairs = 64;
+struct IdxGeo {
+    int32_t dim, nd;
+    float eps;
+    double invf[kIdxMaxPairs];
+};
+bool idx_kernels_for(int32_t dim);
+// Rows [n_rows][dim] (fp32, rounded to nearest even, or fp16) into the raw
+// cache at (seq_ids[r] or seq_const, pos[r] or pos0 + r).
+hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
+                            const void *src, int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
+                            int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st);
+// Pool the blocks of rows (seq_ids[i] or 0, pos[i] / bt) when pos != NULL (a
+// run of rows in one block pools it once), else blocks blk0 + [0, n_items) of
+// sequence seq_const.
+hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,
+                           float *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
+                           int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st);
 // seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r.
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
                          int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,

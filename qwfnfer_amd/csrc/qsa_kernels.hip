@@ -9,16 +9,13 @@
 #include <math.h>
 #include <stdint.h>
 
-#include "qsa_internal.h"
+#include "qsa_device.h"
 
 namespace qwfn_qsa {
 
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // Byte offsets inside a page (layout in include/qwfn_qsa.h).
 __device__ __forceinline__ int64_t quant_off(const Geo &g, int gh, int row, int d) {
@@ -35,20 +32,10 @@ __device__ __forceinline__ int64_t scale_off(const Geo &g, int gh, int row, int 
     return g.qbytes + ((int64_t)(gh * g.pt + row) * (g.hd / 32) + j) * 2;
 }
 
-__device__ __forceinline__ void set_status(int32_t *st, int32_t bits) {
-    if (st) atomicOr(st, bits);
-}
-
 // Cache sequence and length of launch sequence s (prefill: query s of one
 // cache sequence, see Geo::pf).  `raw` is seq_len[s] as loaded.
 __device__ __forceinline__ int cache_seq(const Geo &g, int s) { return g.pf ? g.pf_seq : s; }
 __device__ __forceinline__ int seq_length(const Geo &g, int raw, int s) { return g.pf ? g.pf_pos0 + s + 1 : raw; }
-
-// Physical page of (seq, t) or -1.  Caller has range-checked seq and t.
-__device__ __forceinline__ int32_t phys_page(const Geo &g, const int32_t *pt, int seq, int t) {
-    const int32_t p = pt[(int64_t)seq * g.pps + t / g.pt];
-    return (p >= 0 && p < g.n_phys) ? p : -1;
-}
 
 __device__ __forceinline__ int8_t to_i8(float r) {
     if (r != r) return 0;
@@ -431,6 +418,15 @@ __device__ __forceinline__ Ranges qsa_ranges(const Geo &g, int L) {
     return r;
 }
 
+// Eligible blocks kept: top_k_blocks, less the forced ones (sink + window)
+// when the count includes them.  Only meaningful past the short-context case
+// (e_hi > e_lo, so the window starts after the sink blocks).
+__device__ __forceinline__ int eff_topk(const Geo &g, const Ranges &r) {
+    if (!g.keep_total) return g.topk;
+    const int k = g.topk - g.sink - (r.b_last - r.fw + 1);
+    return k > 0 ? k : 0;
+}
+
 constexpr int kIdxThreads = 256;
 constexpr int kBlocksPerChunk = kIdxThreads / 4;   // 4 lanes share one block's dot
 constexpr int kKeysMax = 32 * kIdxThreads;        // eligible blocks the register selection holds
@@ -569,8 +565,8 @@ __device__ void find_bin(IdxShared &sh, int need) {
 // ties) or more eligible blocks than the register path holds takes three
 // radix passes over the keys in memory and an index-ordered tie count.
 template <int KPT>
-__device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const Ranges &r, int32_t *out,
-                                            IdxShared &sh) {
+__device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const Ranges &r, int topk,
+                                            int32_t *out, IdxShared &sh) {
     static_assert(KPT % 4 == 0 && KPT <= 32, "KPT: whole 16-byte vectors, at most 32 bits per thread");
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int base = r.e_lo & ~3;
@@ -630,13 +626,13 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
         const int incl = wave_incl_scan((int)own);
         const int total = __builtin_amdgcn_readlane(incl, 63);
         const int above = total - incl;               // keys in the bins of higher lanes
-        const int ls = __builtin_ctzll(__ballot(above < g.topk && above + (int)own >= g.topk));
+        const int ls = __builtin_ctzll(__ballot(above < topk && above + (int)own >= topk));
         const int above_l = __builtin_amdgcn_readlane(above, ls);
         const int c = (int)sh.hist[ls * 64 + lane];
         const int ic = wave_incl_scan(c);
         const int run = above_l + __builtin_amdgcn_readlane(ic, 63) - ic;   // keys in higher bins
-        const int j = __builtin_ctzll(__ballot(run < g.topk && run + c >= g.topk));
-        if (lane == j) { sh.bin = ls * 64 + j; sh.need = g.topk - run; sh.cnt_b = c; }
+        const int j = __builtin_ctzll(__ballot(run < topk && run + c >= topk));
+        if (lane == j) { sh.bin = ls * 64 + j; sh.need = topk - run; sh.cnt_b = c; }
     }
     __syncthreads();
     const uint32_t B = (uint32_t)sh.bin;
@@ -699,7 +695,7 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
             uint32_t x = w4[q];
             const int tb = base + (4 * lane + q) * KPT;
             while (x) {
-                if (pos < g.topk) out[g.sink + pos] = tb + __builtin_ctz(x);
+                if (pos < topk) out[g.sink + pos] = tb + __builtin_ctz(x);
                 ++pos;
                 x &= x - 1u;
             }
@@ -708,7 +704,7 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     return true;
 }
 
-__device__ __forceinline__ void select_radix(const Geo &g, const float *sc, const Ranges &r,
+__device__ __forceinline__ void select_radix(const Geo &g, const float *sc, const Ranges &r, int topk,
                                                        int32_t *out, IdxShared &sh) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads of the scores below
     const int tid = threadIdx.x;
@@ -718,7 +714,7 @@ __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, cons
     const int b1 = min(b0 + per, r.e_hi);
     __syncthreads();                               // the register path may still read sh.hist
     uint32_t prefix = 0;
-    int need = g.topk;
+    int need = topk;
     radix_pass<12>(sh, sc, r.e_lo, r.e_hi, 20, prefix, need, true);
     radix_pass<12>(sh, sc, r.e_lo, r.e_hi, 8, prefix, need, false);
     radix_pass<8>(sh, sc, r.e_lo, r.e_hi, 0, prefix, need, false);
@@ -741,7 +737,7 @@ __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, cons
         const uint32_t k = score_key(sc[b]);
         bool tk = k > T;
         if (k == T) tk = (eqi++ < need);
-        if (tk && pos < g.sink + g.topk) out[pos++] = b;
+        if (tk && pos < g.sink + topk) out[pos++] = b;
     }
 }
 
@@ -750,25 +746,28 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     const int ne = r.e_hi - r.e_lo;
-    if (g.topk <= 0 || ne <= g.topk) {
+    const int topk = eff_topk(g, r);
+    if (g.topk <= 0 || ne <= topk) {
         const int n = r.b_last + 1;
         for (int i = tid; i < n; i += kIdxThreads) out[i] = i;
         if (tid == 0) *nout = n;
         return;
     }
-    bool done = false;
-    const int span = r.e_hi - (r.e_lo & ~3);      // blocks the register path covers
-    if (span <= 4 * kIdxThreads) done = select_regs<4>(g, sc, r, out, sh);
-    else if (span <= 8 * kIdxThreads) done = select_regs<8>(g, sc, r, out, sh);
-    else if (span <= 12 * kIdxThreads) done = select_regs<12>(g, sc, r, out, sh);
-    else if (span <= 16 * kIdxThreads) done = select_regs<16>(g, sc, r, out, sh);
-    else if (span <= 24 * kIdxThreads) done = select_regs<24>(g, sc, r, out, sh);
-    else if (span <= kKeysMax) done = select_regs<kKeysMax / kIdxThreads>(g, sc, r, out, sh);
-    if (!done) select_radix(g, sc, r, out, sh);
+    if (topk > 0) {                               // (none scored when the forced blocks fill the count)
+        bool done = false;
+        const int span = r.e_hi - (r.e_lo & ~3);  // blocks the register path covers
+        if (span <= 4 * kIdxThreads) done = select_regs<4>(g, sc, r, topk, out, sh);
+        else if (span <= 8 * kIdxThreads) done = select_regs<8>(g, sc, r, topk, out, sh);
+        else if (span <= 12 * kIdxThreads) done = select_regs<12>(g, sc, r, topk, out, sh);
+        else if (span <= 16 * kIdxThreads) done = select_regs<16>(g, sc, r, topk, out, sh);
+        else if (span <= 24 * kIdxThreads) done = select_regs<24>(g, sc, r, topk, out, sh);
+        else if (span <= kKeysMax) done = select_regs<kKeysMax / kIdxThreads>(g, sc, r, topk, out, sh);
+        if (!done) select_radix(g, sc, r, topk, out, sh);
+    }
     for (int i = tid; i < g.sink; i += kIdxThreads) out[i] = i;
     const int nwin = r.b_last - r.fw + 1;
-    for (int i = tid; i < nwin; i += kIdxThreads) out[g.sink + g.topk + i] = r.fw + i;
-    if (tid == 0) *nout = g.sink + g.topk + nwin;
+    for (int i = tid; i < nwin; i += kIdxThreads) out[g.sink + topk + i] = r.fw + i;
+    if (tid == 0) *nout = g.sink + topk + nwin;
 }
 
 // Shared selection (shared_selection = 1): one selection for every KV head of
@@ -780,6 +779,7 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
 // count, to every head's row.
 __device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t sc_stride, int L, int32_t *out0,
                                               int64_t out_stride, int32_t *nout0, IdxShared &sh) {
+    // scores: g.Hkv rows; selection: g.sel_rows rows
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     const BufRsrc rs = buf_rsrc(sc0, (uint32_t)(((int64_t)(g.Hkv - 1) * sc_stride + r.e_hi) * 4));
@@ -798,10 +798,10 @@ __device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t 
     const int n = __builtin_bit_cast(int, BufLoad<1, kCpolSc1>::at(rn, 0, 0)[0]);
     for (int i = tid; i < n; i += kIdxThreads) {
         const int32_t x = __builtin_bit_cast(int32_t, BufLoad<1, kCpolSc1>::at(ro, i * 4, 0)[0]);
-        for (int h = 1; h < g.Hkv; ++h) out0[h * out_stride + i] = x;
+        for (int h = 1; h < g.sel_rows; ++h) out0[h * out_stride + i] = x;
     }
     if (tid == 0)
-        for (int h = 1; h < g.Hkv; ++h) nout0[h] = n;
+        for (int h = 1; h < g.sel_rows; ++h) nout0[h] = n;
 }
 
 // grid (n_chunks [+1 with the fused append], Hkv, n_seq)
@@ -839,7 +839,7 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     if (ok && g.topk > 0) {
         const Ranges r = qsa_ranges(g, L);
         const int ne = r.e_hi - r.e_lo;
-        if (ne > g.topk && c * kBlocksPerChunk < ne) {
+        if (ne > eff_topk(g, r) && c * kBlocksPerChunk < ne) {
             const bool act = bi < ne;
             const int b = r.e_lo + bi;
 #pragma unroll
@@ -881,14 +881,17 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     int32_t *out = sel + (int64_t)pair * max_sel;
     if (!ok) {
         if (tid == 0) {
-            for (int h = g.shared ? 0 : gh; h <= (g.shared ? g.Hkv - 1 : gh); ++h) nsel[s * g.Hkv + h] = 0;
+            if (g.shared)
+                for (int h = 0; h < g.sel_rows; ++h) nsel[s * g.sel_rows + h] = 0;
+            else
+                nsel[pair] = 0;
             set_status(v.status, QWFN_STATUS_LEN_RANGE);
         }
         return;
     }
     if (g.shared)
-        select_shared(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L, sel + (int64_t)s * g.Hkv * max_sel,
-                      max_sel, nsel + s * g.Hkv, sh);
+        select_shared(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L,
+                      sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
     else
         select_blocks(g, sc, L, out, nsel + pair, sh);
 }
@@ -1871,8 +1874,8 @@ k_pf_select(Geo g, float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, i
     const int gh = blockIdx.x, s = blockIdx.y;             // (gh = 0 with a shared selection)
     const int pair = s * g.Hkv + gh;
     if (g.shared)
-        select_shared(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
-                      max_sel, nsel + pair, sh);
+        select_shared(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1,
+                      sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
     else
         select_blocks(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
                       nsel + pair, sh);

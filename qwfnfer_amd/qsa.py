@@ -21,13 +21,15 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import KvView, QsaShape, call
+from ._lib import IdxShape, IdxView, KvView, QsaShape, call
 
 __all__ = [
     "QsaConfig", "KvCache", "KvState", "Workspace",
     "append_q8_0", "pool_update", "pool_rebuild", "indexer_topk", "gather_dequant",
     "sparse_decode_attn", "decode_append_select", "sparse_attn_decode", "sparse_attn_prefill",
     "export_rows_q8_0", "import_rows_q8_0", "read_status",
+    "IdxConfig", "IdxCache", "idx_append_pool", "idx_pool_rebuild", "idx_select", "idx_sparse_attn_prefill",
+    "checkpoint_config",
 ]
 
 
@@ -47,6 +49,7 @@ class QsaConfig:
     relu_per_head: int = 0
     shared_selection: int = 0
     quant_variant: int = _lib.Q8_X86_RNE
+    topk_counts_forced: int = 0
 
     @property
     def group(self) -> int:
@@ -60,7 +63,7 @@ class QsaConfig:
         return QsaShape(self.n_head, self.n_head_kv, self.head_dim, self.block_tokens,
                         self.page_tokens, self.top_k_blocks, self.sink_blocks,
                         self.local_tokens, self.relu_per_head, self.shared_selection,
-                        self.quant_variant)
+                        self.quant_variant, self.topk_counts_forced)
 
     def check(self) -> None:
         s = self.shape()
@@ -475,3 +478,162 @@ def read_status(cache: KvCache, stream=None) -> int:
     out = C.c_int32()
     call("qwfn_qsa_read_status", C.byref(cache.view()), C.byref(out), _stream(stream))
     return out.value
+
+
+# ---- the checkpoint's own indexer ------------------------------------------
+
+@dataclass(frozen=True)
+class IdxConfig:
+    """The released checkpoint's lightning indexer (src/qwfn_hparams.h:35, 52-53;
+    src/qwfn_graph.cpp:233-305, 410-495): raw keys of idx_dim values per token,
+    n_idx_head query heads, blocks pooled with RMSNorm * k_norm and rotated on
+    their first rope_dim dims."""
+    idx_dim: int = 128
+    n_idx_head: int = 4
+    rope_dim: int = 64
+    rope_freq_base: float = 10000000.0
+    rms_eps: float = 1e-6
+
+    def shape(self) -> IdxShape:
+        return IdxShape(self.idx_dim, self.n_idx_head, self.rope_dim, self.rope_freq_base, self.rms_eps)
+
+
+def checkpoint_config(idx_top_k: int = 2048, ratio: int = 4, page_tokens: int = 256,
+                      quant_variant: int = _lib.Q8_X86_RNE) -> QsaConfig:
+    """The attention layer of the released checkpoint (src/qwfn_hparams.h:22-26,
+    52-54): 24 query heads, 2 KV heads of 256, blocks of ``ratio`` tokens,
+    k_blocks = ceil((idx_top_k + ratio - 1) / ratio) kept blocks in all
+    (src/qwfn_engine.cpp:430), only a partial tail block forced
+    (:748-753), relu per indexer head, one selection for both KV heads."""
+    kb = (idx_top_k + ratio - 1 + ratio - 1) // ratio
+    return QsaConfig(n_head=24, n_head_kv=2, head_dim=256, block_tokens=ratio, page_tokens=page_tokens,
+                     top_k_blocks=kb, sink_blocks=0, local_tokens=0, relu_per_head=1, shared_selection=1,
+                     quant_variant=quant_variant, topk_counts_forced=1)
+
+
+@dataclass
+class IdxCache:
+    """One attention layer's indexer keys, paged by a :class:`KvCache`'s page
+    table: raw fp16 keys [n_phys_pages, page_tokens, idx_dim] (the reference's
+    idx cache) and the pooled block keys [n_seq, blocks_per_seq, idx_dim] (its
+    F16 pool cache, kept as fp32 holding fp16 values), plus k_norm [idx_dim]."""
+    icfg: IdxConfig
+    kv: KvCache
+    raw: torch.Tensor
+    pooled: torch.Tensor
+    k_norm: torch.Tensor
+    _view: IdxView = field(default=None, repr=False)
+
+    @classmethod
+    def allocate(cls, icfg: IdxConfig, kv: KvCache, k_norm: torch.Tensor) -> "IdxCache":
+        cfg = kv.cfg
+        rpb, pb = C.c_size_t(), C.c_size_t()
+        call("qwfn_idx_cache_bytes", C.byref(cfg.shape()), C.byref(icfg.shape()), kv.n_seq, kv.pages_per_seq,
+             C.byref(rpb), C.byref(pb))
+        dev = kv.k_pages.device
+        raw = torch.zeros((kv.n_phys_pages, cfg.page_tokens, icfg.idx_dim), dtype=torch.float16, device=dev)
+        bps = kv.pages_per_seq * cfg.page_tokens // cfg.block_tokens
+        pooled = torch.zeros((kv.n_seq, bps, icfg.idx_dim), dtype=torch.float32, device=dev)
+        assert raw.numel() * 2 == rpb.value * kv.n_phys_pages and pooled.numel() * 4 == pb.value
+        k_norm = k_norm.to(device=dev, dtype=torch.float32).contiguous()
+        _need(k_norm, "k_norm", torch.float32, icfg.idx_dim)
+        return cls(icfg, kv, raw, pooled, k_norm)
+
+    def view(self) -> IdxView:
+        if self._view is None:
+            self._view = IdxView(self.raw.data_ptr(), self.pooled.data_ptr(), self.k_norm.data_ptr())
+        return self._view
+
+    def workspace_bytes(self, n_seq: int, max_seq_len: int) -> int:
+        out = C.c_size_t()
+        call("qwfn_idx_workspace_bytes", C.byref(self.kv.cfg.shape()), C.byref(self.icfg.shape()), n_seq,
+             max_seq_len, C.byref(out))
+        return out.value
+
+
+def idx_append_pool(ic: IdxCache, k_raw: torch.Tensor, pos: torch.Tensor,
+                    seq_ids: Optional[torch.Tensor] = None, stream=None) -> None:
+    """The decode step's raw indexer key (src/qwfn_graph.cpp:463-470) and the
+    re-pooled block holding it (:471-476): rows k_raw [n_rows, idx_dim] (f32
+    or f16) at ``pos`` of ``seq_ids`` (default 0)."""
+    n_rows = pos.numel()
+    if k_raw.dtype not in (torch.float32, torch.float16):
+        raise TypeError("k_raw must be float32 or float16")
+    _need(k_raw, "k_raw", k_raw.dtype, n_rows * ic.icfg.idx_dim)
+    _need(pos, "pos", torch.int32)
+    if seq_ids is not None:
+        _need(seq_ids, "seq_ids", torch.int32, n_rows)
+    call("qwfn_idx_append_pool", C.byref(ic.kv.cfg.shape()), C.byref(ic.kv.view()), C.byref(ic.icfg.shape()),
+         C.byref(ic.view()), k_raw.data_ptr(), _lib.SRC_F16 if k_raw.dtype == torch.float16 else _lib.SRC_F32,
+         _ptr(seq_ids), pos.data_ptr(), n_rows, _stream(stream))
+
+
+def idx_pool_rebuild(ic: IdxCache, seq: int, n_whole: int, stream=None) -> None:
+    """Pool the indexer keys of blocks [0, n_whole) of ``seq`` (qsa_pool_rebuild,
+    src/qwfn_graph.cpp:431-448)."""
+    call("qwfn_idx_pool_rebuild", C.byref(ic.kv.cfg.shape()), C.byref(ic.kv.view()), C.byref(ic.icfg.shape()),
+         C.byref(ic.view()), seq, n_whole, _stream(stream))
+
+
+def idx_select(ic: IdxCache, q_idx: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int, ws: Workspace,
+               sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None, stream=None):
+    """The checkpoint indexer's scores and top-k for one decode token per
+    sequence (src/qwfn_graph.cpp:477-495): q_idx [n_seq, n_idx_head, idx_dim]
+    (normed and rotated).  Returns (sel [n_seq, n_head_kv, max_sel], n_sel
+    [n_seq, n_head_kv]) with one selection repeated for every KV head."""
+    cfg, icfg = ic.kv.cfg, ic.icfg
+    n_seq = seq_len.numel()
+    _need(q_idx, "q_idx", torch.float32, n_seq * icfg.n_idx_head * icfg.idx_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    max_sel = cfg.max_selected(max_seq_len)
+    if sel is None:
+        sel = torch.empty((n_seq, cfg.n_head_kv, max_sel), dtype=torch.int32, device=q_idx.device)
+    if n_sel is None:
+        n_sel = torch.empty((n_seq, cfg.n_head_kv), dtype=torch.int32, device=q_idx.device)
+    _need(sel, "sel", torch.int32)
+    _need(n_sel, "n_sel", torch.int32, n_seq * cfg.n_head_kv)
+    call("qwfn_idx_select", C.byref(cfg.shape()), C.byref(ic.kv.view()), C.byref(icfg.shape()), C.byref(ic.view()),
+         q_idx.data_ptr(), seq_len.data_ptr(), n_seq, max_seq_len, sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1],
+         ws.ptr(), ws.nbytes, _stream(stream))
+    return sel, n_sel
+
+
+def idx_sparse_attn_prefill(ic: IdxCache, q: torch.Tensor, q_idx: torch.Tensor, seq: int, pos0: int,
+                            ws: Workspace, k_new: Optional[torch.Tensor] = None,
+                            v_new: Optional[torch.Tensor] = None, k_raw: Optional[torch.Tensor] = None,
+                            out: Optional[torch.Tensor] = None, sel: Optional[torch.Tensor] = None,
+                            n_sel: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """:func:`sparse_attn_prefill` with the checkpoint's indexer (qsa_top_k and
+    the masked attention of graph_builder::sparse_attn, src/qwfn_graph.cpp:
+    233-408): k_raw [n_q, idx_dim] (with k_new / v_new) is appended and pooled,
+    query i is selected by q_idx[i] and attends causally over its selection."""
+    cache, cfg, icfg = ic.kv, ic.kv.cfg, ic.icfg
+    n_q = q.numel() // (cfg.n_head * cfg.head_dim)
+    _need(q, "q", torch.float32, n_q * cfg.n_head * cfg.head_dim)
+    _need(q_idx, "q_idx", torch.float32, n_q * icfg.n_idx_head * icfg.idx_dim)
+    src = _lib.SRC_F32
+    if (k_new is None) != (v_new is None):
+        raise ValueError("pass both k_new and v_new or neither")
+    if k_raw is not None and k_new is None:
+        raise ValueError("k_raw comes with k_new / v_new")
+    if k_new is not None:
+        if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype:
+            raise TypeError("k_new and v_new must both be float32 or both float16")
+        _need(k_new, "k_new", k_new.dtype, n_q * cfg.kv_dim)
+        _need(v_new, "v_new", k_new.dtype, n_q * cfg.kv_dim)
+        if k_raw is not None:
+            _need(k_raw, "k_raw", k_new.dtype, n_q * icfg.idx_dim)
+        src = _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32
+    if out is None:
+        out = torch.empty((n_q, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
+    if (sel is None) != (n_sel is None):
+        raise ValueError("pass both sel and n_sel or neither")
+    max_sel = 0
+    if sel is not None:
+        _need(sel, "sel", torch.int32)
+        _need(n_sel, "n_sel", torch.int32, n_q * cfg.n_head_kv)
+        max_sel = sel.shape[-1]
+    call("qwfn_idx_sparse_attn_prefill", C.byref(cfg.shape()), C.byref(cache.view()), C.byref(icfg.shape()),
+         C.byref(ic.view()), q.data_ptr(), q_idx.data_ptr(), _ptr(k_new), _ptr(v_new), _ptr(k_raw), src, seq,
+         pos0, n_q, out.data_ptr(), _ptr(sel), _ptr(n_sel), max_sel, ws.ptr(), ws.nbytes, _stream(stream))
+    return out

@@ -27,6 +27,7 @@ class Cfg:
     relu_per_head: int = 0
     shared_selection: int = 0
     quant_variant: int = 0
+    topk_counts_forced: int = 0
 
     @property
     def group(self):
@@ -119,7 +120,8 @@ def block_score_exact(q_group: np.ndarray, p: np.ndarray, relu: bool) -> np.floa
 def select_ref(cfg: Cfg, scores: np.ndarray, seq_len: int) -> np.ndarray:
     """Kept blocks from the definition: F = sink blocks U blocks meeting the last
     local_tokens tokens; E = whole blocks not in F; F U top-k(E) by (score desc,
-    index asc), NaN lowest; ascending."""
+    index asc), NaN lowest; ascending.  k = top_k_blocks, less |F| when
+    topk_counts_forced."""
     bt = cfg.block_tokens
     last = seq_len - 1
     blocks = range(last // bt + 1)
@@ -128,11 +130,14 @@ def select_ref(cfg: Cfg, scores: np.ndarray, seq_len: int) -> np.ndarray:
     lo = last - cfg.local_tokens + 1
     F = {b for b in blocks if b < cfg.sink_blocks or b * bt + bt - 1 >= lo}
     E = [b for b in blocks if (b + 1) * bt <= seq_len and b not in F]
-    if len(E) > cfg.top_k_blocks:
+    k = cfg.top_k_blocks
+    if getattr(cfg, "topk_counts_forced", 0):
+        k = max(k - len(F), 0)
+    if len(E) > k:
         def key(b):
             s = float(scores[b])
             return (1, 0.0, b) if s != s else (0, -s, b)
-        E = sorted(E, key=key)[:cfg.top_k_blocks]
+        E = sorted(E, key=key)[:k]
     return np.array(sorted(F | set(E)), dtype=np.int32)
 
 

@@ -6,7 +6,7 @@ import re
 
 import pytest
 
-from qwfnfer_amd import _lib
+from qwfnfer_amd import _lib, qsa
 from qwfnfer_amd.qsa import QsaConfig
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.qwfn_qsa_abi_version() == 1
+    assert lib.qwfn_qsa_abi_version() == 2
 
 
 def _code(name, *args):
@@ -39,7 +39,8 @@ def test_shape_validation():
     assert _code("qwfn_qsa_check_shape", C.byref(s)) == 0
     bad = [
         dict(n_head=15), dict(head_dim=100), dict(page_tokens=100), dict(block_tokens=48),
-        dict(local_tokens=0), dict(sink_blocks=-1), dict(quant_variant=3), dict(relu_per_head=2),
+        dict(local_tokens=-1), dict(sink_blocks=-1), dict(quant_variant=3), dict(relu_per_head=2),
+        dict(topk_counts_forced=2), dict(topk_counts_forced=1, top_k_blocks=1),   # 1 < sink + window
     ]
     for kw in bad:
         s = QsaConfig(**{**ok.__dict__, **kw}).shape()
@@ -51,6 +52,34 @@ def test_shape_validation():
     assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_EINVAL
     s = QsaConfig(**{**ok.__dict__, "n_head": 6, "n_head_kv": 2, "head_dim": 96}).shape()
     assert _code("qwfn_qsa_check_shape", C.byref(s)) == _lib.QWFN_ENOTSUP
+    # the checkpoint's rule: only a partial tail forced, counted in top_k
+    s = qsa.checkpoint_config().shape()
+    assert _code("qwfn_qsa_check_shape", C.byref(s)) == 0
+
+
+def test_idx_argument_validation():
+    cfg = qsa.checkpoint_config()
+    icfg = qsa.IdxConfig()
+    out, out2 = C.c_size_t(), C.c_size_t()
+    assert _code("qwfn_idx_cache_bytes", C.byref(cfg.shape()), C.byref(icfg.shape()), 1, 4, C.byref(out),
+                 C.byref(out2)) == 0
+    assert out.value == 256 * 128 * 2 and out2.value == 4 * 256 // 4 * 128 * 4
+    bad = [dict(idx_dim=96), dict(rope_dim=63), dict(rope_dim=256), dict(rope_freq_base=0.0),
+           dict(rms_eps=-1.0), dict(n_idx_head=0)]
+    for kw in bad:
+        i = qsa.IdxConfig(**{**icfg.__dict__, **kw}).shape()
+        rc = _code("qwfn_idx_cache_bytes", C.byref(cfg.shape()), C.byref(i), 1, 4, C.byref(out), C.byref(out2))
+        assert rc in (_lib.QWFN_EINVAL, _lib.QWFN_ENOTSUP), kw
+    i = qsa.IdxConfig(n_idx_head=3).shape()                 # no (128, 3) indexer instantiation
+    assert _code("qwfn_idx_workspace_bytes", C.byref(cfg.shape()), C.byref(i), 1, 100, C.byref(out)) == \
+        _lib.QWFN_ENOTSUP
+    # NULL views and misaligned rows are rejected before any launch
+    view = _lib.KvView(0, 0, 0, 0, 0, 1, 1, 1)
+    iv = _lib.IdxView(0, 0, 0)
+    assert _code("qwfn_idx_append_pool", C.byref(cfg.shape()), C.byref(view), C.byref(icfg.shape()), C.byref(iv),
+                 None, 0, None, None, 1, None) == _lib.QWFN_EINVAL
+    assert _code("qwfn_idx_select", C.byref(cfg.shape()), C.byref(view), C.byref(icfg.shape()), C.byref(iv),
+                 None, None, 1, 1, None, None, 1, None, 0, None) == _lib.QWFN_EINVAL
 
 
 def test_sizes():

@@ -1,0 +1,221 @@
+"""Parity of the checkpoint's own indexer (qwfn_idx_*) with the CPU oracle, at
+the checkpoint's attention shape (24 query heads, 2 KV heads of 256, blocks of
+4 tokens, 513 kept blocks, only a partial tail forced, one selection for both
+KV heads).
+
+Bit-exact: the raw fp16 keys, the pooled keys (same arithmetic order as the
+oracle; the rotation's fp64 cos / sin are rounded to fp32, so a last-bit
+difference between the device and host libm would surface here), the
+selection.  Attention: |o - o_ref| <= 2e-3 + 1e-3 |o_ref| against the fp64
+oracle over the same selection."""
+import numpy as np
+import pytest
+import torch
+
+from _ckpt import CKPT, ICfg, oracle_pool_all, oracle_select
+from _gpu import assert_close_attn, cfg_of, kv_rows, make_pair, np_of
+from qwfnfer_amd import qsa
+
+pytestmark = pytest.mark.gpu
+
+ICFG = ICfg()
+
+
+def _pair(cfg, n_seq, pps, seed, spare=0):
+    dev, host = make_pair(cfg, n_seq, pps, seed=seed, spare=spare)
+    rng = np.random.default_rng(seed + 1)
+    k_norm = rng.uniform(0.5, 1.5, ICFG.idx_dim).astype(np.float32)
+    ic = qsa.IdxCache.allocate(qsa.IdxConfig(**ICFG.__dict__), dev, torch.from_numpy(k_norm))
+    return dev, host, ic, k_norm
+
+
+def _raw_rows(dev, ic, seq, n):
+    """The device's raw keys of positions [0, n) of seq, in position order."""
+    pt = np_of(dev.page_table)[seq]
+    t = np.arange(n)
+    return np_of(ic.raw)[pt[t // dev.cfg.page_tokens], t % dev.cfg.page_tokens]
+
+
+def _ws(cfg, ic, n_seq, L):
+    c = cfg_of(cfg)
+    return qsa.Workspace(c, n_seq, L, nbytes=max(c.workspace_bytes(n_seq, L), ic.workspace_bytes(n_seq, L)))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_idx_append_pool_matches_oracle(dtype):
+    cfg = CKPT
+    rng = np.random.default_rng(800)
+    dev, host, ic, w = _pair(cfg, 2, 5, seed=801, spare=1)
+    L = 1001
+    kr = (rng.standard_normal((L, 128)) * 2).astype(dtype)
+    qsa.idx_append_pool(ic, torch.from_numpy(kr).cuda(), torch.arange(L, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    rows = _raw_rows(dev, ic, 0, L)
+    np.testing.assert_array_equal(rows.view(np.uint16), kr.astype(np.float16).view(np.uint16))
+    nb = (L + 3) // 4
+    want = oracle_pool_all(cfg, ICFG, kr.astype(np.float16), w, nb)
+    np.testing.assert_array_equal(np_of(ic.pooled)[0, :nb], want)
+    # decode steps: one row at a time, each re-pooling its (partial or just
+    # completed) block
+    allr = kr.astype(np.float16)
+    for step in range(7):
+        p = L + step
+        x = (rng.standard_normal((1, 128)) * 2).astype(dtype)
+        qsa.idx_append_pool(ic, torch.from_numpy(x).cuda(), torch.tensor([p], dtype=torch.int32, device="cuda"))
+        torch.cuda.synchronize()
+        allr = np.concatenate([allr, x.astype(np.float16)])
+        b = p // 4
+        got = np_of(ic.pooled)[0, b]
+        np.testing.assert_array_equal(got, oracle_pool_all(cfg, ICFG, allr, w, b + 1)[b], err_msg=f"step {step}")
+    # rows of the other sequence through seq_ids, out of order
+    pos = rng.permutation(64).astype(np.int32)
+    x = (rng.standard_normal((64, 128))).astype(dtype)
+    qsa.idx_append_pool(ic, torch.from_numpy(x).cuda(), torch.from_numpy(pos).cuda(),
+                        seq_ids=torch.ones(64, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    r1 = np.zeros((64, 128), np.float16)
+    r1[pos] = x.astype(np.float16)
+    np.testing.assert_array_equal(_raw_rows(dev, ic, 1, 64), r1)
+    np.testing.assert_array_equal(np_of(ic.pooled)[1, :16], oracle_pool_all(cfg, ICFG, r1, w, 16))
+    assert qsa.read_status(dev) == 0
+
+
+def test_idx_rebuild_matches_oracle():
+    cfg = CKPT
+    rng = np.random.default_rng(810)
+    dev, host, ic, w = _pair(cfg, 1, 12, seed=811)
+    L = 3000
+    kr = rng.standard_normal((L, 128)).astype(np.float32)
+    qsa.idx_append_pool(ic, torch.from_numpy(kr).cuda(), torch.arange(L, dtype=torch.int32, device="cuda"))
+    ic.pooled.zero_()
+    qsa.idx_pool_rebuild(ic, 0, L // 4)
+    torch.cuda.synchronize()
+    want = oracle_pool_all(cfg, ICFG, kr.astype(np.float16), w, L // 4)
+    np.testing.assert_array_equal(np_of(ic.pooled)[0, :L // 4], want)
+    assert not np_of(ic.pooled)[0, L // 4:].any()
+
+
+@pytest.mark.parametrize("lengths", [[1500], [6000], [6001, 2053], [6003, 4]])
+def test_idx_select_matches_oracle(lengths):
+    cfg = CKPT
+    rng = np.random.default_rng(820 + sum(lengths))
+    n = len(lengths)
+    pps = max(lengths) // cfg.page_tokens + 1
+    dev, host, ic, w = _pair(cfg, n, pps, seed=821)
+    for s, L in enumerate(lengths):
+        kr = rng.standard_normal((L, 128)).astype(np.float32)
+        qsa.idx_append_pool(ic, torch.from_numpy(kr).cuda(), torch.arange(L, dtype=torch.int32, device="cuda"),
+                            seq_ids=torch.full((L,), s, dtype=torch.int32, device="cuda"))
+    q = rng.standard_normal((n, 4, 128)).astype(np.float32)
+    Lmax = max(lengths)
+    ws = _ws(cfg, ic, n, Lmax)
+    sel, nsel = qsa.idx_select(ic, torch.from_numpy(q).cuda(), torch.tensor(lengths, dtype=torch.int32,
+                                                                             device="cuda"), Lmax, ws)
+    torch.cuda.synchronize()
+    gs, gn, pooled = np_of(sel), np_of(nsel), np_of(ic.pooled)
+    for s, L in enumerate(lengths):
+        want = oracle_select(cfg, ICFG, pooled[s], q[s], L, sel.shape[-1])
+        assert len(want) == min(513, (L + 3) // 4)
+        for g in range(2):
+            assert gn[s, g] == len(want)
+            np.testing.assert_array_equal(gs[s, g, :gn[s, g]], want, err_msg=f"seq {s} head {g}")
+    assert qsa.read_status(dev) == 0
+
+
+def test_checkpoint_decode_steps():
+    """Decode steps of the checkpoint layer: K/V and the raw indexer key
+    appended, the indexer's block pooled, one selection for both KV heads, the
+    attention over it -- each step against the oracle."""
+    cfg = CKPT
+    rng = np.random.default_rng(830)
+    L0 = 5000
+    pps = (L0 + 16) // cfg.page_tokens + 1
+    dev, host, ic, w = _pair(cfg, 1, pps, seed=831)
+    k, v = kv_rows(rng, L0, cfg)
+    host.append(k, v, np.arange(L0, dtype=np.int32))
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                    torch.arange(L0, dtype=torch.int32, device="cuda"))
+    kr = rng.standard_normal((L0, 128)).astype(np.float32)
+    qsa.idx_append_pool(ic, torch.from_numpy(kr).cuda(), torch.arange(L0, dtype=torch.int32, device="cuda"))
+    c = cfg_of(cfg)
+    Lmax = L0 + 6
+    ws = _ws(cfg, ic, 1, Lmax)
+    msel = c.max_selected(Lmax)
+    for step in range(6):
+        p = L0 + step
+        kn, vn = kv_rows(rng, 1, cfg)
+        xr = rng.standard_normal((1, 128)).astype(np.float32)
+        q = rng.standard_normal((1, 24, 256)).astype(np.float32)
+        qi = rng.standard_normal((1, 4, 128)).astype(np.float32)
+        pos = torch.tensor([p], dtype=torch.int32, device="cuda")
+        qsa.append_q8_0(dev, torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda(), pos)
+        qsa.idx_append_pool(ic, torch.from_numpy(xr).cuda(), pos)
+        L = torch.tensor([p + 1], dtype=torch.int32, device="cuda")
+        sel = torch.empty((1, 2, msel), dtype=torch.int32, device="cuda")
+        nsel = torch.empty((1, 2), dtype=torch.int32, device="cuda")
+        qsa.idx_select(ic, torch.from_numpy(qi).cuda(), L, Lmax, ws, sel=sel, n_sel=nsel)
+        out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), L, Lmax, ws, sel=sel, n_sel=nsel)
+        torch.cuda.synchronize()
+        host.append(kn, vn, [p])
+        kr = np.concatenate([kr, xr])
+        want = oracle_select(cfg, ICFG, np_of(ic.pooled)[0], qi[0], p + 1, msel)
+        np.testing.assert_array_equal(np_of(ic.pooled)[0, p // 4],
+                                      oracle_pool_all(cfg, ICFG, kr.astype(np.float16), w, p // 4 + 1)[p // 4])
+        gs, gn = np_of(sel), np_of(nsel)
+        hs = np.full((1, 2, msel), -1, np.int32)
+        for g in range(2):
+            assert gn[0, g] == len(want)
+            np.testing.assert_array_equal(gs[0, g, :gn[0, g]], want, err_msg=f"step {step} head {g}")
+            hs[0, g, :len(want)] = want
+        ref = host.attention_f64(q, [p + 1], hs, gn)
+        assert_close_attn(np_of(out), ref, f"step {step}")
+    assert qsa.read_status(dev) == 0
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_checkpoint_prefill(dtype):
+    """A prefill chunk with the checkpoint's indexer: K/V and raw keys appended,
+    the touched blocks pooled, each query selected by its q_idx and attending
+    causally -- selections for every query, outputs for a sample."""
+    cfg = CKPT
+    rng = np.random.default_rng(840)
+    pre, n_q = 2600, 203
+    end = pre + n_q
+    pps = end // cfg.page_tokens + 1
+    dev, host, ic, w = _pair(cfg, 1, pps, seed=841)
+    k, v = kv_rows(rng, pre, cfg)
+    host.append(k, v, np.arange(pre, dtype=np.int32))
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                    torch.arange(pre, dtype=torch.int32, device="cuda"))
+    kr0 = rng.standard_normal((pre, 128)).astype(np.float32)
+    qsa.idx_append_pool(ic, torch.from_numpy(kr0).cuda(), torch.arange(pre, dtype=torch.int32, device="cuda"))
+    kn, vn = kv_rows(rng, n_q, cfg)
+    kn, vn = kn.astype(dtype), vn.astype(dtype)
+    krn = rng.standard_normal((n_q, 128)).astype(dtype)
+    q = rng.standard_normal((n_q, 24, 256)).astype(np.float32)
+    qi = rng.standard_normal((n_q, 4, 128)).astype(np.float32)
+    c = cfg_of(cfg)
+    msel = c.max_selected(end)
+    sel = torch.empty((n_q, 2, msel), dtype=torch.int32, device="cuda")
+    nsel = torch.empty((n_q, 2), dtype=torch.int32, device="cuda")
+    ws = qsa.Workspace.for_prefill(c, end, 64)
+    out = qsa.idx_sparse_attn_prefill(ic, torch.from_numpy(q).cuda(), torch.from_numpy(qi).cuda(), 0, pre, ws,
+                                      k_new=torch.from_numpy(kn).cuda(), v_new=torch.from_numpy(vn).cuda(),
+                                      k_raw=torch.from_numpy(krn).cuda(), sel=sel, n_sel=nsel)
+    torch.cuda.synchronize()
+    assert qsa.read_status(dev) == 0
+    host.append(kn, vn, np.arange(pre, end, dtype=np.int32))
+    allr = np.concatenate([kr0.astype(np.float16), krn.astype(np.float16)])
+    nb = (end + 3) // 4
+    pooled = np_of(ic.pooled)[0]
+    np.testing.assert_array_equal(pooled[:nb], oracle_pool_all(cfg, ICFG, allr, w, nb))
+    np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+    gs, gn, o = np_of(sel), np_of(nsel), np_of(out)
+    for i in range(n_q):
+        want = oracle_select(cfg, ICFG, pooled, qi[i], pre + i + 1, msel)
+        for g in range(2):
+            assert gn[i, g] == len(want), f"query {i}"
+            np.testing.assert_array_equal(gs[i, g, :gn[i, g]], want, err_msg=f"query {i} head {g}")
+        if i % 29 == 0 or i == n_q - 1:
+            ref = host.attention_f64(q[i:i + 1], [pre + i + 1], gs[i:i + 1], gn[i:i + 1])
+            assert_close_attn(o[i:i + 1], ref, f"query {i}")
