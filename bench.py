@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
+    ap.add_argument("--no-checkpoint", action="store_true",
+                    help="skip the checkpoint-layer decode line (the released model's own indexer)")
     ap.add_argument("--prefill-batch", type=int, default=8192,
                     help="queries per batch of the prefill chunk (sizes its workspace; 8192 = the whole "
                          "chunk in one batch, ~170 MB)")
@@ -66,9 +68,9 @@ def parse():
 
 # ---------------------------------------------------------------------------
 
-def fill_layer(qsa, torch, cache, lengths, gen, chunk=32768):
+def fill_layer(qsa, torch, cache, lengths, gen, chunk=32768, pool=True):
     """K/V ~ N(0,1) times a per-q8_0-block log-uniform [0.1, 10] scale, appended
-    for tokens [0, L_s) of each sequence, then every whole block pooled."""
+    for tokens [0, L_s) of each sequence, then (pool) every whole block pooled."""
     cfg = cache.cfg
     nb = cfg.head_dim // 32
     for s, L in enumerate(lengths):
@@ -83,7 +85,7 @@ def fill_layer(qsa, torch, cache, lengths, gen, chunk=32768):
             pos = torch.arange(t0, t0 + n, dtype=torch.int32, device="cuda")
             sid = torch.full((n,), s, dtype=torch.int32, device="cuda")
             qsa.append_q8_0(cache, kv[0], kv[1], pos, sid)
-        if L // cfg.block_tokens:
+        if pool and L // cfg.block_tokens:
             qsa.pool_rebuild(cache, s, L // cfg.block_tokens)
 
 
@@ -335,6 +337,116 @@ def bench_prefill(qsa, torch, cfg, gen, q_batch, reps=3):
                 "fp32 operands as fp16 hi + lo pairs); frac is against the dense fp16/bf16 MFMA peak")
 
 
+class CheckpointRunner:
+    """The released checkpoint's attention layer (24 query heads, 2 KV heads of
+    256, q8_0 KV, blocks of 4 tokens pooled by its own indexer of 4 heads x 128,
+    513 kept blocks) stepped one decode token at a time: per layer the K/V
+    append, the raw indexer key + its block's pooled key, the indexer's
+    selection and the attention -- five launches."""
+
+    def __init__(self, qsa, torch, ctx, n_layer, gen):
+        self.qsa, self.torch = qsa, torch
+        cfg = self.cfg = qsa.checkpoint_config()
+        icfg = qsa.IdxConfig()
+        self.max_len = ctx + DECODE_ROOM
+        pps = (self.max_len + cfg.page_tokens - 1) // cfg.page_tokens
+        pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+        self.layers = []
+        for _ in range(n_layer):
+            c = qsa.KvCache.allocate(cfg, 1, pps, page_table=pt, n_phys_pages=pps)
+            fill_layer(qsa, torch, c, [ctx], gen, pool=False)
+            ic = qsa.IdxCache.allocate(icfg, c, torch.rand(icfg.idx_dim, device="cuda", generator=gen) + 0.5)
+            for t0 in range(0, ctx, 32768):
+                n = min(32768, ctx - t0)
+                kr = torch.randn((n, icfg.idx_dim), device="cuda", generator=gen)
+                qsa.idx_append_pool(ic, kr, torch.arange(t0, t0 + n, dtype=torch.int32, device="cuda"))
+            self.layers.append((c, ic))
+        H, Hkv, hd = cfg.n_head, cfg.n_head_kv, cfg.head_dim
+        r = lambda *s: torch.randn(s, device="cuda", generator=gen)
+        self.q = [r(1, H, hd) for _ in range(n_layer)]
+        self.qi = [r(1, icfg.n_idx_head, icfg.idx_dim) for _ in range(n_layer)]
+        self.kn = [r(1, Hkv, hd) for _ in range(n_layer)]
+        self.vn = [r(1, Hkv, hd) for _ in range(n_layer)]
+        self.kr = [r(1, icfg.idx_dim) for _ in range(n_layer)]
+        self.out = [torch.empty((1, H, hd), device="cuda") for _ in range(n_layer)]
+        self.seq_len = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+        self.pos = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
+        ic0 = self.layers[0][1]
+        self.ws = qsa.Workspace(cfg, 1, self.max_len, nbytes=max(cfg.workspace_bytes(1, self.max_len),
+                                                                 ic0.workspace_bytes(1, self.max_len)))
+        msel = cfg.max_selected(self.max_len)
+        self.sel = torch.empty((1, Hkv, msel), dtype=torch.int32, device="cuda")
+        self.nsel = torch.empty((1, Hkv), dtype=torch.int32, device="cuda")
+        self.n_layer = n_layer
+        torch.cuda.synchronize()
+
+    def layer(self, il):
+        qsa = self.qsa
+        c, ic = self.layers[il]
+        qsa.append_q8_0(c, self.kn[il], self.vn[il], self.pos)
+        qsa.idx_append_pool(ic, self.kr[il], self.pos)
+        qsa.idx_select(ic, self.qi[il], self.seq_len, self.max_len, self.ws, sel=self.sel, n_sel=self.nsel)
+        qsa.sparse_decode_attn(c, self.q[il], self.seq_len, self.max_len, self.ws, self.sel, self.nsel,
+                               out=self.out[il])
+
+    def step(self):
+        self.seq_len.add_(1)
+        self.pos.add_(1)
+        for il in range(self.n_layer):
+            self.layer(il)
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            self.step()
+        e1.record()
+        torch.cuda.synchronize()
+        eager = e0.elapsed_time(e1) / steps
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        # the replay against an eager step from the same position
+        p0 = self.seq_len.clone()
+        self.seq_len.copy_(p0); self.pos.copy_(p0 - 1)
+        self.step()
+        torch.cuda.synchronize()
+        ref = [o.clone() for o in self.out]
+        self.seq_len.copy_(p0); self.pos.copy_(p0 - 1)
+        g.replay()
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
+            raise RuntimeError("checkpoint graph replay differs from the eager step")
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph = e0.elapsed_time(e1) / steps
+        if int(self.seq_len.item()) > self.max_len:
+            raise RuntimeError("checkpoint decode ran past DECODE_ROOM")
+        n = int(self.nsel[0, 0].item())
+        L = int(self.seq_len.item())
+        blocks = self.sel[0, 0, :n].cpu().tolist()
+        cells = sum(max(0, min(4, L - 4 * b)) for b in blocks)
+        row = self.cfg.head_dim + self.cfg.head_dim // 32 * 2
+        return dict(us_per_layer=graph * 1e3 / self.n_layer, eager_us_per_layer=eager * 1e3 / self.n_layer,
+                    blocks_kept=n, cells_per_kv_head=cells,
+                    selected_kv_bytes=cells * row * 2 * self.cfg.n_head_kv)
+
+
 def cpu_baseline(cfg, ctx, seconds, seed):
     """The oracle's fp32 decode step (the ggml CPU path restated: append,
     pool, scores, selection, attention over fp16-cast K/V) on one layer at
@@ -453,6 +565,21 @@ def main():
         log(f"[bench] config 4 prefill chunk (8192 queries at 155648): {prefill['ms_per_chunk']:.3f} ms, "
             f"{prefill['attn_tflops']:.1f} TFLOP/s on the selected-cell FLOPs")
 
+    checkpoint = None
+    if not args.no_checkpoint:
+        ck = {}
+        for ctx in (min(contexts), max(contexts)):
+            r = CheckpointRunner(qsa, torch, ctx, args.layers, gen)
+            ck[str(ctx)] = {k: (round(v, 3) if isinstance(v, float) else v)
+                            for k, v in r.run(max(20, args.steps // 3), args.warmup).items()}
+            log(f"[bench] checkpoint layer ctx {ctx}: {ck[str(ctx)]['us_per_layer']:.2f} us/layer "
+                f"(eager {ck[str(ctx)]['eager_us_per_layer']:.2f}), {ck[str(ctx)]['blocks_kept']} blocks kept")
+            del r
+            torch.cuda.empty_cache()
+        checkpoint = dict(per_context=ck, workload="the released checkpoint's attention layer: 24q/2kv heads "
+                          "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
+                          "keys), 513 kept blocks shared by both KV heads; 5 launches per layer, hipGraph")
+
     big = max(contexts)
     small = min(contexts)
     top = per_ctx[big]
@@ -508,6 +635,7 @@ def main():
         "layer_roofline_frac": round(top["layer_gbs_selected"] / HBM_PEAK_GBS, 4),
         "batched_config5": batched,
         "prefill_config4": prefill,
+        "checkpoint_decode": checkpoint,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }

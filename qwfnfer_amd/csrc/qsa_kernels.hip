@@ -9,6 +9,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "qsa_device.h"
 
 namespace qwfn_qsa {
@@ -496,24 +498,33 @@ __device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const Fus
 }
 
 
-template <int NB> __device__ void find_bin(IdxShared &sh, int need);
+// ---------------------------------------------------------------------------
+// block selection
+// ---------------------------------------------------------------------------
+// The routines below are templates over the workgroup size NT and its LDS
+// struct SH: IdxShared for the 256-thread indexer workgroup, BigSelShared for
+// the 1024-thread selection of long contexts (k_select_big).  SH provides
+// hist[4096 + 64], cand_key / cand_b[kCandMax + 1], tmask[NT] (32 or 64 bits a
+// thread), selbits, red[2 * NT/64], tmp[NT/64] and bin, need, ncand, cnt_b.
+
+template <int NT, int NB, typename SH> __device__ void find_bin(SH &sh, int need);
 
 // One radix pass over the eligible keys that match `prefix` above bit
 // shift+BITS: histogram of the BITS-bit digit at `shift`, then the digit of
 // the need-th largest key.  Updates prefix (appending the digit) and need.
-template <int BITS>
-__device__ void radix_pass(IdxShared &sh, const float *sc, int e_lo, int e_hi, int shift, uint32_t &prefix,
+template <int NT, int BITS, typename SH>
+__device__ void radix_pass(SH &sh, const float *sc, int e_lo, int e_hi, int shift, uint32_t &prefix,
                            int &need, bool first) {
     constexpr int NB = 1 << BITS;
     const int tid = threadIdx.x;
-    for (int i = tid; i < NB; i += kIdxThreads) sh.hist[i] = 0u;
+    for (int i = tid; i < NB; i += NT) sh.hist[i] = 0u;
     __syncthreads();
-    for (int b = e_lo + tid; b < e_hi; b += kIdxThreads) {
+    for (int b = e_lo + tid; b < e_hi; b += NT) {
         const uint32_t k = score_key(sc[b]);
         if (first || (k >> (shift + BITS)) == prefix) atomicAdd(&sh.hist[(k >> shift) & (NB - 1)], 1u);
     }
     __syncthreads();
-    find_bin<NB>(sh, need);
+    find_bin<NT, NB>(sh, need);
     prefix = first ? (uint32_t)sh.bin : ((prefix << BITS) | (uint32_t)sh.bin);
     need = sh.need;
     __syncthreads();
@@ -522,16 +533,16 @@ __device__ void radix_pass(IdxShared &sh, const float *sc, int e_lo, int e_hi, i
 // The digit of the need-th largest key from an NB-bin histogram in LDS
 // (bins in ascending key order): sh.bin = that digit, sh.need = how many keys
 // of that bin are still needed.  All threads call.
-template <int NB>
-__device__ void find_bin(IdxShared &sh, int need) {
-    constexpr int PER = NB / kIdxThreads > 0 ? NB / kIdxThreads : 1;
+template <int NT, int NB, typename SH>
+__device__ void find_bin(SH &sh, int need) {
+    constexpr int PER = NB / NT > 0 ? NB / NT : 1;
     const int tid = threadIdx.x;
     int own = 0;
     if (tid * PER < NB)
 #pragma unroll
         for (int i = 0; i < PER; ++i) own += (int)sh.hist[tid * PER + i];
     int total;
-    const int excl = block_excl_sum<kIdxThreads>(own, sh.tmp, &total);
+    const int excl = block_excl_sum<NT>(own, sh.tmp, &total);
     const int above = total - excl - own;          // keys in the bins of higher threads
     if (tid * PER < NB && above < need && above + own >= need) {
         int run = above;
@@ -544,9 +555,9 @@ __device__ void find_bin(IdxShared &sh, int need) {
     __syncthreads();
 }
 
-// Selection of one (sequence, KV head) by the last scoring workgroup: the
-// top_k eligible blocks by (score desc, index asc) on orderable 32-bit keys,
-// emitted ascending between the forced sink and window blocks.
+// Selection of one (sequence, KV head): the topk eligible blocks by (score
+// desc, index asc) on orderable 32-bit keys, emitted ascending between the
+// forced sink and window blocks.
 //
 // Register path (select_regs): thread t holds the KPT scores of blocks
 // base + [t*KPT, t*KPT+KPT) (base = e_lo rounded down to 4) in registers,
@@ -558,16 +569,22 @@ __device__ void find_bin(IdxShared &sh, int need) {
 // usual case: near the threshold a bin holds about one key) every key of it
 // is taken; otherwise its keys are ranked exactly against each other.  Each
 // thread then publishes a bit mask of its taken blocks and wave 0 writes them
-// in order.  The code is straight-line and predicated where it can be: it
-// runs once per layer in one workgroup, from a cold instruction cache.
+// in order.  The code is straight-line and predicated where it can be: in
+// the indexer it runs once per layer in one workgroup, from a cold
+// instruction cache.  KEEP keeps each key's bin in a register (else it is
+// recomputed from the key: the 1024-thread variant has half the registers).
 //
 // Fallback (select_radix): a threshold bin of more than kCandMax keys (heavy
 // ties) or more eligible blocks than the register path holds takes three
 // radix passes over the keys in memory and an index-ordered tie count.
-template <int KPT>
+template <int NT, int KPT, bool KEEP, typename SH>
 __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const Ranges &r, int topk,
-                                            int32_t *out, IdxShared &sh) {
-    static_assert(KPT % 4 == 0 && KPT <= 32, "KPT: whole 16-byte vectors, at most 32 bits per thread");
+                                            int32_t *out, SH &sh) {
+    static_assert(KPT % 4 == 0 && (KPT <= 32 || (KPT % 8 == 0 && KPT <= 48) || KPT == 64),
+                  "KPT: whole 16-byte vectors, a thread's bits within two aligned words");
+    using MT = typename std::conditional<(KPT > 32), uint64_t, uint32_t>::type;
+    static_assert(sizeof(sh.tmask) >= NT * sizeof(MT), "tmask holds a thread's bits");
+    static_assert(sizeof(sh.selbits) >= (NT * KPT / 32 + 1) * 4, "selbits holds every key's bit");
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int base = r.e_lo & ~3;
     const int b0 = base + tid * KPT;
@@ -590,31 +607,36 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     }
     hi = wave_max(hi);
     lo = -wave_max(-lo);
-    if (lane == 0) { sh.red[wid] = hi; sh.red[kIdxThreads / 64 + wid] = lo; }
+    if (lane == 0) { sh.red[wid] = hi; sh.red[NT / 64 + wid] = lo; }
     uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
 #pragma unroll
-    for (int i = 0; i < 4096 / 4 / kIdxThreads; ++i) h4[tid + i * kIdxThreads] = make_uint4(0u, 0u, 0u, 0u);
-    for (int i = tid; i < KPT * kIdxThreads / 32 + 1; i += kIdxThreads) sh.selbits[i] = 0u;
+    for (int i = 0; i < 4096 / 4 / NT; ++i) h4[tid + i * NT] = make_uint4(0u, 0u, 0u, 0u);
+    for (int i = tid; i < KPT * NT / 32 + 1; i += NT) sh.selbits[i] = 0u;
     if (tid == 0) sh.ncand = 0;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kIdxThreads / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[kIdxThreads / 64 + i]); }
+    for (int i = 0; i < NT / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[NT / 64 + i]); }
     const float span = hi - lo, scale = 4096.0f / span;
     const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
     // both bin maps, blended with a uniform mask (no per-element branch)
     const uint32_t lm = lin ? 0xffffffffu : 0u;
-    uint32_t bin[KPT];
+    auto bin_of = [&](float x) -> uint32_t {
+        const uint32_t lb = (uint32_t)fminf((x - lo) * scale, 4095.0f);   // x - lo >= 0 unless NaN
+        return ((x == x ? lb : 0u) & lm) | ((score_key(x) >> 20) & ~lm);
+    };
+    uint32_t bin[KEEP ? KPT : 1];
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-        const uint32_t lb = (uint32_t)fminf((sv[i] - lo) * scale, 4095.0f);   // sv - lo >= 0 unless NaN
-        bin[i] = ((sv[i] == sv[i] ? lb : 0u) & lm) | ((score_key(sv[i]) >> 20) & ~lm);
+        const uint32_t bi = bin_of(sv[i]);
+        if (KEEP) bin[i] = bi;
         // unconditional (no skip branch); masked-off keys go to this lane's
         // trash bin, so they never pile onto one address
-        atomicAdd(&sh.hist[valid(i) ? bin[i] : 4096u + (uint32_t)lane], 1u);
+        atomicAdd(&sh.hist[valid(i) ? bi : 4096u + (uint32_t)lane], 1u);
     }
+    auto bin_at = [&](int i) -> uint32_t { return KEEP ? bin[KEEP ? i : 0] : bin_of(sv[i]); };
     __syncthreads();
     // threshold bin, by wave 0: lane l sums bins [64l, 64l+64); the lane whose
-    // bins straddle the top_k-th largest key is found by a scan and a ballot,
+    // bins straddle the topk-th largest key is found by a scan and a ballot,
     // then its 64 bins are spread over the wave for the same search
     if (wid == 0) {
         uint32_t own = 0;
@@ -643,12 +665,12 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
         // rank the threshold bin's keys exactly: (key desc, index asc)
         int nc = 0;
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) nc += (valid(i) && bin[i] == B);
+        for (int i = 0; i < KPT; ++i) nc += (valid(i) && bin_at(i) == B);
         if (nc > 0) {
             int slot = atomicAdd(&sh.ncand, nc);
 #pragma unroll
             for (int i = 0; i < KPT; ++i) {
-                const bool c = valid(i) && bin[i] == B;
+                const bool c = valid(i) && bin_at(i) == B;
                 const int at = c ? slot : kCandMax;
                 sh.cand_key[at] = score_key(sv[i]);
                 sh.cand_b[at] = b0 + i;
@@ -669,33 +691,35 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
         __syncthreads();
     }
     // the thread's KPT bits start at bit tid*KPT: two words cover them
-    uint32_t wb = 0xffffffffu;
+    uint64_t wb = ~0ull;
     if (cB > need) {
         const int e = tid * KPT;
         const uint64_t w2 = (uint64_t)sh.selbits[e >> 5] | ((uint64_t)sh.selbits[(e >> 5) + 1] << 32);
-        wb = (uint32_t)(w2 >> (e & 31));
+        wb = w2 >> (e & 31);
     }
-    uint32_t m = 0;
+    MT m = 0;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-        const bool take = valid(i) && (bin[i] > B || (bin[i] == B && ((wb >> i) & 1u)));
-        m |= (uint32_t)take << i;
+        const uint32_t bi = bin_at(i);
+        const bool take = valid(i) && (bi > B || (bi == B && ((wb >> i) & 1u)));
+        m |= (MT)take << i;
     }
-    sh.tmask[tid] = m;
+    MT *tm = reinterpret_cast<MT *>(sh.tmask);
+    tm[tid] = m;
     __syncthreads();
-    // ordered emission by wave 0: lane l owns threads 4l .. 4l+3
+    // ordered emission by wave 0: lane l owns threads TPL*l .. TPL*l + TPL-1
     if (wid == 0) {
-        const uint4 mm = reinterpret_cast<const uint4 *>(sh.tmask)[lane];
-        const uint32_t w4[4] = {mm.x, mm.y, mm.z, mm.w};
-        const int cnt = __builtin_popcount(mm.x) + __builtin_popcount(mm.y) + __builtin_popcount(mm.z) +
-                        __builtin_popcount(mm.w);
+        constexpr int TPL = NT / 64;
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < TPL; ++q) cnt += (int)__builtin_popcountll((uint64_t)tm[TPL * lane + q]);
         int pos = wave_incl_scan(cnt) - cnt;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t x = w4[q];
-            const int tb = base + (4 * lane + q) * KPT;
+        for (int q = 0; q < TPL; ++q) {
+            uint64_t x = (uint64_t)tm[TPL * lane + q];
+            const int tb = base + (TPL * lane + q) * KPT;
             while (x) {
-                if (pos < topk) out[g.sink + pos] = tb + __builtin_ctz(x);
+                if (pos < topk) out[g.sink + pos] = tb + __builtin_ctzll(x);
                 ++pos;
                 x &= x - 1u;
             }
@@ -704,24 +728,165 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     return true;
 }
 
+// Streaming path (the 1024-thread k_select_big): thread t owns blocks base +
+// [t*per, t*per + per) (per <= 64, a multiple of 4, 64 when above 32 so its
+// bits sit in two aligned words) and reads them three times, each in one
+// round trip, keeping none in registers between the passes: min / max, the
+// 4096-bin histogram (as in the register path), then the take bits together
+// with the threshold bin's candidates.  After the candidates are ranked each
+// thread writes its taken blocks at its exclusive-scan offset.
+template <int NT, typename SH>
+__device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, const Ranges &r, int topk, int32_t *out,
+                                           SH &sh) {
+    constexpr int MAXV = 16;                       // 16-byte vectors a thread: 64 keys
+    static_assert(sizeof(sh.selbits) >= (NT * 4 * MAXV / 32 + 2) * 4, "selbits holds every key's bit");
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int base = r.e_lo & ~3;
+    int per = (((r.e_hi - base) + NT - 1) / NT + 3) & ~3;
+    if (per > 32) per = 64;
+    const int nv = per / 4;
+    const int b0 = base + tid * per;
+    const uint32_t nrec = (uint32_t)((r.e_hi + 3) & ~3) * 4u;
+    const BufRsrc rs = buf_rsrc(sc, nrec);
+    // unconditional loads: vectors past this thread's share read past the
+    // buffer's end and return 0 without a memory access
+#define QWFN_STREAM_LOAD(x)                                                                  \
+    float x[4 * MAXV];                                                                       \
+    _Pragma("unroll") for (int k = 0; k < MAXV; ++k) {                                       \
+        const auto v_ = BufLoad<4, kCpolSc1>::at(rs, k < nv ? (b0 + 4 * k) * 4 : (int)nrec, 0); \
+        x[4 * k] = v_[0]; x[4 * k + 1] = v_[1]; x[4 * k + 2] = v_[2]; x[4 * k + 3] = v_[3];  \
+    }
+    auto valid = [&](int i) { return (i >> 2) < nv && b0 + i >= r.e_lo && b0 + i < r.e_hi; };
+    QWFN_STREAM_LOAD(x)
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4 * MAXV; ++i) {
+        const bool use = valid(i) && x[i] == x[i];
+        lo = fminf(lo, use ? x[i] : INFINITY);
+        hi = fmaxf(hi, use ? x[i] : -INFINITY);
+    }
+    hi = wave_max(hi);
+    lo = -wave_max(-lo);
+    if (lane == 0) { sh.red[wid] = hi; sh.red[NT / 64 + wid] = lo; }
+    uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
+    for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+    for (int i = tid; i < NT * per / 32 + 2; i += NT) sh.selbits[i] = 0u;
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[NT / 64 + i]); }
+    const float span = hi - lo, scale = 4096.0f / span;
+    const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
+    const uint32_t lm = lin ? 0xffffffffu : 0u;
+    auto bin_of = [&](float v) -> uint32_t {
+        const uint32_t lb = (uint32_t)fminf((v - lo) * scale, 4095.0f);
+        return ((v == v ? lb : 0u) & lm) | ((score_key(v) >> 20) & ~lm);
+    };
+    {
+        QWFN_STREAM_LOAD(y)
+#pragma unroll
+        for (int i = 0; i < 4 * MAXV; ++i)
+            atomicAdd(&sh.hist[valid(i) ? bin_of(y[i]) : 4096u + (uint32_t)lane], 1u);
+    }
+    __syncthreads();
+    if (wid == 0) {                                // the threshold bin, as in the register path
+        uint32_t own = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const uint4 y = h4[lane * 16 + k];
+            own += y.x + y.y + y.z + y.w;
+        }
+        const int incl = wave_incl_scan((int)own);
+        const int total = __builtin_amdgcn_readlane(incl, 63);
+        const int above = total - incl;
+        const int ls = __builtin_ctzll(__ballot(above < topk && above + (int)own >= topk));
+        const int above_l = __builtin_amdgcn_readlane(above, ls);
+        const int c = (int)sh.hist[ls * 64 + lane];
+        const int ic = wave_incl_scan(c);
+        const int run = above_l + __builtin_amdgcn_readlane(ic, 63) - ic;
+        const int j = __builtin_ctzll(__ballot(run < topk && run + c >= topk));
+        if (lane == j) { sh.bin = ls * 64 + j; sh.need = topk - run; sh.cnt_b = c; }
+    }
+    __syncthreads();
+    const uint32_t B = (uint32_t)sh.bin;
+    const int need = sh.need;
+    const int cB = sh.cnt_b;
+    if (cB > kCandMax) return false;
+    const bool rank = cB > need;                   // else every key of bin B is taken
+    uint64_t m = 0;
+    {
+        QWFN_STREAM_LOAD(z)
+        uint64_t cm = 0;                           // the threshold bin's keys
+#pragma unroll
+        for (int i = 0; i < 4 * MAXV; ++i) {
+            const uint32_t bi = bin_of(z[i]);
+            const bool v = valid(i);
+            m |= (uint64_t)(v && (bi > B || (!rank && bi == B))) << i;
+            cm |= (uint64_t)(rank && v && bi == B) << i;
+        }
+        if (cm) {
+            int slot = atomicAdd(&sh.ncand, (int)__builtin_popcountll(cm));
+            while (cm) {
+                const int i = __builtin_ctzll(cm);
+                float zi = z[0];
+#pragma unroll
+                for (int k = 1; k < 4 * MAXV; ++k) zi = k == i ? z[k] : zi;
+                sh.cand_key[slot] = score_key(zi);
+                sh.cand_b[slot] = b0 + i;
+                ++slot;
+                cm &= cm - 1ull;
+            }
+        }
+    }
+#undef QWFN_STREAM_LOAD
+    if (rank) {
+        __syncthreads();
+        if (tid < cB) {
+            const uint32_t k = sh.cand_key[tid];
+            const int b = sh.cand_b[tid];
+            int rk = 0;
+            for (int jj = 0; jj < cB; ++jj) {
+                const uint32_t kj = sh.cand_key[jj];
+                rk += (kj > k) || (kj == k && sh.cand_b[jj] < b);
+            }
+            if (rk < need) atomicOr(&sh.selbits[(b - base) >> 5], 1u << ((b - base) & 31));
+        }
+        __syncthreads();
+        const int e = tid * per;                   // per <= 32 or per == 64: two words hold the bits
+        const uint64_t w2 = (uint64_t)sh.selbits[e >> 5] | ((uint64_t)sh.selbits[(e >> 5) + 1] << 32);
+        const uint64_t mine = per == 64 ? ~0ull : ((1ull << per) - 1ull);
+        m |= (w2 >> (e & 31)) & mine;
+    }
+    const int cnt = (int)__builtin_popcountll(m);
+    int tot;
+    int pos = block_excl_sum<NT>(cnt, sh.tmp, &tot);
+    while (m) {
+        if (pos < topk) out[g.sink + pos] = b0 + __builtin_ctzll(m);
+        ++pos;
+        m &= m - 1ull;
+    }
+    return true;
+}
+
+template <int NT, typename SH>
 __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, const Ranges &r, int topk,
-                                                       int32_t *out, IdxShared &sh) {
+                                                       int32_t *out, SH &sh) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads of the scores below
     const int tid = threadIdx.x;
     const int ne = r.e_hi - r.e_lo;
-    const int per = (ne + kIdxThreads - 1) / kIdxThreads;
+    const int per = (ne + NT - 1) / NT;
     const int b0 = r.e_lo + tid * per;
     const int b1 = min(b0 + per, r.e_hi);
     __syncthreads();                               // the register path may still read sh.hist
     uint32_t prefix = 0;
     int need = topk;
-    radix_pass<12>(sh, sc, r.e_lo, r.e_hi, 20, prefix, need, true);
-    radix_pass<12>(sh, sc, r.e_lo, r.e_hi, 8, prefix, need, false);
-    radix_pass<8>(sh, sc, r.e_lo, r.e_hi, 0, prefix, need, false);
+    radix_pass<NT, 12>(sh, sc, r.e_lo, r.e_hi, 20, prefix, need, true);
+    radix_pass<NT, 12>(sh, sc, r.e_lo, r.e_hi, 8, prefix, need, false);
+    radix_pass<NT, 8>(sh, sc, r.e_lo, r.e_hi, 0, prefix, need, false);
     const uint32_t T = prefix;
     int tot, eq = 0;
     for (int b = b0; b < b1; ++b) eq += (score_key(sc[b]) == T);
-    int eqi = block_excl_sum<kIdxThreads>(eq, sh.tmp, &tot);
+    int eqi = block_excl_sum<NT>(eq, sh.tmp, &tot);
     int cnt = 0;
     {
         int e2 = eqi;
@@ -732,7 +897,7 @@ __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, cons
             cnt += tk;
         }
     }
-    int pos = g.sink + block_excl_sum<kIdxThreads>(cnt, sh.tmp, &tot);
+    int pos = g.sink + block_excl_sum<NT>(cnt, sh.tmp, &tot);
     for (int b = b0; b < b1; ++b) {
         const uint32_t k = score_key(sc[b]);
         bool tk = k > T;
@@ -741,32 +906,40 @@ __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, cons
     }
 }
 
+// Eligible blocks the register path of an NT-thread selection holds.
+template <int NT> constexpr int keys_max() { return NT == kIdxThreads ? kKeysMax : 64 * NT; }
+
+template <int NT, typename SH>
 __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out, int32_t *nout,
-                                              IdxShared &sh) {
+                                              SH &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     const int ne = r.e_hi - r.e_lo;
     const int topk = eff_topk(g, r);
     if (g.topk <= 0 || ne <= topk) {
         const int n = r.b_last + 1;
-        for (int i = tid; i < n; i += kIdxThreads) out[i] = i;
+        for (int i = tid; i < n; i += NT) out[i] = i;
         if (tid == 0) *nout = n;
         return;
     }
     if (topk > 0) {                               // (none scored when the forced blocks fill the count)
         bool done = false;
         const int span = r.e_hi - (r.e_lo & ~3);  // blocks the register path covers
-        if (span <= 4 * kIdxThreads) done = select_regs<4>(g, sc, r, topk, out, sh);
-        else if (span <= 8 * kIdxThreads) done = select_regs<8>(g, sc, r, topk, out, sh);
-        else if (span <= 12 * kIdxThreads) done = select_regs<12>(g, sc, r, topk, out, sh);
-        else if (span <= 16 * kIdxThreads) done = select_regs<16>(g, sc, r, topk, out, sh);
-        else if (span <= 24 * kIdxThreads) done = select_regs<24>(g, sc, r, topk, out, sh);
-        else if (span <= kKeysMax) done = select_regs<kKeysMax / kIdxThreads>(g, sc, r, topk, out, sh);
-        if (!done) select_radix(g, sc, r, topk, out, sh);
+        if constexpr (NT == kIdxThreads) {
+            if (span <= 4 * NT) done = select_regs<NT, 4, true>(g, sc, r, topk, out, sh);
+            else if (span <= 8 * NT) done = select_regs<NT, 8, true>(g, sc, r, topk, out, sh);
+            else if (span <= 12 * NT) done = select_regs<NT, 12, true>(g, sc, r, topk, out, sh);
+            else if (span <= 16 * NT) done = select_regs<NT, 16, true>(g, sc, r, topk, out, sh);
+            else if (span <= 24 * NT) done = select_regs<NT, 24, true>(g, sc, r, topk, out, sh);
+            else if (span <= keys_max<NT>()) done = select_regs<NT, keys_max<NT>() / NT, true>(g, sc, r, topk, out, sh);
+        } else {
+            if (span <= keys_max<NT>()) done = select_stream<NT>(g, sc, r, topk, out, sh);
+        }
+        if (!done) select_radix<NT>(g, sc, r, topk, out, sh);
     }
-    for (int i = tid; i < g.sink; i += kIdxThreads) out[i] = i;
+    for (int i = tid; i < g.sink; i += NT) out[i] = i;
     const int nwin = r.b_last - r.fw + 1;
-    for (int i = tid; i < nwin; i += kIdxThreads) out[g.sink + topk + i] = r.fw + i;
+    for (int i = tid; i < nwin; i += NT) out[g.sink + topk + i] = r.fw + i;
     if (tid == 0) *nout = g.sink + topk + nwin;
 }
 
@@ -776,27 +949,27 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
 // KV head's group summed first).  Called by the one workgroup that saw every
 // head's scores: it sums the rows into row 0 (device-coherent loads of the
 // other workgroups' stores), selects on it and copies the selection, and its
-// count, to every head's row.
+// count, to every one of g.sel_rows selection rows.
+template <int NT, typename SH>
 __device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t sc_stride, int L, int32_t *out0,
-                                              int64_t out_stride, int32_t *nout0, IdxShared &sh) {
-    // scores: g.Hkv rows; selection: g.sel_rows rows
+                                              int64_t out_stride, int32_t *nout0, SH &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     const BufRsrc rs = buf_rsrc(sc0, (uint32_t)(((int64_t)(g.Hkv - 1) * sc_stride + r.e_hi) * 4));
-    for (int b = r.e_lo + tid; b < r.e_hi; b += kIdxThreads) {
+    for (int b = r.e_lo + tid; b < r.e_hi; b += NT) {
         float acc = BufLoad<1, kCpolSc1>::at(rs, b * 4, 0)[0];
         for (int h = 1; h < g.Hkv; ++h) acc += BufLoad<1, kCpolSc1>::at(rs, (int)((h * sc_stride + b) * 4), 0)[0];
         sc0[b] = acc;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the summed row, for the selection's loads
     __syncthreads();
-    select_blocks(g, sc0, L, out0, nout0, sh);
+    select_blocks<NT>(g, sc0, L, out0, nout0, sh);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the selection, for the copy below
     __syncthreads();
     const BufRsrc ro = buf_rsrc(out0, (uint32_t)out_stride * 4u);
     const BufRsrc rn = buf_rsrc(nout0, 4u);
     const int n = __builtin_bit_cast(int, BufLoad<1, kCpolSc1>::at(rn, 0, 0)[0]);
-    for (int i = tid; i < n; i += kIdxThreads) {
+    for (int i = tid; i < n; i += NT) {
         const int32_t x = __builtin_bit_cast(int32_t, BufLoad<1, kCpolSc1>::at(ro, i * 4, 0)[0]);
         for (int h = 1; h < g.sel_rows; ++h) out0[h * out_stride + i] = x;
     }
@@ -804,11 +977,53 @@ __device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t 
         for (int h = 1; h < g.sel_rows; ++h) nout0[h] = n;
 }
 
+// The selection of long contexts (more eligible blocks than the indexer
+// workgroup's registers hold) as its own launch after a scoring-only
+// indexer: one 1024-thread workgroup per (sequence or prefill query, KV head)
+// -- per sequence with a shared selection -- holding up to 64 keys a thread.
+constexpr int kBigSelThreads = 1024;
+struct BigSelShared {
+    uint32_t hist[4096 + 64];
+    uint32_t cand_key[kCandMax + 1];
+    int32_t cand_b[kCandMax + 1];
+    uint32_t selbits[64 * kBigSelThreads / 32 + 2];
+    float red[2 * (kBigSelThreads / 64)];
+    int tmp[kBigSelThreads / 64];
+    int bin, need, ncand, cnt_b;
+};
+
+// grid (shared ? 1 : Hkv, n_seq or n_q)
+__global__ void __launch_bounds__(kBigSelThreads)
+k_select_big(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, float *scores, int32_t nb_cap,
+             int32_t *sel, int32_t *nsel, int32_t max_sel) {
+    __shared__ BigSelShared sh;
+    const int gh = blockIdx.x, s = blockIdx.y;
+    const int L = seq_length(g, g.pf ? 0 : seq_len[s], s);
+    if (L < 1 || L > max_seq_len) {
+        if (threadIdx.x == 0) {
+            if (g.shared)
+                for (int h = 0; h < g.sel_rows; ++h) nsel[s * g.sel_rows + h] = 0;
+            else
+                nsel[s * g.Hkv + gh] = 0;
+            set_status(v.status, QWFN_STATUS_LEN_RANGE);
+        }
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // the scoring launch's stores
+    if (g.shared)
+        select_shared<kBigSelThreads>(g, scores + (int64_t)s * g.Hkv * nb_cap, nb_cap, L,
+                                      sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
+    else
+        select_blocks<kBigSelThreads>(g, scores + ((int64_t)s * g.Hkv + gh) * nb_cap, L,
+                                      sel + ((int64_t)s * g.Hkv + gh) * max_sel, nsel + s * g.Hkv + gh, sh);
+}
+
 // grid (n_chunks [+1 with the fused append], Hkv, n_seq)
 template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
 k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
-          int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t n_chunks, FusedAppend fa) {
+          int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t n_chunks, FusedAppend fa,
+          int32_t select_here) {
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
@@ -872,6 +1087,8 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
             __syncthreads();                       // q reads done before the union is reused
         }
     }
+    // selection in a launch of its own (long contexts: k_select_big)
+    if (!select_here) return;
     // completion count: the last workgroup of this (sequence, KV head) -- of
     // this sequence with a shared selection -- selects; the selection reads
     // the scores with device-coherent loads (or fences)
@@ -890,10 +1107,10 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         return;
     }
     if (g.shared)
-        select_shared(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L,
+        select_shared<kIdxThreads>(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L,
                       sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
     else
-        select_blocks(g, sc, L, out, nsel + pair, sh);
+        select_blocks<kIdxThreads>(g, sc, L, out, nsel + pair, sh);
 }
 
 template <int HD, int G>
@@ -905,8 +1122,13 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
     int n_chunks = (nb_max + kBlocksPerChunk - 1) / kBlocksPerChunk;
     if (n_chunks < 1) n_chunks = 1;
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
+    const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
-                       sel, nsel, max_sel, ws, n_chunks, fa);
+                       sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)!big);
+    if (big)
+        hipLaunchKernelGGL(k_select_big, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
+                           dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws.scores, ws.nb_cap, sel,
+                           nsel, max_sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -1874,10 +2096,10 @@ k_pf_select(Geo g, float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, i
     const int gh = blockIdx.x, s = blockIdx.y;             // (gh = 0 with a shared selection)
     const int pair = s * g.Hkv + gh;
     if (g.shared)
-        select_shared(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1,
+        select_shared<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1,
                       sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
     else
-        select_blocks(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
+        select_blocks<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
                       nsel + pair, sh);
 }
 
@@ -1892,8 +2114,13 @@ static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *
         hipLaunchKernelGGL((k_pf_scores<HD, G>), grid, dim3(256), 0, st, g, v, q, n_q, n_blk, ws.scores,
                            ws.nb_cap);
     }
-    hipLaunchKernelGGL(k_pf_select, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_q), dim3(kIdxThreads), 0, st,
-                       g, ws.scores, ws.nb_cap, sel, nsel, max_sel);
+    if (n_blk > kKeysMax)
+        hipLaunchKernelGGL(k_select_big, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_q),
+                           dim3(kBigSelThreads), 0, st, g, v, nullptr, max_seq_len, ws.scores, ws.nb_cap, sel,
+                           nsel, max_sel);
+    else
+        hipLaunchKernelGGL(k_pf_select, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_q), dim3(kIdxThreads),
+                           0, st, g, ws.scores, ws.nb_cap, sel, nsel, max_sel);
 }
 
 // ---------------------------------------------------------------------------

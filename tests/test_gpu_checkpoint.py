@@ -219,3 +219,107 @@ def test_checkpoint_prefill(dtype):
         if i % 29 == 0 or i == n_q - 1:
             ref = host.attention_f64(q[i:i + 1], [pre + i + 1], gs[i:i + 1], gn[i:i + 1])
             assert_close_attn(o[i:i + 1], ref, f"query {i}")
+
+
+# ---- long contexts: more eligible blocks than the indexer workgroup's
+# registers hold (8192), selected by the 1024-thread k_select_big ----------------
+
+@pytest.mark.parametrize("lengths,tie", [([40003], False), ([33000, 45001], False), ([36000], True)])
+def test_idx_select_long_context(lengths, tie):
+    """The checkpoint selection over 8,250 .. 11,250 blocks; `tie`: all-zero raw
+    keys, so every block scores the same and the index order decides (the
+    threshold bin overflows the candidate list: the radix fallback)."""
+    cfg = CKPT
+    rng = np.random.default_rng(850 + sum(lengths) + tie)
+    n = len(lengths)
+    pps = max(lengths) // cfg.page_tokens + 1
+    dev, host, ic, w = _pair(cfg, n, pps, seed=851)
+    for s, L in enumerate(lengths):
+        kr = np.zeros((L, 128), np.float32) if tie else rng.standard_normal((L, 128)).astype(np.float32)
+        qsa.idx_append_pool(ic, torch.from_numpy(kr).cuda(), torch.arange(L, dtype=torch.int32, device="cuda"),
+                            seq_ids=torch.full((L,), s, dtype=torch.int32, device="cuda"))
+    q = rng.standard_normal((n, 4, 128)).astype(np.float32)
+    Lmax = max(lengths)
+    ws = _ws(cfg, ic, n, Lmax)
+    sel, nsel = qsa.idx_select(ic, torch.from_numpy(q).cuda(),
+                               torch.tensor(lengths, dtype=torch.int32, device="cuda"), Lmax, ws)
+    torch.cuda.synchronize()
+    gs, gn, pooled = np_of(sel), np_of(nsel), np_of(ic.pooled)
+    for s, L in enumerate(lengths):
+        want = oracle_select(cfg, ICFG, pooled[s], q[s], L, sel.shape[-1])
+        assert len(want) == 513
+        if tie:                                    # the lowest indices, and the partial tail
+            nb = L // 4
+            exp = list(range(513 - (1 if L % 4 else 0))) + ([nb] if L % 4 else [])
+            np.testing.assert_array_equal(want, np.array(exp, np.int32))
+        for g in range(2):
+            assert gn[s, g] == 513
+            np.testing.assert_array_equal(gs[s, g, :513], want, err_msg=f"seq {s} head {g}")
+    assert qsa.read_status(dev) == 0
+
+
+def test_per_head_selection_long_context():
+    """A per-KV-head selection (no shared selection) over 10,000 4-token blocks:
+    k_select_big with one workgroup per (sequence, KV head)."""
+    from _gpu import fill
+    from _refs import Cfg
+    cfg = Cfg(n_head=24, n_head_kv=2, head_dim=256, block_tokens=4, page_tokens=256, top_k_blocks=300,
+              sink_blocks=1, local_tokens=16)
+    rng = np.random.default_rng(860)
+    L = 40004
+    dev, host = make_pair(cfg, 1, L // 256 + 1, seed=861)
+    fill(dev, host, rng, [L])
+    q = rng.standard_normal((1, 24, 256)).astype(np.float32)
+    c = cfg_of(cfg)
+    ws = qsa.Workspace(c, 1, L)
+    sel, nsel = qsa.indexer_topk(dev, torch.from_numpy(q).cuda(), torch.tensor([L], dtype=torch.int32,
+                                                                                 device="cuda"), L, ws)
+    torch.cuda.synchronize()
+    hs, hn = host.indexer_topk(q, [L], max_sel=sel.shape[-1])
+    gs, gn = np_of(sel), np_of(nsel)
+    np.testing.assert_array_equal(gn, hn)
+    for g in range(2):
+        np.testing.assert_array_equal(gs[0, g, :gn[0, g]], hs[0, g, :hn[0, g]], err_msg=f"head {g}")
+    assert qsa.read_status(dev) == 0
+
+
+def test_checkpoint_prefill_long_context():
+    """Prefill queries at positions past 32,768 (over 8192 eligible blocks each):
+    the per-query selections come from k_select_big in prefill mode."""
+    cfg = CKPT
+    rng = np.random.default_rng(870)
+    pre, n_q = 36001, 37
+    end = pre + n_q
+    pps = end // cfg.page_tokens + 1
+    dev, host, ic, w = _pair(cfg, 1, pps, seed=871)
+    kr0 = rng.standard_normal((pre, 128)).astype(np.float32)
+    qsa.idx_append_pool(ic, torch.from_numpy(kr0).cuda(), torch.arange(pre, dtype=torch.int32, device="cuda"))
+    k, v = kv_rows(rng, pre, cfg)
+    host.append(k, v, np.arange(pre, dtype=np.int32))
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                    torch.arange(pre, dtype=torch.int32, device="cuda"))
+    kn, vn = kv_rows(rng, n_q, cfg)
+    krn = rng.standard_normal((n_q, 128)).astype(np.float32)
+    q = rng.standard_normal((n_q, 24, 256)).astype(np.float32)
+    qi = rng.standard_normal((n_q, 4, 128)).astype(np.float32)
+    c = cfg_of(cfg)
+    msel = c.max_selected(end)
+    sel = torch.empty((n_q, 2, msel), dtype=torch.int32, device="cuda")
+    nsel = torch.empty((n_q, 2), dtype=torch.int32, device="cuda")
+    ws = qsa.Workspace.for_prefill(c, end, n_q)
+    out = qsa.idx_sparse_attn_prefill(ic, torch.from_numpy(q).cuda(), torch.from_numpy(qi).cuda(), 0, pre, ws,
+                                      k_new=torch.from_numpy(kn).cuda(), v_new=torch.from_numpy(vn).cuda(),
+                                      k_raw=torch.from_numpy(krn).cuda(), sel=sel, n_sel=nsel)
+    torch.cuda.synchronize()
+    assert qsa.read_status(dev) == 0
+    host.append(kn, vn, np.arange(pre, end, dtype=np.int32))
+    pooled = np_of(ic.pooled)[0]
+    gs, gn, o = np_of(sel), np_of(nsel), np_of(out)
+    for i in range(n_q):
+        want = oracle_select(cfg, ICFG, pooled, qi[i], pre + i + 1, msel)
+        assert len(want) == 513
+        for g in range(2):
+            np.testing.assert_array_equal(gs[i, g, :gn[i, g]], want, err_msg=f"query {i} head {g}")
+        if i % 9 == 0:
+            ref = host.attention_f64(q[i:i + 1], [pre + i + 1], gs[i:i + 1], gn[i:i + 1])
+            assert_close_attn(o[i:i + 1], ref, f"query {i}")
