@@ -729,48 +729,56 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
 }
 
 // Streaming path (the 1024-thread k_select_big): thread t owns blocks base +
-// [t*per, t*per + per) (per <= 64, a multiple of 4, 64 when above 32 so its
-// bits sit in two aligned words) and reads them three times, each in one
-// round trip, keeping none in registers between the passes: min / max, the
-// 4096-bin histogram (as in the register path), then the take bits together
-// with the threshold bin's candidates.  After the candidates are ranked each
-// thread writes its taken blocks at its exclusive-scan offset.
+// [t*per, t*per + per) (per <= 64, a multiple of 4) and reads them three
+// times, each in one round trip, keeping none in registers between the
+// passes: min / max, the 4096-bin histogram (as in the register path), then
+// the take bits together with the threshold bin's candidates, which are
+// ranked in LDS; each owner then reads back its candidates' verdicts and
+// writes its taken blocks at its exclusive-scan offset.  Vectors past `per`
+// are skipped by a branch that is uniform over the workgroup.
 template <int NT, typename SH>
 __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, const Ranges &r, int topk, int32_t *out,
-                                           SH &sh) {
+                                              SH &sh) {
     constexpr int MAXV = 16;                       // 16-byte vectors a thread: 64 keys
-    static_assert(sizeof(sh.selbits) >= (NT * 4 * MAXV / 32 + 2) * 4, "selbits holds every key's bit");
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int base = r.e_lo & ~3;
-    int per = (((r.e_hi - base) + NT - 1) / NT + 3) & ~3;
-    if (per > 32) per = 64;
-    const int nv = per / 4;
+    const int per = (((r.e_hi - base) + NT - 1) / NT + 3) & ~3;
+    const int nv = per / 4;                        // uniform
     const int b0 = base + tid * per;
-    const uint32_t nrec = (uint32_t)((r.e_hi + 3) & ~3) * 4u;
-    const BufRsrc rs = buf_rsrc(sc, nrec);
-    // unconditional loads: vectors past this thread's share read past the
-    // buffer's end and return 0 without a memory access
-#define QWFN_STREAM_LOAD(x)                                                                  \
-    float x[4 * MAXV];                                                                       \
-    _Pragma("unroll") for (int k = 0; k < MAXV; ++k) {                                       \
-        const auto v_ = BufLoad<4, kCpolSc1>::at(rs, k < nv ? (b0 + 4 * k) * 4 : (int)nrec, 0); \
-        x[4 * k] = v_[0]; x[4 * k + 1] = v_[1]; x[4 * k + 2] = v_[2]; x[4 * k + 3] = v_[3];  \
+    const int i_lo = r.e_lo - b0, i_hi = r.e_hi - b0;   // this thread's valid slots: [i_lo, i_hi)
+    const BufRsrc rs = buf_rsrc(sc, (uint32_t)((r.e_hi + 3) & ~3) * 4u);
+#define QWFN_STREAM_LOAD(x)                                                                   \
+    float x[4 * MAXV];                                                                        \
+    _Pragma("unroll") for (int k = 0; k < MAXV; ++k) {                                        \
+        if (k < nv) {                                                                         \
+            const auto v_ = BufLoad<4, kCpolSc1>::at(rs, (b0 + 4 * k) * 4, 0);                \
+            x[4 * k] = v_[0]; x[4 * k + 1] = v_[1]; x[4 * k + 2] = v_[2]; x[4 * k + 3] = v_[3]; \
+        } else {                                                                              \
+            x[4 * k] = x[4 * k + 1] = x[4 * k + 2] = x[4 * k + 3] = 0.0f;                     \
+        }                                                                                     \
     }
-    auto valid = [&](int i) { return (i >> 2) < nv && b0 + i >= r.e_lo && b0 + i < r.e_hi; };
-    QWFN_STREAM_LOAD(x)
+    auto valid = [&](int i) { return i >= i_lo && i < i_hi; };
     float lo = INFINITY, hi = -INFINITY;
+    {
+        QWFN_STREAM_LOAD(x)
 #pragma unroll
-    for (int i = 0; i < 4 * MAXV; ++i) {
-        const bool use = valid(i) && x[i] == x[i];
-        lo = fminf(lo, use ? x[i] : INFINITY);
-        hi = fmaxf(hi, use ? x[i] : -INFINITY);
+        for (int k = 0; k < MAXV; ++k) {
+            if (k < nv) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 4 * k + j;
+                    const bool use = valid(i) && x[i] == x[i];
+                    lo = fminf(lo, use ? x[i] : INFINITY);
+                    hi = fmaxf(hi, use ? x[i] : -INFINITY);
+                }
+            }
+        }
     }
     hi = wave_max(hi);
     lo = -wave_max(-lo);
     if (lane == 0) { sh.red[wid] = hi; sh.red[NT / 64 + wid] = lo; }
     uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
     for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
-    for (int i = tid; i < NT * per / 32 + 2; i += NT) sh.selbits[i] = 0u;
     if (tid == 0) sh.ncand = 0;
     __syncthreads();
 #pragma unroll
@@ -785,8 +793,15 @@ __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, con
     {
         QWFN_STREAM_LOAD(y)
 #pragma unroll
-        for (int i = 0; i < 4 * MAXV; ++i)
-            atomicAdd(&sh.hist[valid(i) ? bin_of(y[i]) : 4096u + (uint32_t)lane], 1u);
+        for (int k = 0; k < MAXV; ++k) {
+            if (k < nv) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 4 * k + j;
+                    atomicAdd(&sh.hist[valid(i) ? bin_of(y[i]) : 4096u + (uint32_t)lane], 1u);
+                }
+            }
+        }
     }
     __syncthreads();
     if (wid == 0) {                                // the threshold bin, as in the register path
@@ -813,35 +828,41 @@ __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, con
     const int cB = sh.cnt_b;
     if (cB > kCandMax) return false;
     const bool rank = cB > need;                   // else every key of bin B is taken
-    uint64_t m = 0;
+    uint64_t m = 0, cm = 0;                        // taken keys; the threshold bin's keys (to rank)
+    int slot0 = 0;
     {
         QWFN_STREAM_LOAD(z)
-        uint64_t cm = 0;                           // the threshold bin's keys
 #pragma unroll
-        for (int i = 0; i < 4 * MAXV; ++i) {
-            const uint32_t bi = bin_of(z[i]);
-            const bool v = valid(i);
-            m |= (uint64_t)(v && (bi > B || (!rank && bi == B))) << i;
-            cm |= (uint64_t)(rank && v && bi == B) << i;
+        for (int k = 0; k < MAXV; ++k) {
+            if (k < nv) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 4 * k + j;
+                    const uint32_t bi = bin_of(z[i]);
+                    const bool v = valid(i);
+                    m |= (uint64_t)(v && (bi > B || (!rank && bi == B))) << i;
+                    cm |= (uint64_t)(rank && v && bi == B) << i;
+                }
+            }
         }
         if (cm) {
-            int slot = atomicAdd(&sh.ncand, (int)__builtin_popcountll(cm));
-            while (cm) {
-                const int i = __builtin_ctzll(cm);
+            slot0 = atomicAdd(&sh.ncand, (int)__builtin_popcountll(cm));
+            int slot = slot0;
+            for (uint64_t c2 = cm; c2; c2 &= c2 - 1ull) {
+                const int i = __builtin_ctzll(c2);
                 float zi = z[0];
 #pragma unroll
                 for (int k = 1; k < 4 * MAXV; ++k) zi = k == i ? z[k] : zi;
                 sh.cand_key[slot] = score_key(zi);
                 sh.cand_b[slot] = b0 + i;
                 ++slot;
-                cm &= cm - 1ull;
             }
         }
     }
 #undef QWFN_STREAM_LOAD
     if (rank) {
         __syncthreads();
-        if (tid < cB) {
+        if (tid < cB) {                            // rank: (key desc, index asc)
             const uint32_t k = sh.cand_key[tid];
             const int b = sh.cand_b[tid];
             int rk = 0;
@@ -849,13 +870,12 @@ __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, con
                 const uint32_t kj = sh.cand_key[jj];
                 rk += (kj > k) || (kj == k && sh.cand_b[jj] < b);
             }
-            if (rk < need) atomicOr(&sh.selbits[(b - base) >> 5], 1u << ((b - base) & 31));
+            sh.cand_ok[tid] = rk < need;
         }
         __syncthreads();
-        const int e = tid * per;                   // per <= 32 or per == 64: two words hold the bits
-        const uint64_t w2 = (uint64_t)sh.selbits[e >> 5] | ((uint64_t)sh.selbits[(e >> 5) + 1] << 32);
-        const uint64_t mine = per == 64 ? ~0ull : ((1ull << per) - 1ull);
-        m |= (w2 >> (e & 31)) & mine;
+        int slot = slot0;
+        for (uint64_t c2 = cm; c2; c2 &= c2 - 1ull, ++slot)
+            if (sh.cand_ok[slot]) m |= 1ull << __builtin_ctzll(c2);
     }
     const int cnt = (int)__builtin_popcountll(m);
     int tot;
@@ -955,11 +975,27 @@ __device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t 
                                               int64_t out_stride, int32_t *nout0, SH &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
-    const BufRsrc rs = buf_rsrc(sc0, (uint32_t)(((int64_t)(g.Hkv - 1) * sc_stride + r.e_hi) * 4));
-    for (int b = r.e_lo + tid; b < r.e_hi; b += NT) {
-        float acc = BufLoad<1, kCpolSc1>::at(rs, b * 4, 0)[0];
-        for (int h = 1; h < g.Hkv; ++h) acc += BufLoad<1, kCpolSc1>::at(rs, (int)((h * sc_stride + b) * 4), 0)[0];
-        sc0[b] = acc;
+    if (g.Hkv > 1) {                               // one score row needs no sum
+        const BufRsrc rs = buf_rsrc(sc0, (uint32_t)(((int64_t)(g.Hkv - 1) * sc_stride + r.e_hi) * 4));
+        // eight blocks a thread per round, every load of a round issued before
+        // any is summed (a rolled loop would wait out one round trip per block)
+        constexpr int U = 8;
+        for (int b0 = r.e_lo + tid; b0 < r.e_hi; b0 += U * NT) {
+            float acc[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc[u] = BufLoad<1, kCpolSc1>::at(rs, (b0 + u * NT) * 4, 0)[0];
+            for (int h = 1; h < g.Hkv; ++h) {
+                float x[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    x[u] = BufLoad<1, kCpolSc1>::at(rs, (int)((h * sc_stride + b0 + u * NT) * 4), 0)[0];
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc[u] += x[u];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (b0 + u * NT < r.e_hi) sc0[b0 + u * NT] = acc[u];
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the summed row, for the selection's loads
     __syncthreads();
@@ -986,7 +1022,7 @@ struct BigSelShared {
     uint32_t hist[4096 + 64];
     uint32_t cand_key[kCandMax + 1];
     int32_t cand_b[kCandMax + 1];
-    uint32_t selbits[64 * kBigSelThreads / 32 + 2];
+    int32_t cand_ok[kCandMax + 1];                // the ranking's verdicts
     float red[2 * (kBigSelThreads / 64)];
     int tmp[kBigSelThreads / 64];
     int bin, need, ncand, cnt_b;
@@ -1151,9 +1187,10 @@ struct MergeCfg {
     static constexpr int MAXP = 80 / (VW * OPT) > 40 ? 40 : 80 / (VW * OPT);
 };
 
+// Parts beyond what the LDS scratch holds weights for (dense attention over
+// long contexts): every weight recomputed from memory, one part at a time.
 template <int G, int HD, int NT>
-__device__ __forceinline__ void merge_partials_general(const Ws &ws, int pair, int parts_act, float *og,
-                                                                 float *Lh) {
+__device__ __forceinline__ void merge_partials_mem(const Ws &ws, int pair, int parts_act, float *og, float *Lh) {
     using M = MergeCfg<G, HD, NT>;
     constexpr int VW = M::VW, OPT = M::OPT, NV = G * HD / VW, NW = NT / 64;
     using vec = float __attribute__((ext_vector_type(VW)));
@@ -1189,6 +1226,64 @@ __device__ __forceinline__ void merge_partials_general(const Ws &ws, int pair, i
     }
 }
 
+// More parts than the registers hold: the weights w_i,h go to LDS (`wt`, at
+// least parts_act * G floats), then every thread sums its output vectors over
+// the parts eight at a time, each batch's loads issued before any is summed.
+template <int G, int HD, int NT>
+__device__ __forceinline__ void merge_partials_general(const Ws &ws, int pair, int parts_act, float *og,
+                                                                 float *Lh, float *wt) {
+    using M = MergeCfg<G, HD, NT>;
+    constexpr int VW = M::VW, OPT = M::OPT, NV = G * HD / VW, NW = NT / 64, U = 8;
+    using vec = float __attribute__((ext_vector_type(VW)));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads below
+    const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
+    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
+    const float *pml = ws.part_ml + pb * 2;
+    const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
+    for (int h = wv; h < G; h += NW) {
+        float Mx = -INFINITY;
+        for (int i = ln; i < parts_act; i += 64) Mx = fmaxf(Mx, pml[((int64_t)i * G + h) * 2]);
+        Mx = wave_max(Mx);
+        float Ls = 0.0f;
+        for (int i = ln; i < parts_act; i += 64) {
+            const float m = pml[((int64_t)i * G + h) * 2], l = pml[((int64_t)i * G + h) * 2 + 1];
+            const float w = m == -INFINITY ? 0.0f : exp2f(m - Mx);
+            wt[i * G + h] = w;
+            Ls += w * l;
+        }
+        Ls = wave_sum(Ls);
+        if (ln == 0) Lh[h] = Ls;
+    }
+    __syncthreads();
+    // all of a thread's output vectors per batch: one round trip per U parts
+    vec acc[OPT];
+#pragma unroll
+    for (int r = 0; r < OPT; ++r) acc[r] = vec(0.0f);
+    for (int i0 = 0; i0 < parts_act; i0 += U) {
+        vec x[OPT][U];
+#pragma unroll
+        for (int r = 0; r < OPT; ++r)
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                x[r][u] = po[(int64_t)min(i0 + u, parts_act - 1) * NV + min(tid + r * NT, NV - 1)];
+#pragma unroll
+        for (int r = 0; r < OPT; ++r) {
+            const int h = min(tid + r * NT, NV - 1) * VW / HD;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (i0 + u < parts_act) acc[r] += wt[(i0 + u) * G + h] * x[r][u];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < OPT; ++r) {
+        const int k = tid + r * NT;
+        if (k < NV) {
+            const float Ls = Lh[k * VW / HD];
+            reinterpret_cast<vec *>(og)[k] = Ls > 0.0f ? acc[r] * (1.0f / Ls) : vec(0.0f);
+        }
+    }
+}
+
 template <int G, int HD, int NT>
 __device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Lh,
                                                float *scratch, int scratch_floats) {
@@ -1197,7 +1292,8 @@ __device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts
     constexpr int NW = NT / 64, HPW = (G + NW - 1) / NW;
     using vec = float __attribute__((ext_vector_type(VW)));
     if (parts_act > MAXP || 64 * G > scratch_floats) {
-        merge_partials_general<G, HD, NT>(ws, pair, parts_act, og, Lh);
+        if (parts_act * G <= scratch_floats) merge_partials_general<G, HD, NT>(ws, pair, parts_act, og, Lh, scratch);
+        else merge_partials_mem<G, HD, NT>(ws, pair, parts_act, og, Lh);
         return;
     }
     // Straight-line path: every load unconditional, through buffer
