@@ -568,7 +568,7 @@ def main():
     checkpoint = None
     if not args.no_checkpoint:
         ck = {}
-        for ctx in (min(contexts), max(contexts)):
+        for ctx in sorted({min(contexts), max(contexts)}):
             r = CheckpointRunner(qsa, torch, ctx, args.layers, gen)
             ck[str(ctx)] = {k: (round(v, 3) if isinstance(v, float) else v)
                             for k, v in r.run(max(20, args.steps // 3), args.warmup).items()}
