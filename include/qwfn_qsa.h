@@ -39,6 +39,11 @@
  *             tokens is 64 contiguous bytes, the operand of a per-dim dot
  *             product over tokens); otherwise the K layout
  *    scales : fp16  [n_head_kv][page_tokens][head_dim/32]  (one per q8_0 block)
+ *  Other kv_type values keep the K layout's 16-byte chunks for K and V alike
+ *  (R = a head row's bytes, R/16 chunks per row):
+ *    Q4_0 : R = head_dim/2, chunk j = the 16 qs bytes of ggml block j (ggml's
+ *           nibble order), then the fp16 scales as above
+ *    F16  : R = 2*head_dim, chunk c = dims 8c .. 8c+7, no scales
  *  A logical position t of sequence s lives in physical page
  *  page_table[s*pages_per_seq + t/page_tokens] at row t%page_tokens.
  *  pooled = fp32 [n_seq][n_head_kv][blocks_per_seq][head_dim], where
@@ -56,7 +61,7 @@
 extern "C" {
 #endif
 
-#define QWFN_QSA_ABI_VERSION 2
+#define QWFN_QSA_ABI_VERSION 3
 
 /* return codes */
 #define QWFN_OK        0
@@ -72,6 +77,17 @@ extern "C" {
  * Both store d = fp16_rne(amax/127).  A non-finite x*id stores q = 0.        */
 #define QWFN_Q8_X86_RNE     0
 #define QWFN_Q8_REF_ROUNDF  1
+
+/* K/V cache element types (the reference's --kv q8_0|q4_0|f16,
+ * tools/qwfn_gen.cpp:55-57; README.md:176):
+ *  Q8_0: ggml block_q8_0 {fp16 d; int8 qs[32]}, quant_variant's rounding
+ *  Q4_0: ggml block_q4_0 {fp16 d; uint8 qs[16]}: d = m / -8 with m the element
+ *        of largest magnitude (the first such), q = min(15, trunc(x/d + 8.5)),
+ *        qs[j] = q[j] | q[j+16] << 4 (quantize_row_q4_0_ref)
+ *  F16 : fp16, round to nearest even                                          */
+#define QWFN_KV_Q8_0  0
+#define QWFN_KV_Q4_0  1
+#define QWFN_KV_F16   2
 
 /* element type of K/V rows handed to the append */
 #define QWFN_SRC_F32  0
@@ -108,6 +124,7 @@ typedef struct qwfn_qsa_shape {
                               * src/qwfn_graph.cpp:493, src/qwfn_engine.cpp:
                               * 430); 0: top_k_blocks scored blocks on top of
                               * the forced ones                              */
+    int32_t kv_type;         /* QWFN_KV_Q8_0 / QWFN_KV_Q4_0 / QWFN_KV_F16       */
 } qwfn_qsa_shape;
 
 typedef struct qwfn_kv_view {

@@ -26,7 +26,7 @@ class Shape(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_head", "n_head_kv", "head_dim", "block_tokens", "page_tokens", "top_k_blocks",
         "sink_blocks", "local_tokens", "relu_per_head", "shared_selection", "quant_variant",
-        "topk_counts_forced")]
+        "topk_counts_forced", "kv_type")]
 
 
 class IdxShape(C.Structure):
@@ -63,6 +63,8 @@ def lib() -> C.CDLL:
             "qwfn_oracle_f32_to_f16_n": (None, [P, C.c_int64, P]),
             "qwfn_oracle_quantize_block": (None, [P, I, P, P]),
             "qwfn_oracle_quantize_row_ggml": (None, [P, C.c_int64, I, P]),
+            "qwfn_oracle_quantize_block_q4_0": (None, [P, P, P]),
+            "qwfn_oracle_quantize_row_type": (None, [P, C.c_int64, I, I, P]),
             "qwfn_oracle_page_bytes": (C.c_size_t, [S]),
             "qwfn_oracle_quant_offset": (C.c_int64, [S, I, I, I, I]),
             "qwfn_oracle_scale_offset": (C.c_int64, [S, I, I, I]),
@@ -97,7 +99,8 @@ def shape_of(cfg) -> Shape:
     """A Shape from any object with the QsaConfig field names."""
     return Shape(cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.block_tokens, cfg.page_tokens,
                  cfg.top_k_blocks, cfg.sink_blocks, cfg.local_tokens, cfg.relu_per_head,
-                 cfg.shared_selection, cfg.quant_variant, getattr(cfg, "topk_counts_forced", 0))
+                 cfg.shared_selection, cfg.quant_variant, getattr(cfg, "topk_counts_forced", 0),
+                 getattr(cfg, "kv_type", 0))
 
 
 # ---- scalar / block helpers -------------------------------------------------
@@ -128,6 +131,25 @@ def quantize_row_ggml(x, variant: int = Q8_X86_RNE) -> np.ndarray:
     x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).ravel())
     out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
     lib().qwfn_oracle_quantize_row_ggml(_p(x), x.size, variant, _p(out))
+    return out
+
+
+def quantize_block_q4_0(x):
+    """(d fp16 bits, qs uint8[16]) of one 32-value q4_0 block."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).ravel())
+    assert x.size == 32
+    d = np.zeros(1, dtype=np.uint16)
+    qs = np.zeros(16, dtype=np.uint8)
+    lib().qwfn_oracle_quantize_block_q4_0(_p(x), _p(d), _p(qs))
+    return int(d[0]), qs
+
+
+def quantize_row_type(x, kv_type: int, variant: int = Q8_X86_RNE) -> np.ndarray:
+    """ggml's row bytes of the cache type for values x (a multiple of 32)."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).ravel())
+    per = {0: 34, 1: 18, 2: 64}[kv_type]
+    out = np.zeros(x.size // 32 * per, dtype=np.uint8)
+    lib().qwfn_oracle_quantize_row_type(_p(x), x.size, kv_type, variant, _p(out))
     return out
 
 

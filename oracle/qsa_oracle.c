@@ -120,26 +120,85 @@ void qwfn_oracle_quantize_row_ggml(const float *x, int64_t n, int32_t variant,
     }
 }
 
+/* ggml's q4_0 quantizer (quantize_row_q4_0_ref), restated from its published
+ * algorithm: m = the element of largest magnitude (the first one; it starts at
+ * +0 and only a strictly larger |x| replaces it, so NaN never wins), d = m / -8
+ * stored as fp16, id = 1/d (0 when d == 0), q = min(15, (int8)(x*id + 8.5)),
+ * qs[j] = q[j] | q[j+16] << 4.  A NaN x*id + 8.5 stores 0 (x86's truncating
+ * conversion gives INT_MIN, whose low byte is 0).  Reached through the
+ * reference's --kv q4_0 (tools/qwfn_gen.cpp:55-57). */
+void qwfn_oracle_quantize_block_q4_0(const float *x, uint16_t *dout, uint8_t *qs) {
+    float amax = 0.0f, m = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        const float a = fabsf(x[j]);
+        if (amax < a) { amax = a; m = x[j]; }
+    }
+    const float d = m / -8.0f;
+    *dout = qwfn_oracle_f32_to_f16(d);
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t q[32];
+    for (int j = 0; j < 32; j++) {
+        const float r = x[j] * id + 8.5f;
+        const int t = r != r ? 0 : (int)r;
+        q[j] = (uint8_t)(t < 15 ? t : 15);
+    }
+    for (int j = 0; j < 16; j++) qs[j] = (uint8_t)(q[j] | (q[j + 16] << 4));
+}
+
+/* One row of n values in ggml's layout of the cache type: q8_0 34-byte blocks,
+ * q4_0 18-byte blocks {fp16 d; qs[16]}, or fp16 values. */
+void qwfn_oracle_quantize_row_type(const float *x, int64_t n, int32_t kv_type, int32_t variant,
+                                   uint8_t *out) {
+    if (kv_type == QWFN_KV_F16) {
+        for (int64_t i = 0; i < n; i++) {
+            const uint16_t h = qwfn_oracle_f32_to_f16(x[i]);
+            memcpy(out + 2 * i, &h, 2);
+        }
+    } else if (kv_type == QWFN_KV_Q4_0) {
+        for (int64_t b = 0; b < n / 32; b++) {
+            uint16_t d;
+            qwfn_oracle_quantize_block_q4_0(x + 32 * b, &d, out + 18 * b + 2);
+            memcpy(out + 18 * b, &d, 2);
+        }
+    } else {
+        qwfn_oracle_quantize_row_ggml(x, n, variant, out);
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* layout                                                                    */
 /* ------------------------------------------------------------------------ */
 
+/* Bytes of a head row of K (or V) in a page: q8_0 one per value, q4_0 a
+ * nibble, fp16 two. */
+static int64_t row_bytes(const qwfn_qsa_shape *s) {
+    return s->kv_type == QWFN_KV_Q4_0 ? s->head_dim / 2 : s->kv_type == QWFN_KV_F16 ? 2 * s->head_dim
+                                                                                    : s->head_dim;
+}
+
 static size_t quant_bytes_per_page(const qwfn_qsa_shape *s) {
-    return (size_t)s->n_head_kv * (size_t)s->page_tokens * (size_t)s->head_dim;
+    return (size_t)s->n_head_kv * (size_t)s->page_tokens * (size_t)row_bytes(s);
 }
 
 size_t qwfn_oracle_page_bytes(const qwfn_qsa_shape *s) {
+    if (s->kv_type == QWFN_KV_F16) return quant_bytes_per_page(s);
     return quant_bytes_per_page(s) +
            (size_t)s->n_head_kv * (size_t)s->page_tokens * (size_t)(s->head_dim / 32) * 2u;
 }
 
+/* Byte offset of value d of head g's row in a page (for q4_0: the byte whose
+ * low (d%32 < 16) or high nibble holds it; for fp16: its first byte). */
 int64_t qwfn_oracle_quant_offset(const qwfn_qsa_shape *s, int32_t which, int32_t g,
                                  int32_t row, int32_t d) {
-    const int64_t tiles = s->page_tokens / 64, chunks = s->head_dim / 16;
-    if (which && s->block_tokens % 64 == 0)       /* V, dim-major 64-token tiles */
-        return (((int64_t)g * tiles + row / 64) * s->head_dim + d) * 64 + row % 64;
-    return (((int64_t)g * tiles + row / 64) * chunks + d / 16) * 1024 +
-           (int64_t)(row % 64) * 16 + d % 16;
+    const int64_t tiles = s->page_tokens / 64, chunks = row_bytes(s) / 16;
+    const int64_t tile_row = ((int64_t)g * tiles + row / 64);
+    if (s->kv_type == QWFN_KV_Q4_0)                /* chunk = ggml block d/32's qs bytes */
+        return (tile_row * chunks + d / 32) * 1024 + (int64_t)(row % 64) * 16 + d % 16;
+    if (s->kv_type == QWFN_KV_F16)                 /* chunk = dims 8c .. 8c+7 */
+        return (tile_row * chunks + d / 8) * 1024 + (int64_t)(row % 64) * 16 + (d % 8) * 2;
+    if (which && s->block_tokens % 64 == 0)       /* q8_0 V, dim-major 64-token tiles */
+        return (tile_row * s->head_dim + d) * 64 + row % 64;
+    return (tile_row * chunks + d / 16) * 1024 + (int64_t)(row % 64) * 16 + d % 16;
 }
 
 int64_t qwfn_oracle_scale_offset(const qwfn_qsa_shape *s, int32_t g, int32_t row,
@@ -186,11 +245,23 @@ int qwfn_oracle_append(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                     for (int e = 0; e < 32; e++)
                         x[e] = src_at(src, src_dtype, ((int64_t)i * H + g) * hd + 32 * j + e);
                     uint16_t d;
-                    int8_t qs[32];
-                    qwfn_oracle_quantize_block(x, s->quant_variant, &d, qs);
-                    memcpy(page + qwfn_oracle_scale_offset(s, g, row, j), &d, 2);
-                    for (int e = 0; e < 32; e++)
-                        page[qwfn_oracle_quant_offset(s, which, g, row, 32 * j + e)] = (uint8_t)qs[e];
+                    if (s->kv_type == QWFN_KV_F16) {
+                        for (int e = 0; e < 32; e++) {
+                            d = qwfn_oracle_f32_to_f16(x[e]);
+                            memcpy(page + qwfn_oracle_quant_offset(s, which, g, row, 32 * j + e), &d, 2);
+                        }
+                    } else if (s->kv_type == QWFN_KV_Q4_0) {
+                        uint8_t qs[16];
+                        qwfn_oracle_quantize_block_q4_0(x, &d, qs);
+                        memcpy(page + qwfn_oracle_scale_offset(s, g, row, j), &d, 2);
+                        for (int e = 0; e < 16; e++) page[qwfn_oracle_quant_offset(s, which, g, row, 32 * j + e)] = qs[e];
+                    } else {
+                        int8_t qs[32];
+                        qwfn_oracle_quantize_block(x, s->quant_variant, &d, qs);
+                        memcpy(page + qwfn_oracle_scale_offset(s, g, row, j), &d, 2);
+                        for (int e = 0; e < 32; e++)
+                            page[qwfn_oracle_quant_offset(s, which, g, row, 32 * j + e)] = (uint8_t)qs[e];
+                    }
                 }
         }
     }
@@ -208,8 +279,20 @@ int qwfn_oracle_dequant_row(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
     const int32_t which = pool == v->v_pages;
     for (int32_t d = 0; d < s->head_dim; d++) {
         uint16_t h;
+        const int64_t off = qwfn_oracle_quant_offset(s, which, g, row, d);
+        if (s->kv_type == QWFN_KV_F16) {           /* ggml_get_rows of F16: the value itself */
+            memcpy(&h, page + off, 2);
+            out[d] = qwfn_oracle_f16_to_f32(h);
+            continue;
+        }
         memcpy(&h, page + qwfn_oracle_scale_offset(s, g, row, d / 32), 2);
-        const int8_t q = (int8_t)page[qwfn_oracle_quant_offset(s, which, g, row, d)];
+        if (s->kv_type == QWFN_KV_Q4_0) {           /* dequantize_row_q4_0: (nibble - 8) * d */
+            const uint8_t b = page[off];
+            const int q = (d % 32 < 16 ? (b & 15) : (b >> 4)) - 8;
+            out[d] = (float)q * qwfn_oracle_f16_to_f32(h);
+            continue;
+        }
+        const int8_t q = (int8_t)page[off];
         out[d] = qwfn_oracle_f16_to_f32(h) * (float)q;
     }
     return 0;

@@ -18,6 +18,8 @@
  * Pinning (what checks each function independently of this restatement):
  *   fp16 conversion   numpy float16 over special values and random sweeps
  *   q8_0 quantize     closed-form known answers + numpy rint/round restatement
+ *   q4_0 quantize     closed-form known answers (d = m/-8, grids of exact
+ *                     multiples, ties of magnitude, signs), reconstruction bound
  *   layout / gather   exact round trip, brute force over tiny caches
  *   pooling           numpy sequential float32 chain + constant-block invariant
  *   block score       exact rational arithmetic (fractions) on small cases
@@ -50,6 +52,11 @@ void qwfn_oracle_quantize_block(const float *x, int32_t variant, uint16_t *d,
                                 int8_t *qs);
 /* n values (a multiple of 32) -> ggml block_q8_0 bytes (34 per block). */
 void qwfn_oracle_quantize_row_ggml(const float *x, int64_t n, int32_t variant,
+                                   uint8_t *out);
+/* One q4_0 block (32 values): *d = fp16 scale, qs = 16 packed nibble bytes. */
+void qwfn_oracle_quantize_block_q4_0(const float *x, uint16_t *d, uint8_t *qs);
+/* n values -> ggml's row bytes of the cache type (kv_type QWFN_KV_*). */
+void qwfn_oracle_quantize_row_type(const float *x, int64_t n, int32_t kv_type, int32_t variant,
                                    uint8_t *out);
 
 /* Byte offsets inside one page (see include/qwfn_qsa.h); which = 0 for a K

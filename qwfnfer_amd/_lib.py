@@ -17,6 +17,9 @@ QWFN_ENOTSUP = -95
 
 Q8_X86_RNE = 0
 Q8_REF_ROUNDF = 1
+KV_Q8_0 = 0
+KV_Q4_0 = 1
+KV_F16 = 2
 SRC_F32 = 0
 SRC_F16 = 1
 
@@ -73,6 +76,7 @@ class QsaShape(C.Structure):
         ("shared_selection", C.c_int32),
         ("quant_variant", C.c_int32),
         ("topk_counts_forced", C.c_int32),
+        ("kv_type", C.c_int32),
     ]
 
 

@@ -56,6 +56,8 @@ int check_shape(const qwfn_qsa_shape *s) {
     if (s->local_tokens < 0) return fail(QWFN_EINVAL, "local_tokens (%d) < 0", s->local_tokens);
     if (s->quant_variant != QWFN_Q8_X86_RNE && s->quant_variant != QWFN_Q8_REF_ROUNDF)
         return fail(QWFN_EINVAL, "quant_variant %d unknown", s->quant_variant);
+    if (s->kv_type != QWFN_KV_Q8_0 && s->kv_type != QWFN_KV_Q4_0 && s->kv_type != QWFN_KV_F16)
+        return fail(QWFN_EINVAL, "kv_type %d unknown", s->kv_type);
     if ((s->relu_per_head | s->shared_selection | s->topk_counts_forced) & ~1)
         return fail(QWFN_EINVAL, "relu_per_head / shared_selection / topk_counts_forced are 0 or 1");
     if (s->topk_counts_forced && s->top_k_blocks > 0 &&
@@ -94,10 +96,15 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->relu = s->relu_per_head; g->variant = s->quant_variant; g->shared = s->shared_selection;
     g->keep_total = s->topk_counts_forced;
     g->sel_rows = s->n_head_kv;
-    g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * s->head_dim;
-    g->page_bytes = g->qbytes + (int64_t)s->n_head_kv * s->page_tokens * (s->head_dim / 32) * 2;
+    g->kt = s->kv_type;
+    g->chunks = kv_row_bytes(s->kv_type, s->head_dim) / 16;
+    g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * kv_row_bytes(s->kv_type, s->head_dim);
+    g->page_bytes = g->qbytes +
+                    (s->kv_type == QWFN_KV_F16 ? 0 : (int64_t)s->n_head_kv * s->page_tokens * (s->head_dim / 32) * 2);
     g->inv_bt = 1.0f / (float)s->block_tokens;
-    g->vdim = s->block_tokens % 64 == 0;
+    // the matrix-core kernels read q8_0 (V dim-major per 64-token tile); other
+    // element types run the general kernels over the K layout
+    g->vdim = s->block_tokens % 64 == 0 && s->kv_type == QWFN_KV_Q8_0;
     g->scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)s->head_dim));
     g->pf = 0; g->pf_seq = 0; g->pf_pos0 = 0;
     if (v) {
@@ -276,7 +283,10 @@ int qwfn_kv_row_bytes(const qwfn_qsa_shape *shape, size_t *bytes) {
     int rc = make_geo(shape, nullptr, &g, false);
     if (rc) return rc;
     if (!bytes) return fail(QWFN_EINVAL, "bytes is NULL");
-    *bytes = (size_t)g.Hkv * (size_t)(g.hd / 32) * 34u;
+    // ggml's row of the cache type: block_q8_0 34 B, block_q4_0 18 B per 32
+    // values; fp16 2 B per value
+    *bytes = g.kt == QWFN_KV_F16 ? (size_t)g.Hkv * g.hd * 2u
+                                 : (size_t)g.Hkv * (size_t)(g.hd / 32) * (g.kt == QWFN_KV_Q4_0 ? 18u : 34u);
     return ok();
 }
 

@@ -19,6 +19,8 @@ struct Geo {
     int32_t relu, variant;           // indexer relu, q8_0 rounding
     int32_t shared;                  // one selection for all KV heads (scores summed in head order)
     int32_t keep_total;              // top_k counts the forced blocks (topk_counts_forced)
+    int32_t kt;                      // K/V element type (QWFN_KV_*)
+    int32_t chunks;                  // 16-byte chunks in a head row of K/V (head_dim/16 for q8_0)
     int32_t sel_rows;                // rows a shared selection is written to per sequence (Hkv;
                                      // the attention's n_head_kv for the checkpoint indexer)
     int32_t pps, n_phys, n_seq_view; // pages per sequence, pool pages, view seqs
@@ -64,6 +66,11 @@ struct FusedAppend {
 
 bool kernels_for(int32_t hd, int32_t G);   // an instantiation exists
 
+// Bytes of one token's head row of K (or V) quants / values in a page.
+inline int32_t kv_row_bytes(int32_t kt, int32_t hd) {
+    return kt == QWFN_KV_Q4_0 ? hd / 2 : kt == QWFN_KV_F16 ? 2 * hd : hd;
+}
+
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
 
 // The checkpoint's own indexer keys (qwfn_idx_shape): raw fp16 keys of `dim`
@@ -88,14 +95,17 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,
                            float *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
                            int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st);
-// seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r.
+// seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r;
+// len (decode): row r is sequence r's token at position len[r] - 1.
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
                          int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
-                         int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st);
-// seq_ids NULL: every block in seq_const; block_ids NULL: blocks blk0 + [0, n_blocks).
+                         int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st,
+                         const int32_t *len = nullptr);
+// seq_ids NULL: every block in seq_const; block_ids NULL: blocks blk0 + [0, n_blocks);
+// len (decode): sequence i's block holding len[i] - 1 when that token completes it.
 hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
-                       int32_t blk0, hipStream_t st);
+                       int32_t blk0, hipStream_t st, const int32_t *len = nullptr);
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,

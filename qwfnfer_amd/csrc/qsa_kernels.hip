@@ -33,6 +33,12 @@ __device__ __forceinline__ int64_t vquant_off(const Geo &g, int gh, int row, int
 __device__ __forceinline__ int64_t scale_off(const Geo &g, int gh, int row, int j) {
     return g.qbytes + ((int64_t)(gh * g.pt + row) * (g.hd / 32) + j) * 2;
 }
+// 16-byte chunk c of KV head gh's row `row` (the K layout, every element
+// type; q8_0 chunks hold 16 dims, q4_0 chunks one ggml block's 16 qs bytes,
+// fp16 chunks 8 dims).
+__device__ __forceinline__ int64_t chunk_off(const Geo &g, int gh, int row, int c) {
+    return ((int64_t)(gh * (g.pt / 64) + row / 64) * g.chunks + c) * 1024 + (row % 64) * 16;
+}
 
 // Cache sequence and length of launch sequence s (prefill: query s of one
 // cache sequence, see Geo::pf).  `raw` is seq_len[s] as loaded.
@@ -237,6 +243,16 @@ __device__ __forceinline__ void store_q4(const Geo &g, uint8_t *page, bool is_v,
     }
 }
 
+__device__ __forceinline__ void load2(const void *src, int32_t f16, int64_t idx, float x[2]) {
+    if (f16) {
+        const uint32_t u = *reinterpret_cast<const uint32_t *>((const uint16_t *)src + idx);
+        x[0] = h2f((uint16_t)(u & 0xFFFF)); x[1] = h2f((uint16_t)(u >> 16));
+    } else {
+        const float2 f = *reinterpret_cast<const float2 *>((const float *)src + idx);
+        x[0] = f.x; x[1] = f.y;
+    }
+}
+
 __device__ __forceinline__ void load4(const void *src, int32_t f16, int64_t idx, float x[4]) {
     if (f16) {
         const uint2 u = *reinterpret_cast<const uint2 *>((const uint16_t *)src + idx);
@@ -270,10 +286,52 @@ hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st) {
 // append: quantize rows to q8_0 and overwrite them in the paged cache
 // ---------------------------------------------------------------------------
 
-// Lane i: 4 values of one q8_0 block; blocks enumerate (row, K|V, head, j).
+// One q4_0 block by 8 consecutive lanes, lane e holding values 2e, 2e+1,
+// 16+2e, 17+2e (x[0..3]): ggml's quantize_row_q4_0_ref -- m = the element of
+// largest magnitude (the first one on ties; +0 when every |x| is 0 or NaN),
+// d = m / -8 stored as fp16, id = 1/d (0 when d == 0), q = min(15,
+// trunc(x*id + 8.5)) (0 for a NaN), qs[j] = q[j] | q[j+16] << 4.  Returns this
+// lane's two qs bytes (2e, 2e+1) packed little-endian and the fp16 scale.
+__device__ __forceinline__ uint32_t quant_q4(const float x[4], int e, uint16_t *dh_out) {
+#pragma clang fp contract(off)
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a = fmaxf(a, fabsf(x[k]));
+    a = fmaxf(a, dppf<kDppQuadXor1>(a, a));
+    a = fmaxf(a, dppf<kDppQuadXor2>(a, a));
+    a = fmaxf(a, dppf<kDppRowHalfMirror>(a, a));
+    // the first index holding the largest magnitude, and its value
+    const int idx[4] = {2 * e, 2 * e + 1, 16 + 2 * e, 17 + 2 * e};
+    int bi = 32;
+    float bv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (a > 0.0f && fabsf(x[k]) == a && idx[k] < bi) { bi = idx[k]; bv = x[k]; }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        const int oi = __shfl_xor(bi, off, 8);
+        const float ov = __shfl_xor(bv, off, 8);
+        if (oi < bi) { bi = oi; bv = ov; }
+    }
+    const float d = bv / -8.0f;
+    *dh_out = f2h(d);
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t q[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float r = x[k] * id + 8.5f;
+        const int t = r != r ? 0 : (int)r;          // truncation; |x*id| <= 8 keeps it in 0 .. 16
+        q[k] = (uint32_t)(t < 15 ? t : 15);
+    }
+    return (q[0] | q[2] << 4) | ((q[1] | q[3] << 4) << 8);
+}
+
+// Lane i: 4 values of one 32-value block; blocks enumerate (row, K|V, head,
+// j).  len (when set): row r is sequence r's token at position len[r] - 1.
 __global__ void __launch_bounds__(256)
 k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
-         const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, int32_t seq_const, int32_t pos0) {
+         const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, int32_t seq_const, int32_t pos0,
+         const int32_t *len) {
     const int nj = g.hd / 32;
     const int64_t total = (int64_t)n_rows * 2 * g.Hkv * nj * 8;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -284,30 +342,51 @@ k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
     const int gh = (int)(qb % g.Hkv); qb /= g.Hkv;
     const int which = (int)(qb & 1);
     const int r = (int)(qb >> 1);
-    const int seq = seq_ids ? seq_ids[r] : seq_const;
-    const int t = pos ? pos[r] : pos0 + r;
+    const int seq = len ? r : seq_ids ? seq_ids[r] : seq_const;
+    const int t = len ? len[r] - 1 : pos ? pos[r] : pos0 + r;
     const bool report = (e4 == 0 && j == 0 && gh == 0 && which == 0);
+    // the lanes of one block stay together past the checks: they are uniform per block
     if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
     if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (report) set_status(v.status, QWFN_STATUS_POS_RANGE); return; }
     const int32_t pp = phys_page(g, v.page_table, seq, t);
     if (pp < 0) { if (report) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
-    float x[4];
-    load4(which ? vsrc : ksrc, f16, ((int64_t)r * g.Hkv + gh) * g.hd + 32 * j + 4 * e4, x);
-    uint16_t dh;
-    const uint32_t pk = quant4(x, g.variant, &dh, nullptr);
+    const void *src = which ? vsrc : ksrc;
+    const int64_t base = ((int64_t)r * g.Hkv + gh) * g.hd + 32 * j;
     uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
     const int row = t % g.pt;
-    store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
-    if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+    float x[4];
+    if (g.kt == QWFN_KV_Q4_0) {
+        float a[2], b[2];
+        load2(src, f16, base + 2 * e4, a);
+        load2(src, f16, base + 16 + 2 * e4, b);
+        x[0] = a[0]; x[1] = a[1]; x[2] = b[0]; x[3] = b[1];
+        uint16_t dh;
+        const uint32_t qs = quant_q4(x, e4, &dh);
+        *reinterpret_cast<uint16_t *>(page + chunk_off(g, gh, row, j) + 2 * e4) = (uint16_t)qs;
+        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+    } else if (g.kt == QWFN_KV_F16) {
+        load4(src, f16, base + 4 * e4, x);
+        const uint32_t lo = (uint32_t)f2h(x[0]) | (uint32_t)f2h(x[1]) << 16;
+        const uint32_t hi = (uint32_t)f2h(x[2]) | (uint32_t)f2h(x[3]) << 16;
+        const int d = 32 * j + 4 * e4;
+        *reinterpret_cast<uint2 *>(page + chunk_off(g, gh, row, d / 8) + (d % 8) * 2) = make_uint2(lo, hi);
+    } else {
+        load4(src, f16, base + 4 * e4, x);
+        uint16_t dh;
+        const uint32_t pk = quant4(x, g.variant, &dh, nullptr);
+        store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
+        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+    }
 }
 
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
                          int32_t src_f16, const int32_t *seq_ids, const int32_t *pos,
-                         int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st) {
+                         int32_t n_rows, int32_t seq_const, int32_t pos0, hipStream_t st,
+                         const int32_t *len) {
     const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
     const int64_t blocks = (total + 255) / 256;
     hipLaunchKernelGGL(k_append, dim3((unsigned)blocks), dim3(256), 0, st, g, v, k, vv, src_f16,
-                       seq_ids, pos, n_rows, seq_const, pos0);
+                       seq_ids, pos, n_rows, seq_const, pos0, len);
     return hipGetLastError();
 }
 
@@ -315,33 +394,61 @@ hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, con
 // pooled keys: sequential fp32 add chain over the block's members, * 1/bt
 // ---------------------------------------------------------------------------
 
-// One dequantized member value straight from global memory (gather path).
+// One dequantized value straight from global memory (gather path): q8_0
+// d*q, q4_0 d*(nibble - 8) (dims 0..15 of a block in the low nibbles of its
+// 16 bytes, dims 16..31 in the high ones), fp16 as stored.
 __device__ __forceinline__ float member_k(const Geo &g, const uint8_t *page, int gh, int row, int d,
                                           bool is_v = false) {
-    const int8_t q = (int8_t)page[(is_v && g.vdim) ? vquant_off(g, gh, row, d) : quant_off(g, gh, row, d)];
+    if (g.kt == QWFN_KV_F16)
+        return h2f(*reinterpret_cast<const uint16_t *>(page + chunk_off(g, gh, row, d / 8) + (d % 8) * 2));
     const uint16_t s = *reinterpret_cast<const uint16_t *>(page + scale_off(g, gh, row, d / 32));
+    if (g.kt == QWFN_KV_Q4_0) {
+        const uint8_t b = page[chunk_off(g, gh, row, d / 32) + d % 16];
+        return h2f(s) * (float)((d % 32 < 16 ? (b & 15) : (b >> 4)) - 8);
+    }
+    const int8_t q = (int8_t)page[(is_v && g.vdim) ? vquant_off(g, gh, row, d) : quant_off(g, gh, row, d)];
     return h2f(s) * (float)q;
 }
 
 constexpr int kStageRows = 64;   // member rows staged through LDS per round
 
-// Rows [row0, row0+n) (n <= kStageRows) of KV head gh of one page, copied into
-// LDS as int8 q8[n][HD] and fp16 sc[n][HD/32] -- every load issued before any
-// is consumed, so the copy costs one memory round trip.
-template <int HD>
+// Head-row bytes of K/V of an element type (compile-time twin of kv_row_bytes).
+template <int HD, int KT> constexpr int row_bytes_t() { return KT == QWFN_KV_Q4_0 ? HD / 2 : KT == QWFN_KV_F16 ? 2 * HD : HD; }
+// Member rows one staging round holds in kStageRows * HD bytes of LDS.
+template <int HD, int KT> constexpr int stage_max_t() { return kStageRows * HD / row_bytes_t<HD, KT>() < kStageRows ? kStageRows * HD / row_bytes_t<HD, KT>() : kStageRows; }
+
+// Rows [row0, row0+n) (n <= stage_max_t) of KV head gh of one page, copied
+// into LDS as their raw row bytes raw[n][row bytes] and fp16 sc[n][HD/32] (no
+// scales for fp16) -- every load issued before any is consumed, so the copy
+// costs one memory round trip.
+template <int HD, int KT = QWFN_KV_Q8_0>
 __device__ __forceinline__ void stage_rows(const Geo &g, const uint8_t *page, int gh, int row0, int n,
-                                           int8_t *q8, uint16_t *sc, int tid, int nt) {
-    constexpr int CH = HD / 16;
+                                           int8_t *raw, uint16_t *sc, int tid, int nt) {
+    constexpr int RB = row_bytes_t<HD, KT>(), CH = RB / 16;
 #pragma unroll 4
     for (int k = tid; k < n * CH; k += nt) {
         const int r = k % n, c = k / n, row = row0 + r;
         const uint4 val = *reinterpret_cast<const uint4 *>(
             page + ((int64_t)(gh * (g.pt / 64) + row / 64) * CH + c) * 1024 + (row % 64) * 16);
-        *reinterpret_cast<uint4 *>(q8 + r * HD + c * 16) = val;
+        *reinterpret_cast<uint4 *>(raw + r * RB + c * 16) = val;
     }
+    if (KT == QWFN_KV_F16) return;
     const uint16_t *s = reinterpret_cast<const uint16_t *>(page + scale_off(g, gh, row0, 0));
 #pragma unroll 4
     for (int k = tid; k < n * (HD / 32); k += nt) sc[k] = s[k];
+}
+
+// Dimension d of staged row t.
+template <int HD, int KT>
+__device__ __forceinline__ float staged_value(const int8_t *raw, const uint16_t *sc, int t, int d) {
+    constexpr int RB = row_bytes_t<HD, KT>();
+    if (KT == QWFN_KV_F16) return h2f(reinterpret_cast<const uint16_t *>(raw + t * RB)[d]);
+    const float s = h2f(sc[t * (HD / 32) + d / 32]);
+    if (KT == QWFN_KV_Q4_0) {
+        const uint8_t b = (uint8_t)raw[t * RB + (d / 32) * 16 + d % 16];
+        return s * (float)((d % 32 < 16 ? (b & 15) : (b >> 4)) - 8);
+    }
+    return s * (float)raw[t * RB + d];
 }
 
 // Pooled key of one block of KV head gh: thread d < HD keeps dimension d's
@@ -350,29 +457,30 @@ __device__ __forceinline__ void stage_rows(const Geo &g, const uint8_t *page, in
 // memory.  All nt threads must call (it synchronises).
 // Dimension tid's chain over n staged rows: acc + m_0 + ... + m_{n-1}, or
 // m_0 + ... when `first` (the block's first member starts the chain).
-template <int HD>
-__device__ __forceinline__ float pool_chain(const int8_t *q8, const uint16_t *sc, int n, int tid, float acc,
+template <int HD, int KT = QWFN_KV_Q8_0>
+__device__ __forceinline__ float pool_chain(const int8_t *raw, const uint16_t *sc, int n, int tid, float acc,
                                             bool first) {
 #pragma clang fp contract(off)
 #pragma unroll 8
     for (int t = 0; t < n; ++t) {
-        const float m = h2f(sc[t * (HD / 32) + tid / 32]) * (float)q8[t * HD + tid];
+        const float m = staged_value<HD, KT>(raw, sc, t, tid);
         acc = (first && t == 0) ? m : acc + m;
     }
     return acc;
 }
 
-template <int HD>
+template <int HD, int KT = QWFN_KV_Q8_0>
 __device__ void pool_block_dev(const Geo &g, const uint8_t *page, int gh, int row0, float *dst,
                                const float *last, int8_t *q8, uint16_t *sc, int tid, int nt) {
 #pragma clang fp contract(off)
+    constexpr int SM = stage_max_t<HD, KT>();
     const int from_mem = last ? g.bt - 1 : g.bt;
     float acc = 0.0f;
-    for (int r0 = 0; r0 < from_mem; r0 += kStageRows) {
-        const int n = min(kStageRows, from_mem - r0);
-        stage_rows<HD>(g, page, gh, row0 + r0, n, q8, sc, tid, nt);
+    for (int r0 = 0; r0 < from_mem; r0 += SM) {
+        const int n = min(SM, from_mem - r0);
+        stage_rows<HD, KT>(g, page, gh, row0 + r0, n, q8, sc, tid, nt);
         __syncthreads();
-        if (tid < HD) acc = pool_chain<HD>(q8, sc, n, tid, acc, r0 == 0);
+        if (tid < HD) acc = pool_chain<HD, KT>(q8, sc, n, tid, acc, r0 == 0);
         __syncthreads();
     }
     if (tid < HD) {
@@ -381,16 +489,18 @@ __device__ void pool_block_dev(const Geo &g, const uint8_t *page, int gh, int ro
     }
 }
 
-// grid (n_blocks, Hkv), 256 threads
-template <int HD>
+// grid (n_blocks, Hkv), 256 threads.  len (decode): entry bi is sequence bi's
+// block holding position len[bi] - 1, pooled only when that token completes it.
+template <int HD, int KT>
 __global__ void __launch_bounds__(256)
 k_pool(Geo g, qwfn_kv_view v, const int32_t *seq_ids, const int32_t *block_ids, int32_t seq_const,
-       int32_t blk0) {
+       int32_t blk0, const int32_t *len) {
     __shared__ int8_t q8[kStageRows * HD];
     __shared__ uint16_t sc[kStageRows * (HD / 32)];
     const int bi = blockIdx.x, gh = blockIdx.y, tid = threadIdx.x;
-    const int seq = seq_ids ? seq_ids[bi] : seq_const;
-    const int b = block_ids ? block_ids[bi] : blk0 + bi;
+    if (len && (len[bi] < 1 || len[bi] % g.bt)) return;   // no block completed (a bad length is the append's report)
+    const int seq = len ? bi : seq_ids ? seq_ids[bi] : seq_const;
+    const int b = len ? (len[bi] - 1) / g.bt : block_ids ? block_ids[bi] : blk0 + bi;
     const bool report = (gh == 0 && tid == 0);
     if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
     if (b < 0 || b >= g.bps) { if (report) set_status(v.status, QWFN_STATUS_BLOCK_RANGE); return; }
@@ -398,8 +508,8 @@ k_pool(Geo g, qwfn_kv_view v, const int32_t *seq_ids, const int32_t *block_ids, 
     const int32_t pp = phys_page(g, v.page_table, seq, t0);   // a block never straddles pages
     if (pp < 0) { if (report) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
     const uint8_t *page = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
-    pool_block_dev<HD>(g, page, gh, t0 % g.pt, v.pooled + (((int64_t)seq * g.Hkv + gh) * g.bps + b) * HD,
-                       nullptr, q8, sc, tid, 256);
+    pool_block_dev<HD, KT>(g, page, gh, t0 % g.pt, v.pooled + (((int64_t)seq * g.Hkv + gh) * g.bps + b) * HD,
+                           nullptr, q8, sc, tid, 256);
 }
 
 // ---------------------------------------------------------------------------
@@ -1153,7 +1263,15 @@ template <int HD, int G>
 static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                              int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                             const FusedAppend &fa, hipStream_t st) {
+                             FusedAppend fa, hipStream_t st) {
+    // The append workgroup is q8_0's, and its pooled block must not be one the
+    // scoring workgroups read: with local_tokens = 0 a just-completed block is
+    // eligible.  Otherwise the append and the pooling run as launches of their own.
+    if (fa.enabled && (g.kt != QWFN_KV_Q8_0 || g.local == 0)) {
+        launch_append(g, v, fa.k_new, fa.v_new, fa.src_f16, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
+        launch_pool(g, v, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
+        fa.enabled = 0;
+    }
     const int nb_max = max_seq_len / g.bt;
     int n_chunks = (nb_max + kBlocksPerChunk - 1) / kBlocksPerChunk;
     if (n_chunks < 1) n_chunks = 1;
@@ -1380,12 +1498,15 @@ struct AttnShared {
     int flag;
 };
 
-template <int HD, int G, int TG>
+// KT: the K/V element type (chunks of a head row, and their dequantization).
+template <int HD, int G, int TG, int KT>
 __global__ void __launch_bounds__((AttnCfg<HD, G, TG>::NT))
 k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len,
        int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
        float *__restrict__ out, Ws ws, int32_t n_parts) {
     using C = AttnCfg<HD, G, TG>;
+    constexpr int CHK = row_bytes_t<HD, KT>() / 16;               // 16-byte chunks per head row
+    constexpr int PERK = (64 * CHK + C::NTG - 1) / C::NTG;      // K (and V) chunk loads per thread
     __shared__ AttnShared<HD, G, TG> sh;
     const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);   // tile group (wave-uniform)
@@ -1428,23 +1549,23 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         }
         __syncthreads();
         // every global load of the tile is issued before any is consumed
-        uint4 kq[C::PER], vq[C::PER];
+        uint4 kq[PERK], vq[PERK];
 #pragma unroll
-        for (int i = 0; i < C::PER; ++i) {
+        for (int i = 0; i < PERK; ++i) {
             const int k = lt + i * C::NTG;
             kq[i] = make_uint4(0, 0, 0, 0);
             vq[i] = make_uint4(0, 0, 0, 0);
-            if (k < 64 * C::CH) {
+            if (k < 64 * CHK) {
                 const int cell = k % 64, ch = k / 64, rw = gr.row[cell];
                 if (rw >= 0) {
                     const int64_t off = (int64_t)gr.page[cell] * g.page_bytes +
-                                        ((int64_t)(gh * (g.pt / 64) + rw / 64) * C::CH + ch) * 1024 + (rw % 64) * 16;
+                                        ((int64_t)(gh * (g.pt / 64) + rw / 64) * CHK + ch) * 1024 + (rw % 64) * 16;
                     kq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.k_pages + off);
                     vq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.v_pages + off);
                 }
             }
         }
-        for (int k = lt; k < 128; k += C::NTG) {
+        for (int k = lt; k < (KT == QWFN_KV_F16 ? 0 : 128); k += C::NTG) {
             const int cell = k % 64, rw = gr.row[cell];
             const bool isv = k >= 64;
             uint16_t *dst = isv ? gr.vsc[cell] : gr.ksc[cell];
@@ -1463,21 +1584,49 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
         // dequantize (exact: fp16 scale times int8) into the group's LDS tile
         auto dequant = [&](const uint4 *qv, uint16_t (*scl)[HD / 32]) {
 #pragma unroll
-            for (int i = 0; i < C::PER; ++i) {
+            for (int i = 0; i < PERK; ++i) {
                 const int k = lt + i * C::NTG;
-                if (k < 64 * C::CH) {
+                if (k < 64 * CHK) {
                     const int cell = k % 64, ch = k / 64;
-                    const float scf = h2f(scl[cell][ch / 2]);
                     const uint32_t w[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
-                    float *dst = &gr.kv[cell * C::ROWF + ch * 16];
+                    if (KT == QWFN_KV_F16) {              // chunk = dims 8ch .. 8ch+7
+                        float *dst = &gr.kv[cell * C::ROWF + ch * 8];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        float4 f;
-                        f.x = scf * (float)(int8_t)(w[u] & 0xFF);
-                        f.y = scf * (float)(int8_t)((w[u] >> 8) & 0xFF);
-                        f.z = scf * (float)(int8_t)((w[u] >> 16) & 0xFF);
-                        f.w = scf * (float)(int8_t)(w[u] >> 24);
-                        *reinterpret_cast<float4 *>(dst + 4 * u) = f;
+                        for (int u = 0; u < 2; ++u) {
+                            const uint32_t a = w[2 * u], b = w[2 * u + 1];
+                            *reinterpret_cast<float4 *>(dst + 4 * u) =
+                                make_float4(h2f((uint16_t)a), h2f((uint16_t)(a >> 16)), h2f((uint16_t)b),
+                                            h2f((uint16_t)(b >> 16)));
+                        }
+                    } else if (KT == QWFN_KV_Q4_0) {      // chunk = ggml block ch: dims 32ch .. 32ch+31
+                        const float scf = h2f(scl[cell][ch]);
+                        float *dst = &gr.kv[cell * C::ROWF + ch * 32];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            float4 lo, hi;               // bytes 4u .. 4u+3: dims 4u.. (low), 16+4u.. (high)
+                            lo.x = scf * (float)((int)(w[u] & 15) - 8);
+                            lo.y = scf * (float)((int)((w[u] >> 8) & 15) - 8);
+                            lo.z = scf * (float)((int)((w[u] >> 16) & 15) - 8);
+                            lo.w = scf * (float)((int)((w[u] >> 24) & 15) - 8);
+                            hi.x = scf * (float)((int)((w[u] >> 4) & 15) - 8);
+                            hi.y = scf * (float)((int)((w[u] >> 12) & 15) - 8);
+                            hi.z = scf * (float)((int)((w[u] >> 20) & 15) - 8);
+                            hi.w = scf * (float)((int)(w[u] >> 28) - 8);
+                            *reinterpret_cast<float4 *>(dst + 4 * u) = lo;
+                            *reinterpret_cast<float4 *>(dst + 16 + 4 * u) = hi;
+                        }
+                    } else {                              // chunk = 16 dims of int8
+                        const float scf = h2f(scl[cell][ch / 2]);
+                        float *dst = &gr.kv[cell * C::ROWF + ch * 16];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            float4 f;
+                            f.x = scf * (float)(int8_t)(w[u] & 0xFF);
+                            f.y = scf * (float)(int8_t)((w[u] >> 8) & 0xFF);
+                            f.z = scf * (float)(int8_t)((w[u] >> 16) & 0xFF);
+                            f.w = scf * (float)(int8_t)(w[u] >> 24);
+                            *reinterpret_cast<float4 *>(dst + 4 * u) = f;
+                        }
                     }
                 }
             }
@@ -1592,8 +1741,16 @@ static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const Ws &ws, hipStream_t st) {
     const int n_parts = (ws.n_tiles + TG - 1) / TG;
     const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
-    hipLaunchKernelGGL((k_attn<HD, G, TG>), grid, dim3(AttnCfg<HD, G, TG>::NT), 0, st, g, v, q, seq_len,
-                       max_seq_len, sel, nsel, max_sel, out, ws, n_parts);
+    const dim3 blk(AttnCfg<HD, G, TG>::NT);
+    if (g.kt == QWFN_KV_Q4_0)
+        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q4_0>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
+                           nsel, max_sel, out, ws, n_parts);
+    else if (g.kt == QWFN_KV_F16)
+        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_F16>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
+                           nsel, max_sel, out, ws, n_parts);
+    else
+        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q8_0>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
+                           nsel, max_sel, out, ws, n_parts);
 }
 
 // ---------------------------------------------------------------------------
@@ -1976,6 +2133,38 @@ k_kv_rows(Geo g, qwfn_kv_view v, int32_t seq, int32_t pos0, int32_t n, uint8_t *
         uint8_t *rows = which ? v_rows : k_rows;
         if (!rows) continue;
         uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
+        if (g.kt != QWFN_KV_Q8_0) {
+            // q4_0: ggml block {fp16 d; uint8 qs[16]} = the scale + chunk j;
+            // fp16: the block's 32 values = chunks 4j .. 4j+3.  Rows are 2-byte aligned.
+            const bool q4 = g.kt == QWFN_KV_Q4_0;
+            uint16_t *rb = reinterpret_cast<uint16_t *>(rows + i * (q4 ? 18 : 64));
+            uint16_t *cb = q4 ? rb + 1 : rb;
+            const int nc = q4 ? 1 : 4, c0 = q4 ? j : 4 * j;
+            for (int c = 0; c < nc; ++c) {
+                uint4 *cp = reinterpret_cast<uint4 *>(page + chunk_off(g, gh, row, c0 + c));
+                if (EXPORT) {
+                    const uint4 a = *cp;
+                    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        cb[8 * c + 2 * k] = (uint16_t)w[k];
+                        cb[8 * c + 2 * k + 1] = (uint16_t)(w[k] >> 16);
+                    }
+                } else {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        w[k] = (uint32_t)cb[8 * c + 2 * k] | ((uint32_t)cb[8 * c + 2 * k + 1] << 16);
+                    *cp = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+            if (q4) {
+                uint16_t *sp = reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j));
+                if (EXPORT) rb[0] = *sp;
+                else *sp = rb[0];
+            }
+            continue;
+        }
         uint16_t *rb = reinterpret_cast<uint16_t *>(rows + i * 34);          // 2-byte aligned
         uint16_t *sp = reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j));
         if (!(which && g.vdim)) {                  // 16 dims of one token per 16-byte chunk
@@ -2233,17 +2422,28 @@ bool kernels_for(int32_t hd, int32_t G) {
     return false;
 }
 
-hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
-                       const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
-                       int32_t blk0, hipStream_t st) {
+template <int KT>
+static hipError_t launch_pool_t(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
+                                const int32_t *block_ids, int32_t n_blocks, int32_t seq_const, int32_t blk0,
+                                hipStream_t st, const int32_t *len) {
     const dim3 grid((unsigned)n_blocks, (unsigned)g.Hkv);
     switch (g.hd) {
-    case 64:  hipLaunchKernelGGL(k_pool<64>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0); break;
-    case 128: hipLaunchKernelGGL(k_pool<128>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0); break;
-    case 256: hipLaunchKernelGGL(k_pool<256>, grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0); break;
+    case 64:  hipLaunchKernelGGL((k_pool<64, KT>), grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0, len); break;
+    case 128: hipLaunchKernelGGL((k_pool<128, KT>), grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0, len); break;
+    case 256: hipLaunchKernelGGL((k_pool<256, KT>), grid, dim3(256), 0, st, g, v, seq_ids, block_ids, seq_const, blk0, len); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
+                       const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
+                       int32_t blk0, hipStream_t st, const int32_t *len) {
+    switch (g.kt) {
+    case QWFN_KV_Q4_0: return launch_pool_t<QWFN_KV_Q4_0>(g, v, seq_ids, block_ids, n_blocks, seq_const, blk0, st, len);
+    case QWFN_KV_F16:  return launch_pool_t<QWFN_KV_F16>(g, v, seq_ids, block_ids, n_blocks, seq_const, blk0, st, len);
+    default:           return launch_pool_t<QWFN_KV_Q8_0>(g, v, seq_ids, block_ids, n_blocks, seq_const, blk0, st, len);
+    }
 }
 
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,

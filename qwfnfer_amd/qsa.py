@@ -50,6 +50,7 @@ class QsaConfig:
     shared_selection: int = 0
     quant_variant: int = _lib.Q8_X86_RNE
     topk_counts_forced: int = 0
+    kv_type: int = _lib.KV_Q8_0
 
     @property
     def group(self) -> int:
@@ -63,7 +64,7 @@ class QsaConfig:
         return QsaShape(self.n_head, self.n_head_kv, self.head_dim, self.block_tokens,
                         self.page_tokens, self.top_k_blocks, self.sink_blocks,
                         self.local_tokens, self.relu_per_head, self.shared_selection,
-                        self.quant_variant, self.topk_counts_forced)
+                        self.quant_variant, self.topk_counts_forced, self.kv_type)
 
     def check(self) -> None:
         s = self.shape()

@@ -3,18 +3,20 @@ reference's own cache rows.
 
 The reference keeps no snapshot of its caches (its state lives only in the
 backend buffers of ``state::init``, /root/reference src/qwfn_state.cpp:18-96).
-A snapshot here is the token-major q8_0 rows of that state -- row t = the
-token's ``n_head_kv * head_dim / 32`` ggml ``block_q8_0`` {fp16 d; int8
-qs[32]}, head-major (src/qwfn_state.cpp:40, 52-53) -- for K and for V, behind a
-small self-describing header, so a C++ engine can write or read the same bytes
-with fread/fwrite and no other dependency.
+A snapshot here is the token-major rows of that state -- row t = the token's
+``n_head_kv * head_dim`` values, head-major (src/qwfn_state.cpp:40, 52-53), in
+ggml's layout of the cache type: ``block_q8_0`` {fp16 d; int8 qs[32]},
+``block_q4_0`` {fp16 d; uint8 qs[16]} or fp16 values -- for K and for V, behind
+a small self-describing header, so a C++ engine can write or read the same
+bytes with fread/fwrite and no other dependency.
 
 File format, little-endian:
 
     offset 0   8 bytes   magic b"QWFNKV\\x00\\x01"
     offset 8   4 bytes   u32 H, the header length
-    offset 12  H bytes   UTF-8 JSON object: format ("ggml-q8_0-rows"),
-                         n_head_kv, head_dim, block_tokens, quant_variant,
+    offset 12  H bytes   UTF-8 JSON object: format ("ggml-q8_0-rows",
+                         "ggml-q4_0-rows" or "ggml-f16-rows"), n_head_kv,
+                         head_dim, block_tokens, quant_variant, kv_type,
                          n_tokens, row_bytes, k_offset, v_offset
     k_offset             K rows, n_tokens * row_bytes bytes
     v_offset             V rows, n_tokens * row_bytes bytes
@@ -31,13 +33,16 @@ from typing import Optional, Tuple
 import numpy as np
 
 MAGIC = b"QWFNKV\x00\x01"
-FORMAT = "ggml-q8_0-rows"
+FORMATS = {0: "ggml-q8_0-rows", 1: "ggml-q4_0-rows", 2: "ggml-f16-rows"}   # by kv_type
+FORMAT = FORMATS[0]
 _FIELDS = ("n_head_kv", "head_dim", "block_tokens", "quant_variant")
 
 
-def row_bytes(n_head_kv: int, head_dim: int) -> int:
-    """One token's row of the reference's q8_0 cache tensor."""
-    return n_head_kv * (head_dim // 32) * 34
+def row_bytes(n_head_kv: int, head_dim: int, kv_type: int = 0) -> int:
+    """One token's row of the reference's cache tensor of the type."""
+    if kv_type == 2:
+        return n_head_kv * head_dim * 2
+    return n_head_kv * (head_dim // 32) * (18 if kv_type == 1 else 34)
 
 
 def write_snapshot_file(path: str, header: dict, k_rows: np.ndarray, v_rows: np.ndarray) -> dict:
@@ -49,13 +54,16 @@ def write_snapshot_file(path: str, header: dict, k_rows: np.ndarray, v_rows: np.
     missing = [f for f in _FIELDS if f not in header]
     if missing:
         raise ValueError(f"snapshot header lacks {missing}")
-    rb = row_bytes(int(header["n_head_kv"]), int(header["head_dim"]))
+    kt = int(header.get("kv_type", 0))
+    if kt not in FORMATS:
+        raise ValueError(f"kv_type {kt} unknown")
+    rb = row_bytes(int(header["n_head_kv"]), int(header["head_dim"]), kt)
     if k_rows.ndim != 2 or k_rows.shape[1] != rb or v_rows.shape != k_rows.shape:
         raise ValueError(f"rows must be uint8 [n_tokens, {rb}] for K and V alike, got "
                          f"{k_rows.shape} and {v_rows.shape}")
     n = int(k_rows.shape[0])
-    h = {"format": FORMAT, **{f: int(header[f]) for f in _FIELDS}, "n_tokens": n, "row_bytes": rb,
-         "k_offset": 0, "v_offset": 0}
+    h = {"format": FORMATS[kt], **{f: int(header[f]) for f in _FIELDS}, "kv_type": kt, "n_tokens": n,
+         "row_bytes": rb, "k_offset": 0, "v_offset": 0}
     # the offsets depend on the header's own length: iterate to the fixed point
     # (the length only grows with the offsets' digits, so this settles at once)
     while True:
@@ -82,10 +90,11 @@ def read_snapshot_file(path: str) -> Tuple[dict, np.ndarray, np.ndarray]:
             raise ValueError(f"{path}: not a KV snapshot (magic {magic!r})")
         (hl,) = struct.unpack("<I", f.read(4))
         h = json.loads(f.read(hl).decode("utf-8"))
-    if h.get("format") != FORMAT:
+    kt = int(h.get("kv_type", 0))
+    if kt not in FORMATS or h.get("format") != FORMATS[kt]:
         raise ValueError(f"{path}: unknown snapshot format {h.get('format')!r}")
     n, rb = int(h["n_tokens"]), int(h["row_bytes"])
-    if rb != row_bytes(int(h["n_head_kv"]), int(h["head_dim"])):
+    if rb != row_bytes(int(h["n_head_kv"]), int(h["head_dim"]), kt):
         raise ValueError(f"{path}: row_bytes {rb} does not match the head shape")
     mm = np.memmap(path, dtype=np.uint8, mode="r")
     k0, v0 = int(h["k_offset"]), int(h["v_offset"])
@@ -103,7 +112,8 @@ def save_snapshot(cache, path: str, seq: int, n_tokens: int, stream=None) -> dic
     torch.cuda.synchronize()
     cfg = cache.cfg
     return write_snapshot_file(path, {"n_head_kv": cfg.n_head_kv, "head_dim": cfg.head_dim,
-                                      "block_tokens": cfg.block_tokens, "quant_variant": cfg.quant_variant},
+                                      "block_tokens": cfg.block_tokens, "quant_variant": cfg.quant_variant,
+                                      "kv_type": cfg.kv_type},
                                kr.cpu().numpy(), vr.cpu().numpy())
 
 
@@ -115,8 +125,8 @@ def load_snapshot(cache, path: str, seq: int, stream=None) -> int:
     from . import qsa
     h, kr, vr = read_snapshot_file(path)
     cfg = cache.cfg
-    for f in ("n_head_kv", "head_dim", "block_tokens"):
-        if int(h[f]) != int(getattr(cfg, f)):
+    for f in ("n_head_kv", "head_dim", "block_tokens", "kv_type"):
+        if int(h.get(f, 0)) != int(getattr(cfg, f)):
             raise ValueError(f"{path}: {f} {h[f]} does not match the cache's {getattr(cfg, f)}")
     n = int(h["n_tokens"])
     dev = cache.k_pages.device

@@ -28,6 +28,7 @@ class Cfg:
     shared_selection: int = 0
     quant_variant: int = 0
     topk_counts_forced: int = 0
+    kv_type: int = 0
 
     @property
     def group(self):

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.qwfn_qsa_abi_version() == 2
+    assert lib.qwfn_qsa_abi_version() == 3
 
 
 def _code(name, *args):
@@ -41,6 +41,7 @@ def test_shape_validation():
         dict(n_head=15), dict(head_dim=100), dict(page_tokens=100), dict(block_tokens=48),
         dict(local_tokens=-1), dict(sink_blocks=-1), dict(quant_variant=3), dict(relu_per_head=2),
         dict(topk_counts_forced=2), dict(topk_counts_forced=1, top_k_blocks=1),   # 1 < sink + window
+        dict(kv_type=3), dict(kv_type=-1),
     ]
     for kw in bad:
         s = QsaConfig(**{**ok.__dict__, **kw}).shape()

@@ -1,0 +1,140 @@
+"""Parity of the q4_0 and fp16 cache types (the reference's --kv q4_0 / f16,
+tools/qwfn_gen.cpp:55-57) with the CPU oracle, through the C ABI.
+
+Bit-exact: cache bytes after appends (f32 and f16 sources, permuted pages),
+pooled keys, selected blocks, exported rows (ggml's block_q4_0 / fp16 rows).
+Attention within 2e-3 + 1e-3 |ref| of the fp64 oracle over the same
+dequantized cache: fused decode steps and prefill chunks, at BASELINE shapes
+(the general attention kernel for these types), the tiny shape and the
+checkpoint head shape."""
+import numpy as np
+import pytest
+import torch
+
+from _gpu import cfg_of, fill, kv_rows, make_pair, np_of
+from _refs import BASELINE, TINY, Cfg
+from oracle import oracle as O
+from qwfnfer_amd import qsa, snapshot
+from test_gpu_parity import _decode_steps, _prefill_case
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [1, 2]                              # QWFN_KV_Q4_0, QWFN_KV_F16
+G12 = Cfg(n_head=24, n_head_kv=2, head_dim=256, block_tokens=4, page_tokens=128, top_k_blocks=40,
+          sink_blocks=1, local_tokens=16)
+
+
+def with_type(cfg, kt):
+    return Cfg(**{**cfg.__dict__, "kv_type": kt})
+
+
+@pytest.mark.parametrize("kt", TYPES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_append_bytes_match_oracle(kt, dtype):
+    cfg = with_type(BASELINE, kt)
+    rng = np.random.default_rng(950 + kt)
+    dev, host = make_pair(cfg, 2, 3, seed=951, spare=2)
+    n = 300
+    seq = rng.integers(0, 2, n).astype(np.int32)
+    pos = rng.permutation(3 * 256)[:n].astype(np.int32)
+    k, v = kv_rows(rng, n, cfg)
+    k[0, 0, :32] = 0.0                                 # a zero block: d = -0
+    k[1, 0, :32] = np.arange(32) % 16 - 8              # magnitude ties
+    k, v = k.astype(dtype), v.astype(dtype)
+    assert host.append(k, v, pos, seq) == 0
+    for _ in range(2):                                 # idempotent overwrite
+        qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                        torch.from_numpy(pos).cuda(), torch.from_numpy(seq).cuda())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+        np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
+    assert qsa.read_status(dev) == 0
+
+
+@pytest.mark.parametrize("kt", TYPES)
+def test_pool_and_select_match_oracle(kt):
+    cfg = with_type(BASELINE, kt)
+    rng = np.random.default_rng(960 + kt)
+    L = 6000
+    dev, host = make_pair(cfg, 1, L // 256 + 1, seed=961)
+    fill(dev, host, rng, [L])                          # appends + pool_rebuild, compared below
+    np.testing.assert_array_equal(np_of(dev.pooled)[:, :, :L // 64], host.pooled[:, :, :L // 64])
+    q = rng.standard_normal((1, 16, 128), dtype=np.float32)
+    ws = qsa.Workspace(cfg_of(cfg), 1, L)
+    sel, nsel = qsa.indexer_topk(dev, torch.from_numpy(q).cuda(), torch.tensor([L], dtype=torch.int32,
+                                                                                 device="cuda"), L, ws)
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), torch.tensor([L], dtype=torch.int32,
+                                                                                  device="cuda"), L, ws, sel, nsel)
+    torch.cuda.synchronize()
+    hs, hn = host.indexer_topk(q, [L], max_sel=sel.shape[-1])
+    np.testing.assert_array_equal(np_of(nsel), hn)
+    for g in range(2):
+        np.testing.assert_array_equal(np_of(sel)[0, g, :hn[0, g]], hs[0, g, :hn[0, g]])
+    from _gpu import assert_close_attn
+    assert_close_attn(np_of(out), host.attention_f64(q, [L], hs, hn), f"kv_type {kt}")
+
+
+@pytest.mark.parametrize("kt", TYPES)
+def test_decode_steps(kt):
+    _decode_steps(with_type(BASELINE, kt), [4096 - 3], steps=6, seed=970 + kt)
+    _decode_steps(with_type(TINY, kt), [130, 61], steps=6, seed=972 + kt, dtype=np.float16)
+
+
+@pytest.mark.parametrize("kt", TYPES)
+def test_decode_steps_checkpoint_heads(kt):
+    _decode_steps(with_type(G12, kt), [700], steps=5, seed=975 + kt)
+
+
+@pytest.mark.parametrize("kt", TYPES)
+def test_prefill(kt):
+    _prefill_case(with_type(BASELINE, kt), 3000, 150, seed=980 + kt)
+    _prefill_case(with_type(TINY, kt), 90, 70, seed=982 + kt, dtype=np.float16)
+
+
+@pytest.mark.parametrize("kt", TYPES)
+def test_export_import_rows(kt):
+    cfg = with_type(BASELINE, kt)
+    rng = np.random.default_rng(990 + kt)
+    dev, host = make_pair(cfg, 1, 2, seed=991)
+    L = 400
+    k, v = kv_rows(rng, L, cfg)
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                    torch.arange(L, dtype=torch.int32, device="cuda"))
+    rb = cfg_of(cfg).row_bytes()
+    assert rb == (2 * 4 * 18 if kt == 1 else 2 * 128 * 2)
+    kr, vr = qsa.export_rows_q8_0(dev, 0, 0, L)
+    torch.cuda.synchronize()
+    want_k = np.stack([O.quantize_row_type(k[t].ravel(), kt) for t in range(L)])
+    want_v = np.stack([O.quantize_row_type(v[t].ravel(), kt) for t in range(L)])
+    np.testing.assert_array_equal(np_of(kr), want_k)
+    np.testing.assert_array_equal(np_of(vr), want_v)
+    # import into a fresh cache (other pages) gives the same bytes; arbitrary bytes round-trip
+    dev2, _ = make_pair(cfg, 1, 2, seed=992)
+    qsa.import_rows_q8_0(dev2, 0, 0, kr, vr)
+    kr2, vr2 = qsa.export_rows_q8_0(dev2, 0, 0, L)
+    junk = torch.randint(0, 256, (L, rb), dtype=torch.uint8, device="cuda")
+    if kt == 2:                                        # keep fp16 rows free of NaN bit patterns for the compare
+        junk[:, 1::2] &= 0x3F
+    qsa.import_rows_q8_0(dev2, 0, 0, junk, junk)
+    kj, vj = qsa.export_rows_q8_0(dev2, 0, 0, L)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np_of(kr2), np_of(kr))
+    np.testing.assert_array_equal(np_of(vr2), np_of(vr))
+    np.testing.assert_array_equal(np_of(kj), np_of(junk))
+    np.testing.assert_array_equal(np_of(vj), np_of(junk))
+    assert qsa.read_status(dev) == 0 and qsa.read_status(dev2) == 0
+
+
+@pytest.mark.parametrize("kt", TYPES)
+def test_snapshot_round_trip(kt, tmp_path):
+    cfg = with_type(BASELINE, kt)
+    rng = np.random.default_rng(995 + kt)
+    dev, host = make_pair(cfg, 1, 3, seed=996)
+    fill(dev, host, rng, [700])
+    path = str(tmp_path / "kv.snap")
+    h = snapshot.save_snapshot(dev, path, 0, 700)
+    assert h["format"] == snapshot.FORMATS[kt] and h["kv_type"] == kt
+    dev2, _ = make_pair(cfg, 2, 3, seed=997)
+    assert snapshot.load_snapshot(dev2, path, 1) == 700
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np_of(dev2.pooled)[1, :, :700 // 64], np_of(dev.pooled)[0, :, :700 // 64])
