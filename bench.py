@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
+    ap.add_argument("--no-kv-types", action="store_true",
+                    help="skip the q4_0 / fp16 cache lines (config 3 at the longest context)")
     ap.add_argument("--no-checkpoint", action="store_true",
                     help="skip the checkpoint-layer decode line (the released model's own indexer)")
     ap.add_argument("--prefill-batch", type=int, default=8192,
@@ -268,7 +270,9 @@ class Runner:
         sel = self.sel.cpu().numpy()
         nsel = self.nsel.cpu().numpy()
         cells = selected_cells(sel, nsel, lengths, cfg.block_tokens)
-        row = cfg.head_dim + cfg.head_dim // 32 * 2              # 136 B per (token, KV head)
+        # bytes per (token, KV head): q8_0 136 B, q4_0 72 B, fp16 256 B at head_dim 128
+        row = {0: cfg.head_dim + cfg.head_dim // 16, 1: cfg.head_dim // 2 + cfg.head_dim // 16,
+               2: 2 * cfg.head_dim}[cfg.kv_type]
         kv = cells * row * 2
         pooled = 0
         for L in lengths:
@@ -565,6 +569,30 @@ def main():
         log(f"[bench] config 4 prefill chunk (8192 queries at 155648): {prefill['ms_per_chunk']:.3f} ms, "
             f"{prefill['attn_tflops']:.1f} TFLOP/s on the selected-cell FLOPs")
 
+    kv_types = None
+    if not args.no_kv_types:
+        import dataclasses
+        kv_types = {}
+        ctx = max(contexts)
+        for kt, name in ((1, "q4_0"), (2, "f16")):
+            c2 = dataclasses.replace(cfg, kv_type=kt)
+            pps = (ctx + DECODE_ROOM + c2.page_tokens - 1) // c2.page_tokens
+            pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+            r = Runner(qsa, torch, c2, [ctx], args.layers, pps, pt, gen)
+            r.capture()
+            ms = r.time_steps(max(30, args.steps // 3), args.warmup, graph=True)
+            sel_us, att_us = r.time_kernels(64)
+            r.check_room()
+            kv, pooled, cells = r.bytes_per_layer()
+            kv_types[name] = dict(context=ctx, us_per_layer=round(ms * 1e3 / args.layers, 3),
+                                  select_kernel_us=round(sel_us, 3), attn_kernel_us=round(att_us, 3),
+                                  cells_per_layer=cells, selected_kv_bytes=kv,
+                                  attn_gbs=round(kv / (att_us * 1e-6) / 1e9, 1), replicas=r.n_inst)
+            log(f"[bench] kv {name} ctx {ctx}: {ms * 1e3 / args.layers:.2f} us/layer, select {sel_us:.2f} us, "
+                f"attn {att_us:.2f} us (general attention kernel)")
+            del r
+            torch.cuda.empty_cache()
+
     checkpoint = None
     if not args.no_checkpoint:
         ck = {}
@@ -636,6 +664,7 @@ def main():
         "batched_config5": batched,
         "prefill_config4": prefill,
         "checkpoint_decode": checkpoint,
+        "kv_types": kv_types,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }
