@@ -380,3 +380,13 @@ def test_prefill_other_shapes():
 def test_prefill_shared_selection():
     _prefill_case(Cfg(shared_selection=1), 6000, 96, seed=650)
     _prefill_case(Cfg(**{**TINY.__dict__, "shared_selection": 1, "relu_per_head": 1}), 90, 70, seed=651)
+
+
+def test_prefill_odd_chunks_and_batches():
+    # an odd chunk in odd batches (5 queries per launch pair) gives the same
+    # bytes as one batch; a group of 4 heads on the matrix cores
+    a = _prefill_case(BASELINE, 5003, 37, seed=660)
+    b = _prefill_case(BASELINE, 5003, 37, seed=660, q_batch=5)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    _prefill_case(Cfg(n_head=8, n_head_kv=2, top_k_blocks=8, local_tokens=100), 3000, 41, seed=661)   # G = 4
