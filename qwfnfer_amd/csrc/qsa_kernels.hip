@@ -1466,34 +1466,72 @@ __device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts
     }
 }
 
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef int32_t i4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));   // plain 16-byte load/store (no struct copy)
+
+// Sum / max over the lanes l, l^16, l^32, l^48 (the four k-groups of one MFMA
+// column), by the gfx950 row swaps: v_permlane32_swap pairs lane l with l^32
+// and v_permlane16_swap pairs row 2r with 2r+1; both results are symmetric, so
+// every lane of the column ends with the same value.
+__device__ __forceinline__ unsigned opaque_copy(unsigned x) {
+    unsigned y;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+    return y;
+}
+// Lane l with lane l ^ 32 (permlane32) or l ^ 16 (permlane16), combined by op.
+// The swap gets two registers the compiler cannot prove equal: given one value
+// twice it would take the two results as equal and keep only the first.
+template <typename Op>
+__device__ __forceinline__ float swap32_op(float v, Op op) {
+    const unsigned b = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, opaque_copy(b), false, false);
+    const unsigned r0 = r[0], r1 = r[1];                  // (bit_cast of r[i] reads element 0)
+    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+template <typename Op>
+__device__ __forceinline__ float swap16_op(float v, Op op) {
+    const unsigned b = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, opaque_copy(b), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float col_sum4(float v) {
+    const auto add = [](float a, float b) { return a + b; };
+    return swap16_op(swap32_op(v, add), add);
+}
+__device__ __forceinline__ float col_max4(float v) {
+    const auto mx = [](float a, float b) { return fmaxf(a, b); };
+    return swap16_op(swap32_op(v, mx), mx);
+}
+
 template <int HD, int G, int TG>
 struct AttnCfg {
-    static constexpr int NW = G >= 4 ? 4 : G;          // waves per group
-    static constexpr int HPW = G / NW;                 // query heads per wave
+    static constexpr int NW = 4;                       // waves per group (a 64-cell tile)
     static constexpr int NTG = NW * 64;                // threads per group
     static constexpr int NT = TG * NTG;                // threads per workgroup
-    static constexpr int CH = HD / 16;                 // 16-byte chunks per head row
-    static constexpr int ROWF = HD + 4;                // padded LDS row (floats)
-    static constexpr int DPL = HD / 64;                // PV dims per lane
-    static constexpr int PER = (64 * CH + NTG - 1) / NTG;   // 16-byte K (and V) loads per thread
+    static constexpr int ROWF = HD + 4;                // K' row (floats): cell-major, padded
+    static constexpr int VROWF = 64 + 4;               // V' row (floats): dim-major, padded
+    static constexpr int KVF = 64 * ROWF > HD * VROWF ? 64 * ROWF : HD * VROWF;   // K', then V', then O
     static constexpr int OPT = (G * HD + NT - 1) / NT; // merged outputs per thread
-    static_assert(G % NW == 0, "group size");
+    static_assert(G <= 16, "one MFMA output column per query head");
     static_assert(HD % 64 == 0, "head_dim");
 };
 
 template <int HD, int G>
 struct AttnGroup {
-    float kv[64 * (HD + 4)];                   // K' then V' (dequantized), then the group's O
-    float p[G][64];
+    float kv[AttnCfg<HD, G, 1>::KVF];          // K' [cell][HD], then V' [dim][cell], then the group's O [G][HD]
+    float p[16][64 + 4];                       // softmax weights, [column][cell]
     uint16_t ksc[64][HD / 32], vsc[64][HD / 32];
     int32_t page[64], row[64];
     float m[G], l[G];
+    float rm[4][16], rl[4][16];                // per-wave column max / sum
 };
 
 template <int HD, int G, int TG>
 struct AttnShared {
     AttnGroup<HD, G> grp[TG];
-    float q[G * HD];                           // the KV head's query heads
     float Lh[2 * G];                           // combine: L_h, then M_h
     int flag;
 };
@@ -1507,6 +1545,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     using C = AttnCfg<HD, G, TG>;
     constexpr int CHK = row_bytes_t<HD, KT>() / 16;               // 16-byte chunks per head row
     constexpr int PERK = (64 * CHK + C::NTG - 1) / C::NTG;      // K (and V) chunk loads per thread
+    static_assert(sizeof(AttnShared<HD, G, TG>) <= 160 * 1024, "LDS of the tile groups");
     __shared__ AttnShared<HD, G, TG> sh;
     const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);   // tile group (wave-uniform)
@@ -1524,10 +1563,15 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     const int parts_act = (tiles_act + TG - 1) / TG;
     const int part = blockIdx.x;
     if (ok && part < parts_act) {
-        {   // the group of query heads, staged once for all waves
-            const float *qg = q + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
-            for (int i = tid * 4; i < G * HD; i += C::NT * 4)
-                *reinterpret_cast<float4 *>(&sh.q[i]) = *reinterpret_cast<const float4 *>(qg + i);
+        // the query as the QK operand: lane l holds head l%16 (0 past the
+        // group), dims 16i + 4(l/16) .. +3 of every 16-dim step i
+        const int lane = lt & 63, wq = __builtin_amdgcn_readfirstlane(lt >> 6), qcol = lane & 15, qk = lane >> 4;
+        float4 qreg[HD / 16];
+        {
+            const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + min(qcol, G - 1)) * HD + 4 * qk;
+#pragma unroll
+            for (int i = 0; i < HD / 16; ++i)
+                qreg[i] = qcol < G ? *reinterpret_cast<const float4 *>(qh + 16 * i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
         const int tile = part * TG + gi;
         const bool active = tile < tiles_act;
@@ -1581,116 +1625,127 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
             }
         }
         __syncthreads();
-        // dequantize (exact: fp16 scale times int8) into the group's LDS tile
-        auto dequant = [&](const uint4 *qv, uint16_t (*scl)[HD / 32]) {
+        // dequantize exactly (fp16 scale times the quant, or the fp16 value)
+        // into the group's LDS tile: K' cell-major, V' dim-major (transposed)
+        auto dequant = [&](const uint4 *qv, uint16_t (*scl)[HD / 32], bool vt) {
+            float *base = gr.kv;
 #pragma unroll
             for (int i = 0; i < PERK; ++i) {
                 const int k = lt + i * C::NTG;
                 if (k < 64 * CHK) {
                     const int cell = k % 64, ch = k / 64;
                     const uint32_t w[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+                    float x[KT == QWFN_KV_Q4_0 ? 32 : KT == QWFN_KV_F16 ? 8 : 16];
+                    int d0;
                     if (KT == QWFN_KV_F16) {              // chunk = dims 8ch .. 8ch+7
-                        float *dst = &gr.kv[cell * C::ROWF + ch * 8];
+                        d0 = 8 * ch;
 #pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            const uint32_t a = w[2 * u], b = w[2 * u + 1];
-                            *reinterpret_cast<float4 *>(dst + 4 * u) =
-                                make_float4(h2f((uint16_t)a), h2f((uint16_t)(a >> 16)), h2f((uint16_t)b),
-                                            h2f((uint16_t)(b >> 16)));
+                        for (int u = 0; u < 4; ++u) {
+                            x[2 * u] = h2f((uint16_t)w[u]);
+                            x[2 * u + 1] = h2f((uint16_t)(w[u] >> 16));
                         }
                     } else if (KT == QWFN_KV_Q4_0) {      // chunk = ggml block ch: dims 32ch .. 32ch+31
+                        d0 = 32 * ch;
                         const float scf = h2f(scl[cell][ch]);
-                        float *dst = &gr.kv[cell * C::ROWF + ch * 32];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            float4 lo, hi;               // bytes 4u .. 4u+3: dims 4u.. (low), 16+4u.. (high)
-                            lo.x = scf * (float)((int)(w[u] & 15) - 8);
-                            lo.y = scf * (float)((int)((w[u] >> 8) & 15) - 8);
-                            lo.z = scf * (float)((int)((w[u] >> 16) & 15) - 8);
-                            lo.w = scf * (float)((int)((w[u] >> 24) & 15) - 8);
-                            hi.x = scf * (float)((int)((w[u] >> 4) & 15) - 8);
-                            hi.y = scf * (float)((int)((w[u] >> 12) & 15) - 8);
-                            hi.z = scf * (float)((int)((w[u] >> 20) & 15) - 8);
-                            hi.w = scf * (float)((int)(w[u] >> 28) - 8);
-                            *reinterpret_cast<float4 *>(dst + 4 * u) = lo;
-                            *reinterpret_cast<float4 *>(dst + 16 + 4 * u) = hi;
-                        }
+                        for (int u = 0; u < 4; ++u)
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) {
+                                x[4 * u + b] = scf * (float)((int)((w[u] >> (8 * b)) & 15) - 8);
+                                x[16 + 4 * u + b] = scf * (float)((int)((w[u] >> (8 * b + 4)) & 15) - 8);
+                            }
                     } else {                              // chunk = 16 dims of int8
+                        d0 = 16 * ch;
                         const float scf = h2f(scl[cell][ch / 2]);
-                        float *dst = &gr.kv[cell * C::ROWF + ch * 16];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            float4 f;
-                            f.x = scf * (float)(int8_t)(w[u] & 0xFF);
-                            f.y = scf * (float)(int8_t)((w[u] >> 8) & 0xFF);
-                            f.z = scf * (float)(int8_t)((w[u] >> 16) & 0xFF);
-                            f.w = scf * (float)(int8_t)(w[u] >> 24);
-                            *reinterpret_cast<float4 *>(dst + 4 * u) = f;
-                        }
+                        for (int u = 0; u < 4; ++u)
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) x[4 * u + b] = scf * (float)(int8_t)((w[u] >> (8 * b)) & 0xFF);
+                    }
+                    constexpr int NX = sizeof(x) / sizeof(float);
+                    if (vt) {                             // lanes hold consecutive cells: coalesced rows
+#pragma unroll
+                        for (int e = 0; e < NX; ++e) base[(d0 + e) * C::VROWF + cell] = x[e];
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < NX; e += 4)
+                            *reinterpret_cast<float4 *>(base + cell * C::ROWF + d0 + e) =
+                                make_float4(x[e], x[e + 1], x[e + 2], x[e + 3]);
                     }
                 }
             }
         };
-        dequant(kq, gr.ksc);
+        dequant(kq, gr.ksc, false);
         __syncthreads();
-        // QK: lane = cell, wave w of the group owns heads [w*HPW, (w+1)*HPW)
-        const int w = __builtin_amdgcn_readfirstlane(lt >> 6), lane = lt & 63;
-        const int h0 = w * C::HPW;
-        float sacc[C::HPW];
+        // QK on the matrix cores in fp32 (exact products): wave wq takes cells
+        // 16wq .. +15, all 16 columns; v_mfma_f32_16x16x4f32 with the 16-dim
+        // step's four k slots read as one 16-byte row segment per lane
+        f4v sacc = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        {
+            const float *krow = &gr.kv[(16 * wq + qcol) * C::ROWF + 4 * qk];
 #pragma unroll
-        for (int hh = 0; hh < C::HPW; ++hh) sacc[hh] = 0.0f;
-        const float *krow = &gr.kv[lane * C::ROWF];
-#pragma unroll 4
-        for (int d4 = 0; d4 < HD / 4; ++d4) {
-            const float4 kf = *reinterpret_cast<const float4 *>(krow + 4 * d4);
-#pragma unroll
-            for (int hh = 0; hh < C::HPW; ++hh) {
-                const float4 qv = *reinterpret_cast<const float4 *>(&sh.q[(h0 + hh) * HD + 4 * d4]);
-                sacc[hh] += qv.x * kf.x + qv.y * kf.y + qv.z * kf.z + qv.w * kf.w;
+            for (int i = 0; i < HD / 16; ++i) {
+                const float4 a = *reinterpret_cast<const float4 *>(krow + 16 * i);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qreg[i].x, sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qreg[i].y, sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qreg[i].z, sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qreg[i].w, sacc, 0, 0, 0);
             }
         }
-        const bool valid = gr.row[lane] >= 0;
+        // lane holds cells 16wq + 4qk + r (r < 4) of column qcol
+        float s2[4];
+        float tm = -INFINITY;
 #pragma unroll
-        for (int hh = 0; hh < C::HPW; ++hh) {
-            const float s2 = valid ? sacc[hh] * g.scale_log2 : -INFINITY;
-            const float m = wave_max(s2);
-            const float p = valid ? exp2f(s2 - m) : 0.0f;
-            const float l = wave_sum(p);
-            gr.p[h0 + hh][lane] = p;
-            if (lane == 0) { gr.m[h0 + hh] = m; gr.l[h0 + hh] = l; }
+        for (int r = 0; r < 4; ++r) {
+            const bool valid = gr.row[16 * wq + 4 * qk + r] >= 0;
+            s2[r] = valid ? sacc[r] * g.scale_log2 : -INFINITY;
+            tm = fmaxf(tm, s2[r]);
         }
-        __syncthreads();                          // K reads done, p visible
-        dequant(vq, gr.vsc);
-        __syncthreads();
-        // PV: lane owns DPL consecutive dims of each of the wave's heads
-        float o[C::HPW][C::DPL];
+        tm = col_max4(tm);
+        if (qk == 0) gr.rm[wq][qcol] = tm;
+        __syncthreads();                          // K' reads done, the waves' maxima visible
+        const float m = fmaxf(fmaxf(gr.rm[0][qcol], gr.rm[1][qcol]), fmaxf(gr.rm[2][qcol], gr.rm[3][qcol]));
+        float4 pw;
+        float ts = 0.0f;
 #pragma unroll
-        for (int hh = 0; hh < C::HPW; ++hh)
+        for (int r = 0; r < 4; ++r) {
+            const float pr = s2[r] == -INFINITY ? 0.0f : exp2f(s2[r] - m);
+            (&pw.x)[r] = pr;
+            ts += pr;
+        }
+        *reinterpret_cast<float4 *>(&gr.p[qcol][16 * wq + 4 * qk]) = pw;
+        ts = col_sum4(ts);
+        if (qk == 0) gr.rl[wq][qcol] = ts;
+        dequant(vq, gr.vsc, true);
+        __syncthreads();                          // V' and the weights visible
+        if (lt < G) {
+            gr.m[lt] = fmaxf(fmaxf(gr.rm[0][lt], gr.rm[1][lt]), fmaxf(gr.rm[2][lt], gr.rm[3][lt]));
+            gr.l[lt] = (gr.rl[0][lt] + gr.rl[1][lt]) + (gr.rl[2][lt] + gr.rl[3][lt]);
+        }
+        // PV on the matrix cores: wave wq takes dim blocks wq, wq+4, ..; O[dim][column]
+        constexpr int NDB = HD / 64;              // dim blocks per wave
+        f4v o[NDB];
 #pragma unroll
-            for (int k = 0; k < C::DPL; ++k) o[hh][k] = 0.0f;
-#pragma unroll 2
-        for (int c4 = 0; c4 < 64; c4 += 4) {
-            float4 p4[C::HPW];
+        for (int j = 0; j < NDB; ++j) {
+            o[j] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+            const float *vrow = &gr.kv[(16 * (wq + 4 * j) + qcol) * C::VROWF + 4 * qk];
 #pragma unroll
-            for (int hh = 0; hh < C::HPW; ++hh) p4[hh] = *reinterpret_cast<const float4 *>(&gr.p[h0 + hh][c4]);
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                float vv[C::DPL];
-#pragma unroll
-                for (int k = 0; k < C::DPL; ++k) vv[k] = gr.kv[(c4 + cc) * C::ROWF + lane * C::DPL + k];
-#pragma unroll
-                for (int hh = 0; hh < C::HPW; ++hh) {
-                    const float p = cc == 0 ? p4[hh].x : cc == 1 ? p4[hh].y : cc == 2 ? p4[hh].z : p4[hh].w;
-#pragma unroll
-                    for (int k = 0; k < C::DPL; ++k) o[hh][k] += p * vv[k];
-                }
+            for (int c = 0; c < 4; ++c) {         // 16 cells a step
+                const float4 a = *reinterpret_cast<const float4 *>(vrow + 16 * c);
+                const float4 b = *reinterpret_cast<const float4 *>(&gr.p[qcol][16 * c + 4 * qk]);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, o[j], 0, 0, 0);
             }
         }
-        __syncthreads();                          // V' reads done: kv becomes the group's O
+        __syncthreads();                          // V' reads done: kv becomes the group's O [head][dim]
+        if (qcol < G) {
 #pragma unroll
-        for (int hh = 0; hh < C::HPW; ++hh)
+            for (int j = 0; j < NDB; ++j)
 #pragma unroll
-            for (int k = 0; k < C::DPL; ++k) gr.kv[(h0 + hh) * HD + lane * C::DPL + k] = o[hh][k];
+                for (int r = 0; r < 4; ++r) gr.kv[qcol * HD + 16 * (wq + 4 * j) + 4 * qk + r] = o[j][r];
+        }
         __syncthreads();
         // merge the TG groups into this workgroup's partial (unnormalised O, max, sum)
         const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
@@ -1781,10 +1836,6 @@ __device__ __forceinline__ void q8x4_to_h2(uint32_t w, half2v &lo, half2v &hi) {
     hi = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + bias;
 }
 
-typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef int32_t i4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));   // plain 16-byte load/store (no struct copy)
 
 // Eight int8 quants -> eight exact fp16 values, in order.
 __device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
@@ -2413,7 +2464,7 @@ static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *
 // ---------------------------------------------------------------------------
 
 // (head_dim, group, tile groups per attention workgroup)
-#define QWFN_FOR_EACH_SHAPE(X) X(128, 8, 4) X(128, 4, 4) X(128, 2, 4) X(64, 8, 4) X(256, 12, 2) X(256, 8, 2)
+#define QWFN_FOR_EACH_SHAPE(X) X(128, 8, 3) X(128, 4, 3) X(128, 2, 3) X(64, 8, 4) X(256, 12, 2) X(256, 8, 2)
 
 bool kernels_for(int32_t hd, int32_t G) {
 #define X(HD_, G_, TG_) if (hd == HD_ && G == G_) return true;
@@ -2471,41 +2522,6 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-}
-
-// Sum / max over the lanes l, l^16, l^32, l^48 (the four k-groups of one MFMA
-// column), by the gfx950 row swaps: v_permlane32_swap pairs lane l with l^32
-// and v_permlane16_swap pairs row 2r with 2r+1; both results are symmetric, so
-// every lane of the column ends with the same value.
-__device__ __forceinline__ unsigned opaque_copy(unsigned x) {
-    unsigned y;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
-    return y;
-}
-// Lane l with lane l ^ 32 (permlane32) or l ^ 16 (permlane16), combined by op.
-// The swap gets two registers the compiler cannot prove equal: given one value
-// twice it would take the two results as equal and keep only the first.
-template <typename Op>
-__device__ __forceinline__ float swap32_op(float v, Op op) {
-    const unsigned b = __builtin_bit_cast(unsigned, v);
-    const auto r = __builtin_amdgcn_permlane32_swap(b, opaque_copy(b), false, false);
-    const unsigned r0 = r[0], r1 = r[1];                  // (bit_cast of r[i] reads element 0)
-    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
-}
-template <typename Op>
-__device__ __forceinline__ float swap16_op(float v, Op op) {
-    const unsigned b = __builtin_bit_cast(unsigned, v);
-    const auto r = __builtin_amdgcn_permlane16_swap(b, opaque_copy(b), false, false);
-    const unsigned r0 = r[0], r1 = r[1];
-    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
-}
-__device__ __forceinline__ float col_sum4(float v) {
-    const auto add = [](float a, float b) { return a + b; };
-    return swap16_op(swap32_op(v, add), add);
-}
-__device__ __forceinline__ float col_max4(float v) {
-    const auto mx = [](float a, float b) { return fmaxf(a, b); };
-    return swap16_op(swap32_op(v, mx), mx);
 }
 
 // One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): lane
