@@ -566,7 +566,7 @@ struct IdxShared {
 // src/qwfn_graph.cpp:465-476, 520-528 as one workgroup.  The new K row is
 // kept dequantized in LDS as the block's last member.
 template <int HD>
-__device__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const FusedAppend &fa,
+__device__ __forceinline__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const FusedAppend &fa,
                                   int s, int gh, const int32_t *seq_len, int32_t max_seq_len, IdxShared &sh) {
     const int tid = threadIdx.x, per = (HD / 32) * 8;   // lanes per row
     const int which = tid / per, j = (tid % per) / 8, e4 = tid % 8;
@@ -665,6 +665,34 @@ __device__ void find_bin(SH &sh, int need) {
     __syncthreads();
 }
 
+// The threshold bin of a 4096-bin histogram in LDS (bins in ascending key
+// order) for the topk-th largest key, by wave 0: lane l sums bins [64l,
+// 64l+64); the lane whose bins straddle that key is found by a scan and a
+// ballot, then its 64 bins are spread over the wave for the same search.
+// Sets sh.bin, sh.need (keys of that bin still needed) and sh.cnt_b (its
+// keys).  Wave 0 calls it; the caller synchronizes after.
+template <typename SH>
+__device__ __forceinline__ void hist_cut(SH &sh, int topk) {
+    const int lane = threadIdx.x & 63;
+    const uint4 *h4 = reinterpret_cast<const uint4 *>(sh.hist);
+    uint32_t own = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint4 x = h4[lane * 16 + k];
+        own += x.x + x.y + x.z + x.w;
+    }
+    const int incl = wave_incl_scan((int)own);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    const int above = total - incl;                   // keys in the bins of higher lanes
+    const int ls = __builtin_ctzll(__ballot(above < topk && above + (int)own >= topk));
+    const int above_l = __builtin_amdgcn_readlane(above, ls);
+    const int c = (int)sh.hist[ls * 64 + lane];
+    const int ic = wave_incl_scan(c);
+    const int run = above_l + __builtin_amdgcn_readlane(ic, 63) - ic;   // keys in higher bins
+    const int j = __builtin_ctzll(__ballot(run < topk && run + c >= topk));
+    if (lane == j) { sh.bin = ls * 64 + j; sh.need = topk - run; sh.cnt_b = c; }
+}
+
 // Selection of one (sequence, KV head): the topk eligible blocks by (score
 // desc, index asc) on orderable 32-bit keys, emitted ascending between the
 // forced sink and window blocks.
@@ -745,27 +773,7 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
     }
     auto bin_at = [&](int i) -> uint32_t { return KEEP ? bin[KEEP ? i : 0] : bin_of(sv[i]); };
     __syncthreads();
-    // threshold bin, by wave 0: lane l sums bins [64l, 64l+64); the lane whose
-    // bins straddle the topk-th largest key is found by a scan and a ballot,
-    // then its 64 bins are spread over the wave for the same search
-    if (wid == 0) {
-        uint32_t own = 0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const uint4 x = h4[lane * 16 + k];
-            own += x.x + x.y + x.z + x.w;
-        }
-        const int incl = wave_incl_scan((int)own);
-        const int total = __builtin_amdgcn_readlane(incl, 63);
-        const int above = total - incl;               // keys in the bins of higher lanes
-        const int ls = __builtin_ctzll(__ballot(above < topk && above + (int)own >= topk));
-        const int above_l = __builtin_amdgcn_readlane(above, ls);
-        const int c = (int)sh.hist[ls * 64 + lane];
-        const int ic = wave_incl_scan(c);
-        const int run = above_l + __builtin_amdgcn_readlane(ic, 63) - ic;   // keys in higher bins
-        const int j = __builtin_ctzll(__ballot(run < topk && run + c >= topk));
-        if (lane == j) { sh.bin = ls * 64 + j; sh.need = topk - run; sh.cnt_b = c; }
-    }
+    if (wid == 0) hist_cut(sh, topk);               // the threshold bin
     __syncthreads();
     const uint32_t B = (uint32_t)sh.bin;
     const int need = sh.need;
@@ -914,24 +922,7 @@ __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, con
         }
     }
     __syncthreads();
-    if (wid == 0) {                                // the threshold bin, as in the register path
-        uint32_t own = 0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const uint4 y = h4[lane * 16 + k];
-            own += y.x + y.y + y.z + y.w;
-        }
-        const int incl = wave_incl_scan((int)own);
-        const int total = __builtin_amdgcn_readlane(incl, 63);
-        const int above = total - incl;
-        const int ls = __builtin_ctzll(__ballot(above < topk && above + (int)own >= topk));
-        const int above_l = __builtin_amdgcn_readlane(above, ls);
-        const int c = (int)sh.hist[ls * 64 + lane];
-        const int ic = wave_incl_scan(c);
-        const int run = above_l + __builtin_amdgcn_readlane(ic, 63) - ic;
-        const int j = __builtin_ctzll(__ballot(run < topk && run + c >= topk));
-        if (lane == j) { sh.bin = ls * 64 + j; sh.need = topk - run; sh.cnt_b = c; }
-    }
+    if (wid == 0) hist_cut(sh, topk);               // the threshold bin
     __syncthreads();
     const uint32_t B = (uint32_t)sh.bin;
     const int need = sh.need;
@@ -994,6 +985,192 @@ __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, con
         if (pos < topk) out[g.sink + pos] = b0 + __builtin_ctzll(m);
         ++pos;
         m &= m - 1ull;
+    }
+    return true;
+}
+
+// Sampled-cut path (the 1024-thread k_select_big, many eligible blocks): a
+// cut placed from kSelSample evenly spaced scores, low enough that the topk
+// largest lie above it with a wide margin (the sample's rs-th largest, rs =
+// mu + 4 sqrt(mu) + 8 for mu = topk * kSelSample / eligible, the sample keys
+// expected above the topk-th key), leaves about rs / mu times topk
+// candidates.  One pass over the scores compacts them into LDS in block
+// order, where the exact selection runs on them alone: a 4096-bin histogram
+// linear in the key between their smallest and largest key, then the
+// threshold bin ranked by (key desc, index asc) -- candidate order is block
+// order.  The cut is a bin of a map that never decreases in the key order, so
+// the candidates are every key at or above some key: when they number at
+// least topk they hold the exact top topk, ties included.  Fewer than topk
+// candidates, more than kSelCandMax, or a threshold bin of more than kCandMax
+// keys: returns false with nothing written, and the streaming path runs.
+constexpr int kSelSample = 4096;
+constexpr int kSelCandMax = 4096;
+template <int NT, typename SH>
+__device__ __forceinline__ bool select_sample(const Geo &g, const float *sc, const Ranges &r, int topk, int32_t *out,
+                                              SH &sh) {
+    constexpr int SPT = kSelSample / NT, CPT = kSelCandMax / NT, MAXV = 16;
+    static_assert(SPT * NT == kSelSample && CPT * NT == kSelCandMax, "whole samples / candidates a thread");
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int ne = r.e_hi - r.e_lo;
+    const float mu = (float)topk * (float)kSelSample / (float)ne;
+    const int rs = (int)ceilf(mu + 4.0f * sqrtf(mu) + 8.0f);
+    if (ne < 2 * kSelSample || rs > kSelSample / 8) return false;   // (uniform)
+    const BufRsrc rsc = buf_rsrc(sc, (uint32_t)((r.e_hi + 3) & ~3) * 4u);
+    float sv[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+        const int j = tid + k * NT;
+        sv[k] = BufLoad<1, kCpolSc1>::at(rsc, (r.e_lo + (int)((int64_t)j * ne / kSelSample)) * 4, 0)[0];
+    }
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+        const bool use = sv[k] == sv[k];
+        lo = fminf(lo, use ? sv[k] : INFINITY);
+        hi = fmaxf(hi, use ? sv[k] : -INFINITY);
+    }
+    hi = wave_max(hi);
+    lo = -wave_max(-lo);
+    if (lane == 0) { sh.red[wid] = hi; sh.red[NT / 64 + wid] = lo; }
+    uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
+    for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[NT / 64 + i]); }
+    const float span = hi - lo, scale = 4096.0f / span;
+    const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
+    const uint32_t lm = lin ? 0xffffffffu : 0u;
+    // linear in the score over the sample's range (below it bin 0, above it
+    // bin 4095), NaN in bin 0; without a finite spread the top 12 key bits
+    auto bin_of = [&](float x) -> uint32_t {
+        const uint32_t lb = (uint32_t)fminf(fmaxf((x - lo) * scale, 0.0f), 4095.0f);
+        return ((x == x ? lb : 0u) & lm) | ((score_key(x) >> 20) & ~lm);
+    };
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) atomicAdd(&sh.hist[bin_of(sv[k])], 1u);
+    __syncthreads();
+    if (wid == 0) hist_cut(sh, rs);
+    __syncthreads();
+    const uint32_t Bs = (uint32_t)sh.bin;
+    for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);   // for the candidates
+    // the pass: thread t owns blocks base + [t*per, t*per + per), per <= 64
+    const int base = r.e_lo & ~3;
+    const int per = (((r.e_hi - base) + NT - 1) / NT + 3) & ~3;
+    const int nv = per / 4;                        // uniform
+    const int b0 = base + tid * per;
+    const int i_lo = r.e_lo - b0, i_hi = r.e_hi - b0;
+    float z[4 * MAXV];
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        if (k < nv) {
+            const auto v_ = BufLoad<4, kCpolSc1>::at(rsc, (b0 + 4 * k) * 4, 0);
+            z[4 * k] = v_[0]; z[4 * k + 1] = v_[1]; z[4 * k + 2] = v_[2]; z[4 * k + 3] = v_[3];
+        } else {
+            z[4 * k] = z[4 * k + 1] = z[4 * k + 2] = z[4 * k + 3] = 0.0f;
+        }
+    }
+    uint64_t cm = 0;
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        if (k < nv) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * k + j;
+                cm |= (uint64_t)(i >= i_lo && i < i_hi && bin_of(z[i]) >= Bs) << i;
+            }
+        }
+    }
+    int C;
+    int slot = block_excl_sum<NT>((int)__builtin_popcountll(cm), sh.tmp, &C);
+    if (C < topk || C > kSelCandMax) return false;   // (uniform)
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        if (k < nv) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * k + j;
+                if ((cm >> i) & 1ull) {
+                    sh.ckey[slot] = score_key(z[i]);
+                    sh.cblk[slot] = b0 + i;
+                    ++slot;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // exact selection among the C candidates: thread t owns [CPT t, CPT t + CPT)
+    uint32_t kc[CPT];
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = CPT * tid + u;
+        kc[u] = c < C ? sh.ckey[c] : 0u;
+        kmin = c < C ? min(kmin, kc[u]) : kmin;
+        kmax = c < C ? max(kmax, kc[u]) : kmax;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    }
+    if (lane == 0) { sh.kred[wid] = kmin; sh.kred[NT / 64 + wid] = kmax; }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) { kmin = min(kmin, sh.kred[i]); kmax = max(kmax, sh.kred[NT / 64 + i]); }
+    const float sc2 = 4096.0f / ((float)(kmax - kmin) + 1.0f);
+    auto bin2 = [&](uint32_t k) -> uint32_t { return (uint32_t)fminf((float)(k - kmin) * sc2, 4095.0f); };
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = CPT * tid + u;
+        atomicAdd(&sh.hist[c < C ? bin2(kc[u]) : 4096u + (uint32_t)lane], 1u);
+    }
+    __syncthreads();
+    if (wid == 0) hist_cut(sh, topk);
+    __syncthreads();
+    const uint32_t B = (uint32_t)sh.bin;
+    const int need = sh.need, cB = sh.cnt_b;
+    if (cB > need) {                               // rank the threshold bin: (key desc, index asc)
+        if (cB > kCandMax) return false;           // (uniform)
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const int c = CPT * tid + u;
+            if (c < C && bin2(kc[u]) == B) {
+                const int at = atomicAdd(&sh.ncand, 1);
+                sh.cand_key[at] = kc[u];
+                sh.cand_b[at] = c;
+            }
+        }
+        __syncthreads();
+        if (tid < cB) {
+            const uint32_t k = sh.cand_key[tid];
+            const int c = sh.cand_b[tid];
+            int rk = 0;
+            for (int jj = 0; jj < cB; ++jj) {
+                const uint32_t kj = sh.cand_key[jj];
+                rk += (kj > k) || (kj == k && sh.cand_b[jj] < c);
+            }
+            sh.cok[c] = rk < need;
+        }
+        __syncthreads();
+    }
+    bool tk[CPT];
+    int cnt = 0;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = CPT * tid + u;
+        const uint32_t bi = bin2(kc[u]);
+        tk[u] = c < C && (bi > B || (bi == B && (cB <= need || sh.cok[c])));
+        cnt += tk[u];
+    }
+    int tot;
+    int pos = block_excl_sum<NT>(cnt, sh.tmp, &tot);
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        if (tk[u]) {
+            if (pos < topk) out[g.sink + pos] = sh.cblk[CPT * tid + u];
+            ++pos;
+        }
     }
     return true;
 }
@@ -1063,7 +1240,13 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
             else if (span <= 24 * NT) done = select_regs<NT, 24, true>(g, sc, r, topk, out, sh);
             else if (span <= keys_max<NT>()) done = select_regs<NT, keys_max<NT>() / NT, true>(g, sc, r, topk, out, sh);
         } else {
-            if (span <= keys_max<NT>()) done = select_stream<NT>(g, sc, r, topk, out, sh);
+            if (span <= keys_max<NT>()) {
+                done = select_sample<NT>(g, sc, r, topk, out, sh);
+                if (!done) {
+                    __syncthreads();               // the sampled path's LDS reads are done
+                    done = select_stream<NT>(g, sc, r, topk, out, sh);
+                }
+            }
         }
         if (!done) select_radix<NT>(g, sc, r, topk, out, sh);
     }
@@ -1133,6 +1316,10 @@ struct BigSelShared {
     uint32_t cand_key[kCandMax + 1];
     int32_t cand_b[kCandMax + 1];
     int32_t cand_ok[kCandMax + 1];                // the ranking's verdicts
+    uint32_t ckey[kSelCandMax];                   // sampled-cut candidates, in block order
+    int32_t cblk[kSelCandMax];
+    uint8_t cok[kSelCandMax];                     // their threshold-bin verdicts
+    uint32_t kred[2 * (kBigSelThreads / 64)];
     float red[2 * (kBigSelThreads / 64)];
     int tmp[kBigSelThreads / 64];
     int bin, need, ncand, cnt_b;

@@ -166,6 +166,58 @@ def test_indexer_more_blocks_than_lds_keys():
     _indexer_case(cfg, [16600], seed=241, equal_scores=True)
 
 
+# The 1024-thread selection first tries a cut placed from 4096 evenly spaced
+# scores (block e_lo + j * n_eligible // 4096), then falls back to three passes
+# over the keys.  With top_k 600 over 8,296 eligible blocks the cut keeps about
+# 370 sample keys, so scores planted at exactly those blocks steer each branch;
+# every case must select what the oracle selects.
+BIG = Cfg(n_head=8, n_head_kv=1, head_dim=64, block_tokens=2, page_tokens=64, top_k_blocks=600,
+          sink_blocks=1, local_tokens=5)
+BIG_L = 16600
+
+
+def _big_sample_blocks():
+    last = BIG_L - 1
+    w0 = last - BIG.local_tokens + 1
+    e_lo, e_hi = BIG.sink_blocks, min(BIG_L // BIG.block_tokens, w0 // BIG.block_tokens)
+    ne = e_hi - e_lo
+    assert ne == 8296
+    return e_lo + np.arange(4096) * ne // 4096
+
+
+def _score_is_dim0(p, q, rng):                        # every query head reads dim 0 only
+    q[...] = 0.0
+    q[..., 0] = 1.0
+    p[..., 0] = rng.standard_normal(p.shape[:-1]).astype(np.float32)
+
+
+def _sample_high(p, q, rng):                           # the sampled blocks hold the top scores:
+    _score_is_dim0(p, q, rng)                          # fewer candidates than top_k
+    p[:, :, _big_sample_blocks(), 0] = np.float32(100) + np.arange(4096, dtype=np.float32) * np.float32(0.01)
+
+
+def _sample_low(p, q, rng):                            # the sampled blocks hold the lowest scores:
+    _score_is_dim0(p, q, rng)                          # more candidates than the LDS list holds
+    p[:, :, _big_sample_blocks(), 0] = np.float32(-100) - np.arange(4096, dtype=np.float32) * np.float32(0.01)
+
+
+def _wide_tie(p, q, rng):                              # 700 equal top scores: the candidates'
+    _score_is_dim0(p, q, rng)                          # threshold bin overflows the rank list
+    p[:, :, rng.choice(np.arange(1, 8297), 700, replace=False), 0] = np.float32(10)
+
+
+def _sample_near_tie(p, q, rng):                       # 40 equal scores straddling the top-k edge
+    _score_is_dim0(p, q, rng)
+    top = np.argsort(-p[0, 0, 1:8297, 0], kind="stable")[:620] + 1
+    p[:, :, top[580:620], 0] = p[0, 0, top[590], 0]
+
+
+@pytest.mark.parametrize("mutate", [None, _sample_high, _sample_low, _wide_tie, _sample_near_tie, _inf_nan, _outlier,
+                                    _small_spread])
+def test_select_big_sampled_cut(mutate):
+    _indexer_case(BIG, [BIG_L], seed=245, mutate=mutate)
+
+
 @pytest.mark.parametrize("cfg", [TINY, G12, Cfg(relu_per_head=1), Cfg(top_k_blocks=3, sink_blocks=2, local_tokens=100)])
 def test_indexer_other_shapes(cfg):
     _indexer_case(cfg, [3 * cfg.page_tokens - 1, cfg.page_tokens + 7], seed=220)
