@@ -154,7 +154,7 @@ int bind_ws(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, v
 
 namespace qwfn_qsa {
 
-WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, bool partials) {
+WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, bool partials, bool cut) {
     WsLayout l;
     // per-pair score rows padded to 64 floats: 16-byte vector loads of a row
     // stay aligned and inside it
@@ -169,6 +169,13 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.scores = take(pairs * l.nb_cap * sizeof(float));
     l.part_o = take(partials ? pairs * l.n_tiles * g.G * g.hd * sizeof(float) : 0);
     l.part_ml = take(partials ? pairs * l.n_tiles * g.G * 2 * sizeof(float) : 0);
+    // the multi-workgroup selection: decode contexts past the register
+    // selection, per-head or over one score row
+    const int32_t nb_max = max_seq_len / g.bt;
+    const int32_t cut_wg = (nb_max + kCutKeys - 1) / kCutKeys;
+    l.cut_wg = cut && nb_max > kIdxRegKeys && !(g.shared && g.Hkv > 1) && cut_wg <= kCutWgMax ? cut_wg : 0;
+    l.cand = take(pairs * l.cut_wg * kCutKeys * sizeof(uint2));
+    l.ccnt = take(l.cut_wg ? pairs * kCutWgMax * sizeof(int32_t) : 0);
     l.total = off;
     return l;
 }
@@ -183,6 +190,9 @@ Ws ws_bind(void *base, const WsLayout &l) {
     w.scores = (float *)(b + l.scores);
     w.part_o = (float *)(b + l.part_o);
     w.part_ml = (float *)(b + l.part_ml);
+    w.cand = (uint2 *)(b + l.cand);
+    w.ccnt = (int32_t *)(b + l.ccnt);
+    w.cut_wg = l.cut_wg;
     w.nb_cap = l.nb_cap;
     w.max_sel = l.max_sel;
     w.n_tiles = l.n_tiles;
@@ -469,7 +479,7 @@ int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_se
     if (!g.vdim && (int64_t)q_batch * shape->n_head_kv > kMaxCounters)
         return fail(QWFN_ERANGE, "q_batch * n_head_kv exceeds %d", kMaxCounters);
     if (q_batch > kPrefillBatchMax) return fail(QWFN_ERANGE, "q_batch %d exceeds %d", q_batch, kPrefillBatchMax);
-    *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len), !g.vdim).total;
+    *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len), !g.vdim, false).total;
     return ok();
 }
 
@@ -517,11 +527,11 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
     if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "prefill: workspace NULL or not 256-byte aligned");
     const bool parts = !g.vdim;                    // the general kernel merges partials in memory
     int32_t batch = std::min<int64_t>(n_q, g.vdim ? kPrefillBatchMax : kMaxCounters / shape->n_head_kv);
-    while (batch > 1 && ws_layout(g, batch, max_len, need, parts).total > ws_bytes) batch = (batch + 1) / 2;
-    if (ws_layout(g, batch, max_len, need, parts).total > ws_bytes)
+    while (batch > 1 && ws_layout(g, batch, max_len, need, parts, false).total > ws_bytes) batch = (batch + 1) / 2;
+    if (ws_layout(g, batch, max_len, need, parts, false).total > ws_bytes)
         return fail(QWFN_ERANGE, "prefill: workspace of %zu bytes holds no query batch (need %zu)", ws_bytes,
-                    ws_layout(g, 1, max_len, need, parts).total);
-    const Ws w = ws_bind(ws, ws_layout(g, batch, max_len, need, parts));
+                    ws_layout(g, 1, max_len, need, parts, false).total);
+    const Ws w = ws_bind(ws, ws_layout(g, batch, max_len, need, parts, false));
     hipStream_t st = (hipStream_t)stream;
     hipError_t e = hipSuccess;
     // the chunk's rows, then every block they complete (and a block they finish)

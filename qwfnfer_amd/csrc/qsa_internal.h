@@ -39,6 +39,12 @@ struct Geo {
 // call layout agrees on it; all other regions are per-call scratch.
 constexpr int32_t kMaxCounters = 4096;   // (sequence, KV head) pairs per call
 constexpr int32_t kPrefillBatchMax = 32768;   // queries per prefill batch (one grid dimension)
+// Eligible blocks the indexer workgroup selects from registers; longer decode
+// contexts select in a launch of their own, over kCutKeys scores per
+// workgroup when at most kCutWgMax workgroups cover them.
+constexpr int32_t kIdxRegKeys = 8192;
+constexpr int32_t kCutKeys = 4096;
+constexpr int32_t kCutWgMax = 64;
 struct Ws {
     int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
     int32_t *cnt_attn;   // [kMaxCounters] attention completion counters
@@ -47,15 +53,20 @@ struct Ws {
     float   *scores;     // [n_seq][Hkv][nb_cap]
     float   *part_o;     // [n_seq][Hkv][n_tiles][G][hd]
     float   *part_ml;    // [n_seq][Hkv][n_tiles][G][2]
+    uint2   *cand;       // [n_seq][Hkv][cut_wg][kCutKeys] (key, block) candidates of the multi-workgroup selection
+    int32_t *ccnt;       // [n_seq][Hkv][kCutWgMax] their counts
     int32_t  nb_cap, max_sel, n_tiles;
+    int32_t  cut_wg;     // workgroups of the multi-workgroup selection (0: one workgroup)
 };
 
 struct WsLayout {
-    size_t sel, nsel, scores, part_o, part_ml, total;
-    int32_t nb_cap, max_sel, n_tiles;
+    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, total;
+    int32_t nb_cap, max_sel, n_tiles, cut_wg;
 };
-// partials = false: no attention partials (the prefill kernel keeps its state on chip)
-WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, bool partials = true);
+// partials = false: no attention partials (the prefill kernel keeps its state on chip);
+// cut = false: no multi-workgroup selection regions (prefill selects per query)
+WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel, bool partials = true,
+                   bool cut = true);
 Ws ws_bind(void *base, const WsLayout &l);
 
 // Fused-append arguments of the decode step (enabled == 0: plain indexer).

@@ -542,6 +542,7 @@ __device__ __forceinline__ int eff_topk(const Geo &g, const Ranges &r) {
 constexpr int kIdxThreads = 256;
 constexpr int kBlocksPerChunk = kIdxThreads / 4;   // 4 lanes share one block's dot
 constexpr int kKeysMax = 32 * kIdxThreads;        // eligible blocks the register selection holds
+static_assert(kKeysMax == kIdxRegKeys, "the workspace sizes the long-context selection by this bound");
 
 constexpr int kCandMax = 256;                      // threshold-bin candidates ranked exactly
 
@@ -665,6 +666,26 @@ __device__ void find_bin(SH &sh, int need) {
     __syncthreads();
 }
 
+// Where a selection goes: row 0 and its count, and `rows` rows in all, each
+// `stride` entries after the previous, with consecutive counts (a shared
+// selection writes every KV head's row; otherwise rows = 1).
+struct SelOut {
+    int32_t *p, *n;
+    int64_t stride;
+    int rows;
+    __device__ __forceinline__ void put(int i, int32_t b) const {
+        for (int h = 0; h < rows; ++h) p[h * stride + i] = b;
+    }
+    __device__ __forceinline__ void count(int c) const {
+        for (int h = 0; h < rows; ++h) n[h] = c;
+    }
+};
+__device__ __forceinline__ SelOut sel_out(const Geo &g, int32_t *sel, int32_t *nsel, int32_t max_sel, int s,
+                                          int pair) {
+    return g.shared ? SelOut{sel + (int64_t)s * g.sel_rows * max_sel, nsel + s * g.sel_rows, max_sel, g.sel_rows}
+                    : SelOut{sel + (int64_t)pair * max_sel, nsel + pair, max_sel, 1};
+}
+
 // The threshold bin of a 4096-bin histogram in LDS (bins in ascending key
 // order) for the topk-th largest key, by wave 0: lane l sums bins [64l,
 // 64l+64); the lane whose bins straddle that key is found by a scan and a
@@ -717,7 +738,7 @@ __device__ __forceinline__ void hist_cut(SH &sh, int topk) {
 // radix passes over the keys in memory and an index-ordered tie count.
 template <int NT, int KPT, bool KEEP, typename SH>
 __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const Ranges &r, int topk,
-                                            int32_t *out, SH &sh) {
+                                            const SelOut &out, SH &sh) {
     static_assert(KPT % 4 == 0 && (KPT <= 32 || (KPT % 8 == 0 && KPT <= 48) || KPT == 64),
                   "KPT: whole 16-byte vectors, a thread's bits within two aligned words");
     using MT = typename std::conditional<(KPT > 32), uint64_t, uint32_t>::type;
@@ -837,7 +858,7 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
             uint64_t x = (uint64_t)tm[TPL * lane + q];
             const int tb = base + (TPL * lane + q) * KPT;
             while (x) {
-                if (pos < topk) out[g.sink + pos] = tb + __builtin_ctzll(x);
+                if (pos < topk) out.put(g.sink + pos, tb + __builtin_ctzll(x));
                 ++pos;
                 x &= x - 1u;
             }
@@ -855,8 +876,8 @@ __device__ __forceinline__ bool select_regs(const Geo &g, const float *sc, const
 // writes its taken blocks at its exclusive-scan offset.  Vectors past `per`
 // are skipped by a branch that is uniform over the workgroup.
 template <int NT, typename SH>
-__device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, const Ranges &r, int topk, int32_t *out,
-                                              SH &sh) {
+__device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, const Ranges &r, int topk,
+                                              const SelOut &out, SH &sh) {
     constexpr int MAXV = 16;                       // 16-byte vectors a thread: 64 keys
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int base = r.e_lo & ~3;
@@ -982,40 +1003,56 @@ __device__ __forceinline__ bool select_stream(const Geo &g, const float *sc, con
     int tot;
     int pos = block_excl_sum<NT>(cnt, sh.tmp, &tot);
     while (m) {
-        if (pos < topk) out[g.sink + pos] = b0 + __builtin_ctzll(m);
+        if (pos < topk) out.put(g.sink + pos, b0 + __builtin_ctzll(m));
         ++pos;
         m &= m - 1ull;
     }
     return true;
 }
 
-// Sampled-cut path (the 1024-thread k_select_big, many eligible blocks): a
-// cut placed from kSelSample evenly spaced scores, low enough that the topk
-// largest lie above it with a wide margin (the sample's rs-th largest, rs =
-// mu + 4 sqrt(mu) + 8 for mu = topk * kSelSample / eligible, the sample keys
-// expected above the topk-th key), leaves about rs / mu times topk
-// candidates.  One pass over the scores compacts them into LDS in block
-// order, where the exact selection runs on them alone: a 4096-bin histogram
-// linear in the key between their smallest and largest key, then the
-// threshold bin ranked by (key desc, index asc) -- candidate order is block
-// order.  The cut is a bin of a map that never decreases in the key order, so
-// the candidates are every key at or above some key: when they number at
-// least topk they hold the exact top topk, ties included.  Fewer than topk
-// candidates, more than kSelCandMax, or a threshold bin of more than kCandMax
-// keys: returns false with nothing written, and the streaming path runs.
+// Sampled cut (long contexts, the 1024-thread selections): a cut placed from
+// kSelSample evenly spaced scores (block e_lo + j * eligible / kSelSample),
+// low enough that the topk largest lie above it with a wide margin -- the
+// sample's rs-th largest, rs = mu + 4 sqrt(mu) + 8 for mu = topk * kSelSample
+// / eligible, the sample keys expected above the topk-th key -- leaves about
+// rs / mu times topk candidates, on which the exact selection runs alone.
+// The cut is a bin of a map that never decreases in the key order, so the
+// candidates are every key at or above some key: when they number at least
+// topk they hold the exact top topk, ties included.
 constexpr int kSelSample = 4096;
 constexpr int kSelCandMax = 4096;
-template <int NT, typename SH>
-__device__ __forceinline__ bool select_sample(const Geo &g, const float *sc, const Ranges &r, int topk, int32_t *out,
-                                              SH &sh) {
-    constexpr int SPT = kSelSample / NT, CPT = kSelCandMax / NT, MAXV = 16;
-    static_assert(SPT * NT == kSelSample && CPT * NT == kSelCandMax, "whole samples / candidates a thread");
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+
+// rs, or 0 when the sampled cut does not apply (few eligible blocks, or a
+// topk that is a large share of them).
+__device__ __forceinline__ int sample_rank(const Ranges &r, int topk) {
     const int ne = r.e_hi - r.e_lo;
+    if (ne < 2 * kSelSample || topk <= 0) return 0;
     const float mu = (float)topk * (float)kSelSample / (float)ne;
     const int rs = (int)ceilf(mu + 4.0f * sqrtf(mu) + 8.0f);
-    if (ne < 2 * kSelSample || rs > kSelSample / 8) return false;   // (uniform)
-    const BufRsrc rsc = buf_rsrc(sc, (uint32_t)((r.e_hi + 3) & ~3) * 4u);
+    return rs <= kSelSample / 8 ? rs : 0;
+}
+
+// The bin map of the sample -- linear in the score over the sample's range
+// (below it bin 0, above it bin 4095), NaN in bin 0; without a finite spread
+// the top 12 key bits -- and the cut bin.
+struct CutMap {
+    float lo, scale;
+    uint32_t lm, cut;
+    __device__ __forceinline__ uint32_t bin(float x) const {
+        const uint32_t lb = (uint32_t)fminf(fmaxf((x - lo) * scale, 0.0f), 4095.0f);
+        return ((x == x ? lb : 0u) & lm) | ((score_key(x) >> 20) & ~lm);
+    }
+    __device__ __forceinline__ bool keep(float x) const { return bin(x) >= cut; }
+};
+
+// The sample's cut, by all NT threads (kSelSample / NT device-coherent loads
+// each); leaves sh.hist for reuse after a barrier.
+template <int NT, typename SH>
+__device__ __forceinline__ CutMap sample_cut(const BufRsrc &rsc, const Ranges &r, int rs, SH &sh) {
+    constexpr int SPT = kSelSample / NT;
+    static_assert(SPT * NT == kSelSample, "whole samples a thread");
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int ne = r.e_hi - r.e_lo;
     float sv[SPT];
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
@@ -1034,72 +1071,41 @@ __device__ __forceinline__ bool select_sample(const Geo &g, const float *sc, con
     if (lane == 0) { sh.red[wid] = hi; sh.red[NT / 64 + wid] = lo; }
     uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
     for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid == 0) sh.ncand = 0;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NT / 64; ++i) { hi = fmaxf(hi, sh.red[i]); lo = fminf(lo, sh.red[NT / 64 + i]); }
-    const float span = hi - lo, scale = 4096.0f / span;
-    const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
-    const uint32_t lm = lin ? 0xffffffffu : 0u;
-    // linear in the score over the sample's range (below it bin 0, above it
-    // bin 4095), NaN in bin 0; without a finite spread the top 12 key bits
-    auto bin_of = [&](float x) -> uint32_t {
-        const uint32_t lb = (uint32_t)fminf(fmaxf((x - lo) * scale, 0.0f), 4095.0f);
-        return ((x == x ? lb : 0u) & lm) | ((score_key(x) >> 20) & ~lm);
-    };
+    CutMap m;
+    const float span = hi - lo;
+    m.lo = lo;
+    m.scale = 4096.0f / span;
+    m.lm = hi > lo && span < INFINITY && m.scale < INFINITY ? 0xffffffffu : 0u;
+    m.cut = 0;
 #pragma unroll
-    for (int k = 0; k < SPT; ++k) atomicAdd(&sh.hist[bin_of(sv[k])], 1u);
+    for (int k = 0; k < SPT; ++k) atomicAdd(&sh.hist[m.bin(sv[k])], 1u);
     __syncthreads();
     if (wid == 0) hist_cut(sh, rs);
     __syncthreads();
-    const uint32_t Bs = (uint32_t)sh.bin;
-    for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);   // for the candidates
-    // the pass: thread t owns blocks base + [t*per, t*per + per), per <= 64
-    const int base = r.e_lo & ~3;
-    const int per = (((r.e_hi - base) + NT - 1) / NT + 3) & ~3;
-    const int nv = per / 4;                        // uniform
-    const int b0 = base + tid * per;
-    const int i_lo = r.e_lo - b0, i_hi = r.e_hi - b0;
-    float z[4 * MAXV];
-#pragma unroll
-    for (int k = 0; k < MAXV; ++k) {
-        if (k < nv) {
-            const auto v_ = BufLoad<4, kCpolSc1>::at(rsc, (b0 + 4 * k) * 4, 0);
-            z[4 * k] = v_[0]; z[4 * k + 1] = v_[1]; z[4 * k + 2] = v_[2]; z[4 * k + 3] = v_[3];
-        } else {
-            z[4 * k] = z[4 * k + 1] = z[4 * k + 2] = z[4 * k + 3] = 0.0f;
-        }
-    }
-    uint64_t cm = 0;
-#pragma unroll
-    for (int k = 0; k < MAXV; ++k) {
-        if (k < nv) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 4 * k + j;
-                cm |= (uint64_t)(i >= i_lo && i < i_hi && bin_of(z[i]) >= Bs) << i;
-            }
-        }
-    }
-    int C;
-    int slot = block_excl_sum<NT>((int)__builtin_popcountll(cm), sh.tmp, &C);
-    if (C < topk || C > kSelCandMax) return false;   // (uniform)
-#pragma unroll
-    for (int k = 0; k < MAXV; ++k) {
-        if (k < nv) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 4 * k + j;
-                if ((cm >> i) & 1ull) {
-                    sh.ckey[slot] = score_key(z[i]);
-                    sh.cblk[slot] = b0 + i;
-                    ++slot;
-                }
-            }
-        }
-    }
+    m.cut = (uint32_t)sh.bin;
+    return m;
+}
+
+// The exact selection among C candidates in LDS (sh.ckey / sh.cblk[0, C), in
+// block order, topk <= C <= kSelCandMax): a 4096-bin histogram linear in the
+// key between the candidates' smallest and largest key, the threshold bin
+// ranked by (key desc, index asc) -- the candidate index stands in for the
+// block index --, emission in candidate (block) order after the sink blocks.
+// Returns false, with nothing written, when that bin holds more than
+// kCandMax keys.
+template <int NT, typename SH>
+__device__ __forceinline__ bool select_cands(const Geo &g, int C, int topk, const SelOut &out, SH &sh) {
+    constexpr int CPT = kSelCandMax / NT;
+    static_assert(CPT * NT == kSelCandMax, "whole candidates a thread");
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    uint4 *h4 = reinterpret_cast<uint4 *>(sh.hist);
+    for (int i = tid; i < 4096 / 4; i += NT) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 0) sh.ncand = 0;
     __syncthreads();
-    // exact selection among the C candidates: thread t owns [CPT t, CPT t + CPT)
+    // thread t owns candidates [CPT t, CPT t + CPT)
     uint32_t kc[CPT];
     uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
@@ -1168,16 +1174,77 @@ __device__ __forceinline__ bool select_sample(const Geo &g, const float *sc, con
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
         if (tk[u]) {
-            if (pos < topk) out[g.sink + pos] = sh.cblk[CPT * tid + u];
+            if (pos < topk) out.put(g.sink + pos, sh.cblk[CPT * tid + u]);
             ++pos;
         }
     }
     return true;
 }
 
+// One workgroup: the sampled cut, then one pass over the scores (thread t owns
+// blocks base + [t*per, t*per + per), per <= 64) compacting the candidates
+// into LDS in block order, then the exact selection.  Fewer than topk
+// candidates, more than kSelCandMax, or an overfull threshold bin: returns
+// false with nothing written, and the streaming path runs.
+template <int NT, typename SH>
+__device__ __forceinline__ bool select_sample(const Geo &g, const float *sc, const Ranges &r, int topk,
+                                              const SelOut &out, SH &sh) {
+    constexpr int MAXV = 16;
+    const int tid = threadIdx.x;
+    const int rs = sample_rank(r, topk);
+    if (rs == 0) return false;                     // (uniform)
+    const BufRsrc rsc = buf_rsrc(sc, (uint32_t)((r.e_hi + 3) & ~3) * 4u);
+    const CutMap cut = sample_cut<NT>(rsc, r, rs, sh);
+    const int base = r.e_lo & ~3;
+    const int per = (((r.e_hi - base) + NT - 1) / NT + 3) & ~3;
+    const int nv = per / 4;                        // uniform
+    const int b0 = base + tid * per;
+    const int i_lo = r.e_lo - b0, i_hi = r.e_hi - b0;
+    float z[4 * MAXV];
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        if (k < nv) {
+            const auto v_ = BufLoad<4, kCpolSc1>::at(rsc, (b0 + 4 * k) * 4, 0);
+            z[4 * k] = v_[0]; z[4 * k + 1] = v_[1]; z[4 * k + 2] = v_[2]; z[4 * k + 3] = v_[3];
+        } else {
+            z[4 * k] = z[4 * k + 1] = z[4 * k + 2] = z[4 * k + 3] = 0.0f;
+        }
+    }
+    uint64_t cm = 0;
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        if (k < nv) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * k + j;
+                cm |= (uint64_t)(i >= i_lo && i < i_hi && cut.keep(z[i])) << i;
+            }
+        }
+    }
+    int C;
+    int slot = block_excl_sum<NT>((int)__builtin_popcountll(cm), sh.tmp, &C);
+    if (C < topk || C > kSelCandMax) return false;   // (uniform)
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+        if (k < nv) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * k + j;
+                if ((cm >> i) & 1ull) {
+                    sh.ckey[slot] = score_key(z[i]);
+                    sh.cblk[slot] = b0 + i;
+                    ++slot;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    return select_cands<NT>(g, C, topk, out, sh);
+}
+
 template <int NT, typename SH>
 __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, const Ranges &r, int topk,
-                                                       int32_t *out, SH &sh) {
+                                             const SelOut &out, SH &sh) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads of the scores below
     const int tid = threadIdx.x;
     const int ne = r.e_hi - r.e_lo;
@@ -1209,24 +1276,34 @@ __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, cons
         const uint32_t k = score_key(sc[b]);
         bool tk = k > T;
         if (k == T) tk = (eqi++ < need);
-        if (tk && pos < g.sink + topk) out[pos++] = b;
+        if (tk && pos < g.sink + topk) out.put(pos++, b);
     }
 }
 
 // Eligible blocks the register path of an NT-thread selection holds.
 template <int NT> constexpr int keys_max() { return NT == kIdxThreads ? kKeysMax : 64 * NT; }
 
+// The forced blocks around a selection of topk eligible blocks: the sink
+// blocks first, the window blocks after the topk, and the count.
+template <int NT>
+__device__ __forceinline__ void emit_forced(const Geo &g, const Ranges &r, int topk, const SelOut &out) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < g.sink; i += NT) out.put(i, i);
+    const int nwin = r.b_last - r.fw + 1;
+    for (int i = tid; i < nwin; i += NT) out.put(g.sink + topk + i, r.fw + i);
+    if (tid == 0) out.count(g.sink + topk + nwin);
+}
+
 template <int NT, typename SH>
-__device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int L, int32_t *out, int32_t *nout,
-                                              SH &sh) {
+__device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int L, const SelOut &out, SH &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     const int ne = r.e_hi - r.e_lo;
     const int topk = eff_topk(g, r);
     if (g.topk <= 0 || ne <= topk) {
         const int n = r.b_last + 1;
-        for (int i = tid; i < n; i += NT) out[i] = i;
-        if (tid == 0) *nout = n;
+        for (int i = tid; i < n; i += NT) out.put(i, i);
+        if (tid == 0) out.count(n);
         return;
     }
     if (topk > 0) {                               // (none scored when the forced blocks fill the count)
@@ -1250,10 +1327,7 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
         }
         if (!done) select_radix<NT>(g, sc, r, topk, out, sh);
     }
-    for (int i = tid; i < g.sink; i += NT) out[i] = i;
-    const int nwin = r.b_last - r.fw + 1;
-    for (int i = tid; i < nwin; i += NT) out[g.sink + topk + i] = r.fw + i;
-    if (tid == 0) *nout = g.sink + topk + nwin;
+    emit_forced<NT>(g, r, topk, out);
 }
 
 // Shared selection (shared_selection = 1): one selection for every KV head of
@@ -1261,11 +1335,11 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
 // (score = sum over all query heads of their -- relu'd when set -- dots, each
 // KV head's group summed first).  Called by the one workgroup that saw every
 // head's scores: it sums the rows into row 0 (device-coherent loads of the
-// other workgroups' stores), selects on it and copies the selection, and its
-// count, to every one of g.sel_rows selection rows.
+// other workgroups' stores) and selects on it into every one of the
+// g.sel_rows selection rows.
 template <int NT, typename SH>
-__device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t sc_stride, int L, int32_t *out0,
-                                              int64_t out_stride, int32_t *nout0, SH &sh) {
+__device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t sc_stride, int L, const SelOut &out,
+                                              SH &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
     if (g.Hkv > 1) {                               // one score row needs no sum
@@ -1289,21 +1363,10 @@ __device__ __forceinline__ void select_shared(const Geo &g, float *sc0, int64_t 
             for (int u = 0; u < U; ++u)
                 if (b0 + u * NT < r.e_hi) sc0[b0 + u * NT] = acc[u];
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the summed row, for the selection's loads
+        __syncthreads();
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the summed row, for the selection's loads
-    __syncthreads();
-    select_blocks<NT>(g, sc0, L, out0, nout0, sh);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the selection, for the copy below
-    __syncthreads();
-    const BufRsrc ro = buf_rsrc(out0, (uint32_t)out_stride * 4u);
-    const BufRsrc rn = buf_rsrc(nout0, 4u);
-    const int n = __builtin_bit_cast(int, BufLoad<1, kCpolSc1>::at(rn, 0, 0)[0]);
-    for (int i = tid; i < n; i += NT) {
-        const int32_t x = __builtin_bit_cast(int32_t, BufLoad<1, kCpolSc1>::at(ro, i * 4, 0)[0]);
-        for (int h = 1; h < g.sel_rows; ++h) out0[h * out_stride + i] = x;
-    }
-    if (tid == 0)
-        for (int h = 1; h < g.sel_rows; ++h) nout0[h] = n;
+    select_blocks<NT>(g, sc0, L, out, sh);
 }
 
 // The selection of long contexts (more eligible blocks than the indexer
@@ -1320,6 +1383,8 @@ struct BigSelShared {
     int32_t cblk[kSelCandMax];
     uint8_t cok[kSelCandMax];                     // their threshold-bin verdicts
     uint32_t kred[2 * (kBigSelThreads / 64)];
+    int wpre[kCutWgMax];                          // multi-workgroup selection: region offsets
+    int ctot, flag;
     float red[2 * (kBigSelThreads / 64)];
     int tmp[kBigSelThreads / 64];
     int bin, need, ncand, cnt_b;
@@ -1332,23 +1397,125 @@ k_select_big(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len,
     __shared__ BigSelShared sh;
     const int gh = blockIdx.x, s = blockIdx.y;
     const int L = seq_length(g, g.pf ? 0 : seq_len[s], s);
+    const SelOut out = sel_out(g, sel, nsel, max_sel, s, s * g.Hkv + gh);
     if (L < 1 || L > max_seq_len) {
         if (threadIdx.x == 0) {
-            if (g.shared)
-                for (int h = 0; h < g.sel_rows; ++h) nsel[s * g.sel_rows + h] = 0;
-            else
-                nsel[s * g.Hkv + gh] = 0;
+            out.count(0);
             set_status(v.status, QWFN_STATUS_LEN_RANGE);
         }
         return;
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // the scoring launch's stores
     if (g.shared)
-        select_shared<kBigSelThreads>(g, scores + (int64_t)s * g.Hkv * nb_cap, nb_cap, L,
-                                      sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
+        select_shared<kBigSelThreads>(g, scores + (int64_t)s * g.Hkv * nb_cap, nb_cap, L, out, sh);
     else
-        select_blocks<kBigSelThreads>(g, scores + ((int64_t)s * g.Hkv + gh) * nb_cap, L,
-                                      sel + ((int64_t)s * g.Hkv + gh) * max_sel, nsel + s * g.Hkv + gh, sh);
+        select_blocks<kBigSelThreads>(g, scores + ((int64_t)s * g.Hkv + gh) * nb_cap, L, out, sh);
+}
+
+// The multi-workgroup selection of long decode contexts: ws.cut_wg
+// workgroups a selection, each over kCutKeys scores (thread t: 4 aligned
+// blocks).  Every workgroup takes the same sampled cut and compacts the
+// candidates among its scores into its own region of ws.cand, in block order,
+// with their count; the last to arrive gathers the regions in order into LDS
+// and makes the exact selection on them.  A selection the cut does not serve
+// (it does not apply, or the candidates number fewer than topk or more than
+// kSelCandMax, or their threshold bin overflows) that last workgroup makes
+// alone, as k_select_big does.  One score row a selection: per KV head, or
+// shared with one scoring head group.
+// grid (ws.cut_wg, shared ? 1 : Hkv, n_seq)
+static_assert(kCutKeys == 4 * kBigSelThreads, "four scores a thread");
+__global__ void __launch_bounds__(kBigSelThreads)
+k_select_cut(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, Ws ws, int32_t *sel,
+             int32_t *nsel, int32_t max_sel) {
+    constexpr int NT = kBigSelThreads, CPT = kSelCandMax / NT;
+    __shared__ BigSelShared sh;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int w = blockIdx.x, nw = gridDim.x, gh = blockIdx.y, s = blockIdx.z;
+    const int pair = s * g.Hkv + gh;
+    const int L = seq_len[s];
+    const bool ok = L >= 1 && L <= max_seq_len;
+    const float *sc = ws.scores + (int64_t)pair * ws.nb_cap;
+    Ranges r{0, 0, 0, 0};
+    int topk = 0, rs = 0;                          // rs > 0: the cut serves this selection
+    if (ok) {
+        r = qsa_ranges(g, L);
+        topk = eff_topk(g, r);
+        const int span = r.e_hi - (r.e_lo & ~3);
+        if (g.topk > 0 && r.e_hi - r.e_lo > topk && span <= nw * kCutKeys && span <= 64 * NT)
+            rs = sample_rank(r, topk);
+    }
+    const BufRsrc rsc = buf_rsrc(sc, (uint32_t)((r.e_hi + 3) & ~3) * 4u);
+    uint2 *cand = ws.cand + (int64_t)pair * nw * kCutKeys;
+    int32_t *ccnt = ws.ccnt + (int64_t)pair * kCutWgMax;
+    if (rs > 0) {                                  // (uniform over the selection's workgroups)
+        const CutMap cut = sample_cut<NT>(rsc, r, rs, sh);
+        const int b0 = (r.e_lo & ~3) + w * kCutKeys + 4 * tid;
+        const auto z = BufLoad<4, kCpolSc1>::at(rsc, b0 * 4, 0);   // past e_hi: 0, not kept
+        uint32_t cm = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cm |= (uint32_t)(b0 + j >= r.e_lo && b0 + j < r.e_hi && cut.keep(z[j])) << j;
+        int cw;
+        int slot = block_excl_sum<NT>(__builtin_popcount(cm), sh.tmp, &cw);
+        uint2 *reg = cand + (int64_t)w * kCutKeys;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if ((cm >> j) & 1u) reg[slot++] = make_uint2(score_key(z[j]), (uint32_t)(b0 + j));
+        if (tid == 0) ccnt[w] = cw;
+    }
+    // the regions and counts are read with device-coherent loads
+    if (!arrive_last<false>(&ws.cnt_idx[pair], nw, &sh.flag)) return;
+    if (tid == 0) ws.cnt_idx[pair] = 0;
+    const SelOut out = sel_out(g, sel, nsel, max_sel, s, pair);
+    if (!ok) {
+        if (tid == 0) {
+            out.count(0);
+            set_status(v.status, QWFN_STATUS_LEN_RANGE);
+        }
+        return;
+    }
+    bool done = false;
+    if (rs > 0) {
+        if (wid == 0) {                            // region offsets: an exclusive scan of the counts
+            const BufRsrc rc = buf_rsrc(ccnt, (uint32_t)nw * 4u);
+            const int c = lane < nw ? __builtin_bit_cast(int, BufLoad<1, kCpolSc1>::at(rc, lane * 4, 0)[0]) : 0;
+            const int incl = wave_incl_scan(c);
+            sh.wpre[lane] = incl - c;
+            if (lane == 63) sh.ctot = incl;
+        }
+        __syncthreads();
+        const int C = sh.ctot;
+        if (C >= topk && C <= kSelCandMax) {       // (uniform)
+            const BufRsrc rg = buf_rsrc(cand, (uint32_t)nw * kCutKeys * 8u);
+            float2 e[CPT];
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {        // candidate c: the last region starting at or before it
+                const int c = tid + u * NT;
+                int lo = 0, hi = nw - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (sh.wpre[mid] <= c) lo = mid; else hi = mid - 1;
+                }
+                const int off = c < C ? (lo * kCutKeys + c - sh.wpre[lo]) * 8 : 0;
+                const auto x = BufLoad<2, kCpolSc1>::at(rg, off, 0);
+                e[u] = make_float2(x[0], x[1]);
+            }
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                const int c = tid + u * NT;
+                if (c < C) {
+                    sh.ckey[c] = __builtin_bit_cast(uint32_t, e[u].x);
+                    sh.cblk[c] = __builtin_bit_cast(int32_t, e[u].y);
+                }
+            }
+            __syncthreads();
+            done = select_cands<NT>(g, C, topk, out, sh);
+            if (done) emit_forced<NT>(g, r, topk, out);
+        }
+    }
+    if (!done) {
+        __syncthreads();                           // LDS reads of the cut path are done
+        select_blocks<NT>(g, sc, L, out, sh);
+    }
 }
 
 // grid (n_chunks [+1 with the fused append], Hkv, n_seq)
@@ -1428,22 +1595,18 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     const int cpair = g.shared ? s * g.Hkv : pair;
     if (!arrive_last<false>(&ws.cnt_idx[cpair], g.shared ? n_chunks * g.Hkv : n_chunks, &sh.flag)) return;
     if (tid == 0) ws.cnt_idx[cpair] = 0;
-    int32_t *out = sel + (int64_t)pair * max_sel;
+    const SelOut out = sel_out(g, sel, nsel, max_sel, s, pair);
     if (!ok) {
         if (tid == 0) {
-            if (g.shared)
-                for (int h = 0; h < g.sel_rows; ++h) nsel[s * g.sel_rows + h] = 0;
-            else
-                nsel[pair] = 0;
+            out.count(0);
             set_status(v.status, QWFN_STATUS_LEN_RANGE);
         }
         return;
     }
     if (g.shared)
-        select_shared<kIdxThreads>(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L,
-                      sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
+        select_shared<kIdxThreads>(g, ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, ws.nb_cap, L, out, sh);
     else
-        select_blocks<kIdxThreads>(g, sc, L, out, nsel + pair, sh);
+        select_blocks<kIdxThreads>(g, sc, L, out, sh);
 }
 
 template <int HD, int G>
@@ -1466,7 +1629,10 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
                        sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)!big);
-    if (big)
+    if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
+        hipLaunchKernelGGL(k_select_cut, dim3((unsigned)ws.cut_wg, (unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
+                           dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws, sel, nsel, max_sel);
+    else if (big)
         hipLaunchKernelGGL(k_select_big, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws.scores, ws.nb_cap, sel,
                            nsel, max_sel);
@@ -2618,12 +2784,11 @@ k_pf_select(Geo g, float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, i
     __shared__ IdxShared sh;
     const int gh = blockIdx.x, s = blockIdx.y;             // (gh = 0 with a shared selection)
     const int pair = s * g.Hkv + gh;
+    const SelOut out = sel_out(g, sel, nsel, max_sel, s, pair);
     if (g.shared)
-        select_shared<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1,
-                      sel + (int64_t)s * g.sel_rows * max_sel, max_sel, nsel + s * g.sel_rows, sh);
+        select_shared<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, nb_cap, g.pf_pos0 + s + 1, out, sh);
     else
-        select_blocks<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, sel + (int64_t)pair * max_sel,
-                      nsel + pair, sh);
+        select_blocks<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, out, sh);
 }
 
 template <int HD, int G>

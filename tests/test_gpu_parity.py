@@ -218,6 +218,15 @@ def test_select_big_sampled_cut(mutate):
     _indexer_case(BIG, [BIG_L], seed=245, mutate=mutate)
 
 
+def test_select_big_per_head_and_shared():
+    """Two KV heads past 8192 eligible blocks: per-head selections (one
+    multi-workgroup selection per head, three sequences), and one shared
+    selection on the summed rows (the one-workgroup selection)."""
+    two = Cfg(**{**BIG.__dict__, "n_head": 16, "n_head_kv": 2})
+    _indexer_case(two, [BIG_L, 9000, BIG_L - 3], seed=246)
+    _indexer_case(Cfg(**{**two.__dict__, "shared_selection": 1}), [BIG_L, BIG_L - 3], seed=247)
+
+
 @pytest.mark.parametrize("cfg", [TINY, G12, Cfg(relu_per_head=1), Cfg(top_k_blocks=3, sink_blocks=2, local_tokens=100)])
 def test_indexer_other_shapes(cfg):
     _indexer_case(cfg, [3 * cfg.page_tokens - 1, cfg.page_tokens + 7], seed=220)
