@@ -162,7 +162,7 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.max_sel = max_sel;
     l.n_tiles = (int32_t)(((int64_t)max_sel * g.bt + 63) / 64);
     const size_t pairs = (size_t)n_seq * g.Hkv;
-    size_t off = align256(2 * (size_t)kMaxCounters * sizeof(int32_t));
+    size_t off = align256((size_t)kMaxCounters * sizeof(int32_t));
     auto take = [&](size_t bytes) { const size_t o = off; off = align256(off + bytes); return o; };
     l.sel = take(pairs * max_sel * sizeof(int32_t));
     l.nsel = take(pairs * sizeof(int32_t));
@@ -184,7 +184,6 @@ Ws ws_bind(void *base, const WsLayout &l) {
     uint8_t *b = (uint8_t *)base;
     Ws w;
     w.cnt_idx = (int32_t *)b;
-    w.cnt_attn = (int32_t *)b + kMaxCounters;
     w.sel = (int32_t *)(b + l.sel);
     w.nsel = (int32_t *)(b + l.nsel);
     w.scores = (float *)(b + l.scores);

@@ -47,7 +47,6 @@ constexpr int32_t kCutKeys = 4096;
 constexpr int32_t kCutWgMax = 64;
 struct Ws {
     int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
-    int32_t *cnt_attn;   // [kMaxCounters] attention completion counters
     int32_t *sel;        // [n_seq][Hkv][max_sel]  selection of the fused step
     int32_t *nsel;       // [n_seq][Hkv]
     float   *scores;     // [n_seq][Hkv][nb_cap]

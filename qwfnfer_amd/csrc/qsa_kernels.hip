@@ -1618,8 +1618,9 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
     // scoring workgroups read: with local_tokens = 0 a just-completed block is
     // eligible.  Otherwise the append and the pooling run as launches of their own.
     if (fa.enabled && (g.kt != QWFN_KV_Q8_0 || g.local == 0)) {
-        launch_append(g, v, fa.k_new, fa.v_new, fa.src_f16, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
-        launch_pool(g, v, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
+        // (a failed launch surfaces through hipGetLastError after the indexer's)
+        (void)launch_append(g, v, fa.k_new, fa.v_new, fa.src_f16, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
+        (void)launch_pool(g, v, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
         fa.enabled = 0;
     }
     const int nb_max = max_seq_len / g.bt;
@@ -1641,182 +1642,111 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
 // ---------------------------------------------------------------------------
 // attention: TG groups of NW waves per workgroup, one 64-cell tile per group;
 // the groups merge in LDS into one partial softmax state per workgroup, and
-// the last workgroup of a (sequence, KV head) merges the partials.
+// a merge launch (k_merge) combines the workgroups' partials.
 // ---------------------------------------------------------------------------
 
-// The last workgroup of a (sequence, KV head) merges the parts' (m, l, O):
-// og = sum_i w_i O_i / sum_i w_i l_i with w_i = exp2(m_i - max_i m_i).  One
-// wave per head reduces the parts' m and l with DPP while the O loads are in
-// flight; each thread owns VW consecutive output dims and keeps up to MAXP
-// parts of them in registers, so a combine of MAXP parts or fewer costs one
-// round trip.  `scratch` is LDS of scratch_floats floats, `Lh` LDS of 2*G
-// floats.  All threads call.
-template <int G, int HD, int NT>
-struct MergeCfg {
-    static constexpr int VW = (G * HD >= 4 * NT && HD % 4 == 0) ? 4 : (G * HD >= 2 * NT && HD % 2 == 0) ? 2 : 1;
-    static constexpr int OPT = (G * HD / VW + NT - 1) / NT;      // output vectors per thread
-    static constexpr int MAXP = 80 / (VW * OPT) > 40 ? 40 : 80 / (VW * OPT);
-};
-
-// Parts beyond what the LDS scratch holds weights for (dense attention over
-// long contexts): every weight recomputed from memory, one part at a time.
-template <int G, int HD, int NT>
-__device__ __forceinline__ void merge_partials_mem(const Ws &ws, int pair, int parts_act, float *og, float *Lh) {
-    using M = MergeCfg<G, HD, NT>;
-    constexpr int VW = M::VW, OPT = M::OPT, NV = G * HD / VW, NW = NT / 64;
-    using vec = float __attribute__((ext_vector_type(VW)));
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads below
-    const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
-    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
-    const float *pml = ws.part_ml + pb * 2;
-    const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
-    for (int h = wv; h < G; h += NW) {
-        float Mx = -INFINITY;
-        for (int i = ln; i < parts_act; i += 64) Mx = fmaxf(Mx, pml[((int64_t)i * G + h) * 2]);
-        Mx = wave_max(Mx);
-        float Ls = 0.0f;
-        for (int i = ln; i < parts_act; i += 64) {
-            const float m = pml[((int64_t)i * G + h) * 2], l = pml[((int64_t)i * G + h) * 2 + 1];
-            Ls += (m == -INFINITY ? 0.0f : exp2f(m - Mx)) * l;
-        }
-        Ls = wave_sum(Ls);
-        if (ln == 0) { Lh[h] = Ls; Lh[G + h] = Mx; }
+// The combine of a (sequence, KV head)'s attention partials, a launch of its
+// own after the attention: one workgroup per query head, so the parts are read
+// by G workgroups on as many CUs rather than by one.
+//   og = sum_i w_i O_i / sum_i w_i l_i,  w_i = exp2(m_i - max_i m_i)
+// over the parts the attention wrote (its workgroups of tg tile groups, the
+// count recomputed from the length and the selection as the attention counts
+// it).  Thread t sums dim t % HD over the parts congruent to t / HD, its first
+// batch of part loads issued before the weights are known; a length out of
+// range or no cell gives zeros (and, for a length, the status bit).
+// grid (G, Hkv, n_seq or n_q)
+constexpr int kMergeThreads = 256;
+constexpr int kMergeWts = 2048;                   // parts whose weights LDS keeps
+template <int G, int HD>
+__global__ void __launch_bounds__(kMergeThreads)
+k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, const int32_t *nsel,
+        int32_t max_sel, int32_t dense, float *__restrict__ out, Ws ws, int32_t tg) {
+    constexpr int NT = kMergeThreads, R = NT / HD, NW = NT / 64, U = 24;
+    static_assert(R * HD == NT, "whole dims a thread");
+    __shared__ float wts[kMergeWts];
+    __shared__ float red[R][HD];
+    __shared__ float wred[2][NW];
+    const int h = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int pair = s * g.Hkv + gh;
+    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
+    const bool ok = L >= 1 && L <= max_seq_len;
+    int n = 0;
+    if (ok) {
+        n = dense ? (L - 1) / g.bt + 1 : nsel[pair];
+        n = n < max_sel ? n : max_sel;
     }
-    __syncthreads();
-    for (int r = 0; r < OPT; ++r) {
-        const int k = tid + r * NT;
-        if (k >= NV) break;
-        const int h = k * VW / HD;
-        const float Mx = Lh[G + h], Ls = Lh[h];
-        vec acc = vec(0.0f);
-        for (int i = 0; i < parts_act; ++i) {
-            const float m = pml[((int64_t)i * G + h) * 2];
-            if (m != -INFINITY) acc += exp2f(m - Mx) * po[(int64_t)i * NV + k];
-        }
-        reinterpret_cast<vec *>(og)[k] = Ls > 0.0f ? acc * (1.0f / Ls) : vec(0.0f);
-    }
-}
-
-// More parts than the registers hold: the weights w_i,h go to LDS (`wt`, at
-// least parts_act * G floats), then every thread sums its output vectors over
-// the parts eight at a time, each batch's loads issued before any is summed.
-template <int G, int HD, int NT>
-__device__ __forceinline__ void merge_partials_general(const Ws &ws, int pair, int parts_act, float *og,
-                                                                 float *Lh, float *wt) {
-    using M = MergeCfg<G, HD, NT>;
-    constexpr int VW = M::VW, OPT = M::OPT, NV = G * HD / VW, NW = NT / 64, U = 8;
-    using vec = float __attribute__((ext_vector_type(VW)));
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // plain loads below
-    const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
-    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
-    const float *pml = ws.part_ml + pb * 2;
-    const vec *po = reinterpret_cast<const vec *>(ws.part_o + pb * HD);
-    for (int h = wv; h < G; h += NW) {
-        float Mx = -INFINITY;
-        for (int i = ln; i < parts_act; i += 64) Mx = fmaxf(Mx, pml[((int64_t)i * G + h) * 2]);
-        Mx = wave_max(Mx);
-        float Ls = 0.0f;
-        for (int i = ln; i < parts_act; i += 64) {
-            const float m = pml[((int64_t)i * G + h) * 2], l = pml[((int64_t)i * G + h) * 2 + 1];
-            const float w = m == -INFINITY ? 0.0f : exp2f(m - Mx);
-            wt[i * G + h] = w;
-            Ls += w * l;
-        }
-        Ls = wave_sum(Ls);
-        if (ln == 0) Lh[h] = Ls;
-    }
-    __syncthreads();
-    // all of a thread's output vectors per batch: one round trip per U parts
-    vec acc[OPT];
-#pragma unroll
-    for (int r = 0; r < OPT; ++r) acc[r] = vec(0.0f);
-    for (int i0 = 0; i0 < parts_act; i0 += U) {
-        vec x[OPT][U];
-#pragma unroll
-        for (int r = 0; r < OPT; ++r)
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                x[r][u] = po[(int64_t)min(i0 + u, parts_act - 1) * NV + min(tid + r * NT, NV - 1)];
-#pragma unroll
-        for (int r = 0; r < OPT; ++r) {
-            const int h = min(tid + r * NT, NV - 1) * VW / HD;
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (i0 + u < parts_act) acc[r] += wt[(i0 + u) * G + h] * x[r][u];
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < OPT; ++r) {
-        const int k = tid + r * NT;
-        if (k < NV) {
-            const float Ls = Lh[k * VW / HD];
-            reinterpret_cast<vec *>(og)[k] = Ls > 0.0f ? acc[r] * (1.0f / Ls) : vec(0.0f);
-        }
-    }
-}
-
-template <int G, int HD, int NT>
-__device__ __forceinline__ void merge_partials(const Ws &ws, int pair, int parts_act, float *og, float *Lh,
-                                               float *scratch, int scratch_floats) {
-    using M = MergeCfg<G, HD, NT>;
-    constexpr int VW = M::VW, OPT = M::OPT, MAXP = M::MAXP, NV = G * HD / VW;
-    constexpr int NW = NT / 64, HPW = (G + NW - 1) / NW;
-    using vec = float __attribute__((ext_vector_type(VW)));
-    if (parts_act > MAXP || 64 * G > scratch_floats) {
-        if (parts_act * G <= scratch_floats) merge_partials_general<G, HD, NT>(ws, pair, parts_act, og, Lh, scratch);
-        else merge_partials_mem<G, HD, NT>(ws, pair, parts_act, og, Lh);
+    const int parts = ((n * g.bt + 63) / 64 + tg - 1) / tg;
+    float *og = out + ((int64_t)s * g.H + (int64_t)gh * G + h) * HD;
+    if (!ok || parts == 0) {
+        for (int i = tid; i < HD; i += NT) og[i] = 0.0f;
+        if (!ok && tid == 0 && gh == 0 && h == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    // Straight-line path: every load unconditional, through buffer
-    // descriptors sized to the live parts (loads past them read 0), so a cold
-    // instruction cache sees no taken branch.
-    const int tid = threadIdx.x, wv = tid >> 6, ln = tid & 63;
-    const int64_t pb = (int64_t)pair * ws.n_tiles * G;
-    using L = BufLoad<VW, kCpolSc1>;
-    const BufRsrc rm = buf_rsrc(ws.part_ml + pb * 2, (uint32_t)parts_act * G * 8u);
-    const BufRsrc ro = buf_rsrc(ws.part_o + pb * HD, (uint32_t)parts_act * G * HD * 4u);
-    float2 ml[HPW];
+    const int64_t row = (int64_t)pair * ws.n_tiles * G + h;     // part i: row + i * G
+    const float *pml = ws.part_ml + row * 2;
+    const int d = tid % HD, r = tid / HD;
+    const float *po = ws.part_o + row * HD + d;
+    float x[U];
 #pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-        const int h = min(wv + j * NW, G - 1);
-        const auto x = BufLoad<2, kCpolSc1>::at(rm, (ln * G + h) * 8, 0);
-        ml[j] = make_float2(x[0], x[1]);
-    }
-    typename L::T ov[OPT][MAXP];
-#pragma unroll
-    for (int r = 0; r < OPT; ++r) {
-        const int k = min(tid + r * NT, NV - 1);
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i) ov[r][i] = L::at(ro, k * VW * 4, i * G * HD * 4);
-    }
-    // weights w_i,h = 2^(m_i,h - M_h) into LDS (lane = part), L_h = sum_i w_i,h l_i,h
-    float *wt = scratch;                                   // [64][G]
-#pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-        const int h = wv + j * NW;
-        if (h < G) {
-            const bool valid = ln < parts_act;
-            const float m = valid ? ml[j].x : -INFINITY;
-            const float Mx = wave_max(m);
-            const float w = m == -INFINITY ? 0.0f : exp2f(m - Mx);
-            wt[ln * G + h] = w;
-            const float Ls = wave_sum(valid ? w * ml[j].y : 0.0f);
-            if (ln == 0) Lh[h] = Ls;
-        }
-    }
+    for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(r + u * R, parts - 1) * G * HD];
+    float m0 = -INFINITY, l0 = 0.0f;
+    if (tid < parts) { m0 = pml[(int64_t)tid * 2 * G]; l0 = pml[(int64_t)tid * 2 * G + 1]; }
+    float Mx = m0;
+    for (int i = tid + NT; i < parts; i += NT) Mx = fmaxf(Mx, pml[(int64_t)i * 2 * G]);
+    Mx = wave_max(Mx);
+    if (lane == 0) wred[0][wid] = Mx;
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < OPT; ++r) {
-        const int k = tid + r * NT;
-        const int h = min(k, NV - 1) * VW / HD;
-        vec acc = vec(0.0f);
-        // parts past parts_act read 0 with weight 0
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i) acc += wt[i * G + h] * ov[r][i];
-        const float Ls = Lh[h];
-        const vec o = Ls > 0.0f ? acc * (1.0f / Ls) : vec(0.0f);
-        if (k < NV) reinterpret_cast<vec *>(og)[k] = o;
+    for (int i = 0; i < NW; ++i) Mx = fmaxf(Mx, wred[0][i]);
+    auto weight = [&](float m) { return m == -INFINITY ? 0.0f : exp2f(m - Mx); };
+    float Ls = 0.0f;
+    if (tid < parts) {
+        const float w = weight(m0);
+        if (tid < kMergeWts) wts[tid] = w;
+        Ls = w * l0;
     }
+    for (int i = tid + NT; i < parts; i += NT) {
+        const float w = weight(pml[(int64_t)i * 2 * G]);
+        if (i < kMergeWts) wts[i] = w;
+        Ls += w * pml[(int64_t)i * 2 * G + 1];
+    }
+    Ls = wave_sum(Ls);
+    if (lane == 0) wred[1][wid] = Ls;
+    __syncthreads();
+    Ls = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) Ls += wred[1][i];
+    auto wt = [&](int i) { return i < kMergeWts ? wts[i] : weight(pml[(int64_t)i * 2 * G]); };
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (r + u * R < parts) acc += wt(r + u * R) * x[u];
+    for (int i0 = r + U * R; i0 < parts; i0 += U * R) {   // more parts than one batch
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(i0 + u * R, parts - 1) * G * HD];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (i0 + u * R < parts) acc += wt(i0 + u * R) * x[u];
+    }
+    if constexpr (R > 1) {
+        red[r][d] = acc;
+        __syncthreads();
+        if (r == 0) {
+            acc = red[0][d];
+#pragma unroll
+            for (int k = 1; k < R; ++k) acc += red[k][d];
+        }
+    }
+    if (r == 0) og[d] = Ls > 0.0f ? acc * (1.0f / Ls) : 0.0f;
+}
+
+template <int G, int HD>
+static void launch_merge_t(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len, int32_t n_seq,
+                           int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
+                           float *out, const Ws &ws, int32_t tg, hipStream_t st) {
+    hipLaunchKernelGGL((k_merge<G, HD>), dim3((unsigned)G, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kMergeThreads), 0,
+                       st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)(sel == nullptr), out, ws, tg);
 }
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
@@ -1885,8 +1815,6 @@ struct AttnGroup {
 template <int HD, int G, int TG>
 struct AttnShared {
     AttnGroup<HD, G> grp[TG];
-    float Lh[2 * G];                           // combine: L_h, then M_h
-    int flag;
 };
 
 // KT: the K/V element type (chunks of a head row, and their dequantization).
@@ -2129,17 +2057,6 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
             }
         }
     }
-    // completion count; the last workgroup of the pair merges the partials
-    // the combine reads the partials with device-coherent loads (or fences)
-    if (!arrive_last<false>(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
-    if (tid == 0) ws.cnt_attn[pair] = 0;
-    float *og = out + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
-    if (!ok || parts_act == 0) {
-        for (int i = tid; i < G * HD; i += C::NT) og[i] = 0.0f;
-        if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
-        return;
-    }
-    merge_partials<G, HD, C::NT>(ws, pair, parts_act, og, sh.Lh, sh.grp[0].kv, 64 * C::ROWF);
 }
 
 template <int HD, int G, int TG>
@@ -2159,6 +2076,7 @@ static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
     else
         hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q8_0>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
                            nsel, max_sel, out, ws, n_parts);
+    launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -2231,8 +2149,6 @@ struct FastShared {
     FastGroup<HD, G> grp[TG];
     int32_t qa[G][HD / 4], qb[G][HD / 4], qc[G][HD / 4];   // the query as three int8 parts, packed
     float qs[G];                               // q ~= qs * (qa + qb/254 + qc/254^2)
-    float Lh[2 * G];                           // combine: L_h, then M_h
-    int flag;
 };
 
 // DENSE: attend every block of the sequence (sel is not read).
@@ -2481,17 +2397,6 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
             }
         }
     }
-    // the combine reads the partials with device-coherent loads (or fences)
-    if (!arrive_last<false>(&ws.cnt_attn[pair], (int)gridDim.x, &sh.flag)) return;
-    if (tid == 0) ws.cnt_attn[pair] = 0;
-    float *og = out + ((int64_t)s * g.H + (int64_t)gh * G) * HD;
-    if (!ok || parts_act == 0) {
-        for (int i = tid; i < G * HD; i += C::NT) og[i] = 0.0f;
-        if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
-        return;
-    }
-    merge_partials<G, HD, C::NT>(ws, pair, parts_act, og, sh.Lh, reinterpret_cast<float *>(&sh.grp[0]),
-                                 (int)(sizeof(FastGroup<HD, G>) / sizeof(float)));
 }
 
 template <int HD, int G, int TG>
@@ -2507,6 +2412,7 @@ static void launch_attn_q8_t(const Geo &g, const qwfn_kv_view &v, const float *q
     else
         hipLaunchKernelGGL((k_attn_q8<HD, G, TG, true>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q,
                            seq_len, max_seq_len, sel, nsel, max_sel, out, ws);
+    launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
 }
 
 // ---------------------------------------------------------------------------
