@@ -623,9 +623,9 @@ def main():
     traffic = None
     if os.path.exists(TRAFFIC_JSON):
         with open(TRAFFIC_JSON) as f:
-            tj = json.load(f).get("k_attn_q8", {})
+            tj = json.load(f).get("attention_call", {})
         if tj.get("context") == big:
-            traffic = tj.get("hbm_bytes_per_launch")
+            traffic = tj.get("hbm_bytes_per_call")
     line = {
         "metric": METRIC,
         "value": round(top["us_per_layer"], 3),
@@ -651,7 +651,8 @@ def main():
                         for c, v in per_ctx.items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_attn_q8 (sparse decode attention, selected q8_0 K+V)",
+            "kernel": "sparse decode attention call: k_attn_q8 (selected q8_0 K+V, split into partials), "
+                      "then k_merge (one workgroup per query head combines them)",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
