@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define QWFN_QSA_ABI_VERSION 3
+#define QWFN_QSA_ABI_VERSION 4
 
 /* return codes */
 #define QWFN_OK        0
@@ -326,8 +326,8 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
  * 492), and ONE top-k selection serves every KV head.
  *
  * Here the raw keys are paged like K and V (the KV view's page table and
- * page_tokens); the pooled keys are kept as fp32 holding the fp16-rounded
- * values.  The selection rule comes from qwfn_qsa_shape as usual: the
+ * page_tokens); the pooled keys are fp16, as in the reference's pool cache.
+ * The selection rule comes from qwfn_qsa_shape as usual: the
  * checkpoint's is sink_blocks 0, local_tokens 0, topk_counts_forced 1,
  * top_k_blocks = k_blocks (513 = ceil((idx_top_k + r - 1) / r), src/
  * qwfn_engine.cpp:430), relu_per_head 1.  The selection is written to each of
@@ -344,7 +344,7 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
  *           position for text (src/qwfn_engine.cpp:741, 781, 926, 934), which
  *           makes it this rotation; per-section (vision) positions are not
  *           supported.
- *   store   fp16 round to nearest even, kept as fp32.                        */
+ *   store   fp16 round to nearest even.                                     */
 typedef struct qwfn_idx_shape {
     int32_t idx_dim;         /* 128: indexer key length (src/qwfn_hparams.h:53) */
     int32_t n_idx_head;      /* 4: indexer query heads (:52)                     */
@@ -356,7 +356,7 @@ typedef struct qwfn_idx_shape {
 typedef struct qwfn_idx_view {
     void        *raw;        /* fp16 [n_phys_pages][page_tokens][idx_dim], device,
                               * paged by the KV view's page_table (16-B aligned) */
-    float       *pooled;     /* fp32 [n_seq][blocks_per_seq][idx_dim], device   */
+    void        *pooled;     /* fp16 [n_seq][blocks_per_seq][idx_dim], device   */
     const float *k_norm;     /* fp32 [idx_dim] indexer.k_norm.weight, device    */
 } qwfn_idx_view;
 

@@ -107,6 +107,7 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->vdim = s->block_tokens % 64 == 0 && s->kv_type == QWFN_KV_Q8_0;
     g->scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)s->head_dim));
     g->pf = 0; g->pf_seq = 0; g->pf_pos0 = 0;
+    g->pooled_f16 = 0;
     if (v) {
         g->pps = v->pages_per_seq; g->n_phys = v->n_phys_pages; g->n_seq_view = v->n_seq;
         g->bps = (int32_t)((int64_t)v->pages_per_seq * s->page_tokens / s->block_tokens);
@@ -550,7 +551,7 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
                              nullptr, nullptr, n_q, seq, pos0, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer keys");
         const int32_t b0 = pos0 / g.bt, b1 = (max_len + g.bt - 1) / g.bt;
-        e = launch_idx_pool(g, *view, ix->ig, (const uint16_t *)ix->iv->raw, ix->iv->pooled, ix->iv->k_norm,
+        e = launch_idx_pool(g, *view, ix->ig, (const uint16_t *)ix->iv->raw, (uint16_t *)ix->iv->pooled, ix->iv->k_norm,
                             nullptr, nullptr, b1 - b0, seq, b0, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer pool");
     }
@@ -615,6 +616,7 @@ Geo idx_scoring_geo(const Geo &g, const qwfn_idx_shape *is) {
     gi.H = is->n_idx_head; gi.Hkv = 1; gi.hd = is->idx_dim; gi.G = is->n_idx_head;
     gi.shared = 1;
     gi.sel_rows = g.Hkv;
+    gi.pooled_f16 = 1;
     return gi;
 }
 
@@ -648,7 +650,7 @@ int qwfn_idx_cache_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *isha
         return fail(QWFN_EINVAL, "idx_cache_bytes: NULL output or n_seq / pages_per_seq < 1");
     *raw_page_bytes = (size_t)shape->page_tokens * ishape->idx_dim * 2;
     *pooled_bytes = (size_t)n_seq * ((size_t)pages_per_seq * shape->page_tokens / shape->block_tokens) *
-                    ishape->idx_dim * 4;
+                    ishape->idx_dim * 2;
     return ok();
 }
 
@@ -682,7 +684,7 @@ int qwfn_idx_append_pool(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, 
     hipError_t e = launch_idx_write(g, *view, ig, (uint16_t *)iview->raw, k_raw, src_dtype == QWFN_SRC_F16, seq_ids,
                                     pos, n_rows, 0, 0, st);
     if (e != hipSuccess) return hip_fail(e, "idx_append_pool: write");
-    e = launch_idx_pool(g, *view, ig, (const uint16_t *)iview->raw, iview->pooled, iview->k_norm, seq_ids, pos,
+    e = launch_idx_pool(g, *view, ig, (const uint16_t *)iview->raw, (uint16_t *)iview->pooled, iview->k_norm, seq_ids, pos,
                         n_rows, 0, 0, st);
     return e == hipSuccess ? ok() : hip_fail(e, "idx_append_pool: pool");
 }
@@ -697,7 +699,7 @@ int qwfn_idx_pool_rebuild(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
     if (seq < 0 || seq >= view->n_seq) return fail(QWFN_EINVAL, "idx_pool_rebuild: seq %d outside the view", seq);
     if (n_whole < 0) return fail(QWFN_EINVAL, "idx_pool_rebuild: n_whole %d < 0", n_whole);
     if (n_whole > g.bps) return fail(QWFN_ERANGE, "idx_pool_rebuild: n_whole %d > %d blocks", n_whole, g.bps);
-    const hipError_t e = launch_idx_pool(g, *view, ig, (const uint16_t *)iview->raw, iview->pooled, iview->k_norm,
+    const hipError_t e = launch_idx_pool(g, *view, ig, (const uint16_t *)iview->raw, (uint16_t *)iview->pooled, iview->k_norm,
                                          nullptr, nullptr, n_whole, seq, 0, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "idx_pool_rebuild");
 }
@@ -722,7 +724,7 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const
     if (ws_bytes < l.total) return fail(QWFN_ERANGE, "idx_select: workspace of %zu bytes < %zu", ws_bytes, l.total);
     const Ws w = ws_bind(ws, l);
     qwfn_kv_view vi = *view;
-    vi.pooled = iview->pooled;
+    vi.pooled = (float *)iview->pooled;                   // fp16 keys (Geo::pooled_f16)
     const FusedAppend fa{nullptr, nullptr, 0, 0};
     const hipError_t e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, w, fa,
                                         (hipStream_t)stream);
@@ -746,7 +748,7 @@ int qwfn_idx_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view
         return fail(QWFN_EINVAL, "idx prefill: k_raw must be 16-byte aligned and come with k_new / v_new");
     ix.gi = idx_scoring_geo(g, ishape);
     ix.vi = *view;
-    ix.vi.pooled = iview->pooled;
+    ix.vi.pooled = (float *)iview->pooled;                // fp16 keys (Geo::pooled_f16)
     ix.iv = iview;
     ix.q_idx = q_idx;
     ix.k_raw = k_raw;

@@ -3,8 +3,7 @@
 // idx_dim values per token, paged like K and V, and its pooled block keys --
 // the mean of a block's block_tokens raw keys, RMSNorm * k_norm, then the
 // rotary position of the block's first token -- rounded to fp16 as the
-// reference's fp16 pool cache holds them (src/qwfn_engine.cpp:389-394) and
-// stored as fp32 for the indexer's scoring.
+// reference's fp16 pool cache holds them (src/qwfn_engine.cpp:389-394).
 //
 // Everything here is bandwidth- or latency-trivial next to the attention (one
 // block per decode step, a few MB for a rebuild), so the kernels favour an
@@ -71,10 +70,10 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 //            reference's IMROPE (:425-427) is this rotation: it gives every
 //            position section the same position for text (src/qwfn_engine.cpp:
 //            741, 781, 926, 934).
-//   store  : rounded to fp16, as fp32.
+//   store  : rounded to fp16 (the reference's F16 pool cache).
 template <int D>
 __global__ void __launch_bounds__(256)
-k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, float *__restrict__ pooled,
+k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
            const float *__restrict__ k_norm, const int32_t *seq_ids, const int32_t *pos, int32_t n_items,
            int32_t seq_const, int32_t blk0) {
 #pragma clang fp contract(off)
@@ -126,7 +125,7 @@ k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, f
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    float *dst = pooled + ((int64_t)seq * g.bps + b) * D;
+    uint16_t *dst = pooled + ((int64_t)seq * g.bps + b) * D;
     const int half = ig.nd / 2;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -139,12 +138,12 @@ k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, f
             const float x0 = ys[w][i], x1 = ys[w][i + half];
             o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
         }
-        dst[d] = h2f(f2h(o));
+        dst[d] = f2h(o);
     }
 }
 
 hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,
-                           float *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
+                           uint16_t *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
                            int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st) {
     if (n_items <= 0) return hipSuccess;
     const dim3 grid((unsigned)((n_items + 3) / 4));

@@ -26,6 +26,7 @@ struct Geo {
     int32_t pps, n_phys, n_seq_view; // pages per sequence, pool pages, view seqs
     int32_t bps;                     // pooled blocks per sequence
     int32_t vdim;                    // V quants dim-major per 64-token tile (bt % 64 == 0)
+    int32_t pooled_f16;              // view.pooled holds fp16 keys (the checkpoint indexer's)
     int64_t page_bytes, qbytes;      // page size, quant bytes per page
     float inv_bt;                    // 1.0f / block_tokens (host-rounded)
     float scale_log2;                // log2(e) / sqrt(head_dim)
@@ -103,7 +104,7 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 // run of rows in one block pools it once), else blocks blk0 + [0, n_items) of
 // sequence seq_const.
 hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,
-                           float *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
+                           uint16_t *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
                            int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st);
 // seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r;
 // len (decode): row r is sequence r's token at position len[r] - 1.

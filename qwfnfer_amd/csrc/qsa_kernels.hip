@@ -1547,10 +1547,21 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     const int bl = tid >> 2, j = tid & 3;
     const int bi = c * kBlocksPerChunk + bl;
     const int bp = min(g.sink + bi, g.bps - 1);
-    const float *P = v.pooled + (((int64_t)cache_seq(g, s) * g.Hkv + gh) * g.bps + bp) * HD;
+    const int64_t prow = (((int64_t)cache_seq(g, s) * g.Hkv + gh) * g.bps + bp) * HD;
     float4 p4[HD / 16];
+    if (g.pooled_f16) {                            // fp16 keys (the checkpoint indexer's pool cache)
+        const uint16_t *P = reinterpret_cast<const uint16_t *>(v.pooled) + prow;
 #pragma unroll
-    for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
+        for (int i = 0; i < HD / 16; ++i) {
+            const uint2 x = *reinterpret_cast<const uint2 *>(P + 16 * i + 4 * j);
+            p4[i] = make_float4(h2f((uint16_t)x.x), h2f((uint16_t)(x.x >> 16)), h2f((uint16_t)x.y),
+                                h2f((uint16_t)(x.y >> 16)));
+        }
+    } else {
+        const float *P = v.pooled + prow;
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
+    }
     if (ok && g.topk > 0) {
         const Ranges r = qsa_ranges(g, L);
         const int ne = r.e_hi - r.e_lo;
@@ -2609,11 +2620,18 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
     const int tid = threadIdx.x, gh = blockIdx.z;
     const int b_base = g.sink + (int)blockIdx.x * kPfB;
     const int q_base = (int)blockIdx.y * kPfQ;
-    const float *P = v.pooled + ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps * HD;
+    const int64_t prow = ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps * HD;
     for (int i = tid; i < kPfB * NDC; i += 256) {
         const int b = i / NDC, dc = i % NDC;
         const int bb = min(b_base + b, g.bps - 1);
-        sh.p[dc][b] = *reinterpret_cast<const float4 *>(P + (int64_t)bb * HD + 4 * dc);
+        if (g.pooled_f16) {                        // fp16 keys (the checkpoint indexer's pool cache)
+            const uint2 x = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(v.pooled) + prow +
+                                                             (int64_t)bb * HD + 4 * dc);
+            sh.p[dc][b] = make_float4(h2f((uint16_t)x.x), h2f((uint16_t)(x.x >> 16)), h2f((uint16_t)x.y),
+                                      h2f((uint16_t)(x.y >> 16)));
+        } else {
+            sh.p[dc][b] = *reinterpret_cast<const float4 *>(v.pooled + prow + (int64_t)bb * HD + 4 * dc);
+        }
     }
     const int qi0 = QA * (tid / 16), bi0 = tid % 16;
     float score[QA][4];

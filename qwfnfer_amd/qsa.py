@@ -517,7 +517,7 @@ class IdxCache:
     """One attention layer's indexer keys, paged by a :class:`KvCache`'s page
     table: raw fp16 keys [n_phys_pages, page_tokens, idx_dim] (the reference's
     idx cache) and the pooled block keys [n_seq, blocks_per_seq, idx_dim] (its
-    F16 pool cache, kept as fp32 holding fp16 values), plus k_norm [idx_dim]."""
+    F16 pool cache), plus k_norm [idx_dim]."""
     icfg: IdxConfig
     kv: KvCache
     raw: torch.Tensor
@@ -534,8 +534,8 @@ class IdxCache:
         dev = kv.k_pages.device
         raw = torch.zeros((kv.n_phys_pages, cfg.page_tokens, icfg.idx_dim), dtype=torch.float16, device=dev)
         bps = kv.pages_per_seq * cfg.page_tokens // cfg.block_tokens
-        pooled = torch.zeros((kv.n_seq, bps, icfg.idx_dim), dtype=torch.float32, device=dev)
-        assert raw.numel() * 2 == rpb.value * kv.n_phys_pages and pooled.numel() * 4 == pb.value
+        pooled = torch.zeros((kv.n_seq, bps, icfg.idx_dim), dtype=torch.float16, device=dev)
+        assert raw.numel() * 2 == rpb.value * kv.n_phys_pages and pooled.numel() * 2 == pb.value
         k_norm = k_norm.to(device=dev, dtype=torch.float32).contiguous()
         _need(k_norm, "k_norm", torch.float32, icfg.idx_dim)
         return cls(icfg, kv, raw, pooled, k_norm)

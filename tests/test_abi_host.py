@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.qwfn_qsa_abi_version() == 3
+    assert lib.qwfn_qsa_abi_version() == 4
 
 
 def _code(name, *args):
@@ -64,7 +64,7 @@ def test_idx_argument_validation():
     out, out2 = C.c_size_t(), C.c_size_t()
     assert _code("qwfn_idx_cache_bytes", C.byref(cfg.shape()), C.byref(icfg.shape()), 1, 4, C.byref(out),
                  C.byref(out2)) == 0
-    assert out.value == 256 * 128 * 2 and out2.value == 4 * 256 // 4 * 128 * 4
+    assert out.value == 256 * 128 * 2 and out2.value == 4 * 256 // 4 * 128 * 2
     bad = [dict(idx_dim=96), dict(rope_dim=63), dict(rope_dim=256), dict(rope_freq_base=0.0),
            dict(rms_eps=-1.0), dict(n_idx_head=0)]
     for kw in bad:
