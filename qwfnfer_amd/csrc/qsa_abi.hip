@@ -681,6 +681,12 @@ int qwfn_idx_append_pool(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, 
         return fail(QWFN_EINVAL, "idx_append_pool: NULL or misaligned k_raw (16) / NULL pos / n_rows < 0");
     if (n_rows == 0) return ok();
     hipStream_t st = (hipStream_t)stream;
+    if (n_rows <= 64) {                           // a decode step: one launch
+        const hipError_t e1 = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled,
+                                                     iview->k_norm, k_raw, src_dtype == QWFN_SRC_F16, seq_ids, pos,
+                                                     n_rows, st);
+        return e1 == hipSuccess ? ok() : hip_fail(e1, "idx_append_pool");
+    }
     hipError_t e = launch_idx_write(g, *view, ig, (uint16_t *)iview->raw, k_raw, src_dtype == QWFN_SRC_F16, seq_ids,
                                     pos, n_rows, 0, 0, st);
     if (e != hipSuccess) return hip_fail(e, "idx_append_pool: write");

@@ -58,9 +58,12 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
     return hipGetLastError();
 }
 
-// One wave per block; lane l owns dims l + 64k (k < D/64).
+// The pooled key of one block from its bt members m[0 .. bt) (fp16 rows of D
+// values, position order), by one wave; lane l owns dims l + 64k (k < D/64).
+// ys is the wave's own D floats of LDS.
 //   mean   : fp32 add chain over the members in position order, * (1/bt)
-//            (ggml_add chain + ggml_scale, src/qwfn_graph.cpp:415-422)
+//            (ggml_add chain + ggml_scale, src/qwfn_graph.cpp:415-422); the
+//            members' loads go out eight at a time before any is summed
 //   RMSNorm: sum of the fp32 squares in fp64 -- per lane in k order, then a
 //            butterfly over lane distance 32, 16, .., 1 --, mean = (float)
 //            (sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm[d]
@@ -72,12 +75,69 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 //            741, 781, 926, 934).
 //   store  : rounded to fp16 (the reference's F16 pool cache).
 template <int D>
+__device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, const uint16_t *m,
+                                               const float *__restrict__ k_norm, float *ys, uint16_t *dst, int t0,
+                                               int lane) {
+#pragma clang fp contract(off)
+    constexpr int K = D / 64, U = 8;
+    float x[K];
+    for (int r0 = 0; r0 < g.bt; r0 += U) {
+        float y[U][K];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = min(r0 + u, g.bt - 1);
+#pragma unroll
+            for (int k = 0; k < K; ++k) y[u][k] = h2f(m[(int64_t)r * D + lane + 64 * k]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+                if (r0 + u < g.bt) x[k] = r0 + u == 0 ? y[u][k] : x[k] + y[u][k];
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        x[k] = x[k] * g.inv_bt;
+        const float sq = x[k] * x[k];
+        ss = ss + (double)sq;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off);
+    const float mean = (float)(ss / (double)D);
+    const float scale = 1.0f / sqrtf(mean + ig.eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int d = lane + 64 * k;
+        ys[d] = (x[k] * scale) * k_norm[d];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    const int half = ig.nd / 2;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int d = lane + 64 * k;
+        float o = ys[d];
+        if (d < ig.nd) {
+            const int i = d < half ? d : d - half;
+            const double th = (double)t0 * ig.invf[i];
+            const float c = (float)cos(th), s = (float)sin(th);
+            const float x0 = ys[i], x1 = ys[i + half];
+            o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
+        }
+        dst[d] = f2h(o);
+    }
+}
+
+// One wave per block, four blocks a workgroup: the blocks of rows (seq_ids[i]
+// or 0, pos[i] / bt) when pos != NULL (a run of rows in one block pools it
+// once, at its last row), else blocks blk0 + [0, n_items) of sequence seq_const.
+template <int D>
 __global__ void __launch_bounds__(256)
 k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
            const float *__restrict__ k_norm, const int32_t *seq_ids, const int32_t *pos, int32_t n_items,
            int32_t seq_const, int32_t blk0) {
-#pragma clang fp contract(off)
-    constexpr int K = D / 64;
     __shared__ float ys[4][D];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int item = blockIdx.x * 4 + w;
@@ -99,47 +159,88 @@ k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, u
     const int t0 = b * g.bt;
     const int32_t pp = phys_page(g, v.page_table, seq, t0);
     if (pp < 0) { if (lane == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
-    const uint16_t *m = raw + ((int64_t)pp * g.pt + t0 % g.pt) * D;
-    float x[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) x[k] = h2f(m[lane + 64 * k]);
-    for (int r = 1; r < g.bt; ++r)
-#pragma unroll
-        for (int k = 0; k < K; ++k) x[k] = x[k] + h2f(m[(int64_t)r * D + lane + 64 * k]);
-    double ss = 0.0;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        x[k] = x[k] * g.inv_bt;
-        const float sq = x[k] * x[k];
-        ss = ss + (double)sq;
+    pool_idx_block<D>(g, ig, raw + ((int64_t)pp * g.pt + t0 % g.pt) * D, k_norm, ys[w],
+                      pooled + ((int64_t)seq * g.bps + b) * D, t0, lane);
+}
+
+// A call of at most kIdxFuseRows rows (a decode step) in one workgroup: the
+// rows are range-checked into LDS; each is written unless a later row has the
+// same (sequence, position) -- the last one is kept --, and after a barrier
+// the last row touching each block pools it from the cache, one wave a block.
+constexpr int kIdxFuseRows = 64;
+constexpr int kIdxFuseThreads = 1024;
+template <int D>
+__global__ void __launch_bounds__(kIdxFuseThreads)
+k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
+                  const float *__restrict__ k_norm, const void *src, int32_t f16, const int32_t *seq_ids,
+                  const int32_t *pos, int32_t n_rows) {
+    constexpr int NW = kIdxFuseThreads / 64, PER = D / 8;
+    __shared__ int32_t s_seq[kIdxFuseRows], s_pos[kIdxFuseRows], s_pp[kIdxFuseRows];
+    __shared__ uint8_t s_write[kIdxFuseRows], s_pool[kIdxFuseRows];
+    __shared__ float ys[NW][D];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (tid < n_rows) {
+        const int seq = seq_ids ? seq_ids[tid] : 0, t = pos[tid];
+        int32_t pp = -1;
+        if (seq < 0 || seq >= g.n_seq_view) set_status(v.status, QWFN_STATUS_SEQ_RANGE);
+        else if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) set_status(v.status, QWFN_STATUS_POS_RANGE);
+        else if ((pp = phys_page(g, v.page_table, seq, t)) < 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+        s_seq[tid] = pp >= 0 ? seq : -1;
+        s_pos[tid] = pp >= 0 ? t : -1;
+        s_pp[tid] = pp;
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off);
-    const float mean = (float)(ss / (double)D);
-    const float scale = 1.0f / sqrtf(mean + ig.eps);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int d = lane + 64 * k;
-        ys[w][d] = (x[k] * scale) * k_norm[d];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    uint16_t *dst = pooled + ((int64_t)seq * g.bps + b) * D;
-    const int half = ig.nd / 2;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int d = lane + 64 * k;
-        float o = ys[w][d];
-        if (d < ig.nd) {
-            const int i = d < half ? d : d - half;
-            const double th = (double)t0 * ig.invf[i];
-            const float c = (float)cos(th), s = (float)sin(th);
-            const float x0 = ys[w][i], x1 = ys[w][i + half];
-            o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
+    __syncthreads();
+    if (tid < n_rows) {
+        const int seq = s_seq[tid], t = s_pos[tid];
+        bool wr = seq >= 0, pl = seq >= 0;
+        for (int r2 = tid + 1; r2 < n_rows; ++r2) {
+            if (seq >= 0 && s_seq[r2] == seq) {
+                wr = wr && s_pos[r2] != t;
+                pl = pl && s_pos[r2] / g.bt != t / g.bt;
+            }
         }
-        dst[d] = f2h(o);
+        s_write[tid] = wr;
+        s_pool[tid] = pl;
     }
+    __syncthreads();
+    for (int i = tid; i < n_rows * PER; i += kIdxFuseThreads) {
+        const int r = i / PER, c = i % PER;
+        if (!s_write[r]) continue;
+        uint4 out;
+        if (f16) {
+            out = reinterpret_cast<const uint4 *>((const uint16_t *)src + (int64_t)r * D)[c];
+        } else {
+            const float4 *s4 = reinterpret_cast<const float4 *>((const float *)src + (int64_t)r * D) + 2 * c;
+            const float4 a = s4[0], b = s4[1];
+            out.x = (uint32_t)f2h(a.x) | (uint32_t)f2h(a.y) << 16;
+            out.y = (uint32_t)f2h(a.z) | (uint32_t)f2h(a.w) << 16;
+            out.z = (uint32_t)f2h(b.x) | (uint32_t)f2h(b.y) << 16;
+            out.w = (uint32_t)f2h(b.z) | (uint32_t)f2h(b.w) << 16;
+        }
+        reinterpret_cast<uint4 *>(raw + ((int64_t)s_pp[r] * g.pt + s_pos[r] % g.pt) * D)[c] = out;
+    }
+    __syncthreads();                               // the rows' stores, for this workgroup's pooling
+    for (int r = w; r < n_rows; r += NW) {
+        if (!s_pool[r]) continue;                  // (uniform over the wave)
+        const int seq = s_seq[r], b = s_pos[r] / g.bt, t0 = b * g.bt;
+        const int32_t pp = phys_page(g, v.page_table, seq, t0);
+        if (pp < 0) { if (lane == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE); continue; }
+        pool_idx_block<D>(g, ig, raw + ((int64_t)pp * g.pt + t0 % g.pt) * D, k_norm, ys[w],
+                          pooled + ((int64_t)seq * g.bps + b) * D, t0, lane);
+    }
+}
+
+hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
+                                  uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
+                                  const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st) {
+    if (n_rows > kIdxFuseRows) return hipErrorInvalidValue;
+    switch (ig.dim) {
+    case 64:  hipLaunchKernelGGL(k_idx_append_pool<64>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, src, src_f16, seq_ids, pos, n_rows); break;
+    case 128: hipLaunchKernelGGL(k_idx_append_pool<128>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, src, src_f16, seq_ids, pos, n_rows); break;
+    case 256: hipLaunchKernelGGL(k_idx_append_pool<256>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, src, src_f16, seq_ids, pos, n_rows); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,

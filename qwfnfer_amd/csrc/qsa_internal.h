@@ -106,6 +106,11 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, const uint16_t *raw,
                            uint16_t *pooled, const float *k_norm, const int32_t *seq_ids, const int32_t *pos,
                            int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st);
+// Write and pool in one launch, for calls of at most 64 rows (a decode step):
+// among rows with the same (sequence, position) the last one is kept.
+hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
+                                  uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
+                                  const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st);
 // seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r;
 // len (decode): row r is sequence r's token at position len[r] - 1.
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,

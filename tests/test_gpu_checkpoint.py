@@ -14,7 +14,7 @@ import torch
 
 from _ckpt import CKPT, ICfg, oracle_pool_all, oracle_select
 from _gpu import assert_close_attn, cfg_of, kv_rows, make_pair, np_of
-from qwfnfer_amd import qsa
+from qwfnfer_amd import _lib, qsa
 
 pytestmark = pytest.mark.gpu
 
@@ -78,6 +78,38 @@ def test_idx_append_pool_matches_oracle(dtype):
     np.testing.assert_array_equal(_raw_rows(dev, ic, 1, 64), r1)
     np.testing.assert_array_equal(np_of(ic.pooled)[1, :16], oracle_pool_all(cfg, ICFG, r1, w, 16))
     assert qsa.read_status(dev) == 0
+
+
+def test_idx_append_pool_decode_call_rows():
+    """A decode-sized call (one launch): rows of two sequences interleaved, a
+    repeated (sequence, position) whose last row is kept, and a row past the
+    view's sequences that only sets the status bit."""
+    cfg = CKPT
+    rng = np.random.default_rng(820)
+    dev, host, ic, w = _pair(cfg, 2, 2, seed=821)
+    L = 37
+    base = rng.standard_normal((2, L, 128)).astype(np.float32)
+    for s in range(2):
+        qsa.idx_append_pool(ic, torch.from_numpy(base[s]).cuda(), torch.arange(L, dtype=torch.int32, device="cuda"),
+                            seq_ids=torch.full((L,), s, dtype=torch.int32, device="cuda"))
+    seqs = np.array([0, 1, 0, 1, 0, 7], np.int32)
+    pos = np.array([37, 37, 38, 12, 37, 3], np.int32)
+    x = rng.standard_normal((6, 128)).astype(np.float32)
+    qsa.idx_append_pool(ic, torch.from_numpy(x).cuda(), torch.from_numpy(pos).cuda(),
+                        seq_ids=torch.from_numpy(seqs).cuda())
+    torch.cuda.synchronize()
+    assert qsa.read_status(dev) == _lib.STATUS_SEQ_RANGE
+    rows = [np.concatenate([base[0], np.zeros((2, 128), np.float32)]).astype(np.float16),
+            np.concatenate([base[1], np.zeros((2, 128), np.float32)]).astype(np.float16)]
+    rows[0][37] = x[4].astype(np.float16)              # the later of the two rows at (0, 37)
+    rows[0][38] = x[2].astype(np.float16)
+    rows[1][37] = x[1].astype(np.float16)
+    rows[1][12] = x[3].astype(np.float16)
+    for s in range(2):
+        np.testing.assert_array_equal(_raw_rows(dev, ic, s, 39), rows[s], err_msg=f"seq {s}")
+        nb = 10                                        # blocks 0 .. 9 hold positions 0 .. 39
+        np.testing.assert_array_equal(np_of(ic.pooled)[s, :nb], oracle_pool_all(cfg, ICFG, rows[s], w, nb),
+                                      err_msg=f"seq {s}")
 
 
 def test_idx_rebuild_matches_oracle():
