@@ -474,10 +474,7 @@ int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_se
     if (rc) return rc;
     if (!bytes || max_seq_len < 1 || q_batch < 1)
         return fail(QWFN_EINVAL, "prefill_workspace_bytes: bytes NULL or max_seq_len / q_batch < 1");
-    // the general attention kernel merges partials through per-pair counters;
-    // the matrix-core prefill kernels use none (a batch is one grid dimension)
-    if (!g.vdim && (int64_t)q_batch * shape->n_head_kv > kMaxCounters)
-        return fail(QWFN_ERANGE, "q_batch * n_head_kv exceeds %d", kMaxCounters);
+    // no completion counters: a batch is one grid dimension of every launch
     if (q_batch > kPrefillBatchMax) return fail(QWFN_ERANGE, "q_batch %d exceeds %d", q_batch, kPrefillBatchMax);
     *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len), !g.vdim, false).total;
     return ok();
@@ -526,7 +523,7 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
     // the largest query batch whose workspace fits
     if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "prefill: workspace NULL or not 256-byte aligned");
     const bool parts = !g.vdim;                    // the general kernel merges partials in memory
-    int32_t batch = std::min<int64_t>(n_q, g.vdim ? kPrefillBatchMax : kMaxCounters / shape->n_head_kv);
+    int32_t batch = std::min<int32_t>(n_q, kPrefillBatchMax);
     while (batch > 1 && ws_layout(g, batch, max_len, need, parts, false).total > ws_bytes) batch = (batch + 1) / 2;
     if (ws_layout(g, batch, max_len, need, parts, false).total > ws_bytes)
         return fail(QWFN_ERANGE, "prefill: workspace of %zu bytes holds no query batch (need %zu)", ws_bytes,
