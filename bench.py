@@ -6,10 +6,14 @@ heads, head_dim 128), q8_0 K/V ~ N(0,1) with a log-uniform [0.1, 10] scale per
 q8_0 block, 64-token pooled blocks, top-64 blocks + block 0 + the last 512
 tokens, one decode token per step at contexts 4096, 65536 and 163840.
 
-A step = one decode token through all 12 layers; each layer is the fused path
-of graph_builder::sparse_attn_decode: append the token's K/V (q8_0), pool the
-block it completes, score the pooled blocks, select, attend (two kernels:
-append+select, attention).  The decode position advances one token per step
+A step = one decode token through all 12 layers; each layer is one
+qwfn_sparse_attn_decode call, the fused path of graph_builder::sparse_attn_decode:
+append the token's K/V (q8_0), pool the block it completes, score the pooled
+blocks, select, attend.  At one sequence that is three launches: the indexer
+(append, pooling, scores), the attention (each workgroup selects from the
+scores, then attends over its tiles) and the partials' merge.  --two-call steps
+through qwfn_decode_append_select + qwfn_sparse_decode_attn instead (the last
+indexer workgroup selects).  The decode position advances one token per step
 (seq_len += 1 on the device at the start of every step, one small kernel), so
 one step in 64 completes a block and pools it, as in a real decode; every
 replica keeps its own position and its caches have room for DECODE_ROOM more
@@ -52,6 +56,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only")
+    ap.add_argument("--two-call", action="store_true",
+                    help="step each layer through qwfn_decode_append_select + qwfn_sparse_decode_attn "
+                         "instead of one qwfn_sparse_attn_decode")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
     ap.add_argument("--no-kv-types", action="store_true",
@@ -105,8 +112,9 @@ class Runner:
     """n_inst replicas of an n_layer stack of caches at fixed sequence lengths,
     stepped by the fused decode (append+select, attention per layer)."""
 
-    def __init__(self, qsa, torch, cfg, lengths, n_layer, pages_per_seq, page_table, gen):
+    def __init__(self, qsa, torch, cfg, lengths, n_layer, pages_per_seq, page_table, gen, fused=False):
         self.qsa, self.torch, self.cfg = qsa, torch, cfg
+        self.fused = fused
         self.lengths = lengths
         n_seq = len(lengths)
         self.n_seq = n_seq
@@ -149,6 +157,10 @@ class Runner:
         qsa = self.qsa
         c = self.stacks[inst][il]
         sl = self.seq_lens[inst]
+        if self.fused:                                  # qwfn_sparse_attn_decode: one call
+            qsa.sparse_attn_decode(c, self.q[il], self.kn[il], self.vn[il], sl, self.max_len, self.ws,
+                                   out=self.out[il], sel=self.sel, n_sel=self.nsel)
+            return
         qsa.decode_append_select(c, self.q[il], self.kn[il], self.vn[il], sl, self.max_len, self.ws,
                                  self.sel, self.nsel)
         qsa.sparse_decode_attn(c, self.q[il], sl, self.max_len, self.ws, self.sel, self.nsel, out=self.out[il])
@@ -221,10 +233,12 @@ class Runner:
         return e0.elapsed_time(e1) / steps            # ms per step
 
     def time_kernels(self, steps, per_graph=16):
-        """Average device time per launch of the append+select kernel and of
-        the attention kernel: each is captured `per_graph` times back to back
-        (layer 0 of every replica in turn, after a step has set the
-        selection; both kernels are idempotent at a fixed position), and the
+        """Average device time per call of the two-call path's pieces:
+        qwfn_decode_append_select (append, pooling, scores, the selection by
+        the indexer's last workgroup) and qwfn_sparse_decode_attn (attention
+        over that selection, then the merge).  Each is captured `per_graph`
+        times back to back (layer 0 of every replica in turn, after a step has
+        set the selection; both are idempotent at a fixed position), and the
         replays are timed with HIP events on the capturing stream."""
         torch, qsa = self.torch, self.qsa
         self.step(0)
@@ -516,7 +530,7 @@ def main():
     for ctx in contexts:
         pps = (ctx + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
-        r = Runner(qsa, torch, cfg, [ctx], args.layers, pps, pt, gen)
+        r = Runner(qsa, torch, cfg, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
         eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
         graph_ms = None
         if not args.no_graph:
@@ -549,7 +563,7 @@ def main():
         lens = [int(math.exp(rng.uniform(math.log(4096), math.log(262144)))) for _ in range(8)]
         pps = (max(lens) + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         perm = torch.from_numpy(rng.permutation(8 * pps).astype(np.int32)).view(8, pps)
-        r = Runner(qsa, torch, cfg, lens, 1, pps, perm, gen)
+        r = Runner(qsa, torch, cfg, lens, 1, pps, perm, gen, fused=not args.two_call)
         ms = r.time_steps(args.steps, args.warmup, graph=False)
         sel_us, att_us = r.time_kernels(max(64, args.steps))
         r.check_room()
@@ -578,7 +592,7 @@ def main():
             c2 = dataclasses.replace(cfg, kv_type=kt)
             pps = (ctx + DECODE_ROOM + c2.page_tokens - 1) // c2.page_tokens
             pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
-            r = Runner(qsa, torch, c2, [ctx], args.layers, pps, pt, gen)
+            r = Runner(qsa, torch, c2, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
             r.capture()
             ms = r.time_steps(max(30, args.steps // 3), args.warmup, graph=True)
             sel_us, att_us = r.time_kernels(64)
@@ -644,6 +658,8 @@ def main():
                         f"top-64 64-token blocks + block 0 + 512-token window, 1 decode token/step",
             "contexts": contexts,
             "launch": "hipGraph" if top["graph_us_per_layer"] is not None else "eager",
+            "decode_call": "qwfn_decode_append_select + qwfn_sparse_decode_attn" if args.two_call
+                           else "qwfn_sparse_attn_decode (fused: the attention selects)",
         },
         "us_per_layer": {str(c): round(v["us_per_layer"], 3) for c, v in per_ctx.items()},
         "flatness": round(top["us_per_layer"] / per_ctx[small]["us_per_layer"], 4),
@@ -651,8 +667,9 @@ def main():
                         for c, v in per_ctx.items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": "sparse decode attention call: k_attn_q8 (selected q8_0 K+V, split into partials), "
-                      "then k_merge (one workgroup per query head combines them)",
+            "kernel": "sparse decode attention call over a given selection (qwfn_sparse_decode_attn): "
+                      "k_attn_q8 (selected q8_0 K+V, split into partials), then k_merge (one workgroup per "
+                      "query head combines them)",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -461,9 +461,12 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
     int32_t *nsel = n_sel_out ? n_sel_out : w.nsel;
     const FusedAppend fa{k_new, v_new, src_dtype == QWFN_SRC_F16, 1};
     hipStream_t st = (hipStream_t)stream;
-    hipError_t e = launch_indexer(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, w, fa, st);
+    // one or a few sequences: the attention workgroups select for themselves
+    const bool own = attn_select_fits(g, n_seq, max_seq_len, msel);
+    hipError_t e = launch_indexer(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, w, fa, st, !own);
     if (e != hipSuccess) return hip_fail(e, "decode: indexer");
-    e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st);
+    e = own ? launch_attention_select(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st)
+            : launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st);
     return e == hipSuccess ? ok() : hip_fail(e, "decode: attention");
 }
 

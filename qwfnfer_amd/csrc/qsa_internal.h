@@ -122,10 +122,11 @@ hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, con
 hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
                        int32_t blk0, hipStream_t st, const int32_t *len = nullptr);
+// select = false: scores only (the attention selects, launch_attention_select)
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                          const FusedAppend &fa, hipStream_t st);
+                          const FusedAppend &fa, hipStream_t st, bool select = true);
 // Prefill: scores of n_q queries (Geo::pf) into ws.scores, then each query's
 // selection into sel / nsel.
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
@@ -136,6 +137,14 @@ hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float
 hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                                     const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
                                     hipStream_t st);
+// Decode attention that makes its own selection from the scores of a
+// scores-only indexer launch, writing it to sel / nsel (matrix-core shapes,
+// per-head selections of at most 8192 eligible blocks, fewer than four
+// sequences, max_sel <= 1024: attn_select_fits).
+bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel);
+hipError_t launch_attention_select(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                                   int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel,
+                                   int32_t max_sel, float *out, const Ws &ws, hipStream_t st);
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,

@@ -1280,8 +1280,10 @@ __device__ __forceinline__ void select_radix(const Geo &g, const float *sc, cons
     }
 }
 
-// Eligible blocks the register path of an NT-thread selection holds.
-template <int NT> constexpr int keys_max() { return NT == kIdxThreads ? kKeysMax : 64 * NT; }
+// Eligible blocks the register path of an NT-thread selection holds (256
+// threads: 32 keys a thread; 512, the attention's in-kernel selection: 16),
+// or, at 1024 threads, the streaming path.
+template <int NT> constexpr int keys_max() { return NT == kIdxThreads ? kKeysMax : NT == 512 ? 16 * NT : 64 * NT; }
 
 // The forced blocks around a selection of topk eligible blocks: the sink
 // blocks first, the window blocks after the topk, and the count.
@@ -1316,6 +1318,11 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
             else if (span <= 16 * NT) done = select_regs<NT, 16, true>(g, sc, r, topk, out, sh);
             else if (span <= 24 * NT) done = select_regs<NT, 24, true>(g, sc, r, topk, out, sh);
             else if (span <= keys_max<NT>()) done = select_regs<NT, keys_max<NT>() / NT, true>(g, sc, r, topk, out, sh);
+        } else if constexpr (NT == 512) {
+            if (span <= 4 * NT) done = select_regs<NT, 4, true>(g, sc, r, topk, out, sh);
+            else if (span <= 8 * NT) done = select_regs<NT, 8, true>(g, sc, r, topk, out, sh);
+            else if (span <= 12 * NT) done = select_regs<NT, 12, true>(g, sc, r, topk, out, sh);
+            else if (span <= keys_max<NT>()) done = select_regs<NT, 16, true>(g, sc, r, topk, out, sh);
         } else {
             if (span <= keys_max<NT>()) {
                 done = select_sample<NT>(g, sc, r, topk, out, sh);
@@ -1388,6 +1395,23 @@ struct BigSelShared {
     float red[2 * (kBigSelThreads / 64)];
     int tmp[kBigSelThreads / 64];
     int bin, need, ncand, cnt_b;
+};
+
+// LDS of the attention's in-kernel selection (k_attn_q8<..., SEL>): the
+// register path's state at NT threads, and the selection itself.
+constexpr int kAttnSelMax = 1024;                 // selected blocks it holds
+template <int NT>
+struct AttnSelShared {
+    uint32_t hist[4096 + 64];
+    uint32_t cand_key[kCandMax + 1];
+    int32_t cand_b[kCandMax + 1];
+    uint32_t tmask[NT];
+    uint32_t selbits[keys_max<NT>() / 32 + 1];
+    float red[2 * (NT / 64)];
+    int tmp[NT / 64];
+    int bin, need, ncand, cnt_b;
+    int32_t sel[kAttnSelMax];
+    int32_t nsel;
 };
 
 // grid (shared ? 1 : Hkv, n_seq or n_q)
@@ -1624,7 +1648,7 @@ template <int HD, int G>
 static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                              int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                             FusedAppend fa, hipStream_t st) {
+                             FusedAppend fa, hipStream_t st, bool select) {
     // The append workgroup is q8_0's, and its pooled block must not be one the
     // scoring workgroups read: with local_tokens = 0 a just-completed block is
     // eligible.  Otherwise the append and the pooling run as launches of their own.
@@ -1640,7 +1664,8 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
-                       sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)!big);
+                       sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big));
+    if (!select) return;                           // the attention selects (k_attn_q8<..., SEL>)
     if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
         hipLaunchKernelGGL(k_select_cut, dim3((unsigned)ws.cut_wg, (unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws, sel, nsel, max_sel);
@@ -2162,8 +2187,34 @@ struct FastShared {
     float qs[G];                               // q ~= qs * (qa + qb/254 + qc/254^2)
 };
 
-// DENSE: attend every block of the sequence (sel is not read).
-template <int HD, int G, int TG, bool DENSE>
+// The attention's own selection (SEL): every workgroup runs the decode
+// selection of its (sequence, KV head) on the indexer's score row into LDS,
+// with all of its threads, and takes its tiles' blocks from there; part 0 also
+// writes the selection and its count out (for the caller and the merge).  The
+// indexer launch before it only scores, so the decode step waits for no
+// completion counter and no single selecting workgroup.
+struct NoShared {};
+template <int NT, typename SH>
+__device__ __forceinline__ void attn_select(const Geo &g, const Ws &ws, int L, int max_seq_len, int max_sel,
+                                            int pair, int part, int32_t *gsel, int32_t *gnsel, SH &ssh) {
+    const int tid = threadIdx.x;
+    if (L >= 1 && L <= max_seq_len) {
+        const SelOut lo{ssh.sel, &ssh.nsel, 0, 1};
+        select_blocks<NT>(g, ws.scores + (int64_t)pair * ws.nb_cap, L, lo, ssh);
+    } else if (tid == 0) {
+        ssh.nsel = 0;
+    }
+    __syncthreads();
+    if (part == 0) {
+        const int n = min(ssh.nsel, max_sel);
+        for (int i = tid; i < n; i += NT) gsel[(int64_t)pair * max_sel + i] = ssh.sel[i];
+        if (tid == 0) gnsel[pair] = n;
+    }
+}
+
+// DENSE: attend every block of the sequence (sel is not read).  SEL: select
+// in the kernel (above); sel / nsel are then outputs.
+template <int HD, int G, int TG, bool DENSE, bool SEL = false>
 __global__ void __launch_bounds__((FastCfg<HD, G, TG>::NT))
 k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len,
           int32_t max_seq_len, const int32_t *__restrict__ sel, const int32_t *__restrict__ nsel, int32_t max_sel,
@@ -2171,7 +2222,9 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
     using C = FastCfg<HD, G, TG>;
     constexpr int NB = C::NB;
     static_assert(G <= 16, "one matrix-core column per query head");
+    static_assert(!(SEL && DENSE), "a dense call has no selection");
     __shared__ FastShared<HD, G, TG> sh;
+    __shared__ typename std::conditional<SEL, AttnSelShared<C::NT>, NoShared>::type ssh;
     const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);
     const int lt = tid % C::NTG;
@@ -2188,8 +2241,16 @@ k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__r
     // used: no branch may sit between them (a branch makes the compiler wait
     // for every load in flight).
     const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
-    const int n_raw = DENSE ? 0 : nsel[pair];
-    const int blk_raw = DENSE ? 0 : sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
+    int n_raw, blk_raw;
+    if constexpr (SEL) {
+        attn_select<C::NT>(g, ws, L, max_seq_len, max_sel, pair, part, const_cast<int32_t *>(sel),
+                           const_cast<int32_t *>(nsel), ssh);
+        n_raw = ssh.nsel;
+        blk_raw = ssh.sel[min(tile / tpb, kAttnSelMax - 1)];
+    } else {
+        n_raw = DENSE ? 0 : nsel[pair];
+        blk_raw = DENSE ? 0 : sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
+    }
     constexpr int DPL = HD / 64, NWV = C::NT / 64, QPW = (G + NWV - 1) / NWV;
     float xq[QPW][DPL];
     {
@@ -2776,10 +2837,10 @@ hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_i
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                          const FusedAppend &fa, hipStream_t st) {
+                          const FusedAppend &fa, hipStream_t st, bool select) {
 #define X(HD_, G_, TG_)                                                                          \
     if (g.hd == HD_ && g.G == G_) {                                                              \
-        launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st); \
+        launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st, select); \
         return hipGetLastError();                                                                \
     }
     QWFN_FOR_EACH_SHAPE(X)
@@ -3203,6 +3264,33 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
     }
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
+    return hipErrorInvalidValue;
+}
+
+bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
+    if (!g.vdim || g.shared || g.topk <= 0 || g.pf || n_seq >= kFastBatchSeqs || max_sel > kAttnSelMax ||
+        max_seq_len / g.bt > kKeysMax)
+        return false;
+#define F(HD_, G_, TG_) if (g.hd == HD_ && g.G == G_) return true;
+    QWFN_FOR_EACH_FAST(F)
+#undef F
+    return false;
+}
+
+hipError_t launch_attention_select(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                                   int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel,
+                                   int32_t max_sel, float *out, const Ws &ws, hipStream_t st) {
+    if (!attn_select_fits(g, n_seq, max_seq_len, max_sel)) return hipErrorInvalidValue;
+#define F(HD_, G_, TG_)                                                                                          \
+    if (g.hd == HD_ && g.G == G_) {                                                                              \
+        const dim3 grid((unsigned)((ws.n_tiles + TG_ - 1) / TG_), (unsigned)g.Hkv, (unsigned)n_seq);            \
+        hipLaunchKernelGGL((k_attn_q8<HD_, G_, TG_, false, true>), grid, dim3(FastCfg<HD_, G_, TG_>::NT), 0, st, \
+                           g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, out, ws);                          \
+        launch_merge_t<G_, HD_>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG_, st);      \
+        return hipGetLastError();                                                                                \
+    }
+    QWFN_FOR_EACH_FAST(F)
+#undef F
     return hipErrorInvalidValue;
 }
 

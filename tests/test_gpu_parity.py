@@ -274,14 +274,18 @@ def test_dense_attention_matches_f64(L):
     assert_close_attn(np_of(out), host.attention_f64(q, [L]), "dense attention")
 
 
-def _decode_steps(cfg, lengths, steps, seed, dtype=np.float32):
+def _decode_steps(cfg, lengths, steps, seed, dtype=np.float32, zero_pooled=False):
     """Fused decode steps on a batch of sequences vs the oracle's append + pool on
-    completion + indexer + fp64 attention."""
+    completion + indexer + fp64 attention.  zero_pooled: every pooled key of the
+    filled prefix set to 0 on both sides (all scores tie)."""
     rng = np.random.default_rng(seed)
     n_seq = len(lengths)
     pps = (max(lengths) + steps) // cfg.page_tokens + 1
     dev, host = make_pair(cfg, n_seq, pps, seed=seed)
     fill(dev, host, rng, lengths)
+    if zero_pooled:
+        host.pooled[...] = 0
+        dev.pooled.zero_()
     cur = np.array(lengths, np.int32)
     max_len = int(cur.max()) + steps
     ws = qsa.Workspace(cfg_of(cfg), n_seq, max_len)
@@ -343,6 +347,24 @@ def test_decode_steps_shared_selection(relu):
 def test_decode_steps_tiny_and_checkpoint_shapes():
     _decode_steps(TINY, [61, 130], steps=10, seed=320)
     _decode_steps(G12, [250], steps=6, seed=321)
+
+
+# One to three sequences of a matrix-core shape: the attention workgroups make
+# the selection themselves from a scores-only indexer launch (and write it out).
+@pytest.mark.parametrize("cfg", [
+    BASELINE,
+    Cfg(n_head=8, n_head_kv=2),                                     # group 4
+    Cfg(n_head=4, n_head_kv=2),                                     # group 2
+    Cfg(n_head=16, n_head_kv=2, head_dim=64),                       # 256-thread workgroups
+    Cfg(n_head=24, n_head_kv=2, head_dim=256),                      # group 12, head_dim 256
+])
+def test_decode_steps_attention_selects(cfg):
+    _decode_steps(cfg, [3000, 64 * 70 + 5, 100], steps=3, seed=350)
+
+
+def test_decode_steps_attention_selects_ties():
+    # every pooled key 0: ties everywhere, the radix path of the in-kernel selection
+    _decode_steps(BASELINE, [20000], steps=2, seed=355, zero_pooled=True)
 
 
 def test_decode_is_deterministic():
