@@ -272,8 +272,12 @@ int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *v
  * 450-546) from the K/V projections on: append k_new/v_new
  * ([n_seq][n_head_kv][head_dim], src_dtype) at position seq_len-1, re-pool the
  * block that position completes, score + select, and attend.  sel_out/n_sel_out
- * (optional) receive the selection as qwfn_indexer_topk would.  Two launches:
- * qwfn_decode_append_select, then qwfn_sparse_decode_attn's kernel.           */
+ * (optional) receive the selection as qwfn_indexer_topk would.  Three
+ * launches: the indexer, the attention and the merge of its partials.  Up to
+ * eight sequences of a matrix-core shape (block_tokens % 64 == 0, q8_0) with
+ * per-head selections of at most 8192 eligible blocks, the indexer only
+ * scores and the attention's workgroups select for themselves; otherwise the
+ * launches are qwfn_decode_append_select's and qwfn_sparse_decode_attn's.     */
 int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                             const float *q, const void *k_new, const void *v_new,
                             int32_t src_dtype, const int32_t *seq_len,
@@ -306,8 +310,9 @@ int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_se
  *  - sel_out [n_q][n_head_kv][max_sel] / n_sel_out [n_q][n_head_kv] (optional)
  *    receive each query's selection.
  * The queries are processed in batches sized to ws_bytes (see
- * qwfn_qsa_prefill_workspace_bytes), each batch an indexer launch and an
- * attention launch on `stream`. */
+ * qwfn_qsa_prefill_workspace_bytes), each batch a scoring, a selection and
+ * an attention launch (and the merge of its partials for the general
+ * attention kernel) on `stream`. */
 int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                              const float *q, const void *k_new, const void *v_new,
                              int32_t src_dtype, int32_t seq, int32_t pos0, int32_t n_q,
