@@ -60,6 +60,8 @@ def parse():
                     help="step each layer through qwfn_decode_append_select + qwfn_sparse_decode_attn "
                          "instead of one qwfn_sparse_attn_decode")
     ap.add_argument("--no-batched", action="store_true", help="skip the config-5 batched line")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the config-1 (dense, ctx 4096) and config-2 (sparse, ctx 32768) lines")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
     ap.add_argument("--no-kv-types", action="store_true",
                     help="skip the q4_0 / fp16 cache lines (config 3 at the longest context)")
@@ -556,6 +558,33 @@ def main():
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
 
+    # configs 1 and 2: the same decode step (one call a layer, 12 layers a step)
+    extra = None
+    if not args.no_extra:
+        extra = {}
+        for name, c, ctx in (("config1_dense", qsa.QsaConfig(top_k_blocks=0), 4096), ("config2", cfg, 32768)):
+            pps = (ctx + DECODE_ROOM + c.page_tokens - 1) // c.page_tokens
+            pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+            r = Runner(qsa, torch, c, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
+            eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
+            graph_ms = None
+            if not args.no_graph:
+                r.capture()
+                graph_ms = r.time_steps(args.steps, args.warmup, graph=True)
+            r.check_room()
+            kv, _, cells = r.bytes_per_layer()
+            ms = graph_ms if graph_ms is not None else eager_ms
+            us = ms * 1e3 / args.layers
+            extra[name] = dict(context=ctx, us_per_layer=round(us, 3),
+                               eager_us_per_layer=round(eager_ms * 1e3 / args.layers, 3),
+                               cells_per_layer=cells, selected_kv_bytes=kv,
+                               layer_gbs_selected=round(kv / (us * 1e-6) / 1e9, 1))
+            log(f"[bench] {name} ctx {ctx}: {us:.2f} us/layer (eager {eager_ms * 1e3 / args.layers:.2f}), "
+                f"{cells} cells, {kv} B of K/V")
+            del r
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+
     batched = None
     if not args.no_batched:
         import numpy as np
@@ -679,6 +708,7 @@ def main():
             "launch_us": round(top["attn_kernel_us"], 3),
         },
         "layer_roofline_frac": round(top["layer_gbs_selected"] / HBM_PEAK_GBS, 4),
+        "configs_1_2": extra,
         "batched_config5": batched,
         "prefill_config4": prefill,
         "checkpoint_decode": checkpoint,
