@@ -3257,6 +3257,13 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
         QWFN_FOR_EACH_FAST(F)
 #undef F
     }
+    // Prefill at head_dim 256: one tile group a workgroup, so two fit a CU's
+    // LDS and one's round trips hide behind the other's work (the batch fills
+    // the chip many times over; one decode sequence wants two groups instead).
+    if (g.pf && g.hd == 256) {
+        if (g.G == 12) { launch_attn_t<256, 12, 1>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); return hipGetLastError(); }
+        if (g.G == 8) { launch_attn_t<256, 8, 1>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); return hipGetLastError(); }
+    }
 #define X(HD_, G_, TG_)                                                                         \
     if (g.hd == HD_ && g.G == G_) {                                                             \
         launch_attn_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
