@@ -357,6 +357,48 @@ def bench_prefill(qsa, torch, cfg, gen, q_batch, reps=3):
                 "fp32 operands as fp16 hi + lo pairs); frac is against the dense fp16/bf16 MFMA peak")
 
 
+def bench_checkpoint_prefill(qsa, torch, gen, reps=3):
+    """The checkpoint layer's prefill chunk at config 4's place: 8192 tokens
+    (K/V rows and raw indexer keys) appended at 155648 into a cache and
+    indexer cache holding [0, 155648), the blocks they touch pooled, and 8192
+    queries selected by their own indexer queries and attending causally --
+    one qwfn_idx_sparse_attn_prefill call with a workspace for the whole chunk,
+    timed with HIP events after one untimed call (an idempotent overwrite)."""
+    cfg, icfg = qsa.checkpoint_config(), qsa.IdxConfig()
+    end = PREFILL_POS0 + PREFILL_N
+    pps = (end + cfg.page_tokens - 1) // cfg.page_tokens
+    pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+    cache = qsa.KvCache.allocate(cfg, 1, pps, page_table=pt, n_phys_pages=pps)
+    fill_layer(qsa, torch, cache, [PREFILL_POS0], gen, pool=False)
+    ic = qsa.IdxCache.allocate(icfg, cache, torch.rand(icfg.idx_dim, device="cuda", generator=gen) + 0.5)
+    for t0 in range(0, PREFILL_POS0, 32768):
+        n = min(32768, PREFILL_POS0 - t0)
+        kr = torch.randn((n, icfg.idx_dim), device="cuda", generator=gen)
+        qsa.idx_append_pool(ic, kr, torch.arange(t0, t0 + n, dtype=torch.int32, device="cuda"))
+    r = lambda *shape: torch.randn(shape, device="cuda", generator=gen)
+    q, qi = r(PREFILL_N, cfg.n_head, cfg.head_dim), r(PREFILL_N, icfg.n_idx_head, icfg.idx_dim)
+    kn, vn = r(PREFILL_N, cfg.n_head_kv, cfg.head_dim).half(), r(PREFILL_N, cfg.n_head_kv, cfg.head_dim).half()
+    kr = r(PREFILL_N, icfg.idx_dim).half()
+    ws = qsa.Workspace.for_prefill(cfg, end, PREFILL_N)
+    out = torch.empty((PREFILL_N, cfg.n_head, cfg.head_dim), device="cuda")
+    run = lambda: qsa.idx_sparse_attn_prefill(ic, q, qi, 0, PREFILL_POS0, ws, k_new=kn, v_new=vn, k_raw=kr, out=out)
+    run()
+    torch.cuda.synchronize()
+    if qsa.read_status(cache):
+        raise RuntimeError("checkpoint prefill reported out-of-range rows")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del cache, ic, ws, out
+    torch.cuda.empty_cache()
+    return dict(queries=PREFILL_N, pos0=PREFILL_POS0, ms_per_chunk=round(ms, 3),
+                us_per_query=round(ms * 1e3 / PREFILL_N, 3))
+
+
 class CheckpointRunner:
     """The released checkpoint's attention layer (24 query heads, 2 KV heads of
     256, q8_0 KV, blocks of 4 tokens pooled by its own indexer of 4 heads x 128,
@@ -649,7 +691,11 @@ def main():
             torch.cuda.empty_cache()
         checkpoint = dict(per_context=ck, workload="the released checkpoint's attention layer: 24q/2kv heads "
                           "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
-                          "keys), 513 kept blocks shared by both KV heads; 5 launches per layer, hipGraph")
+                          "keys), 513 kept blocks shared by both KV heads; 6 launches per layer, hipGraph")
+        if not args.no_prefill:
+            checkpoint["prefill"] = bench_checkpoint_prefill(qsa, torch, gen)
+            log(f"[bench] checkpoint prefill chunk ({PREFILL_N} queries at {PREFILL_POS0}): "
+                f"{checkpoint['prefill']['ms_per_chunk']:.3f} ms")
 
     big = max(contexts)
     small = min(contexts)
