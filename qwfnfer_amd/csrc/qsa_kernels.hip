@@ -2800,8 +2800,12 @@ static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *
 // dispatch over the instantiated (head_dim, group) pairs
 // ---------------------------------------------------------------------------
 
-// (head_dim, group, tile groups per attention workgroup)
-#define QWFN_FOR_EACH_SHAPE(X) X(128, 8, 3) X(128, 4, 3) X(128, 2, 3) X(64, 8, 4) X(256, 12, 2) X(256, 8, 2)
+// (head_dim, group, tile groups per general attention workgroup).  One group:
+// the partials go to k_merge, so more groups per workgroup only add an LDS
+// merge, and a smaller workgroup lets two or more share a CU's LDS (measured:
+// checkpoint layer 49.6 -> 45.8 us, q4_0 / F16 layers 32.5 -> 30 us, checkpoint
+// prefill chunk of 2048 queries 6.13 -> 5.25 ms, against 2-3 groups).
+#define QWFN_FOR_EACH_SHAPE(X) X(128, 8, 1) X(128, 4, 1) X(128, 2, 1) X(64, 8, 1) X(256, 12, 1) X(256, 8, 1)
 
 bool kernels_for(int32_t hd, int32_t G) {
 #define X(HD_, G_, TG_) if (hd == HD_ && G == G_) return true;
@@ -3256,13 +3260,6 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
         if (n_seq >= kFastBatchSeqs) { QWFN_FOR_EACH_FAST_BATCH(F) }
         QWFN_FOR_EACH_FAST(F)
 #undef F
-    }
-    // Prefill at head_dim 256: one tile group a workgroup, so two fit a CU's
-    // LDS and one's round trips hide behind the other's work (the batch fills
-    // the chip many times over; one decode sequence wants two groups instead).
-    if (g.pf && g.hd == 256) {
-        if (g.G == 12) { launch_attn_t<256, 12, 1>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); return hipGetLastError(); }
-        if (g.G == 8) { launch_attn_t<256, 8, 1>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); return hipGetLastError(); }
     }
 #define X(HD_, G_, TG_)                                                                         \
     if (g.hd == HD_ && g.G == G_) {                                                             \
