@@ -565,16 +565,28 @@ struct IdxShared {
 // Append of the decode token (K and V rows of KV head gh) and, when it
 // completes its block, the block's pooled key -- the decode writes of
 // src/qwfn_graph.cpp:465-476, 520-528 as one workgroup.  The new K row is
-// kept dequantized in LDS as the block's last member.
-template <int HD>
+// kept dequantized in LDS as the block's last member.  KT: the cache type;
+// lane (which, j, e4) holds the 4 values k_append's lane holds (q4_0: dims
+// 2e4, 2e4+1, 16+2e4, 17+2e4 of block j; otherwise 4e4 .. 4e4+3).
+template <int HD, int KT>
 __device__ __forceinline__ void fused_append_pool(const Geo &g, const qwfn_kv_view &v, const FusedAppend &fa,
                                   int s, int gh, const int32_t *seq_len, int32_t max_seq_len, IdxShared &sh) {
     const int tid = threadIdx.x, per = (HD / 32) * 8;   // lanes per row
     const int which = tid / per, j = (tid % per) / 8, e4 = tid % 8;
     // the new rows do not depend on the length: their loads go out first
     float x[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dq[4];
-    if (tid < 2 * per)
-        load4(which ? fa.v_new : fa.k_new, fa.src_f16, ((int64_t)s * g.Hkv + gh) * HD + 32 * j + 4 * e4, x);
+    const void *src = which ? fa.v_new : fa.k_new;
+    const int64_t base = ((int64_t)s * g.Hkv + gh) * HD + 32 * j;
+    if (tid < 2 * per) {
+        if (KT == QWFN_KV_Q4_0) {
+            float a[2], b[2];
+            load2(src, fa.src_f16, base + 2 * e4, a);
+            load2(src, fa.src_f16, base + 16 + 2 * e4, b);
+            x[0] = a[0]; x[1] = a[1]; x[2] = b[0]; x[3] = b[1];
+        } else {
+            load4(src, fa.src_f16, base + 4 * e4, x);
+        }
+    }
     const int L = seq_len[s];
     if (L < 1 || L > max_seq_len) return;
     const int p = L - 1;
@@ -583,17 +595,47 @@ __device__ __forceinline__ void fused_append_pool(const Geo &g, const qwfn_kv_vi
     const int row = p % g.pt;
     // a completed block's older members go to LDS while the new row is quantized
     const bool complete = L % g.bt == 0;
-    const bool early = complete && g.bt > 1 && g.bt - 1 <= kStageRows;
+    const bool early = complete && g.bt > 1 && g.bt - 1 <= stage_max_t<HD, KT>();
     const uint8_t *kpage = (const uint8_t *)v.k_pages + (int64_t)pp * g.page_bytes;
-    if (early) stage_rows<HD>(g, kpage, gh, row - (g.bt - 1), g.bt - 1, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
-    uint16_t dh;
-    const uint32_t pk = quant4(x, g.variant, &dh, dq);   // all lanes: DPP needs full groups
-    if (tid < 2 * per) {
-        uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
-        store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
-        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
-        if (which == 0)
-            for (int k = 0; k < 4; ++k) sh.newk[32 * j + 4 * e4 + k] = dq[k];
+    if (early)
+        stage_rows<HD, KT>(g, kpage, gh, row - (g.bt - 1), g.bt - 1, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
+    uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
+    if (KT == QWFN_KV_Q4_0) {
+        uint16_t dh;
+        const uint32_t qs = quant_q4(x, e4, &dh);     // all lanes: the shuffles need full groups
+        const float d = h2f(dh);
+        dq[0] = d * (float)((int)(qs & 15) - 8);
+        dq[2] = d * (float)((int)((qs >> 4) & 15) - 8);
+        dq[1] = d * (float)((int)((qs >> 8) & 15) - 8);
+        dq[3] = d * (float)((int)((qs >> 12) & 15) - 8);
+        if (tid < 2 * per) {
+            *reinterpret_cast<uint16_t *>(page + chunk_off(g, gh, row, j) + 2 * e4) = (uint16_t)qs;
+            if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+            if (which == 0) {
+                const int d0 = 32 * j + 2 * e4;
+                sh.newk[d0] = dq[0]; sh.newk[d0 + 1] = dq[1]; sh.newk[d0 + 16] = dq[2]; sh.newk[d0 + 17] = dq[3];
+            }
+        }
+    } else if (KT == QWFN_KV_F16) {
+        uint16_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { h[k] = f2h(x[k]); dq[k] = h2f(h[k]); }
+        if (tid < 2 * per) {
+            const int d = 32 * j + 4 * e4;
+            *reinterpret_cast<uint2 *>(page + chunk_off(g, gh, row, d / 8) + (d % 8) * 2) =
+                make_uint2((uint32_t)h[0] | (uint32_t)h[1] << 16, (uint32_t)h[2] | (uint32_t)h[3] << 16);
+            if (which == 0)
+                for (int k = 0; k < 4; ++k) sh.newk[d + k] = dq[k];
+        }
+    } else {
+        uint16_t dh;
+        const uint32_t pk = quant4(x, g.variant, &dh, dq);   // all lanes: DPP needs full groups
+        if (tid < 2 * per) {
+            store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
+            if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+            if (which == 0)
+                for (int k = 0; k < 4; ++k) sh.newk[32 * j + 4 * e4 + k] = dq[k];
+        }
     }
     __syncthreads();
     if (!complete) return;                         // the block is not complete yet
@@ -601,11 +643,12 @@ __device__ __forceinline__ void fused_append_pool(const Geo &g, const qwfn_kv_vi
     float *dst = v.pooled + (((int64_t)s * g.Hkv + gh) * g.bps + b) * HD;
     if (early) {
 #pragma clang fp contract(off)
-        if (tid < HD) dst[tid] = (pool_chain<HD>(sh.u.st.q8, sh.u.st.sc, g.bt - 1, tid, 0.0f, true) + sh.newk[tid]) *
-                                 g.inv_bt;
+        if (tid < HD)
+            dst[tid] = (pool_chain<HD, KT>(sh.u.st.q8, sh.u.st.sc, g.bt - 1, tid, 0.0f, true) + sh.newk[tid]) *
+                       g.inv_bt;
         return;
     }
-    pool_block_dev<HD>(g, kpage, gh, row - (g.bt - 1), dst, sh.newk, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
+    pool_block_dev<HD, KT>(g, kpage, gh, row - (g.bt - 1), dst, sh.newk, sh.u.st.q8, sh.u.st.sc, tid, kIdxThreads);
 }
 
 
@@ -1552,7 +1595,9 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
     if (fa.enabled && c == n_chunks) {             // the append workgroup
-        fused_append_pool<HD>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
+        if (g.kt == QWFN_KV_Q4_0) fused_append_pool<HD, QWFN_KV_Q4_0>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
+        else if (g.kt == QWFN_KV_F16) fused_append_pool<HD, QWFN_KV_F16>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
+        else fused_append_pool<HD, QWFN_KV_Q8_0>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
         return;
     }
     // the group's query rows do not depend on the length either
@@ -1649,10 +1694,10 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                              int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                              FusedAppend fa, hipStream_t st, bool select) {
-    // The append workgroup is q8_0's, and its pooled block must not be one the
-    // scoring workgroups read: with local_tokens = 0 a just-completed block is
-    // eligible.  Otherwise the append and the pooling run as launches of their own.
-    if (fa.enabled && (g.kt != QWFN_KV_Q8_0 || g.local == 0)) {
+    // The append workgroup's pooled block must not be one the scoring
+    // workgroups read: with local_tokens = 0 a just-completed block is
+    // eligible, and the append and the pooling run as launches of their own.
+    if (fa.enabled && g.local == 0) {
         // (a failed launch surfaces through hipGetLastError after the indexer's)
         (void)launch_append(g, v, fa.k_new, fa.v_new, fa.src_f16, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
         (void)launch_pool(g, v, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
