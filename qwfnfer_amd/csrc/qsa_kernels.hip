@@ -1750,11 +1750,28 @@ k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, cons
     const int h = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int pair = s * g.Hkv + gh;
-    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
+    // The length, the count, the first batch of part rows and the (max, sum)
+    // pairs go out together: the part loads are clamped to the pair's n_tiles
+    // rows of the workspace (in bounds whatever the count), a dense call reads
+    // the length in place of the count, and rows past the parts are dropped
+    // once the count is known.
+    const int32_t *pl = seq_len + (g.pf ? 0 : s);
+    const int L = seq_length(g, *pl, s);
+    const int n_raw = *(dense ? pl : nsel + pair);
+    const int64_t row = (int64_t)pair * ws.n_tiles * G + h;     // part i: row + i * G
+    const float *pml = ws.part_ml + row * 2;
+    const int d = tid % HD, r = tid / HD;
+    const float *po = ws.part_o + row * HD + d;
+    const int last = ws.n_tiles - 1;
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(r + u * R, last) * G * HD];
+    const int tc = min(tid, last);
+    float m0 = pml[(int64_t)tc * 2 * G], l0 = pml[(int64_t)tc * 2 * G + 1];
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
-        n = dense ? (L - 1) / g.bt + 1 : nsel[pair];
+        n = dense ? (L - 1) / g.bt + 1 : n_raw;
         n = n < max_sel ? n : max_sel;
     }
     const int parts = ((n * g.bt + 63) / 64 + tg - 1) / tg;
@@ -1764,15 +1781,7 @@ k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, cons
         if (!ok && tid == 0 && gh == 0 && h == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    const int64_t row = (int64_t)pair * ws.n_tiles * G + h;     // part i: row + i * G
-    const float *pml = ws.part_ml + row * 2;
-    const int d = tid % HD, r = tid / HD;
-    const float *po = ws.part_o + row * HD + d;
-    float x[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(r + u * R, parts - 1) * G * HD];
-    float m0 = -INFINITY, l0 = 0.0f;
-    if (tid < parts) { m0 = pml[(int64_t)tid * 2 * G]; l0 = pml[(int64_t)tid * 2 * G + 1]; }
+    if (tid >= parts) { m0 = -INFINITY; l0 = 0.0f; }
     float Mx = m0;
     for (int i = tid + NT; i < parts; i += NT) Mx = fmaxf(Mx, pml[(int64_t)i * 2 * G]);
     Mx = wave_max(Mx);
@@ -1914,35 +1923,49 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     const int lt = tid % C::NTG;
     AttnGroup<HD, G> &gr = sh.grp[gi];
     const int pair = s * g.Hkv + gh;
-    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
+    const int part = blockIdx.x;
+    const int tile = part * TG + gi;
+    const int lane = lt & 63, qcol = lane & 15, qk = lane >> 4;
+    const int cidx = tile * 64 + lane;
+    // The length, the selection count, the selected block of this lane's cell
+    // and the query rows go out together: unconditional loads through pointers
+    // chosen without a branch (the selection index clamped into the pair's
+    // row; a dense call reads the length in place of the count and the block),
+    // checked after they arrive.
+    const int32_t *pl = seq_len + (g.pf ? 0 : s);
+    const int32_t *pn = sel ? nsel + pair : pl;
+    const int32_t *pb = sel ? sel + (int64_t)pair * max_sel + min(cidx / g.bt, max_sel - 1) : pl;
+    const int L = seq_length(g, *pl, s);
+    const int n_raw = *pn, blk_raw = *pb;
+    // the query as the QK operand: lane l holds head l%16 (0 past the
+    // group), dims 16i + 4(l/16) .. +3 of every 16-dim step i
+    float4 qreg[HD / 16];
+    {
+        const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + min(qcol, G - 1)) * HD + 4 * qk;
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) qreg[i] = *reinterpret_cast<const float4 *>(qh + 16 * i);
+    }
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
-        n = sel ? nsel[pair] : (L - 1) / g.bt + 1;
+        n = sel ? n_raw : (L - 1) / g.bt + 1;
         n = n < max_sel ? n : max_sel;
     }
     const int tiles_act = (n * g.bt + 63) / 64;
     const int parts_act = (tiles_act + TG - 1) / TG;
-    const int part = blockIdx.x;
     if (ok && part < parts_act) {
-        // the query as the QK operand: lane l holds head l%16 (0 past the
-        // group), dims 16i + 4(l/16) .. +3 of every 16-dim step i
-        const int lane = lt & 63, wq = __builtin_amdgcn_readfirstlane(lt >> 6), qcol = lane & 15, qk = lane >> 4;
-        float4 qreg[HD / 16];
-        {
-            const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + min(qcol, G - 1)) * HD + 4 * qk;
+        const int wq = __builtin_amdgcn_readfirstlane(lt >> 6);
+        if (qcol >= G) {
 #pragma unroll
-            for (int i = 0; i < HD / 16; ++i)
-                qreg[i] = qcol < G ? *reinterpret_cast<const float4 *>(qh + 16 * i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int i = 0; i < HD / 16; ++i) qreg[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-        const int tile = part * TG + gi;
         const bool active = tile < tiles_act;
         // cells of this group's tile -> (physical page, row) or row -1
         if (lt < 64) {
             int pg = -1, rw = -1;
-            const int cidx = tile * 64 + lt, slot = cidx / g.bt;
+            const int slot = cidx / g.bt;
             if (active && slot < n) {
-                const int blk = sel ? sel[(int64_t)pair * max_sel + slot] : slot;
+                const int blk = sel ? blk_raw : slot;
                 const int t = blk * g.bt + cidx % g.bt;
                 if (blk >= 0 && t < L) {
                     pg = phys_page(g, v.page_table, cache_seq(g, s), t);
