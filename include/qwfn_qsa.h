@@ -274,8 +274,8 @@ int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *v
  * block that position completes, score + select, and attend.  sel_out/n_sel_out
  * (optional) receive the selection as qwfn_indexer_topk would.  Three
  * launches: the indexer, the attention and the merge of its partials.  Up to
- * eight sequences of a matrix-core shape (block_tokens % 64 == 0, q8_0) with
- * per-head selections of at most 8192 eligible blocks, the indexer only
+ * eight sequences with per-head selections (shared_selection 0) of at most
+ * 8192 eligible blocks and max selected blocks <= 1024, the indexer only
  * scores and the attention's workgroups select for themselves; otherwise the
  * launches are qwfn_decode_append_select's and qwfn_sparse_decode_attn's.     */
 int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,

@@ -138,9 +138,10 @@ hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const f
                                     const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
                                     hipStream_t st);
 // Decode attention that makes its own selection from the scores of a
-// scores-only indexer launch, writing it to sel / nsel (matrix-core shapes,
-// per-head selections of at most 8192 eligible blocks, at most eight
-// sequences, max_sel <= 1024: attn_select_fits).
+// scores-only indexer launch, writing it to sel / nsel (the q8_0 matrix-core
+// kernel for its shapes, the general kernel for the other element types and
+// block sizes; per-head selections of at most 8192 eligible blocks, at most
+// eight sequences, max_sel <= 1024: attn_select_fits).
 bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel);
 hipError_t launch_attention_select(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                    int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel,

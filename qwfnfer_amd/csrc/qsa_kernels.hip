@@ -1440,8 +1440,8 @@ struct BigSelShared {
     int bin, need, ncand, cnt_b;
 };
 
-// LDS of the attention's in-kernel selection (k_attn_q8<..., SEL>): the
-// register path's state at NT threads, and the selection itself.
+// LDS of the attention's in-kernel selection (k_attn_q8 / k_attn with SEL):
+// the register path's state at NT threads, and the selection itself.
 constexpr int kAttnSelMax = 1024;                 // selected blocks it holds
 template <int NT>
 struct AttnSelShared {
@@ -1456,6 +1456,31 @@ struct AttnSelShared {
     int32_t sel[kAttnSelMax];
     int32_t nsel;
 };
+
+// The attention's own selection (SEL): every workgroup runs the decode
+// selection of its (sequence, KV head) on the indexer's score row into LDS,
+// with all of its threads, and takes its tiles' blocks from there; part 0 also
+// writes the selection and its count out (for the caller and the merge).  The
+// indexer launch before it only scores, so the decode step waits for no
+// completion counter and no single selecting workgroup.
+struct NoShared {};
+template <int NT, typename SH>
+__device__ __forceinline__ void attn_select(const Geo &g, const Ws &ws, int L, int max_seq_len, int max_sel,
+                                            int pair, int part, int32_t *gsel, int32_t *gnsel, SH &ssh) {
+    const int tid = threadIdx.x;
+    if (L >= 1 && L <= max_seq_len) {
+        const SelOut lo{ssh.sel, &ssh.nsel, 0, 1};
+        select_blocks<NT>(g, ws.scores + (int64_t)pair * ws.nb_cap, L, lo, ssh);
+    } else if (tid == 0) {
+        ssh.nsel = 0;
+    }
+    __syncthreads();
+    if (part == 0) {
+        const int n = min(ssh.nsel, max_sel);
+        for (int i = tid; i < n; i += NT) gsel[(int64_t)pair * max_sel + i] = ssh.sel[i];
+        if (tid == 0) gnsel[pair] = n;
+    }
+}
 
 // grid (shared ? 1 : Hkv, n_seq or n_q)
 __global__ void __launch_bounds__(kBigSelThreads)
@@ -1908,7 +1933,9 @@ struct AttnShared {
 };
 
 // KT: the K/V element type (chunks of a head row, and their dequantization).
-template <int HD, int G, int TG, int KT>
+// SEL: the workgroups select for themselves, as k_attn_q8's do; sel / nsel
+// are then outputs.
+template <int HD, int G, int TG, int KT, bool SEL = false>
 __global__ void __launch_bounds__((AttnCfg<HD, G, TG>::NT))
 k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len,
        int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
@@ -1918,6 +1945,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     constexpr int PERK = (64 * CHK + C::NTG - 1) / C::NTG;      // K (and V) chunk loads per thread
     static_assert(sizeof(AttnShared<HD, G, TG>) <= 160 * 1024, "LDS of the tile groups");
     __shared__ AttnShared<HD, G, TG> sh;
+    __shared__ typename std::conditional<SEL, AttnSelShared<C::NT>, NoShared>::type ssh;
     const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);   // tile group (wave-uniform)
     const int lt = tid % C::NTG;
@@ -1932,11 +1960,24 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     // chosen without a branch (the selection index clamped into the pair's
     // row; a dense call reads the length in place of the count and the block),
     // checked after they arrive.
+    // With SEL the count and the blocks come from the workgroup's own
+    // selection in LDS.
     const int32_t *pl = seq_len + (g.pf ? 0 : s);
-    const int32_t *pn = sel ? nsel + pair : pl;
-    const int32_t *pb = sel ? sel + (int64_t)pair * max_sel + min(cidx / g.bt, max_sel - 1) : pl;
-    const int L = seq_length(g, *pl, s);
-    const int n_raw = *pn, blk_raw = *pb;
+    const bool has_sel = SEL || sel;
+    int L, n_raw, blk_raw;
+    if constexpr (SEL) {
+        L = seq_length(g, *pl, s);
+        attn_select<C::NT>(g, ws, L, max_seq_len, max_sel, pair, part, const_cast<int32_t *>(sel),
+                           const_cast<int32_t *>(nsel), ssh);
+        n_raw = ssh.nsel;
+        blk_raw = ssh.sel[min(cidx / g.bt, kAttnSelMax - 1)];
+    } else {
+        const int32_t *pn = sel ? nsel + pair : pl;
+        const int32_t *pb = sel ? sel + (int64_t)pair * max_sel + min(cidx / g.bt, max_sel - 1) : pl;
+        L = seq_length(g, *pl, s);
+        n_raw = *pn;
+        blk_raw = *pb;
+    }
     // the query as the QK operand: lane l holds head l%16 (0 past the
     // group), dims 16i + 4(l/16) .. +3 of every 16-dim step i
     float4 qreg[HD / 16];
@@ -1948,7 +1989,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
-        n = sel ? n_raw : (L - 1) / g.bt + 1;
+        n = has_sel ? n_raw : (L - 1) / g.bt + 1;
         n = n < max_sel ? n : max_sel;
     }
     const int tiles_act = (n * g.bt + 63) / 64;
@@ -1965,7 +2006,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
             int pg = -1, rw = -1;
             const int slot = cidx / g.bt;
             if (active && slot < n) {
-                const int blk = sel ? blk_raw : slot;
+                const int blk = has_sel ? blk_raw : slot;
                 const int t = blk * g.bt + cidx % g.bt;
                 if (blk >= 0 && t < L) {
                     pg = phys_page(g, v.page_table, cache_seq(g, s), t);
@@ -2183,6 +2224,27 @@ static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
     launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
 }
 
+// The general attention selecting for itself (SEL): sel / nsel are outputs.
+template <int HD, int G, int TG>
+static void launch_attn_sel_t(const Geo &g, const qwfn_kv_view &v, const float *q,
+                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                              int32_t *sel, int32_t *nsel, int32_t max_sel, float *out,
+                              const Ws &ws, hipStream_t st) {
+    const int n_parts = (ws.n_tiles + TG - 1) / TG;
+    const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
+    const dim3 blk(AttnCfg<HD, G, TG>::NT);
+    if (g.kt == QWFN_KV_Q4_0)
+        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q4_0, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
+                           sel, nsel, max_sel, out, ws, n_parts);
+    else if (g.kt == QWFN_KV_F16)
+        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_F16, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
+                           sel, nsel, max_sel, out, ws, n_parts);
+    else
+        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q8_0, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
+                           sel, nsel, max_sel, out, ws, n_parts);
+    launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
+}
+
 // ---------------------------------------------------------------------------
 // attention, q8_0 fast path (block_tokens a multiple of 64): one tile = 64
 // consecutive tokens of one selected block.  Wave w of a tile owns q8_0
@@ -2254,31 +2316,6 @@ struct FastShared {
     int32_t qa[G][HD / 4], qb[G][HD / 4], qc[G][HD / 4];   // the query as three int8 parts, packed
     float qs[G];                               // q ~= qs * (qa + qb/254 + qc/254^2)
 };
-
-// The attention's own selection (SEL): every workgroup runs the decode
-// selection of its (sequence, KV head) on the indexer's score row into LDS,
-// with all of its threads, and takes its tiles' blocks from there; part 0 also
-// writes the selection and its count out (for the caller and the merge).  The
-// indexer launch before it only scores, so the decode step waits for no
-// completion counter and no single selecting workgroup.
-struct NoShared {};
-template <int NT, typename SH>
-__device__ __forceinline__ void attn_select(const Geo &g, const Ws &ws, int L, int max_seq_len, int max_sel,
-                                            int pair, int part, int32_t *gsel, int32_t *gnsel, SH &ssh) {
-    const int tid = threadIdx.x;
-    if (L >= 1 && L <= max_seq_len) {
-        const SelOut lo{ssh.sel, &ssh.nsel, 0, 1};
-        select_blocks<NT>(g, ws.scores + (int64_t)pair * ws.nb_cap, L, lo, ssh);
-    } else if (tid == 0) {
-        ssh.nsel = 0;
-    }
-    __syncthreads();
-    if (part == 0) {
-        const int n = min(ssh.nsel, max_sel);
-        for (int i = tid; i < n; i += NT) gsel[(int64_t)pair * max_sel + i] = ssh.sel[i];
-        if (tid == 0) gnsel[pair] = n;
-    }
-}
 
 // DENSE: attend every block of the sequence (sel is not read).  SEL: select
 // in the kernel (above); sel / nsel are then outputs.
@@ -3344,13 +3381,24 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
 // eight); past it the chip fills and the redundant selections would compete.
 constexpr int32_t kAttnSelSeqs = 8;
 
-bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
-    if (!g.vdim || g.shared || g.topk <= 0 || g.pf || n_seq > kAttnSelSeqs || max_sel > kAttnSelMax ||
-        max_seq_len / g.bt > kKeysMax)
-        return false;
+// The matrix-core kernel's selecting variant for its shapes, the general
+// kernel's for every other element type and block size.
+static bool attn_select_fast(const Geo &g) {
+    if (!g.vdim) return false;
 #define F(HD_, G_, TG_) if (g.hd == HD_ && g.G == G_) return true;
     QWFN_FOR_EACH_FAST(F)
 #undef F
+    return false;
+}
+
+bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
+    if (g.shared || g.topk <= 0 || g.pf || n_seq > kAttnSelSeqs || max_sel > kAttnSelMax ||
+        max_seq_len / g.bt > kKeysMax)
+        return false;
+    if (attn_select_fast(g)) return true;
+#define X(HD_, G_, TG_) if (g.hd == HD_ && g.G == G_) return true;
+    QWFN_FOR_EACH_SHAPE(X)
+#undef X
     return false;
 }
 
@@ -3358,6 +3406,16 @@ hipError_t launch_attention_select(const Geo &g, const qwfn_kv_view &v, const fl
                                    int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel,
                                    int32_t max_sel, float *out, const Ws &ws, hipStream_t st) {
     if (!attn_select_fits(g, n_seq, max_seq_len, max_sel)) return hipErrorInvalidValue;
+    if (!attn_select_fast(g)) {
+#define X(HD_, G_, TG_)                                                                                     \
+        if (g.hd == HD_ && g.G == G_) {                                                                     \
+            launch_attn_sel_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
+            return hipGetLastError();                                                                       \
+        }
+        QWFN_FOR_EACH_SHAPE(X)
+#undef X
+        return hipErrorInvalidValue;
+    }
 #define F(HD_, G_, TG_)                                                                                          \
     if (g.hd == HD_ && g.G == G_) {                                                                              \
         const dim3 grid((unsigned)((ws.n_tiles + TG_ - 1) / TG_), (unsigned)g.Hkv, (unsigned)n_seq);            \

@@ -81,6 +81,15 @@ def test_decode_steps(kt):
 
 
 @pytest.mark.parametrize("kt", TYPES)
+def test_decode_steps_attention_selects(kt):
+    # up to eight sequences, the general attention's workgroups select for
+    # themselves: several lengths, and 4-token blocks past 4096 eligible ones
+    # (the larger per-thread key counts of the 256-thread selection)
+    _decode_steps(with_type(BASELINE, kt), [3000, 64 * 70 + 5, 100], steps=3, seed=990 + kt)
+    _decode_steps(with_type(TINY, kt), [20000, 9000], steps=2, seed=992 + kt)
+
+
+@pytest.mark.parametrize("kt", TYPES)
 def test_decode_steps_checkpoint_heads(kt):
     _decode_steps(with_type(G12, kt), [700], steps=5, seed=975 + kt)
 
