@@ -1776,10 +1776,11 @@ k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, cons
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int pair = s * g.Hkv + gh;
     // The length, the count, the first batch of part rows and the (max, sum)
-    // pairs go out together: the part loads are clamped to the pair's n_tiles
-    // rows of the workspace (in bounds whatever the count), a dense call reads
-    // the length in place of the count, and rows past the parts are dropped
-    // once the count is known.
+    // pairs go out together: the part loads are clamped to the most parts the
+    // attention can write, ceil(n_tiles / tg), inside the pair's n_tiles rows
+    // of the workspace whatever the count; a dense call reads the length in
+    // place of the count, and rows past the parts are dropped once the count
+    // is known.
     const int32_t *pl = seq_len + (g.pf ? 0 : s);
     const int L = seq_length(g, *pl, s);
     const int n_raw = *(dense ? pl : nsel + pair);
@@ -1787,7 +1788,7 @@ k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, cons
     const float *pml = ws.part_ml + row * 2;
     const int d = tid % HD, r = tid / HD;
     const float *po = ws.part_o + row * HD + d;
-    const int last = ws.n_tiles - 1;
+    const int last = (ws.n_tiles + tg - 1) / tg - 1;
     float x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(r + u * R, last) * G * HD];
