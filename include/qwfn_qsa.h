@@ -273,7 +273,10 @@ int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *v
  * ([n_seq][n_head_kv][head_dim], src_dtype) at position seq_len-1, re-pool the
  * block that position completes, score + select, and attend.  sel_out/n_sel_out
  * (optional) receive the selection as qwfn_indexer_topk would.  Three
- * launches: the indexer, the attention and the merge of its partials.  Up to
+ * launches: the indexer, the attention and the merge of its partials (five
+ * with local_tokens = 0, where the block a token completes is eligible at
+ * once: its append and pooling then run first, as launches of their own, so
+ * the scoring reads the completed key).  Up to
  * eight sequences with per-head selections (shared_selection 0) of at most
  * 8192 eligible blocks and max selected blocks <= 1024, the indexer only
  * scores and the attention's workgroups select for themselves; otherwise the

@@ -78,6 +78,7 @@ def lib() -> C.CDLL:
             "qwfn_oracle_attention_f64": (C.c_int, [S, V, P, P, I, P, P, I, P]),
             "qwfn_oracle_decode_step_f32": (C.c_int, [S, V, P, P, P, P, I, P, P, P, I]),
             "qwfn_oracle_prefill_f64": (C.c_int, [S, V, P, I, I, I, P, P, I, P]),
+            "qwfn_oracle_prefill_f64_strided": (C.c_int, [S, V, P, I, I, I, I, P, P, I, P]),
             "qwfn_oracle_idx_pool_block": (C.c_int, [S, C.POINTER(IdxShape), P, P, I, P]),
         }
         for name, (res, args) in sig.items():
@@ -240,9 +241,10 @@ class HostCache:
             raise RuntimeError(f"oracle attention -> {rc}")
         return out
 
-    def prefill_f64(self, q, seq: int, pos0: int, max_sel=None):
+    def prefill_f64(self, q, seq: int, pos0: int, max_sel=None, attn_stride: int = 1):
         """Selections and fp64 outputs of prefill queries pos0.. of sequence seq
-        (rows and pooled keys already in place)."""
+        (rows and pooled keys already in place).  attn_stride > 1: outputs of
+        every attn_stride-th query and the last one only (the rest zero)."""
         q = np.ascontiguousarray(np.asarray(q, dtype=np.float32))
         n_q = q.size // (self.cfg.n_head * self.cfg.head_dim)
         if max_sel is None:
@@ -251,8 +253,8 @@ class HostCache:
         nsel = np.zeros((n_q, self.cfg.n_head_kv), dtype=np.int32)
         out = np.zeros((n_q, self.cfg.n_head, self.cfg.head_dim), dtype=np.float64)
         view = self.view()
-        rc = lib().qwfn_oracle_prefill_f64(C.byref(self.shape), C.byref(view), _p(q), seq, pos0, n_q,
-                                           _p(sel), _p(nsel), max_sel, _p(out))
+        rc = lib().qwfn_oracle_prefill_f64_strided(C.byref(self.shape), C.byref(view), _p(q), seq, pos0, n_q,
+                                                   attn_stride, _p(sel), _p(nsel), max_sel, _p(out))
         if rc < 0:
             raise RuntimeError(f"oracle prefill -> {rc}")
         return sel, nsel, out

@@ -578,6 +578,13 @@ int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
 int qwfn_oracle_prefill_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const float *q,
                             int32_t seq, int32_t pos0, int32_t n_q, int32_t *sel, int32_t *n_sel,
                             int32_t max_sel, double *out) {
+    return qwfn_oracle_prefill_f64_strided(s, v, q, seq, pos0, n_q, 1, sel, n_sel, max_sel, out);
+}
+
+int qwfn_oracle_prefill_f64_strided(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const float *q,
+                                    int32_t seq, int32_t pos0, int32_t n_q, int32_t attn_stride,
+                                    int32_t *sel, int32_t *n_sel, int32_t max_sel, double *out) {
+    if (attn_stride < 1) return QWFN_EINVAL;
     if (seq < 0 || seq >= v->n_seq || pos0 < 0 || n_q < 1) return QWFN_EINVAL;
     if ((int64_t)pos0 + n_q > (int64_t)v->pages_per_seq * s->page_tokens) return QWFN_ERANGE;
     qwfn_kv_view sv = *v;                          /* the one sequence as a view */
@@ -593,8 +600,10 @@ int qwfn_oracle_prefill_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v, cons
         int32_t *si = sel + (int64_t)i * s->n_head_kv * max_sel;
         int32_t *ni = n_sel + (int64_t)i * s->n_head_kv;
         int rc = qwfn_oracle_indexer_topk(s, &sv, q + i * qstride, &L, 1, si, ni, max_sel);
-        if (rc >= 0) rc = qwfn_oracle_attention_f64(s, &sv, q + i * qstride, &L, 1, si, ni, max_sel,
-                                                    out + i * qstride);
+        if (rc >= 0 && (i % attn_stride == 0 || i == n_q - 1))
+            rc = qwfn_oracle_attention_f64(s, &sv, q + i * qstride, &L, 1, si, ni, max_sel, out + i * qstride);
+        else if (rc >= 0)
+            memset(out + i * qstride, 0, sizeof(double) * (size_t)qstride);
         if (rc < rc_all) rc_all = rc;
     }
     return rc_all < 0 ? rc_all : 0;

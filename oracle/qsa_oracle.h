@@ -109,6 +109,13 @@ int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
 int qwfn_oracle_prefill_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const float *q,
                             int32_t seq, int32_t pos0, int32_t n_q, int32_t *sel, int32_t *n_sel,
                             int32_t max_sel, double *out);
+/* The same with the attention of every attn_stride-th query only (query i with
+ * i % attn_stride == 0, and the last query); the other queries get their
+ * selection and zero outputs.  A chunk of thousands of long-context queries
+ * checks every selection and a strided sample of the outputs. */
+int qwfn_oracle_prefill_f64_strided(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const float *q,
+                                    int32_t seq, int32_t pos0, int32_t n_q, int32_t attn_stride,
+                                    int32_t *sel, int32_t *n_sel, int32_t max_sel, double *out);
 /* CPU baseline: one decode token of the whole path in fp32 (append at
  * seq_len-1, pool on block completion, scores, selection, attention with the
  * gathered K/V cast to fp16 as the reference's decode does, online softmax),

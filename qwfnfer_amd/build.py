@@ -37,11 +37,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libqwfn_qsa.so)")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile the kernels and the C ABI into ``qwfnfer_amd/libqwfn_qsa.so``."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -49,6 +45,23 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
     if verbose and res.stderr.strip():
         print(res.stderr, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the kernels and the C ABI into ``qwfnfer_amd/libqwfn_qsa.so``:
+    one object per source, compiled in parallel, then one link."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    objs = [os.path.join(CSRC, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with ThreadPoolExecutor(len(srcs)) as ex:
+        list(ex.map(lambda so: _run([hipcc(), *compile_flags, "-c", "-o", so[1], so[0]], verbose),
+                    zip(srcs, objs)))
+    tmp = LIB + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    for o in objs:
+        os.remove(o)
     os.replace(tmp, LIB)
     return LIB
 

@@ -1715,17 +1715,20 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
 }
 
 template <int HD, int G>
-static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
-                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
-                             int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                             FusedAppend fa, hipStream_t st, bool select) {
+static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
+                                   const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                                   int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
+                                   FusedAppend fa, hipStream_t st, bool select) {
     // The append workgroup's pooled block must not be one the scoring
     // workgroups read: with local_tokens = 0 a just-completed block is
-    // eligible, and the append and the pooling run as launches of their own.
+    // eligible, so the append and the pooling run as launches of their own,
+    // ordered before the scoring on the stream.
     if (fa.enabled && g.local == 0) {
-        // (a failed launch surfaces through hipGetLastError after the indexer's)
-        (void)launch_append(g, v, fa.k_new, fa.v_new, fa.src_f16, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
-        (void)launch_pool(g, v, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
+        hipError_t e = launch_append(g, v, fa.k_new, fa.v_new, fa.src_f16, nullptr, nullptr, n_seq, 0, 0, st,
+                                     seq_len);
+        if (e != hipSuccess) return e;
+        e = launch_pool(g, v, nullptr, nullptr, n_seq, 0, 0, st, seq_len);
+        if (e != hipSuccess) return e;
         fa.enabled = 0;
     }
     const int nb_max = max_seq_len / g.bt;
@@ -1735,7 +1738,8 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
                        sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big));
-    if (!select) return;                           // the attention selects (k_attn_q8<..., SEL>)
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !select) return e;      // !select: the attention selects (k_attn_q8<..., SEL>)
     if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
         hipLaunchKernelGGL(k_select_cut, dim3((unsigned)ws.cut_wg, (unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws, sel, nsel, max_sel);
@@ -1743,6 +1747,7 @@ static void launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q
         hipLaunchKernelGGL(k_select_big, dim3((unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws.scores, ws.nb_cap, sel,
                            nsel, max_sel);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -2949,10 +2954,8 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                           const FusedAppend &fa, hipStream_t st, bool select) {
 #define X(HD_, G_, TG_)                                                                          \
-    if (g.hd == HD_ && g.G == G_) {                                                              \
-        launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st, select); \
-        return hipGetLastError();                                                                \
-    }
+    if (g.hd == HD_ && g.G == G_)                                                                \
+        return launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st, select);
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
     return hipErrorInvalidValue;

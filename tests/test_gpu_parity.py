@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from _gpu import assert_close_attn, cfg_of, fill, kv_rows, make_pair, np_of
+from _gpu import assert_close_attn, cfg_of, decode_steps, fill, kv_rows, make_pair, np_of
 from _refs import BASELINE, TINY, Cfg
 from qwfnfer_amd import _lib, qsa
 
@@ -275,54 +275,8 @@ def test_dense_attention_matches_f64(L):
 
 
 def _decode_steps(cfg, lengths, steps, seed, dtype=np.float32, zero_pooled=False):
-    """Fused decode steps on a batch of sequences vs the oracle's append + pool on
-    completion + indexer + fp64 attention.  zero_pooled: every pooled key of the
-    filled prefix set to 0 on both sides (all scores tie)."""
-    rng = np.random.default_rng(seed)
-    n_seq = len(lengths)
-    pps = (max(lengths) + steps) // cfg.page_tokens + 1
-    dev, host = make_pair(cfg, n_seq, pps, seed=seed)
-    fill(dev, host, rng, lengths)
-    if zero_pooled:
-        host.pooled[...] = 0
-        dev.pooled.zero_()
-    cur = np.array(lengths, np.int32)
-    max_len = int(cur.max()) + steps
-    ws = qsa.Workspace(cfg_of(cfg), n_seq, max_len)
-    msel = cfg_of(cfg).max_selected(max_len)
-    sel = torch.empty((n_seq, cfg.n_head_kv, msel), dtype=torch.int32, device="cuda")
-    nsel = torch.empty((n_seq, cfg.n_head_kv), dtype=torch.int32, device="cuda")
-    outs = []
-    for step in range(steps):
-        cur = cur + 1
-        q = rng.standard_normal((n_seq, cfg.n_head, cfg.head_dim), dtype=np.float32)
-        kn, vn = kv_rows(rng, n_seq, cfg)
-        kn, vn = kn.astype(dtype), vn.astype(dtype)
-        out = qsa.sparse_attn_decode(dev, torch.from_numpy(q).cuda(), torch.from_numpy(kn).cuda(),
-                                     torch.from_numpy(vn).cuda(), torch.from_numpy(cur).cuda(), max_len, ws,
-                                     sel=sel, n_sel=nsel)
-        torch.cuda.synchronize()
-        for s in range(n_seq):
-            p = int(cur[s]) - 1
-            assert host.append(kn[s:s + 1], vn[s:s + 1], [p], [s]) == 0
-            if cur[s] % cfg.block_tokens == 0:
-                host.pool_block(s, p // cfg.block_tokens)
-        hs, hn = host.indexer_topk(q, cur, max_sel=msel)
-        gs, gn = np_of(sel), np_of(nsel)
-        np.testing.assert_array_equal(gn, hn, err_msg=f"step {step}")
-        for s in range(n_seq):
-            for g in range(cfg.n_head_kv):
-                np.testing.assert_array_equal(gs[s, g, :gn[s, g]], hs[s, g, :hn[s, g]],
-                                              err_msg=f"step {step} seq {s} head {g}")
-        ref = host.attention_f64(q, cur, hs, hn)
-        assert_close_attn(np_of(out), ref, f"decode step {step}")
-        outs.append(np_of(out))
-    np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
-    np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
-    for s in range(n_seq):
-        nw = int(cur[s]) // cfg.block_tokens
-        np.testing.assert_array_equal(np_of(dev.pooled)[s, :, :nw], host.pooled[s, :, :nw])
-    return outs
+    """Fused decode steps on a batch of sequences vs the oracle."""
+    return decode_steps(cfg, lengths, steps, seed, dtype=dtype, zero_pooled=zero_pooled)
 
 
 def test_decode_steps_cross_block_boundaries():
