@@ -288,6 +288,23 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             int32_t *sel_out, int32_t *n_sel_out,
                             void *ws, size_t ws_bytes, void *stream);
 
+/* qwfn_sparse_attn_decode without a workspace argument, for callers that
+ * cannot allocate device memory (code under hipGraph capture that may not
+ * call hipMalloc, tight serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference.  The workspace is a file-scope device array
+ * of the library, 8 MiB per device, held until the process ends: calls whose
+ * qwfn_qsa_workspace_bytes(shape, n_seq, max_seq_len) exceeds it return
+ * QWFN_ERANGE (8 MiB holds eight sequences of the BASELINE shape up to 1M
+ * tokens).  The first call on a device enqueues one fill kernel on `stream`
+ * that clears the array.  Every call on a device shares its array, so calls
+ * that overlap on one device (other streams, other threads) race; calls in
+ * stream order do not.  Nothing here allocates or frees.                    */
+int qwfn_sparse_attn_decode_noalloc(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                                    const float *q, const void *k_new, const void *v_new,
+                                    int32_t src_dtype, const int32_t *seq_len, int32_t n_seq,
+                                    int32_t max_seq_len, float *out, int32_t *sel_out,
+                                    int32_t *n_sel_out, void *stream);
+
 /* ---- prefill ------------------------------------------------------------- */
 
 /* Workspace for qwfn_sparse_attn_prefill processing q_batch queries per

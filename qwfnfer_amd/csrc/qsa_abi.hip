@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "qsa_internal.h"
@@ -468,6 +469,65 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
     e = own ? launch_attention_select(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st)
             : launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st);
     return e == hipSuccess ? ok() : hip_fail(e, "decode: attention");
+}
+
+}  // extern "C"
+
+namespace {
+
+// The workspace of qwfn_sparse_attn_decode_noalloc: one array per device,
+// held until the process ends.  In host code `scratch` names a host-side
+// stand-in; the device address of each GPU's copy comes from
+// hipGetSymbolAddress, looked up once per device and kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices];
+
+// This device's copy of `scratch`.  The first call on a device looks up its
+// address and clears it with a fill kernel on `st` (the workspace's
+// completion counters must start at zero; every call leaves them at zero).
+int scratch_of_device(hipStream_t st, void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "decode_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kScratchDevices)
+        return fail(QWFN_ENOTSUP, "decode_noalloc: device %d beyond the %d this library serves", dev,
+                    kScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e, "decode_noalloc: hipGetSymbolAddress(scratch)");
+        e = launch_fill_zero(p, kScratchBytes, st);
+        if (e != hipSuccess) return hip_fail(e, "decode_noalloc: clearing the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return QWFN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwfn_sparse_attn_decode_noalloc(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                                    const void *k_new, const void *v_new, int32_t src_dtype,
+                                    const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, float *out,
+                                    int32_t *sel_out, int32_t *n_sel_out, void *stream) {
+    size_t need = 0;
+    int rc = qwfn_qsa_workspace_bytes(shape, n_seq, max_seq_len, &need);
+    if (rc) return rc;
+    if (need > kScratchBytes)
+        return fail(QWFN_ERANGE,
+                    "decode_noalloc: n_seq %d at max_seq_len %d needs %zu bytes of workspace, more than the "
+                    "%zu of the library's scratch array; call qwfn_sparse_attn_decode with a workspace",
+                    n_seq, max_seq_len, need, kScratchBytes);
+    void *ws = nullptr;
+    if ((rc = scratch_of_device((hipStream_t)stream, &ws))) return rc;
+    return qwfn_sparse_attn_decode(shape, view, q, k_new, v_new, src_dtype, seq_len, n_seq, max_seq_len, out,
+                                   sel_out, n_sel_out, ws, kScratchBytes, stream);
 }
 
 int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_seq_len, int32_t q_batch,

@@ -413,6 +413,31 @@ def sparse_attn_decode(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_n
     return out
 
 
+def sparse_attn_decode_noalloc(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                               seq_len: torch.Tensor, max_seq_len: int, out: torch.Tensor,
+                               sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None,
+                               stream=None) -> torch.Tensor:
+    """:func:`sparse_attn_decode` without a workspace: the library's own
+    per-device scratch array serves as one (qwfn_sparse_attn_decode_noalloc).
+    ``out`` is required, so the call allocates nothing."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    _need(q, "q", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype:
+        raise TypeError("k_new and v_new must both be float32 or both float16")
+    _need(k_new, "k_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(v_new, "v_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    _need(out, "out", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    if (sel is None) != (n_sel is None):
+        raise ValueError("pass both sel and n_sel or neither")
+    s = cfg.shape()
+    call("qwfn_sparse_attn_decode_noalloc", C.byref(s), C.byref(cache.view()), q.data_ptr(), k_new.data_ptr(),
+         v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,
+         seq_len.data_ptr(), n_seq, max_seq_len, out.data_ptr(), _ptr(sel), _ptr(n_sel), _stream(stream))
+    return out
+
+
 def sparse_attn_prefill(cache: KvCache, q: torch.Tensor, seq: int, pos0: int, ws: Workspace,
                         k_new: Optional[torch.Tensor] = None, v_new: Optional[torch.Tensor] = None,
                         out: Optional[torch.Tensor] = None, sel: Optional[torch.Tensor] = None,

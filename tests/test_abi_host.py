@@ -189,3 +189,19 @@ def test_row_interop_rejects_bad_arguments_before_launch():
         assert call(n=0) == _lib.QWFN_EINVAL
         assert call(pos0=1020, n=5) == _lib.QWFN_ERANGE       # past the view's capacity
         assert "capacity" in _lib.load().qwfn_qsa_last_error().decode()
+
+
+def test_noalloc_decode_rejects_what_its_array_cannot_hold():
+    """qwfn_sparse_attn_decode_noalloc checks the workspace its arguments need
+    against the library's 8 MiB scratch array before any device call."""
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view(pps=4)
+    call = lambda n_seq, max_len: _code("qwfn_sparse_attn_decode_noalloc", C.byref(s), C.byref(v), 4096, 4096,
+                                        4096, 0, 4096, n_seq, max_len, 4096, None, None, None)
+    assert call(16, 1 << 20) == _lib.QWFN_ERANGE          # 15.4 MiB of workspace
+    assert "scratch" in _lib.load().qwfn_qsa_last_error().decode()
+    assert call(0, 1024) == _lib.QWFN_EINVAL
+    need = C.c_size_t()
+    assert _code("qwfn_qsa_workspace_bytes", C.byref(s), 8, 1 << 20, C.byref(need)) == 0
+    assert need.value <= 8 << 20                          # eight sequences of 1M tokens fit
