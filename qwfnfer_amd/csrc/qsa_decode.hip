@@ -1,0 +1,718 @@
+// qsa_decode.hip -- decode attention over q8_0 caches whose blocks are whole
+// 64-token tiles (V quants dim-major per tile): the attention of
+// qwfn_sparse_decode_attn (a given selection or dense) and of the fused
+// qwfn_sparse_attn_decode (the workgroup selects from the indexer's scores).
+//
+// One workgroup of four waves (one per SIMD) per part of a (sequence, KV head)'s
+// tiles; wave w owns cells 16w .. 16w+15 of every tile, so a wave's logits need
+// no other wave:
+//   QK  v_mfma_f32_16x16x32_f16: the int8 key quants (exact in fp16) against the
+//       query scaled by a power of two and split into fp16 high + low parts;
+//       one accumulator per 32-dim q8_0 block, combined with the keys' scales.
+//   PV  v_mfma_f32_16x16x16_f16: the V quants (exact in fp16) against the
+//       weights p * d_v * 2^k split into fp16 high + low parts.  The QK
+//       accumulator layout (cells 4lg..4lg+3 of column hn in lane 16lg+hn) is
+//       the B-operand layout of this shape, so the weights never leave their
+//       lanes.
+// Each wave keeps an online-softmax state over the part's tiles; the four
+// states merge through LDS into one partial (max, sum, unnormalised O) per
+// workgroup, which k_merge combines.
+//
+// The latency of one sequence is a chain of dependent steps, so everything
+// that does not depend on the selection (the length, the score row, the query
+// rows, the sequence's page-table row) is loaded in the first round trip, the
+// query split runs while the tile loads are in flight, and the selection is a
+// short exact top-k over a 2048-bin histogram held by the four waves.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "qsa_device.h"
+
+namespace qwfn_qsa {
+
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = kDecThreads / 64;
+constexpr int kDecBins = 2048;                  // selection histogram bins
+constexpr int kDecCand = 256;                   // threshold-bin keys ranked pairwise
+constexpr int kDecPtLds = 4096;                 // page-table entries parked in LDS
+constexpr int kDecSelMax = 1024;                // selected blocks kept in LDS
+constexpr int kDecTpwMax = 4;                   // tiles per workgroup (the i4v of their blocks)
+
+enum DecMode { kGiven = 0, kDense = 1, kSelect = 2 };
+
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+template <int HD, int G>
+struct DecShared {
+    union {
+        struct {                                 // the selection
+            uint32_t hist[kDecBins + 64];        // + one trash bin per lane
+            uint32_t cand_key[kDecWaves * kDecCand + 64];   // threshold-bin keys, a region per wave
+            int32_t cand_b[kDecWaves * kDecCand + 64];      // (+ one trash slot per lane)
+        } s;
+        float wo[kDecWaves][G][HD];              // the waves' O, merged into the partial
+    } u;
+    float wml[kDecWaves][G][2];                  // the waves' (max, sum)
+    int32_t wcnt[kDecWaves];
+    int32_t ccnt[kDecWaves];
+    int32_t nsel;
+    int32_t sel[kDecSelMax + 64];                // + one trash slot per lane
+    int32_t ptab[kDecPtLds];
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Four int8 quants -> four exact fp16 values, in order (bias to unsigned, splice
+// under the fp16 exponent of 1024, subtract 1152).
+__device__ __forceinline__ h4v q8x4_to_h4(uint32_t w) {
+    half2v lo, hi;
+    q8x4_to_h2(w, lo, hi);
+    h4v r;
+    r[0] = lo[0]; r[1] = lo[1]; r[2] = hi[0]; r[3] = hi[1];
+    return r;
+}
+
+// The selection histogram is stored transposed: bin b at word
+// (b % 32) * 64 + b / 32, so lane l's 32 bins [32l, 32l+32) are the words
+// j*64 + l, j = 0..31, and each of the wave's 32 reads touches 64 consecutive
+// words (no bank conflicts; an untransposed 128-byte run per lane put every
+// lane on the same banks).
+__device__ __forceinline__ int hist_word(int b) { return (b & 31) * 64 + (b >> 5); }
+
+// Threshold bin of the selection histogram (kDecBins bins in ascending key
+// order) for the topk-th largest key, found by each wave on its own (no barrier
+// after): lane l sums bins [32l, 32l+32), a scan finds the lane holding that
+// key, then that lane's 32 bins are spread over lanes 0..31 for the same
+// search.  Returns the bin; *need = keys of it still needed, *cnt = its keys.
+__device__ __forceinline__ int dec_cut(const uint32_t *hist, int topk, int *need, int *cnt) {
+    const int lane = threadIdx.x & 63;
+    uint32_t own = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) own += hist[j * 64 + lane];
+    const int incl = wave_incl_scan((int)own);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    const int above = total - incl;                      // keys in the bins of higher lanes
+    const int ls = __builtin_ctzll(__ballot(above < topk && above + (int)own >= topk));
+    const int above_l = __builtin_amdgcn_readlane(above, ls);
+    const int c = (int)hist[(lane & 31) * 64 + ls] & -(lane < 32);
+    const int ic = wave_incl_scan(c);
+    const int run = above_l + __builtin_amdgcn_readlane(ic, 31) - ic;   // keys in higher bins
+    const int j = __builtin_ctzll(__ballot(lane < 32 && run < topk && run + c >= topk));
+    *need = topk - __builtin_amdgcn_readlane(run, j);
+    *cnt = __builtin_amdgcn_readlane(c, j);
+    return ls * 32 + j;
+}
+
+// Block-wide exclusive prefix sum over the four waves; *total = the sum.  All
+// threads call (one barrier).
+__device__ __forceinline__ int dec_excl_sum(int v, int32_t *wcnt, int *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int x = wave_incl_scan(v);
+    if (lane == 63) wcnt[w] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < kDecWaves; ++i) {
+        const int t = wcnt[i];
+        base += i < w ? t : 0;
+        tot += t;
+    }
+    *total = tot;
+    return base + x - v;
+}
+
+// The decode selection of one (sequence, KV head) into sh.sel / sh.nsel: the
+// forced blocks (sink, window) and the topk eligible blocks by (score desc,
+// block asc), ascending.  Thread t holds the scores of blocks base +
+// [t*KPT, t*KPT + KPT) in sv (base = e_lo rounded down to 4, 0 past e_hi).
+// A histogram linear in the score between the smallest and the largest
+// eligible score lo, hi (from the scoring launch's per-chunk bounds; NaN in bin
+// 0; with no finite spread every key lands in bin 0 and the exact fallback
+// below decides), zeroed by the caller before its barrier, locates the
+// threshold bin; every
+// key above it is taken and, when the bin holds just the keys still needed
+// (the usual case: near the threshold a bin holds about one key), all of its
+// keys.  Otherwise the bin's keys are ranked exactly (at most kDecCand of
+// them), or for heavier ties refined by radix passes over their 32-bit keys,
+// ties then taken in block order.  Straight-line per key: no branch on a
+// key's value or eligibility.  Ends with a barrier; sh.sel is then valid.
+template <int KPT, int HD, int G>
+__device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT], const Ranges &r, int topk,
+                                           float lo, float hi, DecShared<HD, G> &sh) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int base = r.e_lo & ~3;
+    const int b0 = base + tid * KPT;
+    const uint32_t lo_i = (uint32_t)(r.e_lo - b0);     // keys i with i - lo_i < n_i are eligible
+    const uint32_t n_i = (uint32_t)(r.e_hi - r.e_lo);
+    auto valid = [&](int i) { return (uint32_t)i - lo_i < n_i; };
+    const float span = hi - lo;
+    float scale = (float)kDecBins / span;
+    scale = hi > lo && span < INFINITY && scale < INFINITY ? scale : 0.0f;   // no finite spread: all in bin 0
+    const float c0 = -lo * scale;
+    // each key's bin: fma (monotone in the score), then a saturating conversion
+    // (NaN and negatives to 0) and a clamp; -1 outside the eligible range
+    int ib[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const float f = __builtin_fmaf(sv[i], scale, c0);
+        uint32_t u;
+        asm("v_cvt_u32_f32 %0, %1" : "=v"(u) : "v"(f));
+        ib[i] = valid(i) ? (int)min(u, (uint32_t)(kDecBins - 1)) : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) atomicAdd(&sh.u.s.hist[ib[i] >= 0 ? hist_word(ib[i]) : kDecBins + lane], 1u);
+    __syncthreads();
+    int need, cB;
+    const int B = dec_cut(sh.u.s.hist, topk, &need, &cB);
+    uint32_t mask = 0, cm = 0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        mask |= (uint32_t)(ib[i] > B) << i;
+        cm |= (uint32_t)(ib[i] == B) << i;
+    }
+    if (cB == need) {                              // the whole threshold bin is taken
+        mask |= cm;
+    } else if (cB <= kDecCand) {
+        // the bin's keys into a region per wave (wave-local offsets; keys of
+        // other bins go to the lane's trash slot), then each owner ranks its
+        // own, read back from LDS, against all of them: (key desc, block asc)
+        const int c = __builtin_popcount(cm);
+        const int wi = wave_incl_scan(c);
+        const int slot0 = w * kDecCand + wi - c;
+        int slot = slot0;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool in = ib[i] == B;
+            const int at = in ? slot : kDecWaves * kDecCand + lane;
+            sh.u.s.cand_key[at] = score_key(sv[i]);
+            sh.u.s.cand_b[at] = b0 + i;
+            slot += in;
+        }
+        if (lane == 63) sh.ccnt[w] = wi;
+        __syncthreads();
+        for (int jo = slot0; jo < slot0 + c; ++jo) {
+            const uint32_t k = sh.u.s.cand_key[jo];
+            const int b = sh.u.s.cand_b[jo];
+            int rank = 0;
+#pragma unroll
+            for (int ww = 0; ww < kDecWaves; ++ww) {
+                const int n = sh.ccnt[ww];
+                for (int jj = 0; jj < n; ++jj) {
+                    const uint32_t kj = sh.u.s.cand_key[ww * kDecCand + jj];
+                    rank += (kj > k) || (kj == k && sh.u.s.cand_b[ww * kDecCand + jj] < b);
+                }
+            }
+            mask |= (uint32_t)(rank < need) << (b - b0);
+        }
+    } else {
+        // Heavy ties: the need-th largest key of the bin by four 8-bit radix
+        // passes over the bin's keys (256-bin histograms, each wave finding
+        // the digit on its own), then
+        // keys above it and the first ties in block order.
+        uint32_t *h = sh.u.s.hist;
+        uint32_t prefix = 0;
+        int nd = need;
+#pragma unroll 1
+        for (int pass = 0; pass < 4; ++pass) {
+            const int shift = 24 - 8 * pass;
+            __syncthreads();                       // readers of the previous histogram are done
+            h[tid] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                const uint32_t k = score_key(sv[i]);
+                const bool m = ib[i] == B && (uint32_t)((uint64_t)k >> (shift + 8)) == prefix;
+                atomicAdd(&h[m ? (k >> shift) & 255u : 256u + (uint32_t)lane], 1u);
+            }
+            __syncthreads();
+            // digit of the nd-th largest: lane l holds bins 4l .. 4l+3
+            const u4v hv = reinterpret_cast<const u4v *>(h)[lane];
+            const int own = (int)(hv[0] + hv[1] + hv[2] + hv[3]);
+            const int incl = wave_incl_scan(own);
+            const int above = __builtin_amdgcn_readlane(incl, 63) - incl;
+            const int ls = __builtin_ctzll(__ballot(above < nd && above + own >= nd));
+            const u4v hl = reinterpret_cast<const u4v *>(h)[ls];
+            int run = __builtin_amdgcn_readlane(above, ls);
+            int dig = 0;
+#pragma unroll
+            for (int q = 3; q >= 0; --q) {
+                const bool here = dig == 0 && run < nd && run + (int)hl[q] >= nd;
+                dig = here ? 4 * ls + q + 1 : dig;
+                run += dig == 0 ? (int)hl[q] : 0;
+            }
+            nd -= run;
+            prefix = (prefix << 8) | (uint32_t)(dig - 1);
+        }
+        const uint32_t T = prefix;                 // the threshold key; nd ties at T are taken
+        int eq = 0;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const uint32_t k = score_key(sv[i]);
+            mask |= (uint32_t)(ib[i] == B && k > T) << i;
+            eq += ib[i] == B && k == T;
+        }
+        int tot;
+        int before = dec_excl_sum(eq, sh.wcnt, &tot);
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool tie = ib[i] == B && score_key(sv[i]) == T;
+            mask |= (uint32_t)(tie && before < nd) << i;
+            before += tie;
+        }
+        __syncthreads();                           // wcnt is reused below
+    }
+    // emission in block order after the sink blocks, then the forced ones
+    int tot;
+    int pos = g.sink + dec_excl_sum(__builtin_popcount(mask), sh.wcnt, &tot);
+    for (uint32_t x = mask; x; x &= x - 1u) {
+        sh.sel[pos < g.sink + topk && pos < kDecSelMax ? pos : kDecSelMax + lane] = b0 + __builtin_ctz(x);
+        ++pos;
+    }
+    const int nwin = r.b_last - r.fw + 1;
+    // forced blocks: thread t writes sink block t and window block t (a trash
+    // slot when out of range); longer windows loop
+    sh.sel[tid < g.sink && tid < kDecSelMax ? tid : kDecSelMax + lane] = tid;
+    for (int i = tid + kDecThreads; i < g.sink && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+    {
+        const int at = g.sink + topk + tid;
+        sh.sel[tid < nwin && at < kDecSelMax ? at : kDecSelMax + lane] = r.fw + tid;
+    }
+    for (int i = tid + kDecThreads; i < nwin; i += kDecThreads) {
+        const int at = g.sink + topk + i;
+        sh.sel[at < kDecSelMax ? at : kDecSelMax + lane] = r.fw + i;
+    }
+    if (tid == 0) sh.nsel = g.sink + topk + nwin;
+    __syncthreads();
+}
+
+// Loads of one tile for wave w: K quants in QK A-operand layout (cell 16w+hn,
+// dims 32kb+8lg .. +8), V quants in PV A-operand layout (dim 16db+hn, cells
+// 16w+4lg .. +4), and the K / V scales of the lane's D-layout cells
+// 16w+4lg .. +4 (NB fp16 per cell).
+template <int HD>
+struct DecTile {
+    static constexpr int NB = HD / 32, ND = HD / 16, NS = NB / 2 > 0 ? NB / 2 : 1;
+    u2v k[NB];                                       // native vectors: a copy stays in registers
+    uint32_t v[ND];
+    u4v dk[NS], dv[NS];
+    int nv;                                          // valid cells of the tile (0: none)
+};
+
+template <int HD>
+__device__ __forceinline__ void dec_load_tile(const Geo &g, const qwfn_kv_view &v, int gh, int32_t page,
+                                              int row0, int nv, DecTile<HD> &t) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hn = lane & 15, lg = lane >> 4;
+    constexpr int NB = DecTile<HD>::NB, ND = DecTile<HD>::ND, NS = DecTile<HD>::NS;
+    t.nv = nv;
+    const int64_t pbase = (int64_t)(nv > 0 ? page : 0) * g.page_bytes;
+    const uint8_t *kp = (const uint8_t *)v.k_pages + pbase;
+    const uint8_t *vp = (const uint8_t *)v.v_pages + pbase;
+    const int tl = gh * (g.pt / 64) + row0 / 64;
+    const uint8_t *kq = kp + ((int64_t)tl * ND + (lg >> 1)) * 1024 + (16 * w + hn) * 16 + 8 * (lg & 1);
+    const uint8_t *vq = vp + ((int64_t)tl * HD + hn) * 64 + 16 * w + 4 * lg;
+    const int64_t so = g.qbytes + ((int64_t)(gh * g.pt + row0 + 16 * w + 4 * lg) * NB) * 2;
+    // unconditional: an empty tile reads page 0 (in bounds), and every value
+    // of its cells is masked by nv == 0 (logits -inf, V scales 0)
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) t.k[kb] = *reinterpret_cast<const u2v *>(kq + kb * 2048);
+#pragma unroll
+    for (int db = 0; db < ND; ++db) t.v[db] = *reinterpret_cast<const uint32_t *>(vq + db * 1024);
+    if constexpr (NB >= 2) {
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            t.dk[i] = *reinterpret_cast<const u4v *>(kp + so + 16 * i);
+            t.dv[i] = *reinterpret_cast<const u4v *>(vp + so + 16 * i);
+        }
+    } else {
+        const u2v a = *reinterpret_cast<const u2v *>(kp + so), b = *reinterpret_cast<const u2v *>(vp + so);
+        t.dk[0] = u4v{a[0], a[1], 0u, 0u};
+        t.dv[0] = u4v{b[0], b[1], 0u, 0u};
+    }
+}
+
+// fp16 scale j (0 .. 4*NB-1, cell-major: cell i = j / NB, block kb = j % NB)
+// of a lane's scale vector.
+template <int NS>
+__device__ __forceinline__ float scale_at(const u4v (&d)[NS], int j) {
+    const uint32_t wd = d[j / 8][(j % 8) / 2];
+    return h2f((uint16_t)(j % 2 ? wd >> 16 : wd & 0xffffu));
+}
+
+// grid (parts, Hkv, n_seq); part p attends tiles [p*tpw, p*tpw + tpw) of its
+// (sequence, KV head).  MODE: kGiven (sel / nsel read), kDense (every block
+// below the length), kSelect (the workgroup selects from ws.scores with KPT
+// keys a thread; part 0 writes sel / nsel out).
+template <int HD, int G, int MODE, int KPT>
+__global__ void __launch_bounds__(kDecThreads)
+k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len, int32_t max_seq_len,
+      int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t tpw) {
+#pragma clang fp contract(off)
+    static_assert(G <= 16, "one matrix-core column per query head");
+    constexpr int NB = HD / 32, ND = HD / 16;
+    __shared__ DecShared<HD, G> sh;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hn = lane & 15, lg = lane >> 4;
+    const int part = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    const int pair = s * g.Hkv + gh;
+    const int tpb = g.bt / 64;
+    const int t_first = part * tpw;
+    // ---- first round trip: everything that does not depend on the selection
+    const int L = seq_len[s];
+    const int32_t *prow = v.page_table + (int64_t)s * g.pps;
+    const int npt = min(g.pps, (max_seq_len + g.pt - 1) / g.pt);
+    const bool park = MODE != kDense && npt <= kDecPtLds;
+    constexpr int PTV = kDecPtLds / (4 * kDecThreads);   // 16-byte page-table loads a thread
+    u4v pt4[PTV];
+    if (park) {                                    // entries past npt read 0 (never looked up)
+        const BufRsrc prs = buf_rsrc(prow, (uint32_t)npt * 4u);
+#pragma unroll
+        for (int k = 0; k < PTV; ++k)
+            pt4[k] = __builtin_bit_cast(u4v, BufLoad<4>::at(prs, (4 * tid + 4 * kDecThreads * k) * 4, 0));
+    }
+    float sv[MODE == kSelect ? KPT : 1];
+    if constexpr (MODE == kSelect) {
+        const int base = g.sink & ~3;
+        const BufRsrc rs = buf_rsrc(ws.scores + (int64_t)pair * ws.nb_cap, (uint32_t)ws.nb_cap * 4u);
+#pragma unroll
+        for (int k = 0; k < KPT / 4; ++k) {
+            const auto x = BufLoad<4>::at(rs, (base + tid * KPT) * 4 + 16 * k, 0);
+            sv[4 * k] = x[0]; sv[4 * k + 1] = x[1]; sv[4 * k + 2] = x[2]; sv[4 * k + 3] = x[3];
+        }
+    }
+    float2 rec[2];                                 // kSelect: the scoring chunks' (min, max), lanes l, l + 64
+    if constexpr (MODE == kSelect) {
+        const int n_ch = ws.nb_cap / 64;           // at most 128: 8192 eligible blocks
+        const BufRsrc rr = buf_rsrc(ws.cmm + (int64_t)pair * n_ch, (uint32_t)n_ch * 8u);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const auto x = BufLoad<2>::at(rr, (lane + 64 * k) * 8, 0);
+            rec[k] = make_float2(x[0], x[1]);
+        }
+    }
+    int n_given = 0;
+    i4v pre;                                       // kGiven: the tiles' blocks; kDense: their pages
+#pragma unroll
+    for (int i = 0; i < kDecTpwMax; ++i) {
+        const int tile = t_first + min(i, tpw - 1);
+        if constexpr (MODE == kGiven) {
+            pre[i] = sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
+        } else if constexpr (MODE == kDense) {
+            const int64_t t0 = (int64_t)(tile / tpb) * g.bt + (tile % tpb) * 64;
+            pre[i] = prow[min((int)(t0 / g.pt), g.pps - 1)];
+        } else {
+            pre[i] = 0;
+        }
+    }
+    if constexpr (MODE == kGiven) n_given = nsel[pair];
+    const int hq = min(hn, G - 1);
+    float qv[NB][8];
+    {
+        const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + hq) * HD + 8 * lg;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            const float4 a = *reinterpret_cast<const float4 *>(qh + 32 * kb);
+            const float4 b = *reinterpret_cast<const float4 *>(qh + 32 * kb + 4);
+            qv[kb][0] = a.x; qv[kb][1] = a.y; qv[kb][2] = a.z; qv[kb][3] = a.w;
+            qv[kb][4] = b.x; qv[kb][5] = b.y; qv[kb][6] = b.z; qv[kb][7] = b.w;
+        }
+    }
+    if (park) {
+#pragma unroll
+        for (int k = 0; k < PTV; ++k) *reinterpret_cast<u4v *>(&sh.ptab[4 * tid + 4 * kDecThreads * k]) = pt4[k];
+    }
+    if constexpr (MODE == kSelect) {               // the selection histogram starts at zero
+        u4v *h4 = reinterpret_cast<u4v *>(sh.u.s.hist);
+        const u4v z = {0u, 0u, 0u, 0u};
+        h4[tid] = z;
+        h4[tid + kDecThreads] = z;
+        if (tid < 16) h4[2 * kDecThreads + tid] = z;
+    }
+    const bool ok = L >= 1 && L <= max_seq_len;
+    // ---- the blocks of this part's tiles
+    int n = 0;
+    if constexpr (MODE == kSelect) {
+        __syncthreads();                           // the parked page table, the zeroed histogram
+        if (ok) {
+            const Ranges r = qsa_ranges(g, L);
+            const int ne = r.e_hi - r.e_lo, topk = eff_topk(g, r);
+            if (g.topk <= 0 || ne <= topk) {       // every block below the length
+                const int nb = r.b_last + 1;
+                for (int i = tid; i < nb && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+                if (tid == 0) sh.nsel = nb;
+                __syncthreads();
+            } else if (topk == 0) {                // the forced blocks fill the count
+                const int nwin = r.b_last - r.fw + 1;
+                for (int i = tid; i < g.sink && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+                for (int i = tid; i < nwin; i += kDecThreads)
+                    if (g.sink + i < kDecSelMax) sh.sel[g.sink + i] = r.fw + i;
+                if (tid == 0) sh.nsel = g.sink + nwin;
+                __syncthreads();
+            } else {
+                // the score bounds over the chunks (records past the grid: empty)
+                const int n_ch = ws.nb_cap / 64;
+                float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const bool in = lane + 64 * k < n_ch;
+                    lo = in && rec[k].x < lo ? rec[k].x : lo;
+                    hi = in && rec[k].y > hi ? rec[k].y : hi;
+                }
+                hi = wave_max(hi);
+                lo = -wave_max(-lo);
+                dec_select<KPT>(g, sv, r, topk, lo, hi, sh);
+            }
+            n = min(sh.nsel, max_sel);
+        }
+        if (part == 0) {                           // the selection for the caller and the merge
+            for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
+            if (tid == 0) nsel[pair] = n;
+        }
+    } else {
+        if (MODE == kGiven) __syncthreads();       // the parked page table
+        if (ok) {
+            n = MODE == kDense ? (L - 1) / g.bt + 1 : n_given;
+            n = n < max_sel ? n : max_sel;
+        }
+    }
+    const int tiles_act = n * tpb;
+    if (!ok || t_first >= tiles_act) return;       // (uniform) no partial: the merge reads fewer parts
+    const int t_end = min(t_first + tpw, tiles_act);
+    // ---- the tiles
+    auto tile_page = [&](int tile, int32_t &page, int &row0) -> int {   // valid cells of the tile
+        const int i = tile - t_first;
+        auto pre_at = [&](int k) { return k == 0 ? pre[0] : k == 1 ? pre[1] : k == 2 ? pre[2] : pre[3]; };
+        int blk;
+        if constexpr (MODE == kSelect) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
+        else if constexpr (MODE == kGiven) blk = pre_at(i);
+        else blk = tile / tpb;
+        const int64_t t0 = (int64_t)blk * g.bt + (tile % tpb) * 64;
+        const int t0c = (int)min(max(t0, (int64_t)0), (int64_t)g.pps * g.pt - 1);
+        int32_t praw;
+        if constexpr (MODE == kDense) praw = pre_at(i);
+        else if (park) praw = sh.ptab[min(t0c / g.pt, npt - 1)];
+        else praw = prow[t0c / g.pt];
+        const bool in = blk >= 0 && t0 < L;
+        const bool pg_ok = praw >= 0 && praw < g.n_phys;
+        if (in && !pg_ok && tid == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+        page = praw;
+        row0 = t0c % g.pt;
+        return in && pg_ok ? min(64, L - t0c) : 0;
+    };
+    DecTile<HD> cur;
+    {
+        int32_t page;
+        int row0;
+        const int nv = tile_page(t_first, page, row0);
+        dec_load_tile<HD>(g, v, gh, page, row0, nv, cur);
+    }
+    // the query split, while the first tile's loads are in flight: scaled by a
+    // power of two so its largest magnitude is in [2^13, 2^14), then fp16
+    // high + low parts (residual below 2^-22 of the largest)
+    h8v qhi[NB], qlo[NB];
+    float qfac;
+    {
+        float a = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(qv[kb][e]));
+        a = col_max4(a);
+        int ex = 0;
+        frexpf(a, &ex);                            // a in [2^(ex-1), 2^ex)
+        const float up = a > 0.0f ? ldexpf(1.0f, 14 - ex) : 1.0f;
+        qfac = (a > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f) * g.scale_log2;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qv[kb][e] * up;
+                const _Float16 h = (_Float16)x;
+                qhi[kb][e] = h;
+                qlo[kb][e] = (_Float16)(x - (float)h);
+            }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    f4v o[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) o[db] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+    for (int tile = t_first; tile < t_end; ++tile) {
+        DecTile<HD> nxt;
+        const bool more = tile + 1 < t_end;
+        if (more) {                                // the next tile's loads go out first
+            int32_t page;
+            int row0;
+            const int nv = tile_page(tile + 1, page, row0);
+            dec_load_tile<HD>(g, v, gh, page, row0, nv, nxt);
+        }
+        // QK: one accumulator per 32-dim block
+        f4v acc[NB];
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            const h8v ka = q8x8_to_h8(make_uint2(cur.k[kb][0], cur.k[kb][1]));
+            acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[kb], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[kb], acc[kb], 0, 0, 0);
+        }
+        // logits of cells 16w + 4lg + i (column hn), the keys' scales applied in block order
+        float sl[4];
+        const int c0 = 16 * w + 4 * lg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float x = scale_at(cur.dk, i * NB) * acc[0][i];
+#pragma unroll
+            for (int kb = 1; kb < NB; ++kb) x += scale_at(cur.dk, i * NB + kb) * acc[kb][i];
+            sl[i] = c0 + i < cur.nv ? x * qfac : -INFINITY;
+        }
+        // online softmax over the wave's cells, per column
+        const float mt = col_max4(fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3])));
+        const float m_new = fmaxf(m_run, mt);
+        const float corr = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = sl[i] == -INFINITY ? 0.0f : fast_exp2(sl[i] - m_new);
+        l_run = l_run * corr + col_sum4((p[0] + p[1]) + (p[2] + p[3]));
+        m_run = m_new;
+        // PV: weights times the V scale and 2^k (the largest valid scale of
+        // the wave near 2^15) in fp16 high + low parts
+        float dvm = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4 * NB; ++j) dvm = fmaxf(dvm, c0 + j / NB < cur.nv ? scale_at(cur.dv, j) : 0.0f);
+        dvm = wave_max(dvm);
+        int ev = 0;
+        frexpf(dvm, &ev);
+        const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - ev) : 1.0f;
+        const float down = dvm > 0.0f ? ldexpf(1.0f, ev - 15) : 1.0f;
+        h4v bhi[NB], blo[NB];
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float dvi = c0 + i < cur.nv ? scale_at(cur.dv, i * NB + kb) : 0.0f;
+                const float x = p[i] * dvi * up;
+                const _Float16 h = (_Float16)x;
+                bhi[kb][i] = h;
+                blo[kb][i] = (_Float16)(x - (float)h);
+            }
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+            const h4v va = q8x4_to_h4(cur.v[db]);
+            f4v a = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[db / 2], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[db / 2], a, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[db][j] = o[db][j] * corr + a[j] * down;
+        }
+        if (more) cur = nxt;
+    }
+    // ---- the four waves' states into one partial
+    if (hn < G) {
+        if (lg == 0) { sh.wml[w][hn][0] = m_run; sh.wml[w][hn][1] = l_run; }
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+            *reinterpret_cast<float4 *>(&sh.u.wo[w][hn][16 * db + 4 * lg]) =
+                make_float4(o[db][0], o[db][1], o[db][2], o[db][3]);
+    }
+    __syncthreads();
+    const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
+    static_assert((G * HD) % kDecThreads == 0 || G * HD < kDecThreads, "whole outputs a thread");
+#pragma unroll
+    for (int r = 0; r < (G * HD + kDecThreads - 1) / kDecThreads; ++r) {
+        const int k = tid + r * kDecThreads;
+        if (k >= G * HD) break;
+        const int h = k / HD, d = k % HD;
+        float M = sh.wml[0][h][0];
+#pragma unroll
+        for (int i = 1; i < kDecWaves; ++i) M = fmaxf(M, sh.wml[i][h][0]);
+        float O = 0.0f, Ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDecWaves; ++i) {
+            const float mi = sh.wml[i][h][0];
+            const float wt = mi == -INFINITY ? 0.0f : fast_exp2(mi - M);
+            O += wt * sh.u.wo[i][h][d];
+            Ls += wt * sh.wml[i][h][1];
+        }
+        ws.part_o[(pb + h) * HD + d] = O;
+        if (d == 0) {
+            ws.part_ml[(pb + h) * 2 + 0] = M;
+            ws.part_ml[(pb + h) * 2 + 1] = Ls;
+        }
+    }
+}
+
+template <int HD, int G, int MODE, int KPT>
+void launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
+                  int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, int32_t tpw,
+                  hipStream_t st) {
+    const int parts = (ws.n_tiles + tpw - 1) / tpw;
+    hipLaunchKernelGGL((k_dec<HD, G, MODE, KPT>), dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq),
+                       dim3(kDecThreads), 0, st, g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, ws, tpw);
+}
+
+template <int HD, int G>
+hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                            int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
+                            int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
+    // one tile a workgroup while the sequences leave the chip's CUs idle;
+    // more per workgroup (fewer partials, the next tile's loads overlapping
+    // this one's arithmetic) once the tiles fill it several times over
+    const int64_t tiles = (int64_t)n_seq * g.Hkv * ws.n_tiles;
+    const int tpw = tiles >= 4096 ? kDecTpwMax : tiles >= 1024 ? 2 : 1;
+    int32_t *sl = const_cast<int32_t *>(sel), *ns = const_cast<int32_t *>(nsel);
+    if (select) {
+        const Ranges span_r{0, 0, g.sink, max_seq_len / g.bt};
+        const int span = span_r.e_hi - (span_r.e_lo & ~3);
+        if (span <= 4 * kDecThreads)
+            launch_dec_t<HD, G, kSelect, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+        else if (span <= 8 * kDecThreads)
+            launch_dec_t<HD, G, kSelect, 8>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+        else if (span <= 16 * kDecThreads)
+            launch_dec_t<HD, G, kSelect, 16>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+        else if (span <= 32 * kDecThreads)
+            launch_dec_t<HD, G, kSelect, 32>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+        else
+            return hipErrorInvalidValue;
+    } else if (sel) {
+        launch_dec_t<HD, G, kGiven, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+    } else {
+        launch_dec_t<HD, G, kDense, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_merge(g, v, seq_len, n_seq, max_seq_len, select ? ns : nsel, max_sel, !select && !sel, out, ws,
+                        tpw, st);
+}
+
+}  // namespace
+
+#define QWFN_FOR_EACH_DEC(X) X(128, 8) X(128, 4) X(128, 2) X(64, 8) X(256, 12) X(256, 8)
+
+bool dec_kernels_for(const Geo &g) {
+    if (!g.vdim || g.pf) return false;
+#define X(HD_, G_) if (g.hd == HD_ && g.G == G_) return true;
+    QWFN_FOR_EACH_DEC(X)
+#undef X
+    return false;
+}
+
+bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel) {
+    return dec_kernels_for(g) && !g.shared && g.topk > 0 && max_sel <= kDecSelMax &&
+           max_seq_len / g.bt - (g.sink & ~3) <= 32 * kDecThreads;
+}
+
+hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                                int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
+                                int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
+    if (!dec_kernels_for(g) || (select && !dec_select_fits(g, max_seq_len, max_sel))) return hipErrorInvalidValue;
+#define X(HD_, G_)                                                                                        \
+    if (g.hd == HD_ && g.G == G_)                                                                         \
+        return launch_dec_shape<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, \
+                                         select, st);
+    QWFN_FOR_EACH_DEC(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+}  // namespace qwfn_qsa

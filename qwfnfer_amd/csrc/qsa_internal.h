@@ -55,12 +55,14 @@ struct Ws {
     float   *part_ml;    // [n_seq][Hkv][n_tiles][G][2]
     uint2   *cand;       // [n_seq][Hkv][cut_wg][kCutKeys] (key, block) candidates of the multi-workgroup selection
     int32_t *ccnt;       // [n_seq][Hkv][kCutWgMax] their counts
+    float2  *cmm;        // [n_seq][Hkv][nb_cap / 64] each scoring chunk's (min, max) eligible score
+                         // (the attention's own selection reads them; (+inf, -inf) when empty)
     int32_t  nb_cap, max_sel, n_tiles;
     int32_t  cut_wg;     // workgroups of the multi-workgroup selection (0: one workgroup)
 };
 
 struct WsLayout {
-    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, total;
+    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, total;
     int32_t nb_cap, max_sel, n_tiles, cut_wg;
 };
 // partials = false: no attention partials (the prefill kernel keeps its state on chip);
@@ -146,6 +148,21 @@ bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t 
 hipError_t launch_attention_select(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                    int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel,
                                    int32_t max_sel, float *out, const Ws &ws, hipStream_t st);
+// Combine of the attention partials: og = sum_i w_i O_i / sum_i w_i l_i over
+// the parts of tg tiles each (dense: every block below the length).
+hipError_t launch_merge(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len, int32_t n_seq,
+                        int32_t max_seq_len, const int32_t *nsel, int32_t max_sel, bool dense, float *out,
+                        const Ws &ws, int32_t tg, hipStream_t st);
+// The decode attention of q8_0 caches whose blocks are whole 64-token tiles
+// (qsa_decode.hip): over a given selection (sel), dense (sel NULL), or
+// selecting from the indexer's scores (select; writes sel / nsel), then the
+// merge.  dec_select_fits: per-head selections of at most 8192 eligible
+// blocks and 1024 selected.
+bool dec_kernels_for(const Geo &g);
+bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
+hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                                int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
+                                int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st);
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,

@@ -19,132 +19,6 @@ namespace qwfn_qsa {
 // device helpers
 // ---------------------------------------------------------------------------
 
-// Byte offsets inside a page (layout in include/qwfn_qsa.h).
-__device__ __forceinline__ int64_t quant_off(const Geo &g, int gh, int row, int d) {
-    return ((int64_t)(gh * (g.pt / 64) + row / 64) * (g.hd / 16) + d / 16) * 1024 +
-           (row % 64) * 16 + d % 16;
-}
-// V quants when the block size is a multiple of 64: per 64-token tile, each
-// dimension's 64 cells are contiguous, so a lane owning a dimension reads its
-// cells with wide loads for the dot2 products of the attention.
-__device__ __forceinline__ int64_t vquant_off(const Geo &g, int gh, int row, int d) {
-    return ((int64_t)(gh * (g.pt / 64) + row / 64) * g.hd + d) * 64 + row % 64;
-}
-__device__ __forceinline__ int64_t scale_off(const Geo &g, int gh, int row, int j) {
-    return g.qbytes + ((int64_t)(gh * g.pt + row) * (g.hd / 32) + j) * 2;
-}
-// 16-byte chunk c of KV head gh's row `row` (the K layout, every element
-// type; q8_0 chunks hold 16 dims, q4_0 chunks one ggml block's 16 qs bytes,
-// fp16 chunks 8 dims).
-__device__ __forceinline__ int64_t chunk_off(const Geo &g, int gh, int row, int c) {
-    return ((int64_t)(gh * (g.pt / 64) + row / 64) * g.chunks + c) * 1024 + (row % 64) * 16;
-}
-
-// Cache sequence and length of launch sequence s (prefill: query s of one
-// cache sequence, see Geo::pf).  `raw` is seq_len[s] as loaded.
-__device__ __forceinline__ int cache_seq(const Geo &g, int s) { return g.pf ? g.pf_seq : s; }
-__device__ __forceinline__ int seq_length(const Geo &g, int raw, int s) { return g.pf ? g.pf_pos0 + s + 1 : raw; }
-
-__device__ __forceinline__ int8_t to_i8(float r) {
-    if (r != r) return 0;
-    if (r > 127.0f) return 127;
-    if (r < -128.0f) return -128;
-    return (int8_t)(int)r;
-}
-
-// Orderable key of a score: larger key = larger score; NaN lowest; -0 == +0.
-__device__ __forceinline__ uint32_t score_key(float x) {
-    const uint32_t u = __float_as_uint(x);
-    uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    k = x == 0.0f ? 0x80000000u : k;               // -0 == +0
-    return x != x ? 0u : k;                        // NaN lowest
-}
-
-// Cross-lane steps on the DPP network (gfx9 encodings): a wave64 reduction
-// is quad xor-1, quad xor-2, half-row mirror, row mirror, then row_bcast:15
-// into rows 1/3 and row_bcast:31 into rows 2/3, leaving the total in lane 63;
-// no LDS traffic, unlike ds_bpermute shuffles.
-template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_ZERO = false>
-__device__ __forceinline__ float dppf(float old, float src) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
-                                                                 __builtin_bit_cast(int, src), CTRL,
-                                                                 ROW_MASK, BANK_MASK, BOUND_ZERO));
-}
-template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_ZERO = false>
-__device__ __forceinline__ int dppi(int old, int src) {
-    return __builtin_amdgcn_update_dpp(old, src, CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO);
-}
-constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
-constexpr int kDppRowShr = 0x110, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
-
-__device__ __forceinline__ float lane63(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-// Raw buffer loads: one descriptor per array, a per-lane byte offset and a
-// uniform (SGPR) byte offset, so a run of loads costs one instruction each
-// with no 64-bit address arithmetic.  Offsets at or past `bytes` read 0.
-using BufRsrc = __amdgpu_buffer_rsrc_t;
-__device__ __forceinline__ BufRsrc buf_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-// Cache policy of a load that must see other workgroups' released stores
-// without an L2 invalidate: sc1, the agent-scope coherent load.
-constexpr int kCpolSc1 = 16;
-template <int VW, int CP = 0> struct BufLoad;
-template <int CP> struct BufLoad<1, CP> {
-    using T = float __attribute__((ext_vector_type(1)));
-    static __device__ __forceinline__ T at(BufRsrc r, int voff, int soff) {
-        T v; v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CP)); return v;
-    }
-};
-template <int CP> struct BufLoad<2, CP> {
-    using T = float __attribute__((ext_vector_type(2)));
-    static __device__ __forceinline__ T at(BufRsrc r, int voff, int soff) {
-        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, CP));
-    }
-};
-template <int CP> struct BufLoad<4, CP> {
-    using T = float __attribute__((ext_vector_type(4)));
-    static __device__ __forceinline__ T at(BufRsrc r, int voff, int soff) {
-        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CP));
-    }
-};
-
-// Maximum over the wave, returned to every lane.
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dppf<kDppQuadXor1>(v, v));
-    v = fmaxf(v, dppf<kDppQuadXor2>(v, v));
-    v = fmaxf(v, dppf<kDppRowHalfMirror>(v, v));
-    v = fmaxf(v, dppf<kDppRowMirror>(v, v));
-    v = fmaxf(v, dppf<kDppRowBcast15, 0xa>(v, v));
-    v = fmaxf(v, dppf<kDppRowBcast31, 0xc>(v, v));
-    return lane63(v);
-}
-
-// Sum over the wave, returned to every lane.
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dppf<kDppQuadXor1>(0.0f, v);
-    v += dppf<kDppQuadXor2>(0.0f, v);
-    v += dppf<kDppRowHalfMirror>(0.0f, v);
-    v += dppf<kDppRowMirror>(0.0f, v);
-    v += dppf<kDppRowBcast15, 0xa>(0.0f, v);
-    v += dppf<kDppRowBcast31, 0xc>(0.0f, v);
-    return lane63(v);
-}
-
-// Inclusive prefix sum over the wave (Hillis-Steele inside each 16-lane row,
-// then the row totals broadcast forward).
-__device__ __forceinline__ int wave_incl_scan(int x) {
-    x += dppi<kDppRowShr + 1, 0xf, 0xf, true>(0, x);
-    x += dppi<kDppRowShr + 2, 0xf, 0xf, true>(0, x);
-    x += dppi<kDppRowShr + 4, 0xf, 0xf, true>(0, x);
-    x += dppi<kDppRowShr + 8, 0xf, 0xf, true>(0, x);
-    x += dppi<kDppRowBcast15, 0xa>(0, x);
-    x += dppi<kDppRowBcast31, 0xc>(0, x);
-    return x;
-}
-
 // Completion protocol of a split reduction, called by EVERY thread of a
 // workgroup that has finished writing its share (the barriers inside must be
 // reached from one call site by all waves).  Each thread waits for its own
@@ -516,28 +390,6 @@ k_pool(Geo g, qwfn_kv_view v, const int32_t *seq_ids, const int32_t *block_ids, 
 // indexer: scores of the eligible blocks, then top-k in the last workgroup
 // ---------------------------------------------------------------------------
 
-// Forced/eligible ranges of a sequence of length L (same rule as the oracle):
-// F = [0, sink) U [fw, b_last], E = [sink, min(L/bt, fw)).
-struct Ranges { int b_last, fw, e_lo, e_hi; };
-__device__ __forceinline__ Ranges qsa_ranges(const Geo &g, int L) {
-    Ranges r;
-    const int last = L - 1, w0 = last - g.local + 1, nbw = L / g.bt;
-    r.b_last = last / g.bt;
-    r.fw = w0 > 0 ? w0 / g.bt : 0;
-    r.e_lo = g.sink;
-    r.e_hi = nbw < r.fw ? nbw : r.fw;
-    if (r.e_hi < r.e_lo) r.e_hi = r.e_lo;
-    return r;
-}
-
-// Eligible blocks kept: top_k_blocks, less the forced ones (sink + window)
-// when the count includes them.  Only meaningful past the short-context case
-// (e_hi > e_lo, so the window starts after the sink blocks).
-__device__ __forceinline__ int eff_topk(const Geo &g, const Ranges &r) {
-    if (!g.keep_total) return g.topk;
-    const int k = g.topk - g.sink - (r.b_last - r.fw + 1);
-    return k > 0 ? k : 0;
-}
 
 constexpr int kIdxThreads = 256;
 constexpr int kBlocksPerChunk = kIdxThreads / 4;   // 4 lanes share one block's dot
@@ -1440,7 +1292,7 @@ struct BigSelShared {
     int bin, need, ncand, cnt_b;
 };
 
-// LDS of the attention's in-kernel selection (k_attn_q8 / k_attn with SEL):
+// LDS of the general attention's in-kernel selection (k_attn with SEL):
 // the register path's state at NT threads, and the selection itself.
 constexpr int kAttnSelMax = 1024;                 // selected blocks it holds
 template <int NT>
@@ -1615,7 +1467,7 @@ template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
 k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
           int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t n_chunks, FusedAppend fa,
-          int32_t select_here) {
+          int32_t select_here, int32_t chunk_minmax) {
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
@@ -1656,6 +1508,7 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
 #pragma unroll
         for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
     }
+    float cmx = -INFINITY, cmn = INFINITY;        // this chunk's largest / smallest score (not NaN)
     if (ok && g.topk > 0) {
         const Ranges r = qsa_ranges(g, L);
         const int ne = r.e_hi - r.e_lo;
@@ -1689,7 +1542,25 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
                 score = (h == 0) ? dot : score + dot;
             }
             if (act && j == 0) sc[b] = score;
+            cmx = act && score > cmx ? score : cmx;
+            cmn = act && score < cmn ? score : cmn;
             __syncthreads();                       // q reads done before the union is reused
+        }
+    }
+    // the attention selects: the chunk's (min, max) for its histogram bounds
+    // (every chunk of the grid writes one, (+inf, -inf) when it scored nothing)
+    if (chunk_minmax) {
+        cmx = wave_max(cmx);
+        cmn = -wave_max(-cmn);
+        if ((tid & 63) == 0) { sh.red[tid >> 6] = cmx; sh.red[kIdxThreads / 64 + (tid >> 6)] = cmn; }
+        __syncthreads();
+        if (tid == 0) {
+#pragma unroll
+            for (int i = 1; i < kIdxThreads / 64; ++i) {
+                cmx = fmaxf(cmx, sh.red[i]);
+                cmn = fminf(cmn, sh.red[kIdxThreads / 64 + i]);
+            }
+            ws.cmm[(int64_t)pair * (ws.nb_cap / 64) + c] = make_float2(cmn, cmx);
         }
     }
     // selection in a launch of its own (long contexts: k_select_big)
@@ -1737,9 +1608,9 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
-                       sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big));
+                       sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big), (int32_t)!select);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !select) return e;      // !select: the attention selects (k_attn_q8<..., SEL>)
+    if (e != hipSuccess || !select) return e;      // !select: the attention selects (k_dec / k_attn<..., SEL>)
     if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
         hipLaunchKernelGGL(k_select_cut, dim3((unsigned)ws.cut_wg, (unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws, sel, nsel, max_sel);
@@ -1766,7 +1637,7 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
 // batch of part loads issued before the weights are known; a length out of
 // range or no cell gives zeros (and, for a length, the status bit).
 // grid (G, Hkv, n_seq or n_q)
-constexpr int kMergeThreads = 256;
+constexpr int kMergeThreads = 512;               // parts r, r + R, ... a thread (R = 512 / head_dim): one load round up to 24 R parts
 constexpr int kMergeWts = 2048;                   // parts whose weights LDS keeps
 template <int G, int HD>
 __global__ void __launch_bounds__(kMergeThreads)
@@ -1870,45 +1741,22 @@ static void launch_merge_t(const Geo &g, const qwfn_kv_view &v, const int32_t *s
                        st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)(sel == nullptr), out, ws, tg);
 }
 
-typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef int32_t i4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));   // plain 16-byte load/store (no struct copy)
+#define QWFN_FOR_EACH_MERGE(X) X(128, 8) X(128, 4) X(128, 2) X(64, 8) X(256, 12) X(256, 8)
+hipError_t launch_merge(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len, int32_t n_seq,
+                        int32_t max_seq_len, const int32_t *nsel, int32_t max_sel, bool dense, float *out,
+                        const Ws &ws, int32_t tg, hipStream_t st) {
+#define X(HD_, G_)                                                                                            \
+    if (g.hd == HD_ && g.G == G_) {                                                                           \
+        hipLaunchKernelGGL((k_merge<G_, HD_>), dim3((unsigned)G_, (unsigned)g.Hkv, (unsigned)n_seq),          \
+                           dim3(kMergeThreads), 0, st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)dense, \
+                           out, ws, tg);                                                                      \
+        return hipGetLastError();                                                                             \
+    }
+    QWFN_FOR_EACH_MERGE(X)
+#undef X
+    return hipErrorInvalidValue;
+}
 
-// Sum / max over the lanes l, l^16, l^32, l^48 (the four k-groups of one MFMA
-// column), by the gfx950 row swaps: v_permlane32_swap pairs lane l with l^32
-// and v_permlane16_swap pairs row 2r with 2r+1; both results are symmetric, so
-// every lane of the column ends with the same value.
-__device__ __forceinline__ unsigned opaque_copy(unsigned x) {
-    unsigned y;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
-    return y;
-}
-// Lane l with lane l ^ 32 (permlane32) or l ^ 16 (permlane16), combined by op.
-// The swap gets two registers the compiler cannot prove equal: given one value
-// twice it would take the two results as equal and keep only the first.
-template <typename Op>
-__device__ __forceinline__ float swap32_op(float v, Op op) {
-    const unsigned b = __builtin_bit_cast(unsigned, v);
-    const auto r = __builtin_amdgcn_permlane32_swap(b, opaque_copy(b), false, false);
-    const unsigned r0 = r[0], r1 = r[1];                  // (bit_cast of r[i] reads element 0)
-    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
-}
-template <typename Op>
-__device__ __forceinline__ float swap16_op(float v, Op op) {
-    const unsigned b = __builtin_bit_cast(unsigned, v);
-    const auto r = __builtin_amdgcn_permlane16_swap(b, opaque_copy(b), false, false);
-    const unsigned r0 = r[0], r1 = r[1];
-    return op(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
-}
-__device__ __forceinline__ float col_sum4(float v) {
-    const auto add = [](float a, float b) { return a + b; };
-    return swap16_op(swap32_op(v, add), add);
-}
-__device__ __forceinline__ float col_max4(float v) {
-    const auto mx = [](float a, float b) { return fmaxf(a, b); };
-    return swap16_op(swap32_op(v, mx), mx);
-}
 
 template <int HD, int G, int TG>
 struct AttnCfg {
@@ -1939,7 +1787,7 @@ struct AttnShared {
 };
 
 // KT: the K/V element type (chunks of a head row, and their dequantization).
-// SEL: the workgroups select for themselves, as k_attn_q8's do; sel / nsel
+// SEL: the workgroups select for themselves; sel / nsel
 // are then outputs.
 template <int HD, int G, int TG, int KT, bool SEL = false>
 __global__ void __launch_bounds__((AttnCfg<HD, G, TG>::NT))
@@ -2248,353 +2096,6 @@ static void launch_attn_sel_t(const Geo &g, const qwfn_kv_view &v, const float *
     else
         hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q8_0, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
                            sel, nsel, max_sel, out, ws, n_parts);
-    launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
-}
-
-// ---------------------------------------------------------------------------
-// attention, q8_0 fast path (block_tokens a multiple of 64): one tile = 64
-// consecutive tokens of one selected block.  Wave w of a tile owns q8_0
-// block w of the head dims (32 dims) for every query head of the group, so K
-// and V are each read exactly once per tile, in matrix-core operand layouts:
-//   QK  v_mfma_i32_16x16x32_i8 of the int8 key quants (16 cells x 32 dims)
-//       against each of the query's three int8 parts (32 dims x 16 heads):
-//       exact int32 dots, combined once in fp32; per-wave partial logits
-//       scaled by the key scale and summed in wave order by the softmax.
-//   softmax per head (DPP), p' = p * dv * 2^sh as an fp16 high part plus an
-//       fp16 remainder ([head][block][cell]), sh a per-tile power of two that
-//       keeps p' inside fp16's range.
-//   PV  v_mfma_f32_16x16x32_f16 of the V quants (exact in fp16, 16 dims x 32
-//       cells of the dim-major tile) against p' high and low (32 cells x 16
-//       heads), fp32 accumulation, then * 2^-sh.
-// ---------------------------------------------------------------------------
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-// Four int8 quants of consecutive cells -> two exact fp16 pairs: bias to
-// unsigned, splice under the fp16 exponent of 1024, subtract 1152.
-__device__ __forceinline__ void q8x4_to_h2(uint32_t w, half2v &lo, half2v &hi) {
-    const uint32_t u = w ^ 0x80808080u;
-    const half2v bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    lo = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + bias;
-    hi = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + bias;
-}
-
-
-// Eight int8 quants -> eight exact fp16 values, in order.
-__device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
-    half2v a, b, c, d;
-    q8x4_to_h2(w.x, a, b);
-    q8x4_to_h2(w.y, c, d);
-    h8v r;
-    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-    return r;
-}
-
-// Matrix-core operand layouts (v_mfma_*_16x16x32_*, wave64), lane l = 16*lg + hn:
-//   A: row hn, k = 8*lg .. 8*lg+7;  B: column hn, k = 8*lg .. 8*lg+7;
-//   D: rows 4*lg .. 4*lg+3, column hn.
-__device__ __forceinline__ i4v mfma_i8(uint2 a, uint2 b, i4v c) {
-    return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)__builtin_bit_cast(uint64_t, a),
-                                                 (long)__builtin_bit_cast(uint64_t, b), c, 0, 0, 0);
-}
-
-template <int HD, int G, int TG>
-struct FastCfg {
-    static constexpr int NB = HD / 32;                 // q8_0 blocks per head row = waves per tile
-    static constexpr int NTG = NB * 64;                // threads per tile group
-    static constexpr int NT = TG * NTG;
-    static constexpr int OPT = (G * HD + NT - 1) / NT;
-};
-
-template <int HD, int G>
-struct alignas(16) FastGroup {
-    float lg[HD / 32][G][64];                  // unscaled partial logits, one per owning wave
-    uint16_t pp[G][HD / 32][64];               // fp16 p * dv * 2^sh (high part)
-    uint16_t pl[G][HD / 32][64];               // its fp16 remainder (low part)
-    float o[G][HD];                            // the tile's O
-    float m[G], l[G];
-};
-
-template <int HD, int G, int TG>
-struct FastShared {
-    FastGroup<HD, G> grp[TG];
-    int32_t qa[G][HD / 4], qb[G][HD / 4], qc[G][HD / 4];   // the query as three int8 parts, packed
-    float qs[G];                               // q ~= qs * (qa + qb/254 + qc/254^2)
-};
-
-// DENSE: attend every block of the sequence (sel is not read).  SEL: select
-// in the kernel (above); sel / nsel are then outputs.
-template <int HD, int G, int TG, bool DENSE, bool SEL = false>
-__global__ void __launch_bounds__((FastCfg<HD, G, TG>::NT))
-k_attn_q8(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len,
-          int32_t max_seq_len, const int32_t *__restrict__ sel, const int32_t *__restrict__ nsel, int32_t max_sel,
-          float *__restrict__ out, Ws ws) {
-    using C = FastCfg<HD, G, TG>;
-    constexpr int NB = C::NB;
-    static_assert(G <= 16, "one matrix-core column per query head");
-    static_assert(!(SEL && DENSE), "a dense call has no selection");
-    __shared__ FastShared<HD, G, TG> sh;
-    __shared__ typename std::conditional<SEL, AttnSelShared<C::NT>, NoShared>::type ssh;
-    const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
-    const int gi = __builtin_amdgcn_readfirstlane(tid / C::NTG);
-    const int lt = tid % C::NTG;
-    const int w = __builtin_amdgcn_readfirstlane(lt >> 6), lane = lt & 63;
-    FastGroup<HD, G> &gr = sh.grp[gi];
-    const int pair = s * g.Hkv + gh;
-    const int part = blockIdx.x;
-    const int tile = part * TG + gi;                   // uniform per tile group
-    const int tpb = g.bt / 64;                         // tiles per block
-    // The length, the selection count and this tile's selected block go out
-    // together (the block index is clamped for the load and checked after),
-    // and so do the query rows of the heads this wave quantizes.
-    // Unconditional loads from selected pointers, all issued before any is
-    // used: no branch may sit between them (a branch makes the compiler wait
-    // for every load in flight).
-    const int L = seq_length(g, seq_len[g.pf ? 0 : s], s);
-    int n_raw, blk_raw;
-    if constexpr (SEL) {
-        attn_select<C::NT>(g, ws, L, max_seq_len, max_sel, pair, part, const_cast<int32_t *>(sel),
-                           const_cast<int32_t *>(nsel), ssh);
-        n_raw = ssh.nsel;
-        blk_raw = ssh.sel[min(tile / tpb, kAttnSelMax - 1)];
-    } else {
-        n_raw = DENSE ? 0 : nsel[pair];
-        blk_raw = DENSE ? 0 : sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
-    }
-    constexpr int DPL = HD / 64, NWV = C::NT / 64, QPW = (G + NWV - 1) / NWV;
-    float xq[QPW][DPL];
-    {
-        const int wid = tid >> 6;
-#pragma unroll
-        for (int j = 0; j < QPW; ++j) {
-            const int h = min(wid + j * NWV, G - 1);
-            const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + h) * HD + lane * DPL;
-#pragma unroll
-            for (int k = 0; k < DPL; ++k) xq[j][k] = qh[k];
-        }
-    }
-    const int blk = DENSE ? tile / tpb : blk_raw;
-    // the tile's page-table entry needs only the block: its load goes out
-    // before the length and the count are known (clamped into the table)
-    const int off = (tile % tpb) * 64;
-    const int64_t t0 = (int64_t)blk * g.bt + off;
-    const int t0c = (int)min(max(t0, (int64_t)0), (int64_t)g.pps * g.pt - 1);
-    const int32_t *__restrict__ ptab = v.page_table;
-    const int32_t praw = ptab[(int64_t)cache_seq(g, s) * g.pps + t0c / g.pt];
-    const bool ok = L >= 1 && L <= max_seq_len;
-    int n = 0;
-    if (ok) {
-        n = DENSE ? (L - 1) / g.bt + 1 : n_raw;
-        n = n < max_sel ? n : max_sel;
-    }
-    const int tiles_act = n * tpb;
-    const int parts_act = (tiles_act + TG - 1) / TG;
-    if (ok && part < parts_act) {
-        // the tile's page, computed by every lane of the group (no LDS hand-off)
-        const bool in = tile < tiles_act && blk >= 0 && t0 < L;
-        const bool pg_ok = praw >= 0 && praw < g.n_phys;
-        if (in && !pg_ok && lt == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
-        const int nv = in && pg_ok ? min(64, L - t0c) : 0;
-        const int row0 = t0c % g.pt;
-        const int64_t pbase = (int64_t)(nv > 0 ? praw : 0) * g.page_bytes;
-        const uint8_t *kp = (const uint8_t *)v.k_pages + pbase;
-        const uint8_t *vp = (const uint8_t *)v.v_pages + pbase;
-        const int tl = gh * (g.pt / 64) + row0 / 64;       // tile index inside the pool page
-        // every load of the tile first, in operand layout (lane = 16*lg + hn):
-        // K of cells 16mb+hn, dims 32w+8lg .. +8 (mb = 0..3); V of dims
-        // 32w+16db+hn, cells 32ks+8lg .. +8; the K and V scale rows of cell `lane`
-        const int hn = lane & 15, lg = lane >> 4;
-        const uint8_t *kq = kp + ((int64_t)tl * (HD / 16) + 2 * w + (lg >> 1)) * 1024 + hn * 16 + 8 * (lg & 1);
-        const uint8_t *vq = vp + ((int64_t)tl * HD + 32 * w + hn) * 64 + 8 * lg;
-        uint2 kw[4], vw[2][2];
-        uint16_t dkh[NB], dvh[NB];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kw[i] = make_uint2(0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) vw[i / 2][i % 2] = make_uint2(0, 0);
-#pragma unroll
-        for (int j = 0; j < NB; ++j) dkh[j] = dvh[j] = 0;
-        if (nv > 0) {
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) kw[mb] = *reinterpret_cast<const uint2 *>(kq + mb * 256);
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) vw[db][ks] = *reinterpret_cast<const uint2 *>(vq + db * 1024 + ks * 32);
-            const int64_t so = g.qbytes + ((int64_t)(gh * g.pt + row0 + lane) * NB) * 2;
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                dkh[j] = *reinterpret_cast<const uint16_t *>(kp + so + 2 * j);
-                dvh[j] = *reinterpret_cast<const uint16_t *>(vp + so + 2 * j);
-            }
-        }
-        // The group's query heads split into three int8 parts per head,
-        // q ~= qs * (qa + qb/254 + qc/254^2), qs = amax/127 (residual below
-        // 2e-7 * amax): the operands of exact integer dot products against the
-        // int8 key quants.  One wave per head.
-        {
-            const int wid = tid >> 6;
-#pragma unroll
-            for (int jq = 0; jq < QPW; ++jq) {
-                const int h = wid + jq * NWV;
-                if (h >= G) break;
-                float x[DPL], a = 0.0f;
-#pragma unroll
-                for (int k = 0; k < DPL; ++k) { x[k] = xq[jq][k]; a = fmaxf(a, fabsf(x[k])); }
-                const float amax = wave_max(a);
-                const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-                int8_t *pa = reinterpret_cast<int8_t *>(sh.qa[h]) + lane * DPL;
-                int8_t *pb = reinterpret_cast<int8_t *>(sh.qb[h]) + lane * DPL;
-                int8_t *pc = reinterpret_cast<int8_t *>(sh.qc[h]) + lane * DPL;
-#pragma unroll
-                for (int k = 0; k < DPL; ++k) {
-                    const float t = x[k] * inv;
-                    const float ai = __builtin_rintf(t);
-                    const float r1 = (t - ai) * 254.0f;
-                    const float bi = __builtin_rintf(r1);
-                    const float ci = __builtin_rintf((r1 - bi) * 254.0f);
-                    pa[k] = (int8_t)max(-127, min(127, ai == ai ? (int)ai : 0));
-                    pb[k] = (int8_t)max(-127, min(127, bi == bi ? (int)bi : 0));
-                    pc[k] = (int8_t)max(-127, min(127, ci == ci ? (int)ci : 0));
-                }
-                if (lane == 0) sh.qs[h] = amax / 127.0f;
-            }
-        }
-        __syncthreads();
-        // QK over block w on the matrix cores: exact int32 dots of the key
-        // quants against each query part, combined once in fp32 (the key
-        // scale is applied by the softmax)
-        {
-            const int hq = min(hn, G - 1);
-            uint2 qp[3];
-            {
-                const uint2 *pa = reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(sh.qa[hq]) + 32 * w + 8 * lg);
-                const uint2 *pb = reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(sh.qb[hq]) + 32 * w + 8 * lg);
-                const uint2 *pc = reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(sh.qc[hq]) + 32 * w + 8 * lg);
-                const uint2 z = make_uint2(0, 0);
-                qp[0] = hn < G ? *pa : z;
-                qp[1] = hn < G ? *pb : z;
-                qp[2] = hn < G ? *pc : z;
-            }
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const i4v zero = {0, 0, 0, 0};
-                const i4v da = mfma_i8(kw[mb], qp[0], zero);
-                const i4v db = mfma_i8(kw[mb], qp[1], zero);
-                const i4v dc = mfma_i8(kw[mb], qp[2], zero);
-                float r[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    r[i] = (float)da[i] + ((float)db[i] + (float)dc[i] * (1.0f / 254.0f)) * (1.0f / 254.0f);
-                if (hn < G)
-                    *reinterpret_cast<float4 *>(&gr.lg[w][hn][16 * mb + 4 * lg]) = make_float4(r[0], r[1], r[2], r[3]);
-            }
-        }
-        __syncthreads();
-        // softmax: wave w owns heads w, w+NB, ...; lane = cell
-        {
-            const bool valid = lane < nv;
-            float dvf[NB], dvm = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NB; ++j) { dvf[j] = valid ? h2f(dvh[j]) : 0.0f; dvm = fmaxf(dvm, dvf[j]); }
-            dvm = wave_max(valid ? dvm : 0.0f);
-            int e = 0;
-            frexpf(dvm, &e);
-            const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e) : 1.0f;
-            float dkf[NB];
-#pragma unroll
-            for (int j = 0; j < NB; ++j) dkf[j] = h2f(dkh[j]);
-            for (int h = w; h < G; h += NB) {
-#pragma clang fp contract(off)
-                float lsum = dkf[0] * gr.lg[0][h][lane];
-#pragma unroll
-                for (int ww = 1; ww < NB; ++ww) lsum += dkf[ww] * gr.lg[ww][h][lane];
-                const float s2 = valid ? lsum * sh.qs[h] * g.scale_log2 : -INFINITY;
-                const float m = wave_max(s2);
-                const float p = valid ? exp2f(s2 - m) : 0.0f;
-                const float l = wave_sum(p);
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const float pj = p * dvf[j] * up;
-                    const uint16_t hi = f2h(pj);
-                    gr.pp[h][j][lane] = hi;
-                    gr.pl[h][j][lane] = f2h(pj - h2f(hi));
-                }
-                if (lane == 0) { gr.m[h] = m; gr.l[h] = l; }
-            }
-            const float down = 1.0f / up;              // exact: up is a power of two
-            __syncthreads();
-            // PV on the matrix cores: O[dim][head] over dims 32w+16db .. +16,
-            // cells in two steps of 32, p' high then low
-            {
-                const int hq = min(hn, G - 1);
-                f4v o2[2] = {f4v{0.0f, 0.0f, 0.0f, 0.0f}, f4v{0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const h8v z = {};
-                    const h8v bh = hn < G ? *reinterpret_cast<const h8v *>(&gr.pp[hq][w][32 * ks + 8 * lg]) : z;
-                    const h8v bl = hn < G ? *reinterpret_cast<const h8v *>(&gr.pl[hq][w][32 * ks + 8 * lg]) : z;
-#pragma unroll
-                    for (int db = 0; db < 2; ++db) {
-                        const h8v va = q8x8_to_h8(vw[db][ks]);
-                        o2[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, bh, o2[db], 0, 0, 0);
-                        o2[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, bl, o2[db], 0, 0, 0);
-                    }
-                }
-                if (hn < G) {
-#pragma unroll
-                    for (int db = 0; db < 2; ++db)
-                        *reinterpret_cast<float4 *>(&gr.o[hn][32 * w + 16 * db + 4 * lg]) =
-                            make_float4(o2[db][0] * down, o2[db][1] * down, o2[db][2] * down, o2[db][3] * down);
-                }
-            }
-        }
-        __syncthreads();
-        // merge the TG tiles into this workgroup's partial (unnormalised O, max, sum)
-        const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
-#pragma unroll
-        for (int r = 0; r < C::OPT; ++r) {
-            const int k = tid + r * C::NT;
-            if (k < G * HD) {
-                const int h = k / HD, dd = k % HD;
-                float M = -INFINITY;
-#pragma unroll
-                for (int t = 0; t < TG; ++t)
-                    if (part * TG + t < tiles_act) M = fmaxf(M, sh.grp[t].m[h]);
-                float O = 0.0f, Ls = 0.0f;
-#pragma unroll
-                for (int t = 0; t < TG; ++t) {
-                    if (part * TG + t < tiles_act) {
-                        const float mt = sh.grp[t].m[h];
-                        const float wt = mt == -INFINITY ? 0.0f : exp2f(mt - M);
-                        O += wt * sh.grp[t].o[h][dd];
-                        Ls += wt * sh.grp[t].l[h];
-                    }
-                }
-                ws.part_o[pb * HD + k] = O;
-                if (dd == 0) {
-                    ws.part_ml[(pb + h) * 2 + 0] = M;
-                    ws.part_ml[(pb + h) * 2 + 1] = Ls;
-                }
-            }
-        }
-    }
-}
-
-template <int HD, int G, int TG>
-static void launch_attn_q8_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
-                             int32_t n_seq,
-                             int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
-                             float *out, const Ws &ws, hipStream_t st) {
-    const int n_parts = (ws.n_tiles + TG - 1) / TG;
-    const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
-    if (sel)
-        hipLaunchKernelGGL((k_attn_q8<HD, G, TG, false>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q,
-                           seq_len, max_seq_len, sel, nsel, max_sel, out, ws);
-    else
-        hipLaunchKernelGGL((k_attn_q8<HD, G, TG, true>), grid, dim3(FastCfg<HD, G, TG>::NT), 0, st, g, v, q,
-                           seq_len, max_seq_len, sel, nsel, max_sel, out, ws);
     launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
 }
 
@@ -3348,28 +2849,12 @@ hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float
     return hipErrorInvalidValue;
 }
 
-// q8_0 fast attention instantiations (head_dim, group, tiles per workgroup);
-// used when block_tokens is a multiple of 64.  One sequence wants small
-// workgroups (latency: the compute phase runs with fewer waves per CU); a
-// batch of sequences fills the chip anyway and wants fewer partials to merge.
-#define QWFN_FOR_EACH_FAST_BATCH(X) X(128, 8, 4)
-constexpr int32_t kFastBatchSeqs = 4;              // from this many sequences on
-#define QWFN_FOR_EACH_FAST(X) X(128, 8, 2) X(128, 4, 2) X(128, 2, 2) X(64, 8, 2) X(256, 12, 1) X(256, 8, 1)
-
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,
                             float *out, const Ws &ws, hipStream_t st) {
-    if (g.vdim) {
-#define F(HD_, G_, TG_)                                                                          \
-        if (g.hd == HD_ && g.G == G_) {                                                          \
-            launch_attn_q8_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
-            return hipGetLastError();                                                            \
-        }
-        if (n_seq >= kFastBatchSeqs) { QWFN_FOR_EACH_FAST_BATCH(F) }
-        QWFN_FOR_EACH_FAST(F)
-#undef F
-    }
+    if (dec_kernels_for(g))
+        return launch_dec_attention(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, false, st);
 #define X(HD_, G_, TG_)                                                                         \
     if (g.hd == HD_ && g.G == G_) {                                                             \
         launch_attn_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
@@ -3385,21 +2870,11 @@ hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
 // eight); past it the chip fills and the redundant selections would compete.
 constexpr int32_t kAttnSelSeqs = 8;
 
-// The matrix-core kernel's selecting variant for its shapes, the general
-// kernel's for every other element type and block size.
-static bool attn_select_fast(const Geo &g) {
-    if (!g.vdim) return false;
-#define F(HD_, G_, TG_) if (g.hd == HD_ && g.G == G_) return true;
-    QWFN_FOR_EACH_FAST(F)
-#undef F
-    return false;
-}
-
 bool attn_select_fits(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max_sel) {
-    if (g.shared || g.topk <= 0 || g.pf || n_seq > kAttnSelSeqs || max_sel > kAttnSelMax ||
-        max_seq_len / g.bt > kKeysMax)
-        return false;
-    if (attn_select_fast(g)) return true;
+    if (g.shared || g.topk <= 0 || g.pf || n_seq > kAttnSelSeqs) return false;
+    if (dec_kernels_for(g))
+        return dec_select_fits(g, max_seq_len, max_sel);
+    if (max_sel > kAttnSelMax || max_seq_len / g.bt > kKeysMax) return false;
 #define X(HD_, G_, TG_) if (g.hd == HD_ && g.G == G_) return true;
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
@@ -3410,26 +2885,15 @@ hipError_t launch_attention_select(const Geo &g, const qwfn_kv_view &v, const fl
                                    int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel,
                                    int32_t max_sel, float *out, const Ws &ws, hipStream_t st) {
     if (!attn_select_fits(g, n_seq, max_seq_len, max_sel)) return hipErrorInvalidValue;
-    if (!attn_select_fast(g)) {
+    if (dec_kernels_for(g))
+        return launch_dec_attention(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, true, st);
 #define X(HD_, G_, TG_)                                                                                     \
-        if (g.hd == HD_ && g.G == G_) {                                                                     \
-            launch_attn_sel_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
-            return hipGetLastError();                                                                       \
-        }
-        QWFN_FOR_EACH_SHAPE(X)
+    if (g.hd == HD_ && g.G == G_) {                                                                         \
+        launch_attn_sel_t<HD_, G_, TG_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st); \
+        return hipGetLastError();                                                                           \
+    }
+    QWFN_FOR_EACH_SHAPE(X)
 #undef X
-        return hipErrorInvalidValue;
-    }
-#define F(HD_, G_, TG_)                                                                                          \
-    if (g.hd == HD_ && g.G == G_) {                                                                              \
-        const dim3 grid((unsigned)((ws.n_tiles + TG_ - 1) / TG_), (unsigned)g.Hkv, (unsigned)n_seq);            \
-        hipLaunchKernelGGL((k_attn_q8<HD_, G_, TG_, false, true>), grid, dim3(FastCfg<HD_, G_, TG_>::NT), 0, st, \
-                           g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, out, ws);                          \
-        launch_merge_t<G_, HD_>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG_, st);      \
-        return hipGetLastError();                                                                                \
-    }
-    QWFN_FOR_EACH_FAST(F)
-#undef F
     return hipErrorInvalidValue;
 }
 
