@@ -18,8 +18,16 @@ indexer workgroup selects).  The decode position advances one token per step
 one step in 64 completes a block and pools it, as in a real decode; every
 replica keeps its own position and its caches have room for DECODE_ROOM more
 tokens past the context.
-Inputs are resident in HBM before the timed region; per-context working sets
-below 512 MiB are replicated and rotated so the 256 MB MALL does not serve them.
+Inputs are resident in HBM before the timed region.  Each context keeps enough
+replicas of its 12-layer stack (each with its own queries and new rows) that a
+step's bytes -- the selected K/V and the pooled keys it reads -- come round
+again only after 512 MiB of other replicas' bytes, so the 256 MB MALL does not
+serve them; consecutive steps use consecutive replicas.
+
+The roofline is the attention launch's: its algorithmic bytes (the selected
+K/V) over its own average duration, which an eager pass over the same
+replicas measures per launch with HIP events that hipExtLaunchKernel stamps
+with the kernel's begin and end (qwfn_qsa_time_next_call).
 
 Prints one JSON line: value = us per layer at the largest context.
 """
@@ -110,9 +118,54 @@ def selected_cells(sel, nsel, lengths, bt):
     return tot
 
 
+def kv_row_bytes(cfg):
+    """Bytes of one token's K (or V) head row: q8_0 136, q4_0 72, fp16 256 at head_dim 128."""
+    return {0: cfg.head_dim + cfg.head_dim // 16, 1: cfg.head_dim // 2 + cfg.head_dim // 16,
+            2: 2 * cfg.head_dim}[cfg.kv_type]
+
+
+def best_launch(graph_ms, eager_ms):
+    """The faster of the two ways a caller runs the step: one hipGraph replay
+    a step, or the calls launched one by one (both time the same K steps of
+    the same work; each graph replay also pays the runtime's fixed cost of a
+    graph launch, about 7 us here)."""
+    if graph_ms is not None and graph_ms <= eager_ms:
+        return graph_ms, "hipGraph (one replay a step)"
+    return eager_ms, "eager (one launch a kernel)"
+
+
+def dominant_kernel(cfg, max_len, two_call):
+    """rocprofv3's name of the attention launch a decode layer makes at
+    sequences up to max_len tokens (the selecting variant in the fused call:
+    its keys-per-thread tier covers max_len / block_tokens blocks)."""
+    if two_call:
+        return f"k_dec<{cfg.head_dim}, {cfg.n_head // cfg.n_head_kv}, 0, 4>"
+    span = max_len // cfg.block_tokens - (cfg.sink_blocks & ~3)
+    kpt = next(k for k in (4, 8, 16, 32) if span <= k * 256)
+    return f"k_dec<{cfg.head_dim}, {cfg.n_head // cfg.n_head_kv}, 2, {kpt}>"
+
+
+def touched_bytes_per_layer(cfg, lengths):
+    """HBM bytes one decode layer touches at most: every sequence's selected
+    K/V (the forced and top-k blocks whole, K and V) and its pooled keys."""
+    if cfg.top_k_blocks == 0:
+        keep = None
+    else:
+        keep = (cfg.top_k_blocks + cfg.sink_blocks + cfg.local_tokens // cfg.block_tokens + 2) * cfg.block_tokens
+    tot = 0
+    for L in lengths:
+        tot += (L if keep is None else min(L, keep)) * cfg.n_head_kv * kv_row_bytes(cfg) * 2
+        tot += (L // cfg.block_tokens) * cfg.n_head_kv * cfg.head_dim * 4
+    return tot
+
+
 class Runner:
     """n_inst replicas of an n_layer stack of caches at fixed sequence lengths,
-    stepped by the fused decode (append+select, attention per layer)."""
+    stepped one decode token at a time.  Consecutive steps use consecutive
+    replicas, and there are enough of them that a step's bytes are touched
+    again only after ROTATE_BYTES of other replicas' bytes, more than the
+    256 MB MALL holds.  Every replica has its own queries and new K/V rows, so
+    its selections differ from its neighbours'."""
 
     def __init__(self, qsa, torch, cfg, lengths, n_layer, pages_per_seq, page_table, gen, fused=False):
         self.qsa, self.torch, self.cfg = qsa, torch, cfg
@@ -122,9 +175,8 @@ class Runner:
         self.n_seq = n_seq
         self.max_len = max(lengths) + DECODE_ROOM
         assert pages_per_seq * cfg.page_tokens >= self.max_len, "page table leaves no decode room"
-        pb = cfg.page_bytes()
-        per_stack = n_layer * 2 * page_table.numel() * pb
-        self.n_inst = max(1, math.ceil(ROTATE_BYTES / per_stack))
+        self.touched_per_step = n_layer * touched_bytes_per_layer(cfg, lengths)
+        self.n_inst = max(1, math.ceil(ROTATE_BYTES / self.touched_per_step))
         self.stacks = []
         for _ in range(self.n_inst):
             layers = []
@@ -134,12 +186,10 @@ class Runner:
                 fill_layer(qsa, torch, c, lengths, gen)
                 layers.append(c)
             self.stacks.append(layers)
-        self.q = [torch.randn((n_seq, cfg.n_head, cfg.head_dim), device="cuda", generator=gen)
-                  for _ in range(n_layer)]
-        self.kn = [torch.randn((n_seq, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
-                   for _ in range(n_layer)]
-        self.vn = [torch.randn((n_seq, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
-                   for _ in range(n_layer)]
+        r = lambda *shape: torch.randn(shape, device="cuda", generator=gen)
+        self.q = [[r(n_seq, cfg.n_head, cfg.head_dim) for _ in range(n_layer)] for _ in range(self.n_inst)]
+        self.kn = [[r(n_seq, cfg.n_head_kv, cfg.head_dim) for _ in range(n_layer)] for _ in range(self.n_inst)]
+        self.vn = [[r(n_seq, cfg.n_head_kv, cfg.head_dim) for _ in range(n_layer)] for _ in range(self.n_inst)]
         self.out = [torch.empty((n_seq, cfg.n_head, cfg.head_dim), device="cuda") for _ in range(n_layer)]
         # one position per replica, advanced by one token at the start of every step
         self.seq_lens = [torch.tensor(lengths, dtype=torch.int32, device="cuda") for _ in range(self.n_inst)]
@@ -155,17 +205,25 @@ class Runner:
                 if qsa.read_status(c):
                     raise RuntimeError("cache fill reported out-of-range rows")
 
-    def layer(self, inst, il):
+    def layer(self, inst, il, timers=None):
+        """One layer's decode call(s).  timers: {kernel: (start, end)} events
+        armed on the call(s) (qwfn_qsa_time_next_call)."""
         qsa = self.qsa
         c = self.stacks[inst][il]
         sl = self.seq_lens[inst]
+        q, kn, vn = self.q[inst][il], self.kn[inst][il], self.vn[inst][il]
         if self.fused:                                  # qwfn_sparse_attn_decode: one call
-            qsa.sparse_attn_decode(c, self.q[il], self.kn[il], self.vn[il], sl, self.max_len, self.ws,
-                                   out=self.out[il], sel=self.sel, n_sel=self.nsel)
+            if timers:
+                qsa.time_next_call(timers)
+            qsa.sparse_attn_decode(c, q, kn, vn, sl, self.max_len, self.ws, out=self.out[il], sel=self.sel,
+                                   n_sel=self.nsel)
             return
-        qsa.decode_append_select(c, self.q[il], self.kn[il], self.vn[il], sl, self.max_len, self.ws,
-                                 self.sel, self.nsel)
-        qsa.sparse_decode_attn(c, self.q[il], sl, self.max_len, self.ws, self.sel, self.nsel, out=self.out[il])
+        if timers:
+            qsa.time_next_call({"indexer": timers["indexer"]})
+        qsa.decode_append_select(c, q, kn, vn, sl, self.max_len, self.ws, self.sel, self.nsel)
+        if timers:
+            qsa.time_next_call({k: timers[k] for k in ("attention", "merge")})
+        qsa.sparse_decode_attn(c, q, sl, self.max_len, self.ws, self.sel, self.nsel, out=self.out[il])
 
     def advance(self, inst):
         """Next decode position of replica inst (one small device op, part of the step)."""
@@ -184,7 +242,7 @@ class Runner:
                 raise RuntimeError("decode ran past DECODE_ROOM; raise it or take fewer steps")
 
     def capture(self):
-        """One hipGraph per replica holding a whole step (2 launches per layer).
+        """One hipGraph per replica holding a whole step (3 launches per layer).
         Every replay is checked against an eager step on the same inputs."""
         torch = self.torch
         s = torch.cuda.Stream()
@@ -234,62 +292,50 @@ class Runner:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps            # ms per step
 
-    def time_kernels(self, steps, per_graph=16):
-        """Average device time per call of the two-call path's pieces:
-        qwfn_decode_append_select (append, pooling, scores, the selection by
-        the indexer's last workgroup) and qwfn_sparse_decode_attn (attention
-        over that selection, then the merge).  Each is captured `per_graph`
-        times back to back (layer 0 of every replica in turn, after a step has
-        set the selection; both are idempotent at a fixed position), and the
-        replays are timed with HIP events on the capturing stream."""
+    def time_kernels(self, steps):
+        """Each decode kernel's own duration in us, averaged over every layer of
+        `steps` eager steps that rotate the replicas as the timed region does.
+        Every call is armed with qwfn_qsa_time_next_call: its indexer,
+        attention and merge launches go through hipExtLaunchKernel, which
+        stamps a pair of HIP events with that kernel's begin and end on the
+        stream it runs on (what rocprofv3's kernel trace reports)."""
         torch, qsa = self.torch, self.qsa
-        self.step(0)
+        names = qsa.TIMED_KERNELS
+        ev = [{k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for k in names}
+              for _ in range(self.n_layer)]
+        for row in ev:
+            for a, b in row.values():
+                a.record()
+                b.record()
         torch.cuda.synchronize()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        gs, ga = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(gs, stream=s):
-                for k in range(per_graph):
-                    c = self.stacks[k % self.n_inst][0]
-                    qsa.decode_append_select(c, self.q[0], self.kn[0], self.vn[0], self.seq_lens[k % self.n_inst],
-                                             self.max_len, self.ws, self.sel, self.nsel)
-            with torch.cuda.graph(ga, stream=s):
-                for k in range(per_graph):
-                    c = self.stacks[k % self.n_inst][0]
-                    qsa.sparse_decode_attn(c, self.q[0], self.seq_lens[k % self.n_inst], self.max_len, self.ws,
-                                           self.sel, self.nsel, out=self.out[0])
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        res = []
-        for g in (gs, ga):
-            g.replay()
+        tot = dict.fromkeys(names, 0.0)
+        for i in range(steps):
+            inst = i % self.n_inst
+            self.advance(inst)
+            for il in range(self.n_layer):
+                self.layer(inst, il, timers=ev[il])
             torch.cuda.synchronize()
-            reps = max(1, steps // per_graph)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            with torch.cuda.stream(s):
-                e0.record(s)
-                for _ in range(reps):
-                    g.replay()
-                e1.record(s)
-            torch.cuda.synchronize()
-            res.append(e0.elapsed_time(e1) / (reps * per_graph) * 1e3)
-        return res[0], res[1]
+            for row in ev:
+                for k, (a, b) in row.items():
+                    tot[k] += a.elapsed_time(b)
+        n = steps * self.n_layer
+        return {k: v / n * 1e3 for k, v in tot.items()}, n
 
     def bytes_per_layer(self):
-        """Algorithmic bytes of one layer: selected KV (q8_0, K and V) read by the
-        attention kernel; pooled keys scanned by the select kernel."""
+        """Algorithmic bytes of one layer, averaged over one fresh step of every
+        replica (its last layer's selection): the selected K/V (q8_0 / q4_0 /
+        fp16 rows of K and V) the attention reads, the pooled keys the indexer
+        scans."""
         cfg = self.cfg
-        self.step(0)                        # a fresh selection at replica 0's current position
-        self.torch.cuda.synchronize()
-        lengths = [int(x) for x in self.seq_lens[0].tolist()]
-        sel = self.sel.cpu().numpy()
-        nsel = self.nsel.cpu().numpy()
-        cells = selected_cells(sel, nsel, lengths, cfg.block_tokens)
-        # bytes per (token, KV head): q8_0 136 B, q4_0 72 B, fp16 256 B at head_dim 128
-        row = {0: cfg.head_dim + cfg.head_dim // 16, 1: cfg.head_dim // 2 + cfg.head_dim // 16,
-               2: 2 * cfg.head_dim}[cfg.kv_type]
-        kv = cells * row * 2
+        cells = 0
+        lengths = None
+        for inst in range(self.n_inst):
+            self.step(inst)
+            self.torch.cuda.synchronize()
+            lengths = [int(x) for x in self.seq_lens[inst].tolist()]
+            cells += selected_cells(self.sel.cpu().numpy(), self.nsel.cpu().numpy(), lengths, cfg.block_tokens)
+        cells = cells / self.n_inst
+        kv = cells * kv_row_bytes(cfg) * 2
         pooled = 0
         for L in lengths:
             last = L - 1
@@ -580,22 +626,23 @@ def main():
         if not args.no_graph:
             r.capture()
             graph_ms = r.time_steps(args.steps, args.warmup, graph=True)
-        sel_us, att_us = r.time_kernels(max(64, args.steps))
+        kern, n_timed = r.time_kernels(args.steps)
         r.check_room()
         kv, pooled, cells = r.bytes_per_layer()
-        ms = graph_ms if graph_ms is not None else eager_ms
-        res = dict(us_per_layer=ms * 1e3 / args.layers, eager_us_per_layer=eager_ms * 1e3 / args.layers,
+        ms, mode = best_launch(graph_ms, eager_ms)
+        res = dict(us_per_layer=ms * 1e3 / args.layers, launch=mode, eager_us_per_layer=eager_ms * 1e3 / args.layers,
                    graph_us_per_layer=None if graph_ms is None else graph_ms * 1e3 / args.layers,
-                   ms_per_step=ms, select_kernel_us=sel_us, attn_kernel_us=att_us,
+                   ms_per_step=ms, kernel_us=kern, kernel_launches_timed=n_timed,
                    selected_kv_bytes=kv, pooled_scan_bytes=pooled, cells_per_layer=cells,
-                   replicas=r.n_inst)
-        res["attn_gbs"] = kv / (att_us * 1e-6) / 1e9
+                   replicas=r.n_inst, touched_bytes_per_step=r.touched_per_step)
+        res["attn_gbs"] = kv / (kern["attention"] * 1e-6) / 1e9
         res["layer_gbs_selected"] = kv / (res["us_per_layer"] * 1e-6) / 1e9
         res["layer_gbs_all"] = (kv + pooled) / (res["us_per_layer"] * 1e-6) / 1e9
         per_ctx[ctx] = res
-        log(f"[bench] ctx {ctx}: {res['us_per_layer']:.2f} us/layer (eager {res['eager_us_per_layer']:.2f}), "
-            f"select {sel_us:.2f} us, attn {att_us:.2f} us = {res['attn_gbs']:.0f} GB/s on {kv} B, "
-            f"pooled scan {pooled} B, replicas {r.n_inst}")
+        log(f"[bench] ctx {ctx}: {res['us_per_layer']:.2f} us/layer (eager {res['eager_us_per_layer']:.2f}); "
+            f"kernels: indexer {kern['indexer']:.2f} us, attention {kern['attention']:.2f} us "
+            f"= {res['attn_gbs']:.0f} GB/s on {kv:.0f} B, merge {kern['merge']:.2f} us; "
+            f"pooled scan {pooled} B; {r.n_inst} replicas x {r.touched_per_step / 2**20:.1f} MiB touched a step")
         del r
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
@@ -615,9 +662,9 @@ def main():
                 graph_ms = r.time_steps(args.steps, args.warmup, graph=True)
             r.check_room()
             kv, _, cells = r.bytes_per_layer()
-            ms = graph_ms if graph_ms is not None else eager_ms
+            ms, mode = best_launch(graph_ms, eager_ms)
             us = ms * 1e3 / args.layers
-            extra[name] = dict(context=ctx, us_per_layer=round(us, 3),
+            extra[name] = dict(context=ctx, us_per_layer=round(us, 3), launch=mode,
                                eager_us_per_layer=round(eager_ms * 1e3 / args.layers, 3),
                                cells_per_layer=cells, selected_kv_bytes=kv,
                                layer_gbs_selected=round(kv / (us * 1e-6) / 1e9, 1))
@@ -635,16 +682,25 @@ def main():
         pps = (max(lens) + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         perm = torch.from_numpy(rng.permutation(8 * pps).astype(np.int32)).view(8, pps)
         r = Runner(qsa, torch, cfg, lens, 1, pps, perm, gen, fused=not args.two_call)
-        ms = r.time_steps(args.steps, args.warmup, graph=False)
-        sel_us, att_us = r.time_kernels(max(64, args.steps))
+        eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
+        graph_ms = None
+        if not args.no_graph:
+            r.capture()
+            graph_ms = r.time_steps(args.steps, args.warmup, graph=True)
+        kern, n_timed = r.time_kernels(args.steps)
         r.check_room()
         kv, pooled, cells = r.bytes_per_layer()
-        batched = dict(lengths=lens, us_per_launch_pair=ms * 1e3, select_kernel_us=sel_us, attn_kernel_us=att_us,
-                       selected_kv_bytes=kv, pooled_scan_bytes=pooled,
-                       attn_gbs=kv / (att_us * 1e-6) / 1e9,
-                       attn_frac=kv / (att_us * 1e-6) / 1e9 / HBM_PEAK_GBS)
-        log(f"[bench] config 5 batched (8 seqs {lens}): {ms * 1e3:.2f} us per layer-step, attn {att_us:.2f} us "
-            f"= {batched['attn_gbs']:.0f} GB/s")
+        ms, mode = best_launch(graph_ms, eager_ms)
+        batched = dict(lengths=lens, us_per_step=ms * 1e3, launch=mode, eager_us_per_step=eager_ms * 1e3,
+                       graph_us_per_step=None if graph_ms is None else graph_ms * 1e3,
+                       kernel_us=kern, kernel_launches_timed=n_timed, selected_kv_bytes=kv,
+                       pooled_scan_bytes=pooled, replicas=r.n_inst, touched_bytes_per_step=r.touched_per_step,
+                       attn_gbs=kv / (kern["attention"] * 1e-6) / 1e9,
+                       attn_frac=kv / (kern["attention"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                       step_gbs=kv / (ms * 1e-3) / 1e9)
+        log(f"[bench] config 5 batched (8 seqs {lens}): {ms * 1e3:.2f} us a step (eager {eager_ms * 1e3:.2f}); "
+            f"indexer {kern['indexer']:.2f} us, attention {kern['attention']:.2f} us = {batched['attn_gbs']:.0f} "
+            f"GB/s, merge {kern['merge']:.2f} us; {r.n_inst} replicas")
         del r
         torch.cuda.empty_cache()
 
@@ -666,15 +722,16 @@ def main():
             r = Runner(qsa, torch, c2, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
             r.capture()
             ms = r.time_steps(max(30, args.steps // 3), args.warmup, graph=True)
-            sel_us, att_us = r.time_kernels(64)
+            kern, n_timed = r.time_kernels(max(30, args.steps // 3))
             r.check_room()
             kv, pooled, cells = r.bytes_per_layer()
             kv_types[name] = dict(context=ctx, us_per_layer=round(ms * 1e3 / args.layers, 3),
-                                  select_kernel_us=round(sel_us, 3), attn_kernel_us=round(att_us, 3),
+                                  kernel_us={k: round(v, 3) for k, v in kern.items()},
                                   cells_per_layer=cells, selected_kv_bytes=kv,
-                                  attn_gbs=round(kv / (att_us * 1e-6) / 1e9, 1), replicas=r.n_inst)
-            log(f"[bench] kv {name} ctx {ctx}: {ms * 1e3 / args.layers:.2f} us/layer, select {sel_us:.2f} us, "
-                f"attn {att_us:.2f} us (general attention kernel)")
+                                  attn_gbs=round(kv / (kern["attention"] * 1e-6) / 1e9, 1), replicas=r.n_inst)
+            log(f"[bench] kv {name} ctx {ctx}: {ms * 1e3 / args.layers:.2f} us/layer, indexer "
+                f"{kern['indexer']:.2f} us, attention {kern['attention']:.2f} us, merge {kern['merge']:.2f} us "
+                f"(general attention kernel)")
             del r
             torch.cuda.empty_cache()
 
@@ -709,12 +766,13 @@ def main():
         log(f"[bench] cpu baseline: {cpu_us:.1f} us/layer on {threads} threads ({n} steps)")
 
     attn_gbs = top["attn_gbs"]
+    dom = dominant_kernel(cfg, big + DECODE_ROOM, args.two_call)
     traffic = None
     if os.path.exists(TRAFFIC_JSON):
         with open(TRAFFIC_JSON) as f:
-            tj = json.load(f).get("attention_call", {})
+            tj = json.load(f).get(dom, {})
         if tj.get("context") == big:
-            traffic = tj.get("hbm_bytes_per_call")
+            traffic = tj.get("hbm_bytes_per_launch")
     line = {
         "metric": METRIC,
         "value": round(top["us_per_layer"], 3),
@@ -732,7 +790,7 @@ def main():
             "workload": f"config3: {args.layers} sparse layers, ctx {big}, 16q/2kv heads x 128, q8_0 KV, "
                         f"top-64 64-token blocks + block 0 + 512-token window, 1 decode token/step",
             "contexts": contexts,
-            "launch": "hipGraph" if top["graph_us_per_layer"] is not None else "eager",
+            "launch": top["launch"],
             "decode_call": "qwfn_decode_append_select + qwfn_sparse_decode_attn" if args.two_call
                            else "qwfn_sparse_attn_decode (fused: the attention selects)",
         },
@@ -742,16 +800,22 @@ def main():
                         for c, v in per_ctx.items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": "sparse decode attention call over a given selection (qwfn_sparse_decode_attn): "
-                      "k_attn_q8 (selected q8_0 K+V, split into partials), then k_merge (one workgroup per "
-                      "query head combines them)",
+            "kernel": dom,
+            "kernel_role": "the timed step's attention launch: selects its (KV head's) blocks from the indexer's "
+                           "scores, then attends over the selected q8_0 K/V on the matrix cores, one partial "
+                           "per workgroup (k_merge combines them)" if not args.two_call else
+                           "the two-call step's attention launch over a given selection",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "bytes_per_launch": top["selected_kv_bytes"],
-            "launch_us": round(top["attn_kernel_us"], 3),
+            "bytes_per_launch": round(top["selected_kv_bytes"]),
+            "bytes": "algorithmic: the selected cells' q8_0 K and V rows (136 B each per KV head)",
+            "launch_us": round(top["kernel_us"]["attention"], 3),
+            "launches_timed": top["kernel_launches_timed"],
+            "timing": "each launch's own begin/end: HIP events stamped by hipExtLaunchKernel on its stream "
+                      "(qwfn_qsa_time_next_call), over eager steps rotating the replicas like the timed region",
         },
         "layer_roofline_frac": round(top["layer_gbs_selected"] / HBM_PEAK_GBS, 4),
         "configs_1_2": extra,

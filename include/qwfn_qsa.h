@@ -141,6 +141,17 @@ typedef struct qwfn_kv_view {
 /* ---- introspection / sizing ------------------------------------------------ */
 int         qwfn_qsa_abi_version(void);
 const char *qwfn_qsa_last_error(void);
+/* Measurement hook; it has no counterpart in the reference and serves
+ * benchmarks and profilers of the path.  Arms per-kernel timing of the next
+ * qwfn_sparse_attn_decode / qwfn_decode_append_select /
+ * qwfn_sparse_decode_attn call on the calling thread.  events[0..5] are
+ * hipEvent_t created with timing (or NULL pairs): (0, 1) the indexer launch,
+ * (2, 3) the attention launch, (4, 5) the merge launch.  Each armed kernel is
+ * launched with hipExtLaunchKernel, which stamps its pair with that kernel's
+ * own begin and end; read them with hipEventElapsedTime once the stream has
+ * completed.  A call on a capturing stream times nothing.  The call disarms
+ * what it did not use; events == NULL disarms.                               */
+int         qwfn_qsa_time_next_call(void *const events[6]);
 /* Validates a shape (QWFN_EINVAL) and whether this build has kernels for it
  * (QWFN_ENOTSUP).  Replaces the reference's shape constants
  * (src/qwfn_hparams.h:22-36, src/qwfn_engine.cpp:382-435).                   */

@@ -33,6 +33,7 @@ STATUS_BLOCK_RANGE = 0x10
 EXPORTS = (
     "qwfn_qsa_abi_version",
     "qwfn_qsa_last_error",
+    "qwfn_qsa_time_next_call",
     "qwfn_qsa_check_shape",
     "qwfn_qsa_page_bytes",
     "qwfn_qsa_pooled_bytes",
@@ -134,6 +135,7 @@ _Z = C.c_size_t
 _SIGS = {
     "qwfn_qsa_abi_version": (C.c_int, []),
     "qwfn_qsa_last_error": (C.c_char_p, []),
+    "qwfn_qsa_time_next_call": (C.c_int, [C.POINTER(C.c_void_p)]),
     "qwfn_qsa_check_shape": (C.c_int, [_S]),
     "qwfn_qsa_page_bytes": (C.c_int, [_S, C.POINTER(_Z)]),
     "qwfn_qsa_pooled_bytes": (C.c_int, [_S, _I, _I, C.POINTER(_Z)]),

@@ -14,9 +14,17 @@
 
 using namespace qwfn_qsa;
 
+thread_local KernelTimer qwfn_qsa::g_kernel_timer{};
+
 namespace {
 
 thread_local std::string g_err;
+
+// Disarms, on return from a decode entry point, the kernel timing its call
+// did not use (qwfn_qsa_time_next_call arms it for one call only).
+struct TimerDisarm {
+    ~TimerDisarm() { g_kernel_timer = KernelTimer{}; }
+};
 
 int fail(int code, const char *fmt, ...) {
     char buf[512];
@@ -210,6 +218,20 @@ int qwfn_qsa_abi_version(void) { return QWFN_QSA_ABI_VERSION; }
 
 const char *qwfn_qsa_last_error(void) { return g_err.c_str(); }
 
+int qwfn_qsa_time_next_call(void *const events[6]) {
+    g_kernel_timer = KernelTimer{};
+    if (!events) return ok();
+    for (int k = 0; k < kTimedKinds; ++k)
+        if ((events[2 * k] == nullptr) != (events[2 * k + 1] == nullptr))
+            return fail(QWFN_EINVAL, "time_next_call: kernel %d has a start event without a stop event, or "
+                                     "the reverse", k);
+    for (int k = 0; k < kTimedKinds; ++k) {
+        g_kernel_timer.ev[k][0] = (hipEvent_t)events[2 * k];
+        g_kernel_timer.ev[k][1] = (hipEvent_t)events[2 * k + 1];
+    }
+    return ok();
+}
+
 int qwfn_qsa_check_shape(const qwfn_qsa_shape *shape) {
     const int rc = check_shape(shape);
     return rc ? rc : ok();
@@ -396,6 +418,7 @@ int qwfn_sparse_decode_attn(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *n_sel, int32_t max_sel, float *out,
                             void *ws, size_t ws_bytes, void *stream) {
+    TimerDisarm disarm;
     Geo g;
     int rc = make_geo(shape, view, &g);
     if (rc) return rc;
@@ -420,6 +443,7 @@ int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *v
                               const void *k_new, const void *v_new, int32_t src_dtype,
                               const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, int32_t *sel,
                               int32_t *n_sel, int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+    TimerDisarm disarm;
     Geo g;
     int rc = make_geo(shape, view, &g);
     if (rc) return rc;
@@ -445,6 +469,7 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, float *out,
                             int32_t *sel_out, int32_t *n_sel_out, void *ws, size_t ws_bytes,
                             void *stream) {
+    TimerDisarm disarm;
     Geo g;
     int rc = make_geo(shape, view, &g);
     if (rc) return rc;

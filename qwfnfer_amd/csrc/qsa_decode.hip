@@ -647,8 +647,9 @@ void launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int
                   int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, int32_t tpw,
                   hipStream_t st) {
     const int parts = (ws.n_tiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_dec<HD, G, MODE, KPT>), dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq),
-                       dim3(kDecThreads), 0, st, g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, ws, tpw);
+    QWFN_LAUNCH(kTimedAttention, (k_dec<HD, G, MODE, KPT>),
+                dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kDecThreads), st, g, v, q, seq_len,
+                max_seq_len, sel, nsel, max_sel, ws, tpw);
 }
 
 template <int HD, int G>

@@ -2,6 +2,7 @@
 // the gfx950 kernels (qsa_kernels.hip) and the C ABI (qsa_abi.hip).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -78,6 +79,39 @@ struct FusedAppend {
 };
 
 bool kernels_for(int32_t hd, int32_t G);   // an instantiation exists
+
+// Per-kernel timing of a decode call (qwfn_qsa_time_next_call).  While a
+// kind's pair of events is armed, its next launch on this thread goes
+// through hipExtLaunchKernel, which stamps the pair with that kernel's own
+// begin and end, and the pair is disarmed.  A stream under capture launches
+// as usual (the pair is dropped).  The decode entry points disarm whatever
+// their call did not use before they return.
+enum TimedKind { kTimedIndexer = 0, kTimedAttention = 1, kTimedMerge = 2, kTimedKinds = 3 };
+struct KernelTimer {
+    hipEvent_t ev[kTimedKinds][2];
+};
+extern thread_local KernelTimer g_kernel_timer;
+
+// The armed pair of `kind` (disarming it), or false when it is unarmed or
+// the stream is capturing.
+inline bool take_timer(int kind, hipStream_t st, hipEvent_t *a, hipEvent_t *b) {
+    hipEvent_t *e = g_kernel_timer.ev[kind];
+    if (e[0] == nullptr) return false;
+    *a = e[0];
+    *b = e[1];
+    e[0] = e[1] = nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
+}
+
+#define QWFN_LAUNCH(kind, kern, grid, block, st, ...)                                 \
+    do {                                                                              \
+        hipEvent_t qwfn_a_, qwfn_b_;                                                  \
+        if (take_timer((kind), (st), &qwfn_a_, &qwfn_b_))                             \
+            hipExtLaunchKernelGGL(kern, grid, block, 0, st, qwfn_a_, qwfn_b_, 0, __VA_ARGS__); \
+        else                                                                          \
+            hipLaunchKernelGGL(kern, grid, block, 0, st, __VA_ARGS__);                \
+    } while (0)
 
 // Bytes of one token's head row of K (or V) quants / values in a page.
 inline int32_t kv_row_bytes(int32_t kt, int32_t hd) {

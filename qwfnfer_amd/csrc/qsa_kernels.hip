@@ -1607,8 +1607,8 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
     if (n_chunks < 1) n_chunks = 1;
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
-    hipLaunchKernelGGL((k_indexer<HD, G>), grid, dim3(kIdxThreads), 0, st, g, v, q, seq_len, max_seq_len,
-                       sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big), (int32_t)!select);
+    QWFN_LAUNCH(kTimedIndexer, (k_indexer<HD, G>), grid, dim3(kIdxThreads), st, g, v, q, seq_len, max_seq_len,
+                sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big), (int32_t)!select);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !select) return e;      // !select: the attention selects (k_dec / k_attn<..., SEL>)
     if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
@@ -1737,8 +1737,9 @@ template <int G, int HD>
 static void launch_merge_t(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_len, int32_t n_seq,
                            int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
                            float *out, const Ws &ws, int32_t tg, hipStream_t st) {
-    hipLaunchKernelGGL((k_merge<G, HD>), dim3((unsigned)G, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kMergeThreads), 0,
-                       st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)(sel == nullptr), out, ws, tg);
+    QWFN_LAUNCH(kTimedMerge, (k_merge<G, HD>), dim3((unsigned)G, (unsigned)g.Hkv, (unsigned)n_seq),
+                dim3(kMergeThreads), st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)(sel == nullptr), out,
+                ws, tg);
 }
 
 #define QWFN_FOR_EACH_MERGE(X) X(128, 8) X(128, 4) X(128, 2) X(64, 8) X(256, 12) X(256, 8)
@@ -1747,9 +1748,9 @@ hipError_t launch_merge(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_
                         const Ws &ws, int32_t tg, hipStream_t st) {
 #define X(HD_, G_)                                                                                            \
     if (g.hd == HD_ && g.G == G_) {                                                                           \
-        hipLaunchKernelGGL((k_merge<G_, HD_>), dim3((unsigned)G_, (unsigned)g.Hkv, (unsigned)n_seq),          \
-                           dim3(kMergeThreads), 0, st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)dense, \
-                           out, ws, tg);                                                                      \
+        QWFN_LAUNCH(kTimedMerge, (k_merge<G_, HD_>), dim3((unsigned)G_, (unsigned)g.Hkv, (unsigned)n_seq),    \
+                    dim3(kMergeThreads), st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)dense, out, ws,  \
+                    tg);                                                                                      \
         return hipGetLastError();                                                                             \
     }
     QWFN_FOR_EACH_MERGE(X)
@@ -2067,14 +2068,14 @@ static void launch_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q,
     const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
     const dim3 blk(AttnCfg<HD, G, TG>::NT);
     if (g.kt == QWFN_KV_Q4_0)
-        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q4_0>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
-                           nsel, max_sel, out, ws, n_parts);
+        QWFN_LAUNCH(kTimedAttention, (k_attn<HD, G, TG, QWFN_KV_Q4_0>), grid, blk, st, g, v, q, seq_len, max_seq_len,
+                    sel, nsel, max_sel, out, ws, n_parts);
     else if (g.kt == QWFN_KV_F16)
-        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_F16>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
-                           nsel, max_sel, out, ws, n_parts);
+        QWFN_LAUNCH(kTimedAttention, (k_attn<HD, G, TG, QWFN_KV_F16>), grid, blk, st, g, v, q, seq_len, max_seq_len,
+                    sel, nsel, max_sel, out, ws, n_parts);
     else
-        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q8_0>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len, sel,
-                           nsel, max_sel, out, ws, n_parts);
+        QWFN_LAUNCH(kTimedAttention, (k_attn<HD, G, TG, QWFN_KV_Q8_0>), grid, blk, st, g, v, q, seq_len, max_seq_len,
+                    sel, nsel, max_sel, out, ws, n_parts);
     launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
 }
 
@@ -2088,14 +2089,14 @@ static void launch_attn_sel_t(const Geo &g, const qwfn_kv_view &v, const float *
     const dim3 grid((unsigned)n_parts, (unsigned)g.Hkv, (unsigned)n_seq);
     const dim3 blk(AttnCfg<HD, G, TG>::NT);
     if (g.kt == QWFN_KV_Q4_0)
-        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q4_0, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
-                           sel, nsel, max_sel, out, ws, n_parts);
+        QWFN_LAUNCH(kTimedAttention, (k_attn<HD, G, TG, QWFN_KV_Q4_0, true>), grid, blk, st, g, v, q, seq_len,
+                    max_seq_len, sel, nsel, max_sel, out, ws, n_parts);
     else if (g.kt == QWFN_KV_F16)
-        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_F16, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
-                           sel, nsel, max_sel, out, ws, n_parts);
+        QWFN_LAUNCH(kTimedAttention, (k_attn<HD, G, TG, QWFN_KV_F16, true>), grid, blk, st, g, v, q, seq_len,
+                    max_seq_len, sel, nsel, max_sel, out, ws, n_parts);
     else
-        hipLaunchKernelGGL((k_attn<HD, G, TG, QWFN_KV_Q8_0, true>), grid, blk, 0, st, g, v, q, seq_len, max_seq_len,
-                           sel, nsel, max_sel, out, ws, n_parts);
+        QWFN_LAUNCH(kTimedAttention, (k_attn<HD, G, TG, QWFN_KV_Q8_0, true>), grid, blk, st, g, v, q, seq_len,
+                    max_seq_len, sel, nsel, max_sel, out, ws, n_parts);
     launch_merge_t<G, HD>(g, v, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, TG, st);
 }
 

@@ -27,7 +27,7 @@ __all__ = [
     "QsaConfig", "KvCache", "KvState", "Workspace",
     "append_q8_0", "pool_update", "pool_rebuild", "indexer_topk", "gather_dequant",
     "sparse_decode_attn", "decode_append_select", "sparse_attn_decode", "sparse_attn_prefill",
-    "export_rows_q8_0", "import_rows_q8_0", "read_status",
+    "export_rows_q8_0", "import_rows_q8_0", "read_status", "time_next_call",
     "IdxConfig", "IdxCache", "idx_append_pool", "idx_pool_rebuild", "idx_select", "idx_sparse_attn_prefill",
     "checkpoint_config",
 ]
@@ -504,6 +504,29 @@ def read_status(cache: KvCache, stream=None) -> int:
     out = C.c_int32()
     call("qwfn_qsa_read_status", C.byref(cache.view()), C.byref(out), _stream(stream))
     return out.value
+
+
+TIMED_KERNELS = ("indexer", "attention", "merge")
+
+
+def time_next_call(events: Optional[dict] = None) -> None:
+    """Arm per-kernel timing of the next decode call on this thread
+    (qwfn_qsa_time_next_call).  ``events`` maps names of TIMED_KERNELS to
+    (start, end) pairs of ``torch.cuda.Event(enable_timing=True)``; after the
+    stream completes, ``start.elapsed_time(end)`` is that kernel's own
+    duration.  torch creates an event's handle at its first record, so each
+    event must have been recorded once.  None disarms."""
+    arr = (C.c_void_p * 6)()
+    for k, name in enumerate(TIMED_KERNELS):
+        pair = (events or {}).get(name)
+        if pair is None:
+            continue
+        for j, ev in enumerate(pair):
+            h = ev.cuda_event
+            if not h:
+                raise ValueError(f"time_next_call: the {name} event {j} has no handle yet (record it once)")
+            arr[2 * k + j] = h
+    call("qwfn_qsa_time_next_call", arr)
 
 
 # ---- the checkpoint's own indexer ------------------------------------------

@@ -205,3 +205,15 @@ def test_noalloc_decode_rejects_what_its_array_cannot_hold():
     need = C.c_size_t()
     assert _code("qwfn_qsa_workspace_bytes", C.byref(s), 8, 1 << 20, C.byref(need)) == 0
     assert need.value <= 8 << 20                          # eight sequences of 1M tokens fit
+
+
+def test_time_next_call_arms_pairs_only():
+    """The timing hook takes (start, stop) pairs; half a pair is refused, NULL
+    disarms (no GPU call: arming only stores the handles)."""
+    lib = _lib.load()
+    arr = (C.c_void_p * 6)()
+    assert lib.qwfn_qsa_time_next_call(arr) == 0                 # all NULL: nothing armed
+    arr[2] = 0x1000                                              # attention start without its stop
+    assert lib.qwfn_qsa_time_next_call(arr) == _lib.QWFN_EINVAL
+    assert "stop" in lib.qwfn_qsa_last_error().decode()
+    assert lib.qwfn_qsa_time_next_call(None) == 0                # disarm
