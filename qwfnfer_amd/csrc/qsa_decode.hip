@@ -28,6 +28,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "qsa_device.h"
 
 namespace qwfn_qsa {
@@ -642,43 +644,66 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
 }
 
+// Workgroups of one k_dec instantiation the device holds at once: its
+// occupancy per CU (registers, LDS) times the CUs, looked up once per device.
+constexpr int kResDevices = 64;
 template <int HD, int G, int MODE, int KPT>
-void launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
-                  int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, int32_t tpw,
-                  hipStream_t st) {
+int dec_resident() {
+    static std::atomic<int> cache[kResDevices];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kResDevices) return 0;
+    int r = cache[dev].load(std::memory_order_relaxed);
+    if (r > 0) return r;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT>, kDecThreads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    r = per_cu * cus;
+    cache[dev].store(r, std::memory_order_relaxed);
+    return r;
+}
+
+// Launches k_dec; returns the tiles a workgroup took.  One tile a workgroup
+// unless the grid would then not be resident at once (a second round of
+// workgroups starts only when the first ends): then the fewest tiles a
+// workgroup, up to kDecTpwMax, that fit it.
+template <int HD, int G, int MODE, int KPT>
+int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
+                 int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
+    const int64_t pairs = (int64_t)n_seq * g.Hkv;
+    const int res = dec_resident<HD, G, MODE, KPT>();
+    int tpw = 1;
+    while (tpw < kDecTpwMax && res > 0 && pairs * ((ws.n_tiles + tpw - 1) / tpw) > res) ++tpw;
     const int parts = (ws.n_tiles + tpw - 1) / tpw;
     QWFN_LAUNCH(kTimedAttention, (k_dec<HD, G, MODE, KPT>),
                 dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kDecThreads), st, g, v, q, seq_len,
                 max_seq_len, sel, nsel, max_sel, ws, tpw);
+    return tpw;
 }
 
 template <int HD, int G>
 hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                             int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                             int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
-    // one tile a workgroup while the sequences leave the chip's CUs idle;
-    // more per workgroup (fewer partials, the next tile's loads overlapping
-    // this one's arithmetic) once the tiles fill it several times over
-    const int64_t tiles = (int64_t)n_seq * g.Hkv * ws.n_tiles;
-    const int tpw = tiles >= 4096 ? kDecTpwMax : tiles >= 1024 ? 2 : 1;
     int32_t *sl = const_cast<int32_t *>(sel), *ns = const_cast<int32_t *>(nsel);
+    int tpw;
     if (select) {
         const Ranges span_r{0, 0, g.sink, max_seq_len / g.bt};
         const int span = span_r.e_hi - (span_r.e_lo & ~3);
         if (span <= 4 * kDecThreads)
-            launch_dec_t<HD, G, kSelect, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+            tpw = launch_dec_t<HD, G, kSelect, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 8 * kDecThreads)
-            launch_dec_t<HD, G, kSelect, 8>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+            tpw = launch_dec_t<HD, G, kSelect, 8>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 16 * kDecThreads)
-            launch_dec_t<HD, G, kSelect, 16>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+            tpw = launch_dec_t<HD, G, kSelect, 16>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 32 * kDecThreads)
-            launch_dec_t<HD, G, kSelect, 32>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+            tpw = launch_dec_t<HD, G, kSelect, 32>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else
             return hipErrorInvalidValue;
     } else if (sel) {
-        launch_dec_t<HD, G, kGiven, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+        tpw = launch_dec_t<HD, G, kGiven, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
     } else {
-        launch_dec_t<HD, G, kDense, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, tpw, st);
+        tpw = launch_dec_t<HD, G, kDense, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
