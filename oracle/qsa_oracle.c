@@ -6,6 +6,9 @@
 #include "qsa_oracle.h"
 
 #include <math.h>
+#ifdef __F16C__
+#include <immintrin.h>
+#endif
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -613,12 +616,67 @@ int qwfn_oracle_prefill_f64_strided(const qwfn_qsa_shape *s, const qwfn_kv_view 
 
 static float f16_round(float x) { return qwfn_oracle_f16_to_f32(qwfn_oracle_f32_to_f16(x)); }
 
+/* x[0..n) rounded to fp16 and back (round to nearest even, as
+ * qwfn_oracle_f32_to_f16), eight at a time with F16C where the build has it. */
+static void round_f16_row(float *x, int32_t n) {
+    int32_t d = 0;
+#ifdef __F16C__
+    for (; d + 8 <= n; d += 8) {
+        const __m256 a = _mm256_loadu_ps(x + d);
+        _mm256_storeu_ps(x + d, _mm256_cvtph_ps(_mm256_cvtps_ph(a, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC)));
+    }
+#endif
+    for (; d < n; d++) x[d] = f16_round(x[d]);
+}
+
+/* Token t of KV head g of one pool as the reference's attention sees it:
+ * dequantized (ggml_get_rows of q8_0: each 32-value block's fp16 scale times
+ * its quants) and cast to F16 (src/qwfn_graph.cpp:530-532).  q8_0 rows are
+ * read straight from their page (K quants in 16-byte chunks 1024 bytes apart,
+ * V quants dim-major 64 bytes apart); other types through
+ * qwfn_oracle_dequant_row. */
+static int32_t baseline_row(const qwfn_qsa_shape *s, const qwfn_kv_view *v, const void *pool, int32_t seq,
+                            int32_t t, int32_t g, float *out) {
+    const int32_t hd = s->head_dim;
+    if (s->kv_type != QWFN_KV_Q8_0) {
+        const int32_t rc = qwfn_oracle_dequant_row(s, v, pool, seq, t, g, out);
+        if (!rc) round_f16_row(out, hd);
+        return rc;
+    }
+    int32_t status = 0;
+    const uint8_t *page = page_of(s, v, pool, seq, t, &status);
+    if (!page) return status;
+    const int32_t row = t % s->page_tokens, is_v = pool == v->v_pages;
+    float scale[16];
+    for (int32_t j = 0; j < hd / 32; j++) {
+        uint16_t h;
+        memcpy(&h, page + qwfn_oracle_scale_offset(s, g, row, j), 2);
+        scale[j] = qwfn_oracle_f16_to_f32(h);
+    }
+    const int8_t *q0 = (const int8_t *)(page + qwfn_oracle_quant_offset(s, is_v, g, row, 0));
+    if (is_v && s->block_tokens % 64 == 0)
+        for (int32_t d = 0; d < hd; d++) out[d] = scale[d / 32] * (float)q0[(int64_t)d * 64];
+    else
+        for (int32_t d = 0; d < hd; d++) out[d] = scale[d / 32] * (float)q0[(d / 16) * 1024 + d % 16];
+    round_f16_row(out, hd);
+    return 0;
+}
+
+/* a . b over n (a multiple of 8) as eight interleaved partial sums. */
+static float dot8(const float *a, const float *b, int32_t n) {
+    float p[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int32_t d = 0; d < n; d += 8)
+        for (int j = 0; j < 8; j++) p[j] += a[d + j] * b[d + j];
+    return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
 int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                                 const float *q, const float *k_new,
                                 const float *v_new, const int32_t *seq_len,
                                 int32_t n_seq, float *out, int32_t *sel,
                                 int32_t *n_sel, int32_t max_sel) {
     const int32_t H = s->n_head_kv, hd = s->head_dim, G = s->n_head / H, bt = s->block_tokens;
+    if (G > 16 || hd > 512 || hd % 32) return QWFN_EINVAL;      /* the per-task buffers below */
     const int64_t bps = blocks_per_seq(s, v);
     int threads = 1;
 #ifdef _OPENMP
@@ -652,52 +710,69 @@ int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
             n_sel[seq * H + g] = qwfn_oracle_select(s, scores, L, sel + ((int64_t)seq * H + g) * max_sel, max_sel);
         }
     free(scores);
-    /* attention: online softmax per (sequence, query head, split of blocks),
-     * gathered K/V cast to fp16 (src/qwfn_graph.cpp:530-541), then a merge. */
-    const int32_t splits = 8;
-    const int64_t n_task = (int64_t)n_seq * s->n_head * splits;
-    float *part = (float *)malloc(sizeof(float) * (size_t)n_task * (hd + 2));
+    /* attention: one task per (sequence, KV head, split of its selected
+     * blocks).  Each selected row is dequantized and cast to F16 once (the
+     * reference gathers and casts K/V once per KV head, src/qwfn_graph.cpp:
+     * 530-541) and serves the group's G query heads, each with its own online
+     * softmax; the splits are merged per query head. */
+    const int32_t splits = 16;
+    const int64_t n_task = (int64_t)n_seq * H * splits;
+    const int64_t rec = (int64_t)hd + 2;
+    float *part = (float *)malloc(sizeof(float) * (size_t)(n_task * G * rec));
+    int32_t row_err = 0;
 #pragma omp parallel for schedule(dynamic)
     for (int64_t task = 0; task < n_task; task++) {
         const int32_t sp = (int32_t)(task % splits);
-        const int32_t hq = (int32_t)((task / splits) % s->n_head);
-        const int32_t seq = (int32_t)(task / splits / s->n_head);
-        const int32_t g = hq / G, L = seq_len[seq];
+        const int32_t g = (int32_t)((task / splits) % H);
+        const int32_t seq = (int32_t)(task / splits / H);
+        const int32_t L = seq_len[seq];
         const int32_t nb = n_sel[seq * H + g];
         const int32_t *sl = sel + ((int64_t)seq * H + g) * max_sel;
-        const float *qh = q + ((int64_t)seq * s->n_head + hq) * hd;
-        float *pp = part + task * (hd + 2);
-        float m = -INFINITY, l = 0.0f;
-        float kr[512], vr[512];
-        for (int32_t d = 0; d < hd; d++) pp[2 + d] = 0.0f;
+        const float *qg = q + ((int64_t)seq * s->n_head + (int64_t)g * G) * hd;
+        float m[16], l[16], sc[16];
+        float acc[16 * 512], kr[512], vr[512];
+        for (int32_t h = 0; h < G; h++) { m[h] = -INFINITY; l[h] = 0.0f; }
+        for (int64_t i = 0; i < (int64_t)G * hd; i++) acc[i] = 0.0f;
         const float scale = 1.0f / sqrtf((float)hd);
         for (int32_t i = sp; i < nb; i += splits) {
             const int32_t b = sl[i];
             for (int32_t t = b * bt; t < b * bt + bt && t < L; t++) {
-                qwfn_oracle_dequant_row(s, v, v->k_pages, seq, t, g, kr);
-                float sc = 0.0f;
-                for (int32_t d = 0; d < hd; d++) sc += qh[d] * f16_round(kr[d]);
-                sc *= scale;
-                const float mn = sc > m ? sc : m;
-                const float corr = expf(m - mn), pw = expf(sc - mn);
-                qwfn_oracle_dequant_row(s, v, v->v_pages, seq, t, g, vr);
-                for (int32_t d = 0; d < hd; d++) pp[2 + d] = pp[2 + d] * corr + pw * f16_round(vr[d]);
-                l = l * corr + pw;
-                m = mn;
+                if (baseline_row(s, v, v->k_pages, seq, t, g, kr) || baseline_row(s, v, v->v_pages, seq, t, g, vr)) {
+#pragma omp atomic write
+                    row_err = 1;
+                    continue;
+                }
+                for (int32_t h = 0; h < G; h++) sc[h] = dot8(qg + (int64_t)h * hd, kr, hd) * scale;
+                for (int32_t h = 0; h < G; h++) {
+                    const float mn = sc[h] > m[h] ? sc[h] : m[h];
+                    const float corr = expf(m[h] - mn), pw = expf(sc[h] - mn);
+                    float *a = acc + (int64_t)h * hd;
+                    for (int32_t d = 0; d < hd; d++) a[d] = a[d] * corr + pw * vr[d];
+                    l[h] = l[h] * corr + pw;
+                    m[h] = mn;
+                }
             }
         }
-        pp[0] = m;
-        pp[1] = l;
+        for (int32_t h = 0; h < G; h++) {
+            float *pp = part + (task * G + h) * rec;
+            pp[0] = m[h];
+            pp[1] = l[h];
+            memcpy(pp + 2, acc + (int64_t)h * hd, sizeof(float) * (size_t)hd);
+        }
     }
+    if (row_err) { free(part); return QWFN_ERANGE; }
     for (int32_t seq = 0; seq < n_seq; seq++)
         for (int32_t hq = 0; hq < s->n_head; hq++) {
-            const float *pp = part + ((int64_t)seq * s->n_head + hq) * splits * (hd + 2);
+            const int32_t g = hq / G, h = hq % G;
             float M = -INFINITY, Lsum = 0.0f;
-            for (int32_t sp = 0; sp < splits; sp++) if (pp[sp * (hd + 2)] > M) M = pp[sp * (hd + 2)];
+            for (int32_t sp = 0; sp < splits; sp++) {
+                const float *x = part + ((((int64_t)seq * H + g) * splits + sp) * G + h) * rec;
+                if (x[1] > 0.0f && x[0] > M) M = x[0];
+            }
             float *o = out + ((int64_t)seq * s->n_head + hq) * hd;
             for (int32_t d = 0; d < hd; d++) o[d] = 0.0f;
             for (int32_t sp = 0; sp < splits; sp++) {
-                const float *x = pp + sp * (hd + 2);
+                const float *x = part + ((((int64_t)seq * H + g) * splits + sp) * G + h) * rec;
                 if (x[1] == 0.0f) continue;
                 const float w = expf(x[0] - M);
                 Lsum += w * x[1];

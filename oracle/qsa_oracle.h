@@ -118,8 +118,14 @@ int qwfn_oracle_prefill_f64_strided(const qwfn_qsa_shape *s, const qwfn_kv_view 
                                     int32_t *sel, int32_t *n_sel, int32_t max_sel, double *out);
 /* CPU baseline: one decode token of the whole path in fp32 (append at
  * seq_len-1, pool on block completion, scores, selection, attention with the
- * gathered K/V cast to fp16 as the reference's decode does, online softmax),
- * OpenMP over blocks and heads.  Returns the thread count used, or < 0. */
+ * gathered K/V cast to fp16 as the reference's decode does, online softmax).
+ * Like the reference's CPU path it dequantizes and casts each selected row once
+ * per KV head and serves the group's query heads from it; OpenMP over scoring
+ * blocks and over (sequence, KV head, split) attention tasks.  Its selection
+ * equals qwfn_oracle_indexer_topk's and its output is within the attention
+ * tolerance of qwfn_oracle_attention_f64's (tests/test_oracle_baseline.py).
+ * head_dim <= 512 (a multiple of 32), at most 16 query heads a KV head.
+ * Returns the thread count used, or < 0. */
 int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                                 const float *q, const float *k_new,
                                 const float *v_new, const int32_t *seq_len,
