@@ -73,6 +73,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill-chunk line")
     ap.add_argument("--no-kv-types", action="store_true",
                     help="skip the q4_0 / fp16 cache lines (config 3 at the longest context)")
+    ap.add_argument("--no-interop", action="store_true",
+                    help="skip the reference-format import / export line (one layer at the longest context)")
     ap.add_argument("--no-checkpoint", action="store_true",
                     help="skip the checkpoint-layer decode line (the released model's own indexer)")
     ap.add_argument("--prefill-batch", type=int, default=8192,
@@ -555,6 +557,47 @@ class CheckpointRunner:
                     selected_kv_bytes=cells * row * 2 * self.cfg.n_head_kv)
 
 
+def bench_interop(qsa, torch, cfg, gen, ctx, reps=20):
+    """The reference-format boundary on one layer of ctx tokens: K and V rows
+    in ggml's block_q8_0 row format (the reference's cache tensors) imported
+    into the pages (qwfn_kv_import_q8_0), the pooled keys rebuilt from them
+    (qwfn_pool_rebuild), and exported back (qwfn_kv_export_q8_0).  Each is
+    timed with HIP events around `reps` calls; the rows and pages are ~90 MB
+    each way, so the MALL does not hold them."""
+    pps = (ctx + cfg.page_tokens - 1) // cfg.page_tokens
+    pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
+    cache = qsa.KvCache.allocate(cfg, 1, pps, page_table=pt, n_phys_pages=pps)
+    fill_layer(qsa, torch, cache, [ctx], gen)
+    k_rows, v_rows = qsa.export_rows_q8_0(cache, 0, 0, ctx)
+    torch.cuda.synchronize()
+    res = {}
+    for name, fn in (("import", lambda: qsa.import_rows_q8_0(cache, 0, 0, k_rows, v_rows)),
+                     ("pool_rebuild", lambda: qsa.pool_rebuild(cache, 0, ctx // cfg.block_tokens)),
+                     ("export", lambda: qsa.export_rows_q8_0(cache, 0, 0, ctx))):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / reps * 1e3
+    if qsa.read_status(cache):
+        raise RuntimeError("interop reported out-of-range rows")
+    rows = ctx * cfg.row_bytes() * 2                 # K and V rows, read or written once each way
+    out = dict(context=ctx, row_bytes=cfg.row_bytes(), kv_row_bytes_total=rows,
+               import_us=round(res["import"], 2), export_us=round(res["export"], 2),
+               pool_rebuild_us=round(res["pool_rebuild"], 2),
+               import_gbs=round(2 * rows / (res["import"] * 1e-6) / 1e9, 1),
+               export_gbs=round(2 * rows / (res["export"] * 1e-6) / 1e9, 1),
+               note="import/export read the rows (or pages) once and write the pages (or rows) once: "
+                    "2 x kv_row_bytes_total per call")
+    del cache, k_rows, v_rows
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(cfg, ctx, seconds, seed):
     """The oracle's fp32 decode step (the ggml CPU path restated: append,
     pool, scores, selection, attention over fp16-cast K/V) on one layer at
@@ -735,6 +778,13 @@ def main():
             del r
             torch.cuda.empty_cache()
 
+    interop = None
+    if not args.no_interop:
+        interop = bench_interop(qsa, torch, cfg, gen, max(contexts))
+        log(f"[bench] interop at {interop['context']}: import {interop['import_us']:.1f} us "
+            f"({interop['import_gbs']:.0f} GB/s), pool rebuild {interop['pool_rebuild_us']:.1f} us, "
+            f"export {interop['export_us']:.1f} us ({interop['export_gbs']:.0f} GB/s)")
+
     checkpoint = None
     if not args.no_checkpoint:
         ck = {}
@@ -823,6 +873,7 @@ def main():
         "prefill_config4": prefill,
         "checkpoint_decode": checkpoint,
         "kv_types": kv_types,
+        "interop": interop,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }

@@ -48,8 +48,12 @@
  *  page_table[s*pages_per_seq + t/page_tokens] at row t%page_tokens.
  *  pooled = fp32 [n_seq][n_head_kv][blocks_per_seq][head_dim], where
  *  blocks_per_seq = pages_per_seq*page_tokens/block_tokens.
- *  The reference's contiguous token-major cache (src/qwfn_state.cpp:52-54) is
- *  the special case of one sequence with an identity page table.
+ *  The reference's cache (src/qwfn_state.cpp:50-54) is a different byte
+ *  layout: one 1-D tensor per layer of token-major ggml block_q8_0 rows (each
+ *  head row a run of 34-byte blocks, fp16 scale then 32 quants).  The kernels
+ *  read only the layout above; state::init allocates these pages in its place
+ *  (qwfn_qsa_page_bytes), and rows in the reference's format enter or leave
+ *  through qwfn_kv_import_q8_0 / qwfn_kv_export_q8_0, a copy.
  */
 #ifndef QWFN_QSA_H
 #define QWFN_QSA_H

@@ -70,9 +70,15 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 //            (ggml_rms_norm also sums in fp64; :423)
 //   rotary : pair (i, i + nd/2), angle pos * invf[i] in fp64, cos/sin rounded
 //            to fp32: (x0 c - x1 s, x0 s + x1 c); dims >= nd unchanged.  The
-//            reference's IMROPE (:425-427) is this rotation: it gives every
-//            position section the same position for text (src/qwfn_engine.cpp:
-//            741, 781, 926, 934).
+//            reference's IMROPE (:425-427) is this rotation for text, where
+//            every position section gets the same position (src/qwfn_engine.cpp:
+//            741, 781, 926, 934).  The angle here is the exact fp64 product;
+//            ggml's rope builds theta in fp32 (a running product of the
+//            per-pair factor), which at block positions near 1.6e5 differs
+//            from it by up to about 1e-2 rad.  Parity with the reference's
+//            pooled keys is therefore unpinned at long positions: the oracle
+//            restates this fp64 rule, and the selections are pinned given the
+//            pooled keys.
 //   store  : rounded to fp16 (the reference's F16 pool cache).
 template <int D>
 __device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, const uint16_t *m,

@@ -5,13 +5,15 @@
   block completion, then steps through the two-call path, with the attention
   also re-run over each step's selection.
 * Longer contexts that reach every register path of the two selections: the
-  indexer's 256-thread selection (two-call path) holds 4 .. 32 keys a thread
-  and the attention's 512-thread in-kernel selection (fused path) 4 .. 16, each
-  chosen by the eligible span (<= KPT * threads).
+  indexer's 256-thread selection (two-call path) holds 4 .. 32 keys a thread,
+  chosen by the eligible span, and the attention's own selection (k_dec, fused
+  path) 4 .. 32 keys over its 256 threads, chosen by the span of max_seq_len.
+* Configs 1 and 2: the bench's dense 4,096-token step and its 32,768-token
+  sparse step through the fused call.
 * Config 5: the bench's eight log-uniform lengths on a permuted page table,
-  through the fused call (the attention selects for itself at up to eight
-  sequences) and qwfn_sparse_decode_attn, which runs four tiles a workgroup
-  from four sequences on.
+  through the fused call (the attention selects for itself) and
+  qwfn_sparse_decode_attn (k_dec over a given selection, several tiles a
+  workgroup when one tile each would not fit the device at once).
 * Config 4: one 8,192-query chunk of fp16 rows appended at 155,648: cache
   bytes and pooled keys bit-exact, every query's selection bit-exact,
   attention of a strided sample of queries within the tolerance.
@@ -53,20 +55,28 @@ def _span(cfg, L):
 
 
 # Config 3's contexts, then one length for each keys-per-thread tier past
-# them: (256-thread KPT, 512-thread KPT) = (4, 4) at 65,536; (12, 8) at
-# 163,840; (16, 8) at 230,400; (24, 12) at 320,000; (32, 16) at 480,000.
-@pytest.mark.parametrize("L0,kpt256,kpt512", [(65536, 4, 4), (163840, 12, 8), (230400, 16, 8),
-                                               (320000, 24, 12), (480000, 32, 16)])
-def test_config3_long_context_decode(L0, kpt256, kpt512):
+# them: (indexer KPT, k_dec KPT) = (4, 4) at 65,536; (12, 16) at 163,840;
+# (16, 16) at 230,400; (24, 32) at 320,000; (32, 32) at 480,000.  Config 5
+# runs k_dec's KPT 8.
+@pytest.mark.parametrize("L0,kpt_idx,kpt_dec", [(65536, 4, 4), (163840, 12, 16), (230400, 16, 16),
+                                                (320000, 24, 32), (480000, 32, 32)])
+def test_config3_long_context_decode(L0, kpt_idx, kpt_dec):
     span = _span(BASELINE, L0)
-    tiers256 = [4, 8, 12, 16, 24, 32]
-    tiers512 = [4, 8, 12, 16]
-    assert min(t for t in tiers256 if span <= t * 256) == kpt256
-    assert min(t for t in tiers512 if span <= t * 512) == kpt512
+    assert min(t for t in [4, 8, 12, 16, 24, 32] if span <= t * 256) == kpt_idx
+    max_len = L0 - 2 + 5                          # decode_steps' max_seq_len: the fill plus the steps
+    assert min(t for t in [4, 8, 16, 32] if max_len // BASELINE.block_tokens <= t * 256) == kpt_dec
     # fill L0 - 2 tokens: the second fused step completes block L0/64 - 1 and
     # pools it; two two-call steps follow
     decode_steps(BASELINE, [L0 - 2], steps=5, seed=700 + L0 % 997,
                  modes=["fused", "fused", "fused", "two_call", "two_call"], reattend=True, verbose=True)
+
+
+def test_config1_dense_and_config2_sparse_steps():
+    # config 1: dense attention over every key, the fused call at 4,096 tokens
+    # (the indexer selects every block); config 2: 32,768 tokens, top-64
+    decode_steps(Cfg(top_k_blocks=0), [4096 - 2], steps=3, seed=740, verbose=True)
+    decode_steps(BASELINE, [32768 - 2], steps=3, seed=741, modes=["fused", "fused", "two_call"], reattend=True,
+                 verbose=True)
 
 
 @pytest.mark.parametrize("shift", [False, True])
