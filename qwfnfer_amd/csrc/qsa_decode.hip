@@ -3,31 +3,38 @@
 // qwfn_sparse_decode_attn (a given selection or dense) and of the fused
 // qwfn_sparse_attn_decode (the workgroup selects from the indexer's scores).
 //
-// One workgroup of four waves (one per SIMD) per part of a (sequence, KV head)'s
-// tiles; wave w owns cells 16w .. 16w+15 of every tile, so a wave's logits need
-// no other wave:
-//   QK  v_mfma_f32_16x16x32_f16: the int8 key quants (exact in fp16) against the
-//       query scaled by a power of two and split into fp16 high + low parts;
-//       one accumulator per 32-dim q8_0 block, combined with the keys' scales.
-//   PV  v_mfma_f32_16x16x16_f16: the V quants (exact in fp16) against the
-//       weights p * d_v * 2^k split into fp16 high + low parts.  The QK
+// One workgroup of four waves (one per SIMD) per part of TM tiles of a
+// (sequence, KV head); wave w owns cells 16w .. 16w+15 of every tile, so a
+// wave's logits need no other wave.  All of a part's tiles go out at once as
+// 16-byte global -> LDS transfers into the wave's own staging slots (no
+// registers held while they fly, no barrier before reading them), and the
+// wave runs a two-pass softmax over them:
+//   QK  v_mfma_f32_16x16x32_f16 per tile as it lands: the int8 key quants
+//       (exact in fp16) against the query scaled by a power of two and split
+//       into fp16 high + low parts, one accumulator per 32-dim q8_0 block,
+//       combined with the keys' scales; the logits of all TM tiles stay in
+//       registers, and their column maximum is the softmax reference.
+//   PV  v_mfma_f32_16x16x16_f16 accumulating straight into O: the V quants
+//       (exact in fp16) against the weights p * d_v * 2^k split into fp16
+//       high + low parts, k fixed per column over the part (its largest V
+//       scale near 2^15), so O needs no rescaling between tiles.  The QK
 //       accumulator layout (cells 4lg..4lg+3 of column hn in lane 16lg+hn) is
 //       the B-operand layout of this shape, so the weights never leave their
 //       lanes.
-// Each wave keeps an online-softmax state over the part's tiles; the four
-// states merge through LDS into one partial (max, sum, unnormalised O) per
-// workgroup, which k_merge combines.
+// The four waves' states merge through LDS into one partial (max, sum,
+// unnormalised O) per workgroup, which k_merge combines.
 //
 // The latency of one sequence is a chain of dependent steps, so everything
 // that does not depend on the selection (the length, the score row, the query
-// rows, the sequence's page-table row) is loaded in the first round trip, the
-// query split runs while the tile loads are in flight, and the selection is a
-// short exact top-k over a 2048-bin histogram held by the four waves.
+// rows, the sequence's page-table row) is loaded in the first round trip and
+// the selection is a short exact top-k over a 2048-bin histogram held by the
+// four waves.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "qsa_device.h"
@@ -40,32 +47,55 @@ constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecBins = 2048;                  // selection histogram bins
 constexpr int kDecCand = 256;                   // threshold-bin keys ranked pairwise
-constexpr int kDecPtLds = 4096;                 // page-table entries parked in LDS
+constexpr int kDecPtLds = 4096;                 // page-table entries parked in LDS at most
 constexpr int kDecSelMax = 1024;                // selected blocks kept in LDS
-constexpr int kDecTpwMax = 4;                   // tiles per workgroup (the i4v of their blocks)
 
 enum DecMode { kGiven = 0, kDense = 1, kSelect = 2 };
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
-template <int HD, int G>
+// The selection's scratch (kSelect); it shares the dynamic LDS region with
+// the tile staging and the waves' O, which are used only after it.
+struct DecSel {
+    uint32_t hist[kDecBins + 64];                // + one trash bin per lane
+    uint32_t cand_key[kDecWaves * kDecCand + 64];   // threshold-bin keys, a region per wave
+    int32_t cand_b[kDecWaves * kDecCand + 64];      // (+ one trash slot per lane)
+};
+
+template <int G>
 struct DecShared {
-    union {
-        struct {                                 // the selection
-            uint32_t hist[kDecBins + 64];        // + one trash bin per lane
-            uint32_t cand_key[kDecWaves * kDecCand + 64];   // threshold-bin keys, a region per wave
-            int32_t cand_b[kDecWaves * kDecCand + 64];      // (+ one trash slot per lane)
-        } s;
-        float wo[kDecWaves][G][HD];              // the waves' O, merged into the partial
-    } u;
     float wml[kDecWaves][G][2];                  // the waves' (max, sum)
     int32_t wcnt[kDecWaves];
     int32_t ccnt[kDecWaves];
     int32_t nsel;
     int32_t sel[kDecSelMax + 64];                // + one trash slot per lane
-    int32_t ptab[kDecPtLds];
 };
+
+// One wave's share of a staged tile: the K quants of its 16 cells (chunk c at
+// c * 256, cell i at i * 16), the V quants (dim d at d * 16: its 16 cells),
+// then the K and the V scales of its 16 cells (cell-major, NB fp16 a cell).
+template <int HD>
+struct DecStage {
+    static constexpr int NB = HD / 32, ND = HD / 16, NS = NB / 2;
+    static constexpr int NKV = HD / 64;                  // 1 KB transfers of K (and of V) a tile
+    static constexpr int KOFF = 0, VOFF = HD * 16, SOFF = 2 * HD * 16;
+    static constexpr int SROW = 16 * NB * 2;             // one scale set of the wave's 16 cells
+    static constexpr int BYTES = SOFF + 2 * SROW;
+    static constexpr int NL = 2 * NKV + 1;               // transfers a wave issues per tile
+    static_assert(HD % 64 == 0 && SROW % 16 == 0 && 2 * SROW / 16 <= 64, "whole 16-byte transfers");
+};
+
+// Bytes of the dynamic LDS region shared by the selection scratch, the
+// staged tiles and the waves' O (the page-table row follows it).
+template <int HD, int G, int MODE, int TM>
+constexpr int dec_union_bytes() {
+    constexpr int st = TM * kDecWaves * DecStage<HD>::BYTES;
+    constexpr int wo = kDecWaves * G * HD * 4;
+    constexpr int se = MODE == kSelect ? (int)sizeof(DecSel) : 0;
+    constexpr int m = st > wo ? st : wo;
+    return ((m > se ? m : se) + 15) / 16 * 16;
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -143,9 +173,9 @@ __device__ __forceinline__ int dec_excl_sum(int v, int32_t *wcnt, int *total) {
 // them), or for heavier ties refined by radix passes over their 32-bit keys,
 // ties then taken in block order.  Straight-line per key: no branch on a
 // key's value or eligibility.  Ends with a barrier; sh.sel is then valid.
-template <int KPT, int HD, int G>
+template <int KPT, int G>
 __device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT], const Ranges &r, int topk,
-                                           float lo, float hi, DecShared<HD, G> &sh) {
+                                           float lo, float hi, DecSel &ss, DecShared<G> &sh) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int base = r.e_lo & ~3;
     const int b0 = base + tid * KPT;
@@ -167,10 +197,10 @@ __device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT],
         ib[i] = valid(i) ? (int)min(u, (uint32_t)(kDecBins - 1)) : -1;
     }
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) atomicAdd(&sh.u.s.hist[ib[i] >= 0 ? hist_word(ib[i]) : kDecBins + lane], 1u);
+    for (int i = 0; i < KPT; ++i) atomicAdd(&ss.hist[ib[i] >= 0 ? hist_word(ib[i]) : kDecBins + lane], 1u);
     __syncthreads();
     int need, cB;
-    const int B = dec_cut(sh.u.s.hist, topk, &need, &cB);
+    const int B = dec_cut(ss.hist, topk, &need, &cB);
     uint32_t mask = 0, cm = 0;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
@@ -191,22 +221,22 @@ __device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT],
         for (int i = 0; i < KPT; ++i) {
             const bool in = ib[i] == B;
             const int at = in ? slot : kDecWaves * kDecCand + lane;
-            sh.u.s.cand_key[at] = score_key(sv[i]);
-            sh.u.s.cand_b[at] = b0 + i;
+            ss.cand_key[at] = score_key(sv[i]);
+            ss.cand_b[at] = b0 + i;
             slot += in;
         }
         if (lane == 63) sh.ccnt[w] = wi;
         __syncthreads();
         for (int jo = slot0; jo < slot0 + c; ++jo) {
-            const uint32_t k = sh.u.s.cand_key[jo];
-            const int b = sh.u.s.cand_b[jo];
+            const uint32_t k = ss.cand_key[jo];
+            const int b = ss.cand_b[jo];
             int rank = 0;
 #pragma unroll
             for (int ww = 0; ww < kDecWaves; ++ww) {
                 const int n = sh.ccnt[ww];
                 for (int jj = 0; jj < n; ++jj) {
-                    const uint32_t kj = sh.u.s.cand_key[ww * kDecCand + jj];
-                    rank += (kj > k) || (kj == k && sh.u.s.cand_b[ww * kDecCand + jj] < b);
+                    const uint32_t kj = ss.cand_key[ww * kDecCand + jj];
+                    rank += (kj > k) || (kj == k && ss.cand_b[ww * kDecCand + jj] < b);
                 }
             }
             mask |= (uint32_t)(rank < need) << (b - b0);
@@ -216,7 +246,7 @@ __device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT],
         // passes over the bin's keys (256-bin histograms, each wave finding
         // the digit on its own), then
         // keys above it and the first ties in block order.
-        uint32_t *h = sh.u.s.hist;
+        uint32_t *h = ss.hist;
         uint32_t prefix = 0;
         int nd = need;
 #pragma unroll 1
@@ -292,51 +322,6 @@ __device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT],
     __syncthreads();
 }
 
-// Loads of one tile for wave w: K quants in QK A-operand layout (cell 16w+hn,
-// dims 32kb+8lg .. +8), V quants in PV A-operand layout (dim 16db+hn, cells
-// 16w+4lg .. +4), and the K / V scales of the lane's D-layout cells
-// 16w+4lg .. +4 (NB fp16 per cell).
-template <int HD>
-struct DecTile {
-    static constexpr int NB = HD / 32, ND = HD / 16, NS = NB / 2 > 0 ? NB / 2 : 1;
-    u2v k[NB];                                       // native vectors: a copy stays in registers
-    uint32_t v[ND];
-    u4v dk[NS], dv[NS];
-    int nv;                                          // valid cells of the tile (0: none)
-};
-
-template <int HD>
-__device__ __forceinline__ void dec_load_tile(const Geo &g, const qwfn_kv_view &v, int gh, int32_t page,
-                                              int row0, int nv, DecTile<HD> &t) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hn = lane & 15, lg = lane >> 4;
-    constexpr int NB = DecTile<HD>::NB, ND = DecTile<HD>::ND, NS = DecTile<HD>::NS;
-    t.nv = nv;
-    const int64_t pbase = (int64_t)(nv > 0 ? page : 0) * g.page_bytes;
-    const uint8_t *kp = (const uint8_t *)v.k_pages + pbase;
-    const uint8_t *vp = (const uint8_t *)v.v_pages + pbase;
-    const int tl = gh * (g.pt / 64) + row0 / 64;
-    const uint8_t *kq = kp + ((int64_t)tl * ND + (lg >> 1)) * 1024 + (16 * w + hn) * 16 + 8 * (lg & 1);
-    const uint8_t *vq = vp + ((int64_t)tl * HD + hn) * 64 + 16 * w + 4 * lg;
-    const int64_t so = g.qbytes + ((int64_t)(gh * g.pt + row0 + 16 * w + 4 * lg) * NB) * 2;
-    // unconditional: an empty tile reads page 0 (in bounds), and every value
-    // of its cells is masked by nv == 0 (logits -inf, V scales 0)
-#pragma unroll
-    for (int kb = 0; kb < NB; ++kb) t.k[kb] = *reinterpret_cast<const u2v *>(kq + kb * 2048);
-#pragma unroll
-    for (int db = 0; db < ND; ++db) t.v[db] = *reinterpret_cast<const uint32_t *>(vq + db * 1024);
-    if constexpr (NB >= 2) {
-#pragma unroll
-        for (int i = 0; i < NS; ++i) {
-            t.dk[i] = *reinterpret_cast<const u4v *>(kp + so + 16 * i);
-            t.dv[i] = *reinterpret_cast<const u4v *>(vp + so + 16 * i);
-        }
-    } else {
-        const u2v a = *reinterpret_cast<const u2v *>(kp + so), b = *reinterpret_cast<const u2v *>(vp + so);
-        t.dk[0] = u4v{a[0], a[1], 0u, 0u};
-        t.dv[0] = u4v{b[0], b[1], 0u, 0u};
-    }
-}
-
 // fp16 scale j (0 .. 4*NB-1, cell-major: cell i = j / NB, block kb = j % NB)
 // of a lane's scale vector.
 template <int NS>
@@ -346,17 +331,25 @@ __device__ __forceinline__ float scale_at(const u4v (&d)[NS], int j) {
 }
 
 // grid (parts, Hkv, n_seq); part p attends tiles [p*tpw, p*tpw + tpw) of its
-// (sequence, KV head).  MODE: kGiven (sel / nsel read), kDense (every block
-// below the length), kSelect (the workgroup selects from ws.scores with KPT
-// keys a thread; part 0 writes sel / nsel out).
-template <int HD, int G, int MODE, int KPT>
+// (sequence, KV head), tpw <= TM.  MODE: kGiven (sel / nsel read), kDense
+// (every block below the length), kSelect (the workgroup selects from
+// ws.scores with KPT keys a thread; part 0 writes sel / nsel out).  Dynamic
+// LDS: dec_union_bytes<HD, G, MODE, TM>() for the union, then npt_lds page
+// entries (the sequence's page-table row, when parked).
+template <int HD, int G, int MODE, int KPT, int TM>
 __global__ void __launch_bounds__(kDecThreads)
 k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len, int32_t max_seq_len,
-      int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t tpw) {
+      int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t tpw, int32_t npt_lds) {
 #pragma clang fp contract(off)
     static_assert(G <= 16, "one matrix-core column per query head");
-    constexpr int NB = HD / 32, ND = HD / 16;
-    __shared__ DecShared<HD, G> sh;
+    static_assert(TM >= 1 && TM <= 4, "tiles a part");
+    using S = DecStage<HD>;
+    constexpr int NB = S::NB, ND = S::ND, NS = S::NS;
+    constexpr int UB = dec_union_bytes<HD, G, MODE, TM>();
+    __shared__ DecShared<G> sh;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dec_dyn[];
+    DecSel &ss = *reinterpret_cast<DecSel *>(dec_dyn);
+    int32_t *ptab = reinterpret_cast<int32_t *>(dec_dyn + UB);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hn = lane & 15, lg = lane >> 4;
     const int part = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const int pair = s * g.Hkv + gh;
@@ -367,13 +360,14 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     const int32_t *prow = v.page_table + (int64_t)s * g.pps;
     const int npt = min(g.pps, (max_seq_len + g.pt - 1) / g.pt);
     const bool park = MODE != kDense && npt <= kDecPtLds;
-    constexpr int PTV = kDecPtLds / (4 * kDecThreads);   // 16-byte page-table loads a thread
+    constexpr int PTV = kDecPtLds / (4 * kDecThreads);   // 16-byte page-table loads a thread at most
     u4v pt4[PTV];
     if (park) {                                    // entries past npt read 0 (never looked up)
         const BufRsrc prs = buf_rsrc(prow, (uint32_t)npt * 4u);
 #pragma unroll
         for (int k = 0; k < PTV; ++k)
-            pt4[k] = __builtin_bit_cast(u4v, BufLoad<4>::at(prs, (4 * tid + 4 * kDecThreads * k) * 4, 0));
+            if (4 * kDecThreads * k < npt_lds)
+                pt4[k] = __builtin_bit_cast(u4v, BufLoad<4>::at(prs, (4 * tid + 4 * kDecThreads * k) * 4, 0));
     }
     float sv[MODE == kSelect ? KPT : 1];
     if constexpr (MODE == kSelect) {
@@ -396,9 +390,9 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         }
     }
     int n_given = 0;
-    i4v pre;                                       // kGiven: the tiles' blocks; kDense: their pages
+    int32_t pre[TM];                               // kGiven: the tiles' blocks; kDense: their pages
 #pragma unroll
-    for (int i = 0; i < kDecTpwMax; ++i) {
+    for (int i = 0; i < TM; ++i) {
         const int tile = t_first + min(i, tpw - 1);
         if constexpr (MODE == kGiven) {
             pre[i] = sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
@@ -424,10 +418,12 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
     if (park) {
 #pragma unroll
-        for (int k = 0; k < PTV; ++k) *reinterpret_cast<u4v *>(&sh.ptab[4 * tid + 4 * kDecThreads * k]) = pt4[k];
+        for (int k = 0; k < PTV; ++k)
+            if (4 * tid + 4 * kDecThreads * k < npt_lds)
+                *reinterpret_cast<u4v *>(&ptab[4 * tid + 4 * kDecThreads * k]) = pt4[k];
     }
     if constexpr (MODE == kSelect) {               // the selection histogram starts at zero
-        u4v *h4 = reinterpret_cast<u4v *>(sh.u.s.hist);
+        u4v *h4 = reinterpret_cast<u4v *>(ss.hist);
         const u4v z = {0u, 0u, 0u, 0u};
         h4[tid] = z;
         h4[tid + kDecThreads] = z;
@@ -465,7 +461,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
                 }
                 hi = wave_max(hi);
                 lo = -wave_max(-lo);
-                dec_select<KPT>(g, sv, r, topk, lo, hi, sh);
+                dec_select<KPT>(g, sv, r, topk, lo, hi, ss, sh);
             }
             n = min(sh.nsel, max_sel);
         }
@@ -482,38 +478,36 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
     const int tiles_act = n * tpb;
     if (!ok || t_first >= tiles_act) return;       // (uniform) no partial: the merge reads fewer parts
-    const int t_end = min(t_first + tpw, tiles_act);
-    // ---- the tiles
-    auto tile_page = [&](int tile, int32_t &page, int &row0) -> int {   // valid cells of the tile
-        const int i = tile - t_first;
-        auto pre_at = [&](int k) { return k == 0 ? pre[0] : k == 1 ? pre[1] : k == 2 ? pre[2] : pre[3]; };
+    const int nt = min(tpw, tiles_act - t_first);  // tiles of this part, 1 .. TM
+    // ---- the tiles' pages, rows and valid cells (tiles past nt repeat the
+    // last one's addresses with no valid cell, so every wait count below is
+    // a constant)
+    int32_t tpage[TM];
+    int trow[TM], tnv[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int tile = t_first + min(i, nt - 1);
         int blk;
         if constexpr (MODE == kSelect) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
-        else if constexpr (MODE == kGiven) blk = pre_at(i);
+        else if constexpr (MODE == kGiven) blk = pre[min(i, nt - 1)];
         else blk = tile / tpb;
         const int64_t t0 = (int64_t)blk * g.bt + (tile % tpb) * 64;
         const int t0c = (int)min(max(t0, (int64_t)0), (int64_t)g.pps * g.pt - 1);
         int32_t praw;
-        if constexpr (MODE == kDense) praw = pre_at(i);
-        else if (park) praw = sh.ptab[min(t0c / g.pt, npt - 1)];
+        if constexpr (MODE == kDense) praw = pre[min(i, nt - 1)];
+        else if (park) praw = ptab[min(t0c / g.pt, npt - 1)];
         else praw = prow[t0c / g.pt];
         const bool in = blk >= 0 && t0 < L;
         const bool pg_ok = praw >= 0 && praw < g.n_phys;
-        if (in && !pg_ok && tid == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
-        page = praw;
-        row0 = t0c % g.pt;
-        return in && pg_ok ? min(64, L - t0c) : 0;
-    };
-    DecTile<HD> cur;
-    {
-        int32_t page;
-        int row0;
-        const int nv = tile_page(t_first, page, row0);
-        dec_load_tile<HD>(g, v, gh, page, row0, nv, cur);
+        if (i < nt && in && !pg_ok && tid == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+        tpage[i] = in && pg_ok ? praw : 0;         // an empty tile reads page 0 (in bounds), all masked
+        trow[i] = t0c % g.pt;
+        tnv[i] = i < nt && in && pg_ok ? min(64, L - t0c) : 0;
     }
-    // the query split, while the first tile's loads are in flight: scaled by a
-    // power of two so its largest magnitude is in [2^13, 2^14), then fp16
-    // high + low parts (residual below 2^-22 of the largest)
+    // the query split: scaled by a power of two so its largest magnitude is in
+    // [2^13, 2^14), then fp16 high + low parts (residual below 2^-22 of the
+    // largest).  Done before the tile transfers go out, so that no wait for
+    // the query loads can also wait for them.
     h8v qhi[NB], qlo[NB];
     float qfac;
     {
@@ -537,85 +531,126 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
                 qlo[kb][e] = (_Float16)(x - (float)h);
             }
     }
-    float m_run = -INFINITY, l_run = 0.0f;
-    f4v o[ND];
+    // ---- every transfer of the part's tiles, wave w its own cells' bytes:
+    // K chunk c of cells 16w..16w+15 (256 B), V dim d of them (16 B), their
+    // K and V scale rows; NL transfers a tile, in tile order
+    const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dec_dyn);
 #pragma unroll
-    for (int db = 0; db < ND; ++db) o[db] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 1
-    for (int tile = t_first; tile < t_end; ++tile) {
-        DecTile<HD> nxt;
-        const bool more = tile + 1 < t_end;
-        if (more) {                                // the next tile's loads go out first
-            int32_t page;
-            int row0;
-            const int nv = tile_page(tile + 1, page, row0);
-            dec_load_tile<HD>(g, v, gh, page, row0, nv, nxt);
+    for (int i = 0; i < TM; ++i) {
+        const uint32_t wb = __builtin_amdgcn_readfirstlane(sbase + (uint32_t)((i * kDecWaves + w) * S::BYTES));
+        const int64_t pb = (int64_t)tpage[i] * g.page_bytes;
+        const uint8_t *kp = (const uint8_t *)v.k_pages + pb;
+        const uint8_t *vp = (const uint8_t *)v.v_pages + pb;
+        const int tl = gh * (g.pt / 64) + trow[i] / 64;
+#pragma unroll
+        for (int j = 0; j < S::NKV; ++j)
+            lds_dma16(kp + ((int64_t)tl * ND + 4 * j + (lane >> 4)) * 1024 + (16 * w + (lane & 15)) * 16,
+                      wb + S::KOFF + j * 1024);
+#pragma unroll
+        for (int j = 0; j < S::NKV; ++j)
+            lds_dma16(vp + ((int64_t)tl * HD + 64 * j + lane) * 64 + 16 * w, wb + S::VOFF + j * 1024);
+        constexpr int SL = S::SROW / 16;           // lanes a scale set takes
+        const int64_t so = g.qbytes + (int64_t)(gh * g.pt + trow[i] + 16 * w) * NB * 2;
+        const uint8_t *ssrc = lane < SL ? kp + so + 16 * lane : vp + so + 16 * (lane - SL);
+        if (lane < 2 * SL) lds_dma16(ssrc, wb + S::SOFF);
+    }
+    // ---- pass 1: the logits of every tile as it lands, the largest V scale
+    const int c0 = 16 * w + 4 * lg;                // the lane's cells c0 .. c0+3 (column hn)
+    float sl[TM][4];
+    float dvm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        switch (TM - 1 - i) {                      // tile i has landed (transfers retire in order)
+            case 0: wait_vmcnt<0>(); break;
+            case 1: wait_vmcnt<S::NL>(); break;
+            case 2: wait_vmcnt<2 * S::NL>(); break;
+            default: wait_vmcnt<3 * S::NL>(); break;
         }
-        // QK: one accumulator per 32-dim block
+        const uint8_t *st = dec_dyn + (i * kDecWaves + w) * S::BYTES;
         f4v acc[NB];
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb) {
-            const h8v ka = q8x8_to_h8(make_uint2(cur.k[kb][0], cur.k[kb][1]));
+            const u2v kw = *reinterpret_cast<const u2v *>(st + S::KOFF + (2 * kb + (lg >> 1)) * 256 + hn * 16 +
+                                                          8 * (lg & 1));
+            const h8v ka = q8x8_to_h8(make_uint2(kw[0], kw[1]));
             acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[kb], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[kb], acc[kb], 0, 0, 0);
         }
-        // logits of cells 16w + 4lg + i (column hn), the keys' scales applied in block order
-        float sl[4];
-        const int c0 = 16 * w + 4 * lg;
+        u4v dk[NS], dv[NS];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float x = scale_at(cur.dk, i * NB) * acc[0][i];
-#pragma unroll
-            for (int kb = 1; kb < NB; ++kb) x += scale_at(cur.dk, i * NB + kb) * acc[kb][i];
-            sl[i] = c0 + i < cur.nv ? x * qfac : -INFINITY;
+        for (int k = 0; k < NS; ++k) {
+            dk[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + 4 * lg * NB * 2 + 16 * k);
+            dv[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + S::SROW + 4 * lg * NB * 2 + 16 * k);
         }
-        // online softmax over the wave's cells, per column
-        const float mt = col_max4(fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3])));
-        const float m_new = fmaxf(m_run, mt);
-        const float corr = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        // logits of cells c0 + c (column hn), the keys' scales applied in block order
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float x = scale_at(dk, c * NB) * acc[0][c];
+#pragma unroll
+            for (int kb = 1; kb < NB; ++kb) x += scale_at(dk, c * NB + kb) * acc[kb][c];
+            sl[i][c] = c0 + c < tnv[i] ? x * qfac : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < 4 * NB; ++j) dvm = fmaxf(dvm, c0 + j / NB < tnv[i] ? scale_at(dv, j) : 0.0f);
+    }
+    // the part's column maximum, and the column's weight scale 2^k that puts
+    // its largest V scale near 2^15 (p <= 1, so every weight stays below 2^15)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+        mx = fmaxf(mx, fmaxf(fmaxf(sl[i][0], sl[i][1]), fmaxf(sl[i][2], sl[i][3])));
+    const float m = col_max4(mx);
+    dvm = col_max4(dvm);
+    int ev = 0;
+    frexpf(dvm, &ev);
+    const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - ev) : 1.0f;
+    const float down = dvm > 0.0f ? ldexpf(1.0f, ev - 15) : 1.0f;
+    // ---- pass 2: weights and PV, O accumulated on the matrix cores
+    f4v o[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) o[db] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    float ls = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const uint8_t *st = dec_dyn + (i * kDecWaves + w) * S::BYTES;
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = sl[i] == -INFINITY ? 0.0f : fast_exp2(sl[i] - m_new);
-        l_run = l_run * corr + col_sum4((p[0] + p[1]) + (p[2] + p[3]));
-        m_run = m_new;
-        // PV: weights times the V scale and 2^k (the largest valid scale of
-        // the wave near 2^15) in fp16 high + low parts
-        float dvm = 0.0f;
+        for (int c = 0; c < 4; ++c) p[c] = sl[i][c] == -INFINITY ? 0.0f : fast_exp2(sl[i][c] - m);
+        ls += (p[0] + p[1]) + (p[2] + p[3]);
+        u4v dv[NS];
 #pragma unroll
-        for (int j = 0; j < 4 * NB; ++j) dvm = fmaxf(dvm, c0 + j / NB < cur.nv ? scale_at(cur.dv, j) : 0.0f);
-        dvm = wave_max(dvm);
-        int ev = 0;
-        frexpf(dvm, &ev);
-        const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - ev) : 1.0f;
-        const float down = dvm > 0.0f ? ldexpf(1.0f, ev - 15) : 1.0f;
+        for (int k = 0; k < NS; ++k)
+            dv[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + S::SROW + 4 * lg * NB * 2 + 16 * k);
         h4v bhi[NB], blo[NB];
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float dvi = c0 + i < cur.nv ? scale_at(cur.dv, i * NB + kb) : 0.0f;
-                const float x = p[i] * dvi * up;
+            for (int c = 0; c < 4; ++c) {
+                const float dvi = c0 + c < tnv[i] ? scale_at(dv, c * NB + kb) * up : 0.0f;
+                const float x = p[c] * dvi;
                 const _Float16 h = (_Float16)x;
-                bhi[kb][i] = h;
-                blo[kb][i] = (_Float16)(x - (float)h);
+                bhi[kb][c] = h;
+                blo[kb][c] = (_Float16)(x - (float)h);
             }
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-            const h4v va = q8x4_to_h4(cur.v[db]);
-            f4v a = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[db / 2], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            a = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[db / 2], a, 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) o[db][j] = o[db][j] * corr + a[j] * down;
+            const h4v va = q8x4_to_h4(*reinterpret_cast<const uint32_t *>(st + S::VOFF + (16 * db + hn) * 16 + 4 * lg));
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[db / 2], o[db], 0, 0, 0);
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[db / 2], o[db], 0, 0, 0);
         }
-        if (more) cur = nxt;
     }
-    // ---- the four waves' states into one partial
+    const float l = col_sum4(ls);
+    // ---- the four waves' states into one partial (the waves' O overlays the
+    // staged tiles: every wave has read its own first)
+    __syncthreads();
+    float *wo = reinterpret_cast<float *>(dec_dyn);   // [kDecWaves][G][HD]
     if (hn < G) {
-        if (lg == 0) { sh.wml[w][hn][0] = m_run; sh.wml[w][hn][1] = l_run; }
+        if (lg == 0) { sh.wml[w][hn][0] = m; sh.wml[w][hn][1] = l; }
 #pragma unroll
         for (int db = 0; db < ND; ++db)
-            *reinterpret_cast<float4 *>(&sh.u.wo[w][hn][16 * db + 4 * lg]) =
-                make_float4(o[db][0], o[db][1], o[db][2], o[db][3]);
+            *reinterpret_cast<float4 *>(&wo[(w * G + hn) * HD + 16 * db + 4 * lg]) =
+                make_float4(o[db][0] * down, o[db][1] * down, o[db][2] * down, o[db][3] * down);
     }
     __syncthreads();
     const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
@@ -633,7 +668,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         for (int i = 0; i < kDecWaves; ++i) {
             const float mi = sh.wml[i][h][0];
             const float wt = mi == -INFINITY ? 0.0f : fast_exp2(mi - M);
-            O += wt * sh.u.wo[i][h][d];
+            O += wt * wo[(i * G + h) * HD + d];
             Ls += wt * sh.wml[i][h][1];
         }
         ws.part_o[(pb + h) * HD + d] = O;
@@ -644,41 +679,93 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
 }
 
-// Workgroups of one k_dec instantiation the device holds at once: its
-// occupancy per CU (registers, LDS) times the CUs, looked up once per device.
+// Workgroups of one k_dec instantiation a CU holds: its register-bound
+// occupancy (looked up once per device) against the LDS its launch asks for.
 constexpr int kResDevices = 64;
-template <int HD, int G, int MODE, int KPT>
-int dec_resident() {
-    static std::atomic<int> cache[kResDevices];
+struct DecRes {
+    int per_cu, cus, lds_cu, lds_static;
+};
+template <int HD, int G, int MODE, int KPT, int TM>
+bool dec_res(DecRes *out) {
+    static std::atomic<int> cache[kResDevices][4];
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kResDevices) return 0;
-    int r = cache[dev].load(std::memory_order_relaxed);
-    if (r > 0) return r;
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT>, kDecThreads, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    r = per_cu * cus;
-    cache[dev].store(r, std::memory_order_relaxed);
-    return r;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kResDevices) return false;
+    std::atomic<int> *c = cache[dev];
+    if (c[0].load(std::memory_order_acquire) <= 0) {
+        int per_cu = 0, cus = 0, lds_cu = 0;
+        hipFuncAttributes fa;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT, TM>, kDecThreads, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+            hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(k_dec<HD, G, MODE, KPT, TM>)) != hipSuccess)
+            return false;
+        c[1].store(cus, std::memory_order_relaxed);
+        c[2].store(lds_cu, std::memory_order_relaxed);
+        c[3].store((int)fa.sharedSizeBytes, std::memory_order_relaxed);
+        c[0].store(per_cu > 0 ? per_cu : 1, std::memory_order_release);
+    }
+    out->per_cu = c[0].load(std::memory_order_acquire);
+    out->cus = c[1].load(std::memory_order_relaxed);
+    out->lds_cu = c[2].load(std::memory_order_relaxed);
+    out->lds_static = c[3].load(std::memory_order_relaxed);
+    return true;
+}
+
+// Parked page-table entries of a launch (0: the row is looked up in memory).
+inline int dec_npt_lds(const Geo &g, int32_t max_seq_len, int mode) {
+    const int npt = std::min(g.pps, (int)(((int64_t)max_seq_len + g.pt - 1) / g.pt));
+    return mode != kDense && npt <= kDecPtLds ? (npt + 3) / 4 * 4 : 0;
+}
+
+// Resident workgroups of the TM instantiation at this launch's LDS (0 when
+// unknown).
+template <int HD, int G, int MODE, int KPT, int TM>
+int64_t dec_resident(int dyn_bytes) {
+    DecRes r;
+    if (!dec_res<HD, G, MODE, KPT, TM>(&r)) return 0;
+    int per = r.per_cu;
+    const int lds = r.lds_static + dyn_bytes;
+    if (r.lds_cu > 0 && lds > 0) per = std::min(per, r.lds_cu / lds);
+    return (int64_t)std::max(per, 0) * r.cus;
+}
+
+template <int HD, int G, int MODE, int KPT, int TM>
+void launch_dec_tm(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
+                   int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, int npt_lds,
+                   int dyn, hipStream_t st) {
+    const int parts = (ws.n_tiles + TM - 1) / TM;
+    QWFN_LAUNCH_SHM(kTimedAttention, (k_dec<HD, G, MODE, KPT, TM>),
+                    dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kDecThreads), (unsigned)dyn, st,
+                    g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, ws, (int32_t)TM, (int32_t)npt_lds);
 }
 
 // Launches k_dec; returns the tiles a workgroup took.  One tile a workgroup
 // unless the grid would then not be resident at once (a second round of
-// workgroups starts only when the first ends): then the fewest tiles a
-// workgroup, up to kDecTpwMax, that fit it.
+// workgroups starts only when the first ends): then two, else four.
 template <int HD, int G, int MODE, int KPT>
 int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                  int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
     const int64_t pairs = (int64_t)n_seq * g.Hkv;
-    const int res = dec_resident<HD, G, MODE, KPT>();
-    int tpw = 1;
-    while (tpw < kDecTpwMax && res > 0 && pairs * ((ws.n_tiles + tpw - 1) / tpw) > res) ++tpw;
-    const int parts = (ws.n_tiles + tpw - 1) / tpw;
-    QWFN_LAUNCH(kTimedAttention, (k_dec<HD, G, MODE, KPT>),
-                dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kDecThreads), st, g, v, q, seq_len,
-                max_seq_len, sel, nsel, max_sel, ws, tpw);
-    return tpw;
+    const int npt_lds = dec_npt_lds(g, max_seq_len, MODE);
+    const int d1 = dec_union_bytes<HD, G, MODE, 1>() + 4 * npt_lds;
+    const int d2 = dec_union_bytes<HD, G, MODE, 2>() + 4 * npt_lds;
+    const int d4 = dec_union_bytes<HD, G, MODE, 4>() + 4 * npt_lds;
+    const int64_t r1 = dec_resident<HD, G, MODE, KPT, 1>(d1);
+    if (r1 <= 0 || pairs * ws.n_tiles <= r1) {
+        launch_dec_tm<HD, G, MODE, KPT, 1>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
+                                           d1, st);
+        return 1;
+    }
+    const int64_t r2 = dec_resident<HD, G, MODE, KPT, 2>(d2);
+    if (pairs * ((ws.n_tiles + 1) / 2) <= r2) {
+        launch_dec_tm<HD, G, MODE, KPT, 2>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
+                                           d2, st);
+        return 2;
+    }
+    launch_dec_tm<HD, G, MODE, KPT, 4>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, d4,
+                                       st);
+    return 4;
 }
 
 template <int HD, int G>

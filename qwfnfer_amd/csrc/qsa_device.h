@@ -248,6 +248,28 @@ __device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
     return r;
 }
 
+// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): lane
+// l's 16 bytes land at LDS byte address lds + 16 l.  Issued from asm so the
+// compiler adds no wait of its own; the caller waits with wait_vmem_all()
+// before reading the destination.  m0 (the LDS base operand) is restored.
+__device__ __forceinline__ void lds_dma16(const void *gsrc, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(gsrc), "s"(lds)
+                 : "memory");
+}
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Wait until at most N of the wave's vector-memory operations are in flight
+// (loads retire in issue order, so the oldest have landed); asm so that no
+// memory access is moved across it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"I"(N) : "memory");
+}
+
 // Matrix-core operand layouts (v_mfma_*_16x16x32_*, wave64), lane l = 16*lg + hn:
 //   A: row hn, k = 8*lg .. 8*lg+7;  B: column hn, k = 8*lg .. 8*lg+7;
 //   D: rows 4*lg .. 4*lg+3, column hn.

@@ -104,14 +104,15 @@ inline bool take_timer(int kind, hipStream_t st, hipEvent_t *a, hipEvent_t *b) {
     return hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
 }
 
-#define QWFN_LAUNCH(kind, kern, grid, block, st, ...)                                 \
+#define QWFN_LAUNCH_SHM(kind, kern, grid, block, shm, st, ...)                        \
     do {                                                                              \
         hipEvent_t qwfn_a_, qwfn_b_;                                                  \
         if (take_timer((kind), (st), &qwfn_a_, &qwfn_b_))                             \
-            hipExtLaunchKernelGGL(kern, grid, block, 0, st, qwfn_a_, qwfn_b_, 0, __VA_ARGS__); \
+            hipExtLaunchKernelGGL(kern, grid, block, shm, st, qwfn_a_, qwfn_b_, 0, __VA_ARGS__); \
         else                                                                          \
-            hipLaunchKernelGGL(kern, grid, block, 0, st, __VA_ARGS__);                \
+            hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__);              \
     } while (0)
+#define QWFN_LAUNCH(kind, kern, grid, block, st, ...) QWFN_LAUNCH_SHM(kind, kern, grid, block, 0, st, __VA_ARGS__)
 
 // Bytes of one token's head row of K (or V) quants / values in a page.
 inline int32_t kv_row_bytes(int32_t kt, int32_t hd) {

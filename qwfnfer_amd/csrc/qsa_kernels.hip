@@ -2132,18 +2132,6 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
-// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): lane
-// l's 16 bytes land at LDS byte address lds + 16 l.  Issued from asm so the
-// compiler adds no wait of its own; the caller waits with wait_vmem_all()
-// before reading the destination.  m0 (the LDS base operand) is restored.
-__device__ __forceinline__ void lds_dma16(const void *gsrc, uint32_t lds) {
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(gsrc), "s"(lds)
-                 : "memory");
-}
-__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int HD, int G>
 struct PfAttnCfg {
