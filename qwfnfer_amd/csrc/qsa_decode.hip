@@ -558,7 +558,8 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     // ---- pass 1: the logits of every tile as it lands, the largest V scale
     const int c0 = 16 * w + 4 * lg;                // the lane's cells c0 .. c0+3 (column hn)
     float sl[TM][4];
-    float dvm = 0.0f;
+    u4v dvw[TM][NS];                               // the cells' V scales, 0 past the tile's valid cells
+    h8v dmx = {};                                  // their running maximum (fp16 scales are >= 0)
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         switch (TM - 1 - i) {                      // tile i has landed (transfers retire in order)
@@ -577,22 +578,30 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[kb], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[kb], acc[kb], 0, 0, 0);
         }
-        u4v dk[NS], dv[NS];
+        h8v dk[NS];
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
-            dk[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + 4 * lg * NB * 2 + 16 * k);
-            dv[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + S::SROW + 4 * lg * NB * 2 + 16 * k);
+            dk[k] = __builtin_bit_cast(h8v, *reinterpret_cast<const u4v *>(st + S::SOFF + 4 * lg * NB * 2 + 16 * k));
+            dvw[i][k] = *reinterpret_cast<const u4v *>(st + S::SOFF + S::SROW + 4 * lg * NB * 2 + 16 * k);
         }
-        // logits of cells c0 + c (column hn), the keys' scales applied in block order
+        // logits of cells c0 + c (column hn): the keys' scales applied in block
+        // order, each a fused multiply-add with the scale taken as fp16
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            float x = scale_at(dk, c * NB) * acc[0][c];
+            float x = 0.0f;
 #pragma unroll
-            for (int kb = 1; kb < NB; ++kb) x += scale_at(dk, c * NB + kb) * acc[kb][c];
+            for (int kb = 0; kb < NB; ++kb)
+                x = __builtin_fmaf((float)dk[(c * NB + kb) / 8][(c * NB + kb) % 8], acc[kb][c], x);
             sl[i][c] = c0 + c < tnv[i] ? x * qfac : -INFINITY;
         }
+        // a word holds two blocks' scales of one cell: NB / 2 words a cell
 #pragma unroll
-        for (int j = 0; j < 4 * NB; ++j) dvm = fmaxf(dvm, c0 + j / NB < tnv[i] ? scale_at(dv, j) : 0.0f);
+        for (int k = 0; k < NS; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c0 + (4 * k + e) / (NB / 2) >= tnv[i]) dvw[i][k][e] = 0u;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) dmx = __builtin_elementwise_max(dmx, __builtin_bit_cast(h8v, dvw[i][k]));
     }
     // the part's column maximum, and the column's weight scale 2^k that puts
     // its largest V scale near 2^15 (p <= 1, so every weight stays below 2^15)
@@ -601,6 +610,9 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     for (int i = 0; i < TM; ++i)
         mx = fmaxf(mx, fmaxf(fmaxf(sl[i][0], sl[i][1]), fmaxf(sl[i][2], sl[i][3])));
     const float m = col_max4(mx);
+    float dvm = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dvm = fmaxf(dvm, (float)dmx[e]);
     dvm = col_max4(dvm);
     int ev = 0;
     frexpf(dvm, &ev);
@@ -614,24 +626,25 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const uint8_t *st = dec_dyn + (i * kDecWaves + w) * S::BYTES;
-        float p[4];
+        float pu[4];                               // the weights times 2^k (0 past the valid cells)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) p[c] = sl[i][c] == -INFINITY ? 0.0f : fast_exp2(sl[i][c] - m);
-        ls += (p[0] + p[1]) + (p[2] + p[3]);
-        u4v dv[NS];
-#pragma unroll
-        for (int k = 0; k < NS; ++k)
-            dv[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + S::SROW + 4 * lg * NB * 2 + 16 * k);
+        for (int c = 0; c < 4; ++c) {
+            const float p = sl[i][c] == -INFINITY ? 0.0f : fast_exp2(sl[i][c] - m);
+            ls += p;
+            pu[c] = p * up;
+        }
+        // weight of (cell c, block kb) = pu[c] * d_v(c, kb), rounded once, as
+        // fp16 high + low parts
         h4v bhi[NB], blo[NB];
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const float dvi = c0 + c < tnv[i] ? scale_at(dv, c * NB + kb) * up : 0.0f;
-                const float x = p[c] * dvi;
-                const _Float16 h = (_Float16)x;
+                const h8v dw = __builtin_bit_cast(h8v, dvw[i][(c * NB + kb) / 8]);
+                const float dv = (float)dw[(c * NB + kb) % 8];
+                const _Float16 h = (_Float16)__builtin_fmaf(pu[c], dv, 0.0f);
                 bhi[kb][c] = h;
-                blo[kb][c] = (_Float16)(x - (float)h);
+                blo[kb][c] = (_Float16)__builtin_fmaf(pu[c], dv, -(float)h);
             }
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
