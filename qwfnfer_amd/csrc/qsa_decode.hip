@@ -356,6 +356,19 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     const int tpb = g.bt / 64;
     const int t_first = part * tpw;
     // ---- first round trip: everything that does not depend on the selection
+    // (the query rows first: their split below runs while the rest is in flight)
+    const int hq = min(hn, G - 1);
+    float qv[NB][8];
+    {
+        const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + hq) * HD + 8 * lg;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            const float4 a = *reinterpret_cast<const float4 *>(qh + 32 * kb);
+            const float4 b = *reinterpret_cast<const float4 *>(qh + 32 * kb + 4);
+            qv[kb][0] = a.x; qv[kb][1] = a.y; qv[kb][2] = a.z; qv[kb][3] = a.w;
+            qv[kb][4] = b.x; qv[kb][5] = b.y; qv[kb][6] = b.z; qv[kb][7] = b.w;
+        }
+    }
     const int L = seq_len[s];
     const int32_t *prow = v.page_table + (int64_t)s * g.pps;
     const int npt = min(g.pps, (max_seq_len + g.pt - 1) / g.pt);
@@ -404,30 +417,45 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         }
     }
     if constexpr (MODE == kGiven) n_given = nsel[pair];
-    const int hq = min(hn, G - 1);
-    float qv[NB][8];
-    {
-        const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + hq) * HD + 8 * lg;
-#pragma unroll
-        for (int kb = 0; kb < NB; ++kb) {
-            const float4 a = *reinterpret_cast<const float4 *>(qh + 32 * kb);
-            const float4 b = *reinterpret_cast<const float4 *>(qh + 32 * kb + 4);
-            qv[kb][0] = a.x; qv[kb][1] = a.y; qv[kb][2] = a.z; qv[kb][3] = a.w;
-            qv[kb][4] = b.x; qv[kb][5] = b.y; qv[kb][6] = b.z; qv[kb][7] = b.w;
-        }
-    }
-    if (park) {
-#pragma unroll
-        for (int k = 0; k < PTV; ++k)
-            if (4 * tid + 4 * kDecThreads * k < npt_lds)
-                *reinterpret_cast<u4v *>(&ptab[4 * tid + 4 * kDecThreads * k]) = pt4[k];
-    }
     if constexpr (MODE == kSelect) {               // the selection histogram starts at zero
         u4v *h4 = reinterpret_cast<u4v *>(ss.hist);
         const u4v z = {0u, 0u, 0u, 0u};
         h4[tid] = z;
         h4[tid + kDecThreads] = z;
         if (tid < 16) h4[2 * kDecThreads + tid] = z;
+    }
+    // the query split: scaled by a power of two so its largest magnitude is in
+    // [2^13, 2^14), then fp16 high + low parts (residual below 2^-22 of the
+    // largest).  The query loads went out first, so this waits for them alone
+    // and runs while the page table and the scores are still in flight.
+    h8v qhi[NB], qlo[NB];
+    float qfac;
+    {
+        float a = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(qv[kb][e]));
+        a = col_max4(a);
+        int ex = 0;
+        frexpf(a, &ex);                            // a in [2^(ex-1), 2^ex)
+        const float up = a > 0.0f ? ldexpf(1.0f, 14 - ex) : 1.0f;
+        qfac = (a > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f) * g.scale_log2;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qv[kb][e] * up;
+                const _Float16 h = (_Float16)x;
+                qhi[kb][e] = h;
+                qlo[kb][e] = (_Float16)(x - (float)h);
+            }
+    }
+    if (park) {
+#pragma unroll
+        for (int k = 0; k < PTV; ++k)
+            if (4 * tid + 4 * kDecThreads * k < npt_lds)
+                *reinterpret_cast<u4v *>(&ptab[4 * tid + 4 * kDecThreads * k]) = pt4[k];
     }
     const bool ok = L >= 1 && L <= max_seq_len;
     // ---- the blocks of this part's tiles
@@ -504,33 +532,6 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         trow[i] = t0c % g.pt;
         tnv[i] = i < nt && in && pg_ok ? min(64, L - t0c) : 0;
     }
-    // the query split: scaled by a power of two so its largest magnitude is in
-    // [2^13, 2^14), then fp16 high + low parts (residual below 2^-22 of the
-    // largest).  Done before the tile transfers go out, so that no wait for
-    // the query loads can also wait for them.
-    h8v qhi[NB], qlo[NB];
-    float qfac;
-    {
-        float a = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(qv[kb][e]));
-        a = col_max4(a);
-        int ex = 0;
-        frexpf(a, &ex);                            // a in [2^(ex-1), 2^ex)
-        const float up = a > 0.0f ? ldexpf(1.0f, 14 - ex) : 1.0f;
-        qfac = (a > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f) * g.scale_log2;
-#pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float x = qv[kb][e] * up;
-                const _Float16 h = (_Float16)x;
-                qhi[kb][e] = h;
-                qlo[kb][e] = (_Float16)(x - (float)h);
-            }
-    }
     // ---- every transfer of the part's tiles, wave w its own cells' bytes:
     // K chunk c of cells 16w..16w+15 (256 B), V dim d of them (16 B), their
     // K and V scale rows; NL transfers a tile, in tile order
@@ -538,7 +539,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dec_dyn);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        const uint32_t wb = __builtin_amdgcn_readfirstlane(sbase + (uint32_t)((i * kDecWaves + w) * S::BYTES));
+        const uint32_t wb = __builtin_amdgcn_readfirstlane(sbase + (uint32_t)((w * TM + i) * S::BYTES));
         const int64_t pb = (int64_t)tpage[i] * g.page_bytes;
         const uint8_t *kp = (const uint8_t *)v.k_pages + pb;
         const uint8_t *vp = (const uint8_t *)v.v_pages + pb;
@@ -568,7 +569,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             case 2: wait_vmcnt<2 * S::NL>(); break;
             default: wait_vmcnt<3 * S::NL>(); break;
         }
-        const uint8_t *st = dec_dyn + (i * kDecWaves + w) * S::BYTES;
+        const uint8_t *st = dec_dyn + (w * TM + i) * S::BYTES;
         f4v acc[NB];
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb) {
@@ -625,7 +626,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     float ls = 0.0f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        const uint8_t *st = dec_dyn + (i * kDecWaves + w) * S::BYTES;
+        const uint8_t *st = dec_dyn + (w * TM + i) * S::BYTES;
         float pu[4];                               // the weights times 2^k (0 past the valid cells)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -654,41 +655,54 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         }
     }
     const float l = col_sum4(ls);
-    // ---- the four waves' states into one partial (the waves' O overlays the
-    // staged tiles: every wave has read its own first)
-    __syncthreads();
-    float *wo = reinterpret_cast<float *>(dec_dyn);   // [kDecWaves][G][HD]
+    // ---- the four waves' states into one partial.  A wave's O goes over its
+    // own staging slots (only it reads them, so no barrier first) when they
+    // hold it, else over the region start once every wave is done.
+    constexpr bool kOwnSlots = G * HD * 4 <= TM * S::BYTES;
+    auto wave_o = [&](int i) {
+        return reinterpret_cast<float *>(dec_dyn + (kOwnSlots ? i * TM * S::BYTES : i * G * HD * 4));
+    };
+    if constexpr (!kOwnSlots) __syncthreads();
     if (hn < G) {
         if (lg == 0) { sh.wml[w][hn][0] = m; sh.wml[w][hn][1] = l; }
+        float *wo = wave_o(w);
 #pragma unroll
         for (int db = 0; db < ND; ++db)
-            *reinterpret_cast<float4 *>(&wo[(w * G + hn) * HD + 16 * db + 4 * lg]) =
+            *reinterpret_cast<float4 *>(&wo[hn * HD + 16 * db + 4 * lg]) =
                 make_float4(o[db][0] * down, o[db][1] * down, o[db][2] * down, o[db][3] * down);
     }
     __syncthreads();
+    // thread t: head t / (HD / 4), dims 4 (t % (HD / 4)) .. +3; every wave's
+    // (max, sum) and O of them read in one round, summed in wave order
+    constexpr int TPH = HD / 4;
     const int64_t pb = ((int64_t)pair * ws.n_tiles + part) * G;
-    static_assert((G * HD) % kDecThreads == 0 || G * HD < kDecThreads, "whole outputs a thread");
 #pragma unroll
-    for (int r = 0; r < (G * HD + kDecThreads - 1) / kDecThreads; ++r) {
-        const int k = tid + r * kDecThreads;
-        if (k >= G * HD) break;
-        const int h = k / HD, d = k % HD;
-        float M = sh.wml[0][h][0];
-#pragma unroll
-        for (int i = 1; i < kDecWaves; ++i) M = fmaxf(M, sh.wml[i][h][0]);
-        float O = 0.0f, Ls = 0.0f;
+    for (int k = tid; k < G * TPH; k += kDecThreads) {
+        const int h = k / TPH, d = 4 * (k % TPH);
+        float mi[kDecWaves], li[kDecWaves];
+        float4 oi[kDecWaves];
 #pragma unroll
         for (int i = 0; i < kDecWaves; ++i) {
-            const float mi = sh.wml[i][h][0];
-            const float wt = mi == -INFINITY ? 0.0f : fast_exp2(mi - M);
-            O += wt * wo[(i * G + h) * HD + d];
-            Ls += wt * sh.wml[i][h][1];
+            mi[i] = sh.wml[i][h][0];
+            li[i] = sh.wml[i][h][1];
+            oi[i] = *reinterpret_cast<const float4 *>(&wave_o(i)[h * HD + d]);
         }
-        ws.part_o[(pb + h) * HD + d] = O;
-        if (d == 0) {
-            ws.part_ml[(pb + h) * 2 + 0] = M;
-            ws.part_ml[(pb + h) * 2 + 1] = Ls;
+        float M = mi[0];
+#pragma unroll
+        for (int i = 1; i < kDecWaves; ++i) M = fmaxf(M, mi[i]);
+        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float Ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDecWaves; ++i) {
+            const float wt = mi[i] == -INFINITY ? 0.0f : fast_exp2(mi[i] - M);
+            O.x += wt * oi[i].x;
+            O.y += wt * oi[i].y;
+            O.z += wt * oi[i].z;
+            O.w += wt * oi[i].w;
+            Ls += wt * li[i];
         }
+        *reinterpret_cast<float4 *>(&ws.part_o[(pb + h) * HD + d]) = O;
+        if (d == 0) *reinterpret_cast<float2 *>(&ws.part_ml[(pb + h) * 2]) = make_float2(M, Ls);
     }
 }
 
