@@ -186,7 +186,7 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.cut_wg = cut && nb_max > kIdxRegKeys && !(g.shared && g.Hkv > 1) && cut_wg <= kCutWgMax ? cut_wg : 0;
     l.cand = take(pairs * l.cut_wg * kCutKeys * sizeof(uint2));
     l.ccnt = take(l.cut_wg ? pairs * kCutWgMax * sizeof(int32_t) : 0);
-    l.cmm = take(partials ? pairs * (l.nb_cap / 64) * sizeof(float2) : 0);
+    l.cmm = take(partials ? pairs * (l.nb_cap / kScoreRecBlocks) * sizeof(float2) : 0);
     l.total = off;
     return l;
 }

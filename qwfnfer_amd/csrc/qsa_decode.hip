@@ -392,12 +392,16 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             sv[4 * k] = x[0]; sv[4 * k + 1] = x[1]; sv[4 * k + 2] = x[2]; sv[4 * k + 3] = x[3];
         }
     }
-    float2 rec[2];                                 // kSelect: the scoring chunks' (min, max), lanes l, l + 64
+    // kSelect: the scoring launch's (min, max) records, one per kScoreRecBlocks
+    // blocks: record lane + 64 k in rec[k] (the span this instantiation
+    // selects over needs at most KPT/4 + 1 of them a lane)
+    constexpr int RPL = MODE == kSelect ? KPT / 4 + 2 : 1;
+    float2 rec[RPL];
     if constexpr (MODE == kSelect) {
-        const int n_ch = ws.nb_cap / 64;           // at most 128: 8192 eligible blocks
+        const int n_ch = ws.nb_cap / kScoreRecBlocks;
         const BufRsrc rr = buf_rsrc(ws.cmm + (int64_t)pair * n_ch, (uint32_t)n_ch * 8u);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
+        for (int k = 0; k < RPL; ++k) {
             const auto x = BufLoad<2>::at(rr, (lane + 64 * k) * 8, 0);
             rec[k] = make_float2(x[0], x[1]);
         }
@@ -478,11 +482,13 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
                 if (tid == 0) sh.nsel = g.sink + nwin;
                 __syncthreads();
             } else {
-                // the score bounds over the chunks (records past the grid: empty)
-                const int n_ch = ws.nb_cap / 64;
+                // the score bounds over the records (a record that scored nothing
+                // is (+inf, -inf); bounds that miss some scores only make the
+                // threshold bin larger, the selection stays exact)
+                const int n_ch = ws.nb_cap / kScoreRecBlocks;
                 float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
-                for (int k = 0; k < 2; ++k) {
+                for (int k = 0; k < RPL; ++k) {
                     const bool in = lane + 64 * k < n_ch;
                     lo = in && rec[k].x < lo ? rec[k].x : lo;
                     hi = in && rec[k].y > hi ? rec[k].y : hi;

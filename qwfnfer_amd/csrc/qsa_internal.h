@@ -47,6 +47,7 @@ constexpr int32_t kPrefillBatchMax = 32768;   // queries per prefill batch (one 
 constexpr int32_t kIdxRegKeys = 8192;
 constexpr int32_t kCutKeys = 4096;
 constexpr int32_t kCutWgMax = 64;
+constexpr int32_t kScoreRecBlocks = 16;   // blocks per (min, max) score record of the fused call's scoring
 struct Ws {
     int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
     int32_t *sel;        // [n_seq][Hkv][max_sel]  selection of the fused step
@@ -56,7 +57,7 @@ struct Ws {
     float   *part_ml;    // [n_seq][Hkv][n_tiles][G][2]
     uint2   *cand;       // [n_seq][Hkv][cut_wg][kCutKeys] (key, block) candidates of the multi-workgroup selection
     int32_t *ccnt;       // [n_seq][Hkv][kCutWgMax] their counts
-    float2  *cmm;        // [n_seq][Hkv][nb_cap / 64] each scoring chunk's (min, max) eligible score
+    float2  *cmm;        // [n_seq][Hkv][nb_cap / kScoreRecBlocks] (min, max) eligible score of each record's blocks
                          // (the attention's own selection reads them; (+inf, -inf) when empty)
     int32_t  nb_cap, max_sel, n_tiles;
     int32_t  cut_wg;     // workgroups of the multi-workgroup selection (0: one workgroup)

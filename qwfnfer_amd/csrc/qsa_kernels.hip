@@ -1123,7 +1123,7 @@ template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
 k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
           int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t n_chunks, FusedAppend fa,
-          int32_t select_here, int32_t chunk_minmax) {
+          int32_t select_here) {
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
@@ -1164,7 +1164,6 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
 #pragma unroll
         for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
     }
-    float cmx = -INFINITY, cmn = INFINITY;        // this chunk's largest / smallest score (not NaN)
     if (ok && g.topk > 0) {
         const Ranges r = qsa_ranges(g, L);
         const int ne = r.e_hi - r.e_lo;
@@ -1198,25 +1197,7 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
                 score = (h == 0) ? dot : score + dot;
             }
             if (act && j == 0) sc[b] = score;
-            cmx = act && score > cmx ? score : cmx;
-            cmn = act && score < cmn ? score : cmn;
             __syncthreads();                       // q reads done before the union is reused
-        }
-    }
-    // the attention selects: the chunk's (min, max) for its histogram bounds
-    // (every chunk of the grid writes one, (+inf, -inf) when it scored nothing)
-    if (chunk_minmax) {
-        cmx = wave_max(cmx);
-        cmn = -wave_max(-cmn);
-        if ((tid & 63) == 0) { sh.red[tid >> 6] = cmx; sh.red[kIdxThreads / 64 + (tid >> 6)] = cmn; }
-        __syncthreads();
-        if (tid == 0) {
-#pragma unroll
-            for (int i = 1; i < kIdxThreads / 64; ++i) {
-                cmx = fmaxf(cmx, sh.red[i]);
-                cmn = fminf(cmn, sh.red[kIdxThreads / 64 + i]);
-            }
-            ws.cmm[(int64_t)pair * (ws.nb_cap / 64) + c] = make_float2(cmn, cmx);
         }
     }
     // selection in a launch of its own (long contexts: k_select_big)
@@ -1241,6 +1222,133 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         select_blocks<kIdxThreads>(g, sc, L, out, sh);
 }
 
+// ---------------------------------------------------------------------------
+// scoring of the fused decode call (the attention selects): small workgroups
+// so the query rows every lane reads from LDS spread over many CUs
+// ---------------------------------------------------------------------------
+
+// Workgroup size and blocks a workgroup scores: 128 threads (two waves) and 16
+// blocks, 256 and 32 at head_dim 256 (the append workgroup pools with one
+// thread per dimension).  Every 128 threads keep one (min, max) record.
+template <int HD> constexpr int score_threads() { return HD > 128 ? 256 : 128; }
+
+template <int HD, int G>
+struct ScoreShared {
+    union {
+        float q[G * HD];                           // the group's query rows
+        struct { int8_t q8[kStageRows * 256]; uint16_t sc[kStageRows * 8]; } st;   // the append's pooling
+    } u;
+    float newk[256];
+    float red[2][score_threads<HD>() / 64];
+};
+
+// grid (n_wg [+1 with the fused append], Hkv, n_seq).  Lane (b, hh, j) of a
+// workgroup (j = tid & 3, hh = (tid >> 2) & 1, b = tid >> 3) holds dims
+// 16i + 4j .. +3 of block b's pooled key and runs the decode indexer's four
+// fmaf chains of heads hh*G/2 .. hh*G/2 + G/2 - 1 over them; the chains
+// combine (c0+c1)+(c2+c3) across the j lanes and the heads sum in order, the
+// second half continuing the first's sum (so every score is bit-identical to
+// k_indexer's).  Each 128 threads write their 16 blocks' (min, max) eligible
+// score to ws.cmm (+inf, -inf when none), the attention's histogram bounds.
+template <int HD, int G>
+__global__ void __launch_bounds__(score_threads<HD>())
+k_score(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len, Ws ws,
+        int32_t n_wg, FusedAppend fa) {
+#pragma clang fp contract(off)
+    constexpr int NT = score_threads<HD>(), BPW = NT / 8, GH = G / 2;
+    static_assert(G % 2 == 0 && NT >= HD, "two head halves; one pooling thread a dimension");
+    __shared__ ScoreShared<HD, G> sh;
+    const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    if (fa.enabled && c == n_wg) {                 // the append workgroup
+        if (g.kt == QWFN_KV_Q4_0) fused_append_pool<HD, QWFN_KV_Q4_0, NT>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
+        else if (g.kt == QWFN_KV_F16) fused_append_pool<HD, QWFN_KV_F16, NT>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
+        else fused_append_pool<HD, QWFN_KV_Q8_0, NT>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
+        return;
+    }
+    // the query rows, the length and the pooled keys go out together
+    constexpr int QV = (G * HD / 4 + NT - 1) / NT;
+    const float4 *qg4 = reinterpret_cast<const float4 *>(q + ((int64_t)s * g.H + (int64_t)gh * G) * HD);
+    float4 qv[QV];
+#pragma unroll
+    for (int i = 0; i < QV; ++i) qv[i] = qg4[min(tid + i * NT, G * HD / 4 - 1)];
+    const int L = seq_len[s];
+    const bool ok = L >= 1 && L <= max_seq_len;
+    const int pair = s * g.Hkv + gh;
+    const int j = tid & 3, hh = (tid >> 2) & 1, bl = tid >> 3;
+    const int bi = c * BPW + bl;
+    const int bp = min(g.sink + bi, g.bps - 1);
+    const int64_t prow = (((int64_t)s * g.Hkv + gh) * g.bps + bp) * HD;
+    float4 p4[HD / 16];
+    if (g.pooled_f16) {
+        const uint16_t *P = reinterpret_cast<const uint16_t *>(v.pooled) + prow;
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) {
+            const uint2 x = *reinterpret_cast<const uint2 *>(P + 16 * i + 4 * j);
+            p4[i] = make_float4(h2f((uint16_t)x.x), h2f((uint16_t)(x.x >> 16)), h2f((uint16_t)x.y),
+                                h2f((uint16_t)(x.y >> 16)));
+        }
+    } else {
+        const float *P = v.pooled + prow;
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
+    }
+#pragma unroll
+    for (int i = 0; i < QV; ++i)
+        if (tid + i * NT < G * HD / 4) reinterpret_cast<float4 *>(sh.u.q)[tid + i * NT] = qv[i];
+    __syncthreads();
+    float cmx = -INFINITY, cmn = INFINITY;         // this record's largest / smallest score (not NaN)
+    if (ok && g.topk > 0) {
+        const Ranges r = qsa_ranges(g, L);
+        const int ne = r.e_hi - r.e_lo;
+        if (ne > eff_topk(g, r) && c * BPW < ne) {
+            const bool act = bi < ne;
+            float acc[GH];
+#pragma unroll
+            for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD / 16; ++i) {
+#pragma unroll
+                for (int h = 0; h < GH; ++h) {
+                    const float4 q4 = *reinterpret_cast<const float4 *>(&sh.u.q[(hh * GH + h) * HD + 16 * i + 4 * j]);
+                    acc[h] = fmaf(q4.x, p4[i].x, acc[h]);
+                    acc[h] = fmaf(q4.y, p4[i].y, acc[h]);
+                    acc[h] = fmaf(q4.z, p4[i].z, acc[h]);
+                    acc[h] = fmaf(q4.w, p4[i].w, acc[h]);
+                }
+            }
+            float dots[GH];
+#pragma unroll
+            for (int h = 0; h < GH; ++h) {
+                const float t01 = acc[h] + __shfl_xor(acc[h], 1);   // (c0+c1) / (c2+c3)
+                float dot = t01 + __shfl_xor(t01, 2);               // (c0+c1)+(c2+c3)
+                dots[h] = g.relu && !(dot > 0.0f) ? 0.0f : dot;
+            }
+            // the sum of this half's heads in order; the second half (hh = 1)
+            // continues from the first half's: dot_0 + dot_1 + ... + dot_{G-1}
+            float part = dots[0];
+#pragma unroll
+            for (int h = 1; h < GH; ++h) part = part + dots[h];
+            float score = __shfl_xor(part, 4) + dots[0];
+#pragma unroll
+            for (int h = 1; h < GH; ++h) score = score + dots[h];
+            score = hh ? score : part;
+            const int b = r.e_lo + bi;
+            if (act && hh == 1 && j == 0) ws.scores[(int64_t)pair * ws.nb_cap + b] = score;
+            cmx = act && score > cmx ? score : cmx;
+            cmn = act && score < cmn ? score : cmn;
+        }
+    }
+    // this 128-thread half's (min, max): every record of the grid is written
+    cmx = wave_max(cmx);
+    cmn = -wave_max(-cmn);
+    const int w = tid >> 6;
+    if ((tid & 63) == 0) { sh.red[0][w] = cmx; sh.red[1][w] = cmn; }
+    __syncthreads();
+    if ((tid & 127) == 0)
+        ws.cmm[(int64_t)pair * (ws.nb_cap / kScoreRecBlocks) + c * (NT / 128) + (tid >> 7)] =
+            make_float2(fminf(sh.red[1][w], sh.red[1][w + 1]), fmaxf(sh.red[0][w], sh.red[0][w + 1]));
+}
+
 template <int HD, int G>
 static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                                    const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
@@ -1258,15 +1366,22 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
         if (e != hipSuccess) return e;
         fa.enabled = 0;
     }
+    if (!select) {                                 // the attention selects (k_dec / k_attn<..., SEL>)
+        const int n_wg = ws.nb_cap / (score_threads<HD>() / 8);   // every (min, max) record written
+        const dim3 grid((unsigned)(n_wg + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
+        QWFN_LAUNCH(kTimedIndexer, (k_score<HD, G>), grid, dim3(score_threads<HD>()), st, g, v, q, seq_len,
+                    max_seq_len, ws, n_wg, fa);
+        return hipGetLastError();
+    }
     const int nb_max = max_seq_len / g.bt;
     int n_chunks = (nb_max + kBlocksPerChunk - 1) / kBlocksPerChunk;
     if (n_chunks < 1) n_chunks = 1;
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     QWFN_LAUNCH(kTimedIndexer, (k_indexer<HD, G>), grid, dim3(kIdxThreads), st, g, v, q, seq_len, max_seq_len,
-                sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)(select && !big), (int32_t)!select);
+                sel, nsel, max_sel, ws, n_chunks, fa, (int32_t)!big);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !select) return e;      // !select: the attention selects (k_dec / k_attn<..., SEL>)
+    if (e != hipSuccess) return e;
     if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
         hipLaunchKernelGGL(k_select_cut, dim3((unsigned)ws.cut_wg, (unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws, sel, nsel, max_sel);
