@@ -1404,43 +1404,42 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
 //   og = sum_i w_i O_i / sum_i w_i l_i,  w_i = exp2(m_i - max_i m_i)
 // over the parts the attention wrote (its workgroups of tg tile groups, the
 // count recomputed from the length and the selection as the attention counts
-// it).  Thread t sums dim t % HD over the parts congruent to t / HD, its first
-// batch of part loads issued before the weights are known; a length out of
-// range or no cell gives zeros (and, for a length, the status bit).
-// grid (G, Hkv, n_seq or n_q)
-constexpr int kMergeThreads = 512;               // parts r, r + R, ... a thread (R = 512 / head_dim): one load round up to 24 R parts
-constexpr int kMergeWts = 2048;                   // parts whose weights LDS keeps
+// it).  Thread (r, d), r = tid / HD (uniform in a wave), sums dimension d over
+// the parts congruent to r mod R.  The length, the count, the (max, sum)
+// pairs of parts lane and lane + 64, and the thread's first U part rows all go
+// out in the first round trip (rows clamped to the most parts the attention
+// can write, inside the pair's n_tiles rows).  Every wave reduces the maxima
+// and weighted sums itself and takes a part's weight from the lane holding it
+// (no LDS); one barrier adds the R sums.  A length out of range or no cell
+// gives zeros (and, for a length, the status bit).
+// grid (G, Hkv, n_seq or n_q), R * head_dim threads
+template <int HD> constexpr int merge_r() { return HD > 128 ? 2 : 4; }
+constexpr int kMergeRound = 24;                   // part rows a thread loads in one round
 template <int G, int HD>
-__global__ void __launch_bounds__(kMergeThreads)
+__global__ void __launch_bounds__(merge_r<HD>() * HD)
 k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, const int32_t *nsel,
         int32_t max_sel, int32_t dense, float *__restrict__ out, Ws ws, int32_t tg) {
-    constexpr int NT = kMergeThreads, R = NT / HD, NW = NT / 64, U = 24;
-    static_assert(R * HD == NT, "whole dims a thread");
-    __shared__ float wts[kMergeWts];
+#pragma clang fp contract(off)
+    constexpr int R = merge_r<HD>(), U = kMergeRound, PR = R * U;   // parts a round
+    static_assert(PR <= 128 && HD % 64 == 0, "round weights in two lanes' registers; whole waves");
     __shared__ float red[R][HD];
-    __shared__ float wred[2][NW];
     const int h = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, d = tid % HD, r = tid / HD, lane = tid & 63;
     const int pair = s * g.Hkv + gh;
-    // The length, the count, the first batch of part rows and the (max, sum)
-    // pairs go out together: the part loads are clamped to the most parts the
-    // attention can write, ceil(n_tiles / tg), inside the pair's n_tiles rows
-    // of the workspace whatever the count; a dense call reads the length in
-    // place of the count, and rows past the parts are dropped once the count
-    // is known.
     const int32_t *pl = seq_len + (g.pf ? 0 : s);
     const int L = seq_length(g, *pl, s);
     const int n_raw = *(dense ? pl : nsel + pair);
     const int64_t row = (int64_t)pair * ws.n_tiles * G + h;     // part i: row + i * G
     const float *pml = ws.part_ml + row * 2;
-    const int d = tid % HD, r = tid / HD;
     const float *po = ws.part_o + row * HD + d;
     const int last = (ws.n_tiles + tg - 1) / tg - 1;
+    float2 ml[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        ml[k] = *reinterpret_cast<const float2 *>(pml + (int64_t)min(lane + 64 * k, last) * 2 * G);
     float x[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(r + u * R, last) * G * HD];
-    const int tc = min(tid, last);
-    float m0 = pml[(int64_t)tc * 2 * G], l0 = pml[(int64_t)tc * 2 * G + 1];
+    for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(r + R * u, last) * G * HD];
     const bool ok = L >= 1 && L <= max_seq_len;
     int n = 0;
     if (ok) {
@@ -1450,58 +1449,57 @@ k_merge(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len, cons
     const int parts = ((n * g.bt + 63) / 64 + tg - 1) / tg;
     float *og = out + ((int64_t)s * g.H + (int64_t)gh * G + h) * HD;
     if (!ok || parts == 0) {
-        for (int i = tid; i < HD; i += NT) og[i] = 0.0f;
+        if (r == 0) og[d] = 0.0f;
         if (!ok && tid == 0 && gh == 0 && h == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
         return;
     }
-    if (tid >= parts) { m0 = -INFINITY; l0 = 0.0f; }
-    float Mx = m0;
-    for (int i = tid + NT; i < parts; i += NT) Mx = fmaxf(Mx, pml[(int64_t)i * 2 * G]);
-    Mx = wave_max(Mx);
-    if (lane == 0) wred[0][wid] = Mx;
-    __syncthreads();
+    auto m_of = [&](int i) { return pml[(int64_t)i * 2 * G]; };
+    float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) Mx = fmaxf(Mx, wred[0][i]);
-    auto weight = [&](float m) { return m == -INFINITY ? 0.0f : exp2f(m - Mx); };
-    float Ls = 0.0f;
-    if (tid < parts) {
-        const float w = weight(m0);
-        if (tid < kMergeWts) wts[tid] = w;
-        Ls = w * l0;
-    }
-    for (int i = tid + NT; i < parts; i += NT) {
-        const float w = weight(pml[(int64_t)i * 2 * G]);
-        if (i < kMergeWts) wts[i] = w;
-        Ls += w * pml[(int64_t)i * 2 * G + 1];
-    }
-    Ls = wave_sum(Ls);
-    if (lane == 0) wred[1][wid] = Ls;
-    __syncthreads();
-    Ls = 0.0f;
+    for (int k = 0; k < 2; ++k) mx = lane + 64 * k < parts ? fmaxf(mx, ml[k].x) : mx;
+    for (int i = lane + 128; i < parts; i += 64) mx = fmaxf(mx, m_of(i));
+    const float M = wave_max(mx);
+    auto weight = [&](float m) { return m == -INFINITY ? 0.0f : exp2f(m - M); };
+    float wk[2];                                   // weights of parts lane, lane + 64 (0 past the parts)
+    float ls = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) Ls += wred[1][i];
-    auto wt = [&](int i) { return i < kMergeWts ? wts[i] : weight(pml[(int64_t)i * 2 * G]); };
+    for (int k = 0; k < 2; ++k) {
+        const bool in = lane + 64 * k < parts;
+        wk[k] = in ? weight(ml[k].x) : 0.0f;
+        ls += wk[k] * (in ? ml[k].y : 0.0f);
+    }
+    for (int i = lane + 128; i < parts; i += 64) ls += weight(m_of(i)) * pml[(int64_t)i * 2 * G + 1];
+    const float Ls = wave_sum(ls);
+    // straight-line over the round: a part past the count has weight 0 and
+    // its row, not written by this call, is replaced by 0
     float acc = 0.0f;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-        if (r + u * R < parts) acc += wt(r + u * R) * x[u];
-    for (int i0 = r + U * R; i0 < parts; i0 += U * R) {   // more parts than one batch
-#pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = po[(int64_t)min(i0 + u * R, parts - 1) * G * HD];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (i0 + u * R < parts) acc += wt(i0 + u * R) * x[u];
+    for (int u = 0; u < U; ++u) {
+        const int p = r + R * u;                   // wave-uniform
+        const int w0 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk[0]), p & 63);
+        const int w1 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk[1]), p & 63);
+        const float wp = __builtin_bit_cast(float, p < 64 ? w0 : w1);
+        acc += wp * (p < parts ? x[u] : 0.0f);
     }
-    if constexpr (R > 1) {
-        red[r][d] = acc;
-        __syncthreads();
-        if (r == 0) {
-            acc = red[0][d];
+    for (int i0 = PR; i0 < parts; i0 += PR) {     // more parts than one round
+        float mu[U];
 #pragma unroll
-            for (int k = 1; k < R; ++k) acc += red[k][d];
+        for (int u = 0; u < U; ++u) {
+            const int p = min(i0 + r + R * u, parts - 1);
+            x[u] = po[(int64_t)p * G * HD];
+            mu[u] = m_of(p);
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += (i0 + r + R * u < parts ? weight(mu[u]) : 0.0f) * x[u];
     }
-    if (r == 0) og[d] = Ls > 0.0f ? acc * (1.0f / Ls) : 0.0f;
+    red[r][d] = acc;
+    __syncthreads();
+    if (r == 0) {
+        float o = red[0][d];
+#pragma unroll
+        for (int k = 1; k < R; ++k) o += red[k][d];
+        og[d] = Ls > 0.0f ? o * (1.0f / Ls) : 0.0f;
+    }
 }
 
 template <int G, int HD>
@@ -1509,7 +1507,7 @@ static void launch_merge_t(const Geo &g, const qwfn_kv_view &v, const int32_t *s
                            int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel,
                            float *out, const Ws &ws, int32_t tg, hipStream_t st) {
     QWFN_LAUNCH(kTimedMerge, (k_merge<G, HD>), dim3((unsigned)G, (unsigned)g.Hkv, (unsigned)n_seq),
-                dim3(kMergeThreads), st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)(sel == nullptr), out,
+                dim3(merge_r<HD>() * HD), st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)(sel == nullptr), out,
                 ws, tg);
 }
 
@@ -1520,7 +1518,7 @@ hipError_t launch_merge(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_
 #define X(HD_, G_)                                                                                            \
     if (g.hd == HD_ && g.G == G_) {                                                                           \
         QWFN_LAUNCH(kTimedMerge, (k_merge<G_, HD_>), dim3((unsigned)G_, (unsigned)g.Hkv, (unsigned)n_seq),    \
-                    dim3(kMergeThreads), st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)dense, out, ws,  \
+                    dim3(merge_r<HD_>() * HD_), st, g, v, seq_len, max_seq_len, nsel, max_sel, (int32_t)dense, out, ws, \
                     tg);                                                                                      \
         return hipGetLastError();                                                                             \
     }
