@@ -65,7 +65,7 @@
 extern "C" {
 #endif
 
-#define QWFN_QSA_ABI_VERSION 4
+#define QWFN_QSA_ABI_VERSION 5
 
 /* return codes */
 #define QWFN_OK        0
@@ -302,6 +302,26 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             int32_t n_seq, int32_t max_seq_len, float *out,
                             int32_t *sel_out, int32_t *n_sel_out,
                             void *ws, size_t ws_bytes, void *stream);
+/* n_pos (1 .. 8) chained decode positions of every sequence in one call: the
+ * multi-position decode of the MTP verify step, where the engine builds T
+ * sparse_attn_decode calls into one graph and each reads through the writes
+ * of the ones before (src/qwfn_engine.cpp:1892-1906, the qsa_chain of
+ * src/qwfn_graph.h:104-109).  Position k of sequence s appends k_new[k][s] at
+ * seq_len[s] - 1 + k and attends with length seq_len[s] + k, exactly as the
+ * k-th of n_pos qwfn_sparse_attn_decode calls would: q [n_pos][n_seq][n_head]
+ * [head_dim], k_new / v_new [n_pos][n_seq][n_head_kv][head_dim], out
+ * [n_pos][n_seq][n_head][head_dim], sel_out [n_pos][n_seq][n_head_kv]
+ * [qwfn_qsa_max_selected] and n_sel_out [n_pos][n_seq][n_head_kv] (optional).
+ * max_seq_len bounds seq_len + n_pos - 1.  One small launch derives the
+ * positions' lengths into the workspace, then each position makes
+ * qwfn_sparse_attn_decode's launches; all on `stream`, so the chain captures
+ * into one hipGraph.  n_pos = 1 is qwfn_sparse_attn_decode.                   */
+int qwfn_sparse_attn_decode_chain(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                                  const float *q, const void *k_new, const void *v_new,
+                                  int32_t src_dtype, const int32_t *seq_len, int32_t n_seq,
+                                  int32_t n_pos, int32_t max_seq_len, float *out,
+                                  int32_t *sel_out, int32_t *n_sel_out,
+                                  void *ws, size_t ws_bytes, void *stream);
 
 /* qwfn_sparse_attn_decode without a workspace argument, for callers that
  * cannot allocate device memory (code under hipGraph capture that may not

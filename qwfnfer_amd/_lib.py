@@ -52,6 +52,7 @@ EXPORTS = (
     "qwfn_sparse_decode_attn",
     "qwfn_decode_append_select",
     "qwfn_sparse_attn_decode",
+    "qwfn_sparse_attn_decode_chain",
     "qwfn_sparse_attn_decode_noalloc",
     "qwfn_qsa_prefill_workspace_bytes",
     "qwfn_sparse_attn_prefill",
@@ -154,6 +155,7 @@ _SIGS = {
     "qwfn_sparse_decode_attn": (C.c_int, [_S, _V, _P, _P, _I, _I, _P, _P, _I, _P, _P, _Z, _P]),
     "qwfn_decode_append_select": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _P, _Z, _P]),
     "qwfn_sparse_attn_decode": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _Z, _P]),
+    "qwfn_sparse_attn_decode_chain": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _Z, _P]),
     "qwfn_sparse_attn_decode_noalloc": (C.c_int, [_S, _V, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P]),
     "qwfn_qsa_prefill_workspace_bytes": (C.c_int, [_S, _I, _I, C.POINTER(_Z)]),
     "qwfn_sparse_attn_prefill": (C.c_int, [_S, _V, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _Z, _P]),

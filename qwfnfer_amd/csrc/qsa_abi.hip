@@ -187,6 +187,7 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.cand = take(pairs * l.cut_wg * kCutKeys * sizeof(uint2));
     l.ccnt = take(l.cut_wg ? pairs * kCutWgMax * sizeof(int32_t) : 0);
     l.cmm = take(partials ? pairs * (l.nb_cap / kScoreRecBlocks) * sizeof(float2) : 0);
+    l.lens = take((size_t)kMaxChain * n_seq * sizeof(int32_t));
     l.total = off;
     return l;
 }
@@ -203,6 +204,7 @@ Ws ws_bind(void *base, const WsLayout &l) {
     w.cand = (uint2 *)(b + l.cand);
     w.ccnt = (int32_t *)(b + l.ccnt);
     w.cmm = (float2 *)(b + l.cmm);
+    w.lens = (int32_t *)(b + l.lens);
     w.cut_wg = l.cut_wg;
     w.nb_cap = l.nb_cap;
     w.max_sel = l.max_sel;
@@ -469,11 +471,21 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, float *out,
                             int32_t *sel_out, int32_t *n_sel_out, void *ws, size_t ws_bytes,
                             void *stream) {
+    return qwfn_sparse_attn_decode_chain(shape, view, q, k_new, v_new, src_dtype, seq_len, n_seq, 1, max_seq_len,
+                                         out, sel_out, n_sel_out, ws, ws_bytes, stream);
+}
+
+int qwfn_sparse_attn_decode_chain(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                                  const void *k_new, const void *v_new, int32_t src_dtype,
+                                  const int32_t *seq_len, int32_t n_seq, int32_t n_pos, int32_t max_seq_len,
+                                  float *out, int32_t *sel_out, int32_t *n_sel_out, void *ws, size_t ws_bytes,
+                                  void *stream) {
     TimerDisarm disarm;
     Geo g;
     int rc = make_geo(shape, view, &g);
     if (rc) return rc;
     if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (n_pos < 1 || n_pos > kMaxChain) return fail(QWFN_EINVAL, "decode: n_pos %d outside [1, %d]", n_pos, kMaxChain);
     if (src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16)
         return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
     const size_t al = src_dtype == QWFN_SRC_F32 ? 16 : 8;
@@ -485,17 +497,29 @@ int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *vie
     const int32_t msel = max_selected(shape, max_seq_len);
     Ws w;
     if ((rc = bind_ws(g, n_seq, max_seq_len, msel, ws, ws_bytes, &w))) return rc;
-    int32_t *sel = sel_out ? sel_out : w.sel;
-    int32_t *nsel = n_sel_out ? n_sel_out : w.nsel;
-    const FusedAppend fa{k_new, v_new, src_dtype == QWFN_SRC_F16, 1};
     hipStream_t st = (hipStream_t)stream;
+    // position k's lengths: seq_len + k (the first position reads seq_len itself)
+    hipError_t e = n_pos > 1 ? launch_chain_lens(seq_len, n_seq, n_pos, w.lens, st) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "decode: chain lengths");
     // one or a few sequences: the attention workgroups select for themselves
     const bool own = attn_select_fits(g, n_seq, max_seq_len, msel);
-    hipError_t e = launch_indexer(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, w, fa, st, !own);
-    if (e != hipSuccess) return hip_fail(e, "decode: indexer");
-    e = own ? launch_attention_select(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st)
-            : launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, nsel, msel, out, w, st);
-    return e == hipSuccess ? ok() : hip_fail(e, "decode: attention");
+    const size_t row_b = (size_t)g.hd * (src_dtype == QWFN_SRC_F32 ? 4 : 2);
+    for (int32_t k = 0; k < n_pos; ++k) {
+        const int32_t *len_k = k == 0 ? seq_len : w.lens + (size_t)k * n_seq;
+        const float *q_k = q + (size_t)k * n_seq * g.H * g.hd;
+        const size_t kv_off = (size_t)k * n_seq * g.Hkv * row_b;
+        const FusedAppend fa{(const uint8_t *)k_new + kv_off, (const uint8_t *)v_new + kv_off,
+                             src_dtype == QWFN_SRC_F16, 1};
+        float *out_k = out + (size_t)k * n_seq * g.H * g.hd;
+        int32_t *sel = sel_out ? sel_out + (size_t)k * n_seq * g.Hkv * msel : w.sel;
+        int32_t *nsel = n_sel_out ? n_sel_out + (size_t)k * n_seq * g.Hkv : w.nsel;
+        e = launch_indexer(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, w, fa, st, !own);
+        if (e != hipSuccess) return hip_fail(e, "decode: indexer");
+        e = own ? launch_attention_select(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, out_k, w, st)
+                : launch_attention(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, out_k, w, st);
+        if (e != hipSuccess) return hip_fail(e, "decode: attention");
+    }
+    return ok();
 }
 
 }  // extern "C"

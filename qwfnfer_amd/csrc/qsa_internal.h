@@ -47,6 +47,7 @@ constexpr int32_t kPrefillBatchMax = 32768;   // queries per prefill batch (one 
 constexpr int32_t kIdxRegKeys = 8192;
 constexpr int32_t kCutKeys = 4096;
 constexpr int32_t kCutWgMax = 64;
+constexpr int32_t kMaxChain = 8;          // positions of one chained decode call (qwfn_sparse_attn_decode_chain)
 constexpr int32_t kScoreRecBlocks = 16;   // blocks per (min, max) score record of the fused call's scoring
 struct Ws {
     int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
@@ -59,12 +60,13 @@ struct Ws {
     int32_t *ccnt;       // [n_seq][Hkv][kCutWgMax] their counts
     float2  *cmm;        // [n_seq][Hkv][nb_cap / kScoreRecBlocks] (min, max) eligible score of each record's blocks
                          // (the attention's own selection reads them; (+inf, -inf) when empty)
+    int32_t *lens;       // [kMaxChain][n_seq] lengths of a chained call's positions
     int32_t  nb_cap, max_sel, n_tiles;
     int32_t  cut_wg;     // workgroups of the multi-workgroup selection (0: one workgroup)
 };
 
 struct WsLayout {
-    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, total;
+    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, lens, total;
     int32_t nb_cap, max_sel, n_tiles, cut_wg;
 };
 // partials = false: no attention partials (the prefill kernel keeps its state on chip);
@@ -121,6 +123,8 @@ inline int32_t kv_row_bytes(int32_t kt, int32_t hd) {
 }
 
 hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st);
+// lens[k][s] = seq_len[s] + k for k < n_pos (one small launch)
+hipError_t launch_chain_lens(const int32_t *seq_len, int32_t n_seq, int32_t n_pos, int32_t *lens, hipStream_t st);
 
 // The checkpoint's own indexer keys (qwfn_idx_shape): raw fp16 keys of `dim`
 // values per token, pooled per block with RMSNorm * k_norm, then the first nd

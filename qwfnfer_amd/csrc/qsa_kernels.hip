@@ -34,6 +34,16 @@ hipError_t launch_fill_zero(void *p, size_t bytes, hipStream_t st) {
     return hipGetLastError();
 }
 
+__global__ void k_chain_lens(const int32_t *__restrict__ seq_len, int32_t n_seq, int32_t n_pos,
+                             int32_t *__restrict__ lens) {
+    for (int i = (int)threadIdx.x; i < n_seq * n_pos; i += (int)blockDim.x) lens[i] = seq_len[i % n_seq] + i / n_seq;
+}
+
+hipError_t launch_chain_lens(const int32_t *seq_len, int32_t n_seq, int32_t n_pos, int32_t *lens, hipStream_t st) {
+    hipLaunchKernelGGL(k_chain_lens, dim3(1), dim3(256), 0, st, seq_len, n_seq, n_pos, lens);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // append: quantize rows to q8_0 and overwrite them in the paged cache
 // (the quantizers are in qsa_append.h)

@@ -413,6 +413,44 @@ def sparse_attn_decode(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_n
     return out
 
 
+def sparse_attn_decode_chain(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                             seq_len: torch.Tensor, max_seq_len: int, ws: Workspace,
+                             out: Optional[torch.Tensor] = None, sel: Optional[torch.Tensor] = None,
+                             n_sel: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """n_pos chained decode positions of every sequence in one call, the
+    multi-position decode of the MTP verify step (src/qwfn_engine.cpp:1892-1906):
+    q [n_pos][n_seq][n_head][head_dim], k_new / v_new [n_pos][n_seq][n_head_kv]
+    [head_dim]; position k appends at seq_len - 1 + k and attends with length
+    seq_len + k, reading through the writes of the positions before it.
+    ``sel`` [n_pos][n_seq][n_head_kv][max_selected] / ``n_sel`` [n_pos][n_seq]
+    [n_head_kv] (optional, both or neither) receive each position's selection."""
+    cfg = cache.cfg
+    n_seq = seq_len.numel()
+    if q.dim() != 4 or q.shape[1] != n_seq:
+        raise ValueError("q must be [n_pos][n_seq][n_head][head_dim]")
+    n_pos = q.shape[0]
+    _need(q, "q", torch.float32, n_pos * n_seq * cfg.n_head * cfg.head_dim)
+    if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype:
+        raise TypeError("k_new and v_new must both be float32 or both float16")
+    _need(k_new, "k_new", k_new.dtype, n_pos * n_seq * cfg.kv_dim)
+    _need(v_new, "v_new", k_new.dtype, n_pos * n_seq * cfg.kv_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    if out is None:
+        out = torch.empty((n_pos, n_seq, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, n_pos * n_seq * cfg.n_head * cfg.head_dim)
+    if (sel is None) != (n_sel is None):
+        raise ValueError("pass both sel and n_sel or neither")
+    if sel is not None:
+        _need(sel, "sel", torch.int32, n_pos * n_seq * cfg.n_head_kv * cfg.max_selected(max_seq_len))
+        _need(n_sel, "n_sel", torch.int32, n_pos * n_seq * cfg.n_head_kv)
+    s = cfg.shape()
+    call("qwfn_sparse_attn_decode_chain", C.byref(s), C.byref(cache.view()), q.data_ptr(), k_new.data_ptr(),
+         v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,
+         seq_len.data_ptr(), n_seq, n_pos, max_seq_len, out.data_ptr(), _ptr(sel), _ptr(n_sel), ws.ptr(),
+         ws.nbytes, _stream(stream))
+    return out
+
+
 def sparse_attn_decode_noalloc(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                                seq_len: torch.Tensor, max_seq_len: int, out: torch.Tensor,
                                sel: Optional[torch.Tensor] = None, n_sel: Optional[torch.Tensor] = None,

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.qwfn_qsa_abi_version() == 4
+    assert lib.qwfn_qsa_abi_version() == 5
 
 
 def _code(name, *args):
@@ -127,6 +127,21 @@ def test_decode_rejects_exhausted_context_and_small_workspace():
     assert _code(f, *args(1024, 1 << 30, n_seq=2)) == _lib.QWFN_EINVAL
     msg = _lib.load().qwfn_qsa_last_error().decode()
     assert "n_seq" in msg
+
+
+def test_decode_chain_rejects_bad_position_counts():
+    """qwfn_sparse_attn_decode_chain takes 1 .. 8 positions; the checks run
+    before any launch (n_pos = 1 is qwfn_sparse_attn_decode's own path)."""
+    cfg = QsaConfig()
+    s = cfg.shape()
+    v = _view(pps=4)
+    f = "qwfn_sparse_attn_decode_chain"
+    args = lambda n_pos, max_len=1024: (C.byref(s), C.byref(v), 4096, 4096, 4096, 0, 4096, 1, n_pos, max_len,
+                                        4096, None, None, 256 * 64, 1 << 30, None)
+    for n_pos in (0, -1, 9):
+        assert _code(f, *args(n_pos)) == _lib.QWFN_EINVAL, n_pos
+        assert "n_pos" in _lib.load().qwfn_qsa_last_error().decode()
+    assert _code(f, *args(2, 1025)) == _lib.QWFN_ERANGE      # past the view's 1024 tokens
 
 
 def test_indexer_rejects_short_selection_buffer():
