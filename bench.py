@@ -557,6 +557,25 @@ class CheckpointRunner:
                     selected_kv_bytes=cells * row * 2 * self.cfg.n_head_kv)
 
 
+def round_f16_delta(qsa, torch, r):
+    """Largest |o(kv_round_f16) - o(exact dequant)| over one decode call of
+    every layer of replica 0: the same cache, queries and new rows (the
+    append rewrites the same row), attended once in each mode.  The size of
+    the reference's F16 cast of its gathered K/V (src/qwfn_graph.cpp:530-537)
+    next to exact fp32 attention."""
+    import dataclasses
+    worst = 0.0
+    for il, c in enumerate(r.stacks[0]):
+        outs = []
+        for rf in (1, 0):
+            cc = dataclasses.replace(c, cfg=dataclasses.replace(c.cfg, kv_round_f16=rf))
+            outs.append(qsa.sparse_attn_decode(cc, r.q[0][il], r.kn[0][il], r.vn[0][il], r.seq_lens[0], r.max_len,
+                                               r.ws))
+        torch.cuda.synchronize()
+        worst = max(worst, float((outs[0] - outs[1]).abs().max()))
+    return worst
+
+
 def bench_interop(qsa, torch, cfg, gen, ctx, reps=20):
     """The reference-format boundary on one layer of ctx tokens: K and V rows
     in ggml's block_q8_0 row format (the reference's cache tensors) imported
@@ -758,8 +777,8 @@ def main():
         import dataclasses
         kv_types = {}
         ctx = max(contexts)
-        for kt, name in ((1, "q4_0"), (2, "f16")):
-            c2 = dataclasses.replace(cfg, kv_type=kt)
+        for kt, rf, name in ((1, 0, "q4_0"), (2, 0, "f16"), (0, 1, "q8_0_round_f16")):
+            c2 = dataclasses.replace(cfg, kv_type=kt, kv_round_f16=rf)
             pps = (ctx + DECODE_ROOM + c2.page_tokens - 1) // c2.page_tokens
             pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
             r = Runner(qsa, torch, c2, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
@@ -772,9 +791,12 @@ def main():
                                   kernel_us={k: round(v, 3) for k, v in kern.items()},
                                   cells_per_layer=cells, selected_kv_bytes=kv,
                                   attn_gbs=round(kv / (kern["attention"] * 1e-6) / 1e9, 1), replicas=r.n_inst)
+            if rf:
+                kv_types[name]["max_abs_delta_vs_exact"] = round_f16_delta(qsa, torch, r)
             log(f"[bench] kv {name} ctx {ctx}: {ms * 1e3 / args.layers:.2f} us/layer, indexer "
                 f"{kern['indexer']:.2f} us, attention {kern['attention']:.2f} us, merge {kern['merge']:.2f} us "
-                f"(general attention kernel)")
+                f"(general attention kernel)" + (f", max |delta| vs exact {kv_types[name]['max_abs_delta_vs_exact']:.3g}"
+                                                 if rf else ""))
             del r
             torch.cuda.empty_cache()
 

@@ -129,6 +129,15 @@ typedef struct qwfn_qsa_shape {
                               * 430); 0: top_k_blocks scored blocks on top of
                               * the forced ones                              */
     int32_t kv_type;         /* QWFN_KV_Q8_0 / QWFN_KV_Q4_0 / QWFN_KV_F16       */
+    int32_t kv_round_f16;    /* 1: the decode attention rounds every dequantized
+                              * K and V value to fp16 (round to nearest even)
+                              * before its arithmetic, as the reference's
+                              * gather casts K/V to F16 ahead of
+                              * flash_attn_ext (src/qwfn_graph.cpp:530-537);
+                              * 0: the exact dequantized values.  Prefill
+                              * ignores it (the reference's prefill reads the
+                              * cache rows directly, src/qwfn_graph.cpp:
+                              * 365-403)                                     */
 } qwfn_qsa_shape;
 
 typedef struct qwfn_kv_view {

@@ -26,7 +26,7 @@ class Shape(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_head", "n_head_kv", "head_dim", "block_tokens", "page_tokens", "top_k_blocks",
         "sink_blocks", "local_tokens", "relu_per_head", "shared_selection", "quant_variant",
-        "topk_counts_forced", "kv_type")]
+        "topk_counts_forced", "kv_type", "kv_round_f16")]
 
 
 class IdxShape(C.Structure):
@@ -101,7 +101,7 @@ def shape_of(cfg) -> Shape:
     return Shape(cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.block_tokens, cfg.page_tokens,
                  cfg.top_k_blocks, cfg.sink_blocks, cfg.local_tokens, cfg.relu_per_head,
                  cfg.shared_selection, cfg.quant_variant, getattr(cfg, "topk_counts_forced", 0),
-                 getattr(cfg, "kv_type", 0))
+                 getattr(cfg, "kv_type", 0), getattr(cfg, "kv_round_f16", 0))
 
 
 # ---- scalar / block helpers -------------------------------------------------

@@ -511,6 +511,24 @@ int qwfn_oracle_indexer_topk(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
  * selected cells with the cell mask cell <= n_past (src/qwfn_graph.cpp:
  * 497-502, 539-541), restated as the textbook softmax in fp64 on the exactly
  * dequantized K/V.  GQA: query head h reads KV head h / (n_head/n_head_kv). */
+static float f16_round(float x) { return qwfn_oracle_f16_to_f32(qwfn_oracle_f32_to_f16(x)); }
+
+/* x[0..n) rounded to fp16 and back (round to nearest even, as
+ * qwfn_oracle_f32_to_f16), eight at a time with F16C where the build has it. */
+static void round_f16_row(float *x, int32_t n) {
+    int32_t d = 0;
+#ifdef __F16C__
+    for (; d + 8 <= n; d += 8) {
+        const __m256 a = _mm256_loadu_ps(x + d);
+        _mm256_storeu_ps(x + d, _mm256_cvtph_ps(_mm256_cvtps_ph(a, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC)));
+    }
+#endif
+    for (; d < n; d++) x[d] = f16_round(x[d]);
+}
+
+/* With kv_round_f16 every dequantized K and V value is rounded to fp16 first:
+ * the reference's gather casts its rows to F16 before flash_attn_ext
+ * (src/qwfn_graph.cpp:530-537). */
 int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
                               const float *q, const int32_t *seq_len, int32_t n_seq,
                               const int32_t *sel, const int32_t *n_sel,
@@ -538,6 +556,7 @@ int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
             const double scale = 1.0 / sqrt((double)hd);
             for (int64_t c = 0; c < nc; c++) {
                 status |= qwfn_oracle_dequant_row(s, v, v->k_pages, seq, cells[c], g, krow);
+                if (s->kv_round_f16) round_f16_row(krow, hd);
                 for (int32_t h = 0; h < G; h++) {
                     const float *qh = q + ((int64_t)seq * s->n_head + (int64_t)g * G + h) * hd;
                     double acc = 0.0;
@@ -557,6 +576,7 @@ int qwfn_oracle_attention_f64(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
             }
             for (int64_t c = 0; c < nc; c++) {
                 status |= qwfn_oracle_dequant_row(s, v, v->v_pages, seq, cells[c], g, vrow);
+                if (s->kv_round_f16) round_f16_row(vrow, hd);
                 for (int32_t h = 0; h < G; h++)
                     for (int32_t d = 0; d < hd; d++) o[(int64_t)h * hd + d] += lg[c * G + h] * (double)vrow[d];
             }
@@ -590,6 +610,9 @@ int qwfn_oracle_prefill_f64_strided(const qwfn_qsa_shape *s, const qwfn_kv_view 
     if (attn_stride < 1) return QWFN_EINVAL;
     if (seq < 0 || seq >= v->n_seq || pos0 < 0 || n_q < 1) return QWFN_EINVAL;
     if ((int64_t)pos0 + n_q > (int64_t)v->pages_per_seq * s->page_tokens) return QWFN_ERANGE;
+    qwfn_qsa_shape s0 = *s;                        /* prefill reads the exact rows (kv_round_f16 is decode's) */
+    s0.kv_round_f16 = 0;
+    s = &s0;
     qwfn_kv_view sv = *v;                          /* the one sequence as a view */
     const int64_t bps = (int64_t)v->pages_per_seq * s->page_tokens / s->block_tokens;
     sv.pooled = v->pooled + (int64_t)seq * s->n_head_kv * bps * s->head_dim;
@@ -613,21 +636,6 @@ int qwfn_oracle_prefill_f64_strided(const qwfn_qsa_shape *s, const qwfn_kv_view 
 }
 
 /* ------------------------------------------------------------------------ */
-
-static float f16_round(float x) { return qwfn_oracle_f16_to_f32(qwfn_oracle_f32_to_f16(x)); }
-
-/* x[0..n) rounded to fp16 and back (round to nearest even, as
- * qwfn_oracle_f32_to_f16), eight at a time with F16C where the build has it. */
-static void round_f16_row(float *x, int32_t n) {
-    int32_t d = 0;
-#ifdef __F16C__
-    for (; d + 8 <= n; d += 8) {
-        const __m256 a = _mm256_loadu_ps(x + d);
-        _mm256_storeu_ps(x + d, _mm256_cvtph_ps(_mm256_cvtps_ph(a, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC)));
-    }
-#endif
-    for (; d < n; d++) x[d] = f16_round(x[d]);
-}
 
 /* Token t of KV head g of one pool as the reference's attention sees it:
  * dequantized (ggml_get_rows of q8_0: each 32-value block's fp16 scale times

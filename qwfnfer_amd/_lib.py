@@ -80,6 +80,7 @@ class QsaShape(C.Structure):
         ("quant_variant", C.c_int32),
         ("topk_counts_forced", C.c_int32),
         ("kv_type", C.c_int32),
+        ("kv_round_f16", C.c_int32),
     ]
 
 

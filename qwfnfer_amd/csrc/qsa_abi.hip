@@ -67,8 +67,8 @@ int check_shape(const qwfn_qsa_shape *s) {
         return fail(QWFN_EINVAL, "quant_variant %d unknown", s->quant_variant);
     if (s->kv_type != QWFN_KV_Q8_0 && s->kv_type != QWFN_KV_Q4_0 && s->kv_type != QWFN_KV_F16)
         return fail(QWFN_EINVAL, "kv_type %d unknown", s->kv_type);
-    if ((s->relu_per_head | s->shared_selection | s->topk_counts_forced) & ~1)
-        return fail(QWFN_EINVAL, "relu_per_head / shared_selection / topk_counts_forced are 0 or 1");
+    if ((s->relu_per_head | s->shared_selection | s->topk_counts_forced | s->kv_round_f16) & ~1)
+        return fail(QWFN_EINVAL, "relu_per_head / shared_selection / topk_counts_forced / kv_round_f16 are 0 or 1");
     if (s->topk_counts_forced && s->top_k_blocks > 0 &&
         s->top_k_blocks < s->sink_blocks + (s->local_tokens + s->block_tokens - 2) / s->block_tokens + 1)
         return fail(QWFN_EINVAL, "topk_counts_forced: top_k_blocks (%d) must hold the sink and window blocks",
@@ -106,6 +106,7 @@ int make_geo(const qwfn_qsa_shape *s, const qwfn_kv_view *v, Geo *g, bool view_r
     g->keep_total = s->topk_counts_forced;
     g->sel_rows = s->n_head_kv;
     g->kt = s->kv_type;
+    g->round_f16 = s->kv_round_f16;
     g->chunks = kv_row_bytes(s->kv_type, s->head_dim) / 16;
     g->qbytes = (int64_t)s->n_head_kv * s->page_tokens * kv_row_bytes(s->kv_type, s->head_dim);
     g->page_bytes = g->qbytes +
@@ -669,6 +670,7 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
     Geo gp = g;
     gp.pf = 1;
     gp.pf_seq = seq;
+    gp.round_f16 = 0;                              // prefill reads the exact rows (kv_round_f16 is decode's)
     for (int32_t i0 = 0; i0 < n_q; i0 += batch) {
         const int32_t nb = std::min(batch, n_q - i0);
         gp.pf_pos0 = pos0 + i0;

@@ -836,7 +836,8 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
 #define QWFN_FOR_EACH_DEC(X) X(128, 8) X(128, 4) X(128, 2) X(64, 8) X(256, 12) X(256, 8)
 
 bool dec_kernels_for(const Geo &g) {
-    if (!g.vdim || g.pf) return false;
+    // (fp16-rounded K/V: the general kernel, which dequantizes each value)
+    if (!g.vdim || g.pf || g.round_f16) return false;
 #define X(HD_, G_) if (g.hd == HD_ && g.G == G_) return true;
     QWFN_FOR_EACH_DEC(X)
 #undef X

@@ -21,6 +21,7 @@ struct Geo {
     int32_t shared;                  // one selection for all KV heads (scores summed in head order)
     int32_t keep_total;              // top_k counts the forced blocks (topk_counts_forced)
     int32_t kt;                      // K/V element type (QWFN_KV_*)
+    int32_t round_f16;               // decode attention rounds dequantized K/V to fp16 (kv_round_f16)
     int32_t chunks;                  // 16-byte chunks in a head row of K/V (head_dim/16 for q8_0)
     int32_t sel_rows;                // rows a shared selection is written to per sequence (Hkv;
                                      // the attention's n_head_kv for the checkpoint indexer)

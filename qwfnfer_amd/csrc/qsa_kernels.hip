@@ -1576,6 +1576,7 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
        float *__restrict__ out, Ws ws, int32_t n_parts) {
     using C = AttnCfg<HD, G, TG>;
     constexpr int CHK = row_bytes_t<HD, KT>() / 16;               // 16-byte chunks per head row
+    const bool VDIM = KT == QWFN_KV_Q8_0 && g.vdim;               // V quants dim-major per 64-token tile
     constexpr int PERK = (64 * CHK + C::NTG - 1) / C::NTG;      // K (and V) chunk loads per thread
     static_assert(sizeof(AttnShared<HD, G, TG>) <= 160 * 1024, "LDS of the tile groups");
     __shared__ AttnShared<HD, G, TG> sh;
@@ -1665,6 +1666,15 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
                     const int64_t off = (int64_t)gr.page[cell] * g.page_bytes +
                                         ((int64_t)(gh * (g.pt / 64) + rw / 64) * CHK + ch) * 1024 + (rw % 64) * 16;
                     kq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.k_pages + off);
+                    if (!VDIM) vq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.v_pages + off);
+                }
+                // q8_0 in whole 64-token tiles: V quants dim-major, 64 bytes a
+                // dim; chunk k = dim k / 4, cells 16 (k % 4) .. +15 of the tile
+                // (one block, so one page and 64 aligned rows from cell 0's)
+                const int rw0 = gr.row[0];
+                if (VDIM && rw0 >= 0) {
+                    const int64_t off = (int64_t)gr.page[0] * g.page_bytes +
+                                        ((int64_t)(gh * (g.pt / 64) + rw0 / 64) * HD + k / 4) * 64 + (k % 4) * 16;
                     vq[i] = *reinterpret_cast<const uint4 *>((const uint8_t *)v.v_pages + off);
                 }
             }
@@ -1685,8 +1695,8 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
             }
         }
         __syncthreads();
-        // dequantize exactly (fp16 scale times the quant, or the fp16 value)
-        // into the group's LDS tile: K' cell-major, V' dim-major (transposed)
+        // dequantize exactly (fp16 scale times the quant, or the fp16 value;
+        // then rounded to fp16 with kv_round_f16) into the group's LDS tile: K' cell-major, V' dim-major (transposed)
         auto dequant = [&](const uint4 *qv, uint16_t (*scl)[HD / 32], bool vt) {
             float *base = gr.kv;
 #pragma unroll
@@ -1714,6 +1724,23 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
                                 x[4 * u + b] = scf * (float)((int)((w[u] >> (8 * b)) & 15) - 8);
                                 x[16 + 4 * u + b] = scf * (float)((int)((w[u] >> (8 * b + 4)) & 15) - 8);
                             }
+                    } else if (VDIM && vt) {              // chunk = cells 16 (k % 4) .. +15 of dim k / 4
+                        const int dim = k / 4, c0 = 16 * (k % 4);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) {
+                                const int c = c0 + 4 * u + b;
+                                const float xv = h2f(scl[c][dim / 32]) * (float)(int8_t)((w[u] >> (8 * b)) & 0xFF);
+                                x[4 * u + b] = gr.row[c] >= 0 ? xv : 0.0f;
+                            }
+                        if (g.round_f16) {
+#pragma unroll
+                            for (int e = 0; e < 16; ++e) x[e] = (float)(_Float16)x[e];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) base[dim * C::VROWF + c0 + e] = x[e];
+                        continue;
                     } else {                              // chunk = 16 dims of int8
                         d0 = 16 * ch;
                         const float scf = h2f(scl[cell][ch / 2]);
@@ -1723,6 +1750,10 @@ k_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_le
                             for (int b = 0; b < 4; ++b) x[4 * u + b] = scf * (float)(int8_t)((w[u] >> (8 * b)) & 0xFF);
                     }
                     constexpr int NX = sizeof(x) / sizeof(float);
+                    if (g.round_f16) {                    // kv_round_f16: the reference's F16 cast (RNE)
+#pragma unroll
+                        for (int e = 0; e < NX; ++e) x[e] = (float)(_Float16)x[e];
+                    }
                     if (vt) {                             // lanes hold consecutive cells: coalesced rows
 #pragma unroll
                         for (int e = 0; e < NX; ++e) base[(d0 + e) * C::VROWF + cell] = x[e];

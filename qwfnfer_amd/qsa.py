@@ -51,6 +51,7 @@ class QsaConfig:
     quant_variant: int = _lib.Q8_X86_RNE
     topk_counts_forced: int = 0
     kv_type: int = _lib.KV_Q8_0
+    kv_round_f16: int = 0          # 1: decode attention on fp16-rounded K/V (the reference's F16 cast)
 
     @property
     def group(self) -> int:
@@ -64,7 +65,7 @@ class QsaConfig:
         return QsaShape(self.n_head, self.n_head_kv, self.head_dim, self.block_tokens,
                         self.page_tokens, self.top_k_blocks, self.sink_blocks,
                         self.local_tokens, self.relu_per_head, self.shared_selection,
-                        self.quant_variant, self.topk_counts_forced, self.kv_type)
+                        self.quant_variant, self.topk_counts_forced, self.kv_type, self.kv_round_f16)
 
     def check(self) -> None:
         s = self.shape()
@@ -137,9 +138,12 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, numel: Optional[int] =
 class KvCache:
     """One attention layer's paged q8_0 K/V pools and pooled block keys.
 
-    ``page_table[s, p]`` is the physical page of logical page p of sequence s;
-    the reference's contiguous token-major cache is one sequence with the
-    identity table (src/qwfn_state.cpp:52-54)."""
+    ``page_table[s, p]`` is the physical page of logical page p of sequence s.
+    Pages hold K quants in 16-byte chunks of 64-token tiles, V quants dim-major
+    per tile (q8_0 in whole 64-token blocks) and the fp16 scales in a region
+    of their own, so the reference's token-major block_q8_0 rows
+    (src/qwfn_state.cpp:52-54) enter and leave through export_rows_q8_0 /
+    import_rows_q8_0."""
     cfg: QsaConfig
     k_pages: torch.Tensor
     v_pages: torch.Tensor

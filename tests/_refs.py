@@ -29,6 +29,7 @@ class Cfg:
     quant_variant: int = 0
     topk_counts_forced: int = 0
     kv_type: int = 0
+    kv_round_f16: int = 0
 
     @property
     def group(self):

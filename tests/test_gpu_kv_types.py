@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from _gpu import cfg_of, fill, kv_rows, make_pair, np_of
+from _gpu import cfg_of, decode_steps, fill, kv_rows, make_pair, np_of
 from _refs import BASELINE, TINY, Cfg
 from oracle import oracle as O
 from qwfnfer_amd import qsa, snapshot
@@ -147,3 +147,35 @@ def test_snapshot_round_trip(kt, tmp_path):
     assert snapshot.load_snapshot(dev2, path, 1) == 700
     torch.cuda.synchronize()
     np.testing.assert_array_equal(np_of(dev2.pooled)[1, :, :700 // 64], np_of(dev.pooled)[0, :, :700 // 64])
+
+
+# kv_round_f16: the decode attention on every dequantized K and V value rounded
+# to fp16, as the reference's gather casts its rows to F16 before
+# flash_attn_ext (src/qwfn_graph.cpp:530-537); against the oracle run on the
+# same rounded values
+ROUND_TYPES = [0, 1, 2]                     # q8_0, q4_0, fp16 (a no-op for fp16 rows)
+
+
+@pytest.mark.parametrize("kt", ROUND_TYPES)
+def test_decode_steps_kv_round_f16(kt):
+    cfg = Cfg(**{**with_type(BASELINE, kt).__dict__, "kv_round_f16": 1})
+    decode_steps(cfg, [65536 - 2, 3000], steps=3, seed=1000 + kt, modes=["fused", "two_call", "fused"],
+                 reattend=True)
+    decode_steps(Cfg(**{**TINY.__dict__, "kv_type": kt, "kv_round_f16": 1}), [2000, 61], steps=2,
+                 seed=1003 + kt, dtype=np.float16)
+
+
+def test_kv_round_f16_changes_q8_0_outputs():
+    """The two modes on the same cache and queries, each checked against its
+    own fp64 oracle inside decode_steps: q8_0 values d * q are not all fp16
+    numbers, so the outputs differ.  With the configuration's per-block scales
+    up to 10 the difference reaches about 1e-2, more than the 2e-3 + 1e-3 |ref|
+    bound between either mode and its own reference: the reference's F16 cast
+    moves its outputs that far from exact fp32 attention."""
+    outs = []
+    for r in (0, 1):
+        cfg = Cfg(**{**BASELINE.__dict__, "kv_round_f16": r})
+        outs.append(decode_steps(cfg, [20000], steps=1, seed=1010)[0])
+    d = np.abs(outs[0] - outs[1])
+    print(f"max |o(kv_round_f16) - o(exact)| = {d.max():.3g}", flush=True)
+    assert d.max() > 0

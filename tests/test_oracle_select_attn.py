@@ -117,6 +117,37 @@ def test_attention_f64_matches_textbook(oracle):
         np.testing.assert_allclose(out[0, h], attention_ref(q[0, h], K, V), rtol=1e-12, atol=1e-13)
 
 
+def test_attention_f64_kv_round_f16(oracle):
+    """kv_round_f16: the oracle's attention runs on every dequantized K and V
+    value rounded to fp16 (numpy's float16 conversion, round to nearest even,
+    as the reference's F16 cast of its gathered rows); the prefill oracle
+    ignores the flag."""
+    base = Cfg(**{**TINY.__dict__, "kv_round_f16": 0})
+    cfg = Cfg(**{**TINY.__dict__, "kv_round_f16": 1})
+    rng = np.random.default_rng(29)
+    n = 100
+    k = (rng.standard_normal((n, 2, cfg.head_dim)) * 3.7).astype(np.float32)
+    v = (rng.standard_normal((n, 2, cfg.head_dim)) * 3.7).astype(np.float32)
+    caches = []
+    for c_ in (base, cfg):
+        c = oracle.HostCache(c_, 1, 2)
+        c.append(k, v, np.arange(n, dtype=np.int32))
+        caches.append(c)
+    q = rng.standard_normal((1, cfg.n_head, cfg.head_dim)).astype(np.float32)
+    L = 99
+    exact = caches[0].attention_f64(q, [L])
+    out = caches[1].attention_f64(q, [L])
+    c = caches[1]
+    for h in range(cfg.n_head):
+        g = h // cfg.group
+        K = np.stack([c.dequant_row("k", 0, t, g) for t in range(L)]).astype(np.float16).astype(np.float32)
+        V = np.stack([c.dequant_row("v", 0, t, g) for t in range(L)]).astype(np.float16).astype(np.float32)
+        np.testing.assert_allclose(out[0, h], attention_ref(q[0, h], K, V), rtol=1e-12, atol=1e-13)
+    assert np.abs(out - exact).max() > 0                 # the rounding is visible at these values
+    pf = [c_.prefill_f64(q, 0, L - 1)[-1] for c_ in caches]
+    np.testing.assert_array_equal(pf[0], pf[1])
+
+
 def test_attention_closed_forms(oracle):
     cfg = TINY
     c = oracle.HostCache(cfg, 1, 1)
