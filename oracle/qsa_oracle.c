@@ -801,9 +801,11 @@ int qwfn_oracle_decode_step_f32(const qwfn_qsa_shape *s, const qwfn_kv_view *v,
  * dims l + 64k, then a butterfly over lane distances 32..1 --, mean =
  * fp32(sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm (:423);
  * then the rotation of the block's first position b*bt (IMROPE with every
- * section at that position, :425-427; src/qwfn_engine.cpp:741, 781, 926,
- * 934): pairs (i, i + nd/2), angle pos * base^(-2i/nd) in fp64, cos / sin
- * rounded to fp32; finally fp16 round to nearest even (the F16 pool cache,
+ * section at that position, :425-427; src/qwfn_engine.cpp:741-743, 926,
+ * 934): pairs (i, i + nd/2), the angle of ggml's rope (ggml, not in the tree:
+ * theta_scale = powf(base, -2/nd), theta_0 = pos, theta_{i+1} = theta_i *
+ * theta_scale in fp32), cos / sin of that fp32 angle in fp64 rounded to
+ * fp32; finally fp16 round to nearest even (the F16 pool cache,
  * src/qwfn_engine.cpp:389-394), returned as fp32. */
 int qwfn_oracle_idx_pool_block(const qwfn_qsa_shape *s, const qwfn_idx_shape *is,
                                const uint16_t *members, const float *k_norm, int32_t b,
@@ -834,12 +836,15 @@ int qwfn_oracle_idx_pool_block(const qwfn_qsa_shape *s, const qwfn_idx_shape *is
     const float scale = 1.0f / sqrtf(mean + is->rms_eps);
     for (int32_t d = 0; d < D; d++) y[d] = (x[d] * scale) * k_norm[d];
     const int32_t half = nd / 2, t0 = b * bt;
+    const float theta_scale = powf(is->rope_freq_base, -2.0f / (float)nd);
+    float theta[128];
+    theta[0] = (float)t0;
+    for (int32_t i = 1; i < half; i++) theta[i] = theta[i - 1] * theta_scale;
     for (int32_t d = 0; d < D; d++) {
         float o = y[d];
         if (d < nd) {
             const int32_t i = d < half ? d : d - half;
-            const double invf = pow((double)is->rope_freq_base, -2.0 * i / (double)nd);
-            const double th = (double)t0 * invf;
+            const double th = (double)theta[i];
             const float c = (float)cos(th), sn = (float)sin(th);
             const float x0 = y[i], x1 = y[i + half];
             o = d < half ? x0 * c - x1 * sn : x0 * sn + x1 * c;

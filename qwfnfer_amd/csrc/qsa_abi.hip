@@ -716,8 +716,8 @@ int make_idx_geo(const qwfn_qsa_shape *s, const qwfn_idx_shape *is, IdxGeo *ig) 
     ig->dim = is->idx_dim;
     ig->nd = is->rope_dim;
     ig->eps = is->rms_eps;
-    for (int i = 0; i < kIdxMaxPairs; ++i)
-        ig->invf[i] = i < is->rope_dim / 2 ? std::pow((double)is->rope_freq_base, -2.0 * i / (double)is->rope_dim) : 0.0;
+    // ggml's theta_scale (fp32 powf, as ggml-cpu's rope computes it)
+    ig->theta_scale = powf(is->rope_freq_base, -2.0f / (float)is->rope_dim);
     return QWFN_OK;
 }
 

@@ -68,17 +68,16 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 //            butterfly over lane distance 32, 16, .., 1 --, mean = (float)
 //            (sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm[d]
 //            (ggml_rms_norm also sums in fp64; :423)
-//   rotary : pair (i, i + nd/2), angle pos * invf[i] in fp64, cos/sin rounded
-//            to fp32: (x0 c - x1 s, x0 s + x1 c); dims >= nd unchanged.  The
-//            reference's IMROPE (:425-427) is this rotation for text, where
-//            every position section gets the same position (src/qwfn_engine.cpp:
-//            741, 781, 926, 934).  The angle here is the exact fp64 product;
-//            ggml's rope builds theta in fp32 (a running product of the
-//            per-pair factor), which at block positions near 1.6e5 differs
-//            from it by up to about 1e-2 rad.  Parity with the reference's
-//            pooled keys is therefore unpinned at long positions: the oracle
-//            restates this fp64 rule, and the selections are pinned given the
-//            pooled keys.
+//   rotary : pair (i, i + nd/2) turned by (x0 c - x1 s, x0 s + x1 c), dims
+//            >= nd unchanged, with ggml's IMROPE angle (:425-427): theta_0 =
+//            (float)pos, theta_{i+1} = theta_i * theta_scale rounded to fp32,
+//            theta_scale = powf(base, -2/nd) -- the running product ggml's
+//            rope cache builds, one factor per pair --; cos / sin of that
+//            fp32 angle evaluated in fp64 and rounded to fp32.  IMROPE gives
+//            each pair the position of its section (t, h, w interleaved); the
+//            reference fills every section of a block's position with the
+//            block's first position b * bt (src/qwfn_engine.cpp:741-743, 926,
+//            934), so every pair takes pos = b * bt.
 //   store  : rounded to fp16 (the reference's F16 pool cache).
 template <int D>
 __device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, const uint16_t *m,
@@ -127,8 +126,11 @@ __device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, c
         float o = ys[d];
         if (d < ig.nd) {
             const int i = d < half ? d : d - half;
-            const double th = (double)t0 * ig.invf[i];
-            const float c = (float)cos(th), s = (float)sin(th);
+            // ggml's angle of pair i: the block position times theta_scale, i
+            // times over, each product rounded to fp32
+            float th = (float)t0;
+            for (int k = 0; k < i; ++k) th = __fmul_rn(th, ig.theta_scale);
+            const float c = (float)cos((double)th), s = (float)sin((double)th);
             const float x0 = ys[i], x1 = ys[i + half];
             o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
         }

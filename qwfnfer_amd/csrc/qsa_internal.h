@@ -129,13 +129,15 @@ hipError_t launch_chain_lens(const int32_t *seq_len, int32_t n_seq, int32_t n_po
 
 // The checkpoint's own indexer keys (qwfn_idx_shape): raw fp16 keys of `dim`
 // values per token, pooled per block with RMSNorm * k_norm, then the first nd
-// dims rotated in pairs (i, i + nd/2) by angle pos * invf[i] at the block's
-// first position.  invf[i] = base^(-2i/nd) in fp64, computed on the host.
+// dims rotated in pairs (i, i + nd/2) at the block's first position pos, by
+// ggml's rope angle: theta_0 = (float)pos, theta_{i+1} = theta_i * theta_scale
+// in fp32, theta_scale = powf(base, -2/nd) computed on the host; cos / sin of
+// the fp32 angle in fp64, rounded to fp32.
 constexpr int kIdxMaxPairs = 64;
 struct IdxGeo {
     int32_t dim, nd;
     float eps;
-    double invf[kIdxMaxPairs];
+    float theta_scale;
 };
 bool idx_kernels_for(int32_t dim);
 // Rows [n_rows][dim] (fp32, rounded to nearest even, or fp16) into the raw

@@ -4,9 +4,12 @@ against what the mathematics fixes, independently of its loop:
     RMSNorm(mean of the members) * k_norm, checked against numpy float64;
   - a block whose members are one basis vector e_i is rotated by the closed
     form: after RMSNorm it is sqrt(D) * w_i e_i, and the pair (i, i + nd/2)
-    turns by pos * base^(-2i/nd) (dims >= nd stay), so a wrong pairing
-    (adjacent instead of split halves), a sign, the exponent or the position
-    (b instead of b * block_tokens) fails;
+    turns by ggml's fp32 angle -- pos times theta_scale = base^(-2/nd) (the
+    float64 power rounded to float32), i times over, each product rounded to
+    float32 by numpy -- (dims >= nd stay), so a wrong pairing (adjacent
+    instead of split halves), a sign, the exponent, the position (b instead
+    of b * block_tokens) or the exact float64 angle in place of the fp32 one
+    fails;
   - the rotation keeps every pair's length and leaves dims >= nd alone;
   - the shared selection over the indexer scores is the definition's.
 Each comparison allows one fp16 ulp: the stored key is fp16-rounded."""
@@ -55,12 +58,44 @@ def test_basis_vector_rotates_by_the_closed_form(b, i):
         want[i] = amp
     else:
         pair = i % h
-        th = pos * base ** (-2.0 * pair / nd)
+        th = ggml_theta(pos, pair, base, nd)
         if i < h:        # (x0, x1) = (amp, 0)
             want[i], want[i + h] = amp * np.cos(th), amp * np.sin(th)
         else:            # (x0, x1) = (0, amp)
             want[i - h], want[i] = -amp * np.sin(th), amp * np.cos(th)
     f16_close(got, want)
+
+
+def ggml_theta(pos, pair, base, nd):
+    """ggml's rope angle of pair `pair`: float32(pos) times float32(base **
+    (-2 / nd)), `pair` times over, each product rounded to float32."""
+    scale = np.float32(base ** (-2.0 / nd))
+    th = np.float32(pos)
+    for _ in range(pair):
+        th = np.float32(th * scale)
+    return float(th)
+
+
+def test_fp32_angle_is_observable():
+    """At long positions the fp32 angle and the exact float64 one put the
+    stored key more than the comparison's tolerance apart, so the closed-form
+    test above tells them apart."""
+    D, nd, base, bt, b = 128, 64, 10000000.0, 4, 40959
+    icfg = ICfg(idx_dim=D, rope_dim=nd, rope_freq_base=base, rms_eps=0.0)
+    amp, pos = np.sqrt(D), b * bt
+    apart = 0
+    for i in range(1, nd // 2):
+        m = np.zeros((bt, D), np.float16)
+        m[:, i] = 1.0
+        got = O.idx_pool_block(CKPT, icfg, m, np.ones(D, np.float32), b)
+        th = pos * base ** (-2.0 * i / nd)
+        exact = np.zeros(D)
+        exact[i], exact[i + nd // 2] = amp * np.cos(th), amp * np.sin(th)
+        try:
+            f16_close(got, exact)
+        except AssertionError:
+            apart += 1
+    assert apart > 0
 
 
 def test_rotation_keeps_pair_lengths_and_tail_dims():
