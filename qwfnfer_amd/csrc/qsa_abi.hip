@@ -189,6 +189,7 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.ccnt = take(l.cut_wg ? pairs * kCutWgMax * sizeof(int32_t) : 0);
     l.cmm = take(partials ? pairs * (l.nb_cap / kScoreRecBlocks) * sizeof(float2) : 0);
     l.lens = take((size_t)kMaxChain * n_seq * sizeof(int32_t));
+    l.vmax = take(partials ? 0 : (size_t)g.Hkv * kVmaxWg * sizeof(float));
     l.total = off;
     return l;
 }
@@ -206,6 +207,7 @@ Ws ws_bind(void *base, const WsLayout &l) {
     w.ccnt = (int32_t *)(b + l.ccnt);
     w.cmm = (float2 *)(b + l.cmm);
     w.lens = (int32_t *)(b + l.lens);
+    w.vmax = (float *)(b + l.vmax);
     w.cut_wg = l.cut_wg;
     w.nb_cap = l.nb_cap;
     w.max_sel = l.max_sel;
@@ -671,6 +673,10 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
     gp.pf = 1;
     gp.pf_seq = seq;
     gp.round_f16 = 0;                              // prefill reads the exact rows (kv_round_f16 is decode's)
+    if (g.vdim) {
+        e = launch_prefill_vmax(gp, *view, max_len, w.vmax, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill: V scales");
+    }
     for (int32_t i0 = 0; i0 < n_q; i0 += batch) {
         const int32_t nb = std::min(batch, n_q - i0);
         gp.pf_pos0 = pos0 + i0;
@@ -690,7 +696,7 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
             e = launch_prefill_index(gp, *view, qb, nb, max_len, sb, nsb, sel_stride, w, st);
         }
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer");
-        e = g.vdim ? launch_prefill_attention(gp, *view, qb, nb, sb, nsb, sel_stride, ob, st)
+        e = g.vdim ? launch_prefill_attention(gp, *view, qb, nb, sb, nsb, sel_stride, w.vmax, ob, st)
                    : launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: attention");
     }

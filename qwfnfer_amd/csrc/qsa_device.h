@@ -259,6 +259,16 @@ __device__ __forceinline__ void lds_dma16(const void *gsrc, uint32_t lds) {
                  : "v"(gsrc), "s"(lds)
                  : "memory");
 }
+// The same transfer from a wave-uniform base (an SGPR pair) plus a 32-bit
+// per-lane byte offset: no 64-bit address arithmetic in the lanes.
+__device__ __forceinline__ void lds_dma16_sv(const void *sbase, uint32_t voff, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
+
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Wait until at most N of the wave's vector-memory operations are in flight

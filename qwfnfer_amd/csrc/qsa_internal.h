@@ -42,6 +42,7 @@ struct Geo {
 // call layout agrees on it; all other regions are per-call scratch.
 constexpr int32_t kMaxCounters = 4096;   // (sequence, KV head) pairs per call
 constexpr int32_t kPrefillBatchMax = 32768;   // queries per prefill batch (one grid dimension)
+constexpr int32_t kVmaxWg = 64;               // partial V-scale maxima per KV head (prefill)
 // Eligible blocks the indexer workgroup selects from registers; longer decode
 // contexts select in a launch of their own, over kCutKeys scores per
 // workgroup when at most kCutWgMax workgroups cover them.
@@ -62,12 +63,13 @@ struct Ws {
     float2  *cmm;        // [n_seq][Hkv][nb_cap / kScoreRecBlocks] (min, max) eligible score of each record's blocks
                          // (the attention's own selection reads them; (+inf, -inf) when empty)
     int32_t *lens;       // [kMaxChain][n_seq] lengths of a chained call's positions
+    float   *vmax;       // [Hkv][kVmaxWg] partial maxima of the V scales a prefill call reads
     int32_t  nb_cap, max_sel, n_tiles;
     int32_t  cut_wg;     // workgroups of the multi-workgroup selection (0: one workgroup)
 };
 
 struct WsLayout {
-    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, lens, total;
+    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, lens, vmax, total;
     int32_t nb_cap, max_sel, n_tiles, cut_wg;
 };
 // partials = false: no attention partials (the prefill kernel keeps its state on chip);
@@ -177,11 +179,15 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                                 int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                                 const Ws &ws, hipStream_t st);
+// The largest q8_0 V scale of each KV head over positions [0, n_pos) of
+// sequence g.pf_seq, as kVmaxWg partial maxima per head (vmax).
+hipError_t launch_prefill_vmax(const Geo &g, const qwfn_kv_view &v, int32_t n_pos, float *vmax, hipStream_t st);
 // Prefill attention on the matrix cores (block_tokens % 64 == 0): one wave
-// per (query, KV head) over its selection, no partials.
+// per (query, KV head) over its selection, no partials; vmax from
+// launch_prefill_vmax over every position the queries read.
 hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
-                                    const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
-                                    hipStream_t st);
+                                    const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax,
+                                    float *out, hipStream_t st);
 // Decode attention that makes its own selection from the scores of a
 // scores-only indexer launch, writing it to sel / nsel (the q8_0 matrix-core
 // kernel for its shapes, the general kernel for the other element types and

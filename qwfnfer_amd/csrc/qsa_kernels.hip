@@ -2073,12 +2073,19 @@ hipError_t launch_gather(const Geo &g, const qwfn_kv_view &v, const int32_t *seq
 
 constexpr int kPfQA = 8;                   // queries per thread
 constexpr int kPfQ = 16 * kPfQA, kPfB = 64;  // queries x blocks per scoring workgroup
-constexpr int kPfSD = 16;                  // 16-byte dim chunks of the query rows per LDS stage
+constexpr int kPfSD = 8;                   // 16-byte dim chunks of the query rows per LDS stage
+
+constexpr int kPfQPad = kPfQ + kPfQ / kPfQA;   // one spare chunk after every 8 queries
+
+// Query qq of a stage sits at chunk qq + qq / 8 of its dim row: the four
+// 8-query groups one wave reads at a time land 144 bytes apart, on different
+// LDS banks.
+__device__ __forceinline__ int pf_qslot(int qq) { return qq + qq / kPfQA; }
 
 template <int HD>
 struct PfScoreShared {
     float4 p[HD / 4][kPfB];                // the tile's pooled keys, dim-chunk major
-    float4 q[kPfSD][kPfQ];                 // a 64-dim stage of the current head's query rows
+    float4 q[kPfSD][kPfQPad];              // a 64-dim stage of the current head's query rows
 };
 
 // grid (ceil((n_blk - sink) / 64), ceil(n_q / 128), Hkv), 256 threads.  The
@@ -2087,6 +2094,8 @@ struct PfScoreShared {
 // 64 dims at a time (reused 64 times); thread t owns queries 8*(t/16) .. +8 x
 // blocks t%16 + {0, 16, 32, 48} (16 consecutive blocks per read across a row
 // of lanes: no LDS bank conflicts), so each pooled-key read feeds 32 FMAs.
+// The next stage's query rows are loaded into registers while the current
+// stage is computed, so the global reads of a stage overlap the FMAs.
 // Each dot is formed in the decode indexer's order (chain j over the dims d
 // with (d/4)%4 == j in increasing order, then (c0+c1)+(c2+c3), relu when set,
 // heads summed in order), so a query's scores are bit-identical to a decode
@@ -2123,6 +2132,21 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
     for (int a = 0; a < QA; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) score[a][b] = 0.0f;
+    constexpr int NST = NDC / SD;                          // stages per head
+    constexpr int QPT = kPfQ * SD / 256;                   // query chunks a thread stages
+    static_assert(kPfQ * SD % 256 == 0, "whole stages per thread");
+    // the next stage's chunks, in flight: thread t stages chunk i = t + 256 r
+    // of (query i / SD, dim chunk i % SD) for r < QPT
+    const float *qsrc[QPT];
+#pragma unroll
+    for (int r = 0; r < QPT; ++r) {
+        const int i = tid + 256 * r;
+        const int qn = min(q_base + i / SD, n_q - 1);
+        qsrc[r] = q + ((int64_t)qn * g.H + gh * G) * HD + 4 * (i % SD);
+    }
+    f4v nq[QPT];
+#pragma unroll
+    for (int r = 0; r < QPT; ++r) nq[r] = *reinterpret_cast<const f4v *>(qsrc[r]);
     for (int h = 0; h < G; ++h) {
         float c[QA][4][4];                           // [query][block][chain]
 #pragma unroll
@@ -2131,22 +2155,29 @@ k_pf_scores(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) c[a][b][j] = 0.0f;
-        for (int st = 0; st < NDC; st += SD) {
+        for (int sti = 0; sti < NST; ++sti) {
+            const int st = sti * SD;
             __syncthreads();                         // the previous stage's rows are consumed
-            for (int i = tid; i < kPfQ * SD; i += 256) {
-                const int qq = i / SD, dc = i % SD;
-                const int qn = min(q_base + qq, n_q - 1);
-                sh.q[dc][qq] =
-                    *reinterpret_cast<const float4 *>(q + ((int64_t)qn * g.H + gh * G + h) * HD + 4 * (st + dc));
+#pragma unroll
+            for (int r = 0; r < QPT; ++r) {
+                const int i = tid + 256 * r;
+                *reinterpret_cast<f4v *>(&sh.q[i % SD][pf_qslot(i / SD)]) = nq[r];
             }
             __syncthreads();
+            if (h * NST + sti + 1 < G * NST) {
+                const int nx = h * NST + sti + 1;
+                const int off = nx / NST * HD + nx % NST * SD * 4;   // head nx / NST, dims of stage nx % NST
+#pragma unroll
+                for (int r = 0; r < QPT; ++r) nq[r] = *reinterpret_cast<const f4v *>(qsrc[r] + off);
+            }
             for (int d16 = 0; d16 < SD / 4; ++d16) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {        // dims 16*d16 + 4j .. +3 belong to chain j
                     const int dcl = 4 * d16 + j;
                     float4 qv[QA], pv[4];
+                    const int qs0 = pf_qslot(qi0);   // the thread's 8 queries share one group
 #pragma unroll
-                    for (int a = 0; a < QA; ++a) qv[a] = sh.q[dcl][qi0 + a];
+                    for (int a = 0; a < QA; ++a) qv[a] = sh.q[dcl][qs0 + a];
 #pragma unroll
                     for (int b = 0; b < 4; ++b) pv[b] = sh.p[st + dcl][bi0 + 16 * b];
 #pragma unroll
@@ -2287,6 +2318,48 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 
+// grid (kVmaxWg, Hkv), 256 threads: partial maxima of KV head gh's q8_0 V
+// scales over positions [0, n_pos) of sequence pf_seq, each a 64-cell tile's
+// scale row read as 16-byte chunks (cell c's NJ scales are halfs c*NJ ..
+// c*NJ+NJ-1 of the row); cells at or past n_pos and unmapped pages are left
+// out.  vmax[gh * kVmaxWg + blockIdx.x] gets the workgroup's maximum.
+template <int HD>
+__global__ void __launch_bounds__(256)
+k_pf_vmax(Geo g, qwfn_kv_view v, int32_t n_pos, float *__restrict__ vmax) {
+    constexpr int NJ = HD / 32, CPT = 64 * NJ * 2 / 16;    // 16-byte chunks per tile scale row
+    __shared__ float red[4];
+    const int gh = blockIdx.y;
+    const int n_chunks = (n_pos + 63) / 64 * CPT;
+    float mx = 0.0f;
+    for (int i = (int)blockIdx.x * 256 + (int)threadIdx.x; i < n_chunks; i += kVmaxWg * 256) {
+        const int t0 = i / CPT * 64, c = i % CPT;
+        const int32_t pg = phys_page(g, v.page_table, g.pf_seq, t0);
+        if (pg < 0) continue;
+        const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)pg * g.page_bytes;
+        const u4v w = *reinterpret_cast<const u4v *>(vp + scale_off(g, gh, t0 % g.pt, 0) + 16 * c);
+        const h8v x = __builtin_bit_cast(h8v, w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (t0 + (8 * c + e) / NJ < n_pos) mx = fmaxf(mx, fabsf((float)x[e]));
+    }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        vmax[gh * kVmaxWg + blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+hipError_t launch_prefill_vmax(const Geo &g, const qwfn_kv_view &v, int32_t n_pos, float *vmax, hipStream_t st) {
+    const dim3 grid((unsigned)kVmaxWg, (unsigned)g.Hkv);
+    switch (g.hd) {
+    case 64:  hipLaunchKernelGGL((k_pf_vmax<64>), grid, dim3(256), 0, st, g, v, n_pos, vmax); break;
+    case 128: hipLaunchKernelGGL((k_pf_vmax<128>), grid, dim3(256), 0, st, g, v, n_pos, vmax); break;
+    case 256: hipLaunchKernelGGL((k_pf_vmax<256>), grid, dim3(256), 0, st, g, v, n_pos, vmax); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int HD, int G>
 struct PfAttnCfg {
     static constexpr int NK4 = HD / 16;                   // 1 KB transfers per K (or V) tile
@@ -2323,18 +2396,23 @@ struct PfAttnLds {
 //    only the fp32 accumulation rounds;
 //  - PV: O[dim][head] += V[dim][cell] * P'_j[cell][head] with the V quants
 //    exact in fp16 and P'_j = p * dv(cell, j) * 2^k split into fp16 hi + lo
-//    (2^k keeps the tile's largest V scale near 2^15; O is carried in the
-//    current tile's units and rescaled with the softmax).
+//    (2^k, one per KV head and call, brings the head's largest V scale near
+//    2^15, so P' stays finite in fp16 and its low half normal; the softmax
+//    weights are formed as exp2(s * scale - m + k), and O and the weight sum
+//    carry the same 2^k).
 // Cells past the query's position have weight 0 and their V scale masked.
+// K and V tiles are addressed from a wave-uniform base plus a fixed per-lane
+// offset (no per-lane 64-bit address arithmetic per tile).
 template <int HD, int G>
 __global__ void __launch_bounds__((PfAttnCfg<HD, G>::WAVES * 64))
 k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const int32_t *__restrict__ sel,
-          const int32_t *__restrict__ nsel, int32_t max_sel, float *__restrict__ out) {
+          const int32_t *__restrict__ nsel, int32_t max_sel, const float *__restrict__ vmax,
+          float *__restrict__ out) {
     using C = PfAttnCfg<HD, G>;
     constexpr int NJ = HD / 32, ND = HD / 16, NK4 = C::NK4, NS4 = C::NS4;
     static_assert(G <= 16, "one MFMA output column per query head");
     __shared__ PfAttnLds<HD, G> shw[C::WAVES];
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
     const int pair = (int)blockIdx.x * C::WAVES + wv;
     if (pair >= n_q * g.Hkv) return;                 // a whole wave; no workgroup barrier follows
     PfAttnLds<HD, G> &W = shw[wv];
@@ -2377,14 +2455,28 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 ql[j][i] = (_Float16)(y - (float)hi);
             }
     }
-    const float lscale = qs * g.scale_log2;
+    const float lscale = qs * g.scale_log2;          // > 0
+    // the weights enter PV scaled by 2^kup, which brings the KV head's largest
+    // V scale (k_pf_vmax, over every row the call's queries read) near 2^15:
+    // p * dv * 2^kup stays below the fp16 maximum and its low half normal
+    float kup;
+    {
+        float dvm = vmax[gh * kVmaxWg + l % kVmaxWg];
+        dvm = wave_max(dvm);
+        int e2 = 0;
+        frexpf(dvm, &e2);
+        kup = dvm > 0.0f ? (float)(15 - e2) : 0.0f;
+    }
     f4v o[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) o[d] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     // running max starts at a finite floor far below any score, so exp2 of
     // (score - max) never sees inf - inf
-    float m = -1e30f, lsum = 0.0f, up_cur = 1.0f;
+    float m = -1e30f, lsum = 0.0f;                   // lsum in units of 2^kup
     const int n_tiles = n * tpb;
+    // lane l's 16 bytes of a V tile's 1 KB transfer: dim row l / 4, quarter
+    // (l % 4) ^ (row / 4 % 4)
+    const uint32_t v_lane = (uint32_t)((l >> 2) * 64 + (((l & 3) ^ ((l >> 4) & 3)) << 4));
     for (int tc = 0; tc < n_tiles; tc += 64) {
         // lane l describes tile tc + l: page, first row, cells at or before the
         // query -- looked up for 64 tiles at once, read back per tile by readlane
@@ -2422,9 +2514,9 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
             const uint8_t *kp, *vp;
             int tl, row0;
             tile_src(ti, kp, vp, tl, row0);
-            const uint8_t *ksrc = kp + (int64_t)tl * (HD / 16) * 1024 + 16 * l;
+            const uint8_t *ksrc = kp + (int64_t)tl * (HD / 16) * 1024;
 #pragma unroll
-            for (int i = 0; i < NK4; ++i) lds_dma16(ksrc + i * 1024, base + C::KOFF + i * 1024);
+            for (int i = 0; i < NK4; ++i) lds_dma16_sv(ksrc + i * 1024, 16 * l, base + C::KOFF + i * 1024);
             const uint8_t *kss = kp + scale_off(g, gh, row0, 0);
             const uint8_t *vss = vp + scale_off(g, gh, row0, 0);
 #pragma unroll
@@ -2437,9 +2529,9 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
             const uint8_t *kp, *vp;
             int tl, row0;
             tile_src(ti, kp, vp, tl, row0);
-            const uint8_t *vsrc = vp + (int64_t)tl * HD * 64 + (l >> 2) * 64 + (((l & 3) ^ ((l >> 4) & 3)) << 4);
+            const uint8_t *vsrc = vp + (int64_t)tl * HD * 64;
 #pragma unroll
-            for (int i = 0; i < NK4; ++i) lds_dma16(vsrc + i * 1024, base + C::VOFF + i * 1024);
+            for (int i = 0; i < NK4; ++i) lds_dma16_sv(vsrc + i * 1024, v_lane, base + C::VOFF + i * 1024);
         };
         issue_k(0);
         issue_v(0);
@@ -2480,7 +2572,7 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                         for (int i = 0; i < 4; ++i)
                             acc[i] = __builtin_fmaf((float)dk[(i * NJ + j) / 8][(i * NJ + j) % 8], c[j][i], acc[i]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) sv[mb][i] = acc[i] * lscale;
+                    for (int i = 0; i < 4; ++i) sv[mb][i] = acc[i];   // log2 units after * lscale
                 }
                 // V scales of this lane's PV cells 32ks+8lg .. +8, every block (NJ words per ks)
                 u4v dvw[2][NJ];
@@ -2512,40 +2604,25 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
-                tm = col_max4(tm);
+                tm = col_max4(tm) * lscale;          // lscale > 0: the max commutes
                 const float m_new = fmaxf(m, tm);
                 const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+                const float bias = kup - m_new;
                 float tsum = 0.0f;
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float p = __builtin_amdgcn_exp2f(sv[mb][i] - m_new);
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[mb][i], lscale, bias));
                         tsum += p;
                         if (hv) W.p[hn][16 * mb + 4 * lg + i] = p;
                     }
                 tsum = col_sum4(tsum);
                 lsum = lsum * alpha + tsum;
                 m = m_new;
-                // the tile's largest V scale sets the weight exponent (scales are >= 0)
-                h8v dmx = __builtin_bit_cast(h8v, dvw[0][0]);
+                if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int w = 0; w < NJ; ++w)
-                        dmx = __builtin_elementwise_max(dmx, __builtin_bit_cast(h8v, dvw[ks][w]));
-                float dvm = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dvm = fmaxf(dvm, (float)dmx[e]);
-                dvm = wave_max(dvm);
-                int e2 = 0;
-                frexpf(dvm, &e2);
-                const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - e2) : 1.0f;
-                const float rs = alpha * (up / up_cur);  // O moves to this tile's units (power-of-two ratio)
-                up_cur = up;
-                if (__builtin_amdgcn_ballot_w64(rs != 1.0f) != 0) {
-#pragma unroll
-                    for (int d = 0; d < ND; ++d) o[d] *= rs;
+                    for (int d = 0; d < ND; ++d) o[d] *= alpha;
                 }
                 wave_lds_sync();
                 // ---- PV operands: the weights of head hn and the V quants this lane feeds
@@ -2557,7 +2634,7 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                         const float4 p1 = *reinterpret_cast<const float4 *>(&W.p[hq][32 * ks + 8 * lg + 4]);
                         const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) pcr[ks][i] = hv ? pc[i] * up : 0.0f;
+                        for (int i = 0; i < 8; ++i) pcr[ks][i] = hv ? pc[i] : 0.0f;
 #pragma unroll
                         for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -2607,7 +2684,7 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
         }
     }
     if (hv) {
-        const float inv = lsum > 0.0f ? 1.0f / (lsum * up_cur) : 0.0f;
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
         float *orow = out + ((int64_t)s * g.H + gh * G + hn) * HD;
 #pragma unroll
         for (int d = 0; d < ND; ++d)
@@ -2618,20 +2695,20 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
 
 template <int HD, int G>
 static void launch_pf_attn_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
-                             const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
-                             hipStream_t st) {
+                             const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax,
+                             float *out, hipStream_t st) {
     constexpr int WAVES = PfAttnCfg<HD, G>::WAVES;
     const int pairs = n_q * g.Hkv;
     hipLaunchKernelGGL((k_pf_attn<HD, G>), dim3((unsigned)((pairs + WAVES - 1) / WAVES)), dim3(WAVES * 64), 0, st, g,
-                       v, q, n_q, sel, nsel, max_sel, out);
+                       v, q, n_q, sel, nsel, max_sel, vmax, out);
 }
 
 hipError_t launch_prefill_attention(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
-                                    const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
-                                    hipStream_t st) {
+                                    const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax,
+                                    float *out, hipStream_t st) {
 #define X(HD_, G_, TG_)                                                                          \
     if (g.hd == HD_ && g.G == G_) {                                                              \
-        launch_pf_attn_t<HD_, G_>(g, v, q, n_q, sel, nsel, max_sel, out, st);                   \
+        launch_pf_attn_t<HD_, G_>(g, v, q, n_q, sel, nsel, max_sel, vmax, out, st);             \
         return hipGetLastError();                                                                \
     }
     QWFN_FOR_EACH_SHAPE(X)
