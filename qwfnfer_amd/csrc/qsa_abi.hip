@@ -189,7 +189,10 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     l.ccnt = take(l.cut_wg ? pairs * kCutWgMax * sizeof(int32_t) : 0);
     l.cmm = take(partials ? pairs * (l.nb_cap / kScoreRecBlocks) * sizeof(float2) : 0);
     l.lens = take((size_t)kMaxChain * n_seq * sizeof(int32_t));
-    l.vmax = take(partials ? 0 : (size_t)g.Hkv * kVmaxWg * sizeof(float));
+    // prefill layouts (cut = false): the V-scale maxima of the matrix-core
+    // attention (partials = false) and the pooled keys' norms of the scoring
+    l.vmax = take(!cut && !partials ? (size_t)g.Hkv * kVmaxWg * sizeof(float) : 0);
+    l.pnorm = take(!cut ? (size_t)g.Hkv * l.nb_cap * sizeof(float) : 0);
     l.total = off;
     return l;
 }
@@ -208,6 +211,7 @@ Ws ws_bind(void *base, const WsLayout &l) {
     w.cmm = (float2 *)(b + l.cmm);
     w.lens = (int32_t *)(b + l.lens);
     w.vmax = (float *)(b + l.vmax);
+    w.pnorm = (float *)(b + l.pnorm);
     w.cut_wg = l.cut_wg;
     w.nb_cap = l.nb_cap;
     w.max_sel = l.max_sel;

@@ -64,12 +64,13 @@ struct Ws {
                          // (the attention's own selection reads them; (+inf, -inf) when empty)
     int32_t *lens;       // [kMaxChain][n_seq] lengths of a chained call's positions
     float   *vmax;       // [Hkv][kVmaxWg] partial maxima of the V scales a prefill call reads
+    float   *pnorm;      // [Hkv][nb_cap] prefill: each pooled block's key norm (the scoring bound)
     int32_t  nb_cap, max_sel, n_tiles;
     int32_t  cut_wg;     // workgroups of the multi-workgroup selection (0: one workgroup)
 };
 
 struct WsLayout {
-    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, lens, vmax, total;
+    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, lens, vmax, pnorm, total;
     int32_t nb_cap, max_sel, n_tiles, cut_wg;
 };
 // partials = false: no attention partials (the prefill kernel keeps its state on chip);

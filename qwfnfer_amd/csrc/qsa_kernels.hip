@@ -2230,11 +2230,502 @@ k_pf_select(Geo g, float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, i
         select_blocks<kIdxThreads>(g, scores + (int64_t)pair * nb_cap, g.pf_pos0 + s + 1, out, sh);
 }
 
+// ---------------------------------------------------------------------------
+// prefill scoring on the matrix cores: approximate scores with an error
+// bound, then exact scores for the blocks the bound leaves open
+// ---------------------------------------------------------------------------
+
+constexpr int kPaQ = 64;              // queries per approximate-scoring workgroup (16 a wave)
+constexpr int kPaB = 64;              // pooled blocks per staged tile
+constexpr int kPaSplit = 4;           // workgroups sharing one query tile's blocks
+constexpr int kRefineMax = 512;       // candidates ranked exactly (more: the whole row exactly)
+constexpr int kRefineBlocks = 4096;   // eligible blocks the approximate path takes
+// |approximate - exact| <= kPaRel * (sum over the group's heads of |q_h|) * |p|
+// + kPaAbs (Euclidean norms: sum_d |q_hd p_d| <= |q_h| |p|).  The terms: fp16
+// rounding of both operands, 2 * 2^-11 + 2^-22 of each product; the matrix
+// cores' fp32 sums over a head's dims, the relu'd head sum and the
+// power-of-two rescale, below 2 * 128 * 2^-24; the exact scores' own rounding
+// (four chains of HD / 4 fmas, their two sums, the head sum), below
+// 80 * 2^-24; fp16 subnormals, below 2^-30.  They sum to 9.97e-4; 5 % more
+// covers the rounding of the norms and of the bound itself.
+constexpr float kPaRel = 1.05e-3f;
+// an absolute floor: a score that underflows fp32 keeps no relative precision
+constexpr float kPaAbs = 1e-37f;
+
+template <int HD, int G> constexpr bool pf_approx_fits() { return G * HD <= 1024 && HD % 32 == 0 && 256 % G == 0; }
+
+// The power of two that scales a row whose largest magnitude is m into
+// [2^14, 2^15) (fp16 keeps 11 significant bits there): 15 - e for m = f 2^e.
+__device__ __forceinline__ int fp16_shift(float m) {
+    int e = 0;
+    frexpf(m, &e);
+    return m > 0.0f ? 15 - e : 0;
+}
+
+template <int HD>
+struct PaShared {
+    uint2 p[kPaB][HD / 4 + 2];            // the tile's pooled keys as fp16, each block scaled; rows + 16 bytes
+    int pe[kPaB];                         // the blocks' scale exponents
+};
+
+// grid (ceil(n_q / 64), kPaSplit, Hkv), 256 threads.  Approximate scores of
+// 64 queries against the eligible blocks [sink, n_blk) of KV head gh (tiles
+// blockIdx.y, blockIdx.y + kPaSplit, ... of 64 blocks): S[query][block] = sum
+// over the group's heads of (relu'd when set) q_h . p on
+// v_mfma_f32_16x16x32_f16.  The A operand, the query scaled by a power of two
+// (its largest element over the group's heads in [2^14, 2^15)), stays in
+// registers for the launch; each tile of pooled keys, every block scaled the
+// same way, is staged in LDS as the B operand.  Wave w owns queries 16w ..
+// 16w+15; a lane's outputs are 4 queries x 1 block, scaled back exactly.  The
+// query-tile-0 workgroups also write each block's |p| (rounded up) to pnorm.
+template <int HD, int G>
+__global__ void __launch_bounds__(256, 2)
+k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int32_t n_blk,
+            float *__restrict__ scores, int32_t nb_cap, float *__restrict__ pnorm) {
+    constexpr int NK = HD / 32;                        // k-steps of one head
+    constexpr int CPT = HD / 16;                       // 16-byte fp32 chunks a thread stages (4 threads a block)
+    static_assert(pf_approx_fits<HD, G>(), "a wave's query fragments fit its registers");
+    __shared__ PaShared<HD> sh;
+    const int tid = threadIdx.x, l = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gh = blockIdx.z, row = l & 15, kg = l >> 4;
+    const int qbase = (int)blockIdx.x * kPaQ + 16 * wv;
+    // A operand: query qbase + row, dims 32 ks + 8 kg .. +8 of each head
+    const float *qrow = q + ((int64_t)min(qbase + row, n_q - 1) * g.H + gh * G) * HD + 8 * kg;
+    float qm = 0.0f;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) {
+            const float4 a = *reinterpret_cast<const float4 *>(qrow + h * HD + 32 * ks);
+            const float4 b = *reinterpret_cast<const float4 *>(qrow + h * HD + 32 * ks + 4);
+            qm = fmaxf(qm, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+            qm = fmaxf(qm, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        }
+    qm = fmaxf(qm, __shfl_xor(qm, 16));
+    qm = fmaxf(qm, __shfl_xor(qm, 32));
+    const int qe = fp16_shift(qm);
+    h8v qa[G][NK];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) {
+            const float4 a = *reinterpret_cast<const float4 *>(qrow + h * HD + 32 * ks);
+            const float4 b = *reinterpret_cast<const float4 *>(qrow + h * HD + 32 * ks + 4);
+            qa[h][ks] = h8v{(_Float16)ldexpf(a.x, qe), (_Float16)ldexpf(a.y, qe), (_Float16)ldexpf(a.z, qe),
+                            (_Float16)ldexpf(a.w, qe), (_Float16)ldexpf(b.x, qe), (_Float16)ldexpf(b.y, qe),
+                            (_Float16)ldexpf(b.z, qe), (_Float16)ldexpf(b.w, qe)};
+        }
+    // the scale exponents of this lane's output rows (queries qbase + 4 kg + i)
+    int qe_o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qe_o[i] = __shfl(qe, 4 * kg + i);
+    const int n_tiles = (n_blk - g.sink + kPaB - 1) / kPaB;
+    const int64_t prow = ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps;   // the row's first pooled block
+    const int sb = tid >> 2, sc = tid & 3;             // staging: block sb of the tile, chunks sc + 4 i
+    for (int t = (int)blockIdx.y; t < n_tiles; t += kPaSplit) {
+        const int b0 = g.sink + t * kPaB;
+        const int bb = min(b0 + sb, n_blk - 1);
+        auto chunk = [&](int dc) -> float4 {           // 4 consecutive dims of block bb
+            if (g.pooled_f16) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(v.pooled) +
+                                                                 (prow + bb) * HD + 4 * dc);
+                return make_float4(h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16)), h2f((uint16_t)w.y),
+                                   h2f((uint16_t)(w.y >> 16)));
+            }
+            return *reinterpret_cast<const float4 *>(v.pooled + (prow + bb) * HD + 4 * dc);
+        };
+        // the block's largest element, then (a second, cache-hot read) its
+        // scaled fp16 values and squares
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const float4 x = chunk(sc + 4 * i);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+        }
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        const int pe = fp16_shift(m);
+        __syncthreads();                               // the previous tile's fragments are read
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const float4 x = chunk(sc + 4 * i);
+            const float y0 = ldexpf(x.x, pe), y1 = ldexpf(x.y, pe), y2 = ldexpf(x.z, pe), y3 = ldexpf(x.w, pe);
+            ss = __builtin_fmaf(y0, y0, ss);
+            ss = __builtin_fmaf(y1, y1, ss);
+            ss = __builtin_fmaf(y2, y2, ss);
+            ss = __builtin_fmaf(y3, y3, ss);
+            const half2v lo2 = {(_Float16)y0, (_Float16)y1}, hi2 = {(_Float16)y2, (_Float16)y3};
+            sh.p[sb][sc + 4 * i] = make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
+        }
+        if (sc == 0) sh.pe[sb] = pe;
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        if (blockIdx.x == 0 && sc == 0 && b0 + sb < n_blk)
+            pnorm[(int64_t)gh * nb_cap + b0 + sb] = ldexpf(sqrtf(ss) * (1.0f + 0x1p-14f), -pe);
+        __syncthreads();
+#pragma unroll
+        for (int ct = 0; ct < kPaB / 16; ++ct) {
+            h8v bf[NK];                                // B operand: block 16 ct + row, dims 32 ks + 8 kg .. +8
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks)
+                bf[ks] = *reinterpret_cast<const h8v *>(&sh.p[16 * ct + row][2 * (4 * ks + kg)]);
+            f4v tot = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (g.relu) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int ks = 0; ks < NK; ++ks)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], acc, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) tot[i] += fmaxf(acc[i], 0.0f);
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < G; ++h)
+#pragma unroll
+                    for (int ks = 0; ks < NK; ++ks)
+                        tot = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], tot, 0, 0, 0);
+            }
+            const int blk = b0 + 16 * ct + row;
+            const int pb = sh.pe[16 * ct + row];
+            if (blk < n_blk) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qo = qbase + 4 * kg + i;
+                    if (qo < n_q) scores[((int64_t)qo * g.Hkv + gh) * nb_cap + blk] = ldexpf(tot[i], -(qe_o[i] + pb));
+                }
+            }
+        }
+    }
+}
+
+// Exact dots of a pooled block with heads [h0, h0 + NH) in the decode
+// indexer's order (k_pf_scores): chain j over the dims d with (d / 4) % 4 == j
+// in increasing order, then (c0 + c1) + (c2 + c3), relu'd when set.  pchunk(dc)
+// gives the key's dims 4 dc .. 4 dc + 3; qs holds the group's query rows,
+// qstride floats apart.  Each key chunk is read once and feeds NH * 4 fmas.
+template <int HD, int NH, class PC>
+__device__ __forceinline__ void pf_exact_dots(const Geo &g, PC pchunk, const float *qs, int qstride, int h0,
+                                              float (&dot)[NH]) {
+#pragma clang fp contract(off)
+    float c[NH][4];
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[h][j] = 0.0f;
+#pragma unroll 2
+    for (int d16 = 0; d16 < HD / 16; ++d16)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int dc = 4 * d16 + j;
+            const float4 p4 = pchunk(dc);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(qs + (h0 + h) * qstride + 4 * dc);
+                float x = c[h][j];
+                x = fmaf(q4.x, p4.x, x);
+                x = fmaf(q4.y, p4.y, x);
+                x = fmaf(q4.z, p4.z, x);
+                x = fmaf(q4.w, p4.w, x);
+                c[h][j] = x;
+            }
+        }
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        float d = (c[h][0] + c[h][1]) + (c[h][2] + c[h][3]);
+        if (g.relu) d = d > 0.0f ? d : 0.0f;
+        dot[h] = d;
+    }
+}
+
+// Chunk dc of pooled block b as fp32 (fp16 keys widened exactly).
+__device__ __forceinline__ float4 pooled_chunk(const Geo &g, const qwfn_kv_view &v, int64_t off) {
+    if (g.pooled_f16) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(v.pooled) + off);
+        return make_float4(h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16)), h2f((uint16_t)w.y),
+                           h2f((uint16_t)(w.y >> 16)));
+    }
+    return *reinterpret_cast<const float4 *>(v.pooled + off);
+}
+
+// LDS of the 256-thread selection (select_blocks: register path, radix
+// fallback) without the indexer's scoring and pooling stage.
+struct RefineSel {
+    uint32_t hist[4096 + 64];
+    uint32_t cand_key[kCandMax + 1];
+    int32_t cand_b[kCandMax + 1];
+    uint32_t tmask[kIdxThreads];
+    uint32_t selbits[kKeysMax / 32 + 1];
+    float red[2 * (kIdxThreads / 64)];
+    int tmp[16];
+    int flag, bin, need, ncand, cnt_b;
+};
+
+template <int HD, int G>
+struct RefineShared {
+    float q[G * (HD + 4)];                        // the group's query rows, padded
+    RefineSel s;                                  // the histogram; select_blocks' state on the fallback
+    uint32_t ckey[kRefineMax];                    // candidates in block order: exact score keys, blocks
+    int32_t cblk[kRefineMax];
+    int32_t rk[kRefineMax];                       // their ranks
+    int32_t cbase[kRefineBlocks / 64];            // candidates before each (thread row, wave) group
+    float qn[G];
+};
+
+// grid (Hkv, n_q), kIdxThreads: query s's selection for KV head gh at its
+// length pf_pos0 + s + 1, identical to the selection on the exact scores.
+// The exact score of block b (k_pf_scores' order) lies within E_b = kPaRel *
+// sum_h |q_h| * |p_b| + kPaAbs of its approximate score a_b (k_pf_approx).
+// Let T be the topk-th largest lower bound a_b - E_b over the eligible
+// blocks: at least topk blocks score at least T exactly, so every block of
+// the exact top-k has a_b + E_b >= T.  The candidates -- upper bounds in or
+// above T's bin of a 4096-bin histogram of the lower bounds, a monotone map --
+// are gathered in block order and scored exactly; the top-k of them by (score
+// desc, index asc) is the selection, emitted at its prefix-sum places.  A
+// non-finite approximate score or bound, or more than kRefineMax candidates,
+// scores the whole row exactly for select_blocks instead.
+template <int HD, int G>
+__global__ void __launch_bounds__(kIdxThreads, 2)
+k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, int32_t nb_cap,
+            const float *__restrict__ pnorm, int32_t *sel, int32_t *nsel, int32_t max_sel) {
+#pragma clang fp contract(off)
+    constexpr int NT = kIdxThreads, QS = HD + 4, KPT = kRefineBlocks / NT, NW = NT / 64;
+    constexpr int NCH = HD / 16;                       // key chunks of one chain
+    static_assert(pf_approx_fits<HD, G>() && KPT * NW <= kRefineBlocks / 64, "group table");
+    __shared__ RefineShared<HD, G> sh;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int gh = blockIdx.x, s = blockIdx.y;
+    const int pair = s * g.Hkv + gh;
+    const int L = g.pf_pos0 + s + 1;
+    const SelOut out = sel_out(g, sel, nsel, max_sel, s, pair);
+    float *row = scores + (int64_t)pair * nb_cap;
+    const Ranges r = qsa_ranges(g, L);
+    const int topk = eff_topk(g, r);
+    if (g.topk <= 0 || r.e_hi - r.e_lo <= topk || topk == 0) {   // nothing ranked: no score is read
+        select_blocks<NT>(g, row, L, out, sh.s);
+        return;
+    }
+    const int64_t prow = ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps;
+    // the approximate scores and key norms of this thread's blocks e_lo + tid + NT i
+    float av[KPT], pv[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int b = min(r.e_lo + tid + NT * i, r.e_hi - 1);
+        av[i] = row[b];
+        pv[i] = pnorm[(int64_t)gh * nb_cap + b];
+    }
+    float *qs = sh.q;
+    const float *qrow = q + ((int64_t)s * g.H + gh * G) * HD;
+    for (int i = tid; i < G * HD / 4; i += NT) {
+        const int h = i / (HD / 4), c = i % (HD / 4);
+        *reinterpret_cast<float4 *>(qs + h * QS + 4 * c) = *reinterpret_cast<const float4 *>(qrow + h * HD + 4 * c);
+    }
+    __syncthreads();
+    // |q_h| (rounded up), one wave a head, scaled by a power of two against overflow and underflow
+    for (int h = wid; h < G; h += NW) {
+        float m = 0.0f;
+        for (int d = lane; d < HD; d += 64) m = fmaxf(m, fabsf(qs[h * QS + d]));
+        const int e = fp16_shift(wave_max(m));
+        float ss = 0.0f;
+        for (int d = lane; d < HD; d += 64) {
+            const float y = ldexpf(qs[h * QS + d], e);
+            ss = __builtin_fmaf(y, y, ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) sh.qn[h] = ldexpf(sqrtf(ss) * (1.0f + 0x1p-14f), -e);
+    }
+    __syncthreads();
+    float qn = 0.0f;
+#pragma unroll
+    for (int h = 0; h < G; ++h) qn += sh.qn[h];
+    const float ec = kPaRel * qn * (1.0f + 0x1p-14f);
+    float lb[KPT], ub[KPT];
+    bool bad = !(ec < INFINITY);
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const bool in = r.e_lo + tid + NT * i < r.e_hi;
+        const float e = __builtin_fmaf(ec, pv[i], kPaAbs);
+        lb[i] = in ? av[i] - e : -INFINITY;
+        ub[i] = in ? av[i] + e : -INFINITY;
+        bad |= in && (!(fabsf(av[i]) < INFINITY) || !(e < INFINITY));
+        lo = fminf(lo, in ? lb[i] : INFINITY);
+        hi = fmaxf(hi, lb[i]);
+    }
+    hi = wave_max(hi);
+    lo = -wave_max(-lo);
+    if (lane == 0) { sh.s.red[wid] = hi; sh.s.red[NW + wid] = lo; }
+    uint4 *h4 = reinterpret_cast<uint4 *>(sh.s.hist);
+#pragma unroll
+    for (int i = 0; i < 4096 / 4 / NT; ++i) h4[tid + i * NT] = make_uint4(0u, 0u, 0u, 0u);
+    bad = __syncthreads_or(bad);
+    int nc = 0;
+    if (!bad) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) { hi = fmaxf(hi, sh.s.red[i]); lo = fminf(lo, sh.s.red[NW + i]); }
+        const float span = hi - lo, scale = 4096.0f / span;
+        const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
+        // monotone in x: a linear map of [lo, hi], else the top 12 key bits
+        auto bin_of = [&](float x) -> uint32_t {
+            return lin ? (uint32_t)fminf(fmaxf((x - lo) * scale, 0.0f), 4095.0f) : score_key(x) >> 20;
+        };
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool in = r.e_lo + tid + NT * i < r.e_hi;
+            atomicAdd(&sh.s.hist[in ? bin_of(lb[i]) : 4096u + (uint32_t)lane], 1u);
+        }
+        __syncthreads();
+        if (wid == 0) hist_cut(sh.s, topk);
+        __syncthreads();
+        const uint32_t B = (uint32_t)sh.s.bin;
+        // candidates in block order: group (i, wave) holds blocks e_lo + NT i + 64 wave + lane
+        uint32_t cm = 0;                              // this thread's candidate bits, one per i
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool c = r.e_lo + tid + NT * i < r.e_hi && bin_of(ub[i]) >= B;
+            cm |= (uint32_t)c << i;
+            const uint64_t m = __ballot(c);
+            if (lane == 0) sh.cbase[i * NW + wid] = (int)__builtin_popcountll(m);
+        }
+        __syncthreads();
+        if (wid == 0) {                               // exclusive scan of the group counts
+            const int x = lane < KPT * NW ? sh.cbase[lane] : 0;
+            const int incl = wave_incl_scan(x);
+            if (lane < KPT * NW) sh.cbase[lane] = incl - x;
+            if (lane == 63) sh.s.ncand = incl;
+        }
+        __syncthreads();
+        nc = sh.s.ncand;
+        if (nc <= kRefineMax) {
+            const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                const bool c = (cm >> i) & 1u;
+                const uint64_t m = __ballot(c);
+                if (c) sh.cblk[sh.cbase[i * NW + wid] + (int)__builtin_popcountll(m & below)] = r.e_lo + tid + NT * i;
+            }
+        }
+        for (int i = tid; i < kRefineMax; i += NT) sh.rk[i] = 0;
+        __syncthreads();
+    }
+    if (bad || nc > kRefineMax) {
+        // the whole row exactly (k_pf_scores' values), then the plain selection
+        constexpr int HPT = G < 4 ? G : 4;
+        for (int b = r.e_lo + tid; b < r.e_hi; b += NT) {
+            float sc = 0.0f;
+            for (int h0 = 0; h0 < G; h0 += HPT) {     // HPT heads at a time, summed in head order
+                float d[HPT];
+                pf_exact_dots<HD, HPT>(g, [&](int dc) { return pooled_chunk(g, v, (prow + b) * HD + 4 * dc); }, qs,
+                                       QS, h0, d);
+#pragma unroll
+                for (int h = 0; h < HPT; ++h) sc = h0 + h == 0 ? d[h] : sc + d[h];
+            }
+            row[b] = sc;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the exact row, for the selection's loads
+        __syncthreads();
+        select_blocks<NT>(g, row, L, out, sh.s);
+        return;
+    }
+    // exact scores of the candidates, 128 at a time, two threads each: thread
+    // half takes chains 2 half and 2 half + 1 of every head, reading its key
+    // chunks 4 d16 + chain straight from memory (all of them in flight); the
+    // pair combines (c0 + c1) + (c2 + c3), then the first sums the heads in order
+    for (int c0 = 0; c0 < nc; c0 += NT / 2) {
+        const int ci = c0 + (tid >> 1), half = tid & 1;
+        const int b = sh.cblk[min(ci, nc - 1)];
+        float4 pk[2][NCH];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+            for (int d16 = 0; d16 < NCH; ++d16)
+                pk[k][d16] = pooled_chunk(g, v, (prow + b) * HD + 4 * (4 * d16 + 2 * half + k));
+        float score = 0.0f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float cc[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float x = 0.0f;
+#pragma unroll
+                for (int d16 = 0; d16 < NCH; ++d16) {
+                    const float4 q4 = *reinterpret_cast<const float4 *>(qs + h * QS + 4 * (4 * d16 + 2 * half + k));
+                    x = fmaf(q4.x, pk[k][d16].x, x);
+                    x = fmaf(q4.y, pk[k][d16].y, x);
+                    x = fmaf(q4.z, pk[k][d16].z, x);
+                    x = fmaf(q4.w, pk[k][d16].w, x);
+                }
+                cc[k] = x;
+            }
+            const float pair_sum = cc[0] + cc[1];        // c0 + c1 (half 0), c2 + c3 (half 1)
+            float dot = pair_sum + __shfl_xor(pair_sum, 1);
+            if (g.relu) dot = dot > 0.0f ? dot : 0.0f;
+            score = h == 0 ? dot : score + dot;
+        }
+        if (half == 0 && ci < nc) sh.ckey[ci] = score_key(score);
+    }
+    __syncthreads();
+    // rank by (key desc, index asc) -- the order of the composite (key, ~block),
+    // above 2^31 for every candidate -- the first topk taken.  Candidates i0 ..
+    // i0+63 sit one a lane in every wave; each wave counts the larger keys among
+    // 16 of every 64 candidates, broadcast from registers.
+    auto order_key = [&](int i) -> uint64_t {
+        return i < nc ? ((uint64_t)sh.ckey[i] << 32) | (uint32_t)~sh.cblk[i] : 0ull;
+    };
+    for (int i0 = 0; i0 < nc; i0 += 64) {
+        const uint64_t ci = order_key(i0 + lane);
+        int part = 0;
+        for (int j0 = 0; j0 < nc; j0 += 64) {
+            const uint64_t cj = order_key(j0 + lane);
+            const uint32_t jh = (uint32_t)(cj >> 32), jl = (uint32_t)cj;
+            const int k_end = min(min(64, nc - j0), 16 * wid + 16);
+            for (int k = 16 * wid; k < k_end; ++k) {
+                const uint64_t ck = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(jh, k) << 32) |
+                                    (uint32_t)__builtin_amdgcn_readlane(jl, k);
+                part += ck > ci;
+            }
+        }
+        if (i0 + lane < nc) atomicAdd(&sh.rk[i0 + lane], part);
+    }
+    __syncthreads();
+    // emission in block order between the sink and the window blocks: a taken
+    // candidate's place is the count of taken candidates before it
+    {
+        constexpr int PER = kRefineMax / NT;          // candidates a thread, consecutive
+        int cnt = 0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = PER * tid + k;
+            cnt += i < nc && sh.rk[i] < topk;
+        }
+        int tot;
+        int pos = block_excl_sum<NT>(cnt, sh.s.tmp, &tot);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = PER * tid + k;
+            if (i < nc && sh.rk[i] < topk) out.put(g.sink + pos++, sh.cblk[i]);
+        }
+    }
+    emit_forced<NT>(g, r, topk, out);
+}
+
 template <int HD, int G>
 static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                               int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                               const Ws &ws, hipStream_t st) {
     const int32_t n_blk = max_seq_len / g.bt;                   // whole blocks of the longest query
+    if constexpr (pf_approx_fits<HD, G>()) {
+        if (!g.shared && g.topk > 0 && n_blk > g.sink && n_blk - g.sink <= kRefineBlocks) {
+            hipLaunchKernelGGL((k_pf_approx<HD, G>),
+                               dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv), dim3(256),
+                               0, st, g, v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm);
+            hipLaunchKernelGGL((k_pf_refine<HD, G>), dim3((unsigned)g.Hkv, (unsigned)n_q), dim3(kIdxThreads), 0, st, g,
+                               v, q, ws.scores, ws.nb_cap, ws.pnorm, sel, nsel, max_sel);
+            return;
+        }
+    }
     if (g.topk > 0 && n_blk > g.sink) {
         const dim3 grid((unsigned)((n_blk - g.sink + kPfB - 1) / kPfB), (unsigned)((n_q + kPfQ - 1) / kPfQ),
                         (unsigned)g.Hkv);
