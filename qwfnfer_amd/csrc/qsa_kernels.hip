@@ -2278,6 +2278,7 @@ struct PaShared {
 // same way, is staged in LDS as the B operand.  Wave w owns queries 16w ..
 // 16w+15; a lane's outputs are 4 queries x 1 block, scaled back exactly.  The
 // query-tile-0 workgroups also write each block's |p| (rounded up) to pnorm.
+// Pooled keys are fp32 (the checkpoint indexer's fp16 pool scores exactly).
 template <int HD, int G>
 __global__ void __launch_bounds__(256, 2)
 k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int32_t n_blk,
@@ -2326,12 +2327,6 @@ k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
         const int b0 = g.sink + t * kPaB;
         const int bb = min(b0 + sb, n_blk - 1);
         auto chunk = [&](int dc) -> float4 {           // 4 consecutive dims of block bb
-            if (g.pooled_f16) {
-                const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(v.pooled) +
-                                                                 (prow + bb) * HD + 4 * dc);
-                return make_float4(h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16)), h2f((uint16_t)w.y),
-                                   h2f((uint16_t)(w.y >> 16)));
-            }
             return *reinterpret_cast<const float4 *>(v.pooled + (prow + bb) * HD + 4 * dc);
         };
         // the block's largest element, then (a second, cache-hot read) its
@@ -2717,7 +2712,8 @@ static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *
                               const Ws &ws, hipStream_t st) {
     const int32_t n_blk = max_seq_len / g.bt;                   // whole blocks of the longest query
     if constexpr (pf_approx_fits<HD, G>()) {
-        if (!g.shared && g.topk > 0 && n_blk > g.sink && n_blk - g.sink <= kRefineBlocks) {
+        // fp32 pooled keys, per-KV-head selections, up to kRefineBlocks eligible blocks
+        if (!g.shared && !g.pooled_f16 && g.topk > 0 && n_blk > g.sink && n_blk - g.sink <= kRefineBlocks) {
             hipLaunchKernelGGL((k_pf_approx<HD, G>),
                                dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv), dim3(256),
                                0, st, g, v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm);

@@ -45,17 +45,18 @@ def kv_rows(rng, n: int, cfg, scaled: bool = True):
 FILL_CHUNK = 65536
 
 
-def fill(dev, host, rng, lengths, scaled: bool = True, pool: bool = True):
+def fill(dev, host, rng, lengths, scaled: bool = True, pool: bool = True, rows=None):
     """Append tokens [0, L_s) of every sequence s on both sides and pool every
     whole block.  Up to FILL_CHUNK tokens a sequence take one device call;
-    longer ones are drawn and appended FILL_CHUNK tokens at a time."""
+    longer ones are drawn and appended FILL_CHUNK tokens at a time.  `rows`
+    (rng, n, cfg) -> (k, v) replaces the default draw."""
     cfg = host.cfg
     for s, L in enumerate(lengths):
         if L <= 0:
             continue
         for t0 in range(0, L, FILL_CHUNK):
             n = min(FILL_CHUNK, L - t0)
-            k, v = kv_rows(rng, n, cfg, scaled)
+            k, v = rows(rng, n, cfg) if rows else kv_rows(rng, n, cfg, scaled)
             pos = np.arange(t0, t0 + n, dtype=np.int32)
             sid = np.full(n, s, dtype=np.int32)
             assert host.append(k, v, pos, sid) == 0

@@ -340,17 +340,18 @@ def test_decode_is_deterministic():
 
 # ---- prefill ------------------------------------------------------------------------
 
-def _prefill_case(cfg, pre, n_q, seed, q_batch=None, rows=True, dtype=np.float32, seq=1):
+def _prefill_case(cfg, pre, n_q, seed, q_batch=None, rows=True, dtype=np.float32, seq=1, kv=None):
     """A prefill chunk of sequence `seq` at positions pre .. pre+n_q-1 (the rows
     appended and the completed blocks pooled by the call when `rows`) against
     the oracle: cache bytes and pooled keys bit-exact, every query's selection
-    bit-exact, outputs within the attention tolerance."""
+    bit-exact, outputs within the attention tolerance.  `kv` (rng, n, cfg) ->
+    (k, v) draws the cache's and the chunk's rows instead of kv_rows."""
     rng = np.random.default_rng(seed)
     max_len = pre + n_q
     pps = max_len // cfg.page_tokens + 1
     dev, host = make_pair(cfg, 2, pps, seed=seed)
-    fill(dev, host, rng, [pre // 2, pre] if seq == 1 else [pre, pre // 2])
-    kn, vn = kv_rows(rng, n_q, cfg)
+    fill(dev, host, rng, [pre // 2, pre] if seq == 1 else [pre, pre // 2], rows=kv)
+    kn, vn = kv(rng, n_q, cfg) if kv else kv_rows(rng, n_q, cfg)
     kn, vn = kn.astype(dtype), vn.astype(dtype)
     q = rng.standard_normal((n_q, cfg.n_head, cfg.head_dim), dtype=np.float32)
     bt = cfg.block_tokens
@@ -412,6 +413,30 @@ def test_prefill_rows_already_in_place():
 def test_prefill_other_shapes():
     _prefill_case(TINY, 90, 70, seed=640)            # 4-token blocks: the general attention kernel
     _prefill_case(G12, 200, 40, seed=641)
+
+
+def _tied_keys(rng, n, cfg):
+    """Every key row the same vector (so every pooled key, and every block
+    score of a query, is the same); V ~ N(0,1)."""
+    k = np.broadcast_to(np.linspace(-1.0, 1.0, cfg.head_dim, dtype=np.float32),
+                        (n, cfg.n_head_kv, cfg.head_dim)).copy()
+    v = rng.standard_normal((n, cfg.n_head_kv, cfg.head_dim), dtype=np.float32)
+    return k, v
+
+
+def test_prefill_tied_scores_rank_by_index():
+    """All block scores equal: every eligible block is a candidate of the
+    bounded scoring, and the exact ranking takes the lowest indices -- below
+    the candidate cap (90 eligible blocks) and, past it (about 600), through
+    the exact-row fallback."""
+    _prefill_case(BASELINE, 6200, 24, seed=670, kv=_tied_keys)
+    _prefill_case(BASELINE, 39000, 12, seed=671, kv=_tied_keys)
+
+
+def test_prefill_relu_per_head_selection():
+    """relu'd head dots with per-KV-head selections (the matrix-core scoring's
+    relu path), at a context where most blocks are eligible."""
+    _prefill_case(Cfg(relu_per_head=1), 9000, 48, seed=672)
 
 
 def test_prefill_shared_selection():
