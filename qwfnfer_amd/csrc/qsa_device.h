@@ -237,6 +237,26 @@ __device__ __forceinline__ void q8x4_to_h2(uint32_t w, half2v &lo, half2v &hi) {
 }
 
 
+// Two weights times their V scales as exact fp16 pairs: hi = f16(p * dv), lo
+// = f16(p * dv - hi) (the fma's exact residual), packed two to a word (the
+// second weight's in the high halves).  Each dv is the low (SEL 0) or high
+// (SEL 1) half of its scale word; the mix instructions read the packed
+// halves in place (op_sel), four instructions for the two pairs.
+template <int SEL>
+__device__ __forceinline__ void p_split2(float p0, uint32_t d0, float p1, uint32_t d1, uint32_t &hi, uint32_t &lo) {
+    if constexpr (SEL == 0) {
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(hi) : "v"(p0), "v"(d0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,1,1]" : "=v"(lo) : "v"(p0), "v"(d0), "v"(hi));
+        asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "+v"(hi) : "v"(p1), "v"(d1));
+        asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,0,1] op_sel_hi:[0,1,1]" : "+v"(lo) : "v"(p1), "v"(d1), "v"(hi));
+    } else {
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(hi) : "v"(p0), "v"(d0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel:[0,1,0] op_sel_hi:[0,1,1]" : "=v"(lo) : "v"(p0), "v"(d0), "v"(hi));
+        asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(hi) : "v"(p1), "v"(d1));
+        asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,1,1] op_sel_hi:[0,1,1]" : "+v"(lo) : "v"(p1), "v"(d1), "v"(hi));
+    }
+}
+
 // Eight int8 quants -> eight exact fp16 values, in order.
 __device__ __forceinline__ h8v q8x8_to_h8(uint2 w) {
     half2v a, b, c, d;

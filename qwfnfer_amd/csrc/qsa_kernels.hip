@@ -3148,15 +3148,20 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                     for (int j = 0; j < NJ; ++j) {
-                        h8v bh, bl;
+                        // cell i's block-j scale: half i * NJ + j of the cells' scale row,
+                        // the low or high half of its word as j is even or odd
+                        u4v bhw, blw;
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const h8v dw = __builtin_bit_cast(h8v, dvw_pv[ks][(i * NJ + j) / 8]);
-                            const float dv = (float)dw[(i * NJ + j) % 8];
-                            const _Float16 hi = (_Float16)__builtin_fmaf(pcr[ks][i], dv, 0.0f);
-                            bh[i] = hi;
-                            bl[i] = (_Float16)__builtin_fmaf(pcr[ks][i], dv, -(float)hi);
+                        for (int m = 0; m < 4; ++m) {
+                            const int e0 = 2 * m * NJ + j, e1 = e0 + NJ;
+                            const uint32_t d0 = dvw_pv[ks][e0 / 8][e0 % 8 / 2], d1 = dvw_pv[ks][e1 / 8][e1 % 8 / 2];
+                            uint32_t hw, lw;
+                            if (j % 2 == 0) p_split2<0>(pcr[ks][2 * m], d0, pcr[ks][2 * m + 1], d1, hw, lw);
+                            else p_split2<1>(pcr[ks][2 * m], d0, pcr[ks][2 * m + 1], d1, hw, lw);
+                            bhw[m] = hw;
+                            blw[m] = lw;
                         }
+                        const h8v bh = __builtin_bit_cast(h8v, bhw), bl = __builtin_bit_cast(h8v, blw);
 #pragma unroll
                         for (int db = 0; db < 2; ++db) {
                             const int dblk = 2 * j + db;
