@@ -857,7 +857,9 @@ __device__ __forceinline__ void emit_forced(const Geo &g, const Ranges &r, int t
     if (tid == 0) out.count(g.sink + topk + nwin);
 }
 
-template <int NT, typename SH>
+// MAXSPAN: the most eligible blocks a caller passes (smaller register paths
+// only; a longer span takes the radix fallback).
+template <int NT, typename SH, int MAXSPAN = keys_max<NT>()>
 __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int L, const SelOut &out, SH &sh) {
     const int tid = threadIdx.x;
     const Ranges r = qsa_ranges(g, L);
@@ -877,8 +879,10 @@ __device__ __forceinline__ void select_blocks(const Geo &g, const float *sc, int
             else if (span <= 8 * NT) done = select_regs<NT, 8, true>(g, sc, r, topk, out, sh);
             else if (span <= 12 * NT) done = select_regs<NT, 12, true>(g, sc, r, topk, out, sh);
             else if (span <= 16 * NT) done = select_regs<NT, 16, true>(g, sc, r, topk, out, sh);
-            else if (span <= 24 * NT) done = select_regs<NT, 24, true>(g, sc, r, topk, out, sh);
-            else if (span <= keys_max<NT>()) done = select_regs<NT, keys_max<NT>() / NT, true>(g, sc, r, topk, out, sh);
+            else if constexpr (MAXSPAN > 16 * NT) {
+                if (span <= 24 * NT) done = select_regs<NT, 24, true>(g, sc, r, topk, out, sh);
+                else if (span <= keys_max<NT>()) done = select_regs<NT, keys_max<NT>() / NT, true>(g, sc, r, topk, out, sh);
+            }
         } else if constexpr (NT == 512) {
             if (span <= 4 * NT) done = select_regs<NT, 4, true>(g, sc, r, topk, out, sh);
             else if (span <= 8 * NT) done = select_regs<NT, 8, true>(g, sc, r, topk, out, sh);
@@ -2482,7 +2486,7 @@ struct RefineShared {
 // non-finite approximate score or bound, or more than kRefineMax candidates,
 // scores the whole row exactly for select_blocks instead.
 template <int HD, int G>
-__global__ void __launch_bounds__(kIdxThreads, 2)
+__global__ void __launch_bounds__(kIdxThreads, 3)
 k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, int32_t nb_cap,
             const float *__restrict__ pnorm, int32_t *sel, int32_t *nsel, int32_t max_sel) {
 #pragma clang fp contract(off)
@@ -2499,7 +2503,7 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
     const Ranges r = qsa_ranges(g, L);
     const int topk = eff_topk(g, r);
     if (g.topk <= 0 || r.e_hi - r.e_lo <= topk || topk == 0) {   // nothing ranked: no score is read
-        select_blocks<NT>(g, row, L, out, sh.s);
+        select_blocks<NT, RefineSel, kRefineBlocks>(g, row, L, out, sh.s);
         return;
     }
     const int64_t prow = ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps;
@@ -2621,7 +2625,7 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the exact row, for the selection's loads
         __syncthreads();
-        select_blocks<NT>(g, row, L, out, sh.s);
+        select_blocks<NT, RefineSel, kRefineBlocks>(g, row, L, out, sh.s);
         return;
     }
     // exact scores of the candidates, 128 at a time, two threads each: thread
