@@ -2494,7 +2494,7 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
     constexpr int NCH = HD / 16;                       // key chunks of one chain
     static_assert(pf_approx_fits<HD, G>() && KPT * NW <= kRefineBlocks / 64, "group table");
     __shared__ RefineShared<HD, G> sh;
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gh = blockIdx.x, s = blockIdx.y;
     const int pair = s * g.Hkv + gh;
     const int L = g.pf_pos0 + s + 1;
@@ -2596,7 +2596,7 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
             if (lane == 63) sh.s.ncand = incl;
         }
         __syncthreads();
-        nc = sh.s.ncand;
+        nc = __builtin_amdgcn_readfirstlane(sh.s.ncand);   // uniform: scalar loop bounds below
         if (nc <= kRefineMax) {
             const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
