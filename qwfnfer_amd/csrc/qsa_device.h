@@ -85,6 +85,7 @@ __device__ __forceinline__ int dppi(int old, int src) {
 }
 constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
 constexpr int kDppRowShr = 0x110, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+constexpr int kDppRowRor8 = 0x128;   // lane l of a 16-lane row takes lane l ^ 8's value
 
 __device__ __forceinline__ float lane63(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));

@@ -2914,17 +2914,27 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
     const int n = min(nsel[pair], max_sel);
     const int tpb = g.bt / 64;
     const int32_t *selp = sel + (int64_t)pair * max_sel;
-    // query head hn, dims 32j + 8lg .. +8, as fp16 hi + lo of q / qs
-    const float *qrow = q + ((int64_t)s * g.H + gh * G + (hv ? hn : 0)) * HD;
-    h8v qh[NJ], ql[NJ];
+    // PAIR (8 heads, head_dim >= 128): QK's 16 columns hold every head twice,
+    // columns h + 8 jp taking q8_0 blocks jj + jp NJ/2 -- so a lane's key
+    // scales are one half of a scale word -- and each lane keeps two of the
+    // four rows of an MFMA tile after the halves are added; the softmax then
+    // runs on 8 values a lane, not 16.  Else column hn is head hn (or zero).
+    constexpr bool PAIR = G == 8 && NJ % 4 == 0;
+    constexpr int NQ = PAIR ? NJ / 2 : NJ;           // query blocks a lane holds
+    constexpr int R = PAIR ? 2 : 4;                  // rows of each 16-cell tile a lane keeps
+    const int jp = PAIR ? hn >> 3 : 0;
+    // query head hn (PAIR: hn mod 8), dims 32 j + 8 lg .. +8 of its blocks, as fp16 hi + lo of q / qs
+    const float *qrow = q + ((int64_t)s * g.H + gh * G + (PAIR ? (hn & 7) : (hv ? hn : 0))) * HD;
+    h8v qh[NQ], ql[NQ];
     float qs;
     {
-        float x[NJ][8];
+        float x[NQ][8];
         float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg);
-            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * j + 8 * lg + 4);
+        for (int j = 0; j < NQ; ++j) {
+            const int blk = PAIR ? j + jp * (NJ / 2) : j;
+            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * blk + 8 * lg);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * blk + 8 * lg + 4);
             x[j][0] = x0.x; x[j][1] = x0.y; x[j][2] = x0.z; x[j][3] = x0.w;
             x[j][4] = x1.x; x[j][5] = x1.y; x[j][6] = x1.z; x[j][7] = x1.w;
 #pragma unroll
@@ -2932,19 +2942,32 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
         }
         amax = fmaxf(amax, __shfl_xor(amax, 16));
         amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if constexpr (PAIR) amax = fmaxf(amax, dppf<kDppRowRor8>(0.0f, amax));
         int ex = 0;
         frexpf(amax, &ex);
         qs = amax > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f;   // |q / qs| < 2^14
         const float qinv = 1.0f / qs;                        // a power of two: exact
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
+        for (int j = 0; j < NQ; ++j)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float y = hv ? x[j][i] * qinv : 0.0f;
+                const float y = PAIR || hv ? x[j][i] * qinv : 0.0f;
                 const _Float16 hi = (_Float16)y;
                 qh[j][i] = hi;
                 ql[j][i] = (_Float16)(y - (float)hi);
             }
+    }
+    // PAIR: the B operands of the two column halves (the other half zero)
+    h8v qb[PAIR ? 2 : 1][NQ][2];
+    if constexpr (PAIR) {
+        const h8v z = {};
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+            qb[0][j][0] = jp == 0 ? qh[j] : z;
+            qb[0][j][1] = jp == 0 ? ql[j] : z;
+            qb[1][j][0] = jp == 1 ? qh[j] : z;
+            qb[1][j][1] = jp == 1 ? ql[j] : z;
+        }
     }
     const float lscale = qs * g.scale_log2;          // > 0
     // the weights enter PV scaled by 2^kup, which brings the KV head's largest
@@ -3039,10 +3062,49 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 // cell c's NJ fp16 scales: halfs c*NJ .. c*NJ+NJ of the K (V) scale row
                 const u4v *wks = reinterpret_cast<const u4v *>(reinterpret_cast<const uint8_t *>(&W.buf[0]) + C::SOFF);
                 const u4v *wvs = wks + NS4;
-                // ---- QK
-                float sv[4][4];
+                // ---- QK: sv[mb][r] is cell 16 mb + 4 lg + (PAIR ? 2 jp : 0) + r
+                float sv[4][R];
+                auto cell_of = [&](int mb, int r) { return 16 * mb + 4 * lg + (PAIR ? 2 * jp : 0) + r; };
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb) {
+                    if constexpr (PAIR) {
+                        // the lane's blocks jj + jp NJ/2 of its cells 16mb+4lg+i: halves
+                        // jj % 2 of the scale words (cell) NJ/2 + jp NJ/4 + jj/2
+                        const uint32_t *wkw = reinterpret_cast<const uint32_t *>(wks);
+                        uint32_t dkw[4][NJ / 4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+#pragma unroll
+                            for (int w = 0; w < NJ / 4; ++w)
+                                dkw[i][w] = wkw[(16 * mb + 4 * lg + i) * (NJ / 2) + jp * (NJ / 4) + w];
+                        f4v c[NQ];
+#pragma unroll
+                        for (int jj = 0; jj < NQ; ++jj) {
+                            c[jj] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                            for (int side = 0; side < 2; ++side) {
+                                const int j = jj + side * (NJ / 2);
+                                const uint2 kw = *reinterpret_cast<const uint2 *>(
+                                    wk + ((2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
+                                const h8v kh = q8x8_to_h8(kw);
+                                c[jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qb[side][jj][0], c[jj], 0, 0, 0);
+                                c[jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qb[side][jj][1], c[jj], 0, 0, 0);
+                            }
+                        }
+                        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int jj = 0; jj < NQ; ++jj)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                acc[i] = __builtin_fmaf(
+                                    (float)__builtin_bit_cast(half2v, dkw[i][jj / 2])[jj % 2], c[jj][i], acc[i]);
+                        // add the column halves: lane jp keeps rows 2 jp, 2 jp + 1
+                        const float k0 = jp ? acc[2] : acc[0], k1 = jp ? acc[3] : acc[1];
+                        const float s0 = jp ? acc[0] : acc[2], s1 = jp ? acc[1] : acc[3];
+                        sv[mb][0] = k0 + dppf<kDppRowRor8>(0.0f, s0);
+                        sv[mb][1] = k1 + dppf<kDppRowRor8>(0.0f, s1);
+                        continue;
+                    }
                     h8v dk[NJ / 2];                  // cells 16mb+4lg .. +4, every block
 #pragma unroll
                     for (int w = 0; w < NJ / 2; ++w)
@@ -3053,8 +3115,8 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                         const uint2 kw = *reinterpret_cast<const uint2 *>(
                             wk + ((2 * j + (lg >> 1)) * 64 + 16 * mb + hn) * 16 + 8 * (lg & 1));
                         const h8v kh = q8x8_to_h8(kw);
-                        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], c[j], 0, 0, 0);
+                        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j % NQ], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j % NQ], c[j], 0, 0, 0);
                     }
                     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -3063,7 +3125,7 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                         for (int i = 0; i < 4; ++i)
                             acc[i] = __builtin_fmaf((float)dk[(i * NJ + j) / 8][(i * NJ + j) % 8], c[j][i], acc[i]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) sv[mb][i] = acc[i];   // log2 units after * lscale
+                    for (int i = 0; i < R; ++i) sv[mb][i] = acc[i];   // log2 units after * lscale
                 }
                 // V scales of this lane's PV cells 32ks+8lg .. +8, every block (NJ words per ks)
                 u4v dvw[2][NJ];
@@ -3078,8 +3140,8 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (16 * mb + 4 * lg + i >= nv) sv[mb][i] = -INFINITY;
+                        for (int i = 0; i < R; ++i)
+                            if (cell_of(mb, i) >= nv) sv[mb][i] = -INFINITY;
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -3088,27 +3150,38 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                             for (int e = 0; e < 4; ++e)  // a dword holds two blocks of one cell (NJ even)
                                 if (32 * ks + 8 * lg + (8 * w + 2 * e) / NJ >= nv) dvw[ks][w][e] = 0u;
                 }
-                // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32).
-                // Columns past the group's heads see q = 0: their weights are finite and unused.
+                // ---- online softmax (head hn; the four lanes of a column reduce by xor 16, 32,
+                // PAIR also with the other column half by xor 8).  Columns past the
+                // group's heads see q = 0: their weights are finite and unused.
                 float tm = -INFINITY;
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) tm = fmaxf(tm, sv[mb][i]);
-                tm = col_max4(tm) * lscale;          // lscale > 0: the max commutes
+                    for (int i = 0; i < R; ++i) tm = fmaxf(tm, sv[mb][i]);
+                tm = col_max4(tm);
+                if constexpr (PAIR) tm = fmaxf(tm, dppf<kDppRowRor8>(0.0f, tm));
+                tm *= lscale;                        // lscale > 0: the max commutes
                 const float m_new = fmaxf(m, tm);
                 const float alpha = __builtin_amdgcn_exp2f(m - m_new);
                 const float bias = kup - m_new;
                 float tsum = 0.0f;
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
+                for (int mb = 0; mb < 4; ++mb) {
+                    float pr[R];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[mb][i], lscale, bias));
-                        tsum += p;
-                        if (hv) W.p[hn][16 * mb + 4 * lg + i] = p;
+                    for (int i = 0; i < R; ++i) {
+                        pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[mb][i], lscale, bias));
+                        tsum += pr[i];
                     }
+                    if constexpr (PAIR) {
+                        *reinterpret_cast<float2 *>(&W.p[hn & 7][cell_of(mb, 0)]) = make_float2(pr[0], pr[1]);
+                    } else if (hv) {
+#pragma unroll
+                        for (int i = 0; i < R; ++i) W.p[hn][cell_of(mb, i)] = pr[i];
+                    }
+                }
                 tsum = col_sum4(tsum);
+                if constexpr (PAIR) tsum += dppf<kDppRowRor8>(0.0f, tsum);
                 lsum = lsum * alpha + tsum;
                 m = m_new;
                 if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {

@@ -433,6 +433,13 @@ def test_prefill_tied_scores_rank_by_index():
     _prefill_case(BASELINE, 39000, 12, seed=671, kv=_tied_keys)
 
 
+def test_prefill_head_dim_256_group_8():
+    """head_dim 256 with 8 query heads a KV head: the prefill attention's
+    paired-block QK with two scale words a cell (and the exact scoring path,
+    whose query fragments the matrix-core scoring cannot hold)."""
+    _prefill_case(Cfg(head_dim=256), 5000, 40, seed=673)
+
+
 def test_prefill_relu_per_head_selection():
     """relu'd head dots with per-KV-head selections (the matrix-core scoring's
     relu path), at a context where most blocks are eligible."""
