@@ -2484,9 +2484,11 @@ struct RefineShared {
 // are gathered in block order and scored exactly; the top-k of them by (score
 // desc, index asc) is the selection, emitted at its prefix-sum places.  A
 // non-finite approximate score or bound, or more than kRefineMax candidates,
-// scores the whole row exactly for select_blocks instead.
+// scores the whole row exactly for select_blocks instead.  Four waves a
+// SIMD (128 registers; the fallback's registers spill) ran the config-4
+// chunk faster than three or two.
 template <int HD, int G>
-__global__ void __launch_bounds__(kIdxThreads, 3)
+__global__ void __launch_bounds__(kIdxThreads, 4)
 k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, int32_t nb_cap,
             const float *__restrict__ pnorm, int32_t *sel, int32_t *nsel, int32_t max_sel) {
 #pragma clang fp contract(off)
