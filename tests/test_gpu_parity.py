@@ -433,6 +433,39 @@ def test_prefill_tied_scores_rank_by_index():
     _prefill_case(BASELINE, 39000, 12, seed=671, kv=_tied_keys)
 
 
+def _near_tied_keys(rng, n, cfg):
+    """Key rows one vector times (1 + 1e-4 noise): block scores differ in their
+    last few bits, so the bounded scoring rules out almost nothing."""
+    base = np.linspace(-1.0, 1.0, cfg.head_dim, dtype=np.float32)
+    k = base * (1.0 + 1e-4 * rng.standard_normal((n, cfg.n_head_kv, cfg.head_dim), dtype=np.float32))
+    v = rng.standard_normal((n, cfg.n_head_kv, cfg.head_dim), dtype=np.float32)
+    return k.astype(np.float32), v
+
+
+def _wide_range_keys(rng, n, cfg):
+    """K, V ~ N(0,1), each q8_0 block times a log-uniform scale in [1e-3, 1e3]."""
+    k = rng.standard_normal((n, cfg.n_head_kv, cfg.head_dim), dtype=np.float32)
+    v = rng.standard_normal((n, cfg.n_head_kv, cfg.head_dim), dtype=np.float32)
+    nb = cfg.head_dim // 32
+    for x in (k, v):
+        sc = np.exp(rng.uniform(np.log(1e-3), np.log(1e3), (n, cfg.n_head_kv, nb))).astype(np.float32)
+        x.reshape(n, cfg.n_head_kv, nb, 32)[...] *= sc[..., None]
+    return k, v
+
+
+def test_prefill_near_tied_scores():
+    """Block scores equal but for their last bits: every eligible block is a
+    candidate (below and past the candidate cap) and the exact scores decide."""
+    _prefill_case(BASELINE, 6200, 24, seed=674, kv=_near_tied_keys)
+    _prefill_case(BASELINE, 39000, 12, seed=675, kv=_near_tied_keys)
+
+
+def test_prefill_wide_dynamic_range():
+    """Keys over six decades of block scale: the bound's relative terms span the
+    same range and every selection stays exact."""
+    _prefill_case(BASELINE, 9000, 40, seed=676, kv=_wide_range_keys)
+
+
 def test_prefill_head_dim_256_group_8():
     """head_dim 256 with 8 query heads a KV head: the prefill attention's
     paired-block QK with two scale words a cell (and the exact scoring path,
