@@ -2242,6 +2242,7 @@ k_pf_select(Geo g, float *scores, int32_t nb_cap, int32_t *sel, int32_t *nsel, i
 constexpr int kPaQ = 64;              // queries per approximate-scoring workgroup (16 a wave)
 constexpr int kPaB = 64;              // pooled blocks per staged tile
 constexpr int kPaSplit = 2;           // workgroups sharing one query tile's blocks (measured best of 1, 2, 4, 8)
+constexpr int kPaSplitBig = 16;       // the same for one 40960-block row: 40 tiles a workgroup
 constexpr int kRefineMax = 512;       // candidates ranked exactly (more: the whole row exactly)
 constexpr int kRefineBlocks = 4096;   // eligible blocks the approximate path takes
 // |approximate - exact| <= kPaRel * (sum over the group's heads of |q_h|) * |p|
@@ -2266,15 +2267,45 @@ __device__ __forceinline__ int fp16_shift(float m) {
     return m > 0.0f ? 15 - e : 0;
 }
 
+// Chunk dc of pooled block b as fp32 (fp16 keys widened exactly).
+__device__ __forceinline__ float4 pooled_chunk(const Geo &g, const qwfn_kv_view &v, int64_t off) {
+    if (g.pooled_f16) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(v.pooled) + off);
+        return make_float4(h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16)), h2f((uint16_t)w.y),
+                           h2f((uint16_t)(w.y >> 16)));
+    }
+    return *reinterpret_cast<const float4 *>(v.pooled + off);
+}
+
+// N chunks of the pooled keys as fp32, chunk i at element offset off(i):
+// the format test taken once, every load issued before any is used (a test
+// per load leaves one memory round trip per chunk).
+template <int N, typename F>
+__device__ __forceinline__ void pooled_chunks(const Geo &g, const qwfn_kv_view &v, F off, float4 (&x)[N]) {
+    if (g.pooled_f16) {
+        const uint16_t *p = reinterpret_cast<const uint16_t *>(v.pooled);
+        uint2 w[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = *reinterpret_cast<const uint2 *>(p + off(i));
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            x[i] = make_float4(h2f((uint16_t)w[i].x), h2f((uint16_t)(w[i].x >> 16)), h2f((uint16_t)w[i].y),
+                               h2f((uint16_t)(w[i].y >> 16)));
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = *reinterpret_cast<const float4 *>(v.pooled + off(i));
+    }
+}
+
 template <int HD>
 struct PaShared {
     uint2 p[kPaB][HD / 4 + 2];            // the tile's pooled keys as fp16, each block scaled; rows + 16 bytes
     int pe[kPaB];                         // the blocks' scale exponents
 };
 
-// grid (ceil(n_q / 64), kPaSplit, Hkv), 256 threads.  Approximate scores of
+// grid (ceil(n_q / 64), split, Hkv), 256 threads.  Approximate scores of
 // 64 queries against the eligible blocks [sink, n_blk) of KV head gh (tiles
-// blockIdx.y, blockIdx.y + kPaSplit, ... of 64 blocks): S[query][block] = sum
+// blockIdx.y, blockIdx.y + split, ... of 64 blocks): S[query][block] = sum
 // over the group's heads of (relu'd when set) q_h . p on
 // v_mfma_f32_16x16x32_f16.  The A operand, the query scaled by a power of two
 // (its largest element over the group's heads in [2^14, 2^15)), stays in
@@ -2282,7 +2313,7 @@ struct PaShared {
 // same way, is staged in LDS as the B operand.  Wave w owns queries 16w ..
 // 16w+15; a lane's outputs are 4 queries x 1 block, scaled back exactly.  The
 // query-tile-0 workgroups also write each block's |p| (rounded up) to pnorm.
-// Pooled keys are fp32 (the checkpoint indexer's fp16 pool scores exactly).
+// Pooled keys are fp32, or fp16 (the checkpoint indexer's pool) widened exactly.
 template <int HD, int G>
 __global__ void __launch_bounds__(256, 2)
 k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int32_t n_blk,
@@ -2327,28 +2358,33 @@ k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
     const int n_tiles = (n_blk - g.sink + kPaB - 1) / kPaB;
     const int64_t prow = ((int64_t)g.pf_seq * g.Hkv + gh) * g.bps;   // the row's first pooled block
     const int sb = tid >> 2, sc = tid & 3;             // staging: block sb of the tile, chunks sc + 4 i
-    for (int t = (int)blockIdx.y; t < n_tiles; t += kPaSplit) {
+    for (int t = (int)blockIdx.y; t < n_tiles; t += (int)gridDim.y) {
         const int b0 = g.sink + t * kPaB;
         const int bb = min(b0 + sb, n_blk - 1);
-        auto chunk = [&](int dc) -> float4 {           // 4 consecutive dims of block bb
-            return *reinterpret_cast<const float4 *>(v.pooled + (prow + bb) * HD + 4 * dc);
-        };
+        // chunks sc + 4 i of block bb: 4 consecutive dims each
+        const auto chunk_off = [&](int i) -> int64_t { return (prow + bb) * HD + 4 * (sc + 4 * i); };
         // the block's largest element, then (a second, cache-hot read) its
         // scaled fp16 values and squares
         float m = 0.0f;
+        {
+            float4 xs[CPT];
+            pooled_chunks<CPT>(g, v, chunk_off, xs);
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const float4 x = chunk(sc + 4 * i);
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+            for (int i = 0; i < CPT; ++i) {
+                const float4 x = xs[i];
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+            }
         }
         m = fmaxf(m, __shfl_xor(m, 1));
         m = fmaxf(m, __shfl_xor(m, 2));
         const int pe = fp16_shift(m);
         __syncthreads();                               // the previous tile's fragments are read
         float ss = 0.0f;
+        float4 xs[CPT];
+        pooled_chunks<CPT>(g, v, chunk_off, xs);
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-            const float4 x = chunk(sc + 4 * i);
+            const float4 x = xs[i];
             const float y0 = ldexpf(x.x, pe), y1 = ldexpf(x.y, pe), y2 = ldexpf(x.z, pe), y3 = ldexpf(x.w, pe);
             ss = __builtin_fmaf(y0, y0, ss);
             ss = __builtin_fmaf(y1, y1, ss);
@@ -2439,15 +2475,6 @@ __device__ __forceinline__ void pf_exact_dots(const Geo &g, PC pchunk, const flo
     }
 }
 
-// Chunk dc of pooled block b as fp32 (fp16 keys widened exactly).
-__device__ __forceinline__ float4 pooled_chunk(const Geo &g, const qwfn_kv_view &v, int64_t off) {
-    if (g.pooled_f16) {
-        const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(v.pooled) + off);
-        return make_float4(h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16)), h2f((uint16_t)w.y),
-                           h2f((uint16_t)(w.y >> 16)));
-    }
-    return *reinterpret_cast<const float4 *>(v.pooled + off);
-}
 
 // LDS of the 256-thread selection (select_blocks: register path, radix
 // fallback) without the indexer's scoring and pooling stage.
@@ -2637,12 +2664,10 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
     for (int c0 = 0; c0 < nc; c0 += NT / 2) {
         const int ci = c0 + (tid >> 1), half = tid & 1;
         const int b = sh.cblk[min(ci, nc - 1)];
-        float4 pk[2][NCH];
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-#pragma unroll
-            for (int d16 = 0; d16 < NCH; ++d16)
-                pk[k][d16] = pooled_chunk(g, v, (prow + b) * HD + 4 * (4 * d16 + 2 * half + k));
+        float4 pk[2 * NCH];                            // chunk 4 d16 + 2 half + k at pk[k NCH + d16]
+        pooled_chunks<2 * NCH>(g, v, [&](int i) -> int64_t {
+            return (prow + b) * HD + 4 * (4 * (i % NCH) + 2 * half + i / NCH);
+        }, pk);
         float score = 0.0f;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -2653,10 +2678,10 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
 #pragma unroll
                 for (int d16 = 0; d16 < NCH; ++d16) {
                     const float4 q4 = *reinterpret_cast<const float4 *>(qs + h * QS + 4 * (4 * d16 + 2 * half + k));
-                    x = fmaf(q4.x, pk[k][d16].x, x);
-                    x = fmaf(q4.y, pk[k][d16].y, x);
-                    x = fmaf(q4.z, pk[k][d16].z, x);
-                    x = fmaf(q4.w, pk[k][d16].w, x);
+                    x = fmaf(q4.x, pk[k * NCH + d16].x, x);
+                    x = fmaf(q4.y, pk[k * NCH + d16].y, x);
+                    x = fmaf(q4.z, pk[k * NCH + d16].z, x);
+                    x = fmaf(q4.w, pk[k * NCH + d16].w, x);
                 }
                 cc[k] = x;
             }
@@ -2712,14 +2737,275 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
     emit_forced<NT>(g, r, topk, out);
 }
 
+// The same refinement for one score row of up to kRbBlocks eligible blocks
+// (a single KV head, or a selection shared by every KV head through one
+// scoring head group: the checkpoint indexer's 4-token blocks): one
+// 1024-thread workgroup per query, thread t holding blocks e_lo + t + 1024 i,
+// i < kRbKpt, up to kRbMax candidates; the LDS of k_select_big, whose
+// candidate arrays hold the candidates and whose selection is the fallback.
+constexpr int kRbThreads = kBigSelThreads, kRbKpt = 40, kRbBlocks = kRbThreads * kRbKpt, kRbMax = 2048;
+static_assert(kRbMax <= kSelCandMax, "the candidates fit BigSelShared's arrays");
+
+template <int HD, int G>
+struct RefineBigShared {
+    BigSelShared s;                               // histogram, reductions; ckey / cblk: the candidates
+    float q[G * (HD + 4)];                        // the group's query rows, padded
+    int32_t cbase[kRbKpt * (kRbThreads / 64)];    // candidates before each (thread row, wave) group
+    int32_t rk[kRbMax];                           // the ranks of the threshold bin's candidates
+    int32_t mem[kRbMax];                          // the threshold bin's candidates
+    float qn[G];
+};
+
+// grid (1, n_q), kRbThreads: query s's selection (g.Hkv == 1; with a shared
+// selection every KV head's row) from k_pf_approx's scores, by the bound and
+// candidate argument of k_pf_refine.
+template <int HD, int G>
+__global__ void __launch_bounds__(kRbThreads)
+k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, int32_t nb_cap,
+                const float *__restrict__ pnorm, int32_t *sel, int32_t *nsel, int32_t max_sel) {
+#pragma clang fp contract(off)
+    constexpr int NT = kRbThreads, QS = HD + 4, KPT = kRbKpt, NW = NT / 64, NCH = HD / 16;
+    constexpr int NG = KPT * NW;                       // (thread row, wave) groups
+    static_assert(pf_approx_fits<HD, G>() && G * HD / 4 <= NT && G <= NW && NG <= NT, "shapes");
+    __shared__ RefineBigShared<HD, G> sh;
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = blockIdx.y;
+    const int L = g.pf_pos0 + s + 1;
+    const SelOut out = sel_out(g, sel, nsel, max_sel, s, s);
+    float *row = scores + (int64_t)s * nb_cap;
+    const Ranges r = qsa_ranges(g, L);
+    const int topk = eff_topk(g, r);
+    if (g.topk <= 0 || r.e_hi - r.e_lo <= topk || topk == 0) {   // nothing ranked: no score is read
+        select_blocks<NT>(g, row, L, out, sh.s);
+        return;
+    }
+    const int64_t prow = (int64_t)g.pf_seq * g.bps;
+    float av[KPT], pv[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int b = min(r.e_lo + tid + NT * i, r.e_hi - 1);
+        av[i] = row[b];
+        pv[i] = pnorm[b];
+    }
+    float *qs = sh.q;
+    const float *qrow = q + (int64_t)s * g.H * HD;
+    if (tid < G * HD / 4) {
+        const int h = tid / (HD / 4), c = tid % (HD / 4);
+        *reinterpret_cast<float4 *>(qs + h * QS + 4 * c) = *reinterpret_cast<const float4 *>(qrow + h * HD + 4 * c);
+    }
+    __syncthreads();
+    if (wid < G) {                                     // |q_h| (rounded up), one wave a head
+        float m = 0.0f;
+        for (int d = lane; d < HD; d += 64) m = fmaxf(m, fabsf(qs[wid * QS + d]));
+        const int e = fp16_shift(wave_max(m));
+        float ss = 0.0f;
+        for (int d = lane; d < HD; d += 64) {
+            const float y = ldexpf(qs[wid * QS + d], e);
+            ss = __builtin_fmaf(y, y, ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) sh.qn[wid] = ldexpf(sqrtf(ss) * (1.0f + 0x1p-14f), -e);
+    }
+    __syncthreads();
+    float qn = 0.0f;
+#pragma unroll
+    for (int h = 0; h < G; ++h) qn += sh.qn[h];
+    const float ec = kPaRel * qn * (1.0f + 0x1p-14f);
+    // bounds, in place: av becomes the lower, pv the upper bound
+    bool bad = !(ec < INFINITY);
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const bool in = r.e_lo + tid + NT * i < r.e_hi;
+        const float e = __builtin_fmaf(ec, pv[i], kPaAbs);
+        bad |= in && (!(fabsf(av[i]) < INFINITY) || !(e < INFINITY));
+        const float a = av[i];
+        av[i] = in ? a - e : -INFINITY;
+        pv[i] = in ? a + e : -INFINITY;
+        lo = fminf(lo, in ? av[i] : INFINITY);
+        hi = fmaxf(hi, av[i]);
+    }
+    hi = wave_max(hi);
+    lo = -wave_max(-lo);
+    if (lane == 0) { sh.s.red[wid] = hi; sh.s.red[NW + wid] = lo; }
+    reinterpret_cast<uint4 *>(sh.s.hist)[tid] = make_uint4(0u, 0u, 0u, 0u);   // 4096 bins, 4 a thread
+    if (tid < 64) sh.s.hist[4096 + tid] = 0u;
+    bad = __syncthreads_or(bad);
+    int nc = 0;
+    if (!bad) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) { hi = fmaxf(hi, sh.s.red[i]); lo = fminf(lo, sh.s.red[NW + i]); }
+        const float span = hi - lo, scale = 4096.0f / span;
+        const bool lin = hi > lo && span < INFINITY && scale < INFINITY;
+        auto bin_of = [&](float x) -> uint32_t {
+            return lin ? (uint32_t)fminf(fmaxf((x - lo) * scale, 0.0f), 4095.0f) : score_key(x) >> 20;
+        };
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool in = r.e_lo + tid + NT * i < r.e_hi;
+            atomicAdd(&sh.s.hist[in ? bin_of(av[i]) : 4096u + (uint32_t)lane], 1u);
+        }
+        __syncthreads();
+        if (wid == 0) hist_cut(sh.s, topk);
+        __syncthreads();
+        const uint32_t B = (uint32_t)sh.s.bin;
+        uint64_t cm = 0;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool c = r.e_lo + tid + NT * i < r.e_hi && bin_of(pv[i]) >= B;
+            cm |= (uint64_t)c << i;
+            const uint64_t m = __ballot(c);
+            if (lane == 0) sh.cbase[i * NW + wid] = (int)__builtin_popcountll(m);
+        }
+        __syncthreads();
+        {                                              // exclusive scan of the group counts
+            const int x = tid < NG ? sh.cbase[tid] : 0;
+            int tot;
+            const int ex = block_excl_sum<NT>(x, sh.s.tmp, &tot);
+            if (tid < NG) sh.cbase[tid] = ex;
+            if (tid == 0) sh.s.ncand = tot;
+        }
+        __syncthreads();
+        nc = __builtin_amdgcn_readfirstlane(sh.s.ncand);
+        if (nc <= kRbMax) {
+            const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                const bool c = (cm >> i) & 1u;
+                const uint64_t m = __ballot(c);
+                if (c) sh.s.cblk[sh.cbase[i * NW + wid] + (int)__builtin_popcountll(m & below)] = r.e_lo + tid + NT * i;
+            }
+        }
+        for (int i = tid; i < kRbMax; i += NT) sh.rk[i] = 0;
+        __syncthreads();
+    }
+    if (bad || nc > kRbMax) {
+        // the whole row exactly (k_pf_scores' values), then the plain selection
+        for (int b = r.e_lo + tid; b < r.e_hi; b += NT) {
+            float sc = 0.0f;
+            float d[G];
+            pf_exact_dots<HD, G>(g, [&](int dc) { return pooled_chunk(g, v, (prow + b) * HD + 4 * dc); }, qs, QS, 0, d);
+#pragma unroll
+            for (int h = 0; h < G; ++h) sc = h == 0 ? d[h] : sc + d[h];
+            row[b] = sc;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the exact row, for the selection's loads
+        __syncthreads();
+        select_blocks<NT>(g, row, L, out, sh.s);
+        return;
+    }
+    // exact scores of the candidates, NT / 2 at a time, two threads each (as k_pf_refine)
+    for (int c0 = 0; c0 < nc; c0 += NT / 2) {
+        const int ci = c0 + (tid >> 1), half = tid & 1;
+        const int b = sh.s.cblk[min(ci, nc - 1)];
+        float4 pk[2 * NCH];                            // chunk 4 d16 + 2 half + k at pk[k NCH + d16]
+        pooled_chunks<2 * NCH>(g, v, [&](int i) -> int64_t {
+            return (prow + b) * HD + 4 * (4 * (i % NCH) + 2 * half + i / NCH);
+        }, pk);
+        float score = 0.0f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float cc[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float x = 0.0f;
+#pragma unroll
+                for (int d16 = 0; d16 < NCH; ++d16) {
+                    const float4 q4 = *reinterpret_cast<const float4 *>(qs + h * QS + 4 * (4 * d16 + 2 * half + k));
+                    x = fmaf(q4.x, pk[k * NCH + d16].x, x);
+                    x = fmaf(q4.y, pk[k * NCH + d16].y, x);
+                    x = fmaf(q4.z, pk[k * NCH + d16].z, x);
+                    x = fmaf(q4.w, pk[k * NCH + d16].w, x);
+                }
+                cc[k] = x;
+            }
+            const float pair_sum = cc[0] + cc[1];
+            float dot = pair_sum + __shfl_xor(pair_sum, 1);
+            if (g.relu) dot = dot > 0.0f ? dot : 0.0f;
+            score = h == 0 ? dot : score + dot;
+        }
+        if (half == 0 && ci < nc) sh.s.ckey[ci] = score_key(score);
+    }
+    __syncthreads();
+    // The topk-th largest exact score lies among the candidates (every other
+    // block scores below it): the bin of its top 12 key bits over the
+    // candidates, then that bin's candidates ranked by (key desc, index asc).
+    for (int i = tid; i < 4096 + 64; i += NT) sh.s.hist[i] = 0u;
+    if (tid == 0) sh.s.ctot = 0;
+    __syncthreads();
+    for (int i = tid; i < nc; i += NT) atomicAdd(&sh.s.hist[sh.s.ckey[i] >> 20], 1u);
+    __syncthreads();
+    if (wid == 0) hist_cut(sh.s, topk);
+    __syncthreads();
+    const uint32_t B1 = (uint32_t)sh.s.bin;
+    const int need = sh.s.need;
+    for (int i = tid; i < nc; i += NT)
+        if (sh.s.ckey[i] >> 20 == B1) sh.mem[atomicAdd(&sh.s.ctot, 1)] = i;
+    __syncthreads();
+    const int nm = __builtin_amdgcn_readfirstlane(sh.s.ctot);
+    // members j0 .. j0+63 one a lane in every wave; each wave counts the larger
+    // composite keys (key, ~block) among 64 / NW of every 64 members
+    auto order_key = [&](int j) -> uint64_t {
+        if (j >= nm) return 0ull;
+        const int i = sh.mem[j];
+        return ((uint64_t)sh.s.ckey[i] << 32) | (uint32_t)~sh.s.cblk[i];
+    };
+    constexpr int KW = 64 / NW;
+    for (int i0 = 0; i0 < nm; i0 += 64) {
+        const uint64_t ci = order_key(i0 + lane);
+        int part = 0;
+        for (int j0 = 0; j0 < nm; j0 += 64) {
+            const uint64_t cj = order_key(j0 + lane);
+            const uint32_t jh = (uint32_t)(cj >> 32), jl = (uint32_t)cj;
+            const int k_end = min(min(64, nm - j0), KW * wid + KW);
+            for (int k = KW * wid; k < k_end; ++k) {
+                const uint64_t ck = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(jh, k) << 32) |
+                                    (uint32_t)__builtin_amdgcn_readlane(jl, k);
+                part += ck > ci;
+            }
+        }
+        if (i0 + lane < nm) atomicAdd(&sh.rk[sh.mem[i0 + lane]], part);
+    }
+    __syncthreads();
+    {
+        constexpr int PER = kRbMax / NT;               // candidates a thread, consecutive
+        auto taken = [&](int i) {
+            const uint32_t bn = sh.s.ckey[i] >> 20;
+            return i < nc && (bn > B1 || (bn == B1 && sh.rk[i] < need));
+        };
+        int cnt = 0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) cnt += taken(PER * tid + k);
+        int tot;
+        int pos = block_excl_sum<NT>(cnt, sh.s.tmp, &tot);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = PER * tid + k;
+            if (taken(i)) out.put(g.sink + pos++, sh.s.cblk[i]);
+        }
+    }
+    emit_forced<NT>(g, r, topk, out);
+}
+
 template <int HD, int G>
 static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                               int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                               const Ws &ws, hipStream_t st) {
     const int32_t n_blk = max_seq_len / g.bt;                   // whole blocks of the longest query
     if constexpr (pf_approx_fits<HD, G>()) {
-        // fp32 pooled keys, per-KV-head selections, up to kRefineBlocks eligible blocks
-        if (!g.shared && !g.pooled_f16 && g.topk > 0 && n_blk > g.sink && n_blk - g.sink <= kRefineBlocks) {
+        // one score row (a single KV head, or one shared by every KV head) of up
+        // to kRbBlocks eligible blocks: the 1024-thread refinement
+        if (g.Hkv == 1 && g.topk > 0 && n_blk > g.sink && n_blk - g.sink > kRefineBlocks &&
+            n_blk - g.sink <= kRbBlocks) {
+            hipLaunchKernelGGL((k_pf_approx<HD, G>),
+                               dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplitBig, 1u), dim3(256), 0, st, g,
+                               v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm);
+            hipLaunchKernelGGL((k_pf_refine_big<HD, G>), dim3(1u, (unsigned)n_q), dim3(kRbThreads), 0, st, g, v, q,
+                               ws.scores, ws.nb_cap, ws.pnorm, sel, nsel, max_sel);
+            return;
+        }
+        // per-KV-head selections (or one KV head's row shared), up to kRefineBlocks eligible blocks
+        if ((!g.shared || g.Hkv == 1) && g.topk > 0 && n_blk > g.sink && n_blk - g.sink <= kRefineBlocks) {
             hipLaunchKernelGGL((k_pf_approx<HD, G>),
                                dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv), dim3(256),
                                0, st, g, v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm);
