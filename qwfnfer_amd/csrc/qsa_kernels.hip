@@ -2297,6 +2297,68 @@ __device__ __forceinline__ void pooled_chunks(const Geo &g, const qwfn_kv_view &
     }
 }
 
+// The G query rows at qg (head h at qg + h HD) spread over the wave: lane l
+// holds dims l + 64 t of every head, to be broadcast one value at a time.
+template <int HD, int G>
+struct PfQLanes {
+    float x[G][HD / 64];
+};
+template <int HD, int G>
+__device__ __forceinline__ PfQLanes<HD, G> pf_q_lanes(const float *qg) {
+    const int lane = threadIdx.x & 63;
+    PfQLanes<HD, G> r;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int t = 0; t < HD / 64; ++t) r.x[h][t] = qg[h * HD + 64 * t + lane];
+    return r;
+}
+
+// The exact score of the pooled block at element offset koff for those query
+// rows, one lane a block, in k_pf_scores' order: per head four fmaf chains,
+// chain j over the dims of the chunks 4 d16 + j, combined (c0 + c1) + (c2 +
+// c3), relu'd when set, the heads summed in order.  Each query value is read
+// out of its lane (v_readlane with a constant lane; every lane must be
+// active, its value defined): the same values as broadcast LDS reads, two
+// addresses a wave, measured ten times slower.
+template <int HD, int G>
+__device__ __forceinline__ float pf_exact_score(const Geo &g, const qwfn_kv_view &v, int64_t koff,
+                                                const PfQLanes<HD, G> &ql) {
+#pragma clang fp contract(off)
+    constexpr int NCH = HD / 16;
+    float c[G][4];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[h][j] = 0.0f;
+    auto qv = [&](int h, int d) -> float {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ql.x[h][d / 64]), d % 64));
+    };
+#pragma unroll
+    for (int d16 = 0; d16 < NCH; ++d16) {
+        float4 k4[4];
+        pooled_chunks<4>(g, v, [&](int j) -> int64_t { return koff + 16 * d16 + 4 * j; }, k4);
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = 16 * d16 + 4 * j;
+                c[h][j] = fmaf(qv(h, d + 0), k4[j].x, c[h][j]);
+                c[h][j] = fmaf(qv(h, d + 1), k4[j].y, c[h][j]);
+                c[h][j] = fmaf(qv(h, d + 2), k4[j].z, c[h][j]);
+                c[h][j] = fmaf(qv(h, d + 3), k4[j].w, c[h][j]);
+            }
+    }
+    float score = 0.0f;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float dot = (c[h][0] + c[h][1]) + (c[h][2] + c[h][3]);
+        if (g.relu) dot = dot > 0.0f ? dot : 0.0f;
+        score = h == 0 ? dot : score + dot;
+    }
+    return score;
+}
+
 template <int HD>
 struct PaShared {
     uint2 p[kPaB][HD / 4 + 2];            // the tile's pooled keys as fp16, each block scaled; rows + 16 bytes
@@ -2894,37 +2956,14 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
         select_blocks<NT>(g, row, L, out, sh.s);
         return;
     }
-    // exact scores of the candidates, NT / 2 at a time, two threads each (as k_pf_refine)
-    for (int c0 = 0; c0 < nc; c0 += NT / 2) {
-        const int ci = c0 + (tid >> 1), half = tid & 1;
-        const int b = sh.s.cblk[min(ci, nc - 1)];
-        float4 pk[2 * NCH];                            // chunk 4 d16 + 2 half + k at pk[k NCH + d16]
-        pooled_chunks<2 * NCH>(g, v, [&](int i) -> int64_t {
-            return (prow + b) * HD + 4 * (4 * (i % NCH) + 2 * half + i / NCH);
-        }, pk);
-        float score = 0.0f;
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float cc[2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                float x = 0.0f;
-#pragma unroll
-                for (int d16 = 0; d16 < NCH; ++d16) {
-                    const float4 q4 = *reinterpret_cast<const float4 *>(qs + h * QS + 4 * (4 * d16 + 2 * half + k));
-                    x = fmaf(q4.x, pk[k * NCH + d16].x, x);
-                    x = fmaf(q4.y, pk[k * NCH + d16].y, x);
-                    x = fmaf(q4.z, pk[k * NCH + d16].z, x);
-                    x = fmaf(q4.w, pk[k * NCH + d16].w, x);
-                }
-                cc[k] = x;
-            }
-            const float pair_sum = cc[0] + cc[1];
-            float dot = pair_sum + __shfl_xor(pair_sum, 1);
-            if (g.relu) dot = dot > 0.0f ? dot : 0.0f;
-            score = h == 0 ? dot : score + dot;
-        }
-        if (half == 0 && ci < nc) sh.s.ckey[ci] = score_key(score);
+    // exact scores of the candidates, one a lane
+    // (whole waves, every lane active: the query values are read out of lanes)
+    const PfQLanes<HD, G> ql = pf_q_lanes<HD, G>(qrow);
+    for (int c0 = 0; c0 < nc; c0 += NT) {
+        if (c0 + 64 * wid >= nc) continue;             // wave-uniform
+        const int ci = min(c0 + tid, nc - 1);
+        const float sc = pf_exact_score<HD, G>(g, v, (prow + sh.s.cblk[ci]) * HD, ql);
+        if (c0 + tid < nc) sh.s.ckey[ci] = score_key(sc);
     }
     __syncthreads();
     // The topk-th largest exact score lies among the candidates (every other
