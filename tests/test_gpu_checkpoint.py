@@ -315,23 +315,26 @@ def test_per_head_selection_long_context():
     assert qsa.read_status(dev) == 0
 
 
-def test_checkpoint_prefill_long_context():
-    """Prefill queries at positions past 32,768 (over 8192 eligible blocks each):
-    the per-query selections come from k_select_big in prefill mode."""
+def _long_prefill(seed, raw_keys=None):
+    """A 37-query chunk appended at 36,001 (over 9,000 eligible 4-token blocks
+    a query): selections bit for bit against the oracle's on the pooled keys
+    the device built, every ninth query's attention within tolerance.
+    raw_keys(rng, n, t0) gives the indexer's raw keys of tokens t0 .. t0+n-1."""
     cfg = CKPT
-    rng = np.random.default_rng(870)
+    rng = np.random.default_rng(seed)
     pre, n_q = 36001, 37
     end = pre + n_q
     pps = end // cfg.page_tokens + 1
-    dev, host, ic, w = _pair(cfg, 1, pps, seed=871)
-    kr0 = rng.standard_normal((pre, 128)).astype(np.float32)
+    dev, host, ic, w = _pair(cfg, 1, pps, seed=seed + 1)
+    raw = raw_keys or (lambda r, n, t0: r.standard_normal((n, 128)).astype(np.float32))
+    kr0 = raw(rng, pre, 0)
     qsa.idx_append_pool(ic, torch.from_numpy(kr0).cuda(), torch.arange(pre, dtype=torch.int32, device="cuda"))
     k, v = kv_rows(rng, pre, cfg)
     host.append(k, v, np.arange(pre, dtype=np.int32))
     qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
                     torch.arange(pre, dtype=torch.int32, device="cuda"))
     kn, vn = kv_rows(rng, n_q, cfg)
-    krn = rng.standard_normal((n_q, 128)).astype(np.float32)
+    krn = raw(rng, n_q, pre)
     q = rng.standard_normal((n_q, 24, 256)).astype(np.float32)
     qi = rng.standard_normal((n_q, 4, 128)).astype(np.float32)
     c = cfg_of(cfg)
@@ -355,3 +358,43 @@ def test_checkpoint_prefill_long_context():
         if i % 9 == 0:
             ref = host.attention_f64(q[i:i + 1], [pre + i + 1], gs[i:i + 1], gn[i:i + 1])
             assert_close_attn(o[i:i + 1], ref, f"query {i}")
+    return pooled
+
+
+def test_checkpoint_prefill_long_context():
+    """Prefill queries at positions past 32,768 (over 8192 eligible blocks
+    each): the bounded scoring and the 1024-thread refinement of one shared row."""
+    _long_prefill(870)
+
+
+def _class_keys(classes):
+    """Raw indexer keys whose pooled blocks take one of a few values: the
+    rotated dims zero (so the position does not enter), the rest the block's
+    class vector; classes[b] is block b's class (4-token blocks)."""
+    vecs = np.random.default_rng(77).standard_normal((int(classes.max()) + 1, 128)).astype(np.float32)
+    vecs[:, :64] = 0.0
+
+    def raw(rng, n, t0):
+        b = (np.arange(t0, t0 + n) // 4).clip(max=len(classes) - 1)
+        return vecs[classes[b]].copy()
+    return raw
+
+
+def test_checkpoint_prefill_long_context_all_keys_equal():
+    """Every pooled block the same: every score ties, far more candidates than
+    the refinement holds, so it scores the whole row exactly and selects the
+    lowest-indexed blocks."""
+    pooled = _long_prefill(880, _class_keys(np.zeros(9100, dtype=np.int64)))
+    assert (pooled[1:9000] == pooled[0]).all()
+
+
+def test_checkpoint_prefill_long_context_three_key_values():
+    """Pooled blocks of three values (300, 400 and the rest of the blocks):
+    whole classes tie, so the selection's threshold falls inside a class of
+    equal scores and its blocks are taken by index, with the refinement's own
+    candidates where the two small classes lead, the exact row where not."""
+    cls = np.full(9100, 2, dtype=np.int64)
+    perm = np.random.default_rng(78).permutation(9000)
+    cls[perm[:300]] = 0
+    cls[perm[300:700]] = 1
+    _long_prefill(890, _class_keys(cls))
