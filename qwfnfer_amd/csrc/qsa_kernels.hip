@@ -2632,7 +2632,7 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
     for (int h = 0; h < G; ++h) qn += sh.qn[h];
     const float ec = kPaRel * qn * (1.0f + 0x1p-14f);
     float lb[KPT], ub[KPT];
-    bool bad = !(ec < INFINITY);
+    bool bad = !(ec < INFINITY) || r.e_hi - r.e_lo > KPT * NT;   // (the launch keeps rows within KPT * NT)
     float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
@@ -2874,7 +2874,7 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
     for (int h = 0; h < G; ++h) qn += sh.qn[h];
     const float ec = kPaRel * qn * (1.0f + 0x1p-14f);
     // bounds, in place: av becomes the lower, pv the upper bound
-    bool bad = !(ec < INFINITY);
+    bool bad = !(ec < INFINITY) || r.e_hi - r.e_lo > KPT * NT;   // (the launch keeps rows within KPT * NT)
     float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
