@@ -2802,8 +2802,10 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
 // The same refinement for one score row of up to kRbBlocks eligible blocks
 // (a single KV head, or a selection shared by every KV head through one
 // scoring head group: the checkpoint indexer's 4-token blocks): one
-// 1024-thread workgroup per query, thread t holding blocks e_lo + t + 1024 i,
-// i < kRbKpt, up to kRbMax candidates; the LDS of k_select_big, whose
+// 1024-thread workgroup per query, thread t holding the kRbKpt consecutive
+// blocks from base + kRbKpt t (base = e_lo rounded down to a multiple of 4:
+// 16-byte loads), so that its candidates follow thread t - 1's in block order;
+// up to kRbMax candidates; the LDS of k_select_big, whose
 // candidate arrays hold the candidates and whose selection is the fallback.
 constexpr int kRbThreads = kBigSelThreads, kRbKpt = 40, kRbBlocks = kRbThreads * kRbKpt, kRbMax = 2048;
 static_assert(kRbMax <= kSelCandMax, "the candidates fit BigSelShared's arrays");
@@ -2812,7 +2814,6 @@ template <int HD, int G>
 struct RefineBigShared {
     BigSelShared s;                               // histogram, reductions; ckey / cblk: the candidates
     float q[G * (HD + 4)];                        // the group's query rows, padded
-    int32_t cbase[kRbKpt * (kRbThreads / 64)];    // candidates before each (thread row, wave) group
     int32_t rk[kRbMax];                           // the ranks of the threshold bin's candidates
     int32_t mem[kRbMax];                          // the threshold bin's candidates
     float qn[G];
@@ -2827,8 +2828,7 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
                 const float *__restrict__ pnorm, int32_t *sel, int32_t *nsel, int32_t max_sel) {
 #pragma clang fp contract(off)
     constexpr int NT = kRbThreads, QS = HD + 4, KPT = kRbKpt, NW = NT / 64, NCH = HD / 16;
-    constexpr int NG = KPT * NW;                       // (thread row, wave) groups
-    static_assert(pf_approx_fits<HD, G>() && G * HD / 4 <= NT && G <= NW && NG <= NT, "shapes");
+    static_assert(pf_approx_fits<HD, G>() && G * HD / 4 <= NT && G <= NW && KPT % 4 == 0, "shapes");
     __shared__ RefineBigShared<HD, G> sh;
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int s = blockIdx.y;
@@ -2842,13 +2842,20 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
         return;
     }
     const int64_t prow = (int64_t)g.pf_seq * g.bps;
+    const int b0 = (r.e_lo & ~3) + KPT * tid;          // this thread's first block
+    // rows start 256-byte aligned (nb_cap is a multiple of 64) and every
+    // 16-byte group read starts below e_hi <= nb_cap
+    const int last4 = (r.e_hi - 1) & ~3;
     float av[KPT], pv[KPT];
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-        const int b = min(r.e_lo + tid + NT * i, r.e_hi - 1);
-        av[i] = row[b];
-        pv[i] = pnorm[b];
+    for (int j = 0; j < KPT / 4; ++j) {
+        const int b = min(b0 + 4 * j, last4);
+        const float4 a4 = *reinterpret_cast<const float4 *>(row + b);
+        const float4 p4 = *reinterpret_cast<const float4 *>(pnorm + b);
+        av[4 * j] = a4.x; av[4 * j + 1] = a4.y; av[4 * j + 2] = a4.z; av[4 * j + 3] = a4.w;
+        pv[4 * j] = p4.x; pv[4 * j + 1] = p4.y; pv[4 * j + 2] = p4.z; pv[4 * j + 3] = p4.w;
     }
+    auto in_row = [&](int i) { return b0 + i >= r.e_lo && b0 + i < r.e_hi; };
     float *qs = sh.q;
     const float *qrow = q + (int64_t)s * g.H * HD;
     if (tid < G * HD / 4) {
@@ -2874,11 +2881,11 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
     for (int h = 0; h < G; ++h) qn += sh.qn[h];
     const float ec = kPaRel * qn * (1.0f + 0x1p-14f);
     // bounds, in place: av becomes the lower, pv the upper bound
-    bool bad = !(ec < INFINITY) || r.e_hi - r.e_lo > KPT * NT;   // (the launch keeps rows within KPT * NT)
+    bool bad = !(ec < INFINITY) || r.e_hi - (r.e_lo & ~3) > KPT * NT;   // (the launch keeps rows within)
     float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-        const bool in = r.e_lo + tid + NT * i < r.e_hi;
+        const bool in = in_row(i);
         const float e = __builtin_fmaf(ec, pv[i], kPaAbs);
         bad |= in && (!(fabsf(av[i]) < INFINITY) || !(e < INFINITY));
         const float a = av[i];
@@ -2903,40 +2910,20 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
             return lin ? (uint32_t)fminf(fmaxf((x - lo) * scale, 0.0f), 4095.0f) : score_key(x) >> 20;
         };
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const bool in = r.e_lo + tid + NT * i < r.e_hi;
-            atomicAdd(&sh.s.hist[in ? bin_of(av[i]) : 4096u + (uint32_t)lane], 1u);
-        }
+        for (int i = 0; i < KPT; ++i) atomicAdd(&sh.s.hist[in_row(i) ? bin_of(av[i]) : 4096u + (uint32_t)lane], 1u);
         __syncthreads();
         if (wid == 0) hist_cut(sh.s, topk);
         __syncthreads();
         const uint32_t B = (uint32_t)sh.s.bin;
         uint64_t cm = 0;
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const bool c = r.e_lo + tid + NT * i < r.e_hi && bin_of(pv[i]) >= B;
-            cm |= (uint64_t)c << i;
-            const uint64_t m = __ballot(c);
-            if (lane == 0) sh.cbase[i * NW + wid] = (int)__builtin_popcountll(m);
-        }
-        __syncthreads();
-        {                                              // exclusive scan of the group counts
-            const int x = tid < NG ? sh.cbase[tid] : 0;
-            int tot;
-            const int ex = block_excl_sum<NT>(x, sh.s.tmp, &tot);
-            if (tid < NG) sh.cbase[tid] = ex;
-            if (tid == 0) sh.s.ncand = tot;
-        }
-        __syncthreads();
-        nc = __builtin_amdgcn_readfirstlane(sh.s.ncand);
-        if (nc <= kRbMax) {
-            const uint64_t below = (1ull << lane) - 1ull;
+        for (int i = 0; i < KPT; ++i) cm |= (uint64_t)(in_row(i) && bin_of(pv[i]) >= B) << i;
+        int pos = block_excl_sum<NT>((int)__builtin_popcountll(cm), sh.s.tmp, &nc);
+        nc = __builtin_amdgcn_readfirstlane(nc);
+        if (nc <= kRbMax) {                            // in block order: thread by thread
 #pragma unroll
-            for (int i = 0; i < KPT; ++i) {
-                const bool c = (cm >> i) & 1u;
-                const uint64_t m = __ballot(c);
-                if (c) sh.s.cblk[sh.cbase[i * NW + wid] + (int)__builtin_popcountll(m & below)] = r.e_lo + tid + NT * i;
-            }
+            for (int i = 0; i < KPT; ++i)
+                if ((cm >> i) & 1u) sh.s.cblk[pos++] = b0 + i;
         }
         for (int i = tid; i < kRbMax; i += NT) sh.rk[i] = 0;
         __syncthreads();
