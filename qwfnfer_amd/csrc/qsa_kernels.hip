@@ -2802,10 +2802,11 @@ k_pf_refine(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *scores, i
 // The same refinement for one score row of up to kRbBlocks eligible blocks
 // (a single KV head, or a selection shared by every KV head through one
 // scoring head group: the checkpoint indexer's 4-token blocks): one
-// 1024-thread workgroup per query, thread t holding the kRbKpt consecutive
-// blocks from base + kRbKpt t (base = e_lo rounded down to a multiple of 4:
-// 16-byte loads), so that its candidates follow thread t - 1's in block order;
-// up to kRbMax candidates; the LDS of k_select_big, whose
+// 1024-thread workgroup per query, thread t holding the 4-block groups
+// base + 4 (t + 1024 j), j < kRbKpt / 4 (base = e_lo rounded down to a
+// multiple of 4: coalesced 16-byte loads; every 64-lane wave row then covers
+// 256 consecutive blocks, in block order by (j, wave, lane)), up to kRbMax
+// candidates; the LDS of k_select_big, whose
 // candidate arrays hold the candidates and whose selection is the fallback.
 constexpr int kRbThreads = kBigSelThreads, kRbKpt = 40, kRbBlocks = kRbThreads * kRbKpt, kRbMax = 2048;
 static_assert(kRbMax <= kSelCandMax, "the candidates fit BigSelShared's arrays");
@@ -2814,6 +2815,7 @@ template <int HD, int G>
 struct RefineBigShared {
     BigSelShared s;                               // histogram, reductions; ckey / cblk: the candidates
     float q[G * (HD + 4)];                        // the group's query rows, padded
+    int32_t cbase[kRbKpt / 4 * (kRbThreads / 64)]; // candidates before each (j, wave) row
     int32_t rk[kRbMax];                           // the ranks of the threshold bin's candidates
     int32_t mem[kRbMax];                          // the threshold bin's candidates
     float qn[G];
@@ -2828,7 +2830,8 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
                 const float *__restrict__ pnorm, int32_t *sel, int32_t *nsel, int32_t max_sel) {
 #pragma clang fp contract(off)
     constexpr int NT = kRbThreads, QS = HD + 4, KPT = kRbKpt, NW = NT / 64, NCH = HD / 16;
-    static_assert(pf_approx_fits<HD, G>() && G * HD / 4 <= NT && G <= NW && KPT % 4 == 0, "shapes");
+    constexpr int NJ = KPT / 4, NG = NJ * NW;          // 4-block groups a thread; (j, wave) rows
+    static_assert(pf_approx_fits<HD, G>() && G * HD / 4 <= NT && G <= NW && KPT % 4 == 0 && NG <= NT, "shapes");
     __shared__ RefineBigShared<HD, G> sh;
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int s = blockIdx.y;
@@ -2842,20 +2845,21 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
         return;
     }
     const int64_t prow = (int64_t)g.pf_seq * g.bps;
-    const int b0 = (r.e_lo & ~3) + KPT * tid;          // this thread's first block
+    const int b0 = (r.e_lo & ~3) + 4 * tid;            // group j starts at b0 + 4 NT j
     // rows start 256-byte aligned (nb_cap is a multiple of 64) and every
     // 16-byte group read starts below e_hi <= nb_cap
     const int last4 = (r.e_hi - 1) & ~3;
+    auto blk = [&](int i) { return b0 + 4 * NT * (i / 4) + (i % 4); };   // block of register i
     float av[KPT], pv[KPT];
 #pragma unroll
-    for (int j = 0; j < KPT / 4; ++j) {
-        const int b = min(b0 + 4 * j, last4);
+    for (int j = 0; j < NJ; ++j) {
+        const int b = min(b0 + 4 * NT * j, last4);
         const float4 a4 = *reinterpret_cast<const float4 *>(row + b);
         const float4 p4 = *reinterpret_cast<const float4 *>(pnorm + b);
         av[4 * j] = a4.x; av[4 * j + 1] = a4.y; av[4 * j + 2] = a4.z; av[4 * j + 3] = a4.w;
         pv[4 * j] = p4.x; pv[4 * j + 1] = p4.y; pv[4 * j + 2] = p4.z; pv[4 * j + 3] = p4.w;
     }
-    auto in_row = [&](int i) { return b0 + i >= r.e_lo && b0 + i < r.e_hi; };
+    auto in_row = [&](int i) { return blk(i) >= r.e_lo && blk(i) < r.e_hi; };
     float *qs = sh.q;
     const float *qrow = q + (int64_t)s * g.H * HD;
     if (tid < G * HD / 4) {
@@ -2918,12 +2922,31 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
         uint64_t cm = 0;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) cm |= (uint64_t)(in_row(i) && bin_of(pv[i]) >= B) << i;
-        int pos = block_excl_sum<NT>((int)__builtin_popcountll(cm), sh.s.tmp, &nc);
-        nc = __builtin_amdgcn_readfirstlane(nc);
-        if (nc <= kRbMax) {                            // in block order: thread by thread
+        // in block order: row (j, wave) after the rows before it, lane after lane
+        int ex[NJ];
 #pragma unroll
-            for (int i = 0; i < KPT; ++i)
-                if ((cm >> i) & 1u) sh.s.cblk[pos++] = b0 + i;
+        for (int j = 0; j < NJ; ++j) {
+            const int c = (int)__builtin_popcount((uint32_t)(cm >> (4 * j)) & 0xFu);
+            const int incl = wave_incl_scan(c);
+            ex[j] = incl - c;
+            if (lane == 63) sh.cbase[j * NW + wid] = incl;
+        }
+        __syncthreads();
+        {
+            const int x = tid < NG ? sh.cbase[tid] : 0;
+            const int e = block_excl_sum<NT>(x, sh.s.tmp, &nc);
+            if (tid < NG) sh.cbase[tid] = e;
+        }
+        __syncthreads();
+        nc = __builtin_amdgcn_readfirstlane(nc);
+        if (nc <= kRbMax) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                int pos = sh.cbase[j * NW + wid] + ex[j];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if ((cm >> (4 * j + k)) & 1u) sh.s.cblk[pos++] = blk(4 * j + k);
+            }
         }
         for (int i = tid; i < kRbMax; i += NT) sh.rk[i] = 0;
         __syncthreads();
