@@ -131,10 +131,14 @@ typedef struct qwfn_qsa_shape {
     int32_t kv_type;         /* QWFN_KV_Q8_0 / QWFN_KV_Q4_0 / QWFN_KV_F16       */
     int32_t kv_round_f16;    /* 1: the decode attention rounds every dequantized
                               * K and V value to fp16 (round to nearest even)
-                              * before its arithmetic, as the reference's
-                              * gather casts K/V to F16 ahead of
-                              * flash_attn_ext (src/qwfn_graph.cpp:530-537);
-                              * 0: the exact dequantized values.  Prefill
+                              * before its arithmetic: the F16 cast of the
+                              * gathered K/V ahead of flash_attn_ext
+                              * (src/qwfn_graph.cpp:530-537).  What ggml's
+                              * flash_attn_ext then does with Q and its
+                              * accumulators is not in the reference tree, so
+                              * parity beyond the K/V cast is unpinned; the
+                              * attention here stays fp32 over the rounded
+                              * values.  0: the exact dequantized values.  Prefill
                               * ignores it (the reference's prefill reads the
                               * cache rows directly, src/qwfn_graph.cpp:
                               * 365-403)                                     */
@@ -165,6 +169,19 @@ const char *qwfn_qsa_last_error(void);
  * completed.  A call on a capturing stream times nothing.  The call disarms
  * what it did not use; events == NULL disarms.                               */
 int         qwfn_qsa_time_next_call(void *const events[6]);
+/* Test hook; it has no counterpart in the reference and serves the tests that
+ * check the prefill scoring's error bound on the hardware.  Runs the
+ * prefill's approximate matrix-core scoring alone: queries q
+ * [n_q][n_head][head_dim] (fp32) of sequence `seq` against the pooled blocks
+ * [sink_blocks, n_blk) of every KV head, writing the approximate scores to
+ * scores [n_q][n_head_kv][nb_cap] and each block's key norm, rounded up, to
+ * pnorm [n_head_kv][nb_cap] (device fp32; other entries untouched).  The
+ * prefill's selection is exact because |approximate - exact| <= 1.05e-3 *
+ * (sum over the query's group of |q_h|) * |p| + 1e-37.  QWFN_ENOTSUP for shapes
+ * without the matrix-core scoring (group * head_dim > 1024).                */
+int qwfn_qsa_test_prefill_scores(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                                 const float *q, int32_t n_q, int32_t seq, int32_t n_blk,
+                                 float *scores, float *pnorm, int32_t nb_cap, void *stream);
 /* Validates a shape (QWFN_EINVAL) and whether this build has kernels for it
  * (QWFN_ENOTSUP).  Replaces the reference's shape constants
  * (src/qwfn_hparams.h:22-36, src/qwfn_engine.cpp:382-435).                   */
@@ -340,7 +357,9 @@ int qwfn_sparse_attn_decode_chain(const qwfn_qsa_shape *shape, const qwfn_kv_vie
  * qwfn_qsa_workspace_bytes(shape, n_seq, max_seq_len) exceeds it return
  * QWFN_ERANGE (8 MiB holds eight sequences of the BASELINE shape up to 1M
  * tokens).  The first call on a device enqueues one fill kernel on `stream`
- * that clears the array.  Every call on a device shares its array, so calls
+ * that clears the array, unless `stream` is capturing (the array is zero when
+ * the library loads, and a captured fill would rerun on every replay).  Every
+ * call leaves the array's counters at zero.  Every call on a device shares its array, so calls
  * that overlap on one device (other streams, other threads) race; calls in
  * stream order do not.  Nothing here allocates or frees.                    */
 int qwfn_sparse_attn_decode_noalloc(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
@@ -407,8 +426,11 @@ int qwfn_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *vi
  *   RMSNorm sum of fp32 squares in fp64, lane partials (dims d = l + 64k)
  *           then a butterfly over lanes 32..1; scale = 1/sqrtf(fp32(sum/D) +
  *           eps); x * scale * k_norm[d]
- *   rotary  pairs (i, i + rope_dim/2), angle = pos * base^(-2i/rope_dim) in
- *           fp64, cos / sin rounded to fp32; dims >= rope_dim pass through.
+ *   rotary  pairs (i, i + rope_dim/2), ggml's angle: theta_0 = (float)pos,
+ *           theta_{i+1} = theta_i * theta_scale, each product rounded to
+ *           fp32, theta_scale = powf(rope_base, -2/rope_dim) on the host;
+ *           cos / sin of that fp32 angle evaluated in fp64 and rounded to
+ *           fp32; dims >= rope_dim pass through.
  *           The reference's IMROPE gives all four position sections the same
  *           position for text (src/qwfn_engine.cpp:741, 781, 926, 934), which
  *           makes it this rotation; per-section (vision) positions are not

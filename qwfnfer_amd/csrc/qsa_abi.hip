@@ -241,6 +241,27 @@ int qwfn_qsa_time_next_call(void *const events[6]) {
     return ok();
 }
 
+int qwfn_qsa_test_prefill_scores(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
+                                 int32_t n_q, int32_t seq, int32_t n_blk, float *scores, float *pnorm,
+                                 int32_t nb_cap, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    if (!pf_approx_fits_shape(g.hd, g.G))
+        return fail(QWFN_ENOTSUP, "test_prefill_scores: no matrix-core scoring for head_dim %d, group %d", g.hd,
+                    g.G);
+    if (seq < 0 || seq >= view->n_seq) return fail(QWFN_EINVAL, "test_prefill_scores: seq %d outside the view", seq);
+    if (n_q < 1 || !q || !aligned(q, 16) || !scores || !pnorm)
+        return fail(QWFN_EINVAL, "test_prefill_scores: n_q < 1, NULL or misaligned q, NULL scores / pnorm");
+    if (n_blk <= g.sink || n_blk > g.bps || nb_cap < n_blk)
+        return fail(QWFN_ERANGE, "test_prefill_scores: n_blk %d outside (sink %d, %d] or above nb_cap %d", n_blk,
+                    g.sink, g.bps, nb_cap);
+    g.pf = 1;
+    g.pf_seq = seq;
+    const hipError_t e = launch_pf_approx_scores(g, *view, q, n_q, n_blk, scores, nb_cap, pnorm, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "test_prefill_scores");
+}
+
 int qwfn_qsa_check_shape(const qwfn_qsa_shape *shape) {
     const int rc = check_shape(shape);
     return rc ? rc : ok();
@@ -544,8 +565,11 @@ std::mutex g_scratch_mu;
 void *g_scratch_ptr[kScratchDevices];
 
 // This device's copy of `scratch`.  The first call on a device looks up its
-// address and clears it with a fill kernel on `st` (the workspace's
-// completion counters must start at zero; every call leaves them at zero).
+// address and, unless `st` is capturing, clears it with a fill kernel on `st`
+// (the workspace's completion counters must start at zero; every call leaves
+// them at zero).  Under capture the fill would be recorded into the graph and
+// rerun on every replay, so it is skipped: the array is zero when the code
+// object is loaded, which is all the counters need.
 int scratch_of_device(hipStream_t st, void **out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -558,8 +582,13 @@ int scratch_of_device(hipStream_t st, void **out) {
         void *p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p) return hip_fail(e, "decode_noalloc: hipGetSymbolAddress(scratch)");
-        e = launch_fill_zero(p, kScratchBytes, st);
-        if (e != hipSuccess) return hip_fail(e, "decode_noalloc: clearing the scratch array");
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess) return hip_fail(e, "decode_noalloc: hipStreamIsCapturing");
+        if (cs == hipStreamCaptureStatusNone) {
+            e = launch_fill_zero(p, kScratchBytes, st);
+            if (e != hipSuccess) return hip_fail(e, "decode_noalloc: clearing the scratch array");
+        }
         g_scratch_ptr[dev] = p;
     }
     *out = g_scratch_ptr[dev];

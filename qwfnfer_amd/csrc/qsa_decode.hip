@@ -336,7 +336,7 @@ __device__ __forceinline__ float scale_at(const u4v (&d)[NS], int j) {
 // ws.scores with KPT keys a thread; part 0 writes sel / nsel out).  Dynamic
 // LDS: dec_union_bytes<HD, G, MODE, TM>() for the union, then npt_lds page
 // entries (the sequence's page-table row, when parked).
-template <int HD, int G, int MODE, int KPT, int TM>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF>
 __global__ void __launch_bounds__(kDecThreads)
 k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len, int32_t max_seq_len,
       int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t tpw, int32_t npt_lds) {
@@ -576,12 +576,25 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             default: wait_vmcnt<3 * S::NL>(); break;
         }
         const uint8_t *st = dec_dyn + (w * TM + i) * S::BYTES;
+        // RF: the scales of the lane's A-operand cell hn (its K row), one a block
+        uint32_t ksw[RF ? NB / 2 : 1];
+        if constexpr (RF) {
+#pragma unroll
+            for (int k = 0; k < NB / 2; ++k)
+                ksw[k] = *reinterpret_cast<const uint32_t *>(st + S::SOFF + hn * NB * 2 + 4 * k);
+        }
         f4v acc[NB];
 #pragma unroll
         for (int kb = 0; kb < NB; ++kb) {
             const u2v kw = *reinterpret_cast<const u2v *>(st + S::KOFF + (2 * kb + (lg >> 1)) * 256 + hn * 16 +
                                                           8 * (lg & 1));
-            const h8v ka = q8x8_to_h8(make_uint2(kw[0], kw[1]));
+            h8v ka = q8x8_to_h8(make_uint2(kw[0], kw[1]));
+            if constexpr (RF) {
+                // fp16(d * q) per element: the product of two fp16 values rounded
+                // once, as the F16 cast of the exact fp32 d * q
+                const half2v d2 = __builtin_bit_cast(half2v, ksw[kb / 2]);
+                ka = ka * (kb % 2 ? d2[1] : d2[0]);
+            }
             acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[kb], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[kb], acc[kb], 0, 0, 0);
         }
@@ -598,7 +611,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             float x = 0.0f;
 #pragma unroll
             for (int kb = 0; kb < NB; ++kb)
-                x = __builtin_fmaf((float)dk[(c * NB + kb) / 8][(c * NB + kb) % 8], acc[kb][c], x);
+                x = RF ? x + acc[kb][c] : __builtin_fmaf((float)dk[(c * NB + kb) / 8][(c * NB + kb) % 8], acc[kb][c], x);
             sl[i][c] = c0 + c < tnv[i] ? x * qfac : -INFINITY;
         }
         // a word holds two blocks' scales of one cell: NB / 2 words a cell
@@ -607,8 +620,9 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (c0 + (4 * k + e) / (NB / 2) >= tnv[i]) dvw[i][k][e] = 0u;
+        if constexpr (!RF)
 #pragma unroll
-        for (int k = 0; k < NS; ++k) dmx = __builtin_elementwise_max(dmx, __builtin_bit_cast(h8v, dvw[i][k]));
+            for (int k = 0; k < NS; ++k) dmx = __builtin_elementwise_max(dmx, __builtin_bit_cast(h8v, dvw[i][k]));
     }
     // the part's column maximum, and the column's weight scale 2^k that puts
     // its largest V scale near 2^15 (p <= 1, so every weight stays below 2^15)
@@ -617,14 +631,18 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     for (int i = 0; i < TM; ++i)
         mx = fmaxf(mx, fmaxf(fmaxf(sl[i][0], sl[i][1]), fmaxf(sl[i][2], sl[i][3])));
     const float m = col_max4(mx);
-    float dvm = 0.0f;
+    // RF: the V values carry their scales, so the weights p <= 1 go up by 2^15
+    float up = 0x1p15f, down = 0x1p-15f;
+    if constexpr (!RF) {
+        float dvm = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dvm = fmaxf(dvm, (float)dmx[e]);
-    dvm = col_max4(dvm);
-    int ev = 0;
-    frexpf(dvm, &ev);
-    const float up = dvm > 0.0f ? ldexpf(1.0f, 15 - ev) : 1.0f;
-    const float down = dvm > 0.0f ? ldexpf(1.0f, ev - 15) : 1.0f;
+        for (int e = 0; e < 8; ++e) dvm = fmaxf(dvm, (float)dmx[e]);
+        dvm = col_max4(dvm);
+        int ev = 0;
+        frexpf(dvm, &ev);
+        up = dvm > 0.0f ? ldexpf(1.0f, 15 - ev) : 1.0f;
+        down = dvm > 0.0f ? ldexpf(1.0f, ev - 15) : 1.0f;
+    }
     // ---- pass 2: weights and PV, O accumulated on the matrix cores
     f4v o[ND];
 #pragma unroll
@@ -641,23 +659,37 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             pu[c] = p * up;
         }
         // weight of (cell c, block kb) = pu[c] * d_v(c, kb), rounded once, as
-        // fp16 high + low parts
-        h4v bhi[NB], blo[NB];
+        // fp16 high + low parts (RF: pu[c] alone, the same for every block)
+        constexpr int NW = RF ? 1 : NB;
+        h4v bhi[NW], blo[NW];
 #pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
+        for (int kb = 0; kb < NW; ++kb)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const h8v dw = __builtin_bit_cast(h8v, dvw[i][(c * NB + kb) / 8]);
-                const float dv = (float)dw[(c * NB + kb) % 8];
+                float dv = 1.0f;
+                if constexpr (!RF) {
+                    const h8v dw = __builtin_bit_cast(h8v, dvw[i][(c * NB + kb) / 8]);
+                    dv = (float)dw[(c * NB + kb) % 8];
+                }
                 const _Float16 h = (_Float16)__builtin_fmaf(pu[c], dv, 0.0f);
                 bhi[kb][c] = h;
                 blo[kb][c] = (_Float16)__builtin_fmaf(pu[c], dv, -(float)h);
             }
+        // RF: the four cells' V scales of each block (0 past the valid cells)
+        h4v dvc[RF ? NB : 1];
+        if constexpr (RF) {
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    dvc[kb][c] = __builtin_bit_cast(h8v, dvw[i][(c * NB + kb) / 8])[(c * NB + kb) % 8];
+        }
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-            const h4v va = q8x4_to_h4(*reinterpret_cast<const uint32_t *>(st + S::VOFF + (16 * db + hn) * 16 + 4 * lg));
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[db / 2], o[db], 0, 0, 0);
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[db / 2], o[db], 0, 0, 0);
+            h4v va = q8x4_to_h4(*reinterpret_cast<const uint32_t *>(st + S::VOFF + (16 * db + hn) * 16 + 4 * lg));
+            if constexpr (RF) va = va * dvc[db / 2];       // fp16(d * q) per element
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[RF ? 0 : db / 2], o[db], 0, 0, 0);
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[RF ? 0 : db / 2], o[db], 0, 0, 0);
         }
     }
     const float l = col_sum4(ls);
@@ -718,7 +750,7 @@ constexpr int kResDevices = 64;
 struct DecRes {
     int per_cu, cus, lds_cu, lds_static;
 };
-template <int HD, int G, int MODE, int KPT, int TM>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF>
 bool dec_res(DecRes *out) {
     static std::atomic<int> cache[kResDevices][4];
     int dev = -1;
@@ -727,11 +759,11 @@ bool dec_res(DecRes *out) {
     if (c[0].load(std::memory_order_acquire) <= 0) {
         int per_cu = 0, cus = 0, lds_cu = 0;
         hipFuncAttributes fa;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT, TM>, kDecThreads, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT, TM, RF>, kDecThreads, 0) !=
                 hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
-            hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(k_dec<HD, G, MODE, KPT, TM>)) != hipSuccess)
+            hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(k_dec<HD, G, MODE, KPT, TM, RF>)) != hipSuccess)
             return false;
         c[1].store(cus, std::memory_order_relaxed);
         c[2].store(lds_cu, std::memory_order_relaxed);
@@ -753,22 +785,22 @@ inline int dec_npt_lds(const Geo &g, int32_t max_seq_len, int mode) {
 
 // Resident workgroups of the TM instantiation at this launch's LDS (0 when
 // unknown).
-template <int HD, int G, int MODE, int KPT, int TM>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF>
 int64_t dec_resident(int dyn_bytes) {
     DecRes r;
-    if (!dec_res<HD, G, MODE, KPT, TM>(&r)) return 0;
+    if (!dec_res<HD, G, MODE, KPT, TM, RF>(&r)) return 0;
     int per = r.per_cu;
     const int lds = r.lds_static + dyn_bytes;
     if (r.lds_cu > 0 && lds > 0) per = std::min(per, r.lds_cu / lds);
     return (int64_t)std::max(per, 0) * r.cus;
 }
 
-template <int HD, int G, int MODE, int KPT, int TM>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF>
 void launch_dec_tm(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                    int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, int npt_lds,
                    int dyn, hipStream_t st) {
     const int parts = (ws.n_tiles + TM - 1) / TM;
-    QWFN_LAUNCH_SHM(kTimedAttention, (k_dec<HD, G, MODE, KPT, TM>),
+    QWFN_LAUNCH_SHM(kTimedAttention, (k_dec<HD, G, MODE, KPT, TM, RF>),
                     dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kDecThreads), (unsigned)dyn, st,
                     g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, ws, (int32_t)TM, (int32_t)npt_lds);
 }
@@ -776,7 +808,7 @@ void launch_dec_tm(const Geo &g, const qwfn_kv_view &v, const float *q, const in
 // Launches k_dec; returns the tiles a workgroup took.  One tile a workgroup
 // unless the grid would then not be resident at once (a second round of
 // workgroups starts only when the first ends): then two, else four.
-template <int HD, int G, int MODE, int KPT>
+template <int HD, int G, int MODE, int KPT, bool RF>
 int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                  int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
     const int64_t pairs = (int64_t)n_seq * g.Hkv;
@@ -784,24 +816,24 @@ int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int3
     const int d1 = dec_union_bytes<HD, G, MODE, 1>() + 4 * npt_lds;
     const int d2 = dec_union_bytes<HD, G, MODE, 2>() + 4 * npt_lds;
     const int d4 = dec_union_bytes<HD, G, MODE, 4>() + 4 * npt_lds;
-    const int64_t r1 = dec_resident<HD, G, MODE, KPT, 1>(d1);
+    const int64_t r1 = dec_resident<HD, G, MODE, KPT, 1, RF>(d1);
     if (r1 <= 0 || pairs * ws.n_tiles <= r1) {
-        launch_dec_tm<HD, G, MODE, KPT, 1>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
+        launch_dec_tm<HD, G, MODE, KPT, 1, RF>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
                                            d1, st);
         return 1;
     }
-    const int64_t r2 = dec_resident<HD, G, MODE, KPT, 2>(d2);
+    const int64_t r2 = dec_resident<HD, G, MODE, KPT, 2, RF>(d2);
     if (pairs * ((ws.n_tiles + 1) / 2) <= r2) {
-        launch_dec_tm<HD, G, MODE, KPT, 2>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
+        launch_dec_tm<HD, G, MODE, KPT, 2, RF>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
                                            d2, st);
         return 2;
     }
-    launch_dec_tm<HD, G, MODE, KPT, 4>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, d4,
+    launch_dec_tm<HD, G, MODE, KPT, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, d4,
                                        st);
     return 4;
 }
 
-template <int HD, int G>
+template <int HD, int G, bool RF>
 hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                             int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                             int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
@@ -811,19 +843,19 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
         const Ranges span_r{0, 0, g.sink, max_seq_len / g.bt};
         const int span = span_r.e_hi - (span_r.e_lo & ~3);
         if (span <= 4 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 8 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 8>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 8, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 16 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 16>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 16, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 32 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 32>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 32, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else
             return hipErrorInvalidValue;
     } else if (sel) {
-        tpw = launch_dec_t<HD, G, kGiven, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+        tpw = launch_dec_t<HD, G, kGiven, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
     } else {
-        tpw = launch_dec_t<HD, G, kDense, 4>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+        tpw = launch_dec_t<HD, G, kDense, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -834,10 +866,18 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
 }  // namespace
 
 #define QWFN_FOR_EACH_DEC(X) X(128, 8) X(128, 4) X(128, 2) X(64, 8) X(256, 12) X(256, 8)
+// Shapes whose fp16-rounded K/V (kv_round_f16) run here; the others take the
+// general kernel, which dequantizes each value into LDS.
+#define QWFN_FOR_EACH_DEC_RF(X) X(128, 8)
 
 bool dec_kernels_for(const Geo &g) {
-    // (fp16-rounded K/V: the general kernel, which dequantizes each value)
-    if (!g.vdim || g.pf || g.round_f16) return false;
+    if (!g.vdim || g.pf) return false;
+    if (g.round_f16) {
+#define X(HD_, G_) if (g.hd == HD_ && g.G == G_) return true;
+        QWFN_FOR_EACH_DEC_RF(X)
+#undef X
+        return false;
+    }
 #define X(HD_, G_) if (g.hd == HD_ && g.G == G_) return true;
     QWFN_FOR_EACH_DEC(X)
 #undef X
@@ -853,10 +893,19 @@ hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                                 int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
     if (!dec_kernels_for(g) || (select && !dec_select_fits(g, max_seq_len, max_sel))) return hipErrorInvalidValue;
+    if (g.round_f16) {
+#define X(HD_, G_)                                                                                              \
+        if (g.hd == HD_ && g.G == G_)                                                                           \
+            return launch_dec_shape<HD_, G_, true>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, \
+                                                   ws, select, st);
+        QWFN_FOR_EACH_DEC_RF(X)
+#undef X
+        return hipErrorInvalidValue;
+    }
 #define X(HD_, G_)                                                                                        \
     if (g.hd == HD_ && g.G == G_)                                                                         \
-        return launch_dec_shape<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, \
-                                         select, st);
+        return launch_dec_shape<HD_, G_, false>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, \
+                                                ws, select, st);
     QWFN_FOR_EACH_DEC(X)
 #undef X
     return hipErrorInvalidValue;

@@ -180,6 +180,14 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                                 int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                                 const Ws &ws, hipStream_t st);
+// The prefill's approximate matrix-core scores alone (k_pf_approx): n_q
+// queries of sequence g.pf_seq against blocks [g.sink, n_blk) of every KV
+// head into scores [n_q][Hkv][nb_cap], each block's key norm (rounded up)
+// into pnorm [Hkv][nb_cap].  For the test entry point that checks the
+// scoring bound on the hardware.
+bool pf_approx_fits_shape(int32_t hd, int32_t G);
+hipError_t launch_pf_approx_scores(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                                   int32_t n_blk, float *scores, int32_t nb_cap, float *pnorm, hipStream_t st);
 // The largest q8_0 V scale of each KV head over positions [0, n_pos) of
 // sequence g.pf_seq, as kVmaxWg partial maxima per head (vmax).
 hipError_t launch_prefill_vmax(const Geo &g, const qwfn_kv_view &v, int32_t n_pos, float *vmax, hipStream_t st);

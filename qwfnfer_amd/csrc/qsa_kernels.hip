@@ -2246,13 +2246,18 @@ constexpr int kPaSplitBig = 16;       // the same for one 40960-block row: 40 ti
 constexpr int kRefineMax = 512;       // candidates ranked exactly (more: the whole row exactly)
 constexpr int kRefineBlocks = 4096;   // eligible blocks the approximate path takes
 // |approximate - exact| <= kPaRel * (sum over the group's heads of |q_h|) * |p|
-// + kPaAbs (Euclidean norms: sum_d |q_hd p_d| <= |q_h| |p|).  The terms: fp16
-// rounding of both operands, 2 * 2^-11 + 2^-22 of each product; the matrix
-// cores' fp32 sums over a head's dims, the relu'd head sum and the
-// power-of-two rescale, below 2 * 128 * 2^-24; the exact scores' own rounding
-// (four chains of HD / 4 fmas, their two sums, the head sum), below
-// 80 * 2^-24; fp16 subnormals, below 2^-30.  They sum to 9.97e-4; 5 % more
-// covers the rounding of the norms and of the bound itself.
+// + kPaAbs (Euclidean norms: sum_d |q_hd p_d| <= |q_h| |p|).  The terms, each
+// relative to sum_h |q_h| |p|: fp16 rounding of both operands, 2 * 2^-11 +
+// 2^-22 of each product; the matrix cores' fp32 sums, one accumulator a head
+// (HD - 1 adds, rounded at each in the worst case), then the G head sums in
+// order (relu'd when set) and the power-of-two rescale (exact), below
+// (HD + G - 2) * 2^-24 <= 258 * 2^-24 for every instantiation (G * HD <= 1024,
+// HD <= 256); the exact scores' own rounding (four chains of HD / 4 fmas,
+// their two sums, the head sum), below 80 * 2^-24; fp16 subnormals, below
+// 2^-30.  They sum to at most 9.97e-4; the 5 % left covers the rounding of
+// the norms (rounded up by 2^-14) and of the bound itself.  The budget is
+// restated and checked per instantiated shape on the CPU, and the kernel's
+// outputs against it on the GPU.
 constexpr float kPaRel = 1.05e-3f;
 // an absolute floor: a score that underflows fp32 keeps no relative precision
 constexpr float kPaAbs = 1e-37f;
@@ -2467,23 +2472,18 @@ k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
 #pragma unroll
             for (int ks = 0; ks < NK; ++ks)
                 bf[ks] = *reinterpret_cast<const h8v *>(&sh.p[16 * ct + row][2 * (4 * ks + kg)]);
+            // one accumulator a head (HD products), the heads' sums (relu'd
+            // when set) added in order: the fp32 sums of one score stay within
+            // (HD - 1) + (G - 1) roundings, the budget of kPaRel
             f4v tot = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (g.relu) {
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int h = 0; h < G; ++h) {
+                f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int ks = 0; ks < NK; ++ks)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], acc, 0, 0, 0);
+                for (int ks = 0; ks < NK; ++ks)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], acc, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) tot[i] += fmaxf(acc[i], 0.0f);
-                }
-            } else {
-#pragma unroll
-                for (int h = 0; h < G; ++h)
-#pragma unroll
-                    for (int ks = 0; ks < NK; ++ks)
-                        tot = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], tot, 0, 0, 0);
+                for (int i = 0; i < 4; ++i) tot[i] += g.relu ? fmaxf(acc[i], 0.0f) : acc[i];
             }
             const int blk = b0 + 16 * ct + row;
             const int pb = sh.pe[16 * ct + row];
@@ -3626,6 +3626,28 @@ hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float
                                 int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                                 const Ws &ws, hipStream_t st) {
 #define X(HD_, G_, TG_)                                                                              if (g.hd == HD_ && g.G == G_) {                                                                      launch_pf_index_t<HD_, G_>(g, v, q, n_q, max_seq_len, sel, nsel, max_sel, ws, st);              return hipGetLastError();                                                                    }
+    QWFN_FOR_EACH_SHAPE(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+bool pf_approx_fits_shape(int32_t hd, int32_t G) {
+#define X(HD_, G_, TG_) if (hd == HD_ && G == G_) return pf_approx_fits<HD_, G_>();
+    QWFN_FOR_EACH_SHAPE(X)
+#undef X
+    return false;
+}
+
+hipError_t launch_pf_approx_scores(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                                   int32_t n_blk, float *scores, int32_t nb_cap, float *pnorm, hipStream_t st) {
+#define X(HD_, G_, TG_)                                                                                   \
+    if constexpr (pf_approx_fits<HD_, G_>())                                                              \
+        if (g.hd == HD_ && g.G == G_) {                                                                   \
+            hipLaunchKernelGGL((k_pf_approx<HD_, G_>),                                                    \
+                               dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv), \
+                               dim3(256), 0, st, g, v, q, n_q, n_blk, scores, nb_cap, pnorm);              \
+            return hipGetLastError();                                                                     \
+        }
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
     return hipErrorInvalidValue;

@@ -409,6 +409,9 @@ def sparse_attn_decode(cache: KvCache, q: torch.Tensor, k_new: torch.Tensor, v_n
         out = torch.empty((n_seq, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
     if (sel is None) != (n_sel is None):
         raise ValueError("pass both sel and n_sel or neither")
+    if sel is not None:                            # the kernels write max_selected entries a (sequence, KV head)
+        _need(sel, "sel", torch.int32, n_seq * cfg.n_head_kv * cfg.max_selected(max_seq_len))
+        _need(n_sel, "n_sel", torch.int32, n_seq * cfg.n_head_kv)
     s = cfg.shape()
     call("qwfn_sparse_attn_decode", C.byref(s), C.byref(cache.view()), q.data_ptr(), k_new.data_ptr(),
          v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,
@@ -473,6 +476,9 @@ def sparse_attn_decode_noalloc(cache: KvCache, q: torch.Tensor, k_new: torch.Ten
     _need(out, "out", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
     if (sel is None) != (n_sel is None):
         raise ValueError("pass both sel and n_sel or neither")
+    if sel is not None:                            # the kernels write max_selected entries a (sequence, KV head)
+        _need(sel, "sel", torch.int32, n_seq * cfg.n_head_kv * cfg.max_selected(max_seq_len))
+        _need(n_sel, "n_sel", torch.int32, n_seq * cfg.n_head_kv)
     s = cfg.shape()
     call("qwfn_sparse_attn_decode_noalloc", C.byref(s), C.byref(cache.view()), q.data_ptr(), k_new.data_ptr(),
          v_new.data_ptr(), _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32,

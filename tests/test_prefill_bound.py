@@ -125,3 +125,40 @@ def test_bound_fails_without_the_rounding_term():
         small = 2.0e-5 * qn * float(np.linalg.norm(p.astype(np.float64)))
         missed += abs(a - s) > small
     assert missed > 0
+
+
+# (head_dim, group) pairs with the matrix-core scoring: every instantiation
+# of qsa_kernels.hip's QWFN_FOR_EACH_SHAPE whose group * head_dim <= 1024
+SHAPES = [(128, 8), (128, 4), (128, 2), (64, 8)]
+
+
+def test_kparel_covers_the_budget_of_every_shape():
+    """kPaRel against its terms, per instantiated shape: fp16 rounding of both
+    operands (2 * 2^-11 + 2^-22), the matrix cores' fp32 sums with one
+    accumulator a head (HD - 1 adds) and the G head sums (G - 1 adds), the
+    exact score's own rounding (80 * 2^-24), with 5 % to spare.  A single
+    accumulator over all G * HD products (the mistake of summing every head in
+    one chain) would need (G * HD - 1) * 2^-24 and is caught at G * HD = 1024."""
+    u = 2.0 ** -24
+    text = open(SRC).read()
+    shapes = re.search(r"#define QWFN_FOR_EACH_SHAPE\(X\) (.*)", text).group(1)
+    inst = {(int(a), int(b)) for a, b in re.findall(r"X\((\d+), (\d+), \d+\)", shapes)}
+    assert set(SHAPES) == {(h, g) for h, g in inst if h * g <= 1024}
+    for hd, g in SHAPES:
+        need = 2 * 2.0 ** -11 + 2.0 ** -22 + (hd - 1 + g - 1) * u + 80 * u
+        assert KPA_REL >= 1.05 * need, (hd, g, need)
+    one_chain = 2 * 2.0 ** -11 + 2.0 ** -22 + (1024 - 1) * u + 80 * u
+    assert KPA_REL < 1.05 * one_chain
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_approx_score_within_bound_at_1024_products(relu):
+    """Eight heads of 128 (G * HD = 1024, the largest group of the matrix-core
+    scoring), each head's 128 products summed in one fp32 chain taken in both
+    orders, against the exact order."""
+    rng = np.random.default_rng(4321 + relu)
+    for q, p in _cases(rng, 60):
+        s = float(exact_score(q, p, relu))
+        e = bound(q, p)
+        for rev in (False, True):
+            assert abs(float(approx_score(q, p, relu, rev)) - s) <= e
