@@ -36,6 +36,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 #include "qsa_device.h"
 
@@ -322,6 +323,86 @@ __device__ __forceinline__ void dec_select(const Geo &g, const float (&sv)[KPT],
     __syncthreads();
 }
 
+// Records (the scoring launch's (min, max) eligible score of each 16 blocks)
+// a lane holds for a KPT-keys-a-thread selection: record lane + 64 k in
+// rec[k].
+template <int KPT> constexpr int dec_rpl() { return KPT / 4 + 2; }
+
+// The selection's inputs of (sequence, KV head) `pair`, issued together: thread
+// t's KPT scores of blocks base + [t*KPT, t*KPT + KPT) (base = sink rounded
+// down to 4) and the lane's records.
+template <int KPT>
+__device__ __forceinline__ void dec_load_sel_inputs(const Geo &g, const Ws &ws, int pair, float (&sv)[KPT],
+                                                    float2 (&rec)[dec_rpl<KPT>()]) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int base = g.sink & ~3;
+    const BufRsrc rs = buf_rsrc(ws.scores + (int64_t)pair * ws.nb_cap, (uint32_t)ws.nb_cap * 4u);
+#pragma unroll
+    for (int k = 0; k < KPT / 4; ++k) {
+        const auto x = BufLoad<4>::at(rs, (base + tid * KPT) * 4 + 16 * k, 0);
+        sv[4 * k] = x[0]; sv[4 * k + 1] = x[1]; sv[4 * k + 2] = x[2]; sv[4 * k + 3] = x[3];
+    }
+    const int n_ch = ws.nb_cap / kScoreRecBlocks;
+    const BufRsrc rr = buf_rsrc(ws.cmm + (int64_t)pair * n_ch, (uint32_t)n_ch * 8u);
+#pragma unroll
+    for (int k = 0; k < dec_rpl<KPT>(); ++k) {
+        const auto x = BufLoad<2>::at(rr, (lane + 64 * k) * 8, 0);
+        rec[k] = make_float2(x[0], x[1]);
+    }
+}
+
+// Zero the selection histogram (before the caller's barrier).
+__device__ __forceinline__ void dec_zero_hist(DecSel &ss) {
+    const int tid = threadIdx.x;
+    u4v *h4 = reinterpret_cast<u4v *>(ss.hist);
+    const u4v z = {0u, 0u, 0u, 0u};
+    h4[tid] = z;
+    h4[tid + kDecThreads] = z;
+    if (tid < 16) h4[2 * kDecThreads + tid] = z;
+}
+
+// The selection of one (sequence, KV head) of length L into sh.sel / sh.nsel
+// (all threads; the histogram zeroed and a barrier passed since).  Returns
+// min(count, max_sel), 0 for a length out of range.
+template <int KPT, int G>
+__device__ __forceinline__ int dec_choose(const Geo &g, const Ws &ws, int L, int max_seq_len, int max_sel,
+                                          const float (&sv)[KPT], const float2 (&rec)[dec_rpl<KPT>()], DecSel &ss,
+                                          DecShared<G> &sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (!(L >= 1 && L <= max_seq_len)) return 0;
+    const Ranges r = qsa_ranges(g, L);
+    const int ne = r.e_hi - r.e_lo, topk = eff_topk(g, r);
+    if (g.topk <= 0 || ne <= topk) {               // every block below the length
+        const int nb = r.b_last + 1;
+        for (int i = tid; i < nb && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+        if (tid == 0) sh.nsel = nb;
+        __syncthreads();
+    } else if (topk == 0) {                        // the forced blocks fill the count
+        const int nwin = r.b_last - r.fw + 1;
+        for (int i = tid; i < g.sink && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+        for (int i = tid; i < nwin; i += kDecThreads)
+            if (g.sink + i < kDecSelMax) sh.sel[g.sink + i] = r.fw + i;
+        if (tid == 0) sh.nsel = g.sink + nwin;
+        __syncthreads();
+    } else {
+        // the score bounds over the records of eligible blocks (16 each, from
+        // e_lo); bounds that miss some scores only make the threshold bin
+        // larger, the selection stays exact
+        const int n_rec = min(ws.nb_cap / kScoreRecBlocks, (ne + kScoreRecBlocks - 1) / kScoreRecBlocks);
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < dec_rpl<KPT>(); ++k) {
+            const bool in = lane + 64 * k < n_rec;
+            lo = in && rec[k].x < lo ? rec[k].x : lo;
+            hi = in && rec[k].y > hi ? rec[k].y : hi;
+        }
+        hi = wave_max(hi);
+        lo = -wave_max(-lo);
+        dec_select<KPT>(g, sv, r, topk, lo, hi, ss, sh);
+    }
+    return min(sh.nsel, max_sel);
+}
+
 // fp16 scale j (0 .. 4*NB-1, cell-major: cell i = j / NB, block kb = j % NB)
 // of a lane's scale vector.
 template <int NS>
@@ -336,13 +417,14 @@ __device__ __forceinline__ float scale_at(const u4v (&d)[NS], int j) {
 // ws.scores with KPT keys a thread; part 0 writes sel / nsel out).  Dynamic
 // LDS: dec_union_bytes<HD, G, MODE, TM>() for the union, then npt_lds page
 // entries (the sequence's page-table row, when parked).
-template <int HD, int G, int MODE, int KPT, int TM, bool RF>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF, bool GATH>
 __global__ void __launch_bounds__(kDecThreads)
 k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restrict__ seq_len, int32_t max_seq_len,
       int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t tpw, int32_t npt_lds) {
 #pragma clang fp contract(off)
     static_assert(G <= 16, "one matrix-core column per query head");
     static_assert(TM >= 1 && TM <= 4, "tiles a part");
+    static_assert(!GATH || (MODE != kSelect && !RF), "gathered tiles: a given selection or dense, exact values");
     using S = DecStage<HD>;
     constexpr int NB = S::NB, ND = S::ND, NS = S::NS;
     constexpr int UB = dec_union_bytes<HD, G, MODE, TM>();
@@ -369,10 +451,12 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             qv[kb][4] = b.x; qv[kb][5] = b.y; qv[kb][6] = b.z; qv[kb][7] = b.w;
         }
     }
-    const int L = seq_len[s];
-    const int32_t *prow = v.page_table + (int64_t)s * g.pps;
+    // prefill mode (gathered tiles): launch "sequence" s is query s of cache
+    // sequence pf_seq, of length pf_pos0 + s + 1
+    const int L = GATH ? seq_length(g, seq_len[g.pf ? 0 : s], s) : seq_len[s];
+    const int32_t *prow = v.page_table + (int64_t)(GATH ? cache_seq(g, s) : s) * g.pps;
     const int npt = min(g.pps, (max_seq_len + g.pt - 1) / g.pt);
-    const bool park = MODE != kDense && npt <= kDecPtLds;
+    const bool park = (MODE != kDense || GATH) && npt <= kDecPtLds;
     constexpr int PTV = kDecPtLds / (4 * kDecThreads);   // 16-byte page-table loads a thread at most
     u4v pt4[PTV];
     if (park) {                                    // entries past npt read 0 (never looked up)
@@ -382,36 +466,22 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             if (4 * kDecThreads * k < npt_lds)
                 pt4[k] = __builtin_bit_cast(u4v, BufLoad<4>::at(prs, (4 * tid + 4 * kDecThreads * k) * 4, 0));
     }
-    float sv[MODE == kSelect ? KPT : 1];
-    if constexpr (MODE == kSelect) {
-        const int base = g.sink & ~3;
-        const BufRsrc rs = buf_rsrc(ws.scores + (int64_t)pair * ws.nb_cap, (uint32_t)ws.nb_cap * 4u);
-#pragma unroll
-        for (int k = 0; k < KPT / 4; ++k) {
-            const auto x = BufLoad<4>::at(rs, (base + tid * KPT) * 4 + 16 * k, 0);
-            sv[4 * k] = x[0]; sv[4 * k + 1] = x[1]; sv[4 * k + 2] = x[2]; sv[4 * k + 3] = x[3];
-        }
-    }
-    // kSelect: the scoring launch's (min, max) records, one per kScoreRecBlocks
-    // blocks: record lane + 64 k in rec[k] (the span this instantiation
-    // selects over needs at most KPT/4 + 1 of them a lane)
-    constexpr int RPL = MODE == kSelect ? KPT / 4 + 2 : 1;
-    float2 rec[RPL];
-    if constexpr (MODE == kSelect) {
-        const int n_ch = ws.nb_cap / kScoreRecBlocks;
-        const BufRsrc rr = buf_rsrc(ws.cmm + (int64_t)pair * n_ch, (uint32_t)n_ch * 8u);
-#pragma unroll
-        for (int k = 0; k < RPL; ++k) {
-            const auto x = BufLoad<2>::at(rr, (lane + 64 * k) * 8, 0);
-            rec[k] = make_float2(x[0], x[1]);
-        }
-    }
+    // kSelect: the scores and the scoring launch's (min, max) records
+    constexpr int KS = MODE == kSelect ? KPT : 4;
+    float sv[KS];
+    float2 rec[dec_rpl<KS>()];
+    if constexpr (MODE == kSelect) dec_load_sel_inputs<KS>(g, ws, pair, sv, rec);
     int n_given = 0;
-    int32_t pre[TM];                               // kGiven: the tiles' blocks; kDense: their pages
+    // kGiven: the tiles' blocks; kDense: their pages.  GATH: the block of the
+    // lane's cell (lane & 15 of the wave's 16) in each tile
+    int32_t pre[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int tile = t_first + min(i, tpw - 1);
-        if constexpr (MODE == kGiven) {
+        if constexpr (GATH) {
+            const int slot = (tile * 64 + 16 * w + (lane & 15)) / g.bt;
+            pre[i] = MODE == kGiven ? sel[(int64_t)pair * max_sel + min(slot, max_sel - 1)] : slot;
+        } else if constexpr (MODE == kGiven) {
             pre[i] = sel[(int64_t)pair * max_sel + min(tile / tpb, max_sel - 1)];
         } else if constexpr (MODE == kDense) {
             const int64_t t0 = (int64_t)(tile / tpb) * g.bt + (tile % tpb) * 64;
@@ -421,13 +491,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         }
     }
     if constexpr (MODE == kGiven) n_given = nsel[pair];
-    if constexpr (MODE == kSelect) {               // the selection histogram starts at zero
-        u4v *h4 = reinterpret_cast<u4v *>(ss.hist);
-        const u4v z = {0u, 0u, 0u, 0u};
-        h4[tid] = z;
-        h4[tid + kDecThreads] = z;
-        if (tid < 16) h4[2 * kDecThreads + tid] = z;
-    }
+    if constexpr (MODE == kSelect) dec_zero_hist(ss);   // the selection histogram starts at zero
     // the query split: scaled by a power of two so its largest magnitude is in
     // [2^13, 2^14), then fp16 high + low parts (residual below 2^-22 of the
     // largest).  The query loads went out first, so this waits for them alone
@@ -466,51 +530,19 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     int n = 0;
     if constexpr (MODE == kSelect) {
         __syncthreads();                           // the parked page table, the zeroed histogram
-        if (ok) {
-            const Ranges r = qsa_ranges(g, L);
-            const int ne = r.e_hi - r.e_lo, topk = eff_topk(g, r);
-            if (g.topk <= 0 || ne <= topk) {       // every block below the length
-                const int nb = r.b_last + 1;
-                for (int i = tid; i < nb && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
-                if (tid == 0) sh.nsel = nb;
-                __syncthreads();
-            } else if (topk == 0) {                // the forced blocks fill the count
-                const int nwin = r.b_last - r.fw + 1;
-                for (int i = tid; i < g.sink && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
-                for (int i = tid; i < nwin; i += kDecThreads)
-                    if (g.sink + i < kDecSelMax) sh.sel[g.sink + i] = r.fw + i;
-                if (tid == 0) sh.nsel = g.sink + nwin;
-                __syncthreads();
-            } else {
-                // the score bounds over the records (a record that scored nothing
-                // is (+inf, -inf); bounds that miss some scores only make the
-                // threshold bin larger, the selection stays exact)
-                const int n_ch = ws.nb_cap / kScoreRecBlocks;
-                float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-                for (int k = 0; k < RPL; ++k) {
-                    const bool in = lane + 64 * k < n_ch;
-                    lo = in && rec[k].x < lo ? rec[k].x : lo;
-                    hi = in && rec[k].y > hi ? rec[k].y : hi;
-                }
-                hi = wave_max(hi);
-                lo = -wave_max(-lo);
-                dec_select<KPT>(g, sv, r, topk, lo, hi, ss, sh);
-            }
-            n = min(sh.nsel, max_sel);
-        }
+        n = dec_choose<KS>(g, ws, L, max_seq_len, max_sel, sv, rec, ss, sh);
         if (part == 0) {                           // the selection for the caller and the merge
             for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
             if (tid == 0) nsel[pair] = n;
         }
     } else {
-        if (MODE == kGiven) __syncthreads();       // the parked page table
+        if (MODE == kGiven || GATH) __syncthreads();   // the parked page table
         if (ok) {
             n = MODE == kDense ? (L - 1) / g.bt + 1 : n_given;
             n = n < max_sel ? n : max_sel;
         }
     }
-    const int tiles_act = n * tpb;
+    const int tiles_act = GATH ? (n * g.bt + 63) / 64 : n * tpb;
     if (!ok || t_first >= tiles_act) return;       // (uniform) no partial: the merge reads fewer parts
     const int nt = min(tpw, tiles_act - t_first);  // tiles of this part, 1 .. TM
     // ---- the tiles' pages, rows and valid cells (tiles past nt repeat the
@@ -518,8 +550,29 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     // a constant)
     int32_t tpage[TM];
     int trow[TM], tnv[TM];
+    uint32_t vm[TM];                               // GATH: valid cells of the wave's 16, bit i = cell 16w + i
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        if constexpr (GATH) {
+            // the lane's cell (lane & 15): its block's token, page and row
+            const int tile = t_first + min(i, nt - 1);
+            const int cidx = tile * 64 + 16 * w + (lane & 15);
+            const int slot = cidx / g.bt;
+            const int blk = pre[min(i, nt - 1)];
+            const int64_t t = (int64_t)blk * g.bt + cidx % g.bt;
+            const bool in = i < nt && slot < n && blk >= 0 && t < L;
+            const int tc = (int)min(max(t, (int64_t)0), (int64_t)g.pps * g.pt - 1);
+            const int32_t praw = park ? ptab[min(tc / g.pt, npt - 1)] : prow[tc / g.pt];
+            const bool pg_ok = praw >= 0 && praw < g.n_phys;
+            if (in && !pg_ok) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+            const bool valid = in && pg_ok;
+            tpage[i] = valid ? praw : 0;           // an empty cell reads page 0, row 0 (in bounds), masked
+            trow[i] = valid ? tc % g.pt : 0;
+            vm[i] = (uint32_t)__ballot(valid) & 0xffffu;
+            tnv[i] = 0;
+            continue;
+        }
+        vm[i] = 0;
         const int tile = t_first + min(i, nt - 1);
         int blk;
         if constexpr (MODE == kSelect) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
@@ -546,6 +599,27 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const uint32_t wb = __builtin_amdgcn_readfirstlane(sbase + (uint32_t)((w * TM + i) * S::BYTES));
+        if constexpr (GATH) {
+            // lane l: chunk 4j + l/16 of cell l % 16, from that cell's page and
+            // row; V in the K layout (token-major 16-byte chunks) the same way;
+            // the scale rows a 16-byte chunk of CPL cells a lane (the cells of
+            // one block: contiguous), addressed by the lane holding the first
+            const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)tpage[i] * g.page_bytes;
+            const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)tpage[i] * g.page_bytes;
+            const int64_t co = ((int64_t)(gh * (g.pt / 64) + trow[i] / 64) * ND * 64 + trow[i] % 64) * 16;
+#pragma unroll
+            for (int j = 0; j < S::NKV; ++j)
+                lds_dma16(kp + co + (int64_t)(4 * j + (lane >> 4)) * 1024, wb + S::KOFF + j * 1024);
+#pragma unroll
+            for (int j = 0; j < S::NKV; ++j)
+                lds_dma16(vp + co + (int64_t)(4 * j + (lane >> 4)) * 1024, wb + S::VOFF + j * 1024);
+            constexpr int SL = S::SROW / 16, CPL = 16 / (2 * NB);
+            const int sc = (lane < SL ? lane : lane - SL) * CPL;
+            const int32_t spg = __shfl(tpage[i], sc & 15), srw = __shfl(trow[i], sc & 15);
+            const uint8_t *sp = (const uint8_t *)(lane < SL ? v.k_pages : v.v_pages) + (int64_t)spg * g.page_bytes;
+            if (lane < 2 * SL) lds_dma16(sp + g.qbytes + (int64_t)(gh * g.pt + srw) * NB * 2, wb + S::SOFF);
+            continue;
+        }
         const int64_t pb = (int64_t)tpage[i] * g.page_bytes;
         const uint8_t *kp = (const uint8_t *)v.k_pages + pb;
         const uint8_t *vp = (const uint8_t *)v.v_pages + pb;
@@ -612,14 +686,18 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
 #pragma unroll
             for (int kb = 0; kb < NB; ++kb)
                 x = RF ? x + acc[kb][c] : __builtin_fmaf((float)dk[(c * NB + kb) / 8][(c * NB + kb) % 8], acc[kb][c], x);
-            sl[i][c] = c0 + c < tnv[i] ? x * qfac : -INFINITY;
+            const bool cv = GATH ? ((vm[i] >> (4 * lg + c)) & 1u) != 0 : c0 + c < tnv[i];
+            sl[i][c] = cv ? x * qfac : -INFINITY;
         }
         // a word holds two blocks' scales of one cell: NB / 2 words a cell
 #pragma unroll
         for (int k = 0; k < NS; ++k)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (c0 + (4 * k + e) / (NB / 2) >= tnv[i]) dvw[i][k][e] = 0u;
+            for (int e = 0; e < 4; ++e) {
+                const int cc = (4 * k + e) / (NB / 2);    // the word's cell, 0 .. 3
+                const bool cv = GATH ? ((vm[i] >> (4 * lg + cc)) & 1u) != 0 : c0 + cc < tnv[i];
+                if (!cv) dvw[i][k][e] = 0u;
+            }
         if constexpr (!RF)
 #pragma unroll
             for (int k = 0; k < NS; ++k) dmx = __builtin_elementwise_max(dmx, __builtin_bit_cast(h8v, dvw[i][k]));
@@ -684,12 +762,37 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
                 for (int c = 0; c < 4; ++c)
                     dvc[kb][c] = __builtin_bit_cast(h8v, dvw[i][(c * NB + kb) / 8])[(c * NB + kb) % 8];
         }
+        if constexpr (GATH) {
+            // V in the K layout: the A operand of block kb's MFMA j holds dims
+            // 32 kb + 2 hn + j of cells 4 lg .. +3 (rows of one q8_0 block, so
+            // the block's weights serve it), the four cells' two dims read as
+            // 16-bit words and transposed with byte permutes
 #pragma unroll
-        for (int db = 0; db < ND; ++db) {
-            h4v va = q8x4_to_h4(*reinterpret_cast<const uint32_t *>(st + S::VOFF + (16 * db + hn) * 16 + 4 * lg));
-            if constexpr (RF) va = va * dvc[db / 2];       // fp16(d * q) per element
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[RF ? 0 : db / 2], o[db], 0, 0, 0);
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[RF ? 0 : db / 2], o[db], 0, 0, 0);
+            for (int kb = 0; kb < NB; ++kb) {
+                uint32_t wv[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    wv[c] = *reinterpret_cast<const uint16_t *>(st + S::VOFF + ((2 * kb + (hn >> 3)) * 16 + 4 * lg + c) * 16 +
+                                                               2 * (hn & 7));
+                const uint32_t p01 = __builtin_amdgcn_perm(wv[1], wv[0], 0x05010400u);
+                const uint32_t p23 = __builtin_amdgcn_perm(wv[3], wv[2], 0x05010400u);
+                const uint32_t t2[2] = {__builtin_amdgcn_perm(p23, p01, 0x05040100u),
+                                        __builtin_amdgcn_perm(p23, p01, 0x07060302u)};
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const h4v va = q8x4_to_h4(t2[j]);
+                    o[2 * kb + j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[kb], o[2 * kb + j], 0, 0, 0);
+                    o[2 * kb + j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[kb], o[2 * kb + j], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int db = 0; db < ND; ++db) {
+                h4v va = q8x4_to_h4(*reinterpret_cast<const uint32_t *>(st + S::VOFF + (16 * db + hn) * 16 + 4 * lg));
+                if constexpr (RF) va = va * dvc[db / 2];       // fp16(d * q) per element
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[RF ? 0 : db / 2], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[RF ? 0 : db / 2], o[db], 0, 0, 0);
+            }
         }
     }
     const float l = col_sum4(ls);
@@ -704,10 +807,21 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     if (hn < G) {
         if (lg == 0) { sh.wml[w][hn][0] = m; sh.wml[w][hn][1] = l; }
         float *wo = wave_o(w);
+        if constexpr (GATH) {                      // o[2kb + j][r]: dim 32 kb + 8 lg + 2 r + j
 #pragma unroll
-        for (int db = 0; db < ND; ++db)
-            *reinterpret_cast<float4 *>(&wo[hn * HD + 16 * db + 4 * lg]) =
-                make_float4(o[db][0] * down, o[db][1] * down, o[db][2] * down, o[db][3] * down);
+            for (int kb = 0; kb < NB; ++kb) {
+                const f4v a = o[2 * kb], b = o[2 * kb + 1];
+                *reinterpret_cast<float4 *>(&wo[hn * HD + 32 * kb + 8 * lg]) =
+                    make_float4(a[0] * down, b[0] * down, a[1] * down, b[1] * down);
+                *reinterpret_cast<float4 *>(&wo[hn * HD + 32 * kb + 8 * lg + 4]) =
+                    make_float4(a[2] * down, b[2] * down, a[3] * down, b[3] * down);
+            }
+        } else {
+#pragma unroll
+            for (int db = 0; db < ND; ++db)
+                *reinterpret_cast<float4 *>(&wo[hn * HD + 16 * db + 4 * lg]) =
+                    make_float4(o[db][0] * down, o[db][1] * down, o[db][2] * down, o[db][3] * down);
+        }
     }
     __syncthreads();
     // thread t: head t / (HD / 4), dims 4 (t % (HD / 4)) .. +3; every wave's
@@ -744,13 +858,36 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
 }
 
+// grid (Hkv, n_seq): the selection of each (sequence, KV head) from the
+// scoring launch's scores and records, written to sel / nsel, once per pair
+// (batched decode: the attention then reads it, instead of each of its
+// workgroups selecting again).  The same selection as k_dec's kSelect mode.
+template <int KPT>
+__global__ void __launch_bounds__(kDecThreads)
+k_sel(Geo g, const int32_t *__restrict__ seq_len, int32_t max_seq_len, int32_t *__restrict__ sel,
+      int32_t *__restrict__ nsel, int32_t max_sel, Ws ws) {
+    __shared__ DecShared<1> sh;
+    __shared__ DecSel ss;
+    const int tid = threadIdx.x, gh = blockIdx.x, s = blockIdx.y;
+    const int pair = s * g.Hkv + gh;
+    float sv[KPT];
+    float2 rec[dec_rpl<KPT>()];
+    dec_load_sel_inputs<KPT>(g, ws, pair, sv, rec);
+    const int L = seq_len[s];
+    dec_zero_hist(ss);
+    __syncthreads();
+    const int n = dec_choose<KPT>(g, ws, L, max_seq_len, max_sel, sv, rec, ss, sh);
+    for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
+    if (tid == 0) nsel[pair] = n;
+}
+
 // Workgroups of one k_dec instantiation a CU holds: its register-bound
 // occupancy (looked up once per device) against the LDS its launch asks for.
 constexpr int kResDevices = 64;
 struct DecRes {
     int per_cu, cus, lds_cu, lds_static;
 };
-template <int HD, int G, int MODE, int KPT, int TM, bool RF>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF, bool GATH>
 bool dec_res(DecRes *out) {
     static std::atomic<int> cache[kResDevices][4];
     int dev = -1;
@@ -759,11 +896,11 @@ bool dec_res(DecRes *out) {
     if (c[0].load(std::memory_order_acquire) <= 0) {
         int per_cu = 0, cus = 0, lds_cu = 0;
         hipFuncAttributes fa;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT, TM, RF>, kDecThreads, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_dec<HD, G, MODE, KPT, TM, RF, GATH>, kDecThreads, 0) !=
                 hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
-            hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(k_dec<HD, G, MODE, KPT, TM, RF>)) != hipSuccess)
+            hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(k_dec<HD, G, MODE, KPT, TM, RF, GATH>)) != hipSuccess)
             return false;
         c[1].store(cus, std::memory_order_relaxed);
         c[2].store(lds_cu, std::memory_order_relaxed);
@@ -785,22 +922,22 @@ inline int dec_npt_lds(const Geo &g, int32_t max_seq_len, int mode) {
 
 // Resident workgroups of the TM instantiation at this launch's LDS (0 when
 // unknown).
-template <int HD, int G, int MODE, int KPT, int TM, bool RF>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF, bool GATH>
 int64_t dec_resident(int dyn_bytes) {
     DecRes r;
-    if (!dec_res<HD, G, MODE, KPT, TM, RF>(&r)) return 0;
+    if (!dec_res<HD, G, MODE, KPT, TM, RF, GATH>(&r)) return 0;
     int per = r.per_cu;
     const int lds = r.lds_static + dyn_bytes;
     if (r.lds_cu > 0 && lds > 0) per = std::min(per, r.lds_cu / lds);
     return (int64_t)std::max(per, 0) * r.cus;
 }
 
-template <int HD, int G, int MODE, int KPT, int TM, bool RF>
+template <int HD, int G, int MODE, int KPT, int TM, bool RF, bool GATH>
 void launch_dec_tm(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                    int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, int npt_lds,
                    int dyn, hipStream_t st) {
     const int parts = (ws.n_tiles + TM - 1) / TM;
-    QWFN_LAUNCH_SHM(kTimedAttention, (k_dec<HD, G, MODE, KPT, TM, RF>),
+    QWFN_LAUNCH_SHM(kTimedAttention, (k_dec<HD, G, MODE, KPT, TM, RF, GATH>),
                     dim3((unsigned)parts, (unsigned)g.Hkv, (unsigned)n_seq), dim3(kDecThreads), (unsigned)dyn, st,
                     g, v, q, seq_len, max_seq_len, sel, nsel, max_sel, ws, (int32_t)TM, (int32_t)npt_lds);
 }
@@ -808,54 +945,67 @@ void launch_dec_tm(const Geo &g, const qwfn_kv_view &v, const float *q, const in
 // Launches k_dec; returns the tiles a workgroup took.  One tile a workgroup
 // unless the grid would then not be resident at once (a second round of
 // workgroups starts only when the first ends): then two, else four.
-template <int HD, int G, int MODE, int KPT, bool RF>
+template <int HD, int G, int MODE, int KPT, bool RF, bool GATH>
 int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                  int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
     const int64_t pairs = (int64_t)n_seq * g.Hkv;
-    const int npt_lds = dec_npt_lds(g, max_seq_len, MODE);
+    const int npt_lds = dec_npt_lds(g, max_seq_len, GATH ? kGiven : MODE);
+    if (const char *e = std::getenv("QWFN_DEC_TM")) {   // measurement override
+        const int tm = std::atoi(e);
+        const int dd = (tm == 1 ? dec_union_bytes<HD, G, MODE, 1>() : tm == 2 ? dec_union_bytes<HD, G, MODE, 2>()
+                                                                              : dec_union_bytes<HD, G, MODE, 4>()) +
+                       4 * npt_lds;
+        if (tm == 1) { launch_dec_tm<HD, G, MODE, KPT, 1, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, dd, st); return 1; }
+        if (tm == 2) { launch_dec_tm<HD, G, MODE, KPT, 2, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, dd, st); return 2; }
+        if (tm == 4) { launch_dec_tm<HD, G, MODE, KPT, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, dd, st); return 4; }
+    }
     const int d1 = dec_union_bytes<HD, G, MODE, 1>() + 4 * npt_lds;
     const int d2 = dec_union_bytes<HD, G, MODE, 2>() + 4 * npt_lds;
     const int d4 = dec_union_bytes<HD, G, MODE, 4>() + 4 * npt_lds;
-    const int64_t r1 = dec_resident<HD, G, MODE, KPT, 1, RF>(d1);
+    const int64_t r1 = dec_resident<HD, G, MODE, KPT, 1, RF, GATH>(d1);
     if (r1 <= 0 || pairs * ws.n_tiles <= r1) {
-        launch_dec_tm<HD, G, MODE, KPT, 1, RF>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
+        launch_dec_tm<HD, G, MODE, KPT, 1, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
                                            d1, st);
         return 1;
     }
-    const int64_t r2 = dec_resident<HD, G, MODE, KPT, 2, RF>(d2);
+    const int64_t r2 = dec_resident<HD, G, MODE, KPT, 2, RF, GATH>(d2);
     if (pairs * ((ws.n_tiles + 1) / 2) <= r2) {
-        launch_dec_tm<HD, G, MODE, KPT, 2, RF>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
+        launch_dec_tm<HD, G, MODE, KPT, 2, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
                                            d2, st);
         return 2;
     }
-    launch_dec_tm<HD, G, MODE, KPT, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, d4,
+    launch_dec_tm<HD, G, MODE, KPT, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, d4,
                                        st);
     return 4;
 }
 
-template <int HD, int G, bool RF>
+template <int HD, int G, bool RF, bool GATH>
 hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                             int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                             int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
     int32_t *sl = const_cast<int32_t *>(sel), *ns = const_cast<int32_t *>(nsel);
     int tpw;
-    if (select) {
+    if constexpr (GATH) {                          // gathered tiles: a given selection or dense
+        if (select) return hipErrorInvalidValue;
+        tpw = sel ? launch_dec_t<HD, G, kGiven, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st)
+                  : launch_dec_t<HD, G, kDense, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+    } else if (select) {
         const Ranges span_r{0, 0, g.sink, max_seq_len / g.bt};
         const int span = span_r.e_hi - (span_r.e_lo & ~3);
         if (span <= 4 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 8 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 8, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 8, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 16 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 16, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 16, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else if (span <= 32 * kDecThreads)
-            tpw = launch_dec_t<HD, G, kSelect, 32, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+            tpw = launch_dec_t<HD, G, kSelect, 32, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
         else
             return hipErrorInvalidValue;
     } else if (sel) {
-        tpw = launch_dec_t<HD, G, kGiven, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+        tpw = launch_dec_t<HD, G, kGiven, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
     } else {
-        tpw = launch_dec_t<HD, G, kDense, 4, RF>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
+        tpw = launch_dec_t<HD, G, kDense, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sl, ns, max_sel, ws, st);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -869,8 +1019,25 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
 // Shapes whose fp16-rounded K/V (kv_round_f16) run here; the others take the
 // general kernel, which dequantizes each value into LDS.
 #define QWFN_FOR_EACH_DEC_RF(X) X(128, 8)
+// Shapes whose q8_0 blocks are shorter than a tile (block_tokens dividing 64)
+// run here with gathered tiles: the checkpoint's (256, 12), the tiny test
+// shape's (128, 2) and the BASELINE heads.
+#define QWFN_FOR_EACH_DEC_GATH(X) X(128, 8) X(128, 2) X(256, 12)
+
+// Blocks of bt tokens gathered into 64-cell tiles: bt divides 64, and a scale
+// row's 16-byte chunk (16 / (2 * head_dim / 32) cells) stays in one block.
+bool dec_gath(const Geo &g) {
+    if (g.vdim || g.round_f16 || g.kt != QWFN_KV_Q8_0 || g.bt < 2 || 64 % g.bt) return false;
+    const int cpl = 16 / (2 * (g.hd / 32));
+    if (cpl > 1 && g.bt % cpl) return false;
+#define X(HD_, G_) if (g.hd == HD_ && g.G == G_) return true;
+    QWFN_FOR_EACH_DEC_GATH(X)
+#undef X
+    return false;
+}
 
 bool dec_kernels_for(const Geo &g) {
+    if (dec_gath(g)) return true;
     if (!g.vdim || g.pf) return false;
     if (g.round_f16) {
 #define X(HD_, G_) if (g.hd == HD_ && g.G == G_) return true;
@@ -884,8 +1051,27 @@ bool dec_kernels_for(const Geo &g) {
     return false;
 }
 
+hipError_t launch_dec_select_once(const Geo &g, const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                                  int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
+    if (!dec_select_fits(g, max_seq_len, max_sel)) return hipErrorInvalidValue;
+    const Ranges span_r{0, 0, g.sink, max_seq_len / g.bt};
+    const int span = span_r.e_hi - (span_r.e_lo & ~3);
+    const dim3 grid((unsigned)g.Hkv, (unsigned)n_seq);
+    if (span <= 4 * kDecThreads)
+        hipLaunchKernelGGL(k_sel<4>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel, ws);
+    else if (span <= 8 * kDecThreads)
+        hipLaunchKernelGGL(k_sel<8>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel, ws);
+    else if (span <= 16 * kDecThreads)
+        hipLaunchKernelGGL(k_sel<16>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel,
+                           ws);
+    else
+        hipLaunchKernelGGL(k_sel<32>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel,
+                           ws);
+    return hipGetLastError();
+}
+
 bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel) {
-    return dec_kernels_for(g) && !g.shared && g.topk > 0 && max_sel <= kDecSelMax &&
+    return dec_kernels_for(g) && g.vdim && !g.shared && g.topk > 0 && max_sel <= kDecSelMax &&
            max_seq_len / g.bt - (g.sink & ~3) <= 32 * kDecThreads;
 }
 
@@ -893,10 +1079,19 @@ hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                                 int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {
     if (!dec_kernels_for(g) || (select && !dec_select_fits(g, max_seq_len, max_sel))) return hipErrorInvalidValue;
+    if (dec_gath(g)) {
+#define X(HD_, G_)                                                                                               \
+        if (g.hd == HD_ && g.G == G_)                                                                            \
+            return launch_dec_shape<HD_, G_, false, true>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, \
+                                                          out, ws, false, st);
+        QWFN_FOR_EACH_DEC_GATH(X)
+#undef X
+        return hipErrorInvalidValue;
+    }
     if (g.round_f16) {
 #define X(HD_, G_)                                                                                              \
         if (g.hd == HD_ && g.G == G_)                                                                           \
-            return launch_dec_shape<HD_, G_, true>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, \
+            return launch_dec_shape<HD_, G_, true, false>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, \
                                                    ws, select, st);
         QWFN_FOR_EACH_DEC_RF(X)
 #undef X
@@ -904,7 +1099,7 @@ hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float
     }
 #define X(HD_, G_)                                                                                        \
     if (g.hd == HD_ && g.G == G_)                                                                         \
-        return launch_dec_shape<HD_, G_, false>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, \
+        return launch_dec_shape<HD_, G_, false, false>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, \
                                                 ws, select, st);
     QWFN_FOR_EACH_DEC(X)
 #undef X

@@ -1263,7 +1263,9 @@ struct ScoreShared {
 // combine (c0+c1)+(c2+c3) across the j lanes and the heads sum in order, the
 // second half continuing the first's sum (so every score is bit-identical to
 // k_indexer's).  Each 128 threads write their 16 blocks' (min, max) eligible
-// score to ws.cmm (+inf, -inf when none), the attention's histogram bounds.
+// score to ws.cmm (+inf, -inf when none), the selection's histogram bounds;
+// workgroups past the eligible blocks write nothing (the selection reads the
+// records of eligible blocks only).
 template <int HD, int G>
 __global__ void __launch_bounds__(score_threads<HD>())
 k_score(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len, Ws ws,
@@ -1306,53 +1308,55 @@ k_score(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_l
 #pragma unroll
         for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
     }
+    // a workgroup whose blocks are not scored (no selection at this length, or
+    // past the eligible blocks) ends here: the selection reads the records of
+    // the eligible blocks only
+    const Ranges r = qsa_ranges(g, L);
+    const int ne = r.e_hi - r.e_lo;
+    if (!(ok && g.topk > 0 && ne > eff_topk(g, r) && c * BPW < ne)) return;
 #pragma unroll
     for (int i = 0; i < QV; ++i)
         if (tid + i * NT < G * HD / 4) reinterpret_cast<float4 *>(sh.u.q)[tid + i * NT] = qv[i];
     __syncthreads();
     float cmx = -INFINITY, cmn = INFINITY;         // this record's largest / smallest score (not NaN)
-    if (ok && g.topk > 0) {
-        const Ranges r = qsa_ranges(g, L);
-        const int ne = r.e_hi - r.e_lo;
-        if (ne > eff_topk(g, r) && c * BPW < ne) {
-            const bool act = bi < ne;
-            float acc[GH];
+    {
+        const bool act = bi < ne;
+        float acc[GH];
 #pragma unroll
-            for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
+        for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
 #pragma unroll
-            for (int i = 0; i < HD / 16; ++i) {
-#pragma unroll
-                for (int h = 0; h < GH; ++h) {
-                    const float4 q4 = *reinterpret_cast<const float4 *>(&sh.u.q[(hh * GH + h) * HD + 16 * i + 4 * j]);
-                    acc[h] = fmaf(q4.x, p4[i].x, acc[h]);
-                    acc[h] = fmaf(q4.y, p4[i].y, acc[h]);
-                    acc[h] = fmaf(q4.z, p4[i].z, acc[h]);
-                    acc[h] = fmaf(q4.w, p4[i].w, acc[h]);
-                }
-            }
-            float dots[GH];
+        for (int i = 0; i < HD / 16; ++i) {
 #pragma unroll
             for (int h = 0; h < GH; ++h) {
-                const float t01 = acc[h] + __shfl_xor(acc[h], 1);   // (c0+c1) / (c2+c3)
-                float dot = t01 + __shfl_xor(t01, 2);               // (c0+c1)+(c2+c3)
-                dots[h] = g.relu && !(dot > 0.0f) ? 0.0f : dot;
+                const float4 q4 = *reinterpret_cast<const float4 *>(&sh.u.q[(hh * GH + h) * HD + 16 * i + 4 * j]);
+                acc[h] = fmaf(q4.x, p4[i].x, acc[h]);
+                acc[h] = fmaf(q4.y, p4[i].y, acc[h]);
+                acc[h] = fmaf(q4.z, p4[i].z, acc[h]);
+                acc[h] = fmaf(q4.w, p4[i].w, acc[h]);
             }
-            // the sum of this half's heads in order; the second half (hh = 1)
-            // continues from the first half's: dot_0 + dot_1 + ... + dot_{G-1}
-            float part = dots[0];
-#pragma unroll
-            for (int h = 1; h < GH; ++h) part = part + dots[h];
-            float score = __shfl_xor(part, 4) + dots[0];
-#pragma unroll
-            for (int h = 1; h < GH; ++h) score = score + dots[h];
-            score = hh ? score : part;
-            const int b = r.e_lo + bi;
-            if (act && hh == 1 && j == 0) ws.scores[(int64_t)pair * ws.nb_cap + b] = score;
-            cmx = act && score > cmx ? score : cmx;
-            cmn = act && score < cmn ? score : cmn;
         }
+        float dots[GH];
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            const float t01 = acc[h] + __shfl_xor(acc[h], 1);   // (c0+c1) / (c2+c3)
+            float dot = t01 + __shfl_xor(t01, 2);               // (c0+c1)+(c2+c3)
+            dots[h] = g.relu && !(dot > 0.0f) ? 0.0f : dot;
+        }
+        // the sum of this half's heads in order; the second half (hh = 1)
+        // continues from the first half's: dot_0 + dot_1 + ... + dot_{G-1}
+        float part = dots[0];
+#pragma unroll
+        for (int h = 1; h < GH; ++h) part = part + dots[h];
+        float score = __shfl_xor(part, 4) + dots[0];
+#pragma unroll
+        for (int h = 1; h < GH; ++h) score = score + dots[h];
+        score = hh ? score : part;
+        const int b = r.e_lo + bi;
+        if (act && hh == 1 && j == 0) ws.scores[(int64_t)pair * ws.nb_cap + b] = score;
+        cmx = act && score > cmx ? score : cmx;
+        cmn = act && score < cmn ? score : cmn;
     }
-    // this 128-thread half's (min, max): every record of the grid is written
+    // this 128-thread half's (min, max) record
     cmx = wave_max(cmx);
     cmn = -wave_max(-cmn);
     const int w = tid >> 6;
@@ -3257,6 +3261,11 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
     // four rows of an MFMA tile after the halves are added; the softmax then
     // runs on 8 values a lane, not 16.  Else column hn is head hn (or zero).
     constexpr bool PAIR = G == 8 && NJ % 4 == 0;
+    // SPLITCOL (with PAIR): PV's 16 columns carry the weights' fp16 high
+    // halves in columns h and their low halves in columns h + 8, so one MFMA
+    // takes both (the column halves share the head's softmax state), and the
+    // two columns are added at the end
+    constexpr bool SPLITCOL = PAIR;
     constexpr int NQ = PAIR ? NJ / 2 : NJ;           // query blocks a lane holds
     constexpr int R = PAIR ? 2 : 4;                  // rows of each 16-cell tile a lane keeps
     const int jp = PAIR ? hn >> 3 : 0;
@@ -3528,14 +3537,14 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                 wave_lds_sync();
                 // ---- PV operands: the weights of head hn and the V quants this lane feeds
                 {
-                    const int hq = min(hn, G - 1);
+                    const int hq = SPLITCOL ? (hn & 7) : min(hn, G - 1);
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
                         const float4 p0 = *reinterpret_cast<const float4 *>(&W.p[hq][32 * ks + 8 * lg]);
                         const float4 p1 = *reinterpret_cast<const float4 *>(&W.p[hq][32 * ks + 8 * lg + 4]);
                         const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) pcr[ks][i] = hv ? pc[i] : 0.0f;
+                        for (int i = 0; i < 8; ++i) pcr[ks][i] = SPLITCOL || hv ? pc[i] : 0.0f;
 #pragma unroll
                         for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -3576,18 +3585,29 @@ k_pf_attn(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, const
                             blw[m] = lw;
                         }
                         const h8v bh = __builtin_bit_cast(h8v, bhw), bl = __builtin_bit_cast(h8v, blw);
+                        const h8v bs = hn >= 8 ? bl : bh;   // SPLITCOL: this lane's column half
 #pragma unroll
                         for (int db = 0; db < 2; ++db) {
                             const int dblk = 2 * j + db;
                             const h8v vh = q8x8_to_h8(vwr[ks][j][db]);
-                            o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
-                            o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                            if constexpr (SPLITCOL) {
+                                o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bs, o[dblk], 0, 0, 0);
+                            } else {
+                                o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[dblk], 0, 0, 0);
+                                o[dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[dblk], 0, 0, 0);
+                            }
                         }
                     }
                 }
             }
             wave_lds_sync();                         // the weight strip is rewritten next
         }
+    }
+    if constexpr (SPLITCOL) {                        // column h += column h + 8 (the low halves' sums)
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[d][i] += dppf<kDppRowRor8>(0.0f, o[d][i]);
     }
     if (hv) {
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;

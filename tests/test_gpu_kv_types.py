@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from _gpu import cfg_of, decode_steps, fill, kv_rows, make_pair, np_of
+from _gpu import assert_close_attn, cfg_of, decode_steps, fill, kv_rows, make_pair, np_of
 from _refs import BASELINE, TINY, Cfg
 from oracle import oracle as O
 from qwfnfer_amd import qsa, snapshot
@@ -163,6 +163,28 @@ def test_decode_steps_kv_round_f16(kt):
                  reattend=True)
     decode_steps(Cfg(**{**TINY.__dict__, "kv_type": kt, "kv_round_f16": 1}), [2000, 61], steps=2,
                  seed=1003 + kt, dtype=np.float16)
+
+
+def test_kv_round_f16_dense_and_batched_q8_0():
+    """q8_0 with kv_round_f16 on the matrix-core decode kernel's other modes:
+    the dense attention call (every block, no selection), the dense fused call
+    (top_k 0) and eight sequences of config 5's lengths (fused, then the
+    two-call path over a given selection, several tiles a workgroup)."""
+    from test_gpu_workloads import CONFIG5_LENGTHS
+    cfg = Cfg(**{**BASELINE.__dict__, "top_k_blocks": 0, "kv_round_f16": 1})
+    rng = np.random.default_rng(1020)
+    L = 4096 + 37
+    dev, host = make_pair(cfg, 1, L // 256 + 1)
+    fill(dev, host, rng, [L], pool=False)
+    q = rng.standard_normal((1, 16, 128), dtype=np.float32)
+    ws = qsa.Workspace(cfg_of(cfg), 1, L)
+    Lt = torch.tensor([L], dtype=torch.int32, device="cuda")
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), Lt, L, ws)
+    torch.cuda.synchronize()
+    assert_close_attn(np_of(out), host.attention_f64(q, [L]), "dense attention, kv_round_f16")
+    decode_steps(cfg, [4096 - 2], steps=2, seed=1021)
+    decode_steps(Cfg(**{**BASELINE.__dict__, "kv_round_f16": 1}), CONFIG5_LENGTHS, steps=2, seed=1022,
+                 modes=["fused", "two_call"], reattend=True)
 
 
 def test_kv_round_f16_changes_q8_0_outputs():

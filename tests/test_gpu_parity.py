@@ -274,6 +274,51 @@ def test_dense_attention_matches_f64(L):
     assert_close_attn(np_of(out), host.attention_f64(q, [L]), "dense attention")
 
 
+# blocks shorter than a 64-cell tile (the attention gathers 64 / block_tokens
+# blocks a tile): dense calls over every block, at lengths that end inside a
+# block and inside a tile, for the checkpoint's heads, the tiny shape and the
+# BASELINE heads at 2-, 4-, 16- and 32-token blocks (permuted pages)
+GATH_DENSE = [(G12, [1, 5, 67, 2053]), (TINY, [3, 64, 301]),
+              (Cfg(block_tokens=16, top_k_blocks=0), [17, 1000]), (Cfg(block_tokens=32, top_k_blocks=0), [95]),
+              (Cfg(block_tokens=2, top_k_blocks=0), [129])]
+
+
+@pytest.mark.parametrize("cfg,lengths", GATH_DENSE)
+def test_dense_attention_gathered_tiles(cfg, lengths):
+    cfg = Cfg(**{**cfg.__dict__, "top_k_blocks": 0})
+    rng = np.random.default_rng(255)
+    n = len(lengths)
+    pps = max(lengths) // cfg.page_tokens + 2
+    dev, host = make_pair(cfg, n, pps, seed=256)        # permuted pages
+    fill(dev, host, rng, lengths, pool=False)
+    q = rng.standard_normal((n, cfg.n_head, cfg.head_dim), dtype=np.float32)
+    L = np.array(lengths, np.int32)
+    ws = qsa.Workspace(cfg_of(cfg), n, int(L.max()))
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), torch.from_numpy(L).cuda(), int(L.max()), ws)
+    torch.cuda.synchronize()
+    assert qsa.read_status(dev) == 0
+    assert_close_attn(np_of(out), host.attention_f64(q, L), "dense attention, gathered tiles")
+
+
+def test_sparse_attention_gathered_unsorted_selection():
+    """A given selection in no particular order, with a block past the length
+    in the middle: gathered tiles mask per cell, not per prefix."""
+    cfg = TINY
+    dev, host, q, L, sel, nsel, ws = _indexer_case(cfg, [250, 77], seed=241)
+    rng = np.random.default_rng(242)
+    for s in range(len(L)):
+        for g in range(cfg.n_head_kv):
+            k = nsel[s, g]
+            row = sel[s, g, :k].copy()
+            rng.shuffle(row)
+            row[k // 2] = (L[s] - 1) // cfg.block_tokens + 1      # the block after the last: masked
+            sel[s, g, :k] = row
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), torch.from_numpy(L).cuda(), int(L.max()), ws,
+                                 torch.from_numpy(sel).cuda(), torch.from_numpy(nsel).cuda())
+    torch.cuda.synchronize()
+    assert_close_attn(np_of(out), host.attention_f64(q, L, sel, nsel), "gathered attention, shuffled selection")
+
+
 def _decode_steps(cfg, lengths, steps, seed, dtype=np.float32, zero_pooled=False):
     """Fused decode steps on a batch of sequences vs the oracle."""
     return decode_steps(cfg, lengths, steps, seed, dtype=dtype, zero_pooled=zero_pooled)

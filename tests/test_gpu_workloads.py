@@ -25,6 +25,7 @@ Selections, cache bytes and pooled keys are bit-exact; attention is within
 |o - o_ref| <= 2e-3 + 1e-3 |o_ref| of the fp64 oracle.
 """
 import math
+import time
 
 import numpy as np
 import pytest
@@ -88,7 +89,9 @@ def test_config5_batched_decode(shift):
                  reattend=True, verbose=True)
 
 
-def test_config4_prefill_chunk():
+@pytest.mark.parametrize("stride", [1])
+def test_config4_prefill_chunk(stride):
+    # stride 1: the attention of every one of the 8192 queries is checked
     cfg = BASELINE
     pre, n_q = 155648, 8192
     seq = 0
@@ -118,8 +121,9 @@ def test_config4_prefill_chunk():
     np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
     nw = max_len // bt
     np.testing.assert_array_equal(np_of(dev.pooled)[:, :, :nw], host.pooled[:, :, :nw])
-    stride = 61
+    t0 = time.perf_counter()
     hs, hn, ref = host.prefill_f64(q, seq, pre, max_sel=msel, attn_stride=stride)
+    print(f"  oracle prefill (attention stride {stride}): {time.perf_counter() - t0:.1f} s", flush=True)
     gs, gn = np_of(sel), np_of(nsel)
     np.testing.assert_array_equal(gn, hn)
     bad = [(i, g) for i in range(n_q) for g in range(cfg.n_head_kv)
