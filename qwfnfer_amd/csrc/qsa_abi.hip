@@ -7,7 +7,6 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
-#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -495,21 +494,6 @@ int qwfn_decode_append_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *v
     return e == hipSuccess ? ok() : hip_fail(e, "append_select");
 }
 
-}  // extern "C"
-
-namespace {
-// Sequences from which a decode step selects once per (sequence, KV head) in
-// a launch of its own (QWFN_SEL_ONCE_MIN overrides, for measurement).
-int32_t sel_once_min_seqs() {
-    static const int32_t v = [] {
-        const char *e = std::getenv("QWFN_SEL_ONCE_MIN");
-        return e ? std::atoi(e) : 2;
-    }();
-    return v;
-}
-}  // namespace
-
-extern "C" {
 
 int qwfn_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const float *q,
                             const void *k_new, const void *v_new, int32_t src_dtype,
@@ -546,12 +530,11 @@ int qwfn_sparse_attn_decode_chain(const qwfn_qsa_shape *shape, const qwfn_kv_vie
     // position k's lengths: seq_len + k (the first position reads seq_len itself)
     hipError_t e = n_pos > 1 ? launch_chain_lens(seq_len, n_seq, n_pos, w.lens, st) : hipSuccess;
     if (e != hipSuccess) return hip_fail(e, "decode: chain lengths");
-    // several sequences: one selection launch per (sequence, KV head), then the
-    // attention over it; one sequence: the attention workgroups select for
-    // themselves (no launch between the scores and the attention)
-    const bool once = n_seq >= sel_once_min_seqs() && dec_kernels_for(g) && !g.shared && g.topk > 0 && !g.pf &&
-                      dec_select_fits(g, max_seq_len, msel);
-    const bool own = !once && attn_select_fits(g, n_seq, max_seq_len, msel);
+    // one or a few sequences: the attention workgroups select for themselves
+    // (no launch between the scores and the attention; at eight sequences a
+    // selection launch of one workgroup per (sequence, KV head) before a
+    // given-selection attention measured 29.4 against 26.9 us a step)
+    const bool own = attn_select_fits(g, n_seq, max_seq_len, msel);
     const size_t row_b = (size_t)g.hd * (src_dtype == QWFN_SRC_F32 ? 4 : 2);
     for (int32_t k = 0; k < n_pos; ++k) {
         const int32_t *len_k = k == 0 ? seq_len : w.lens + (size_t)k * n_seq;
@@ -562,12 +545,8 @@ int qwfn_sparse_attn_decode_chain(const qwfn_qsa_shape *shape, const qwfn_kv_vie
         float *out_k = out + (size_t)k * n_seq * g.H * g.hd;
         int32_t *sel = sel_out ? sel_out + (size_t)k * n_seq * g.Hkv * msel : w.sel;
         int32_t *nsel = n_sel_out ? n_sel_out + (size_t)k * n_seq * g.Hkv : w.nsel;
-        e = launch_indexer(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, w, fa, st, !(own || once));
+        e = launch_indexer(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, w, fa, st, !own);
         if (e != hipSuccess) return hip_fail(e, "decode: indexer");
-        if (once) {
-            e = launch_dec_select_once(g, len_k, n_seq, max_seq_len, sel, nsel, msel, w, st);
-            if (e != hipSuccess) return hip_fail(e, "decode: selection");
-        }
         e = own ? launch_attention_select(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, out_k, w, st)
                 : launch_attention(g, *view, q_k, len_k, n_seq, max_seq_len, sel, nsel, msel, out_k, w, st);
         if (e != hipSuccess) return hip_fail(e, "decode: attention");

@@ -36,7 +36,6 @@
 
 #include <algorithm>
 #include <atomic>
-#include <cstdlib>
 
 #include "qsa_device.h"
 
@@ -858,29 +857,6 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
 }
 
-// grid (Hkv, n_seq): the selection of each (sequence, KV head) from the
-// scoring launch's scores and records, written to sel / nsel, once per pair
-// (batched decode: the attention then reads it, instead of each of its
-// workgroups selecting again).  The same selection as k_dec's kSelect mode.
-template <int KPT>
-__global__ void __launch_bounds__(kDecThreads)
-k_sel(Geo g, const int32_t *__restrict__ seq_len, int32_t max_seq_len, int32_t *__restrict__ sel,
-      int32_t *__restrict__ nsel, int32_t max_sel, Ws ws) {
-    __shared__ DecShared<1> sh;
-    __shared__ DecSel ss;
-    const int tid = threadIdx.x, gh = blockIdx.x, s = blockIdx.y;
-    const int pair = s * g.Hkv + gh;
-    float sv[KPT];
-    float2 rec[dec_rpl<KPT>()];
-    dec_load_sel_inputs<KPT>(g, ws, pair, sv, rec);
-    const int L = seq_len[s];
-    dec_zero_hist(ss);
-    __syncthreads();
-    const int n = dec_choose<KPT>(g, ws, L, max_seq_len, max_sel, sv, rec, ss, sh);
-    for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
-    if (tid == 0) nsel[pair] = n;
-}
-
 // Workgroups of one k_dec instantiation a CU holds: its register-bound
 // occupancy (looked up once per device) against the LDS its launch asks for.
 constexpr int kResDevices = 64;
@@ -944,21 +920,13 @@ void launch_dec_tm(const Geo &g, const qwfn_kv_view &v, const float *q, const in
 
 // Launches k_dec; returns the tiles a workgroup took.  One tile a workgroup
 // unless the grid would then not be resident at once (a second round of
-// workgroups starts only when the first ends): then two, else four.
+// workgroups starts only when the first ends): then two, or four when two do
+// not fit either and four keep more tiles resident.
 template <int HD, int G, int MODE, int KPT, bool RF, bool GATH>
 int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                  int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
     const int64_t pairs = (int64_t)n_seq * g.Hkv;
     const int npt_lds = dec_npt_lds(g, max_seq_len, GATH ? kGiven : MODE);
-    if (const char *e = std::getenv("QWFN_DEC_TM")) {   // measurement override
-        const int tm = std::atoi(e);
-        const int dd = (tm == 1 ? dec_union_bytes<HD, G, MODE, 1>() : tm == 2 ? dec_union_bytes<HD, G, MODE, 2>()
-                                                                              : dec_union_bytes<HD, G, MODE, 4>()) +
-                       4 * npt_lds;
-        if (tm == 1) { launch_dec_tm<HD, G, MODE, KPT, 1, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, dd, st); return 1; }
-        if (tm == 2) { launch_dec_tm<HD, G, MODE, KPT, 2, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, dd, st); return 2; }
-        if (tm == 4) { launch_dec_tm<HD, G, MODE, KPT, 4, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds, dd, st); return 4; }
-    }
     const int d1 = dec_union_bytes<HD, G, MODE, 1>() + 4 * npt_lds;
     const int d2 = dec_union_bytes<HD, G, MODE, 2>() + 4 * npt_lds;
     const int d4 = dec_union_bytes<HD, G, MODE, 4>() + 4 * npt_lds;
@@ -968,8 +936,12 @@ int launch_dec_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int3
                                            d1, st);
         return 1;
     }
+    // a grid larger than the device holds: two tiles a workgroup unless four
+    // keep more tiles in flight (measured: the checkpoint's prefill attention
+    // 10.6 ms at two, 11.8 at four, where four leave one wave a SIMD)
     const int64_t r2 = dec_resident<HD, G, MODE, KPT, 2, RF, GATH>(d2);
-    if (pairs * ((ws.n_tiles + 1) / 2) <= r2) {
+    const int64_t r4 = dec_resident<HD, G, MODE, KPT, 4, RF, GATH>(d4);
+    if (pairs * ((ws.n_tiles + 1) / 2) <= r2 || 2 * r2 >= 4 * r4) {
         launch_dec_tm<HD, G, MODE, KPT, 2, RF, GATH>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, npt_lds,
                                            d2, st);
         return 2;
@@ -1049,25 +1021,6 @@ bool dec_kernels_for(const Geo &g) {
     QWFN_FOR_EACH_DEC(X)
 #undef X
     return false;
-}
-
-hipError_t launch_dec_select_once(const Geo &g, const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
-                                  int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st) {
-    if (!dec_select_fits(g, max_seq_len, max_sel)) return hipErrorInvalidValue;
-    const Ranges span_r{0, 0, g.sink, max_seq_len / g.bt};
-    const int span = span_r.e_hi - (span_r.e_lo & ~3);
-    const dim3 grid((unsigned)g.Hkv, (unsigned)n_seq);
-    if (span <= 4 * kDecThreads)
-        hipLaunchKernelGGL(k_sel<4>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel, ws);
-    else if (span <= 8 * kDecThreads)
-        hipLaunchKernelGGL(k_sel<8>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel, ws);
-    else if (span <= 16 * kDecThreads)
-        hipLaunchKernelGGL(k_sel<16>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel,
-                           ws);
-    else
-        hipLaunchKernelGGL(k_sel<32>, grid, dim3(kDecThreads), 0, st, g, seq_len, max_seq_len, sel, nsel, max_sel,
-                           ws);
-    return hipGetLastError();
 }
 
 bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel) {

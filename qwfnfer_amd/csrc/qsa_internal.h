@@ -218,11 +218,6 @@ hipError_t launch_merge(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_
 // blocks and 1024 selected.
 bool dec_kernels_for(const Geo &g);
 bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
-// The same selection once per (sequence, KV head), from a scores-only
-// indexer launch, into sel / nsel (k_sel; dec_select_fits shapes), for the
-// attention to read as a given selection.
-hipError_t launch_dec_select_once(const Geo &g, const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
-                                  int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws, hipStream_t st);
 hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                                 int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st);
