@@ -801,8 +801,9 @@ def main():
                                   kernel_us={k: round(v, 3) for k, v in kern.items()},
                                   cells_per_layer=cells, selected_kv_bytes=kv,
                                   attn_gbs=round(kv / (kern["attention"] * 1e-6) / 1e9, 1), replicas=r.n_inst)
-            kv_types[name]["attention_kernel"] = ("k_dec (q8_0 on the matrix cores, K/V rounded to fp16 in "
-                                                  "registers)" if rf else "k_attn (the general attention kernel)")
+            kv_types[name]["attention_kernel"] = (
+                "k_dec (q8_0 on the matrix cores, K/V rounded to fp16 in registers)" if rf else
+                f"k_dec ({name} rows in the K layout on the matrix cores, read a cell at a time)")
             if rf:
                 kv_types[name]["max_abs_delta_vs_exact"] = round_f16_delta(qsa, torch, r)
             log(f"[bench] kv {name} ctx {ctx}: {ms * 1e3 / args.layers:.2f} us/layer, indexer "

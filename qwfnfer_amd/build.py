@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libqwfn_qsa.so")
-SOURCES = ["qsa_kernels.hip", "qsa_decode.hip", "qsa_idx.hip", "qsa_abi.hip"]
+SOURCES = ["qsa_kernels.hip", "qsa_decode.hip", "qsa_decode_kv.hip", "qsa_idx.hip", "qsa_abi.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: v_pk_{add,mul,fma}_f32 are never emitted.

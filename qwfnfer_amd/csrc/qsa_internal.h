@@ -217,6 +217,12 @@ hipError_t launch_merge(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_
 // merge.  dec_select_fits: per-head selections of at most 8192 eligible
 // blocks and 1024 selected.
 bool dec_kernels_for(const Geo &g);
+// q4_0 / F16 caches (qsa_decode_kv.hip): a shape with instantiations, and the
+// attention with its merge, as launch_dec_attention
+bool dec_kv_shape(const Geo &g);
+hipError_t launch_dec_kv(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
+                         int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
+                         const Ws &ws, bool select, hipStream_t st);
 bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
 hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,

@@ -79,7 +79,7 @@ def assert_close_attn(got: np.ndarray, ref: np.ndarray, what: str = ""):
     """The acceptance bound: |o - o_ref| <= 2e-3 + 1e-3 |o_ref| elementwise."""
     err = np.abs(got.astype(np.float64) - ref)
     bound = 2e-3 + 1e-3 * np.abs(ref)
-    bad = err > bound
+    bad = ~(err <= bound)                     # a NaN or inf output (NaN error) fails too
     assert not bad.any(), (f"{what}: {bad.sum()} elements out of tolerance, max abs err "
                            f"{err.max():.3g}, max rel {np.max(err / np.maximum(np.abs(ref), 1e-30)):.3g}")
     return float(err.max())

@@ -201,3 +201,96 @@ def test_kv_round_f16_changes_q8_0_outputs():
     d = np.abs(outs[0] - outs[1])
     print(f"max |o(kv_round_f16) - o(exact)| = {d.max():.3g}", flush=True)
     assert d.max() > 0
+
+
+@pytest.mark.parametrize("kt", [0, 1, 2])
+def test_decode_independent_of_the_workspace_history(kt):
+    """Layers sharing one workspace, as the bench's replicas do: a layer's
+    fused step gives the same bytes whatever call used the workspace before
+    it (here another layer of a different length), at a context whose
+    selection holds 16 keys a thread; and a hipGraph replay of the step
+    equals the eager one."""
+    cfg = qsa.QsaConfig(kv_type=kt)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(90 + kt)
+    lens = [140000, 90000]
+    max_len = 140000 + 8
+    pps = max_len // cfg.page_tokens + 1
+    caches = []
+    for L in lens:
+        c = qsa.KvCache.allocate(cfg, 1, pps)
+        for t0 in range(0, L, 32768):
+            n = min(32768, L - t0)
+            k = torch.randn((n, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
+            v = torch.randn((n, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen)
+            qsa.append_q8_0(c, k, v, torch.arange(t0, t0 + n, dtype=torch.int32, device="cuda"))
+        qsa.pool_rebuild(c, 0, L // cfg.block_tokens)
+        caches.append(c)
+    ws = qsa.Workspace(cfg, 1, max_len)
+    q = [torch.randn((1, cfg.n_head, cfg.head_dim), device="cuda", generator=gen) for _ in lens]
+    kn = [torch.randn((1, cfg.n_head_kv, cfg.head_dim), device="cuda", generator=gen) for _ in lens]
+    sl = [torch.tensor([L + 1], dtype=torch.int32, device="cuda") for L in lens]
+    outs = [torch.empty((1, cfg.n_head, cfg.head_dim), device="cuda") for _ in lens]
+
+    def step(i):
+        qsa.sparse_attn_decode(caches[i], q[i], kn[i], kn[i], sl[i], max_len, ws, out=outs[i])
+
+    step(0)
+    torch.cuda.synchronize()
+    ref = outs[0].clone()
+    for order in ([1, 0], [0, 1, 0], [1, 1, 0]):
+        for i in order:
+            step(i)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], ref), f"kv_type {kt}: layer 0 after {order} differs"
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(1)
+            step(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        outs[0].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], ref), f"kv_type {kt}: graph replay {rep} differs"
+        step(0)
+        torch.cuda.synchronize()
+
+
+def test_q4_0_negative_scale_dominant_cell():
+    """ggml's q4_0 scale is signed (d = max / -8, max the element of largest
+    magnitude): a cell whose V blocks have large negative scales and which
+    takes nearly all the softmax weight, among cells of small positive
+    scales.  The attention's weight range must follow the scales' magnitudes
+    (a range set by the largest positive scale overflows fp16 here)."""
+    cfg = Cfg(**{**BASELINE.__dict__, "kv_type": 1, "top_k_blocks": 0})
+    rng = np.random.default_rng(1030)
+    L = 200
+    k = rng.standard_normal((L, cfg.n_head_kv, cfg.head_dim)).astype(np.float32) * 0.05
+    v = rng.standard_normal((L, cfg.n_head_kv, cfg.head_dim)).astype(np.float32)
+    blocks = v.reshape(L, cfg.n_head_kv, cfg.head_dim // 32, 32)
+    # every block's element of largest magnitude negative (d > 0), small
+    idx = np.abs(blocks).argmax(-1)
+    np.put_along_axis(blocks, idx[..., None], -np.abs(np.take_along_axis(blocks, idx[..., None], -1)) - 1.0, -1)
+    blocks *= 0.1
+    hot = [7, 131]
+    for t in hot:                              # large positive maxima: d < 0, |d| 1000x the others
+        blocks[t] = np.abs(blocks[t]) * 1000.0
+    q = np.zeros((1, cfg.n_head, cfg.head_dim), np.float32)
+    for g in range(cfg.n_head_kv):
+        q[0, g * cfg.group:(g + 1) * cfg.group] = k[hot[g], g] * 400.0
+    dev, host = make_pair(cfg, 1, 1)
+    pos = np.arange(L, dtype=np.int32)
+    assert host.append(k, v, pos) == 0
+    qsa.append_q8_0(dev, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), torch.from_numpy(pos).cuda())
+    Lt = torch.tensor([L], dtype=torch.int32, device="cuda")
+    ws = qsa.Workspace(cfg_of(cfg), 1, L)
+    out = qsa.sparse_decode_attn(dev, torch.from_numpy(q).cuda(), Lt, L, ws)
+    torch.cuda.synchronize()
+    got = np_of(out)
+    assert np.isfinite(got).all(), "non-finite attention output"
+    assert_close_attn(got, host.attention_f64(q, [L]), "q4_0, negative scales dominating")
