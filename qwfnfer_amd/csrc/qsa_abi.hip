@@ -630,7 +630,12 @@ int qwfn_qsa_prefill_workspace_bytes(const qwfn_qsa_shape *shape, int32_t max_se
         return fail(QWFN_EINVAL, "prefill_workspace_bytes: bytes NULL or max_seq_len / q_batch < 1");
     // no completion counters: a batch is one grid dimension of every launch
     if (q_batch > kPrefillBatchMax) return fail(QWFN_ERANGE, "q_batch %d exceeds %d", q_batch, kPrefillBatchMax);
-    *bytes = ws_layout(g, q_batch, max_seq_len, max_selected(shape, max_seq_len), !g.vdim, false).total;
+    Geo gpf = g;
+    gpf.pf = 1;
+    gpf.round_f16 = 0;
+    const int32_t need = max_selected(shape, max_seq_len);
+    const bool parts = !g.vdim && !dec_loop_fits(gpf, need);   // as prefill_impl lays it out
+    *bytes = ws_layout(g, q_batch, max_seq_len, need, parts, false).total;
     return ok();
 }
 
@@ -676,7 +681,13 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
     const int32_t sel_stride = sel_out ? max_sel : need;
     // the largest query batch whose workspace fits
     if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "prefill: workspace NULL or not 256-byte aligned");
-    const bool parts = !g.vdim;                    // the general kernel merges partials in memory
+    Geo gpf = g;
+    gpf.pf = 1;
+    gpf.round_f16 = 0;
+    // the K layouts' attention walks each query's tiles in one workgroup
+    // (k_dec_loop); the general kernel merges partials in memory
+    const bool loop = !g.vdim && dec_loop_fits(gpf, sel_stride);
+    const bool parts = !g.vdim && !loop;
     int32_t batch = std::min<int32_t>(n_q, kPrefillBatchMax);
     while (batch > 1 && ws_layout(g, batch, max_len, need, parts, false).total > ws_bytes) batch = (batch + 1) / 2;
     if (ws_layout(g, batch, max_len, need, parts, false).total > ws_bytes)
@@ -710,7 +721,7 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
     gp.pf = 1;
     gp.pf_seq = seq;
     gp.round_f16 = 0;                              // prefill reads the exact rows (kv_round_f16 is decode's)
-    if (g.vdim) {
+    if (g.vdim || (loop && g.kt != QWFN_KV_F16)) {
         e = launch_prefill_vmax(gp, *view, max_len, w.vmax, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: V scales");
     }
@@ -734,6 +745,7 @@ int prefill_impl(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const Id
         }
         if (e != hipSuccess) return hip_fail(e, "prefill: indexer");
         e = g.vdim ? launch_prefill_attention(gp, *view, qb, nb, sb, nsb, sel_stride, w.vmax, ob, st)
+            : loop ? launch_dec_loop(gp, *view, qb, nb, max_len, sb, nsb, sel_stride, w.vmax, ob, st)
                    : launch_attention(gp, *view, qb, dummy_len, nb, max_len, sb, nsb, sel_stride, ob, w, st);
         if (e != hipSuccess) return hip_fail(e, "prefill: attention");
     }

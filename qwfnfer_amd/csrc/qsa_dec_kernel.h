@@ -957,6 +957,372 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
 }
 
+// Prefill attention over a given per-query selection for the K layouts (LY
+// != kLyQ8): grid (1, Hkv, n_q), one workgroup per (query, KV head) walking
+// all of its 64-cell tiles, two staging slots a wave (tile t + 1's transfers
+// in flight while tile t is computed), an online softmax per column across
+// the tiles, and the four waves' states combined into the normalised output
+// (no partials, no merge launch).  The tile math is k_dec's: QK with the
+// query as fp16 hi + lo against exact fp16 keys, PV with the weights p * d_v *
+// 2^kup as fp16 hi + lo against exact fp16 values; kup is fixed per KV head
+// and call from the largest V-scale magnitude (vmax, k_pf_vmax's partial
+// maxima; F16 has no scales: 2^15), so O needs no rescaling beyond the
+// softmax's.  The selection row and the sequence's page-table row are parked
+// in LDS.  Dynamic LDS: dec_loop_bytes<HD, G, LY>(), then npt_lds entries.
+template <int HD, int G, int LY>
+constexpr int dec_loop_bytes() {
+    constexpr int st = 2 * kDecWaves * DecStage<HD, LY>::BYTES;
+    constexpr int wo = kDecWaves * G * HD * 4;
+    return ((st > wo ? st : wo) + 15) / 16 * 16;
+}
+
+template <int HD, int G, int LY>
+__global__ void __launch_bounds__(kDecThreads)
+k_dec_loop(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t max_seq_len, const int32_t *__restrict__ sel,
+           const int32_t *__restrict__ nsel, int32_t max_sel, const float *__restrict__ vmax, float *__restrict__ out,
+           int32_t npt_lds) {
+#pragma clang fp contract(off)
+    constexpr bool Q4 = LY == kLyQ4, F16 = LY == kLyF16;
+    static_assert(LY != kLyQ8, "V in the K layout");
+    static_assert(G <= 16, "one matrix-core column per query head");
+    using S = DecStage<HD, LY>;
+    constexpr int NB = S::NB, ND = S::ND, NS = S::NS;
+    constexpr int UB = dec_loop_bytes<HD, G, LY>();
+    __shared__ DecShared<G> sh;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dec_dyn[];
+    int32_t *ptab = reinterpret_cast<int32_t *>(dec_dyn + UB);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hn = lane & 15, lg = lane >> 4;
+    const int gh = blockIdx.y, s = blockIdx.z;
+    const int pair = s * g.Hkv + gh;
+    // ---- first round trip: query rows, page-table row, selection row, V-scale maxima
+    const int hq = min(hn, G - 1);
+    float qv[NB][8];
+    {
+        const float *qh = q + ((int64_t)s * g.H + (int64_t)gh * G + hq) * HD + (Q4 ? 4 : 8) * lg;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            const float4 a = *reinterpret_cast<const float4 *>(qh + 32 * kb);
+            const float4 b = *reinterpret_cast<const float4 *>(qh + 32 * kb + (Q4 ? 16 : 4));
+            qv[kb][0] = a.x; qv[kb][1] = a.y; qv[kb][2] = a.z; qv[kb][3] = a.w;
+            qv[kb][4] = b.x; qv[kb][5] = b.y; qv[kb][6] = b.z; qv[kb][7] = b.w;
+        }
+    }
+    const int L = seq_length(g, 0, s);
+    const int32_t *prow = v.page_table + (int64_t)cache_seq(g, s) * g.pps;
+    const int npt = min(g.pps, (max_seq_len + g.pt - 1) / g.pt);
+    const bool park = npt <= kDecPtLds;
+    constexpr int PTV = kDecPtLds / (4 * kDecThreads);
+    u4v pt4[PTV];
+    if (park) {
+        const BufRsrc prs = buf_rsrc(prow, (uint32_t)npt * 4u);
+#pragma unroll
+        for (int k = 0; k < PTV; ++k)
+            if (4 * kDecThreads * k < npt_lds)
+                pt4[k] = __builtin_bit_cast(u4v, BufLoad<4>::at(prs, (4 * tid + 4 * kDecThreads * k) * 4, 0));
+    }
+    constexpr int SLV = kDecSelMax / kDecThreads;   // selection entries a thread parks
+    int32_t sl4[SLV];
+    {
+        const BufRsrc srs = buf_rsrc(sel + (int64_t)pair * max_sel, (uint32_t)max_sel * 4u);
+#pragma unroll
+        for (int k = 0; k < SLV; ++k)
+            sl4[k] = __builtin_bit_cast(int32_t, BufLoad<1>::at(srs, (tid + kDecThreads * k) * 4, 0)[0]);
+    }
+    const int n_raw = nsel[pair];
+    float kup = 15.0f;                             // F16: the weights p <= 1 alone
+    if constexpr (!F16) {
+        float dvm = vmax[gh * kVmaxWg + lane % kVmaxWg];
+        dvm = wave_max(dvm);
+        int e2 = 0;
+        frexpf(dvm, &e2);
+        kup = dvm > 0.0f ? (float)(15 - e2) : 0.0f;
+    }
+    const float up = ldexpf(1.0f, (int)kup), down = ldexpf(1.0f, -(int)kup);
+    // ---- the query split (as k_dec)
+    h8v qhi[NB], qlo[NB];
+    float qfac;
+    {
+        float a = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(qv[kb][e]));
+        a = col_max4(a);
+        int ex = 0;
+        frexpf(a, &ex);
+        const float qup = a > 0.0f ? ldexpf(1.0f, 14 - ex) : 1.0f;
+        qfac = (a > 0.0f ? ldexpf(1.0f, ex - 14) : 1.0f) * g.scale_log2;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qv[kb][e] * qup;
+                const _Float16 h = (_Float16)x;
+                qhi[kb][e] = h;
+                qlo[kb][e] = (_Float16)(x - (float)h);
+            }
+    }
+    if (park) {
+#pragma unroll
+        for (int k = 0; k < PTV; ++k)
+            if (4 * tid + 4 * kDecThreads * k < npt_lds)
+                *reinterpret_cast<u4v *>(&ptab[4 * tid + 4 * kDecThreads * k]) = pt4[k];
+    }
+#pragma unroll
+    for (int k = 0; k < SLV; ++k) sh.sel[tid + kDecThreads * k] = sl4[k];
+    __syncthreads();
+    const bool ok = L >= 1 && L <= max_seq_len;
+    const int n = ok ? min(n_raw, max_sel) : 0;
+    const int tiles = (n * g.bt + 63) / 64;
+    // ---- the lane's cell (lane & 15 of the wave's 16) of tile t: page, row, validity
+    auto cell_of = [&](int t, int32_t &page, int &row) -> bool {
+        const int cidx = t * 64 + 16 * w + (lane & 15);
+        const int slot = cidx / g.bt;
+        const int blk = sh.sel[min(slot, kDecSelMax - 1)];
+        const int64_t tt = (int64_t)blk * g.bt + cidx % g.bt;
+        const bool in = slot < n && blk >= 0 && tt < L;
+        const int tc = (int)min(max(tt, (int64_t)0), (int64_t)g.pps * g.pt - 1);
+        const int32_t praw = park ? ptab[min(tc / g.pt, npt - 1)] : prow[tc / g.pt];
+        const bool pg_ok = praw >= 0 && praw < g.n_phys;
+        if (in && !pg_ok) set_status(v.status, QWFN_STATUS_PAGE_RANGE);
+        const bool valid = in && pg_ok;
+        page = valid ? praw : 0;
+        row = valid ? tc % g.pt : 0;
+        return valid;
+    };
+    const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dec_dyn);
+    // tile t's transfers into slot b: NL of them, as k_dec's gathered tiles
+    auto issue = [&](int b, int32_t page, int row) {
+        const uint32_t wb = __builtin_amdgcn_readfirstlane(sbase + (uint32_t)((w * 2 + b) * S::BYTES));
+        const uint8_t *kp = (const uint8_t *)v.k_pages + (int64_t)page * g.page_bytes;
+        const uint8_t *vp = (const uint8_t *)v.v_pages + (int64_t)page * g.page_bytes;
+        const int64_t co = ((int64_t)(gh * (g.pt / 64) + row / 64) * S::CH * 64 + row % 64) * 16;
+#pragma unroll
+        for (int j = 0; j < S::NKV; ++j)
+            lds_dma16(kp + co + (int64_t)(4 * j + (lane >> 4)) * 1024, wb + S::KOFF + j * 1024);
+#pragma unroll
+        for (int j = 0; j < S::NKV; ++j)
+            lds_dma16(vp + co + (int64_t)(4 * j + (lane >> 4)) * 1024, wb + S::VOFF + j * 1024);
+        if constexpr (S::SROW > 0) {
+            constexpr int SL = S::SROW / 16, CPL = 16 / (2 * NB);
+            const int sc = (lane < SL ? lane : lane - SL) * CPL;
+            const int32_t spg = __shfl(page, sc & 15), srw = __shfl(row, sc & 15);
+            const uint8_t *sp = (const uint8_t *)(lane < SL ? v.k_pages : v.v_pages) + (int64_t)spg * g.page_bytes;
+            if (lane < 2 * SL) lds_dma16(sp + g.qbytes + (int64_t)(gh * g.pt + srw) * NB * 2, wb + S::SOFF);
+        }
+    };
+    float m = -1e30f, ls = 0.0f;                   // running column max (finite floor) and the lane's sum
+    f4v o[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) o[db] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    int32_t pg_n = 0;
+    int rw_n = 0;
+    bool va_n = false;
+    if (tiles > 0) {
+        va_n = cell_of(0, pg_n, rw_n);
+        issue(0, pg_n, rw_n);
+    }
+#pragma unroll 1
+    for (int t = 0; t < tiles; ++t) {
+        const uint32_t vm = (uint32_t)__ballot(va_n) & 0xffffu;   // this tile's valid cells of the wave
+        if (t + 1 < tiles) {
+            va_n = cell_of(t + 1, pg_n, rw_n);
+            issue((t + 1) & 1, pg_n, rw_n);
+            wait_vmcnt<S::NL>();                   // tile t has landed (transfers retire in order)
+        } else {
+            wait_vmcnt<0>();
+        }
+        const uint8_t *st = dec_dyn + (w * 2 + (t & 1)) * S::BYTES;
+        // ---- QK
+        f4v acc[NB];
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            h8v ka;
+            if constexpr (F16) {
+                ka = __builtin_bit_cast(h8v, *reinterpret_cast<const u4v *>(st + S::KOFF + (4 * kb + lg) * 256 + hn * 16));
+            } else if constexpr (Q4) {
+                const uint32_t kw = *reinterpret_cast<const uint32_t *>(st + S::KOFF + kb * 256 + hn * 16 + 4 * lg);
+                const h4v a = q4x4_to_h4(kw & 0x0f0f0f0fu), b = q4x4_to_h4((kw >> 4) & 0x0f0f0f0fu);
+                ka = h8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+            } else {
+                const u2v kw = *reinterpret_cast<const u2v *>(st + S::KOFF + (2 * kb + (lg >> 1)) * 256 + hn * 16 +
+                                                              8 * (lg & 1));
+                ka = q8x8_to_h8(make_uint2(kw[0], kw[1]));
+            }
+            acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[kb], f4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[kb], acc[kb], 0, 0, 0);
+        }
+        h8v dk[NS];
+        u4v dvw[NS];
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            if constexpr (F16) {
+                dk[k] = h8v{};
+                dvw[k] = u4v{0u, 0u, 0u, 0u};
+            } else {
+                dk[k] = __builtin_bit_cast(h8v, *reinterpret_cast<const u4v *>(st + S::SOFF + 4 * lg * NB * 2 + 16 * k));
+                dvw[k] = *reinterpret_cast<const u4v *>(st + S::SOFF + S::SROW + 4 * lg * NB * 2 + 16 * k);
+            }
+        }
+        float sl[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float x = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb)
+                x = F16 ? x + acc[kb][c] : __builtin_fmaf((float)dk[(c * NB + kb) / 8][(c * NB + kb) % 8], acc[kb][c], x);
+            sl[c] = ((vm >> (4 * lg + c)) & 1u) ? x * qfac : -INFINITY;
+        }
+        if constexpr (!F16) {
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (!((vm >> (4 * lg + (4 * k + e) / (NB / 2))) & 1u)) dvw[k][e] = 0u;
+        }
+        // ---- online softmax of column hn
+        const float tm = col_max4(fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3])));
+        const float m_new = fmaxf(m, tm);
+        const float alpha = fast_exp2(m - m_new);
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int db = 0; db < ND; ++db) o[db] *= alpha;
+        }
+        ls *= alpha;
+        m = m_new;
+        float pu[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float p = sl[c] == -INFINITY ? 0.0f : fast_exp2(sl[c] - m);
+            ls += p;
+            pu[c] = p * up;
+        }
+        // ---- PV
+        constexpr int NW = F16 ? 1 : NB;
+        h4v bhi[NW], blo[NW];
+#pragma unroll
+        for (int kb = 0; kb < NW; ++kb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float dv = 1.0f;
+                if constexpr (!F16) {
+                    const h8v dw = __builtin_bit_cast(h8v, dvw[(c * NB + kb) / 8]);
+                    dv = (float)dw[(c * NB + kb) % 8];
+                }
+                const _Float16 h = (_Float16)__builtin_fmaf(pu[c], dv, 0.0f);
+                bhi[kb][c] = h;
+                blo[kb][c] = (_Float16)__builtin_fmaf(pu[c], dv, -(float)h);
+            }
+        if constexpr (F16) {
+            const uint32_t vb = vm >> (4 * lg);
+            const uint32_t m01 = ((vb & 1u) ? 0x0000ffffu : 0u) | ((vb & 2u) ? 0xffff0000u : 0u);
+            const uint32_t m23 = ((vb & 4u) ? 0x0000ffffu : 0u) | ((vb & 8u) ? 0xffff0000u : 0u);
+#pragma unroll
+            for (int db = 0; db < ND; ++db) {
+                uint32_t wv[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    wv[c] = *reinterpret_cast<const uint16_t *>(st + S::VOFF + ((2 * db + (hn >> 3)) * 16 + 4 * lg + c) * 16 +
+                                                               2 * (hn & 7));
+                const uint32_t p01 = __builtin_amdgcn_perm(wv[1], wv[0], 0x05040100u) & m01;
+                const uint32_t p23 = __builtin_amdgcn_perm(wv[3], wv[2], 0x05040100u) & m23;
+                const h4v va = __builtin_bit_cast(h4v, u2v{p01, p23});
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[0], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[0], o[db], 0, 0, 0);
+            }
+        } else if constexpr (Q4) {
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb) {
+                uint32_t wv[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) wv[c] = st[S::VOFF + (kb * 16 + 4 * lg + c) * 16 + hn];
+                const uint32_t tq = pack4_lo8(wv);
+                const h4v v0 = q4x4_to_h4(tq & 0x0f0f0f0fu), v1 = q4x4_to_h4((tq >> 4) & 0x0f0f0f0fu);
+                o[2 * kb] = __builtin_amdgcn_mfma_f32_16x16x16f16(v0, bhi[kb], o[2 * kb], 0, 0, 0);
+                o[2 * kb] = __builtin_amdgcn_mfma_f32_16x16x16f16(v0, blo[kb], o[2 * kb], 0, 0, 0);
+                o[2 * kb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(v1, bhi[kb], o[2 * kb + 1], 0, 0, 0);
+                o[2 * kb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(v1, blo[kb], o[2 * kb + 1], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb) {
+                uint32_t wv[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    wv[c] = *reinterpret_cast<const uint16_t *>(st + S::VOFF + ((2 * kb + (hn >> 3)) * 16 + 4 * lg + c) * 16 +
+                                                               2 * (hn & 7));
+                const uint32_t p01 = __builtin_amdgcn_perm(wv[1], wv[0], 0x05010400u);
+                const uint32_t p23 = __builtin_amdgcn_perm(wv[3], wv[2], 0x05010400u);
+                const uint32_t t2[2] = {__builtin_amdgcn_perm(p23, p01, 0x05040100u),
+                                        __builtin_amdgcn_perm(p23, p01, 0x07060302u)};
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const h4v va = q8x4_to_h4(t2[j]);
+                    o[2 * kb + j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, bhi[kb], o[2 * kb + j], 0, 0, 0);
+                    o[2 * kb + j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, blo[kb], o[2 * kb + j], 0, 0, 0);
+                }
+            }
+        }
+        // this slot's LDS reads are done before tile t + 2's transfers reuse it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    const float l = col_sum4(ls);
+    // ---- the four waves' states into the output of the query's heads
+    __syncthreads();                               // every wave is done with the staging slots
+    float *wo = reinterpret_cast<float *>(dec_dyn + w * G * HD * 4);
+    if (hn < G) {
+        if (lg == 0) { sh.wml[w][hn][0] = m; sh.wml[w][hn][1] = l; }
+        if constexpr (LY == kLyQ8K) {              // o[2kb + j][r]: dim 32 kb + 8 lg + 2 r + j
+#pragma unroll
+            for (int kb = 0; kb < NB; ++kb) {
+                const f4v a = o[2 * kb], b = o[2 * kb + 1];
+                *reinterpret_cast<float4 *>(&wo[hn * HD + 32 * kb + 8 * lg]) =
+                    make_float4(a[0] * down, b[0] * down, a[1] * down, b[1] * down);
+                *reinterpret_cast<float4 *>(&wo[hn * HD + 32 * kb + 8 * lg + 4]) =
+                    make_float4(a[2] * down, b[2] * down, a[3] * down, b[3] * down);
+            }
+        } else {
+#pragma unroll
+            for (int db = 0; db < ND; ++db)
+                *reinterpret_cast<float4 *>(&wo[hn * HD + 16 * db + 4 * lg]) =
+                    make_float4(o[db][0] * down, o[db][1] * down, o[db][2] * down, o[db][3] * down);
+        }
+    }
+    __syncthreads();
+    constexpr int TPH = HD / 4;
+#pragma unroll
+    for (int k = tid; k < G * TPH; k += kDecThreads) {
+        const int h = k / TPH, d = 4 * (k % TPH);
+        float mi[kDecWaves], li[kDecWaves];
+        float4 oi[kDecWaves];
+#pragma unroll
+        for (int i = 0; i < kDecWaves; ++i) {
+            mi[i] = sh.wml[i][h][0];
+            li[i] = sh.wml[i][h][1];
+            oi[i] = *reinterpret_cast<const float4 *>(dec_dyn + (i * G * HD + h * HD + d) * 4);
+        }
+        float M = mi[0];
+#pragma unroll
+        for (int i = 1; i < kDecWaves; ++i) M = fmaxf(M, mi[i]);
+        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float Ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDecWaves; ++i) {
+            const float wt = fast_exp2(mi[i] - M);
+            O.x += wt * oi[i].x;
+            O.y += wt * oi[i].y;
+            O.z += wt * oi[i].z;
+            O.w += wt * oi[i].w;
+            Ls += wt * li[i];
+        }
+        const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+        *reinterpret_cast<float4 *>(&out[((int64_t)s * g.H + (int64_t)gh * G + h) * HD + d]) =
+            make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+    }
+    if (!ok && tid == 0 && gh == 0) set_status(v.status, QWFN_STATUS_LEN_RANGE);
+}
+
 // Workgroups of one k_dec instantiation a CU holds: its register-bound
 // occupancy (looked up once per device) against the LDS its launch asks for.
 constexpr int kResDevices = 64;
@@ -1083,6 +1449,18 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
     if (e != hipSuccess) return e;
     return launch_merge(g, v, seq_len, n_seq, max_seq_len, select ? ns : nsel, max_sel, !select && !sel, out, ws,
                         tpw, st);
+}
+
+template <int HD, int G, int LY>
+hipError_t launch_dec_loop_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q, int32_t max_seq_len,
+                             const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax, float *out,
+                             hipStream_t st) {
+    if (max_sel > kDecSelMax) return hipErrorInvalidValue;
+    const int npt_lds = dec_npt_lds(g, max_seq_len, kGiven);
+    const int dyn = dec_loop_bytes<HD, G, LY>() + 4 * npt_lds;
+    hipLaunchKernelGGL((k_dec_loop<HD, G, LY>), dim3(1u, (unsigned)g.Hkv, (unsigned)n_q), dim3(kDecThreads),
+                       (unsigned)dyn, st, g, v, q, max_seq_len, sel, nsel, max_sel, vmax, out, (int32_t)npt_lds);
+    return hipGetLastError();
 }
 
 }  // namespace

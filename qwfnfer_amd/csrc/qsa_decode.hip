@@ -59,6 +59,26 @@ bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel) {
            max_sel <= kDecSelMax && max_seq_len / g.bt - (g.sink & ~3) <= 32 * kDecThreads;
 }
 
+bool dec_loop_fits(const Geo &g, int32_t max_sel) {
+    const int ly = dec_layout(g);
+    return g.pf && (ly == kLyQ8K || ly == kLyQ4 || ly == kLyF16) && max_sel >= 1 && max_sel <= kDecSelMax;
+}
+
+hipError_t launch_dec_loop(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q, int32_t max_seq_len,
+                           const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax, float *out,
+                           hipStream_t st) {
+    if (!dec_loop_fits(g, max_sel)) return hipErrorInvalidValue;
+    const int ly = dec_layout(g);
+    if (ly == kLyQ4 || ly == kLyF16)
+        return launch_dec_kv_loop(g, v, q, n_q, max_seq_len, sel, nsel, max_sel, vmax, out, st);
+#define X(HD_, G_)                                                                                               \
+    if (g.hd == HD_ && g.G == G_)                                                                                \
+        return launch_dec_loop_t<HD_, G_, kLyQ8K>(g, v, q, n_q, max_seq_len, sel, nsel, max_sel, vmax, out, st);
+    QWFN_FOR_EACH_DEC_GATH(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                                 int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {

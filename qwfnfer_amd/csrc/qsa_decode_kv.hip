@@ -34,4 +34,19 @@ hipError_t launch_dec_kv(const Geo &g, const qwfn_kv_view &v, const float *q, co
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_dec_kv_loop(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q, int32_t max_seq_len,
+                              const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax, float *out,
+                              hipStream_t st) {
+#define X(HD_, G_)                                                                                                 \
+    if (g.hd == HD_ && g.G == G_) {                                                                                \
+        if (g.kt == QWFN_KV_Q4_0)                                                                                  \
+            return launch_dec_loop_t<HD_, G_, kLyQ4>(g, v, q, n_q, max_seq_len, sel, nsel, max_sel, vmax, out, st); \
+        if (g.kt == QWFN_KV_F16)                                                                                   \
+            return launch_dec_loop_t<HD_, G_, kLyF16>(g, v, q, n_q, max_seq_len, sel, nsel, max_sel, vmax, out, st); \
+    }
+    QWFN_FOR_EACH_DEC_KV(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
 }  // namespace qwfn_qsa

@@ -220,6 +220,18 @@ bool dec_kernels_for(const Geo &g);
 // q4_0 / F16 caches (qsa_decode_kv.hip): a shape with instantiations, and the
 // attention with its merge, as launch_dec_attention
 bool dec_kv_shape(const Geo &g);
+// Prefill attention of the K layouts (q8_0 in blocks shorter than a tile,
+// q4_0, F16) over a given per-query selection, one workgroup per (query, KV
+// head) walking all its tiles (k_dec_loop): the normalised output, no
+// partials; vmax from launch_prefill_vmax (unused for F16).  Fits: prefill
+// geometry (Geo::pf) of such a shape, max_sel <= 1024.
+bool dec_loop_fits(const Geo &g, int32_t max_sel);
+hipError_t launch_dec_loop(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q, int32_t max_seq_len,
+                           const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax, float *out,
+                           hipStream_t st);
+hipError_t launch_dec_kv_loop(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q, int32_t max_seq_len,
+                              const int32_t *sel, const int32_t *nsel, int32_t max_sel, const float *vmax, float *out,
+                              hipStream_t st);
 hipError_t launch_dec_kv(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len, int32_t n_seq,
                          int32_t max_seq_len, const int32_t *sel, const int32_t *nsel, int32_t max_sel, float *out,
                          const Ws &ws, bool select, hipStream_t st);
