@@ -977,7 +977,7 @@ constexpr int dec_loop_bytes() {
 }
 
 template <int HD, int G, int LY>
-__global__ void __launch_bounds__(kDecThreads)
+__global__ void __launch_bounds__(kDecThreads, 2)
 k_dec_loop(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t max_seq_len, const int32_t *__restrict__ sel,
            const int32_t *__restrict__ nsel, int32_t max_sel, const float *__restrict__ vmax, float *__restrict__ out,
            int32_t npt_lds) {
