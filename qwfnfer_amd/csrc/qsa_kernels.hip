@@ -2252,11 +2252,13 @@ constexpr int kRefineBlocks = 4096;   // eligible blocks the approximate path ta
 // |approximate - exact| <= kPaRel * (sum over the group's heads of |q_h|) * |p|
 // + kPaAbs (Euclidean norms: sum_d |q_hd p_d| <= |q_h| |p|).  The terms, each
 // relative to sum_h |q_h| |p|: fp16 rounding of both operands, 2 * 2^-11 +
-// 2^-22 of each product; the matrix cores' fp32 sums, one accumulator a head
-// (HD - 1 adds, rounded at each in the worst case), then the G head sums in
-// order (relu'd when set) and the power-of-two rescale (exact), below
-// (HD + G - 2) * 2^-24 <= 258 * 2^-24 for every instantiation (G * HD <= 1024,
-// HD <= 256); the exact scores' own rounding (four chains of HD / 4 fmas,
+// 2^-22 of each product; the matrix cores' fp32 sums, one accumulator a chain
+// of pa_chain<HD, G>(relu) heads (one with relu, else as many as keep the
+// chain at 256 products: CH * HD - 1 adds, rounded at each in the worst case),
+// then the G / CH chain sums in order (relu'd when set) and the
+// power-of-two rescale (exact), below (CH * HD - 1 + G / CH - 1) * 2^-24 <=
+// 258 * 2^-24 for every instantiation (G * HD <= 1024, so G / CH <= 4 without
+// relu; HD <= 256, G <= 8 with it); the exact scores' own rounding (four chains of HD / 4 fmas,
 // their two sums, the head sum), below 80 * 2^-24; fp16 subnormals, below
 // 2^-30.  They sum to at most 9.97e-4; the 5 % left covers the rounding of
 // the norms (rounded up by 2^-14) and of the bound itself.  The budget is
@@ -2267,6 +2269,10 @@ constexpr float kPaRel = 1.05e-3f;
 constexpr float kPaAbs = 1e-37f;
 
 template <int HD, int G> constexpr bool pf_approx_fits() { return G * HD <= 1024 && HD % 32 == 0 && 256 % G == 0; }
+// heads whose products k_pf_approx sums in one accumulator (see kPaRel)
+template <int HD, int G> constexpr int pa_chain(bool relu) {
+    return relu || HD >= 256 ? 1 : (256 / HD < G ? 256 / HD : G);
+}
 
 // The power of two that scales a row whose largest magnitude is m into
 // [2^14, 2^15) (fp16 keeps 11 significant bits there): 15 - e for m = f 2^e.
@@ -2385,13 +2391,14 @@ struct PaShared {
 // 16w+15; a lane's outputs are 4 queries x 1 block, scaled back exactly.  The
 // query-tile-0 workgroups also write each block's |p| (rounded up) to pnorm.
 // Pooled keys are fp32, or fp16 (the checkpoint indexer's pool) widened exactly.
-template <int HD, int G>
+template <int HD, int G, bool RELU>
 __global__ void __launch_bounds__(256, 2)
 k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int32_t n_blk,
             float *__restrict__ scores, int32_t nb_cap, float *__restrict__ pnorm) {
     constexpr int NK = HD / 32;                        // k-steps of one head
     constexpr int CPT = HD / 16;                       // 16-byte fp32 chunks a thread stages (4 threads a block)
-    static_assert(pf_approx_fits<HD, G>(), "a wave's query fragments fit its registers");
+    constexpr int CH = pa_chain<HD, G>(RELU);          // heads a chain
+    static_assert(pf_approx_fits<HD, G>() && G % CH == 0, "a wave's query fragments fit its registers");
     __shared__ PaShared<HD> sh;
     const int tid = threadIdx.x, l = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gh = blockIdx.z, row = l & 15, kg = l >> 4;
@@ -2476,18 +2483,24 @@ k_pf_approx(Geo g, qwfn_kv_view v, const float *__restrict__ q, int32_t n_q, int
 #pragma unroll
             for (int ks = 0; ks < NK; ++ks)
                 bf[ks] = *reinterpret_cast<const h8v *>(&sh.p[16 * ct + row][2 * (4 * ks + kg)]);
-            // one accumulator a head (HD products), the heads' sums (relu'd
-            // when set) added in order: the fp32 sums of one score stay within
-            // (HD - 1) + (G - 1) roundings, the budget of kPaRel
-            f4v tot = {0.0f, 0.0f, 0.0f, 0.0f};
+            // one accumulator a chain of CH heads (CH * HD products), the
+            // chains' sums (relu'd when set) added in order: the fp32 sums of
+            // one score stay within (CH * HD - 1) + (G / CH - 1) roundings,
+            // the budget of kPaRel
+            f4v tot;
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
+            for (int h0 = 0; h0 < G; h0 += CH) {
                 f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int ks = 0; ks < NK; ++ks)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], acc, 0, 0, 0);
+                for (int h = h0; h < h0 + CH; ++h)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) tot[i] += g.relu ? fmaxf(acc[i], 0.0f) : acc[i];
+                    for (int ks = 0; ks < NK; ++ks)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[h][ks], bf[ks], acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float x = RELU ? fmaxf(acc[i], 0.0f) : acc[i];
+                    tot[i] = h0 == 0 ? x : tot[i] + x;
+                }
             }
             const int blk = b0 + 16 * ct + row;
             const int pb = sh.pe[16 * ct + row];
@@ -3041,6 +3054,17 @@ k_pf_refine_big(Geo g, qwfn_kv_view v, const float *__restrict__ q, float *score
 }
 
 template <int HD, int G>
+static void launch_pf_approx(const Geo &g, dim3 grid, const qwfn_kv_view &v, const float *q, int32_t n_q,
+                             int32_t n_blk, float *scores, int32_t nb_cap, float *pnorm, hipStream_t st) {
+    if (g.relu)
+        hipLaunchKernelGGL((k_pf_approx<HD, G, true>), grid, dim3(256), 0, st, g, v, q, n_q, n_blk, scores, nb_cap,
+                           pnorm);
+    else
+        hipLaunchKernelGGL((k_pf_approx<HD, G, false>), grid, dim3(256), 0, st, g, v, q, n_q, n_blk, scores, nb_cap,
+                           pnorm);
+}
+
+template <int HD, int G>
 static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
                               int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                               const Ws &ws, hipStream_t st) {
@@ -3050,18 +3074,16 @@ static void launch_pf_index_t(const Geo &g, const qwfn_kv_view &v, const float *
         // to kRbBlocks eligible blocks: the 1024-thread refinement
         if (g.Hkv == 1 && g.topk > 0 && n_blk > g.sink && n_blk - g.sink > kRefineBlocks &&
             n_blk - g.sink <= kRbBlocks) {
-            hipLaunchKernelGGL((k_pf_approx<HD, G>),
-                               dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplitBig, 1u), dim3(256), 0, st, g,
-                               v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm);
+            launch_pf_approx<HD, G>(g, dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplitBig, 1u), v, q, n_q,
+                                    n_blk, ws.scores, ws.nb_cap, ws.pnorm, st);
             hipLaunchKernelGGL((k_pf_refine_big<HD, G>), dim3(1u, (unsigned)n_q), dim3(kRbThreads), 0, st, g, v, q,
                                ws.scores, ws.nb_cap, ws.pnorm, sel, nsel, max_sel);
             return;
         }
         // per-KV-head selections (or one KV head's row shared), up to kRefineBlocks eligible blocks
         if ((!g.shared || g.Hkv == 1) && g.topk > 0 && n_blk > g.sink && n_blk - g.sink <= kRefineBlocks) {
-            hipLaunchKernelGGL((k_pf_approx<HD, G>),
-                               dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv), dim3(256),
-                               0, st, g, v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm);
+            launch_pf_approx<HD, G>(g, dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv),
+                                    v, q, n_q, n_blk, ws.scores, ws.nb_cap, ws.pnorm, st);
             hipLaunchKernelGGL((k_pf_refine<HD, G>), dim3((unsigned)g.Hkv, (unsigned)n_q), dim3(kIdxThreads), 0, st, g,
                                v, q, ws.scores, ws.nb_cap, ws.pnorm, sel, nsel, max_sel);
             return;
@@ -3663,9 +3685,9 @@ hipError_t launch_pf_approx_scores(const Geo &g, const qwfn_kv_view &v, const fl
 #define X(HD_, G_, TG_)                                                                                   \
     if constexpr (pf_approx_fits<HD_, G_>())                                                              \
         if (g.hd == HD_ && g.G == G_) {                                                                   \
-            hipLaunchKernelGGL((k_pf_approx<HD_, G_>),                                                    \
-                               dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit, (unsigned)g.Hkv), \
-                               dim3(256), 0, st, g, v, q, n_q, n_blk, scores, nb_cap, pnorm);              \
+            launch_pf_approx<HD_, G_>(g, dim3((unsigned)((n_q + kPaQ - 1) / kPaQ), (unsigned)kPaSplit,      \
+                                              (unsigned)g.Hkv),                                            \
+                                      v, q, n_q, n_blk, scores, nb_cap, pnorm, st);                        \
             return hipGetLastError();                                                                     \
         }
     QWFN_FOR_EACH_SHAPE(X)

@@ -16,7 +16,7 @@
   workgroup when one tile each would not fit the device at once).
 * Config 4: one 8,192-query chunk of fp16 rows appended at 155,648: cache
   bytes and pooled keys bit-exact, every query's selection bit-exact,
-  attention of a strided sample of queries within the tolerance.
+  attention of every query within the tolerance.
 * The checkpoint's bias rule (local_tokens 0, topk_counts_forced 1) through
   both decode paths across block completions: a completed block is eligible
   at the same step, so it must be pooled before it is scored.

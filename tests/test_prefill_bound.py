@@ -40,15 +40,23 @@ def _fp32_chain_sum(terms, reverse=False):
     return acc
 
 
+def chain_heads(hd, g, relu):
+    """Heads whose products share one fp32 accumulator (pa_chain in the
+    kernel): one with relu, else as many as keep a chain at 256 products."""
+    return 1 if relu or hd >= 256 else min(g, 256 // hd)
+
+
 def approx_score(q, p, relu, reverse=False):
     """q [G, HD] fp32, p [HD] fp32 -> the approximate score (fp32)."""
+    G, HD = q.shape
+    ch = chain_heads(HD, G, relu)
     qe = int(_shift(np.abs(q).max()))
     pe = int(_shift(np.abs(p).max()))
     qh = np.ldexp(q, qe).astype(np.float16).astype(np.float32)
     ph = np.ldexp(p, pe).astype(np.float16).astype(np.float32)
     tot = np.float32(0.0)
-    for h in range(q.shape[0]):
-        prods = (qh[h].astype(np.float64) * ph.astype(np.float64)).astype(np.float32)   # exact in fp32
+    for h0 in range(0, G, ch):
+        prods = (qh[h0:h0 + ch].astype(np.float64) * ph.astype(np.float64)).astype(np.float32).ravel()  # exact
         d = _fp32_chain_sum(prods, reverse)
         if relu:
             d = max(d, np.float32(0.0))
@@ -133,20 +141,25 @@ SHAPES = [(128, 8), (128, 4), (128, 2), (64, 8)]
 
 
 def test_kparel_covers_the_budget_of_every_shape():
-    """kPaRel against its terms, per instantiated shape: fp16 rounding of both
-    operands (2 * 2^-11 + 2^-22), the matrix cores' fp32 sums with one
-    accumulator a head (HD - 1 adds) and the G head sums (G - 1 adds), the
-    exact score's own rounding (80 * 2^-24), with 5 % to spare.  A single
-    accumulator over all G * HD products (the mistake of summing every head in
-    one chain) would need (G * HD - 1) * 2^-24 and is caught at G * HD = 1024."""
+    """kPaRel against its terms, per instantiated shape and relu flag: fp16
+    rounding of both operands (2 * 2^-11 + 2^-22), the matrix cores' fp32 sums
+    with one accumulator a chain of CH heads (CH * HD - 1 adds) and the G / CH
+    chain sums (G / CH - 1 adds), the exact score's own rounding (80 * 2^-24),
+    with 5 % to spare.  A single accumulator over all G * HD products (the
+    mistake of summing every head in one chain) would need (G * HD - 1) * 2^-24
+    and is caught at G * HD = 1024."""
     u = 2.0 ** -24
     text = open(SRC).read()
     shapes = re.search(r"#define QWFN_FOR_EACH_SHAPE\(X\) (.*)", text).group(1)
     inst = {(int(a), int(b)) for a, b in re.findall(r"X\((\d+), (\d+), \d+\)", shapes)}
     assert set(SHAPES) == {(h, g) for h, g in inst if h * g <= 1024}
+    assert chain_heads(128, 8, False) == 2 and chain_heads(64, 8, False) == 4 and chain_heads(128, 8, True) == 1
     for hd, g in SHAPES:
-        need = 2 * 2.0 ** -11 + 2.0 ** -22 + (hd - 1 + g - 1) * u + 80 * u
-        assert KPA_REL >= 1.05 * need, (hd, g, need)
+        for relu in (False, True):
+            ch = chain_heads(hd, g, relu)
+            assert g % ch == 0
+            need = 2 * 2.0 ** -11 + 2.0 ** -22 + (ch * hd - 1 + g // ch - 1) * u + 80 * u
+            assert KPA_REL >= 1.05 * need, (hd, g, relu, need)
     one_chain = 2 * 2.0 ** -11 + 2.0 ** -22 + (1024 - 1) * u + 80 * u
     assert KPA_REL < 1.05 * one_chain
 
@@ -154,8 +167,9 @@ def test_kparel_covers_the_budget_of_every_shape():
 @pytest.mark.parametrize("relu", [False, True])
 def test_approx_score_within_bound_at_1024_products(relu):
     """Eight heads of 128 (G * HD = 1024, the largest group of the matrix-core
-    scoring), each head's 128 products summed in one fp32 chain taken in both
-    orders, against the exact order."""
+    scoring), each chain's products (one head with relu, two heads' 256
+    without) summed in one fp32 chain taken in both orders, against the exact
+    order."""
     rng = np.random.default_rng(4321 + relu)
     for q, p in _cases(rng, 60):
         s = float(exact_score(q, p, relu))
