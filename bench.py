@@ -460,9 +460,11 @@ def bench_checkpoint_prefill(qsa, torch, gen, reps=5):
 class CheckpointRunner:
     """The released checkpoint's attention layer (24 query heads, 2 KV heads of
     256, q8_0 KV, blocks of 4 tokens pooled by its own indexer of 4 heads x 128,
-    513 kept blocks) stepped one decode token at a time: per layer the K/V
-    append, the raw indexer key + its block's pooled key, the indexer's
-    selection and the attention -- five launches."""
+    513 kept blocks) stepped one decode token at a time through
+    qwfn_idx_sparse_attn_decode: per layer one launch for the K/V rows, the raw
+    indexer key and its block's pooled key, then the indexer's scores (and,
+    past 8,192 candidate blocks, the multi-workgroup selection), the attention
+    and its merge -- four launches at 4,096 tokens, five at 163,840."""
 
     def __init__(self, qsa, torch, ctx, n_layer, gen):
         self.qsa, self.torch = qsa, torch
@@ -490,7 +492,6 @@ class CheckpointRunner:
         self.kr = [r(1, icfg.idx_dim) for _ in range(n_layer)]
         self.out = [torch.empty((1, H, hd), device="cuda") for _ in range(n_layer)]
         self.seq_len = torch.tensor([ctx], dtype=torch.int32, device="cuda")
-        self.pos = torch.tensor([ctx - 1], dtype=torch.int32, device="cuda")
         ic0 = self.layers[0][1]
         self.ws = qsa.Workspace(cfg, 1, self.max_len, nbytes=max(cfg.workspace_bytes(1, self.max_len),
                                                                  ic0.workspace_bytes(1, self.max_len)))
@@ -501,17 +502,13 @@ class CheckpointRunner:
         torch.cuda.synchronize()
 
     def layer(self, il):
-        qsa = self.qsa
-        c, ic = self.layers[il]
-        qsa.append_q8_0(c, self.kn[il], self.vn[il], self.pos)
-        qsa.idx_append_pool(ic, self.kr[il], self.pos)
-        qsa.idx_select(ic, self.qi[il], self.seq_len, self.max_len, self.ws, sel=self.sel, n_sel=self.nsel)
-        qsa.sparse_decode_attn(c, self.q[il], self.seq_len, self.max_len, self.ws, self.sel, self.nsel,
-                               out=self.out[il])
+        _, ic = self.layers[il]
+        self.qsa.idx_sparse_attn_decode(ic, self.q[il], self.qi[il], self.kn[il], self.vn[il], self.kr[il],
+                                        self.seq_len, self.max_len, self.ws, out=self.out[il], sel=self.sel,
+                                        n_sel=self.nsel)
 
     def step(self):
         self.seq_len.add_(1)
-        self.pos.add_(1)
         for il in range(self.n_layer):
             self.layer(il)
 
@@ -537,11 +534,11 @@ class CheckpointRunner:
         torch.cuda.synchronize()
         # the replay against an eager step from the same position
         p0 = self.seq_len.clone()
-        self.seq_len.copy_(p0); self.pos.copy_(p0 - 1)
+        self.seq_len.copy_(p0)
         self.step()
         torch.cuda.synchronize()
         ref = [o.clone() for o in self.out]
-        self.seq_len.copy_(p0); self.pos.copy_(p0 - 1)
+        self.seq_len.copy_(p0)
         g.replay()
         torch.cuda.synchronize()
         if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
@@ -833,7 +830,8 @@ def main():
             torch.cuda.empty_cache()
         checkpoint = dict(per_context=ck, workload="the released checkpoint's attention layer: 24q/2kv heads "
                           "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
-                          "keys), 513 kept blocks shared by both KV heads; 6 launches per layer, hipGraph")
+                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (4 launches at "
+                          "4,096 tokens, 5 at 163,840), hipGraph")
         if not args.no_prefill:
             checkpoint["prefill"] = bench_checkpoint_prefill(qsa, torch, gen)
             log(f"[bench] checkpoint prefill chunk ({PREFILL_N} queries at {PREFILL_POS0}): "

@@ -492,6 +492,27 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                     const float *q_idx, const int32_t *seq_len, int32_t n_seq,
                     int32_t max_seq_len, int32_t *sel, int32_t *n_sel, int32_t max_sel,
                     void *ws, size_t ws_bytes, void *stream);
+/* One decode token of graph_builder::sparse_attn_decode with the checkpoint's
+ * indexer (src/qwfn_graph.cpp:450-546): for sequence i < n_seq (at most 64)
+ * at position seq_len[i]-1, the raw indexer key k_raw [n_seq][idx_dim] is
+ * written and its block re-pooled (:463-476) and k_new / v_new
+ * [n_seq][n_head_kv][head_dim] appended (:520-528), all in one launch; then
+ * the indexer's scores and selection from q_idx as qwfn_idx_select
+ * (:477-495) and the attention of q over it as qwfn_sparse_decode_attn
+ * (:497-542).  src_dtype covers k_new, v_new and k_raw.  sel [n_seq]
+ * [n_head_kv][max_sel] and n_sel [n_seq][n_head_kv] (required: the selection
+ * passes through them) receive the selection as qwfn_idx_select writes it.
+ * Workspace: the larger of qwfn_qsa_workspace_bytes and qwfn_idx_workspace_
+ * bytes.  Replaces the four calls qwfn_kv_append_q8_0, qwfn_idx_append_pool,
+ * qwfn_idx_select and qwfn_sparse_decode_attn of a decode step with one
+ * launch fewer. */
+int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
+                                const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
+                                const float *q, const float *q_idx, const void *k_new,
+                                const void *v_new, const void *k_raw, int32_t src_dtype,
+                                const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
+                                float *out, int32_t *sel, int32_t *n_sel, int32_t max_sel,
+                                void *ws, size_t ws_bytes, void *stream);
 /* qwfn_sparse_attn_prefill with the checkpoint's indexer: k_raw (optional,
  * with k_new / v_new) [n_q][idx_dim] is written at pos0.. and every block it
  * touches re-pooled; query i is selected by q_idx [n_q][n_idx_head][idx_dim]

@@ -62,6 +62,7 @@ EXPORTS = (
     "qwfn_idx_append_pool",
     "qwfn_idx_pool_rebuild",
     "qwfn_idx_select",
+    "qwfn_idx_sparse_attn_decode",
     "qwfn_idx_sparse_attn_prefill",
 )
 
@@ -167,6 +168,8 @@ _SIGS = {
     "qwfn_idx_append_pool": (C.c_int, [_S, _V, _IS, _IV, _P, _I, _P, _P, _I, _P]),
     "qwfn_idx_pool_rebuild": (C.c_int, [_S, _V, _IS, _IV, _I, _I, _P]),
     "qwfn_idx_select": (C.c_int, [_S, _V, _IS, _IV, _P, _P, _I, _I, _P, _P, _I, _P, _Z, _P]),
+    "qwfn_idx_sparse_attn_decode": (C.c_int, [_S, _V, _IS, _IV, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _I,
+                                              _P, _Z, _P]),
     "qwfn_idx_sparse_attn_prefill": (C.c_int, [_S, _V, _IS, _IV, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P,
                                                _I, _P, _Z, _P]),
 }

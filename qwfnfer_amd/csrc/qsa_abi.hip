@@ -849,7 +849,7 @@ int qwfn_idx_append_pool(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, 
         return fail(QWFN_EINVAL, "idx_append_pool: NULL or misaligned k_raw (16) / NULL pos / n_rows < 0");
     if (n_rows == 0) return ok();
     hipStream_t st = (hipStream_t)stream;
-    if (n_rows <= 64) {                           // a decode step: one launch
+    if (n_rows <= kIdxFuseRows) {                 // a decode step: one launch
         const hipError_t e1 = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled,
                                                      iview->k_norm, k_raw, src_dtype == QWFN_SRC_F16, seq_ids, pos,
                                                      n_rows, st);
@@ -903,6 +903,53 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const
     const hipError_t e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, w, fa,
                                         (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "idx_select");
+}
+
+int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view, const qwfn_idx_shape *ishape,
+                                const qwfn_idx_view *iview, const float *q, const float *q_idx, const void *k_new,
+                                const void *v_new, const void *k_raw, int32_t src_dtype, const int32_t *seq_len,
+                                int32_t n_seq, int32_t max_seq_len, float *out, int32_t *sel, int32_t *n_sel,
+                                int32_t max_sel, void *ws, size_t ws_bytes, void *stream) {
+    TimerDisarm disarm;
+    Geo g;
+    int rc = make_geo(shape, view, &g);
+    if (rc) return rc;
+    IdxGeo ig;
+    if ((rc = make_idx_geo(shape, ishape, &ig)) || (rc = check_idx_view(iview, true, true, true))) return rc;
+    if ((rc = check_batch(shape, view, n_seq, max_seq_len))) return rc;
+    if (n_seq > kIdxFuseRows)
+        return fail(QWFN_ERANGE, "idx decode: n_seq %d > %d (call qwfn_kv_append_q8_0, qwfn_idx_append_pool, "
+                    "qwfn_idx_select and qwfn_sparse_decode_attn)", n_seq, kIdxFuseRows);
+    if (src_dtype != QWFN_SRC_F32 && src_dtype != QWFN_SRC_F16) return fail(QWFN_EINVAL, "src_dtype %d unknown", src_dtype);
+    const size_t al = src_dtype == QWFN_SRC_F32 ? 16 : 8;
+    if (!q || !aligned(q, 16) || !q_idx || !aligned(q_idx, 16) || !k_new || !v_new || !aligned(k_new, al) ||
+        !aligned(v_new, al) || !k_raw || !aligned(k_raw, 16) || !seq_len || !out || !sel || !n_sel)
+        return fail(QWFN_EINVAL, "idx decode: NULL or misaligned q / q_idx / k_new / v_new / k_raw (16) / seq_len / "
+                    "out / sel / n_sel");
+    const int32_t need = max_selected(shape, max_seq_len);
+    if (max_sel < need) return fail(QWFN_ERANGE, "idx decode: max_sel %d < %d", max_sel, need);
+    // the indexer and the attention run one after the other over the same
+    // workspace: it must hold the larger of their layouts
+    const Geo gi = idx_scoring_geo(g, ishape);
+    const WsLayout li = ws_layout(gi, n_seq, max_seq_len, need, false);
+    const WsLayout la = ws_layout(g, n_seq, max_seq_len, max_sel);
+    const size_t total = li.total > la.total ? li.total : la.total;
+    if (!ws || !aligned(ws, 256)) return fail(QWFN_EINVAL, "idx decode: workspace NULL or not 256-byte aligned");
+    if (ws_bytes < total) return fail(QWFN_ERANGE, "idx decode: workspace of %zu bytes < %zu", ws_bytes, total);
+    hipStream_t st = (hipStream_t)stream;
+    const int32_t f16 = src_dtype == QWFN_SRC_F16;
+    // the K/V rows, the raw indexer key and its block's pooled key: one launch
+    hipError_t e = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled,
+                                          iview->k_norm, k_raw, f16, nullptr, nullptr, n_seq, st,
+                                          FusedAppend{k_new, v_new, f16, 1}, seq_len);
+    if (e != hipSuccess) return hip_fail(e, "idx decode: append");
+    qwfn_kv_view vi = *view;
+    vi.pooled = (float *)iview->pooled;                   // fp16 keys (Geo::pooled_f16)
+    e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, ws_bind(ws, li),
+                       FusedAppend{nullptr, nullptr, 0, 0}, st);
+    if (e != hipSuccess) return hip_fail(e, "idx decode: indexer");
+    e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, ws_bind(ws, la), st);
+    return e == hipSuccess ? ok() : hip_fail(e, "idx decode: attention");
 }
 
 int qwfn_idx_sparse_attn_prefill(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,

@@ -173,6 +173,60 @@ __device__ __forceinline__ uint32_t quant_q4(const float x[4], int e, uint16_t *
     return (q[0] | q[2] << 4) | ((q[1] | q[3] << 4) << 8);
 }
 
+// One lane of a K/V row append (k_append, and the decode step's append in
+// k_idx_append_pool): lane i quantizes (q8_0, q4_0) or converts (F16) 4 values
+// of one 32-value block and stores them with the block's scale.  Blocks
+// enumerate (row, K|V, KV head, j), 8 lanes a block, which must be active
+// together (the quantizers' DPP and shuffles span them); row r is sequence
+// seq's token at position t, row_at(r, seq, t).  A bad sequence, position or
+// page skips the block and is reported once a row.
+template <class RowAt>
+__device__ __forceinline__ void append_lane(const Geo &g, const qwfn_kv_view &v, const void *ksrc, const void *vsrc,
+                                            int32_t f16, int64_t i, RowAt row_at) {
+    const int nj = g.hd / 32;
+    const int e4 = (int)(i & 7);
+    int64_t qb = i >> 3;
+    const int j = (int)(qb % nj); qb /= nj;
+    const int gh = (int)(qb % g.Hkv); qb /= g.Hkv;
+    const int which = (int)(qb & 1);
+    const int r = (int)(qb >> 1);
+    int seq, t;
+    row_at(r, seq, t);
+    const bool report = (e4 == 0 && j == 0 && gh == 0 && which == 0);
+    // the lanes of one block stay together past the checks: they are uniform per block
+    if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
+    if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (report) set_status(v.status, QWFN_STATUS_POS_RANGE); return; }
+    const int32_t pp = phys_page(g, v.page_table, seq, t);
+    if (pp < 0) { if (report) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
+    const void *src = which ? vsrc : ksrc;
+    const int64_t base = ((int64_t)r * g.Hkv + gh) * g.hd + 32 * j;
+    uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
+    const int row = t % g.pt;
+    float x[4];
+    if (g.kt == QWFN_KV_Q4_0) {
+        float a[2], b[2];
+        load2(src, f16, base + 2 * e4, a);
+        load2(src, f16, base + 16 + 2 * e4, b);
+        x[0] = a[0]; x[1] = a[1]; x[2] = b[0]; x[3] = b[1];
+        uint16_t dh;
+        const uint32_t qs = quant_q4(x, e4, &dh);
+        *reinterpret_cast<uint16_t *>(page + chunk_off(g, gh, row, j) + 2 * e4) = (uint16_t)qs;
+        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+    } else if (g.kt == QWFN_KV_F16) {
+        load4(src, f16, base + 4 * e4, x);
+        const uint32_t lo = (uint32_t)f2h(x[0]) | (uint32_t)f2h(x[1]) << 16;
+        const uint32_t hi = (uint32_t)f2h(x[2]) | (uint32_t)f2h(x[3]) << 16;
+        const int d = 32 * j + 4 * e4;
+        *reinterpret_cast<uint2 *>(page + chunk_off(g, gh, row, d / 8) + (d % 8) * 2) = make_uint2(lo, hi);
+    } else {
+        load4(src, f16, base + 4 * e4, x);
+        uint16_t dh;
+        const uint32_t pk = quant4(x, g.variant, &dh, nullptr);
+        store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
+        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
+    }
+}
+
 // One dequantized value straight from global memory (gather path): q8_0
 // d*q, q4_0 d*(nibble - 8) (dims 0..15 of a block in the low nibbles of its
 // 16 bytes, dims 16..31 in the high ones), fp16 as stored.

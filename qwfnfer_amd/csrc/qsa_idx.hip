@@ -13,6 +13,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "qsa_append.h"
 #include "qsa_device.h"
 
 namespace qwfn_qsa {
@@ -175,20 +176,33 @@ k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, u
 // rows are range-checked into LDS; each is written unless a later row has the
 // same (sequence, position) -- the last one is kept --, and after a barrier
 // the last row touching each block pools it from the cache, one wave a block.
-constexpr int kIdxFuseRows = 64;
+// len (the fused decode step): row r is sequence r's token at position
+// len[r] - 1, and kv (when enabled) brings the same rows' K and V, which the
+// workgroup's upper threads append as k_append does, alongside.
 constexpr int kIdxFuseThreads = 1024;
 template <int D>
 __global__ void __launch_bounds__(kIdxFuseThreads)
 k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
                   const float *__restrict__ k_norm, const void *src, int32_t f16, const int32_t *seq_ids,
-                  const int32_t *pos, int32_t n_rows) {
+                  const int32_t *pos, int32_t n_rows, FusedAppend kv, const int32_t *len) {
     constexpr int NW = kIdxFuseThreads / 64, PER = D / 8;
     __shared__ int32_t s_seq[kIdxFuseRows], s_pos[kIdxFuseRows], s_pp[kIdxFuseRows];
     __shared__ uint8_t s_write[kIdxFuseRows], s_pool[kIdxFuseRows];
     __shared__ float ys[NW][D];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (kv.enabled) {
+        // lane i of the K/V append on thread i ^ 512: whole waves keep their
+        // lane order (the quantizers' 8-lane groups), and the rows' checks
+        // below run on threads 0 .. n_rows - 1
+        const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
+        for (int64_t i = tid ^ (kIdxFuseThreads / 2); i < total; i += kIdxFuseThreads)
+            append_lane(g, v, kv.k_new, kv.v_new, kv.src_f16, i, [&](int r, int &seq, int &t) {
+                seq = r;
+                t = len[r] - 1;
+            });
+    }
     if (tid < n_rows) {
-        const int seq = seq_ids ? seq_ids[tid] : 0, t = pos[tid];
+        const int seq = len ? tid : seq_ids ? seq_ids[tid] : 0, t = len ? len[tid] - 1 : pos[tid];
         int32_t pp = -1;
         if (seq < 0 || seq >= g.n_seq_view) set_status(v.status, QWFN_STATUS_SEQ_RANGE);
         else if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) set_status(v.status, QWFN_STATUS_POS_RANGE);
@@ -240,14 +254,19 @@ k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, 
 
 hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
                                   uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
-                                  const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st) {
-    if (n_rows > kIdxFuseRows) return hipErrorInvalidValue;
+                                  const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st,
+                                  const FusedAppend &kv, const int32_t *len) {
+    if (n_rows > kIdxFuseRows || (kv.enabled && !len) || (!len && !pos)) return hipErrorInvalidValue;
+#define QWFN_IDX_AP(D_)                                                                                        \
+    hipLaunchKernelGGL(k_idx_append_pool<D_>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, \
+                       src, src_f16, seq_ids, pos, n_rows, kv, len)
     switch (ig.dim) {
-    case 64:  hipLaunchKernelGGL(k_idx_append_pool<64>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, src, src_f16, seq_ids, pos, n_rows); break;
-    case 128: hipLaunchKernelGGL(k_idx_append_pool<128>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, src, src_f16, seq_ids, pos, n_rows); break;
-    case 256: hipLaunchKernelGGL(k_idx_append_pool<256>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, src, src_f16, seq_ids, pos, n_rows); break;
+    case 64:  QWFN_IDX_AP(64); break;
+    case 128: QWFN_IDX_AP(128); break;
+    case 256: QWFN_IDX_AP(256); break;
     default: return hipErrorInvalidValue;
     }
+#undef QWFN_IDX_AP
     return hipGetLastError();
 }
 

@@ -156,9 +156,14 @@ hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig
                            int32_t n_items, int32_t seq_const, int32_t blk0, hipStream_t st);
 // Write and pool in one launch, for calls of at most 64 rows (a decode step):
 // among rows with the same (sequence, position) the last one is kept.
+// Rows of one k_idx_append_pool launch (a decode step of up to this many
+// sequences); kv enabled (with len): the rows' K/V appended by the same launch
+constexpr int kIdxFuseRows = 64;
 hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
                                   uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
-                                  const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st);
+                                  const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st,
+                                  const FusedAppend &kv = FusedAppend{nullptr, nullptr, 0, 0},
+                                  const int32_t *len = nullptr);
 // seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r;
 // len (decode): row r is sequence r's token at position len[r] - 1.
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,

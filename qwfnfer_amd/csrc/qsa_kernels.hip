@@ -55,51 +55,13 @@ __global__ void __launch_bounds__(256)
 k_append(Geo g, qwfn_kv_view v, const void *ksrc, const void *vsrc, int32_t f16,
          const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, int32_t seq_const, int32_t pos0,
          const int32_t *len) {
-    const int nj = g.hd / 32;
-    const int64_t total = (int64_t)n_rows * 2 * g.Hkv * nj * 8;
+    const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
-    const int e4 = (int)(i & 7);
-    int64_t qb = i >> 3;
-    const int j = (int)(qb % nj); qb /= nj;
-    const int gh = (int)(qb % g.Hkv); qb /= g.Hkv;
-    const int which = (int)(qb & 1);
-    const int r = (int)(qb >> 1);
-    const int seq = len ? r : seq_ids ? seq_ids[r] : seq_const;
-    const int t = len ? len[r] - 1 : pos ? pos[r] : pos0 + r;
-    const bool report = (e4 == 0 && j == 0 && gh == 0 && which == 0);
-    // the lanes of one block stay together past the checks: they are uniform per block
-    if (seq < 0 || seq >= g.n_seq_view) { if (report) set_status(v.status, QWFN_STATUS_SEQ_RANGE); return; }
-    if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (report) set_status(v.status, QWFN_STATUS_POS_RANGE); return; }
-    const int32_t pp = phys_page(g, v.page_table, seq, t);
-    if (pp < 0) { if (report) set_status(v.status, QWFN_STATUS_PAGE_RANGE); return; }
-    const void *src = which ? vsrc : ksrc;
-    const int64_t base = ((int64_t)r * g.Hkv + gh) * g.hd + 32 * j;
-    uint8_t *page = (uint8_t *)(which ? v.v_pages : v.k_pages) + (int64_t)pp * g.page_bytes;
-    const int row = t % g.pt;
-    float x[4];
-    if (g.kt == QWFN_KV_Q4_0) {
-        float a[2], b[2];
-        load2(src, f16, base + 2 * e4, a);
-        load2(src, f16, base + 16 + 2 * e4, b);
-        x[0] = a[0]; x[1] = a[1]; x[2] = b[0]; x[3] = b[1];
-        uint16_t dh;
-        const uint32_t qs = quant_q4(x, e4, &dh);
-        *reinterpret_cast<uint16_t *>(page + chunk_off(g, gh, row, j) + 2 * e4) = (uint16_t)qs;
-        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
-    } else if (g.kt == QWFN_KV_F16) {
-        load4(src, f16, base + 4 * e4, x);
-        const uint32_t lo = (uint32_t)f2h(x[0]) | (uint32_t)f2h(x[1]) << 16;
-        const uint32_t hi = (uint32_t)f2h(x[2]) | (uint32_t)f2h(x[3]) << 16;
-        const int d = 32 * j + 4 * e4;
-        *reinterpret_cast<uint2 *>(page + chunk_off(g, gh, row, d / 8) + (d % 8) * 2) = make_uint2(lo, hi);
-    } else {
-        load4(src, f16, base + 4 * e4, x);
-        uint16_t dh;
-        const uint32_t pk = quant4(x, g.variant, &dh, nullptr);
-        store_q4(g, page, which, gh, row, 32 * j + 4 * e4, pk);
-        if (e4 == 0) *reinterpret_cast<uint16_t *>(page + scale_off(g, gh, row, j)) = dh;
-    }
+    append_lane(g, v, ksrc, vsrc, f16, i, [&](int r, int &seq, int &t) {
+        seq = len ? r : seq_ids ? seq_ids[r] : seq_const;
+        t = len ? len[r] - 1 : pos ? pos[r] : pos0 + r;
+    });
 }
 
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,

@@ -695,6 +695,47 @@ def idx_select(ic: IdxCache, q_idx: torch.Tensor, seq_len: torch.Tensor, max_seq
     return sel, n_sel
 
 
+def idx_sparse_attn_decode(ic: IdxCache, q: torch.Tensor, q_idx: torch.Tensor, k_new: torch.Tensor,
+                           v_new: torch.Tensor, k_raw: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int,
+                           ws: Workspace, out: Optional[torch.Tensor] = None, sel: Optional[torch.Tensor] = None,
+                           n_sel: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """One decode token of graph_builder::sparse_attn_decode with the
+    checkpoint's indexer (src/qwfn_graph.cpp:450-546): k_raw [n_seq, idx_dim]
+    and k_new / v_new [n_seq, n_head_kv, head_dim] (one dtype, f32 or f16) are
+    written at seq_len - 1 and the raw key's block re-pooled in one launch,
+    then q_idx selects as :func:`idx_select` and q attends as
+    :func:`sparse_decode_attn`.  ``sel`` / ``n_sel`` receive the selection
+    (allocated here when not given); ``ws`` must hold both the attention's and
+    the indexer's workspace."""
+    cache, cfg, icfg = ic.kv, ic.kv.cfg, ic.icfg
+    n_seq = seq_len.numel()
+    _need(q, "q", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    _need(q_idx, "q_idx", torch.float32, n_seq * icfg.n_idx_head * icfg.idx_dim)
+    if k_new.dtype not in (torch.float32, torch.float16) or v_new.dtype != k_new.dtype or k_raw.dtype != k_new.dtype:
+        raise TypeError("k_new, v_new and k_raw must share one dtype, float32 or float16")
+    _need(k_new, "k_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(v_new, "v_new", k_new.dtype, n_seq * cfg.kv_dim)
+    _need(k_raw, "k_raw", k_new.dtype, n_seq * icfg.idx_dim)
+    _need(seq_len, "seq_len", torch.int32)
+    max_sel = cfg.max_selected(max_seq_len)
+    if sel is None:
+        sel = torch.empty((n_seq, cfg.n_head_kv, max_sel), dtype=torch.int32, device=q.device)
+    if n_sel is None:
+        n_sel = torch.empty((n_seq, cfg.n_head_kv), dtype=torch.int32, device=q.device)
+    if sel.shape[-1] < max_sel:
+        raise ValueError(f"sel rows of {sel.shape[-1]} < max_selected {max_sel}")
+    _need(sel, "sel", torch.int32, n_seq * cfg.n_head_kv * sel.shape[-1])
+    _need(n_sel, "n_sel", torch.int32, n_seq * cfg.n_head_kv)
+    if out is None:
+        out = torch.empty((n_seq, cfg.n_head, cfg.head_dim), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, n_seq * cfg.n_head * cfg.head_dim)
+    call("qwfn_idx_sparse_attn_decode", C.byref(cfg.shape()), C.byref(cache.view()), C.byref(icfg.shape()),
+         C.byref(ic.view()), q.data_ptr(), q_idx.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_raw.data_ptr(),
+         _lib.SRC_F16 if k_new.dtype == torch.float16 else _lib.SRC_F32, seq_len.data_ptr(), n_seq, max_seq_len,
+         out.data_ptr(), sel.data_ptr(), n_sel.data_ptr(), sel.shape[-1], ws.ptr(), ws.nbytes, _stream(stream))
+    return out
+
+
 def idx_sparse_attn_prefill(ic: IdxCache, q: torch.Tensor, q_idx: torch.Tensor, seq: int, pos0: int,
                             ws: Workspace, k_new: Optional[torch.Tensor] = None,
                             v_new: Optional[torch.Tensor] = None, k_raw: Optional[torch.Tensor] = None,

@@ -205,6 +205,88 @@ def test_checkpoint_decode_steps():
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_checkpoint_fused_decode_steps(dtype):
+    """qwfn_idx_sparse_attn_decode (the K/V rows, the raw indexer key and its
+    pooled block in one launch, then the indexer and the attention) for two
+    sequences over steps that complete blocks in each: the cache bytes, raw and
+    pooled keys and selections bit-exact against the oracle, the attention
+    within the tolerance; a twin cache stepped through the four separate calls
+    ends with the same bytes, selections and outputs bit for bit."""
+    cfg = CKPT
+    rng = np.random.default_rng(850)
+    L0 = [4998, 3001]                                  # block completions at steps 1 and 2, 5 and 6
+    steps = 7
+    pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
+    pairs = [_pair(cfg, 2, pps, seed=851), _pair(cfg, 2, pps, seed=851)]
+    dev, host, ic, w = pairs[0]
+    dev2, _, ic2, _ = pairs[1]
+    kr = []
+    for s in range(2):
+        k, v = kv_rows(rng, L0[s], cfg)
+        assert host.append(k, v, np.arange(L0[s], dtype=np.int32), np.full(L0[s], s, np.int32)) == 0
+        x = rng.standard_normal((L0[s], 128)).astype(np.float32)
+        kr.append(x)
+        for d, c in ((dev, ic), (dev2, ic2)):
+            qsa.append_q8_0(d, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            torch.arange(L0[s], dtype=torch.int32, device="cuda"),
+                            seq_ids=torch.full((L0[s],), s, dtype=torch.int32, device="cuda"))
+            qsa.idx_append_pool(c, torch.from_numpy(x).cuda(), torch.arange(L0[s], dtype=torch.int32, device="cuda"),
+                                seq_ids=torch.full((L0[s],), s, dtype=torch.int32, device="cuda"))
+    c = cfg_of(cfg)
+    Lmax = max(L0) + steps + 1
+    ws, ws2 = _ws(cfg, ic, 2, Lmax), _ws(cfg, ic2, 2, Lmax)
+    msel = c.max_selected(Lmax)
+    tdt = torch.float16 if dtype == np.float16 else torch.float32
+    for step in range(steps):
+        lens = [L + step + 1 for L in L0]
+        print(f"  fused idx decode step {step}, lengths {lens}, {np.dtype(dtype).name} rows", flush=True)
+        kn, vn = kv_rows(rng, 2, cfg)
+        kn, vn = kn.astype(dtype), vn.astype(dtype)
+        xr = rng.standard_normal((2, 128)).astype(dtype)
+        q = rng.standard_normal((2, 24, 256)).astype(np.float32)
+        qi = rng.standard_normal((2, 4, 128)).astype(np.float32)
+        L = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        sel = torch.full((2, 2, msel), -7, dtype=torch.int32, device="cuda")   # entries past n_sel stay as filled
+        nsel = torch.empty((2, 2), dtype=torch.int32, device="cuda")
+        qd, qid = torch.from_numpy(q).cuda(), torch.from_numpy(qi).cuda()
+        knd, vnd, xrd = (torch.from_numpy(a).cuda() for a in (kn, vn, xr))
+        out = qsa.idx_sparse_attn_decode(ic, qd, qid, knd, vnd, xrd, L, Lmax, ws, sel=sel, n_sel=nsel)
+        # the twin: the four calls of the same step
+        pos = L - 1
+        qsa.append_q8_0(dev2, knd, vnd, pos, seq_ids=torch.arange(2, dtype=torch.int32, device="cuda"))
+        qsa.idx_append_pool(ic2, xrd, pos, seq_ids=torch.arange(2, dtype=torch.int32, device="cuda"))
+        sel2 = torch.full_like(sel, -7)
+        nsel2 = torch.empty_like(nsel)
+        qsa.idx_select(ic2, qid, L, Lmax, ws2, sel=sel2, n_sel=nsel2)
+        out2 = qsa.sparse_decode_attn(dev2, qd, L, Lmax, ws2, sel=sel2, n_sel=nsel2)
+        torch.cuda.synchronize()
+        assert host.append(kn, vn, np.array([l - 1 for l in lens], np.int32), np.arange(2, dtype=np.int32)) == 0
+        hs = np.full((2, 2, msel), -1, np.int32)
+        gs, gn = np_of(sel), np_of(nsel)
+        for s in range(2):
+            p = lens[s] - 1
+            kr[s] = np.concatenate([kr[s], xr[s:s + 1].astype(np.float32)])
+            np.testing.assert_array_equal(np_of(ic.pooled)[s, p // 4],
+                                          oracle_pool_all(cfg, ICFG, kr[s].astype(np.float16), w, p // 4 + 1)[p // 4],
+                                          err_msg=f"step {step} seq {s} pooled key")
+            want = oracle_select(cfg, ICFG, np_of(ic.pooled)[s], qi[s], lens[s], msel)
+            for g in range(2):
+                assert gn[s, g] == len(want)
+                np.testing.assert_array_equal(gs[s, g, :gn[s, g]], want, err_msg=f"step {step} seq {s} head {g}")
+                hs[s, g, :len(want)] = want
+        ref = host.attention_f64(q, lens, hs, gn)
+        assert_close_attn(np_of(out), ref, f"step {step}")
+        assert torch.equal(out, out2) and torch.equal(sel, sel2) and torch.equal(nsel, nsel2), f"step {step}"
+    np.testing.assert_array_equal(np_of(dev.k_pages), host.k_pages)
+    np.testing.assert_array_equal(np_of(dev.v_pages), host.v_pages)
+    for a, b in ((dev.k_pages, dev2.k_pages), (dev.v_pages, dev2.v_pages), (ic.raw, ic2.raw), (ic.pooled, ic2.pooled)):
+        assert torch.equal(a, b)
+    for s in range(2):
+        np.testing.assert_array_equal(_raw_rows(dev, ic, s, L0[s] + steps), kr[s].astype(np.float16), err_msg=f"seq {s}")
+    assert qsa.read_status(dev) == 0
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
 def test_checkpoint_prefill(dtype):
     """A prefill chunk with the checkpoint's indexer: K/V and raw keys appended,
     the touched blocks pooled, each query selected by its q_idx and attending
