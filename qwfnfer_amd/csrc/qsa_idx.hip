@@ -80,10 +80,36 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
 //            block's first position b * bt (src/qwfn_engine.cpp:741-743, 926,
 //            934), so every pair takes pos = b * bt.
 //   store  : rounded to fp16 (the reference's F16 pool cache).
+// cos / sin of the rotation of dims lane + 64 k (see pool_idx_block) for a
+// block at position t0: 1, 0 for the dims past nd.
 template <int D>
-__device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, const uint16_t *m,
-                                               const float *__restrict__ k_norm, float *ys, uint16_t *dst, int t0,
-                                               int lane) {
+__device__ __forceinline__ void idx_rot_cs(const IdxGeo &ig, int t0, int lane, float (&cc)[D / 64],
+                                           float (&sn)[D / 64]) {
+    const int half = ig.nd / 2;
+#pragma unroll
+    for (int k = 0; k < D / 64; ++k) {
+        const int d = lane + 64 * k;
+        cc[k] = 1.0f;
+        sn[k] = 0.0f;
+        if (d < ig.nd) {
+            const int i = d < half ? d : d - half;
+            // ggml's angle of pair i: the block position times theta_scale, i
+            // times over, each product rounded to fp32
+            float th = (float)t0;
+            for (int e = 0; e < i; ++e) th = __fmul_rn(th, ig.theta_scale);
+            cc[k] = (float)cos((double)th);
+            sn[k] = (float)sin((double)th);
+        }
+    }
+}
+
+// The pooled key of one block from its bt members (row(r, k): member r's dim
+// lane + 64 k as fp32, position order) and its rotation's cos / sin, by one
+// wave (pool_idx_block's arithmetic).
+template <int D, class Row>
+__device__ __forceinline__ void pool_idx_rows(const Geo &g, const IdxGeo &ig, Row row, const float *__restrict__ k_norm,
+                                              float *ys, uint16_t *dst, int lane, const float (&cc)[D / 64],
+                                              const float (&sn)[D / 64]) {
 #pragma clang fp contract(off)
     constexpr int K = D / 64, U = 8;
     float x[K];
@@ -93,7 +119,7 @@ __device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, c
         for (int u = 0; u < U; ++u) {
             const int r = min(r0 + u, g.bt - 1);
 #pragma unroll
-            for (int k = 0; k < K; ++k) y[u][k] = h2f(m[(int64_t)r * D + lane + 64 * k]);
+            for (int k = 0; k < K; ++k) y[u][k] = row(r, k);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -127,16 +153,43 @@ __device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, c
         float o = ys[d];
         if (d < ig.nd) {
             const int i = d < half ? d : d - half;
-            // ggml's angle of pair i: the block position times theta_scale, i
-            // times over, each product rounded to fp32
-            float th = (float)t0;
-            for (int k = 0; k < i; ++k) th = __fmul_rn(th, ig.theta_scale);
-            const float c = (float)cos((double)th), s = (float)sin((double)th);
+            const float c = cc[k], s = sn[k];
             const float x0 = ys[i], x1 = ys[i + half];
             o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
         }
         dst[d] = f2h(o);
     }
+}
+
+// The pooled key of one block from its bt members m[0 .. bt) (fp16 rows of D
+// values, position order), by one wave; lane l owns dims l + 64k (k < D/64).
+// ys is the wave's own D floats of LDS.
+//   mean   : fp32 add chain over the members in position order, * (1/bt)
+//            (ggml_add chain + ggml_scale, src/qwfn_graph.cpp:415-422); the
+//            members' loads go out eight at a time before any is summed
+//   RMSNorm: sum of the fp32 squares in fp64 -- per lane in k order, then a
+//            butterfly over lane distance 32, 16, .., 1 --, mean = (float)
+//            (sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm[d]
+//            (ggml_rms_norm also sums in fp64; :423)
+//   rotary : pair (i, i + nd/2) turned by (x0 c - x1 s, x0 s + x1 c), dims
+//            >= nd unchanged, with ggml's IMROPE angle (:425-427): theta_0 =
+//            (float)pos, theta_{i+1} = theta_i * theta_scale rounded to fp32,
+//            theta_scale = powf(base, -2/nd) -- the running product ggml's
+//            rope cache builds, one factor per pair --; cos / sin of that
+//            fp32 angle evaluated in fp64 and rounded to fp32.  IMROPE gives
+//            each pair the position of its section (t, h, w interleaved); the
+//            reference fills every section of a block's position with the
+//            block's first position b * bt (src/qwfn_engine.cpp:741-743, 926,
+//            934), so every pair takes pos = b * bt.
+//   store  : rounded to fp16 (the reference's F16 pool cache).
+template <int D>
+__device__ __forceinline__ void pool_idx_block(const Geo &g, const IdxGeo &ig, const uint16_t *m,
+                                               const float *__restrict__ k_norm, float *ys, uint16_t *dst, int t0,
+                                               int lane) {
+    float cc[D / 64], sn[D / 64];
+    idx_rot_cs<D>(ig, t0, lane, cc, sn);
+    pool_idx_rows<D>(g, ig, [&](int r, int k) { return h2f(m[(int64_t)r * D + lane + 64 * k]); }, k_norm, ys, dst,
+                     lane, cc, sn);
 }
 
 // One wave per block, four blocks a workgroup: the blocks of rows (seq_ids[i]
@@ -176,33 +229,19 @@ k_idx_pool(Geo g, qwfn_kv_view v, IdxGeo ig, const uint16_t *__restrict__ raw, u
 // rows are range-checked into LDS; each is written unless a later row has the
 // same (sequence, position) -- the last one is kept --, and after a barrier
 // the last row touching each block pools it from the cache, one wave a block.
-// len (the fused decode step): row r is sequence r's token at position
-// len[r] - 1, and kv (when enabled) brings the same rows' K and V, which the
-// workgroup's upper threads append as k_append does, alongside.
 constexpr int kIdxFuseThreads = 1024;
 template <int D>
 __global__ void __launch_bounds__(kIdxFuseThreads)
 k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
                   const float *__restrict__ k_norm, const void *src, int32_t f16, const int32_t *seq_ids,
-                  const int32_t *pos, int32_t n_rows, FusedAppend kv, const int32_t *len) {
+                  const int32_t *pos, int32_t n_rows) {
     constexpr int NW = kIdxFuseThreads / 64, PER = D / 8;
     __shared__ int32_t s_seq[kIdxFuseRows], s_pos[kIdxFuseRows], s_pp[kIdxFuseRows];
     __shared__ uint8_t s_write[kIdxFuseRows], s_pool[kIdxFuseRows];
     __shared__ float ys[NW][D];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (kv.enabled) {
-        // lane i of the K/V append on thread i ^ 512: whole waves keep their
-        // lane order (the quantizers' 8-lane groups), and the rows' checks
-        // below run on threads 0 .. n_rows - 1
-        const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
-        for (int64_t i = tid ^ (kIdxFuseThreads / 2); i < total; i += kIdxFuseThreads)
-            append_lane(g, v, kv.k_new, kv.v_new, kv.src_f16, i, [&](int r, int &seq, int &t) {
-                seq = r;
-                t = len[r] - 1;
-            });
-    }
     if (tid < n_rows) {
-        const int seq = len ? tid : seq_ids ? seq_ids[tid] : 0, t = len ? len[tid] - 1 : pos[tid];
+        const int seq = seq_ids ? seq_ids[tid] : 0, t = pos[tid];
         int32_t pp = -1;
         if (seq < 0 || seq >= g.n_seq_view) set_status(v.status, QWFN_STATUS_SEQ_RANGE);
         else if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) set_status(v.status, QWFN_STATUS_POS_RANGE);
@@ -252,14 +291,68 @@ k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, 
     }
 }
 
+// The fused decode step's rows (at most kIdxFuseRows sequences, one row
+// each): sequence r's raw key written at position len[r] - 1 and its block
+// re-pooled by wave r mod 16, the block's other members read from the cache
+// and the new row taken from registers, the rotation's cos / sin computed
+// while the page-table load is in flight.  No barrier: each wave owns its
+// sequences and its slice of LDS.  kv (when enabled): the rows' K and V
+// appended as k_append does, lane i on thread i ^ 512.  Results equal
+// k_idx_append_pool's on the same rows.
+template <int D>
+__global__ void __launch_bounds__(kIdxFuseThreads)
+k_idx_decode_append(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
+                    const float *__restrict__ k_norm, const void *src, int32_t f16, const int32_t *len,
+                    int32_t n_rows, FusedAppend kv) {
+    constexpr int NW = kIdxFuseThreads / 64, K = D / 64;
+    __shared__ float ys[NW][D];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (kv.enabled) {
+        const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
+        for (int64_t i = tid ^ (kIdxFuseThreads / 2); i < total; i += kIdxFuseThreads)
+            append_lane(g, v, kv.k_new, kv.v_new, kv.src_f16, i, [&](int r, int &seq, int &t) {
+                seq = r;
+                t = len[r] - 1;
+            });
+    }
+    for (int s = w; s < n_rows; s += NW) {
+        const int L = len[s];
+        uint16_t nh[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int64_t e = (int64_t)s * D + lane + 64 * k;
+            nh[k] = f16 ? reinterpret_cast<const uint16_t *>(src)[e] : f2h(reinterpret_cast<const float *>(src)[e]);
+        }
+        const int t = L - 1;
+        if (s >= g.n_seq_view) { if (lane == 0) set_status(v.status, QWFN_STATUS_SEQ_RANGE); continue; }
+        if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (lane == 0) set_status(v.status, QWFN_STATUS_POS_RANGE); continue; }
+        const int32_t pp = phys_page(g, v.page_table, s, t);
+        const int b = t / g.bt, t0 = b * g.bt, rn = t - t0;
+        float cc[K], sn[K];
+        idx_rot_cs<D>(ig, t0, lane, cc, sn);
+        if (pp < 0) { if (lane == 0) set_status(v.status, QWFN_STATUS_PAGE_RANGE); continue; }
+        uint16_t *row = raw + ((int64_t)pp * g.pt + t % g.pt) * D;
+#pragma unroll
+        for (int k = 0; k < K; ++k) row[lane + 64 * k] = nh[k];
+        const uint16_t *m = raw + ((int64_t)pp * g.pt + t0 % g.pt) * D;   // a block never straddles pages
+        pool_idx_rows<D>(g, ig,
+                         [&](int r, int k) { return h2f(r == rn ? nh[k] : m[(int64_t)r * D + lane + 64 * k]); },
+                         k_norm, ys[w], pooled + ((int64_t)s * g.bps + b) * D, lane, cc, sn);
+    }
+}
+
 hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
                                   uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
                                   const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st,
                                   const FusedAppend &kv, const int32_t *len) {
     if (n_rows > kIdxFuseRows || (kv.enabled && !len) || (!len && !pos)) return hipErrorInvalidValue;
 #define QWFN_IDX_AP(D_)                                                                                        \
-    hipLaunchKernelGGL(k_idx_append_pool<D_>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, k_norm, \
-                       src, src_f16, seq_ids, pos, n_rows, kv, len)
+    if (len)                                                                                                   \
+        hipLaunchKernelGGL(k_idx_decode_append<D_>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, \
+                           k_norm, src, src_f16, len, n_rows, kv);                                             \
+    else                                                                                                       \
+        hipLaunchKernelGGL(k_idx_append_pool<D_>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, \
+                           k_norm, src, src_f16, seq_ids, pos, n_rows)
     switch (ig.dim) {
     case 64:  QWFN_IDX_AP(64); break;
     case 128: QWFN_IDX_AP(128); break;

@@ -157,7 +157,9 @@ hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig
 // Write and pool in one launch, for calls of at most 64 rows (a decode step):
 // among rows with the same (sequence, position) the last one is kept.
 // Rows of one k_idx_append_pool launch (a decode step of up to this many
-// sequences); kv enabled (with len): the rows' K/V appended by the same launch
+// rows).  len (the fused decode step, k_idx_decode_append): row r is sequence
+// r's at position len[r] - 1, and kv (when enabled) brings the rows' K and V,
+// appended by the same launch.
 constexpr int kIdxFuseRows = 64;
 hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
                                   uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,

@@ -336,23 +336,31 @@ def test_checkpoint_prefill(dtype):
 
 
 # ---- long contexts: more eligible blocks than the indexer workgroup's
-# registers hold (8192), selected by the 1024-thread k_select_big ----------------
+# registers hold (8192), selected by the multi-workgroup k_select_cut ------------
 
-@pytest.mark.parametrize("lengths,tie", [([40003], False), ([33000, 45001], False), ([36000], True)])
-def test_idx_select_long_context(lengths, tie):
-    """The checkpoint selection over 8,250 .. 11,250 blocks; `tie`: all-zero raw
-    keys, so every block scores the same and the index order decides (the
-    threshold bin overflows the candidate list: the radix fallback)."""
+@pytest.mark.parametrize("lengths,mode", [([40003], "random"), ([33000, 45001], "random"), ([36000], "tie"),
+                                          ([40003], "cluster")])
+def test_idx_select_long_context(lengths, mode):
+    """The checkpoint selection over 8,250 .. 11,250 blocks.  random: the top
+    blocks spread over the score row.  tie: all-zero raw keys, so every block
+    scores the same and the index order decides (the threshold bin overflows
+    the candidate list: the radix fallback).  cluster: 200 consecutive blocks
+    whose unrotated dims align with the query heads, so the top blocks crowd
+    into a few of the selection workgroups' regions."""
     cfg = CKPT
-    rng = np.random.default_rng(850 + sum(lengths) + tie)
+    tie = mode == "tie"
+    rng = np.random.default_rng(850 + sum(lengths) + tie + 7 * (mode == "cluster"))
     n = len(lengths)
     pps = max(lengths) // cfg.page_tokens + 1
     dev, host, ic, w = _pair(cfg, n, pps, seed=851)
+    q = rng.standard_normal((n, 4, 128)).astype(np.float32)
     for s, L in enumerate(lengths):
         kr = np.zeros((L, 128), np.float32) if tie else rng.standard_normal((L, 128)).astype(np.float32)
+        if mode == "cluster":                      # blocks 2000 .. 2199: dims 64.. along the heads' sum
+            kr[8000:8800, :64] *= 0.01
+            kr[8000:8800, 64:] = 0.01 * kr[8000:8800, 64:] + q[s, :, 64:].sum(0)
         qsa.idx_append_pool(ic, torch.from_numpy(kr).cuda(), torch.arange(L, dtype=torch.int32, device="cuda"),
                             seq_ids=torch.full((L,), s, dtype=torch.int32, device="cuda"))
-    q = rng.standard_normal((n, 4, 128)).astype(np.float32)
     Lmax = max(lengths)
     ws = _ws(cfg, ic, n, Lmax)
     sel, nsel = qsa.idx_select(ic, torch.from_numpy(q).cuda(),
@@ -366,6 +374,8 @@ def test_idx_select_long_context(lengths, tie):
             nb = L // 4
             exp = list(range(513 - (1 if L % 4 else 0))) + ([nb] if L % 4 else [])
             np.testing.assert_array_equal(want, np.array(exp, np.int32))
+        if mode == "cluster":                      # the whole cluster is selected
+            assert set(range(2000, 2200)) <= set(want.tolist())
         for g in range(2):
             assert gn[s, g] == 513
             np.testing.assert_array_equal(gs[s, g, :513], want, err_msg=f"seq {s} head {g}")
