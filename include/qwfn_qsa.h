@@ -182,6 +182,19 @@ int         qwfn_qsa_time_next_call(void *const events[6]);
 int qwfn_qsa_test_prefill_scores(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                                  const float *q, int32_t n_q, int32_t seq, int32_t n_blk,
                                  float *scores, float *pnorm, int32_t nb_cap, void *stream);
+/* Test hook; it has no counterpart in the reference and serves the tests of
+ * the attention's own selection over long score rows (the checkpoint layer's
+ * decode past 8192 eligible blocks).  Runs that selection alone, one
+ * workgroup per sequence: the forced/eligible rule and the exact top-k by
+ * (score desc, block asc) of row s of scores [n_seq][nb_cap] (device fp32,
+ * 16-byte aligned, nb_cap a multiple of 4 and at least max_seq_len /
+ * block_tokens + 4) at length seq_len[s], into sel [n_seq][max_sel] and
+ * n_sel [n_seq] (device int32).  QWFN_ERANGE when a row of max_seq_len holds
+ * more eligible blocks than that selection covers (49,152) or max_sel is
+ * outside [qwfn_qsa_max_selected, 1024].                                       */
+int qwfn_qsa_test_select_rows(const qwfn_qsa_shape *shape, const float *scores, int32_t nb_cap,
+                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, int32_t *sel,
+                              int32_t *n_sel, int32_t max_sel, void *stream);
 /* Validates a shape (QWFN_EINVAL) and whether this build has kernels for it
  * (QWFN_ENOTSUP).  Replaces the reference's shape constants
  * (src/qwfn_hparams.h:22-36, src/qwfn_engine.cpp:382-435).                   */

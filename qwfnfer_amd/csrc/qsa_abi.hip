@@ -185,8 +185,15 @@ WsLayout ws_layout(const Geo &g, int32_t n_seq, int32_t max_seq_len, int32_t max
     const int32_t nb_max = max_seq_len / g.bt;
     const int32_t cut_wg = (nb_max + kCutKeys - 1) / kCutKeys;
     l.cut_wg = cut && nb_max > kIdxRegKeys && !(g.shared && g.Hkv > 1) && cut_wg <= kCutWgMax ? cut_wg : 0;
-    l.cand = take(pairs * l.cut_wg * kCutKeys * sizeof(uint2));
-    l.ccnt = take(l.cut_wg ? pairs * kCutWgMax * sizeof(int32_t) : 0);
+    // ... and the per-chunk candidates of a long row's indexer workgroups
+    // (the attention then selects from them, launch_dec_selbig)
+    const int64_t n_chunks = (nb_max + kIdxChunkBlocks - 1) / kIdxChunkBlocks;
+    const bool chunks = cut && nb_max > kIdxRegKeys;
+    l.cand = take(pairs * std::max<int64_t>((int64_t)l.cut_wg * kCutKeys, chunks ? n_chunks * kIdxChunkBlocks : 0) *
+                  sizeof(uint2));
+    l.ccnt = take(l.cut_wg || chunks ? pairs * std::max<int64_t>(kCutWgMax, chunks ? n_chunks : 0) * sizeof(int32_t)
+                                     : 0);
+    l.cutk = take(chunks ? pairs * kIdxCutParts * sizeof(uint32_t) : 0);
     l.cmm = take(partials ? pairs * (l.nb_cap / kScoreRecBlocks) * sizeof(float2) : 0);
     l.lens = take((size_t)kMaxChain * n_seq * sizeof(int32_t));
     // prefill layouts (cut = false): the V-scale maxima of the matrix-core
@@ -208,6 +215,7 @@ Ws ws_bind(void *base, const WsLayout &l) {
     w.part_ml = (float *)(b + l.part_ml);
     w.cand = (uint2 *)(b + l.cand);
     w.ccnt = (int32_t *)(b + l.ccnt);
+    w.cutk = (uint32_t *)(b + l.cutk);
     w.cmm = (float2 *)(b + l.cmm);
     w.lens = (int32_t *)(b + l.lens);
     w.vmax = (float *)(b + l.vmax);
@@ -260,6 +268,29 @@ int qwfn_qsa_test_prefill_scores(const qwfn_qsa_shape *shape, const qwfn_kv_view
     g.pf_seq = seq;
     const hipError_t e = launch_pf_approx_scores(g, *view, q, n_q, n_blk, scores, nb_cap, pnorm, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "test_prefill_scores");
+}
+
+int qwfn_qsa_test_select_rows(const qwfn_qsa_shape *shape, const float *scores, int32_t nb_cap,
+                              const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, int32_t *sel,
+                              int32_t *n_sel, int32_t max_sel, void *stream) {
+    Geo g;
+    int rc = make_geo(shape, nullptr, &g, false);
+    if (rc) return rc;
+    if (!scores || !aligned(scores, 16) || !seq_len || !sel || !n_sel || n_seq < 1)
+        return fail(QWFN_EINVAL, "test_select_rows: NULL or misaligned scores (16), NULL seq_len / sel / n_sel, "
+                    "or n_seq < 1");
+    if (max_seq_len < 1 || nb_cap % 4 || nb_cap < max_seq_len / g.bt + 4)
+        return fail(QWFN_ERANGE, "test_select_rows: nb_cap %d not a multiple of 4 or below max_seq_len / "
+                    "block_tokens + 4", nb_cap);
+    const int32_t need = max_selected(shape, max_seq_len);
+    if (max_sel < need || max_sel > 1024)
+        return fail(QWFN_ERANGE, "test_select_rows: max_sel %d outside [%d, 1024]", max_sel, need);
+    const hipError_t e = launch_test_select_big(g, scores, nb_cap, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel,
+                                                (hipStream_t)stream);
+    if (e == hipErrorInvalidValue)
+        return fail(QWFN_ERANGE, "test_select_rows: a row of max_seq_len %d is longer than the selection holds",
+                    max_seq_len);
+    return e == hipSuccess ? ok() : hip_fail(e, "test_select_rows");
 }
 
 int qwfn_qsa_check_shape(const qwfn_qsa_shape *shape) {
@@ -832,7 +863,11 @@ int qwfn_idx_workspace_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *
     if (!bytes || n_seq < 1 || max_seq_len < 1)
         return fail(QWFN_EINVAL, "idx_workspace_bytes: bytes NULL or n_seq / max_seq_len < 1");
     if (n_seq > kMaxCounters) return fail(QWFN_ERANGE, "n_seq exceeds %d", kMaxCounters);
-    *bytes = ws_layout(idx_scoring_geo(g, ishape), n_seq, max_seq_len, max_selected(shape, max_seq_len), false).total;
+    // the indexer's layout, then the attention's (the fused decode call keeps
+    // the indexer's candidates while the attention writes its partials)
+    const int32_t need = max_selected(shape, max_seq_len);
+    *bytes = align256(ws_layout(idx_scoring_geo(g, ishape), n_seq, max_seq_len, need, false).total) +
+             ws_layout(g, n_seq, max_seq_len, need).total;
     return ok();
 }
 
@@ -938,17 +973,38 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     if (ws_bytes < total) return fail(QWFN_ERANGE, "idx decode: workspace of %zu bytes < %zu", ws_bytes, total);
     hipStream_t st = (hipStream_t)stream;
     const int32_t f16 = src_dtype == QWFN_SRC_F16;
+    // Rows longer than the indexer workgroup's registers hold: the attention
+    // workgroups select for themselves (no selection launch).  The append
+    // launch also places a sampled cut of each row, the indexer's workgroups
+    // keep the keys above it as candidates, and the attention ranks those
+    // exactly.  The attention's layout then follows the indexer's in the
+    // workspace (qwfn_idx_workspace_bytes sizes both), so its partials never
+    // touch the candidates; a workspace sized for one layout keeps the
+    // selection launch.
+    const bool fused_sel = max_seq_len / g.bt > kIdxRegKeys && dec_selbig_fits(g, max_seq_len, max_sel) &&
+                           ishape->idx_dim <= 128 && ishape->n_idx_head * ishape->idx_dim <= kIdxMaxCutHeads * 128 &&
+                           ws_bytes >= align256(li.total) + la.total;
+    const Ws wi = ws_bind(ws, li);
+    const IdxCut cut{fused_sel ? q_idx : nullptr, wi.cutk, ishape->n_idx_head, max_seq_len};
     // the K/V rows, the raw indexer key and its block's pooled key: one launch
     hipError_t e = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled,
                                           iview->k_norm, k_raw, f16, nullptr, nullptr, n_seq, st,
-                                          FusedAppend{k_new, v_new, f16, 1}, seq_len);
+                                          FusedAppend{k_new, v_new, f16, 1}, seq_len, cut);
     if (e != hipSuccess) return hip_fail(e, "idx decode: append");
     qwfn_kv_view vi = *view;
     vi.pooled = (float *)iview->pooled;                   // fp16 keys (Geo::pooled_f16)
-    e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, ws_bind(ws, li),
-                       FusedAppend{nullptr, nullptr, 0, 0}, st);
+    e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, wi,
+                       FusedAppend{nullptr, nullptr, 0, 0}, st, true, !fused_sel);
     if (e != hipSuccess) return hip_fail(e, "idx decode: indexer");
-    e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, ws_bind(ws, la), st);
+    if (fused_sel) {
+        Ws wa = ws_bind((uint8_t *)ws + align256(li.total), la);
+        wa.scores = wi.scores;
+        wa.cand = wi.cand;
+        wa.ccnt = wi.ccnt;
+        e = launch_dec_selbig(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, wa, st);
+    } else {
+        e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, ws_bind(ws, la), st);
+    }
     return e == hipSuccess ? ok() : hip_fail(e, "idx decode: attention");
 }
 

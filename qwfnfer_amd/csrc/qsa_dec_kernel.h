@@ -2,8 +2,10 @@
 // helpers, shared by qsa_decode.hip (q8_0) and qsa_decode_kv.hip (q4_0, F16),
 // which instantiate disjoint sets of it: the attention of
 // qwfn_sparse_decode_attn (a given selection or dense), of the fused
-// qwfn_sparse_attn_decode (the workgroup selects from the indexer's scores)
-// and of prefill chunks whose cache rows are in the K layout.
+// qwfn_sparse_attn_decode (the workgroup selects from the indexer's scores),
+// of the checkpoint layer's fused qwfn_idx_sparse_attn_decode past 8192
+// blocks (the workgroup ranks the indexer's candidates) and of prefill chunks
+// whose cache rows are in the K layout.
 //
 // One workgroup of four waves (one per SIMD) per part of TM tiles of a
 // (sequence, KV head); wave w owns cells 16w .. 16w+15 of every tile, so a
@@ -30,7 +32,7 @@
 // that does not depend on the selection (the length, the score row, the query
 // rows, the sequence's page-table row) is loaded in the first round trip and
 // the selection is a short exact top-k over a 2048-bin histogram held by the
-// four waves.
+// four waves (kSelect), or over the candidates the indexer left (kSelBig).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -42,6 +44,7 @@
 #include <atomic>
 
 #include "qsa_device.h"
+#include "qsa_select.h"
 
 namespace qwfn_qsa {
 
@@ -54,7 +57,14 @@ constexpr int kDecCand = 256;                   // threshold-bin keys ranked pai
 constexpr int kDecPtLds = 4096;                 // page-table entries parked in LDS at most
 constexpr int kDecSelMax = 1024;                // selected blocks kept in LDS
 
-enum DecMode { kGiven = 0, kDense = 1, kSelect = 2 };
+enum DecMode { kGiven = 0, kDense = 1, kSelect = 2, kSelBig = 3 };
+
+// kSelBig: a long row of at most kDecBigRnd * kDecThreads * 4 = 49,152 blocks
+// (longer rows take the selection launch), kDecBigChunks indexer chunks.
+constexpr int kDecBigRnd = 48;
+constexpr int kDecBigChunks = kDecBigRnd * kDecThreads * 4 / kIdxChunkBlocks;   // the indexer's chunks a row
+constexpr int kDecBigCpt = kDecBigChunks / kDecThreads;                          // chunks a thread gathers
+constexpr int kDecBigPre = 12;                  // candidate slots of a chunk read in the first round trip
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
@@ -65,6 +75,23 @@ struct DecSel {
     uint32_t hist[kDecBins + 64];                // + one trash bin per lane
     uint32_t cand_key[kDecWaves * kDecCand + 64];   // threshold-bin keys, a region per wave
     int32_t cand_b[kDecWaves * kDecCand + 64];      // (+ one trash slot per lane)
+};
+
+// The selection scratch of kSelBig (the candidates, their histogram, the
+// threshold bin and the winners' bit map); the fields the shared selection
+// routines (sample_cut_of, hist_cut, select_radix) use.
+struct DecSelBig {
+    uint32_t hist[4096 + 64];                    // + one trash bin per lane
+    u2v cand[kSelCandMax + 64];                  // candidates (key, block), in block order (+ one trash slot per lane)
+    uint8_t cok[kSelCandMax];                    // the threshold bin's verdicts, by candidate
+    uint32_t wbits[kSelCandMax / 32];            // the winners, bit c % 32 of word c / 32
+    int32_t wpre[kSelCandMax / 32];              // winners in the words before
+    uint32_t cand_key[kCandMax + 64];            // the threshold bin's keys, blocks
+    int32_t cand_b[kCandMax + 64];
+    float red[2 * kDecWaves];
+    uint32_t kred[2 * kDecWaves];
+    int tmp[kDecWaves];
+    int bin, need, cnt_b, ncand, nbin;
 };
 
 template <int G>
@@ -107,7 +134,7 @@ template <int HD, int G, int MODE, int TM, int LY = kLyQ8>
 constexpr int dec_union_bytes() {
     constexpr int st = TM * kDecWaves * DecStage<HD, LY>::BYTES;
     constexpr int wo = kDecWaves * G * HD * 4;
-    constexpr int se = MODE == kSelect ? (int)sizeof(DecSel) : 0;
+    constexpr int se = MODE == kSelect ? (int)sizeof(DecSel) : MODE == kSelBig ? (int)sizeof(DecSelBig) : 0;
     constexpr int m = st > wo ? st : wo;
     return ((m > se ? m : se) + 15) / 16 * 16;
 }
@@ -435,6 +462,184 @@ __device__ __forceinline__ int dec_choose(const Geo &g, const Ws &ws, int L, int
     return min(sh.nsel, max_sel);
 }
 
+// kSelBig: the histogram and the threshold bin's count start at zero (before
+// the caller's first barrier).
+__device__ __forceinline__ void dec_big_zero(DecSelBig &bs) {
+    const int tid = threadIdx.x;
+    u4v *h4 = reinterpret_cast<u4v *>(bs.hist);
+    const u4v z = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < (4096 + 64) / 4; i += kDecThreads) h4[i] = z;
+    if (tid == 0) { bs.ncand = 0; bs.nbin = 0; }
+}
+
+// The exact selection among the C candidates (key, block) of bs.cand, in
+// block order, their keys within [kmin, kmax] (topk <= C <= kSelCandMax; the
+// histogram zeroed): a 4096-bin histogram linear in the key locates the
+// threshold bin; the keys above it are taken, and the bin's own keys too
+// when it holds just the keys still needed, else they are ranked by (key
+// desc, candidate asc -- block asc).  Thread t reads candidates u NT + t
+// (consecutive lanes, consecutive LDS words); each round's winners become two
+// words of a bit map by one ballot, and thread t < kSelCandMax / 32 emits the
+// winners of word t, so they go out in candidate (block) order after the
+// sink blocks.  Returns false, with nothing emitted, when the threshold bin
+// holds more than kCandMax keys.
+__device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uint32_t kmin, uint32_t kmax,
+                                              const SelOut &out, DecSelBig &bs) {
+    constexpr int NT = kDecThreads, CPT = kSelCandMax / NT;
+    static_assert(CPT * NT == kSelCandMax && kSelCandMax / 32 <= NT, "whole candidate rounds; a bit-map word a thread");
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const float sc2 = 4096.0f / ((float)(kmax - kmin) + 1.0f);
+    // every round's reads are independent and go out together (a round past
+    // the candidates reads slot 0 and changes nothing)
+    uint32_t kb[CPT];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = u * NT + tid;
+        kb[u] = (uint32_t)fminf((float)(bs.cand[c < C ? c : 0][0] - kmin) * sc2, 4095.0f);
+        atomicAdd(&bs.hist[c < C ? kb[u] : 4096u + (uint32_t)lane], 1u);
+    }
+    __syncthreads();
+    if (wid == 0) hist_cut(bs, topk);
+    __syncthreads();
+    const uint32_t B = (uint32_t)bs.bin;
+    const int need = bs.need, cB = bs.cnt_b;
+    if (cB > need) {                               // (uniform) rank the threshold bin
+        if (cB > kCandMax) return false;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const int c = u * NT + tid;
+            if (c < C && kb[u] == B) {
+                const int at = atomicAdd(&bs.nbin, 1);
+                bs.cand_key[at] = bs.cand[c][0];
+                bs.cand_b[at] = c;
+            }
+        }
+        __syncthreads();
+        if (tid < cB) {
+            const uint32_t k = bs.cand_key[tid];
+            const int c = bs.cand_b[tid];
+            int rk = 0;
+            for (int jj = 0; jj < cB; ++jj) {
+                const uint32_t kj = bs.cand_key[jj];
+                rk += (kj > k) || (kj == k && bs.cand_b[jj] < c);
+            }
+            bs.cok[c] = rk < need;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = u * NT + tid;
+        const bool win = c < C && (kb[u] > B || (kb[u] == B && (cB <= need || bs.cok[c])));
+        const uint64_t m = __ballot(win);
+        if (lane == 0) {                           // candidates u NT + 64 wid .. + 63
+            bs.wbits[(u * NT + 64 * wid) / 32] = (uint32_t)m;
+            bs.wbits[(u * NT + 64 * wid) / 32 + 1] = (uint32_t)(m >> 32);
+        }
+    }
+    __syncthreads();
+    // emission: a winner's place is the winners in the words before its own
+    // plus those below it in its word; thread t emits candidates u NT + t
+    const uint32_t wv = tid < kSelCandMax / 32 ? bs.wbits[tid] : 0u;
+    int tot;
+    const int pre = block_excl_sum<NT>(__builtin_popcount(wv), bs.tmp, &tot);
+    if (tid < kSelCandMax / 32) bs.wpre[tid] = pre;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int c = u * NT + tid;
+        const uint32_t wd = bs.wbits[c >> 5];
+        const int pos = bs.wpre[c >> 5] + __builtin_popcount(wd & ((1u << (c & 31)) - 1u));
+        const int32_t b = (int32_t)bs.cand[c][1];
+        if (((wd >> (c & 31)) & 1u) && pos < topk) out.put(g.sink + pos, b);
+    }
+    return true;
+}
+
+// The end of a long row's selection from C candidates in bs.cand (an upper
+// set of the row's eligible keys, in block order, their keys within [kmin,
+// kmax]): the exact selection among them, or, when
+// they number fewer than topk or more than kSelCandMax or their threshold bin
+// overflows, the radix passes over the row sc; then the forced blocks.
+__device__ __forceinline__ void dec_big_tail(const Geo &g, const Ranges &r, int C, int topk, uint32_t kmin,
+                                             uint32_t kmax, const float *sc, const SelOut &out, DecSelBig &bs) {
+    bool done = false;
+    if (C >= topk && C <= kSelCandMax) done = dec_big_exact(g, C, topk, kmin, kmax, out, bs);   // (uniform)
+    if (!done) {
+        __syncthreads();                           // the candidate path's LDS reads are done
+        select_radix<kDecThreads>(g, sc, r, topk, out, bs);
+    }
+    emit_forced<kDecThreads>(g, r, topk, out);
+}
+
+// kSelBig: the selection of sequence s's long row into sh.sel / sh.nsel by
+// all threads (dec_big_zero and a barrier passed since).  The indexer's
+// workgroups left, per chunk of kIdxChunkBlocks blocks, the eligible keys at
+// or above the append launch's cut key (ws.cand, in block order, counts in
+// ws.ccnt).  Thread t owns chunks kDecBigCpt t ..: their counts cc and first
+// kDecBigPre slots ce came in the first round trip; they are placed into
+// bs.cand in block order (a chunk's further candidates, rarely any, are read
+// here) and dec_big_tail selects.  Returns min(count, max_sel), 0 for a length out of
+// range.
+template <int G>
+__device__ __forceinline__ int dec_choose_big(const Geo &g, const Ws &ws, int s, int n_chunks,
+                                              const int (&cc)[kDecBigCpt], const u2v (&ce)[kDecBigCpt][kDecBigPre], int L,
+                                              int max_seq_len, int max_sel, DecSelBig &bs, DecShared<G> &sh) {
+    constexpr int NT = kDecThreads;
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (!(L >= 1 && L <= max_seq_len)) return 0;
+    const Ranges r = qsa_ranges(g, L);
+    const int ne = r.e_hi - r.e_lo, topk = eff_topk(g, r);
+    const SelOut out{sh.sel, &sh.nsel, 0, 1};
+    if (g.topk <= 0 || ne <= topk) {               // every block below the length
+        const int nb = r.b_last + 1;
+        for (int i = tid; i < nb && i < kDecSelMax; i += NT) sh.sel[i] = i;
+        if (tid == 0) sh.nsel = nb;
+    } else if (topk == 0) {                        // the forced blocks fill the count
+        emit_forced<NT>(g, r, 0, out);
+    } else {
+        int my = 0;
+#pragma unroll
+        for (int i = 0; i < kDecBigCpt; ++i) my += cc[i];
+        int C;
+        int off = block_excl_sum<NT>(my, bs.tmp, &C);
+        uint32_t kmn = 0xffffffffu, kmx = 0u;
+        if (C >= topk && C <= kSelCandMax) {       // (uniform)
+            const uint2 *cand = ws.cand + (int64_t)s * n_chunks * kIdxChunkBlocks;
+#pragma unroll
+            for (int i = 0; i < kDecBigCpt; ++i) {
+                const int n = cc[i];
+#pragma unroll
+                for (int j = 0; j < kDecBigPre; ++j) {
+                    bs.cand[j < n ? off + j : kSelCandMax + lane] = ce[i][j];
+                    kmn = j < n ? min(kmn, ce[i][j][0]) : kmn;
+                    kmx = j < n ? max(kmx, ce[i][j][0]) : kmx;
+                }
+                const uint2 *src = cand + (int64_t)(kDecBigCpt * tid + i) * kIdxChunkBlocks;
+                for (int j = kDecBigPre; j < n; ++j) {
+                    const uint2 x = src[j];
+                    bs.cand[off + j] = u2v{x.x, x.y};
+                    kmn = min(kmn, x.x);
+                    kmx = max(kmx, x.x);
+                }
+                off += n;
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                kmn = min(kmn, (uint32_t)__shfl_xor((int)kmn, o));
+                kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o));
+            }
+            if (lane == 0) { bs.kred[tid >> 6] = kmn; bs.kred[kDecWaves + (tid >> 6)] = kmx; }
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) { kmn = min(kmn, bs.kred[w]); kmx = max(kmx, bs.kred[kDecWaves + w]); }
+        }
+        dec_big_tail(g, r, C, topk, kmn, kmx, ws.scores + (int64_t)s * ws.nb_cap, out, bs);
+    }
+    __syncthreads();
+    return min(sh.nsel, max_sel);
+}
+
 // fp16 scale j (0 .. 4*NB-1, cell-major: cell i = j / NB, block kb = j % NB)
 // of a lane's scale vector.
 template <int NS>
@@ -460,7 +665,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     static_assert(G <= 16, "one matrix-core column per query head");
     static_assert(TM >= 1 && TM <= 4, "tiles a part");
     static_assert(!RF || LY == kLyQ8, "fp16-rounded K/V: q8_0 with V dim-major");
-    static_assert(LY != kLyQ8K || MODE != kSelect, "gathered q8_0 tiles: a given selection or dense");
+    static_assert(LY != kLyQ8K || MODE != kSelect, "gathered q8_0 tiles: a given selection, dense or kSelBig");
     using S = DecStage<HD, LY>;
     constexpr int NB = S::NB, ND = S::ND, NS = S::NS;
     constexpr int UB = dec_union_bytes<HD, G, MODE, TM, LY>();
@@ -510,6 +715,25 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     float sv[KS];
     float2 rec[dec_rpl<KS>()];
     if constexpr (MODE == kSelect) dec_load_sel_inputs<KS>(g, ws, pair, sv, rec);
+    // kSelBig: the candidate counts of this thread's chunks of the sequence's row
+    const int n_chunks = (max_seq_len / g.bt + kIdxChunkBlocks - 1) / kIdxChunkBlocks;
+    int cc[kDecBigCpt];
+    u2v ce[kDecBigCpt][kDecBigPre];                // (the first candidate slots of each chunk)
+#pragma unroll
+    for (int i = 0; i < kDecBigCpt; ++i) {
+        const int ch = min(kDecBigCpt * tid + i, n_chunks - 1);
+        cc[i] = 0;
+        if constexpr (MODE == kSelBig) {
+            cc[i] = kDecBigCpt * tid + i < n_chunks ? ws.ccnt[(int64_t)s * n_chunks + ch] : 0;
+            const u4v *src = reinterpret_cast<const u4v *>(ws.cand + ((int64_t)s * n_chunks + ch) * kIdxChunkBlocks);
+#pragma unroll
+            for (int j = 0; j < kDecBigPre / 2; ++j) {
+                const u4v x = src[j];
+                ce[i][2 * j] = u2v{x[0], x[1]};
+                ce[i][2 * j + 1] = u2v{x[2], x[3]};
+            }
+        }
+    }
     int n_given = 0;
     // kGiven: the tiles' blocks; kDense: their pages.  GATH: the block of the
     // lane's cell (lane & 15 of the wave's 16) in each tile
@@ -532,6 +756,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     }
     if constexpr (MODE == kGiven) n_given = nsel[pair];
     if constexpr (MODE == kSelect) dec_zero_hist(ss);   // the selection histogram starts at zero
+    if constexpr (MODE == kSelBig) dec_big_zero(*reinterpret_cast<DecSelBig *>(dec_dyn));
     // the query split: scaled by a power of two so its largest magnitude is in
     // [2^13, 2^14), then fp16 high + low parts (residual below 2^-22 of the
     // largest).  The query loads went out first, so this waits for them alone
@@ -575,6 +800,15 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
             if (tid == 0) nsel[pair] = n;
         }
+    } else if constexpr (MODE == kSelBig) {
+        // one shared row a sequence (ws.scores, ws.cand, ws.ccnt: the indexer's)
+        __syncthreads();                           // the parked page table, the zeroed bit map
+        n = dec_choose_big<G>(g, ws, s, n_chunks, cc, ce, L, max_seq_len, max_sel,
+                              *reinterpret_cast<DecSelBig *>(dec_dyn), sh);
+        if (part == 0) {
+            for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
+            if (tid == 0) nsel[pair] = n;
+        }
     } else {
         if (MODE == kGiven || GATH) __syncthreads();   // the parked page table
         if (ok) {
@@ -599,7 +833,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             const int cidx = tile * 64 + 16 * w + (lane & 15);
             const int slot = cidx / g.bt;
             int blk;
-            if constexpr (MODE == kSelect) blk = sh.sel[min(slot, kDecSelMax - 1)];
+            if constexpr (MODE == kSelect || MODE == kSelBig) blk = sh.sel[min(slot, kDecSelMax - 1)];
             else blk = pre[min(i, nt - 1)];
             const int64_t t = (int64_t)blk * g.bt + cidx % g.bt;
             const bool in = i < nt && slot < n && blk >= 0 && t < L;
@@ -617,7 +851,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         vm[i] = 0;
         const int tile = t_first + min(i, nt - 1);
         int blk;
-        if constexpr (MODE == kSelect) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
+        if constexpr (MODE == kSelect || MODE == kSelBig) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
         else if constexpr (MODE == kGiven) blk = pre[min(i, nt - 1)];
         else blk = tile / tpb;
         const int64_t t0 = (int64_t)blk * g.bt + (tile % tpb) * 64;
@@ -1449,6 +1683,104 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
     if (e != hipSuccess) return e;
     return launch_merge(g, v, seq_len, n_seq, max_seq_len, select ? ns : nsel, max_sel, !select && !sel, out, ws,
                         tpw, st);
+}
+
+// kSelBig: the attention selecting from one long shared row a sequence (the
+// indexer's candidates ws.cand / ws.ccnt, its scores ws.scores for the
+// fallback), one tile a workgroup, then the merge.
+template <int HD, int G, int LY>
+hipError_t launch_dec_selbig_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                               int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                               float *out, const Ws &ws, hipStream_t st) {
+    const int npt_lds = dec_npt_lds(g, max_seq_len, kGiven);
+    const int dyn = dec_union_bytes<HD, G, kSelBig, 1, LY>() + 4 * npt_lds;
+    launch_dec_tm<HD, G, kSelBig, kDecBigRnd, 1, false, LY>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel,
+                                                            ws, npt_lds, dyn, st);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_merge(g, v, seq_len, n_seq, max_seq_len, nsel, max_sel, false, out, ws, 1, st);
+}
+
+// The selection of kSelBig alone, for the test entry point: one workgroup a
+// sequence over its score row (rows of nb_cap), the selection written out.
+// The inputs the product path takes from the append and indexer launches are
+// restated on the row itself: the cut from kIdxCutSamples evenly spaced scores
+// (sample_cut_of, cut_key over the indexer's four samples a thread), then, per
+// chunk of kIdxChunkBlocks eligible blocks (one a wave at a time), the keys at
+// or above it as candidates in block order; dec_big_tail selects.
+__global__ void __launch_bounds__(kDecThreads)
+k_test_select_big(Geo g, const float *scores, int32_t nb_cap, const int32_t *seq_len, int32_t max_seq_len,
+                  int32_t *sel, int32_t *nsel, int32_t max_sel) {
+    constexpr int NT = kDecThreads;
+    __shared__ DecShared<1> sh;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dec_dyn[];
+    DecSelBig &bs = *reinterpret_cast<DecSelBig *>(dec_dyn);
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int L = seq_len[s];
+    const float *sc = scores + (int64_t)s * nb_cap;
+    dec_big_zero(bs);
+    __syncthreads();
+    int n = 0;
+    if (L >= 1 && L <= max_seq_len) {
+        const Ranges r = qsa_ranges(g, L);
+        const int ne = r.e_hi - r.e_lo, topk = eff_topk(g, r);
+        const SelOut out{sh.sel, &sh.nsel, 0, 1};
+        if (g.topk <= 0 || ne <= topk) {
+            const int nb = r.b_last + 1;
+            for (int i = tid; i < nb && i < kDecSelMax; i += NT) sh.sel[i] = i;
+            if (tid == 0) sh.nsel = nb;
+        } else if (topk == 0) {
+            emit_forced<NT>(g, r, 0, out);
+        } else {
+            const BufRsrc rsc = buf_rsrc(sc, (uint32_t)r.e_hi * 4u);
+            const int rs = sample_rank<kIdxCutSamples>(r, topk);
+            uint32_t tk = 0u;                      // no cut: every key a candidate
+            if (rs > 0) {
+                float sv[kIdxCutSamples / NT];
+                sample_load<NT, 0, kIdxCutSamples>(rsc, r, sv);
+                const CutMap cut = sample_cut_of<NT>(sv, rs, bs);
+                tk = cut_key<NT>(cut, sv, bs.kred);
+                u4v *h4 = reinterpret_cast<u4v *>(bs.hist);
+                for (int i = tid; i < (4096 + 64) / 4; i += NT) h4[i] = u4v{0u, 0u, 0u, 0u};
+            }
+            uint32_t kmn = 0xffffffffu, kmx = 0u;
+            int run = 0;                           // candidates of the chunks before (uniform)
+#pragma unroll 1
+            for (int c0 = 0; c0 * kIdxChunkBlocks < ne; c0 += kDecWaves) {
+                const int b = r.e_lo + (c0 + w) * kIdxChunkBlocks + lane;
+                const uint32_t k = score_key(BufLoad<1>::at(rsc, b * 4, 0)[0]);
+                const bool in = b < r.e_hi && k >= tk;
+                const uint64_t m = __ballot(in);
+                if (lane == 0) bs.tmp[w] = __builtin_popcountll(m);
+                __syncthreads();
+                int at = run + __builtin_popcountll(m & ((1ull << lane) - 1ull)), tot = 0;
+#pragma unroll
+                for (int i = 0; i < kDecWaves; ++i) {
+                    at += i < w ? bs.tmp[i] : 0;
+                    tot += bs.tmp[i];
+                }
+                if (in && at < kSelCandMax) bs.cand[at] = u2v{k, (uint32_t)b};
+                kmn = in ? min(kmn, k) : kmn;
+                kmx = in ? max(kmx, k) : kmx;
+                run += tot;
+                __syncthreads();
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                kmn = min(kmn, (uint32_t)__shfl_xor((int)kmn, o));
+                kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o));
+            }
+            if (lane == 0) { bs.kred[w] = kmn; bs.kred[kDecWaves + w] = kmx; }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kDecWaves; ++i) { kmn = min(kmn, bs.kred[i]); kmx = max(kmx, bs.kred[kDecWaves + i]); }
+            dec_big_tail(g, r, run, topk, kmn, kmx, sc, out, bs);
+        }
+        __syncthreads();
+        n = min(sh.nsel, max_sel);
+    }
+    for (int i = tid; i < n; i += NT) sel[(int64_t)s * max_sel + i] = sh.sel[i];
+    if (tid == 0) nsel[s] = n;
 }
 
 template <int HD, int G, int LY>

@@ -79,6 +79,33 @@ hipError_t launch_dec_loop(const Geo &g, const qwfn_kv_view &v, const float *q, 
     return hipErrorInvalidValue;
 }
 
+// A long row the attention's own selection covers: at most kDecBigChunks
+// indexer chunks of kIdxChunkBlocks blocks.
+static bool dec_selbig_row(const Geo &g, int32_t max_seq_len) {
+    return (int64_t)max_seq_len / g.bt <= (int64_t)kDecBigChunks * kIdxChunkBlocks;
+}
+
+bool dec_selbig_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel) {
+    return dec_layout(g) == kLyQ8K && g.shared && !g.pf && g.topk > 0 && max_sel <= kDecSelMax &&
+           g.hd == 256 && g.G == 12 && dec_selbig_row(g, max_seq_len);
+}
+
+hipError_t launch_dec_selbig(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                             int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                             float *out, const Ws &ws, hipStream_t st) {
+    if (!dec_selbig_fits(g, max_seq_len, max_sel)) return hipErrorInvalidValue;
+    return launch_dec_selbig_t<256, 12, kLyQ8K>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st);
+}
+
+hipError_t launch_test_select_big(const Geo &g, const float *scores, int32_t nb_cap, const int32_t *seq_len,
+                                  int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                                  hipStream_t st) {
+    if (max_sel > kDecSelMax || !dec_selbig_row(g, max_seq_len)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_test_select_big, dim3((unsigned)n_seq), dim3(kDecThreads), (unsigned)sizeof(DecSelBig), st, g,
+                       scores, nb_cap, seq_len, max_seq_len, sel, nsel, max_sel);
+    return hipGetLastError();
+}
+
 hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                                 int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st) {

@@ -15,6 +15,7 @@
 
 #include "qsa_append.h"
 #include "qsa_device.h"
+#include "qsa_select.h"
 
 namespace qwfn_qsa {
 
@@ -291,6 +292,84 @@ k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, 
     }
 }
 
+// Part p of sequence s's cut for the attention's own selection (one of the
+// kIdxCutParts workgroups a sequence of the fused decode step's append
+// launch): the eligible blocks e_lo + j * n_eligible / kIdxCutSamples, j = p
+// kIdxCutPer .. + kIdxCutPer - 1, are scored from the pool cache (8 lanes a
+// block, dims 32 i + 4 lane .. + 3 a lane, the query heads' dots relu'd when
+// set and summed); wave 0 then finds the ceil(rs / kIdxCutParts)-th largest
+// of their keys by a bitwise search (the largest key T with that many sample
+// keys at or above it: one compare and ballot count a bit) into cutk[s][p].
+// The indexer takes every eligible key at or above the parts' 4th smallest
+// threshold as a candidate, and the attention ranks them exactly when they
+// number at least topk (the selection is exact for any threshold; this one
+// makes that the usual case), so the samples need not match the indexer's
+// scores bit for bit.  The block this launch re-pools (the row's last) is
+// never a sample.
+constexpr int kIdxCutPer = kIdxCutSamples / kIdxCutParts;     // samples a workgroup
+constexpr int kIdxCutLanes = kIdxFuseThreads / kIdxCutPer;    // lanes a sample
+static_assert(kIdxCutLanes == 8 && kIdxCutPer == 2 * 64, "8 lanes a sample; 2 keys a lane of wave 0");
+struct IdxCutShared {
+    float q[kIdxMaxCutHeads * 128];
+    uint32_t key[kIdxCutPer];
+};
+template <int D>
+__device__ __forceinline__ void idx_sample_cut(const Geo &g, const uint16_t *pooled, const int32_t *len,
+                                               const IdxCut &ct, int s, int part, IdxCutShared &sh) {
+    constexpr int NT = kIdxFuseThreads, NL = kIdxCutLanes;
+    static_assert(D % (4 * NL) == 0, "whole 4-dim pieces a lane");
+    const int tid = threadIdx.x, jl = tid % NL;
+    const int L = len[s];
+    int rs = 0;
+    Ranges r{0, 0, 0, 0};
+    if (L >= 1 && L <= ct.max_seq_len && s < g.n_seq_view) {
+        r = qsa_ranges(g, L);
+        const int topk = eff_topk(g, r);
+        if (g.topk > 0 && r.e_hi - r.e_lo > topk) rs = sample_rank<kIdxCutSamples>(r, topk);
+    }
+    uint32_t tk = 0u;                              // no cut: every key a candidate
+    if (rs > 0) {                                  // (uniform)
+        const int nq = ct.n_head * D;
+        const int j = part * kIdxCutPer + tid / NL;
+        const uint16_t *P =
+            pooled + ((int64_t)s * g.bps + r.e_lo + (int)((int64_t)j * (r.e_hi - r.e_lo) / kIdxCutSamples)) * D;
+        uint2 pk[D / (4 * NL)];
+#pragma unroll
+        for (int i = 0; i < D / (4 * NL); ++i) pk[i] = *reinterpret_cast<const uint2 *>(P + 4 * NL * i + 4 * jl);
+        for (int i = tid; i < nq; i += NT) sh.q[i] = ct.q_idx[(int64_t)s * nq + i];
+        __syncthreads();
+        float score = 0.0f;
+        for (int h = 0; h < ct.n_head; ++h) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < D / (4 * NL); ++i) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(&sh.q[h * D + 4 * NL * i + 4 * jl]);
+                acc = fmaf(q4.x, h2f((uint16_t)pk[i].x), acc);
+                acc = fmaf(q4.y, h2f((uint16_t)(pk[i].x >> 16)), acc);
+                acc = fmaf(q4.z, h2f((uint16_t)pk[i].y), acc);
+                acc = fmaf(q4.w, h2f((uint16_t)(pk[i].y >> 16)), acc);
+            }
+            acc += __shfl_xor(acc, 1);
+            acc += __shfl_xor(acc, 2);
+            acc += __shfl_xor(acc, 4);
+            score += g.relu && !(acc > 0.0f) ? 0.0f : acc;
+        }
+        if (jl == 0) sh.key[tid / NL] = score_key(score);
+        __syncthreads();
+        if (tid < 64) {                            // wave 0: two sample keys a lane
+            const uint2 k2 = reinterpret_cast<const uint2 *>(sh.key)[tid];
+            const int need = (rs + kIdxCutParts - 1) / kIdxCutParts;
+#pragma unroll 1
+            for (int bit = 31; bit >= 0; --bit) {
+                const uint32_t t = tk | (1u << bit);
+                const int n = __builtin_popcountll(__ballot(k2.x >= t)) + __builtin_popcountll(__ballot(k2.y >= t));
+                tk = n >= need ? t : tk;
+            }
+        }
+    }
+    if (tid == 0) ct.cutk[(int64_t)s * kIdxCutParts + part] = tk;
+}
+
 // The fused decode step's rows (at most kIdxFuseRows sequences, one row
 // each): sequence r's raw key written at position len[r] - 1 and its block
 // re-pooled by wave r mod 16, the block's other members read from the cache
@@ -303,10 +382,20 @@ template <int D>
 __global__ void __launch_bounds__(kIdxFuseThreads)
 k_idx_decode_append(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, uint16_t *__restrict__ pooled,
                     const float *__restrict__ k_norm, const void *src, int32_t f16, const int32_t *len,
-                    int32_t n_rows, FusedAppend kv) {
+                    int32_t n_rows, FusedAppend kv, IdxCut ct) {
     constexpr int NW = kIdxFuseThreads / 64, K = D / 64;
-    __shared__ float ys[NW][D];
+    __shared__ union {
+        float ys[NW][D];
+        IdxCutShared cut;
+    } shu;
+    float (&ys)[NW][D] = shu.ys;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (blockIdx.x > 0) {                          // workgroup 1 + p + kIdxCutParts s: part p of sequence s's cut
+        if constexpr (D <= 128)
+            idx_sample_cut<D>(g, pooled, len, ct, (blockIdx.x - 1) / kIdxCutParts, (blockIdx.x - 1) % kIdxCutParts,
+                              shu.cut);
+        return;
+    }
     if (kv.enabled) {
         const int64_t total = (int64_t)n_rows * 2 * g.Hkv * (g.hd / 32) * 8;
         for (int64_t i = tid ^ (kIdxFuseThreads / 2); i < total; i += kIdxFuseThreads)
@@ -344,12 +433,15 @@ k_idx_decode_append(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw
 hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
                                   uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
                                   const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st,
-                                  const FusedAppend &kv, const int32_t *len) {
+                                  const FusedAppend &kv, const int32_t *len, const IdxCut &cut) {
     if (n_rows > kIdxFuseRows || (kv.enabled && !len) || (!len && !pos)) return hipErrorInvalidValue;
+    if (cut.q_idx && (!len || ig.dim > 128 || cut.n_head < 1 || cut.n_head * ig.dim > kIdxMaxCutHeads * 128))
+        return hipErrorInvalidValue;
 #define QWFN_IDX_AP(D_)                                                                                        \
     if (len)                                                                                                   \
-        hipLaunchKernelGGL(k_idx_decode_append<D_>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, \
-                           k_norm, src, src_f16, len, n_rows, kv);                                             \
+        hipLaunchKernelGGL(k_idx_decode_append<D_>, dim3(1 + (cut.q_idx ? n_rows * kIdxCutParts : 0)),          \
+                           dim3(kIdxFuseThreads), 0,                                                            \
+                           st, g, v, ig, raw, pooled, k_norm, src, src_f16, len, n_rows, kv, cut);              \
     else                                                                                                       \
         hipLaunchKernelGGL(k_idx_append_pool<D_>, dim3(1), dim3(kIdxFuseThreads), 0, st, g, v, ig, raw, pooled, \
                            k_norm, src, src_f16, seq_ids, pos, n_rows)

@@ -51,6 +51,8 @@ constexpr int32_t kCutKeys = 4096;
 constexpr int32_t kCutWgMax = 64;
 constexpr int32_t kMaxChain = 8;          // positions of one chained decode call (qwfn_sparse_attn_decode_chain)
 constexpr int32_t kScoreRecBlocks = 16;   // blocks per (min, max) score record of the fused call's scoring
+constexpr int32_t kIdxChunkBlocks = 64;   // blocks an indexer workgroup scores (its candidate slots)
+constexpr int32_t kIdxCutSamples = 1024;  // sampled scores of a long decode row's cut
 struct Ws {
     int32_t *cnt_idx;    // [kMaxCounters] indexer completion counters
     int32_t *sel;        // [n_seq][Hkv][max_sel]  selection of the fused step
@@ -59,7 +61,9 @@ struct Ws {
     float   *part_o;     // [n_seq][Hkv][n_tiles][G][hd]
     float   *part_ml;    // [n_seq][Hkv][n_tiles][G][2]
     uint2   *cand;       // [n_seq][Hkv][cut_wg][kCutKeys] (key, block) candidates of the multi-workgroup selection
-    int32_t *ccnt;       // [n_seq][Hkv][kCutWgMax] their counts
+    int32_t *ccnt;       // [n_seq][Hkv][kCutWgMax] their counts; past kIdxRegKeys decode blocks also
+                         // [n_seq][n_chunks] the indexer workgroups' candidate counts (cand: 64 slots a chunk)
+    uint32_t *cutk;      // [n_seq][Hkv][kIdxCutParts] a long decode row's cut keys (the append launch's)
     float2  *cmm;        // [n_seq][Hkv][nb_cap / kScoreRecBlocks] (min, max) eligible score of each record's blocks
                          // (the attention's own selection reads them; (+inf, -inf) when empty)
     int32_t *lens;       // [kMaxChain][n_seq] lengths of a chained call's positions
@@ -70,7 +74,7 @@ struct Ws {
 };
 
 struct WsLayout {
-    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cmm, lens, vmax, pnorm, total;
+    size_t sel, nsel, scores, part_o, part_ml, cand, ccnt, cutk, cmm, lens, vmax, pnorm, total;
     int32_t nb_cap, max_sel, n_tiles, cut_wg;
 };
 // partials = false: no attention partials (the prefill kernel keeps its state on chip);
@@ -161,11 +165,27 @@ hipError_t launch_idx_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig
 // r's at position len[r] - 1, and kv (when enabled) brings the rows' K and V,
 // appended by the same launch.
 constexpr int kIdxFuseRows = 64;
+// The cut of a long decode row, placed by the fused decode step's append
+// launch for the attention's own selection (launch_dec_selbig): q_idx
+// [n_seq][n_head][dim] (fp32) scores kIdxCutSamples evenly spaced eligible
+// blocks of each sequence from the pool cache, kIdxCutParts workgroups a
+// sequence, and cutk[s][p] receives part p's threshold: the ceil(rs /
+// kIdxCutParts)-th largest key of its samples (0, every key a candidate, when
+// no cut applies).  Every key at or above the 4th smallest of them is a
+// candidate (about 1.6 topk keys; the attention checks that there are at
+// least topk and at most its list's capacity).  q_idx NULL: no cut.
+constexpr int kIdxCutParts = 8;
+constexpr int kIdxMaxCutHeads = 16;   // query heads * dim <= 16 * 128
+struct IdxCut {
+    const float *q_idx;
+    uint32_t *cutk;
+    int32_t n_head, max_seq_len;
+};
 hipError_t launch_idx_append_pool(const Geo &g, const qwfn_kv_view &v, const IdxGeo &ig, uint16_t *raw,
                                   uint16_t *pooled, const float *k_norm, const void *src, int32_t src_f16,
                                   const int32_t *seq_ids, const int32_t *pos, int32_t n_rows, hipStream_t st,
                                   const FusedAppend &kv = FusedAppend{nullptr, nullptr, 0, 0},
-                                  const int32_t *len = nullptr);
+                                  const int32_t *len = nullptr, const IdxCut &cut = IdxCut{nullptr, nullptr, 0, 0});
 // seq_ids NULL: every row in seq_const; pos NULL: row r at position pos0 + r;
 // len (decode): row r is sequence r's token at position len[r] - 1.
 hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, const void *vv,
@@ -177,11 +197,13 @@ hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, con
 hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
                        int32_t blk0, hipStream_t st, const int32_t *len = nullptr);
-// select = false: scores only (the attention selects, launch_attention_select)
+// select = false: scores only (the attention selects, launch_attention_select);
+// sel_launch = false: rows past the indexer workgroup's registers are scored
+// only (the attention selects from them, launch_dec_selbig)
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                          const FusedAppend &fa, hipStream_t st, bool select = true);
+                          const FusedAppend &fa, hipStream_t st, bool select = true, bool sel_launch = true);
 // Prefill: scores of n_q queries (Geo::pf) into ws.scores, then each query's
 // selection into sel / nsel.
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,
@@ -246,6 +268,23 @@ bool dec_select_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
 hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                                 int32_t n_seq, int32_t max_seq_len, const int32_t *sel, const int32_t *nsel,
                                 int32_t max_sel, float *out, const Ws &ws, bool select, hipStream_t st);
+// The checkpoint's decode attention selecting for itself from the indexer's
+// per-chunk candidates of each sequence's shared row (ws.cand / ws.ccnt: the
+// eligible keys at or above the append launch's sampled cut; ws.scores, rows
+// of ws.nb_cap, for the fallback), then the merge: every workgroup ranks the
+// candidates exactly (the radix passes over the row when they number fewer
+// than topk or more than its list holds) and writes the selection to sel /
+// nsel.  Fits: q8_0 blocks shorter than a tile at head_dim 256 and group 12,
+// a shared selection, rows up to 49,152 blocks, max_sel <= 1024.
+bool dec_selbig_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
+hipError_t launch_dec_selbig(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                             int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                             float *out, const Ws &ws, hipStream_t st);
+// That selection alone over given score rows (rows of nb_cap), one workgroup
+// a sequence: the test entry point's.
+hipError_t launch_test_select_big(const Geo &g, const float *scores, int32_t nb_cap, const int32_t *seq_len,
+                                  int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                                  hipStream_t st);
 hipError_t launch_attention(const Geo &g, const qwfn_kv_view &v, const float *q,
                             const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                             const int32_t *sel, const int32_t *nsel, int32_t max_sel,

@@ -382,6 +382,83 @@ def test_idx_select_long_context(lengths, mode):
     assert qsa.read_status(dev) == 0
 
 
+@pytest.mark.parametrize("mode", ["random", "cluster"])
+def test_checkpoint_fused_decode_long_context(mode):
+    """qwfn_idx_sparse_attn_decode past 8192 eligible blocks, where the
+    attention workgroups select from the indexer's score row themselves (no
+    selection launch): two sequences over two steps, the selections bit for
+    bit against the oracle's, the attention within the tolerance, and the
+    outputs and selections bit for bit equal to the four separate calls
+    (qwfn_idx_select's multi-workgroup selection, then the given-selection
+    attention).  cluster: 200 consecutive blocks aligned with the query heads'
+    sum, so the winners crowd into one run of the row."""
+    cfg = CKPT
+    rng = np.random.default_rng(880 + (mode == "cluster"))
+    L0 = [40003, 45001]
+    steps = 2
+    pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
+    pairs = [_pair(cfg, 2, pps, seed=881), _pair(cfg, 2, pps, seed=881)]
+    dev, host, ic, w = pairs[0]
+    dev2, _, ic2, _ = pairs[1]
+    qi_all = rng.standard_normal((steps, 2, 4, 128)).astype(np.float32)
+    for s in range(2):
+        k, v = kv_rows(rng, L0[s], cfg)
+        assert host.append(k, v, np.arange(L0[s], dtype=np.int32), np.full(L0[s], s, np.int32)) == 0
+        x = rng.standard_normal((L0[s], 128)).astype(np.float32)
+        if mode == "cluster":                      # blocks 2000 .. 2199 along the heads' sum of step 0
+            x[8000:8800, :64] *= 0.01
+            x[8000:8800, 64:] = 0.01 * x[8000:8800, 64:] + qi_all[0, s, :, 64:].sum(0)
+        for d, c in ((dev, ic), (dev2, ic2)):
+            qsa.append_q8_0(d, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            torch.arange(L0[s], dtype=torch.int32, device="cuda"),
+                            seq_ids=torch.full((L0[s],), s, dtype=torch.int32, device="cuda"))
+            qsa.idx_append_pool(c, torch.from_numpy(x).cuda(), torch.arange(L0[s], dtype=torch.int32, device="cuda"),
+                                seq_ids=torch.full((L0[s],), s, dtype=torch.int32, device="cuda"))
+    c = cfg_of(cfg)
+    Lmax = max(L0) + steps + 1
+    ws, ws2 = _ws(cfg, ic, 2, Lmax), _ws(cfg, ic2, 2, Lmax)
+    msel = c.max_selected(Lmax)
+    for step in range(steps):
+        lens = [L + step + 1 for L in L0]
+        print(f"  fused idx decode, long context ({mode}), step {step}, lengths {lens}", flush=True)
+        kn, vn = kv_rows(rng, 2, cfg)
+        xr = rng.standard_normal((2, 128)).astype(np.float32)
+        q = rng.standard_normal((2, 24, 256)).astype(np.float32)
+        qi = qi_all[step]
+        L = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        sel = torch.full((2, 2, msel), -7, dtype=torch.int32, device="cuda")
+        nsel = torch.empty((2, 2), dtype=torch.int32, device="cuda")
+        qd, qid = torch.from_numpy(q).cuda(), torch.from_numpy(qi).cuda()
+        knd, vnd, xrd = (torch.from_numpy(a).cuda() for a in (kn, vn, xr))
+        out = qsa.idx_sparse_attn_decode(ic, qd, qid, knd, vnd, xrd, L, Lmax, ws, sel=sel, n_sel=nsel)
+        pos = L - 1
+        qsa.append_q8_0(dev2, knd, vnd, pos, seq_ids=torch.arange(2, dtype=torch.int32, device="cuda"))
+        qsa.idx_append_pool(ic2, xrd, pos, seq_ids=torch.arange(2, dtype=torch.int32, device="cuda"))
+        sel2 = torch.full_like(sel, -7)
+        nsel2 = torch.empty_like(nsel)
+        qsa.idx_select(ic2, qid, L, Lmax, ws2, sel=sel2, n_sel=nsel2)
+        out2 = qsa.sparse_decode_attn(dev2, qd, L, Lmax, ws2, sel=sel2, n_sel=nsel2)
+        torch.cuda.synchronize()
+        assert host.append(kn, vn, np.array([l - 1 for l in lens], np.int32), np.arange(2, dtype=np.int32)) == 0
+        hs = np.full((2, 2, msel), -1, np.int32)
+        gs, gn = np_of(sel), np_of(nsel)
+        pooled = np_of(ic.pooled)
+        for s in range(2):
+            want = oracle_select(cfg, ICFG, pooled[s], qi[s], lens[s], msel)
+            assert len(want) == 513
+            if mode == "cluster" and step == 0:
+                assert set(range(2000, 2200)) <= set(want.tolist())
+            for g in range(2):
+                assert gn[s, g] == len(want)
+                np.testing.assert_array_equal(gs[s, g, :gn[s, g]], want, err_msg=f"step {step} seq {s} head {g}")
+                hs[s, g, :len(want)] = want
+        ref = host.attention_f64(q, lens, hs, gn)
+        assert_close_attn(np_of(out), ref, f"step {step}")
+        assert torch.equal(sel, sel2) and torch.equal(nsel, nsel2), f"step {step}: selections differ"
+        assert torch.equal(out, out2), f"step {step}: outputs differ from the four calls'"
+    assert qsa.read_status(dev) == 0
+
+
 def test_per_head_selection_long_context():
     """A per-KV-head selection (no shared selection) over 10,000 4-token blocks:
     k_select_big with one workgroup per (sequence, KV head)."""
