@@ -295,20 +295,20 @@ k_idx_append_pool(Geo g, qwfn_kv_view v, IdxGeo ig, uint16_t *__restrict__ raw, 
 // Part p of sequence s's cut for the attention's own selection (one of the
 // kIdxCutParts workgroups a sequence of the fused decode step's append
 // launch): the eligible blocks e_lo + j * n_eligible / kIdxCutSamples, j = p
-// kIdxCutPer .. + kIdxCutPer - 1, are scored from the pool cache (8 lanes a
-// block, dims 32 i + 4 lane .. + 3 a lane, the query heads' dots relu'd when
+// kIdxCutPer .. + kIdxCutPer - 1, are scored from the pool cache (16 lanes a
+// block, dims 64 i + 4 lane .. + 3 a lane, the query heads' dots relu'd when
 // set and summed); wave 0 then finds the ceil(rs / kIdxCutParts)-th largest
 // of their keys by a bitwise search (the largest key T with that many sample
 // keys at or above it: one compare and ballot count a bit) into cutk[s][p].
-// The indexer takes every eligible key at or above the parts' 4th smallest
-// threshold as a candidate, and the attention ranks them exactly when they
+// The indexer takes every eligible key at or above the mean of the parts'
+// threshold keys as a candidate, and the attention ranks them exactly when they
 // number at least topk (the selection is exact for any threshold; this one
 // makes that the usual case), so the samples need not match the indexer's
 // scores bit for bit.  The block this launch re-pools (the row's last) is
 // never a sample.
 constexpr int kIdxCutPer = kIdxCutSamples / kIdxCutParts;     // samples a workgroup
 constexpr int kIdxCutLanes = kIdxFuseThreads / kIdxCutPer;    // lanes a sample
-static_assert(kIdxCutLanes == 8 && kIdxCutPer == 2 * 64, "8 lanes a sample; 2 keys a lane of wave 0");
+static_assert(kIdxCutLanes == 16 && kIdxCutPer == 64, "16 lanes a sample; a key a lane of wave 0");
 struct IdxCutShared {
     float q[kIdxMaxCutHeads * 128];
     uint32_t key[kIdxCutPer];
@@ -352,18 +352,18 @@ __device__ __forceinline__ void idx_sample_cut(const Geo &g, const uint16_t *poo
             acc += __shfl_xor(acc, 1);
             acc += __shfl_xor(acc, 2);
             acc += __shfl_xor(acc, 4);
+            acc += __shfl_xor(acc, 8);
             score += g.relu && !(acc > 0.0f) ? 0.0f : acc;
         }
         if (jl == 0) sh.key[tid / NL] = score_key(score);
         __syncthreads();
-        if (tid < 64) {                            // wave 0: two sample keys a lane
-            const uint2 k2 = reinterpret_cast<const uint2 *>(sh.key)[tid];
+        if (tid < 64) {                            // wave 0: a sample key a lane
+            const uint32_t k1 = sh.key[tid];
             const int need = (rs + kIdxCutParts - 1) / kIdxCutParts;
 #pragma unroll 1
             for (int bit = 31; bit >= 0; --bit) {
                 const uint32_t t = tk | (1u << bit);
-                const int n = __builtin_popcountll(__ballot(k2.x >= t)) + __builtin_popcountll(__ballot(k2.y >= t));
-                tk = n >= need ? t : tk;
+                tk = __builtin_popcountll(__ballot(k1 >= t)) >= need ? t : tk;
             }
         }
     }

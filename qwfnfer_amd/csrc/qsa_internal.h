@@ -171,10 +171,12 @@ constexpr int kIdxFuseRows = 64;
 // blocks of each sequence from the pool cache, kIdxCutParts workgroups a
 // sequence, and cutk[s][p] receives part p's threshold: the ceil(rs /
 // kIdxCutParts)-th largest key of its samples (0, every key a candidate, when
-// no cut applies).  Every key at or above the 4th smallest of them is a
-// candidate (about 1.6 topk keys; the attention checks that there are at
-// least topk and at most its list's capacity).  q_idx NULL: no cut.
-constexpr int kIdxCutParts = 8;
+// no cut applies).  Every key at or above their mean is a candidate (keys
+// are monotone in the score, so the mean lies between the parts' estimates;
+// about 3.5 topk keys at the checkpoint's shape, and the attention checks
+// that there are at least topk and at most its list's capacity).  q_idx
+// NULL: no cut.
+constexpr int kIdxCutParts = 16;
 constexpr int kIdxMaxCutHeads = 16;   // query heads * dim <= 16 * 128
 struct IdxCut {
     const float *q_idx;

@@ -317,20 +317,15 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     const bool emit = select_here == 2;
     const int pair = s * g.Hkv + gh;
     uint32_t tk = 0u;
-    if (emit) {                                    // the append launch's part thresholds: their 4th smallest
-        static_assert(kIdxCutParts == 8, "two 16-byte loads");
-        const u4v t0 = reinterpret_cast<const u4v *>(ws.cutk)[2 * pair];
-        const u4v t1 = reinterpret_cast<const u4v *>(ws.cutk)[2 * pair + 1];
-        uint32_t t[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+    if (emit) {                                    // the append launch's part thresholds: their mean key
+        static_assert(kIdxCutParts == 16, "four 16-byte loads");
+        uint64_t sum = 0;
 #pragma unroll
-        for (int i = 0; i < 7; ++i)
-#pragma unroll
-            for (int j = 0; j < 7 - i; ++j) {
-                const uint32_t a = min(t[j], t[j + 1]), b = max(t[j], t[j + 1]);
-                t[j] = a;
-                t[j + 1] = b;
-            }
-        tk = t[3];
+        for (int k = 0; k < kIdxCutParts / 4; ++k) {
+            const u4v x = reinterpret_cast<const u4v *>(ws.cutk)[kIdxCutParts / 4 * pair + k];
+            sum += (uint64_t)x[0] + x[1] + x[2] + x[3];
+        }
+        tk = (uint32_t)(sum / kIdxCutParts);
     }
     // the group's query rows do not depend on the length either
     constexpr int QV = (G * HD / 4 + kIdxThreads - 1) / kIdxThreads;
