@@ -462,9 +462,11 @@ class CheckpointRunner:
     256, q8_0 KV, blocks of 4 tokens pooled by its own indexer of 4 heads x 128,
     513 kept blocks) stepped one decode token at a time through
     qwfn_idx_sparse_attn_decode: per layer one launch for the K/V rows, the raw
-    indexer key and its block's pooled key, then the indexer's scores (and,
-    past 8,192 candidate blocks, the multi-workgroup selection), the attention
-    and its merge -- four launches at 4,096 tokens, five at 163,840."""
+    indexer key and its block's pooled key (past 8,192 candidate blocks it also
+    scores a sample of the row and places a cut), then the indexer (its last
+    workgroup selects; past 8,192 blocks its workgroups keep the keys above the
+    cut as candidates), the attention (ranking those candidates itself) and its
+    merge -- four launches at either length."""
 
     def __init__(self, qsa, torch, ctx, n_layer, gen):
         self.qsa, self.torch = qsa, torch
@@ -830,8 +832,8 @@ def main():
             torch.cuda.empty_cache()
         checkpoint = dict(per_context=ck, workload="the released checkpoint's attention layer: 24q/2kv heads "
                           "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
-                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (4 launches at "
-                          "4,096 tokens, 5 at 163,840), hipGraph")
+                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (4 launches: "
+                          "append (+ the sampled cut past 8,192 blocks), indexer, attention, merge), hipGraph")
         if not args.no_prefill:
             checkpoint["prefill"] = bench_checkpoint_prefill(qsa, torch, gen)
             log(f"[bench] checkpoint prefill chunk ({PREFILL_N} queries at {PREFILL_POS0}): "
