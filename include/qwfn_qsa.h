@@ -470,8 +470,11 @@ typedef struct qwfn_idx_view {
 int qwfn_idx_cache_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *ishape,
                          int32_t n_seq, int32_t pages_per_seq,
                          size_t *raw_page_bytes, size_t *pooled_bytes);
-/* Workspace of qwfn_idx_select (counters shared with qwfn_qsa_workspace_*:
- * one workspace initialised once serves both when it is the larger size). */
+/* Workspace of qwfn_idx_select and qwfn_idx_sparse_attn_decode (counters
+ * shared with qwfn_qsa_workspace_*: one workspace initialised once serves both
+ * when it is the larger size).  It holds the indexer's layout and, after it,
+ * the attention's, so that the decode call can leave rows of more than 8,192
+ * candidate blocks to the attention's own selection. */
 int qwfn_idx_workspace_bytes(const qwfn_qsa_shape *shape, const qwfn_idx_shape *ishape,
                              int32_t n_seq, int32_t max_seq_len, size_t *bytes);
 /* Write n_rows raw keys k_raw [n_rows][idx_dim] (F32 rounded to fp16, or F16)
@@ -515,10 +518,18 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
  * (:497-542).  src_dtype covers k_new, v_new and k_raw.  sel [n_seq]
  * [n_head_kv][max_sel] and n_sel [n_seq][n_head_kv] (required: the selection
  * passes through them) receive the selection as qwfn_idx_select writes it.
- * Workspace: the larger of qwfn_qsa_workspace_bytes and qwfn_idx_workspace_
- * bytes.  Replaces the four calls qwfn_kv_append_q8_0, qwfn_idx_append_pool,
- * qwfn_idx_select and qwfn_sparse_decode_attn of a decode step with one
- * launch fewer. */
+ * Workspace: qwfn_idx_workspace_bytes.  Past 8,192 candidate blocks (the
+ * 4-token blocks past 32,768 tokens) the append launch also scores 1,024
+ * sampled blocks of each row and places a cut, the indexer keeps each chunk's
+ * scores above it, and the attention workgroups rank those candidates
+ * exactly (a fallback over the whole row where the cut leaves too few or too
+ * many), so no selection launch runs.  That covers the checkpoint's heads
+ * (24 x 256, 4 indexer heads of at most 128) up to 49,152 blocks; longer
+ * rows, other shapes and a workspace smaller than qwfn_idx_workspace_bytes
+ * (at least what qwfn_qsa_workspace_bytes and qwfn_idx_select each need)
+ * keep the selection launch.  Replaces the four calls qwfn_kv_append_q8_0,
+ * qwfn_idx_append_pool, qwfn_idx_select and qwfn_sparse_decode_attn of a
+ * decode step with one launch fewer (two past 8,192 blocks). */
 int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                                 const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
                                 const float *q, const float *q_idx, const void *k_new,
