@@ -4,11 +4,17 @@ qwfn_qsa_test_select_rows on score rows planted on the host, against the
 oracle's selection (qwfn_oracle_select) on the same rows: counts and blocks
 bit-exact, ties to the lower block.
 
-The selection takes a cut from 4096 evenly spaced scores (block e_lo + j *
-n_eligible // 4096), keeps every eligible score at or above it as a candidate
-and ranks the candidates exactly; too few or too many candidates, or an
-overfull threshold bin, fall back to three radix passes over the row.
-Scores planted at the sampled blocks steer each branch."""
+The hook restates on the row what the product takes from the append and
+indexer launches: a cut from 1,024 evenly spaced scores (block e_lo + j *
+n_eligible // 1024; the hook keeps the smallest key of the sample's top rank,
+the product the mean of 16 part keys), every eligible score at or above it as
+a candidate in block order.  The attention's selection ranks the candidates
+exactly; too few or too many candidates, or an overfull threshold bin, fall
+back to three radix passes over the row.  Any cut leaves the result exact, so
+the test pins the ranking and the fallbacks; scores planted at 4,096 evenly
+spaced blocks (a superset of the 1,024 samples) steer each branch.  The
+product's own cut is covered end to end by tests/test_gpu_checkpoint.py's
+long-context fused decode."""
 import ctypes as C
 
 import numpy as np
@@ -74,7 +80,7 @@ def _eligible(cfg, L):
     return e_lo, max(e_lo, min(L // cfg.block_tokens, fw))
 
 
-def _samples(e):
+def _samples(e):                                      # 4,096 positions: the 1,024 samples among them
     e_lo, e_hi = e
     ne = e_hi - e_lo
     return e_lo + np.arange(4096) * ne // 4096
