@@ -84,8 +84,8 @@ struct DecSelBig {
     uint32_t hist[4096 + 64];                    // + one trash bin per lane
     u2v cand[kSelCandMax + 64];                  // candidates (key, block), in block order (+ one trash slot per lane)
     uint8_t cok[kSelCandMax];                    // the threshold bin's verdicts, by candidate
-    uint32_t wbits[kSelCandMax / 32];            // the winners, bit c % 32 of word c / 32
-    int32_t wpre[kSelCandMax / 32];              // winners in the words before
+    int32_t rwin[kSelCandMax / kDecThreads * kDecWaves];   // winners of each (round, wave)
+    u4v xch[kDecWaves];                          // each wave's (count, key min, key max, overflow)
     uint32_t cand_key[kCandMax + 64];            // the threshold bin's keys, blocks
     int32_t cand_b[kCandMax + 64];
     float red[2 * kDecWaves];
@@ -478,24 +478,31 @@ __device__ __forceinline__ void dec_big_zero(DecSelBig &bs) {
 // threshold bin; the keys above it are taken, and the bin's own keys too
 // when it holds just the keys still needed, else they are ranked by (key
 // desc, candidate asc -- block asc).  Thread t reads candidates u NT + t
-// (consecutive lanes, consecutive LDS words); each round's winners become two
-// words of a bit map by one ballot, and thread t < kSelCandMax / 32 emits the
-// winners of word t, so they go out in candidate (block) order after the
-// sink blocks.  Returns false, with nothing emitted, when the threshold bin
-// holds more than kCandMax keys.
+// (consecutive lanes, consecutive LDS words) and keeps their bins, blocks and
+// verdicts in registers; each round's winners are one ballot a wave.
+// Candidate order is (round, wave, lane), so a winner's place is
+// the winners of the (round, wave) pairs before its own (one exchange of the
+// pairs' counts and a wave scan) plus those below its lane: the winners go
+// out in block order after the sink blocks with no further LDS reads.
+// Returns false, with nothing emitted, when the threshold bin holds more than
+// kCandMax keys.
 __device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uint32_t kmin, uint32_t kmax,
                                               const SelOut &out, DecSelBig &bs) {
     constexpr int NT = kDecThreads, CPT = kSelCandMax / NT;
-    static_assert(CPT * NT == kSelCandMax && kSelCandMax / 32 <= NT, "whole candidate rounds; a bit-map word a thread");
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    static_assert(CPT * NT == kSelCandMax && CPT * kDecWaves == 64, "whole candidate rounds; a (round, wave) a lane");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float sc2 = 4096.0f / ((float)(kmax - kmin) + 1.0f);
     // every round's reads are independent and go out together (a round past
     // the candidates reads slot 0 and changes nothing)
     uint32_t kb[CPT];
+    int32_t bid[CPT];
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
         const int c = u * NT + tid;
-        kb[u] = (uint32_t)fminf((float)(bs.cand[c < C ? c : 0][0] - kmin) * sc2, 4095.0f);
+        const u2v x = bs.cand[c < C ? c : 0];
+        kb[u] = (uint32_t)fminf((float)(x[0] - kmin) * sc2, 4095.0f);
+        bid[u] = (int32_t)x[1];
         atomicAdd(&bs.hist[c < C ? kb[u] : 4096u + (uint32_t)lane], 1u);
     }
     __syncthreads();
@@ -503,6 +510,7 @@ __device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uin
     __syncthreads();
     const uint32_t B = (uint32_t)bs.bin;
     const int need = bs.need, cB = bs.cnt_b;
+    uint32_t wm = 0u;                              // bit u: candidate u NT + t is in
     if (cB > need) {                               // (uniform) rank the threshold bin
         if (cB > kCandMax) return false;
 #pragma unroll
@@ -526,32 +534,35 @@ __device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uin
             bs.cok[c] = rk < need;
         }
         __syncthreads();
-    }
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-        const int c = u * NT + tid;
-        const bool win = c < C && (kb[u] > B || (kb[u] == B && (cB <= need || bs.cok[c])));
-        const uint64_t m = __ballot(win);
-        if (lane == 0) {                           // candidates u NT + 64 wid .. + 63
-            bs.wbits[(u * NT + 64 * wid) / 32] = (uint32_t)m;
-            bs.wbits[(u * NT + 64 * wid) / 32 + 1] = (uint32_t)(m >> 32);
+        for (int u = 0; u < CPT; ++u) {
+            const int c = u * NT + tid;
+            wm |= (uint32_t)(c < C && (kb[u] > B || (kb[u] == B && bs.cok[c]))) << u;
         }
+    } else {                                       // every key of the threshold bin is in
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) wm |= (uint32_t)(u * NT + tid < C && kb[u] >= B) << u;
     }
-    __syncthreads();
-    // emission: a winner's place is the winners in the words before its own
-    // plus those below it in its word; thread t emits candidates u NT + t
-    const uint32_t wv = tid < kSelCandMax / 32 ? bs.wbits[tid] : 0u;
-    int tot;
-    const int pre = block_excl_sum<NT>(__builtin_popcount(wv), bs.tmp, &tot);
-    if (tid < kSelCandMax / 32) bs.wpre[tid] = pre;
-    __syncthreads();
+    // the ballots are recomputed where they are used (one compare each) rather
+    // than kept: sixteen 64-bit masks would spill scalar registers
+    int cnt = 0;                                   // lane u: round u's winners in this wave
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-        const int c = u * NT + tid;
-        const uint32_t wd = bs.wbits[c >> 5];
-        const int pos = bs.wpre[c >> 5] + __builtin_popcount(wd & ((1u << (c & 31)) - 1u));
-        const int32_t b = (int32_t)bs.cand[c][1];
-        if (((wd >> (c & 31)) & 1u) && pos < topk) out.put(g.sink + pos, b);
+        const int n = (int)__builtin_popcountll(__ballot((wm >> u) & 1u));
+        cnt = lane == u ? n : cnt;
+    }
+    if (lane < CPT) bs.rwin[lane * kDecWaves + wid] = cnt;
+    __syncthreads();
+    const int x = bs.rwin[lane];                   // pair (lane / kDecWaves, lane % kDecWaves)
+    const int ex = wave_incl_scan(x) - x;
+    asm volatile("" : "+v"(wm));                   // no reuse of the counting loop's masks across the barrier
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const uint64_t mu = __ballot((wm >> u) & 1u);
+        const int pos = __builtin_amdgcn_readlane(ex, u * kDecWaves + wid) +
+                        (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mu >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)mu, 0u));
+        if (((wm >> u) & 1u) && pos < topk) out.put(g.sink + pos, bid[u]);
     }
     return true;
 }
@@ -598,41 +609,71 @@ __device__ __forceinline__ int dec_choose_big(const Geo &g, const Ws &ws, int s,
     } else if (topk == 0) {                        // the forced blocks fill the count
         emit_forced<NT>(g, r, 0, out);
     } else {
-        int my = 0;
-#pragma unroll
-        for (int i = 0; i < kDecBigCpt; ++i) my += cc[i];
-        int C;
-        int off = block_excl_sum<NT>(my, bs.tmp, &C);
+        // one exchange gives every thread its offset, the count C, the range
+        // of the preloaded keys and whether any chunk holds more than the
+        // preloaded slots (then those keys widen the range: a second one)
+        int my = 0, more = 0;
         uint32_t kmn = 0xffffffffu, kmx = 0u;
+#pragma unroll
+        for (int i = 0; i < kDecBigCpt; ++i) {
+            const int n = cc[i];
+            my += n;
+            more |= n > kDecBigPre;
+#pragma unroll
+            for (int j = 0; j < kDecBigPre; ++j) {
+                kmn = j < n ? min(kmn, ce[i][j][0]) : kmn;
+                kmx = j < n ? max(kmx, ce[i][j][0]) : kmx;
+            }
+        }
+        const int incl = wave_incl_scan(my);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            kmn = min(kmn, (uint32_t)__shfl_xor((int)kmn, o));
+            kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o));
+        }
+        more = __ballot(more != 0) != 0ull;
+        const int w = tid >> 6;
+        if (lane == 63) bs.xch[w] = u4v{(uint32_t)incl, kmn, kmx, (uint32_t)more};
+        __syncthreads();
+        int off = incl - my, C = 0;
+#pragma unroll
+        for (int v = 0; v < kDecWaves; ++v) {
+            const u4v e = bs.xch[v];
+            off += v < w ? (int)e[0] : 0;
+            C += (int)e[0];
+            kmn = min(kmn, e[1]);
+            kmx = max(kmx, e[2]);
+            more |= (int)e[3];
+        }
         if (C >= topk && C <= kSelCandMax) {       // (uniform)
             const uint2 *cand = ws.cand + (int64_t)s * n_chunks * kIdxChunkBlocks;
+            uint32_t xmn = 0xffffffffu, xmx = 0u;  // keys past the preloaded slots
 #pragma unroll
             for (int i = 0; i < kDecBigCpt; ++i) {
                 const int n = cc[i];
 #pragma unroll
-                for (int j = 0; j < kDecBigPre; ++j) {
-                    bs.cand[j < n ? off + j : kSelCandMax + lane] = ce[i][j];
-                    kmn = j < n ? min(kmn, ce[i][j][0]) : kmn;
-                    kmx = j < n ? max(kmx, ce[i][j][0]) : kmx;
-                }
+                for (int j = 0; j < kDecBigPre; ++j) bs.cand[j < n ? off + j : kSelCandMax + lane] = ce[i][j];
                 const uint2 *src = cand + (int64_t)(kDecBigCpt * tid + i) * kIdxChunkBlocks;
                 for (int j = kDecBigPre; j < n; ++j) {
                     const uint2 x = src[j];
                     bs.cand[off + j] = u2v{x.x, x.y};
-                    kmn = min(kmn, x.x);
-                    kmx = max(kmx, x.x);
+                    xmn = min(xmn, x.x);
+                    xmx = max(xmx, x.x);
                 }
                 off += n;
             }
+            if (more) {                            // (uniform) rare: widen the range by those keys
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) {
-                kmn = min(kmn, (uint32_t)__shfl_xor((int)kmn, o));
-                kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, o));
+                for (int o = 32; o >= 1; o >>= 1) {
+                    xmn = min(xmn, (uint32_t)__shfl_xor((int)xmn, o));
+                    xmx = max(xmx, (uint32_t)__shfl_xor((int)xmx, o));
+                }
+                if (lane == 0) { bs.kred[w] = xmn; bs.kred[kDecWaves + w] = xmx; }
+                __syncthreads();
+#pragma unroll
+                for (int v = 0; v < kDecWaves; ++v) { kmn = min(kmn, bs.kred[v]); kmx = max(kmx, bs.kred[kDecWaves + v]); }
             }
-            if (lane == 0) { bs.kred[tid >> 6] = kmn; bs.kred[kDecWaves + (tid >> 6)] = kmx; }
-            __syncthreads();
-#pragma unroll
-            for (int w = 0; w < kDecWaves; ++w) { kmn = min(kmn, bs.kred[w]); kmx = max(kmx, bs.kred[kDecWaves + w]); }
+            __syncthreads();                       // the placed candidates, before dec_big_exact reads them
         }
         dec_big_tail(g, r, C, topk, kmn, kmx, ws.scores + (int64_t)s * ws.nb_cap, out, bs);
     }
