@@ -981,9 +981,14 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     // workspace (qwfn_idx_workspace_bytes sizes both), so its partials never
     // touch the candidates; a workspace sized for one layout keeps the
     // selection launch.
+    const bool split_ws = ws_bytes >= align256(li.total) + la.total;
     const bool fused_sel = max_seq_len / g.bt > kIdxRegKeys && dec_selbig_fits(g, max_seq_len, max_sel) &&
                            ishape->idx_dim <= 128 && ishape->n_idx_head * ishape->idx_dim <= kIdxMaxCutHeads * 128 &&
-                           ws_bytes >= align256(li.total) + la.total;
+                           split_ws;
+    // Rows the indexer workgroup's registers hold: the indexer only scores and
+    // every attention workgroup selects from the row (no last-workgroup
+    // selection in the indexer); the same split workspace.
+    const bool row_sel = max_seq_len / g.bt <= kIdxRegKeys && dec_selrow_fits(g, max_seq_len, max_sel) && split_ws;
     const Ws wi = ws_bind(ws, li);
     const IdxCut cut{fused_sel ? q_idx : nullptr, wi.cutk, ishape->n_idx_head, max_seq_len};
     // the K/V rows, the raw indexer key and its block's pooled key: one launch
@@ -994,14 +999,16 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     qwfn_kv_view vi = *view;
     vi.pooled = (float *)iview->pooled;                   // fp16 keys (Geo::pooled_f16)
     e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, wi,
-                       FusedAppend{nullptr, nullptr, 0, 0}, st, true, !fused_sel);
+                       FusedAppend{nullptr, nullptr, 0, 0}, st, true, !(fused_sel || row_sel));
     if (e != hipSuccess) return hip_fail(e, "idx decode: indexer");
-    if (fused_sel) {
+    if (fused_sel || row_sel) {
         Ws wa = ws_bind((uint8_t *)ws + align256(li.total), la);
         wa.scores = wi.scores;
+        wa.nb_cap = wi.nb_cap;
         wa.cand = wi.cand;
         wa.ccnt = wi.ccnt;
-        e = launch_dec_selbig(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, wa, st);
+        e = fused_sel ? launch_dec_selbig(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, wa, st)
+                      : launch_dec_selrow(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, wa, st);
     } else {
         e = launch_attention(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, ws_bind(ws, la), st);
     }

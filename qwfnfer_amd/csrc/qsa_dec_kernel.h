@@ -57,7 +57,7 @@ constexpr int kDecCand = 256;                   // threshold-bin keys ranked pai
 constexpr int kDecPtLds = 4096;                 // page-table entries parked in LDS at most
 constexpr int kDecSelMax = 1024;                // selected blocks kept in LDS
 
-enum DecMode { kGiven = 0, kDense = 1, kSelect = 2, kSelBig = 3 };
+enum DecMode { kGiven = 0, kDense = 1, kSelect = 2, kSelBig = 3, kSelRow = 4 };
 
 // kSelBig: a long row of at most kDecBigRnd * kDecThreads * 4 = 49,152 blocks
 // (longer rows take the selection launch), kDecBigChunks indexer chunks.
@@ -99,6 +99,7 @@ struct DecShared {
     float wml[kDecWaves][G][2];                  // the waves' (max, sum)
     int32_t wcnt[kDecWaves];
     int32_t ccnt[kDecWaves];
+    float2 wlh[kDecWaves];                       // kSelRow: each wave's (smallest, largest) eligible score
     int32_t nsel;
     int32_t sel[kDecSelMax + 64];                // + one trash slot per lane
 };
@@ -134,7 +135,9 @@ template <int HD, int G, int MODE, int TM, int LY = kLyQ8>
 constexpr int dec_union_bytes() {
     constexpr int st = TM * kDecWaves * DecStage<HD, LY>::BYTES;
     constexpr int wo = kDecWaves * G * HD * 4;
-    constexpr int se = MODE == kSelect ? (int)sizeof(DecSel) : MODE == kSelBig ? (int)sizeof(DecSelBig) : 0;
+    constexpr int se = MODE == kSelect || MODE == kSelRow ? (int)sizeof(DecSel)
+                       : MODE == kSelBig                   ? (int)sizeof(DecSelBig)
+                                                           : 0;
     constexpr int m = st > wo ? st : wo;
     return ((m > se ? m : se) + 15) / 16 * 16;
 }
@@ -462,6 +465,78 @@ __device__ __forceinline__ int dec_choose(const Geo &g, const Ws &ws, int L, int
     return min(sh.nsel, max_sel);
 }
 
+// kSelRow: thread t's KPT scores of sequence s's shared row (the checkpoint
+// indexer's, one row for every KV head), blocks base + [t*KPT, t*KPT + KPT),
+// base = sink rounded down to 4.
+template <int KPT>
+__device__ __forceinline__ void dec_load_row(const Geo &g, const Ws &ws, int s, float (&sv)[KPT]) {
+    const int tid = threadIdx.x;
+    const int base = g.sink & ~3;
+    const BufRsrc rs = buf_rsrc(ws.scores + (int64_t)s * ws.nb_cap, (uint32_t)ws.nb_cap * 4u);
+#pragma unroll
+    for (int k = 0; k < KPT / 4; ++k) {
+        const auto x = BufLoad<4>::at(rs, (base + tid * KPT) * 4 + 16 * k, 0);
+        sv[4 * k] = x[0]; sv[4 * k + 1] = x[1]; sv[4 * k + 2] = x[2]; sv[4 * k + 3] = x[3];
+    }
+}
+
+// kSelRow: each wave's smallest and largest eligible score (NaN ignored) into
+// sh.wlh, before the caller's barrier; the row has no scoring-launch records.
+template <int KPT, int G>
+__device__ __forceinline__ void dec_row_bounds(const Geo &g, int L, int max_seq_len, const float (&sv)[KPT],
+                                               DecShared<G> &sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    float lo = INFINITY, hi = -INFINITY;
+    if (L >= 1 && L <= max_seq_len) {
+        const Ranges r = qsa_ranges(g, L);
+        const int b0 = (r.e_lo & ~3) + tid * KPT;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const bool in = (uint32_t)(b0 + i - r.e_lo) < (uint32_t)(r.e_hi - r.e_lo);
+            lo = in ? fminf(lo, sv[i]) : lo;
+            hi = in ? fmaxf(hi, sv[i]) : hi;
+        }
+    }
+    hi = wave_max(hi);
+    lo = -wave_max(-lo);
+    if (lane == 0) sh.wlh[tid >> 6] = make_float2(lo, hi);
+}
+
+// kSelRow: the selection of sequence s's shared row into sh.sel / sh.nsel (all
+// threads; the histogram zeroed, the waves' bounds written and a barrier
+// passed since).  Returns min(count, max_sel), 0 for a length out of range.
+template <int KPT, int G>
+__device__ __forceinline__ int dec_choose_row(const Geo &g, int L, int max_seq_len, int max_sel,
+                                              const float (&sv)[KPT], DecSel &ss, DecShared<G> &sh) {
+    const int tid = threadIdx.x;
+    if (!(L >= 1 && L <= max_seq_len)) return 0;
+    const Ranges r = qsa_ranges(g, L);
+    const int ne = r.e_hi - r.e_lo, topk = eff_topk(g, r);
+    if (g.topk <= 0 || ne <= topk) {               // every block below the length
+        const int nb = r.b_last + 1;
+        for (int i = tid; i < nb && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+        if (tid == 0) sh.nsel = nb;
+        __syncthreads();
+    } else if (topk == 0) {                        // the forced blocks fill the count
+        const int nwin = r.b_last - r.fw + 1;
+        for (int i = tid; i < g.sink && i < kDecSelMax; i += kDecThreads) sh.sel[i] = i;
+        for (int i = tid; i < nwin; i += kDecThreads)
+            if (g.sink + i < kDecSelMax) sh.sel[g.sink + i] = r.fw + i;
+        if (tid == 0) sh.nsel = g.sink + nwin;
+        __syncthreads();
+    } else {
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) {
+            const float2 x = sh.wlh[w];
+            lo = fminf(lo, x.x);
+            hi = fmaxf(hi, x.y);
+        }
+        dec_select<KPT>(g, sv, r, topk, lo, hi, ss, sh);
+    }
+    return min(sh.nsel, max_sel);
+}
+
 // kSelBig: the histogram and the threshold bin's count start at zero (before
 // the caller's first barrier).
 __device__ __forceinline__ void dec_big_zero(DecSelBig &bs) {
@@ -706,7 +781,8 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
     static_assert(G <= 16, "one matrix-core column per query head");
     static_assert(TM >= 1 && TM <= 4, "tiles a part");
     static_assert(!RF || LY == kLyQ8, "fp16-rounded K/V: q8_0 with V dim-major");
-    static_assert(LY != kLyQ8K || MODE != kSelect, "gathered q8_0 tiles: a given selection, dense or kSelBig");
+    static_assert(LY != kLyQ8K || MODE != kSelect, "gathered q8_0 tiles: a given selection, dense, kSelBig or kSelRow");
+    static_assert(MODE != kSelRow || LY == kLyQ8K, "kSelRow: the checkpoint layer's shared row");
     using S = DecStage<HD, LY>;
     constexpr int NB = S::NB, ND = S::ND, NS = S::NS;
     constexpr int UB = dec_union_bytes<HD, G, MODE, TM, LY>();
@@ -752,10 +828,11 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
                 pt4[k] = __builtin_bit_cast(u4v, BufLoad<4>::at(prs, (4 * tid + 4 * kDecThreads * k) * 4, 0));
     }
     // kSelect: the scores and the scoring launch's (min, max) records
-    constexpr int KS = MODE == kSelect ? KPT : 4;
+    constexpr int KS = MODE == kSelect || MODE == kSelRow ? KPT : 4;
     float sv[KS];
     float2 rec[dec_rpl<KS>()];
     if constexpr (MODE == kSelect) dec_load_sel_inputs<KS>(g, ws, pair, sv, rec);
+    if constexpr (MODE == kSelRow) dec_load_row<KS>(g, ws, s, sv);   // the sequence's shared row
     // kSelBig: the candidate counts of this thread's chunks of the sequence's row
     const int n_chunks = (max_seq_len / g.bt + kIdxChunkBlocks - 1) / kIdxChunkBlocks;
     int cc[kDecBigCpt];
@@ -796,7 +873,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         }
     }
     if constexpr (MODE == kGiven) n_given = nsel[pair];
-    if constexpr (MODE == kSelect) dec_zero_hist(ss);   // the selection histogram starts at zero
+    if constexpr (MODE == kSelect || MODE == kSelRow) dec_zero_hist(ss);   // the selection histogram starts at zero
     if constexpr (MODE == kSelBig) dec_big_zero(*reinterpret_cast<DecSelBig *>(dec_dyn));
     // the query split: scaled by a power of two so its largest magnitude is in
     // [2^13, 2^14), then fp16 high + low parts (residual below 2^-22 of the
@@ -841,6 +918,16 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
             if (tid == 0) nsel[pair] = n;
         }
+    } else if constexpr (MODE == kSelRow) {
+        // one shared row a sequence (ws.scores: the indexer's); its bounds from
+        // the keys themselves, each wave's exchanged at the barrier
+        dec_row_bounds<KS>(g, L, max_seq_len, sv, sh);
+        __syncthreads();                           // the parked page table, the zeroed histogram, the bounds
+        n = dec_choose_row<KS>(g, L, max_seq_len, max_sel, sv, ss, sh);
+        if (part == 0) {
+            for (int i = tid; i < n; i += kDecThreads) sel[(int64_t)pair * max_sel + i] = sh.sel[i];
+            if (tid == 0) nsel[pair] = n;
+        }
     } else if constexpr (MODE == kSelBig) {
         // one shared row a sequence (ws.scores, ws.cand, ws.ccnt: the indexer's)
         __syncthreads();                           // the parked page table, the zeroed bit map
@@ -874,7 +961,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             const int cidx = tile * 64 + 16 * w + (lane & 15);
             const int slot = cidx / g.bt;
             int blk;
-            if constexpr (MODE == kSelect || MODE == kSelBig) blk = sh.sel[min(slot, kDecSelMax - 1)];
+            if constexpr (MODE == kSelect || MODE == kSelBig || MODE == kSelRow) blk = sh.sel[min(slot, kDecSelMax - 1)];
             else blk = pre[min(i, nt - 1)];
             const int64_t t = (int64_t)blk * g.bt + cidx % g.bt;
             const bool in = i < nt && slot < n && blk >= 0 && t < L;
@@ -892,7 +979,7 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
         vm[i] = 0;
         const int tile = t_first + min(i, nt - 1);
         int blk;
-        if constexpr (MODE == kSelect || MODE == kSelBig) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
+        if constexpr (MODE == kSelect || MODE == kSelBig || MODE == kSelRow) blk = sh.sel[min(tile / tpb, kDecSelMax - 1)];
         else if constexpr (MODE == kGiven) blk = pre[min(i, nt - 1)];
         else blk = tile / tpb;
         const int64_t t0 = (int64_t)blk * g.bt + (tile % tpb) * 64;
@@ -1724,6 +1811,29 @@ hipError_t launch_dec_shape(const Geo &g, const qwfn_kv_view &v, const float *q,
     if (e != hipSuccess) return e;
     return launch_merge(g, v, seq_len, n_seq, max_seq_len, select ? ns : nsel, max_sel, !select && !sel, out, ws,
                         tpw, st);
+}
+
+// kSelRow: the attention selecting from one shared row a sequence (the
+// checkpoint indexer's scores, at most 32 keys a thread), then the merge.
+template <int HD, int G, int LY>
+hipError_t launch_dec_selrow_t(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                               int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                               float *out, const Ws &ws, hipStream_t st) {
+    const int span = max_seq_len / g.bt - (g.sink & ~3);
+    int tpw;
+    if (span <= 4 * kDecThreads)
+        tpw = launch_dec_t<HD, G, kSelRow, 4, false, LY>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, st);
+    else if (span <= 8 * kDecThreads)
+        tpw = launch_dec_t<HD, G, kSelRow, 8, false, LY>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, st);
+    else if (span <= 16 * kDecThreads)
+        tpw = launch_dec_t<HD, G, kSelRow, 16, false, LY>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, st);
+    else if (span <= 32 * kDecThreads)
+        tpw = launch_dec_t<HD, G, kSelRow, 32, false, LY>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, st);
+    else
+        return hipErrorInvalidValue;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_merge(g, v, seq_len, n_seq, max_seq_len, nsel, max_sel, false, out, ws, tpw, st);
 }
 
 // kSelBig: the attention selecting from one long shared row a sequence (the

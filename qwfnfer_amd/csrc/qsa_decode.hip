@@ -97,6 +97,20 @@ hipError_t launch_dec_selbig(const Geo &g, const qwfn_kv_view &v, const float *q
     return launch_dec_selbig_t<256, 12, kLyQ8K>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st);
 }
 
+// The checkpoint layer's shared row up to 32 keys a thread: every attention
+// workgroup selects from it (kSelRow), the indexer only scores.
+bool dec_selrow_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel) {
+    return dec_layout(g) == kLyQ8K && g.shared && !g.pf && g.topk > 0 && max_sel <= kDecSelMax && g.hd == 256 &&
+           g.G == 12 && max_seq_len / g.bt - (g.sink & ~3) <= 32 * kDecThreads;
+}
+
+hipError_t launch_dec_selrow(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                             int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                             float *out, const Ws &ws, hipStream_t st) {
+    if (!dec_selrow_fits(g, max_seq_len, max_sel)) return hipErrorInvalidValue;
+    return launch_dec_selrow_t<256, 12, kLyQ8K>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, out, ws, st);
+}
+
 hipError_t launch_test_select_big(const Geo &g, const float *scores, int32_t nb_cap, const int32_t *seq_len,
                                   int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                                   hipStream_t st) {

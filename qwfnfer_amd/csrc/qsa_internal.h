@@ -200,8 +200,10 @@ hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_i
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
                        int32_t blk0, hipStream_t st, const int32_t *len = nullptr);
 // select = false: scores only (the attention selects, launch_attention_select);
-// sel_launch = false: rows past the indexer workgroup's registers are scored
-// only (the attention selects from them, launch_dec_selbig)
+// sel_launch = false: the indexer does not select and no selection launch
+// follows: rows past its workgroup's registers leave each chunk's candidates
+// (the attention ranks them, launch_dec_selbig), shorter rows are scored only
+// (every attention workgroup selects from the row, launch_dec_selrow)
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
@@ -279,6 +281,10 @@ hipError_t launch_dec_attention(const Geo &g, const qwfn_kv_view &v, const float
 // nsel.  Fits: q8_0 blocks shorter than a tile at head_dim 256 and group 12,
 // a shared selection, rows up to 49,152 blocks, max_sel <= 1024.
 bool dec_selbig_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
+bool dec_selrow_fits(const Geo &g, int32_t max_seq_len, int32_t max_sel);
+hipError_t launch_dec_selrow(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
+                             int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
+                             float *out, const Ws &ws, hipStream_t st);
 hipError_t launch_dec_selbig(const Geo &g, const qwfn_kv_view &v, const float *q, const int32_t *seq_len,
                              int32_t n_seq, int32_t max_seq_len, int32_t *sel, int32_t *nsel, int32_t max_sel,
                              float *out, const Ws &ws, hipStream_t st);

@@ -593,13 +593,15 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
     const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     // 1: the last workgroup selects; 0: scores only (a selection launch
-    // follows); 2: scores and each chunk's candidates (the attention selects)
-    const int32_t mode = !big ? 1 : sel_launch ? 0 : 2;
+    // follows, or for a row the workgroup's registers hold the attention
+    // selects: sel_launch false); 2: scores and each chunk's candidates (the
+    // attention selects)
+    const int32_t mode = !big ? (sel_launch ? 1 : 0) : sel_launch ? 0 : 2;
     QWFN_LAUNCH(kTimedIndexer, (k_indexer<HD, G>), grid, dim3(kIdxThreads), st, g, v, q, seq_len, max_seq_len,
                 sel, nsel, max_sel, ws, n_chunks, fa, mode);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (big && !sel_launch) return hipSuccess;    // the attention selects (launch_dec_selbig)
+    if (!sel_launch) return hipSuccess;           // the attention selects (launch_dec_selbig / _selrow)
     if (big && ws.cut_wg > 0 && !(g.shared && g.Hkv > 1))
         hipLaunchKernelGGL(k_select_cut, dim3((unsigned)ws.cut_wg, (unsigned)(g.shared ? 1 : g.Hkv), (unsigned)n_seq),
                            dim3(kBigSelThreads), 0, st, g, v, seq_len, max_seq_len, ws, sel, nsel, max_sel);

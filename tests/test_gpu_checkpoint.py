@@ -204,17 +204,19 @@ def test_checkpoint_decode_steps():
     assert qsa.read_status(dev) == 0
 
 
-@pytest.mark.parametrize("dtype", [np.float32, np.float16])
-def test_checkpoint_fused_decode_steps(dtype):
+@pytest.mark.parametrize("dtype,L0", [(np.float32, [4998, 3001]), (np.float16, [4998, 3001]),
+                                      (np.float32, [12002, 9001]), (np.float16, [31994, 16001])])
+def test_checkpoint_fused_decode_steps(dtype, L0):
     """qwfn_idx_sparse_attn_decode (the K/V rows, the raw indexer key and its
     pooled block in one launch, then the indexer and the attention) for two
     sequences over steps that complete blocks in each: the cache bytes, raw and
     pooled keys and selections bit-exact against the oracle, the attention
     within the tolerance; a twin cache stepped through the four separate calls
-    ends with the same bytes, selections and outputs bit for bit."""
+    ends with the same bytes, selections and outputs bit for bit.  Up to 8,192
+    blocks every attention workgroup selects from the indexer's row, with 8,
+    16 and 32 keys a thread at these lengths."""
     cfg = CKPT
-    rng = np.random.default_rng(850)
-    L0 = [4998, 3001]                                  # block completions at steps 1 and 2, 5 and 6
+    rng = np.random.default_rng(850)            # block completions within the 7 steps in each sequence
     steps = 7
     pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
     pairs = [_pair(cfg, 2, pps, seed=851), _pair(cfg, 2, pps, seed=851)]
