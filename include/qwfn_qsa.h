@@ -518,8 +518,10 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
  * (:497-542).  src_dtype covers k_new, v_new and k_raw.  sel [n_seq]
  * [n_head_kv][max_sel] and n_sel [n_seq][n_head_kv] (required: the selection
  * passes through them) receive the selection as qwfn_idx_select writes it.
- * Workspace: qwfn_idx_workspace_bytes.  Past 8,192 candidate blocks (the
- * 4-token blocks past 32,768 tokens) the append launch also scores 1,024
+ * Workspace: qwfn_idx_workspace_bytes.  Up to 8,192 candidate blocks the
+ * indexer only scores and every attention workgroup selects from the row.
+ * Past 8,192 candidate blocks (the 4-token blocks past 32,768 tokens) the
+ * append launch also scores 1,024
  * sampled blocks of each row and places a cut, the indexer keeps each chunk's
  * scores above it, and the attention workgroups rank those candidates
  * exactly (a fallback over the whole row where the cut leaves too few or too
@@ -527,7 +529,8 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
  * (24 x 256, 4 indexer heads of at most 128) up to 49,152 blocks; longer
  * rows, other shapes and a workspace smaller than qwfn_idx_workspace_bytes
  * (at least what qwfn_qsa_workspace_bytes and qwfn_idx_select each need)
- * keep the selection launch.  Replaces the four calls qwfn_kv_append_q8_0,
+ * select in the indexer's last workgroup or a selection launch, as
+ * qwfn_idx_select does.  Replaces the four calls qwfn_kv_append_q8_0,
  * qwfn_idx_append_pool, qwfn_idx_select and qwfn_sparse_decode_attn of a
  * decode step with one launch fewer (two past 8,192 blocks). */
 int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
