@@ -477,14 +477,22 @@ k_score(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_l
         else fused_append_pool<HD, QWFN_KV_Q8_0, NT>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
         return;
     }
-    // the query rows, the length and the pooled keys go out together
+    // one sequence: the length, the query rows and the pooled keys go out
+    // together.  Several: the grid spans the longest one's blocks, so the
+    // length comes first and a workgroup past its sequence's eligible blocks
+    // ends before reading keys nothing uses
+    const int L = seq_len[s];
+    const bool ok = L >= 1 && L <= max_seq_len;
+    if (gridDim.z > 1) {                           // (uniform)
+        const Ranges r0 = qsa_ranges(g, L);
+        const int ne0 = r0.e_hi - r0.e_lo;
+        if (!(ok && g.topk > 0 && ne0 > eff_topk(g, r0) && c * BPW < ne0)) return;
+    }
     constexpr int QV = (G * HD / 4 + NT - 1) / NT;
     const float4 *qg4 = reinterpret_cast<const float4 *>(q + ((int64_t)s * g.H + (int64_t)gh * G) * HD);
     float4 qv[QV];
 #pragma unroll
     for (int i = 0; i < QV; ++i) qv[i] = qg4[min(tid + i * NT, G * HD / 4 - 1)];
-    const int L = seq_len[s];
-    const bool ok = L >= 1 && L <= max_seq_len;
     const int pair = s * g.Hkv + gh;
     const int j = tid & 3, hh = (tid >> 2) & 1, bl = tid >> 3;
     const int bi = c * BPW + bl;
