@@ -560,11 +560,13 @@ __device__ __forceinline__ void dec_big_zero(DecSelBig &bs) {
 // pairs' counts and a wave scan) plus those below its lane: the winners go
 // out in block order after the sink blocks with no further LDS reads.
 // Returns false, with nothing emitted, when the threshold bin holds more than
-// kCandMax keys.
-__device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uint32_t kmin, uint32_t kmax,
-                                              const SelOut &out, DecSelBig &bs) {
-    constexpr int NT = kDecThreads, CPT = kSelCandMax / NT;
-    static_assert(CPT * NT == kSelCandMax && CPT * kDecWaves == 64, "whole candidate rounds; a (round, wave) a lane");
+// kCandMax keys.  CPT rounds of kDecThreads candidates cover C (the caller
+// takes the 8-round instance when C allows; dec_big_exact picks).
+template <int CPT>
+__device__ __forceinline__ bool dec_big_exact_r(const Geo &g, int C, int topk, uint32_t kmin, uint32_t kmax,
+                                                const SelOut &out, DecSelBig &bs) {
+    constexpr int NT = kDecThreads;
+    static_assert(CPT * NT <= kSelCandMax && kSelCandMax / NT * kDecWaves == 64, "whole candidate rounds; a (round, wave) a lane");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float sc2 = 4096.0f / ((float)(kmax - kmin) + 1.0f);
@@ -626,7 +628,7 @@ __device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uin
         const int n = (int)__builtin_popcountll(__ballot((wm >> u) & 1u));
         cnt = lane == u ? n : cnt;
     }
-    if (lane < CPT) bs.rwin[lane * kDecWaves + wid] = cnt;
+    if (lane < kSelCandMax / NT) bs.rwin[lane * kDecWaves + wid] = cnt;   // (0 past CPT rounds)
     __syncthreads();
     const int x = bs.rwin[lane];                   // pair (lane / kDecWaves, lane % kDecWaves)
     const int ex = wave_incl_scan(x) - x;
@@ -640,6 +642,13 @@ __device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uin
         if (((wm >> u) & 1u) && pos < topk) out.put(g.sink + pos, bid[u]);
     }
     return true;
+}
+
+__device__ __forceinline__ bool dec_big_exact(const Geo &g, int C, int topk, uint32_t kmin, uint32_t kmax,
+                                              const SelOut &out, DecSelBig &bs) {
+    constexpr int R = kSelCandMax / kDecThreads;
+    if (C <= R / 2 * kDecThreads) return dec_big_exact_r<R / 2>(g, C, topk, kmin, kmax, out, bs);   // (uniform)
+    return dec_big_exact_r<R>(g, C, topk, kmin, kmax, out, bs);
 }
 
 // The end of a long row's selection from C candidates in bs.cand (an upper
