@@ -991,15 +991,23 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     const bool row_sel = max_seq_len / g.bt <= kIdxRegKeys && dec_selrow_fits(g, max_seq_len, max_sel) && split_ws;
     const Ws wi = ws_bind(ws, li);
     const IdxCut cut{fused_sel ? q_idx : nullptr, wi.cutk, ishape->n_idx_head, max_seq_len};
-    // the K/V rows, the raw indexer key and its block's pooled key: one launch
-    hipError_t e = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled,
-                                          iview->k_norm, k_raw, f16, nullptr, nullptr, n_seq, st,
-                                          FusedAppend{k_new, v_new, f16, 1}, seq_len, cut);
-    if (e != hipSuccess) return hip_fail(e, "idx decode: append");
+    // the K/V rows, the raw indexer key and its block's pooled key: a launch of
+    // their own, or (row_sel, one score row a sequence) the indexer launch's
+    // append workgroup, which also scores the block the token completes
+    const IdxAppend ia{g, *view, ig, FusedAppend{k_new, v_new, f16, 1}, k_raw, iview->k_norm,
+                       (uint16_t *)iview->raw, f16, row_sel && gi.Hkv == 1 ? 1 : 0};
+    hipError_t e = hipSuccess;
+    if (!ia.enabled) {
+        e = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled, iview->k_norm,
+                                   k_raw, f16, nullptr, nullptr, n_seq, st, FusedAppend{k_new, v_new, f16, 1},
+                                   seq_len, cut);
+        if (e != hipSuccess) return hip_fail(e, "idx decode: append");
+    }
     qwfn_kv_view vi = *view;
     vi.pooled = (float *)iview->pooled;                   // fp16 keys (Geo::pooled_f16)
     e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, wi,
-                       FusedAppend{nullptr, nullptr, 0, 0}, st, true, !(fused_sel || row_sel));
+                       FusedAppend{nullptr, nullptr, 0, 0}, st, true, !(fused_sel || row_sel),
+                       ia.enabled ? &ia : nullptr);
     if (e != hipSuccess) return hip_fail(e, "idx decode: indexer");
     if (fused_sel || row_sel) {
         Ws wa = ws_bind((uint8_t *)ws + align256(li.total), la);

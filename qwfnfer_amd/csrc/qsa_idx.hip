@@ -16,6 +16,7 @@
 #include "qsa_append.h"
 #include "qsa_device.h"
 #include "qsa_select.h"
+#include "qsa_idx_pool.h"
 
 namespace qwfn_qsa {
 
@@ -60,107 +61,6 @@ hipError_t launch_idx_write(const Geo &g, const qwfn_kv_view &v, const IdxGeo &i
     return hipGetLastError();
 }
 
-// The pooled key of one block from its bt members m[0 .. bt) (fp16 rows of D
-// values, position order), by one wave; lane l owns dims l + 64k (k < D/64).
-// ys is the wave's own D floats of LDS.
-//   mean   : fp32 add chain over the members in position order, * (1/bt)
-//            (ggml_add chain + ggml_scale, src/qwfn_graph.cpp:415-422); the
-//            members' loads go out eight at a time before any is summed
-//   RMSNorm: sum of the fp32 squares in fp64 -- per lane in k order, then a
-//            butterfly over lane distance 32, 16, .., 1 --, mean = (float)
-//            (sum / D), scale = 1 / sqrtf(mean + eps), x * scale * k_norm[d]
-//            (ggml_rms_norm also sums in fp64; :423)
-//   rotary : pair (i, i + nd/2) turned by (x0 c - x1 s, x0 s + x1 c), dims
-//            >= nd unchanged, with ggml's IMROPE angle (:425-427): theta_0 =
-//            (float)pos, theta_{i+1} = theta_i * theta_scale rounded to fp32,
-//            theta_scale = powf(base, -2/nd) -- the running product ggml's
-//            rope cache builds, one factor per pair --; cos / sin of that
-//            fp32 angle evaluated in fp64 and rounded to fp32.  IMROPE gives
-//            each pair the position of its section (t, h, w interleaved); the
-//            reference fills every section of a block's position with the
-//            block's first position b * bt (src/qwfn_engine.cpp:741-743, 926,
-//            934), so every pair takes pos = b * bt.
-//   store  : rounded to fp16 (the reference's F16 pool cache).
-// cos / sin of the rotation of dims lane + 64 k (see pool_idx_block) for a
-// block at position t0: 1, 0 for the dims past nd.
-template <int D>
-__device__ __forceinline__ void idx_rot_cs(const IdxGeo &ig, int t0, int lane, float (&cc)[D / 64],
-                                           float (&sn)[D / 64]) {
-    const int half = ig.nd / 2;
-#pragma unroll
-    for (int k = 0; k < D / 64; ++k) {
-        const int d = lane + 64 * k;
-        cc[k] = 1.0f;
-        sn[k] = 0.0f;
-        if (d < ig.nd) {
-            const int i = d < half ? d : d - half;
-            // ggml's angle of pair i: the block position times theta_scale, i
-            // times over, each product rounded to fp32
-            float th = (float)t0;
-            for (int e = 0; e < i; ++e) th = __fmul_rn(th, ig.theta_scale);
-            cc[k] = (float)cos((double)th);
-            sn[k] = (float)sin((double)th);
-        }
-    }
-}
-
-// The pooled key of one block from its bt members (row(r, k): member r's dim
-// lane + 64 k as fp32, position order) and its rotation's cos / sin, by one
-// wave (pool_idx_block's arithmetic).
-template <int D, class Row>
-__device__ __forceinline__ void pool_idx_rows(const Geo &g, const IdxGeo &ig, Row row, const float *__restrict__ k_norm,
-                                              float *ys, uint16_t *dst, int lane, const float (&cc)[D / 64],
-                                              const float (&sn)[D / 64]) {
-#pragma clang fp contract(off)
-    constexpr int K = D / 64, U = 8;
-    float x[K];
-    for (int r0 = 0; r0 < g.bt; r0 += U) {
-        float y[U][K];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = min(r0 + u, g.bt - 1);
-#pragma unroll
-            for (int k = 0; k < K; ++k) y[u][k] = row(r, k);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int k = 0; k < K; ++k)
-                if (r0 + u < g.bt) x[k] = r0 + u == 0 ? y[u][k] : x[k] + y[u][k];
-    }
-    double ss = 0.0;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        x[k] = x[k] * g.inv_bt;
-        const float sq = x[k] * x[k];
-        ss = ss + (double)sq;
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off);
-    const float mean = (float)(ss / (double)D);
-    const float scale = 1.0f / sqrtf(mean + ig.eps);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int d = lane + 64 * k;
-        ys[d] = (x[k] * scale) * k_norm[d];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    const int half = ig.nd / 2;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int d = lane + 64 * k;
-        float o = ys[d];
-        if (d < ig.nd) {
-            const int i = d < half ? d : d - half;
-            const float c = cc[k], s = sn[k];
-            const float x0 = ys[i], x1 = ys[i + half];
-            o = d < half ? x0 * c - x1 * s : x0 * s + x1 * c;
-        }
-        dst[d] = f2h(o);
-    }
-}
 
 // The pooled key of one block from its bt members m[0 .. bt) (fp16 rows of D
 // values, position order), by one wave; lane l owns dims l + 64k (k < D/64).

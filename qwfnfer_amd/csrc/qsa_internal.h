@@ -199,6 +199,21 @@ hipError_t launch_append(const Geo &g, const qwfn_kv_view &v, const void *k, con
 hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_ids,
                        const int32_t *block_ids, int32_t n_blocks, int32_t seq_const,
                        int32_t blk0, hipStream_t st, const int32_t *len = nullptr);
+// The checkpoint indexer's append workgroup inside the indexer launch (the
+// fused decode step when the attention selects from the indexer's row): the
+// token's K / V rows into the attention's pages (ga, va), its raw key src
+// [n_seq][ig.dim] (fp16 or fp32) into the raw cache, its block re-pooled and,
+// when the token completes the block, scored (idx_append_wg).
+struct IdxAppend {
+    Geo ga;
+    qwfn_kv_view va;
+    IdxGeo ig;
+    FusedAppend kv;
+    const void *src;
+    const float *k_norm;
+    uint16_t *raw;
+    int32_t f16, enabled;
+};
 // select = false: scores only (the attention selects, launch_attention_select);
 // sel_launch = false: the indexer does not select and no selection launch
 // follows: rows past its workgroup's registers leave each chunk's candidates
@@ -207,7 +222,8 @@ hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_i
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                          const FusedAppend &fa, hipStream_t st, bool select = true, bool sel_launch = true);
+                          const FusedAppend &fa, hipStream_t st, bool select = true, bool sel_launch = true,
+                          const IdxAppend *ia = nullptr);
 // Prefill: scores of n_q queries (Geo::pf) into ws.scores, then each query's
 // selection into sel / nsel.
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,

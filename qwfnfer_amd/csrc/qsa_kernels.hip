@@ -14,6 +14,7 @@
 #include "qsa_append.h"
 #include "qsa_device.h"
 #include "qsa_select.h"
+#include "qsa_idx_pool.h"
 
 namespace qwfn_qsa {
 
@@ -301,10 +302,15 @@ template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
 k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
           int32_t *sel, int32_t *nsel, int32_t max_sel, Ws ws, int32_t n_chunks, FusedAppend fa,
-          int32_t select_here) {
+          int32_t select_here, IdxAppend ia) {
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    if (ia.enabled && c == n_chunks) {             // the checkpoint indexer's append workgroup (one KV row)
+        idx_append_wg<HD, G, kIdxThreads>(g, ia, q, seq_len, s, reinterpret_cast<uint16_t *>(v.pooled),
+                                          ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, sh.u.q);
+        return;
+    }
     if (fa.enabled && c == n_chunks) {             // the append workgroup
         if (g.kt == QWFN_KV_Q4_0) fused_append_pool<HD, QWFN_KV_Q4_0, kIdxThreads>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
         else if (g.kt == QWFN_KV_F16) fused_append_pool<HD, QWFN_KV_F16, kIdxThreads>(g, v, fa, s, gh, seq_len, max_seq_len, sh);
@@ -362,8 +368,9 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         const Ranges r = qsa_ranges(g, L);
         const int ne = r.e_hi - r.e_lo;
         if (ne > eff_topk(g, r) && c * kBlocksPerChunk < ne) {
-            const bool act = bi < ne;
             const int b = r.e_lo + bi;
+            // the block this token completes is the append workgroup's to score
+            const bool act = bi < ne && !(ia.enabled && L % g.bt == 0 && b == (L - 1) / g.bt);
 #pragma unroll
             for (int i = 0; i < QV; ++i)
                 if (tid + i * kIdxThreads < G * HD / 4) reinterpret_cast<float4 *>(sh.u.q)[tid + i * kIdxThreads] = qv[i];
@@ -575,7 +582,8 @@ template <int HD, int G>
 static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const float *q,
                                    const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                                    int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                                   FusedAppend fa, hipStream_t st, bool select, bool sel_launch) {
+                                   FusedAppend fa, hipStream_t st, bool select, bool sel_launch,
+                                   const IdxAppend *ia) {
     // The append workgroup's pooled block must not be one the scoring
     // workgroups read: with local_tokens = 0 a just-completed block is
     // eligible, so the append and the pooling run as launches of their own,
@@ -598,7 +606,9 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
     const int nb_max = max_seq_len / g.bt;
     int n_chunks = (nb_max + kBlocksPerChunk - 1) / kBlocksPerChunk;
     if (n_chunks < 1) n_chunks = 1;
-    const dim3 grid((unsigned)(n_chunks + (fa.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
+    IdxAppend ian{};
+    if (ia) ian = *ia;
+    const dim3 grid((unsigned)(n_chunks + (fa.enabled || ian.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     // 1: the last workgroup selects; 0: scores only (a selection launch
     // follows, or for a row the workgroup's registers hold the attention
@@ -606,7 +616,7 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
     // attention selects)
     const int32_t mode = !big ? (sel_launch ? 1 : 0) : sel_launch ? 0 : 2;
     QWFN_LAUNCH(kTimedIndexer, (k_indexer<HD, G>), grid, dim3(kIdxThreads), st, g, v, q, seq_len, max_seq_len,
-                sel, nsel, max_sel, ws, n_chunks, fa, mode);
+                sel, nsel, max_sel, ws, n_chunks, fa, mode, ian);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (!sel_launch) return hipSuccess;           // the attention selects (launch_dec_selbig / _selrow)
@@ -2359,11 +2369,12 @@ hipError_t launch_pool(const Geo &g, const qwfn_kv_view &v, const int32_t *seq_i
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
-                          const FusedAppend &fa, hipStream_t st, bool select, bool sel_launch) {
+                          const FusedAppend &fa, hipStream_t st, bool select, bool sel_launch,
+                          const IdxAppend *ia) {
 #define X(HD_, G_, TG_)                                                                          \
     if (g.hd == HD_ && g.G == G_)                                                                \
         return launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st, select, \
-                                         sel_launch);
+                                         sel_launch, ia);
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
     return hipErrorInvalidValue;
