@@ -461,12 +461,13 @@ class CheckpointRunner:
     """The released checkpoint's attention layer (24 query heads, 2 KV heads of
     256, q8_0 KV, blocks of 4 tokens pooled by its own indexer of 4 heads x 128,
     513 kept blocks) stepped one decode token at a time through
-    qwfn_idx_sparse_attn_decode: per layer one launch for the K/V rows, the raw
-    indexer key and its block's pooled key (past 8,192 candidate blocks it also
-    scores a sample of the row and places a cut), then the indexer (its last
-    workgroup selects; past 8,192 blocks its workgroups keep the keys above the
-    cut as candidates), the attention (ranking those candidates itself) and its
-    merge -- four launches at either length."""
+    qwfn_idx_sparse_attn_decode.  Up to 8,192 candidate blocks, three launches
+    a layer: the indexer (one extra workgroup appends the K/V rows and the raw
+    indexer key, re-pools its block and scores it when complete), the attention
+    (every workgroup selects from the indexer's row) and its merge.  Past 8,192
+    blocks, four: the K/V rows, raw key and pooled key with a sampled cut of the
+    row, the indexer (its workgroups keep the keys above the cut as
+    candidates), the attention (ranking the candidates itself) and the merge."""
 
     def __init__(self, qsa, torch, ctx, n_layer, gen):
         self.qsa, self.torch = qsa, torch
@@ -832,8 +833,9 @@ def main():
             torch.cuda.empty_cache()
         checkpoint = dict(per_context=ck, workload="the released checkpoint's attention layer: 24q/2kv heads "
                           "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
-                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (4 launches: "
-                          "append (+ the sampled cut past 8,192 blocks), indexer, attention, merge), hipGraph")
+                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (3 launches "
+                          "up to 8,192 blocks: indexer with the append, attention, merge; 4 past them: append with a "
+                          "sampled cut, indexer, attention, merge), hipGraph")
         if not args.no_prefill:
             checkpoint["prefill"] = bench_checkpoint_prefill(qsa, torch, gen)
             log(f"[bench] checkpoint prefill chunk ({PREFILL_N} queries at {PREFILL_POS0}): "

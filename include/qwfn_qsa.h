@@ -519,7 +519,9 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
  * [n_head_kv][max_sel] and n_sel [n_seq][n_head_kv] (required: the selection
  * passes through them) receive the selection as qwfn_idx_select writes it.
  * Workspace: qwfn_idx_workspace_bytes.  Up to 8,192 candidate blocks the
- * indexer only scores and every attention workgroup selects from the row.
+ * indexer scores (its launch also appends the rows and pools and scores the
+ * block the token completes) and every attention workgroup selects from the
+ * row: three launches.
  * Past 8,192 candidate blocks (the 4-token blocks past 32,768 tokens) the
  * append launch also scores 1,024
  * sampled blocks of each row and places a cut, the indexer keeps each chunk's
@@ -532,7 +534,7 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
  * select in the indexer's last workgroup or a selection launch, as
  * qwfn_idx_select does.  Replaces the four calls qwfn_kv_append_q8_0,
  * qwfn_idx_append_pool, qwfn_idx_select and qwfn_sparse_decode_attn of a
- * decode step with one launch fewer (two past 8,192 blocks). */
+ * decode step (five launches, six past 8,192 blocks) with two fewer. */
 int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                                 const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
                                 const float *q, const float *q_idx, const void *k_new,
