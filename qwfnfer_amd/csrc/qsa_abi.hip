@@ -989,13 +989,22 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     // every attention workgroup selects from the row (no last-workgroup
     // selection in the indexer); the same split workspace.
     const bool row_sel = max_seq_len / g.bt <= kIdxRegKeys && dec_selrow_fits(g, max_seq_len, max_sel) && split_ws;
-    const Ws wi = ws_bind(ws, li);
-    const IdxCut cut{fused_sel ? q_idx : nullptr, wi.cutk, ishape->n_idx_head, max_seq_len};
+    // Past 8,192 blocks with one score row a sequence, the append workgroup
+    // and the cut's sample workgroups run in the indexer launch too, ahead of
+    // the chunks that wait for them (no sample is the row's last block, the
+    // one the append may re-pool; the chunk holding it takes its key from the
+    // append workgroup).
+    const bool in_cut = fused_sel && gi.Hkv == 1;
+    Ws wi = ws_bind(ws, li);
+    const IdxCut cut{fused_sel && !in_cut ? q_idx : nullptr, wi.cutk, ishape->n_idx_head, max_seq_len};
+    if (in_cut) wi.cutk = reinterpret_cast<uint32_t *>(wi.cnt_idx + kCutReadyBase);
     // the K/V rows, the raw indexer key and its block's pooled key: a launch of
-    // their own, or (row_sel, one score row a sequence) the indexer launch's
-    // append workgroup, which also scores the block the token completes
+    // their own, or (row_sel or in_cut, one score row a sequence) the indexer
+    // launch's append workgroup, which also scores the block the token
+    // completes when that block is eligible
     const IdxAppend ia{g, *view, ig, FusedAppend{k_new, v_new, f16, 1}, k_raw, iview->k_norm,
-                       (uint16_t *)iview->raw, f16, row_sel && gi.Hkv == 1 ? 1 : 0};
+                       (uint16_t *)iview->raw, f16, (row_sel || in_cut) && gi.Hkv == 1 ? 1 : 0,
+                       in_cut ? wi.cutk : nullptr};
     hipError_t e = hipSuccess;
     if (!ia.enabled) {
         e = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled, iview->k_norm,
@@ -1007,7 +1016,7 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     vi.pooled = (float *)iview->pooled;                   // fp16 keys (Geo::pooled_f16)
     e = launch_indexer(gi, vi, q_idx, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, wi,
                        FusedAppend{nullptr, nullptr, 0, 0}, st, true, !(fused_sel || row_sel),
-                       ia.enabled ? &ia : nullptr);
+                       ia.enabled ? &ia : nullptr, in_cut);
     if (e != hipSuccess) return hip_fail(e, "idx decode: indexer");
     if (fused_sel || row_sel) {
         Ws wa = ws_bind((uint8_t *)ws + align256(li.total), la);
@@ -1015,6 +1024,7 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
         wa.nb_cap = wi.nb_cap;
         wa.cand = wi.cand;
         wa.ccnt = wi.ccnt;
+        wa.cutk = in_cut ? wi.cutk : nullptr;     // kSelBig clears the in-launch cut's slots
         e = fused_sel ? launch_dec_selbig(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, wa, st)
                       : launch_dec_selrow(g, *view, q, seq_len, n_seq, max_seq_len, sel, n_sel, max_sel, out, wa, st);
     } else {

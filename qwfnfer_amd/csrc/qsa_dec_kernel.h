@@ -861,6 +861,12 @@ k_dec(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *__restr
             }
         }
     }
+    // kSelBig after a cut placed in the indexer launch (ws.cutk set): workgroup
+    // (0, 0) of the sequence sets its cut slots back to zero (that launch has
+    // finished with them), for the next call
+    if constexpr (MODE == kSelBig)
+        if (ws.cutk && blockIdx.x == 0 && blockIdx.y == 0 && tid < kCutSlots)
+            ws.cutk[(int64_t)s * kCutSlots + tid] = 0u;
     int n_given = 0;
     // kGiven: the tiles' blocks; kDense: their pages.  GATH: the block of the
     // lane's cell (lane & 15 of the wave's 16) in each tile

@@ -145,7 +145,11 @@ __device__ __forceinline__ float idx_block_score(const float *yo, const float4 (
 // into the raw cache and its block re-pooled from the members and the new row
 // (wave 0, as k_idx_decode_append); when the token completes the block, wave
 // 0 also scores it from the stored key (idx_block_score) into the sequence's
-// score row, which the scoring workgroups leave to it.  scratch: 2 D floats.
+// score row, which the scoring workgroups leave to it.  With the cut placed in
+// the same launch (ia.slots), that score's key + 1 also goes to the slot after
+// the sequence's part keys, whenever the scoring workgroup of that block
+// expects it (the key 0 when an error ends the append first).  scratch: 2 D
+// floats.
 template <int D, int G, int NT>
 __device__ __forceinline__ void idx_append_wg(const Geo &gi, const IdxAppend &ia, const float *__restrict__ q,
                                               const int32_t *len, int s, uint16_t *pooled, float *sc,
@@ -167,6 +171,18 @@ __device__ __forceinline__ void idx_append_wg(const Geo &gi, const IdxAppend &ia
     }
     constexpr int K = D / 64;
     const int L = len[s];
+    // the block this token completes, when it is eligible: its chunk's scoring
+    // workgroup waits for its key in the slot (the same test on that side)
+    bool expect = false;
+    if (ia.slots && L >= 1 && L % g.bt == 0 && gi.topk > 0) {
+        const Ranges r = qsa_ranges(gi, L);
+        const int bc = (L - 1) / g.bt;
+        expect = r.e_hi - r.e_lo > eff_topk(gi, r) && bc >= r.e_lo && bc < r.e_hi;
+    }
+    uint32_t *slot = ia.slots ? ia.slots + (int64_t)s * kCutSlots + kIdxCutParts : nullptr;
+    auto publish = [&](uint32_t key1) {
+        if (expect && lane == 0) __hip_atomic_store(slot, key1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     uint16_t nh[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -176,13 +192,17 @@ __device__ __forceinline__ void idx_append_wg(const Geo &gi, const IdxAppend &ia
     float4 qr[D / 16];                             // the block score's query values, loaded early
     idx_score_q<D, G>(q + (int64_t)s * gi.H * D, lane, qr);
     const int t = L - 1;
-    if (s >= g.n_seq_view) { if (lane == 0) set_status(ia.va.status, QWFN_STATUS_SEQ_RANGE); return; }
-    if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) { if (lane == 0) set_status(ia.va.status, QWFN_STATUS_POS_RANGE); return; }
+    if (s >= g.n_seq_view) { if (lane == 0) set_status(ia.va.status, QWFN_STATUS_SEQ_RANGE); publish(1u); return; }
+    if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) {
+        if (lane == 0) set_status(ia.va.status, QWFN_STATUS_POS_RANGE);
+        publish(1u);
+        return;
+    }
     const int32_t pp = phys_page(g, ia.va.page_table, s, t);
     const int b = t / g.bt, t0 = b * g.bt, rn = t - t0;
     float cc[K], sn[K];
     idx_rot_cs<D>(ia.ig, t0, lane, cc, sn);
-    if (pp < 0) { if (lane == 0) set_status(ia.va.status, QWFN_STATUS_PAGE_RANGE); return; }
+    if (pp < 0) { if (lane == 0) set_status(ia.va.status, QWFN_STATUS_PAGE_RANGE); publish(1u); return; }
     uint16_t *row = ia.raw + ((int64_t)pp * g.pt + t % g.pt) * D;
 #pragma unroll
     for (int k = 0; k < K; ++k) row[lane + 64 * k] = nh[k];
@@ -198,6 +218,7 @@ __device__ __forceinline__ void idx_append_wg(const Geo &gi, const IdxAppend &ia
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
     const float score = idx_block_score<D, G>(yo, qr, gi.relu, lane);
     if (lane == 0) sc[b] = score;
+    publish(score_key(score) + 1u);
 }
 
 }  // namespace qwfn_qsa

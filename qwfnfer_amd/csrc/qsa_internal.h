@@ -178,6 +178,16 @@ constexpr int kIdxFuseRows = 64;
 // NULL: no cut.
 constexpr int kIdxCutParts = 16;
 constexpr int kIdxMaxCutHeads = 16;   // query heads * dim <= 16 * 128
+// The same cut placed inside the indexer launch (launch_indexer's in_cut): per
+// sequence kCutSlots slots, key + 1 (0 while unwritten), of the kIdxCutParts
+// part keys and then the key of the block the token completes (the append
+// workgroup's score), at the top of the counter region from kCutReadyBase.
+// Every call leaves that region at zero and calls on one workspace do not
+// overlap, so the slots are zero when the indexer launch starts; the attention
+// launch that reads the candidates clears them again.
+constexpr int kCutSlots = 32;
+constexpr int kCutReadyBase = kMaxCounters - kIdxFuseRows * kCutSlots;
+static_assert(kCutReadyBase >= 0, "the cut slots fit the counter region");
 struct IdxCut {
     const float *q_idx;
     uint32_t *cutk;
@@ -213,17 +223,22 @@ struct IdxAppend {
     const float *k_norm;
     uint16_t *raw;
     int32_t f16, enabled;
+    uint32_t *slots;     // the in-launch cut's slots (in_cut), else NULL
 };
 // select = false: scores only (the attention selects, launch_attention_select);
 // sel_launch = false: the indexer does not select and no selection launch
 // follows: rows past its workgroup's registers leave each chunk's candidates
 // (the attention ranks them, launch_dec_selbig), shorter rows are scored only
-// (every attention workgroup selects from the row, launch_dec_selrow)
+// (every attention workgroup selects from the row, launch_dec_selrow).
+// in_cut (with sel_launch false, rows past the registers, one KV head, a local
+// window): kIdxCutParts leading workgroups per sequence place the sampled cut
+// into ws.cutk (the slots at kCutReadyBase) and the chunks wait for it, instead
+// of reading the append launch's
 hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                           const FusedAppend &fa, hipStream_t st, bool select = true, bool sel_launch = true,
-                          const IdxAppend *ia = nullptr);
+                          const IdxAppend *ia = nullptr, bool in_cut = false);
 // Prefill: scores of n_q queries (Geo::pf) into ws.scores, then each query's
 // selection into sel / nsel.
 hipError_t launch_prefill_index(const Geo &g, const qwfn_kv_view &v, const float *q, int32_t n_q,

@@ -297,7 +297,135 @@ k_select_cut(Geo g, qwfn_kv_view v, const int32_t *seq_len, int32_t max_seq_len,
     }
 }
 
-// grid (n_chunks [+1 with the fused append], Hkv, n_seq)
+// Part `part` of sequence s's sampled cut inside the indexer launch (mode 3):
+// kBlocksPerChunk of the row's kIdxCutSamples evenly spaced eligible blocks
+// (the append launch's samples, idx_sample_cut), each scored by four lanes as
+// the chunks score, and the ceil(rs / kIdxCutParts)-th largest of their keys
+// (0, every key a candidate, when no cut applies) stored + 1 into the part's
+// slot (ws.cutk, kCutSlots a sequence) with an agent-scope store.  These
+// workgroups wait for nothing.
+template <int HD, int G>
+__device__ __forceinline__ void idx_cut_part(const Geo &g, const qwfn_kv_view &v, const float *q,
+                                             const int32_t *seq_len, int32_t max_seq_len, const Ws &ws, int s,
+                                             int gh, int part, IdxShared &sh) {
+#pragma clang fp contract(off)
+    static_assert(kIdxCutSamples == kIdxCutParts * kBlocksPerChunk, "a part's samples: one a lane group");
+    const int tid = threadIdx.x, bl = tid >> 2, j = tid & 3;
+    const int L = seq_length(g, seq_len[s], s);
+    int rs = 0;
+    Ranges r{0, 0, 0, 0};
+    if (L >= 1 && L <= max_seq_len && g.topk > 0) {
+        r = qsa_ranges(g, L);
+        const int topk = eff_topk(g, r);
+        if (r.e_hi - r.e_lo > topk) rs = sample_rank<kIdxCutSamples>(r, topk);
+    }
+    uint32_t tk = 0u;
+    if (rs > 0) {                                  // (uniform)
+        const int b =
+            r.e_lo + (int)((int64_t)(part * kBlocksPerChunk + bl) * (r.e_hi - r.e_lo) / kIdxCutSamples);
+        const int64_t prow = (((int64_t)cache_seq(g, s) * g.Hkv + gh) * g.bps + b) * HD;
+        float4 p4[HD / 16];
+        if (g.pooled_f16) {
+            const uint16_t *P = reinterpret_cast<const uint16_t *>(v.pooled) + prow;
+#pragma unroll
+            for (int i = 0; i < HD / 16; ++i) {
+                const uint2 x = *reinterpret_cast<const uint2 *>(P + 16 * i + 4 * j);
+                p4[i] = make_float4(h2f((uint16_t)x.x), h2f((uint16_t)(x.x >> 16)), h2f((uint16_t)x.y),
+                                    h2f((uint16_t)(x.y >> 16)));
+            }
+        } else {
+            const float *P = v.pooled + prow;
+#pragma unroll
+            for (int i = 0; i < HD / 16; ++i) p4[i] = *reinterpret_cast<const float4 *>(P + 16 * i + 4 * j);
+        }
+        const float4 *qg4 = reinterpret_cast<const float4 *>(q + ((int64_t)s * g.H + (int64_t)gh * G) * HD);
+        for (int i = tid; i < G * HD / 4; i += kIdxThreads) reinterpret_cast<float4 *>(sh.u.q)[i] = qg4[i];
+        __syncthreads();
+        float acc[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(&sh.u.q[h * HD + 16 * i + 4 * j]);
+                acc[h] = fmaf(q4.x, p4[i].x, acc[h]);
+                acc[h] = fmaf(q4.y, p4[i].y, acc[h]);
+                acc[h] = fmaf(q4.z, p4[i].z, acc[h]);
+                acc[h] = fmaf(q4.w, p4[i].w, acc[h]);
+            }
+        }
+        float score = 0.0f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float t01 = acc[h] + __shfl_xor(acc[h], 1);
+            float dot = t01 + __shfl_xor(t01, 2);
+            if (g.relu) dot = dot > 0.0f ? dot : 0.0f;
+            score = (h == 0) ? dot : score + dot;
+        }
+        if (j == 0) sh.cand_key[bl] = score_key(score);
+        __syncthreads();
+        if (tid < 64) {                            // wave 0: a sample key a lane
+            const uint32_t k1 = sh.cand_key[tid];
+            const int need = (rs + kIdxCutParts - 1) / kIdxCutParts;
+#pragma unroll 1
+            for (int bit = 31; bit >= 0; --bit) {
+                const uint32_t t = tk | (1u << bit);
+                tk = __builtin_popcountll(__ballot(k1 >= t)) >= need ? t : tk;
+            }
+        }
+    }
+    if (tid == 0)
+        __hip_atomic_store(ws.cutk + (int64_t)(s * g.Hkv + gh) * kCutSlots + part, tk + 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls of a chunk workgroup waiting for the in-launch cut.
+constexpr int kCutSpinMax = 1 << 16;
+
+// The in-launch cut for a chunk workgroup: wave 0 polls the kIdxCutParts part
+// slots of its sequence (lane p reads part p with agent-scope loads) and, with
+// want_b, the completed block's slot (lane kIdxCutParts) until every one is
+// in; the mean of the part keys goes to tk and the block's key to kb.  The
+// append and part workgroups come first in the grid and wait for nothing, so
+// they are dispatched before any workgroup that polls and always finish; the
+// bound on the polls only makes every wave's exit certain.  Returns false
+// (and no cut) when the bound is reached.
+__device__ __forceinline__ bool idx_wait_cut(const uint32_t *slots, bool want_b, uint32_t &tk, uint32_t &kb,
+                                             IdxShared &sh) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const bool rd = lane < kIdxCutParts || (want_b && lane == kIdxCutParts);
+        uint32_t x = 0u;
+        int in = 0;
+#pragma unroll 1
+        for (int it = 0; it < kCutSpinMax; ++it) {
+            x = rd ? __hip_atomic_load(slots + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1u;
+            if (__ballot(x == 0u) == 0ull) {       // (uniform)
+                in = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        uint64_t sum = 0;
+#pragma unroll
+        for (int p = 0; p < kIdxCutParts; ++p) sum += (uint32_t)__builtin_amdgcn_readlane((int)x, p) - 1u;
+        const uint32_t xb = (uint32_t)__builtin_amdgcn_readlane((int)x, kIdxCutParts);
+        if (lane == 0) {
+            sh.cut_tk = (uint32_t)(sum / kIdxCutParts);
+            sh.cut_kb = xb - 1u;
+            sh.cut_in = in;
+        }
+    }
+    __syncthreads();
+    tk = sh.cut_tk;
+    kb = sh.cut_kb;
+    return sh.cut_in != 0;
+}
+
+// grid (n_chunks [+1 with the fused append], Hkv, n_seq); mode 3 (with the
+// checkpoint append) puts the append workgroup and then kIdxCutParts cut
+// workgroups (idx_cut_part) before the chunks
 template <int HD, int G>
 __global__ void __launch_bounds__(kIdxThreads)
 k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq_len, int32_t max_seq_len,
@@ -305,7 +433,17 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
           int32_t select_here, IdxAppend ia) {
 #pragma clang fp contract(off)
     __shared__ IdxShared sh;
-    const int tid = threadIdx.x, c = blockIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
+    const bool incut = select_here == 3;
+    if (incut && (int)blockIdx.x <= kIdxCutParts) {
+        if (blockIdx.x == 0)                       // the checkpoint indexer's append workgroup
+            idx_append_wg<HD, G, kIdxThreads>(g, ia, q, seq_len, s, reinterpret_cast<uint16_t *>(v.pooled),
+                                              ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, sh.u.q);
+        else                                       // part blockIdx.x - 1 of the sequence's cut
+            idx_cut_part<HD, G>(g, v, q, seq_len, max_seq_len, ws, s, gh, (int)blockIdx.x - 1, sh);
+        return;
+    }
+    const int c = (int)blockIdx.x - (incut ? kIdxCutParts + 1 : 0);
     if (ia.enabled && c == n_chunks) {             // the checkpoint indexer's append workgroup (one KV row)
         idx_append_wg<HD, G, kIdxThreads>(g, ia, q, seq_len, s, reinterpret_cast<uint16_t *>(v.pooled),
                                           ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, sh.u.q);
@@ -319,11 +457,14 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     }
     // select_here == 2 (a long decode row whose attention selects): the
     // chunk's eligible keys at or above the append launch's cut go to its
-    // candidate slots, in block order, with their count
-    const bool emit = select_here == 2;
+    // candidate slots, in block order, with their count; 3: the same with the
+    // cut of this launch's part workgroups, waited for after the scoring (a
+    // wait that runs out marks the chunk's count past kSelCandMax, and the
+    // attention selects over the whole row)
+    const bool emit = select_here >= 2;
     const int pair = s * g.Hkv + gh;
     uint32_t tk = 0u;
-    if (emit) {                                    // the append launch's part thresholds: their mean key
+    if (select_here == 2) {                        // the append launch's part thresholds: their mean key
         static_assert(kIdxCutParts == 16, "four 16-byte loads");
         uint64_t sum = 0;
 #pragma unroll
@@ -370,7 +511,8 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
         if (ne > eff_topk(g, r) && c * kBlocksPerChunk < ne) {
             const int b = r.e_lo + bi;
             // the block this token completes is the append workgroup's to score
-            const bool act = bi < ne && !(ia.enabled && L % g.bt == 0 && b == (L - 1) / g.bt);
+            const int bc = ia.enabled && L % g.bt == 0 ? (L - 1) / g.bt : -1;
+            const bool act = bi < ne && b != bc;
 #pragma unroll
             for (int i = 0; i < QV; ++i)
                 if (tid + i * kIdxThreads < G * HD / 4) reinterpret_cast<float4 *>(sh.u.q)[tid + i * kIdxThreads] = qv[i];
@@ -399,7 +541,15 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
             }
             if (act && j == 0) sc[b] = score;
             if (emit) {                            // (uniform)
-                const bool in = act && j == 0 && score_key(score) >= tk;
+                // mode 3: the chunk holding the completed block takes that
+                // block's key from the append workgroup, at the block's lane
+                const int c0 = r.e_lo + c * kBlocksPerChunk;
+                const bool want_b = incut && bc >= c0 && bc < c0 + kBlocksPerChunk && bc < r.e_hi;
+                uint32_t kb = 0u;
+                const bool cut_in =
+                    !incut || idx_wait_cut(ws.cutk + (int64_t)pair * kCutSlots, want_b, tk, kb, sh);
+                const uint32_t key = act ? score_key(score) : kb;
+                const bool in = cut_in && (act || (want_b && b == bc)) && j == 0 && key >= tk;
                 const uint64_t m = __ballot(in);
                 const int lane = tid & 63, w = tid >> 6;
                 if (lane == 0) sh.tmp[w] = __builtin_popcountll(m);
@@ -410,7 +560,8 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
                     at += i < w ? sh.tmp[i] : 0;
                     n_cand += sh.tmp[i];
                 }
-                if (in) ws.cand[((int64_t)pair * n_chunks + c) * kBlocksPerChunk + at] = make_uint2(score_key(score), (uint32_t)b);
+                if (in) ws.cand[((int64_t)pair * n_chunks + c) * kBlocksPerChunk + at] = make_uint2(key, (uint32_t)b);
+                if (!cut_in) n_cand = kSelCandMax + 1;
             }
             __syncthreads();                       // q reads done before the union is reused
         }
@@ -583,7 +734,7 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
                                    const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                                    int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                                    FusedAppend fa, hipStream_t st, bool select, bool sel_launch,
-                                   const IdxAppend *ia) {
+                                   const IdxAppend *ia, bool in_cut) {
     // The append workgroup's pooled block must not be one the scoring
     // workgroups read: with local_tokens = 0 a just-completed block is
     // eligible, so the append and the pooling run as launches of their own,
@@ -608,13 +759,15 @@ static hipError_t launch_indexer_t(const Geo &g, const qwfn_kv_view &v, const fl
     if (n_chunks < 1) n_chunks = 1;
     IdxAppend ian{};
     if (ia) ian = *ia;
-    const dim3 grid((unsigned)(n_chunks + (fa.enabled || ian.enabled ? 1 : 0)), (unsigned)g.Hkv, (unsigned)n_seq);
     const bool big = nb_max > kKeysMax;           // more eligible blocks than the workgroup's registers hold
     // 1: the last workgroup selects; 0: scores only (a selection launch
     // follows, or for a row the workgroup's registers hold the attention
     // selects: sel_launch false); 2: scores and each chunk's candidates (the
-    // attention selects)
-    const int32_t mode = !big ? (sel_launch ? 1 : 0) : sel_launch ? 0 : 2;
+    // attention selects); 3: as 2 with the cut placed in this launch
+    const int32_t mode = !big ? (sel_launch ? 1 : 0) : sel_launch ? 0 : in_cut ? 3 : 2;
+    if (mode == 3 && !(ian.enabled && ian.slots && !fa.enabled)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((mode == 3 ? kIdxCutParts : 0) + n_chunks + (fa.enabled || ian.enabled ? 1 : 0)),
+                    (unsigned)g.Hkv, (unsigned)n_seq);
     QWFN_LAUNCH(kTimedIndexer, (k_indexer<HD, G>), grid, dim3(kIdxThreads), st, g, v, q, seq_len, max_seq_len,
                 sel, nsel, max_sel, ws, n_chunks, fa, mode, ian);
     hipError_t e = hipGetLastError();
@@ -2370,11 +2523,11 @@ hipError_t launch_indexer(const Geo &g, const qwfn_kv_view &v, const float *q,
                           const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len,
                           int32_t *sel, int32_t *nsel, int32_t max_sel, const Ws &ws,
                           const FusedAppend &fa, hipStream_t st, bool select, bool sel_launch,
-                          const IdxAppend *ia) {
+                          const IdxAppend *ia, bool in_cut) {
 #define X(HD_, G_, TG_)                                                                          \
     if (g.hd == HD_ && g.G == G_)                                                                \
         return launch_indexer_t<HD_, G_>(g, v, q, seq_len, n_seq, max_seq_len, sel, nsel, max_sel, ws, fa, st, select, \
-                                         sel_launch, ia);
+                                         sel_launch, ia, in_cut);
     QWFN_FOR_EACH_SHAPE(X)
 #undef X
     return hipErrorInvalidValue;

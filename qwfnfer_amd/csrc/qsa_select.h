@@ -42,6 +42,8 @@ struct IdxShared {
     float red[2 * (kIdxThreads / 64)];             // selection: per-wave max, min
     int tmp[16];
     int flag, bin, need, ncand, cnt_b;
+    uint32_t cut_tk, cut_kb;                       // the in-launch cut (idx_wait_cut)
+    int cut_in;
 };
 
 

@@ -384,7 +384,7 @@ def test_idx_select_long_context(lengths, mode):
     assert qsa.read_status(dev) == 0
 
 
-@pytest.mark.parametrize("mode", ["random", "cluster"])
+@pytest.mark.parametrize("mode", ["random", "cluster", "newest"])
 def test_checkpoint_fused_decode_long_context(mode):
     """qwfn_idx_sparse_attn_decode past 8192 eligible blocks, where the
     attention workgroups select from the indexer's score row themselves (no
@@ -393,10 +393,12 @@ def test_checkpoint_fused_decode_long_context(mode):
     outputs and selections bit for bit equal to the four separate calls
     (qwfn_idx_select's multi-workgroup selection, then the given-selection
     attention).  cluster: 200 consecutive blocks aligned with the query heads'
-    sum, so the winners crowd into one run of the row."""
+    sum, so the winners crowd into one run of the row.  newest: both tokens of
+    step 0 complete a block whose rows (the new one too) are so aligned, so the
+    block the indexer launch's append workgroup re-pools and scores must win."""
     cfg = CKPT
-    rng = np.random.default_rng(880 + (mode == "cluster"))
-    L0 = [40003, 45001]
+    rng = np.random.default_rng(880 + ("random", "cluster", "newest").index(mode))
+    L0 = [40003, 45003] if mode == "newest" else [40003, 45001]
     steps = 2
     pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
     pairs = [_pair(cfg, 2, pps, seed=881), _pair(cfg, 2, pps, seed=881)]
@@ -410,6 +412,9 @@ def test_checkpoint_fused_decode_long_context(mode):
         if mode == "cluster":                      # blocks 2000 .. 2199 along the heads' sum of step 0
             x[8000:8800, :64] *= 0.01
             x[8000:8800, 64:] = 0.01 * x[8000:8800, 64:] + qi_all[0, s, :, 64:].sum(0)
+        if mode == "newest":                       # the block step 0 completes, its first three rows
+            x[-3:, :64] *= 0.01
+            x[-3:, 64:] = 0.01 * x[-3:, 64:] + qi_all[0, s, :, 64:].sum(0)
         for d, c in ((dev, ic), (dev2, ic2)):
             qsa.append_q8_0(d, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
                             torch.arange(L0[s], dtype=torch.int32, device="cuda"),
@@ -427,6 +432,9 @@ def test_checkpoint_fused_decode_long_context(mode):
         xr = rng.standard_normal((2, 128)).astype(np.float32)
         q = rng.standard_normal((2, 24, 256)).astype(np.float32)
         qi = qi_all[step]
+        if mode == "newest" and step == 0:         # the completing row, aligned too
+            xr[:, :64] *= 0.01
+            xr[:, 64:] = 0.01 * xr[:, 64:] + qi[:, :, 64:].sum(1)
         L = torch.tensor(lens, dtype=torch.int32, device="cuda")
         sel = torch.full((2, 2, msel), -7, dtype=torch.int32, device="cuda")
         nsel = torch.empty((2, 2), dtype=torch.int32, device="cuda")
@@ -450,6 +458,8 @@ def test_checkpoint_fused_decode_long_context(mode):
             assert len(want) == 513
             if mode == "cluster" and step == 0:
                 assert set(range(2000, 2200)) <= set(want.tolist())
+            if mode == "newest" and step == 0:
+                assert lens[s] % 4 == 0 and (lens[s] - 1) // 4 in want.tolist()
             for g in range(2):
                 assert gn[s, g] == len(want)
                 np.testing.assert_array_equal(gs[s, g, :gn[s, g]], want, err_msg=f"step {step} seq {s} head {g}")
