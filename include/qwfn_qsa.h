@@ -195,6 +195,15 @@ int qwfn_qsa_test_prefill_scores(const qwfn_qsa_shape *shape, const qwfn_kv_view
 int qwfn_qsa_test_select_rows(const qwfn_qsa_shape *shape, const float *scores, int32_t nb_cap,
                               const int32_t *seq_len, int32_t n_seq, int32_t max_seq_len, int32_t *sel,
                               int32_t *n_sel, int32_t max_sel, void *stream);
+/* Test hook; it has no counterpart in the reference and serves the tests of
+ * the checkpoint decode's failure path past 8192 eligible blocks.  There the
+ * indexer launch's scoring workgroups wait for the launch's sampled cut by at
+ * most `polls` reads of its slots (default 65536, for calls that start after
+ * this one); a wait that runs out leaves no candidates, and the attention then
+ * selects over the whole score row, with the same result.  polls = 0 makes
+ * every wait run out at once.  *previous (optional) gets the bound it
+ * replaces.  QWFN_EINVAL for a negative bound.                                */
+int qwfn_qsa_test_set_cut_polls(int32_t polls, int32_t *previous);
 /* Validates a shape (QWFN_EINVAL) and whether this build has kernels for it
  * (QWFN_ENOTSUP).  Replaces the reference's shape constants
  * (src/qwfn_hparams.h:22-36, src/qwfn_engine.cpp:382-435).                   */

@@ -36,6 +36,7 @@ EXPORTS = (
     "qwfn_qsa_time_next_call",
     "qwfn_qsa_test_prefill_scores",
     "qwfn_qsa_test_select_rows",
+    "qwfn_qsa_test_set_cut_polls",
     "qwfn_qsa_check_shape",
     "qwfn_qsa_page_bytes",
     "qwfn_qsa_pooled_bytes",
@@ -143,6 +144,7 @@ _SIGS = {
     "qwfn_qsa_time_next_call": (C.c_int, [C.POINTER(C.c_void_p)]),
     "qwfn_qsa_test_prefill_scores": (C.c_int, [_S, _V, _P, _I, _I, _I, _P, _P, _I, _P]),
     "qwfn_qsa_test_select_rows": (C.c_int, [_S, _P, _I, _P, _I, _I, _P, _P, _I, _P]),
+    "qwfn_qsa_test_set_cut_polls": (C.c_int, [_I, C.POINTER(_I)]),
     "qwfn_qsa_check_shape": (C.c_int, [_S]),
     "qwfn_qsa_page_bytes": (C.c_int, [_S, C.POINTER(_Z)]),
     "qwfn_qsa_pooled_bytes": (C.c_int, [_S, _I, _I, C.POINTER(_Z)]),

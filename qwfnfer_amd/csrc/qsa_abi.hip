@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -19,6 +20,10 @@ thread_local KernelTimer qwfn_qsa::g_kernel_timer{};
 namespace {
 
 thread_local std::string g_err;
+
+// The bound on the in-launch cut's polls of the checkpoint decode calls that
+// start after it is set (qwfn_qsa_test_set_cut_polls).
+std::atomic<int32_t> g_cut_polls{kCutPollsDefault};
 
 // Disarms, on return from a decode entry point, the kernel timing its call
 // did not use (qwfn_qsa_time_next_call arms it for one call only).
@@ -268,6 +273,13 @@ int qwfn_qsa_test_prefill_scores(const qwfn_qsa_shape *shape, const qwfn_kv_view
     g.pf_seq = seq;
     const hipError_t e = launch_pf_approx_scores(g, *view, q, n_q, n_blk, scores, nb_cap, pnorm, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_fail(e, "test_prefill_scores");
+}
+
+int qwfn_qsa_test_set_cut_polls(int32_t polls, int32_t *previous) {
+    if (polls < 0) return fail(QWFN_EINVAL, "test_set_cut_polls: negative bound %d", polls);
+    const int32_t old = g_cut_polls.exchange(polls);
+    if (previous) *previous = old;
+    return ok();
 }
 
 int qwfn_qsa_test_select_rows(const qwfn_qsa_shape *shape, const float *scores, int32_t nb_cap,
@@ -1004,7 +1016,7 @@ int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view 
     // completes when that block is eligible
     const IdxAppend ia{g, *view, ig, FusedAppend{k_new, v_new, f16, 1}, k_raw, iview->k_norm,
                        (uint16_t *)iview->raw, f16, (row_sel || in_cut) && gi.Hkv == 1 ? 1 : 0,
-                       in_cut ? wi.cutk : nullptr};
+                       in_cut ? wi.cutk : nullptr, g_cut_polls.load()};
     hipError_t e = hipSuccess;
     if (!ia.enabled) {
         e = launch_idx_append_pool(g, *view, ig, (uint16_t *)iview->raw, (uint16_t *)iview->pooled, iview->k_norm,

@@ -171,8 +171,17 @@ __device__ __forceinline__ void idx_append_wg(const Geo &gi, const IdxAppend &ia
     }
     constexpr int K = D / 64;
     const int L = len[s];
+    uint16_t nh[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int64_t e = (int64_t)s * D + lane + 64 * k;
+        nh[k] = ia.f16 ? reinterpret_cast<const uint16_t *>(ia.src)[e] : f2h(reinterpret_cast<const float *>(ia.src)[e]);
+    }
+    float4 qr[D / 16];                             // the block score's query values, loaded early
+    idx_score_q<D, G>(q + (int64_t)s * gi.H * D, lane, qr);
     // the block this token completes, when it is eligible: its chunk's scoring
-    // workgroup waits for its key in the slot (the same test on that side)
+    // workgroup waits for its key in the slot (the same test on that side);
+    // tested once the loads above are out
     bool expect = false;
     if (ia.slots && L >= 1 && L % g.bt == 0 && gi.topk > 0) {
         const Ranges r = qsa_ranges(gi, L);
@@ -183,14 +192,6 @@ __device__ __forceinline__ void idx_append_wg(const Geo &gi, const IdxAppend &ia
     auto publish = [&](uint32_t key1) {
         if (expect && lane == 0) __hip_atomic_store(slot, key1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
-    uint16_t nh[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int64_t e = (int64_t)s * D + lane + 64 * k;
-        nh[k] = ia.f16 ? reinterpret_cast<const uint16_t *>(ia.src)[e] : f2h(reinterpret_cast<const float *>(ia.src)[e]);
-    }
-    float4 qr[D / 16];                             // the block score's query values, loaded early
-    idx_score_q<D, G>(q + (int64_t)s * gi.H * D, lane, qr);
     const int t = L - 1;
     if (s >= g.n_seq_view) { if (lane == 0) set_status(ia.va.status, QWFN_STATUS_SEQ_RANGE); publish(1u); return; }
     if (t < 0 || (int64_t)t >= (int64_t)g.pps * g.pt) {

@@ -224,7 +224,9 @@ struct IdxAppend {
     uint16_t *raw;
     int32_t f16, enabled;
     uint32_t *slots;     // the in-launch cut's slots (in_cut), else NULL
+    int32_t polls;       // the bound on a scoring workgroup's reads of them
 };
+constexpr int32_t kCutPollsDefault = 1 << 16;
 // select = false: scores only (the attention selects, launch_attention_select);
 // sel_launch = false: the indexer does not select and no selection launch
 // follows: rows past its workgroup's registers leave each chunk's candidates

@@ -380,26 +380,23 @@ __device__ __forceinline__ void idx_cut_part(const Geo &g, const qwfn_kv_view &v
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls of a chunk workgroup waiting for the in-launch cut.
-constexpr int kCutSpinMax = 1 << 16;
-
 // The in-launch cut for a chunk workgroup: wave 0 polls the kIdxCutParts part
 // slots of its sequence (lane p reads part p with agent-scope loads) and, with
 // want_b, the completed block's slot (lane kIdxCutParts) until every one is
 // in; the mean of the part keys goes to tk and the block's key to kb.  The
 // append and part workgroups come first in the grid and wait for nothing, so
 // they are dispatched before any workgroup that polls and always finish; the
-// bound on the polls only makes every wave's exit certain.  Returns false
-// (and no cut) when the bound is reached.
-__device__ __forceinline__ bool idx_wait_cut(const uint32_t *slots, bool want_b, uint32_t &tk, uint32_t &kb,
-                                             IdxShared &sh) {
+// bound on the polls (IdxAppend::polls, kCutPollsDefault) only makes every
+// wave's exit certain.  Returns false (and no cut) when the bound is reached.
+__device__ __forceinline__ bool idx_wait_cut(const uint32_t *slots, bool want_b, int polls, uint32_t &tk,
+                                             uint32_t &kb, IdxShared &sh) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         const bool rd = lane < kIdxCutParts || (want_b && lane == kIdxCutParts);
         uint32_t x = 0u;
         int in = 0;
 #pragma unroll 1
-        for (int it = 0; it < kCutSpinMax; ++it) {
+        for (int it = 0; it < polls; ++it) {
             x = rd ? __hip_atomic_load(slots + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1u;
             if (__ballot(x == 0u) == 0ull) {       // (uniform)
                 in = 1;
@@ -435,18 +432,16 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
     __shared__ IdxShared sh;
     const int tid = threadIdx.x, gh = blockIdx.y, s = blockIdx.z;
     const bool incut = select_here == 3;
-    if (incut && (int)blockIdx.x <= kIdxCutParts) {
-        if (blockIdx.x == 0)                       // the checkpoint indexer's append workgroup
-            idx_append_wg<HD, G, kIdxThreads>(g, ia, q, seq_len, s, reinterpret_cast<uint16_t *>(v.pooled),
-                                              ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, sh.u.q);
-        else                                       // part blockIdx.x - 1 of the sequence's cut
-            idx_cut_part<HD, G>(g, v, q, seq_len, max_seq_len, ws, s, gh, (int)blockIdx.x - 1, sh);
-        return;
-    }
     const int c = (int)blockIdx.x - (incut ? kIdxCutParts + 1 : 0);
-    if (ia.enabled && c == n_chunks) {             // the checkpoint indexer's append workgroup (one KV row)
+    // the checkpoint indexer's append workgroup (one KV row): the first of the
+    // grid in mode 3, else the last
+    if (ia.enabled && (incut ? blockIdx.x == 0 : c == n_chunks)) {
         idx_append_wg<HD, G, kIdxThreads>(g, ia, q, seq_len, s, reinterpret_cast<uint16_t *>(v.pooled),
                                           ws.scores + (int64_t)s * g.Hkv * ws.nb_cap, sh.u.q);
+        return;
+    }
+    if (c < 0) {                                   // mode 3: part blockIdx.x - 1 of the sequence's cut
+        idx_cut_part<HD, G>(g, v, q, seq_len, max_seq_len, ws, s, gh, (int)blockIdx.x - 1, sh);
         return;
     }
     if (fa.enabled && c == n_chunks) {             // the append workgroup
@@ -547,7 +542,7 @@ k_indexer(Geo g, qwfn_kv_view v, const float *__restrict__ q, const int32_t *seq
                 const bool want_b = incut && bc >= c0 && bc < c0 + kBlocksPerChunk && bc < r.e_hi;
                 uint32_t kb = 0u;
                 const bool cut_in =
-                    !incut || idx_wait_cut(ws.cutk + (int64_t)pair * kCutSlots, want_b, tk, kb, sh);
+                    !incut || idx_wait_cut(ws.cutk + (int64_t)pair * kCutSlots, want_b, ia.polls, tk, kb, sh);
                 const uint32_t key = act ? score_key(score) : kb;
                 const bool in = cut_in && (act || (want_b && b == bc)) && j == 0 && key >= tk;
                 const uint64_t m = __ballot(in);

@@ -232,3 +232,19 @@ def test_time_next_call_arms_pairs_only():
     assert lib.qwfn_qsa_time_next_call(arr) == _lib.QWFN_EINVAL
     assert "stop" in lib.qwfn_qsa_last_error().decode()
     assert lib.qwfn_qsa_time_next_call(None) == 0                # disarm
+
+
+def test_cut_poll_bound_hook():
+    """qwfn_qsa_test_set_cut_polls swaps the bound (default 65536) and returns
+    the one it replaces; a negative bound is refused and changes nothing."""
+    prev = C.c_int32(-1)
+    assert _code("qwfn_qsa_test_set_cut_polls", 7, C.byref(prev)) == 0
+    try:
+        assert prev.value == 65536
+        again = C.c_int32(-1)
+        assert _code("qwfn_qsa_test_set_cut_polls", -1, C.byref(again)) == _lib.QWFN_EINVAL
+        assert again.value == -1
+        assert _code("qwfn_qsa_test_set_cut_polls", 9, None) == 0
+        assert _code("qwfn_qsa_test_set_cut_polls", 7, C.byref(again)) == 0 and again.value == 9
+    finally:
+        assert _code("qwfn_qsa_test_set_cut_polls", prev.value, None) == 0

@@ -8,6 +8,8 @@ oracle; the rotation's fp64 cos / sin are rounded to fp32, so a last-bit
 difference between the device and host libm would surface here), the
 selection.  Attention: |o - o_ref| <= 2e-3 + 1e-3 |o_ref| against the fp64
 oracle over the same selection."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -384,8 +386,14 @@ def test_idx_select_long_context(lengths, mode):
     assert qsa.read_status(dev) == 0
 
 
-@pytest.mark.parametrize("mode", ["random", "cluster", "newest"])
-def test_checkpoint_fused_decode_long_context(mode):
+def _set_cut_polls(n: int) -> int:
+    prev = C.c_int32()
+    _lib.call("qwfn_qsa_test_set_cut_polls", n, C.byref(prev))
+    return prev.value
+
+
+@pytest.mark.parametrize("mode", ["random", "cluster", "newest", "no_poll"])
+def test_checkpoint_fused_decode_long_context(mode, request):
     """qwfn_idx_sparse_attn_decode past 8192 eligible blocks, where the
     attention workgroups select from the indexer's score row themselves (no
     selection launch): two sequences over two steps, the selections bit for
@@ -395,10 +403,17 @@ def test_checkpoint_fused_decode_long_context(mode):
     attention).  cluster: 200 consecutive blocks aligned with the query heads'
     sum, so the winners crowd into one run of the row.  newest: both tokens of
     step 0 complete a block whose rows (the new one too) are so aligned, so the
-    block the indexer launch's append workgroup re-pools and scores must win."""
+    block the indexer launch's append workgroup re-pools and scores must win.
+    no_poll: the scoring workgroups' wait for the launch's sampled cut bounded
+    at zero polls (qwfn_qsa_test_set_cut_polls), so every chunk leaves no
+    candidates and the attention selects over the whole row; both tokens of
+    step 0 complete a block."""
     cfg = CKPT
-    rng = np.random.default_rng(880 + ("random", "cluster", "newest").index(mode))
-    L0 = [40003, 45003] if mode == "newest" else [40003, 45001]
+    rng = np.random.default_rng(880 + ("random", "cluster", "newest", "no_poll").index(mode))
+    L0 = [40003, 45003] if mode in ("newest", "no_poll") else [40003, 45001]
+    if mode == "no_poll":
+        prev = _set_cut_polls(0)
+        request.addfinalizer(lambda: _set_cut_polls(prev))
     steps = 2
     pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
     pairs = [_pair(cfg, 2, pps, seed=881), _pair(cfg, 2, pps, seed=881)]
