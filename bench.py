@@ -465,9 +465,9 @@ class CheckpointRunner:
     a layer: the indexer (one extra workgroup appends the K/V rows and the raw
     indexer key, re-pools its block and scores it when complete), the attention
     (every workgroup selects from the indexer's row) and its merge.  Past 8,192
-    blocks, four: the K/V rows, raw key and pooled key with a sampled cut of the
-    row, the indexer (its workgroups keep the keys above the cut as
-    candidates), the attention (ranking the candidates itself) and the merge."""
+    blocks, also three: the indexer launch's first workgroups append and place a
+    sampled cut of the row, its scoring workgroups keep the keys above the cut
+    as candidates, the attention ranks the candidates itself, and the merge."""
 
     def __init__(self, qsa, torch, ctx, n_layer, gen):
         self.qsa, self.torch = qsa, torch
@@ -833,9 +833,9 @@ def main():
             torch.cuda.empty_cache()
         checkpoint = dict(per_context=ck, workload="the released checkpoint's attention layer: 24q/2kv heads "
                           "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
-                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (3 launches "
-                          "up to 8,192 blocks: indexer with the append, attention, merge; 4 past them: append with a "
-                          "sampled cut, indexer, attention, merge), hipGraph")
+                          "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (3 launches: "
+                          "indexer with the append, attention, merge; past 8,192 blocks the indexer launch also "
+                          "places a sampled cut and keeps each chunk's candidates above it), hipGraph")
         if not args.no_prefill:
             checkpoint["prefill"] = bench_checkpoint_prefill(qsa, torch, gen)
             log(f"[bench] checkpoint prefill chunk ({PREFILL_N} queries at {PREFILL_POS0}): "

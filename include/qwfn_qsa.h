@@ -531,19 +531,21 @@ int qwfn_idx_select(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
  * indexer scores (its launch also appends the rows and pools and scores the
  * block the token completes) and every attention workgroup selects from the
  * row: three launches.
- * Past 8,192 candidate blocks (the 4-token blocks past 32,768 tokens) the
- * append launch also scores 1,024
- * sampled blocks of each row and places a cut, the indexer keeps each chunk's
- * scores above it, and the attention workgroups rank those candidates
- * exactly (a fallback over the whole row where the cut leaves too few or too
- * many), so no selection launch runs.  That covers the checkpoint's heads
- * (24 x 256, 4 indexer heads of at most 128) up to 49,152 blocks; longer
- * rows, other shapes and a workspace smaller than qwfn_idx_workspace_bytes
- * (at least what qwfn_qsa_workspace_bytes and qwfn_idx_select each need)
- * select in the indexer's last workgroup or a selection launch, as
- * qwfn_idx_select does.  Replaces the four calls qwfn_kv_append_q8_0,
- * qwfn_idx_append_pool, qwfn_idx_select and qwfn_sparse_decode_attn of a
- * decode step (five launches, six past 8,192 blocks) with two fewer. */
+ * Past 8,192 candidate blocks (the 4-token blocks past 32,768 tokens), also
+ * three: 16 more workgroups of the indexer launch score 1,024 sampled blocks
+ * of each row and place a cut, the scoring workgroups wait for it and keep
+ * each chunk's scores above it, and the attention workgroups rank those
+ * candidates exactly (a fallback over the whole row where the cut leaves too
+ * few or too many), so no selection launch runs.  That covers the
+ * checkpoint's heads (24 x 256, 4 indexer heads of at most 128) up to 49,152
+ * blocks (an indexer of more than one KV head puts the append and the cut in a
+ * launch of their own first); longer rows, other shapes and a workspace
+ * smaller than qwfn_idx_workspace_bytes (at least what
+ * qwfn_qsa_workspace_bytes and qwfn_idx_select each need) select in the
+ * indexer's last workgroup or a selection launch, as qwfn_idx_select does.
+ * Replaces the four calls qwfn_kv_append_q8_0, qwfn_idx_append_pool,
+ * qwfn_idx_select and qwfn_sparse_decode_attn of a decode step (five
+ * launches, six past 8,192 blocks) with three. */
 int qwfn_idx_sparse_attn_decode(const qwfn_qsa_shape *shape, const qwfn_kv_view *view,
                                 const qwfn_idx_shape *ishape, const qwfn_idx_view *iview,
                                 const float *q, const float *q_idx, const void *k_new,
