@@ -392,7 +392,7 @@ def _set_cut_polls(n: int) -> int:
     return prev.value
 
 
-@pytest.mark.parametrize("mode", ["random", "cluster", "newest", "no_poll"])
+@pytest.mark.parametrize("mode", ["random", "cluster", "newest", "no_poll", "eight"])
 def test_checkpoint_fused_decode_long_context(mode, request):
     """qwfn_idx_sparse_attn_decode past 8192 eligible blocks, where the
     attention workgroups select from the indexer's score row themselves (no
@@ -407,20 +407,24 @@ def test_checkpoint_fused_decode_long_context(mode, request):
     no_poll: the scoring workgroups' wait for the launch's sampled cut bounded
     at zero polls (qwfn_qsa_test_set_cut_polls), so every chunk leaves no
     candidates and the attention selects over the whole row; both tokens of
-    step 0 complete a block."""
+    step 0 complete a block.  eight: eight sequences, more indexer workgroups
+    than the device holds at once, so later sequences' cut workgroups start
+    only as earlier sequences' scoring workgroups finish."""
     cfg = CKPT
-    rng = np.random.default_rng(880 + ("random", "cluster", "newest", "no_poll").index(mode))
-    L0 = [40003, 45003] if mode in ("newest", "no_poll") else [40003, 45001]
+    rng = np.random.default_rng(880 + ("random", "cluster", "newest", "no_poll", "eight").index(mode))
+    L0 = ([40003, 45003] if mode in ("newest", "no_poll") else
+          [33001 + 997 * i for i in range(8)] if mode == "eight" else [40003, 45001])
+    ns = len(L0)
     if mode == "no_poll":
         prev = _set_cut_polls(0)
         request.addfinalizer(lambda: _set_cut_polls(prev))
     steps = 2
     pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
-    pairs = [_pair(cfg, 2, pps, seed=881), _pair(cfg, 2, pps, seed=881)]
+    pairs = [_pair(cfg, ns, pps, seed=881), _pair(cfg, ns, pps, seed=881)]
     dev, host, ic, w = pairs[0]
     dev2, _, ic2, _ = pairs[1]
-    qi_all = rng.standard_normal((steps, 2, 4, 128)).astype(np.float32)
-    for s in range(2):
+    qi_all = rng.standard_normal((steps, ns, 4, 128)).astype(np.float32)
+    for s in range(ns):
         k, v = kv_rows(rng, L0[s], cfg)
         assert host.append(k, v, np.arange(L0[s], dtype=np.int32), np.full(L0[s], s, np.int32)) == 0
         x = rng.standard_normal((L0[s], 128)).astype(np.float32)
@@ -438,37 +442,37 @@ def test_checkpoint_fused_decode_long_context(mode, request):
                                 seq_ids=torch.full((L0[s],), s, dtype=torch.int32, device="cuda"))
     c = cfg_of(cfg)
     Lmax = max(L0) + steps + 1
-    ws, ws2 = _ws(cfg, ic, 2, Lmax), _ws(cfg, ic2, 2, Lmax)
+    ws, ws2 = _ws(cfg, ic, ns, Lmax), _ws(cfg, ic2, ns, Lmax)
     msel = c.max_selected(Lmax)
     for step in range(steps):
         lens = [L + step + 1 for L in L0]
         print(f"  fused idx decode, long context ({mode}), step {step}, lengths {lens}", flush=True)
-        kn, vn = kv_rows(rng, 2, cfg)
-        xr = rng.standard_normal((2, 128)).astype(np.float32)
-        q = rng.standard_normal((2, 24, 256)).astype(np.float32)
+        kn, vn = kv_rows(rng, ns, cfg)
+        xr = rng.standard_normal((ns, 128)).astype(np.float32)
+        q = rng.standard_normal((ns, 24, 256)).astype(np.float32)
         qi = qi_all[step]
         if mode == "newest" and step == 0:         # the completing row, aligned too
             xr[:, :64] *= 0.01
             xr[:, 64:] = 0.01 * xr[:, 64:] + qi[:, :, 64:].sum(1)
         L = torch.tensor(lens, dtype=torch.int32, device="cuda")
-        sel = torch.full((2, 2, msel), -7, dtype=torch.int32, device="cuda")
-        nsel = torch.empty((2, 2), dtype=torch.int32, device="cuda")
+        sel = torch.full((ns, 2, msel), -7, dtype=torch.int32, device="cuda")
+        nsel = torch.empty((ns, 2), dtype=torch.int32, device="cuda")
         qd, qid = torch.from_numpy(q).cuda(), torch.from_numpy(qi).cuda()
         knd, vnd, xrd = (torch.from_numpy(a).cuda() for a in (kn, vn, xr))
         out = qsa.idx_sparse_attn_decode(ic, qd, qid, knd, vnd, xrd, L, Lmax, ws, sel=sel, n_sel=nsel)
         pos = L - 1
-        qsa.append_q8_0(dev2, knd, vnd, pos, seq_ids=torch.arange(2, dtype=torch.int32, device="cuda"))
-        qsa.idx_append_pool(ic2, xrd, pos, seq_ids=torch.arange(2, dtype=torch.int32, device="cuda"))
+        qsa.append_q8_0(dev2, knd, vnd, pos, seq_ids=torch.arange(ns, dtype=torch.int32, device="cuda"))
+        qsa.idx_append_pool(ic2, xrd, pos, seq_ids=torch.arange(ns, dtype=torch.int32, device="cuda"))
         sel2 = torch.full_like(sel, -7)
         nsel2 = torch.empty_like(nsel)
         qsa.idx_select(ic2, qid, L, Lmax, ws2, sel=sel2, n_sel=nsel2)
         out2 = qsa.sparse_decode_attn(dev2, qd, L, Lmax, ws2, sel=sel2, n_sel=nsel2)
         torch.cuda.synchronize()
-        assert host.append(kn, vn, np.array([l - 1 for l in lens], np.int32), np.arange(2, dtype=np.int32)) == 0
-        hs = np.full((2, 2, msel), -1, np.int32)
+        assert host.append(kn, vn, np.array([l - 1 for l in lens], np.int32), np.arange(ns, dtype=np.int32)) == 0
+        hs = np.full((ns, 2, msel), -1, np.int32)
         gs, gn = np_of(sel), np_of(nsel)
         pooled = np_of(ic.pooled)
-        for s in range(2):
+        for s in range(ns):
             want = oracle_select(cfg, ICFG, pooled[s], qi[s], lens[s], msel)
             assert len(want) == 513
             if mode == "cluster" and step == 0:
