@@ -392,7 +392,7 @@ def _set_cut_polls(n: int) -> int:
     return prev.value
 
 
-@pytest.mark.parametrize("mode", ["random", "cluster", "newest", "no_poll", "eight"])
+@pytest.mark.parametrize("mode", ["random", "cluster", "newest", "no_poll", "eight", "long_max"])
 def test_checkpoint_fused_decode_long_context(mode, request):
     """qwfn_idx_sparse_attn_decode past 8192 eligible blocks, where the
     attention workgroups select from the indexer's score row themselves (no
@@ -409,9 +409,11 @@ def test_checkpoint_fused_decode_long_context(mode, request):
     candidates and the attention selects over the whole row; both tokens of
     step 0 complete a block.  eight: eight sequences, more indexer workgroups
     than the device holds at once, so later sequences' cut workgroups start
-    only as earlier sequences' scoring workgroups finish."""
+    only as earlier sequences' scoring workgroups finish.  long_max: a call bound
+    (max_seq_len 120,001) far past the lengths, so most of the indexer's chunk
+    workgroups lie past the eligible blocks and end without waiting."""
     cfg = CKPT
-    rng = np.random.default_rng(880 + ("random", "cluster", "newest", "no_poll", "eight").index(mode))
+    rng = np.random.default_rng(880 + ("random", "cluster", "newest", "no_poll", "eight", "long_max").index(mode))
     L0 = ([40003, 45003] if mode in ("newest", "no_poll") else
           [33001 + 997 * i for i in range(8)] if mode == "eight" else [40003, 45001])
     ns = len(L0)
@@ -419,7 +421,8 @@ def test_checkpoint_fused_decode_long_context(mode, request):
         prev = _set_cut_polls(0)
         request.addfinalizer(lambda: _set_cut_polls(prev))
     steps = 2
-    pps = (max(L0) + steps + 8) // cfg.page_tokens + 1
+    Lmax = 120001 if mode == "long_max" else max(L0) + steps + 1
+    pps = (Lmax + 8) // cfg.page_tokens + 1
     pairs = [_pair(cfg, ns, pps, seed=881), _pair(cfg, ns, pps, seed=881)]
     dev, host, ic, w = pairs[0]
     dev2, _, ic2, _ = pairs[1]
@@ -441,7 +444,6 @@ def test_checkpoint_fused_decode_long_context(mode, request):
             qsa.idx_append_pool(c, torch.from_numpy(x).cuda(), torch.arange(L0[s], dtype=torch.int32, device="cuda"),
                                 seq_ids=torch.full((L0[s],), s, dtype=torch.int32, device="cuda"))
     c = cfg_of(cfg)
-    Lmax = max(L0) + steps + 1
     ws, ws2 = _ws(cfg, ic, ns, Lmax), _ws(cfg, ic2, ns, Lmax)
     msel = c.max_selected(Lmax)
     for step in range(steps):
