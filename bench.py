@@ -128,12 +128,13 @@ def kv_row_bytes(cfg):
 
 def best_launch(graph_ms, eager_ms):
     """The faster of the two ways a caller runs the step: one hipGraph replay
-    a step, or the calls launched one by one (both time the same K steps of
-    the same work; each graph replay also pays the runtime's fixed cost of a
-    graph launch, about 7 us here)."""
+    a step, or the calls made one by one on the stream (the fused path's from
+    prepared C arguments, Runner.prepare_direct).  Both time the same K steps
+    of the same work; each graph replay also pays the runtime's fixed cost of a
+    graph launch, about 7 us a step here."""
     if graph_ms is not None and graph_ms <= eager_ms:
         return graph_ms, "hipGraph (one replay a step)"
-    return eager_ms, "eager (one launch a kernel)"
+    return eager_ms, "eager (one call a layer, each kernel launched on the stream)"
 
 
 def dominant_kernel(cfg, max_len, two_call):
@@ -280,9 +281,61 @@ class Runner:
     def graph_step(self, i):
         self.graphs[i % self.n_inst].replay()
 
-    def time_steps(self, steps, warmup, graph):
+    def prepare_direct(self):
+        """Every (replica, layer) call of the fused path with its C arguments
+        resolved once, after the wrapper's checks, for eager steps that call
+        qwfn_sparse_attn_decode straight from them as a C++ engine does (the
+        wrapper's per-call checks, structs and stream lookup cost the host about
+        15 us a call, which would pace the stream).  One direct step is checked
+        against a step through the wrapper from the same position."""
+        import ctypes as C
+        qsa, torch = self.qsa, self.torch
+        lib = qsa._lib.load()
+        st = torch.cuda.current_stream().cuda_stream
+        shape = self.cfg.shape()
+        keep, calls = [shape], []
+        n_seq = self.seq_lens[0].numel()
+        for inst in range(self.n_inst):
+            row = []
+            for il in range(self.n_layer):
+                view = self.stacks[inst][il].view()
+                keep.append(view)
+                row.append((C.byref(shape), C.byref(view), self.q[inst][il].data_ptr(), self.kn[inst][il].data_ptr(),
+                            self.vn[inst][il].data_ptr(), qsa._lib.SRC_F32, self.seq_lens[inst].data_ptr(), n_seq,
+                            self.max_len, self.out[il].data_ptr(), self.sel.data_ptr(), self.nsel.data_ptr(),
+                            self.ws.ptr(), self.ws.nbytes, st))
+            calls.append(row)
+        self.direct_keep, self.direct_calls, self.direct_fn = keep, calls, lib.qwfn_sparse_attn_decode
+        p0 = self.seq_lens[0].clone()
+        self.step(0)
+        torch.cuda.synchronize()
+        ref = [o.clone() for o in self.out]
+        for o in self.out:
+            o.fill_(float("nan"))
+        self.seq_lens[0].copy_(p0)
+        self.direct_step(0)
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
+            raise RuntimeError("a direct step differs from the wrapper's step")
+
+    def direct_step(self, i):
+        inst = i % self.n_inst
+        self.advance(inst)
+        fn = self.direct_fn
+        for args in self.direct_calls[inst]:
+            if fn(*args) < 0:
+                raise RuntimeError(self.qsa._lib.load().qwfn_qsa_last_error().decode(errors="replace"))
+
+    def time_eager(self, steps, warmup):
+        """Eager steps, the fused path's calls made from prepared arguments."""
+        if not self.fused:
+            return self.time_steps(steps, warmup, graph=False)
+        self.prepare_direct()
+        return self.time_steps(steps, warmup, graph=False, direct=True)
+
+    def time_steps(self, steps, warmup, graph, direct=False):
         torch = self.torch
-        fn = self.graph_step if graph else self.step
+        fn = self.graph_step if graph else self.direct_step if direct else self.step
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
@@ -693,7 +746,7 @@ def main():
         pps = (ctx + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
         r = Runner(qsa, torch, cfg, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
-        eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
+        eager_ms = r.time_eager(args.steps, args.warmup)
         graph_ms = None
         if not args.no_graph:
             r.capture()
@@ -727,7 +780,7 @@ def main():
             pps = (ctx + DECODE_ROOM + c.page_tokens - 1) // c.page_tokens
             pt = torch.arange(pps, dtype=torch.int32).view(1, pps)
             r = Runner(qsa, torch, c, [ctx], args.layers, pps, pt, gen, fused=not args.two_call)
-            eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
+            eager_ms = r.time_eager(args.steps, args.warmup)
             graph_ms = None
             if not args.no_graph:
                 r.capture()
@@ -754,7 +807,7 @@ def main():
         pps = (max(lens) + DECODE_ROOM + cfg.page_tokens - 1) // cfg.page_tokens
         perm = torch.from_numpy(rng.permutation(8 * pps).astype(np.int32)).view(8, pps)
         r = Runner(qsa, torch, cfg, lens, 1, pps, perm, gen, fused=not args.two_call)
-        eager_ms = r.time_steps(args.steps, args.warmup, graph=False)
+        eager_ms = r.time_eager(args.steps, args.warmup)
         graph_ms = None
         if not args.no_graph:
             r.capture()
