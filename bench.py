@@ -916,7 +916,8 @@ def main():
     flat_mode = {"eager": top["eager_us_per_layer"] / per_ctx[small]["eager_us_per_layer"]}
     if top["graph_us_per_layer"] is not None and per_ctx[small]["graph_us_per_layer"] is not None:
         flat_mode["hipGraph"] = top["graph_us_per_layer"] / per_ctx[small]["graph_us_per_layer"]
-    flat_key = "hipGraph" if "hipGraph" in flat_mode else "eager"
+    # the launch mode `value` was taken in (both legs timed the same way)
+    flat_key = "hipGraph" if "hipGraph" in flat_mode and top["launch"].startswith("hipGraph") else "eager"
     attn_gbs = top["attn_gbs"]
     dom = dominant_kernel(cfg, big + DECODE_ROOM, args.two_call)
     traffic = None
