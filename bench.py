@@ -568,15 +568,55 @@ class CheckpointRunner:
         for il in range(self.n_layer):
             self.layer(il)
 
+    def prepare_direct(self):
+        """Each layer's qwfn_idx_sparse_attn_decode arguments resolved once
+        (as Runner.prepare_direct), one direct step checked against a step
+        through the wrapper from the same position."""
+        import ctypes as C
+        qsa, torch = self.qsa, self.torch
+        st = torch.cuda.current_stream().cuda_stream
+        shape, ishape = self.cfg.shape(), self.layers[0][1].icfg.shape()
+        keep, calls = [shape, ishape], []
+        for il in range(self.n_layer):
+            c, ic = self.layers[il]
+            view, iview = c.view(), ic.view()
+            keep += [view, iview]
+            calls.append((C.byref(shape), C.byref(view), C.byref(ishape), C.byref(iview), self.q[il].data_ptr(),
+                          self.qi[il].data_ptr(), self.kn[il].data_ptr(), self.vn[il].data_ptr(),
+                          self.kr[il].data_ptr(), qsa._lib.SRC_F32, self.seq_len.data_ptr(), self.seq_len.numel(),
+                          self.max_len, self.out[il].data_ptr(), self.sel.data_ptr(), self.nsel.data_ptr(),
+                          self.sel.shape[-1], self.ws.ptr(), self.ws.nbytes, st))
+        self.direct_keep, self.direct_calls = keep, calls
+        self.direct_fn = qsa._lib.load().qwfn_idx_sparse_attn_decode
+        p0 = self.seq_len.clone()
+        self.step()
+        torch.cuda.synchronize()
+        ref = [o.clone() for o in self.out]
+        for o in self.out:
+            o.fill_(float("nan"))
+        self.seq_len.copy_(p0)
+        self.direct_step()
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(self.out, ref)):
+            raise RuntimeError("a direct checkpoint step differs from the wrapper's step")
+
+    def direct_step(self):
+        self.seq_len.add_(1)
+        fn = self.direct_fn
+        for args in self.direct_calls:
+            if fn(*args) < 0:
+                raise RuntimeError(self.qsa._lib.load().qwfn_qsa_last_error().decode(errors="replace"))
+
     def run(self, steps, warmup):
         torch = self.torch
+        self.prepare_direct()
         for _ in range(warmup):
-            self.step()
+            self.direct_step()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
-            self.step()
+            self.direct_step()
         e1.record()
         torch.cuda.synchronize()
         eager = e0.elapsed_time(e1) / steps
@@ -615,8 +655,9 @@ class CheckpointRunner:
         blocks = self.sel[0, 0, :n].cpu().tolist()
         cells = sum(max(0, min(4, L - 4 * b)) for b in blocks)
         row = self.cfg.head_dim + self.cfg.head_dim // 32 * 2
-        return dict(us_per_layer=graph * 1e3 / self.n_layer, eager_us_per_layer=eager * 1e3 / self.n_layer,
-                    blocks_kept=n, cells_per_kv_head=cells,
+        ms, mode = best_launch(graph, eager)
+        return dict(us_per_layer=ms * 1e3 / self.n_layer, launch=mode, eager_us_per_layer=eager * 1e3 / self.n_layer,
+                    graph_us_per_layer=graph * 1e3 / self.n_layer, blocks_kept=n, cells_per_kv_head=cells,
                     selected_kv_bytes=cells * row * 2 * self.cfg.n_head_kv)
 
 
@@ -888,7 +929,8 @@ def main():
                           "x 256, q8_0 KV, 4-token blocks, own indexer (4 heads x 128, RMSNorm + rotary pooled "
                           "keys), 513 kept blocks shared by both KV heads; qwfn_idx_sparse_attn_decode a layer (3 launches: "
                           "indexer with the append, attention, merge; past 8,192 blocks the indexer launch also "
-                          "places a sampled cut and keeps each chunk's candidates above it), hipGraph")
+                          "places a sampled cut and keeps each chunk's candidates above it); the faster of a hipGraph replay "
+                          "and eager calls from prepared arguments")
         if not args.no_prefill:
             checkpoint["prefill"] = bench_checkpoint_prefill(qsa, torch, gen)
             log(f"[bench] checkpoint prefill chunk ({PREFILL_N} queries at {PREFILL_POS0}): "
